@@ -1,0 +1,222 @@
+/*
+ * mrsa.h - C ABI of the MI355X (gfx950) mask-routed sparse attention library.
+ *
+ * Every entry point takes raw device pointers, element counts and scalars,
+ * enqueues its kernels on `stream` (a hipStream_t; NULL = the default stream)
+ * and returns immediately.  Nothing here allocates device memory: callers pass
+ * every output and workspace buffer.  Inputs are never written.
+ *
+ * Tensor conventions: "bf16" buffers hold raw bfloat16 bit patterns, "bool"
+ * buffers hold one byte per element (0 = false, anything else = true), all
+ * tensors are dense row-major with the shapes given in brackets, batch first.
+ *
+ * Return value: MRSA_OK, or a status naming the first problem found.  Shape /
+ * argument problems are detected on the host before anything is launched.
+ *
+ * Reference citations are relative to the root of
+ * NRHLYM/Mask-Routed-Sparse-Attention-for-Long-Context-Diffusion-Language-Models.
+ */
+#ifndef MRSA_H
+#define MRSA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MRSA_OK 0
+#define MRSA_ERR_INVALID_ARGUMENT 1 /* bad shape, size or pointer */
+#define MRSA_ERR_UNSUPPORTED 2      /* valid call outside what the kernels implement */
+#define MRSA_ERR_LAUNCH 3           /* the HIP runtime rejected a launch */
+
+/* Human-readable text for a status code (static storage). */
+const char* mrsa_status_string(int status);
+
+/* Increments whenever an entry point's signature or semantics change. */
+int mrsa_abi_version(void);
+
+/*
+ * Output fusion: out = bf16(float(remote) + float(local_weight) * float(local)).
+ * Replaces fuse_hils_outputs (ops/hils_bidir_output_fusion_tilelang.py:138-148,
+ * kernel :15-37).
+ *   remote_output, local_output, output: bf16 [rows, head_dim]
+ *   local_weight:                        bf16 [rows]
+ * (rows = B * L * H for the reference's [B, L, H, D] tensors.)
+ */
+int mrsa_fuse_hils_outputs_fwd(const void* remote_output, const void* local_output,
+                               const void* local_weight, void* output, int64_t rows,
+                               int64_t head_dim, void* stream);
+
+/*
+ * Landmark (mask-token) chunk-summary attention pool.
+ * Replaces chunk_attn_pool_gqa (ops/chunk_attn_pool_gqa_tilelang.py:425-448):
+ * the fused kernel _pool_gqa_fwd (:47-180) when groups > 1, and the compiled
+ * torch twin _compact_pool_torch (:17-37) when dense_torch_semantics != 0
+ * (the reference takes that branch for groups == 1).
+ *   mu_q:      bf16 [batch_chunks, kv_heads, groups, head_dim]
+ *   k_chunked: bf16 [batch_chunks, chunk_size, kv_heads, head_dim]
+ *   key_valid: bool [batch_chunks, chunk_size]
+ *   landmark_keys (out): bf16 [batch_chunks, kv_heads, groups, head_dim]
+ *   entropy (out):       fp32 [batch_chunks, kv_heads, groups]
+ *   bias_scale:  optional fp32 [kv_heads * groups]; when given together with
+ *   prior_bias (out, fp32 [batch_chunks, kv_heads, groups]) the kernel also
+ *   writes prior_bias = entropy * bias_scale[head] (attention.py:1425-1430).
+ * Limits: 2 <= chunk_size <= 128, groups <= 16, head_dim <= 256, head_dim % 8 == 0.
+ */
+int mrsa_chunk_attn_pool_gqa_fwd(const void* mu_q, const void* k_chunked,
+                                 const uint8_t* key_valid, int64_t batch_chunks,
+                                 int64_t chunk_size, int64_t kv_heads, int64_t groups,
+                                 int64_t head_dim, float sm_scale, int dense_torch_semantics,
+                                 const float* bias_scale, void* landmark_keys, float* entropy,
+                                 float* prior_bias, void* stream);
+
+/*
+ * Remote-route drop mask (1 = the chunk may not be routed to).
+ * Replaces remote_drop_mask (dream_dllm_hils/kernel_utils.py:102-161) with the
+ * chunk-aligned local bounds of chunk_aligned_local_bounds (:75-99).
+ *   valid_mask:   bool [batch, seq_len]
+ *   allowed_mask: optional bool [batch, seq_len, seq_len]
+ *   drop_mask (out): int32 [batch, seq_len, seq_len / chunk_size]
+ */
+int mrsa_remote_drop_mask(const uint8_t* valid_mask, const uint8_t* allowed_mask,
+                          int64_t batch, int64_t seq_len, int64_t window, int64_t chunk_size,
+                          int32_t* drop_mask, void* stream);
+
+/*
+ * Route scoring with per-KV-group top-k ("softmax then max pooling").
+ * Replaces ref_softmax_topk_max_pooling (ops/topk_head_softmax.py:15-156),
+ * which route_topk_g7 (dream_dllm_hils/routing.py:52-171) and
+ * online_softmax_topk_head (ops/topk_head_softmax.py:1242-1415) dispatch to.
+ *   q:   bf16 [batch, seq_len, kv_heads, groups, head_dim] (routing query)
+ *   lmk: bf16 [batch, chunks, kv_heads * groups, head_dim] when per_head_lmk,
+ *        else [batch, chunks, kv_heads, head_dim]
+ *   lse_local: fp32 [batch, seq_len, kv_heads, groups] (unused for pre-softmax)
+ *   bias:      optional fp32 [batch, chunks, kv_heads, groups]
+ *   drop_mask: optional int32 [batch, seq_len, chunks] (nonzero = drop)
+ *   derive_window >= 0 replaces drop_mask by the in-kernel equivalent of
+ *     remote_drop_mask(key_valid, derive_window, block_size) (requires
+ *     chunks * block_size == seq_len); key_valid (bool [batch, seq_len]) may
+ *     then be NULL for all-valid.
+ *   is_causal / window_size / q_offset: the reference's causal chunk mask.
+ *   selection_mode: 0 = "post_softmax", 1 = "pre_softmax".
+ *   indices (out): int32 [batch, seq_len, kv_heads, topk], ascending, -1 last.
+ *   scores (out):  [batch, seq_len, kv_heads, groups, topk] raw scaled q.k at
+ *     the picked chunks (-inf at -1 slots); bf16, or fp32 if scores_fp32.
+ * Ties in the selection score are broken toward the lower chunk index.
+ */
+int mrsa_route_topk_fwd(const void* q, const void* lmk, const float* lse_local,
+                        const float* bias, const int32_t* drop_mask, const uint8_t* key_valid,
+                        int64_t derive_window, int64_t batch, int64_t seq_len, int64_t chunks,
+                        int64_t kv_heads, int64_t groups, int64_t head_dim, int64_t topk,
+                        int64_t block_size, int per_head_lmk, int is_causal, int64_t window_size,
+                        int64_t q_offset, int selection_mode, float sm_scale, int32_t* indices,
+                        void* scores, int scores_fp32, void* stream);
+
+/*
+ * Route weights: softmax over [score_k + bias[idx_k] (k < topk), local_lse].
+ * Replaces _route_weights_torch (dream_dllm_hils/attention.py:126-235; the
+ * topk >= 32 path, selected at :1571-1621) and route_weights
+ * (ops/hils_bidir_route_weights_tilelang.py:276-290, topk <= 31).
+ *   scores: bf16 [batch, seq_len, kv_heads * groups, topk]
+ *   indices: int32 [batch, seq_len, kv_heads, topk]
+ *   prior_bias: fp32 [batch, chunks, kv_heads, groups]
+ *   local_lse: fp32 [batch, seq_len, kv_heads * groups]
+ *   has_gate_scale != 0 selects the affine-sigmoid gate form
+ *   (sigmoid(gate_scale * (remote_lse - local) + gate_offset)); otherwise the
+ *   plain softmax with local_lse - gate_offset when has_gate_offset.
+ *   remote_weights (out): bf16 [batch, seq_len, kv_heads * groups, topk]
+ *   local_weight (out):   bf16 [batch, seq_len, kv_heads * groups]
+ */
+int mrsa_route_weights_fwd(const void* scores, const int32_t* indices, const float* prior_bias,
+                           const float* local_lse, int64_t batch, int64_t seq_len,
+                           int64_t chunks, int64_t kv_heads, int64_t groups, int64_t topk,
+                           float temperature, int has_gate_offset, float gate_offset,
+                           int has_gate_scale, float gate_scale, void* remote_weights,
+                           void* local_weight, void* stream);
+
+/*
+ * Re-lays V out as 64-key tiles, each stored transposed (head_dim rows of 64
+ * keys), so both attention kernels can feed V to the matrix cores with
+ * contiguous loads.  Keys past seq_len inside the last tile are zero.
+ *   v: bf16 [batch, seq_len, kv_heads, head_dim]
+ *   v_tiles (out): bf16 [batch, kv_heads, ceil(seq_len / 64), head_dim, 64]
+ * No reference counterpart: internal layout step of the two attention ops.
+ */
+int64_t mrsa_value_tiles_bytes(int64_t batch, int64_t seq_len, int64_t kv_heads,
+                               int64_t head_dim);
+int mrsa_value_tiles(const void* v, int64_t batch, int64_t seq_len, int64_t kv_heads,
+                     int64_t head_dim, void* v_tiles, void* stream);
+
+/*
+ * Bidirectional sliding-window GQA attention with natural-log LSE.
+ * Replaces the flash-attn window call behind bidir_local_attention and
+ * cached_local_attention (dream_dllm_hils/local_attention.py:67-200):
+ * key j is visible to the query at position p iff |p - j| <= window.
+ * Keys that fail key_valid, and when inert_chunk > 0 the slots with
+ * (j + 1) % inert_chunk == 0, take zero K and zero V (local_attention.py:35-54):
+ * they stay in the softmax denominator with logit 0 and add nothing to the
+ * output.
+ *   q: bf16 [batch, q_len, q_heads, head_dim];  k: bf16 [batch, kv_len, kv_heads, head_dim]
+ *   v_tiles: output of mrsa_value_tiles for v
+ *   key_valid: optional bool [batch, kv_len];  query_positions: optional int64 [q_len]
+ *   (NULL = query row i sits at position i)
+ *   out: bf16 [batch, q_len, q_heads, head_dim];  lse: fp32 [batch, q_len, q_heads]
+ * Limits: head_dim == 128, q_heads / kv_heads <= 8.
+ */
+int mrsa_local_attention_fwd(const void* q, const void* k, const void* v_tiles,
+                             const uint8_t* key_valid, const int64_t* query_positions,
+                             int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
+                             int64_t kv_heads, int64_t head_dim, int64_t window,
+                             int64_t inert_chunk, float sm_scale, void* out, float* lse,
+                             void* stream);
+
+/*
+ * Routed chunk attention: for each query head, the sum over its routed chunks
+ * of weight * softmax over that chunk's keys (each chunk normalised on its
+ * own), times V.  Replaces HiLS_block_M_head
+ * (ops/hils_fwd_bwd_head.py:1113-1150, forward kernel :190-570) as called by
+ * selected_attention_g7 / selected_attention_g7_cached
+ * (dream_dllm_hils/routing.py:305-472); the formula is the reference's
+ * test_hils_non_power_two_topk.py:122-138.
+ *   q: bf16 [batch, q_len, q_heads, head_dim]; k: bf16 [batch, kv_len, kv_heads, head_dim]
+ *   v_tiles: output of mrsa_value_tiles for v
+ *   weights: bf16 [batch, q_len, q_heads, topk]
+ *   indices: int32 [batch, q_len, kv_heads, topk] (chunk ids; entries < 0 or
+ *            >= kv_len / chunk_size are skipped)
+ *   key_valid: optional bool [batch, kv_len]
+ *   out: bf16 [batch, q_len, q_heads, head_dim]
+ * Limits: chunk_size == 64, head_dim == 128, q_heads / kv_heads <= 8, topk <= 64.
+ */
+int mrsa_selected_attention_fwd(const void* q, const void* k, const void* v_tiles,
+                                const void* weights, const int32_t* indices,
+                                const uint8_t* key_valid, int64_t batch, int64_t q_len,
+                                int64_t kv_len, int64_t q_heads, int64_t kv_heads,
+                                int64_t head_dim, int64_t topk, int64_t chunk_size,
+                                int mask_last_token, float sm_scale, void* out, void* stream);
+
+/*
+ * Per-token candidate scores inside routed chunks: max over the query group of
+ * q.k * sm_scale; -inf for the landmark slot, invalid keys and -1 chunks.
+ * Replaces candidate_token_scores_gqa (ops/hils_token_score_gqa_tilelang.py:174-208).
+ *   scores (out): fp32 [batch, q_len, kv_heads, topk, chunk_size]
+ * Limits: as mrsa_selected_attention_fwd.
+ */
+int mrsa_candidate_token_scores_fwd(const void* q, const void* k, const int32_t* indices,
+                                    const uint8_t* key_valid, int64_t batch, int64_t q_len,
+                                    int64_t kv_len, int64_t q_heads, int64_t kv_heads,
+                                    int64_t head_dim, int64_t topk, int64_t chunk_size,
+                                    float sm_scale, float* scores, void* stream);
+
+/*
+ * Self-test of the matrix-core lane layout every kernel above relies on:
+ * c = a @ b for a = bf16 [16, 32], b = bf16 [32, 16], c = fp32 [16, 16],
+ * computed with one v_mfma_f32_16x16x32_bf16.  No reference counterpart.
+ */
+int mrsa_selftest_mfma_layout(const void* a, const void* b, float* c, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MRSA_H */

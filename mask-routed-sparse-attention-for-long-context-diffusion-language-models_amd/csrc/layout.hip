@@ -1,0 +1,99 @@
+// Layout helpers: the remote-route drop mask and the tiled, transposed V.
+#include "mrsa_device.h"
+
+using namespace mrsa;
+
+namespace {
+
+// drop[b, i, c] = chunk c overlaps the chunk-aligned window of query i, or
+// chunk c has no valid real key (or the packed-sequence mask forbids it).
+// kernel_utils.py:75-99 (bounds) and :102-161 (mask).
+__global__ void __launch_bounds__(256)
+    drop_mask_kernel(const uint8_t* __restrict__ valid, const uint8_t* __restrict__ allowed,
+                     int64_t L, int64_t W, int64_t S, int32_t* __restrict__ out) {
+  extern __shared__ unsigned char chunk_ok[];
+  const int64_t b = blockIdx.y;
+  const int64_t C = L / S;
+  for (int64_t c = threadIdx.x; c < C; c += blockDim.x) {
+    bool any = false;
+    for (int64_t s = 0; s < S - 1; ++s) any |= valid[b * L + c * S + s] != 0;
+    chunk_ok[c] = any;
+  }
+  __syncthreads();
+  const int64_t i0 = (int64_t)blockIdx.x * 64;
+  const int64_t rows = min((int64_t)64, L - i0);
+  for (int64_t e = threadIdx.x; e < rows * C; e += blockDim.x) {
+    const int64_t i = i0 + e / C, c = e % C;
+    const int64_t lc = max(i - W, (int64_t)0) / S;
+    const int64_t rc = min(i + W, L - 1) / S;
+    bool drop = (c >= lc && c <= rc) || !chunk_ok[c];
+    if (allowed) drop = drop || allowed[(b * L + i) * L + c * S + S - 1] == 0;
+    out[(b * L + i) * C + c] = drop ? 1 : 0;
+  }
+}
+
+// v[b, j, h, :] -> v_tiles[b, h, j / 64, :, j % 64]
+__global__ void __launch_bounds__(256)
+    value_tiles_kernel(const uint16_t* __restrict__ v, int64_t L, int64_t H, int D, int64_t NT,
+                       uint16_t* __restrict__ vt) {
+  extern __shared__ uint16_t tile[];  // [64][D + 2]
+  const int64_t t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int pitch = D + 2;
+  const int half = D / 2;
+  for (int e = threadIdx.x; e < 64 * half; e += blockDim.x) {
+    const int s = e / half, d2 = e - s * half;
+    const int64_t j = t * 64 + s;
+    uint32_t w = 0;
+    if (j < L) w = *reinterpret_cast<const uint32_t*>(v + ((b * L + j) * H + h) * D + 2 * d2);
+    tile[s * pitch + 2 * d2] = (uint16_t)(w & 0xffffu);
+    tile[s * pitch + 2 * d2 + 1] = (uint16_t)(w >> 16);
+  }
+  __syncthreads();
+  uint16_t* dst = vt + ((b * H + h) * NT + t) * (int64_t)D * 64;
+  for (int e = threadIdx.x; e < D * 32; e += blockDim.x) {
+    const int d = e >> 5, s2 = e & 31;
+    const uint32_t w = (uint32_t)tile[(2 * s2) * pitch + d] |
+                       ((uint32_t)tile[(2 * s2 + 1) * pitch + d] << 16);
+    *reinterpret_cast<uint32_t*>(dst + d * 64 + 2 * s2) = w;
+  }
+}
+
+}  // namespace
+
+extern "C" int mrsa_remote_drop_mask(const uint8_t* valid_mask, const uint8_t* allowed_mask,
+                                     int64_t batch, int64_t seq_len, int64_t window,
+                                     int64_t chunk_size, int32_t* drop_mask, void* stream) {
+  if (batch < 0 || seq_len <= 0 || window < 0 || chunk_size <= 0 || seq_len % chunk_size != 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (batch == 0) return MRSA_OK;
+  if (!valid_mask || !drop_mask) return MRSA_ERR_INVALID_ARGUMENT;
+  const int64_t C = seq_len / chunk_size;
+  if (C > 60 * 1024 || batch > 65535) return MRSA_ERR_UNSUPPORTED;
+  dim3 grid((unsigned)((seq_len + 63) / 64), (unsigned)batch);
+  hipLaunchKernelGGL(drop_mask_kernel, grid, dim3(256), (size_t)C, (hipStream_t)stream, valid_mask,
+                     allowed_mask, seq_len, window, chunk_size, drop_mask);
+  return mrsa_launch_status();
+}
+
+extern "C" int64_t mrsa_value_tiles_bytes(int64_t batch, int64_t seq_len, int64_t kv_heads,
+                                          int64_t head_dim) {
+  if (batch < 0 || seq_len < 0 || kv_heads < 0 || head_dim < 0) return -1;
+  return batch * kv_heads * ((seq_len + 63) / 64) * head_dim * 64 * 2;
+}
+
+extern "C" int mrsa_value_tiles(const void* v, int64_t batch, int64_t seq_len, int64_t kv_heads,
+                                int64_t head_dim, void* v_tiles, void* stream) {
+  if (batch < 0 || seq_len < 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 ||
+      head_dim > 256)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (batch == 0 || seq_len == 0) return MRSA_OK;
+  if (!v || !v_tiles || (uintptr_t)v % 4 != 0 || (uintptr_t)v_tiles % 4 != 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (kv_heads > 65535 || batch > 65535) return MRSA_ERR_UNSUPPORTED;
+  const int64_t NT = (seq_len + 63) / 64;
+  const size_t smem = (size_t)64 * (head_dim + 2) * 2;
+  hipLaunchKernelGGL(value_tiles_kernel, dim3((unsigned)NT, (unsigned)kv_heads, (unsigned)batch),
+                     dim3(256), smem, (hipStream_t)stream, (const uint16_t*)v, seq_len, kv_heads,
+                     (int)head_dim, NT, (uint16_t*)v_tiles);
+  return mrsa_launch_status();
+}

@@ -1,0 +1,129 @@
+// Device-side helpers shared by every MRSA kernel (gfx950 / CDNA4 only).
+//
+// Storage conventions used across the library:
+//   * bf16 tensors are passed as raw uint16_t bit patterns; arithmetic is done
+//     in fp32 after widening, and results are narrowed with round-to-nearest-
+//     even (the rounding torch's .to(torch.bfloat16) uses).
+//   * MFMA operands for v_mfma_f32_16x16x32_bf16 are 8 bf16 values (16 bytes)
+//     per lane.  Lane l supplies row (l % 16) of A and column (l % 16) of B;
+//     lane group (l / 16) supplies one quarter of the 32-deep reduction.  The
+//     16x16 fp32 result lands as C[4 * (l / 16) + i][l % 16], i = 0..3.
+//     Only the M/N placement and the C layout matter for correctness: any
+//     assignment of reduction indices to (lane group, element) is fine as long
+//     as A and B use the same one, which every kernel here guarantees.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "mrsa.h"
+
+namespace mrsa {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// fp32 -> bf16 bits, round to nearest even, NaN kept quiet.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+}
+
+__device__ __forceinline__ f32x4_t mfma_bf16_16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4_t zero4() {
+  f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+  return z;
+}
+
+// Butterfly reductions inside groups of 16 lanes (lanes sharing l / 16).
+__device__ __forceinline__ float group16_max(float v) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float group16_sum(float v) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int group16_sum_i(int v) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+// Reductions across the four lane groups (lanes sharing l % 16).
+__device__ __forceinline__ float across4_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+__device__ __forceinline__ float across4_sum(float v) {
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v = min(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Order-preserving map from fp32 to uint32 (larger float -> larger key).
+__device__ __forceinline__ uint32_t float_order_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// torch.logaddexp for fp32 scalars: both -inf -> -inf.
+__device__ __forceinline__ float logaddexp_f(float a, float b) {
+  float m = fmaxf(a, b);
+  if (m == neg_inf()) return m;
+  return m + log1pf(expf(-fabsf(a - b)));
+}
+
+}  // namespace mrsa
+
+// Host helpers for launch-status mapping.
+static inline int mrsa_launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MRSA_OK : MRSA_ERR_LAUNCH;
+}

@@ -1,0 +1,154 @@
+// Landmark (mask-token) chunk-summary attention pool.
+//
+// One workgroup per (chunk, KV head).  The chunk's keys are staged in LDS once
+// and shared by the `groups` query heads of that KV group.  Semantics follow
+// the fused reference kernel ops/chunk_attn_pool_gqa_tilelang.py:47-180:
+//   * the chunk counts as valid iff any of its first chunk_size-1 keys is valid
+//     (:94-99);
+//   * logits = (mu_q . k) * sm_scale over the chunk_size-1 real keys; a masked
+//     slot gets -inf, except slot 0, which gets logit 0 (:118-129);
+//   * probabilities are normalised in fp32; the entropy -sum p ln p uses the
+//     fp32 probabilities (:142-149), the pooled key uses them rounded to bf16
+//     (P_shared is bf16, :151-158), accumulated in fp32 and rounded to bf16;
+//   * an invalid chunk writes zero keys and zero entropy (:161-178).
+// With dense_torch_semantics the compiled torch twin _compact_pool_torch
+// (:17-37) is followed instead: every masked slot is -inf, a fully masked
+// chunk gives zero probabilities (nan_to_num) and the pooling uses fp32
+// probabilities.
+#include "mrsa_device.h"
+
+using namespace mrsa;
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__global__ void __launch_bounds__(kThreads)
+    pool_kernel(const uint16_t* __restrict__ mu_q, const uint16_t* __restrict__ kc,
+                const uint8_t* __restrict__ key_valid, int S, int H, int G, int D,
+                float sm_scale, int dense, const float* __restrict__ bias_scale,
+                uint16_t* __restrict__ lmk, float* __restrict__ entropy,
+                float* __restrict__ prior) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int64_t bc = blockIdx.x;
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+
+  uint16_t* ks = reinterpret_cast<uint16_t*>(smem);    // [S][D] bf16
+  float* qs = reinterpret_cast<float*>(ks + S * D);     // [G][D]
+  float* ps = qs + G * D;                               // [G][S] logits -> probabilities
+  float* pw = ps + G * S;                               // [G][S] pooling weights
+  int* flag = reinterpret_cast<int*>(pw + G * S);
+  unsigned char* vs = reinterpret_cast<unsigned char*>(flag + 1);  // [S]
+
+  const int vec_per_row = D / 8;
+  for (int v = tid; v < S * vec_per_row; v += kThreads) {
+    const int s = v / vec_per_row, c = v - s * vec_per_row;
+    const u32x4_t* src =
+        reinterpret_cast<const u32x4_t*>(kc + ((bc * S + s) * H + h) * (int64_t)D) + c;
+    reinterpret_cast<u32x4_t*>(ks + s * D)[c] = *src;
+  }
+  for (int e = tid; e < G * D; e += kThreads)
+    qs[e] = bf16_to_f32(mu_q[((bc * H + h) * G) * (int64_t)D + e]);
+  if (tid == 0) flag[0] = 0;
+  for (int s = tid; s < S; s += kThreads) vs[s] = key_valid[bc * S + s] != 0;
+  __syncthreads();
+  if (tid < S - 1 && vs[tid]) flag[0] = 1;
+  __syncthreads();
+  const bool chunk_valid = flag[0] != 0;
+
+  // Logits: each thread owns (g, s) pairs; the start of the reduction over d
+  // is staggered by s so neighbouring threads hit different LDS banks.
+  for (int p = tid; p < G * S; p += kThreads) {
+    const int g = p / S, s = p - g * S;
+    const float* qr = qs + g * D;
+    const uint16_t* kr = ks + s * D;
+    int d = (s * 8) % D;
+    float acc = 0.f;
+    for (int i = 0; i < D; i += 2) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(kr + d);
+      acc = fmaf(qr[d], bf16_lo(w), acc);
+      acc = fmaf(qr[d + 1], bf16_hi(w), acc);
+      d += 2;
+      if (d >= D) d -= D;
+    }
+    const bool real = (s < S - 1) && vs[s];
+    float logit;
+    if (dense) {
+      logit = real ? acc * sm_scale : neg_inf();
+    } else {
+      logit = (real && chunk_valid) ? acc * sm_scale : (s == 0 ? 0.f : neg_inf());
+    }
+    ps[p] = logit;
+  }
+  __syncthreads();
+
+  // Softmax + entropy per query head: one wave per head.
+  for (int g = wave; g < G; g += kThreads / 64) {
+    const float v0 = lane < S ? ps[g * S + lane] : neg_inf();
+    const float v1 = lane + 64 < S ? ps[g * S + lane + 64] : neg_inf();
+    const float m = wave_max(fmaxf(v0, v1));
+    float e0 = 0.f, e1 = 0.f;
+    if (m != neg_inf()) {
+      e0 = (lane < S && v0 != neg_inf()) ? exp2f((v0 - m) * kLog2e) : 0.f;
+      e1 = (lane + 64 < S && v1 != neg_inf()) ? exp2f((v1 - m) * kLog2e) : 0.f;
+    }
+    const float sum = wave_sum(e0 + e1);
+    const float p0 = sum > 0.f ? e0 / sum : 0.f;
+    const float p1 = sum > 0.f ? e1 / sum : 0.f;
+    const float t = (p0 > 0.f ? p0 * logf(p0) : 0.f) + (p1 > 0.f ? p1 * logf(p1) : 0.f);
+    const float ent = -wave_sum(t);
+    if (lane < S) pw[g * S + lane] = dense ? p0 : bf16_to_f32(f32_to_bf16(p0));
+    if (lane + 64 < S) pw[g * S + lane + 64] = dense ? p1 : bf16_to_f32(f32_to_bf16(p1));
+    if (lane == 0) {
+      const float e_out = (dense || chunk_valid) ? ent : 0.f;
+      const int64_t o = (bc * H + h) * G + g;
+      entropy[o] = e_out;
+      if (prior) prior[o] = e_out * bias_scale[h * G + g];
+    }
+  }
+  __syncthreads();
+
+  // Pooled key: lmk[g][d] = sum_s w[g][s] * k[s][d], fp32 accumulation.
+  for (int p = tid; p < G * D; p += kThreads) {
+    const int g = p / D, d = p - g * D;
+    const float* wr = pw + g * S;
+    float acc = 0.f;
+    for (int s = 0; s < S; ++s) acc = fmaf(wr[s], bf16_to_f32(ks[s * D + d]), acc);
+    if (!dense && !chunk_valid) acc = 0.f;
+    lmk[((bc * H + h) * G) * (int64_t)D + p] = (uint16_t)f32_to_bf16(acc);
+  }
+}
+
+}  // namespace
+
+extern "C" int mrsa_chunk_attn_pool_gqa_fwd(const void* mu_q, const void* k_chunked,
+                                            const uint8_t* key_valid, int64_t batch_chunks,
+                                            int64_t chunk_size, int64_t kv_heads, int64_t groups,
+                                            int64_t head_dim, float sm_scale,
+                                            int dense_torch_semantics, const float* bias_scale,
+                                            void* landmark_keys, float* entropy,
+                                            float* prior_bias, void* stream) {
+  if (batch_chunks < 0 || chunk_size < 2 || chunk_size > 128 || kv_heads <= 0 || groups <= 0 ||
+      groups > 16 || head_dim <= 0 || head_dim > 256 || head_dim % 8 != 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if ((prior_bias != nullptr) != (bias_scale != nullptr)) return MRSA_ERR_INVALID_ARGUMENT;
+  if (batch_chunks == 0) return MRSA_OK;
+  if (!mu_q || !k_chunked || !key_valid || !landmark_keys || !entropy)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if ((uintptr_t)k_chunked % 16 != 0) return MRSA_ERR_INVALID_ARGUMENT;
+  if (batch_chunks > 0x7fffffff || kv_heads > 65535) return MRSA_ERR_UNSUPPORTED;
+  const int S = (int)chunk_size, G = (int)groups, D = (int)head_dim;
+  const size_t smem = (size_t)S * D * 2 + (size_t)G * D * 4 + 2 * (size_t)G * S * 4 + 4 + S;
+  if (smem > 64 * 1024) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&pool_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+      return MRSA_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL(pool_kernel, dim3((unsigned)batch_chunks, (unsigned)kv_heads), dim3(kThreads),
+                     smem, (hipStream_t)stream, (const uint16_t*)mu_q, (const uint16_t*)k_chunked,
+                     key_valid, S, (int)kv_heads, G, D, sm_scale, dense_torch_semantics, bias_scale,
+                     (uint16_t*)landmark_keys, entropy, prior_bias);
+  return mrsa_launch_status();
+}

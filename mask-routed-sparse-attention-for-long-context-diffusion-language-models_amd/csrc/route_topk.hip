@@ -1,0 +1,732 @@
+// Route scoring and per-KV-group top-k chunk selection.
+//
+// Semantics follow ref_softmax_topk_max_pooling (ops/topk_head_softmax.py:15-156):
+//   s[q,g,c]     = (q[q,g] . lmk[c,g]) * sm_scale        (causal-masked -> -inf)
+//   x[q,g,c]     = s + bias[c,g]
+//   post_softmax: y = x - logaddexp(lse_local[q,g], logsumexp_c x[q,g,:])
+//   pre_softmax:  y = x
+//   score[q,c]   = max_g y ; dropped chunks -> -inf
+//   top-k over c; -inf picks become -1; indices sorted ascending with -1 last;
+//   returned scores are s (no bias) at the picked chunks for every g.
+// The logsumexp runs over every chunk, dropped ones included.  Ties in the
+// selection score go to the lower chunk index (the rule of the reference's
+// fused selection kernel, topk_head_softmax.py:614-626).
+//
+// Fast path (route_topk_mfma_kernel): head_dim 128, chunks <= 256, bf16
+// scores.  A workgroup holds 64 queries of one KV head (16 per wave).  For
+// each query head g the landmark keys of that head are staged in LDS and the
+// 16x256 logit tile of every wave is computed on the matrix cores, reduced to
+// the head's LSE and folded into the running max over heads.  The logits of
+// every head stay in registers as bf16 so the selection can emit them without
+// recomputation.  The 32nd-largest score of each row is found by bisection on
+// order-preserving integer keys; exact ties at the threshold are broken by
+// chunk index.
+//
+// General path (route_topk_generic_kernel): one workgroup per (token, KV head)
+// with scalar dot products; any head_dim / chunk count that fits LDS.
+#include <utility>
+
+#include "mrsa_device.h"
+
+using namespace mrsa;
+
+namespace {
+
+struct RouteArgs {
+  const uint16_t* q;
+  const uint16_t* lmk;
+  const float* lse;
+  const float* bias;
+  const int32_t* drop;
+  const uint8_t* key_valid;
+  int64_t derive_window;
+  int64_t B, L, C;
+  int Hkv, G, D, K;
+  int64_t block_size;
+  int per_head_lmk;
+  int is_causal;
+  int64_t window_size;
+  int64_t q_offset;
+  int pre_softmax;
+  float sm_scale;
+  int32_t* indices;
+  void* scores;
+  int scores_fp32;
+};
+
+__device__ __forceinline__ int64_t floor_div(int64_t a, int64_t b) {
+  int64_t q = a / b;
+  if ((a % b != 0) && ((a < 0) != (b < 0))) --q;
+  return q;
+}
+
+// First chunk index hidden by the causal mask for query row r (global offset applied).
+__device__ __forceinline__ int64_t causal_limit(const RouteArgs& a, int64_t r) {
+  const int64_t tq = r + a.q_offset;
+  if (a.window_size > 0) return floor_div(tq - a.window_size + 1, a.block_size);
+  return floor_div(tq, a.block_size);
+}
+
+__device__ __forceinline__ const uint16_t* lmk_row(const RouteArgs& a, int64_t b, int64_t c, int h,
+                                                   int g) {
+  if (a.per_head_lmk) return a.lmk + ((b * a.C + c) * (int64_t)(a.Hkv * a.G) + h * a.G + g) * a.D;
+  return a.lmk + ((b * a.C + c) * (int64_t)a.Hkv + h) * a.D;
+}
+
+// ---------------------------------------------------------------------------
+// Fast path.
+// ---------------------------------------------------------------------------
+constexpr int kFastThreads = 512;  // 8 waves: 4 query groups x 2 chunk halves
+constexpr int kFastQ = 64;         // queries per workgroup
+constexpr int kNT = 8;             // chunk tiles of 16 per wave (128 chunks)
+constexpr int kLmkPitch = 136;     // bf16 elements per staged landmark row (128 + 8 pad)
+
+struct FastLayout {
+  static constexpr size_t lmk = 0;                          // [256][136] bf16, later [64][256] f32
+  static constexpr size_t bias = 256 * kLmkPitch * 2;       // [256] f32
+  static constexpr size_t cbad = bias + 256 * 4;            // [256] u8
+  static constexpr size_t red_max = cbad + 256;             // [2][64] f32
+  static constexpr size_t red_sum = red_max + 2 * 64 * 4;   // [2][64] f32
+  static constexpr size_t slot = red_sum + 2 * 64 * 4;      // [64][256] i8
+  static constexpr size_t total = slot + 64 * 256;
+};
+
+template <int G>
+__global__ void __launch_bounds__(kFastThreads, 2) route_topk_mfma_kernel(RouteArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* lmk_s = reinterpret_cast<uint16_t*>(smem + FastLayout::lmk);
+  float* Ms = reinterpret_cast<float*>(smem + FastLayout::lmk);  // after the head loop
+  float* bias_s = reinterpret_cast<float*>(smem + FastLayout::bias);
+  unsigned char* cbad = smem + FastLayout::cbad;
+  float* red_max = reinterpret_cast<float*>(smem + FastLayout::red_max);
+  float* red_sum = reinterpret_cast<float*>(smem + FastLayout::red_sum);
+  int8_t* slot_s = reinterpret_cast<int8_t*>(smem + FastLayout::slot);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int qg = wave & 3, half = wave >> 2;
+  const int64_t b = blockIdx.z;
+  const int h = blockIdx.y;
+  const int64_t q0 = (int64_t)blockIdx.x * kFastQ;
+  const int64_t qbase = q0 + 16 * qg;
+  const int64_t qa = qbase + col;  // the A-operand row this lane supplies
+  const int64_t L = a.L, C = a.C;
+  const int K = a.K;
+  const int cbase = 128 * half;
+  const uint16_t* qb_base = a.q + b * L * (int64_t)(a.Hkv * G * 128);
+  const float* lse_base = a.pre_softmax ? nullptr : a.lse + b * L * (int64_t)(a.Hkv * G);
+
+  if (a.derive_window >= 0) {
+    for (int c = tid; c < 256; c += kFastThreads) {
+      bool any = false;
+      if (c < C) {
+        if (a.key_valid) {
+          const uint8_t* kv = a.key_valid + b * L + (int64_t)c * a.block_size;
+          for (int64_t s = 0; s < a.block_size - 1; ++s) any |= kv[s] != 0;
+        } else {
+          any = a.block_size > 1;
+        }
+      }
+      cbad[c] = !any;
+    }
+  }
+
+  float M[kNT][4];
+  uint32_t raw[G][kNT][2];
+#pragma unroll
+  for (int t = 0; t < kNT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) M[t][i] = neg_inf();
+
+  // One pass per query head; instantiated per compile-time g so raw[g] is
+  // indexed statically.
+  auto head_pass = [&](auto gc) {
+    constexpr int g = decltype(gc)::value;
+    __syncthreads();
+#pragma unroll 2
+    for (int v = tid; v < 256 * 16; v += kFastThreads) {
+      const int c = v >> 4, part = v & 15;
+      u32x4_t val = {0u, 0u, 0u, 0u};
+      if (c < C) val = reinterpret_cast<const u32x4_t*>(lmk_row(a, b, c, h, g))[part];
+      *reinterpret_cast<u32x4_t*>(lmk_s + c * kLmkPitch + part * 8) = val;
+    }
+    if (tid < 256) bias_s[tid] = (a.bias && tid < C) ? a.bias[((b * C + tid) * a.Hkv + h) * G + g] : 0.f;
+    __syncthreads();
+
+    u32x4_t A[4];
+    const uint16_t* qrow = qb_base + (uint32_t)((((int)qa * a.Hkv + h) * G + g) * 128 + 8 * grp);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      u32x4_t z = {0u, 0u, 0u, 0u};
+      A[j] = z;
+      if (qa < L) A[j] = *reinterpret_cast<const u32x4_t*>(qrow + 32 * j);
+    }
+    f32x4_t S[kNT];
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) {
+      f32x4_t acc = zero4();
+      const uint16_t* brow = lmk_s + (cbase + 16 * t + col) * kLmkPitch + 8 * grp;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const u32x4_t B = *reinterpret_cast<const u32x4_t*>(brow + 32 * j);
+        acc = mfma_bf16_16x16x32(A[j], B, acc);
+      }
+      S[t] = acc;
+    }
+
+    // Raw scaled logits (kept as bf16) and biased logits (in S).
+    float rmax[4] = {neg_inf(), neg_inf(), neg_inf(), neg_inf()};
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) {
+      const int c = cbase + 16 * t + col;
+      float xs[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float x = S[t][i] * a.sm_scale;
+        if (c >= C) x = neg_inf();
+        xs[i] = x;
+        const float xb = x + bias_s[c];
+        S[t][i] = xb;
+        rmax[i] = fmaxf(rmax[i], xb);
+      }
+      raw[g][t][0] = pack_bf16x2(xs[0], xs[1]);
+      raw[g][t][1] = pack_bf16x2(xs[2], xs[3]);
+    }
+    // Row LSE over both chunk halves (exchanged through LDS).
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      rmax[i] = group16_max(rmax[i]);
+      if (col == 0) red_max[half * 64 + 16 * qg + 4 * grp + i] = rmax[i];
+    }
+    __syncthreads();
+    float m[4], ssum[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * qg + 4 * grp + i;
+      m[i] = fmaxf(red_max[row], red_max[64 + row]);
+      float s = 0.f;
+      if (m[i] != neg_inf()) {
+#pragma unroll
+        for (int t = 0; t < kNT; ++t) s += expf(S[t][i] - m[i]);
+      }
+      ssum[i] = group16_sum(s);
+      if (col == 0) red_sum[half * 64 + row] = ssum[i];
+    }
+    __syncthreads();
+    float tot[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t r = qbase + 4 * grp + i;
+      const int row = 16 * qg + 4 * grp + i;
+      const float s = red_sum[row] + red_sum[64 + row];
+      const float lse_h = (m[i] == neg_inf()) ? m[i] : m[i] + logf(s);
+      const float lv = (!a.pre_softmax && r < L) ? lse_base[((int)r * a.Hkv + h) * G + g] : 0.f;
+      tot[i] = a.pre_softmax ? 0.f : logaddexp_f(lv, lse_h);
+    }
+#pragma unroll
+    for (int t = 0; t < kNT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float xb = S[t][i];
+        const float y = (xb == neg_inf()) ? xb : xb - tot[i];
+        M[t][i] = fmaxf(M[t][i], y);
+      }
+  };
+  [&]<int... gs>(std::integer_sequence<int, gs...>) {
+    (head_pass(std::integral_constant<int, gs>{}), ...);
+  }(std::make_integer_sequence<int, G>{});
+
+  // Dropped chunks, then the selection scores go to LDS (row-major [64][256]).
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t r = qbase + 4 * grp + i;
+    int64_t lc = 0, rc = -1;
+    if (a.derive_window >= 0 && r < L) {
+      lc = max(r - a.derive_window, (int64_t)0) / a.block_size;
+      rc = min(r + a.derive_window, L - 1) / a.block_size;
+    }
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) {
+      const int c = cbase + 16 * t + col;
+      bool dropped = (c >= C) || (r >= L);
+      if (!dropped) {
+        if (a.derive_window >= 0)
+          dropped = (c >= lc && c <= rc) || cbad[c];
+        else if (a.drop)
+          dropped = a.drop[(b * L + r) * C + c] != 0;
+      }
+      Ms[(16 * qg + 4 * grp + i) * 256 + c] = dropped ? neg_inf() : M[t][i];
+    }
+  }
+  __syncthreads();
+
+  // Selection: wave w handles rows 8w..8w+7, eight lanes per row, each lane
+  // owning the 32 consecutive chunks 32*sub .. 32*sub+31.
+  {
+    const int row = 8 * wave + (lane >> 3);
+    const int sub = lane & 7;
+    const int64_t r = q0 + row;
+    uint32_t key[32];
+#pragma unroll
+    for (int e = 0; e < 32; e += 4) {
+      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(Ms + row * 256 + 32 * sub + e);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) key[e + u] = float_order_key(v[u]);
+    }
+    const uint32_t kNeg = float_order_key(neg_inf());
+    int nfin = 0;
+    uint32_t kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+    for (int e = 0; e < 32; ++e)
+      if (key[e] > kNeg) {
+        ++nfin;
+        kmin = min(kmin, key[e]);
+        kmax = max(kmax, key[e]);
+      }
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+      nfin += __shfl_xor(nfin, o, 64);
+      kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, 64));
+      kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, 64));
+    }
+    uint32_t thr_hi, thr_tie = 0u, lo = kmin, hi = kmax + 1u;
+    int need = 0;
+    bool done;
+    if (nfin <= K) {
+      thr_hi = kNeg + 1u;
+      done = true;
+    } else {
+      thr_hi = 0u;
+      done = false;
+    }
+    for (int it = 0; it < 40; ++it) {
+      if (!__any(!done)) break;
+      const uint32_t mid = lo + ((hi - lo) >> 1);
+      int cnt = 0;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) cnt += key[e] >= mid ? 1 : 0;
+#pragma unroll
+      for (int o = 1; o < 8; o <<= 1) cnt += __shfl_xor(cnt, o, 64);
+      if (!done) {
+        if (hi - lo <= 1u) {
+          done = true;
+        } else if (cnt == K) {
+          thr_hi = mid;
+          done = true;
+        } else if (cnt > K) {
+          lo = mid;
+        } else {
+          hi = mid;
+        }
+      }
+    }
+    if (thr_hi == 0u) {
+      int cnt_hi = 0;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) cnt_hi += key[e] >= hi ? 1 : 0;
+#pragma unroll
+      for (int o = 1; o < 8; o <<= 1) cnt_hi += __shfl_xor(cnt_hi, o, 64);
+      thr_hi = hi;
+      thr_tie = lo;
+      need = K - cnt_hi;
+    }
+    // Exclusive prefix over the 8 lanes of the row (chunk order == lane order).
+    auto excl8 = [&](int v) {
+      int incl = v;
+#pragma unroll
+      for (int o = 1; o < 8; o <<= 1) {
+        const int up = __shfl_up(incl, o, 8);
+        if (sub >= o) incl += up;
+      }
+      return incl - v;
+    };
+    int my_ties = 0;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) my_ties += (need > 0 && key[e] == thr_tie) ? 1 : 0;
+    int tie_rank = excl8(my_ties);
+    int my_picks = 0;
+    uint32_t pickbits = 0u;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const bool tie = need > 0 && key[e] == thr_tie;
+      const bool pick = key[e] >= thr_hi || (tie && tie_rank < need);
+      if (tie) ++tie_rank;
+      if (pick) {
+        pickbits |= 1u << e;
+        ++my_picks;
+      }
+    }
+    int slot = excl8(my_picks);
+    int total = my_picks;
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) total += __shfl_xor(total, o, 64);
+    const int64_t orow = (b * L + r) * a.Hkv + h;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const bool pick = (pickbits >> e) & 1u;
+      slot_s[row * 256 + 32 * sub + e] = pick ? (int8_t)slot : (int8_t)-1;
+      if (pick && r < L) a.indices[orow * K + slot] = 32 * sub + e;
+      slot += pick ? 1 : 0;
+    }
+    if (r < L) {
+      uint16_t* sc16 = reinterpret_cast<uint16_t*>(a.scores);
+      for (int s = total + sub; s < K; s += 8) {
+        a.indices[orow * K + s] = -1;
+#pragma unroll
+        for (int g = 0; g < G; ++g) sc16[(orow * G + g) * K + s] = 0xff80u;  // -inf
+      }
+    }
+  }
+  __syncthreads();
+
+  // Raw logits of every head at the picked chunks.
+  uint16_t* sc16 = reinterpret_cast<uint16_t*>(a.scores);
+#pragma unroll
+  for (int t = 0; t < kNT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * qg + 4 * grp + i;
+      const int c = cbase + 16 * t + col;
+      const int slot = slot_s[row * 256 + c];
+      const int64_t r = q0 + row;
+      if (slot >= 0 && r < L) {
+        const int64_t orow = (b * L + r) * a.Hkv + h;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          sc16[(orow * G + g) * K + slot] = (uint16_t)((raw[g][t][i >> 1] >> (16 * (i & 1))) & 0xffffu);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// General path.
+// ---------------------------------------------------------------------------
+constexpr int kGenThreads = 256;
+
+__device__ __forceinline__ float block_reduce_max(float v, float* red) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < kGenThreads / 64; ++w) r = fmaxf(r, red[w]);
+  return r;
+}
+__device__ __forceinline__ float block_reduce_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = 0.f;
+  for (int w = 0; w < kGenThreads / 64; ++w) r += red[w];
+  return r;
+}
+__device__ __forceinline__ int block_reduce_sum_i(int v, int* red) {
+  v = wave_sum_i(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  int r = 0;
+  for (int w = 0; w < kGenThreads / 64; ++w) r += red[w];
+  return r;
+}
+// Exclusive prefix sum over the block (thread order), plus the total.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* scratch, int* total) {
+  const int tid = threadIdx.x;
+  __syncthreads();
+  scratch[tid] = v;
+  __syncthreads();
+  for (int o = 1; o < kGenThreads; o <<= 1) {
+    const int add = tid >= o ? scratch[tid - o] : 0;
+    __syncthreads();
+    scratch[tid] += add;
+    __syncthreads();
+  }
+  const int incl = scratch[tid];
+  *total = scratch[kGenThreads - 1];
+  __syncthreads();
+  return incl - v;
+}
+
+__global__ void __launch_bounds__(kGenThreads) route_topk_generic_kernel(RouteArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int64_t C = a.C, L = a.L;
+  const int G = a.G, D = a.D, K = a.K;
+  float* raw = reinterpret_cast<float*>(smem);  // [G][C]
+  float* Ms = raw + (int64_t)G * C;             // [C]
+  float* qs = Ms + C;                           // [G][D]
+  float* tot = qs + G * D;                      // [G]
+  float* redf = tot + G;                        // [8]
+  int* redi = reinterpret_cast<int*>(redf + 8);  // [8]
+  int* scan = redi + 8;                          // [256]
+
+  const int tid = threadIdx.x;
+  const int64_t r = blockIdx.x;
+  const int h = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  for (int e = tid; e < G * D; e += kGenThreads) {
+    const int g = e / D, d = e - g * D;
+    qs[e] = bf16_to_f32(a.q[(((b * L + r) * a.Hkv + h) * G + g) * D + d]);
+  }
+  __syncthreads();
+  const int64_t climit = a.is_causal ? causal_limit(a, r) : C;
+  for (int64_t p = tid; p < (int64_t)G * C; p += kGenThreads) {
+    const int g = (int)(p / C);
+    const int64_t c = p - (int64_t)g * C;
+    const uint16_t* kr = lmk_row(a, b, c, h, g);
+    const float* qr = qs + g * D;
+    float acc = 0.f;
+    for (int d = 0; d < D; ++d) acc = fmaf(qr[d], bf16_to_f32(kr[d]), acc);
+    float x = acc * a.sm_scale;
+    if (c >= climit) x = neg_inf();
+    raw[p] = x;
+  }
+  __syncthreads();
+  for (int g = 0; g < G; ++g) {
+    float m = neg_inf();
+    for (int64_t c = tid; c < C; c += kGenThreads) {
+      const float bv = a.bias ? a.bias[((b * C + c) * a.Hkv + h) * G + g] : 0.f;
+      m = fmaxf(m, raw[(int64_t)g * C + c] + bv);
+    }
+    m = block_reduce_max(m, redf);
+    float s = 0.f;
+    if (m != neg_inf())
+      for (int64_t c = tid; c < C; c += kGenThreads) {
+        const float bv = a.bias ? a.bias[((b * C + c) * a.Hkv + h) * G + g] : 0.f;
+        s += expf(raw[(int64_t)g * C + c] + bv - m);
+      }
+    s = block_reduce_sum(s, redf);
+    if (tid == 0) {
+      const float lse_h = (m == neg_inf()) ? m : m + logf(s);
+      const float lv = a.pre_softmax ? 0.f : a.lse[((b * L + r) * a.Hkv + h) * G + g];
+      tot[g] = a.pre_softmax ? 0.f : logaddexp_f(lv, lse_h);
+    }
+  }
+  __syncthreads();
+  int64_t lc = 0, rc = -1;
+  if (a.derive_window >= 0) {
+    lc = max(r - a.derive_window, (int64_t)0) / a.block_size;
+    rc = min(r + a.derive_window, L - 1) / a.block_size;
+  }
+  for (int64_t c = tid; c < C; c += kGenThreads) {
+    float best = neg_inf();
+    for (int g = 0; g < G; ++g) {
+      const float bv = a.bias ? a.bias[((b * C + c) * a.Hkv + h) * G + g] : 0.f;
+      const float xb = raw[(int64_t)g * C + c] + bv;
+      best = fmaxf(best, xb == neg_inf() ? xb : xb - tot[g]);
+    }
+    bool dropped = false;
+    if (a.derive_window >= 0) {
+      bool any = false;
+      if (a.key_valid) {
+        const uint8_t* kv = a.key_valid + b * L + c * a.block_size;
+        for (int64_t s = 0; s < a.block_size - 1; ++s) any |= kv[s] != 0;
+      } else {
+        any = a.block_size > 1;
+      }
+      dropped = (c >= lc && c <= rc) || !any;
+    } else if (a.drop) {
+      dropped = a.drop[(b * L + r) * C + c] != 0;
+    }
+    Ms[c] = dropped ? neg_inf() : best;
+  }
+  __syncthreads();
+
+  // Threshold search on order keys (block-wide counts).
+  const uint32_t kNeg = float_order_key(neg_inf());
+  int nfin = 0;
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
+  for (int64_t c = tid; c < C; c += kGenThreads) {
+    const uint32_t key = float_order_key(Ms[c]);
+    if (key > kNeg) {
+      ++nfin;
+      kmin = min(kmin, key);
+      kmax = max(kmax, key);
+    }
+  }
+  nfin = block_reduce_sum_i(nfin, redi);
+  // min / max through float reductions on the key bits is not order-safe;
+  // reduce the keys as ints instead.
+  {
+    int vmin = (int)(kmin ^ 0x80000000u), vmax = (int)(kmax ^ 0x80000000u);
+    for (int o = 1; o < 64; o <<= 1) {
+      vmin = min(vmin, __shfl_xor(vmin, o, 64));
+      vmax = max(vmax, __shfl_xor(vmax, o, 64));
+    }
+    __syncthreads();
+    if ((tid & 63) == 0) {
+      redi[tid >> 6] = vmin;
+      redi[4 + (tid >> 6)] = vmax;
+    }
+    __syncthreads();
+    for (int w = 1; w < 4; ++w) {
+      vmin = min(vmin, redi[w]);
+      vmax = max(vmax, redi[4 + w]);
+    }
+    vmin = min(vmin, redi[0]);
+    vmax = max(vmax, redi[4]);
+    kmin = (uint32_t)vmin ^ 0x80000000u;
+    kmax = (uint32_t)vmax ^ 0x80000000u;
+  }
+  uint32_t thr_hi, thr_tie = 0u;
+  int need = 0;
+  if (nfin <= K) {
+    thr_hi = kNeg + 1u;
+  } else {
+    uint32_t lo = kmin, hi = kmax + 1u;
+    bool exact = false;
+    thr_hi = 0u;
+    while (hi - lo > 1u) {
+      const uint32_t mid = lo + ((hi - lo) >> 1);
+      int cnt = 0;
+      for (int64_t c = tid; c < C; c += kGenThreads) cnt += float_order_key(Ms[c]) >= mid ? 1 : 0;
+      cnt = block_reduce_sum_i(cnt, redi);
+      if (cnt == K) {
+        thr_hi = mid;
+        exact = true;
+        break;
+      }
+      if (cnt > K) lo = mid; else hi = mid;
+    }
+    if (!exact) {
+      int cnt_hi = 0;
+      for (int64_t c = tid; c < C; c += kGenThreads) cnt_hi += float_order_key(Ms[c]) >= hi ? 1 : 0;
+      cnt_hi = block_reduce_sum_i(cnt_hi, redi);
+      thr_hi = hi;
+      thr_tie = lo;
+      need = K - cnt_hi;
+    }
+  }
+
+  // Each thread owns a contiguous chunk range; scan counts for slots / tie ranks.
+  const int64_t per = (C + kGenThreads - 1) / kGenThreads;
+  const int64_t c0 = tid * per, c1 = min(C, c0 + per);
+  int my_ties = 0;
+  for (int64_t c = c0; c < c1; ++c) my_ties += (need > 0 && float_order_key(Ms[c]) == thr_tie) ? 1 : 0;
+  int total_ties;
+  int tie_base = block_exclusive_scan(my_ties, scan, &total_ties);
+  int my_picks = 0;
+  {
+    int tr = tie_base;
+    for (int64_t c = c0; c < c1; ++c) {
+      const uint32_t key = float_order_key(Ms[c]);
+      const bool tie = need > 0 && key == thr_tie;
+      const bool pick = key >= thr_hi || (tie && tr < need);
+      if (tie) ++tr;
+      my_picks += pick ? 1 : 0;
+    }
+  }
+  int total_picks;
+  int slot = block_exclusive_scan(my_picks, scan, &total_picks);
+  const int64_t row = (b * L + r) * a.Hkv + h;
+  {
+    int tr = tie_base;
+    for (int64_t c = c0; c < c1; ++c) {
+      const uint32_t key = float_order_key(Ms[c]);
+      const bool tie = need > 0 && key == thr_tie;
+      const bool pick = key >= thr_hi || (tie && tr < need);
+      if (tie) ++tr;
+      if (pick) {
+        a.indices[row * K + slot] = (int32_t)c;
+        for (int g = 0; g < G; ++g) {
+          const float v = raw[(int64_t)g * C + c];
+          if (a.scores_fp32)
+            reinterpret_cast<float*>(a.scores)[(row * G + g) * K + slot] = v;
+          else
+            reinterpret_cast<uint16_t*>(a.scores)[(row * G + g) * K + slot] = (uint16_t)f32_to_bf16(v);
+        }
+        ++slot;
+      }
+    }
+  }
+  for (int s = total_picks + tid; s < K; s += kGenThreads) {
+    a.indices[row * K + s] = -1;
+    for (int g = 0; g < G; ++g) {
+      if (a.scores_fp32)
+        reinterpret_cast<float*>(a.scores)[(row * G + g) * K + s] = neg_inf();
+      else
+        reinterpret_cast<uint16_t*>(a.scores)[(row * G + g) * K + s] = 0xff80u;
+    }
+  }
+}
+
+template <int G>
+int launch_fast(const RouteArgs& a, hipStream_t s) {
+  const size_t smem = FastLayout::total;
+  auto kern = route_topk_mfma_kernel<G>;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+    return MRSA_ERR_LAUNCH;
+  dim3 grid((unsigned)((a.L + kFastQ - 1) / kFastQ), (unsigned)a.Hkv, (unsigned)a.B);
+  hipLaunchKernelGGL(kern, grid, dim3(kFastThreads), smem, s, a);
+  return mrsa_launch_status();
+}
+
+}  // namespace
+
+extern "C" int mrsa_route_topk_fwd(const void* q, const void* lmk, const float* lse_local,
+                                   const float* bias, const int32_t* drop_mask,
+                                   const uint8_t* key_valid, int64_t derive_window, int64_t batch,
+                                   int64_t seq_len, int64_t chunks, int64_t kv_heads,
+                                   int64_t groups, int64_t head_dim, int64_t topk,
+                                   int64_t block_size, int per_head_lmk, int is_causal,
+                                   int64_t window_size, int64_t q_offset, int selection_mode,
+                                   float sm_scale, int32_t* indices, void* scores,
+                                   int scores_fp32, void* stream) {
+  if (batch < 0 || seq_len < 0 || chunks <= 0 || kv_heads <= 0 || groups <= 0 ||
+      head_dim <= 0 || topk <= 0 || block_size <= 0 || (selection_mode != 0 && selection_mode != 1))
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (batch == 0 || seq_len == 0) return MRSA_OK;
+  if (!q || !lmk || !indices || !scores) return MRSA_ERR_INVALID_ARGUMENT;
+  if (selection_mode == 0 && !lse_local) return MRSA_ERR_INVALID_ARGUMENT;
+  if (derive_window >= 0 && chunks * block_size != seq_len) return MRSA_ERR_INVALID_ARGUMENT;
+  if (kv_heads > 65535 || batch > 65535) return MRSA_ERR_UNSUPPORTED;
+
+  RouteArgs a;
+  a.q = (const uint16_t*)q;
+  a.lmk = (const uint16_t*)lmk;
+  a.lse = lse_local;
+  a.bias = bias;
+  a.drop = drop_mask;
+  a.key_valid = key_valid;
+  a.derive_window = derive_window;
+  a.B = batch;
+  a.L = seq_len;
+  a.C = chunks;
+  a.Hkv = (int)kv_heads;
+  a.G = (int)groups;
+  a.D = (int)head_dim;
+  a.K = (int)topk;
+  a.block_size = block_size;
+  a.per_head_lmk = per_head_lmk;
+  a.is_causal = is_causal;
+  a.window_size = window_size;
+  a.q_offset = q_offset;
+  a.pre_softmax = selection_mode;
+  a.sm_scale = sm_scale;
+  a.indices = indices;
+  a.scores = scores;
+  a.scores_fp32 = scores_fp32;
+  hipStream_t s = (hipStream_t)stream;
+
+  const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)lmk % 16 == 0);
+  const bool fast = !scores_fp32 && !is_causal && head_dim == 128 &&
+                    seq_len * kv_heads * groups * head_dim < ((int64_t)1 << 31) && chunks <= 256 && topk <= 127 && aligned &&
+                    (groups == 7 || groups == 8);
+  if (fast) return groups == 7 ? launch_fast<7>(a, s) : launch_fast<8>(a, s);
+  const size_t smem = ((size_t)groups * chunks + chunks + groups * head_dim + groups + 16) * 4 +
+                      kGenThreads * 4;
+  if (smem > 150 * 1024) return MRSA_ERR_UNSUPPORTED;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(&route_topk_generic_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+    return MRSA_ERR_LAUNCH;
+  if (seq_len > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
+  dim3 grid((unsigned)seq_len, (unsigned)kv_heads, (unsigned)batch);
+  hipLaunchKernelGGL(route_topk_generic_kernel, grid, dim3(kGenThreads), smem, s, a);
+  return mrsa_launch_status();
+}

@@ -1,0 +1,128 @@
+"""ctypes binding of libmrsa.so, the gfx950 C-ABI library (include/mrsa.h).
+
+The library is loaded lazily, from this directory only.  If it is missing or
+cannot be loaded every op raises immediately: there is no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmrsa.so")
+
+MRSA_OK = 0
+MRSA_ERR_INVALID_ARGUMENT = 1
+MRSA_ERR_UNSUPPORTED = 2
+MRSA_ERR_LAUNCH = 3
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> (restype, argtypes); mirrors include/mrsa.h exactly.
+SIGNATURES = {
+    "mrsa_status_string": (ctypes.c_char_p, [_I]),
+    "mrsa_abi_version": (_I, []),
+    "mrsa_fuse_hils_outputs_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _P]),
+    "mrsa_chunk_attn_pool_gqa_fwd": (
+        _I,
+        [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _P, _P, _P, _P, _P],
+    ),
+    "mrsa_remote_drop_mask": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P, _P]),
+    "mrsa_route_topk_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+         _I64, _I, _I, _I64, _I64, _I, _F, _P, _P, _I, _P],
+    ),
+    "mrsa_route_weights_fwd": (
+        _I,
+        [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _F, _I, _F,
+         _P, _P, _P],
+    ),
+    "mrsa_value_tiles_bytes": (_I64, [_I64, _I64, _I64, _I64]),
+    "mrsa_value_tiles": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P]),
+    "mrsa_local_attention_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F,
+         _P, _P, _P],
+    ),
+    "mrsa_selected_attention_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+         _I, _F, _P, _P],
+    ),
+    "mrsa_candidate_token_scores_fwd": (
+        _I,
+        [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P],
+    ),
+    "mrsa_selftest_mfma_layout": (_I, [_P, _P, _P, _P]),
+}
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+
+
+class MrsaLibraryError(RuntimeError):
+    """libmrsa.so is missing or unusable."""
+
+
+def load() -> ctypes.CDLL:
+    """Load libmrsa.so (once) and attach the C signatures."""
+
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise MrsaLibraryError(
+                f"{LIB_PATH} not found: build it first (python -c "
+                "'import __graft_entry__ as g; g.build()' from the repository root)"
+            )
+        try:
+            lib = ctypes.CDLL(LIB_PATH)
+        except OSError as exc:  # pragma: no cover - environment failure
+            raise MrsaLibraryError(f"cannot load {LIB_PATH}: {exc}") from exc
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+        return lib
+
+
+def status_string(status: int) -> str:
+    return load().mrsa_status_string(int(status)).decode()
+
+
+def check(status: int, op: str) -> None:
+    """Map a C status to the reference's Python exception convention."""
+
+    if status == MRSA_OK:
+        return
+    msg = f"{op}: {status_string(status)} (status {status})"
+    if status in (MRSA_ERR_INVALID_ARGUMENT, MRSA_ERR_UNSUPPORTED):
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """Handle of the current HIP stream of the tensor's device."""
+
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def call(name: str, *args) -> int:
+    return getattr(load(), name)(*args)

@@ -1,0 +1,60 @@
+"""Output fusion: ``remote + local_weight * local``.
+
+Drop-in for ``ops.hils_bidir_output_fusion_tilelang.fuse_hils_outputs``
+(ops/hils_bidir_output_fusion_tilelang.py:138-148); forward only.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _validate(remote_output, local_output, local_weight):
+    # ops/hils_bidir_output_fusion_tilelang.py:103-135
+    if remote_output.device.type != "cuda":
+        raise ValueError("fuse_hils_outputs requires CUDA tensors")
+    if not (remote_output.device == local_output.device == local_weight.device):
+        raise ValueError("all fusion tensors must share one CUDA device")
+    if remote_output.ndim != 4 or local_output.shape != remote_output.shape:
+        raise ValueError(
+            "remote_output and local_output must have the same [B,L,H,D] shape"
+        )
+    if local_weight.shape != remote_output.shape[:-1]:
+        raise ValueError(
+            f"local_weight shape {tuple(local_weight.shape)} must equal "
+            f"{tuple(remote_output.shape[:-1])}"
+        )
+    if remote_output.shape[-1] > 256:
+        raise ValueError(f"head_dim must be <= 256, got {remote_output.shape[-1]}")
+    if not (
+        remote_output.dtype == local_output.dtype == local_weight.dtype == torch.bfloat16
+    ):
+        raise ValueError("fuse_hils_outputs requires BF16 tensors")
+    if not (
+        remote_output.is_contiguous()
+        and local_output.is_contiguous()
+        and local_weight.is_contiguous()
+    ):
+        raise ValueError("fuse_hils_outputs requires contiguous tensors")
+
+
+def fuse_hils_outputs(
+    remote_output: torch.Tensor,
+    local_output: torch.Tensor,
+    local_weight: torch.Tensor,
+) -> torch.Tensor:
+    """Add the weighted local branch to the already weighted remote branch."""
+
+    _validate(remote_output, local_output, local_weight)
+    out = torch.empty_like(remote_output)
+    head_dim = remote_output.shape[-1]
+    rows = remote_output.numel() // max(head_dim, 1)
+    st = _lib.call(
+        "mrsa_fuse_hils_outputs_fwd",
+        _lib.ptr(remote_output), _lib.ptr(local_output), _lib.ptr(local_weight),
+        _lib.ptr(out), rows, head_dim, _lib.stream_of(out),
+    )
+    _lib.check(st, "fuse_hils_outputs")
+    return out

@@ -1,0 +1,149 @@
+"""Bidirectional window attention with natural-log LSE.
+
+Drop-ins for ``bidir_local_attention`` and ``cached_local_attention``
+(dream_dllm_hils/local_attention.py:110-200).  Where the reference zeroes K
+and V of inert slots and calls flash-attn with window_size=(W, W), the gfx950
+kernel applies the same zero-K / zero-V rule while it streams the keys.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Tuple
+
+import torch
+
+from . import _lib
+from .sparse_attention import value_tiles
+
+
+def _validate_layout(q, k, v, key_valid) -> None:
+    # local_attention.py:15-32
+    if q.device.type != "cuda":
+        raise ValueError("local attention requires CUDA tensors")
+    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("local attention requires BF16 q, k, and v")
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, and v must have BLHD layout")
+    batch, seq_len, h_q, dim = q.shape
+    if k.shape[0] != batch or v.shape != k.shape:
+        raise ValueError(f"q/k/v batch mismatch: {q.shape}, {k.shape}, {v.shape}")
+    if k.shape[-1] != dim or h_q % k.shape[2] != 0:
+        raise ValueError("query heads must be divisible by KV heads with equal head_dim")
+    if key_valid.shape[0] != batch or key_valid.shape[-1] != k.shape[1]:
+        raise ValueError(
+            f"key_valid must have shape {(batch, k.shape[1])}, got {tuple(key_valid.shape)}"
+        )
+
+
+def _flash_window(window: int, skip_inert_slots: bool, chunk_size: int) -> int:
+    # local_attention.py:57-64
+    if skip_inert_slots:
+        return int(window + chunk_size - 1)
+    return int(window)
+
+
+def local_attention_launch(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v_tiles: torch.Tensor,
+    key_valid: torch.Tensor | None,
+    flash_window: int,
+    inert_chunk: int,
+    *,
+    query_positions: torch.Tensor | None = None,
+    sm_scale: float | None = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    B, Lq, Hq, D = q.shape
+    Lk, Hkv = k.shape[1], k.shape[2]
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    qc = q.contiguous()
+    kc = k.contiguous()
+    kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
+    pos = None
+    if query_positions is not None:
+        pos = query_positions.to(device=q.device, dtype=torch.int64).contiguous()
+    out = torch.empty(B, Lq, Hq, D, dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty(B, Lq, Hq, dtype=torch.float32, device=q.device)
+    st = _lib.call(
+        "mrsa_local_attention_fwd",
+        _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(kv), _lib.ptr(pos),
+        B, Lq, Lk, Hq, Hkv, D, int(flash_window), int(inert_chunk), float(sm_scale),
+        _lib.ptr(out), _lib.ptr(lse), _lib.stream_of(qc),
+    )
+    _lib.check(st, "local_attention")
+    return out, lse
+
+
+def bidir_local_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    key_valid: torch.Tensor,
+    window: int,
+    chunk_size: int,
+    allowed_mask: torch.Tensor | None = None,
+    skip_inert_slots: bool = False,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Bidirectional local GQA attention and natural-log LSE [B, L, Hq]."""
+
+    _validate_layout(q, k, v, key_valid)
+    seq_len = q.shape[1]
+    if k.shape[1] != seq_len:
+        raise ValueError("prefill local attention requires equal Q/K lengths")
+    if window < 0 or chunk_size <= 0 or seq_len % chunk_size != 0:
+        raise ValueError(
+            f"invalid window/chunk layout: L={seq_len}, W={window}, S={chunk_size}"
+        )
+    if allowed_mask is not None:
+        raise ValueError(
+            "bidir_local_attention only accepts 2D key_valid; "
+            "do not pass a dense L×L allowed_mask"
+        )
+    return local_attention_launch(
+        q, k, value_tiles(v), key_valid,
+        _flash_window(window, skip_inert_slots, chunk_size),
+        chunk_size if skip_inert_slots else 0,
+    )
+
+
+def cached_local_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    key_valid: torch.Tensor,
+    query_positions: torch.Tensor,
+    window: int,
+    chunk_size: int,
+    skip_inert_slots: bool = False,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Fast-dLLM query rows against a windowed K/V cache (local_attention.py:147-200)."""
+
+    _validate_layout(q, k, v, key_valid)
+    batch, query_len, h_q, dim = q.shape
+    seq_len = k.shape[1]
+    if query_positions.shape != (query_len,):
+        raise ValueError(
+            f"query_positions must have shape {(query_len,)}, "
+            f"got {tuple(query_positions.shape)}"
+        )
+    if query_positions.device != q.device or query_positions.dtype != torch.long:
+        raise ValueError("query_positions must be CUDA torch.long")
+    if query_len == 0:
+        empty_lse = q.new_empty((batch, 0, h_q), dtype=torch.float32)
+        return q.new_empty((batch, 0, h_q, dim)), empty_lse
+    if torch.unique(query_positions).numel() != query_len:
+        raise ValueError("query_positions must be unique")
+    if bool(((query_positions < 0) | (query_positions >= seq_len)).any()):
+        raise ValueError("query_positions must be in cache range")
+    if window < 0 or chunk_size <= 0 or seq_len % chunk_size:
+        raise ValueError(
+            f"invalid window/chunk layout: L={seq_len}, W={window}, S={chunk_size}"
+        )
+    return local_attention_launch(
+        q, k, value_tiles(v), key_valid,
+        _flash_window(window, skip_inert_slots, chunk_size),
+        chunk_size if skip_inert_slots else 0,
+        query_positions=query_positions,
+    )

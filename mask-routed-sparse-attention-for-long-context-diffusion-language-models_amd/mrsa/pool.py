@@ -1,0 +1,104 @@
+"""Landmark chunk-summary attention pool.
+
+Drop-in for ``ops.chunk_attn_pool_gqa_tilelang.chunk_attn_pool_gqa``
+(ops/chunk_attn_pool_gqa_tilelang.py:425-448).  Same arguments, validation
+messages and outputs; forward only.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+
+def _validate(mu_q, k_chunked, key_valid):
+    # ops/chunk_attn_pool_gqa_tilelang.py:404-422
+    if mu_q.device.type != "cuda":
+        raise ValueError("chunk_attn_pool_gqa requires CUDA tensors")
+    if mu_q.dtype != torch.bfloat16 or k_chunked.dtype != torch.bfloat16:
+        raise ValueError("chunk_attn_pool_gqa requires BF16 mu_q and K")
+    if mu_q.ndim != 5 or k_chunked.ndim != 5:
+        raise ValueError("mu_q and k_chunked must be 5D")
+    batch, chunks, kv_heads, groups, head_dim = mu_q.shape
+    expected_k = (batch, chunks, k_chunked.shape[2], kv_heads, head_dim)
+    if k_chunked.shape != expected_k:
+        raise ValueError(
+            f"expected compact K shape {expected_k}, got {tuple(k_chunked.shape)}"
+        )
+    if key_valid.shape != (batch, chunks, k_chunked.shape[2]):
+        raise ValueError(f"invalid key_valid shape {tuple(key_valid.shape)}")
+    if groups > 16:
+        raise ValueError(f"groups must be <= 16, got {groups}")
+
+
+def _launch(mu_q, k_chunked, key_valid, sm_scale, bias_scale=None):
+    batch, chunks, kv_heads, groups, head_dim = mu_q.shape
+    chunk_size = k_chunked.shape[2]
+    mu = mu_q.contiguous()
+    kc = k_chunked.contiguous()
+    kv = key_valid.to(device=mu_q.device, dtype=torch.bool).contiguous()
+    lmk = torch.empty_like(mu)
+    entropy = torch.empty(
+        batch, chunks, kv_heads, groups, device=mu.device, dtype=torch.float32
+    )
+    prior = None
+    scale = None
+    if bias_scale is not None:
+        scale = bias_scale.to(device=mu.device, dtype=torch.float32).contiguous()
+        if scale.numel() != kv_heads * groups:
+            raise ValueError(
+                f"bias_scale must have {kv_heads * groups} elements, got {scale.numel()}"
+            )
+        prior = torch.empty_like(entropy)
+    st = _lib.call(
+        "mrsa_chunk_attn_pool_gqa_fwd",
+        _lib.ptr(mu), _lib.ptr(kc), _lib.ptr(kv),
+        batch * chunks, chunk_size, kv_heads, groups, head_dim,
+        float(sm_scale), 1 if groups == 1 else 0,
+        _lib.ptr(scale), _lib.ptr(lmk), _lib.ptr(entropy), _lib.ptr(prior),
+        _lib.stream_of(mu),
+    )
+    _lib.check(st, "chunk_attn_pool_gqa")
+    return lmk, entropy, prior
+
+
+def chunk_attn_pool_gqa(
+    mu_q: torch.Tensor,
+    k_chunked: torch.Tensor,
+    key_valid: torch.Tensor,
+    sm_scale: float | None = None,
+):
+    """Pool compact per-KV-head chunks into per-query-head summaries.
+
+    mu_q [B, C, Hkv, G, D] bf16, k_chunked [B, C, S, Hkv, D] bf16,
+    key_valid [B, C, S] -> (landmark_keys [B, C, Hkv, G, D] bf16,
+    entropy [B, C, Hkv, G] fp32).
+    """
+
+    _validate(mu_q, k_chunked, key_valid)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(mu_q.shape[-1])
+    lmk, entropy, _ = _launch(mu_q, k_chunked, key_valid, sm_scale)
+    return lmk, entropy
+
+
+def chunk_attn_pool_gqa_prior(
+    mu_q: torch.Tensor,
+    k_chunked: torch.Tensor,
+    key_valid: torch.Tensor,
+    entropy_bias_scale: torch.Tensor,
+    sm_scale: float | None = None,
+):
+    """chunk_attn_pool_gqa plus prior_bias = entropy * entropy_bias_scale.
+
+    The product of attention.py:1425-1430 is written by the same kernel.
+    Returns (landmark_keys, entropy, prior_bias).
+    """
+
+    _validate(mu_q, k_chunked, key_valid)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(mu_q.shape[-1])
+    return _launch(mu_q, k_chunked, key_valid, sm_scale, entropy_bias_scale)

@@ -1,0 +1,151 @@
+"""The MRSA route-layer and SWA-layer attention cores on gfx950.
+
+``route_attention`` is the part of ``KernelDreamFullHiLSAttention.forward``
+(dream_dllm_hils/attention.py:1380-1774) between the q/k/v projections and
+o_proj, for the inference configuration the layer ships with (no Gumbel, no
+token budget, fusion weights from the affine gate at topk >= 32):
+
+    local branch   bidir_local_attention(window W + S - 1, landmark K/V zeroed)
+    landmarks      chunk_attn_pool_gqa on the routing query at each landmark slot
+    prior          entropy * entropy_bias_scale
+    routing        route_topk_g7 with remote_drop_mask(key_valid, W, S)
+    weights        _route_weights_torch (affine gate)
+    remote branch  selected_attention_g7
+    output         fuse_hils_outputs(remote, local, local_weight)
+
+``swa_attention`` is ``KernelDreamSlidingWindowAttention.forward``
+(attention.py:1168-1220) between projections and o_proj.
+
+Everything runs on the library's kernels on the current stream; the drop mask
+is derived inside the route kernel instead of being materialised, and V is
+re-laid out once for both attention kernels.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from .fusion import fuse_hils_outputs
+from .local_attention import local_attention_launch
+from .pool import chunk_attn_pool_gqa_prior
+from .route_weights import route_weights_launch
+from .sparse_attention import selected_attention_launch, value_tiles
+from .topk import route_topk_launch
+
+
+@dataclass
+class RouteLayerConfig:
+    """Route-layer hyper-parameters (canonical values of
+    configs/from_dense16k/hils-s2-qcal-rmsnorm-rand-s1000-jingneng.json)."""
+
+    local_window: int = 256
+    chunk_size: int = 64
+    topk: int = 32
+    temperature: float = 1.0
+    gate_offset: float | None = 0.0   # fusion_gate_offset at init (attention.py:913)
+    gate_scale: float | None = 1.0    # fusion_gate_scale at init (attention.py:914)
+    skip_inert_slots: bool = True     # attention.py:902
+
+
+def _check_qkv(q, k, v, route_q):
+    if q.device.type != "cuda":
+        raise ValueError("route attention requires CUDA tensors")
+    for name, t in (("q", q), ("k", k), ("v", v), ("route_q", route_q)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bf16")
+        if t.ndim != 4:
+            raise ValueError(f"{name} must be [B, L, H, D]")
+    if route_q.shape != q.shape:
+        raise ValueError("route_q must have the shape of q")
+    if k.shape != v.shape or k.shape[:2] != q.shape[:2] or k.shape[-1] != q.shape[-1]:
+        raise ValueError(f"incompatible q/k/v shapes {q.shape}, {k.shape}, {v.shape}")
+    if q.shape[2] % k.shape[2]:
+        raise ValueError("query heads must be a multiple of KV heads")
+
+
+def route_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    route_q: torch.Tensor,
+    entropy_bias_scale: torch.Tensor,
+    key_valid: torch.Tensor | None = None,
+    cfg: RouteLayerConfig = RouteLayerConfig(),
+    return_intermediates: bool = False,
+):
+    """Route-layer attention: q, route_q [B, L, Hq, D], k, v [B, L, Hkv, D] bf16.
+
+    Returns the fused output [B, L, Hq, D] bf16 (and a dict of the stage
+    outputs when return_intermediates).
+    """
+
+    _check_qkv(q, k, v, route_q)
+    B, L, Hq, D = q.shape
+    Hkv = k.shape[2]
+    G = Hq // Hkv
+    S = cfg.chunk_size
+    if L % S:
+        raise ValueError(f"sequence length {L} must be divisible by chunk_size={S}")
+    C = L // S
+    if key_valid is None:
+        kv_bool = torch.ones(B, L, dtype=torch.bool, device=q.device)
+    else:
+        kv_bool = key_valid.to(device=q.device, dtype=torch.bool).contiguous()
+
+    vt = value_tiles(v)
+    flash_window = cfg.local_window + S - 1 if cfg.skip_inert_slots else cfg.local_window
+    local_out, local_lse = local_attention_launch(
+        q, k, vt, kv_bool, flash_window, S if cfg.skip_inert_slots else 0
+    )
+    q_lmk = route_q[:, S - 1 :: S].reshape(B, C, Hkv, G, D)
+    k_chunked = k.reshape(B, C, S, Hkv, D)
+    lmk, entropy, prior = chunk_attn_pool_gqa_prior(
+        q_lmk, k_chunked, kv_bool.reshape(B, C, S), entropy_bias_scale
+    )
+    indices, scores = route_topk_launch(
+        route_q.reshape(B, L, Hkv, G, D),
+        lmk.reshape(B, C, Hq, D),
+        local_lse.reshape(B, L, Hkv, G),
+        cfg.topk,
+        S,
+        bias4=prior,
+        derive_window=cfg.local_window,
+        key_valid=kv_bool,
+    )
+    scores = scores.reshape(B, L, Hq, cfg.topk)
+    remote_w, local_w = route_weights_launch(
+        scores, indices, prior, local_lse, temperature=cfg.temperature,
+        gate_offset=cfg.gate_offset, gate_scale=cfg.gate_scale,
+    )
+    remote_out = selected_attention_launch(q, k, vt, remote_w, indices, kv_bool, S)
+    out = fuse_hils_outputs(remote_out, local_out, local_w)
+    if not return_intermediates:
+        return out
+    return out, {
+        "local_output": local_out, "local_lse": local_lse, "landmark_keys": lmk,
+        "entropy": entropy, "prior_bias": prior, "indices": indices, "scores": scores,
+        "remote_weights": remote_w, "local_weight": local_w, "remote_output": remote_out,
+    }
+
+
+def swa_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    key_valid: torch.Tensor | None = None,
+    window: int = 1280,
+    chunk_size: int = 64,
+    skip_inert_slots: bool = False,
+) -> torch.Tensor:
+    """Sliding-window layer attention (radius ``window``); [B, L, Hq, D] bf16."""
+
+    if q.device.type != "cuda" or q.dtype != torch.bfloat16:
+        raise ValueError("swa_attention requires CUDA bf16 tensors")
+    flash_window = window + chunk_size - 1 if skip_inert_slots else window
+    out, _ = local_attention_launch(
+        q, k, value_tiles(v), key_valid, flash_window,
+        chunk_size if skip_inert_slots else 0,
+    )
+    return out

@@ -1,0 +1,140 @@
+"""Dream G=7 routing adapters.
+
+Drop-ins for dream_dllm_hils/routing.py: ``route_topk_g7`` (:52-302),
+``selected_attention_g7`` (:305-328) and ``selected_attention_g7_cached``
+(:331-353).  The gfx950 kernels take the logical G=7 head layout directly,
+so the physical-G=8 padding of the reference is not needed.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .sparse_attention import selected_attention_launch, value_tiles
+from .topk import route_topk_launch
+
+_LOGICAL_G = 7
+
+
+def route_topk_g7(
+    q: torch.Tensor,
+    lmks: torch.Tensor,
+    local_lse: torch.Tensor,
+    prior_bias: torch.Tensor,
+    drop_mask: torch.Tensor,
+    topk: int,
+    chunk_size: int,
+    window: int,
+    *,
+    training: bool = True,
+    use_gumbel: bool = False,
+    gumbel_scale: float = 1.0,
+    return_selected_gumbel: bool = False,
+    selection_mode: str = "post_softmax",
+):
+    """Route logical G=7 query heads; same validation and outputs as the reference.
+
+    Returns (indices [B, L, Hkv, topk], scores [B, L, Hq, topk] bf16).  As in
+    the reference, inference (training=False) indices are int64 and training
+    indices int32.
+    """
+
+    if q.ndim != 4 or lmks.ndim != 5:
+        raise ValueError(
+            f"expected q [B,L,Hq,D] and lmks [B,C,Hkv,7,D], got "
+            f"{tuple(q.shape)} and {tuple(lmks.shape)}"
+        )
+    batch, seq_len, h_q, dim = q.shape
+    if lmks.shape[0] != batch or lmks.shape[3:] != (_LOGICAL_G, dim):
+        raise ValueError(f"invalid landmark shape {tuple(lmks.shape)} for q {tuple(q.shape)}")
+    chunks, h_kv = lmks.shape[1:3]
+    if h_q != h_kv * _LOGICAL_G:
+        raise ValueError(f"expected {h_kv * _LOGICAL_G} query heads, got {h_q}")
+    if local_lse.shape != (batch, seq_len, h_kv, _LOGICAL_G):
+        raise ValueError(f"invalid local_lse shape {tuple(local_lse.shape)}")
+    if prior_bias.shape != (batch, chunks, h_kv, _LOGICAL_G):
+        raise ValueError(f"invalid prior_bias shape {tuple(prior_bias.shape)}")
+    if drop_mask.shape != (batch, seq_len, chunks):
+        raise ValueError(f"invalid drop_mask shape {tuple(drop_mask.shape)}")
+    if topk <= 0:
+        raise ValueError(f"topk must be positive, got {topk}")
+    if gumbel_scale < 0:
+        raise ValueError(f"gumbel_scale must be non-negative, got {gumbel_scale}")
+    if selection_mode not in {"post_softmax", "pre_softmax"}:
+        raise ValueError(f"unsupported selection_mode={selection_mode}")
+    if bool(use_gumbel) and bool(training) and gumbel_scale > 0:
+        raise ValueError("Gumbel route sampling is training-only; not supported by the forward kernels")
+
+    indices, scores = route_topk_launch(
+        q.reshape(batch, seq_len, h_kv, _LOGICAL_G, dim),
+        lmks.reshape(batch, chunks, h_q, dim),
+        local_lse,
+        topk,
+        chunk_size,
+        bias4=prior_bias,
+        drop_mask=drop_mask,
+        selection_mode=selection_mode,
+    )
+    scores = scores.reshape(batch, seq_len, h_q, topk).to(q.dtype)
+    if not training:
+        indices = indices.to(torch.int64)
+    if return_selected_gumbel:
+        return indices, scores, None
+    return indices, scores
+
+
+def _validate_selected(q, k, v, weights, indices, key_valid, chunk_size, token_keep):
+    # dream_dllm_hils/routing.py:368-425
+    if q.ndim != 4 or k.ndim != 4:
+        raise ValueError(
+            f"q and k must be BLHD tensors, got {tuple(q.shape)} and {tuple(k.shape)}"
+        )
+    batch, query_len, h_q, dim = q.shape
+    if k.shape[0] != batch or k.shape[-1] != dim:
+        raise ValueError(f"incompatible q/k shapes {tuple(q.shape)} and {tuple(k.shape)}")
+    kv_len, h_kv = k.shape[1:3]
+    if h_q != h_kv * _LOGICAL_G:
+        raise ValueError(f"Dream G7 requires h_q == 7 * h_kv, got h_q={h_q}, h_kv={h_kv}")
+    if v.shape != k.shape:
+        raise ValueError(f"v shape {tuple(v.shape)} must match k shape {tuple(k.shape)}")
+    selected = indices.shape[-1]
+    if indices.shape != (batch, query_len, h_kv, selected):
+        raise ValueError(f"invalid indices shape {tuple(indices.shape)}")
+    if weights.shape != (batch, query_len, h_q, selected):
+        raise ValueError(f"invalid weights shape {tuple(weights.shape)}")
+    if key_valid.shape != (batch, kv_len):
+        raise ValueError(f"invalid key_valid shape {tuple(key_valid.shape)}")
+    if token_keep is not None:
+        raise ValueError("token_keep (token-level refinement) is not supported yet")
+    if kv_len % chunk_size != 0:
+        raise ValueError(f"cache length {kv_len} must be divisible by chunk_size={chunk_size}")
+    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("selected attention requires BF16 q, k, and v")
+    if q.device != k.device or v.device != q.device:
+        raise ValueError("q, k, and v must share a device")
+    if weights.device != q.device or indices.device != q.device:
+        raise ValueError("weights and indices must share the q device")
+    if key_valid.device != q.device:
+        raise ValueError("key_valid must share the q device")
+    if selected <= 0:
+        raise ValueError("selected attention requires at least one chunk slot")
+
+
+def selected_attention_g7(q, k, v, weights, indices, key_valid, chunk_size, training,
+                          token_keep=None):
+    """Selected-chunk attention with compact KV (routing.py:305-328); forward only."""
+
+    _validate_selected(q, k, v, weights, indices, key_valid, chunk_size, token_keep)
+    return selected_attention_launch(
+        q, k, value_tiles(v), weights, indices, key_valid, chunk_size, mask_last_token=True
+    )
+
+
+def selected_attention_g7_cached(q, k, v, weights, indices, key_valid, chunk_size,
+                                 token_keep=None):
+    """Partial queries against a full compact-GQA cache (routing.py:331-353)."""
+
+    _validate_selected(q, k, v, weights, indices, key_valid, chunk_size, token_keep)
+    return selected_attention_launch(
+        q, k, value_tiles(v), weights, indices, key_valid, chunk_size, mask_last_token=True
+    )

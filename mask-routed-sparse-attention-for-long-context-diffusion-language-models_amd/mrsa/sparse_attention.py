@@ -1,0 +1,96 @@
+"""Routed chunk attention (and the tiled V layout it reads).
+
+Drop-in for ``ops.hils_fwd_bwd_head.HiLS_block_M_head``
+(ops/hils_fwd_bwd_head.py:1113-1150) in its forward role, plus
+``value_tiles``, the V re-layout both attention kernels consume.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+
+def value_tiles(v: torch.Tensor) -> torch.Tensor:
+    """V [B, L, Hkv, D] bf16 -> 64-key tiles stored transposed [B, Hkv, ceil(L/64), D, 64]."""
+
+    if v.device.type != "cuda" or v.dtype != torch.bfloat16 or v.ndim != 4:
+        raise ValueError("value_tiles requires a CUDA BF16 [B, L, Hkv, D] tensor")
+    B, L, H, D = v.shape
+    vc = v.contiguous()
+    out = torch.empty(B, H, (L + 63) // 64, D, 64, dtype=torch.bfloat16, device=v.device)
+    st = _lib.call("mrsa_value_tiles", _lib.ptr(vc), B, L, H, D, _lib.ptr(out), _lib.stream_of(vc))
+    _lib.check(st, "value_tiles")
+    return out
+
+
+def selected_attention_launch(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v_tiles: torch.Tensor,
+    weights: torch.Tensor,
+    indices: torch.Tensor,
+    key_valid: torch.Tensor | None,
+    chunk_size: int,
+    *,
+    mask_last_token: bool = True,
+    sm_scale: float | None = None,
+) -> torch.Tensor:
+    """q [B, Lq, Hq, D], k [B, Lk, Hkv, D], weights [B, Lq, Hq, K] -> [B, Lq, Hq, D] bf16."""
+
+    B, Lq, Hq, D = q.shape
+    Lk, Hkv = k.shape[1], k.shape[2]
+    K = indices.shape[-1]
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    qc = q.contiguous()
+    kc = k.contiguous()
+    w = weights.to(torch.bfloat16).contiguous()
+    idx = indices.to(torch.int32).contiguous()
+    kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
+    out = torch.empty(B, Lq, Hq, D, dtype=torch.bfloat16, device=q.device)
+    st = _lib.call(
+        "mrsa_selected_attention_fwd",
+        _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(w), _lib.ptr(idx), _lib.ptr(kv),
+        B, Lq, Lk, Hq, Hkv, D, K, int(chunk_size), 1 if mask_last_token else 0,
+        float(sm_scale), _lib.ptr(out), _lib.stream_of(qc),
+    )
+    _lib.check(st, "selected_attention")
+    return out
+
+
+def HiLS_block_M_head(
+    q, k, v, weights, indices,
+    block_size=64, sm_scale=None, block_M=None,
+    mask_last_token=True, dtype="bfloat16", accum_dtype="float",
+    num_threads=None, num_threads_fwd=None, num_threads_bwd=None,
+    is_training=True, slope=None, key_valid=None, token_keep=None,
+):
+    """Same arguments as ops/hils_fwd_bwd_head.py:1113-1150, forward only.
+
+    Tiling knobs (block_M, num_threads*) are accepted and ignored: the gfx950
+    kernel picks its own tiling.  ALiBi slopes and token_keep are not
+    supported.
+    """
+
+    B, L, HQ, D = q.shape
+    _, L_kv, H, Dk = k.shape
+    assert D == Dk, f"Q head_dim ({D}) must equal K head_dim ({Dk})"
+    assert HQ % H == 0, f"HQ={HQ} must be divisible by H={H}"
+    if slope is not None:
+        raise ValueError("ALiBi slopes are not supported by the gfx950 routed-attention kernel")
+    if token_keep is not None:
+        raise ValueError("token_keep (token-level refinement) is not supported yet")
+    if dtype != "bfloat16" or accum_dtype != "float":
+        raise ValueError("only bf16 inputs with fp32 accumulation are supported")
+    if key_valid is not None and key_valid.shape != (B, L_kv):
+        raise ValueError(f"key_valid must have shape {(B, L_kv)}, got {tuple(key_valid.shape)}")
+    if any(t.requires_grad for t in (q, k, v, weights)) and torch.is_grad_enabled():
+        raise ValueError("HiLS_block_M_head on gfx950 is forward-only (no autograd)")
+    return selected_attention_launch(
+        q, k, value_tiles(v), weights, indices, key_valid, block_size,
+        mask_last_token=mask_last_token, sm_scale=sm_scale,
+    )

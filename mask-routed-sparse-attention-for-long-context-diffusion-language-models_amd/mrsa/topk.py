@@ -1,0 +1,199 @@
+"""Route scoring with per-KV-group top-k ("softmax then max pooling").
+
+Drop-ins for ``ops.topk_head_softmax.ref_softmax_topk_max_pooling``
+(ops/topk_head_softmax.py:15-156) and ``online_softmax_topk_head``
+(:1242-1415).  Both run the gfx950 route kernel (mrsa_route_topk_fwd).
+Gumbel noise is a training-time input and is not supported here.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from .kernel_utils import group_pad_to
+
+
+def route_topk_launch(
+    q5: torch.Tensor,
+    lmks: torch.Tensor,
+    lse4: torch.Tensor | None,
+    topk: int,
+    block_size: int,
+    *,
+    bias4: torch.Tensor | None = None,
+    drop_mask: torch.Tensor | None = None,
+    derive_window: int = -1,
+    key_valid: torch.Tensor | None = None,
+    is_causal: bool = False,
+    window_size: int = 0,
+    q_offset: int = 0,
+    selection_mode: str = "post_softmax",
+    sm_scale: float | None = None,
+    scores_fp32: bool = False,
+):
+    """Run the route kernel.
+
+    q5 [B, L, Hkv, G, D] bf16; lmks [B, C, Hkv*G, D] (per-head) or
+    [B, C, Hkv, D] (shared) bf16; lse4 [B, L, Hkv, G] fp32; bias4
+    [B, C, Hkv, G] fp32; drop_mask [B, L, C].  With derive_window >= 0 the
+    drop mask of remote_drop_mask(key_valid, derive_window, block_size) is
+    computed inside the kernel instead.
+    Returns indices [B, L, Hkv, topk] int32 and scores [B, L, Hkv, G, topk].
+    """
+
+    if selection_mode not in {"post_softmax", "pre_softmax"}:
+        raise ValueError(f"unsupported selection_mode={selection_mode}")
+    if q5.device.type != "cuda":
+        raise ValueError("route scoring requires CUDA tensors")
+    B, L, Hkv, G, D = q5.shape
+    C = lmks.shape[1]
+    if lmks.shape[2] == Hkv * G:
+        per_head = 1
+    elif lmks.shape[2] == Hkv:
+        per_head = 0
+    else:
+        raise AssertionError(
+            f"k_lmks h dim ({lmks.shape[2]}) must be either h_kv ({Hkv}) or h_kv*G ({Hkv * G})"
+        )
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    qc = q5.to(torch.bfloat16).contiguous()
+    lc = lmks.to(torch.bfloat16).contiguous()
+    lse = None
+    if selection_mode == "post_softmax":
+        if lse4 is None:
+            raise ValueError("post_softmax selection needs the local LSE")
+        lse = lse4.to(device=q5.device, dtype=torch.float32).reshape(B, L, Hkv, G).contiguous()
+    bias = None
+    if bias4 is not None:
+        bias = bias4.to(device=q5.device, dtype=torch.float32).reshape(B, C, Hkv, G).contiguous()
+    drop = None
+    if drop_mask is not None and derive_window < 0:
+        if drop_mask.shape != (B, L, C):
+            raise ValueError(f"invalid drop_mask shape {tuple(drop_mask.shape)}")
+        drop = drop_mask.to(device=q5.device, dtype=torch.int32).contiguous()
+    kv = None
+    if derive_window >= 0 and key_valid is not None:
+        kv = key_valid.to(device=q5.device, dtype=torch.bool).contiguous()
+    indices = torch.empty(B, L, Hkv, topk, dtype=torch.int32, device=q5.device)
+    scores = torch.empty(
+        B, L, Hkv, G, topk,
+        dtype=torch.float32 if scores_fp32 else torch.bfloat16, device=q5.device,
+    )
+    st = _lib.call(
+        "mrsa_route_topk_fwd",
+        _lib.ptr(qc), _lib.ptr(lc), _lib.ptr(lse), _lib.ptr(bias), _lib.ptr(drop),
+        _lib.ptr(kv), int(derive_window), B, L, C, Hkv, G, D, int(topk), int(block_size),
+        per_head, 1 if is_causal else 0, int(window_size), int(q_offset),
+        0 if selection_mode == "post_softmax" else 1, float(sm_scale),
+        _lib.ptr(indices), _lib.ptr(scores), 1 if scores_fp32 else 0, _lib.stream_of(qc),
+    )
+    _lib.check(st, "route_topk")
+    return indices, scores
+
+
+def _bias4(bias, B, C, Hkv, G):
+    if bias is None:
+        return None
+    if bias.dim() == 3:
+        assert bias.shape == (B, C, Hkv * G), (
+            f"bias shape {tuple(bias.shape)} != ({B}, {C}, {Hkv * G})"
+        )
+    elif bias.dim() == 4:
+        assert bias.shape == (B, C, Hkv, G), (
+            f"bias shape {tuple(bias.shape)} != ({B}, {C}, {Hkv}, {G})"
+        )
+    else:
+        raise AssertionError(
+            f"bias must be [B, S, h_q] or [B, S, h_kv, G], got {tuple(bias.shape)}"
+        )
+    return bias.reshape(B, C, Hkv, G)
+
+
+def ref_softmax_topk_max_pooling(
+    q, k_lmks, lse_swa, topk, block_size, window_size, is_causal=False, q_offset=0,
+    drop_mask=None, bias=None, gumbel_noise=None, selection_mode="post_softmax",
+):
+    """Same contract as ops/topk_head_softmax.py:15-156.
+
+    q [B, L, h_kv, G, D]; k_lmks [B, S, h_kv, D] or [B, S, h_kv*G, D];
+    lse_swa [B, L, h_q] or [B, L, h_kv, G]; returns indices [B, L, h_kv, topk]
+    (int64, ascending, -1 last) and fp32 raw scores [B, L, h_kv, G, topk].
+    """
+
+    if selection_mode not in {"post_softmax", "pre_softmax"}:
+        raise ValueError(f"unsupported selection_mode={selection_mode}")
+    if gumbel_noise is not None:
+        raise ValueError("gumbel_noise is a training-only input; the forward kernels do not take it")
+    B, L, Hkv, G, D = q.shape
+    C = k_lmks.shape[1]
+    lse4 = None
+    if selection_mode == "post_softmax":
+        lse4 = lse_swa.reshape(B, L, Hkv, G)
+    indices, scores = route_topk_launch(
+        q, k_lmks, lse4, topk, block_size,
+        bias4=_bias4(bias, B, C, Hkv, G), drop_mask=drop_mask,
+        is_causal=is_causal, window_size=window_size, q_offset=q_offset,
+        selection_mode=selection_mode, sm_scale=1.0 / math.sqrt(D), scores_fp32=True,
+    )
+    return indices.to(torch.int64), scores
+
+
+def online_softmax_topk_head(
+    q, lmks, lse_swa, topk, block_size, window_size, is_causal=True, q_offset=0,
+    is_training=True, drop_mask=None, sm_scale=None, bias=None, use_gumbel=False,
+    gumbel_noise=None, G=1,
+):
+    """Same contract as ops/topk_head_softmax.py:1242-1415 (forward only).
+
+    Returns (indices [B, L, h_kv, topk] int32, scores [B, L, h_q, topk] bf16);
+    for is_training=False with a logical group of 7 the scores come back in
+    the reference's physical G=8 layout (pad slot -inf), as its inference
+    branch does.
+    """
+
+    if use_gumbel or gumbel_noise is not None:
+        raise ValueError("Gumbel route sampling is training-only; not supported by the forward kernels")
+    if q.dim() == 4:
+        B, L, h_q, D = q.shape
+        lmks_h = lmks.shape[2]
+        if lmks.shape[3] != D:
+            ratio = lmks.shape[3] // D
+            lmks = lmks.reshape(lmks.shape[0], lmks.shape[1], lmks_h * ratio, D)
+            lmks_h *= ratio
+        if G == 1:
+            assert h_q % lmks_h == 0, f"h_q ({h_q}) must be divisible by lmks_h ({lmks_h})"
+            h_kv = lmks_h
+            g_eff = h_q // h_kv
+        else:
+            assert lmks_h == h_q, f"when G>1, lmks must have h_q ({h_q}) heads, got {lmks_h}"
+            assert h_q % G == 0, f"h_q ({h_q}) must be divisible by G ({G})"
+            h_kv = h_q // G
+            g_eff = G
+        q5 = q.reshape(B, L, h_kv, g_eff, D)
+    else:
+        B, L, h_kv, g_eff, D = q.shape
+        h_q = h_kv * g_eff
+        q5 = q
+        if G > 1 and (h_q // G != h_kv or G != g_eff):
+            h_kv, g_eff = h_q // G, G
+            q5 = q.reshape(B, L, h_kv, g_eff, D)
+    C = lmks.shape[1]
+    lse4 = lse_swa.reshape(B, L, h_kv, g_eff)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    indices, scores = route_topk_launch(
+        q5, lmks, lse4, topk, block_size,
+        bias4=_bias4(bias, B, C, h_kv, g_eff), drop_mask=drop_mask,
+        is_causal=is_causal, window_size=window_size, q_offset=q_offset,
+        sm_scale=sm_scale if is_training else 1.0 / math.sqrt(D),
+    )
+    if not is_training and g_eff == 7:
+        scores = group_pad_to(
+            scores.reshape(B, L, h_kv * 7, topk), h_kv, 7, 8, value=float("-inf")
+        )
+        return indices.to(torch.int64), scores
+    return indices, scores.reshape(B, L, h_kv * g_eff, topk)

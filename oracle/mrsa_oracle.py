@@ -1,0 +1,422 @@
+"""CPU fp32 restatement of the MRSA route-layer forward -- TEST INFRASTRUCTURE.
+
+This module is the parity oracle.  Only tests/, __graft_entry__.smoke() and
+bench.py's CPU-baseline leg may import it, and only as the checker (or as the
+timed CPU baseline).  The product path (the ``mrsa`` package) never calls it.
+
+Every function restates one stage of the reference
+(NRHLYM/Mask-Routed-Sparse-Attention-for-Long-Context-Diffusion-Language-Models)
+in plain torch on the CPU, in fp32, at the bf16 rounding points the reference
+has between stages.  Citations are file:line in that repository.
+
+Conventions: bf16 tensors in, fp32 math; functions return fp32 unless noted.
+Ties in the route selection are broken toward the lower chunk index (the rule
+of the reference's fused selection kernel, ops/topk_head_softmax.py:614-626;
+its torch path uses torch.topk, whose tie order is implementation-defined).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+NEG_INF = float("-inf")
+
+
+def bf16_round(x: torch.Tensor) -> torch.Tensor:
+    """Round to bf16 (nearest-even) and widen back to fp32."""
+
+    return x.to(torch.bfloat16).to(torch.float32)
+
+
+# ---------------------------------------------------------------------------
+# a4: landmark pool
+# ---------------------------------------------------------------------------
+def chunk_attn_pool(mu_q, k_chunked, key_valid, sm_scale=None, *, dense=None):
+    """Landmark keys and entropy of ops/chunk_attn_pool_gqa_tilelang.py.
+
+    mu_q [B, C, Hkv, G, D], k_chunked [B, C, S, Hkv, D], key_valid [B, C, S].
+    dense=None picks what chunk_attn_pool_gqa dispatches to: the compiled torch
+    twin _compact_pool_torch (:17-37) for G == 1, else the fused kernel
+    semantics of _pool_gqa_fwd (:47-180):
+      * chunk valid iff any of its first S-1 keys is valid (:94-99);
+      * masked slot -> -inf, except slot 0 -> logit 0 (:118-129);
+      * pooling uses the probabilities rounded to bf16 (:151-158);
+      * entropy from the fp32 probabilities (:142-149);
+      * invalid chunk -> zero key and zero entropy (:161-178).
+    Returns (landmark_keys fp32 before the final bf16 rounding, entropy fp32).
+    """
+
+    B, C, H, G, D = mu_q.shape
+    S = k_chunked.shape[2]
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    if dense is None:
+        dense = G == 1
+    q = mu_q.float()
+    k = k_chunked.float()
+    real = key_valid.bool().clone()
+    real[..., -1] = False
+    logits = torch.einsum("bchgd,bcshd->bchgs", q, k) * sm_scale
+    if dense:
+        logits = logits.masked_fill(~real[:, :, None, None, :], NEG_INF)
+        probs = torch.nan_to_num(torch.softmax(logits, dim=-1), nan=0.0)
+        chunk_ok = torch.ones(B, C, dtype=torch.bool)
+        p_pool = probs
+    else:
+        chunk_ok = real.any(dim=-1)
+        ok = real & chunk_ok[..., None]
+        fill = torch.full((S,), NEG_INF)
+        fill[0] = 0.0
+        logits = torch.where(ok[:, :, None, None, :], logits, fill)
+        probs = torch.softmax(logits, dim=-1)
+        p_pool = bf16_round(probs)
+    lmk = torch.einsum("bchgs,bcshd->bchgd", p_pool, k)
+    logp = torch.where(probs > 0, probs.clamp_min(1e-30).log(), torch.zeros_like(probs))
+    entropy = -(probs * logp).sum(dim=-1)
+    zero = ~chunk_ok[:, :, None, None]
+    lmk = lmk.masked_fill(zero[..., None], 0.0)
+    entropy = entropy.masked_fill(zero, 0.0)
+    return lmk, entropy
+
+
+# ---------------------------------------------------------------------------
+# a1: drop mask
+# ---------------------------------------------------------------------------
+def chunk_aligned_local_bounds(seq_len, window, chunk_size):
+    """dream_dllm_hils/kernel_utils.py:75-99."""
+
+    pos = torch.arange(seq_len)
+    left = (pos - window).clamp_min(0).div(chunk_size, rounding_mode="floor") * chunk_size
+    right = ((pos + window).clamp_max(seq_len - 1).div(chunk_size, rounding_mode="floor") + 1) * chunk_size
+    return left, right.clamp_max(seq_len)
+
+
+def remote_drop_mask(valid_mask, window, chunk_size, allowed_mask=None):
+    """dream_dllm_hils/kernel_utils.py:102-161; int32 [B, L, L/S]."""
+
+    B, L = valid_mask.shape
+    C = L // chunk_size
+    pos = torch.arange(L)
+    real = (pos + 1).remainder(chunk_size) != 0
+    chunk_valid = (valid_mask.bool() & real[None]).reshape(B, C, chunk_size).any(-1)
+    left, right = chunk_aligned_local_bounds(L, window, chunk_size)
+    lc = left.div(chunk_size, rounding_mode="floor")
+    rc = (right - 1).div(chunk_size, rounding_mode="floor")
+    ids = torch.arange(C)
+    local = (ids[None, :] >= lc[:, None]) & (ids[None, :] <= rc[:, None])
+    drop = local[None] | ~chunk_valid[:, None, :]
+    if allowed_mask is not None:
+        lmk_pos = torch.arange(chunk_size - 1, L, chunk_size)
+        drop = drop | ~allowed_mask.bool().index_select(-1, lmk_pos)
+    return drop.to(torch.int32)
+
+
+# ---------------------------------------------------------------------------
+# a5: route scoring + top-k
+# ---------------------------------------------------------------------------
+def route_topk(q5, lmks, lse4, topk, block_size, *, drop_mask=None, bias4=None,
+               selection_mode="post_softmax", is_causal=False, window_size=0, q_offset=0,
+               query_block=512):
+    """ref_softmax_topk_max_pooling (ops/topk_head_softmax.py:15-156).
+
+    q5 [B, L, Hkv, G, D]; lmks [B, C, Hkv*G, D] or [B, C, Hkv, D];
+    lse4 [B, L, Hkv, G]; bias4 [B, C, Hkv, G]; drop_mask [B, L, C].
+    Returns indices [B, L, Hkv, topk] int64 (ascending, -1 last), scores
+    [B, L, Hkv, G, topk] fp32 (raw scaled q.k at the picks, -inf at -1) and
+    the selection scores [B, L, Hkv, C] (max over G after the drop mask) used
+    to find near ties.
+    """
+
+    B, L, H, G, D = q5.shape
+    C = lmks.shape[1]
+    per_head = lmks.shape[2] == H * G
+    lm = lmks.float().reshape(B, C, H, G, D) if per_head else lmks.float()
+    scale = 1.0 / math.sqrt(D)
+    idx_out = torch.empty(B, L, H, topk, dtype=torch.int64)
+    sc_out = torch.empty(B, L, H, G, topk)
+    sel_out = torch.empty(B, L, H, C)
+    kk = min(topk, C)
+    for l0 in range(0, L, query_block):
+        l1 = min(L, l0 + query_block)
+        q = q5[:, l0:l1].float()
+        if per_head:
+            logits = torch.einsum("blhgd,bchgd->blhgc", q, lm)
+        else:
+            logits = torch.einsum("blhgd,bchd->blhgc", q, lm)
+        logits = logits * scale
+        if is_causal:
+            i = torch.arange(l0, l1)[:, None] + q_offset
+            j = torch.arange(C)[None, :]
+            thr = (i - window_size + 1).div(block_size, rounding_mode="floor") if window_size > 0 \
+                else i.div(block_size, rounding_mode="floor")
+            cm = (j >= thr).view(1, l1 - l0, 1, 1, C)
+            logits = logits.masked_fill(cm, NEG_INF)
+        x = logits
+        if bias4 is not None:
+            x = x + bias4.float().permute(0, 2, 3, 1)[:, None]
+        if selection_mode == "pre_softmax":
+            y = x
+        else:
+            lse_h = torch.logsumexp(x, dim=-1)
+            tot = torch.logaddexp(lse4[:, l0:l1].float(), lse_h)
+            y = x - tot[..., None]
+        sel = y.max(dim=3).values
+        if drop_mask is not None:
+            sel = sel.masked_fill(drop_mask[:, l0:l1].bool()[:, :, None, :], NEG_INF)
+        sel_out[:, l0:l1] = sel
+        order = torch.sort(sel, dim=-1, descending=True, stable=True).indices[..., :kk]
+        topv = torch.gather(sel, -1, order)
+        order = order.masked_fill(topv == NEG_INF, -1)
+        if kk < topk:
+            pad = torch.full((*order.shape[:-1], topk - kk), -1, dtype=order.dtype)
+            order = torch.cat([order, pad], dim=-1)
+        key = order.masked_fill(order < 0, C + 1000)
+        idx = torch.sort(key, dim=-1).values
+        idx = idx.masked_fill(idx >= C, -1)
+        safe = idx.clamp_min(0)[:, :, :, None, :].expand(-1, -1, -1, G, -1)
+        sc = torch.gather(logits, -1, safe)
+        sc = sc.masked_fill(idx[:, :, :, None, :] < 0, NEG_INF)
+        idx_out[:, l0:l1] = idx
+        sc_out[:, l0:l1] = sc
+    return idx_out, sc_out, sel_out
+
+
+def boundary_gap(sel, topk):
+    """Gap between the topk-th and (topk+1)-th selection scores per row (inf if undefined)."""
+
+    vals = torch.sort(sel, dim=-1, descending=True).values
+    if vals.shape[-1] <= topk:
+        return torch.full(vals.shape[:-1], float("inf"))
+    a = vals[..., topk - 1]
+    b = vals[..., topk]
+    gap = a - b
+    return torch.where(torch.isfinite(a) & torch.isfinite(b), gap, torch.full_like(gap, float("inf")))
+
+
+# ---------------------------------------------------------------------------
+# a7: route weights
+# ---------------------------------------------------------------------------
+def route_weights(scores, indices, prior_bias, local_lse, *, temperature=1.0,
+                  gate_offset=None, gate_scale=None):
+    """_route_weights_torch (dream_dllm_hils/attention.py:126-235), fp32 outputs.
+
+    scores [B, L, Hq, K] (bf16 values), indices [B, L, Hkv, K], prior_bias
+    [B, C, Hkv, G], local_lse [B, L, Hq].  Returns (remote [B, L, Hq, K],
+    local [B, L, Hq]) before the bf16 rounding.
+    """
+
+    B, L, Hq, K = scores.shape
+    _, C, Hkv, G = prior_bias.shape
+    idx = indices.long().repeat_interleave(G, dim=2)
+    valid = (idx >= 0) & (idx < C)
+    safe = idx.clamp(0, C - 1)
+    bias_by_head = prior_bias.float().reshape(B, C, Hq).permute(0, 2, 1)
+    sel_bias = torch.gather(bias_by_head[:, None].expand(B, L, Hq, C), -1, safe)
+    remote_logits = (scores.float() + sel_bias).masked_fill(~valid, NEG_INF)
+    local_logits = local_lse.float()[..., None]
+    affine = gate_scale is not None
+    if gate_offset is not None and not affine:
+        local_logits = local_logits - float(gate_offset)
+    logits = torch.cat((remote_logits, local_logits), dim=-1) / float(temperature)
+    all_masked = torch.isneginf(logits).all(dim=-1, keepdim=True)
+    logits = torch.where(all_masked, torch.zeros_like(logits), logits)
+    if affine:
+        remote_lse = torch.logsumexp(logits[..., :K], dim=-1)
+        gate = float(gate_scale) * (remote_lse - logits[..., K]) + (
+            float(gate_offset) if gate_offset is not None else 0.0)
+        mass = torch.sigmoid(gate)
+        internal = torch.softmax(remote_logits / float(temperature), dim=-1)
+        internal = torch.where((~valid).all(dim=-1, keepdim=True), torch.zeros_like(internal), internal)
+        remote = internal * mass[..., None]
+        local = 1.0 - mass
+        remote = torch.where(all_masked, torch.zeros_like(remote), remote)
+        local = torch.where(all_masked[..., 0], torch.zeros_like(local), local)
+        return remote, local
+    probs = torch.softmax(logits, dim=-1)
+    probs = torch.where(all_masked, torch.zeros_like(probs), probs)
+    return probs[..., :K], probs[..., K]
+
+
+# ---------------------------------------------------------------------------
+# a2 / a3: window attention
+# ---------------------------------------------------------------------------
+def local_attention(q, k, v, key_valid, window, inert_chunk=0, query_positions=None,
+                    query_block=256):
+    """Window attention with the zero-K/V inert rule (local_attention.py:35-107).
+
+    Key j visible to the query at position p iff |p - j| <= window; keys that
+    fail key_valid (and landmark slots when inert_chunk > 0) have K = V = 0.
+    Returns (out fp32 [B, Lq, Hq, D], lse fp32 [B, Lq, Hq]).
+    """
+
+    B, Lq, Hq, D = q.shape
+    Lk, Hkv = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    scale = D ** -0.5
+    valid = torch.ones(B, Lk, dtype=torch.bool) if key_valid is None else key_valid.bool().clone()
+    if inert_chunk > 0:
+        valid &= ((torch.arange(Lk) + 1) % inert_chunk != 0)[None]
+    kz = k.float() * valid[:, :, None, None]
+    vz = v.float() * valid[:, :, None, None]
+    pos = torch.arange(Lq) if query_positions is None else query_positions.long().cpu()
+    out = torch.zeros(B, Lq, Hq, D)
+    lse = torch.zeros(B, Lq, Hq)
+    for i0 in range(0, Lq, query_block):
+        i1 = min(Lq, i0 + query_block)
+        p = pos[i0:i1]
+        lo = max(int(p.min()) - window, 0)
+        hi = min(int(p.max()) + window + 1, Lk)
+        if hi <= lo:
+            lse[:, i0:i1] = NEG_INF
+            continue
+        qb = q[:, i0:i1].float().reshape(B, i1 - i0, Hkv, G, D)
+        s = torch.einsum("bqhgd,bkhd->bqhgk", qb, kz[:, lo:hi]) * scale
+        j = torch.arange(lo, hi)
+        vis = (j[None, :] - p[:, None]).abs() <= window
+        s = s.masked_fill(~vis[None, :, None, None, :], NEG_INF)
+        l = torch.logsumexp(s, dim=-1)
+        pr = torch.softmax(s, dim=-1)
+        o = torch.einsum("bqhgk,bkhd->bqhgd", pr, vz[:, lo:hi])
+        out[:, i0:i1] = o.reshape(B, i1 - i0, Hq, D)
+        lse[:, i0:i1] = l.reshape(B, i1 - i0, Hq)
+    return out, lse
+
+
+# ---------------------------------------------------------------------------
+# a8: routed chunk attention
+# ---------------------------------------------------------------------------
+def selected_attention(q, k, v, weights, indices, key_valid, chunk_size=64,
+                       mask_last_token=True, query_block=256):
+    """Weighted sum of per-chunk softmax attentions.
+
+    Formula of the reference test test_hils_non_power_two_topk.py:122-138 and
+    hils_torch_ref (ops/hils_fwd_bwd_head.py:21-93), with the kernel's key_valid
+    masking (:479-486) and index-list reading (:352-361: a list ends at its
+    first negative entry).  Entries >= kv_len / chunk_size are skipped.
+    q [B, Lq, Hq, D], k/v [B, Lk, Hkv, D], weights [B, Lq, Hq, K],
+    indices [B, Lq, Hkv, K].  Returns fp32 [B, Lq, Hq, D].
+    """
+
+    B, Lq, Hq, D = q.shape
+    Lk, Hkv = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    S = chunk_size
+    C = Lk // S
+    K = indices.shape[-1]
+    scale = 1.0 / math.sqrt(D)
+    kc = k.float().reshape(B, C, S, Hkv, D)
+    vc = v.float().reshape(B, C, S, Hkv, D)
+    allowed = torch.ones(B, C, S, dtype=torch.bool) if key_valid is None else \
+        key_valid.bool().reshape(B, C, S).clone()
+    if mask_last_token:
+        allowed[..., -1] = False
+    idx = indices.long()
+    neg = idx < 0
+    before_neg = torch.cumsum(neg.int(), dim=-1) == 0
+    ok = before_neg & (idx >= 0) & (idx < C)
+    safe = idx.clamp(0, C - 1)
+    out = torch.zeros(B, Lq, Hq, D)
+    bidx = torch.arange(B)[:, None, None]
+    hidx = torch.arange(Hkv)[None, None, :]
+    for i0 in range(0, Lq, query_block):
+        i1 = min(Lq, i0 + query_block)
+        qb = q[:, i0:i1].float().reshape(B, i1 - i0, Hkv, G, D)
+        wb = weights[:, i0:i1].float().reshape(B, i1 - i0, Hkv, G, K)
+        acc = torch.zeros(B, i1 - i0, Hkv, G, D)
+        for kk in range(K):
+            c = safe[:, i0:i1, :, kk]                       # [B, l, Hkv]
+            kg = kc[bidx, c, :, hidx]                       # [B, l, Hkv, S, D]
+            vg = vc[bidx, c, :, hidx]
+            al = allowed[bidx, c]                           # [B, l, Hkv, S]
+            s = torch.einsum("blhgd,blhsd->blhgs", qb, kg) * scale
+            s = s.masked_fill(~al[:, :, :, None, :], NEG_INF)
+            p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
+            o = torch.einsum("blhgs,blhsd->blhgd", p, vg)
+            w = wb[..., kk] * ok[:, i0:i1, :, kk][..., None].float()
+            acc += o * w[..., None]
+        out[:, i0:i1] = acc.reshape(B, i1 - i0, Hq, D)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# a9: fusion
+# ---------------------------------------------------------------------------
+def fuse_outputs(remote_output, local_output, local_weight):
+    """ops/hils_bidir_output_fusion_tilelang.py:28-35; returns bf16."""
+
+    r = remote_output.float()
+    lw = local_weight.float()[..., None]
+    lo = local_output.float()
+    return (r + lw * lo).to(torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
+# a6: candidate token scores
+# ---------------------------------------------------------------------------
+def candidate_token_scores(q, k, indices, key_valid, chunk_size):
+    """candidate_token_scores_reference (dream_dllm_hils/token_refinement.py:10-92)."""
+
+    B, Lq, Hq, D = q.shape
+    Lk, Hkv = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    C = Lk // chunk_size
+    K = indices.shape[-1]
+    kc = k.float().reshape(B, C, chunk_size, Hkv, D)
+    idx = indices.long()
+    safe = idx.clamp(0, max(C - 1, 0))
+    bidx = torch.arange(B)[:, None, None, None]
+    hidx = torch.arange(Hkv)[None, None, :, None]
+    kg = kc[bidx, safe, :, hidx]                           # [B, Lq, Hkv, K, S, D]
+    qg = q.float().reshape(B, Lq, Hkv, G, D)
+    s = torch.einsum("blhgd,blhksd->blhkgs", qg, kg).amax(dim=-2) / math.sqrt(D)
+    valid_chunk = (idx >= 0) & (idx < C)
+    kv = torch.ones(B, Lk, dtype=torch.bool) if key_valid is None else key_valid.bool()
+    sel_valid = kv.reshape(B, C, chunk_size)[torch.arange(B)[:, None, None, None], safe]
+    sel_valid = sel_valid & valid_chunk[..., None]
+    sel_valid[..., -1] = False
+    return s.masked_fill(~sel_valid, NEG_INF)
+
+
+# ---------------------------------------------------------------------------
+# a10: the route layer
+# ---------------------------------------------------------------------------
+def route_layer(q, k, v, route_q, entropy_bias_scale, key_valid=None, *, local_window=256,
+                chunk_size=64, topk=32, temperature=1.0, gate_offset=0.0, gate_scale=1.0,
+                skip_inert_slots=True):
+    """KernelDreamFullHiLSAttention.forward between projections and o_proj
+    (dream_dllm_hils/attention.py:1380-1774), with the reference's bf16
+    rounding between stages.  Returns (out bf16, intermediates dict)."""
+
+    B, L, Hq, D = q.shape
+    Hkv = k.shape[2]
+    G = Hq // Hkv
+    S = chunk_size
+    C = L // S
+    kv = torch.ones(B, L, dtype=torch.bool) if key_valid is None else key_valid.bool()
+    window = local_window + S - 1 if skip_inert_slots else local_window
+    local_out, local_lse = local_attention(q, k, v, kv, window, S if skip_inert_slots else 0)
+    local_out = local_out.to(torch.bfloat16)
+    q_lmk = route_q[:, S - 1 :: S].reshape(B, C, Hkv, G, D)
+    lmk, entropy = chunk_attn_pool(q_lmk, k.reshape(B, C, S, Hkv, D), kv.reshape(B, C, S))
+    lmk = lmk.to(torch.bfloat16)
+    prior = entropy * entropy_bias_scale.float().view(1, 1, Hkv, G)
+    drop = remote_drop_mask(kv, local_window, S)
+    idx, scores, sel = route_topk(
+        route_q.reshape(B, L, Hkv, G, D), lmk.reshape(B, C, Hq, D),
+        local_lse.reshape(B, L, Hkv, G), topk, S, drop_mask=drop, bias4=prior,
+    )
+    scores_bf = scores.reshape(B, L, Hq, topk).to(torch.bfloat16)
+    rw, lw = route_weights(scores_bf, idx, prior, local_lse, temperature=temperature,
+                           gate_offset=gate_offset, gate_scale=gate_scale)
+    rw = rw.to(torch.bfloat16)
+    lw = lw.to(torch.bfloat16)
+    remote = selected_attention(q, k, v, rw, idx, kv, S).to(torch.bfloat16)
+    out = fuse_outputs(remote, local_out, lw)
+    return out, {
+        "local_output": local_out, "local_lse": local_lse, "landmark_keys": lmk,
+        "entropy": entropy, "prior_bias": prior, "indices": idx, "scores": scores_bf,
+        "selection": sel, "remote_weights": rw, "local_weight": lw, "remote_output": remote,
+    }

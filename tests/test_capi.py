@@ -1,0 +1,75 @@
+"""The C-ABI library loads, exports every declared entry point and rejects bad
+arguments on the host (no GPU needed: nothing here launches a kernel)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import PKG_DIR, ROOT
+
+HEADER = os.path.join(ROOT, "include", "mrsa.h")
+LIB = os.path.join(PKG_DIR, "mrsa", "libmrsa.so")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mrsa_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} missing: run __graft_entry__.build() first")
+    return ctypes.CDLL(LIB)
+
+
+def test_header_lists_expected_entry_points():
+    names = _declared()
+    for expected in (
+        "mrsa_chunk_attn_pool_gqa_fwd", "mrsa_remote_drop_mask", "mrsa_route_topk_fwd",
+        "mrsa_route_weights_fwd", "mrsa_local_attention_fwd", "mrsa_selected_attention_fwd",
+        "mrsa_fuse_hils_outputs_fwd", "mrsa_candidate_token_scores_fwd", "mrsa_value_tiles",
+    ):
+        assert expected in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_python_binding_matches_header():
+    import mrsa._lib as L
+
+    assert sorted(L.SIGNATURES) == _declared()
+
+
+def test_status_strings_and_version(lib):
+    lib.mrsa_status_string.restype = ctypes.c_char_p
+    assert lib.mrsa_status_string(0) == b"ok"
+    assert b"invalid" in lib.mrsa_status_string(1)
+    assert lib.mrsa_abi_version() >= 1
+
+
+def test_host_side_argument_errors(lib):
+    import mrsa._lib as L
+
+    L.load()
+    # Negative sizes and NULL pointers are rejected before any launch.
+    assert L.call("mrsa_fuse_hils_outputs_fwd", None, None, None, None, -1, 128, None) == 1
+    assert L.call("mrsa_fuse_hils_outputs_fwd", None, None, None, None, 4, 128, None) == 1
+    assert L.call("mrsa_remote_drop_mask", None, None, 1, 100, 256, 64, None, None) == 1
+    assert L.call("mrsa_chunk_attn_pool_gqa_fwd", None, None, None, 4, 64, 4, 17, 128,
+                  1.0, 0, None, None, None, None, None) == 1
+    assert L.call("mrsa_local_attention_fwd", 16, 16, 16, None, None, 1, 64, 64, 28, 4, 96,
+                  256, 0, 1.0, 16, 16, None) == 2          # head_dim 96 unsupported
+    assert L.call("mrsa_selected_attention_fwd", 16, 16, 16, 16, 16, None, 1, 64, 128, 28, 4,
+                  128, 32, 32, 1, 1.0, 16, None) == 2      # chunk_size 32 unsupported
+    assert L.call("mrsa_route_weights_fwd", 16, 16, 16, 16, 1, 4, 4, 4, 7, 65, 1.0, 0, 0.0,
+                  0, 1.0, 16, 16, None) == 2               # topk > 64
+    assert L.call("mrsa_value_tiles_bytes", 1, 65, 4, 128) == 1 * 4 * 2 * 128 * 64 * 2
+    # Empty problems are a successful no-op.
+    assert L.call("mrsa_fuse_hils_outputs_fwd", None, None, None, None, 0, 128, None) == 0

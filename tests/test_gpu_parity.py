@@ -1,0 +1,334 @@
+"""GPU parity: every gfx950 kernel against the CPU oracle on seeded inputs.
+
+Tolerances (from the build target): routing indices bit-exact except rows
+whose oracle top-k boundary gap is below 1e-5 (reported); attention outputs
+within max-abs 2e-2 and mean-abs 2e-3 (bf16 in, fp32 accumulate).
+"""
+
+import math
+
+import pytest
+import torch
+
+import mrsa
+from mrsa import _lib
+from mrsa.local_attention import local_attention_launch
+from mrsa.route_weights import route_weights_launch
+from mrsa.sparse_attention import selected_attention_launch
+from mrsa.topk import route_topk_launch
+from oracle import mrsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+NEAR_TIE = 1e-5
+
+
+def _note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def _rand(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g) * scale
+
+
+def _planted_kv(L, Hkv, D, seed, sigma=0.3):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(1, L, Hkv, D, generator=g)
+    shift = sigma * torch.randn(L // 64, Hkv, D, generator=g)
+    k = k + shift.repeat_interleave(64, dim=0)[None]
+    v = torch.randn(1, L, Hkv, D, generator=g)
+    return k.bfloat16(), v.bfloat16()
+
+
+def _assert_close_attn(actual, expected, what):
+    err = (actual.float().cpu() - expected.float()).abs()
+    print(f"{what}: max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
+    assert float(err.max()) <= 2e-2, what
+    assert float(err.mean()) <= 2e-3, what
+
+
+def test_mfma_lane_layout():
+    _note("mfma layout")
+    a = _rand((16, 32), 1).bfloat16()
+    b = _rand((32, 16), 2).bfloat16()
+    c = torch.empty(16, 16, device=DEV)
+    ad, bd = a.to(DEV), b.to(DEV)
+    _lib.check(_lib.call("mrsa_selftest_mfma_layout", ad.data_ptr(), bd.data_ptr(),
+                         c.data_ptr(), _lib.stream_of(c)), "selftest")
+    torch.cuda.synchronize()
+    torch.testing.assert_close(c.cpu(), a.float() @ b.float(), atol=1e-4, rtol=1e-4)
+
+
+def test_fusion_bit_exact():
+    _note("fusion")
+    r = _rand((1, 300, 28, 128), 3).bfloat16()
+    lo = _rand((1, 300, 28, 128), 4).bfloat16()
+    w = torch.rand(1, 300, 28).bfloat16()
+    out = mrsa.fuse_hils_outputs(r.to(DEV), lo.to(DEV), w.to(DEV))
+    assert torch.equal(out.cpu(), O.fuse_outputs(r, lo, w))
+    out2 = mrsa.fuse_hils_outputs(r[..., :100].contiguous().to(DEV), lo[..., :100].contiguous().to(DEV),
+                                  w.to(DEV))   # scalar path (head_dim % 8 != 0)
+    assert torch.equal(out2.cpu(), O.fuse_outputs(r[..., :100], lo[..., :100], w))
+
+
+def test_drop_mask_bit_exact():
+    _note("drop mask")
+    L = 2048
+    valid = torch.rand(2, L) > 0.02
+    valid[1, 5 * 64: 5 * 64 + 63] = False
+    allowed = torch.rand(2, L, L) > 0.001
+    for W, al in ((256, None), (100, allowed)):
+        got = mrsa.remote_drop_mask(valid.to(DEV), W, 64, None if al is None else al.to(DEV))
+        assert torch.equal(got.cpu(), O.remote_drop_mask(valid, W, 64, al))
+
+
+def test_value_tiles_layout():
+    _note("value tiles")
+    v = _rand((2, 200, 3, 128), 5).bfloat16()
+    t = mrsa.value_tiles(v.to(DEV)).cpu()
+    vp = torch.zeros(2, 256, 3, 128).bfloat16()
+    vp[:, :200] = v
+    expect = vp.reshape(2, 4, 64, 3, 128).permute(0, 3, 1, 4, 2)
+    assert torch.equal(t, expect)
+
+
+@pytest.mark.parametrize("G,dense", [(7, False), (1, True), (3, False)])
+def test_pool_vs_oracle(G, dense):
+    _note(f"pool G={G}")
+    B, C, H, S, D = 2, 40, 4, 64, 128
+    mu = _rand((B, C, H, G, D), 6).bfloat16()
+    k = _rand((B, C, S, H, D), 7).bfloat16()
+    valid = torch.rand(B, C, S) > 0.1
+    valid[0, 3] = False
+    valid[1, 4, :63] = False
+    valid[1, 5, 0] = False
+    scale = torch.rand(H * G) + 0.5
+    lmk, ent, prior = mrsa.chunk_attn_pool_gqa_prior(mu.to(DEV), k.to(DEV), valid.to(DEV), scale.to(DEV))
+    rl, re = O.chunk_attn_pool(mu, k, valid)
+    torch.testing.assert_close(lmk.cpu().float(), rl.bfloat16().float(), atol=1e-2, rtol=1e-2)
+    assert (lmk.cpu().float() - rl.bfloat16().float()).abs().mean() < 1e-4
+    torch.testing.assert_close(ent.cpu(), re, atol=2e-5, rtol=1e-5)
+    torch.testing.assert_close(prior.cpu(), re * scale.view(1, 1, H, G), atol=5e-5, rtol=1e-5)
+    lmk2, ent2 = mrsa.chunk_attn_pool_gqa(mu.to(DEV), k.to(DEV), valid.to(DEV))
+    assert torch.equal(lmk2, lmk) and torch.equal(ent2, ent)
+
+
+def _route_case(L, C, G, Hkv, seed, derive=False, drop_frac=0.2):
+    D = 128
+    q5 = _rand((1, L, Hkv, G, D), seed).bfloat16()
+    lmk = (_rand((1, C, Hkv * G, D), seed + 1) * 0.5).bfloat16()
+    lse4 = _rand((1, L, Hkv, G), seed + 2) + 3.0
+    bias4 = torch.rand(1, C, Hkv, G) * 0.5 + 3.5
+    if derive:
+        valid = torch.rand(1, L) > 0.01
+        drop = O.remote_drop_mask(valid, 256, L // C)
+    else:
+        valid = None
+        drop = (torch.rand(1, L, C) < drop_frac).to(torch.int32)
+    return q5, lmk, lse4, bias4, drop, valid
+
+
+def _check_route(idx_gpu, sc_gpu, q5, lmk, lse4, bias4, drop, topk, what):
+    ridx, rsc, sel = O.route_topk(q5, lmk, lse4, topk, 64, drop_mask=drop, bias4=bias4)
+    gap = O.boundary_gap(sel, topk)
+    near = gap < NEAR_TIE
+    idx = idx_gpu.cpu().long()
+    rows_bad = (idx != ridx).any(-1)
+    mism = rows_bad & ~near
+    print(f"{what}: rows={rows_bad.numel()} near_ties={int(near.sum())} "
+          f"mismatched_near_tie_rows={int((rows_bad & near).sum())} other_mismatches={int(mism.sum())}",
+          flush=True)
+    assert int(mism.sum()) == 0, f"{what}: {int(mism.sum())} non-tie rows differ"
+    ok = ~rows_bad
+    sc = sc_gpu.cpu().float()
+    expect = rsc.bfloat16().float()
+    okx = ok[:, :, :, None, None].expand_as(sc)
+    torch.testing.assert_close(sc[okx], expect[okx], atol=0.02, rtol=0.01)
+
+
+@pytest.mark.parametrize("L,C,G,topk", [(512, 256, 7, 32), (640, 200, 7, 31), (256, 300, 3, 16)])
+def test_route_topk_vs_oracle(L, C, G, topk):
+    _note(f"route topk L={L} C={C} G={G} K={topk}")
+    q5, lmk, lse4, bias4, drop, _ = _route_case(L, C, G, 4, 10 + L)
+    idx, sc = route_topk_launch(q5.to(DEV), lmk.to(DEV), lse4.to(DEV), topk, 64,
+                                          bias4=bias4.to(DEV), drop_mask=drop.to(DEV))
+    torch.cuda.synchronize()
+    _check_route(idx, sc, q5, lmk, lse4, bias4, drop, topk, f"route L={L} C={C} G={G}")
+
+
+def test_route_topk_derived_drop_equals_explicit():
+    _note("route derived drop")
+    L = 16384 // 8
+    C = L // 64
+    q5, lmk, lse4, bias4, drop, valid = _route_case(L, C, 7, 4, 77, derive=True)
+    a = route_topk_launch(q5.to(DEV), lmk.to(DEV), lse4.to(DEV), 8, 64,
+                                    bias4=bias4.to(DEV), drop_mask=drop.to(DEV))
+    b = route_topk_launch(q5.to(DEV), lmk.to(DEV), lse4.to(DEV), 8, 64,
+                                    bias4=bias4.to(DEV), derive_window=256, key_valid=valid.to(DEV))
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    _check_route(a[0], a[1], q5, lmk, lse4, bias4, drop, 8, "route derived")
+
+
+def test_route_topk_g7_api_and_determinism():
+    _note("route_topk_g7 api")
+    L, C = 1031, 40   # test_hils_non_power_two_topk.py:51-92 shape
+    g = torch.Generator().manual_seed(74)
+    q = torch.randn(1, L, 28, 128, generator=g).bfloat16().to(DEV)
+    lm = torch.randn(1, C, 4, 7, 128, generator=g).bfloat16().to(DEV)
+    lse = torch.randn(1, L, 4, 7, generator=g).to(DEV)
+    bias = torch.randn(1, C, 4, 7, generator=g).to(DEV)
+    dropped = torch.zeros(1, L, C, dtype=torch.int32, device=DEV)
+    dropped[:, ::11, 3] = 1
+    first = mrsa.route_topk_g7(q, lm, lse, bias, dropped, 32, 64, 512, training=False)
+    second = mrsa.route_topk_g7(q, lm, lse, bias, dropped, 32, 64, 512, training=False)
+    assert torch.equal(first[0], second[0]) and torch.equal(first[1], second[1])
+    ri, rs = mrsa.ref_softmax_topk_max_pooling(q.reshape(1, L, 4, 7, 128), lm.reshape(1, C, 28, 128),
+                                               lse, 32, 64, 512, drop_mask=dropped, bias=bias)
+    assert torch.equal(first[0], ri)
+    torch.testing.assert_close(first[1].float(), rs.reshape(1, L, 28, 32), atol=0.02, rtol=0.01)
+    _check_route(first[0], first[1].reshape(1, L, 4, 7, 32), q.cpu().reshape(1, L, 4, 7, 128),
+                 lm.cpu().reshape(1, C, 28, 128), lse.cpu(), bias.cpu(), dropped.cpu(), 32, "g7 api")
+
+
+@pytest.mark.parametrize("affine", [True, False])
+def test_route_weights_vs_oracle(affine):
+    _note(f"route weights affine={affine}")
+    B, L, Hkv, G, K, C = 1, 700, 4, 7, 32, 256
+    scores = _rand((B, L, Hkv * G, K), 20).bfloat16()
+    idx = torch.randint(0, C, (B, L, Hkv, K), generator=torch.Generator().manual_seed(21)).int()
+    idx[0, 3, 1, 20:] = -1
+    idx[0, 4, 2, :] = -1
+    bias = torch.rand(B, C, Hkv, G) + 3.5
+    lse = _rand((B, L, Hkv * G), 22) + 5.0
+    lse[0, 5, 3] = float("-inf")
+    kw = dict(gate_offset=0.0, gate_scale=1.0) if affine else {}
+    rw, lw = route_weights_launch(scores.to(DEV), idx.to(DEV), bias.to(DEV),
+                                                     lse.to(DEV), **kw)
+    er, el = O.route_weights(scores, idx, bias, lse, **kw)
+    torch.testing.assert_close(rw.cpu().float(), er.bfloat16().float(), atol=2e-3, rtol=1e-2)
+    torch.testing.assert_close(lw.cpu().float(), el.bfloat16().float(), atol=2e-3, rtol=1e-2)
+    if not affine:
+        torch.testing.assert_close(
+            mrsa.route_weights(scores[:, :, :, :31].contiguous().to(DEV), idx[..., :31].contiguous().to(DEV),
+                               bias.to(DEV), lse.to(DEV))[1].cpu().float(),
+            O.route_weights(scores[..., :31], idx[..., :31], bias, lse)[1].bfloat16().float(),
+            atol=2e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("L,W,inert,G", [(1024, 319, 64, 7), (2048, 1280, 0, 7), (512, 100, 64, 8)])
+def test_local_attention_vs_oracle(L, W, inert, G):
+    _note(f"local attention L={L} W={W} inert={inert} G={G}")
+    Hkv, D = 4, 128
+    q = _rand((1, L, Hkv * G, D), 30).bfloat16()
+    k, v = _planted_kv(L, Hkv, D, 31)
+    valid = torch.rand(1, L) > 0.05
+    out, lse = local_attention_launch(
+        q.to(DEV), k.to(DEV), mrsa.value_tiles(v.to(DEV)), valid.to(DEV), W, inert)
+    ro, rl = O.local_attention(q, k, v, valid, W, inert)
+    _assert_close_attn(out, ro, f"local L={L} W={W}")
+    torch.testing.assert_close(lse.cpu(), rl, atol=2e-3, rtol=1e-4)
+
+
+def test_bidir_and_cached_local_attention_api():
+    _note("local attention api")
+    L = 1024
+    q = _rand((1, L, 28, 128), 32).bfloat16().to(DEV)
+    k, v = _planted_kv(L, 4, 128, 33)
+    k, v = k.to(DEV), v.to(DEV)
+    valid = torch.ones(1, L, dtype=torch.bool, device=DEV)
+    o, l = mrsa.bidir_local_attention(q, k, v, valid, 256, 64, skip_inert_slots=True)
+    pos = torch.tensor([0, 5, 63, 400, 401, 1023], device=DEV)
+    oc, lc = mrsa.cached_local_attention(q[:, pos], k, v, valid, pos, 256, 64, skip_inert_slots=True)
+    torch.testing.assert_close(oc.float(), o[:, pos].float(), atol=1e-2, rtol=0)
+    torch.testing.assert_close(lc, l[:, pos], atol=1e-4, rtol=0)
+
+
+def _sorted_routes(Lq, Hkv, K, C, seed, neg_rows=()):
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.stack([torch.randperm(C, generator=g)[:K] for _ in range(Lq * Hkv)])
+    idx = idx.sort(-1).values.reshape(1, Lq, Hkv, K).int()
+    for r in neg_rows:
+        idx[0, r, :, K // 2:] = -1
+    return idx
+
+
+@pytest.mark.parametrize("Lq,Lk,K,unsorted", [(1024, 1024, 8, False), (777, 2048, 32, False),
+                                               (300, 4096, 32, True)])
+def test_selected_attention_vs_oracle(Lq, Lk, K, unsorted):
+    _note(f"selected Lq={Lq} Lk={Lk} K={K} unsorted={unsorted}")
+    Hkv, G, D, C = 4, 7, 128, Lk // 64
+    q = _rand((1, Lq, Hkv * G, D), 40).bfloat16()
+    k, v = _planted_kv(Lk, Hkv, D, 41)
+    idx = _sorted_routes(Lq, Hkv, K, C, 42, neg_rows=(0, 5))
+    if unsorted:
+        perm = torch.randperm(K, generator=torch.Generator().manual_seed(43))
+        idx = idx[..., perm].contiguous()
+        idx[0, 7, 0, 3] = C + 5          # out of range -> skipped
+    w = torch.softmax(_rand((1, Lq, Hkv * G, K), 44), -1).bfloat16()
+    valid = torch.rand(1, Lk) > 0.03
+    out = selected_attention_launch(
+        q.to(DEV), k.to(DEV), mrsa.value_tiles(v.to(DEV)), w.to(DEV), idx.to(DEV), valid.to(DEV), 64)
+    ref = O.selected_attention(q, k, v, w, idx, valid, 64)
+    _assert_close_attn(out, ref, f"selected Lq={Lq}")
+
+
+def test_selected_attention_reference_kat():
+    # test_hils_non_power_two_topk.py:95-142 (cached and uncached shapes).
+    for query_len in (35, 2048):
+        _note(f"selected KAT q={query_len}")
+        g = torch.Generator().manual_seed(79)
+        kv_len, h_kv, grp, dim, topk, size = 2048, 4, 7, 128, 31, 64
+        q = torch.randn(1, query_len, h_kv * grp, dim, generator=g).bfloat16()
+        k = torch.randn(1, kv_len, h_kv, dim, generator=g).bfloat16()
+        v = torch.randn(1, kv_len, h_kv, dim, generator=g).bfloat16()
+        indices = torch.arange(topk, dtype=torch.int32).expand(1, query_len, h_kv, -1).clone()
+        indices[:, 0] = -1
+        weights = torch.randn(1, query_len, h_kv * grp, topk, generator=g).softmax(-1).bfloat16()
+        weights[:, 0] = 0
+        valid = torch.ones(1, kv_len, dtype=torch.bool)
+        valid[:, ::97] = False
+        args = [t.to(DEV) for t in (q, k, v, weights, indices, valid)]
+        actual = (mrsa.selected_attention_g7_cached(*args, size) if query_len == 35 else
+                  mrsa.selected_attention_g7(*args, size, training=False))
+        assert actual.shape == q.shape and bool(torch.isfinite(actual).all())
+        assert torch.equal(actual[:, 0].cpu(), torch.zeros_like(actual[:, 0].cpu()))
+        rows = torch.tensor([1, query_len // 2, query_len - 1])
+        ref = O.selected_attention(q[:, rows], k, v, weights[:, rows], indices[:, rows], valid, size)
+        observed = actual.cpu()[:, rows].float()
+        assert float((observed - ref).norm() / ref.norm()) < 0.02
+        torch.testing.assert_close(observed, ref, atol=0.01, rtol=0.025)
+        for value, original in zip(args[3:], (weights, indices, valid)):
+            assert torch.equal(value.cpu(), original)
+
+
+def test_candidate_token_scores_vs_oracle():
+    _note("token scores")
+    Lq, Lk, K = 200, 2048, 8
+    q = _rand((1, Lq, 28, 128), 50).bfloat16()
+    k, _ = _planted_kv(Lk, 4, 128, 51)
+    idx = _sorted_routes(Lq, 4, K, Lk // 64, 52, neg_rows=(3,))
+    valid = torch.rand(1, Lk) > 0.05
+    got = mrsa.candidate_token_scores_gqa(q.to(DEV), k.to(DEV), idx.to(DEV), valid.to(DEV), 64).cpu()
+    ref = O.candidate_token_scores(q, k, idx, valid, 64)
+    fin = torch.isfinite(ref)
+    assert torch.equal(fin, torch.isfinite(got))
+    torch.testing.assert_close(got[fin], ref[fin], atol=1e-3, rtol=1e-3)
+
+
+def test_route_layer_vs_oracle():
+    _note("route layer L=2048")
+    L, Hq, Hkv, D = 2048, 28, 4, 128
+    q = _rand((1, L, Hq, D), 60).bfloat16()
+    rq = _rand((1, L, Hq, D), 61).bfloat16()
+    k, v = _planted_kv(L, Hkv, D, 62)
+    scale = torch.rand(Hq) + 0.5
+    valid = torch.ones(1, L, dtype=torch.bool)
+    valid[0, 700:705] = False
+    out, mid = mrsa.route_attention(q.to(DEV), k.to(DEV), v.to(DEV), rq.to(DEV), scale.to(DEV),
+                                    valid.to(DEV), return_intermediates=True)
+    ref, rmid = O.route_layer(q, k, v, rq, scale, valid)
+    _assert_close_attn(out, ref, "route layer")
+    agree = (mid["indices"].cpu().long() == rmid["indices"]).all(-1).float().mean()
+    print(f"route layer: index rows identical to oracle: {float(agree):.4f}", flush=True)
+    assert float(agree) > 0.98

@@ -1,0 +1,139 @@
+"""Pins the oracle's route scoring / top-k and route weights (CPU)."""
+
+import math
+
+import pytest
+import torch
+
+from oracle import mrsa_oracle as O
+
+
+def _brute_route(q5, lmk, lse4, bias4, drop, topk):
+    """Explicit loops: selection score, top-k with lower-index tie rule."""
+
+    B, L, H, G, D = q5.shape
+    C = lmk.shape[1]
+    idx = torch.full((B, L, H, topk), -1, dtype=torch.int64)
+    for b in range(B):
+        for i in range(L):
+            for h in range(H):
+                sel = []
+                for c in range(C):
+                    best = -math.inf
+                    for g in range(G):
+                        xs = []
+                        for cc in range(C):
+                            s = sum(float(q5[b, i, h, g, d]) * float(lmk[b, cc, h * G + g, d])
+                                    for d in range(D)) / math.sqrt(D)
+                            xs.append(s + float(bias4[b, cc, h, g]))
+                        m = max(xs)
+                        lse_h = m + math.log(sum(math.exp(x - m) for x in xs))
+                        a = float(lse4[b, i, h, g])
+                        mm = max(a, lse_h)
+                        tot = mm + math.log(math.exp(a - mm) + math.exp(lse_h - mm))
+                        best = max(best, xs[c] - tot)
+                    if drop[b, i, c]:
+                        best = -math.inf
+                    sel.append(best)
+                order = sorted(range(C), key=lambda c: (-sel[c], c))[:topk]
+                picks = sorted(c for c in order if sel[c] != -math.inf)
+                for j, c in enumerate(picks):
+                    idx[b, i, h, j] = c
+    return idx
+
+
+def _inputs(seed, B=1, L=6, H=2, G=3, D=8, C=9):
+    g = torch.Generator().manual_seed(seed)
+    q5 = torch.randn(B, L, H, G, D, generator=g).bfloat16()
+    lmk = torch.randn(B, C, H * G, D, generator=g).bfloat16()
+    lse4 = torch.randn(B, L, H, G, generator=g)
+    bias4 = torch.rand(B, C, H, G, generator=g)
+    drop = torch.rand(B, L, C, generator=g) < 0.25
+    return q5, lmk, lse4, bias4, drop
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_route_topk_matches_brute_force(seed):
+    q5, lmk, lse4, bias4, drop = _inputs(seed)
+    idx, scores, _ = O.route_topk(q5, lmk, lse4, 4, 64, drop_mask=drop.int(), bias4=bias4)
+    assert torch.equal(idx, _brute_route(q5, lmk, lse4, bias4, drop, 4))
+
+
+def test_route_topk_reference_properties():
+    # test_hils_non_power_two_topk.py:30-48: ascending picks, in range, raw scores.
+    g = torch.Generator().manual_seed(73)
+    q = torch.randn(1, 35, 28, 128, generator=g).bfloat16()
+    lm = torch.randn(1, 64, 4, 7, 128, generator=g).bfloat16()
+    idx, scores, _ = O.route_topk(
+        q.reshape(1, 35, 4, 7, 128), lm.reshape(1, 64, 28, 128),
+        torch.zeros(1, 35, 4, 7), 31, 64, drop_mask=torch.zeros(1, 35, 64, dtype=torch.int32),
+        bias4=torch.zeros(1, 64, 4, 7),
+    )
+    assert bool((idx >= 0).all()) and bool((idx < 64).all())
+    assert bool((idx[..., 1:] > idx[..., :-1]).all())
+    raw = torch.einsum("bqhgd,bchgd->bqhgc", q.float().reshape(1, 35, 4, 7, 128), lm.float()) / math.sqrt(128)
+    expect = torch.gather(raw, -1, idx[:, :, :, None, :].expand(-1, -1, -1, 7, -1))
+    torch.testing.assert_close(scores, expect, atol=1e-5, rtol=1e-5)
+
+
+def test_route_topk_drops_and_padding():
+    q5, lmk, lse4, bias4, _ = _inputs(5, C=6)
+    drop = torch.zeros(1, 6, 6, dtype=torch.int32)
+    drop[:, :, :4] = 1                       # only 2 chunks routable
+    idx, scores, _ = O.route_topk(q5, lmk, lse4, 4, 64, drop_mask=drop, bias4=bias4)
+    assert bool((idx[..., :2] >= 4).all()) and bool((idx[..., 2:] == -1).all())
+    assert bool(torch.isneginf(scores[..., 2:]).all())
+    idx8, _, _ = O.route_topk(q5, lmk, lse4, 8, 64, drop_mask=drop, bias4=bias4)   # topk > C
+    assert idx8.shape[-1] == 8 and bool((idx8[..., 2:] == -1).all())
+
+
+def test_route_topk_planted_chunk_and_pre_softmax():
+    q5, lmk, lse4, bias4, _ = _inputs(6, C=12)
+    bias4 = bias4.clone()
+    bias4[:, 7] = 50.0                       # chunk 7 dominates every head
+    idx, _, _ = O.route_topk(q5, lmk, lse4, 1, 64, bias4=bias4)
+    assert bool((idx == 7).all())
+    # pre_softmax with zero bias picks argmax_c max_g q.k
+    idx_pre, _, _ = O.route_topk(q5, lmk, None, 1, 64, selection_mode="pre_softmax")
+    raw = torch.einsum("blhgd,bchgd->blhgc", q5.float(), lmk.float().reshape(1, 12, 2, 3, 8))
+    assert torch.equal(idx_pre[..., 0], raw.max(dim=3).values.argmax(-1))
+
+
+def test_route_topk_tie_goes_to_lower_index():
+    q5 = torch.zeros(1, 2, 1, 2, 8).bfloat16()
+    lmk = torch.zeros(1, 10, 2, 8).bfloat16()       # every chunk scores the same
+    idx, _, sel = O.route_topk(q5, lmk, torch.zeros(1, 2, 1, 2), 3, 64)
+    assert idx[0, 0, 0].tolist() == [0, 1, 2]
+    assert bool((O.boundary_gap(sel, 3) == 0).all())
+
+
+def test_route_weights_sum_and_forms_agree():
+    g = torch.Generator().manual_seed(9)
+    B, L, H, G, K, C = 1, 5, 2, 7, 8, 20
+    scores = torch.randn(B, L, H * G, K, generator=g).bfloat16()
+    idx = torch.randint(0, C, (B, L, H, K), generator=g)
+    idx[0, 1, 0, 5:] = -1
+    bias = torch.rand(B, C, H, G, generator=g)
+    lse = torch.randn(B, L, H * G, generator=g)
+    rw, lw = O.route_weights(scores, idx, bias, lse)
+    # test_value_aware_fusion.py:13-29 -- total mass is one.
+    torch.testing.assert_close(rw.sum(-1) + lw, torch.ones_like(lw), atol=1e-5, rtol=0)
+    # test_force_remote.py:299-327 -- affine gate at scale 1, offset 0 equals the softmax.
+    rw2, lw2 = O.route_weights(scores, idx, bias, lse, gate_offset=0.0, gate_scale=1.0)
+    torch.testing.assert_close(rw, rw2, atol=1e-6, rtol=1e-5)
+    torch.testing.assert_close(lw, lw2, atol=1e-6, rtol=1e-5)
+    assert bool((rw[0, 1, :G, 5:] == 0).all())     # -1 slots carry no weight
+
+
+def test_route_weights_closed_form_and_all_masked():
+    scores = torch.tensor([[[[0.5, 0.0]]]]).bfloat16()        # [1,1,1,2]
+    idx = torch.tensor([[[[3, -1]]]])
+    bias = torch.zeros(1, 5, 1, 1)
+    bias[0, 3] = 0.25
+    lse = torch.tensor([[[1.0]]])
+    rw, lw = O.route_weights(scores, idx, bias, lse)
+    expect_local = 1.0 / (1.0 + math.exp(0.75 - 1.0))
+    assert abs(float(lw) - expect_local) < 1e-6 and float(rw[..., 1]) == 0.0
+    rw0, lw0 = O.route_weights(scores, torch.full_like(idx, -1), bias,
+                               torch.full((1, 1, 1), float("-inf")))
+    assert float(rw0.abs().sum()) == 0.0 and float(lw0) == 0.0
