@@ -1,0 +1,216 @@
+"""Benchmark: MRSA route-layer forward tokens/s at L=16384 on one MI355X.
+
+One step = one route-layer attention forward (value tiles, local window
+attention, landmark pool, route scoring + top-32, route weights, routed chunk
+attention, output fusion) over B=1, L=16384, 28 query / 4 KV heads, d=128,
+64-token chunks, local radius 256 on
+synthetic seeded Gaussian Q/K/V with a per-chunk planted key shift (sigma 0.3).
+Inputs are resident in HBM before timing starts.
+
+Prints ONE JSON line (rank 0).  Besides the contract fields it carries:
+  roofline      dominant kernel (routed chunk attention) against bf16 MFMA peak,
+                its average duration from HIP events around each launch in the
+                timed steps, HBM traffic per launch from profiles/pmc_traffic.json
+  cpu_baseline  the CPU oracle's route layer at configuration 1 (L=4096, fp32)
+                timed on this host's cores
+  stages_us     average per-stage times from the same events
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(
+    ROOT, "mask-routed-sparse-attention-for-long-context-diffusion-language-models_amd"
+)
+for _p in (PKG_DIR, ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "MRSA route-layer fwd tokens/s @16k (Dream-7B heads); % MFMA/HBM roofline"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+L_CFG2, HQ, HKV, D, CHUNK, TOPK, WINDOW = 16384, 28, 4, 128, 64, 32, 256
+
+
+def selected_flops(L: int) -> float:
+    """Algorithmic FLOPs of the routed chunk attention: QK^T + PV over every
+    routed (query head, chunk) pair, 64 keys per chunk (2 FLOP per MAC)."""
+
+    return 4.0 * D * HQ * L * TOPK * 64
+
+
+def make_inputs(L: int, seed: int, device, dtype):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(1, L, HQ, D, generator=g)
+    k = torch.randn(1, L, HKV, D, generator=g)
+    v = torch.randn(1, L, HKV, D, generator=g)
+    shift = 0.3 * torch.randn(L // CHUNK, HKV, D, generator=g)
+    k = k + shift.repeat_interleave(CHUNK, dim=0)[None]
+    return q.to(device=device, dtype=dtype), k.to(device=device, dtype=dtype), \
+        v.to(device=device, dtype=dtype)
+
+
+def cpu_baseline(budget_s: float = 20.0):
+    """Oracle route layer at BASELINE configuration 1 on the host CPU."""
+
+    import torch
+
+    from oracle import mrsa_oracle as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    L = 4096
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(1, L, HQ, D, generator=g)
+    k = torch.randn(1, L, HKV, D, generator=g)
+    v = torch.randn(1, L, HKV, D, generator=g)
+    k[:, CHUNK - 1 :: CHUNK] += 0.5    # landmark role offset
+    scale = torch.ones(HQ)
+    runs = []
+    t_end = time.perf_counter() + budget_s
+    while True:
+        t0 = time.perf_counter()
+        O.route_layer(q.bfloat16(), k.bfloat16(), v.bfloat16(), q.bfloat16(), scale)
+        runs.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end or len(runs) >= 3:
+            break
+    best = sorted(runs)[len(runs) // 2]
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": L / best,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{len(runs)} full route-layer forwards at L=4096 (config 1), fp32 CPU oracle, "
+                  f"median {best:.2f} s; cpu={cpu_model}",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
+              "the route layer shards by KV head / sequence as described in DESIGN.md",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    import mrsa
+
+    dev = torch.device("cuda:0")
+    q, k, v = make_inputs(L_CFG2, 1234, dev, torch.bfloat16)
+    route_q = q
+    scale = torch.ones(HQ, device=dev)
+    key_valid = torch.ones(1, L_CFG2, dtype=torch.bool, device=dev)
+    cfg = mrsa.RouteLayerConfig(local_window=WINDOW, chunk_size=CHUNK, topk=TOPK)
+
+    stream = torch.cuda.current_stream(dev)
+    stage_events = []
+
+    def run(record: bool):
+        evs = []
+        mark = None
+        if record:
+            def mark(name):
+                e = torch.cuda.Event(enable_timing=True)
+                e.record(stream)
+                evs.append((name, e))
+        out = mrsa.route_attention(q, k, v, route_q, scale, key_valid, cfg, mark=mark)
+        if record:
+            stage_events.append(evs)
+        return out
+
+    for _ in range(args.warmup):
+        run(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run(True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = 1000.0 * elapsed / args.steps
+
+    stages = {}
+    for evs in stage_events:
+        for (_, a), (name, b) in zip(evs[:-1], evs[1:]):
+            stages.setdefault(name, []).append(a.elapsed_time(b) * 1000.0)
+    stages_us = {n: sum(x) / len(x) for n, x in stages.items()}
+
+    sel_us = stages_us["selected_attention"]
+    achieved = selected_flops(L_CFG2) / (sel_us * 1e-6) / 1e12
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    if os.path.exists(tpath):
+        try:
+            traffic = json.load(open(tpath)).get("selected_attention_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    line = {
+        "metric": METRIC,
+        "value": L_CFG2 / (ms_per_step / 1000.0),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "MRSA route-layer attention forward (BASELINE config 2)",
+            "global_batch": 1,
+            "seq_len": L_CFG2,
+            "q_heads": HQ,
+            "kv_heads": HKV,
+            "head_dim": D,
+            "chunk_size": CHUNK,
+            "topk": TOPK,
+            "local_window": WINDOW,
+            "parallelism": "single-gpu",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "selected_attention (routed chunk attention)",
+            "achieved": achieved,
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / PEAK_BF16_TFLOPS,
+            "traffic": traffic,
+            "flops_per_launch": selected_flops(L_CFG2),
+            "avg_launch_us": sel_us,
+        },
+        "stages_us": stages_us,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

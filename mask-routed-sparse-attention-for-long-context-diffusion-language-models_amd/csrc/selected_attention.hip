@@ -61,15 +61,15 @@ struct SelArgs {
 
 // LDS carve-up of the selected-attention workgroup (byte offsets, 16-aligned).
 struct SelLayout {
-  size_t ks, vs, umask, ulist, omask, comp_idx, comp_slot, comp_len, misc, kvbits, total;
+  size_t ks, vs, umask, ulist, omask, comp_idx, comp_slot, comp_len, misc, kvbits, wts, total;
 };
 __host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
 __host__ __device__ inline SelLayout sel_layout(int TQ, int K, int64_t Ck) {
   SelLayout l;
   const size_t n = (size_t)TQ * K;
   size_t o = 0;
-  l.ks = o;        o = align16(o + (size_t)64 * kKPitch * 2);
-  l.vs = o;        o = align16(o + (size_t)128 * kVPitch * 2);
+  l.ks = o;        o = align16(o + 2 * (size_t)64 * kKPitch * 2);   // two buffers
+  l.vs = o;        o = align16(o + 2 * (size_t)128 * kVPitch * 2);
   l.umask = o;     o = align16(o + n * 8);
   l.ulist = o;     o = align16(o + n * 4);
   l.omask = o;     o = align16(o + (size_t)Ck * 8);
@@ -77,12 +77,13 @@ __host__ __device__ inline SelLayout sel_layout(int TQ, int K, int64_t Ck) {
   l.comp_slot = o; o = align16(o + n);
   l.comp_len = o;  o = align16(o + (size_t)TQ * 4);
   l.misc = o;      o = align16(o + (size_t)(4 + kThreads) * 4);
-  l.kvbits = o;    o = align16(o + 8);
+  l.kvbits = o;    o = align16(o + (size_t)Ck * 8);   // per-chunk key-valid bits
+  l.wts = o;       o = align16(o + (size_t)TQ * 8 * K * 2);  // [TQ][8][K] bf16 weights
   l.total = o;
   return l;
 }
 
-template <int NTILE>
+template <int NTILE, bool TOKEN>
 __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
   constexpr int QPW = 2 * NTILE;      // queries per wave
   constexpr int TQ = kWaves * QPW;    // queries per workgroup (<= 64)
@@ -99,7 +100,8 @@ __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
   uint8_t* comp_slot = smem + lay.comp_slot;                           // [TQ][K]
   int32_t* comp_len = reinterpret_cast<int32_t*>(smem + lay.comp_len);  // [TQ]
   int32_t* misc = reinterpret_cast<int32_t*>(smem + lay.misc);  // [0] unsorted, [1] steps, [4..] scan
-  uint64_t* kvbits = reinterpret_cast<uint64_t*>(smem + lay.kvbits);
+  uint64_t* kvbits = reinterpret_cast<uint64_t*>(smem + lay.kvbits);  // [Ck]
+  uint16_t* wts = reinterpret_cast<uint16_t*>(smem + lay.wts);          // [TQ][8][K]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -194,6 +196,21 @@ __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
   __syncthreads();
   const int nsteps = misc[1];
 
+  // Per-chunk key-valid bits and this tile's routing weights, staged once.
+  for (int64_t c = wave; c < Ck; c += kWaves) {
+    const bool ok = a.key_valid ? a.key_valid[b * a.Lk + c * 64 + lane] != 0 : true;
+    const uint64_t vb = __ballot(ok);
+    if (lane == 0) kvbits[c] = vb;
+  }
+  if (!TOKEN) {
+    for (int e = tid; e < TQ * 8 * K; e += kThreads) {
+      const int qq = e / (8 * K), rem = e - qq * 8 * K;
+      const int gg = rem / K, kk = rem - gg * K;
+      const int64_t qi = q0 + qq;
+      wts[e] = (qi < a.Lq && gg < G) ? a.w[((b * a.Lq + qi) * a.Hq + h * G + gg) * K + kk] : 0;
+    }
+  }
+
   // 3. Q^T operands for this wave's queries (2 per column tile, 8 columns each).
   u32x4_t Qb[NTILE][4];
   f32x4_t acc[NTILE][8];
@@ -216,65 +233,55 @@ __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
     for (int td = 0; td < 8; ++td) acc[nt][td] = zero4();
   }
 
-  // Uniform (scalar) chunk bases plus 32-bit per-lane offsets.
+  // Staging: uniform (scalar) chunk bases plus per-lane 32-bit offsets.
   const uint16_t* kbase = a.k + (b * a.Lk) * (int64_t)a.Hkv * 128 + (int64_t)h * 128;
   const uint16_t* vbase =
-      a.token_mode ? nullptr : a.vt + ((b * a.Hkv + h) * a.NTk) * (int64_t)(128 * 64);
+      TOKEN ? nullptr : a.vt + ((b * a.Hkv + h) * a.NTk) * (int64_t)(128 * 64);
   const int kstride = a.Hkv * 128;
-  uint32_t goff[kPer], loff[kPer];
-#pragma unroll
-  for (int p = 0; p < kPer; ++p) {
-    const int v = tid + p * kThreads;
-    if (v < 1024) {
-      const int s = v >> 4, part = v & 15;
-      goff[p] = (uint32_t)(s * kstride + part * 8);
-      loff[p] = (uint32_t)(s * kKPitch + part * 8);
-    } else {
-      const int d = (v - 1024) >> 3, part = (v - 1024) & 7;
-      goff[p] = (uint32_t)((v - 1024) * 8);
-      loff[p] = (uint32_t)(d * kVPitch + part * 8);
-    }
-  }
   u32x4_t pre[kPer];
   auto prefetch = [&](int64_t c) {
     const uint16_t* kc = kbase + c * 64 * (int64_t)kstride;
-    const uint16_t* vc = a.token_mode ? nullptr : vbase + c * (128 * 64);
+    const uint16_t* vc = TOKEN ? nullptr : vbase + c * (128 * 64);
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
       const int v = tid + p * kThreads;
       if (v < 1024) {
-        pre[p] = *reinterpret_cast<const u32x4_t*>(kc + goff[p]);
-      } else if (!a.token_mode) {
-        pre[p] = *reinterpret_cast<const u32x4_t*>(vc + goff[p]);
+        pre[p] = *reinterpret_cast<const u32x4_t*>(kc + (v >> 4) * kstride + (v & 15) * 8);
+      } else if (!TOKEN) {
+        pre[p] = *reinterpret_cast<const u32x4_t*>(vc + (v - 1024) * 8);
       } else {
         u32x4_t z = {0u, 0u, 0u, 0u};
         pre[p] = z;
       }
     }
   };
-  if (nsteps > 0) prefetch(ulist[0]);
-
-  const uint64_t last_mask = a.mask_last ? (1ull << 63) : 0ull;
-  for (int st = 0; st < nsteps; ++st) {
-    const int64_t c = ulist[st];
-    const uint64_t om = umask[st];
-    __syncthreads();
+  auto commit = [&](int buf) {
+    uint16_t* Kb = Ks + buf * (64 * kKPitch);
+    uint16_t* Vb = Vs + buf * (128 * kVPitch);
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
       const int v = tid + p * kThreads;
-      *reinterpret_cast<u32x4_t*>((v < 1024 ? Ks : Vs) + loff[p]) = pre[p];
+      if (v < 1024)
+        *reinterpret_cast<u32x4_t*>(Kb + (v >> 4) * kKPitch + (v & 15) * 8) = pre[p];
+      else
+        *reinterpret_cast<u32x4_t*>(Vb + ((v - 1024) >> 3) * kVPitch + ((v - 1024) & 7) * 8) = pre[p];
     }
-    if (wave == 0) {
-      const bool ok = a.key_valid ? a.key_valid[b * a.Lk + c * 64 + lane] != 0 : true;
-      const uint64_t vb = __ballot(ok);
-      if (lane == 0) kvbits[0] = vb;
-    }
-    __syncthreads();
-    if (st + 1 < nsteps) prefetch(ulist[st + 1]);
+  };
+  if (nsteps > 0) {
+    prefetch(ulist[0]);
+    commit(0);
+  }
+  __syncthreads();
 
-    const uint64_t masked = (~kvbits[0]) | last_mask;  // keys excluded from the softmax
+  const uint64_t last_mask = a.mask_last ? (1ull << 63) : 0ull;
+  for (int st = 0; st < nsteps; ++st) {
+    const int buf = st & 1;
+    const uint64_t om = umask[st];
+    const uint64_t masked = (~kvbits[ulist[st]]) | last_mask;  // keys excluded from the softmax
+    if (st + 1 < nsteps) prefetch(ulist[st + 1]);
+    const uint16_t* Kb = Ks + buf * (64 * kKPitch);
+    const uint16_t* Vb = Vs + buf * (128 * kVPitch);
     const uint32_t wbits = (uint32_t)((om >> (wave * QPW)) & ((1ull << QPW) - 1ull));
-    if (wbits == 0u) continue;
 
 #pragma unroll
     for (int nt = 0; nt < NTILE; ++nt) {
@@ -284,6 +291,12 @@ __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
       const bool owns = (pair >> half) & 1u;
       const int ql = wave * QPW + 2 * nt + half;
       const int64_t qi = q0 + ql;
+      // Opaque zero: keeps the compiler from hoisting this tile's K / V operand
+      // reads out of the tile loop (that would pin 128 extra registers).
+      int zoff = 0;
+      asm volatile("" : "+v"(zoff));
+      const uint16_t* Kt = Kb + zoff;
+      const uint16_t* Vt = Vb + zoff;
 
       f32x4_t S[4];
 #pragma unroll
@@ -293,10 +306,9 @@ __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const u32x4_t Ka =
-              *reinterpret_cast<const u32x4_t*>(Ks + (16 * t + col) * kKPitch + 32 * j + 8 * grp);
+              *reinterpret_cast<const u32x4_t*>(Kt + (16 * t + col) * kKPitch + 32 * j + 8 * grp);
           S[t] = mfma_bf16_16x16x32(Ka, Qb[nt][j], S[t]);
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
       int slot = 0;
       if (owns) {
@@ -304,7 +316,7 @@ __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
         ++rank[nt];
       }
 
-      if (a.token_mode) {
+      if constexpr (TOKEN) {
         // max over the query's G head columns (lanes sharing col >> 3).
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -332,8 +344,7 @@ __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
         continue;
       }
 
-      float wv = 0.f;
-      if (owns && gg < G) wv = bf16_to_f32(a.w[((b * a.Lq + qi) * a.Hq + h * G + gg) * K + slot]);
+      const float wv = owns ? bf16_to_f32(wts[(ql * 8 + gg) * K + slot]) : 0.f;
       float mx = neg_inf();
 #pragma unroll
       for (int t = 0; t < 4; ++t)
@@ -346,42 +357,42 @@ __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
           mx = fmaxf(mx, v);
         }
       mx = across4_max(mx);
-      float pv[4][4];
       float sum = 0.f;
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float p = (mx == neg_inf()) ? 0.f : exp2f(S[t][i] - mx);
-          pv[t][i] = p;
+          S[t][i] = p;
           sum += p;
         }
       sum = across4_sum(sum);
-      const float f = (sum > 0.f && owns) ? wv / sum : 0.f;
+      const float f = (sum > 0.f) ? wv / sum : 0.f;
       u32x4_t Pb[2];
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        Pb[jj][0] = pack_bf16x2(pv[2 * jj][0] * f, pv[2 * jj][1] * f);
-        Pb[jj][1] = pack_bf16x2(pv[2 * jj][2] * f, pv[2 * jj][3] * f);
-        Pb[jj][2] = pack_bf16x2(pv[2 * jj + 1][0] * f, pv[2 * jj + 1][1] * f);
-        Pb[jj][3] = pack_bf16x2(pv[2 * jj + 1][2] * f, pv[2 * jj + 1][3] * f);
+        Pb[jj][0] = pack_bf16x2(S[2 * jj][0] * f, S[2 * jj][1] * f);
+        Pb[jj][1] = pack_bf16x2(S[2 * jj][2] * f, S[2 * jj][3] * f);
+        Pb[jj][2] = pack_bf16x2(S[2 * jj + 1][0] * f, S[2 * jj + 1][1] * f);
+        Pb[jj][3] = pack_bf16x2(S[2 * jj + 1][2] * f, S[2 * jj + 1][3] * f);
       }
 #pragma unroll
       for (int td = 0; td < 8; ++td) {
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
-          const uint16_t* vrow = Vs + (16 * td + col) * kVPitch + 32 * jj + 4 * grp;
+          const uint16_t* vrow = Vt + (16 * td + col) * kVPitch + 32 * jj + 4 * grp;
           const u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(vrow);
           const u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(vrow + 16);
           u32x4_t Va = {v0[0], v0[1], v1[0], v1[1]};
           acc[nt][td] = mfma_bf16_16x16x32(Va, Pb[jj], acc[nt][td]);
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
+    if (st + 1 < nsteps) commit(buf ^ 1);
+    __syncthreads();
   }
 
-  if (a.token_mode) return;
+  if constexpr (TOKEN) return;
 #pragma unroll
   for (int nt = 0; nt < NTILE; ++nt) {
     const int ql = wave * QPW + 2 * nt + (col >> 3);
@@ -413,7 +424,7 @@ int launch_selected(SelArgs& a, hipStream_t s) {
   constexpr int TQ = kWaves * 2 * kNtile;
   const size_t smem = sel_layout(TQ, a.K, a.Ck).total;
   if (smem > 160 * 1024) return MRSA_ERR_UNSUPPORTED;
-  auto kern = selected_attn_kernel<kNtile>;
+  auto kern = a.token_mode ? selected_attn_kernel<kNtile, true> : selected_attn_kernel<kNtile, false>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
     return MRSA_ERR_LAUNCH;

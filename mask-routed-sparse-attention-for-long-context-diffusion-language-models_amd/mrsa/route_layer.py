@@ -74,12 +74,19 @@ def route_attention(
     key_valid: torch.Tensor | None = None,
     cfg: RouteLayerConfig = RouteLayerConfig(),
     return_intermediates: bool = False,
+    mark=None,
 ):
     """Route-layer attention: q, route_q [B, L, Hq, D], k, v [B, L, Hkv, D] bf16.
 
     Returns the fused output [B, L, Hq, D] bf16 (and a dict of the stage
-    outputs when return_intermediates).
+    outputs when return_intermediates).  ``mark(stage)``, when given, is
+    called after each stage is enqueued (stage timing with stream events).
     """
+
+    def _mark(name):
+        if mark is not None:
+            mark(name)
+
 
     _check_qkv(q, k, v, route_q)
     B, L, Hq, D = q.shape
@@ -94,16 +101,20 @@ def route_attention(
     else:
         kv_bool = key_valid.to(device=q.device, dtype=torch.bool).contiguous()
 
+    _mark("start")
     vt = value_tiles(v)
+    _mark("value_tiles")
     flash_window = cfg.local_window + S - 1 if cfg.skip_inert_slots else cfg.local_window
     local_out, local_lse = local_attention_launch(
         q, k, vt, kv_bool, flash_window, S if cfg.skip_inert_slots else 0
     )
+    _mark("local_attention")
     q_lmk = route_q[:, S - 1 :: S].reshape(B, C, Hkv, G, D)
     k_chunked = k.reshape(B, C, S, Hkv, D)
     lmk, entropy, prior = chunk_attn_pool_gqa_prior(
         q_lmk, k_chunked, kv_bool.reshape(B, C, S), entropy_bias_scale
     )
+    _mark("pool")
     indices, scores = route_topk_launch(
         route_q.reshape(B, L, Hkv, G, D),
         lmk.reshape(B, C, Hq, D),
@@ -115,12 +126,16 @@ def route_attention(
         key_valid=kv_bool,
     )
     scores = scores.reshape(B, L, Hq, cfg.topk)
+    _mark("route_topk")
     remote_w, local_w = route_weights_launch(
         scores, indices, prior, local_lse, temperature=cfg.temperature,
         gate_offset=cfg.gate_offset, gate_scale=cfg.gate_scale,
     )
+    _mark("route_weights")
     remote_out = selected_attention_launch(q, k, vt, remote_w, indices, kv_bool, S)
+    _mark("selected_attention")
     out = fuse_hils_outputs(remote_out, local_out, local_w)
+    _mark("fusion")
     if not return_intermediates:
         return out
     return out, {
