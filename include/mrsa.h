@@ -138,7 +138,9 @@ int mrsa_route_weights_fwd(const void* scores, const int32_t* indices, const flo
 /*
  * Re-lays V out as 64-key tiles, each stored transposed (head_dim rows of 64
  * keys), so both attention kernels can feed V to the matrix cores with
- * contiguous loads.  Keys past seq_len inside the last tile are zero.
+ * contiguous 16-byte loads.  Keys past seq_len inside the last tile are zero.
+ * Inside a tile row, key 32a + 16b + 4c + e (a, b in {0,1}; c, e in 0..3)
+ * sits at position 32a + 8c + 4b + e (matrix-core operand order).
  *   v: bf16 [batch, seq_len, kv_heads, head_dim]
  *   v_tiles (out): bf16 [batch, kv_heads, ceil(seq_len / 64), head_dim, 64]
  * No reference counterpart: internal layout step of the two attention ops.
@@ -162,6 +164,7 @@ int mrsa_value_tiles(const void* v, int64_t batch, int64_t seq_len, int64_t kv_h
  *   key_valid: optional bool [batch, kv_len];  query_positions: optional int64 [q_len]
  *   (NULL = query row i sits at position i)
  *   out: bf16 [batch, q_len, q_heads, head_dim];  lse: fp32 [batch, q_len, q_heads]
+ *   sm_scale: finite and > 0 (MRSA_ERR_INVALID_ARGUMENT otherwise)
  * Limits: head_dim == 128, q_heads / kv_heads <= 8.
  */
 int mrsa_local_attention_fwd(const void* q, const void* k, const void* v_tiles,
@@ -186,6 +189,7 @@ int mrsa_local_attention_fwd(const void* q, const void* k, const void* v_tiles,
  *            >= kv_len / chunk_size are skipped)
  *   key_valid: optional bool [batch, kv_len]
  *   out: bf16 [batch, q_len, q_heads, head_dim]
+ *   sm_scale: finite and > 0 (MRSA_ERR_INVALID_ARGUMENT otherwise)
  * Limits: chunk_size == 64, head_dim == 128, q_heads / kv_heads <= 8, topk <= 64.
  */
 int mrsa_selected_attention_fwd(const void* q, const void* k, const void* v_tiles,

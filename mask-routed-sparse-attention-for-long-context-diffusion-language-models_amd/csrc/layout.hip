@@ -32,7 +32,16 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// v[b, j, h, :] -> v_tiles[b, h, j / 64, :, j % 64]
+// v[b, j, h, :] -> v_tiles[b, h, j / 64, :, tile_pos(j % 64)].
+// Within a 64-key tile, key 32a + 16b + 4c + e (a, b in {0,1}; c, e in 0..3)
+// is stored at position 32a + 8c + 4b + e: the eight keys one lane feeds to
+// a 32-deep matrix-core reduction (keys 4c..4c+3 and 16+4c..16+4c+3 of a
+// 32-key half, the order in which the S^T accumulator hands them out) are
+// then 16 contiguous bytes.
+__device__ __forceinline__ int tile_key_of_pos(int p) {
+  return (p & 32) | (((p >> 2) & 1) << 4) | (((p >> 3) & 3) << 2) | (p & 3);
+}
+
 __global__ void __launch_bounds__(256)
     value_tiles_kernel(const uint16_t* __restrict__ v, int64_t L, int64_t H, int D, int64_t NT,
                        uint16_t* __restrict__ vt) {
@@ -51,10 +60,10 @@ __global__ void __launch_bounds__(256)
   __syncthreads();
   uint16_t* dst = vt + ((b * H + h) * NT + t) * (int64_t)D * 64;
   for (int e = threadIdx.x; e < D * 32; e += blockDim.x) {
-    const int d = e >> 5, s2 = e & 31;
-    const uint32_t w = (uint32_t)tile[(2 * s2) * pitch + d] |
-                       ((uint32_t)tile[(2 * s2 + 1) * pitch + d] << 16);
-    *reinterpret_cast<uint32_t*>(dst + d * 64 + 2 * s2) = w;
+    const int d = e >> 5, p2 = e & 31;
+    const int key = tile_key_of_pos(2 * p2);  // key + 1 sits at position 2 * p2 + 1
+    const uint32_t w = (uint32_t)tile[key * pitch + d] | ((uint32_t)tile[(key + 1) * pitch + d] << 16);
+    *reinterpret_cast<uint32_t*>(dst + d * 64 + 2 * p2) = w;
   }
 }
 

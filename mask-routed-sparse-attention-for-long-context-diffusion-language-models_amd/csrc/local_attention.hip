@@ -214,50 +214,74 @@ __global__ void __launch_bounds__(64 * G) local_attn_kernel(LocalArgs a) {
       __builtin_amdgcn_sched_barrier(0);
     }
 
+    // Logits in units of log2: s * scale_log2.  Keys outside the window (or
+    // past kv_len, or of an absent query) are -inf; inert keys inside it are
+    // exactly 0.  The scale is folded into one FMA before the exponential
+    // (scale_log2 > 0, so the maximum of the raw products is the maximum of
+    // the logits).
+    const float c = a.scale_log2;
+    const uint64_t kLast = 1ull << 63;
     u32x4_t Pb[2][2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      float mx = neg_inf();
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int s = 16 * t + 4 * grp + i;
-          float v = S[nt][t][i] * a.scale_log2;
-          if (!full) {
-            const int dd = rel[nt] + s;
-            if (!((rbits >> s) & 1ull) || dd > W32 || dd < -W32 || !qok[nt]) v = neg_inf();
-          }
-          if (((ibits >> s) & 1ull) && v != neg_inf()) v = 0.f;
-          S[nt][t][i] = v;
-          mx = fmaxf(mx, v);
-        }
-      mx = across4_max(mx);
-      const float m_new = fmaxf(m_run[nt], mx);
-      float alpha = 1.f, rsum = 0.f;
-      float pv[4][4];
-      if (m_new == neg_inf()) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) pv[t][i] = 0.f;
-      } else {
-        alpha = exp2f(m_run[nt] - m_new);
+      if (!full) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int s = 16 * t + 4 * grp + i;
-            const float p = exp2f(S[nt][t][i] - m_new);
-            rsum += p;
-            pv[t][i] = ((ibits >> s) & 1ull) ? 0.f : p;
+            const int dd = rel[nt] + s;
+            if (!((rbits >> s) & 1ull) || dd > W32 || dd < -W32 || !qok[nt])
+              S[nt][t][i] = neg_inf();
           }
       }
-      rsum = across4_sum(rsum);
+      if (ibits == kLast) {
+        // Only the tile's last slot is inert (the landmark of a 64-key chunk).
+        if (grp == 3 && S[nt][3][3] != neg_inf()) S[nt][3][3] = 0.f;
+      } else if (ibits != 0ull) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int s = 16 * t + 4 * grp + i;
+            if (((ibits >> s) & 1ull) && S[nt][t][i] != neg_inf()) S[nt][t][i] = 0.f;
+          }
+      }
+      float mx = fmaxf(fmaxf(S[nt][0][0], S[nt][0][1]), fmaxf(S[nt][0][2], S[nt][0][3]));
+#pragma unroll
+      for (int t = 1; t < 4; ++t)
+        mx = fmaxf(mx, fmaxf(fmaxf(S[nt][t][0], S[nt][t][1]), fmaxf(S[nt][t][2], S[nt][t][3])));
+      mx = across4_max(mx);
+      const float m_new = fmaxf(m_run[nt], mx * c);
+      // A column with no visible key yet keeps m = -inf; exponentiate against 0
+      // there so that every term (and alpha) is exp2(-inf) = 0.
+      const float m_use = m_new == neg_inf() ? 0.f : m_new;
+      const float alpha = exp2_hw(m_run[nt] - m_use);
+      float pv[4][4];
+      float part[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pv[t][i] = exp2_hw(__builtin_fmaf(S[nt][t][i], c, -m_use));
+        part[t] = (pv[t][0] + pv[t][1]) + (pv[t][2] + pv[t][3]);
+      }
+      const float rsum = across4_sum((part[0] + part[1]) + (part[2] + part[3]));
+      // Inert keys count in the denominator but carry zero V.
+      if (ibits == kLast) {
+        if (grp == 3) pv[3][3] = 0.f;
+      } else if (ibits != 0ull) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if ((ibits >> (16 * t + 4 * grp + i)) & 1ull) pv[t][i] = 0.f;
+      }
       l_run[nt] = l_run[nt] * alpha + rsum;
       m_run[nt] = m_new;
+      if (!__all(alpha == 1.f)) {
 #pragma unroll
-      for (int td = 0; td < 8; ++td) acc[nt][td] *= alpha;
+        for (int td = 0; td < 8; ++td) acc[nt][td] *= alpha;
+      }
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
         u32x4_t pb;
@@ -269,14 +293,14 @@ __global__ void __launch_bounds__(64 * G) local_attn_kernel(LocalArgs a) {
       }
     }
 
+    // V^T rows hold each lane's eight reduction keys contiguously (tiled V
+    // layout), so one 16-byte read per operand.
 #pragma unroll
     for (int td = 0; td < 8; ++td) {
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        const uint16_t* vrow = Vs + (16 * td + col) * kVPitch + 32 * jj + 4 * grp;
-        const u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(vrow);
-        const u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(vrow + 16);
-        u32x4_t Va = {v0[0], v0[1], v1[0], v1[1]};
+        const u32x4_t Va =
+            *reinterpret_cast<const u32x4_t*>(Vs + (16 * td + col) * kVPitch + 32 * jj + 8 * grp);
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) acc[nt][td] = mfma_bf16_16x16x32(Va, Pb[nt][jj], acc[nt][td]);
       }
@@ -319,7 +343,8 @@ extern "C" int mrsa_local_attention_fwd(const void* q, const void* k, const void
                                         int64_t window, int64_t inert_chunk, float sm_scale,
                                         void* out, float* lse, void* stream) {
   if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 ||
-      q_heads % kv_heads != 0 || head_dim <= 0 || window < 0 || inert_chunk < 0)
+      q_heads % kv_heads != 0 || head_dim <= 0 || window < 0 || inert_chunk < 0 ||
+      !(sm_scale > 0.f) || sm_scale == __builtin_inff())
     return MRSA_ERR_INVALID_ARGUMENT;
   if (batch == 0 || q_len == 0) return MRSA_OK;
   if (kv_len == 0 || !q || !k || !v_tiles || !out || !lse) return MRSA_ERR_INVALID_ARGUMENT;

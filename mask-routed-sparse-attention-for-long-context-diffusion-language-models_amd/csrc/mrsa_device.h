@@ -74,17 +74,44 @@ __device__ __forceinline__ int group16_sum_i(int v) {
   for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
-// Reductions across the four lane groups (lanes sharing l % 16).
+// Reductions across the four lane groups (lanes sharing l % 16), with the
+// gfx950 row-swap instructions: v_permlane32_swap exchanges the upper half of
+// one operand with the lower half of the other, so swapping a value with
+// itself leaves lane l holding the values of lanes l and l ^ 32 in the two
+// results (v_permlane16_swap likewise pairs lanes l and l ^ 16).  Pure VALU,
+// no LDS round trip.
+__device__ __forceinline__ void pair32(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void pair16(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
 __device__ __forceinline__ float across4_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
+  float a, b;
+  pair32(v, a, b);
+  pair16(fmaxf(a, b), a, b);
+  return fmaxf(a, b);
 }
 __device__ __forceinline__ float across4_sum(float v) {
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+  float a, b;
+  pair32(v, a, b);
+  pair16(a + b, a, b);
+  return a + b;
 }
+
+// 2^x with the hardware instruction (v_exp_f32): exact at 0, 2^-inf = 0;
+// results below the normal range flush to zero, which no caller can observe
+// after bf16 rounding of probabilities that are normalised to at most 1.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// 1/x with the hardware reciprocal (1 ulp).
+__device__ __forceinline__ float rcp_hw(float x) { return __builtin_amdgcn_rcpf(x); }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

@@ -14,19 +14,21 @@
 // its 8 waves owns 6 of those queries (3 column tiles of 2 queries x 8 head
 // columns), whose output accumulators stay in registers for the whole
 // kernel.  The workgroup walks the union of the tile's routed chunks in
-// ascending order.  Each chunk's K and V^T (32 KB) arrive in a 3-slot LDS ring
-// by asynchronous global->LDS DMA issued two chunks ahead, so the only
-// per-chunk synchronisation is one workgroup barrier.  Every wave with a query
-// routed to the chunk consumes it:
+// ascending order.  Each chunk's K and V^T (32 KB) arrive in an R-slot LDS
+// ring by asynchronous global->LDS DMA issued R - CPS chunks ahead; one
+// workgroup barrier covers CPS consecutive chunks.  Every wave with a query
+// routed to a chunk consumes it:
 //   S^T = K_chunk (64 x 128) . Q^T (2 queries x 8 head columns)   16 MFMAs
 //   per-column softmax over the 64 keys, scaled by the routing weight
 //   O^T += V_chunk^T (128 x 64) . P^T                            16 MFMAs
 // Columns of queries that do not own the chunk get P = 0.
 //
-// Ring slot layout (16-byte units, XOR-swizzled so the matrix-operand reads of
-// 16 consecutive rows hit distinct banks):
+// Ring slot layout (16-byte units, XOR-swizzled so that the matrix-operand
+// reads of 8 consecutive lanes hit distinct banks):
 //   K   row r (64 keys),  part p (8 dims):  unit r*16 + (p ^ (r & 15))
 //   V^T row d (128 dims), part p (8 keys):  unit 1024 + d*8 + (p ^ (d & 7))
+// V^T parts hold keys in the tiled-V operand order, so part 4*jj + g is
+// exactly the 8 reduction keys lane group g feeds to the jj-th PV product.
 //
 // Token-score mode (candidate_token_scores_gqa,
 // ops/hils_token_score_gqa_tilelang.py:17-114) reuses the walk and the S^T
@@ -34,18 +36,38 @@
 // times sm_scale for every key, -inf at the last slot and invalid keys.
 #include "mrsa_device.h"
 
+#include <type_traits>
+#include <utility>
+
 using namespace mrsa;
 
 namespace {
 
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kNtile = 3;               // column tiles per wave
-constexpr int kQPW = 2 * kNtile;        // queries per wave
-constexpr int kTQ = kWaves * kQPW;      // queries per workgroup
+constexpr int kDmaWaves = 8;            // waves 0-3 fetch K, 4-7 fetch V^T
 constexpr int kSlotBytes = 32768;       // one chunk: K (16 KB) + V^T (16 KB)
-constexpr int kRing = 3;
 constexpr int kMaxTopk = 64;
+constexpr size_t kMaxLds = 160 * 1024;
+#ifndef MRSA_SEL_CPS4
+#define MRSA_SEL_CPS4 2                 // chunks per barrier with a 4-slot ring
+#endif
+#ifndef MRSA_SEL_WAVES
+#define MRSA_SEL_WAVES 8                // work split: 8 (8 waves x 3 tiles), 82 (8 x 2), 12 (12 x 2)
+#endif
+
+// Work split: NW waves, each owning NT column tiles of 2 queries x 8 head
+// columns; TQ queries per workgroup (at most 64: owner sets are 64-bit masks).
+template <int NW, int NT>
+struct Split {
+  static constexpr int kWaves = NW;
+  static constexpr int kThreads = 64 * NW;
+  static constexpr int kNtile = NT;
+  static constexpr int kQPW = 2 * NT;
+  static constexpr int kTQ = NW * 2 * NT;
+  static_assert(kTQ <= 64 && NW >= kDmaWaves, "work split");
+};
+using Split8 = Split<8, 3>;
+using Split8x2 = Split<8, 2>;
+using Split12 = Split<12, 2>;
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -68,40 +90,50 @@ struct SelArgs {
   float* tscores;
 };
 
-// LDS carve-up (byte offsets, 16-aligned).  comp_idx lives inside the ring: it
-// is only needed before the first chunk is loaded.
+// LDS carve-up (byte offsets, 16-aligned).  The p_* arrays are only used by
+// the prologue and live inside the ring, which is free until the first DMA.
 struct SelLayout {
-  size_t ring, wts, kvbits, omask, ulist, umask, comp_slot, comp_len, misc, total;
-  size_t comp_idx;
+  size_t ring, wr, s_chunk, s_own, s_mask, comp_slot, misc, total;
+  size_t p_idx, p_kv, p_omask, p_len, p_w, p_end;
   int cap;
 };
 __host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
-__host__ __device__ inline SelLayout sel_layout(int K, int64_t Ck) {
+__host__ __device__ inline SelLayout sel_layout(int TQ, int NW, int K, int64_t Ck, int R,
+                                                bool token) {
   SelLayout l;
-  const size_t n = (size_t)kTQ * K;
+  const size_t n = (size_t)TQ * K;
+  const size_t wbytes = token ? 0 : (size_t)TQ * 8 * K * 2;
   l.cap = (int)(Ck < (int64_t)n ? Ck : (int64_t)n);
   size_t o = 0;
-  l.ring = o;      o = align16(o + (size_t)kRing * kSlotBytes);
-  l.wts = o;       o = align16(o + (size_t)kTQ * 8 * K * 2);   // [TQ][8][K] bf16
-  l.kvbits = o;    o = align16(o + (size_t)Ck * 8);
-  l.omask = o;     o = align16(o + (size_t)Ck * 8);
-  l.ulist = o;     o = align16(o + (size_t)l.cap * 4);
-  l.umask = o;     o = align16(o + (size_t)l.cap * 8);
+  l.ring = o;      o = align16(o + (size_t)R * kSlotBytes);
+  l.wr = o;        o = align16(o + wbytes);                 // [TQ][K][8] bf16, list order
+  l.s_chunk = o;   o = align16(o + (size_t)l.cap * 4);
+  l.s_own = o;     o = align16(o + (size_t)l.cap * 8);
+  l.s_mask = o;    o = align16(o + (size_t)l.cap * 8);
   l.comp_slot = o; o = align16(o + n);
-  l.comp_len = o;  o = align16(o + (size_t)kTQ * 4);
-  l.misc = o;      o = align16(o + (size_t)(4 + kThreads) * 4);
+  l.misc = o;      o = align16(o + (size_t)(NW + 4) * 4);
   l.total = o;
-  l.comp_idx = l.ring;
+  o = l.ring;
+  l.p_idx = o;     o = align16(o + n * 4);
+  l.p_kv = o;      o = align16(o + (size_t)Ck * 8);
+  l.p_omask = o;   o = align16(o + (size_t)Ck * 8);
+  l.p_len = o;     o = align16(o + (size_t)TQ * 4);
+  l.p_w = o;       o = align16(o + wbytes);                 // [TQ][8][K] bf16, slot order
+  l.p_end = o;
   return l;
 }
+__host__ __device__ inline bool sel_layout_fits(const SelLayout& l, int R) {
+  return l.total <= kMaxLds && l.p_end <= l.ring + (size_t)R * kSlotBytes;
+}
 
-// Barrier for the chunk ring.  __syncthreads() would also wait for every
-// outstanding global access of the wave (vmcnt(0)), including the DMA of the
-// chunk being prefetched; this waits only for this wave's DMA of the chunk
-// about to be consumed (each wave issues 4 DMA instructions per chunk) and for
-// its LDS accesses, then synchronises the workgroup.
-__device__ __forceinline__ void ring_barrier(bool leave_one_chunk) {
-  if (leave_one_chunk)
+// Waits until at most n chunk DMAs of this wave (4 instructions each) are in
+// flight and its LDS accesses are done, then synchronises the workgroup.
+// __syncthreads() would wait for every outstanding load (vmcnt(0)), including
+// the chunks being prefetched.
+__device__ __forceinline__ void ring_barrier(int n) {
+  if (n >= 2)
+    asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+  else if (n == 1)
     asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
   else
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
@@ -109,22 +141,65 @@ __device__ __forceinline__ void ring_barrier(bool leave_one_chunk) {
   asm volatile("" ::: "memory");
 }
 
-template <bool TOKEN>
-__global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
+// Matrix-operand reads from LDS with explicit waits.  With global->LDS DMA in
+// the same loop the compiler waits for every outstanding LDS read before each
+// use (lgkmcnt(0)); issuing the reads as asm and waiting with lgkmcnt(n) on
+// the value itself keeps eight reads in flight.  LDS reads complete in issue
+// order, so lgkmcnt(n) after a read followed by >= n later LDS reads
+// guarantees that read has landed (other LDS accesses only add to the count).
+template <int OFF>
+__device__ __forceinline__ u32x4_t lds_read_b128(uint32_t addr) {
+  u32x4_t r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+template <int N>
+__device__ __forceinline__ void lds_wait(u32x4_t& v) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "i"(N));
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
+template <int N, class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
+
+template <bool TOKEN, int R, int CPS, class SP>
+__global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) {
+  constexpr int kWaves = SP::kWaves, kThreads = SP::kThreads, kNtile = SP::kNtile;
+  constexpr int kQPW = SP::kQPW, kTQ = SP::kTQ;
+  // Every chunk of a group must have been issued before the group's barrier
+  // (R - CPS >= CPS), and at most 3 chunks are ever in flight past it.
+  static_assert(R - CPS >= CPS && R - CPS <= 3, "ring depth");
+  constexpr int kAhead = R - CPS;  // chunks issued ahead of the group being consumed
   extern __shared__ __align__(16) unsigned char smem[];
   const int K = a.K;
   const int64_t Ck = a.Ck;
-  const SelLayout lay = sel_layout(K, Ck);
+  const SelLayout lay = sel_layout(kTQ, kWaves, K, Ck, R, TOKEN);
   unsigned char* ring = smem + lay.ring;
-  uint16_t* wts = reinterpret_cast<uint16_t*>(smem + lay.wts);          // [TQ][8][K]
-  uint64_t* kvbits = reinterpret_cast<uint64_t*>(smem + lay.kvbits);    // [Ck]
-  uint64_t* omask = reinterpret_cast<uint64_t*>(smem + lay.omask);      // [Ck]
-  int32_t* ulist = reinterpret_cast<int32_t*>(smem + lay.ulist);        // [cap]
-  uint64_t* umask = reinterpret_cast<uint64_t*>(smem + lay.umask);      // [cap]
+  uint16_t* wr = reinterpret_cast<uint16_t*>(smem + lay.wr);            // [TQ][K][8]
+  uint16_t* wts = reinterpret_cast<uint16_t*>(smem + lay.p_w);          // [TQ][8][K]
+  int32_t* s_chunk = reinterpret_cast<int32_t*>(smem + lay.s_chunk);    // [cap] walk order
+  uint64_t* s_own = reinterpret_cast<uint64_t*>(smem + lay.s_own);      // [cap] owner bits
+  uint64_t* s_mask = reinterpret_cast<uint64_t*>(smem + lay.s_mask);    // [cap] masked keys
   uint8_t* comp_slot = smem + lay.comp_slot;                            // [TQ][K]
-  int32_t* comp_len = reinterpret_cast<int32_t*>(smem + lay.comp_len);  // [TQ]
-  int32_t* misc = reinterpret_cast<int32_t*>(smem + lay.misc);          // [1] steps, [4..] scan
-  int32_t* comp_idx = reinterpret_cast<int32_t*>(smem + lay.comp_idx);  // [TQ][K] (prologue)
+  int32_t* misc = reinterpret_cast<int32_t*>(smem + lay.misc);          // [kWaves] scan, [kWaves] n
+  int32_t* p_idx = reinterpret_cast<int32_t*>(smem + lay.p_idx);        // [TQ][K]
+  uint8_t* p_kv = smem + lay.p_kv;                                      // [Ck][8] key-valid bytes
+  uint64_t* p_omask = reinterpret_cast<uint64_t*>(smem + lay.p_omask);  // [Ck]
+  int32_t* p_len = reinterpret_cast<int32_t*>(smem + lay.p_len);        // [TQ]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -133,44 +208,72 @@ __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
   const int h = blockIdx.y;
   const int64_t q0 = (int64_t)blockIdx.x * kTQ;
   const int G = a.G;
+  const int64_t nq = min((int64_t)kTQ, a.Lq - q0);  // queries of this tile that exist
 
-  // 1. Routing weights of the tile ([TQ][8][K], head columns >= G zero) and
-  //    per-chunk key-valid bits.
+  // 1. Stage the tile's index rows (-1 past the end of the sequence), routing
+  //    weights ([TQ][8][K], head columns >= G zero) and key-valid bits
+  //    (one byte of 8 bits per 8 keys).
+  for (int e = tid; e < kTQ * K; e += kThreads) {
+    const int qq = e / K, kk = e - qq * K;
+    p_idx[e] = qq < nq ? a.idx[((b * a.Lq + q0 + qq) * a.Hkv + h) * K + kk] : -1;
+  }
   if constexpr (!TOKEN) {
-    for (int e = tid; e < kTQ * 8 * K; e += kThreads) {
-      const int qq = e / (8 * K), rem = e - qq * 8 * K;
-      const int gg = rem / K, kk = rem - gg * K;
-      const int64_t qi = q0 + qq;
-      wts[e] = (qi < a.Lq && gg < G) ? a.w[((b * a.Lq + qi) * a.Hq + h * G + gg) * K + kk] : 0;
+    const uint16_t* wrow0 = a.w + ((b * a.Lq + q0) * a.Hq + (int64_t)h * G) * K;
+    const int64_t qstride = (int64_t)a.Hq * K;
+    if ((K & 7) == 0 && ((uintptr_t)a.w & 15) == 0) {
+      const int vpr = K >> 3;  // 16-byte vectors per (query, head) row
+      for (int e = tid; e < kTQ * 8 * vpr; e += kThreads) {
+        const int row = e / vpr, v = e - row * vpr;
+        const int qq = row >> 3, gg = row & 7;
+        u32x4_t x = {0u, 0u, 0u, 0u};
+        if (qq < nq && gg < G)
+          x = *reinterpret_cast<const u32x4_t*>(wrow0 + qq * qstride + gg * K + 8 * v);
+        *reinterpret_cast<u32x4_t*>(wts + row * K + 8 * v) = x;
+      }
+    } else {
+      for (int e = tid; e < kTQ * 8 * K; e += kThreads) {
+        const int row = e / K, kk = e - row * K;
+        const int qq = row >> 3, gg = row & 7;
+        wts[e] = (qq < nq && gg < G) ? wrow0[qq * qstride + gg * K + kk] : (uint16_t)0;
+      }
     }
   }
-  for (int64_t c = wave; c < Ck; c += kWaves) {
-    const bool ok = a.key_valid ? a.key_valid[b * a.Lk + c * 64 + lane] != 0 : true;
-    const uint64_t vb = __ballot(ok);
-    if (lane == 0) kvbits[c] = vb;
+  if (a.key_valid) {
+    const uint8_t* kv = a.key_valid + b * a.Lk;
+    const bool al8 = ((uintptr_t)kv & 7) == 0;
+    for (int64_t e = tid; e < Ck * 8; e += kThreads) {
+      uint32_t m = 0;
+      if (al8) {
+        const uint64_t x = *reinterpret_cast<const uint64_t*>(kv + 8 * e);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m |= ((x >> (8 * j)) & 0xffull) ? (1u << j) : 0u;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m |= kv[8 * e + j] ? (1u << j) : 0u;
+      }
+      p_kv[e] = (uint8_t)m;
+    }
   }
+  for (int64_t c = tid; c < Ck; c += kThreads) p_omask[c] = 0ull;
   __syncthreads();
 
   // 2. Per-query lists (thread per query): keep the entries before the first
   //    negative one that are < Ck, sort them by chunk, fold duplicates into one
-  //    entry by summing their weights.  comp_slot maps list rank -> original slot.
+  //    entry by summing their weights.  comp_slot maps list rank -> original
+  //    slot; the compacted chunk ids overwrite the staged index row.
   if (tid < kTQ) {
-    const int64_t qi = q0 + tid;
-    int32_t* ci = comp_idx + tid * K;
+    int32_t* ci = p_idx + tid * K;
     uint8_t* cs = comp_slot + tid * K;
     int n = 0;
     bool sorted = true;
-    if (qi < a.Lq) {
-      const int32_t* row = a.idx + ((b * a.Lq + qi) * a.Hkv + h) * K;
-      for (int kk = 0; kk < K; ++kk) {
-        const int32_t c = row[kk];
-        if (c < 0) break;
-        if (c >= Ck) continue;
-        if (n > 0 && c <= ci[n - 1]) sorted = false;
-        ci[n] = c;
-        cs[n] = (uint8_t)kk;
-        ++n;
-      }
+    for (int kk = 0; kk < K; ++kk) {
+      const int32_t c = ci[kk];
+      if (c < 0) break;
+      if (c >= Ck) continue;
+      if (n > 0 && c <= ci[n - 1]) sorted = false;
+      ci[n] = c;
+      cs[n] = (uint8_t)kk;
+      ++n;
     }
     if (!sorted) {
       for (int i = 1; i < n; ++i) {  // stable insertion sort by chunk id
@@ -203,44 +306,60 @@ __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
       }
       n = m;
     }
-    comp_len[tid] = n;
+    p_len[tid] = n;
   }
-  for (int64_t c = tid; c < Ck; c += kThreads) omask[c] = 0ull;
   __syncthreads();
   for (int e = tid; e < kTQ * K; e += kThreads) {
     const int qq = e / K, r = e - qq * K;
-    if (r < comp_len[qq]) atomicOr((unsigned long long*)&omask[comp_idx[e]], 1ull << qq);
+    if (r < p_len[qq]) atomicOr((unsigned long long*)&p_omask[p_idx[e]], 1ull << qq);
+  }
+  if constexpr (!TOKEN) {
+    // Weights in list order: wr[q][r][g] = weight of the r-th listed chunk.
+    for (int e = tid; e < kTQ * K * 8; e += kThreads) {
+      const int qq = e / (K * 8), rem = e - qq * K * 8;
+      const int r = rem >> 3, gg = rem & 7;
+      wr[e] = r < p_len[qq] ? wts[(qq * 8 + gg) * K + comp_slot[qq * K + r]] : (uint16_t)0;
+    }
   }
   __syncthreads();
 
-  // 3. Ascending chunk walk: compaction of the non-empty owner masks.
+  // 3. Walk list: the chunks with at least one owner, ascending, with their
+  //    owner bits and excluded-key bits (invalid keys, the landmark slot).
   {
+    const uint64_t last_mask = a.mask_last ? (1ull << 63) : 0ull;
     const int64_t per = (Ck + kThreads - 1) / kThreads;
-    const int64_t c0 = tid * per, c1 = min(Ck, c0 + per);
+    const int64_t c0 = min(Ck, tid * per), c1 = min(Ck, c0 + per);
     int cnt = 0;
-    for (int64_t c = c0; c < c1; ++c) cnt += omask[c] != 0ull;
-    int* scan = misc + 4;
-    scan[tid] = cnt;
-    __syncthreads();
-    for (int o = 1; o < kThreads; o <<= 1) {
-      const int add = tid >= o ? scan[tid - o] : 0;
-      __syncthreads();
-      scan[tid] += add;
-      __syncthreads();
+    for (int64_t c = c0; c < c1; ++c) cnt += p_omask[c] != 0ull;
+    int incl = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int up = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += up;
     }
-    int pos = scan[tid] - cnt;
-    if (tid == kThreads - 1) misc[1] = scan[tid];
+    if (lane == 63) misc[wave] = incl;
+    __syncthreads();
+    int pos = incl - cnt, total = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const int x = misc[w];
+      pos += w < wave ? x : 0;
+      total += x;
+    }
     for (int64_t c = c0; c < c1; ++c) {
-      const uint64_t m = omask[c];
+      const uint64_t m = p_omask[c];
       if (m) {
-        ulist[pos] = (int32_t)c;
-        umask[pos] = m;
+        const uint64_t kvb = a.key_valid ? *reinterpret_cast<const uint64_t*>(p_kv + 8 * c) : ~0ull;
+        s_chunk[pos] = (int32_t)c;
+        s_own[pos] = m;
+        s_mask[pos] = ~kvb | last_mask;
         ++pos;
       }
     }
+    if (tid == 0) misc[kWaves] = total;
   }
   __syncthreads();
-  const int nsteps = misc[1];
+  const int nsteps = misc[kWaves];
 
   // 4. Q^T operands and accumulators of this wave's queries.
   u32x4_t Qb[kNtile][4];
@@ -250,15 +369,14 @@ __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
   for (int nt = 0; nt < kNtile; ++nt) {
     const int ql = wave * kQPW + 2 * nt + (col >> 3);
     const int gg = col & 7;
-    const int64_t qi = q0 + ql;
     rank[nt] = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       u32x4_t z = {0u, 0u, 0u, 0u};
       Qb[nt][j] = z;
-      if (qi < a.Lq && gg < G)
+      if (ql < nq && gg < G)
         Qb[nt][j] = *reinterpret_cast<const u32x4_t*>(
-            a.q + ((b * a.Lq + qi) * a.Hq + h * G + gg) * 128 + 32 * j + 8 * grp);
+            a.q + ((b * a.Lq + q0 + ql) * a.Hq + h * G + gg) * 128 + 32 * j + 8 * grp);
     }
 #pragma unroll
     for (int td = 0; td < 8; ++td) acc[nt][td] = zero4();
@@ -270,73 +388,98 @@ __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
   const uint16_t* vbase =
       TOKEN ? nullptr : a.vt + ((b * a.Hkv + h) * a.NTk) * (int64_t)(128 * 64);
   const int kstride = a.Hkv * 128;
-  // Per-lane element offsets of this wave's 4 DMA instructions within a chunk.
-  uint32_t dma_off[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int unit = (4 * wave + i) * 64 + lane;
-    if (wave < 4) {
-      const int r = unit >> 4, p = (unit & 15) ^ (r & 15);
-      dma_off[i] = (uint32_t)(r * kstride + p * 8);
-    } else {
-      const int u = unit - 1024, d = u >> 3, p = (u & 7) ^ (d & 7);
-      dma_off[i] = (uint32_t)(d * 64 + p * 8);
-    }
-  }
+  // Wave w < 4 issues K units (4w + i) * 64 + lane: row 16w + 4i + grp, part
+  // col ^ (4i + grp); wave w in 4..7 issues V^T units: row 32(w - 4) + 8i +
+  // lane / 8, part (lane ^ (lane / 8)) & 7.  Element offsets within a chunk:
+  //   K: (16w + 4i + grp) * kstride + ((col ^ grp) ^ 4i) * 8
+  //   V: (32(w - 4) + 8i + lane / 8) * 64 + ((lane ^ (lane >> 3)) & 7) * 8
+  const int wd = min(wave, kDmaWaves - 1);
+  const uint32_t dma0 =
+      wd < 4 ? (uint32_t)((16 * wd + grp) * kstride + ((col ^ grp) * 8))
+             : (uint32_t)((32 * (wd - 4) + (lane >> 3)) * 64 + ((lane ^ (lane >> 3)) & 7) * 8);
+  const uint32_t dma_step = wd < 4 ? (uint32_t)(4 * kstride) : 512u;
+  const uint32_t dma_flip = wd < 4 ? 32u : 0u;
   auto issue = [&](int st) {
-    const int64_t c = ulist[st];
-    unsigned char* slot = ring + (st % kRing) * kSlotBytes + wave * 4096;
-    if (TOKEN && wave >= 4) return;
+    if (wave >= (TOKEN ? 4 : kDmaWaves)) return;
+    const int64_t c = __builtin_amdgcn_readfirstlane(s_chunk[st]);
+    unsigned char* slot = ring + (st % R) * kSlotBytes + wave * 4096;
     const uint16_t* base = wave < 4 ? kbase + c * 64 * (int64_t)kstride : vbase + c * (128 * 64);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds(base + dma_off[i], (lds_void_t*)(slot + i * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(base + ((dma0 ^ (i * dma_flip)) + i * dma_step),
+                                       (lds_void_t*)(slot + i * 1024), 16, 0, 0);
   };
-  if (nsteps > 0) issue(0);
-  if (nsteps > 1) issue(1);
 
-  const uint64_t last_mask = a.mask_last ? (1ull << 63) : 0ull;
-  for (int st = 0; st < nsteps; ++st) {
-    ring_barrier(st + 1 < nsteps && !TOKEN);
-    if (st + 2 < nsteps) issue(st + 2);
-    const uint64_t om = umask[st];
-    const uint64_t masked = (~kvbits[ulist[st]]) | last_mask;  // keys excluded from the softmax
-    const uint16_t* Kb = reinterpret_cast<const uint16_t*>(ring + (st % kRing) * kSlotBytes);
-    const uint16_t* Vb = Kb + 8192;
+  // Per-lane element offsets of the matrix-operand reads inside a slot:
+  // K row 16t + col, part (4j + grp) ^ col  -> kofs0 ^ 32j + 2048t;
+  // V^T row 16td + col, part (4jj + grp) ^ (col & 7) -> vofs0 ^ 32jj + 1024td.
+  const uint32_t kofs0 = (uint32_t)(col * 128 + ((grp ^ col) * 8));
+  const uint32_t vofs0 = (uint32_t)(8192 + col * 64 + ((grp ^ (col & 7)) * 8));
+  auto kofs = [&](int j) { return kofs0 ^ (uint32_t)(32 * j); };
+  auto vofs = [&](int jj) { return vofs0 ^ (uint32_t)(32 * jj); };
+
+  const float c2 = a.scale_log2;
+  const int half = col >> 3, gg = col & 7;
+
+  auto consume = [&](int st) {
+    const uint64_t om = uniform_u64(s_own[st]);
+    const uint64_t msk = uniform_u64(s_mask[st]);
+    const uint16_t* Kb = reinterpret_cast<const uint16_t*>(ring + (st % R) * kSlotBytes);
     const uint32_t wbits = (uint32_t)((om >> (wave * kQPW)) & ((1ull << kQPW) - 1ull));
+    // This lane's excluded-key bits: bit 16t + i of msh is key 16t + 4grp + i.
+    const uint64_t msh = msk >> (4 * grp);
 
 #pragma unroll
     for (int nt = 0; nt < kNtile; ++nt) {
       const uint32_t pair = (wbits >> (2 * nt)) & 3u;
       if (pair == 0u) continue;
-      const int half = col >> 3, gg = col & 7;
       const bool owns = (pair >> half) & 1u;
       const int ql = wave * kQPW + 2 * nt + half;
-      const int64_t qi = q0 + ql;
+      // List position of this chunk for the owning column; reads are made
+      // unconditional (clamped index) so they do not split the block.
+      const int pos = min(rank[nt], K - 1);
+      rank[nt] += owns ? 1 : 0;
+      int slot = 0;
+      if constexpr (TOKEN) slot = comp_slot[ql * K + pos];
+      float wv = 0.f;
+      if constexpr (!TOKEN) {
+        const float wraw = bf16_to_f32(wr[(ql * K + pos) * 8 + gg]);
+        wv = owns ? wraw : 0.f;
+      }
       // Opaque zero: keeps the compiler from hoisting this tile's K / V operand
       // reads out of the tile loop (that would pin 128 extra registers).
       int zoff = 0;
       asm volatile("" : "+v"(zoff));
       const uint16_t* Kt = Kb + zoff;
-      const uint16_t* Vt = Vb + zoff;
 
+      // S^T = K . Q^T: 16 operand reads and 16 products; read o + 8 is issued
+      // after product o, so eight reads stay in flight.
       f32x4_t S[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) S[t] = zero4();
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int p = 4 * j + grp;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int r = 16 * t + col;
-          const u32x4_t Ka = *reinterpret_cast<const u32x4_t*>(Kt + (r * 16 + (p ^ col)) * 8);
-          S[t] = mfma_bf16_16x16x32(Ka, Qb[nt][j], S[t]);
-        }
-      }
-      int slot = 0;
-      if (owns) {
-        slot = comp_slot[ql * K + rank[nt]];
-        ++rank[nt];
+      const uint32_t kaddr[4] = {lds_addr(Kt + kofs(0)), lds_addr(Kt + kofs(1)),
+                                 lds_addr(Kt + kofs(2)), lds_addr(Kt + kofs(3))};
+      u32x4_t kb[16];
+      static_for<16>([&](auto oc) {
+        constexpr int o = decltype(oc)::value;
+        if constexpr (o < 8) kb[o] = lds_read_b128<(o & 3) * 4096>(kaddr[o >> 2]);
+      });
+      static_for<16>([&](auto oc) {
+        constexpr int o = decltype(oc)::value;
+        lds_wait<(15 - o < 7 ? 15 - o : 7)>(kb[o]);
+        S[o & 3] = mfma_bf16_16x16x32(kb[o], Qb[nt][o >> 2], S[o & 3]);
+        if constexpr (o + 8 < 16) kb[o + 8] = lds_read_b128<((o + 8) & 3) * 4096>(kaddr[(o + 8) >> 2]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      // The first V^T operands do not depend on P: read them now so they land
+      // during the softmax.  PV operand o = 8 * jj + td.
+      const uint32_t vaddr[2] = {lds_addr(Kt + vofs(0)), lds_addr(Kt + vofs(1))};
+      u32x4_t vb[16];
+      if constexpr (!TOKEN) {
+        static_for<4>([&](auto oc) {
+          constexpr int o = decltype(oc)::value;
+          vb[o] = lds_read_b128<(o & 7) * 2048>(vaddr[o >> 3]);
+        });
       }
 
       if constexpr (TOKEN) {
@@ -352,43 +495,44 @@ __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
             S[t][i] = v;
           }
         if (owns && gg == 0) {
+          const int64_t qi = q0 + ql;
           float* dst = a.tscores + (((b * a.Lq + qi) * a.Hkv + h) * K + slot) * 64;
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             f32x4_t o;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int s = 16 * t + 4 * grp + i;
-              o[i] = ((masked >> s) & 1ull) ? neg_inf() : S[t][i] * a.sm_scale;
-            }
+            for (int i = 0; i < 4; ++i)
+              o[i] = ((msh >> (16 * t + i)) & 1ull) ? neg_inf() : S[t][i] * a.sm_scale;
             *reinterpret_cast<f32x4_t*>(dst + 16 * t + 4 * grp) = o;
           }
         }
       } else {
-        const float wv = owns ? bf16_to_f32(wts[(ql * 8 + gg) * K + slot]) : 0.f;
-        float mx = neg_inf();
+        if (msk == (1ull << 63)) {
+          if (grp == 3) S[3][3] = neg_inf();
+        } else if (msk != 0ull) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+          for (int t = 0; t < 4; ++t)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int s = 16 * t + 4 * grp + i;
-            float v = S[t][i] * a.scale_log2;
-            if ((masked >> s) & 1ull) v = neg_inf();
-            S[t][i] = v;
-            mx = fmaxf(mx, v);
-          }
+            for (int i = 0; i < 4; ++i)
+              if ((msh >> (16 * t + i)) & 1ull) S[t][i] = neg_inf();
+        }
+        // Softmax in units of log2 with the scale folded into the FMA
+        // (scale_log2 > 0: the max of the raw products is the max logit).
+        float mx = fmaxf(fmaxf(S[0][0], S[0][1]), fmaxf(S[0][2], S[0][3]));
+#pragma unroll
+        for (int t = 1; t < 4; ++t)
+          mx = fmaxf(mx, fmaxf(fmaxf(S[t][0], S[t][1]), fmaxf(S[t][2], S[t][3])));
         mx = across4_max(mx);
-        float sum = 0.f;
+        const float mb = mx == neg_inf() ? 0.f : mx * c2;
+        float part[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p = (mx == neg_inf()) ? 0.f : exp2f(S[t][i] - mx);
-            S[t][i] = p;
-            sum += p;
-          }
-        sum = across4_sum(sum);
-        const float f = (sum > 0.f) ? wv / sum : 0.f;
+          for (int i = 0; i < 4; ++i) S[t][i] = exp2_hw(__builtin_fmaf(S[t][i], c2, -mb));
+          part[t] = (S[t][0] + S[t][1]) + (S[t][2] + S[t][3]);
+        }
+        const float sum = across4_sum((part[0] + part[1]) + (part[2] + part[3]));
+        const float f = sum > 0.f ? wv * rcp_hw(sum) : 0.f;
         u32x4_t Pb[2];
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
@@ -397,33 +541,45 @@ __global__ void __launch_bounds__(kThreads) selected_attn_kernel(SelArgs a) {
           Pb[jj][2] = pack_bf16x2(S[2 * jj + 1][0] * f, S[2 * jj + 1][1] * f);
           Pb[jj][3] = pack_bf16x2(S[2 * jj + 1][2] * f, S[2 * jj + 1][3] * f);
         }
-#pragma unroll
-        for (int td = 0; td < 8; ++td) {
-          const int d = 16 * td + col;
-#pragma unroll
-          for (int jj = 0; jj < 2; ++jj) {
-            const int p1 = 4 * jj + (grp >> 1), p2 = p1 + 2;
-            const int sub = (grp & 1) * 4;
-            const u32x2_t v0 =
-                *reinterpret_cast<const u32x2_t*>(Vt + (d * 8 + (p1 ^ (d & 7))) * 8 + sub);
-            const u32x2_t v1 =
-                *reinterpret_cast<const u32x2_t*>(Vt + (d * 8 + (p2 ^ (d & 7))) * 8 + sub);
-            u32x4_t Va = {v0[0], v0[1], v1[0], v1[1]};
-            acc[nt][td] = mfma_bf16_16x16x32(Va, Pb[jj], acc[nt][td]);
-          }
-        }
+        // O^T += V^T . P^T with eight reads in flight; consecutive products go
+        // to different accumulators.
+        static_for<4>([&](auto oc) {
+          constexpr int o = decltype(oc)::value + 4;
+          vb[o] = lds_read_b128<(o & 7) * 2048>(vaddr[o >> 3]);
+        });
+        static_for<16>([&](auto oc) {
+          constexpr int o = decltype(oc)::value;
+          lds_wait<(15 - o < 7 ? 15 - o : 7)>(vb[o]);
+          acc[nt][o & 7] = mfma_bf16_16x16x32(vb[o], Pb[o >> 3], acc[nt][o & 7]);
+          if constexpr (o + 8 < 16) vb[o + 8] = lds_read_b128<((o + 8) & 7) * 2048>(vaddr[(o + 8) >> 3]);
+          __builtin_amdgcn_sched_barrier(0);
+        });
       }
     }
+  };
+
+  // 6. The walk: groups of CPS chunks, one barrier per group.
+  const int lead = min(kAhead, nsteps);
+  for (int c = 0; c < lead; ++c) issue(c);
+  for (int first = 0; first < nsteps; first += CPS) {
+    // Chunks issued so far: min(nsteps, first + kAhead); this group needs
+    // every one up to first + CPS - 1.
+    const int in_flight = max(0, min(nsteps, first + kAhead) - (first + CPS));
+    ring_barrier(TOKEN ? 0 : in_flight);
+#pragma unroll
+    for (int x = 0; x < CPS; ++x)
+      if (first + kAhead + x < nsteps) issue(first + kAhead + x);
+#pragma unroll
+    for (int x = 0; x < CPS; ++x)
+      if (first + x < nsteps) consume(first + x);
   }
 
   if constexpr (!TOKEN) {
 #pragma unroll
     for (int nt = 0; nt < kNtile; ++nt) {
-      const int ql = wave * kQPW + 2 * nt + (col >> 3);
-      const int gg = col & 7;
-      const int64_t qi = q0 + ql;
-      if (qi >= a.Lq || gg >= G) continue;
-      uint16_t* orow = a.out + ((b * a.Lq + qi) * a.Hq + h * G + gg) * 128;
+      const int ql = wave * kQPW + 2 * nt + half;
+      if (ql >= nq || gg >= G) continue;
+      uint16_t* orow = a.out + ((b * a.Lq + q0 + ql) * a.Hq + h * G + gg) * 128;
 #pragma unroll
       for (int td = 0; td < 8; ++td) {
         u32x2_t o;
@@ -443,23 +599,35 @@ __global__ void __launch_bounds__(256) fill_neg_inf(float* p, int64_t n) {
     p[e] = neg_inf();
 }
 
-int launch_selected(SelArgs& a, hipStream_t s) {
-  const SelLayout lay = sel_layout(a.K, a.Ck);
-  if (lay.total > 160 * 1024) return MRSA_ERR_UNSUPPORTED;
-  auto kern = a.token_mode ? selected_attn_kernel<true> : selected_attn_kernel<false>;
+template <bool TOKEN, int R, int CPS, class SP>
+int launch_variant(SelArgs& a, const SelLayout& lay, hipStream_t s) {
+  auto kern = selected_attn_kernel<TOKEN, R, CPS, SP>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lay.total) != hipSuccess)
     return MRSA_ERR_LAUNCH;
-  dim3 grid((unsigned)((a.Lq + kTQ - 1) / kTQ), (unsigned)a.Hkv, (unsigned)a.B);
-  hipLaunchKernelGGL(kern, grid, dim3(kThreads), lay.total, s, a);
+  dim3 grid((unsigned)((a.Lq + SP::kTQ - 1) / SP::kTQ), (unsigned)a.Hkv, (unsigned)a.B);
+  hipLaunchKernelGGL(kern, grid, dim3(SP::kThreads), lay.total, s, a);
   return mrsa_launch_status();
+}
+
+// Deepest ring that fits in LDS: 4 slots, else 3.
+template <bool TOKEN>
+int launch_selected(SelArgs& a, hipStream_t s) {
+  using SP = std::conditional_t<MRSA_SEL_WAVES == 12, Split12,
+                                std::conditional_t<MRSA_SEL_WAVES == 82, Split8x2, Split8>>;
+  const SelLayout l4 = sel_layout(SP::kTQ, SP::kWaves, a.K, a.Ck, 4, TOKEN);
+  if (sel_layout_fits(l4, 4)) return launch_variant<TOKEN, 4, MRSA_SEL_CPS4, SP>(a, l4, s);
+  const SelLayout l3 = sel_layout(SP::kTQ, SP::kWaves, a.K, a.Ck, 3, TOKEN);
+  if (sel_layout_fits(l3, 3)) return launch_variant<TOKEN, 3, 1, SP>(a, l3, s);
+  return MRSA_ERR_UNSUPPORTED;
 }
 
 int check_common(const void* q, const void* k, const int32_t* indices, int64_t batch,
                  int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads,
-                 int64_t head_dim, int64_t topk, int64_t chunk_size) {
+                 int64_t head_dim, int64_t topk, int64_t chunk_size, float sm_scale) {
   if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 ||
-      q_heads % kv_heads != 0 || head_dim <= 0 || topk <= 0 || chunk_size <= 0)
+      q_heads % kv_heads != 0 || head_dim <= 0 || topk <= 0 || chunk_size <= 0 ||
+      !(sm_scale > 0.f) || sm_scale == __builtin_inff())
     return MRSA_ERR_INVALID_ARGUMENT;
   if (kv_len % chunk_size != 0) return MRSA_ERR_INVALID_ARGUMENT;
   if (chunk_size != 64 || head_dim != 128 || q_heads / kv_heads > 8 || topk > kMaxTopk)
@@ -480,7 +648,7 @@ extern "C" int mrsa_selected_attention_fwd(const void* q, const void* k, const v
                                            int64_t chunk_size, int mask_last_token,
                                            float sm_scale, void* out, void* stream) {
   int st = check_common(q, k, indices, batch, q_len, kv_len, q_heads, kv_heads, head_dim, topk,
-                        chunk_size);
+                        chunk_size, sm_scale);
   if (st != MRSA_OK) return st;
   if (batch == 0 || q_len == 0) return MRSA_OK;
   if (!v_tiles || !weights || !out || (uintptr_t)v_tiles % 16 != 0 || (uintptr_t)out % 8 != 0)
@@ -507,7 +675,7 @@ extern "C" int mrsa_selected_attention_fwd(const void* q, const void* k, const v
   a.token_mode = 0;
   a.out = (uint16_t*)out;
   a.tscores = nullptr;
-  return launch_selected(a, (hipStream_t)stream);
+  return launch_selected<false>(a, (hipStream_t)stream);
 }
 
 extern "C" int mrsa_candidate_token_scores_fwd(const void* q, const void* k,
@@ -518,7 +686,7 @@ extern "C" int mrsa_candidate_token_scores_fwd(const void* q, const void* k,
                                                int64_t chunk_size, float sm_scale,
                                                float* scores, void* stream) {
   int st = check_common(q, k, indices, batch, q_len, kv_len, q_heads, kv_heads, head_dim, topk,
-                        chunk_size);
+                        chunk_size, sm_scale);
   if (st != MRSA_OK) return st;
   if (batch == 0 || q_len == 0) return MRSA_OK;
   if (!scores || (uintptr_t)scores % 16 != 0) return MRSA_ERR_INVALID_ARGUMENT;
@@ -550,5 +718,5 @@ extern "C" int mrsa_candidate_token_scores_fwd(const void* q, const void* k,
   a.token_mode = 1;
   a.out = nullptr;
   a.tscores = scores;
-  return launch_selected(a, s);
+  return launch_selected<true>(a, s);
 }

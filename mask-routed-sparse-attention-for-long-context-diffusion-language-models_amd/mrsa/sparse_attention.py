@@ -15,7 +15,11 @@ from . import _lib
 
 
 def value_tiles(v: torch.Tensor) -> torch.Tensor:
-    """V [B, L, Hkv, D] bf16 -> 64-key tiles stored transposed [B, Hkv, ceil(L/64), D, 64]."""
+    """V [B, L, Hkv, D] bf16 -> 64-key tiles stored transposed [B, Hkv, ceil(L/64), D, 64].
+
+    Inside a tile row, key 32a + 16b + 4c + e (a, b in {0,1}; c, e in 0..3) sits
+    at position 32a + 8c + 4b + e, the order the matrix-core kernels read it in.
+    """
 
     if v.device.type != "cuda" or v.dtype != torch.bfloat16 or v.ndim != 4:
         raise ValueError("value_tiles requires a CUDA BF16 [B, L, Hkv, D] tensor")

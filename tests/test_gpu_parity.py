@@ -90,7 +90,11 @@ def test_value_tiles_layout():
     vp = torch.zeros(2, 256, 3, 128).bfloat16()
     vp[:, :200] = v
     expect = vp.reshape(2, 4, 64, 3, 128).permute(0, 3, 1, 4, 2)
-    assert torch.equal(t, expect)
+    # position 32a + 8c + 4b + e holds key 32a + 16b + 4c + e
+    key_of_pos = [32 * (p // 32) + 16 * ((p // 4) % 2) + 4 * ((p // 8) % 4) + p % 4
+                  for p in range(64)]
+    assert sorted(key_of_pos) == list(range(64))
+    assert torch.equal(t, expect[..., key_of_pos])
 
 
 @pytest.mark.parametrize("G,dense", [(7, False), (1, True), (3, False)])
