@@ -108,6 +108,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run a plain 1 GiB device copy three times (reference "
+                         "dispatch for scaling FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
@@ -120,6 +123,13 @@ def main() -> int:
     import mrsa
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.empty(1 << 29, dtype=torch.int16, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     q, k, v = make_inputs(L_CFG2, 1234, dev, torch.bfloat16)
     route_q = q
     scale = torch.ones(HQ, device=dev)
