@@ -58,15 +58,28 @@ __device__ __forceinline__ f32x4_t zero4() {
   return z;
 }
 
-// Butterfly reductions inside groups of 16 lanes (lanes sharing l / 16).
+// Reductions inside groups of 16 lanes (lanes sharing l / 16) with DPP lane
+// moves, no LDS round trip: swap neighbours, swap pairs (quad_perm), then
+// mirror within 8 lanes (row_half_mirror) and within 16 (row_mirror).  After
+// each step every lane holds the reduction of a twice larger lane set.  Every
+// lane of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf,
+                                                            0xf, false));
+}
 __device__ __forceinline__ float group16_max(float v) {
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  v = fmaxf(v, dpp_mov<0xb1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_mov<0x4e>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_mov<0x140>(v));  // row_mirror
   return v;
 }
 __device__ __forceinline__ float group16_sum(float v) {
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
+  v += dpp_mov<0xb1>(v);
+  v += dpp_mov<0x4e>(v);
+  v += dpp_mov<0x141>(v);
+  v += dpp_mov<0x140>(v);
   return v;
 }
 __device__ __forceinline__ int group16_sum_i(int v) {
@@ -112,6 +125,9 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 
 // 1/x with the hardware reciprocal (1 ulp).
 __device__ __forceinline__ float rcp_hw(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// log2(x) with the hardware instruction (v_log_f32, ~1 ulp for normal x).
+__device__ __forceinline__ float log2_hw(float x) { return __builtin_amdgcn_logf(x); }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

@@ -79,166 +79,44 @@ __device__ __forceinline__ const uint16_t* lmk_row(const RouteArgs& a, int64_t b
 constexpr int kFastThreads = 512;  // 8 waves: 4 query groups x 2 chunk halves
 constexpr int kFastQ = 64;         // queries per workgroup
 constexpr int kNT = 8;             // chunk tiles of 16 per wave (128 chunks)
-constexpr int kLmkPitch = 136;     // bf16 elements per staged landmark row (128 + 8 pad)
+constexpr int kFastMaxTopk = 64;
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// LDS carve-up.  Two buffers of one head's landmark keys ([256][128] bf16,
+// 16-byte parts XOR-swizzled: part p of row c at unit c*16 + (p ^ (c & 15)))
+// and two of its bias row alternate, so the next head streams in while the
+// current one is computed.  The selection scores ([64][256] f32) reuse the
+// buffer of the last first-pass head.
 struct FastLayout {
-  static constexpr size_t lmk = 0;                          // [256][136] bf16, later [64][256] f32
-  static constexpr size_t bias = 256 * kLmkPitch * 2;       // [256] f32
-  static constexpr size_t cbad = bias + 256 * 4;            // [256] u8
-  static constexpr size_t red_max = cbad + 256;             // [2][64] f32
-  static constexpr size_t red_sum = red_max + 2 * 64 * 4;   // [2][64] f32
-  static constexpr size_t slot = red_sum + 2 * 64 * 4;      // [64][256] i8
-  static constexpr size_t total = slot + 64 * 256;
+  static constexpr size_t lmk = 0;                      // [2][256][128] bf16
+  static constexpr size_t bias = 2 * 256 * 128 * 2;     // [2][256] f32
+  static constexpr size_t cbad = bias + 2 * 256 * 4;    // [256] u8
+  static constexpr size_t red_max = cbad + 256;         // [2][64] f32
+  static constexpr size_t red_sum = red_max + 2 * 64 * 4;
+  static constexpr size_t slot = red_sum + 2 * 64 * 4;  // [64][256] i8
+  static constexpr size_t ntot = slot + 64 * 256;        // [64] i32 picks per row
+  static constexpr size_t sc = ntot + 64 * 4;            // [64][K] bf16, one head's picks
+  static size_t total(int K) { return sc + (size_t)64 * K * 2; }
 };
 
+// Selection of the fast path.  The max-over-heads scores M go to LDS
+// (row-major [64][256] f32, in the landmark buffer `ms_buf`), then wave w
+// selects rows 8w..8w+7 with eight lanes per row, each lane owning the 32
+// consecutive chunks 32*sub .. 32*sub+31: bisection on order-preserving keys
+// for the K-th largest score, exact ties at the threshold broken toward the
+// lower chunk index.  Writes the slot table (chunk -> list position or -1)
+// the indices and the per-row pick counts; slots past the picks get index -1
+// (their scores are written as -inf by the second pass).
 template <int G>
-__global__ void __launch_bounds__(kFastThreads, 2) route_topk_mfma_kernel(RouteArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  uint16_t* lmk_s = reinterpret_cast<uint16_t*>(smem + FastLayout::lmk);
-  float* Ms = reinterpret_cast<float*>(smem + FastLayout::lmk);  // after the head loop
-  float* bias_s = reinterpret_cast<float*>(smem + FastLayout::bias);
-  unsigned char* cbad = smem + FastLayout::cbad;
-  float* red_max = reinterpret_cast<float*>(smem + FastLayout::red_max);
-  float* red_sum = reinterpret_cast<float*>(smem + FastLayout::red_sum);
-  int8_t* slot_s = reinterpret_cast<int8_t*>(smem + FastLayout::slot);
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int col = lane & 15, grp = lane >> 4;
-  const int qg = wave & 3, half = wave >> 2;
-  const int64_t b = blockIdx.z;
-  const int h = blockIdx.y;
-  const int64_t q0 = (int64_t)blockIdx.x * kFastQ;
-  const int64_t qbase = q0 + 16 * qg;
-  const int64_t qa = qbase + col;  // the A-operand row this lane supplies
-  const int64_t L = a.L, C = a.C;
+__device__ __forceinline__ void select_step(const RouteArgs& a, const float (&M)[kNT][4],
+                                            uint16_t* ms_buf, const unsigned char* cbad,
+                                            int8_t* slot_s, int* ntot_s, int64_t q0, int64_t qbase, int64_t L,
+                                            int64_t C, int h, int64_t b, int lane, int wave,
+                                            int col, int grp, int qg, int cbase) {
   const int K = a.K;
-  const int cbase = 128 * half;
-  const uint16_t* qb_base = a.q + b * L * (int64_t)(a.Hkv * G * 128);
-  const float* lse_base = a.pre_softmax ? nullptr : a.lse + b * L * (int64_t)(a.Hkv * G);
-
-  if (a.derive_window >= 0) {
-    for (int c = tid; c < 256; c += kFastThreads) {
-      bool any = false;
-      if (c < C) {
-        if (a.key_valid) {
-          const uint8_t* kv = a.key_valid + b * L + (int64_t)c * a.block_size;
-          for (int64_t s = 0; s < a.block_size - 1; ++s) any |= kv[s] != 0;
-        } else {
-          any = a.block_size > 1;
-        }
-      }
-      cbad[c] = !any;
-    }
-  }
-
-  float M[kNT][4];
-  uint32_t raw[G][kNT][2];
-#pragma unroll
-  for (int t = 0; t < kNT; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) M[t][i] = neg_inf();
-
-  // One pass per query head; instantiated per compile-time g so raw[g] is
-  // indexed statically.
-  auto head_pass = [&](auto gc) {
-    constexpr int g = decltype(gc)::value;
-    __syncthreads();
-#pragma unroll 2
-    for (int v = tid; v < 256 * 16; v += kFastThreads) {
-      const int c = v >> 4, part = v & 15;
-      u32x4_t val = {0u, 0u, 0u, 0u};
-      if (c < C) val = reinterpret_cast<const u32x4_t*>(lmk_row(a, b, c, h, g))[part];
-      *reinterpret_cast<u32x4_t*>(lmk_s + c * kLmkPitch + part * 8) = val;
-    }
-    if (tid < 256) bias_s[tid] = (a.bias && tid < C) ? a.bias[((b * C + tid) * a.Hkv + h) * G + g] : 0.f;
-    __syncthreads();
-
-    u32x4_t A[4];
-    const uint16_t* qrow = qb_base + (uint32_t)((((int)qa * a.Hkv + h) * G + g) * 128 + 8 * grp);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      u32x4_t z = {0u, 0u, 0u, 0u};
-      A[j] = z;
-      if (qa < L) A[j] = *reinterpret_cast<const u32x4_t*>(qrow + 32 * j);
-    }
-    f32x4_t S[kNT];
-#pragma unroll
-    for (int t = 0; t < kNT; ++t) {
-      f32x4_t acc = zero4();
-      const uint16_t* brow = lmk_s + (cbase + 16 * t + col) * kLmkPitch + 8 * grp;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const u32x4_t B = *reinterpret_cast<const u32x4_t*>(brow + 32 * j);
-        acc = mfma_bf16_16x16x32(A[j], B, acc);
-      }
-      S[t] = acc;
-    }
-
-    // Raw scaled logits (kept as bf16) and biased logits (in S).
-    float rmax[4] = {neg_inf(), neg_inf(), neg_inf(), neg_inf()};
-#pragma unroll
-    for (int t = 0; t < kNT; ++t) {
-      const int c = cbase + 16 * t + col;
-      float xs[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float x = S[t][i] * a.sm_scale;
-        if (c >= C) x = neg_inf();
-        xs[i] = x;
-        const float xb = x + bias_s[c];
-        S[t][i] = xb;
-        rmax[i] = fmaxf(rmax[i], xb);
-      }
-      raw[g][t][0] = pack_bf16x2(xs[0], xs[1]);
-      raw[g][t][1] = pack_bf16x2(xs[2], xs[3]);
-    }
-    // Row LSE over both chunk halves (exchanged through LDS).
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      rmax[i] = group16_max(rmax[i]);
-      if (col == 0) red_max[half * 64 + 16 * qg + 4 * grp + i] = rmax[i];
-    }
-    __syncthreads();
-    float m[4], ssum[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 16 * qg + 4 * grp + i;
-      m[i] = fmaxf(red_max[row], red_max[64 + row]);
-      float s = 0.f;
-      if (m[i] != neg_inf()) {
-#pragma unroll
-        for (int t = 0; t < kNT; ++t) s += expf(S[t][i] - m[i]);
-      }
-      ssum[i] = group16_sum(s);
-      if (col == 0) red_sum[half * 64 + row] = ssum[i];
-    }
-    __syncthreads();
-    float tot[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t r = qbase + 4 * grp + i;
-      const int row = 16 * qg + 4 * grp + i;
-      const float s = red_sum[row] + red_sum[64 + row];
-      const float lse_h = (m[i] == neg_inf()) ? m[i] : m[i] + logf(s);
-      const float lv = (!a.pre_softmax && r < L) ? lse_base[((int)r * a.Hkv + h) * G + g] : 0.f;
-      tot[i] = a.pre_softmax ? 0.f : logaddexp_f(lv, lse_h);
-    }
-#pragma unroll
-    for (int t = 0; t < kNT; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float xb = S[t][i];
-        const float y = (xb == neg_inf()) ? xb : xb - tot[i];
-        M[t][i] = fmaxf(M[t][i], y);
-      }
-  };
-  [&]<int... gs>(std::integer_sequence<int, gs...>) {
-    (head_pass(std::integral_constant<int, gs>{}), ...);
-  }(std::make_integer_sequence<int, G>{});
-
-  // Dropped chunks, then the selection scores go to LDS (row-major [64][256]).
-  __syncthreads();
+  float* Ms = reinterpret_cast<float*>(ms_buf);
+  __syncthreads();  // every wave is done with the landmark keys in ms_buf
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t r = qbase + 4 * grp + i;
@@ -262,142 +140,331 @@ __global__ void __launch_bounds__(kFastThreads, 2) route_topk_mfma_kernel(RouteA
   }
   __syncthreads();
 
-  // Selection: wave w handles rows 8w..8w+7, eight lanes per row, each lane
-  // owning the 32 consecutive chunks 32*sub .. 32*sub+31.
-  {
-    const int row = 8 * wave + (lane >> 3);
-    const int sub = lane & 7;
-    const int64_t r = q0 + row;
-    uint32_t key[32];
+  const int row = 8 * wave + (lane >> 3);
+  const int sub = lane & 7;
+  const int64_t r = q0 + row;
+  uint32_t key[32];
 #pragma unroll
-    for (int e = 0; e < 32; e += 4) {
-      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(Ms + row * 256 + 32 * sub + e);
+  for (int e = 0; e < 32; e += 4) {
+    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(Ms + row * 256 + 32 * sub + e);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) key[e + u] = float_order_key(v[u]);
+    for (int u = 0; u < 4; ++u) key[e + u] = float_order_key(v[u]);
+  }
+  const uint32_t kNeg = float_order_key(neg_inf());
+  int nfin = 0;
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+  for (int e = 0; e < 32; ++e)
+    if (key[e] > kNeg) {
+      ++nfin;
+      kmin = min(kmin, key[e]);
+      kmax = max(kmax, key[e]);
     }
-    const uint32_t kNeg = float_order_key(neg_inf());
-    int nfin = 0;
-    uint32_t kmin = 0xffffffffu, kmax = 0u;
 #pragma unroll
-    for (int e = 0; e < 32; ++e)
-      if (key[e] > kNeg) {
-        ++nfin;
-        kmin = min(kmin, key[e]);
-        kmax = max(kmax, key[e]);
-      }
+  for (int o = 1; o < 8; o <<= 1) {
+    nfin += __shfl_xor(nfin, o, 64);
+    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, 64));
+    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, 64));
+  }
+  uint32_t thr_hi, thr_tie = 0u, lo = kmin, hi = kmax + 1u;
+  int need = 0;
+  bool done;
+  if (nfin <= K) {
+    thr_hi = kNeg + 1u;
+    done = true;
+  } else {
+    thr_hi = 0u;
+    done = false;
+  }
+  for (int it = 0; it < 40; ++it) {
+    if (!__any(!done)) break;
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    int cnt = 0;
 #pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {
-      nfin += __shfl_xor(nfin, o, 64);
-      kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, 64));
-      kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, 64));
-    }
-    uint32_t thr_hi, thr_tie = 0u, lo = kmin, hi = kmax + 1u;
-    int need = 0;
-    bool done;
-    if (nfin <= K) {
-      thr_hi = kNeg + 1u;
-      done = true;
-    } else {
-      thr_hi = 0u;
-      done = false;
-    }
-    for (int it = 0; it < 40; ++it) {
-      if (!__any(!done)) break;
-      const uint32_t mid = lo + ((hi - lo) >> 1);
-      int cnt = 0;
+    for (int e = 0; e < 32; ++e) cnt += key[e] >= mid ? 1 : 0;
 #pragma unroll
-      for (int e = 0; e < 32; ++e) cnt += key[e] >= mid ? 1 : 0;
-#pragma unroll
-      for (int o = 1; o < 8; o <<= 1) cnt += __shfl_xor(cnt, o, 64);
-      if (!done) {
-        if (hi - lo <= 1u) {
-          done = true;
-        } else if (cnt == K) {
-          thr_hi = mid;
-          done = true;
-        } else if (cnt > K) {
-          lo = mid;
-        } else {
-          hi = mid;
-        }
-      }
-    }
-    if (thr_hi == 0u) {
-      int cnt_hi = 0;
-#pragma unroll
-      for (int e = 0; e < 32; ++e) cnt_hi += key[e] >= hi ? 1 : 0;
-#pragma unroll
-      for (int o = 1; o < 8; o <<= 1) cnt_hi += __shfl_xor(cnt_hi, o, 64);
-      thr_hi = hi;
-      thr_tie = lo;
-      need = K - cnt_hi;
-    }
-    // Exclusive prefix over the 8 lanes of the row (chunk order == lane order).
-    auto excl8 = [&](int v) {
-      int incl = v;
-#pragma unroll
-      for (int o = 1; o < 8; o <<= 1) {
-        const int up = __shfl_up(incl, o, 8);
-        if (sub >= o) incl += up;
-      }
-      return incl - v;
-    };
-    int my_ties = 0;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) my_ties += (need > 0 && key[e] == thr_tie) ? 1 : 0;
-    int tie_rank = excl8(my_ties);
-    int my_picks = 0;
-    uint32_t pickbits = 0u;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      const bool tie = need > 0 && key[e] == thr_tie;
-      const bool pick = key[e] >= thr_hi || (tie && tie_rank < need);
-      if (tie) ++tie_rank;
-      if (pick) {
-        pickbits |= 1u << e;
-        ++my_picks;
-      }
-    }
-    int slot = excl8(my_picks);
-    int total = my_picks;
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) total += __shfl_xor(total, o, 64);
-    const int64_t orow = (b * L + r) * a.Hkv + h;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      const bool pick = (pickbits >> e) & 1u;
-      slot_s[row * 256 + 32 * sub + e] = pick ? (int8_t)slot : (int8_t)-1;
-      if (pick && r < L) a.indices[orow * K + slot] = 32 * sub + e;
-      slot += pick ? 1 : 0;
-    }
-    if (r < L) {
-      uint16_t* sc16 = reinterpret_cast<uint16_t*>(a.scores);
-      for (int s = total + sub; s < K; s += 8) {
-        a.indices[orow * K + s] = -1;
-#pragma unroll
-        for (int g = 0; g < G; ++g) sc16[(orow * G + g) * K + s] = 0xff80u;  // -inf
+    for (int o = 1; o < 8; o <<= 1) cnt += __shfl_xor(cnt, o, 64);
+    if (!done) {
+      if (hi - lo <= 1u) {
+        done = true;
+      } else if (cnt == K) {
+        thr_hi = mid;
+        done = true;
+      } else if (cnt > K) {
+        lo = mid;
+      } else {
+        hi = mid;
       }
     }
   }
-  __syncthreads();
+  if (thr_hi == 0u) {
+    int cnt_hi = 0;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) cnt_hi += key[e] >= hi ? 1 : 0;
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) cnt_hi += __shfl_xor(cnt_hi, o, 64);
+    thr_hi = hi;
+    thr_tie = lo;
+    need = K - cnt_hi;
+  }
+  // Exclusive prefix over the 8 lanes of the row (chunk order == lane order).
+  auto excl8 = [&](int v) {
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+      const int up = __shfl_up(incl, o, 8);
+      if (sub >= o) incl += up;
+    }
+    return incl - v;
+  };
+  int my_ties = 0;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) my_ties += (need > 0 && key[e] == thr_tie) ? 1 : 0;
+  int tie_rank = excl8(my_ties);
+  int my_picks = 0;
+  uint32_t pickbits = 0u;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    const bool tie = need > 0 && key[e] == thr_tie;
+    const bool pick = key[e] >= thr_hi || (tie && tie_rank < need);
+    if (tie) ++tie_rank;
+    if (pick) {
+      pickbits |= 1u << e;
+      ++my_picks;
+    }
+  }
+  int slot = excl8(my_picks);
+  int total = my_picks;
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) total += __shfl_xor(total, o, 64);
+  const int64_t orow = (b * L + r) * a.Hkv + h;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    const bool pick = (pickbits >> e) & 1u;
+    slot_s[row * 256 + 32 * sub + e] = pick ? (int8_t)slot : (int8_t)-1;
+    if (pick && r < L) a.indices[orow * K + slot] = 32 * sub + e;
+    slot += pick ? 1 : 0;
+  }
+  if (r < L)
+    for (int s = total + sub; s < K; s += 8) a.indices[orow * K + s] = -1;
+  if (sub == 0) ntot_s[row] = total;
+}
 
-  // Raw logits of every head at the picked chunks.
+template <int G>
+__global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int K = a.K;
+  float* bias_s = reinterpret_cast<float*>(smem + FastLayout::bias);
+  unsigned char* cbad = smem + FastLayout::cbad;
+  float* red_max = reinterpret_cast<float*>(smem + FastLayout::red_max);
+  float* red_sum = reinterpret_cast<float*>(smem + FastLayout::red_sum);
+  int8_t* slot_s = reinterpret_cast<int8_t*>(smem + FastLayout::slot);
+  int* ntot_s = reinterpret_cast<int*>(smem + FastLayout::ntot);
+  uint16_t* sc_s = reinterpret_cast<uint16_t*>(smem + FastLayout::sc);
+  auto lmk_buf = [&](int i) { return reinterpret_cast<uint16_t*>(smem + FastLayout::lmk) + i * 256 * 128; };
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int qg = wave & 3, half = wave >> 2;
+  const int64_t b = blockIdx.z;
+  const int h = blockIdx.y;
+  const int64_t q0 = (int64_t)blockIdx.x * kFastQ;
+  const int64_t qbase = q0 + 16 * qg;
+  const int64_t qa = qbase + col;  // the A-operand row this lane supplies
+  const int64_t L = a.L, C = a.C;
+  const int cbase = 128 * half;
+  const uint16_t* qb_base = a.q + b * L * (int64_t)(a.Hkv * G * 128);
+  const float* lse_base = a.pre_softmax ? nullptr : a.lse + b * L * (int64_t)(a.Hkv * G);
   uint16_t* sc16 = reinterpret_cast<uint16_t*>(a.scores);
+
+  if (a.derive_window >= 0) {
+    for (int c = tid; c < 256; c += kFastThreads) {
+      bool any = false;
+      if (c < C) {
+        if (a.key_valid) {
+          const uint8_t* kv = a.key_valid + b * L + (int64_t)c * a.block_size;
+          for (int64_t s = 0; s < a.block_size - 1; ++s) any |= kv[s] != 0;
+        } else {
+          any = a.block_size > 1;
+        }
+      }
+      cbad[c] = !any;
+    }
+  }
+  if (!a.bias)
+    for (int e = tid; e < 512; e += kFastThreads) bias_s[e] = 0.f;
+
+  // The walk is 2G steps: pass 1 over heads 0..G-1 (biased logits, LSE,
+  // running max), then the selection, then pass 2 over heads G-1..0 (raw
+  // logits of the picks).  Step s computes from buffer s & 1.
+  auto head_of = [&](int s) { return s < G ? s : 2 * G - 1 - s; };
+  // Global->LDS DMA of head g's landmark keys into buffer i: wave w,
+  // instruction j moves units (8w + j) * 64 + lane = row 4(8w + j) + lane / 16,
+  // stored part lane & 15 (global part (lane & 15) ^ (row & 15)).  Rows >= C
+  // re-read row C - 1; their logits are masked to -inf.  Wave 0 also moves
+  // the bias row (4-byte units, rows >= C re-read row C - 1 and are unused).
+  auto stage = [&](int g, int i) {
+    uint16_t* dst = lmk_buf(i);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int row = 4 * (8 * wave + j) + (lane >> 4);
+      const int part = (lane & 15) ^ (row & 15);
+      const int64_t c = min((int64_t)row, C - 1);
+      __builtin_amdgcn_global_load_lds(lmk_row(a, b, c, h, g) + part * 8,
+                                       (lds_void_t*)(dst + (8 * wave + j) * 512), 16, 0, 0);
+    }
+    if (a.bias && wave == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t c = min((int64_t)(64 * j + lane), C - 1);
+        __builtin_amdgcn_global_load_lds(a.bias + ((b * C + c) * a.Hkv + h) * G + g,
+                                         (lds_void_t*)(bias_s + 256 * i + 64 * j), 4, 0, 0);
+      }
+    }
+  };
+  auto load_q = [&](int g, u32x4_t (&A)[4]) {
+    const uint16_t* qrow = qb_base + (uint32_t)((((int)qa * a.Hkv + h) * G + g) * 128 + 8 * grp);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      u32x4_t z = {0u, 0u, 0u, 0u};
+      A[j] = z;
+      if (qa < L) A[j] = *reinterpret_cast<const u32x4_t*>(qrow + 32 * j);
+    }
+  };
+  // S[t] = q_g (16 queries of this wave) . lmk (16 chunks of tile t).
+  auto logits = [&](const uint16_t* lmk_s, const u32x4_t (&A)[4], f32x4_t (&S)[kNT]) {
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) {
+      f32x4_t acc = zero4();
+      const uint16_t* brow = lmk_s + (cbase + 16 * t + col) * 128;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const u32x4_t B = *reinterpret_cast<const u32x4_t*>(brow + (((4 * j + grp) ^ col) * 8));
+        acc = mfma_bf16_16x16x32(A[j], B, acc);
+      }
+      S[t] = acc;
+    }
+  };
+
+  float M[kNT][4];
 #pragma unroll
   for (int t = 0; t < kNT; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 16 * qg + 4 * grp + i;
-      const int c = cbase + 16 * t + col;
-      const int slot = slot_s[row * 256 + c];
-      const int64_t r = q0 + row;
-      if (slot >= 0 && r < L) {
-        const int64_t orow = (b * L + r) * a.Hkv + h;
+    for (int i = 0; i < 4; ++i) M[t][i] = neg_inf();
+
+  u32x4_t Acur[4], Anext[4];
+  // Step prologue: head s landed (this wave's DMA and loads) and every wave
+  // is done with the other buffer; then queue step s + 1 -- its q operands
+  // first, then its DMA, so no wait inside the step drains the prefetch.
+  auto begin_step = [&](int s, bool load_next_q) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (s + 1 < 2 * G) {
+      if (load_next_q) load_q(head_of(s + 1), Anext);
+      stage(head_of(s + 1), (s + 1) & 1);
+    }
+  };
+  load_q(0, Acur);
+  stage(0, 0);
+
+  // Pass 1: biased logits, LSE over all chunks, running max over heads.
+  for (int s = 0; s < G; ++s) {
+    const int g = s;
+    begin_step(s, s != G - 1);
+    f32x4_t S[kNT];
+    logits(lmk_buf(s & 1), Acur, S);
+    const float* bias_g = bias_s + 256 * (s & 1);
+    float rmax[4] = {neg_inf(), neg_inf(), neg_inf(), neg_inf()};
 #pragma unroll
-        for (int g = 0; g < G; ++g)
-          sc16[(orow * G + g) * K + slot] = (uint16_t)((raw[g][t][i >> 1] >> (16 * (i & 1))) & 0xffffu);
+    for (int t = 0; t < kNT; ++t) {
+      const int c = cbase + 16 * t + col;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = c < C ? S[t][i] * a.sm_scale : neg_inf();
+        const float xb = x + bias_g[c];
+        S[t][i] = xb;
+        rmax[i] = fmaxf(rmax[i], xb);
       }
     }
+    // Row LSE over both chunk halves, in base 2 with the hardware exp2/log2:
+    // each half reduces (max, sum of exp2) over its 128 chunks; one LDS
+    // exchange combines them with a rescale.
+    float m2[4], s2[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      m2[i] = group16_max(rmax[i]) * kLog2e;
+      float sm = 0.f;
+      if (m2[i] != neg_inf()) {
+#pragma unroll
+        for (int t = 0; t < kNT; ++t) sm += exp2_hw(__builtin_fmaf(S[t][i], kLog2e, -m2[i]));
+      }
+      s2[i] = group16_sum(sm);
+      if (col == 0) {
+        const int row = 16 * qg + 4 * grp + i;
+        red_max[half * 64 + row] = m2[i];
+        red_sum[half * 64 + row] = s2[i];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t r = qbase + 4 * grp + i;
+      const int row = 16 * qg + 4 * grp + i;
+      const float ma = red_max[row], mb = red_max[64 + row];
+      const float mm = fmaxf(ma, mb);
+      float lse2 = neg_inf();  // log2 sum_c 2^(x_c log2 e)
+      if (mm != neg_inf())
+        lse2 = mm + log2_hw((ma == neg_inf() ? 0.f : red_sum[row] * exp2_hw(ma - mm)) +
+                            (mb == neg_inf() ? 0.f : red_sum[64 + row] * exp2_hw(mb - mm)));
+      float tot = 0.f;
+      if (!a.pre_softmax) {
+        // logaddexp(local_lse, lse) in base 2, back to natural units.
+        const float lv2 = r < L ? lse_base[((int)r * a.Hkv + h) * G + g] * kLog2e : 0.f;
+        const float hi = fmaxf(lv2, lse2), lo = fminf(lv2, lse2);
+        tot = hi == neg_inf() ? neg_inf() : (hi + log2_hw(1.f + exp2_hw(lo - hi))) * kLn2;
+      }
+#pragma unroll
+      for (int t = 0; t < kNT; ++t) {
+        const float xb = S[t][i];
+        M[t][i] = fmaxf(M[t][i], xb == neg_inf() ? xb : xb - tot);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) Acur[j] = Anext[j];
+  }
+
+  select_step<G>(a, M, lmk_buf((G - 1) & 1), cbad, slot_s, ntot_s, q0, qbase, L, C, h, b, lane, wave,
+                 col, grp, qg, cbase);
+  load_q(head_of(G), Acur);
+
+  // Pass 2: raw logit bf16(q.lmk * scale) of every picked chunk, heads G-1..0.
+  // The picks of a head are gathered in list order in an LDS row buffer and
+  // written out as contiguous K-slot row segments.
+  const int nrows = (int)min((int64_t)kFastQ, L - q0);
+  for (int s = G; s < 2 * G; ++s) {
+    const int g = head_of(s);
+    begin_step(s, true);
+    f32x4_t S[kNT];
+    logits(lmk_buf(s & 1), Acur, S);
+#pragma unroll
+    for (int t = 0; t < kNT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 16 * qg + 4 * grp + i;
+        const int c = cbase + 16 * t + col;
+        const int slot = slot_s[row * 256 + c];
+        if (slot >= 0) sc_s[row * K + slot] = (uint16_t)f32_to_bf16(S[t][i] * a.sm_scale);
+      }
+    __syncthreads();
+    for (int e = tid; e < nrows * K; e += kFastThreads) {
+      const int row = e / K, slot = e - row * K;
+      sc16[(((b * L + q0 + row) * a.Hkv + h) * G + g) * K + slot] =
+          slot < ntot_s[row] ? sc_s[e] : (uint16_t)0xff80u;  // -inf past the picks
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) Acur[j] = Anext[j];
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -657,7 +724,7 @@ __global__ void __launch_bounds__(kGenThreads) route_topk_generic_kernel(RouteAr
 
 template <int G>
 int launch_fast(const RouteArgs& a, hipStream_t s) {
-  const size_t smem = FastLayout::total;
+  const size_t smem = FastLayout::total(a.K);
   auto kern = route_topk_mfma_kernel<G>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
@@ -716,7 +783,7 @@ extern "C" int mrsa_route_topk_fwd(const void* q, const void* lmk, const float* 
 
   const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)lmk % 16 == 0);
   const bool fast = !scores_fp32 && !is_causal && head_dim == 128 &&
-                    seq_len * kv_heads * groups * head_dim < ((int64_t)1 << 31) && chunks <= 256 && topk <= 127 && aligned &&
+                    seq_len * kv_heads * groups * head_dim < ((int64_t)1 << 31) && chunks <= 256 && topk <= kFastMaxTopk && aligned &&
                     (groups == 7 || groups == 8);
   if (fast) return groups == 7 ? launch_fast<7>(a, s) : launch_fast<8>(a, s);
   const size_t smem = ((size_t)groups * chunks + chunks + groups * head_dim + groups + 16) * 4 +

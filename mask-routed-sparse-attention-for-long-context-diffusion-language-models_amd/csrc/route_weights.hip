@@ -1,5 +1,5 @@
-// Route weights: one lane per (token, query head) normalises the topk routed
-// chunk logits together with the local-branch LSE.
+// Route weights: the topk routed chunk logits of each (token, query head) are
+// normalised together with the local-branch LSE.
 //
 // Semantics: _route_weights_torch (dream_dllm_hils/attention.py:126-235):
 //   remote_k = valid(idx_k) ? float(score_k) + prior_bias[idx_k] : -inf
@@ -10,7 +10,14 @@
 //                remote_w = softmax(remote) * mass, local_w = 1 - mass
 // The TileLang route_weights kernel (ops/hils_bidir_route_weights_tilelang.py:15-94)
 // computes the plain form with temperature 1.
+//
+// Work split: LPR lanes cooperate on one (token, query head) row, 8
+// consecutive slots per lane.  Score, index and weight rows move as 16-byte
+// vectors when topk % 8 == 0, so a wave reads or writes 1 KB per instruction;
+// the row max / sum are reduced across the LPR lanes.
 #include "mrsa_device.h"
+
+#include <type_traits>
 
 using namespace mrsa;
 
@@ -18,88 +25,135 @@ namespace {
 
 constexpr int kMaxTopk = 64;
 
+template <int LPR, bool VEC>
 __global__ void __launch_bounds__(256)
     route_weights_kernel(const uint16_t* __restrict__ scores, const int32_t* __restrict__ indices,
                          const float* __restrict__ bias, const float* __restrict__ lse,
                          int64_t rows, int64_t L, int64_t C, int Hkv, int G, int K, float inv_t,
                          int has_off, float off, int affine, float gscale,
                          uint16_t* __restrict__ rw, uint16_t* __restrict__ lw) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows) return;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int part = (int)(t % LPR);
+  const int64_t r0 = t / LPR;
+  const bool live = r0 < rows;
+  const int64_t r = live ? r0 : rows - 1;  // lanes past the end still join the row reductions
   const int Hq = Hkv * G;
   const int hq = (int)(r % Hq);
   const int64_t bl = r / Hq;
   const int64_t b = bl / L;
   const int hk = hq / G, g = hq - hk * G;
-  const uint16_t* sc = scores + r * K;
-  const int32_t* ix = indices + (bl * Hkv + hk) * K;
+  const int k0 = part * 8;
+  const uint16_t* sc = scores + r * K + k0;
+  const int32_t* ix = indices + (bl * Hkv + hk) * K + k0;
 
-  float x[kMaxTopk];
-  float rmax = neg_inf();
+  uint32_t sv[4] = {0u, 0u, 0u, 0u};
+  int32_t iv[8];
+  if (VEC && k0 < K) {
+    const u32x4_t s4 = *reinterpret_cast<const u32x4_t*>(sc);
+    const u32x4_t i0 = *reinterpret_cast<const u32x4_t*>(ix);
+    const u32x4_t i1 = *reinterpret_cast<const u32x4_t*>(ix + 4);
 #pragma unroll
-  for (int k = 0; k < kMaxTopk; ++k) {
-    if (k < K) {
-      const int32_t c = ix[k];
-      float v = neg_inf();
-      if (c >= 0 && c < C) v = bf16_to_f32(sc[k]) + bias[((b * C + c) * Hkv + hk) * G + g];
-      x[k] = v * inv_t;
-      rmax = fmaxf(rmax, x[k]);
+    for (int j = 0; j < 4; ++j) {
+      sv[j] = s4[j];
+      iv[j] = (int32_t)i0[j];
+      iv[4 + j] = (int32_t)i1[j];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const bool in = k0 + j < K;
+      const uint32_t h = in ? sc[j] : 0u;
+      sv[j >> 1] |= (j & 1) ? (h << 16) : h;
+      iv[j] = in ? ix[j] : -1;
     }
   }
+  float x[8];
+  float rmax = neg_inf();
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int32_t c = iv[j];
+    float v = neg_inf();
+    if (k0 + j < K && c >= 0 && c < C) {
+      const float s = (j & 1) ? bf16_hi(sv[j >> 1]) : bf16_lo(sv[j >> 1]);
+      v = (s + bias[((b * C + c) * Hkv + hk) * G + g]) * inv_t;
+    }
+    x[j] = v;
+    rmax = fmaxf(rmax, v);
+  }
+#pragma unroll
+  for (int o = 1; o < LPR; o <<= 1) rmax = fmaxf(rmax, __shfl_xor(rmax, o, 64));
   float local = lse[r];
   if (has_off && !affine) local -= off;
   local *= inv_t;
 
-  uint16_t* out = rw + r * K;
+  // Every lane of a row takes the same branch (m and rmax are row-uniform),
+  // so the reductions inside the branches stay within active lanes.
+  float lw_val = 0.f;
   const float m = fmaxf(rmax, local);
-  if (m == neg_inf()) {  // every logit masked
-    for (int k = 0; k < K; ++k) out[k] = 0;
-    lw[r] = 0;
-    return;
-  }
-  if (!affine) {
+  if (m == neg_inf()) {  // every logit masked: both outputs zero
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = 0.f;
+  } else if (!affine) {
     float sum = 0.f;
 #pragma unroll
-    for (int k = 0; k < kMaxTopk; ++k)
-      if (k < K) {
-        x[k] = x[k] == neg_inf() ? 0.f : expf(x[k] - m);
-        sum += x[k];
-      }
+    for (int j = 0; j < 8; ++j) {
+      x[j] = x[j] == neg_inf() ? 0.f : expf(x[j] - m);
+      sum += x[j];
+    }
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) sum += __shfl_xor(sum, o, 64);
     const float el = local == neg_inf() ? 0.f : expf(local - m);
     sum += el;
 #pragma unroll
-    for (int k = 0; k < kMaxTopk; ++k)
-      if (k < K) out[k] = (uint16_t)f32_to_bf16(x[k] / sum);
-    lw[r] = (uint16_t)f32_to_bf16(el / sum);
-    return;
-  }
-  // Affine-sigmoid gate.
-  float mass;
-  if (rmax == neg_inf()) {
-    // No routed chunk: softmax of the remote part is zeroed, gate -> local.
-    mass = 0.f;
+    for (int j = 0; j < 8; ++j) x[j] = x[j] / sum;
+    lw_val = el / sum;
+  } else if (rmax == neg_inf()) {
+    // Affine gate with no routed chunk: remote softmax zeroed, gate -> local.
 #pragma unroll
-    for (int k = 0; k < kMaxTopk; ++k)
-      if (k < K) x[k] = 0.f;
+    for (int j = 0; j < 8; ++j) x[j] = 0.f;
+    lw_val = 1.f;
   } else {
     float sum = 0.f;
 #pragma unroll
-    for (int k = 0; k < kMaxTopk; ++k)
-      if (k < K) {
-        x[k] = x[k] == neg_inf() ? 0.f : expf(x[k] - rmax);
-        sum += x[k];
-      }
+    for (int j = 0; j < 8; ++j) {
+      x[j] = x[j] == neg_inf() ? 0.f : expf(x[j] - rmax);
+      sum += x[j];
+    }
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) sum += __shfl_xor(sum, o, 64);
     const float remote_lse = rmax + logf(sum);
     const float gate = gscale * (remote_lse - local) + (has_off ? off : 0.f);
-    mass = 1.f / (1.f + expf(-gate));
+    const float mass = 1.f / (1.f + expf(-gate));
 #pragma unroll
-    for (int k = 0; k < kMaxTopk; ++k)
-      if (k < K) x[k] = x[k] / sum;
+    for (int j = 0; j < 8; ++j) x[j] = (x[j] / sum) * mass;
+    lw_val = 1.f - mass;
   }
+  if (!live) return;
+  uint16_t* out = rw + r * K + k0;
+  if (VEC && k0 < K) {
+    u32x4_t o4;
 #pragma unroll
-  for (int k = 0; k < kMaxTopk; ++k)
-    if (k < K) out[k] = (uint16_t)f32_to_bf16(x[k] * mass);
-  lw[r] = (uint16_t)f32_to_bf16(1.f - mass);
+    for (int j = 0; j < 4; ++j) o4[j] = pack_bf16x2(x[2 * j], x[2 * j + 1]);
+    *reinterpret_cast<u32x4_t*>(out) = o4;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (k0 + j < K) out[j] = (uint16_t)f32_to_bf16(x[j]);
+  }
+  if (part == 0) lw[r] = (uint16_t)f32_to_bf16(lw_val);
+}
+
+template <int LPR>
+int launch_rw(bool vec, hipStream_t s, const uint16_t* scores, const int32_t* indices,
+              const float* bias, const float* lse, int64_t rows, int64_t L, int64_t C, int Hkv,
+              int G, int K, float inv_t, int has_off, float off, int affine, float gscale,
+              uint16_t* rw, uint16_t* lw) {
+  const int64_t blocks = (rows * LPR + 255) / 256;
+  if (blocks > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
+  auto kern = vec ? route_weights_kernel<LPR, true> : route_weights_kernel<LPR, false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, s, scores, indices, bias, lse,
+                     rows, L, C, Hkv, G, K, inv_t, has_off, off, affine, gscale, rw, lw);
+  return mrsa_launch_status();
 }
 
 }  // namespace
@@ -119,12 +173,18 @@ extern "C" int mrsa_route_weights_fwd(const void* scores, const int32_t* indices
   if (rows == 0) return MRSA_OK;
   if (!scores || !indices || !prior_bias || !local_lse || !remote_weights || !local_weight)
     return MRSA_ERR_INVALID_ARGUMENT;
-  const int64_t blocks = (rows + 255) / 256;
-  if (blocks > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(route_weights_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                     (hipStream_t)stream, (const uint16_t*)scores, indices, prior_bias, local_lse,
-                     rows, seq_len, chunks, (int)kv_heads, (int)groups, (int)topk,
-                     1.f / temperature, has_gate_offset, gate_offset, has_gate_scale, gate_scale,
-                     (uint16_t*)remote_weights, (uint16_t*)local_weight);
-  return mrsa_launch_status();
+  const bool vec = topk % 8 == 0 && ((uintptr_t)scores | (uintptr_t)indices |
+                                     (uintptr_t)remote_weights) % 16 == 0;
+  hipStream_t s = (hipStream_t)stream;
+  const int lanes = (int)((topk + 7) / 8);
+  auto go = [&](auto lpr) {
+    return launch_rw<decltype(lpr)::value>(
+        vec, s, (const uint16_t*)scores, indices, prior_bias, local_lse, rows, seq_len, chunks,
+        (int)kv_heads, (int)groups, (int)topk, 1.f / temperature, has_gate_offset, gate_offset,
+        has_gate_scale, gate_scale, (uint16_t*)remote_weights, (uint16_t*)local_weight);
+  };
+  if (lanes <= 1) return go(std::integral_constant<int, 1>{});
+  if (lanes <= 2) return go(std::integral_constant<int, 2>{});
+  if (lanes <= 4) return go(std::integral_constant<int, 4>{});
+  return go(std::integral_constant<int, 8>{});
 }

@@ -176,39 +176,115 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
 }
 
-template <bool TOKEN, int R, int CPS, class SP>
-__global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) {
-  constexpr int kWaves = SP::kWaves, kThreads = SP::kThreads, kNtile = SP::kNtile;
-  constexpr int kQPW = SP::kQPW, kTQ = SP::kTQ;
-  // Every chunk of a group must have been issued before the group's barrier
-  // (R - CPS >= CPS), and at most 3 chunks are ever in flight past it.
-  static_assert(R - CPS >= CPS && R - CPS <= 3, "ring depth");
-  constexpr int kAhead = R - CPS;  // chunks issued ahead of the group being consumed
-  extern __shared__ __align__(16) unsigned char smem[];
+// Per-column softmax of one chunk's S^T tile (64 keys x 16 columns, this
+// lane's 16 values S[t][i] = key 16t + 4grp + i), scaled by the routing weight
+// of the lane's column, rounded to bf16 as the P^T operands of the PV product
+// (reduction slot e of lane group grp for half jj = key 32jj + 16(e/4) +
+// 4grp + e%4).  Keys with a bit in `msk` are excluded (msh = msk >> 4grp);
+// an all-excluded column gives P = 0.  Units of log2 with the scale folded
+// into one FMA (scale_log2 > 0, so the max of the raw products is the max
+// logit).
+__device__ __forceinline__ void masked_softmax_p(f32x4_t (&S)[4], uint64_t msk, uint64_t msh,
+                                                 int grp, float c2, float wv, u32x4_t (&Pb)[2]) {
+  if (msk == (1ull << 63)) {
+    if (grp == 3) S[3][3] = neg_inf();
+  } else if (msk != 0ull) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if ((msh >> (16 * t + i)) & 1ull) S[t][i] = neg_inf();
+  }
+  float mx = fmaxf(fmaxf(S[0][0], S[0][1]), fmaxf(S[0][2], S[0][3]));
+#pragma unroll
+  for (int t = 1; t < 4; ++t)
+    mx = fmaxf(mx, fmaxf(fmaxf(S[t][0], S[t][1]), fmaxf(S[t][2], S[t][3])));
+  mx = across4_max(mx);
+  const float mb = mx == neg_inf() ? 0.f : mx * c2;
+  float part[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) S[t][i] = exp2_hw(__builtin_fmaf(S[t][i], c2, -mb));
+    part[t] = (S[t][0] + S[t][1]) + (S[t][2] + S[t][3]);
+  }
+  const float sum = across4_sum((part[0] + part[1]) + (part[2] + part[3]));
+  const float f = sum > 0.f ? wv * rcp_hw(sum) : 0.f;
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    Pb[jj][0] = pack_bf16x2(S[2 * jj][0] * f, S[2 * jj][1] * f);
+    Pb[jj][1] = pack_bf16x2(S[2 * jj][2] * f, S[2 * jj][3] * f);
+    Pb[jj][2] = pack_bf16x2(S[2 * jj + 1][0] * f, S[2 * jj + 1][1] * f);
+    Pb[jj][3] = pack_bf16x2(S[2 * jj + 1][2] * f, S[2 * jj + 1][3] * f);
+  }
+}
+
+// S^T = K . Q^T for one column tile: 16 K operand reads from an LDS chunk slot
+// (swizzled rows, kaddr[j] = lane address of reduction step j) and 16
+// products, read o + 8 issued after product o so eight reads stay in flight.
+// DEPTH reads stay in flight (8 when registers allow, 4 for the 12-wave split).
+template <int DEPTH = 8>
+__device__ __forceinline__ void qk_tile(const uint32_t (&kaddr)[4], const u32x4_t (&Q)[4],
+                                        f32x4_t (&S)[4]) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) S[t] = zero4();
+  u32x4_t kb[16];
+  static_for<16>([&](auto oc) {
+    constexpr int o = decltype(oc)::value;
+    if constexpr (o < DEPTH) kb[o] = lds_read_b128<(o & 3) * 4096>(kaddr[o >> 2]);
+  });
+  static_for<16>([&](auto oc) {
+    constexpr int o = decltype(oc)::value;
+    lds_wait<(15 - o < DEPTH - 1 ? 15 - o : DEPTH - 1)>(kb[o]);
+    S[o & 3] = mfma_bf16_16x16x32(kb[o], Q[o >> 2], S[o & 3]);
+    if constexpr (o + DEPTH < 16)
+      kb[o + DEPTH] = lds_read_b128<((o + DEPTH) & 3) * 4096>(kaddr[(o + DEPTH) >> 2]);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+}
+
+// LDS arrays the prologue fills (s_*, wr, comp_slot, misc) or uses as
+// scratch (p_*).
+struct WalkLds {
+  uint16_t* wr;         // [TQ][K][8] bf16 weights in list order (attention mode)
+  uint16_t* wts;        // [TQ][8][K] bf16 staged weights (scratch)
+  int32_t* s_chunk;     // [cap] chunk of each walk step
+  uint64_t* s_own;      // [cap] owner bits (query i of the tile -> bit i)
+  uint64_t* s_mask;     // [cap] excluded-key bits (invalid keys, landmark slot)
+  uint8_t* comp_slot;   // [TQ][K] list position -> original slot
+  int32_t* misc;        // [waves] scan, [waves] step count
+  int32_t* p_idx;       // [TQ][K] staged / compacted index rows (scratch)
+  uint8_t* p_kv;        // [Ck][8] key-valid bits (scratch)
+  uint64_t* p_omask;    // [Ck] owner bits by chunk (scratch)
+  int32_t* p_len;       // [TQ] list lengths (scratch)
+};
+
+// Prologue shared by both routed-attention kernels: stages the tile's index
+// rows, weights and key-valid bits, compacts each query's list the way the
+// reference kernel reads it (stop at the first negative entry, skip >= Ck,
+// sort, merge duplicates by summing weights), builds the ascending walk over
+// the union of the tile's chunks, and (attention mode) the weights in list
+// order.  Returns the number of walk steps.  Ends with a workgroup barrier.
+template <bool TOKEN, class SP>
+__device__ int build_walk(const SelArgs& a, const WalkLds& W, int64_t b, int h, int64_t q0,
+                          int64_t nq) {
+  constexpr int kWaves = SP::kWaves, kThreads = SP::kThreads, kTQ = SP::kTQ;
   const int K = a.K;
   const int64_t Ck = a.Ck;
-  const SelLayout lay = sel_layout(kTQ, kWaves, K, Ck, R, TOKEN);
-  unsigned char* ring = smem + lay.ring;
-  uint16_t* wr = reinterpret_cast<uint16_t*>(smem + lay.wr);            // [TQ][K][8]
-  uint16_t* wts = reinterpret_cast<uint16_t*>(smem + lay.p_w);          // [TQ][8][K]
-  int32_t* s_chunk = reinterpret_cast<int32_t*>(smem + lay.s_chunk);    // [cap] walk order
-  uint64_t* s_own = reinterpret_cast<uint64_t*>(smem + lay.s_own);      // [cap] owner bits
-  uint64_t* s_mask = reinterpret_cast<uint64_t*>(smem + lay.s_mask);    // [cap] masked keys
-  uint8_t* comp_slot = smem + lay.comp_slot;                            // [TQ][K]
-  int32_t* misc = reinterpret_cast<int32_t*>(smem + lay.misc);          // [kWaves] scan, [kWaves] n
-  int32_t* p_idx = reinterpret_cast<int32_t*>(smem + lay.p_idx);        // [TQ][K]
-  uint8_t* p_kv = smem + lay.p_kv;                                      // [Ck][8] key-valid bytes
-  uint64_t* p_omask = reinterpret_cast<uint64_t*>(smem + lay.p_omask);  // [Ck]
-  int32_t* p_len = reinterpret_cast<int32_t*>(smem + lay.p_len);        // [TQ]
-
+  const int G = a.G;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int col = lane & 15, grp = lane >> 4;
-  const int64_t b = blockIdx.z;
-  const int h = blockIdx.y;
-  const int64_t q0 = (int64_t)blockIdx.x * kTQ;
-  const int G = a.G;
-  const int64_t nq = min((int64_t)kTQ, a.Lq - q0);  // queries of this tile that exist
+  uint16_t* wr = W.wr;
+  uint16_t* wts = W.wts;
+  int32_t* s_chunk = W.s_chunk;
+  uint64_t* s_own = W.s_own;
+  uint64_t* s_mask = W.s_mask;
+  uint8_t* comp_slot = W.comp_slot;
+  int32_t* misc = W.misc;
+  int32_t* p_idx = W.p_idx;
+  uint8_t* p_kv = W.p_kv;
+  uint64_t* p_omask = W.p_omask;
+  int32_t* p_len = W.p_len;
 
   // 1. Stage the tile's index rows (-1 past the end of the sequence), routing
   //    weights ([TQ][8][K], head columns >= G zero) and key-valid bits
@@ -359,7 +435,47 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
     if (tid == 0) misc[kWaves] = total;
   }
   __syncthreads();
-  const int nsteps = misc[kWaves];
+  return misc[kWaves];
+}
+
+template <bool TOKEN, int R, int CPS, class SP>
+__global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) {
+  constexpr int kWaves = SP::kWaves, kThreads = SP::kThreads, kNtile = SP::kNtile;
+  constexpr int kQPW = SP::kQPW, kTQ = SP::kTQ;
+  constexpr int kDepth = kWaves > 8 ? 4 : 8;  // LDS operand reads in flight
+  // Every chunk of a group must have been issued before the group's barrier
+  // (R - CPS >= CPS), and at most 3 chunks are ever in flight past it.
+  static_assert(R - CPS >= CPS && R - CPS <= 3, "ring depth");
+  constexpr int kAhead = R - CPS;  // chunks issued ahead of the group being consumed
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int K = a.K;
+  const int64_t Ck = a.Ck;
+  const SelLayout lay = sel_layout(kTQ, kWaves, K, Ck, R, TOKEN);
+  unsigned char* ring = smem + lay.ring;
+  uint16_t* wr = reinterpret_cast<uint16_t*>(smem + lay.wr);            // [TQ][K][8]
+  uint16_t* wts = reinterpret_cast<uint16_t*>(smem + lay.p_w);          // [TQ][8][K]
+  int32_t* s_chunk = reinterpret_cast<int32_t*>(smem + lay.s_chunk);    // [cap] walk order
+  uint64_t* s_own = reinterpret_cast<uint64_t*>(smem + lay.s_own);      // [cap] owner bits
+  uint64_t* s_mask = reinterpret_cast<uint64_t*>(smem + lay.s_mask);    // [cap] masked keys
+  uint8_t* comp_slot = smem + lay.comp_slot;                            // [TQ][K]
+  int32_t* misc = reinterpret_cast<int32_t*>(smem + lay.misc);          // [kWaves] scan, [kWaves] n
+  int32_t* p_idx = reinterpret_cast<int32_t*>(smem + lay.p_idx);        // [TQ][K]
+  uint8_t* p_kv = smem + lay.p_kv;                                      // [Ck][8] key-valid bytes
+  uint64_t* p_omask = reinterpret_cast<uint64_t*>(smem + lay.p_omask);  // [Ck]
+  int32_t* p_len = reinterpret_cast<int32_t*>(smem + lay.p_len);        // [TQ]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int64_t b = blockIdx.z;
+  const int h = blockIdx.y;
+  const int64_t q0 = (int64_t)blockIdx.x * kTQ;
+  const int G = a.G;
+  const int64_t nq = min((int64_t)kTQ, a.Lq - q0);  // queries of this tile that exist
+
+  const int nsteps = build_walk<TOKEN, SP>(
+      a, WalkLds{wr, wts, s_chunk, s_own, s_mask, comp_slot, misc, p_idx, p_kv, p_omask, p_len}, b, h,
+      q0, nq);
 
   // 4. Q^T operands and accumulators of this wave's queries.
   u32x4_t Qb[kNtile][4];
@@ -452,25 +568,10 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
       asm volatile("" : "+v"(zoff));
       const uint16_t* Kt = Kb + zoff;
 
-      // S^T = K . Q^T: 16 operand reads and 16 products; read o + 8 is issued
-      // after product o, so eight reads stay in flight.
-      f32x4_t S[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) S[t] = zero4();
       const uint32_t kaddr[4] = {lds_addr(Kt + kofs(0)), lds_addr(Kt + kofs(1)),
                                  lds_addr(Kt + kofs(2)), lds_addr(Kt + kofs(3))};
-      u32x4_t kb[16];
-      static_for<16>([&](auto oc) {
-        constexpr int o = decltype(oc)::value;
-        if constexpr (o < 8) kb[o] = lds_read_b128<(o & 3) * 4096>(kaddr[o >> 2]);
-      });
-      static_for<16>([&](auto oc) {
-        constexpr int o = decltype(oc)::value;
-        lds_wait<(15 - o < 7 ? 15 - o : 7)>(kb[o]);
-        S[o & 3] = mfma_bf16_16x16x32(kb[o], Qb[nt][o >> 2], S[o & 3]);
-        if constexpr (o + 8 < 16) kb[o + 8] = lds_read_b128<((o + 8) & 3) * 4096>(kaddr[(o + 8) >> 2]);
-        __builtin_amdgcn_sched_barrier(0);
-      });
+      f32x4_t S[4];
+      qk_tile<kDepth>(kaddr, Qb[nt], S);
       // The first V^T operands do not depend on P: read them now so they land
       // during the softmax.  PV operand o = 8 * jj + td.
       const uint32_t vaddr[2] = {lds_addr(Kt + vofs(0)), lds_addr(Kt + vofs(1))};
@@ -507,51 +608,20 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
           }
         }
       } else {
-        if (msk == (1ull << 63)) {
-          if (grp == 3) S[3][3] = neg_inf();
-        } else if (msk != 0ull) {
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if ((msh >> (16 * t + i)) & 1ull) S[t][i] = neg_inf();
-        }
-        // Softmax in units of log2 with the scale folded into the FMA
-        // (scale_log2 > 0: the max of the raw products is the max logit).
-        float mx = fmaxf(fmaxf(S[0][0], S[0][1]), fmaxf(S[0][2], S[0][3]));
-#pragma unroll
-        for (int t = 1; t < 4; ++t)
-          mx = fmaxf(mx, fmaxf(fmaxf(S[t][0], S[t][1]), fmaxf(S[t][2], S[t][3])));
-        mx = across4_max(mx);
-        const float mb = mx == neg_inf() ? 0.f : mx * c2;
-        float part[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) S[t][i] = exp2_hw(__builtin_fmaf(S[t][i], c2, -mb));
-          part[t] = (S[t][0] + S[t][1]) + (S[t][2] + S[t][3]);
-        }
-        const float sum = across4_sum((part[0] + part[1]) + (part[2] + part[3]));
-        const float f = sum > 0.f ? wv * rcp_hw(sum) : 0.f;
         u32x4_t Pb[2];
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          Pb[jj][0] = pack_bf16x2(S[2 * jj][0] * f, S[2 * jj][1] * f);
-          Pb[jj][1] = pack_bf16x2(S[2 * jj][2] * f, S[2 * jj][3] * f);
-          Pb[jj][2] = pack_bf16x2(S[2 * jj + 1][0] * f, S[2 * jj + 1][1] * f);
-          Pb[jj][3] = pack_bf16x2(S[2 * jj + 1][2] * f, S[2 * jj + 1][3] * f);
-        }
+        masked_softmax_p(S, msk, msh, grp, c2, wv, Pb);
         // O^T += V^T . P^T with eight reads in flight; consecutive products go
         // to different accumulators.
-        static_for<4>([&](auto oc) {
+        static_for<kDepth - 4>([&](auto oc) {
           constexpr int o = decltype(oc)::value + 4;
           vb[o] = lds_read_b128<(o & 7) * 2048>(vaddr[o >> 3]);
         });
         static_for<16>([&](auto oc) {
           constexpr int o = decltype(oc)::value;
-          lds_wait<(15 - o < 7 ? 15 - o : 7)>(vb[o]);
+          lds_wait<(15 - o < kDepth - 1 ? 15 - o : kDepth - 1)>(vb[o]);
           acc[nt][o & 7] = mfma_bf16_16x16x32(vb[o], Pb[o >> 3], acc[nt][o & 7]);
-          if constexpr (o + 8 < 16) vb[o + 8] = lds_read_b128<((o + 8) & 7) * 2048>(vaddr[(o + 8) >> 3]);
+          if constexpr (o + kDepth < 16)
+            vb[o + kDepth] = lds_read_b128<((o + kDepth) & 7) * 2048>(vaddr[(o + kDepth) >> 3]);
           __builtin_amdgcn_sched_barrier(0);
         });
       }

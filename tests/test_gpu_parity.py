@@ -195,13 +195,13 @@ def test_route_topk_g7_api_and_determinism():
                  lm.cpu().reshape(1, C, 28, 128), lse.cpu(), bias.cpu(), dropped.cpu(), 32, "g7 api")
 
 
-@pytest.mark.parametrize("affine", [True, False])
-def test_route_weights_vs_oracle(affine):
-    _note(f"route weights affine={affine}")
-    B, L, Hkv, G, K, C = 1, 700, 4, 7, 32, 256
+@pytest.mark.parametrize("affine,K", [(True, 32), (False, 32), (False, 64), (True, 8), (True, 20)])
+def test_route_weights_vs_oracle(affine, K):
+    _note(f"route weights affine={affine} K={K}")
+    B, L, Hkv, G, C = 1, 700, 4, 7, 256
     scores = _rand((B, L, Hkv * G, K), 20).bfloat16()
     idx = torch.randint(0, C, (B, L, Hkv, K), generator=torch.Generator().manual_seed(21)).int()
-    idx[0, 3, 1, 20:] = -1
+    idx[0, 3, 1, K // 2:] = -1
     idx[0, 4, 2, :] = -1
     bias = torch.rand(B, C, Hkv, G) + 3.5
     lse = _rand((B, L, Hkv * G), 22) + 5.0
@@ -212,7 +212,7 @@ def test_route_weights_vs_oracle(affine):
     er, el = O.route_weights(scores, idx, bias, lse, **kw)
     torch.testing.assert_close(rw.cpu().float(), er.bfloat16().float(), atol=2e-3, rtol=1e-2)
     torch.testing.assert_close(lw.cpu().float(), el.bfloat16().float(), atol=2e-3, rtol=1e-2)
-    if not affine:
+    if not affine and K == 32:
         torch.testing.assert_close(
             mrsa.route_weights(scores[:, :, :, :31].contiguous().to(DEV), idx[..., :31].contiguous().to(DEV),
                                bias.to(DEV), lse.to(DEV))[1].cpu().float(),
