@@ -47,8 +47,16 @@ constexpr int kDmaWaves = 8;            // waves 0-3 fetch K, 4-7 fetch V^T
 constexpr int kSlotBytes = 32768;       // one chunk: K (16 KB) + V^T (16 KB)
 constexpr int kMaxTopk = 64;
 constexpr size_t kMaxLds = 160 * 1024;
+constexpr int kSyncSlots = 4;           // ring slots the walk counters cover (R <= 4)
+constexpr int kSpinLimit = 1 << 16;     // bound on every wait for a ring slot (~4M clocks)
+#ifndef MRSA_SEL_SYNC
+#define MRSA_SEL_SYNC 1                 // 1: per-slot counters, 0: workgroup barrier per CPS chunks
+#endif
 #ifndef MRSA_SEL_CPS4
 #define MRSA_SEL_CPS4 2                 // chunks per barrier with a 4-slot ring
+#endif
+#ifndef MRSA_SEL_INTERLEAVE
+#define MRSA_SEL_INTERLEAVE 1           // query pairs dealt round-robin over the waves
 #endif
 #ifndef MRSA_SEL_WAVES
 #define MRSA_SEL_WAVES 8                // work split: 8 (8 waves x 3 tiles), 82 (8 x 2), 12 (12 x 2)
@@ -93,7 +101,7 @@ struct SelArgs {
 // LDS carve-up (byte offsets, 16-aligned).  The p_* arrays are only used by
 // the prologue and live inside the ring, which is free until the first DMA.
 struct SelLayout {
-  size_t ring, wr, s_chunk, s_own, s_mask, comp_slot, misc, total;
+  size_t ring, wr, s_chunk, s_own, s_mask, s_done, comp_slot, misc, total;
   size_t p_idx, p_kv, p_omask, p_len, p_w, p_end;
   int cap;
 };
@@ -110,8 +118,9 @@ __host__ __device__ inline SelLayout sel_layout(int TQ, int NW, int K, int64_t C
   l.s_chunk = o;   o = align16(o + (size_t)l.cap * 4);
   l.s_own = o;     o = align16(o + (size_t)l.cap * 8);
   l.s_mask = o;    o = align16(o + (size_t)l.cap * 8);
+  l.s_done = o;    o = align16(o + (size_t)l.cap * 4);
   l.comp_slot = o; o = align16(o + n);
-  l.misc = o;      o = align16(o + (size_t)(NW + 4) * 4);
+  l.misc = o;      o = align16(o + (size_t)(NW + 4 + kSyncSlots) * 4);
   l.total = o;
   o = l.ring;
   l.p_idx = o;     o = align16(o + n * 4);
@@ -161,6 +170,27 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
+// Walk counters in LDS, accessed with asm so the compiler does not order
+// them behind the in-flight global->LDS DMA (it waits for vmcnt(0) before
+// any LDS atomic that may alias a DMA destination).
+__device__ __forceinline__ int lds_load_flag(uint32_t addr) {
+  int v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+__device__ __forceinline__ void lds_store_flag(uint32_t addr, int v) {
+  asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ int lds_fetch_inc(uint32_t addr) {
+  int old;
+  const int one = 1;
+  asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
+               : "=v"(old)
+               : "v"(addr), "v"(one)
+               : "memory");
+  return old;
+}
+
 __device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
@@ -174,49 +204,6 @@ __device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int
 template <int N, class F>
 __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
-}
-
-// Per-column softmax of one chunk's S^T tile (64 keys x 16 columns, this
-// lane's 16 values S[t][i] = key 16t + 4grp + i), scaled by the routing weight
-// of the lane's column, rounded to bf16 as the P^T operands of the PV product
-// (reduction slot e of lane group grp for half jj = key 32jj + 16(e/4) +
-// 4grp + e%4).  Keys with a bit in `msk` are excluded (msh = msk >> 4grp);
-// an all-excluded column gives P = 0.  Units of log2 with the scale folded
-// into one FMA (scale_log2 > 0, so the max of the raw products is the max
-// logit).
-__device__ __forceinline__ void masked_softmax_p(f32x4_t (&S)[4], uint64_t msk, uint64_t msh,
-                                                 int grp, float c2, float wv, u32x4_t (&Pb)[2]) {
-  if (msk == (1ull << 63)) {
-    if (grp == 3) S[3][3] = neg_inf();
-  } else if (msk != 0ull) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if ((msh >> (16 * t + i)) & 1ull) S[t][i] = neg_inf();
-  }
-  float mx = fmaxf(fmaxf(S[0][0], S[0][1]), fmaxf(S[0][2], S[0][3]));
-#pragma unroll
-  for (int t = 1; t < 4; ++t)
-    mx = fmaxf(mx, fmaxf(fmaxf(S[t][0], S[t][1]), fmaxf(S[t][2], S[t][3])));
-  mx = across4_max(mx);
-  const float mb = mx == neg_inf() ? 0.f : mx * c2;
-  float part[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) S[t][i] = exp2_hw(__builtin_fmaf(S[t][i], c2, -mb));
-    part[t] = (S[t][0] + S[t][1]) + (S[t][2] + S[t][3]);
-  }
-  const float sum = across4_sum((part[0] + part[1]) + (part[2] + part[3]));
-  const float f = sum > 0.f ? wv * rcp_hw(sum) : 0.f;
-#pragma unroll
-  for (int jj = 0; jj < 2; ++jj) {
-    Pb[jj][0] = pack_bf16x2(S[2 * jj][0] * f, S[2 * jj][1] * f);
-    Pb[jj][1] = pack_bf16x2(S[2 * jj][2] * f, S[2 * jj][3] * f);
-    Pb[jj][2] = pack_bf16x2(S[2 * jj + 1][0] * f, S[2 * jj + 1][1] * f);
-    Pb[jj][3] = pack_bf16x2(S[2 * jj + 1][2] * f, S[2 * jj + 1][3] * f);
-  }
 }
 
 // S^T = K . Q^T for one column tile: 16 K operand reads from an LDS chunk slot
@@ -441,7 +428,7 @@ __device__ int build_walk(const SelArgs& a, const WalkLds& W, int64_t b, int h, 
 template <bool TOKEN, int R, int CPS, class SP>
 __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) {
   constexpr int kWaves = SP::kWaves, kThreads = SP::kThreads, kNtile = SP::kNtile;
-  constexpr int kQPW = SP::kQPW, kTQ = SP::kTQ;
+  constexpr int kTQ = SP::kTQ;
   constexpr int kDepth = kWaves > 8 ? 4 : 8;  // LDS operand reads in flight
   // Every chunk of a group must have been issued before the group's barrier
   // (R - CPS >= CPS), and at most 3 chunks are ever in flight past it.
@@ -459,6 +446,10 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   uint64_t* s_mask = reinterpret_cast<uint64_t*>(smem + lay.s_mask);    // [cap] masked keys
   uint8_t* comp_slot = smem + lay.comp_slot;                            // [TQ][K]
   int32_t* misc = reinterpret_cast<int32_t*>(smem + lay.misc);          // [kWaves] scan, [kWaves] n
+  // Walk counters: waves done with each walk step, and per ring slot
+  // 1 + the index of the chunk whose data has landed in it.
+  int32_t* s_done = reinterpret_cast<int32_t*>(smem + lay.s_done);       // [cap]
+  int32_t* slot_ready = misc + kWaves + 4;                               // [kSyncSlots]
   int32_t* p_idx = reinterpret_cast<int32_t*>(smem + lay.p_idx);        // [TQ][K]
   uint8_t* p_kv = smem + lay.p_kv;                                      // [Ck][8] key-valid bytes
   uint64_t* p_omask = reinterpret_cast<uint64_t*>(smem + lay.p_omask);  // [Ck]
@@ -473,17 +464,25 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   const int G = a.G;
   const int64_t nq = min((int64_t)kTQ, a.Lq - q0);  // queries of this tile that exist
 
+  // Zeroed counters, published by the prologue's barriers.
+  if (tid < kSyncSlots) slot_ready[tid] = 0;
+  for (int i = tid; i < lay.cap; i += kThreads) s_done[i] = 0;
   const int nsteps = build_walk<TOKEN, SP>(
       a, WalkLds{wr, wts, s_chunk, s_own, s_mask, comp_slot, misc, p_idx, p_kv, p_omask, p_len}, b, h,
       q0, nq);
 
   // 4. Q^T operands and accumulators of this wave's queries.
+  //    Column tile nt of wave w holds query pair qpair(w, nt), i.e. queries
+  //    2 qpair and 2 qpair + 1 of the tile.  Neighbouring queries tend to route
+  //    to the same chunks, so dealing pairs round-robin over the waves spreads
+  //    each chunk's work over more waves than consecutive blocks would.
+  auto qpair = [&](int nt) { return MRSA_SEL_INTERLEAVE ? nt * kWaves + wave : wave * kNtile + nt; };
   u32x4_t Qb[kNtile][4];
   f32x4_t acc[kNtile][8];
   int rank[kNtile];
 #pragma unroll
   for (int nt = 0; nt < kNtile; ++nt) {
-    const int ql = wave * kQPW + 2 * nt + (col >> 3);
+    const int ql = 2 * qpair(nt) + (col >> 3);
     const int gg = col & 7;
     rank[nt] = 0;
 #pragma unroll
@@ -541,16 +540,15 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
     const uint64_t om = uniform_u64(s_own[st]);
     const uint64_t msk = uniform_u64(s_mask[st]);
     const uint16_t* Kb = reinterpret_cast<const uint16_t*>(ring + (st % R) * kSlotBytes);
-    const uint32_t wbits = (uint32_t)((om >> (wave * kQPW)) & ((1ull << kQPW) - 1ull));
     // This lane's excluded-key bits: bit 16t + i of msh is key 16t + 4grp + i.
     const uint64_t msh = msk >> (4 * grp);
 
 #pragma unroll
     for (int nt = 0; nt < kNtile; ++nt) {
-      const uint32_t pair = (wbits >> (2 * nt)) & 3u;
+      const uint32_t pair = (uint32_t)(om >> (2 * qpair(nt))) & 3u;
       if (pair == 0u) continue;
       const bool owns = (pair >> half) & 1u;
-      const int ql = wave * kQPW + 2 * nt + half;
+      const int ql = 2 * qpair(nt) + half;
       // List position of this chunk for the owning column; reads are made
       // unconditional (clamped index) so they do not split the block.
       const int pos = min(rank[nt], K - 1);
@@ -609,7 +607,37 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
         }
       } else {
         u32x4_t Pb[2];
-        masked_softmax_p(S, msk, msh, grp, c2, wv, Pb);
+        if (msk == (1ull << 63)) {
+          if (grp == 3) S[3][3] = neg_inf();
+        } else if (msk != 0ull) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if ((msh >> (16 * t + i)) & 1ull) S[t][i] = neg_inf();
+        }
+        float mx = fmaxf(fmaxf(S[0][0], S[0][1]), fmaxf(S[0][2], S[0][3]));
+#pragma unroll
+        for (int t = 1; t < 4; ++t)
+          mx = fmaxf(mx, fmaxf(fmaxf(S[t][0], S[t][1]), fmaxf(S[t][2], S[t][3])));
+        mx = across4_max(mx);
+        const float mb = mx == neg_inf() ? 0.f : mx * c2;
+        float part[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) S[t][i] = exp2_hw(__builtin_fmaf(S[t][i], c2, -mb));
+          part[t] = (S[t][0] + S[t][1]) + (S[t][2] + S[t][3]);
+        }
+        const float sum = across4_sum((part[0] + part[1]) + (part[2] + part[3]));
+        const float f = sum > 0.f ? wv * rcp_hw(sum) : 0.f;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          Pb[jj][0] = pack_bf16x2(S[2 * jj][0] * f, S[2 * jj][1] * f);
+          Pb[jj][1] = pack_bf16x2(S[2 * jj][2] * f, S[2 * jj][3] * f);
+          Pb[jj][2] = pack_bf16x2(S[2 * jj + 1][0] * f, S[2 * jj + 1][1] * f);
+          Pb[jj][3] = pack_bf16x2(S[2 * jj + 1][2] * f, S[2 * jj + 1][3] * f);
+        }
         // O^T += V^T . P^T with eight reads in flight; consecutive products go
         // to different accumulators.
         static_for<kDepth - 4>([&](auto oc) {
@@ -628,6 +656,105 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
     }
   };
 
+#if MRSA_SEL_SYNC
+  // 6. The walk, synchronised per ring slot instead of per workgroup, so that
+  //    waves drift apart by up to R chunks and the imbalance of their work
+  //    evens out over that window:
+  //    * the wave that frees slot st % R last (the last wave to count itself
+  //      done with step st) issues the whole DMA of chunk st + R into it;
+  //    * that wave publishes the chunk as landed at the start of its step
+  //      st + 2 (after waiting for its own DMA with vmcnt), so the wait
+  //      rarely blocks it;
+  //    * a wave with no query routed to chunk st neither waits for it nor
+  //      reads it.
+  //    Chunk n >= R is issued once every wave finished step n - R and
+  //    published at its issuer's step n - R + 2 <= n - 1, so every wait
+  //    depends only on earlier chunks and the walk cannot deadlock; the
+  //    spin bound keeps every wave finite regardless.
+  constexpr int kChunkDma = TOKEN ? 16 : 32;  // 1 KB DMA instructions per chunk
+  const uint32_t kc = (uint32_t)((col ^ grp) * 8);
+  const uint32_t v0 = (uint32_t)((lane >> 3) * 64 + ((lane ^ (lane >> 3)) & 7) * 8);
+  // DMA instruction j < 16 fetches K units 64j + lane: row 4j + grp, part
+  // (col ^ grp) ^ 4(j & 3); instruction 16 + j' fetches V^T units: row
+  // 8j' + lane / 8, part (lane ^ (lane / 8)) & 7.
+  auto issue_chunk = [&](int n) {
+    const int64_t c = __builtin_amdgcn_readfirstlane(s_chunk[n]);
+    unsigned char* slot = ring + (n % R) * kSlotBytes;
+    const uint16_t* kc0 = kbase + c * 64 * (int64_t)kstride + grp * kstride;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      __builtin_amdgcn_global_load_lds(kc0 + (4 * j) * kstride + (kc ^ (uint32_t)(32 * (j & 3))),
+                                       (lds_void_t*)(slot + j * 1024), 16, 0, 0);
+    if constexpr (!TOKEN) {
+      const uint16_t* vc0 = vbase + c * (128 * 64) + v0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        __builtin_amdgcn_global_load_lds(vc0 + 512 * j, (lds_void_t*)(slot + (16 + j) * 1024), 16,
+                                         0, 0);
+    }
+  };
+  // Publishes chunk n; `newer` = this wave issued another chunk after n, whose
+  // kChunkDma instructions may stay in flight.
+  auto publish = [&](int n, bool newer) {
+    if (!TOKEN && newer)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kChunkDma) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane == 0) lds_store_flag(lds_addr(&slot_ready[n % R]), n + 1);
+  };
+  auto wait_landed = [&](int n) {
+    for (int spins = 0; spins < kSpinLimit; ++spins) {
+      const int v = __builtin_amdgcn_readfirstlane(lds_load_flag(lds_addr(&slot_ready[n % R])));
+      if (v > n) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("" ::: "memory");
+  };
+  // Queries of this wave as owner bits.
+  uint64_t my_bits = 0;
+#pragma unroll
+  for (int nt = 0; nt < kNtile; ++nt) my_bits |= 3ull << (2 * qpair(nt));
+
+  // Chunks this wave issued and has not published: p0 (older), p1; -1 = none.
+  int p0 = -1, p1 = -1, p0_at = 0, p1_at = 0;
+  if (wave < R && wave < nsteps) {
+    issue_chunk(wave);
+    p0 = wave;  // published at step 0
+  }
+  for (int st = 0; st < nsteps; ++st) {
+    if (p0 >= 0 && st >= p0_at) {
+      publish(p0, p1 >= 0);
+      p0 = p1;
+      p0_at = p1_at;
+      p1 = -1;
+    }
+    const uint64_t om = uniform_u64(s_own[st]);
+    if (om & my_bits) {
+      wait_landed(st);
+      consume(st);
+    }
+    // Count this wave done with step st (its reads of the slot have
+    // completed: LDS instructions of a wave execute in order).  The count is
+    // per step, not per slot: a wave with no work runs ahead and may count
+    // itself done with chunk st + R before a slower wave is done with st.
+    asm volatile("" ::: "memory");
+    int old = 0;
+    if (lane == 0) old = lds_fetch_inc(lds_addr(&s_done[st]));
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old == kWaves - 1 && st + R < nsteps) {
+      issue_chunk(st + R);
+      if (p0 < 0) {
+        p0 = st + R;
+        p0_at = st + 2;
+      } else {
+        p1 = st + R;
+        p1_at = st + 2;
+      }
+    }
+  }
+  if (p0 >= 0) publish(p0, p1 >= 0);
+  if (p1 >= 0) publish(p1, false);
+#else
   // 6. The walk: groups of CPS chunks, one barrier per group.
   const int lead = min(kAhead, nsteps);
   for (int c = 0; c < lead; ++c) issue(c);
@@ -644,10 +771,12 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
       if (first + x < nsteps) consume(first + x);
   }
 
+#endif
+
   if constexpr (!TOKEN) {
 #pragma unroll
     for (int nt = 0; nt < kNtile; ++nt) {
-      const int ql = wave * kQPW + 2 * nt + half;
+      const int ql = 2 * qpair(nt) + half;
       if (ql >= nq || gg >= G) continue;
       uint16_t* orow = a.out + ((b * a.Lq + q0 + ql) * a.Hq + h * G + gg) * 128;
 #pragma unroll
