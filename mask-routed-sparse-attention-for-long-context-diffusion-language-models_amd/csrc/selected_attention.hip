@@ -170,6 +170,25 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
+// v_max3 / v_max without the input canonicalisation fmaxf implies; the
+// inputs are products or -inf, never NaN.
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float d;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+__device__ __forceinline__ float max_raw(float a, float b) {
+  float d;
+  asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+// x = -inf in the lanes set in `lanes`, in place (no register copies at the
+// join of the masking branches).
+__device__ __forceinline__ float set_ninf_where(float x, uint64_t lanes, float ninf_v) {
+  asm volatile("v_cndmask_b32_e64 %0, %0, %1, %2" : "+v"(x) : "v"(ninf_v), "s"(lanes));
+  return x;
+}
+
 // Walk counters in LDS, accessed with asm so the compiler does not order
 // them behind the in-flight global->LDS DMA (it waits for vmcnt(0) before
 // any LDS atomic that may alias a DMA destination).
@@ -456,7 +475,9 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   int32_t* p_len = reinterpret_cast<int32_t*>(smem + lay.p_len);        // [TQ]
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  // The wave index is uniform: kept in a scalar register so that per-wave
+  // decisions (tile ownership, DMA duty) are scalar branches.
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
   const int64_t b = blockIdx.z;
   const int h = blockIdx.y;
@@ -535,6 +556,8 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
 
   const float c2 = a.scale_log2;
   const int half = col >> 3, gg = col & 7;
+  float ninf_v = neg_inf();
+  asm volatile("" : "+v"(ninf_v));  // kept in a register for set_ninf_where
 
   auto consume = [&](int st) {
     const uint64_t om = uniform_u64(s_own[st]);
@@ -555,11 +578,11 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
       rank[nt] += owns ? 1 : 0;
       int slot = 0;
       if constexpr (TOKEN) slot = comp_slot[ql * K + pos];
-      float wv = 0.f;
-      if constexpr (!TOKEN) {
-        const float wraw = bf16_to_f32(wr[(ql * K + pos) * 8 + gg]);
-        wv = owns ? wraw : 0.f;
-      }
+      // Routing weight of the lane's column, read with the K operands (LDS
+      // reads complete in order, so it has landed once the S^T product has).
+      uint32_t wbits = 0u;
+      if constexpr (!TOKEN)
+        asm volatile("ds_read_u16 %0, %1" : "=v"(wbits) : "v"(lds_addr(&wr[(ql * K + pos) * 8 + gg])));
       // Opaque zero: keeps the compiler from hoisting this tile's K / V operand
       // reads out of the tile loop (that would pin 128 extra registers).
       int zoff = 0;
@@ -570,6 +593,8 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
                                  lds_addr(Kt + kofs(2)), lds_addr(Kt + kofs(3))};
       f32x4_t S[4];
       qk_tile<kDepth>(kaddr, Qb[nt], S);
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(wbits));  // already satisfied
+      const float wv = owns ? bf16_to_f32(wbits) : 0.f;
       // The first V^T operands do not depend on P: read them now so they land
       // during the softmax.  PV operand o = 8 * jj + td.
       const uint32_t vaddr[2] = {lds_addr(Kt + vofs(0)), lds_addr(Kt + vofs(1))};
@@ -607,19 +632,22 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
         }
       } else {
         u32x4_t Pb[2];
-        if (msk == (1ull << 63)) {
-          if (grp == 3) S[3][3] = neg_inf();
-        } else if (msk != 0ull) {
+        // Excluded keys -> -inf, in place.  Key 63 (the landmark slot, the
+        // usual only exclusion) is S[3][3] of lane group 3 (lanes 48-63);
+        // any other excluded key takes the rare per-bit path.
+        S[3][3] = set_ninf_where(S[3][3], (msk >> 63) ? 0xFFFF000000000000ull : 0ull, ninf_v);
+        if (msk & ~(1ull << 63)) {
 #pragma unroll
           for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              if ((msh >> (16 * t + i)) & 1ull) S[t][i] = neg_inf();
+              S[t][i] = set_ninf_where(
+                  S[t][i], __builtin_amdgcn_ballot_w64((msh >> (16 * t + i)) & 1ull), ninf_v);
         }
-        float mx = fmaxf(fmaxf(S[0][0], S[0][1]), fmaxf(S[0][2], S[0][3]));
-#pragma unroll
-        for (int t = 1; t < 4; ++t)
-          mx = fmaxf(mx, fmaxf(fmaxf(S[t][0], S[t][1]), fmaxf(S[t][2], S[t][3])));
+        float mx = max3_raw(max3_raw(S[0][0], S[0][1], S[0][2]), max3_raw(S[0][3], S[1][0], S[1][1]),
+                            S[3][3]);
+        mx = max3_raw(mx, max3_raw(S[1][2], S[1][3], S[2][0]), max3_raw(S[2][1], S[2][2], S[2][3]));
+        mx = max3_raw(mx, S[3][0], max_raw(S[3][1], S[3][2]));
         mx = across4_max(mx);
         const float mb = mx == neg_inf() ? 0.f : mx * c2;
         float part[4];
