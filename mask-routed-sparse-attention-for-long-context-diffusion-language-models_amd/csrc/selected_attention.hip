@@ -10,14 +10,15 @@
 // first negative entry; entries >= kv_len / 64 are skipped.  A chunk listed
 // twice contributes twice (its weights are summed before use).
 //
-// Work split.  A workgroup owns a tile of 48 queries of one KV head; each of
-// its 8 waves owns 6 of those queries (3 column tiles of 2 queries x 8 head
+// Work split.  A workgroup owns a tile of queries (48 with the default split)
+// of one KV head; each of
+// its waves owns a few query pairs (column tiles of 2 queries x 8 head
 // columns), whose output accumulators stay in registers for the whole
 // kernel.  The workgroup walks the union of the tile's routed chunks in
 // ascending order.  Each chunk's K and V^T (32 KB) arrive in an R-slot LDS
-// ring by asynchronous global->LDS DMA issued R - CPS chunks ahead; one
-// workgroup barrier covers CPS consecutive chunks.  Every wave with a query
-// routed to a chunk consumes it:
+// ring by asynchronous global->LDS DMA; waves synchronise per walk step
+// through LDS counters, not workgroup barriers, so they drift apart by up to
+// R chunks.  Every wave with a query routed to a chunk consumes it:
 //   S^T = K_chunk (64 x 128) . Q^T (2 queries x 8 head columns)   16 MFMAs
 //   per-column softmax over the 64 keys, scaled by the routing weight
 //   O^T += V_chunk^T (128 x 64) . P^T                            16 MFMAs
@@ -43,23 +44,21 @@ using namespace mrsa;
 
 namespace {
 
-constexpr int kDmaWaves = 8;            // waves 0-3 fetch K, 4-7 fetch V^T
 constexpr int kSlotBytes = 32768;       // one chunk: K (16 KB) + V^T (16 KB)
 constexpr int kMaxTopk = 64;
 constexpr size_t kMaxLds = 160 * 1024;
-constexpr int kSyncSlots = 4;           // ring slots the walk counters cover (R <= 4)
 constexpr int kSpinLimit = 1 << 16;     // bound on every wait for a ring slot (~4M clocks)
-#ifndef MRSA_SEL_SYNC
-#define MRSA_SEL_SYNC 1                 // 1: per-slot counters, 0: workgroup barrier per CPS chunks
-#endif
-#ifndef MRSA_SEL_CPS4
-#define MRSA_SEL_CPS4 2                 // chunks per barrier with a 4-slot ring
-#endif
 #ifndef MRSA_SEL_INTERLEAVE
 #define MRSA_SEL_INTERLEAVE 1           // query pairs dealt round-robin over the waves
 #endif
+#ifndef MRSA_SEL_IDLE_HELP
+#define MRSA_SEL_IDLE_HELP 2            // steps ahead a wave with no work still helps fetch
+#endif
+#ifndef MRSA_SEL_DEPTH
+#define MRSA_SEL_DEPTH 0                // LDS operand reads in flight (0: by work split)
+#endif
 #ifndef MRSA_SEL_WAVES
-#define MRSA_SEL_WAVES 8                // work split: 8 (8 waves x 3 tiles), 82 (8 x 2), 12 (12 x 2)
+#define MRSA_SEL_WAVES 12               // work split: 12 (12 waves x 2 tiles), 8 (8 x 3), 82 (8 x 2), 16 (16 x 1)
 #endif
 
 // Work split: NW waves, each owning NT column tiles of 2 queries x 8 head
@@ -71,7 +70,7 @@ struct Split {
   static constexpr int kNtile = NT;
   static constexpr int kQPW = 2 * NT;
   static constexpr int kTQ = NW * 2 * NT;
-  static_assert(kTQ <= 64 && NW >= kDmaWaves, "work split");
+  static_assert(kTQ <= 64, "work split");
 };
 using Split8 = Split<8, 3>;
 using Split8x2 = Split<8, 2>;
@@ -101,7 +100,7 @@ struct SelArgs {
 // LDS carve-up (byte offsets, 16-aligned).  The p_* arrays are only used by
 // the prologue and live inside the ring, which is free until the first DMA.
 struct SelLayout {
-  size_t ring, wr, s_chunk, s_own, s_mask, s_done, comp_slot, misc, total;
+  size_t ring, wr, s_chunk, s_own, s_mask, s_done, s_claim, s_land, comp_slot, misc, total;
   size_t p_idx, p_kv, p_omask, p_len, p_w, p_end;
   int cap;
 };
@@ -119,8 +118,10 @@ __host__ __device__ inline SelLayout sel_layout(int TQ, int NW, int K, int64_t C
   l.s_own = o;     o = align16(o + (size_t)l.cap * 8);
   l.s_mask = o;    o = align16(o + (size_t)l.cap * 8);
   l.s_done = o;    o = align16(o + (size_t)l.cap * 4);
+  l.s_claim = o;   o = align16(o + (size_t)l.cap * 4);
+  l.s_land = o;    o = align16(o + (size_t)l.cap * 4);
   l.comp_slot = o; o = align16(o + n);
-  l.misc = o;      o = align16(o + (size_t)(NW + 4 + kSyncSlots) * 4);
+  l.misc = o;      o = align16(o + (size_t)(NW + 8) * 4);
   l.total = o;
   o = l.ring;
   l.p_idx = o;     o = align16(o + n * 4);
@@ -133,21 +134,6 @@ __host__ __device__ inline SelLayout sel_layout(int TQ, int NW, int K, int64_t C
 }
 __host__ __device__ inline bool sel_layout_fits(const SelLayout& l, int R) {
   return l.total <= kMaxLds && l.p_end <= l.ring + (size_t)R * kSlotBytes;
-}
-
-// Waits until at most n chunk DMAs of this wave (4 instructions each) are in
-// flight and its LDS accesses are done, then synchronises the workgroup.
-// __syncthreads() would wait for every outstanding load (vmcnt(0)), including
-// the chunks being prefetched.
-__device__ __forceinline__ void ring_barrier(int n) {
-  if (n >= 2)
-    asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
-  else if (n == 1)
-    asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
 }
 
 // Matrix-operand reads from LDS with explicit waits.  With global->LDS DMA in
@@ -200,14 +186,48 @@ __device__ __forceinline__ int lds_load_flag(uint32_t addr) {
 __device__ __forceinline__ void lds_store_flag(uint32_t addr, int v) {
   asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(v) : "memory");
 }
-__device__ __forceinline__ int lds_fetch_inc(uint32_t addr) {
+__device__ __forceinline__ int lds_fetch_add(uint32_t addr, int v) {
   int old;
-  const int one = 1;
   asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
                : "=v"(old)
-               : "v"(addr), "v"(one)
+               : "v"(addr), "v"(v)
                : "memory");
   return old;
+}
+__device__ __forceinline__ void lds_add(uint32_t addr, int v) {
+  asm volatile("ds_add_u32 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+
+// One LDS round trip per walk step (lane 0 only): count the wave done with
+// a step (returns the previous count) and read the owner bits, excluded-key
+// bits and ring-slot tag of the next step.
+__device__ __forceinline__ void step_exchange(uint32_t done_addr, uint32_t own_addr,
+                                              uint32_t mask_addr, uint32_t tag_addr,
+                                              uint32_t cur_addr, int& old, uint64_t& own,
+                                              uint64_t& mask, int& tag, int& cur) {
+  const int one = 1;
+  asm volatile(
+      "ds_add_rtn_u32 %0, %5, %10\n\t"
+      "ds_read_b64 %1, %6\n\t"
+      "ds_read_b64 %2, %7\n\t"
+      "ds_read_b32 %3, %8\n\t"
+      "ds_read_b32 %4, %9\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(old), "=&v"(own), "=&v"(mask), "=&v"(tag), "=&v"(cur)
+      : "v"(done_addr), "v"(own_addr), "v"(mask_addr), "v"(tag_addr), "v"(cur_addr), "v"(one)
+      : "memory");
+}
+__device__ __forceinline__ void step_read(uint32_t own_addr, uint32_t mask_addr,
+                                          uint32_t tag_addr, uint64_t& own, uint64_t& mask,
+                                          int& tag) {
+  asm volatile(
+      "ds_read_b64 %0, %3\n\t"
+      "ds_read_b64 %1, %4\n\t"
+      "ds_read_b32 %2, %5\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(own), "=&v"(mask), "=&v"(tag)
+      : "v"(own_addr), "v"(mask_addr), "v"(tag_addr)
+      : "memory");
 }
 
 __device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
@@ -444,15 +464,13 @@ __device__ int build_walk(const SelArgs& a, const WalkLds& W, int64_t b, int h, 
   return misc[kWaves];
 }
 
-template <bool TOKEN, int R, int CPS, class SP>
+template <bool TOKEN, int R, class SP>
 __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) {
   constexpr int kWaves = SP::kWaves, kThreads = SP::kThreads, kNtile = SP::kNtile;
   constexpr int kTQ = SP::kTQ;
-  constexpr int kDepth = kWaves > 8 ? 4 : 8;  // LDS operand reads in flight
-  // Every chunk of a group must have been issued before the group's barrier
-  // (R - CPS >= CPS), and at most 3 chunks are ever in flight past it.
-  static_assert(R - CPS >= CPS && R - CPS <= 3, "ring depth");
-  constexpr int kAhead = R - CPS;  // chunks issued ahead of the group being consumed
+  // LDS operand reads in flight: 8 when registers allow, 4 for 12 waves.
+  constexpr int kDepth = MRSA_SEL_DEPTH > 0 ? MRSA_SEL_DEPTH : (kWaves > 8 ? 4 : 8);
+  static_assert(R >= 2, "ring depth");
   extern __shared__ __align__(16) unsigned char smem[];
   const int K = a.K;
   const int64_t Ck = a.Ck;
@@ -465,10 +483,12 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   uint64_t* s_mask = reinterpret_cast<uint64_t*>(smem + lay.s_mask);    // [cap] masked keys
   uint8_t* comp_slot = smem + lay.comp_slot;                            // [TQ][K]
   int32_t* misc = reinterpret_cast<int32_t*>(smem + lay.misc);          // [kWaves] scan, [kWaves] n
-  // Walk counters: waves done with each walk step, and per ring slot
-  // 1 + the index of the chunk whose data has landed in it.
+  // Walk counters per step: waves done with it, DMA portions of its chunk
+  // claimed and landed.
   int32_t* s_done = reinterpret_cast<int32_t*>(smem + lay.s_done);       // [cap]
-  int32_t* slot_ready = misc + kWaves + 4;                               // [kSyncSlots]
+  int32_t* s_claim = reinterpret_cast<int32_t*>(smem + lay.s_claim);     // [cap]
+  int32_t* s_land = reinterpret_cast<int32_t*>(smem + lay.s_land);       // [cap]
+  int32_t* cursor = misc + kWaves + 4;  // oldest chunk with unclaimed portions
   int32_t* p_idx = reinterpret_cast<int32_t*>(smem + lay.p_idx);        // [TQ][K]
   uint8_t* p_kv = smem + lay.p_kv;                                      // [Ck][8] key-valid bytes
   uint64_t* p_omask = reinterpret_cast<uint64_t*>(smem + lay.p_omask);  // [Ck]
@@ -486,8 +506,8 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   const int64_t nq = min((int64_t)kTQ, a.Lq - q0);  // queries of this tile that exist
 
   // Zeroed counters, published by the prologue's barriers.
-  if (tid < kSyncSlots) slot_ready[tid] = 0;
-  for (int i = tid; i < lay.cap; i += kThreads) s_done[i] = 0;
+  if (tid == 0) *cursor = 0;
+  for (int i = tid; i < lay.cap; i += kThreads) s_done[i] = s_claim[i] = s_land[i] = 0;
   const int nsteps = build_walk<TOKEN, SP>(
       a, WalkLds{wr, wts, s_chunk, s_own, s_mask, comp_slot, misc, p_idx, p_kv, p_omask, p_len}, b, h,
       q0, nq);
@@ -518,33 +538,11 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
     for (int td = 0; td < 8; ++td) acc[nt][td] = zero4();
   }
 
-  // 5. DMA of one chunk into a ring slot: wave w issues instructions for units
-  //    (4w + i) * 64 + lane; waves 0-3 fetch K rows, waves 4-7 fetch V^T rows.
+  // 5. Chunk sources: K rows of this KV head, V^T tiles.
   const uint16_t* kbase = a.k + (b * a.Lk) * (int64_t)a.Hkv * 128 + (int64_t)h * 128;
   const uint16_t* vbase =
       TOKEN ? nullptr : a.vt + ((b * a.Hkv + h) * a.NTk) * (int64_t)(128 * 64);
   const int kstride = a.Hkv * 128;
-  // Wave w < 4 issues K units (4w + i) * 64 + lane: row 16w + 4i + grp, part
-  // col ^ (4i + grp); wave w in 4..7 issues V^T units: row 32(w - 4) + 8i +
-  // lane / 8, part (lane ^ (lane / 8)) & 7.  Element offsets within a chunk:
-  //   K: (16w + 4i + grp) * kstride + ((col ^ grp) ^ 4i) * 8
-  //   V: (32(w - 4) + 8i + lane / 8) * 64 + ((lane ^ (lane >> 3)) & 7) * 8
-  const int wd = min(wave, kDmaWaves - 1);
-  const uint32_t dma0 =
-      wd < 4 ? (uint32_t)((16 * wd + grp) * kstride + ((col ^ grp) * 8))
-             : (uint32_t)((32 * (wd - 4) + (lane >> 3)) * 64 + ((lane ^ (lane >> 3)) & 7) * 8);
-  const uint32_t dma_step = wd < 4 ? (uint32_t)(4 * kstride) : 512u;
-  const uint32_t dma_flip = wd < 4 ? 32u : 0u;
-  auto issue = [&](int st) {
-    if (wave >= (TOKEN ? 4 : kDmaWaves)) return;
-    const int64_t c = __builtin_amdgcn_readfirstlane(s_chunk[st]);
-    unsigned char* slot = ring + (st % R) * kSlotBytes + wave * 4096;
-    const uint16_t* base = wave < 4 ? kbase + c * 64 * (int64_t)kstride : vbase + c * (128 * 64);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds(base + ((dma0 ^ (i * dma_flip)) + i * dma_step),
-                                       (lds_void_t*)(slot + i * 1024), 16, 0, 0);
-  };
 
   // Per-lane element offsets of the matrix-operand reads inside a slot:
   // K row 16t + col, part (4j + grp) ^ col  -> kofs0 ^ 32j + 2048t;
@@ -559,9 +557,7 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   float ninf_v = neg_inf();
   asm volatile("" : "+v"(ninf_v));  // kept in a register for set_ninf_where
 
-  auto consume = [&](int st) {
-    const uint64_t om = uniform_u64(s_own[st]);
-    const uint64_t msk = uniform_u64(s_mask[st]);
+  auto consume = [&](int st, uint64_t om, uint64_t msk) {
     const uint16_t* Kb = reinterpret_cast<const uint16_t*>(ring + (st % R) * kSlotBytes);
     // This lane's excluded-key bits: bit 16t + i of msh is key 16t + 4grp + i.
     const uint64_t msh = msk >> (4 * grp);
@@ -684,122 +680,114 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
     }
   };
 
-#if MRSA_SEL_SYNC
-  // 6. The walk, synchronised per ring slot instead of per workgroup, so that
-  //    waves drift apart by up to R chunks and the imbalance of their work
-  //    evens out over that window:
-  //    * the wave that frees slot st % R last (the last wave to count itself
-  //      done with step st) issues the whole DMA of chunk st + R into it;
-  //    * that wave publishes the chunk as landed at the start of its step
-  //      st + 2 (after waiting for its own DMA with vmcnt), so the wait
-  //      rarely blocks it;
-  //    * a wave with no query routed to chunk st neither waits for it nor
-  //      reads it.
-  //    Chunk n >= R is issued once every wave finished step n - R and
-  //    published at its issuer's step n - R + 2 <= n - 1, so every wait
-  //    depends only on earlier chunks and the walk cannot deadlock; the
-  //    spin bound keeps every wave finite regardless.
-  constexpr int kChunkDma = TOKEN ? 16 : 32;  // 1 KB DMA instructions per chunk
+  // 6. The walk, synchronised through per-step LDS counters instead of
+  //    workgroup barriers, so that waves drift apart by up to R chunks and
+  //    the imbalance of their work evens out over that window.
+  //    * Chunk n lives in ring slot n % R; it may be fetched once every wave
+  //      has counted itself done with step n - R (s_done).
+  //    * Its DMA is split into kPortions portions of 4 KB.  Waves that would
+  //      otherwise idle (waiting for a chunk to land, or with no query routed
+  //      to the current step) claim the oldest fetchable portions (s_claim,
+  //      chunk order kept by `cursor`), issue them, wait for their own DMA
+  //      (vmcnt) and count them landed (s_land).  The slowest wave, which
+  //      frees each slot, thus rarely spends time issuing fetches.
+  //    * A wave consumes chunk st once all its portions have landed; a wave
+  //      with no query routed to it neither waits for it nor reads it.
+  //    Liveness: the first wave to reach step n helps until chunk n is
+  //    claimed, and chunk n becomes fetchable once every wave finished step
+  //    n - R, which depends only on earlier chunks.  The spin bound keeps
+  //    every wave finite regardless.
+  constexpr int kPortions = TOKEN ? 4 : 8;
   const uint32_t kc = (uint32_t)((col ^ grp) * 8);
   const uint32_t v0 = (uint32_t)((lane >> 3) * 64 + ((lane ^ (lane >> 3)) & 7) * 8);
-  // DMA instruction j < 16 fetches K units 64j + lane: row 4j + grp, part
-  // (col ^ grp) ^ 4(j & 3); instruction 16 + j' fetches V^T units: row
-  // 8j' + lane / 8, part (lane ^ (lane / 8)) & 7.
-  auto issue_chunk = [&](int n) {
+  // Portion p < 4: K DMA instructions j = 4p + i (units 64j + lane: row
+  // 4j + grp, part (col ^ grp) ^ 4i); portion 4 + p: V^T instructions
+  // j = 4p + i (units 1024 + 64j + lane: row 8j + lane / 8, part
+  // (lane ^ (lane / 8)) & 7).
+  auto issue_portion = [&](int n, int p) {
     const int64_t c = __builtin_amdgcn_readfirstlane(s_chunk[n]);
     unsigned char* slot = ring + (n % R) * kSlotBytes;
-    const uint16_t* kc0 = kbase + c * 64 * (int64_t)kstride + grp * kstride;
+    if (TOKEN || p < 4) {
+      const uint16_t* kc0 = kbase + c * 64 * (int64_t)kstride + grp * kstride;
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
-      __builtin_amdgcn_global_load_lds(kc0 + (4 * j) * kstride + (kc ^ (uint32_t)(32 * (j & 3))),
-                                       (lds_void_t*)(slot + j * 1024), 16, 0, 0);
-    if constexpr (!TOKEN) {
+      for (int i = 0; i < 4; ++i) {
+        const int j = 4 * p + i;
+        __builtin_amdgcn_global_load_lds(kc0 + (4 * j) * kstride + (kc ^ (uint32_t)(32 * i)),
+                                         (lds_void_t*)(slot + j * 1024), 16, 0, 0);
+      }
+    } else {
       const uint16_t* vc0 = vbase + c * (128 * 64) + v0;
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
-        __builtin_amdgcn_global_load_lds(vc0 + 512 * j, (lds_void_t*)(slot + (16 + j) * 1024), 16,
-                                         0, 0);
+      for (int i = 0; i < 4; ++i) {
+        const int j = 4 * (p - 4) + i;
+        __builtin_amdgcn_global_load_lds(vc0 + 512 * j, (lds_void_t*)(slot + (16 + j) * 1024),
+                                         16, 0, 0);
+      }
     }
   };
-  // Publishes chunk n; `newer` = this wave issued another chunk after n, whose
-  // kChunkDma instructions may stay in flight.
-  auto publish = [&](int n, bool newer) {
-    if (!TOKEN && newer)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kChunkDma) : "memory");
-    else
+  // Claims and fetches fetchable portions of chunks below `limit`, oldest
+  // first, until none is left.
+  auto help = [&](int limit) {
+    limit = min(limit, nsteps);
+    for (int guard = 0; guard < R * kPortions + 2; ++guard) {
+      const int n = __builtin_amdgcn_readfirstlane(lds_load_flag(lds_addr(cursor)));
+      if (n >= limit) return;
+      if (n >= R &&
+          __builtin_amdgcn_readfirstlane(lds_load_flag(lds_addr(&s_done[n - R]))) < kWaves)
+        return;
+      int k = 0;
+      if (lane == 0) k = lds_fetch_add(lds_addr(&s_claim[n]), 1);
+      k = __builtin_amdgcn_readfirstlane(k);
+      if (k >= kPortions) continue;  // chunk taken meanwhile; the cursor moves on
+      if (k == kPortions - 1 && lane == 0) lds_store_flag(lds_addr(cursor), n + 1);
+      issue_portion(n, k);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (lane == 0) lds_store_flag(lds_addr(&slot_ready[n % R]), n + 1);
-  };
-  auto wait_landed = [&](int n) {
-    for (int spins = 0; spins < kSpinLimit; ++spins) {
-      const int v = __builtin_amdgcn_readfirstlane(lds_load_flag(lds_addr(&slot_ready[n % R])));
-      if (v > n) break;
-      __builtin_amdgcn_s_sleep(1);
+      if (lane == 0) lds_add(lds_addr(&s_land[n]), 1);
     }
-    asm volatile("" ::: "memory");
   };
   // Queries of this wave as owner bits.
   uint64_t my_bits = 0;
 #pragma unroll
   for (int nt = 0; nt < kNtile; ++nt) my_bits |= 3ull << (2 * qpair(nt));
 
-  // Chunks this wave issued and has not published: p0 (older), p1; -1 = none.
-  int p0 = -1, p1 = -1, p0_at = 0, p1_at = 0;
-  if (wave < R && wave < nsteps) {
-    issue_chunk(wave);
-    p0 = wave;  // published at step 0
-  }
+  // Words of the current step: owner bits, excluded-key bits, landed portions.
+  uint64_t om = 0, msk = 0;
+  int land = 0, old = 0, cur = 0;
+  if (nsteps > 0 && lane == 0)
+    step_read(lds_addr(&s_own[0]), lds_addr(&s_mask[0]), lds_addr(&s_land[0]), om, msk, land);
   for (int st = 0; st < nsteps; ++st) {
-    if (p0 >= 0 && st >= p0_at) {
-      publish(p0, p1 >= 0);
-      p0 = p1;
-      p0_at = p1_at;
-      p1 = -1;
-    }
-    const uint64_t om = uniform_u64(s_own[st]);
-    if (om & my_bits) {
-      wait_landed(st);
-      consume(st);
-    }
-    // Count this wave done with step st (its reads of the slot have
-    // completed: LDS instructions of a wave execute in order).  The count is
-    // per step, not per slot: a wave with no work runs ahead and may count
-    // itself done with chunk st + R before a slower wave is done with st.
-    asm volatile("" ::: "memory");
-    int old = 0;
-    if (lane == 0) old = lds_fetch_inc(lds_addr(&s_done[st]));
-    old = __builtin_amdgcn_readfirstlane(old);
-    if (old == kWaves - 1 && st + R < nsteps) {
-      issue_chunk(st + R);
-      if (p0 < 0) {
-        p0 = st + R;
-        p0_at = st + 2;
-      } else {
-        p1 = st + R;
-        p1_at = st + 2;
+    om = uniform_u64(om);
+    msk = uniform_u64(msk);
+    const bool mine = (om & my_bits) != 0;
+    // A wave with no work here helps only when the oldest unclaimed chunk
+    // (cursor, read with the step words) is needed within a few steps.
+    const bool helpful = __builtin_amdgcn_readfirstlane(cur) < st + MRSA_SEL_IDLE_HELP;
+    if (mine ? __builtin_amdgcn_readfirstlane(land) < kPortions : helpful) {
+      // Idle: fetch what can be fetched; with work at this step, also wait
+      // until its chunk has landed.
+      for (int spins = 0; spins < kSpinLimit; ++spins) {
+        help(st + R);
+        if (!mine ||
+            __builtin_amdgcn_readfirstlane(lds_load_flag(lds_addr(&s_land[st]))) >= kPortions)
+          break;
+        __builtin_amdgcn_s_sleep(1);
       }
+      asm volatile("" ::: "memory");
     }
+    if (mine) consume(st, om, msk);
+    // Count this wave done with step st (its reads of the slot have
+    // completed: LDS instructions of a wave execute in order) and read the
+    // next step's words in the same round trip.  The count is per step: a
+    // wave with no work runs ahead and may count itself done with chunk
+    // st + R before a slower wave is done with st.  A landed count read
+    // here stays valid: the slot is not refetched before this wave is done
+    // with the step.
+    asm volatile("" ::: "memory");
+    const int nx = min(st + 1, nsteps - 1);
+    if (lane == 0)
+      step_exchange(lds_addr(&s_done[st]), lds_addr(&s_own[nx]), lds_addr(&s_mask[nx]),
+                    lds_addr(&s_land[nx]), lds_addr(cursor), old, om, msk, land, cur);
   }
-  if (p0 >= 0) publish(p0, p1 >= 0);
-  if (p1 >= 0) publish(p1, false);
-#else
-  // 6. The walk: groups of CPS chunks, one barrier per group.
-  const int lead = min(kAhead, nsteps);
-  for (int c = 0; c < lead; ++c) issue(c);
-  for (int first = 0; first < nsteps; first += CPS) {
-    // Chunks issued so far: min(nsteps, first + kAhead); this group needs
-    // every one up to first + CPS - 1.
-    const int in_flight = max(0, min(nsteps, first + kAhead) - (first + CPS));
-    ring_barrier(TOKEN ? 0 : in_flight);
-#pragma unroll
-    for (int x = 0; x < CPS; ++x)
-      if (first + kAhead + x < nsteps) issue(first + kAhead + x);
-#pragma unroll
-    for (int x = 0; x < CPS; ++x)
-      if (first + x < nsteps) consume(first + x);
-  }
-
-#endif
 
   if constexpr (!TOKEN) {
 #pragma unroll
@@ -826,9 +814,9 @@ __global__ void __launch_bounds__(256) fill_neg_inf(float* p, int64_t n) {
     p[e] = neg_inf();
 }
 
-template <bool TOKEN, int R, int CPS, class SP>
+template <bool TOKEN, int R, class SP>
 int launch_variant(SelArgs& a, const SelLayout& lay, hipStream_t s) {
-  auto kern = selected_attn_kernel<TOKEN, R, CPS, SP>;
+  auto kern = selected_attn_kernel<TOKEN, R, SP>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lay.total) != hipSuccess)
     return MRSA_ERR_LAUNCH;
@@ -840,12 +828,14 @@ int launch_variant(SelArgs& a, const SelLayout& lay, hipStream_t s) {
 // Deepest ring that fits in LDS: 4 slots, else 3.
 template <bool TOKEN>
 int launch_selected(SelArgs& a, hipStream_t s) {
-  using SP = std::conditional_t<MRSA_SEL_WAVES == 12, Split12,
-                                std::conditional_t<MRSA_SEL_WAVES == 82, Split8x2, Split8>>;
+  using SP = std::conditional_t<
+      MRSA_SEL_WAVES == 16, Split<16, 1>,
+      std::conditional_t<MRSA_SEL_WAVES == 12, Split12,
+                         std::conditional_t<MRSA_SEL_WAVES == 82, Split8x2, Split8>>>;
   const SelLayout l4 = sel_layout(SP::kTQ, SP::kWaves, a.K, a.Ck, 4, TOKEN);
-  if (sel_layout_fits(l4, 4)) return launch_variant<TOKEN, 4, MRSA_SEL_CPS4, SP>(a, l4, s);
+  if (sel_layout_fits(l4, 4)) return launch_variant<TOKEN, 4, SP>(a, l4, s);
   const SelLayout l3 = sel_layout(SP::kTQ, SP::kWaves, a.K, a.Ck, 3, TOKEN);
-  if (sel_layout_fits(l3, 3)) return launch_variant<TOKEN, 3, 1, SP>(a, l3, s);
+  if (sel_layout_fits(l3, 3)) return launch_variant<TOKEN, 3, SP>(a, l3, s);
   return MRSA_ERR_UNSUPPORTED;
 }
 
