@@ -58,7 +58,7 @@ __global__ void __launch_bounds__(64 * G) local_attn_kernel(LocalArgs a) {
   __shared__ int64_t pos_lo, pos_hi;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, g = tid >> 6;
+  const int lane = tid & 63, g = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
   const int64_t b = blockIdx.z;
   const int h = blockIdx.y;
@@ -247,11 +247,7 @@ __global__ void __launch_bounds__(64 * G) local_attn_kernel(LocalArgs a) {
             if (((ibits >> s) & 1ull) && S[nt][t][i] != neg_inf()) S[nt][t][i] = 0.f;
           }
       }
-      float mx = fmaxf(fmaxf(S[nt][0][0], S[nt][0][1]), fmaxf(S[nt][0][2], S[nt][0][3]));
-#pragma unroll
-      for (int t = 1; t < 4; ++t)
-        mx = fmaxf(mx, fmaxf(fmaxf(S[nt][t][0], S[nt][t][1]), fmaxf(S[nt][t][2], S[nt][t][3])));
-      mx = across4_max(mx);
+      const float mx = across4_max(max16_raw(S[nt]));
       const float m_new = fmaxf(m_run[nt], mx * c);
       // A column with no visible key yet keeps m = -inf; exponentiate against 0
       // there so that every term (and alpha) is exp2(-inf) = 0.

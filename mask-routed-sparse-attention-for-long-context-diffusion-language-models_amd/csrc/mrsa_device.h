@@ -149,6 +149,32 @@ __device__ __forceinline__ int wave_min_i(int v) {
   return v;
 }
 
+// v_max3 / v_max without the input canonicalisation fmaxf implies; for
+// inputs that are never NaN (matrix-core products, -inf masks).
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float d;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+__device__ __forceinline__ float max_raw(float a, float b) {
+  float d;
+  asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+// Max of the 16 accumulator values a lane holds for one 64-row tile.
+__device__ __forceinline__ float max16_raw(const f32x4_t (&S)[4]) {
+  float m = max3_raw(max3_raw(S[0][0], S[0][1], S[0][2]), max3_raw(S[0][3], S[1][0], S[1][1]),
+                     S[3][3]);
+  m = max3_raw(m, max3_raw(S[1][2], S[1][3], S[2][0]), max3_raw(S[2][1], S[2][2], S[2][3]));
+  return max3_raw(m, S[3][0], max_raw(S[3][1], S[3][2]));
+}
+// x = v in the lanes set in `lanes`, in place (no register copies at the join
+// of branches that patch a few accumulator values).
+__device__ __forceinline__ float set_where(float x, uint64_t lanes, float v) {
+  asm("v_cndmask_b32_e64 %0, %0, %1, %2" : "+v"(x) : "v"(v), "s"(lanes));
+  return x;
+}
+
 // Order-preserving map from fp32 to uint32 (larger float -> larger key).
 __device__ __forceinline__ uint32_t float_order_key(float f) {
   uint32_t u = __float_as_uint(f);

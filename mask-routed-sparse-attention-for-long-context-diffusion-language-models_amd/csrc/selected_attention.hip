@@ -156,25 +156,6 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-// v_max3 / v_max without the input canonicalisation fmaxf implies; the
-// inputs are products or -inf, never NaN.
-__device__ __forceinline__ float max3_raw(float a, float b, float c) {
-  float d;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-  return d;
-}
-__device__ __forceinline__ float max_raw(float a, float b) {
-  float d;
-  asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
-  return d;
-}
-// x = -inf in the lanes set in `lanes`, in place (no register copies at the
-// join of the masking branches).
-__device__ __forceinline__ float set_ninf_where(float x, uint64_t lanes, float ninf_v) {
-  asm volatile("v_cndmask_b32_e64 %0, %0, %1, %2" : "+v"(x) : "v"(ninf_v), "s"(lanes));
-  return x;
-}
-
 // Walk counters in LDS, accessed with asm so the compiler does not order
 // them behind the in-flight global->LDS DMA (it waits for vmcnt(0) before
 // any LDS atomic that may alias a DMA destination).
@@ -555,7 +536,7 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   const float c2 = a.scale_log2;
   const int half = col >> 3, gg = col & 7;
   float ninf_v = neg_inf();
-  asm volatile("" : "+v"(ninf_v));  // kept in a register for set_ninf_where
+  asm volatile("" : "+v"(ninf_v));  // kept in a register for set_where
 
   auto consume = [&](int st, uint64_t om, uint64_t msk) {
     const uint16_t* Kb = reinterpret_cast<const uint16_t*>(ring + (st % R) * kSlotBytes);
@@ -631,20 +612,16 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
         // Excluded keys -> -inf, in place.  Key 63 (the landmark slot, the
         // usual only exclusion) is S[3][3] of lane group 3 (lanes 48-63);
         // any other excluded key takes the rare per-bit path.
-        S[3][3] = set_ninf_where(S[3][3], (msk >> 63) ? 0xFFFF000000000000ull : 0ull, ninf_v);
+        S[3][3] = set_where(S[3][3], (msk >> 63) ? 0xFFFF000000000000ull : 0ull, ninf_v);
         if (msk & ~(1ull << 63)) {
 #pragma unroll
           for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              S[t][i] = set_ninf_where(
+              S[t][i] = set_where(
                   S[t][i], __builtin_amdgcn_ballot_w64((msh >> (16 * t + i)) & 1ull), ninf_v);
         }
-        float mx = max3_raw(max3_raw(S[0][0], S[0][1], S[0][2]), max3_raw(S[0][3], S[1][0], S[1][1]),
-                            S[3][3]);
-        mx = max3_raw(mx, max3_raw(S[1][2], S[1][3], S[2][0]), max3_raw(S[2][1], S[2][2], S[2][3]));
-        mx = max3_raw(mx, S[3][0], max_raw(S[3][1], S[3][2]));
-        mx = across4_max(mx);
+        const float mx = across4_max(max16_raw(S));
         const float mb = mx == neg_inf() ? 0.f : mx * c2;
         float part[4];
 #pragma unroll
