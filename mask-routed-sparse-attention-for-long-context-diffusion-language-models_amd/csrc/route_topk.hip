@@ -94,7 +94,8 @@ struct FastLayout {
   static constexpr size_t cbad = bias + 2 * 256 * 4;    // [256] u8
   static constexpr size_t red_max = cbad + 256;         // [2][64] f32
   static constexpr size_t red_sum = red_max + 2 * 64 * 4;
-  static constexpr size_t slot = red_sum + 2 * 64 * 4;  // [64][256] i8
+  static constexpr size_t lse = red_sum + 2 * 64 * 4;  // [2][64] f32 local LSE rows
+  static constexpr size_t slot = lse + 2 * 64 * 4;      // [64][256] i8
   static constexpr size_t ntot = slot + 64 * 256;        // [64] i32 picks per row
   static constexpr size_t sc = ntot + 64 * 4;            // [64][K] bf16, one head's picks
   static size_t total(int K) { return sc + (size_t)64 * K * 2; }
@@ -258,6 +259,7 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
   unsigned char* cbad = smem + FastLayout::cbad;
   float* red_max = reinterpret_cast<float*>(smem + FastLayout::red_max);
   float* red_sum = reinterpret_cast<float*>(smem + FastLayout::red_sum);
+  float* lse_s = reinterpret_cast<float*>(smem + FastLayout::lse);
   int8_t* slot_s = reinterpret_cast<int8_t*>(smem + FastLayout::slot);
   int* ntot_s = reinterpret_cast<int*>(smem + FastLayout::ntot);
   uint16_t* sc_s = reinterpret_cast<uint16_t*>(smem + FastLayout::sc);
@@ -304,8 +306,14 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
   // stored part lane & 15 (global part (lane & 15) ^ (row & 15)).  Rows >= C
   // re-read row C - 1; their logits are masked to -inf.  Wave 0 also moves
   // the bias row (4-byte units, rows >= C re-read row C - 1 and are unused).
-  auto stage = [&](int g, int i) {
+  auto stage = [&](int g, int i, bool with_lse) {
     uint16_t* dst = lmk_buf(i);
+    if (with_lse && lse_base && wave == 1) {
+      // Local LSE of the tile's 64 rows for head g (rows >= L re-read L - 1).
+      const int64_t r = min(q0 + lane, L - 1);
+      __builtin_amdgcn_global_load_lds(lse_base + (r * a.Hkv + h) * G + g,
+                                       (lds_void_t*)(lse_s + 64 * i), 4, 0, 0);
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int row = 4 * (8 * wave + j) + (lane >> 4);
@@ -362,11 +370,11 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
     __syncthreads();
     if (s + 1 < 2 * G) {
       if (load_next_q) load_q(head_of(s + 1), Anext);
-      stage(head_of(s + 1), (s + 1) & 1);
+      stage(head_of(s + 1), (s + 1) & 1, s + 1 < G);
     }
   };
   load_q(0, Acur);
-  stage(0, 0);
+  stage(0, 0, true);
 
   // Pass 1: biased logits, LSE over all chunks, running max over heads.
   for (int s = 0; s < G; ++s) {
@@ -375,18 +383,19 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
     f32x4_t S[kNT];
     logits(lmk_buf(s & 1), Acur, S);
     const float* bias_g = bias_s + 256 * (s & 1);
-    float rmax[4] = {neg_inf(), neg_inf(), neg_inf(), neg_inf()};
+    // x = s * scale + bias, -inf past C.
 #pragma unroll
     for (int t = 0; t < kNT; ++t) {
       const int c = cbase + 16 * t + col;
+      const float bv = c < C ? bias_g[c] : neg_inf();
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x = c < C ? S[t][i] * a.sm_scale : neg_inf();
-        const float xb = x + bias_g[c];
-        S[t][i] = xb;
-        rmax[i] = fmaxf(rmax[i], xb);
-      }
+      for (int i = 0; i < 4; ++i) S[t][i] = __builtin_fmaf(S[t][i], a.sm_scale, bv);
     }
+    float rmax[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      rmax[i] = max_raw(max3_raw(max3_raw(S[0][i], S[1][i], S[2][i]), S[3][i], S[4][i]),
+                        max3_raw(S[5][i], S[6][i], S[7][i]));
     // Row LSE over both chunk halves, in base 2 with the hardware exp2/log2:
     // each half reduces (max, sum of exp2) over its 128 chunks; one LDS
     // exchange combines them with a rescale.
@@ -419,16 +428,15 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
                             (mb == neg_inf() ? 0.f : red_sum[64 + row] * exp2_hw(mb - mm)));
       float tot = 0.f;
       if (!a.pre_softmax) {
-        // logaddexp(local_lse, lse) in base 2, back to natural units.
-        const float lv2 = r < L ? lse_base[((int)r * a.Hkv + h) * G + g] * kLog2e : 0.f;
+        // logaddexp(local_lse, lse) in base 2, back to natural units.  A -inf
+        // total (no visible logit at all) is clamped to -FLT_MAX: finite x - tot
+        // then ties at the top like x - (-inf) = +inf would, and -inf stays.
+        const float lv2 = r < L ? lse_s[64 * (s & 1) + row] * kLog2e : 0.f;
         const float hi = fmaxf(lv2, lse2), lo = fminf(lv2, lse2);
-        tot = hi == neg_inf() ? neg_inf() : (hi + log2_hw(1.f + exp2_hw(lo - hi))) * kLn2;
+        tot = hi == neg_inf() ? -__FLT_MAX__ : (hi + log2_hw(1.f + exp2_hw(lo - hi))) * kLn2;
       }
 #pragma unroll
-      for (int t = 0; t < kNT; ++t) {
-        const float xb = S[t][i];
-        M[t][i] = fmaxf(M[t][i], xb == neg_inf() ? xb : xb - tot);
-      }
+      for (int t = 0; t < kNT; ++t) M[t][i] = max_raw(M[t][i], S[t][i] - tot);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) Acur[j] = Anext[j];
