@@ -24,6 +24,7 @@
 //
 // General path (route_topk_generic_kernel): one workgroup per (token, KV head)
 // with scalar dot products; any head_dim / chunk count that fits LDS.
+#include <type_traits>
 #include <utility>
 
 #include "mrsa_device.h"
@@ -306,30 +307,33 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
   // stored part lane & 15 (global part (lane & 15) ^ (row & 15)).  Rows >= C
   // re-read row C - 1; their logits are masked to -inf.  Wave 0 also moves
   // the bias row (4-byte units, rows >= C re-read row C - 1 and are unused).
-  auto stage = [&](int g, int i, bool with_lse) {
+  // Instruction j (0..7) of the staging of head g into buffer i; j = 0
+  // also moves the local LSE rows (wave 1) and the bias row (wave 0).
+  auto stage_part = [&](int g, int i, int j, bool with_lse) {
     uint16_t* dst = lmk_buf(i);
-    if (with_lse && lse_base && wave == 1) {
+    if (j == 0 && with_lse && lse_base && wave == 1) {
       // Local LSE of the tile's 64 rows for head g (rows >= L re-read L - 1).
       const int64_t r = min(q0 + lane, L - 1);
       __builtin_amdgcn_global_load_lds(lse_base + (r * a.Hkv + h) * G + g,
                                        (lds_void_t*)(lse_s + 64 * i), 4, 0, 0);
     }
+    const int row = 4 * (8 * wave + j) + (lane >> 4);
+    const int part = (lane & 15) ^ (row & 15);
+    const int64_t c = min((int64_t)row, C - 1);
+    __builtin_amdgcn_global_load_lds(lmk_row(a, b, c, h, g) + part * 8,
+                                     (lds_void_t*)(dst + (8 * wave + j) * 512), 16, 0, 0);
+    if (j == 0 && a.bias && wave == 0) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int row = 4 * (8 * wave + j) + (lane >> 4);
-      const int part = (lane & 15) ^ (row & 15);
-      const int64_t c = min((int64_t)row, C - 1);
-      __builtin_amdgcn_global_load_lds(lmk_row(a, b, c, h, g) + part * 8,
-                                       (lds_void_t*)(dst + (8 * wave + j) * 512), 16, 0, 0);
-    }
-    if (a.bias && wave == 0) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t c = min((int64_t)(64 * j + lane), C - 1);
-        __builtin_amdgcn_global_load_lds(a.bias + ((b * C + c) * a.Hkv + h) * G + g,
-                                         (lds_void_t*)(bias_s + 256 * i + 64 * j), 4, 0, 0);
+      for (int jb = 0; jb < 4; ++jb) {
+        const int64_t cb = min((int64_t)(64 * jb + lane), C - 1);
+        __builtin_amdgcn_global_load_lds(a.bias + ((b * C + cb) * a.Hkv + h) * G + g,
+                                         (lds_void_t*)(bias_s + 256 * i + 64 * jb), 4, 0, 0);
       }
     }
+  };
+  auto stage = [&](int g, int i, bool with_lse) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) stage_part(g, i, j, with_lse);
   };
   auto load_q = [&](int g, u32x4_t (&A)[4]) {
     const uint16_t* qrow = qb_base + (uint32_t)((((int)qa * a.Hkv + h) * G + g) * 128 + 8 * grp);
@@ -341,7 +345,12 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
     }
   };
   // S[t] = q_g (16 queries of this wave) . lmk (16 chunks of tile t).
-  auto logits = [&](const uint16_t* lmk_s, const u32x4_t (&A)[4], f32x4_t (&S)[kNT]) {
+  // The next head's staging is issued one instruction per tile, between the
+  // products, so no wave stalls on a burst of DMA issue.
+  // S[t] = q (16 rows) . lmk (16 chunks of tile t); with TRANSPOSED the same
+  // operands give S^T: lane l holds query l % 16, chunks 16t + 4(l / 16) + i.
+  auto logits = [&](auto transposed, const uint16_t* lmk_s, const u32x4_t (&A)[4],
+                    f32x4_t (&S)[kNT], int next_g, int next_buf, bool with_lse) {
 #pragma unroll
     for (int t = 0; t < kNT; ++t) {
       f32x4_t acc = zero4();
@@ -349,9 +358,14 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const u32x4_t B = *reinterpret_cast<const u32x4_t*>(brow + (((4 * j + grp) ^ col) * 8));
-        acc = mfma_bf16_16x16x32(A[j], B, acc);
+        if constexpr (decltype(transposed)::value)
+          acc = mfma_bf16_16x16x32(B, A[j], acc);
+        else
+          acc = mfma_bf16_16x16x32(A[j], B, acc);
       }
       S[t] = acc;
+      if (next_g >= 0) stage_part(next_g, next_buf, t, with_lse);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
@@ -363,25 +377,49 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
 
   u32x4_t Acur[4], Anext[4];
   // Step prologue: head s landed (this wave's DMA and loads) and every wave
-  // is done with the other buffer; then queue step s + 1 -- its q operands
-  // first, then its DMA, so no wait inside the step drains the prefetch.
+  // is done with the other buffer; then queue step s + 1's q operands.  Its
+  // DMA follows inside the step's logits; nothing inside the step waits on
+  // vector memory, so the prefetch is never drained early.
   auto begin_step = [&](int s, bool load_next_q) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (s + 1 < 2 * G) {
-      if (load_next_q) load_q(head_of(s + 1), Anext);
-      stage(head_of(s + 1), (s + 1) & 1, s + 1 < G);
+    if (s + 1 < 2 * G && load_next_q) load_q(head_of(s + 1), Anext);
+  };
+  // Logits of step s, staging step s + 1's head meanwhile.
+  auto step_logits = [&](auto transposed, int s, f32x4_t (&S)[kNT]) {
+    const bool more = s + 1 < 2 * G;
+    logits(transposed, lmk_buf(s & 1), Acur, S, more ? head_of(s + 1) : -1, (s + 1) & 1,
+           s + 1 < G);
+  };
+  // Pass-1 q tiles travel by DMA through the slot table's space (unused
+  // until the selection): [64 rows][16 parts] of 16 bytes, part p of row r at
+  // unit r * 16 + (p ^ (r & 15)); rows >= L re-read row L - 1 (their rows are
+  // dropped).  Wave w moves units (2w + k) * 64 + lane, k = 0, 1.
+  uint16_t* qstage = reinterpret_cast<uint16_t*>(slot_s);
+  auto stage_q = [&](int g) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int row = 4 * (2 * wave + k) + (lane >> 4);
+      const int part = (lane & 15) ^ (row & 15);
+      const int64_t r = min(q0 + row, L - 1);
+      __builtin_amdgcn_global_load_lds(qb_base + ((r * a.Hkv + h) * G + g) * 128 + part * 8,
+                                       (lds_void_t*)(qstage + (2 * wave + k) * 512), 16, 0, 0);
     }
   };
-  load_q(0, Acur);
+  stage_q(0);
   stage(0, 0, true);
 
   // Pass 1: biased logits, LSE over all chunks, running max over heads.
   for (int s = 0; s < G; ++s) {
     const int g = s;
-    begin_step(s, s != G - 1);
+    begin_step(s, false);
+    // This lane's A operand rows: query 16qg + col (row & 15 == col).
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      Acur[j] = *reinterpret_cast<const u32x4_t*>(
+          qstage + ((16 * qg + col) * 16 + ((4 * j + grp) ^ col)) * 8);
     f32x4_t S[kNT];
-    logits(lmk_buf(s & 1), Acur, S);
+    step_logits(std::false_type{}, s, S);
     const float* bias_g = bias_s + 256 * (s & 1);
     // x = s * scale + bias, -inf past C.
 #pragma unroll
@@ -416,6 +454,8 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
       }
     }
     __syncthreads();
+    // Every wave has read this head's q tile: stage the next one.
+    if (s + 1 < G) stage_q(s + 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t r = qbase + 4 * grp + i;
@@ -438,8 +478,6 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
 #pragma unroll
       for (int t = 0; t < kNT; ++t) M[t][i] = max_raw(M[t][i], S[t][i] - tot);
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) Acur[j] = Anext[j];
   }
 
   select_step<G>(a, M, lmk_buf((G - 1) & 1), cbad, slot_s, ntot_s, q0, qbase, L, C, h, b, lane, wave,
@@ -454,16 +492,22 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
     const int g = head_of(s);
     begin_step(s, true);
     f32x4_t S[kNT];
-    logits(lmk_buf(s & 1), Acur, S);
+    step_logits(std::true_type{}, s, S);
+    // S^T: this lane's row and 4 consecutive chunks per tile; one 4-byte read
+    // of the slot table per tile, most of which hold no pick.
+    const int row = 16 * qg + col;
 #pragma unroll
-    for (int t = 0; t < kNT; ++t)
+    for (int t = 0; t < kNT; ++t) {
+      const uint32_t sw =
+          *reinterpret_cast<const uint32_t*>(slot_s + row * 256 + cbase + 16 * t + 4 * grp);
+      if (sw != 0xffffffffu) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 16 * qg + 4 * grp + i;
-        const int c = cbase + 16 * t + col;
-        const int slot = slot_s[row * 256 + c];
-        if (slot >= 0) sc_s[row * K + slot] = (uint16_t)f32_to_bf16(S[t][i] * a.sm_scale);
+        for (int i = 0; i < 4; ++i) {
+          const int slot = (int)(int8_t)(sw >> (8 * i));
+          if (slot >= 0) sc_s[row * K + slot] = (uint16_t)f32_to_bf16(S[t][i] * a.sm_scale);
+        }
       }
+    }
     __syncthreads();
     for (int e = tid; e < nrows * K; e += kFastThreads) {
       const int row = e / K, slot = e - row * K;
