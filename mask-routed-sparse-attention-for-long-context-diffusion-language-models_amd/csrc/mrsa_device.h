@@ -87,6 +87,45 @@ __device__ __forceinline__ int group16_sum_i(int v) {
   for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+// Integer reductions and prefix sums inside groups of 8 consecutive lanes
+// (lanes sharing l / 8), with DPP lane moves instead of LDS permutes:
+// quad_perm swaps, then row_half_mirror pairs the two quads of each 8-lane
+// half-row.  Every lane of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ int group8_sum_i(int v) {
+  v += dpp_mov_i<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov_i<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov_i<0x141>(v);  // row_half_mirror
+  return v;
+}
+__device__ __forceinline__ uint32_t group8_min_u(uint32_t v) {
+  v = min(v, (uint32_t)dpp_mov_i<0xb1>((int)v));
+  v = min(v, (uint32_t)dpp_mov_i<0x4e>((int)v));
+  v = min(v, (uint32_t)dpp_mov_i<0x141>((int)v));
+  return v;
+}
+__device__ __forceinline__ uint32_t group8_max_u(uint32_t v) {
+  v = max(v, (uint32_t)dpp_mov_i<0xb1>((int)v));
+  v = max(v, (uint32_t)dpp_mov_i<0x4e>((int)v));
+  v = max(v, (uint32_t)dpp_mov_i<0x141>((int)v));
+  return v;
+}
+// Exclusive prefix sum over the 8 lanes of a group (sub = l % 8): row_shr:o
+// brings lane l - o, which is in the same group when sub >= o.
+__device__ __forceinline__ int group8_excl_scan_i(int v, int sub) {
+  int incl = v, up;
+  up = dpp_mov_i<0x111>(incl);  // row_shr:1
+  if (sub >= 1) incl += up;
+  up = dpp_mov_i<0x112>(incl);  // row_shr:2
+  if (sub >= 2) incl += up;
+  up = dpp_mov_i<0x114>(incl);  // row_shr:4
+  if (sub >= 4) incl += up;
+  return incl - v;
+}
+
 // Reductions across the four lane groups (lanes sharing l % 16), with the
 // gfx950 row-swap instructions: v_permlane32_swap exchanges the upper half of
 // one operand with the lower half of the other, so swapping a value with

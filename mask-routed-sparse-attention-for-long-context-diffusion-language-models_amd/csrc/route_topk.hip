@@ -162,12 +162,9 @@ __device__ __forceinline__ void select_step(const RouteArgs& a, const float (&M)
       kmin = min(kmin, key[e]);
       kmax = max(kmax, key[e]);
     }
-#pragma unroll
-  for (int o = 1; o < 8; o <<= 1) {
-    nfin += __shfl_xor(nfin, o, 64);
-    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, 64));
-    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, 64));
-  }
+  nfin = group8_sum_i(nfin);
+  kmin = group8_min_u(kmin);
+  kmax = group8_max_u(kmax);
   uint32_t thr_hi, thr_tie = 0u, lo = kmin, hi = kmax + 1u;
   int need = 0;
   bool done;
@@ -184,8 +181,7 @@ __device__ __forceinline__ void select_step(const RouteArgs& a, const float (&M)
     int cnt = 0;
 #pragma unroll
     for (int e = 0; e < 32; ++e) cnt += key[e] >= mid ? 1 : 0;
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) cnt += __shfl_xor(cnt, o, 64);
+    cnt = group8_sum_i(cnt);
     if (!done) {
       if (hi - lo <= 1u) {
         done = true;
@@ -203,22 +199,13 @@ __device__ __forceinline__ void select_step(const RouteArgs& a, const float (&M)
     int cnt_hi = 0;
 #pragma unroll
     for (int e = 0; e < 32; ++e) cnt_hi += key[e] >= hi ? 1 : 0;
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) cnt_hi += __shfl_xor(cnt_hi, o, 64);
+    cnt_hi = group8_sum_i(cnt_hi);
     thr_hi = hi;
     thr_tie = lo;
     need = K - cnt_hi;
   }
   // Exclusive prefix over the 8 lanes of the row (chunk order == lane order).
-  auto excl8 = [&](int v) {
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {
-      const int up = __shfl_up(incl, o, 8);
-      if (sub >= o) incl += up;
-    }
-    return incl - v;
-  };
+  auto excl8 = [&](int v) { return group8_excl_scan_i(v, sub); };
   int my_ties = 0;
 #pragma unroll
   for (int e = 0; e < 32; ++e) my_ties += (need > 0 && key[e] == thr_tie) ? 1 : 0;
@@ -237,8 +224,7 @@ __device__ __forceinline__ void select_step(const RouteArgs& a, const float (&M)
   }
   int slot = excl8(my_picks);
   int total = my_picks;
-#pragma unroll
-  for (int o = 1; o < 8; o <<= 1) total += __shfl_xor(total, o, 64);
+  total = group8_sum_i(total);
   const int64_t orow = (b * L + r) * a.Hkv + h;
 #pragma unroll
   for (int e = 0; e < 32; ++e) {
