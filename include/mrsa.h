@@ -84,6 +84,21 @@ int mrsa_remote_drop_mask(const uint8_t* valid_mask, const uint8_t* allowed_mask
                           int32_t* drop_mask, void* stream);
 
 /*
+ * Rows of the remote drop mask for queries at given cache positions: row i is
+ * row query_positions[i] of mrsa_remote_drop_mask(valid_mask, NULL, ...).
+ * Replaces remote_drop_mask(cache.key_valid, window, chunk_size)
+ * .index_select(1, query_positions) in the cached decode path
+ * (dream_dllm_hils/fastdllm_attention.py:295-299), without materialising the
+ * full [batch, seq_len, chunks] mask.
+ *   valid_mask: bool [batch, seq_len]; query_positions: int64 [rows], each in
+ *   [0, seq_len) (not checked on the device)
+ *   drop_mask (out): int32 [batch, rows, seq_len / chunk_size]
+ */
+int mrsa_remote_drop_mask_rows(const uint8_t* valid_mask, const int64_t* query_positions,
+                               int64_t batch, int64_t seq_len, int64_t rows, int64_t window,
+                               int64_t chunk_size, int32_t* drop_mask, void* stream);
+
+/*
  * Route scoring with per-KV-group top-k ("softmax then max pooling").
  * Replaces ref_softmax_topk_max_pooling (ops/topk_head_softmax.py:15-156),
  * which route_topk_g7 (dream_dllm_hils/routing.py:52-171) and

@@ -10,7 +10,8 @@ namespace {
 // kernel_utils.py:75-99 (bounds) and :102-161 (mask).
 __global__ void __launch_bounds__(256)
     drop_mask_kernel(const uint8_t* __restrict__ valid, const uint8_t* __restrict__ allowed,
-                     int64_t L, int64_t W, int64_t S, int32_t* __restrict__ out) {
+                     const int64_t* __restrict__ qpos, int64_t rows_total, int64_t L, int64_t W,
+                     int64_t S, int32_t* __restrict__ out) {
   extern __shared__ unsigned char chunk_ok[];
   const int64_t b = blockIdx.y;
   const int64_t C = L / S;
@@ -21,14 +22,15 @@ __global__ void __launch_bounds__(256)
   }
   __syncthreads();
   const int64_t i0 = (int64_t)blockIdx.x * 64;
-  const int64_t rows = min((int64_t)64, L - i0);
+  const int64_t rows = min((int64_t)64, rows_total - i0);
   for (int64_t e = threadIdx.x; e < rows * C; e += blockDim.x) {
     const int64_t i = i0 + e / C, c = e % C;
-    const int64_t lc = max(i - W, (int64_t)0) / S;
-    const int64_t rc = min(i + W, L - 1) / S;
+    const int64_t p = qpos ? qpos[i] : i;  // cache position of output row i
+    const int64_t lc = max(p - W, (int64_t)0) / S;
+    const int64_t rc = min(p + W, L - 1) / S;
     bool drop = (c >= lc && c <= rc) || !chunk_ok[c];
-    if (allowed) drop = drop || allowed[(b * L + i) * L + c * S + S - 1] == 0;
-    out[(b * L + i) * C + c] = drop ? 1 : 0;
+    if (allowed) drop = drop || allowed[(b * L + p) * L + c * S + S - 1] == 0;
+    out[(b * rows_total + i) * C + c] = drop ? 1 : 0;
   }
 }
 
@@ -80,7 +82,24 @@ extern "C" int mrsa_remote_drop_mask(const uint8_t* valid_mask, const uint8_t* a
   if (C > 60 * 1024 || batch > 65535) return MRSA_ERR_UNSUPPORTED;
   dim3 grid((unsigned)((seq_len + 63) / 64), (unsigned)batch);
   hipLaunchKernelGGL(drop_mask_kernel, grid, dim3(256), (size_t)C, (hipStream_t)stream, valid_mask,
-                     allowed_mask, seq_len, window, chunk_size, drop_mask);
+                     allowed_mask, nullptr, seq_len, seq_len, window, chunk_size, drop_mask);
+  return mrsa_launch_status();
+}
+
+extern "C" int mrsa_remote_drop_mask_rows(const uint8_t* valid_mask,
+                                          const int64_t* query_positions, int64_t batch,
+                                          int64_t seq_len, int64_t rows, int64_t window,
+                                          int64_t chunk_size, int32_t* drop_mask, void* stream) {
+  if (batch < 0 || seq_len <= 0 || rows < 0 || window < 0 || chunk_size <= 0 ||
+      seq_len % chunk_size != 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (batch == 0 || rows == 0) return MRSA_OK;
+  if (!valid_mask || !query_positions || !drop_mask) return MRSA_ERR_INVALID_ARGUMENT;
+  const int64_t C = seq_len / chunk_size;
+  if (C > 60 * 1024 || batch > 65535 || rows > ((int64_t)1 << 36)) return MRSA_ERR_UNSUPPORTED;
+  dim3 grid((unsigned)((rows + 63) / 64), (unsigned)batch);
+  hipLaunchKernelGGL(drop_mask_kernel, grid, dim3(256), (size_t)C, (hipStream_t)stream, valid_mask,
+                     nullptr, query_positions, rows, seq_len, window, chunk_size, drop_mask);
   return mrsa_launch_status();
 }
 

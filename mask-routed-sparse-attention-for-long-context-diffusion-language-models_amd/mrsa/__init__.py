@@ -15,8 +15,9 @@ hand-written HIP kernels in ../csrc (C ABI: include/mrsa.h).  Module map:
                         (ops/hils_bidir_route_weights_tilelang.py, attention.py:126-235)
     fusion.py           fuse_hils_outputs               (ops/hils_bidir_output_fusion_tilelang.py)
     token_score.py      candidate_token_scores_gqa      (ops/hils_token_score_gqa_tilelang.py)
-    kernel_utils.py     remote_drop_mask, chunk_aligned_local_bounds, group_pad_to/unpad
-    route_layer.py      route_attention, swa_attention  (attention.py route / SWA layers)
+    kernel_utils.py     remote_drop_mask(_rows), chunk_aligned_local_bounds, group_pad_to/unpad
+    route_layer.py      route_attention, swa_attention  (attention.py route / SWA layers),
+                        cached_route_attention + LayerKVCache (fastdllm_attention.py cached step)
 """
 
 from .fusion import fuse_hils_outputs
@@ -25,10 +26,17 @@ from .kernel_utils import (
     group_pad_to,
     group_unpad,
     remote_drop_mask,
+    remote_drop_mask_rows,
 )
 from .local_attention import bidir_local_attention, cached_local_attention
 from .pool import chunk_attn_pool_gqa, chunk_attn_pool_gqa_prior
-from .route_layer import RouteLayerConfig, route_attention, swa_attention
+from .route_layer import (
+    LayerKVCache,
+    RouteLayerConfig,
+    cached_route_attention,
+    route_attention,
+    swa_attention,
+)
 from .route_weights import route_weights, route_weights_torch
 from .routing import route_topk_g7, selected_attention_g7, selected_attention_g7_cached
 from .sparse_attention import HiLS_block_M_head, value_tiles
@@ -40,7 +48,9 @@ __all__ = [
     "HiLS_block_M_head",
     "LIB_PATH",
     "MrsaLibraryError",
+    "LayerKVCache",
     "RouteLayerConfig",
+    "cached_route_attention",
     "bidir_local_attention",
     "cached_local_attention",
     "candidate_token_scores_gqa",
@@ -54,6 +64,7 @@ __all__ = [
     "online_softmax_topk_head",
     "ref_softmax_topk_max_pooling",
     "remote_drop_mask",
+    "remote_drop_mask_rows",
     "route_attention",
     "route_topk_g7",
     "route_weights",

@@ -123,3 +123,44 @@ def remote_drop_mask(
     )
     _lib.check(st, "remote_drop_mask")
     return out
+
+
+def remote_drop_mask_rows(
+    valid_mask: torch.Tensor,
+    window: int,
+    chunk_size: int,
+    query_positions: torch.Tensor,
+) -> torch.Tensor:
+    """``remote_drop_mask(valid_mask, window, chunk_size)[:, query_positions]``
+    without the full [B, L, L/S] mask; int32 [B, len(query_positions), L/S].
+
+    The cached decode path's drop mask (fastdllm_attention.py:295-299).
+    """
+
+    if valid_mask.ndim != 2:
+        raise ValueError(
+            f"valid_mask must have shape [B, L], got {tuple(valid_mask.shape)}"
+        )
+    batch, seq_len = valid_mask.shape
+    if chunk_size <= 0 or seq_len % chunk_size != 0:
+        raise ValueError(
+            f"sequence length {seq_len} must be divisible by chunk_size={chunk_size}"
+        )
+    if window < 0:
+        raise ValueError(f"window must be non-negative, got {window}")
+    if query_positions.ndim != 1 or query_positions.dtype != torch.long:
+        raise ValueError("query_positions must be a 1-D torch.long tensor")
+    if valid_mask.device.type != "cuda" or query_positions.device != valid_mask.device:
+        raise ValueError("remote_drop_mask_rows requires CUDA tensors on one device")
+    rows = query_positions.numel()
+    if rows and bool(((query_positions < 0) | (query_positions >= seq_len)).any()):
+        raise ValueError("query_positions must be in [0, seq_len)")
+    valid = valid_mask.to(torch.bool).contiguous()
+    pos = query_positions.contiguous()
+    out = torch.empty(batch, rows, seq_len // chunk_size, dtype=torch.int32, device=valid.device)
+    st = _lib.call(
+        "mrsa_remote_drop_mask_rows", _lib.ptr(valid), _lib.ptr(pos), batch, seq_len, rows,
+        int(window), int(chunk_size), _lib.ptr(out), _lib.stream_of(out),
+    )
+    _lib.check(st, "remote_drop_mask_rows")
+    return out

@@ -16,6 +16,12 @@ token budget, fusion weights from the affine gate at topk >= 32):
 ``swa_attention`` is ``KernelDreamSlidingWindowAttention.forward``
 (attention.py:1168-1220) between projections and o_proj.
 
+``cached_route_attention`` is the Fast-dLLM cached block step of a route layer
+(``cached_attention_forward``, fastdllm_attention.py:203-382) after the
+projections and the K/V cache update: a block of query rows against the
+layer's cache, with the landmark summaries of the affected chunks refreshed
+in place.
+
 Everything runs on the library's kernels on the current stream; the drop mask
 is derived inside the route kernel instead of being materialised, and V is
 re-laid out once for both attention kernels.
@@ -28,6 +34,7 @@ from dataclasses import dataclass
 import torch
 
 from .fusion import fuse_hils_outputs
+from .kernel_utils import remote_drop_mask_rows
 from .local_attention import local_attention_launch
 from .pool import chunk_attn_pool_gqa_prior
 from .route_weights import route_weights_launch
@@ -164,3 +171,144 @@ def swa_attention(
         chunk_size if skip_inert_slots else 0,
     )
     return out
+
+
+@dataclass
+class LayerKVCache:
+    """The cache fields a cached route layer reads and refreshes
+    (dream_dllm_hils/fastdllm_cache.py:10-161): key, value bf16 [1, L, Hkv, D],
+    key_valid bool [1, L], landmark_keys bf16 [1, C, Hkv, G, D] and prior_bias
+    fp32 [1, C, Hkv, G] (the last two refreshed in place)."""
+
+    key: torch.Tensor
+    value: torch.Tensor
+    key_valid: torch.Tensor
+    landmark_keys: torch.Tensor
+    prior_bias: torch.Tensor
+
+    def __post_init__(self) -> None:
+        # fastdllm_cache.py:20-80 (the checks this path depends on)
+        if self.key.ndim != 4 or self.value.shape != self.key.shape:
+            raise ValueError("key and value must have identical [B,L,Hkv,D] shape")
+        if self.key.shape[0] != 1:
+            raise ValueError("Fast-dLLM cache currently requires batch size one")
+        if self.key_valid.shape != self.key.shape[:2]:
+            raise ValueError("key_valid shape must match the cache batch and sequence")
+        if self.key_valid.dtype != torch.bool:
+            raise ValueError("key_valid must be boolean")
+        batch, _, hkv, dim = self.key.shape
+        lm = self.landmark_keys.shape
+        if self.landmark_keys.ndim != 5 or lm[0] != batch or lm[2] != hkv or lm[4] != dim:
+            raise ValueError(f"landmark_keys must have shape [B,C,{hkv},G,D]")
+        if self.prior_bias.shape != lm[:-1]:
+            raise ValueError(f"prior_bias must have shape {tuple(lm[:-1])}")
+
+
+def _rows_for_positions(query_positions: torch.Tensor, owned_positions: torch.Tensor):
+    # fastdllm_attention.py:54-66
+    if owned_positions.numel() == 0:
+        return owned_positions
+    rows = torch.searchsorted(query_positions, owned_positions)
+    if bool((rows >= query_positions.numel()).any()) or not torch.equal(
+        query_positions.index_select(0, rows), owned_positions
+    ):
+        raise ValueError("all owned positions must also be query positions")
+    return rows
+
+
+def cached_route_attention(
+    q: torch.Tensor,
+    route_q: torch.Tensor,
+    cache: LayerKVCache,
+    query_positions: torch.Tensor,
+    affected_chunks: torch.Tensor,
+    entropy_bias_scale: torch.Tensor,
+    cfg: RouteLayerConfig = RouteLayerConfig(),
+    return_intermediates: bool = False,
+):
+    """Route-layer attention of a query block against a K/V cache
+    (fastdllm_attention.py:203-382 for KernelDreamFullHiLSAttention):
+
+        local branch   cached_local_attention(cache, query_positions, skip_inert_slots)
+        landmarks      chunk_attn_pool_gqa of each affected chunk from route_q at its
+                       landmark row; cache.landmark_keys / prior_bias refreshed in place
+        routing        route_topk_g7 with remote_drop_mask(key_valid, W, S) rows
+        weights        _route_weights_torch(temperature=1.0): the plain 33-way
+                       softmax (this path passes no fusion gate, :315-323)
+        remote branch  selected_attention_g7_cached
+        output         fuse_hils_outputs
+
+    q, route_q: bf16 [1, Lq, Hq, D]; query_positions: sorted unique torch.long
+    [Lq]; affected_chunks: torch.long [n] whose landmark positions are query
+    positions.  Returns the fused output [1, Lq, Hq, D] bf16.
+    """
+
+    if q.device.type != "cuda":
+        raise ValueError("cached route attention requires CUDA tensors")
+    for name, t in (("q", q), ("route_q", route_q)):
+        if t.dtype != torch.bfloat16 or t.ndim != 4:
+            raise ValueError(f"{name} must be bf16 [1, Lq, H, D]")
+    if route_q.shape != q.shape:
+        raise ValueError("route_q must have the shape of q")
+    B, Lq, Hq, D = q.shape
+    L, Hkv = cache.key.shape[1], cache.key.shape[2]
+    if B != 1 or cache.key.shape[3] != D or Hq % Hkv:
+        raise ValueError(f"incompatible q {tuple(q.shape)} and cache {tuple(cache.key.shape)}")
+    G = Hq // Hkv
+    S = cfg.chunk_size
+    if L % S:
+        raise ValueError(f"cache length {L} must be divisible by chunk_size={S}")
+    C = L // S
+    if cache.landmark_keys.shape[1] != C or cache.landmark_keys.shape[3] != G:
+        raise ValueError(f"landmark_keys must have shape [1, {C}, {Hkv}, {G}, {D}]")
+    if query_positions.shape != (Lq,) or query_positions.dtype != torch.long:
+        raise ValueError(f"query_positions must be torch.long of shape {(Lq,)}")
+    if Lq and bool((query_positions[1:] <= query_positions[:-1]).any()):
+        raise ValueError("query_positions must be sorted and unique")
+    if Lq and bool(((query_positions < 0) | (query_positions >= L)).any()):
+        raise ValueError("query_positions must be in cache range")
+
+    vt = value_tiles(cache.value)
+    flash_window = cfg.local_window + S - 1 if cfg.skip_inert_slots else cfg.local_window
+    local_out, local_lse = local_attention_launch(
+        q, cache.key, vt, cache.key_valid, flash_window, S if cfg.skip_inert_slots else 0,
+        query_positions=query_positions,
+    )
+    if affected_chunks.numel():
+        landmark_rows = _rows_for_positions(query_positions, affected_chunks * S + (S - 1))
+        n = affected_chunks.numel()
+        q_lmk = route_q.index_select(1, landmark_rows).reshape(1, n, Hkv, G, D)
+        chunk_positions = (
+            affected_chunks[:, None] * S + torch.arange(S, device=q.device)[None, :]
+        ).reshape(-1)
+        chunk_keys = cache.key.index_select(1, chunk_positions).reshape(1, n, S, Hkv, D)
+        chunk_valid = cache.key_valid.index_select(1, chunk_positions).reshape(1, n, S)
+        lmk, _, prior = chunk_attn_pool_gqa_prior(
+            q_lmk.contiguous(), chunk_keys.contiguous(), chunk_valid.contiguous(),
+            entropy_bias_scale,
+        )
+        cache.landmark_keys.index_copy_(1, affected_chunks, lmk.reshape(1, n, Hkv, G, D))
+        cache.prior_bias.index_copy_(1, affected_chunks, prior.reshape(1, n, Hkv, G))
+    drop = remote_drop_mask_rows(cache.key_valid, cfg.local_window, S, query_positions)
+    indices, scores = route_topk_launch(
+        route_q.reshape(1, Lq, Hkv, G, D),
+        cache.landmark_keys.reshape(1, C, Hq, D),
+        local_lse.reshape(1, Lq, Hkv, G),
+        cfg.topk,
+        S,
+        bias4=cache.prior_bias,
+        drop_mask=drop,
+    )
+    scores = scores.reshape(1, Lq, Hq, cfg.topk)
+    remote_w, local_w = route_weights_launch(
+        scores, indices, cache.prior_bias, local_lse, temperature=1.0
+    )
+    remote_out = selected_attention_launch(q, cache.key, vt, remote_w, indices, cache.key_valid, S)
+    out = fuse_hils_outputs(remote_out, local_out, local_w)
+    if not return_intermediates:
+        return out
+    return out, {
+        "local_output": local_out, "local_lse": local_lse, "indices": indices,
+        "scores": scores, "remote_weights": remote_w, "local_weight": local_w,
+        "remote_output": remote_out, "drop_mask": drop,
+    }

@@ -420,3 +420,56 @@ def route_layer(q, k, v, route_q, entropy_bias_scale, key_valid=None, *, local_w
         "entropy": entropy, "prior_bias": prior, "indices": idx, "scores": scores_bf,
         "selection": sel, "remote_weights": rw, "local_weight": lw, "remote_output": remote,
     }
+
+
+def cached_route_layer(q, route_q, cache_key, cache_value, cache_valid, landmark_keys,
+                       prior_bias, query_positions, affected_chunks, entropy_bias_scale, *,
+                       local_window=256, chunk_size=64, topk=32, skip_inert_slots=True):
+    """Cached block step of a route layer (dream_dllm_hils/fastdllm_attention.py:
+    203-382) after the projections and the K/V update, with the reference's
+    bf16 rounding between stages.  landmark_keys [1, C, Hkv, G, D] bf16 and
+    prior_bias [1, C, Hkv, G] fp32 are refreshed for affected_chunks (copies
+    are returned; the inputs are not modified).  Returns (out bf16,
+    landmark_keys, prior_bias, intermediates dict)."""
+
+    B, Lq, Hq, D = q.shape
+    L, Hkv = cache_key.shape[1], cache_key.shape[2]
+    G = Hq // Hkv
+    S = chunk_size
+    C = L // S
+    kv = cache_valid.bool()
+    pos = query_positions.long().cpu()
+    window = local_window + S - 1 if skip_inert_slots else local_window
+    local_out, local_lse = local_attention(q, cache_key, cache_value, kv, window,
+                                           S if skip_inert_slots else 0, query_positions=pos)
+    local_out = local_out.to(torch.bfloat16)
+    lmk_all = landmark_keys.clone()
+    prior_all = prior_bias.clone()
+    aff = affected_chunks.long().cpu()
+    if aff.numel():
+        # fastdllm_attention.py:236-292 (_rows_for_positions: rows of the
+        # landmark positions in the query block)
+        rows = torch.searchsorted(pos, aff * S + (S - 1))
+        q_lmk = route_q[:, rows].reshape(B, aff.numel(), Hkv, G, D)
+        cpos = (aff[:, None] * S + torch.arange(S)[None]).reshape(-1)
+        chunk_keys = cache_key[:, cpos].reshape(B, aff.numel(), S, Hkv, D)
+        chunk_valid = kv[:, cpos].reshape(B, aff.numel(), S)
+        lmk, entropy = chunk_attn_pool(q_lmk, chunk_keys, chunk_valid)
+        lmk_all[:, aff] = lmk.to(torch.bfloat16)
+        prior_all[:, aff] = entropy * entropy_bias_scale.float().view(1, 1, Hkv, G)
+    drop = remote_drop_mask(kv, local_window, S)[:, pos]
+    idx, scores, sel = route_topk(
+        route_q.reshape(B, Lq, Hkv, G, D), lmk_all.reshape(B, C, Hq, D),
+        local_lse.reshape(B, Lq, Hkv, G), topk, S, drop_mask=drop, bias4=prior_all,
+    )
+    scores_bf = scores.reshape(B, Lq, Hq, topk).to(torch.bfloat16)
+    rw, lw = route_weights(scores_bf, idx, prior_all, local_lse, temperature=1.0)
+    rw = rw.to(torch.bfloat16)
+    lw = lw.to(torch.bfloat16)
+    remote = selected_attention(q, cache_key, cache_value, rw, idx, kv, S).to(torch.bfloat16)
+    out = fuse_outputs(remote, local_out, lw)
+    return out, lmk_all, prior_all, {
+        "local_output": local_out, "local_lse": local_lse, "indices": idx,
+        "scores": scores_bf, "selection": sel, "remote_weights": rw, "local_weight": lw,
+        "remote_output": remote, "drop_mask": drop,
+    }

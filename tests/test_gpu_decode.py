@@ -1,0 +1,127 @@
+"""GPU parity of the Fast-dLLM cached block step of a route layer
+(dream_dllm_hils/fastdllm_attention.py:203-382) against the CPU oracle.
+
+Tolerances as in test_gpu_parity.py: outputs within max-abs 2e-2 and mean-abs
+2e-3; routing rows identical except near ties; drop rows bit-exact.
+"""
+
+import pytest
+import torch
+
+import mrsa
+from oracle import mrsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def _rand(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g) * scale
+
+
+def _planted_kv(L, Hkv, D, seed, sigma=0.3):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(1, L, Hkv, D, generator=g)
+    shift = sigma * torch.randn(L // 64, Hkv, D, generator=g)
+    k = k + shift.repeat_interleave(64, dim=0)[None]
+    v = torch.randn(1, L, Hkv, D, generator=g)
+    return k.bfloat16(), v.bfloat16()
+
+
+def _close(actual, expected, what, max_abs=2e-2, mean_abs=2e-3):
+    err = (actual.float().cpu() - expected.float()).abs()
+    print(f"{what}: max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
+    assert float(err.max()) <= max_abs, what
+    assert float(err.mean()) <= mean_abs, what
+
+
+def test_drop_mask_rows_bit_exact():
+    _note("drop mask rows")
+    L, S, W = 4096, 64, 256
+    valid = torch.rand(1, L, generator=torch.Generator().manual_seed(3)) > 0.02
+    valid[0, 64 * 7 : 64 * 7 + 63] = False  # an invalid chunk (landmark slot alone is valid)
+    pos = torch.tensor([0, 1, 63, 64, 1000, 2047, 2048, 3000, 4095], dtype=torch.long)
+    got = mrsa.remote_drop_mask_rows(valid.to(DEV), W, S, pos.to(DEV))
+    ref = O.remote_drop_mask(valid, W, S)[:, pos]
+    assert torch.equal(got.cpu(), ref)
+    with pytest.raises(ValueError):
+        mrsa.remote_drop_mask_rows(valid.to(DEV), W, S, torch.tensor([L], device=DEV))
+
+
+def _cache_inputs(L, Hq, Hkv, D, seed):
+    q = _rand((1, L, Hq, D), seed).bfloat16()
+    rq = _rand((1, L, Hq, D), seed + 1).bfloat16()
+    k, v = _planted_kv(L, Hkv, D, seed + 2)
+    return q, rq, k, v
+
+
+def test_cached_route_attention_vs_oracle():
+    _note("cached route layer L=4096 block=chunk 31")
+    L, Hq, Hkv, D, S = 4096, 28, 4, 128, 64
+    C, G = L // S, Hq // Hkv
+    q, rq, k, v = _cache_inputs(L, Hq, Hkv, D, 70)
+    valid = torch.ones(1, L, dtype=torch.bool)
+    valid[0, 900:905] = False
+    scale = torch.rand(Hq, generator=torch.Generator().manual_seed(74)) + 0.5
+    g = torch.Generator().manual_seed(75)
+    lmk0 = torch.randn(1, C, Hkv, G, D, generator=g).bfloat16()
+    prior0 = torch.rand(1, C, Hkv, G, generator=g) * 0.5
+    chunk = 31
+    rows = torch.arange(chunk * S, (chunk + 1) * S)
+    aff = torch.tensor([chunk])
+    cache = mrsa.LayerKVCache(k.to(DEV), v.to(DEV), valid.to(DEV), lmk0.clone().to(DEV),
+                              prior0.clone().to(DEV))
+    out, mid = mrsa.cached_route_attention(
+        q[:, rows].to(DEV), rq[:, rows].to(DEV), cache, rows.to(DEV), aff.to(DEV),
+        scale.to(DEV), return_intermediates=True)
+    ref, rlmk, rprior, rmid = O.cached_route_layer(
+        q[:, rows], rq[:, rows], k, v, valid, lmk0, prior0, rows, aff, scale)
+    _close(cache.landmark_keys, rlmk, "refreshed landmark keys")
+    torch.testing.assert_close(cache.prior_bias.cpu(), rprior, atol=1e-3, rtol=1e-3)
+    others = torch.arange(C) != chunk
+    assert torch.equal(cache.landmark_keys.cpu()[:, others], lmk0[:, others])
+    assert torch.equal(mid["drop_mask"].cpu(), rmid["drop_mask"])
+    agree = (mid["indices"].cpu().long() == rmid["indices"]).all(-1).float().mean()
+    print(f"cached route layer: index rows identical to oracle: {float(agree):.4f}", flush=True)
+    assert float(agree) > 0.98
+    _close(mid["local_output"], rmid["local_output"], "cached local branch")
+    _close(out, ref, "cached route layer")
+
+
+def test_cached_refresh_matches_prefill():
+    # Port of unittests/test_qcal.py:124-157: prefill, change the last chunk's
+    # rows, refresh it through the cached step; the output rows and the
+    # refreshed landmark match a new prefill of the changed inputs.
+    _note("cached refresh vs prefill L=2048")
+    L, Hq, Hkv, D, S = 2048, 28, 4, 128, 64
+    q, rq, k, v = _cache_inputs(L, Hq, Hkv, D, 80)
+    valid = torch.ones(1, L, dtype=torch.bool, device=DEV)
+    scale = (torch.rand(Hq, generator=torch.Generator().manual_seed(84)) + 0.5).to(DEV)
+    cfg = mrsa.RouteLayerConfig(gate_offset=None, gate_scale=None)  # the decode path's weights
+    q, rq, k, v = (t.to(DEV) for t in (q, rq, k, v))
+    _, mid = mrsa.route_attention(q, k, v, rq, scale, valid, cfg, return_intermediates=True)
+    original_lmk = mid["landmark_keys"].clone()
+    rows = torch.arange(L - S, L, device=DEV)
+    g = torch.Generator().manual_seed(85)
+    bump = lambda t: t.index_add(1, rows, (torch.randn(t[:, rows].shape, generator=g) * 0.1)
+                                 .to(DEV, torch.bfloat16))
+    q2, rq2, k2, v2 = bump(q), bump(rq), bump(k), bump(v)
+    cache = mrsa.LayerKVCache(k2.clone(), v2.clone(), valid.clone(),
+                              mid["landmark_keys"].clone(), mid["prior_bias"].clone())
+    actual = mrsa.cached_route_attention(q2[:, rows], rq2[:, rows], cache, rows,
+                                         torch.tensor([L // S - 1], device=DEV), scale, cfg)
+    expected, emid = mrsa.route_attention(q2, k2, v2, rq2, scale, valid, cfg,
+                                          return_intermediates=True)
+    expected = expected[:, rows]
+    torch.cuda.synchronize()
+    assert torch.equal(cache.landmark_keys[:, :-1], original_lmk[:, :-1])
+    torch.testing.assert_close(cache.landmark_keys.float(), emid["landmark_keys"].float(),
+                               atol=0.01, rtol=0.03)
+    error = (actual.float() - expected.float()).norm() / expected.float().norm()
+    print(f"cached refresh vs prefill: rel error {float(error):.3e}", flush=True)
+    assert float(error) < 0.03
