@@ -14,6 +14,12 @@ Prints ONE JSON line (rank 0).  Besides the contract fields it carries:
   cpu_baseline  the CPU oracle's route layer at configuration 1 (L=4096, fp32)
                 timed on this host's cores
   stages_us     average per-stage times from the same events
+
+``--workload decode`` instead times the Fast-dLLM cached block step of one
+route layer (SURVEY configuration 5): a K/V cache of L=131072 tokens (2048
+chunks), 64 successive 32-token query blocks at its tail; each step writes the
+block's K/V rows into the cache, refreshes the landmark summary of the chunk
+whose landmark slot the block holds, and runs mrsa.cached_route_attention.
 """
 
 from __future__ import annotations
@@ -108,6 +114,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=("route", "decode"), default="route")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 1 GiB device copy three times (reference "
                          "dispatch for scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -123,6 +130,8 @@ def main() -> int:
     import mrsa
 
     dev = torch.device("cuda:0")
+    if args.workload == "decode":
+        return decode_main(args, torch, mrsa, dev)
     if args.copy_calibration:
         src = torch.empty(1 << 29, dtype=torch.int16, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -218,6 +227,83 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+DECODE_L, DECODE_BLOCK, DECODE_BLOCKS = 131072, 32, 64
+
+
+def decode_main(args, torch, mrsa, dev) -> int:
+    """Cached block decode (configuration 5): tokens/s over DECODE_BLOCKS
+    successive blocks of DECODE_BLOCK query tokens against a DECODE_L cache."""
+
+    L, S, nb, bs = DECODE_L, CHUNK, DECODE_BLOCKS, DECODE_BLOCK
+    C, G = L // S, HQ // HKV
+    g = torch.Generator().manual_seed(4321)
+    k = torch.randn(1, L, HKV, D, generator=g)
+    k = k + 0.3 * torch.randn(C, HKV, D, generator=g).repeat_interleave(S, dim=0)[None]
+    v = torch.randn(1, L, HKV, D, generator=g)
+    k = k.to(device=dev, dtype=torch.bfloat16)
+    v = v.to(device=dev, dtype=torch.bfloat16)
+    valid = torch.ones(1, L, dtype=torch.bool, device=dev)
+    scale = torch.ones(HQ, device=dev)
+    # Landmark summaries of the whole cache (prefill state), not timed.
+    q_lmk = torch.randn(1, C, HKV, G, D, generator=g).to(device=dev, dtype=torch.bfloat16)
+    lmk, _, prior = mrsa.chunk_attn_pool_gqa_prior(q_lmk, k.reshape(1, C, S, HKV, D),
+                                                   valid.reshape(1, C, S), scale)
+    cache = mrsa.LayerKVCache(k, v, valid, lmk.contiguous(), prior.contiguous())
+    cfg = mrsa.RouteLayerConfig(local_window=WINDOW, chunk_size=S, topk=TOPK)
+    start = L - nb * bs
+    blocks = []
+    for i in range(nb):
+        pos = torch.arange(start + i * bs, start + (i + 1) * bs, device=dev)
+        lm = pos[(pos + 1) % S == 0]
+        blocks.append((
+            torch.randn(1, bs, HQ, D, generator=g).to(device=dev, dtype=torch.bfloat16),
+            torch.randn(1, bs, HQ, D, generator=g).to(device=dev, dtype=torch.bfloat16),
+            torch.randn(1, bs, HKV, D, generator=g).to(device=dev, dtype=torch.bfloat16),
+            torch.randn(1, bs, HKV, D, generator=g).to(device=dev, dtype=torch.bfloat16),
+            pos, lm // S,
+        ))
+
+    def step(b):
+        q, rq, kb, vb, pos, aff = b
+        cache.key.index_copy_(1, pos, kb)      # cache.replace (fastdllm_cache.py)
+        cache.value.index_copy_(1, pos, vb)
+        return mrsa.cached_route_attention(q, rq, cache, pos, aff, scale, cfg)
+
+    for b in blocks[: max(1, args.warmup)]:
+        step(b)
+    torch.cuda.synchronize()
+    reps = max(1, args.steps // 10)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        for b in blocks:
+            step(b)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_block = 1000.0 * elapsed / (reps * nb)
+    line = {
+        "metric": "MRSA route-layer cached block decode tokens/s @128k (config 5)",
+        "value": bs / (ms_per_block / 1000.0),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": reps * nb,
+        "warmup": max(1, args.warmup),
+        "ms_per_step": ms_per_block,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "Fast-dLLM cached block step of one route layer (SURVEY config 5)",
+            "cache_len": L, "block": bs, "blocks": nb, "q_heads": HQ, "kv_heads": HKV,
+            "head_dim": D, "chunk_size": S, "topk": TOPK, "local_window": WINDOW,
+            "parallelism": "single-gpu",
+        },
+    }
     print(json.dumps(line), flush=True)
     return 0
 

@@ -100,26 +100,27 @@ struct SelArgs {
 // LDS carve-up (byte offsets, 16-aligned).  The p_* arrays are only used by
 // the prologue and live inside the ring, which is free until the first DMA.
 struct SelLayout {
-  size_t ring, wr, s_chunk, s_own, s_mask, s_done, s_claim, s_land, comp_slot, misc, total;
+  size_t ring, wr, s_chunk, s_own, s_mask, s_cnt, comp_slot, misc, total;
   size_t p_idx, p_kv, p_omask, p_len, p_w, p_end;
   int cap;
 };
 __host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
+// The walk has at most min(Ck, queries x K) steps; a tile holds at most
+// min(TQ, Lq) queries.
 __host__ __device__ inline SelLayout sel_layout(int TQ, int NW, int K, int64_t Ck, int R,
-                                                bool token) {
+                                                bool token, int64_t Lq) {
   SelLayout l;
   const size_t n = (size_t)TQ * K;
   const size_t wbytes = token ? 0 : (size_t)TQ * 8 * K * 2;
-  l.cap = (int)(Ck < (int64_t)n ? Ck : (int64_t)n);
+  const int64_t steps = (Lq < (int64_t)TQ ? Lq : (int64_t)TQ) * (int64_t)K;
+  l.cap = (int)(Ck < steps ? Ck : steps);
   size_t o = 0;
   l.ring = o;      o = align16(o + (size_t)R * kSlotBytes);
   l.wr = o;        o = align16(o + wbytes);                 // [TQ][K][8] bf16, list order
   l.s_chunk = o;   o = align16(o + (size_t)l.cap * 4);
   l.s_own = o;     o = align16(o + (size_t)l.cap * 8);
   l.s_mask = o;    o = align16(o + (size_t)l.cap * 8);
-  l.s_done = o;    o = align16(o + (size_t)l.cap * 4);
-  l.s_claim = o;   o = align16(o + (size_t)l.cap * 4);
-  l.s_land = o;    o = align16(o + (size_t)l.cap * 4);
+  l.s_cnt = o;     o = align16(o + (size_t)l.cap * 4);
   l.comp_slot = o; o = align16(o + n);
   l.misc = o;      o = align16(o + (size_t)(NW + 8) * 4);
   l.total = o;
@@ -455,7 +456,7 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   extern __shared__ __align__(16) unsigned char smem[];
   const int K = a.K;
   const int64_t Ck = a.Ck;
-  const SelLayout lay = sel_layout(kTQ, kWaves, K, Ck, R, TOKEN);
+  const SelLayout lay = sel_layout(kTQ, kWaves, K, Ck, R, TOKEN, a.Lq);
   unsigned char* ring = smem + lay.ring;
   uint16_t* wr = reinterpret_cast<uint16_t*>(smem + lay.wr);            // [TQ][K][8]
   uint16_t* wts = reinterpret_cast<uint16_t*>(smem + lay.p_w);          // [TQ][8][K]
@@ -466,9 +467,11 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   int32_t* misc = reinterpret_cast<int32_t*>(smem + lay.misc);          // [kWaves] scan, [kWaves] n
   // Walk counters per step: waves done with it, DMA portions of its chunk
   // claimed and landed.
-  int32_t* s_done = reinterpret_cast<int32_t*>(smem + lay.s_done);       // [cap]
-  int32_t* s_claim = reinterpret_cast<int32_t*>(smem + lay.s_claim);     // [cap]
-  int32_t* s_land = reinterpret_cast<int32_t*>(smem + lay.s_land);       // [cap]
+  // One word per step: waves done with it (bits 0-7), DMA portions of its
+  // chunk claimed (bits 8-15) and landed (bits 16-23).  No field overflows:
+  // at most 16 waves, and claims stop at kPortions plus one late claim per
+  // wave.
+  int32_t* s_cnt = reinterpret_cast<int32_t*>(smem + lay.s_cnt);         // [cap]
   int32_t* cursor = misc + kWaves + 4;  // oldest chunk with unclaimed portions
   int32_t* p_idx = reinterpret_cast<int32_t*>(smem + lay.p_idx);        // [TQ][K]
   uint8_t* p_kv = smem + lay.p_kv;                                      // [Ck][8] key-valid bytes
@@ -488,7 +491,7 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
 
   // Zeroed counters, published by the prologue's barriers.
   if (tid == 0) *cursor = 0;
-  for (int i = tid; i < lay.cap; i += kThreads) s_done[i] = s_claim[i] = s_land[i] = 0;
+  for (int i = tid; i < lay.cap; i += kThreads) s_cnt[i] = 0;
   const int nsteps = build_walk<TOKEN, SP>(
       a, WalkLds{wr, wts, s_chunk, s_own, s_mask, comp_slot, misc, p_idx, p_kv, p_omask, p_len}, b, h,
       q0, nq);
@@ -661,12 +664,12 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   //    workgroup barriers, so that waves drift apart by up to R chunks and
   //    the imbalance of their work evens out over that window.
   //    * Chunk n lives in ring slot n % R; it may be fetched once every wave
-  //      has counted itself done with step n - R (s_done).
+  //      has counted itself done with step n - R (s_cnt bits 0-7).
   //    * Its DMA is split into kPortions portions of 4 KB.  Waves that would
   //      otherwise idle (waiting for a chunk to land, or with no query routed
-  //      to the current step) claim the oldest fetchable portions (s_claim,
+  //      to the current step) claim the oldest fetchable portions (bits 8-15,
   //      chunk order kept by `cursor`), issue them, wait for their own DMA
-  //      (vmcnt) and count them landed (s_land).  The slowest wave, which
+  //      (vmcnt) and count them landed (bits 16-23).  The slowest wave, which
   //      frees each slot, thus rarely spends time issuing fetches.
   //    * A wave consumes chunk st once all its portions have landed; a wave
   //      with no query routed to it neither waits for it nor reads it.
@@ -710,16 +713,16 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
       const int n = __builtin_amdgcn_readfirstlane(lds_load_flag(lds_addr(cursor)));
       if (n >= limit) return;
       if (n >= R &&
-          __builtin_amdgcn_readfirstlane(lds_load_flag(lds_addr(&s_done[n - R]))) < kWaves)
+          (__builtin_amdgcn_readfirstlane(lds_load_flag(lds_addr(&s_cnt[n - R]))) & 0xff) < kWaves)
         return;
       int k = 0;
-      if (lane == 0) k = lds_fetch_add(lds_addr(&s_claim[n]), 1);
-      k = __builtin_amdgcn_readfirstlane(k);
+      if (lane == 0) k = lds_fetch_add(lds_addr(&s_cnt[n]), 1 << 8);
+      k = (__builtin_amdgcn_readfirstlane(k) >> 8) & 0xff;
       if (k >= kPortions) continue;  // chunk taken meanwhile; the cursor moves on
       if (k == kPortions - 1 && lane == 0) lds_store_flag(lds_addr(cursor), n + 1);
       issue_portion(n, k);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      if (lane == 0) lds_add(lds_addr(&s_land[n]), 1);
+      if (lane == 0) lds_add(lds_addr(&s_cnt[n]), 1 << 16);
     }
   };
   // Queries of this wave as owner bits.
@@ -731,7 +734,7 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   uint64_t om = 0, msk = 0;
   int land = 0, old = 0, cur = 0;
   if (nsteps > 0 && lane == 0)
-    step_read(lds_addr(&s_own[0]), lds_addr(&s_mask[0]), lds_addr(&s_land[0]), om, msk, land);
+    step_read(lds_addr(&s_own[0]), lds_addr(&s_mask[0]), lds_addr(&s_cnt[0]), om, msk, land);
   for (int st = 0; st < nsteps; ++st) {
     om = uniform_u64(om);
     msk = uniform_u64(msk);
@@ -739,13 +742,14 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
     // A wave with no work here helps only when the oldest unclaimed chunk
     // (cursor, read with the step words) is needed within a few steps.
     const bool helpful = __builtin_amdgcn_readfirstlane(cur) < st + MRSA_SEL_IDLE_HELP;
-    if (mine ? __builtin_amdgcn_readfirstlane(land) < kPortions : helpful) {
+    if (mine ? ((__builtin_amdgcn_readfirstlane(land) >> 16) & 0xff) < kPortions : helpful) {
       // Idle: fetch what can be fetched; with work at this step, also wait
       // until its chunk has landed.
       for (int spins = 0; spins < kSpinLimit; ++spins) {
         help(st + R);
         if (!mine ||
-            __builtin_amdgcn_readfirstlane(lds_load_flag(lds_addr(&s_land[st]))) >= kPortions)
+            ((__builtin_amdgcn_readfirstlane(lds_load_flag(lds_addr(&s_cnt[st]))) >> 16) & 0xff) >=
+                kPortions)
           break;
         __builtin_amdgcn_s_sleep(1);
       }
@@ -762,8 +766,8 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
     asm volatile("" ::: "memory");
     const int nx = min(st + 1, nsteps - 1);
     if (lane == 0)
-      step_exchange(lds_addr(&s_done[st]), lds_addr(&s_own[nx]), lds_addr(&s_mask[nx]),
-                    lds_addr(&s_land[nx]), lds_addr(cursor), old, om, msk, land, cur);
+      step_exchange(lds_addr(&s_cnt[st]), lds_addr(&s_own[nx]), lds_addr(&s_mask[nx]),
+                    lds_addr(&s_cnt[nx]), lds_addr(cursor), old, om, msk, land, cur);
   }
 
   if constexpr (!TOKEN) {
@@ -809,9 +813,9 @@ int launch_selected(SelArgs& a, hipStream_t s) {
       MRSA_SEL_WAVES == 16, Split<16, 1>,
       std::conditional_t<MRSA_SEL_WAVES == 12, Split12,
                          std::conditional_t<MRSA_SEL_WAVES == 82, Split8x2, Split8>>>;
-  const SelLayout l4 = sel_layout(SP::kTQ, SP::kWaves, a.K, a.Ck, 4, TOKEN);
+  const SelLayout l4 = sel_layout(SP::kTQ, SP::kWaves, a.K, a.Ck, 4, TOKEN, a.Lq);
   if (sel_layout_fits(l4, 4)) return launch_variant<TOKEN, 4, SP>(a, l4, s);
-  const SelLayout l3 = sel_layout(SP::kTQ, SP::kWaves, a.K, a.Ck, 3, TOKEN);
+  const SelLayout l3 = sel_layout(SP::kTQ, SP::kWaves, a.K, a.Ck, 3, TOKEN, a.Lq);
   if (sel_layout_fits(l3, 3)) return launch_variant<TOKEN, 3, SP>(a, l3, s);
   return MRSA_ERR_UNSUPPORTED;
 }
