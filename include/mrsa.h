@@ -215,6 +215,26 @@ int mrsa_selected_attention_fwd(const void* q, const void* k, const void* v_tile
                                 int mask_last_token, float sm_scale, void* out, void* stream);
 
 /*
+ * The same routed chunk attention for short query blocks, the shape of the
+ * Fast-dLLM cached block step (selected_attention_g7_cached called at
+ * dream_dllm_hils/fastdllm_attention.py:363): each (query tile, KV head)
+ * walk is split over `parts` workgroups, which write fp32 partial outputs
+ * that a second kernel sums into `out`.  Arguments as
+ * mrsa_selected_attention_fwd, plus:
+ *   parts: 1..64 (1: exactly mrsa_selected_attention_fwd; partial unused)
+ *   partial: fp32 workspace of parts * batch * q_len * q_heads * 128 floats,
+ *            16-byte aligned, provided by the caller (no allocation here)
+ * batch * parts must not exceed 65535.
+ */
+int mrsa_selected_attention_split_fwd(const void* q, const void* k, const void* v_tiles,
+                                      const void* weights, const int32_t* indices,
+                                      const uint8_t* key_valid, int64_t batch, int64_t q_len,
+                                      int64_t kv_len, int64_t q_heads, int64_t kv_heads,
+                                      int64_t head_dim, int64_t topk, int64_t chunk_size,
+                                      int mask_last_token, float sm_scale, int64_t parts,
+                                      float* partial, void* out, void* stream);
+
+/*
  * Per-token candidate scores inside routed chunks: max over the query group of
  * q.k * sm_scale; -inf for the landmark slot, invalid keys and -1 chunks.
  * Replaces candidate_token_scores_gqa (ops/hils_token_score_gqa_tilelang.py:174-208).

@@ -47,6 +47,7 @@ namespace {
 constexpr int kSlotBytes = 32768;       // one chunk: K (16 KB) + V^T (16 KB)
 constexpr int kMaxTopk = 64;
 constexpr size_t kMaxLds = 160 * 1024;
+constexpr int64_t kMaxParts = 64;       // walk split limit
 constexpr int kSpinLimit = 1 << 16;     // bound on every wait for a ring slot (~4M clocks)
 #ifndef MRSA_SEL_INTERLEAVE
 #define MRSA_SEL_INTERLEAVE 1           // query pairs dealt round-robin over the waves
@@ -95,13 +96,18 @@ struct SelArgs {
   int token_mode;
   uint16_t* out;
   float* tscores;
+  // Walk split: `parts` workgroups share each (query tile, KV head), each
+  // taking an equal share of the walk's steps and writing fp32 partial
+  // outputs [parts][B][Lq][Hq][128] to `partial` (parts == 1: bf16 `out`).
+  int parts;
+  float* partial;
 };
 
 // LDS carve-up (byte offsets, 16-aligned).  The p_* arrays are only used by
 // the prologue and live inside the ring, which is free until the first DMA.
 struct SelLayout {
-  size_t ring, wr, s_chunk, s_own, s_mask, s_cnt, comp_slot, misc, total;
-  size_t p_idx, p_kv, p_omask, p_len, p_w, p_end;
+  size_t ring, wr, s_chunk, s_own, s_mask, s_cnt, comp_slot, misc, s_rank, total;
+  size_t p_idx, p_omask, p_len, p_w, p_end;
   int cap;
 };
 __host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
@@ -123,10 +129,10 @@ __host__ __device__ inline SelLayout sel_layout(int TQ, int NW, int K, int64_t C
   l.s_cnt = o;     o = align16(o + (size_t)l.cap * 4);
   l.comp_slot = o; o = align16(o + n);
   l.misc = o;      o = align16(o + (size_t)(NW + 8) * 4);
+  l.s_rank = o;    o = align16(o + (size_t)TQ * 4);         // [TQ] first list rank
   l.total = o;
   o = l.ring;
   l.p_idx = o;     o = align16(o + n * 4);
-  l.p_kv = o;      o = align16(o + (size_t)Ck * 8);
   l.p_omask = o;   o = align16(o + (size_t)Ck * 8);
   l.p_len = o;     o = align16(o + (size_t)TQ * 4);
   l.p_w = o;       o = align16(o + wbytes);                 // [TQ][8][K] bf16, slot order
@@ -260,22 +266,45 @@ struct WalkLds {
   uint64_t* s_own;      // [cap] owner bits (query i of the tile -> bit i)
   uint64_t* s_mask;     // [cap] excluded-key bits (invalid keys, landmark slot)
   uint8_t* comp_slot;   // [TQ][K] list position -> original slot
-  int32_t* misc;        // [waves] scan, [waves] step count
+  int32_t* misc;        // [waves] scan, [waves] step count, first chunk
+  int32_t* s_rank;      // [TQ] list rank of each query at the first step
   int32_t* p_idx;       // [TQ][K] staged / compacted index rows (scratch)
-  uint8_t* p_kv;        // [Ck][8] key-valid bits (scratch)
   uint64_t* p_omask;    // [Ck] owner bits by chunk (scratch)
   int32_t* p_len;       // [TQ] list lengths (scratch)
 };
 
+// Excluded-key bits of one 64-key chunk from its 64 key-valid bytes (bit j
+// set: key j invalid).
+__device__ __forceinline__ uint64_t invalid_key_bits(const uint8_t* kv, bool al16) {
+  uint64_t m = 0;
+  if (al16) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const u32x4_t x = *reinterpret_cast<const u32x4_t*>(kv + 16 * v);
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          m |= ((x[w] >> (8 * j)) & 0xffu) ? 0ull : 1ull << (16 * v + 4 * w + j);
+    }
+  } else {
+    for (int j = 0; j < 64; ++j) m |= kv[j] ? 0ull : 1ull << j;
+  }
+  return m;
+}
+
 // Prologue shared by both routed-attention kernels: stages the tile's index
-// rows, weights and key-valid bits, compacts each query's list the way the
-// reference kernel reads it (stop at the first negative entry, skip >= Ck,
-// sort, merge duplicates by summing weights), builds the ascending walk over
-// the union of the tile's chunks, and (attention mode) the weights in list
-// order.  Returns the number of walk steps.  Ends with a workgroup barrier.
+// rows and weights, compacts each query's list the way the reference kernel
+// reads it (stop at the first negative entry, skip >= Ck, sort, merge
+// duplicates by summing weights), builds the ascending walk over the union of
+// the tile's chunks with their excluded keys, and (attention mode) the
+// weights in list order.  With the walk split over a.parts workgroups, part
+// `part` keeps steps [total * part / parts, total * (part + 1) / parts) and
+// each query's list rank at its first kept step (W.s_rank).  Returns the
+// number of kept steps.  Ends with a workgroup barrier.
 template <bool TOKEN, class SP>
 __device__ int build_walk(const SelArgs& a, const WalkLds& W, int64_t b, int h, int64_t q0,
-                          int64_t nq) {
+                          int64_t nq, int part) {
   constexpr int kWaves = SP::kWaves, kThreads = SP::kThreads, kTQ = SP::kTQ;
   const int K = a.K;
   const int64_t Ck = a.Ck;
@@ -290,13 +319,11 @@ __device__ int build_walk(const SelArgs& a, const WalkLds& W, int64_t b, int h, 
   uint8_t* comp_slot = W.comp_slot;
   int32_t* misc = W.misc;
   int32_t* p_idx = W.p_idx;
-  uint8_t* p_kv = W.p_kv;
   uint64_t* p_omask = W.p_omask;
   int32_t* p_len = W.p_len;
 
-  // 1. Stage the tile's index rows (-1 past the end of the sequence), routing
-  //    weights ([TQ][8][K], head columns >= G zero) and key-valid bits
-  //    (one byte of 8 bits per 8 keys).
+  // 1. Stage the tile's index rows (-1 past the end of the sequence) and
+  //    routing weights ([TQ][8][K], head columns >= G zero).
   for (int e = tid; e < kTQ * K; e += kThreads) {
     const int qq = e / K, kk = e - qq * K;
     p_idx[e] = qq < nq ? a.idx[((b * a.Lq + q0 + qq) * a.Hkv + h) * K + kk] : -1;
@@ -320,22 +347,6 @@ __device__ int build_walk(const SelArgs& a, const WalkLds& W, int64_t b, int h, 
         const int qq = row >> 3, gg = row & 7;
         wts[e] = (qq < nq && gg < G) ? wrow0[qq * qstride + gg * K + kk] : (uint16_t)0;
       }
-    }
-  }
-  if (a.key_valid) {
-    const uint8_t* kv = a.key_valid + b * a.Lk;
-    const bool al8 = ((uintptr_t)kv & 7) == 0;
-    for (int64_t e = tid; e < Ck * 8; e += kThreads) {
-      uint32_t m = 0;
-      if (al8) {
-        const uint64_t x = *reinterpret_cast<const uint64_t*>(kv + 8 * e);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) m |= ((x >> (8 * j)) & 0xffull) ? (1u << j) : 0u;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) m |= kv[8 * e + j] ? (1u << j) : 0u;
-      }
-      p_kv[e] = (uint8_t)m;
     }
   }
   for (int64_t c = tid; c < Ck; c += kThreads) p_omask[c] = 0ull;
@@ -408,7 +419,8 @@ __device__ int build_walk(const SelArgs& a, const WalkLds& W, int64_t b, int h, 
   __syncthreads();
 
   // 3. Walk list: the chunks with at least one owner, ascending, with their
-  //    owner bits and excluded-key bits (invalid keys, the landmark slot).
+  //    owner bits and excluded-key bits (invalid keys, the landmark slot);
+  //    this part's share of it.
   {
     const uint64_t last_mask = a.mask_last ? (1ull << 63) : 0ull;
     const int64_t per = (Ck + kThreads - 1) / kThreads;
@@ -430,19 +442,40 @@ __device__ int build_walk(const SelArgs& a, const WalkLds& W, int64_t b, int h, 
       pos += w < wave ? x : 0;
       total += x;
     }
+    const int st_lo = (int)((int64_t)part * total / a.parts);
+    const int st_hi = (int)((int64_t)(part + 1) * total / a.parts);
+    const uint8_t* kv = a.key_valid ? a.key_valid + b * a.Lk : nullptr;
+    const bool al16 = ((uintptr_t)kv & 15) == 0;
     for (int64_t c = c0; c < c1; ++c) {
       const uint64_t m = p_omask[c];
       if (m) {
-        const uint64_t kvb = a.key_valid ? *reinterpret_cast<const uint64_t*>(p_kv + 8 * c) : ~0ull;
-        s_chunk[pos] = (int32_t)c;
-        s_own[pos] = m;
-        s_mask[pos] = ~kvb | last_mask;
+        if (pos >= st_lo && pos < st_hi) {
+          const uint64_t bad = kv ? invalid_key_bits(kv + 64 * c, al16) : 0ull;
+          s_chunk[pos - st_lo] = (int32_t)c;
+          s_own[pos - st_lo] = m;
+          s_mask[pos - st_lo] = bad | last_mask;
+          if (pos == st_lo) misc[kWaves + 1] = (int32_t)c;
+        }
         ++pos;
       }
     }
-    if (tid == 0) misc[kWaves] = total;
+    if (tid == 0) misc[kWaves] = st_hi - st_lo;
   }
   __syncthreads();
+  if (a.parts > 1) {
+    // Rank of the first kept step in each query's list: its listed chunks
+    // below that step's chunk (lists are ascending and duplicate-free).
+    const int nkept = misc[kWaves];
+    const int32_t c_lo = nkept > 0 ? misc[kWaves + 1] : (int32_t)Ck;
+    if (tid < kTQ) {
+      const int32_t* ci = p_idx + tid * K;
+      const int n = p_len[tid];
+      int r = 0;
+      for (int i = 0; i < n; ++i) r += ci[i] < c_lo ? 1 : 0;
+      W.s_rank[tid] = r;
+    }
+    __syncthreads();
+  }
   return misc[kWaves];
 }
 
@@ -473,8 +506,8 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   // wave.
   int32_t* s_cnt = reinterpret_cast<int32_t*>(smem + lay.s_cnt);         // [cap]
   int32_t* cursor = misc + kWaves + 4;  // oldest chunk with unclaimed portions
+  int32_t* s_rank = reinterpret_cast<int32_t*>(smem + lay.s_rank);      // [TQ]
   int32_t* p_idx = reinterpret_cast<int32_t*>(smem + lay.p_idx);        // [TQ][K]
-  uint8_t* p_kv = smem + lay.p_kv;                                      // [Ck][8] key-valid bytes
   uint64_t* p_omask = reinterpret_cast<uint64_t*>(smem + lay.p_omask);  // [Ck]
   int32_t* p_len = reinterpret_cast<int32_t*>(smem + lay.p_len);        // [TQ]
 
@@ -483,7 +516,8 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   // decisions (tile ownership, DMA duty) are scalar branches.
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
-  const int64_t b = blockIdx.z;
+  const int64_t b = blockIdx.z % a.B;
+  const int part = (int)(blockIdx.z / a.B);
   const int h = blockIdx.y;
   const int64_t q0 = (int64_t)blockIdx.x * kTQ;
   const int G = a.G;
@@ -493,8 +527,8 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   if (tid == 0) *cursor = 0;
   for (int i = tid; i < lay.cap; i += kThreads) s_cnt[i] = 0;
   const int nsteps = build_walk<TOKEN, SP>(
-      a, WalkLds{wr, wts, s_chunk, s_own, s_mask, comp_slot, misc, p_idx, p_kv, p_omask, p_len}, b, h,
-      q0, nq);
+      a, WalkLds{wr, wts, s_chunk, s_own, s_mask, comp_slot, misc, s_rank, p_idx, p_omask, p_len},
+      b, h, q0, nq, part);
 
   // 4. Q^T operands and accumulators of this wave's queries.
   //    Column tile nt of wave w holds query pair qpair(w, nt), i.e. queries
@@ -509,7 +543,7 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   for (int nt = 0; nt < kNtile; ++nt) {
     const int ql = 2 * qpair(nt) + (col >> 3);
     const int gg = col & 7;
-    rank[nt] = 0;
+    rank[nt] = a.parts > 1 ? s_rank[ql] : 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       u32x4_t z = {0u, 0u, 0u, 0u};
@@ -775,7 +809,15 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
     for (int nt = 0; nt < kNtile; ++nt) {
       const int ql = 2 * qpair(nt) + half;
       if (ql >= nq || gg >= G) continue;
-      uint16_t* orow = a.out + ((b * a.Lq + q0 + ql) * a.Hq + h * G + gg) * 128;
+      const int64_t row = (b * a.Lq + q0 + ql) * a.Hq + h * G + gg;
+      if (a.parts > 1) {
+        float* prow = a.partial + ((int64_t)part * a.B * a.Lq * a.Hq + row) * 128;
+#pragma unroll
+        for (int td = 0; td < 8; ++td)
+          *reinterpret_cast<f32x4_t*>(prow + 16 * td + 4 * grp) = acc[nt][td];
+        continue;
+      }
+      uint16_t* orow = a.out + row * 128;
 #pragma unroll
       for (int td = 0; td < 8; ++td) {
         u32x2_t o;
@@ -784,6 +826,25 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
         *reinterpret_cast<u32x2_t*>(orow + 16 * td + 4 * grp) = o;
       }
     }
+  }
+}
+
+// Sum of the walk parts' fp32 partial outputs, rounded to bf16 once.
+__global__ void __launch_bounds__(256) sum_parts_kernel(const float* __restrict__ partial,
+                                                        int parts, int64_t n4,
+                                                        uint16_t* __restrict__ out) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n4; e += stride) {
+    f32x4_t s = reinterpret_cast<const f32x4_t*>(partial)[e];
+    for (int p = 1; p < parts; ++p) {
+      const f32x4_t x = reinterpret_cast<const f32x4_t*>(partial)[(int64_t)p * n4 + e];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[i] += x[i];
+    }
+    u32x2_t o;
+    o[0] = pack_bf16x2(s[0], s[1]);
+    o[1] = pack_bf16x2(s[2], s[3]);
+    reinterpret_cast<u32x2_t*>(out)[e] = o;
   }
 }
 
@@ -801,7 +862,8 @@ int launch_variant(SelArgs& a, const SelLayout& lay, hipStream_t s) {
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lay.total) != hipSuccess)
     return MRSA_ERR_LAUNCH;
-  dim3 grid((unsigned)((a.Lq + SP::kTQ - 1) / SP::kTQ), (unsigned)a.Hkv, (unsigned)a.B);
+  dim3 grid((unsigned)((a.Lq + SP::kTQ - 1) / SP::kTQ), (unsigned)a.Hkv,
+            (unsigned)(a.B * a.parts));
   hipLaunchKernelGGL(kern, grid, dim3(SP::kThreads), lay.total, s, a);
   return mrsa_launch_status();
 }
@@ -873,6 +935,8 @@ extern "C" int mrsa_selected_attention_fwd(const void* q, const void* k, const v
   a.token_mode = 0;
   a.out = (uint16_t*)out;
   a.tscores = nullptr;
+  a.parts = 1;
+  a.partial = nullptr;
   return launch_selected<false>(a, (hipStream_t)stream);
 }
 
@@ -916,5 +980,60 @@ extern "C" int mrsa_candidate_token_scores_fwd(const void* q, const void* k,
   a.token_mode = 1;
   a.out = nullptr;
   a.tscores = scores;
+  a.parts = 1;
+  a.partial = nullptr;
   return launch_selected<true>(a, s);
+}
+
+extern "C" int mrsa_selected_attention_split_fwd(
+    const void* q, const void* k, const void* v_tiles, const void* weights,
+    const int32_t* indices, const uint8_t* key_valid, int64_t batch, int64_t q_len,
+    int64_t kv_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t topk,
+    int64_t chunk_size, int mask_last_token, float sm_scale, int64_t parts, float* partial,
+    void* out, void* stream) {
+  if (parts == 1)
+    return mrsa_selected_attention_fwd(q, k, v_tiles, weights, indices, key_valid, batch, q_len,
+                                       kv_len, q_heads, kv_heads, head_dim, topk, chunk_size,
+                                       mask_last_token, sm_scale, out, stream);
+  int st = check_common(q, k, indices, batch, q_len, kv_len, q_heads, kv_heads, head_dim, topk,
+                        chunk_size, sm_scale);
+  if (st != MRSA_OK) return st;
+  if (parts < 1 || parts > kMaxParts) return MRSA_ERR_INVALID_ARGUMENT;
+  if (batch * parts > 65535) return MRSA_ERR_UNSUPPORTED;
+  if (batch == 0 || q_len == 0) return MRSA_OK;
+  if (!v_tiles || !weights || !out || !partial || (uintptr_t)v_tiles % 16 != 0 ||
+      (uintptr_t)out % 8 != 0 || (uintptr_t)partial % 16 != 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  SelArgs a;
+  a.q = (const uint16_t*)q;
+  a.k = (const uint16_t*)k;
+  a.vt = (const uint16_t*)v_tiles;
+  a.w = (const uint16_t*)weights;
+  a.idx = indices;
+  a.key_valid = key_valid;
+  a.B = batch;
+  a.Lq = q_len;
+  a.Lk = kv_len;
+  a.Hq = (int)q_heads;
+  a.Hkv = (int)kv_heads;
+  a.G = (int)(q_heads / kv_heads);
+  a.K = (int)topk;
+  a.Ck = kv_len / 64;
+  a.NTk = (kv_len + 63) / 64;
+  a.mask_last = mask_last_token;
+  a.scale_log2 = sm_scale * kLog2e;
+  a.sm_scale = sm_scale;
+  a.token_mode = 0;
+  a.out = nullptr;
+  a.tscores = nullptr;
+  a.parts = (int)parts;
+  a.partial = partial;
+  hipStream_t s = (hipStream_t)stream;
+  st = launch_selected<false>(a, s);
+  if (st != MRSA_OK) return st;
+  const int64_t n4 = batch * q_len * q_heads * 128 / 4;
+  const int64_t blocks = std::min<int64_t>((n4 + 255) / 256, 4096);
+  hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)blocks), dim3(256), 0, s, partial,
+                     (int)parts, n4, (uint16_t*)out);
+  return mrsa_launch_status();
 }

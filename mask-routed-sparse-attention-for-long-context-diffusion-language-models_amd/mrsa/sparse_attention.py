@@ -31,6 +31,29 @@ def value_tiles(v: torch.Tensor) -> torch.Tensor:
     return out
 
 
+# Queries per routed-attention workgroup (12 waves x 2 column tiles x 2).
+_SEL_TILE_QUERIES = 48
+_SEL_MAX_PARTS = 64
+
+
+def walk_parts(batch: int, q_len: int, kv_heads: int, kv_len: int, topk: int,
+               chunk_size: int = 64) -> int:
+    """Workgroups per (query tile, KV head) walk of the routed attention.
+
+    Long sequences fill the chip with one workgroup per walk.  A short query
+    block (the cached block step: 32 queries, 4 KV heads -> 4 walks of up to
+    1024 chunks) splits each walk into parts of >= 16 steps so that about 512
+    workgroups run.
+    """
+
+    walks = -(-q_len // _SEL_TILE_QUERIES) * kv_heads * batch
+    if walks >= 128 or walks == 0:
+        return 1
+    steps = min(kv_len // chunk_size, min(_SEL_TILE_QUERIES, q_len) * topk)
+    parts = min(_SEL_MAX_PARTS, 512 // walks, steps // 16, 65535 // max(batch, 1))
+    return max(1, parts)
+
+
 def selected_attention_launch(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -42,26 +65,46 @@ def selected_attention_launch(
     *,
     mask_last_token: bool = True,
     sm_scale: float | None = None,
+    parts: int | None = None,
 ) -> torch.Tensor:
-    """q [B, Lq, Hq, D], k [B, Lk, Hkv, D], weights [B, Lq, Hq, K] -> [B, Lq, Hq, D] bf16."""
+    """q [B, Lq, Hq, D], k [B, Lk, Hkv, D], weights [B, Lq, Hq, K] -> [B, Lq, Hq, D] bf16.
+
+    ``parts`` splits each walk over that many workgroups (fp32 partial
+    outputs summed by a second kernel); None picks it with ``walk_parts``.
+    """
 
     B, Lq, Hq, D = q.shape
     Lk, Hkv = k.shape[1], k.shape[2]
     K = indices.shape[-1]
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
+    if parts is None:
+        parts = walk_parts(B, Lq, Hkv, Lk, K, chunk_size)
+    parts = int(parts)
+    if not 1 <= parts <= _SEL_MAX_PARTS:
+        raise ValueError(f"parts must be in [1, {_SEL_MAX_PARTS}], got {parts}")
     qc = q.contiguous()
     kc = k.contiguous()
     w = weights.to(torch.bfloat16).contiguous()
     idx = indices.to(torch.int32).contiguous()
     kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
     out = torch.empty(B, Lq, Hq, D, dtype=torch.bfloat16, device=q.device)
-    st = _lib.call(
-        "mrsa_selected_attention_fwd",
-        _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(w), _lib.ptr(idx), _lib.ptr(kv),
-        B, Lq, Lk, Hq, Hkv, D, K, int(chunk_size), 1 if mask_last_token else 0,
-        float(sm_scale), _lib.ptr(out), _lib.stream_of(qc),
-    )
+    if parts == 1:
+        st = _lib.call(
+            "mrsa_selected_attention_fwd",
+            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(w), _lib.ptr(idx),
+            _lib.ptr(kv), B, Lq, Lk, Hq, Hkv, D, K, int(chunk_size),
+            1 if mask_last_token else 0, float(sm_scale), _lib.ptr(out), _lib.stream_of(qc),
+        )
+    else:
+        partial = torch.empty(parts, B, Lq, Hq, D, dtype=torch.float32, device=q.device)
+        st = _lib.call(
+            "mrsa_selected_attention_split_fwd",
+            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(w), _lib.ptr(idx),
+            _lib.ptr(kv), B, Lq, Lk, Hq, Hkv, D, K, int(chunk_size),
+            1 if mask_last_token else 0, float(sm_scale), parts, _lib.ptr(partial),
+            _lib.ptr(out), _lib.stream_of(qc),
+        )
     _lib.check(st, "selected_attention")
     return out
 

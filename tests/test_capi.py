@@ -70,6 +70,28 @@ def test_host_side_argument_errors(lib):
                   128, 32, 32, 1, 1.0, 16, None) == 2      # chunk_size 32 unsupported
     assert L.call("mrsa_route_weights_fwd", 16, 16, 16, 16, 1, 4, 4, 4, 7, 65, 1.0, 0, 0.0,
                   0, 1.0, 16, 16, None) == 2               # topk > 64
+    # Walk split: parts outside 1..64, or a missing workspace, are rejected.
+    assert L.call("mrsa_selected_attention_split_fwd", 16, 16, 16, 16, 16, None, 1, 64, 128,
+                  28, 4, 128, 32, 64, 1, 1.0, 0, 16, 16, None) == 1
+    assert L.call("mrsa_selected_attention_split_fwd", 16, 16, 16, 16, 16, None, 1, 64, 128,
+                  28, 4, 128, 32, 64, 1, 1.0, 65, 16, 16, None) == 1
+    assert L.call("mrsa_selected_attention_split_fwd", 16, 16, 16, 16, 16, None, 1, 64, 128,
+                  28, 4, 128, 32, 64, 1, 1.0, 4, None, 16, None) == 1
+    assert L.call("mrsa_selected_attention_split_fwd", 16, 16, 16, 16, 16, None, 2000, 64,
+                  128, 28, 4, 128, 32, 64, 1, 1.0, 40, 16, 16, None) == 2  # batch * parts
     assert L.call("mrsa_value_tiles_bytes", 1, 65, 4, 128) == 1 * 4 * 2 * 128 * 64 * 2
     # Empty problems are a successful no-op.
     assert L.call("mrsa_fuse_hils_outputs_fwd", None, None, None, None, 0, 128, None) == 0
+
+
+def test_walk_parts_heuristic():
+    from mrsa.sparse_attention import walk_parts
+
+    # Long sequences: one workgroup per walk.
+    assert walk_parts(1, 16384, 4, 16384, 32) == 1
+    # The cached block step (32 queries, 4 KV heads, 2048 chunks): 64 parts.
+    assert walk_parts(1, 32, 4, 131072, 32) == 64
+    # Parts keep >= 16 steps each: 3 queries x 4 chunks -> 12 steps -> 1.
+    assert walk_parts(1, 3, 4, 131072, 4) == 1
+    assert walk_parts(1, 32, 4, 4096, 32) == 4
+    assert walk_parts(0, 32, 4, 4096, 32) == 1

@@ -277,6 +277,34 @@ def test_selected_attention_vs_oracle(Lq, Lk, K, unsorted):
     _assert_close_attn(out, ref, f"selected Lq={Lq}")
 
 
+@pytest.mark.parametrize("Lq,Lk,K,parts", [(32, 16384, 32, 7), (32, 16384, 32, 64),
+                                             (50, 4096, 16, 5), (3, 4096, 4, 40)])
+def test_selected_attention_walk_split(Lq, Lk, K, parts):
+    # The walk split over `parts` workgroups (fp32 partials summed in a second
+    # kernel) against the oracle and the unsplit kernel: unsorted rows with a
+    # duplicate chunk, -1 tails, an out-of-range id and invalid keys.  The last
+    # case has more parts than walk steps (empty parts contribute zeros).
+    _note(f"selected split Lq={Lq} Lk={Lk} K={K} parts={parts}")
+    Hkv, G, D, C = 4, 7, 128, Lk // 64
+    q = _rand((1, Lq, Hkv * G, D), 45).bfloat16()
+    k, v = _planted_kv(Lk, Hkv, D, 46)
+    idx = _sorted_routes(Lq, Hkv, K, C, 47, neg_rows=(0,))
+    perm = torch.randperm(K, generator=torch.Generator().manual_seed(48))
+    idx = idx[..., perm].contiguous()
+    idx[0, Lq - 1, :, 1] = idx[0, Lq - 1, :, 0]   # duplicate -> weights summed
+    idx[0, Lq // 2, 0, 0] = C + 3                  # out of range -> skipped
+    w = torch.softmax(_rand((1, Lq, Hkv * G, K), 49), -1).bfloat16()
+    valid = torch.rand(1, Lk, generator=torch.Generator().manual_seed(50)) > 0.03
+    args = (q.to(DEV), k.to(DEV), mrsa.value_tiles(v.to(DEV)), w.to(DEV), idx.to(DEV),
+            valid.to(DEV), 64)
+    out = selected_attention_launch(*args, parts=parts)
+    whole = selected_attention_launch(*args, parts=1)
+    ref = O.selected_attention(q, k, v, w, idx, valid, 64)
+    _assert_close_attn(out, ref, f"selected split parts={parts}")
+    # Same terms, different fp32 summation order: within one bf16 step.
+    torch.testing.assert_close(out.float(), whole.float(), atol=8e-3, rtol=8e-3)
+
+
 def test_selected_attention_reference_kat():
     # test_hils_non_power_two_topk.py:95-142 (cached and uncached shapes).
     for query_len in (35, 2048):
