@@ -129,6 +129,28 @@ int mrsa_route_topk_fwd(const void* q, const void* lmk, const float* lse_local,
                         void* scores, int scores_fp32, void* stream);
 
 /*
+ * mrsa_route_topk_fwd with a caller-provided fp32 workspace.  The same
+ * reference call sites; the decode caller is route_topk_g7 at
+ * dream_dllm_hils/fastdllm_attention.py:299-314 (32 query rows against the
+ * whole cache).  When the workspace holds mrsa_route_topk_workspace_bytes()
+ * bytes (16-byte aligned) and head_dim == 128, groups <= 8, chunks <= 4096,
+ * the logits of all rows are computed on the matrix cores into the workspace
+ * and selected by a second kernel, one workgroup per (row, KV head); other
+ * shapes (and a smaller workspace) take mrsa_route_topk_fwd's paths.  Same
+ * results either way.
+ */
+int64_t mrsa_route_topk_workspace_bytes(int64_t batch, int64_t seq_len, int64_t chunks,
+                                        int64_t kv_heads, int64_t groups);
+int mrsa_route_topk_ws_fwd(const void* q, const void* lmk, const float* lse_local,
+                           const float* bias, const int32_t* drop_mask, const uint8_t* key_valid,
+                           int64_t derive_window, int64_t batch, int64_t seq_len, int64_t chunks,
+                           int64_t kv_heads, int64_t groups, int64_t head_dim, int64_t topk,
+                           int64_t block_size, int per_head_lmk, int is_causal,
+                           int64_t window_size, int64_t q_offset, int selection_mode,
+                           float sm_scale, int32_t* indices, void* scores, int scores_fp32,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Route weights: softmax over [score_k + bias[idx_k] (k < topk), local_lse].
  * Replaces _route_weights_torch (dream_dllm_hils/attention.py:126-235; the
  * topk >= 32 path, selected at :1571-1621) and route_weights

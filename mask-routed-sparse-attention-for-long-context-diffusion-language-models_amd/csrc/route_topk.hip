@@ -22,6 +22,11 @@
 // order-preserving integer keys; exact ties at the threshold are broken by
 // chunk index.
 //
+// Short-block path (route_logits_kernel + route_select_kernel, with a caller
+// workspace): logits of few query rows against up to 4096 chunks on the
+// matrix cores, then one workgroup per (row, KV head) for LSE, scores and
+// selection with the keys in registers.
+//
 // General path (route_topk_generic_kernel): one workgroup per (token, KV head)
 // with scalar dot products; any head_dim / chunk count that fits LDS.
 #include <type_traits>
@@ -760,6 +765,335 @@ __global__ void __launch_bounds__(kGenThreads) route_topk_generic_kernel(RouteAr
   }
 }
 
+// ---------------------------------------------------------------------------
+// Short-block path: few query rows against many chunks (the cached block
+// step: 32 rows, thousands of chunks).  Two kernels over a caller-provided
+// fp32 workspace raw [B][L][Hkv][G][C] of scaled logits s = (q . lmk) * scale.
+// ---------------------------------------------------------------------------
+constexpr int kBlkQ = 32;        // query rows per logits workgroup
+constexpr int kSelThreads = 256;
+constexpr int kSelMaxPer = 16;   // chunks per selection thread -> C <= 4096
+
+// Logits: one wave per (16-chunk tile, 32-row tile, KV head, batch).  S^T
+// tiles on the matrix cores: A = 16 landmark rows, B = 16 query rows, both
+// read straight from global memory (each landmark row is used by one wave
+// only); the next head's operands are loaded while the current head's
+// products run.
+__global__ void __launch_bounds__(64) route_logits_kernel(RouteArgs a, float* __restrict__ raw) {
+  const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
+  const int64_t C = a.C, L = a.L;
+  const int G = a.G;
+  const int64_t c0 = (int64_t)blockIdx.x * 16;
+  const int64_t q0 = (int64_t)blockIdx.y * kBlkQ;
+  const int h = (int)(blockIdx.z % a.Hkv);
+  const int64_t b = blockIdx.z / a.Hkv;
+  const int64_t cl = min(c0 + col, C - 1);  // clamped: loads stay in bounds
+  const int64_t qa = q0 + col, qb = q0 + 16 + col;
+  const bool va = qa < L, vb = qb < L;
+  const uint16_t* qrow_a = a.q + ((b * L + min(qa, L - 1)) * a.Hkv + h) * (int64_t)G * 128 + 8 * grp;
+  const uint16_t* qrow_b = a.q + ((b * L + min(qb, L - 1)) * a.Hkv + h) * (int64_t)G * 128 + 8 * grp;
+  u32x4_t An[4], Ban[4], Bbn[4];
+  auto load = [&](int g) {
+    const uint16_t* kr = lmk_row(a, b, cl, h, g) + 8 * grp;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      An[j] = *reinterpret_cast<const u32x4_t*>(kr + 32 * j);
+      Ban[j] = *reinterpret_cast<const u32x4_t*>(qrow_a + g * 128 + 32 * j);
+      Bbn[j] = *reinterpret_cast<const u32x4_t*>(qrow_b + g * 128 + 32 * j);
+    }
+  };
+  load(0);
+  for (int g = 0; g < G; ++g) {
+    u32x4_t A[4], Ba[4], Bb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      A[j] = An[j];
+      Ba[j] = Ban[j];
+      Bb[j] = Bbn[j];
+    }
+    if (g + 1 < G) load(g + 1);
+    f32x4_t Sa = zero4(), Sb = zero4();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      Sa = mfma_bf16_16x16x32(A[j], Ba[j], Sa);
+      Sb = mfma_bf16_16x16x32(A[j], Bb[j], Sb);
+    }
+    // Sa[i]: chunk c0 + 4 grp + i, row qa (Sb: row qb).
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t c = c0 + 4 * grp + i;
+      if (c < C) {
+        if (va) raw[(((b * L + qa) * a.Hkv + h) * G + g) * C + c] = Sa[i] * a.sm_scale;
+        if (vb) raw[(((b * L + qb) * a.Hkv + h) * G + g) * C + c] = Sb[i] * a.sm_scale;
+      }
+    }
+  }
+}
+
+// Block-wide reduction of one value per head (G <= 8) with a single barrier.
+template <bool MAX>
+__device__ __forceinline__ void block_reduce8(float (&v)[8], int G, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    if (g >= G) break;
+    v[g] = MAX ? wave_max(v[g]) : wave_sum(v[g]);
+  }
+  if (lane == 0)
+    for (int g = 0; g < G; ++g) red[wave * 8 + g] = v[g];
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    if (g >= G) break;
+    float r = red[g];
+    for (int w = 1; w < kSelThreads / 64; ++w) r = MAX ? fmaxf(r, red[w * 8 + g]) : r + red[w * 8 + g];
+    v[g] = r;
+  }
+}
+
+// Count of this block's keys >= t (one barrier; `buf` alternates between two
+// LDS slots so a wave that runs ahead cannot overwrite counts still read).
+__device__ __forceinline__ int block_count_ge(const uint32_t (&key)[kSelMaxPer], int n, uint32_t t,
+                                              int* buf) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int cnt = 0;
+#pragma unroll
+  for (int i = 0; i < kSelMaxPer; ++i) {
+    if (i >= n) break;
+    cnt += __builtin_popcountll(__builtin_amdgcn_ballot_w64(key[i] >= t));
+  }
+  if (lane == 0) buf[wave] = cnt;
+  __syncthreads();
+  int r = 0;
+#pragma unroll
+  for (int w = 0; w < kSelThreads / 64; ++w) r += buf[w];
+  return r;
+}
+
+// Selection: one workgroup per (row, KV head, batch); chunk c = tid + 256 i.
+// Same score, LSE, drop and tie rules as the general kernel.
+__global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
+                                                                   const float* __restrict__ raw) {
+  __shared__ float redf[4 * 8];
+  __shared__ int redi[2][8];
+  __shared__ int wcnt[2][kSelMaxPer][4];
+  const int64_t C = a.C, L = a.L;
+  const int G = a.G, K = a.K;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t r = blockIdx.x;
+  const int h = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int n = (int)((C + kSelThreads - 1) / kSelThreads);  // <= kSelMaxPer
+  const int64_t row = (b * L + r) * a.Hkv + h;
+  const float* xr = raw + row * (int64_t)G * C;
+  const int64_t climit = a.is_causal ? causal_limit(a, r) : C;
+  auto xb = [&](int g, int64_t c) {  // s + bias, -inf past the causal limit
+    if (c >= climit) return neg_inf();
+    const float bv = a.bias ? a.bias[((b * C + c) * a.Hkv + h) * G + g] : 0.f;
+    return xr[(int64_t)g * C + c] + bv;
+  };
+
+  // 1. Per-head LSE over every chunk (dropped ones included).
+  float m[8], sum[8];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) m[g] = neg_inf();
+  for (int i = 0; i < n; ++i) {
+    const int64_t c = tid + (int64_t)kSelThreads * i;
+    if (c < C)
+      for (int g = 0; g < G; ++g) m[g] = fmaxf(m[g], xb(g, c));
+  }
+  block_reduce8<true>(m, G, redf);
+#pragma unroll
+  for (int g = 0; g < 8; ++g) sum[g] = 0.f;
+  for (int i = 0; i < n; ++i) {
+    const int64_t c = tid + (int64_t)kSelThreads * i;
+    if (c < C)
+      for (int g = 0; g < G; ++g)
+        if (m[g] != neg_inf()) sum[g] += expf(xb(g, c) - m[g]);
+  }
+  __syncthreads();  // redf reused
+  block_reduce8<false>(sum, G, redf);
+  float tot[8];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    if (g >= G) break;
+    const float lse_h = m[g] == neg_inf() ? m[g] : m[g] + logf(sum[g]);
+    const float lv = a.pre_softmax ? 0.f : a.lse[row * G + g];
+    tot[g] = a.pre_softmax ? 0.f : logaddexp_f(lv, lse_h);
+  }
+
+  // 2. Selection keys: max over heads of x - tot, dropped chunks -inf.
+  int64_t lc = 0, rc = -1;
+  if (a.derive_window >= 0) {
+    lc = max(r - a.derive_window, (int64_t)0) / a.block_size;
+    rc = min(r + a.derive_window, L - 1) / a.block_size;
+  }
+  const uint32_t kNeg = float_order_key(neg_inf());
+  uint32_t key[kSelMaxPer];
+  int nfin = 0;
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+  for (int i = 0; i < kSelMaxPer; ++i) {
+    key[i] = 0u;  // below every real key: never counted, never picked
+    if (i >= n) continue;
+    const int64_t c = tid + (int64_t)kSelThreads * i;
+    if (c >= C) continue;
+    float best = neg_inf();
+    for (int g = 0; g < G; ++g) {
+      const float x = xb(g, c);
+      best = fmaxf(best, x == neg_inf() ? x : x - tot[g]);
+    }
+    bool dropped = false;
+    if (a.derive_window >= 0) {
+      bool any = false;
+      if (a.key_valid) {
+        const uint8_t* kv = a.key_valid + b * L + c * a.block_size;
+        for (int64_t t = 0; t < a.block_size - 1; ++t) any |= kv[t] != 0;
+      } else {
+        any = a.block_size > 1;
+      }
+      dropped = (c >= lc && c <= rc) || !any;
+    } else if (a.drop) {
+      dropped = a.drop[(b * L + r) * C + c] != 0;
+    }
+    key[i] = float_order_key(dropped ? neg_inf() : best);
+    if (key[i] > kNeg) {
+      ++nfin;
+      kmin = min(kmin, key[i]);
+      kmax = max(kmax, key[i]);
+    }
+  }
+  {
+    int vmin = (int)(kmin ^ 0x80000000u), vmax = (int)(kmax ^ 0x80000000u);
+    for (int o = 1; o < 64; o <<= 1) {
+      vmin = min(vmin, __shfl_xor(vmin, o, 64));
+      vmax = max(vmax, __shfl_xor(vmax, o, 64));
+      nfin += __shfl_xor(nfin, o, 64);
+    }
+    if (lane == 0) {
+      wcnt[0][0][wave] = nfin;
+      wcnt[0][1][wave] = vmin;
+      wcnt[0][2][wave] = vmax;
+    }
+    __syncthreads();
+    nfin = 0;
+    for (int w = 0; w < kSelThreads / 64; ++w) {
+      nfin += wcnt[0][0][w];
+      vmin = min(vmin, wcnt[0][1][w]);
+      vmax = max(vmax, wcnt[0][2][w]);
+    }
+    kmin = (uint32_t)vmin ^ 0x80000000u;
+    kmax = (uint32_t)vmax ^ 0x80000000u;
+  }
+
+  // 3. Threshold by bisection on the keys: keys >= thr_hi are picked, plus
+  //    the `need` lowest-index chunks whose key equals thr_tie.
+  uint32_t thr_hi, thr_tie = 0u;
+  int need = 0, it = 0;
+  if (nfin <= K) {
+    thr_hi = kNeg + 1u;
+  } else {
+    uint32_t lo = kmin, hi = kmax + 1u;
+    bool exact = false;
+    thr_hi = 0u;
+    while (hi - lo > 1u) {
+      const uint32_t mid = lo + ((hi - lo) >> 1);
+      const int cnt = block_count_ge(key, n, mid, redi[it++ & 1]);
+      if (cnt == K) {
+        thr_hi = mid;
+        exact = true;
+        break;
+      }
+      if (cnt > K) lo = mid; else hi = mid;
+    }
+    if (!exact) {
+      const int cnt_hi = block_count_ge(key, n, hi, redi[it++ & 1]);
+      thr_hi = hi;
+      thr_tie = lo;
+      need = K - cnt_hi;
+    }
+  }
+
+  // 4. Slots in ascending chunk order (i major, thread minor): tie ranks
+  //    first, then pick positions, from per-wave ballot counts.
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint64_t tie_bits[kSelMaxPer];
+  __syncthreads();  // wcnt reused
+#pragma unroll
+  for (int i = 0; i < kSelMaxPer; ++i) {
+    tie_bits[i] = 0ull;
+    if (i >= n) continue;
+    tie_bits[i] = __builtin_amdgcn_ballot_w64(need > 0 && key[i] == thr_tie);
+    if (lane == 0) wcnt[0][i][wave] = __builtin_popcountll(tie_bits[i]);
+  }
+  __syncthreads();
+  bool pick[kSelMaxPer];
+  {
+    int base = 0;
+#pragma unroll
+    for (int i = 0; i < kSelMaxPer; ++i) {
+      pick[i] = false;
+      if (i >= n) continue;
+      int before = base;
+      for (int w = 0; w < kSelThreads / 64; ++w) {
+        const int x = wcnt[0][i][w];
+        before += w < wave ? x : 0;
+        base += x;
+      }
+      const bool tie = (tie_bits[i] >> lane) & 1ull;
+      const int tr = before + __builtin_popcountll(tie_bits[i] & below);
+      pick[i] = key[i] >= thr_hi || (tie && tr < need);
+      const uint64_t pb = __builtin_amdgcn_ballot_w64(pick[i]);
+      if (lane == 0) wcnt[1][i][wave] = __builtin_popcountll(pb);
+    }
+  }
+  __syncthreads();
+  int slot_base = 0;
+#pragma unroll
+  for (int i = 0; i < kSelMaxPer; ++i) {
+    if (i >= n) continue;
+    const uint64_t pb = __builtin_amdgcn_ballot_w64(pick[i]);
+    int before = slot_base;
+    for (int w = 0; w < kSelThreads / 64; ++w) {
+      const int x = wcnt[1][i][w];
+      before += w < wave ? x : 0;
+      slot_base += x;
+    }
+    if (pick[i]) {
+      const int slot = before + __builtin_popcountll(pb & below);
+      const int64_t c = tid + (int64_t)kSelThreads * i;
+      a.indices[row * K + slot] = (int32_t)c;
+      for (int g = 0; g < G; ++g) {
+        const float v = xr[(int64_t)g * C + c];
+        if (a.scores_fp32)
+          reinterpret_cast<float*>(a.scores)[(row * G + g) * K + slot] = v;
+        else
+          reinterpret_cast<uint16_t*>(a.scores)[(row * G + g) * K + slot] = (uint16_t)f32_to_bf16(v);
+      }
+    }
+  }
+  for (int t = slot_base + tid; t < K; t += kSelThreads) {
+    a.indices[row * K + t] = -1;
+    for (int g = 0; g < G; ++g) {
+      if (a.scores_fp32)
+        reinterpret_cast<float*>(a.scores)[(row * G + g) * K + t] = neg_inf();
+      else
+        reinterpret_cast<uint16_t*>(a.scores)[(row * G + g) * K + t] = 0xff80u;
+    }
+  }
+}
+
+int launch_block(const RouteArgs& a, float* raw, hipStream_t s) {
+  dim3 g1((unsigned)((a.C + 15) / 16), (unsigned)((a.L + kBlkQ - 1) / kBlkQ),
+          (unsigned)(a.Hkv * a.B));
+  hipLaunchKernelGGL(route_logits_kernel, g1, dim3(64), 0, s, a, raw);
+  int st = mrsa_launch_status();
+  if (st != MRSA_OK) return st;
+  dim3 g2((unsigned)a.L, (unsigned)a.Hkv, (unsigned)a.B);
+  hipLaunchKernelGGL(route_select_kernel, g2, dim3(kSelThreads), 0, s, a, raw);
+  return mrsa_launch_status();
+}
+
 template <int G>
 int launch_fast(const RouteArgs& a, hipStream_t s) {
   const size_t smem = FastLayout::total(a.K);
@@ -774,15 +1108,16 @@ int launch_fast(const RouteArgs& a, hipStream_t s) {
 
 }  // namespace
 
-extern "C" int mrsa_route_topk_fwd(const void* q, const void* lmk, const float* lse_local,
-                                   const float* bias, const int32_t* drop_mask,
-                                   const uint8_t* key_valid, int64_t derive_window, int64_t batch,
-                                   int64_t seq_len, int64_t chunks, int64_t kv_heads,
-                                   int64_t groups, int64_t head_dim, int64_t topk,
-                                   int64_t block_size, int per_head_lmk, int is_causal,
-                                   int64_t window_size, int64_t q_offset, int selection_mode,
-                                   float sm_scale, int32_t* indices, void* scores,
-                                   int scores_fp32, void* stream) {
+namespace {
+
+int route_topk_dispatch(const void* q, const void* lmk, const float* lse_local, const float* bias,
+                        const int32_t* drop_mask, const uint8_t* key_valid,
+                        int64_t derive_window, int64_t batch, int64_t seq_len, int64_t chunks,
+                        int64_t kv_heads, int64_t groups, int64_t head_dim, int64_t topk,
+                        int64_t block_size, int per_head_lmk, int is_causal,
+                        int64_t window_size, int64_t q_offset, int selection_mode,
+                        float sm_scale, int32_t* indices, void* scores, int scores_fp32,
+                        void* workspace, int64_t workspace_bytes, void* stream) {
   if (batch < 0 || seq_len < 0 || chunks <= 0 || kv_heads <= 0 || groups <= 0 ||
       head_dim <= 0 || topk <= 0 || block_size <= 0 || (selection_mode != 0 && selection_mode != 1))
     return MRSA_ERR_INVALID_ARGUMENT;
@@ -824,6 +1159,11 @@ extern "C" int mrsa_route_topk_fwd(const void* q, const void* lmk, const float* 
                     seq_len * kv_heads * groups * head_dim < ((int64_t)1 << 31) && chunks <= 256 && topk <= kFastMaxTopk && aligned &&
                     (groups == 7 || groups == 8);
   if (fast) return groups == 7 ? launch_fast<7>(a, s) : launch_fast<8>(a, s);
+  const bool block = workspace && head_dim == 128 && groups <= 8 && aligned &&
+                     chunks <= (int64_t)kSelThreads * kSelMaxPer && seq_len <= 0x7fffffff &&
+                     (uintptr_t)workspace % 16 == 0 &&
+                     workspace_bytes >= batch * seq_len * kv_heads * groups * chunks * 4;
+  if (block) return launch_block(a, (float*)workspace, s);
   const size_t smem = ((size_t)groups * chunks + chunks + groups * head_dim + groups + 16) * 4 +
                       kGenThreads * 4;
   if (smem > 150 * 1024) return MRSA_ERR_UNSUPPORTED;
@@ -834,4 +1174,45 @@ extern "C" int mrsa_route_topk_fwd(const void* q, const void* lmk, const float* 
   dim3 grid((unsigned)seq_len, (unsigned)kv_heads, (unsigned)batch);
   hipLaunchKernelGGL(route_topk_generic_kernel, grid, dim3(kGenThreads), smem, s, a);
   return mrsa_launch_status();
+}
+
+}  // namespace
+
+extern "C" int mrsa_route_topk_fwd(const void* q, const void* lmk, const float* lse_local,
+                                   const float* bias, const int32_t* drop_mask,
+                                   const uint8_t* key_valid, int64_t derive_window, int64_t batch,
+                                   int64_t seq_len, int64_t chunks, int64_t kv_heads,
+                                   int64_t groups, int64_t head_dim, int64_t topk,
+                                   int64_t block_size, int per_head_lmk, int is_causal,
+                                   int64_t window_size, int64_t q_offset, int selection_mode,
+                                   float sm_scale, int32_t* indices, void* scores,
+                                   int scores_fp32, void* stream) {
+  return route_topk_dispatch(q, lmk, lse_local, bias, drop_mask, key_valid, derive_window, batch,
+                             seq_len, chunks, kv_heads, groups, head_dim, topk, block_size,
+                             per_head_lmk, is_causal, window_size, q_offset, selection_mode,
+                             sm_scale, indices, scores, scores_fp32, nullptr, 0, stream);
+}
+
+extern "C" int64_t mrsa_route_topk_workspace_bytes(int64_t batch, int64_t seq_len, int64_t chunks,
+                                                   int64_t kv_heads, int64_t groups) {
+  if (batch < 0 || seq_len < 0 || chunks < 0 || kv_heads < 0 || groups < 0) return -1;
+  return batch * seq_len * kv_heads * groups * chunks * 4;
+}
+
+extern "C" int mrsa_route_topk_ws_fwd(const void* q, const void* lmk, const float* lse_local,
+                                      const float* bias, const int32_t* drop_mask,
+                                      const uint8_t* key_valid, int64_t derive_window,
+                                      int64_t batch, int64_t seq_len, int64_t chunks,
+                                      int64_t kv_heads, int64_t groups, int64_t head_dim,
+                                      int64_t topk, int64_t block_size, int per_head_lmk,
+                                      int is_causal, int64_t window_size, int64_t q_offset,
+                                      int selection_mode, float sm_scale, int32_t* indices,
+                                      void* scores, int scores_fp32, void* workspace,
+                                      int64_t workspace_bytes, void* stream) {
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace)) return MRSA_ERR_INVALID_ARGUMENT;
+  return route_topk_dispatch(q, lmk, lse_local, bias, drop_mask, key_valid, derive_window, batch,
+                             seq_len, chunks, kv_heads, groups, head_dim, topk, block_size,
+                             per_head_lmk, is_causal, window_size, q_offset, selection_mode,
+                             sm_scale, indices, scores, scores_fp32, workspace, workspace_bytes,
+                             stream);
 }

@@ -42,6 +42,12 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
          _I64, _I, _I, _I64, _I64, _I, _F, _P, _P, _I, _P],
     ),
+    "mrsa_route_topk_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
+    "mrsa_route_topk_ws_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+         _I64, _I, _I, _I64, _I64, _I, _F, _P, _P, _I, _P, _I64, _P],
+    ),
     "mrsa_route_weights_fwd": (
         _I,
         [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _F, _I, _F,

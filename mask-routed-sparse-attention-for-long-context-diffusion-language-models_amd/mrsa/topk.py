@@ -15,6 +15,20 @@ import torch
 from . import _lib
 from .kernel_utils import group_pad_to
 
+# Largest fp32 logits workspace the short-block route path may take.
+_WORKSPACE_LIMIT = 4 << 30
+
+
+def _use_block_path(B, L, C, Hkv, G, D, topk, scores_fp32, is_causal):
+    """Whether the logits-workspace path runs: the matrix-core route kernel
+    covers up to 256 chunks; beyond that, with head_dim 128, groups <= 8 and
+    chunks <= 4096, the two-kernel path over an fp32 logits workspace."""
+    fast = (not scores_fp32 and not is_causal and D == 128 and C <= 256 and topk <= 64
+            and G in (7, 8))
+    if fast or D != 128 or G > 8 or C > 4096:
+        return False
+    return B * L * Hkv * G * C * 4 <= _WORKSPACE_LIMIT
+
 
 def route_topk_launch(
     q5: torch.Tensor,
@@ -33,6 +47,7 @@ def route_topk_launch(
     selection_mode: str = "post_softmax",
     sm_scale: float | None = None,
     scores_fp32: bool = False,
+    use_workspace: bool | None = None,
 ):
     """Run the route kernel.
 
@@ -42,6 +57,8 @@ def route_topk_launch(
     drop mask of remote_drop_mask(key_valid, derive_window, block_size) is
     computed inside the kernel instead.
     Returns indices [B, L, Hkv, topk] int32 and scores [B, L, Hkv, G, topk].
+    ``use_workspace`` (None: by shape) runs the short-block path over an fp32
+    logits workspace [B, L, Hkv, G, C] where the kernel supports it.
     """
 
     if selection_mode not in {"post_softmax", "pre_softmax"}:
@@ -83,14 +100,22 @@ def route_topk_launch(
         B, L, Hkv, G, topk,
         dtype=torch.float32 if scores_fp32 else torch.bfloat16, device=q5.device,
     )
-    st = _lib.call(
-        "mrsa_route_topk_fwd",
+    args = (
         _lib.ptr(qc), _lib.ptr(lc), _lib.ptr(lse), _lib.ptr(bias), _lib.ptr(drop),
         _lib.ptr(kv), int(derive_window), B, L, C, Hkv, G, D, int(topk), int(block_size),
         per_head, 1 if is_causal else 0, int(window_size), int(q_offset),
         0 if selection_mode == "post_softmax" else 1, float(sm_scale),
-        _lib.ptr(indices), _lib.ptr(scores), 1 if scores_fp32 else 0, _lib.stream_of(qc),
+        _lib.ptr(indices), _lib.ptr(scores), 1 if scores_fp32 else 0,
     )
+    if use_workspace is None:
+        use_workspace = _use_block_path(B, L, C, Hkv, G, D, topk, scores_fp32, is_causal)
+    if use_workspace:
+        nbytes = _lib.call("mrsa_route_topk_workspace_bytes", B, L, C, Hkv, G)
+        ws = torch.empty(max(nbytes, 0) // 4, dtype=torch.float32, device=q5.device)
+        st = _lib.call("mrsa_route_topk_ws_fwd", *args, _lib.ptr(ws), int(nbytes),
+                       _lib.stream_of(qc))
+    else:
+        st = _lib.call("mrsa_route_topk_fwd", *args, _lib.stream_of(qc))
     _lib.check(st, "route_topk")
     return indices, scores
 

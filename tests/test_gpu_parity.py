@@ -133,8 +133,8 @@ def _route_case(L, C, G, Hkv, seed, derive=False, drop_frac=0.2):
     return q5, lmk, lse4, bias4, drop, valid
 
 
-def _check_route(idx_gpu, sc_gpu, q5, lmk, lse4, bias4, drop, topk, what):
-    ridx, rsc, sel = O.route_topk(q5, lmk, lse4, topk, 64, drop_mask=drop, bias4=bias4)
+def _check_route(idx_gpu, sc_gpu, q5, lmk, lse4, bias4, drop, topk, what, **opts):
+    ridx, rsc, sel = O.route_topk(q5, lmk, lse4, topk, 64, drop_mask=drop, bias4=bias4, **opts)
     gap = O.boundary_gap(sel, topk)
     near = gap < NEAR_TIE
     idx = idx_gpu.cpu().long()
@@ -159,6 +159,35 @@ def test_route_topk_vs_oracle(L, C, G, topk):
                                           bias4=bias4.to(DEV), drop_mask=drop.to(DEV))
     torch.cuda.synchronize()
     _check_route(idx, sc, q5, lmk, lse4, bias4, drop, topk, f"route L={L} C={C} G={G}")
+
+
+@pytest.mark.parametrize("L,C,G,topk,mode,causal,fp32,shared", [
+    (32, 2048, 7, 32, "post_softmax", False, False, False),   # the cached block step
+    (40, 1000, 8, 20, "pre_softmax", False, True, False),
+    (33, 700, 4, 64, "post_softmax", True, True, True),
+    (5, 4096, 7, 32, "post_softmax", False, False, False),
+])
+def test_route_topk_short_block_vs_oracle(L, C, G, topk, mode, causal, fp32, shared):
+    # The logits-workspace path (matrix-core logits, one selection workgroup
+    # per row): selection modes, the causal chunk mask with a query offset,
+    # shared landmarks, fp32 scores, and up to 4096 chunks.
+    _note(f"route short block L={L} C={C} G={G} K={topk} {mode} causal={causal}")
+    Hkv = 4
+    q5, lmk, lse4, bias4, drop, _ = _route_case(L, C, G, Hkv, 300 + L, drop_frac=0.1)
+    if shared:
+        lmk = lmk.reshape(1, C, Hkv, G, 128)[:, :, :, 0].contiguous()
+    opts = dict(selection_mode=mode, is_causal=causal, q_offset=20000 if causal else 0)
+    args = (q5.to(DEV), lmk.to(DEV), lse4.to(DEV), topk, 64)
+    kw = dict(bias4=bias4.to(DEV), drop_mask=drop.to(DEV), scores_fp32=fp32, **opts)
+    idx, sc = route_topk_launch(*args, use_workspace=True, **kw)
+    torch.cuda.synchronize()
+    _check_route(idx, sc, q5, lmk, lse4, bias4, drop, topk, f"route block L={L} C={C}", **opts)
+    if C <= 2048:  # same selection as the general kernel away from near ties
+        gidx, _ = route_topk_launch(*args, use_workspace=False, **kw)
+        _, _, sel = O.route_topk(q5, lmk, lse4, topk, 64, drop_mask=drop, bias4=bias4, **opts)
+        near = O.boundary_gap(sel, topk) < NEAR_TIE
+        differ = (idx.cpu() != gidx.cpu()).any(-1)
+        assert int((differ & ~near).sum()) == 0
 
 
 def test_route_topk_derived_drop_equals_explicit():
