@@ -269,8 +269,7 @@ def decode_main(args, torch, mrsa, dev) -> int:
 
     def step(b):
         q, rq, kb, vb, pos, aff = b
-        cache.key.index_copy_(1, pos, kb)      # cache.replace (fastdllm_cache.py)
-        cache.value.index_copy_(1, pos, vb)
+        cache.replace(pos, kb, vb)             # the block's K/V rows (fastdllm_cache.py)
         return mrsa.cached_route_attention(q, rq, cache, pos, aff, scale, cfg)
 
     for b in blocks[: max(1, args.warmup)]:

@@ -188,6 +188,17 @@ int mrsa_value_tiles(const void* v, int64_t batch, int64_t seq_len, int64_t kv_h
                      int64_t head_dim, void* v_tiles, void* stream);
 
 /*
+ * Rewrites the tiles of the given rows of v after the rows were replaced
+ * (the K/V write of a cached block step, LayerKVCache.replace at
+ * dream_dllm_hils/fastdllm_cache.py:94-125), instead of re-tiling the whole
+ * cache.  positions: int64 [count]; entries outside [0, seq_len) are ignored.
+ * v_tiles as mrsa_value_tiles.
+ */
+int mrsa_value_tiles_rows(const void* v, int64_t batch, int64_t seq_len, int64_t kv_heads,
+                          int64_t head_dim, const int64_t* positions, int64_t count,
+                          void* v_tiles, void* stream);
+
+/*
  * Bidirectional sliding-window GQA attention with natural-log LSE.
  * Replaces the flash-attn window call behind bidir_local_attention and
  * cached_local_attention (dream_dllm_hils/local_attention.py:67-200):

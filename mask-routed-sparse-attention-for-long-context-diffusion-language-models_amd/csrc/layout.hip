@@ -8,27 +8,37 @@ namespace {
 // drop[b, i, c] = chunk c overlaps the chunk-aligned window of query i, or
 // chunk c has no valid real key (or the packed-sequence mask forbids it).
 // kernel_utils.py:75-99 (bounds) and :102-161 (mask).
+constexpr int kDropRows = 8;  // output rows per workgroup (x 256 chunks)
+
 __global__ void __launch_bounds__(256)
     drop_mask_kernel(const uint8_t* __restrict__ valid, const uint8_t* __restrict__ allowed,
                      const int64_t* __restrict__ qpos, int64_t rows_total, int64_t L, int64_t W,
                      int64_t S, int32_t* __restrict__ out) {
-  extern __shared__ unsigned char chunk_ok[];
-  const int64_t b = blockIdx.y;
+  const int64_t b = blockIdx.z;
   const int64_t C = L / S;
-  for (int64_t c = threadIdx.x; c < C; c += blockDim.x) {
-    bool any = false;
-    for (int64_t s = 0; s < S - 1; ++s) any |= valid[b * L + c * S + s] != 0;
-    chunk_ok[c] = any;
+  const int64_t c = (int64_t)blockIdx.y * 256 + threadIdx.x;
+  if (c >= C) return;
+  // Chunk c has a valid real key (the last slot is its landmark).
+  const uint8_t* vc = valid + b * L + c * S;
+  bool any = false;
+  if (S % 16 == 0 && ((uintptr_t)vc & 15) == 0) {
+    u32x4_t acc = {0u, 0u, 0u, 0u};
+    for (int64_t s = 0; s < S - 16; s += 16) {
+      const u32x4_t x = *reinterpret_cast<const u32x4_t*>(vc + s);
+      acc[0] |= x[0]; acc[1] |= x[1]; acc[2] |= x[2]; acc[3] |= x[3];
+    }
+    const u32x4_t t = *reinterpret_cast<const u32x4_t*>(vc + S - 16);  // all but the last byte
+    any = (acc[0] | acc[1] | acc[2] | acc[3] | t[0] | t[1] | t[2] | (t[3] & 0x00ffffffu)) != 0u;
+  } else {
+    for (int64_t s = 0; s < S - 1; ++s) any |= vc[s] != 0;
   }
-  __syncthreads();
-  const int64_t i0 = (int64_t)blockIdx.x * 64;
-  const int64_t rows = min((int64_t)64, rows_total - i0);
-  for (int64_t e = threadIdx.x; e < rows * C; e += blockDim.x) {
-    const int64_t i = i0 + e / C, c = e % C;
+  const int64_t i0 = (int64_t)blockIdx.x * kDropRows;
+  const int64_t i1 = min(rows_total, i0 + kDropRows);
+  for (int64_t i = i0; i < i1; ++i) {
     const int64_t p = qpos ? qpos[i] : i;  // cache position of output row i
     const int64_t lc = max(p - W, (int64_t)0) / S;
     const int64_t rc = min(p + W, L - 1) / S;
-    bool drop = (c >= lc && c <= rc) || !chunk_ok[c];
+    bool drop = (c >= lc && c <= rc) || !any;
     if (allowed) drop = drop || allowed[(b * L + p) * L + c * S + S - 1] == 0;
     out[(b * rows_total + i) * C + c] = drop ? 1 : 0;
   }
@@ -42,6 +52,25 @@ __global__ void __launch_bounds__(256)
 // then 16 contiguous bytes.
 __device__ __forceinline__ int tile_key_of_pos(int p) {
   return (p & 32) | (((p >> 2) & 1) << 4) | (((p >> 3) & 3) << 2) | (p & 3);
+}
+
+__device__ __forceinline__ int tile_pos_of_key(int k) {
+  return (k & 32) | (((k >> 2) & 3) << 3) | (((k >> 4) & 1) << 2) | (k & 3);
+}
+
+// Rewrites the tiled copy of the listed rows only (rows of a cache that
+// were replaced); positions outside [0, L) are ignored.
+__global__ void __launch_bounds__(256)
+    value_tiles_rows_kernel(const uint16_t* __restrict__ v, int64_t L, int64_t H, int D,
+                            int64_t NT, const int64_t* __restrict__ positions,
+                            uint16_t* __restrict__ vt) {
+  const int64_t p = positions[blockIdx.x];
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  if (p < 0 || p >= L) return;
+  const int pos = tile_pos_of_key((int)(p & 63));
+  uint16_t* dst = vt + ((b * H + h) * NT + p / 64) * (int64_t)D * 64 + pos;
+  const uint16_t* src = v + ((b * L + p) * H + h) * D;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) dst[(int64_t)d * 64] = src[d];
 }
 
 __global__ void __launch_bounds__(256)
@@ -79,9 +108,12 @@ extern "C" int mrsa_remote_drop_mask(const uint8_t* valid_mask, const uint8_t* a
   if (batch == 0) return MRSA_OK;
   if (!valid_mask || !drop_mask) return MRSA_ERR_INVALID_ARGUMENT;
   const int64_t C = seq_len / chunk_size;
-  if (C > 60 * 1024 || batch > 65535) return MRSA_ERR_UNSUPPORTED;
-  dim3 grid((unsigned)((seq_len + 63) / 64), (unsigned)batch);
-  hipLaunchKernelGGL(drop_mask_kernel, grid, dim3(256), (size_t)C, (hipStream_t)stream, valid_mask,
+  if (C > 65535 * 256 || batch > 65535 || seq_len > ((int64_t)1 << 33))
+    return MRSA_ERR_UNSUPPORTED;
+  if (C == 0) return MRSA_OK;
+  dim3 grid((unsigned)((seq_len + kDropRows - 1) / kDropRows), (unsigned)((C + 255) / 256),
+            (unsigned)batch);
+  hipLaunchKernelGGL(drop_mask_kernel, grid, dim3(256), 0, (hipStream_t)stream, valid_mask,
                      allowed_mask, nullptr, seq_len, seq_len, window, chunk_size, drop_mask);
   return mrsa_launch_status();
 }
@@ -96,9 +128,10 @@ extern "C" int mrsa_remote_drop_mask_rows(const uint8_t* valid_mask,
   if (batch == 0 || rows == 0) return MRSA_OK;
   if (!valid_mask || !query_positions || !drop_mask) return MRSA_ERR_INVALID_ARGUMENT;
   const int64_t C = seq_len / chunk_size;
-  if (C > 60 * 1024 || batch > 65535 || rows > ((int64_t)1 << 36)) return MRSA_ERR_UNSUPPORTED;
-  dim3 grid((unsigned)((rows + 63) / 64), (unsigned)batch);
-  hipLaunchKernelGGL(drop_mask_kernel, grid, dim3(256), (size_t)C, (hipStream_t)stream, valid_mask,
+  if (C > 65535 * 256 || batch > 65535 || rows > ((int64_t)1 << 33)) return MRSA_ERR_UNSUPPORTED;
+  dim3 grid((unsigned)((rows + kDropRows - 1) / kDropRows), (unsigned)((C + 255) / 256),
+            (unsigned)batch);
+  hipLaunchKernelGGL(drop_mask_kernel, grid, dim3(256), 0, (hipStream_t)stream, valid_mask,
                      nullptr, query_positions, rows, seq_len, window, chunk_size, drop_mask);
   return mrsa_launch_status();
 }
@@ -123,5 +156,22 @@ extern "C" int mrsa_value_tiles(const void* v, int64_t batch, int64_t seq_len, i
   hipLaunchKernelGGL(value_tiles_kernel, dim3((unsigned)NT, (unsigned)kv_heads, (unsigned)batch),
                      dim3(256), smem, (hipStream_t)stream, (const uint16_t*)v, seq_len, kv_heads,
                      (int)head_dim, NT, (uint16_t*)v_tiles);
+  return mrsa_launch_status();
+}
+
+extern "C" int mrsa_value_tiles_rows(const void* v, int64_t batch, int64_t seq_len,
+                                     int64_t kv_heads, int64_t head_dim, const int64_t* positions,
+                                     int64_t count, void* v_tiles, void* stream) {
+  if (batch < 0 || seq_len < 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 ||
+      head_dim > 256 || count < 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (batch == 0 || seq_len == 0 || count == 0) return MRSA_OK;
+  if (!v || !v_tiles || !positions) return MRSA_ERR_INVALID_ARGUMENT;
+  if (kv_heads > 65535 || batch > 65535 || count > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
+  const int64_t NT = (seq_len + 63) / 64;
+  hipLaunchKernelGGL(value_tiles_rows_kernel,
+                     dim3((unsigned)count, (unsigned)kv_heads, (unsigned)batch),
+                     dim3((unsigned)head_dim), 0, (hipStream_t)stream, (const uint16_t*)v,
+                     seq_len, kv_heads, (int)head_dim, NT, positions, (uint16_t*)v_tiles);
   return mrsa_launch_status();
 }

@@ -771,16 +771,17 @@ __global__ void __launch_bounds__(kGenThreads) route_topk_generic_kernel(RouteAr
 // fp32 workspace raw [B][L][Hkv][G][C] of scaled logits s = (q . lmk) * scale.
 // ---------------------------------------------------------------------------
 constexpr int kBlkQ = 32;        // query rows per logits workgroup
-constexpr int kSelThreads = 256;
-constexpr int kSelMaxPer = 16;   // chunks per selection thread -> C <= 4096
+constexpr int kSelThreads = 512;
+constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kSelMaxPer = 8;    // chunks per selection thread -> C <= 4096
 
-// Logits: one wave per (16-chunk tile, 32-row tile, KV head, batch).  S^T
-// tiles on the matrix cores: A = 16 landmark rows, B = 16 query rows, both
-// read straight from global memory (each landmark row is used by one wave
-// only); the next head's operands are loaded while the current head's
-// products run.
-__global__ void __launch_bounds__(64) route_logits_kernel(RouteArgs a, float* __restrict__ raw) {
-  const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
+// Logits: one workgroup per (16-chunk tile, 32-row tile, KV head, batch),
+// one wave per query head g of the group.  S^T tiles on the matrix cores:
+// A = 16 landmark rows, B = 16 query rows, both read straight from global
+// memory (each landmark row is used by one wave only), all in one round trip.
+__global__ void __launch_bounds__(512) route_logits_kernel(RouteArgs a, float* __restrict__ raw) {
+  const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t C = a.C, L = a.L;
   const int G = a.G;
   const int64_t c0 = (int64_t)blockIdx.x * 16;
@@ -790,63 +791,53 @@ __global__ void __launch_bounds__(64) route_logits_kernel(RouteArgs a, float* __
   const int64_t cl = min(c0 + col, C - 1);  // clamped: loads stay in bounds
   const int64_t qa = q0 + col, qb = q0 + 16 + col;
   const bool va = qa < L, vb = qb < L;
-  const uint16_t* qrow_a = a.q + ((b * L + min(qa, L - 1)) * a.Hkv + h) * (int64_t)G * 128 + 8 * grp;
-  const uint16_t* qrow_b = a.q + ((b * L + min(qb, L - 1)) * a.Hkv + h) * (int64_t)G * 128 + 8 * grp;
-  u32x4_t An[4], Ban[4], Bbn[4];
-  auto load = [&](int g) {
-    const uint16_t* kr = lmk_row(a, b, cl, h, g) + 8 * grp;
+  const uint16_t* kr = lmk_row(a, b, cl, h, g) + 8 * grp;
+  const uint16_t* qra = a.q + (((b * L + min(qa, L - 1)) * a.Hkv + h) * G + g) * 128 + 8 * grp;
+  const uint16_t* qrb = a.q + (((b * L + min(qb, L - 1)) * a.Hkv + h) * G + g) * 128 + 8 * grp;
+  u32x4_t A[4], Ba[4], Bb[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      An[j] = *reinterpret_cast<const u32x4_t*>(kr + 32 * j);
-      Ban[j] = *reinterpret_cast<const u32x4_t*>(qrow_a + g * 128 + 32 * j);
-      Bbn[j] = *reinterpret_cast<const u32x4_t*>(qrow_b + g * 128 + 32 * j);
-    }
-  };
-  load(0);
-  for (int g = 0; g < G; ++g) {
-    u32x4_t A[4], Ba[4], Bb[4];
+  for (int j = 0; j < 4; ++j) {
+    A[j] = *reinterpret_cast<const u32x4_t*>(kr + 32 * j);
+    Ba[j] = *reinterpret_cast<const u32x4_t*>(qra + 32 * j);
+    Bb[j] = *reinterpret_cast<const u32x4_t*>(qrb + 32 * j);
+  }
+  f32x4_t Sa = zero4(), Sb = zero4();
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      A[j] = An[j];
-      Ba[j] = Ban[j];
-      Bb[j] = Bbn[j];
-    }
-    if (g + 1 < G) load(g + 1);
-    f32x4_t Sa = zero4(), Sb = zero4();
+  for (int j = 0; j < 4; ++j) {
+    Sa = mfma_bf16_16x16x32(A[j], Ba[j], Sa);
+    Sb = mfma_bf16_16x16x32(A[j], Bb[j], Sb);
+  }
+  // Sa[i]: chunk c0 + 4 grp + i, row qa (Sb: row qb).
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      Sa = mfma_bf16_16x16x32(A[j], Ba[j], Sa);
-      Sb = mfma_bf16_16x16x32(A[j], Bb[j], Sb);
-    }
-    // Sa[i]: chunk c0 + 4 grp + i, row qa (Sb: row qb).
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t c = c0 + 4 * grp + i;
-      if (c < C) {
-        if (va) raw[(((b * L + qa) * a.Hkv + h) * G + g) * C + c] = Sa[i] * a.sm_scale;
-        if (vb) raw[(((b * L + qb) * a.Hkv + h) * G + g) * C + c] = Sb[i] * a.sm_scale;
-      }
+  for (int i = 0; i < 4; ++i) {
+    const int64_t c = c0 + 4 * grp + i;
+    if (c < C) {
+      if (va) raw[(((b * L + qa) * a.Hkv + h) * G + g) * C + c] = Sa[i] * a.sm_scale;
+      if (vb) raw[(((b * L + qb) * a.Hkv + h) * G + g) * C + c] = Sb[i] * a.sm_scale;
     }
   }
 }
 
-// Block-wide reduction of one value per head (G <= 8) with a single barrier.
+// Block-wide reduction of one value per head (G <= 8) with a single barrier
+// (`red` holds kSelWaves x 8 floats and must not be read by a previous
+// reduction any more).
 template <bool MAX>
 __device__ __forceinline__ void block_reduce8(float (&v)[8], int G, float* red) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    if (g >= G) break;
-    v[g] = MAX ? wave_max(v[g]) : wave_sum(v[g]);
-  }
+  for (int g = 0; g < 8; ++g)
+    if (g < G) v[g] = MAX ? wave_max(v[g]) : wave_sum(v[g]);
   if (lane == 0)
-    for (int g = 0; g < G; ++g) red[wave * 8 + g] = v[g];
+#pragma unroll
+    for (int g = 0; g < 8; ++g)
+      if (g < G) red[wave * 8 + g] = v[g];
   __syncthreads();
 #pragma unroll
   for (int g = 0; g < 8; ++g) {
-    if (g >= G) break;
+    if (g >= G) continue;
     float r = red[g];
-    for (int w = 1; w < kSelThreads / 64; ++w) r = MAX ? fmaxf(r, red[w * 8 + g]) : r + red[w * 8 + g];
+#pragma unroll
+    for (int w = 1; w < kSelWaves; ++w) r = MAX ? fmaxf(r, red[w * 8 + g]) : r + red[w * 8 + g];
     v[g] = r;
   }
 }
@@ -858,27 +849,27 @@ __device__ __forceinline__ int block_count_ge(const uint32_t (&key)[kSelMaxPer],
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int cnt = 0;
 #pragma unroll
-  for (int i = 0; i < kSelMaxPer; ++i) {
-    if (i >= n) break;
-    cnt += __builtin_popcountll(__builtin_amdgcn_ballot_w64(key[i] >= t));
-  }
+  for (int i = 0; i < kSelMaxPer; ++i)
+    if (i < n) cnt += __builtin_popcountll(__builtin_amdgcn_ballot_w64(key[i] >= t));
   if (lane == 0) buf[wave] = cnt;
   __syncthreads();
   int r = 0;
 #pragma unroll
-  for (int w = 0; w < kSelThreads / 64; ++w) r += buf[w];
+  for (int w = 0; w < kSelWaves; ++w) r += buf[w];
   return r;
 }
 
-// Selection: one workgroup per (row, KV head, batch); chunk c = tid + 256 i.
-// Same score, LSE, drop and tie rules as the general kernel.
+// Selection: one workgroup per (row, KV head, batch); chunk c = tid + 512 i.
+// The row's logits and bias are read once into registers.  Same score, LSE,
+// drop and tie rules as the general kernel.
+template <int G>
 __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
                                                                    const float* __restrict__ raw) {
-  __shared__ float redf[4 * 8];
-  __shared__ int redi[2][8];
-  __shared__ int wcnt[2][kSelMaxPer][4];
+  __shared__ float redf[2][kSelWaves * 8];
+  __shared__ int redi[2][kSelWaves];
+  __shared__ int wcnt[2][kSelMaxPer][kSelWaves];
   const int64_t C = a.C, L = a.L;
-  const int G = a.G, K = a.K;
+  const int K = a.K;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t r = blockIdx.x;
   const int h = blockIdx.y;
@@ -887,42 +878,59 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
   const int64_t row = (b * L + r) * a.Hkv + h;
   const float* xr = raw + row * (int64_t)G * C;
   const int64_t climit = a.is_causal ? causal_limit(a, r) : C;
-  auto xb = [&](int g, int64_t c) {  // s + bias, -inf past the causal limit
-    if (c >= climit) return neg_inf();
-    const float bv = a.bias ? a.bias[((b * C + c) * a.Hkv + h) * G + g] : 0.f;
-    return xr[(int64_t)g * C + c] + bv;
-  };
 
-  // 1. Per-head LSE over every chunk (dropped ones included).
+  // 1. x = s + bias (-inf past the causal limit or the last chunk).
+  float x[kSelMaxPer][G];
+#pragma unroll
+  for (int i = 0; i < kSelMaxPer; ++i) {
+    const int64_t c = tid + (int64_t)kSelThreads * i;
+    const bool ok = i < n && c < C;
+    const int64_t cc = ok ? c : 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float v = neg_inf();
+      if (ok) {
+        v = xr[(int64_t)g * C + cc];
+        if (a.bias) v += a.bias[((b * C + cc) * a.Hkv + h) * G + g];
+      }
+      x[i][g] = v;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kSelMaxPer; ++i) {
+    const int64_t c = tid + (int64_t)kSelThreads * i;
+    if (c >= climit)
+#pragma unroll
+      for (int g = 0; g < G; ++g) x[i][g] = neg_inf();
+  }
+
+  // 2. Per-head LSE over every chunk (dropped ones included).
   float m[8], sum[8];
 #pragma unroll
-  for (int g = 0; g < 8; ++g) m[g] = neg_inf();
-  for (int i = 0; i < n; ++i) {
-    const int64_t c = tid + (int64_t)kSelThreads * i;
-    if (c < C)
-      for (int g = 0; g < G; ++g) m[g] = fmaxf(m[g], xb(g, c));
-  }
-  block_reduce8<true>(m, G, redf);
-#pragma unroll
-  for (int g = 0; g < 8; ++g) sum[g] = 0.f;
-  for (int i = 0; i < n; ++i) {
-    const int64_t c = tid + (int64_t)kSelThreads * i;
-    if (c < C)
-      for (int g = 0; g < G; ++g)
-        if (m[g] != neg_inf()) sum[g] += expf(xb(g, c) - m[g]);
-  }
-  __syncthreads();  // redf reused
-  block_reduce8<false>(sum, G, redf);
-  float tot[8];
-#pragma unroll
   for (int g = 0; g < 8; ++g) {
-    if (g >= G) break;
+    m[g] = neg_inf();
+    sum[g] = 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < kSelMaxPer; ++i)
+#pragma unroll
+    for (int g = 0; g < G; ++g) m[g] = fmaxf(m[g], x[i][g]);
+  block_reduce8<true>(m, G, redf[0]);
+#pragma unroll
+  for (int i = 0; i < kSelMaxPer; ++i)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      if (m[g] != neg_inf()) sum[g] += expf(x[i][g] - m[g]);
+  block_reduce8<false>(sum, G, redf[1]);
+  float tot[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
     const float lse_h = m[g] == neg_inf() ? m[g] : m[g] + logf(sum[g]);
     const float lv = a.pre_softmax ? 0.f : a.lse[row * G + g];
     tot[g] = a.pre_softmax ? 0.f : logaddexp_f(lv, lse_h);
   }
 
-  // 2. Selection keys: max over heads of x - tot, dropped chunks -inf.
+  // 3. Selection keys: max over heads of x - tot, dropped chunks -inf.
   int64_t lc = 0, rc = -1;
   if (a.derive_window >= 0) {
     lc = max(r - a.derive_window, (int64_t)0) / a.block_size;
@@ -935,14 +943,11 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
 #pragma unroll
   for (int i = 0; i < kSelMaxPer; ++i) {
     key[i] = 0u;  // below every real key: never counted, never picked
-    if (i >= n) continue;
     const int64_t c = tid + (int64_t)kSelThreads * i;
-    if (c >= C) continue;
+    if (i >= n || c >= C) continue;
     float best = neg_inf();
-    for (int g = 0; g < G; ++g) {
-      const float x = xb(g, c);
-      best = fmaxf(best, x == neg_inf() ? x : x - tot[g]);
-    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) best = fmaxf(best, x[i][g] == neg_inf() ? x[i][g] : x[i][g] - tot[g]);
     bool dropped = false;
     if (a.derive_window >= 0) {
       bool any = false;
@@ -977,7 +982,8 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
     }
     __syncthreads();
     nfin = 0;
-    for (int w = 0; w < kSelThreads / 64; ++w) {
+#pragma unroll
+    for (int w = 0; w < kSelWaves; ++w) {
       nfin += wcnt[0][0][w];
       vmin = min(vmin, wcnt[0][1][w]);
       vmax = max(vmax, wcnt[0][2][w]);
@@ -986,7 +992,7 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
     kmax = (uint32_t)vmax ^ 0x80000000u;
   }
 
-  // 3. Threshold by bisection on the keys: keys >= thr_hi are picked, plus
+  // 4. Threshold by bisection on the keys: keys >= thr_hi are picked, plus
   //    the `need` lowest-index chunks whose key equals thr_tie.
   uint32_t thr_hi, thr_tie = 0u;
   int need = 0, it = 0;
@@ -1014,7 +1020,7 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
     }
   }
 
-  // 4. Slots in ascending chunk order (i major, thread minor): tie ranks
+  // 5. Slots in ascending chunk order (i major, thread minor): tie ranks
   //    first, then pick positions, from per-wave ballot counts.
   const uint64_t below = (1ull << lane) - 1ull;
   uint64_t tie_bits[kSelMaxPer];
@@ -1035,10 +1041,11 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
       pick[i] = false;
       if (i >= n) continue;
       int before = base;
-      for (int w = 0; w < kSelThreads / 64; ++w) {
-        const int x = wcnt[0][i][w];
-        before += w < wave ? x : 0;
-        base += x;
+#pragma unroll
+      for (int w = 0; w < kSelWaves; ++w) {
+        const int v = wcnt[0][i][w];
+        before += w < wave ? v : 0;
+        base += v;
       }
       const bool tie = (tie_bits[i] >> lane) & 1ull;
       const int tr = before + __builtin_popcountll(tie_bits[i] & below);
@@ -1054,15 +1061,17 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
     if (i >= n) continue;
     const uint64_t pb = __builtin_amdgcn_ballot_w64(pick[i]);
     int before = slot_base;
-    for (int w = 0; w < kSelThreads / 64; ++w) {
-      const int x = wcnt[1][i][w];
-      before += w < wave ? x : 0;
-      slot_base += x;
+#pragma unroll
+    for (int w = 0; w < kSelWaves; ++w) {
+      const int v = wcnt[1][i][w];
+      before += w < wave ? v : 0;
+      slot_base += v;
     }
     if (pick[i]) {
       const int slot = before + __builtin_popcountll(pb & below);
       const int64_t c = tid + (int64_t)kSelThreads * i;
       a.indices[row * K + slot] = (int32_t)c;
+#pragma unroll
       for (int g = 0; g < G; ++g) {
         const float v = xr[(int64_t)g * C + c];
         if (a.scores_fp32)
@@ -1083,15 +1092,29 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
   }
 }
 
+template <int G>
+int launch_select(const RouteArgs& a, const float* raw, hipStream_t s) {
+  dim3 g2((unsigned)a.L, (unsigned)a.Hkv, (unsigned)a.B);
+  hipLaunchKernelGGL(route_select_kernel<G>, g2, dim3(kSelThreads), 0, s, a, raw);
+  return mrsa_launch_status();
+}
+
 int launch_block(const RouteArgs& a, float* raw, hipStream_t s) {
   dim3 g1((unsigned)((a.C + 15) / 16), (unsigned)((a.L + kBlkQ - 1) / kBlkQ),
           (unsigned)(a.Hkv * a.B));
-  hipLaunchKernelGGL(route_logits_kernel, g1, dim3(64), 0, s, a, raw);
+  hipLaunchKernelGGL(route_logits_kernel, g1, dim3(64 * a.G), 0, s, a, raw);
   int st = mrsa_launch_status();
   if (st != MRSA_OK) return st;
-  dim3 g2((unsigned)a.L, (unsigned)a.Hkv, (unsigned)a.B);
-  hipLaunchKernelGGL(route_select_kernel, g2, dim3(kSelThreads), 0, s, a, raw);
-  return mrsa_launch_status();
+  switch (a.G) {
+    case 1: return launch_select<1>(a, raw, s);
+    case 2: return launch_select<2>(a, raw, s);
+    case 3: return launch_select<3>(a, raw, s);
+    case 4: return launch_select<4>(a, raw, s);
+    case 5: return launch_select<5>(a, raw, s);
+    case 6: return launch_select<6>(a, raw, s);
+    case 7: return launch_select<7>(a, raw, s);
+    default: return launch_select<8>(a, raw, s);
+  }
 }
 
 template <int G>

@@ -55,6 +55,7 @@ SIGNATURES = {
     ),
     "mrsa_value_tiles_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "mrsa_value_tiles": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P]),
+    "mrsa_value_tiles_rows": (_I, [_P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "mrsa_local_attention_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F,

@@ -155,6 +155,15 @@ def remote_drop_mask_rows(
     rows = query_positions.numel()
     if rows and bool(((query_positions < 0) | (query_positions >= seq_len)).any()):
         raise ValueError("query_positions must be in [0, seq_len)")
+    return drop_mask_rows_launch(valid_mask, window, chunk_size, query_positions)
+
+
+def drop_mask_rows_launch(valid_mask, window, chunk_size, query_positions):
+    """remote_drop_mask_rows without the argument checks (positions already
+    validated by the caller; the kernel ignores none of them)."""
+
+    batch, seq_len = valid_mask.shape
+    rows = query_positions.numel()
     valid = valid_mask.to(torch.bool).contiguous()
     pos = query_positions.contiguous()
     out = torch.empty(batch, rows, seq_len // chunk_size, dtype=torch.int32, device=valid.device)

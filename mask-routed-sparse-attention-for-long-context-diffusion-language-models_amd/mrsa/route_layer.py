@@ -29,16 +29,16 @@ re-laid out once for both attention kernels.
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import torch
 
 from .fusion import fuse_hils_outputs
-from .kernel_utils import remote_drop_mask_rows
+from .kernel_utils import drop_mask_rows_launch
 from .local_attention import local_attention_launch
 from .pool import chunk_attn_pool_gqa_prior
 from .route_weights import route_weights_launch
-from .sparse_attention import selected_attention_launch, value_tiles
+from .sparse_attention import selected_attention_launch, value_tiles, value_tiles_rows
 from .topk import route_topk_launch
 
 
@@ -178,13 +178,55 @@ class LayerKVCache:
     """The cache fields a cached route layer reads and refreshes
     (dream_dllm_hils/fastdllm_cache.py:10-161): key, value bf16 [1, L, Hkv, D],
     key_valid bool [1, L], landmark_keys bf16 [1, C, Hkv, G, D] and prior_bias
-    fp32 [1, C, Hkv, G] (the last two refreshed in place)."""
+    fp32 [1, C, Hkv, G] (the last two refreshed in place).
+
+    ``value_tiles`` is the tiled copy of ``value`` the attention kernels read
+    (built on first use).  ``replace`` keeps it in step with the rows it
+    writes; after writing ``value`` any other way, set it to None.
+    """
 
     key: torch.Tensor
     value: torch.Tensor
     key_valid: torch.Tensor
     landmark_keys: torch.Tensor
     prior_bias: torch.Tensor
+    value_tiles: torch.Tensor | None = field(default=None, repr=False)
+
+    @property
+    def physical_length(self) -> int:
+        return int(self.key.shape[1])
+
+    def replace(self, positions: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> None:
+        """Write K/V rows at ``positions`` (fastdllm_cache.py:94-125, same checks
+        and errors; the two position checks share one device round trip)."""
+
+        positions = positions.to(device=self.key.device, dtype=torch.long)
+        if positions.ndim != 1:
+            raise ValueError("cache update positions must be one-dimensional")
+        if positions.numel():
+            srt = positions.sort().values
+            flags = torch.stack([
+                (srt[1:] == srt[:-1]).any(),
+                ((positions < 0) | (positions >= self.physical_length)).any(),
+            ]).tolist()
+            if flags[0]:
+                raise ValueError("cache update positions must be unique")
+            if flags[1]:
+                raise ValueError("cache update positions must be in range")
+        expected = (self.key.shape[0], positions.numel(), self.key.shape[2], self.key.shape[3])
+        if key.shape != expected or value.shape != expected:
+            raise ValueError(
+                f"replacement K/V shape must be {expected}, got "
+                f"{tuple(key.shape)} and {tuple(value.shape)}"
+            )
+        if key.dtype != self.key.dtype or value.dtype != self.value.dtype:
+            raise ValueError("replacement K/V dtype must match the cache")
+        if key.device != self.key.device or value.device != self.value.device:
+            raise ValueError("replacement K/V device must match the cache")
+        self.key.index_copy_(1, positions, key)
+        self.value.index_copy_(1, positions, value)
+        if self.value_tiles is not None:
+            value_tiles_rows(self.value, self.value_tiles, positions)
 
     def __post_init__(self) -> None:
         # fastdllm_cache.py:20-80 (the checks this path depends on)
@@ -202,18 +244,9 @@ class LayerKVCache:
             raise ValueError(f"landmark_keys must have shape [B,C,{hkv},G,D]")
         if self.prior_bias.shape != lm[:-1]:
             raise ValueError(f"prior_bias must have shape {tuple(lm[:-1])}")
-
-
-def _rows_for_positions(query_positions: torch.Tensor, owned_positions: torch.Tensor):
-    # fastdllm_attention.py:54-66
-    if owned_positions.numel() == 0:
-        return owned_positions
-    rows = torch.searchsorted(query_positions, owned_positions)
-    if bool((rows >= query_positions.numel()).any()) or not torch.equal(
-        query_positions.index_select(0, rows), owned_positions
-    ):
-        raise ValueError("all owned positions must also be query positions")
-    return rows
+        if self.value_tiles is not None and self.value_tiles.shape != (
+                batch, hkv, (self.key.shape[1] + 63) // 64, dim, 64):
+            raise ValueError("value_tiles must be value_tiles(value)")
 
 
 def cached_route_attention(
@@ -263,20 +296,48 @@ def cached_route_attention(
         raise ValueError(f"landmark_keys must have shape [1, {C}, {Hkv}, {G}, {D}]")
     if query_positions.shape != (Lq,) or query_positions.dtype != torch.long:
         raise ValueError(f"query_positions must be torch.long of shape {(Lq,)}")
-    if Lq and bool((query_positions[1:] <= query_positions[:-1]).any()):
-        raise ValueError("query_positions must be sorted and unique")
-    if Lq and bool(((query_positions < 0) | (query_positions >= L)).any()):
-        raise ValueError("query_positions must be in cache range")
+    if query_positions.device != q.device or affected_chunks.device != q.device:
+        raise ValueError("query_positions and affected_chunks must be on the device of q")
+    if affected_chunks.ndim != 1 or affected_chunks.dtype != torch.long:
+        raise ValueError("affected_chunks must be a 1-D torch.long tensor")
+    n = affected_chunks.numel()
+    landmark_pos = affected_chunks * S + (S - 1)
+    landmark_rows = None
+    if Lq:
+        # Every argument check that needs device values, in one round trip:
+        # sorted unique positions in range, affected chunks in range, and
+        # each affected chunk's landmark row among the query positions
+        # (fastdllm_attention.py:54-66, :84-118).
+        checks = [
+            (query_positions[1:] <= query_positions[:-1]).any(),
+            ((query_positions < 0) | (query_positions >= L)).any(),
+        ]
+        if n:
+            landmark_rows = torch.searchsorted(query_positions, landmark_pos)
+            found = query_positions[landmark_rows.clamp(max=Lq - 1)]
+            checks += [((affected_chunks < 0) | (affected_chunks >= C)).any(),
+                       ((landmark_rows >= Lq) | (found != landmark_pos)).any()]
+        flags = torch.stack(checks).tolist()
+        if flags[0]:
+            raise ValueError("query_positions must be sorted and unique")
+        if flags[1]:
+            raise ValueError("query_positions must be in cache range")
+        if n and flags[2]:
+            raise ValueError(f"affected_chunks must be in [0, {C})")
+        if n and flags[3]:
+            raise ValueError("all owned positions must also be query positions")
+    elif n:
+        raise ValueError("all owned positions must also be query positions")
 
-    vt = value_tiles(cache.value)
+    if cache.value_tiles is None:
+        cache.value_tiles = value_tiles(cache.value)
+    vt = cache.value_tiles
     flash_window = cfg.local_window + S - 1 if cfg.skip_inert_slots else cfg.local_window
     local_out, local_lse = local_attention_launch(
         q, cache.key, vt, cache.key_valid, flash_window, S if cfg.skip_inert_slots else 0,
         query_positions=query_positions,
     )
-    if affected_chunks.numel():
-        landmark_rows = _rows_for_positions(query_positions, affected_chunks * S + (S - 1))
-        n = affected_chunks.numel()
+    if n:
         q_lmk = route_q.index_select(1, landmark_rows).reshape(1, n, Hkv, G, D)
         chunk_positions = (
             affected_chunks[:, None] * S + torch.arange(S, device=q.device)[None, :]
@@ -289,7 +350,7 @@ def cached_route_attention(
         )
         cache.landmark_keys.index_copy_(1, affected_chunks, lmk.reshape(1, n, Hkv, G, D))
         cache.prior_bias.index_copy_(1, affected_chunks, prior.reshape(1, n, Hkv, G))
-    drop = remote_drop_mask_rows(cache.key_valid, cfg.local_window, S, query_positions)
+    drop = drop_mask_rows_launch(cache.key_valid, cfg.local_window, S, query_positions)
     indices, scores = route_topk_launch(
         route_q.reshape(1, Lq, Hkv, G, D),
         cache.landmark_keys.reshape(1, C, Hq, D),

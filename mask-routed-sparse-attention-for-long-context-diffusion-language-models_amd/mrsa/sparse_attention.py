@@ -54,6 +54,22 @@ def walk_parts(batch: int, q_len: int, kv_heads: int, kv_len: int, topk: int,
     return max(1, parts)
 
 
+def value_tiles_rows(v: torch.Tensor, v_tiles: torch.Tensor, positions: torch.Tensor) -> None:
+    """Rewrite the tiles of rows ``positions`` of v in ``v_tiles`` (in place),
+    after those rows of v were replaced.  Positions outside [0, L) are ignored."""
+
+    if v.device.type != "cuda" or v.dtype != torch.bfloat16 or v.ndim != 4:
+        raise ValueError("value_tiles_rows requires a CUDA BF16 [B, L, Hkv, D] tensor")
+    B, L, H, D = v.shape
+    if v_tiles.shape != (B, H, (L + 63) // 64, D, 64) or not v_tiles.is_contiguous():
+        raise ValueError("v_tiles must be the contiguous value_tiles(v) layout")
+    vc = v.contiguous()
+    pos = positions.to(device=v.device, dtype=torch.long).contiguous()
+    st = _lib.call("mrsa_value_tiles_rows", _lib.ptr(vc), B, L, H, D, _lib.ptr(pos),
+                   pos.numel(), _lib.ptr(v_tiles), _lib.stream_of(vc))
+    _lib.check(st, "value_tiles_rows")
+
+
 def selected_attention_launch(
     q: torch.Tensor,
     k: torch.Tensor,

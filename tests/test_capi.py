@@ -95,3 +95,28 @@ def test_walk_parts_heuristic():
     assert walk_parts(1, 3, 4, 131072, 4) == 1
     assert walk_parts(1, 32, 4, 4096, 32) == 4
     assert walk_parts(0, 32, 4, 4096, 32) == 1
+
+
+def test_layer_cache_replace_on_host_tensors():
+    # fastdllm_cache.py:94-125 on CPU tensors (no tiled copy yet): rows land,
+    # errors as in the reference.
+    import torch
+
+    import mrsa
+
+    k = torch.zeros(1, 256, 4, 8, dtype=torch.bfloat16)
+    v = torch.zeros_like(k)
+    cache = mrsa.LayerKVCache(k, v, torch.ones(1, 256, dtype=torch.bool),
+                              torch.zeros(1, 4, 4, 7, 8, dtype=torch.bfloat16),
+                              torch.zeros(1, 4, 4, 7))
+    pos = torch.tensor([7, 3])
+    cache.replace(pos, torch.ones(1, 2, 4, 8, dtype=torch.bfloat16),
+                  torch.full((1, 2, 4, 8), 2.0, dtype=torch.bfloat16))
+    assert float(cache.key[0, 3].float().sum()) == 32 and float(cache.value[0, 7, 0, 0]) == 2
+    assert cache.physical_length == 256
+    with pytest.raises(ValueError, match="unique"):
+        cache.replace(torch.tensor([1, 1]), k[:, :2], v[:, :2])
+    with pytest.raises(ValueError, match="range"):
+        cache.replace(torch.tensor([256]), k[:, :1], v[:, :1])
+    with pytest.raises(ValueError, match="shape"):
+        cache.replace(torch.tensor([1]), k[:, :2], v[:, :2])

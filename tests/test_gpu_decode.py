@@ -125,3 +125,73 @@ def test_cached_refresh_matches_prefill():
     error = (actual.float() - expected.float()).norm() / expected.float().norm()
     print(f"cached refresh vs prefill: rel error {float(error):.3e}", flush=True)
     assert float(error) < 0.03
+
+
+def test_value_tiles_rows_bit_exact():
+    _note("value tiles rows")
+    L, Hkv, D = 1000, 4, 128   # last tile partial
+    g = torch.Generator().manual_seed(90)
+    v = torch.randn(1, L, Hkv, D, generator=g).bfloat16().to(DEV)
+    vt = mrsa.value_tiles(v)
+    pos = torch.tensor([0, 5, 63, 64, 500, 999], device=DEV)
+    v.index_copy_(1, pos, torch.randn(1, pos.numel(), Hkv, D, generator=g).bfloat16().to(DEV))
+    mrsa.sparse_attention.value_tiles_rows(v, vt, pos)
+    assert torch.equal(vt, mrsa.value_tiles(v))
+
+
+def test_cache_replace_keeps_tiles_and_checks_arguments():
+    # LayerKVCache.replace (fastdllm_cache.py:94-125): rows written, the tiled
+    # V copy kept in step (the next cached step equals one on a fresh cache),
+    # duplicate / out-of-range positions rejected.
+    _note("cache replace")
+    L, Hq, Hkv, D, S = 2048, 28, 4, 128, 64
+    q, rq, k, v = _cache_inputs(L, Hq, Hkv, D, 91)
+    valid = torch.ones(1, L, dtype=torch.bool, device=DEV)
+    scale = torch.ones(Hq, device=DEV)
+    g = torch.Generator().manual_seed(92)
+    lmk = torch.randn(1, L // S, Hkv, Hq // Hkv, D, generator=g).bfloat16().to(DEV)
+    prior = (torch.rand(1, L // S, Hkv, Hq // Hkv, generator=g) * 0.5).to(DEV)
+    k, v = k.to(DEV), v.to(DEV)
+    cache = mrsa.LayerKVCache(k.clone(), v.clone(), valid, lmk.clone(), prior.clone())
+    rows = torch.arange(L - 2 * S, L - S, device=DEV)
+    empty = torch.empty(0, dtype=torch.long, device=DEV)
+    qb, rqb = q[:, rows.cpu()].to(DEV), rq[:, rows.cpu()].to(DEV)
+    mrsa.cached_route_attention(qb, rqb, cache, rows, empty, scale)   # builds the tiles
+    assert cache.value_tiles is not None
+    kb = torch.randn(1, S, Hkv, D, generator=g).bfloat16().to(DEV)
+    vb = torch.randn(1, S, Hkv, D, generator=g).bfloat16().to(DEV)
+    cache.replace(rows, kb, vb)
+    got = mrsa.cached_route_attention(qb, rqb, cache, rows, empty, scale)
+    fresh = mrsa.LayerKVCache(cache.key.clone(), cache.value.clone(), valid, lmk.clone(),
+                              prior.clone())
+    want = mrsa.cached_route_attention(qb, rqb, fresh, rows, empty, scale)
+    assert torch.equal(cache.value_tiles, fresh.value_tiles)
+    assert torch.equal(got, want)
+    with pytest.raises(ValueError, match="unique"):
+        cache.replace(torch.tensor([3, 3], device=DEV), kb[:, :2], vb[:, :2])
+    with pytest.raises(ValueError, match="range"):
+        cache.replace(torch.tensor([L], device=DEV), kb[:, :1], vb[:, :1])
+
+
+def test_cached_route_attention_argument_errors():
+    _note("cached route errors")
+    L, Hq, Hkv, D, S = 1024, 28, 4, 128, 64
+    q, rq, k, v = _cache_inputs(L, Hq, Hkv, D, 93)
+    valid = torch.ones(1, L, dtype=torch.bool, device=DEV)
+    lmk = torch.zeros(1, L // S, Hkv, Hq // Hkv, D, dtype=torch.bfloat16, device=DEV)
+    prior = torch.zeros(1, L // S, Hkv, Hq // Hkv, device=DEV)
+    cache = mrsa.LayerKVCache(k.to(DEV), v.to(DEV), valid, lmk, prior)
+    scale = torch.ones(Hq, device=DEV)
+    qb, rqb = q[:, :4].to(DEV), rq[:, :4].to(DEV)
+    ok = torch.tensor([60, 61, 62, 63], device=DEV)
+    none = torch.empty(0, dtype=torch.long, device=DEV)
+    with pytest.raises(ValueError, match="sorted"):
+        mrsa.cached_route_attention(qb, rqb, cache, ok.flip(0), none, scale)
+    with pytest.raises(ValueError, match="range"):
+        mrsa.cached_route_attention(qb, rqb, cache, ok + L, none, scale)
+    with pytest.raises(ValueError, match="affected_chunks"):
+        mrsa.cached_route_attention(qb, rqb, cache, ok, torch.tensor([L // S], device=DEV), scale)
+    with pytest.raises(ValueError, match="owned positions"):
+        mrsa.cached_route_attention(qb, rqb, cache, ok, torch.tensor([1], device=DEV), scale)
+    out = mrsa.cached_route_attention(qb, rqb, cache, ok, torch.tensor([0], device=DEV), scale)
+    assert bool(torch.isfinite(out.float()).all())
