@@ -223,6 +223,25 @@ int mrsa_local_attention_fwd(const void* q, const void* k, const void* v_tiles,
                              void* stream);
 
 /*
+ * The same window attention for short query blocks (cached_local_attention,
+ * dream_dllm_hils/local_attention.py:147-200, at the cached block step):
+ * each 32-query block's key tiles are split over `parts` workgroups (1..64)
+ * whose unnormalised partial outputs and (max, sum) pairs, kept in the
+ * caller's fp32 workspace of mrsa_local_attention_workspace_bytes() bytes
+ * (16-byte aligned), a second kernel merges.  parts == 1 is
+ * mrsa_local_attention_fwd (workspace unused).  batch * parts <= 65535.
+ */
+int64_t mrsa_local_attention_workspace_bytes(int64_t batch, int64_t q_len, int64_t q_heads,
+                                             int64_t parts);
+int mrsa_local_attention_split_fwd(const void* q, const void* k, const void* v_tiles,
+                                   const uint8_t* key_valid, const int64_t* query_positions,
+                                   int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
+                                   int64_t kv_heads, int64_t head_dim, int64_t window,
+                                   int64_t inert_chunk, float sm_scale, int64_t parts,
+                                   void* workspace, int64_t workspace_bytes, void* out,
+                                   float* lse, void* stream);
+
+/*
  * Routed chunk attention: for each query head, the sum over its routed chunks
  * of weight * softmax over that chunk's keys (each chunk normalised on its
  * own), times V.  Replaces HiLS_block_M_head

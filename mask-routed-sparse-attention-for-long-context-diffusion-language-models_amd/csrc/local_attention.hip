@@ -46,6 +46,13 @@ struct LocalArgs {
   int64_t NTk;
   uint16_t* out;
   float* lse;
+  // Key split: `parts` workgroups share each query block, each taking an
+  // equal share of its key tiles and writing unnormalised fp32 partials
+  // part_o [parts][B][Lq][Hq][128] and (m, l) pairs part_ml [parts][B][Lq][Hq][2]
+  // (m in log2 units) that local_merge_kernel combines.
+  int parts;
+  float* part_o;
+  float* part_ml;
 };
 
 template <int G>
@@ -60,7 +67,8 @@ __global__ void __launch_bounds__(64 * G) local_attn_kernel(LocalArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
-  const int64_t b = blockIdx.z;
+  const int64_t b = blockIdx.z % a.B;
+  const int part = (int)(blockIdx.z / a.B);
   const int h = blockIdx.y;
   const int64_t qb = (int64_t)blockIdx.x * kQB;
   const int hq = h * G + g;
@@ -107,7 +115,13 @@ __global__ void __launch_bounds__(64 * G) local_attn_kernel(LocalArgs a) {
   const int64_t plo = pos_lo, phi = pos_hi;
   const int64_t klo = max(plo - a.W, (int64_t)0);
   const int64_t khi = min(phi + a.W, a.Lk - 1);
-  const int64_t kt0 = klo / 64, kt1 = khi / 64;
+  int64_t kt0 = klo / 64, kt1 = khi / 64;
+  if (a.parts > 1) {
+    const int64_t n = kt1 - kt0 + 1;
+    const int64_t s0 = kt0 + n * part / a.parts;
+    kt1 = kt0 + n * (part + 1) / a.parts - 1;
+    kt0 = s0;
+  }
 
   f32x4_t acc[2][8];
   float m_run[2], l_run[2];
@@ -304,6 +318,22 @@ __global__ void __launch_bounds__(64 * G) local_attn_kernel(LocalArgs a) {
     }
   }
 
+  if (a.parts > 1) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      if (!qok[nt]) continue;
+      const int64_t row = ((int64_t)part * a.B * a.Lq + b * a.Lq + qb + 16 * nt + col) * a.Hq + hq;
+      float* prow = a.part_o + row * 128;
+#pragma unroll
+      for (int td = 0; td < 8; ++td)
+        *reinterpret_cast<f32x4_t*>(prow + 16 * td + 4 * grp) = acc[nt][td];
+      if (grp == 0) {
+        a.part_ml[2 * row] = m_run[nt];
+        a.part_ml[2 * row + 1] = l_run[nt];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     if (!qok[nt]) continue;
@@ -323,21 +353,56 @@ __global__ void __launch_bounds__(64 * G) local_attn_kernel(LocalArgs a) {
   }
 }
 
+// Combines the key-split partials of one (query, head) row: with
+// M = max_p m_p, O = sum_p o_p 2^(m_p - M) / sum_p l_p 2^(m_p - M), as the
+// single-pass online softmax would have; lse = (M + log2 l) ln 2.
+__global__ void __launch_bounds__(256) local_merge_kernel(LocalArgs a, int64_t rows) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (row, 4-dim group)
+  if (e >= rows * 32) return;
+  const int64_t row = e >> 5;
+  const int d4 = (int)(e & 31);
+  float M = neg_inf();
+  for (int p = 0; p < a.parts; ++p) M = fmaxf(M, a.part_ml[2 * (p * rows + row)]);
+  const float Mu = M == neg_inf() ? 0.f : M;
+  float l = 0.f;
+  f32x4_t o = zero4();
+  for (int p = 0; p < a.parts; ++p) {
+    const int64_t pr = p * rows + row;
+    const float w = exp2_hw(a.part_ml[2 * pr] - Mu);
+    l += a.part_ml[2 * pr + 1] * w;
+    const f32x4_t x = reinterpret_cast<const f32x4_t*>(a.part_o + pr * 128)[d4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] += x[i] * w;
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  u32x2_t ob;
+  ob[0] = pack_bf16x2(o[0] * inv, o[1] * inv);
+  ob[1] = pack_bf16x2(o[2] * inv, o[3] * inv);
+  reinterpret_cast<u32x2_t*>(a.out + row * 128)[d4] = ob;
+  if (d4 == 0) a.lse[row] = l > 0.f ? (M + log2f(l)) * kLn2 : neg_inf();
+}
+
 template <int G>
 int launch_local(const LocalArgs& a, hipStream_t s) {
-  dim3 grid((unsigned)((a.Lq + kQB - 1) / kQB), (unsigned)a.Hkv, (unsigned)a.B);
+  dim3 grid((unsigned)((a.Lq + kQB - 1) / kQB), (unsigned)a.Hkv, (unsigned)(a.B * a.parts));
   hipLaunchKernelGGL(local_attn_kernel<G>, grid, dim3(64 * G), 0, s, a);
+  int st = mrsa_launch_status();
+  if (st != MRSA_OK || a.parts == 1) return st;
+  const int64_t rows = a.B * a.Lq * a.Hq;
+  hipLaunchKernelGGL(local_merge_kernel, dim3((unsigned)((rows * 32 + 255) / 256)), dim3(256), 0,
+                     s, a, rows);
   return mrsa_launch_status();
 }
 
 }  // namespace
 
-extern "C" int mrsa_local_attention_fwd(const void* q, const void* k, const void* v_tiles,
-                                        const uint8_t* key_valid, const int64_t* query_positions,
-                                        int64_t batch, int64_t q_len, int64_t kv_len,
-                                        int64_t q_heads, int64_t kv_heads, int64_t head_dim,
-                                        int64_t window, int64_t inert_chunk, float sm_scale,
-                                        void* out, float* lse, void* stream) {
+namespace {
+
+int local_attention(const void* q, const void* k, const void* v_tiles, const uint8_t* key_valid,
+                    const int64_t* query_positions, int64_t batch, int64_t q_len, int64_t kv_len,
+                    int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t window,
+                    int64_t inert_chunk, float sm_scale, int64_t parts, void* workspace,
+                    void* out, float* lse, void* stream) {
   if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 ||
       q_heads % kv_heads != 0 || head_dim <= 0 || window < 0 || inert_chunk < 0 ||
       !(sm_scale > 0.f) || sm_scale == __builtin_inff())
@@ -366,6 +431,9 @@ extern "C" int mrsa_local_attention_fwd(const void* q, const void* k, const void
   a.NTk = (kv_len + 63) / 64;
   a.out = (uint16_t*)out;
   a.lse = lse;
+  a.parts = (int)parts;
+  a.part_o = (float*)workspace;
+  a.part_ml = parts > 1 ? (float*)workspace + parts * batch * q_len * q_heads * 128 : nullptr;
   hipStream_t s = (hipStream_t)stream;
   switch (G) {
     case 1: return launch_local<1>(a, s);
@@ -375,4 +443,43 @@ extern "C" int mrsa_local_attention_fwd(const void* q, const void* k, const void
     case 8: return launch_local<8>(a, s);
     default: return MRSA_ERR_UNSUPPORTED;
   }
+}
+
+}  // namespace
+
+extern "C" int mrsa_local_attention_fwd(const void* q, const void* k, const void* v_tiles,
+                                        const uint8_t* key_valid, const int64_t* query_positions,
+                                        int64_t batch, int64_t q_len, int64_t kv_len,
+                                        int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                        int64_t window, int64_t inert_chunk, float sm_scale,
+                                        void* out, float* lse, void* stream) {
+  return local_attention(q, k, v_tiles, key_valid, query_positions, batch, q_len, kv_len,
+                         q_heads, kv_heads, head_dim, window, inert_chunk, sm_scale, 1, nullptr,
+                         out, lse, stream);
+}
+
+extern "C" int64_t mrsa_local_attention_workspace_bytes(int64_t batch, int64_t q_len,
+                                                        int64_t q_heads, int64_t parts) {
+  if (batch < 0 || q_len < 0 || q_heads < 0 || parts < 1) return -1;
+  return parts > 1 ? parts * batch * q_len * q_heads * 130 * 4 : 0;
+}
+
+extern "C" int mrsa_local_attention_split_fwd(const void* q, const void* k, const void* v_tiles,
+                                              const uint8_t* key_valid,
+                                              const int64_t* query_positions, int64_t batch,
+                                              int64_t q_len, int64_t kv_len, int64_t q_heads,
+                                              int64_t kv_heads, int64_t head_dim, int64_t window,
+                                              int64_t inert_chunk, float sm_scale, int64_t parts,
+                                              void* workspace, int64_t workspace_bytes, void* out,
+                                              float* lse, void* stream) {
+  if (parts < 1 || parts > 64) return MRSA_ERR_INVALID_ARGUMENT;
+  if (parts > 1) {
+    if (!workspace || (uintptr_t)workspace % 16 != 0 ||
+        workspace_bytes < mrsa_local_attention_workspace_bytes(batch, q_len, q_heads, parts))
+      return MRSA_ERR_INVALID_ARGUMENT;
+    if (batch * parts > 65535) return MRSA_ERR_UNSUPPORTED;
+  }
+  return local_attention(q, k, v_tiles, key_valid, query_positions, batch, q_len, kv_len,
+                         q_heads, kv_heads, head_dim, window, inert_chunk, sm_scale, parts,
+                         parts > 1 ? workspace : nullptr, out, lse, stream);
 }

@@ -61,6 +61,12 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F,
          _P, _P, _P],
     ),
+    "mrsa_local_attention_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
+    "mrsa_local_attention_split_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F,
+         _I64, _P, _I64, _P, _P, _P],
+    ),
     "mrsa_selected_attention_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,

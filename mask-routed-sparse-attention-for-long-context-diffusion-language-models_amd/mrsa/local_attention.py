@@ -43,6 +43,19 @@ def _flash_window(window: int, skip_inert_slots: bool, chunk_size: int) -> int:
     return int(window)
 
 
+def key_parts(batch: int, q_len: int, kv_heads: int, kv_len: int, flash_window: int) -> int:
+    """Workgroups per 32-query block of the window attention.  Long
+    sequences: one.  A short block (the cached block step: 32 queries, 4 KV
+    heads -> 4 workgroups over ~11 key tiles) splits its key tiles so that
+    about 64 workgroups run, at least one tile each."""
+
+    blocks = -(-q_len // 32) * kv_heads * batch
+    if blocks >= 128 or blocks == 0:
+        return 1
+    tiles = (min(q_len, kv_len) + 2 * flash_window) // 64 + 2
+    return max(1, min(64, tiles, 64 // blocks, 65535 // max(batch, 1)))
+
+
 def local_attention_launch(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -53,11 +66,18 @@ def local_attention_launch(
     *,
     query_positions: torch.Tensor | None = None,
     sm_scale: float | None = None,
+    parts: int | None = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``parts`` splits each query block's key tiles over that many
+    workgroups (merged by a second kernel); None picks it with key_parts."""
+
     B, Lq, Hq, D = q.shape
     Lk, Hkv = k.shape[1], k.shape[2]
     if sm_scale is None:
         sm_scale = D ** -0.5
+    if parts is None:
+        parts = key_parts(B, Lq, Hkv, Lk, flash_window)
+    parts = int(parts)
     qc = q.contiguous()
     kc = k.contiguous()
     kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
@@ -66,12 +86,16 @@ def local_attention_launch(
         pos = query_positions.to(device=q.device, dtype=torch.int64).contiguous()
     out = torch.empty(B, Lq, Hq, D, dtype=torch.bfloat16, device=q.device)
     lse = torch.empty(B, Lq, Hq, dtype=torch.float32, device=q.device)
-    st = _lib.call(
-        "mrsa_local_attention_fwd",
-        _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(kv), _lib.ptr(pos),
-        B, Lq, Lk, Hq, Hkv, D, int(flash_window), int(inert_chunk), float(sm_scale),
-        _lib.ptr(out), _lib.ptr(lse), _lib.stream_of(qc),
-    )
+    args = (_lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(kv), _lib.ptr(pos),
+            B, Lq, Lk, Hq, Hkv, D, int(flash_window), int(inert_chunk), float(sm_scale))
+    if parts == 1:
+        st = _lib.call("mrsa_local_attention_fwd", *args, _lib.ptr(out), _lib.ptr(lse),
+                       _lib.stream_of(qc))
+    else:
+        nbytes = _lib.call("mrsa_local_attention_workspace_bytes", B, Lq, Hq, parts)
+        ws = torch.empty(max(nbytes, 0) // 4, dtype=torch.float32, device=q.device)
+        st = _lib.call("mrsa_local_attention_split_fwd", *args, parts, _lib.ptr(ws), int(nbytes),
+                       _lib.ptr(out), _lib.ptr(lse), _lib.stream_of(qc))
     _lib.check(st, "local_attention")
     return out, lse
 

@@ -84,6 +84,16 @@ def test_host_side_argument_errors(lib):
     assert L.call("mrsa_fuse_hils_outputs_fwd", None, None, None, None, 0, 128, None) == 0
 
 
+def test_key_parts_heuristic():
+    from mrsa.local_attention import key_parts
+
+    assert key_parts(1, 16384, 4, 16384, 319) == 1
+    # Cached block step: 32 queries, window 319 -> 12 key tiles, 12 parts.
+    assert key_parts(1, 32, 4, 131072, 319) == 12
+    assert key_parts(1, 32, 4, 131072, 0) == 2
+    assert key_parts(0, 32, 4, 4096, 319) == 1
+
+
 def test_walk_parts_heuristic():
     from mrsa.sparse_attention import walk_parts
 

@@ -263,6 +263,27 @@ def test_local_attention_vs_oracle(L, W, inert, G):
     torch.testing.assert_close(lse.cpu(), rl, atol=2e-3, rtol=1e-4)
 
 
+@pytest.mark.parametrize("parts,first", [(1, 8000), (3, 8000), (12, 8160), (40, 0), (5, 100)])
+def test_local_attention_key_split(parts, first):
+    # Key tiles of each 32-query block split over `parts` workgroups and
+    # merged (cached block shape: 32 positions, window 319 with inert landmark
+    # slots, invalid keys); more parts than tiles leaves some empty.  Blocks
+    # at both sequence ends clip the window.
+    _note(f"local key split parts={parts} first={first}")
+    L, Hkv, G, D, W = 8192, 4, 7, 128, 319
+    pos = torch.arange(first, min(L, first + 32))
+    Lq = pos.numel()
+    q = _rand((1, Lq, Hkv * G, D), 33).bfloat16()
+    k, v = _planted_kv(L, Hkv, D, 34)
+    valid = torch.rand(1, L, generator=torch.Generator().manual_seed(35)) > 0.05
+    out, lse = local_attention_launch(
+        q.to(DEV), k.to(DEV), mrsa.value_tiles(v.to(DEV)), valid.to(DEV), W, 64,
+        query_positions=pos.to(DEV), parts=parts)
+    ro, rl = O.local_attention(q, k, v, valid, W, 64, query_positions=pos)
+    _assert_close_attn(out, ro, f"local split parts={parts}")
+    torch.testing.assert_close(lse.cpu(), rl, atol=2e-3, rtol=1e-4)
+
+
 def test_bidir_and_cached_local_attention_api():
     _note("local attention api")
     L = 1024
