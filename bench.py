@@ -115,6 +115,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("route", "decode"), default="route")
+    ap.add_argument("--decode-eager", action="store_true",
+                    help="decode workload without the captured step graph")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 1 GiB device copy three times (reference "
                          "dispatch for scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -267,12 +269,16 @@ def decode_main(args, torch, mrsa, dev) -> int:
             pos, lm // S,
         ))
 
+    graph_step = None if args.decode_eager else mrsa.CachedBlockStep(cache, scale, cfg, bs)
+
     def step(b):
         q, rq, kb, vb, pos, aff = b
+        if graph_step is not None:   # K/V row write + route layer, one HIP graph replay
+            return graph_step(q, rq, kb, vb, pos, aff)
         cache.replace(pos, kb, vb)             # the block's K/V rows (fastdllm_cache.py)
         return mrsa.cached_route_attention(q, rq, cache, pos, aff, scale, cfg)
 
-    for b in blocks[: max(1, args.warmup)]:
+    for b in blocks[: max(2, args.warmup)]:  # both affected-chunk counts captured
         step(b)
     torch.cuda.synchronize()
     reps = max(1, args.steps // 10)
@@ -289,7 +295,7 @@ def decode_main(args, torch, mrsa, dev) -> int:
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": reps * nb,
-        "warmup": max(1, args.warmup),
+        "warmup": max(2, args.warmup),
         "ms_per_step": ms_per_block,
         "higher_is_better": True,
         "scaling": "weak",
@@ -301,6 +307,7 @@ def decode_main(args, torch, mrsa, dev) -> int:
             "cache_len": L, "block": bs, "blocks": nb, "q_heads": HQ, "kv_heads": HKV,
             "head_dim": D, "chunk_size": S, "topk": TOPK, "local_window": WINDOW,
             "parallelism": "single-gpu",
+            "step": "eager" if args.decode_eager else "hip-graph",
         },
     }
     print(json.dumps(line), flush=True)

@@ -31,6 +31,7 @@ from .kernel_utils import (
 from .local_attention import bidir_local_attention, cached_local_attention
 from .pool import chunk_attn_pool_gqa, chunk_attn_pool_gqa_prior
 from .route_layer import (
+    CachedBlockStep,
     LayerKVCache,
     RouteLayerConfig,
     cached_route_attention,
@@ -48,6 +49,7 @@ __all__ = [
     "HiLS_block_M_head",
     "LIB_PATH",
     "MrsaLibraryError",
+    "CachedBlockStep",
     "LayerKVCache",
     "RouteLayerConfig",
     "cached_route_attention",

@@ -276,6 +276,16 @@ def cached_route_attention(
     positions.  Returns the fused output [1, Lq, Hq, D] bf16.
     """
 
+    _check_cached_args(q, route_q, cache, query_positions, affected_chunks, cfg)
+    return _cached_route_body(q, route_q, cache, query_positions, affected_chunks,
+                              entropy_bias_scale, cfg, return_intermediates)
+
+
+def _check_cached_args(q, route_q, cache, query_positions, affected_chunks, cfg,
+                       device_checks=True):
+    """cached_route_attention's argument checks; the ones that read device
+    values share one round trip (skipped with device_checks=False)."""
+
     if q.device.type != "cuda":
         raise ValueError("cached route attention requires CUDA tensors")
     for name, t in (("q", q), ("route_q", route_q)):
@@ -301,9 +311,7 @@ def cached_route_attention(
     if affected_chunks.ndim != 1 or affected_chunks.dtype != torch.long:
         raise ValueError("affected_chunks must be a 1-D torch.long tensor")
     n = affected_chunks.numel()
-    landmark_pos = affected_chunks * S + (S - 1)
-    landmark_rows = None
-    if Lq:
+    if Lq and device_checks:
         # Every argument check that needs device values, in one round trip:
         # sorted unique positions in range, affected chunks in range, and
         # each affected chunk's landmark row among the query positions
@@ -313,6 +321,7 @@ def cached_route_attention(
             ((query_positions < 0) | (query_positions >= L)).any(),
         ]
         if n:
+            landmark_pos = affected_chunks * S + (S - 1)
             landmark_rows = torch.searchsorted(query_positions, landmark_pos)
             found = query_positions[landmark_rows.clamp(max=Lq - 1)]
             checks += [((affected_chunks < 0) | (affected_chunks >= C)).any(),
@@ -329,6 +338,17 @@ def cached_route_attention(
     elif n:
         raise ValueError("all owned positions must also be query positions")
 
+
+def _cached_route_body(q, route_q, cache, query_positions, affected_chunks, entropy_bias_scale,
+                       cfg, return_intermediates=False):
+    """The cached step's launches, with no host synchronisation (arguments
+    already checked); landmark rows located on the device."""
+
+    B, Lq, Hq, D = q.shape
+    L, Hkv = cache.key.shape[1], cache.key.shape[2]
+    G, S = Hq // Hkv, cfg.chunk_size
+    C = L // S
+    n = affected_chunks.numel()
     if cache.value_tiles is None:
         cache.value_tiles = value_tiles(cache.value)
     vt = cache.value_tiles
@@ -338,6 +358,7 @@ def cached_route_attention(
         query_positions=query_positions,
     )
     if n:
+        landmark_rows = torch.searchsorted(query_positions, affected_chunks * S + (S - 1))
         q_lmk = route_q.index_select(1, landmark_rows).reshape(1, n, Hkv, G, D)
         chunk_positions = (
             affected_chunks[:, None] * S + torch.arange(S, device=q.device)[None, :]
@@ -373,3 +394,81 @@ def cached_route_attention(
         "scores": scores, "remote_weights": remote_w, "local_weight": local_w,
         "remote_output": remote_out, "drop_mask": drop,
     }
+
+
+class CachedBlockStep:
+    """One route layer's Fast-dLLM cached block step -- the block's K/V rows
+    written into the cache (LayerKVCache.replace, fastdllm_cache.py:94-125)
+    followed by cached_route_attention (fastdllm_attention.py:203-382) --
+    captured once as a HIP graph and replayed for every block.
+
+    A graph is specific to the block length (fixed here) and to the number of
+    affected chunks (one graph per count, captured on first use).  Each call
+    runs the argument checks of replace and cached_route_attention (one
+    device round trip), copies its inputs into the graph's buffers and
+    replays.  The returned tensor is the graph's output buffer, overwritten
+    by the next call with the same affected-chunk count.
+    """
+
+    def __init__(self, cache: LayerKVCache, entropy_bias_scale: torch.Tensor,
+                 cfg: RouteLayerConfig = RouteLayerConfig(), block_len: int = 32):
+        if cache.key.device.type != "cuda":
+            raise ValueError("CachedBlockStep requires a CUDA cache")
+        self.cache, self.cfg, self.block_len = cache, cfg, int(block_len)
+        dev = cache.key.device
+        _, _, hkv, dim = cache.key.shape
+        hq = hkv * cache.landmark_keys.shape[3]
+        self.scale = entropy_bias_scale.to(device=dev, dtype=torch.float32).contiguous()
+        self.q = torch.zeros(1, block_len, hq, dim, dtype=torch.bfloat16, device=dev)
+        self.route_q = torch.zeros_like(self.q)
+        self.k_rows = torch.zeros(1, block_len, hkv, dim, dtype=cache.key.dtype, device=dev)
+        self.v_rows = torch.zeros_like(self.k_rows)
+        self.positions = torch.zeros(block_len, dtype=torch.long, device=dev)
+        self._graphs = {}  # affected count -> (graph, affected buffer, output)
+        if cache.value_tiles is None:
+            cache.value_tiles = value_tiles(cache.value)
+
+    def _body(self, affected):
+        c = self.cache
+        c.key.index_copy_(1, self.positions, self.k_rows)
+        c.value.index_copy_(1, self.positions, self.v_rows)
+        value_tiles_rows(c.value, c.value_tiles, self.positions)
+        return _cached_route_body(self.q, self.route_q, c, self.positions, affected, self.scale,
+                                  self.cfg)
+
+    def __call__(self, q, route_q, k_rows, v_rows, query_positions, affected_chunks):
+        if q.shape != self.q.shape or route_q.shape != self.q.shape:
+            raise ValueError(f"q and route_q must have shape {tuple(self.q.shape)}")
+        if k_rows.shape != self.k_rows.shape or v_rows.shape != self.k_rows.shape:
+            raise ValueError(
+                f"replacement K/V shape must be {tuple(self.k_rows.shape)}, got "
+                f"{tuple(k_rows.shape)} and {tuple(v_rows.shape)}")
+        if k_rows.dtype != self.k_rows.dtype or v_rows.dtype != self.k_rows.dtype:
+            raise ValueError("replacement K/V dtype must match the cache")
+        # Sorted unique in-range query positions also make the K/V rows'
+        # positions unique and in range (replace's checks).
+        _check_cached_args(q, route_q, self.cache, query_positions, affected_chunks, self.cfg)
+        self.q.copy_(q)
+        self.route_q.copy_(route_q)
+        self.k_rows.copy_(k_rows)
+        self.v_rows.copy_(v_rows)
+        self.positions.copy_(query_positions)
+        n = affected_chunks.numel()
+        entry = self._graphs.get(n)
+        if entry is None:
+            affected = affected_chunks.clone()
+            # One eager pass first (the step is idempotent: the same rows and
+            # landmark refresh are written again by the replay), then capture.
+            side = torch.cuda.Stream(device=self.q.device)
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                self._body(affected)
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                out = self._body(affected)
+            entry = self._graphs[n] = (graph, affected, out)
+        graph, affected, out = entry
+        affected.copy_(affected_chunks)
+        graph.replay()
+        return out

@@ -195,3 +195,41 @@ def test_cached_route_attention_argument_errors():
         mrsa.cached_route_attention(qb, rqb, cache, ok, torch.tensor([1], device=DEV), scale)
     out = mrsa.cached_route_attention(qb, rqb, cache, ok, torch.tensor([0], device=DEV), scale)
     assert bool(torch.isfinite(out.float()).all())
+
+
+def test_cached_block_step_graph_replays_match_eager():
+    # CachedBlockStep (HIP graph of the K/V row write + cached route layer)
+    # against the eager replace + cached_route_attention on a twin cache,
+    # block after block: graphs for 0 and 1 affected chunks, each replayed
+    # several times with eager work and synchronisation in between; every
+    # replay's output and the caches (keys, values, tiles, landmarks) equal.
+    _note("cached block step graph")
+    L, Hq, Hkv, D, S, bs = 4096, 28, 4, 128, 64, 32
+    G = Hq // Hkv
+    g = torch.Generator().manual_seed(95)
+    k, v = _planted_kv(L, Hkv, D, 96)
+    k, v = k.to(DEV), v.to(DEV)
+    valid = torch.ones(1, L, dtype=torch.bool, device=DEV)
+    valid[0, 1000:1003] = False
+    scale = (torch.rand(Hq, generator=g) + 0.5).to(DEV)
+    lmk = torch.randn(1, L // S, Hkv, G, D, generator=g).bfloat16().to(DEV)
+    prior = (torch.rand(1, L // S, Hkv, G, generator=g) * 0.5).to(DEV)
+    twin = lambda: mrsa.LayerKVCache(k.clone(), v.clone(), valid.clone(), lmk.clone(),
+                                     prior.clone())
+    graphed, eager = twin(), twin()
+    step = mrsa.CachedBlockStep(graphed, scale, block_len=bs)
+    start = L - 8 * bs
+    for i in list(range(8)) + [1, 0]:
+        pos = torch.arange(start + i * bs, start + (i + 1) * bs, device=DEV)
+        aff = pos[(pos + 1) % S == 0] // S
+        rnd = lambda *shape: torch.randn(*shape, generator=g).bfloat16().to(DEV)
+        q, rq, kb, vb = rnd(1, bs, Hq, D), rnd(1, bs, Hq, D), rnd(1, bs, Hkv, D), rnd(1, bs, Hkv, D)
+        got = step(q, rq, kb, vb, pos, aff).clone()
+        eager.replace(pos, kb, vb)
+        want = mrsa.cached_route_attention(q, rq, eager, pos, aff, scale)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"block {i}"
+    for name in ("key", "value", "value_tiles", "landmark_keys", "prior_bias"):
+        assert torch.equal(getattr(graphed, name), getattr(eager, name)), name
+    with pytest.raises(ValueError, match="sorted"):
+        step(q, rq, kb, vb, pos.flip(0), aff)
