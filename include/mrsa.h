@@ -287,6 +287,38 @@ int mrsa_selected_attention_split_fwd(const void* q, const void* k, const void* 
                                       float* partial, void* out, void* stream);
 
 /*
+ * Routed chunk attention with the token keep mask of the remote-token
+ * refinement: HiLS_block_M_head / selected_attention_g7[_cached] called with
+ * token_keep (ops/hils_fwd_bwd_head.py:457-507, the TokenKeep[b, q, h, slot,
+ * key] == 0 exclusion; dream_dllm_hils/attention.py:1729-1769).  Arguments as
+ * mrsa_selected_attention_split_fwd (parts == 1: partial unused), plus
+ *   token_keep: int8 [batch, q_len, kv_heads, topk, chunk_size], nonzero = keep
+ * A chunk listed twice for one query counts once with the summed weights and
+ * the keep row of its first slot.
+ */
+int mrsa_selected_attention_keep_fwd(const void* q, const void* k, const void* v_tiles,
+                                     const void* weights, const int32_t* indices,
+                                     const uint8_t* key_valid, const int8_t* token_keep,
+                                     int64_t batch, int64_t q_len, int64_t kv_len,
+                                     int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                     int64_t topk, int64_t chunk_size, int mask_last_token,
+                                     float sm_scale, int64_t parts, float* partial, void* out,
+                                     void* stream);
+
+/*
+ * Global token keep: select_global_token_keep
+ * (dream_dllm_hils/token_refinement.py:112-148) without training noise.  In
+ * each of `rows` rows of n fp32 scores the min(token_budget, n) largest are
+ * kept (1) when finite, others 0; ties at the threshold go to the lower index
+ * (the reference's torch.topk(sorted=False) leaves their order to the device).
+ *   scores: fp32 [rows, n] (the [B, L, Hkv, K, S] candidate scores, n = K * S)
+ *   keep (out): uint8 [rows, n]
+ * Limits: n <= 4096, token_budget > 0.
+ */
+int mrsa_token_keep_fwd(const float* scores, int64_t rows, int64_t n, int64_t token_budget,
+                        uint8_t* keep, void* stream);
+
+/*
  * Per-token candidate scores inside routed chunks: max over the query group of
  * q.k * sm_scale; -inf for the landmark slot, invalid keys and -1 chunks.
  * Replaces candidate_token_scores_gqa (ops/hils_token_score_gqa_tilelang.py:174-208).

@@ -32,6 +32,7 @@
 #include <type_traits>
 #include <utility>
 
+#include "block_select.h"
 #include "mrsa_device.h"
 
 using namespace mrsa;
@@ -842,35 +843,18 @@ __device__ __forceinline__ void block_reduce8(float (&v)[8], int G, float* red) 
   }
 }
 
-// Count of this block's keys >= t (one barrier; `buf` alternates between two
-// LDS slots so a wave that runs ahead cannot overwrite counts still read).
-__device__ __forceinline__ int block_count_ge(const uint32_t (&key)[kSelMaxPer], int n, uint32_t t,
-                                              int* buf) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int cnt = 0;
-#pragma unroll
-  for (int i = 0; i < kSelMaxPer; ++i)
-    if (i < n) cnt += __builtin_popcountll(__builtin_amdgcn_ballot_w64(key[i] >= t));
-  if (lane == 0) buf[wave] = cnt;
-  __syncthreads();
-  int r = 0;
-#pragma unroll
-  for (int w = 0; w < kSelWaves; ++w) r += buf[w];
-  return r;
-}
-
 // Selection: one workgroup per (row, KV head, batch); chunk c = tid + 512 i.
 // The row's logits and bias are read once into registers.  Same score, LSE,
 // drop and tie rules as the general kernel.
 template <int G>
 __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
                                                                    const float* __restrict__ raw) {
+  using Select = BlockSelect<kSelThreads, kSelMaxPer>;
   __shared__ float redf[2][kSelWaves * 8];
-  __shared__ int redi[2][kSelWaves];
-  __shared__ int wcnt[2][kSelMaxPer][kSelWaves];
+  __shared__ typename Select::Lds sel;
   const int64_t C = a.C, L = a.L;
   const int K = a.K;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int64_t r = blockIdx.x;
   const int h = blockIdx.y;
   const int64_t b = blockIdx.z;
@@ -936,13 +920,10 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
     lc = max(r - a.derive_window, (int64_t)0) / a.block_size;
     rc = min(r + a.derive_window, L - 1) / a.block_size;
   }
-  const uint32_t kNeg = float_order_key(neg_inf());
   uint32_t key[kSelMaxPer];
-  int nfin = 0;
-  uint32_t kmin = 0xffffffffu, kmax = 0u;
 #pragma unroll
   for (int i = 0; i < kSelMaxPer; ++i) {
-    key[i] = 0u;  // below every real key: never counted, never picked
+    key[i] = 0u;  // below every real key: never picked
     const int64_t c = tid + (int64_t)kSelThreads * i;
     if (i >= n || c >= C) continue;
     float best = neg_inf();
@@ -962,123 +943,24 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
       dropped = a.drop[(b * L + r) * C + c] != 0;
     }
     key[i] = float_order_key(dropped ? neg_inf() : best);
-    if (key[i] > kNeg) {
-      ++nfin;
-      kmin = min(kmin, key[i]);
-      kmax = max(kmax, key[i]);
-    }
-  }
-  {
-    int vmin = (int)(kmin ^ 0x80000000u), vmax = (int)(kmax ^ 0x80000000u);
-    for (int o = 1; o < 64; o <<= 1) {
-      vmin = min(vmin, __shfl_xor(vmin, o, 64));
-      vmax = max(vmax, __shfl_xor(vmax, o, 64));
-      nfin += __shfl_xor(nfin, o, 64);
-    }
-    if (lane == 0) {
-      wcnt[0][0][wave] = nfin;
-      wcnt[0][1][wave] = vmin;
-      wcnt[0][2][wave] = vmax;
-    }
-    __syncthreads();
-    nfin = 0;
-#pragma unroll
-    for (int w = 0; w < kSelWaves; ++w) {
-      nfin += wcnt[0][0][w];
-      vmin = min(vmin, wcnt[0][1][w]);
-      vmax = max(vmax, wcnt[0][2][w]);
-    }
-    kmin = (uint32_t)vmin ^ 0x80000000u;
-    kmax = (uint32_t)vmax ^ 0x80000000u;
   }
 
-  // 4. Threshold by bisection on the keys: keys >= thr_hi are picked, plus
-  //    the `need` lowest-index chunks whose key equals thr_tie.
-  uint32_t thr_hi, thr_tie = 0u;
-  int need = 0, it = 0;
-  if (nfin <= K) {
-    thr_hi = kNeg + 1u;
-  } else {
-    uint32_t lo = kmin, hi = kmax + 1u;
-    bool exact = false;
-    thr_hi = 0u;
-    while (hi - lo > 1u) {
-      const uint32_t mid = lo + ((hi - lo) >> 1);
-      const int cnt = block_count_ge(key, n, mid, redi[it++ & 1]);
-      if (cnt == K) {
-        thr_hi = mid;
-        exact = true;
-        break;
-      }
-      if (cnt > K) lo = mid; else hi = mid;
-    }
-    if (!exact) {
-      const int cnt_hi = block_count_ge(key, n, hi, redi[it++ & 1]);
-      thr_hi = hi;
-      thr_tie = lo;
-      need = K - cnt_hi;
-    }
-  }
-
-  // 5. Slots in ascending chunk order (i major, thread minor): tie ranks
-  //    first, then pick positions, from per-wave ballot counts.
-  const uint64_t below = (1ull << lane) - 1ull;
-  uint64_t tie_bits[kSelMaxPer];
-  __syncthreads();  // wcnt reused
-#pragma unroll
-  for (int i = 0; i < kSelMaxPer; ++i) {
-    tie_bits[i] = 0ull;
-    if (i >= n) continue;
-    tie_bits[i] = __builtin_amdgcn_ballot_w64(need > 0 && key[i] == thr_tie);
-    if (lane == 0) wcnt[0][i][wave] = __builtin_popcountll(tie_bits[i]);
-  }
-  __syncthreads();
+  // 4. The K largest (ties to the lower chunk), in ascending chunk order.
   bool pick[kSelMaxPer];
-  {
-    int base = 0;
-#pragma unroll
-    for (int i = 0; i < kSelMaxPer; ++i) {
-      pick[i] = false;
-      if (i >= n) continue;
-      int before = base;
-#pragma unroll
-      for (int w = 0; w < kSelWaves; ++w) {
-        const int v = wcnt[0][i][w];
-        before += w < wave ? v : 0;
-        base += v;
-      }
-      const bool tie = (tie_bits[i] >> lane) & 1ull;
-      const int tr = before + __builtin_popcountll(tie_bits[i] & below);
-      pick[i] = key[i] >= thr_hi || (tie && tr < need);
-      const uint64_t pb = __builtin_amdgcn_ballot_w64(pick[i]);
-      if (lane == 0) wcnt[1][i][wave] = __builtin_popcountll(pb);
-    }
-  }
-  __syncthreads();
-  int slot_base = 0;
+  int slot[kSelMaxPer];
+  const int slot_base = Select::run(key, n, K, sel, pick, slot);
 #pragma unroll
   for (int i = 0; i < kSelMaxPer; ++i) {
-    if (i >= n) continue;
-    const uint64_t pb = __builtin_amdgcn_ballot_w64(pick[i]);
-    int before = slot_base;
+    if (i >= n || !pick[i]) continue;
+    const int64_t c = tid + (int64_t)kSelThreads * i;
+    a.indices[row * K + slot[i]] = (int32_t)c;
 #pragma unroll
-    for (int w = 0; w < kSelWaves; ++w) {
-      const int v = wcnt[1][i][w];
-      before += w < wave ? v : 0;
-      slot_base += v;
-    }
-    if (pick[i]) {
-      const int slot = before + __builtin_popcountll(pb & below);
-      const int64_t c = tid + (int64_t)kSelThreads * i;
-      a.indices[row * K + slot] = (int32_t)c;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float v = xr[(int64_t)g * C + c];
-        if (a.scores_fp32)
-          reinterpret_cast<float*>(a.scores)[(row * G + g) * K + slot] = v;
-        else
-          reinterpret_cast<uint16_t*>(a.scores)[(row * G + g) * K + slot] = (uint16_t)f32_to_bf16(v);
-      }
+    for (int g = 0; g < G; ++g) {
+      const float v = xr[(int64_t)g * C + c];
+      if (a.scores_fp32)
+        reinterpret_cast<float*>(a.scores)[(row * G + g) * K + slot[i]] = v;
+      else
+        reinterpret_cast<uint16_t*>(a.scores)[(row * G + g) * K + slot[i]] = (uint16_t)f32_to_bf16(v);
     }
   }
   for (int t = slot_base + tid; t < K; t += kSelThreads) {

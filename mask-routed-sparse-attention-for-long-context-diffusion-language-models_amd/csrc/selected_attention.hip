@@ -101,12 +101,15 @@ struct SelArgs {
   // outputs [parts][B][Lq][Hq][128] to `partial` (parts == 1: bf16 `out`).
   int parts;
   float* partial;
+  // Optional token keep mask int8 [B, Lq, Hkv, K, 64] (nonzero = key kept)
+  // of the remote-token refinement; read only by the KEEP instantiation.
+  const int8_t* keep;
 };
 
 // LDS carve-up (byte offsets, 16-aligned).  The p_* arrays are only used by
 // the prologue and live inside the ring, which is free until the first DMA.
 struct SelLayout {
-  size_t ring, wr, s_chunk, s_own, s_mask, s_cnt, comp_slot, misc, s_rank, total;
+  size_t ring, wr, s_chunk, s_own, s_mask, s_cnt, comp_slot, misc, s_rank, s_keep, total;
   size_t p_idx, p_omask, p_len, p_w, p_end;
   int cap;
 };
@@ -114,7 +117,7 @@ __host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~(size_t
 // The walk has at most min(Ck, queries x K) steps; a tile holds at most
 // min(TQ, Lq) queries.
 __host__ __device__ inline SelLayout sel_layout(int TQ, int NW, int K, int64_t Ck, int R,
-                                                bool token, int64_t Lq) {
+                                                bool token, int64_t Lq, bool keep = false) {
   SelLayout l;
   const size_t n = (size_t)TQ * K;
   const size_t wbytes = token ? 0 : (size_t)TQ * 8 * K * 2;
@@ -130,6 +133,7 @@ __host__ __device__ inline SelLayout sel_layout(int TQ, int NW, int K, int64_t C
   l.comp_slot = o; o = align16(o + n);
   l.misc = o;      o = align16(o + (size_t)(NW + 8) * 4);
   l.s_rank = o;    o = align16(o + (size_t)TQ * 4);         // [TQ] first list rank
+  l.s_keep = o;    o = align16(o + (keep ? n * 8 : 0));       // [TQ][K] kept-key bits
   l.total = o;
   o = l.ring;
   l.p_idx = o;     o = align16(o + n * 4);
@@ -268,6 +272,7 @@ struct WalkLds {
   uint8_t* comp_slot;   // [TQ][K] list position -> original slot
   int32_t* misc;        // [waves] scan, [waves] step count, first chunk
   int32_t* s_rank;      // [TQ] list rank of each query at the first step
+  uint64_t* s_keep;     // [TQ][K] kept-key bits in list order (keep mode)
   int32_t* p_idx;       // [TQ][K] staged / compacted index rows (scratch)
   uint64_t* p_omask;    // [Ck] owner bits by chunk (scratch)
   int32_t* p_len;       // [TQ] list lengths (scratch)
@@ -302,7 +307,7 @@ __device__ __forceinline__ uint64_t invalid_key_bits(const uint8_t* kv, bool al1
 // `part` keeps steps [total * part / parts, total * (part + 1) / parts) and
 // each query's list rank at its first kept step (W.s_rank).  Returns the
 // number of kept steps.  Ends with a workgroup barrier.
-template <bool TOKEN, class SP>
+template <bool TOKEN, class SP, bool KEEP = false>
 __device__ int build_walk(const SelArgs& a, const WalkLds& W, int64_t b, int h, int64_t q0,
                           int64_t nq, int part) {
   constexpr int kWaves = SP::kWaves, kThreads = SP::kThreads, kTQ = SP::kTQ;
@@ -416,6 +421,33 @@ __device__ int build_walk(const SelArgs& a, const WalkLds& W, int64_t b, int h, 
       wr[e] = r < p_len[qq] ? wts[(qq * 8 + gg) * K + comp_slot[qq * K + r]] : (uint16_t)0;
     }
   }
+  if constexpr (KEEP) {
+    // Kept-key bits of each listed (query, chunk), bit j = key j, from the
+    // keep row of the chunk's original slot (a merged duplicate uses its
+    // first slot's row).
+    for (int e = tid; e < kTQ * K; e += kThreads) {
+      const int qq = e / K, r = e - qq * K;
+      uint64_t bits = 0ull;
+      if (r < p_len[qq]) {
+        const int8_t* kr =
+            a.keep + (((b * a.Lq + q0 + qq) * a.Hkv + h) * K + comp_slot[qq * K + r]) * 64;
+        if (((uintptr_t)a.keep & 15) == 0) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const u32x4_t x = *reinterpret_cast<const u32x4_t*>(kr + 16 * v);
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                bits |= ((x[w] >> (8 * j)) & 0xffu) ? 1ull << (16 * v + 4 * w + j) : 0ull;
+          }
+        } else {
+          for (int j = 0; j < 64; ++j) bits |= kr[j] ? 1ull << j : 0ull;
+        }
+      }
+      W.s_keep[e] = bits;
+    }
+  }
   __syncthreads();
 
   // 3. Walk list: the chunks with at least one owner, ascending, with their
@@ -479,7 +511,7 @@ __device__ int build_walk(const SelArgs& a, const WalkLds& W, int64_t b, int h, 
   return misc[kWaves];
 }
 
-template <bool TOKEN, int R, class SP>
+template <bool TOKEN, int R, class SP, bool KEEP>
 __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) {
   constexpr int kWaves = SP::kWaves, kThreads = SP::kThreads, kNtile = SP::kNtile;
   constexpr int kTQ = SP::kTQ;
@@ -489,7 +521,7 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   extern __shared__ __align__(16) unsigned char smem[];
   const int K = a.K;
   const int64_t Ck = a.Ck;
-  const SelLayout lay = sel_layout(kTQ, kWaves, K, Ck, R, TOKEN, a.Lq);
+  const SelLayout lay = sel_layout(kTQ, kWaves, K, Ck, R, TOKEN, a.Lq, KEEP);
   unsigned char* ring = smem + lay.ring;
   uint16_t* wr = reinterpret_cast<uint16_t*>(smem + lay.wr);            // [TQ][K][8]
   uint16_t* wts = reinterpret_cast<uint16_t*>(smem + lay.p_w);          // [TQ][8][K]
@@ -507,6 +539,7 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   int32_t* s_cnt = reinterpret_cast<int32_t*>(smem + lay.s_cnt);         // [cap]
   int32_t* cursor = misc + kWaves + 4;  // oldest chunk with unclaimed portions
   int32_t* s_rank = reinterpret_cast<int32_t*>(smem + lay.s_rank);      // [TQ]
+  uint64_t* s_keep = reinterpret_cast<uint64_t*>(smem + lay.s_keep);    // [TQ][K]
   int32_t* p_idx = reinterpret_cast<int32_t*>(smem + lay.p_idx);        // [TQ][K]
   uint64_t* p_omask = reinterpret_cast<uint64_t*>(smem + lay.p_omask);  // [Ck]
   int32_t* p_len = reinterpret_cast<int32_t*>(smem + lay.p_len);        // [TQ]
@@ -526,8 +559,10 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   // Zeroed counters, published by the prologue's barriers.
   if (tid == 0) *cursor = 0;
   for (int i = tid; i < lay.cap; i += kThreads) s_cnt[i] = 0;
-  const int nsteps = build_walk<TOKEN, SP>(
-      a, WalkLds{wr, wts, s_chunk, s_own, s_mask, comp_slot, misc, s_rank, p_idx, p_omask, p_len},
+  const int nsteps = build_walk<TOKEN, SP, KEEP>(
+      a,
+      WalkLds{wr, wts, s_chunk, s_own, s_mask, comp_slot, misc, s_rank, s_keep, p_idx, p_omask,
+              p_len},
       b, h, q0, nq, part);
 
   // 4. Q^T operands and accumulators of this wave's queries.
@@ -597,6 +632,10 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
       uint32_t wbits = 0u;
       if constexpr (!TOKEN)
         asm volatile("ds_read_u16 %0, %1" : "=v"(wbits) : "v"(lds_addr(&wr[(ql * K + pos) * 8 + gg])));
+      // Kept-key bits of the column's (query, chunk), read the same way.
+      uint64_t kbits = ~0ull;
+      if constexpr (KEEP)
+        asm volatile("ds_read_b64 %0, %1" : "=v"(kbits) : "v"(lds_addr(&s_keep[ql * K + pos])));
       // Opaque zero: keeps the compiler from hoisting this tile's K / V operand
       // reads out of the tile loop (that would pin 128 extra registers).
       int zoff = 0;
@@ -608,6 +647,7 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
       f32x4_t S[4];
       qk_tile<kDepth>(kaddr, Qb[nt], S);
       asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(wbits));  // already satisfied
+      if constexpr (KEEP) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kbits));
       const float wv = owns ? bf16_to_f32(wbits) : 0.f;
       // The first V^T operands do not depend on P: read them now so they land
       // during the softmax.  PV operand o = 8 * jj + td.
@@ -657,6 +697,17 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
             for (int i = 0; i < 4; ++i)
               S[t][i] = set_where(
                   S[t][i], __builtin_amdgcn_ballot_w64((msh >> (16 * t + i)) & 1ull), ninf_v);
+        }
+        if constexpr (KEEP) {
+          // Keys the column's keep row drops -> -inf (bit 16t + i of kb is
+          // key 16t + 4grp + i, as for msh).
+          const uint64_t kb = kbits >> (4 * grp);
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              S[t][i] = set_where(
+                  S[t][i], __builtin_amdgcn_ballot_w64(!((kb >> (16 * t + i)) & 1ull)), ninf_v);
         }
         const float mx = across4_max(max16_raw(S));
         const float mb = mx == neg_inf() ? 0.f : mx * c2;
@@ -856,9 +907,9 @@ __global__ void __launch_bounds__(256) fill_neg_inf(float* p, int64_t n) {
     p[e] = neg_inf();
 }
 
-template <bool TOKEN, int R, class SP>
+template <bool TOKEN, int R, class SP, bool KEEP>
 int launch_variant(SelArgs& a, const SelLayout& lay, hipStream_t s) {
-  auto kern = selected_attn_kernel<TOKEN, R, SP>;
+  auto kern = selected_attn_kernel<TOKEN, R, SP, KEEP>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lay.total) != hipSuccess)
     return MRSA_ERR_LAUNCH;
@@ -869,16 +920,16 @@ int launch_variant(SelArgs& a, const SelLayout& lay, hipStream_t s) {
 }
 
 // Deepest ring that fits in LDS: 4 slots, else 3.
-template <bool TOKEN>
+template <bool TOKEN, bool KEEP = false>
 int launch_selected(SelArgs& a, hipStream_t s) {
   using SP = std::conditional_t<
       MRSA_SEL_WAVES == 16, Split<16, 1>,
       std::conditional_t<MRSA_SEL_WAVES == 12, Split12,
                          std::conditional_t<MRSA_SEL_WAVES == 82, Split8x2, Split8>>>;
-  const SelLayout l4 = sel_layout(SP::kTQ, SP::kWaves, a.K, a.Ck, 4, TOKEN, a.Lq);
-  if (sel_layout_fits(l4, 4)) return launch_variant<TOKEN, 4, SP>(a, l4, s);
-  const SelLayout l3 = sel_layout(SP::kTQ, SP::kWaves, a.K, a.Ck, 3, TOKEN, a.Lq);
-  if (sel_layout_fits(l3, 3)) return launch_variant<TOKEN, 3, SP>(a, l3, s);
+  const SelLayout l4 = sel_layout(SP::kTQ, SP::kWaves, a.K, a.Ck, 4, TOKEN, a.Lq, KEEP);
+  if (sel_layout_fits(l4, 4)) return launch_variant<TOKEN, 4, SP, KEEP>(a, l4, s);
+  const SelLayout l3 = sel_layout(SP::kTQ, SP::kWaves, a.K, a.Ck, 3, TOKEN, a.Lq, KEEP);
+  if (sel_layout_fits(l3, 3)) return launch_variant<TOKEN, 3, SP, KEEP>(a, l3, s);
   return MRSA_ERR_UNSUPPORTED;
 }
 
@@ -937,6 +988,7 @@ extern "C" int mrsa_selected_attention_fwd(const void* q, const void* k, const v
   a.tscores = nullptr;
   a.parts = 1;
   a.partial = nullptr;
+  a.keep = nullptr;
   return launch_selected<false>(a, (hipStream_t)stream);
 }
 
@@ -982,28 +1034,29 @@ extern "C" int mrsa_candidate_token_scores_fwd(const void* q, const void* k,
   a.tscores = scores;
   a.parts = 1;
   a.partial = nullptr;
+  a.keep = nullptr;
   return launch_selected<true>(a, s);
 }
 
-extern "C" int mrsa_selected_attention_split_fwd(
-    const void* q, const void* k, const void* v_tiles, const void* weights,
-    const int32_t* indices, const uint8_t* key_valid, int64_t batch, int64_t q_len,
-    int64_t kv_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t topk,
-    int64_t chunk_size, int mask_last_token, float sm_scale, int64_t parts, float* partial,
-    void* out, void* stream) {
-  if (parts == 1)
-    return mrsa_selected_attention_fwd(q, k, v_tiles, weights, indices, key_valid, batch, q_len,
-                                       kv_len, q_heads, kv_heads, head_dim, topk, chunk_size,
-                                       mask_last_token, sm_scale, out, stream);
+namespace {
+
+// Routed attention with an optional walk split (parts > 1: fp32 partials in
+// `partial`, summed into `out`) and an optional token keep mask.
+int selected_forward(const void* q, const void* k, const void* v_tiles, const void* weights,
+                     const int32_t* indices, const uint8_t* key_valid, const int8_t* keep,
+                     int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
+                     int64_t kv_heads, int64_t head_dim, int64_t topk, int64_t chunk_size,
+                     int mask_last_token, float sm_scale, int64_t parts, float* partial,
+                     void* out, void* stream) {
   int st = check_common(q, k, indices, batch, q_len, kv_len, q_heads, kv_heads, head_dim, topk,
                         chunk_size, sm_scale);
   if (st != MRSA_OK) return st;
   if (parts < 1 || parts > kMaxParts) return MRSA_ERR_INVALID_ARGUMENT;
   if (batch * parts > 65535) return MRSA_ERR_UNSUPPORTED;
   if (batch == 0 || q_len == 0) return MRSA_OK;
-  if (!v_tiles || !weights || !out || !partial || (uintptr_t)v_tiles % 16 != 0 ||
-      (uintptr_t)out % 8 != 0 || (uintptr_t)partial % 16 != 0)
+  if (!v_tiles || !weights || !out || (uintptr_t)v_tiles % 16 != 0 || (uintptr_t)out % 8 != 0)
     return MRSA_ERR_INVALID_ARGUMENT;
+  if (parts > 1 && (!partial || (uintptr_t)partial % 16 != 0)) return MRSA_ERR_INVALID_ARGUMENT;
   SelArgs a;
   a.q = (const uint16_t*)q;
   a.k = (const uint16_t*)k;
@@ -1024,16 +1077,42 @@ extern "C" int mrsa_selected_attention_split_fwd(
   a.scale_log2 = sm_scale * kLog2e;
   a.sm_scale = sm_scale;
   a.token_mode = 0;
-  a.out = nullptr;
+  a.out = parts > 1 ? nullptr : (uint16_t*)out;
   a.tscores = nullptr;
   a.parts = (int)parts;
-  a.partial = partial;
+  a.partial = parts > 1 ? partial : nullptr;
+  a.keep = keep;
   hipStream_t s = (hipStream_t)stream;
-  st = launch_selected<false>(a, s);
-  if (st != MRSA_OK) return st;
+  st = keep ? launch_selected<false, true>(a, s) : launch_selected<false>(a, s);
+  if (st != MRSA_OK || parts == 1) return st;
   const int64_t n4 = batch * q_len * q_heads * 128 / 4;
   const int64_t blocks = std::min<int64_t>((n4 + 255) / 256, 4096);
   hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)blocks), dim3(256), 0, s, partial,
                      (int)parts, n4, (uint16_t*)out);
   return mrsa_launch_status();
+}
+
+}  // namespace
+
+extern "C" int mrsa_selected_attention_split_fwd(
+    const void* q, const void* k, const void* v_tiles, const void* weights,
+    const int32_t* indices, const uint8_t* key_valid, int64_t batch, int64_t q_len,
+    int64_t kv_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t topk,
+    int64_t chunk_size, int mask_last_token, float sm_scale, int64_t parts, float* partial,
+    void* out, void* stream) {
+  return selected_forward(q, k, v_tiles, weights, indices, key_valid, nullptr, batch, q_len,
+                          kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
+                          sm_scale, parts, partial, out, stream);
+}
+
+extern "C" int mrsa_selected_attention_keep_fwd(
+    const void* q, const void* k, const void* v_tiles, const void* weights,
+    const int32_t* indices, const uint8_t* key_valid, const int8_t* token_keep, int64_t batch,
+    int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+    int64_t topk, int64_t chunk_size, int mask_last_token, float sm_scale, int64_t parts,
+    float* partial, void* out, void* stream) {
+  if (batch > 0 && q_len > 0 && !token_keep) return MRSA_ERR_INVALID_ARGUMENT;
+  return selected_forward(q, k, v_tiles, weights, indices, key_valid, token_keep, batch, q_len,
+                          kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
+                          sm_scale, parts, partial, out, stream);
 }

@@ -42,6 +42,7 @@ from .route_weights import route_weights, route_weights_torch
 from .routing import route_topk_g7, selected_attention_g7, selected_attention_g7_cached
 from .sparse_attention import HiLS_block_M_head, value_tiles
 from .token_score import candidate_token_scores_gqa
+from .token_refinement import refine_remote_tokens_g7, select_global_token_keep
 from .topk import online_softmax_topk_head, ref_softmax_topk_max_pooling
 from ._lib import LIB_PATH, MrsaLibraryError, load as load_library
 
@@ -56,6 +57,8 @@ __all__ = [
     "bidir_local_attention",
     "cached_local_attention",
     "candidate_token_scores_gqa",
+    "refine_remote_tokens_g7",
+    "select_global_token_keep",
     "chunk_aligned_local_bounds",
     "chunk_attn_pool_gqa",
     "chunk_attn_pool_gqa_prior",

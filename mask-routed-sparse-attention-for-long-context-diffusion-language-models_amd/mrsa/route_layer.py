@@ -39,6 +39,7 @@ from .local_attention import local_attention_launch
 from .pool import chunk_attn_pool_gqa_prior
 from .route_weights import route_weights_launch
 from .sparse_attention import selected_attention_launch, value_tiles, value_tiles_rows
+from .token_refinement import refine_remote_tokens_g7
 from .topk import route_topk_launch
 
 
@@ -54,6 +55,11 @@ class RouteLayerConfig:
     gate_offset: float | None = 0.0   # fusion_gate_offset at init (attention.py:913)
     gate_scale: float | None = 1.0    # fusion_gate_scale at init (attention.py:914)
     skip_inert_slots: bool = True     # attention.py:902
+    # Remote-token refinement (attention.py:1729-1759, "global_qk" policy):
+    # with token_budget > 0 each (query, KV head) keeps only its budget of
+    # highest-scoring routed tokens.
+    token_budget: int = 0
+    token_policy: str = "global_qk"
 
 
 def _check_qkv(q, k, v, route_q):
@@ -96,6 +102,7 @@ def route_attention(
 
 
     _check_qkv(q, k, v, route_q)
+    _check_token_budget(cfg)
     B, L, Hq, D = q.shape
     Hkv = k.shape[2]
     G = Hq // Hkv
@@ -139,7 +146,13 @@ def route_attention(
         gate_offset=cfg.gate_offset, gate_scale=cfg.gate_scale,
     )
     _mark("route_weights")
-    remote_out = selected_attention_launch(q, k, vt, remote_w, indices, kv_bool, S)
+    token_keep = None
+    if cfg.token_budget > 0:
+        token_keep = refine_remote_tokens_g7(q, k, indices, kv_bool, S, cfg.token_budget,
+                                             training=False)
+        _mark("token_refinement")
+    remote_out = selected_attention_launch(q, k, vt, remote_w, indices, kv_bool, S,
+                                           token_keep=token_keep)
     _mark("selected_attention")
     out = fuse_hils_outputs(remote_out, local_out, local_w)
     _mark("fusion")
@@ -149,7 +162,22 @@ def route_attention(
         "local_output": local_out, "local_lse": local_lse, "landmark_keys": lmk,
         "entropy": entropy, "prior_bias": prior, "indices": indices, "scores": scores,
         "remote_weights": remote_w, "local_weight": local_w, "remote_output": remote_out,
+        "token_keep": token_keep,
     }
+
+
+def _check_token_budget(cfg):
+    # attention.py:1264-1289
+    if cfg.token_budget < 0:
+        raise ValueError(f"token_budget must be >= 0, got {cfg.token_budget}")
+    if cfg.token_budget > cfg.topk * cfg.chunk_size:
+        raise ValueError(
+            f"token_budget={cfg.token_budget} exceeds routed capacity "
+            f"{cfg.topk * cfg.chunk_size}")
+    if cfg.token_policy not in {"global_qk", "entropy_adaptive"}:
+        raise ValueError(f"unsupported token_policy={cfg.token_policy}")
+    if cfg.token_budget > 0 and cfg.token_policy != "global_qk":
+        raise ValueError("token_policy='entropy_adaptive' is not supported by the gfx950 path")
 
 
 def swa_attention(

@@ -104,8 +104,14 @@ def _validate_selected(q, k, v, weights, indices, key_valid, chunk_size, token_k
         raise ValueError(f"invalid weights shape {tuple(weights.shape)}")
     if key_valid.shape != (batch, kv_len):
         raise ValueError(f"invalid key_valid shape {tuple(key_valid.shape)}")
-    if token_keep is not None:
-        raise ValueError("token_keep (token-level refinement) is not supported yet")
+    if token_keep is not None and token_keep.shape != (
+        batch, query_len, h_kv, selected, chunk_size
+    ):
+        raise ValueError(
+            "token_keep must have shape "
+            f"{(batch, query_len, h_kv, selected, chunk_size)}, got "
+            f"{tuple(token_keep.shape)}"
+        )
     if kv_len % chunk_size != 0:
         raise ValueError(f"cache length {kv_len} must be divisible by chunk_size={chunk_size}")
     if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
@@ -116,6 +122,8 @@ def _validate_selected(q, k, v, weights, indices, key_valid, chunk_size, token_k
         raise ValueError("weights and indices must share the q device")
     if key_valid.device != q.device:
         raise ValueError("key_valid must share the q device")
+    if token_keep is not None and token_keep.device != q.device:
+        raise ValueError("token_keep must share the q device")
     if selected <= 0:
         raise ValueError("selected attention requires at least one chunk slot")
 
@@ -126,7 +134,8 @@ def selected_attention_g7(q, k, v, weights, indices, key_valid, chunk_size, trai
 
     _validate_selected(q, k, v, weights, indices, key_valid, chunk_size, token_keep)
     return selected_attention_launch(
-        q, k, value_tiles(v), weights, indices, key_valid, chunk_size, mask_last_token=True
+        q, k, value_tiles(v), weights, indices, key_valid, chunk_size, mask_last_token=True,
+        token_keep=token_keep,
     )
 
 
@@ -136,5 +145,6 @@ def selected_attention_g7_cached(q, k, v, weights, indices, key_valid, chunk_siz
 
     _validate_selected(q, k, v, weights, indices, key_valid, chunk_size, token_keep)
     return selected_attention_launch(
-        q, k, value_tiles(v), weights, indices, key_valid, chunk_size, mask_last_token=True
+        q, k, value_tiles(v), weights, indices, key_valid, chunk_size, mask_last_token=True,
+        token_keep=token_keep,
     )

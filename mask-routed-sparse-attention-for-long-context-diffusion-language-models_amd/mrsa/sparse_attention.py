@@ -82,11 +82,14 @@ def selected_attention_launch(
     mask_last_token: bool = True,
     sm_scale: float | None = None,
     parts: int | None = None,
+    token_keep: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """q [B, Lq, Hq, D], k [B, Lk, Hkv, D], weights [B, Lq, Hq, K] -> [B, Lq, Hq, D] bf16.
 
     ``parts`` splits each walk over that many workgroups (fp32 partial
     outputs summed by a second kernel); None picks it with ``walk_parts``.
+    ``token_keep`` [B, Lq, Hkv, K, chunk_size] (nonzero = kept) additionally
+    masks the keys of each query's slot k.
     """
 
     B, Lq, Hq, D = q.shape
@@ -105,7 +108,19 @@ def selected_attention_launch(
     idx = indices.to(torch.int32).contiguous()
     kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
     out = torch.empty(B, Lq, Hq, D, dtype=torch.bfloat16, device=q.device)
-    if parts == 1:
+    if token_keep is not None:
+        keep = token_keep.to(device=q.device, dtype=torch.int8).contiguous()
+        partial = None
+        if parts > 1:
+            partial = torch.empty(parts, B, Lq, Hq, D, dtype=torch.float32, device=q.device)
+        st = _lib.call(
+            "mrsa_selected_attention_keep_fwd",
+            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(w), _lib.ptr(idx),
+            _lib.ptr(kv), _lib.ptr(keep), B, Lq, Lk, Hq, Hkv, D, K, int(chunk_size),
+            1 if mask_last_token else 0, float(sm_scale), parts, _lib.ptr(partial),
+            _lib.ptr(out), _lib.stream_of(qc),
+        )
+    elif parts == 1:
         st = _lib.call(
             "mrsa_selected_attention_fwd",
             _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(w), _lib.ptr(idx),
@@ -135,8 +150,7 @@ def HiLS_block_M_head(
     """Same arguments as ops/hils_fwd_bwd_head.py:1113-1150, forward only.
 
     Tiling knobs (block_M, num_threads*) are accepted and ignored: the gfx950
-    kernel picks its own tiling.  ALiBi slopes and token_keep are not
-    supported.
+    kernel picks its own tiling.  ALiBi slopes are not supported.
     """
 
     B, L, HQ, D = q.shape
@@ -146,7 +160,12 @@ def HiLS_block_M_head(
     if slope is not None:
         raise ValueError("ALiBi slopes are not supported by the gfx950 routed-attention kernel")
     if token_keep is not None:
-        raise ValueError("token_keep (token-level refinement) is not supported yet")
+        expected_keep_shape = (B, L, H, indices.shape[-1], block_size)
+        if token_keep.shape != expected_keep_shape:
+            raise ValueError(
+                "token_keep must have shape "
+                f"{expected_keep_shape}, got {tuple(token_keep.shape)}"
+            )
     if dtype != "bfloat16" or accum_dtype != "float":
         raise ValueError("only bf16 inputs with fp32 accumulation are supported")
     if key_valid is not None and key_valid.shape != (B, L_kv):
@@ -155,5 +174,5 @@ def HiLS_block_M_head(
         raise ValueError("HiLS_block_M_head on gfx950 is forward-only (no autograd)")
     return selected_attention_launch(
         q, k, value_tiles(v), weights, indices, key_valid, block_size,
-        mask_last_token=mask_last_token, sm_scale=sm_scale,
+        mask_last_token=mask_last_token, sm_scale=sm_scale, token_keep=token_keep,
     )

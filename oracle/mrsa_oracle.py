@@ -289,7 +289,7 @@ def local_attention(q, k, v, key_valid, window, inert_chunk=0, query_positions=N
 # a8: routed chunk attention
 # ---------------------------------------------------------------------------
 def selected_attention(q, k, v, weights, indices, key_valid, chunk_size=64,
-                       mask_last_token=True, query_block=256):
+                       mask_last_token=True, query_block=256, token_keep=None):
     """Weighted sum of per-chunk softmax attentions.
 
     Formula of the reference test test_hils_non_power_two_topk.py:122-138 and
@@ -297,7 +297,9 @@ def selected_attention(q, k, v, weights, indices, key_valid, chunk_size=64,
     masking (:479-486) and index-list reading (:352-361: a list ends at its
     first negative entry).  Entries >= kv_len / chunk_size are skipped.
     q [B, Lq, Hq, D], k/v [B, Lk, Hkv, D], weights [B, Lq, Hq, K],
-    indices [B, Lq, Hkv, K].  Returns fp32 [B, Lq, Hq, D].
+    indices [B, Lq, Hkv, K].  token_keep [B, Lq, Hkv, K, S] (nonzero = keep)
+    additionally masks the keys of slot k of each query (:457-486, the
+    TokenKeep[b, q, h, slot, key] term).  Returns fp32 [B, Lq, Hq, D].
     """
 
     B, Lq, Hq, D = q.shape
@@ -331,6 +333,8 @@ def selected_attention(q, k, v, weights, indices, key_valid, chunk_size=64,
             kg = kc[bidx, c, :, hidx]                       # [B, l, Hkv, S, D]
             vg = vc[bidx, c, :, hidx]
             al = allowed[bidx, c]                           # [B, l, Hkv, S]
+            if token_keep is not None:
+                al = al & (token_keep[:, i0:i1, :, kk] != 0)
             s = torch.einsum("blhgd,blhsd->blhgs", qb, kg) * scale
             s = s.masked_fill(~al[:, :, :, None, :], NEG_INF)
             p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
@@ -356,6 +360,24 @@ def fuse_outputs(remote_output, local_output, local_weight):
 # ---------------------------------------------------------------------------
 # a6: candidate token scores
 # ---------------------------------------------------------------------------
+def select_global_token_keep(scores, token_budget):
+    """select_global_token_keep (dream_dllm_hils/token_refinement.py:112-148)
+    without training noise: in each (b, l, h) row the min(budget, K * S)
+    largest of the flattened [K * S] scores are kept when finite.  Ties at the
+    threshold go to the lower flat index (the reference's torch.topk
+    (sorted=False) leaves their order to the device).  uint8 [B, L, Hkv, K, S].
+    """
+
+    B, L, H, K, S = scores.shape
+    flat = scores.float().reshape(B, L, H, K * S)
+    budget = min(int(token_budget), K * S)
+    order = torch.sort(flat, dim=-1, descending=True, stable=True).indices[..., :budget]
+    picked = torch.gather(flat, -1, order)
+    keep = torch.zeros(B, L, H, K * S, dtype=torch.uint8)
+    keep.scatter_(-1, order, torch.isfinite(picked).to(torch.uint8))
+    return keep.reshape(B, L, H, K, S)
+
+
 def candidate_token_scores(q, k, indices, key_valid, chunk_size):
     """candidate_token_scores_reference (dream_dllm_hils/token_refinement.py:10-92)."""
 
@@ -385,10 +407,13 @@ def candidate_token_scores(q, k, indices, key_valid, chunk_size):
 # ---------------------------------------------------------------------------
 def route_layer(q, k, v, route_q, entropy_bias_scale, key_valid=None, *, local_window=256,
                 chunk_size=64, topk=32, temperature=1.0, gate_offset=0.0, gate_scale=1.0,
-                skip_inert_slots=True):
+                skip_inert_slots=True, token_budget=0):
     """KernelDreamFullHiLSAttention.forward between projections and o_proj
     (dream_dllm_hils/attention.py:1380-1774), with the reference's bf16
-    rounding between stages.  Returns (out bf16, intermediates dict)."""
+    rounding between stages.  token_budget > 0 adds the "global_qk" token
+    refinement (attention.py:1729-1769): candidate token scores of q in the
+    routed chunks, the global keep mask, and the routed attention restricted
+    to it.  Returns (out bf16, intermediates dict)."""
 
     B, L, Hq, D = q.shape
     Hkv = k.shape[2]
@@ -413,12 +438,16 @@ def route_layer(q, k, v, route_q, entropy_bias_scale, key_valid=None, *, local_w
                            gate_offset=gate_offset, gate_scale=gate_scale)
     rw = rw.to(torch.bfloat16)
     lw = lw.to(torch.bfloat16)
-    remote = selected_attention(q, k, v, rw, idx, kv, S).to(torch.bfloat16)
+    keep = None
+    if token_budget > 0:
+        keep = select_global_token_keep(candidate_token_scores(q, k, idx, kv, S), token_budget)
+    remote = selected_attention(q, k, v, rw, idx, kv, S, token_keep=keep).to(torch.bfloat16)
     out = fuse_outputs(remote, local_out, lw)
     return out, {
         "local_output": local_out, "local_lse": local_lse, "landmark_keys": lmk,
         "entropy": entropy, "prior_bias": prior, "indices": idx, "scores": scores_bf,
         "selection": sel, "remote_weights": rw, "local_weight": lw, "remote_output": remote,
+        "token_keep": keep,
     }
 
 
