@@ -115,6 +115,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("route", "decode"), default="route")
+    ap.add_argument("--token-budget", type=int, default=0,
+                    help="route workload with the remote-token refinement (global_qk) at "
+                         "this budget (0: off, the configuration-2 default)")
     ap.add_argument("--decode-eager", action="store_true",
                     help="decode workload without the captured step graph")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -145,7 +148,8 @@ def main() -> int:
     route_q = q
     scale = torch.ones(HQ, device=dev)
     key_valid = torch.ones(1, L_CFG2, dtype=torch.bool, device=dev)
-    cfg = mrsa.RouteLayerConfig(local_window=WINDOW, chunk_size=CHUNK, topk=TOPK)
+    cfg = mrsa.RouteLayerConfig(local_window=WINDOW, chunk_size=CHUNK, topk=TOPK,
+                                token_budget=args.token_budget)
 
     stream = torch.cuda.current_stream(dev)
     stage_events = []
@@ -212,6 +216,7 @@ def main() -> int:
             "chunk_size": CHUNK,
             "topk": TOPK,
             "local_window": WINDOW,
+            "token_budget": args.token_budget,
             "parallelism": "single-gpu",
         },
         "roofline": {

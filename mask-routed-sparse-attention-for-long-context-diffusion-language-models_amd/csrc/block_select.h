@@ -1,4 +1,4 @@
-// Block-wide top-K selection over order keys held in registers.
+// Block-wide (and wave-wide) top-K selection over order keys held in registers.
 //
 // Each of THREADS threads holds PER keys; element (i, tid) has order index
 // i * THREADS + tid.  Keys above kFloor are candidates (kFloor is the order
@@ -155,6 +155,99 @@ struct BlockSelect {
       if (pick[i]) slot[i] = before + __builtin_popcountll(pb & below);
     }
     return total;
+  }
+};
+
+// The same selection by one wave with no barrier: element (i, lane) has
+// order index i * 64 + lane; every count is a sum of ballot popcounts, so
+// the whole search runs on scalar registers after each compare.
+template <int PER>
+struct WaveSelect {
+  __device__ static uint32_t wave_min_u(uint32_t v) {
+    for (int o = 1; o < 64; o <<= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, 64));
+    return v;
+  }
+  __device__ static uint32_t wave_max_u(uint32_t v) {
+    for (int o = 1; o < 64; o <<= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
+    return v;
+  }
+  // Ballots in groups of 8 with a scheduling fence between groups: the
+  // scheduler would otherwise keep all PER ballot masks live in SGPRs.
+  __device__ static int count_ge(const uint32_t (&key)[PER], int n, uint32_t t) {
+    int c = 0;
+#pragma unroll
+    for (int i0 = 0; i0 < PER; i0 += 8) {
+#pragma unroll
+      for (int i = i0; i < i0 + 8 && i < PER; ++i)
+        if (i < n) c += __builtin_popcountll(__builtin_amdgcn_ballot_w64(key[i] >= t));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return c;
+  }
+
+  // n: key slots in use per lane (<= PER <= 64, uniform).  Returns this
+  // lane's picks as bits (bit i: element (i, lane)); per-lane bits keep the
+  // picks in vector registers (an array of bools would take a scalar mask
+  // pair per element).
+  __device__ static uint64_t run(const uint32_t (&key)[PER], int n, int K) {
+    static_assert(PER <= 64, "one pick bit per key slot");
+    const int lane = threadIdx.x & 63;
+    const uint32_t kFloor = float_order_key(neg_inf());
+    int nfin = 0;
+    uint32_t kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      if (i >= n) continue;
+      const bool f = key[i] > kFloor;
+      nfin += f ? 1 : 0;
+      if (f) {
+        kmin = min(kmin, key[i]);
+        kmax = max(kmax, key[i]);
+      }
+    }
+    for (int o = 1; o < 64; o <<= 1) nfin += __shfl_xor(nfin, o, 64);
+    kmin = wave_min_u(kmin);
+    kmax = wave_max_u(kmax);
+    uint32_t thr_hi, thr_tie = 0u;
+    int need = 0;
+    if (nfin <= K) {
+      thr_hi = kFloor + 1u;
+    } else {
+      uint32_t lo = kmin, hi = kmax + 1u;  // count(lo) > K > count(hi)
+      bool exact = false;
+      thr_hi = 0u;
+      while (hi - lo > 1u) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        const int c = count_ge(key, n, mid);
+        if (c == K) {
+          thr_hi = mid;
+          exact = true;
+          break;
+        }
+        if (c > K) lo = mid; else hi = mid;
+      }
+      if (!exact) {
+        thr_hi = hi;
+        thr_tie = lo;
+        need = K - count_ge(key, n, hi);
+      }
+    }
+    const uint64_t below = (1ull << lane) - 1ull;
+    int base = 0;
+    uint64_t picks = 0ull;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      if (i >= n) continue;
+      bool p = key[i] >= thr_hi;
+      if (need > 0) {  // uniform
+        const uint64_t tb = __builtin_amdgcn_ballot_w64(key[i] == thr_tie);
+        p = p || (((tb >> lane) & 1ull) && base + __builtin_popcountll(tb & below) < need);
+        base += __builtin_popcountll(tb);
+      }
+      picks |= p ? 1ull << i : 0ull;
+      if ((i & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+    }
+    return picks;
   }
 };
 

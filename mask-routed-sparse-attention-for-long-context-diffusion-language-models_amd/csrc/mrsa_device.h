@@ -113,6 +113,12 @@ __device__ __forceinline__ uint32_t group8_max_u(uint32_t v) {
   v = max(v, (uint32_t)dpp_mov_i<0x141>((int)v));
   return v;
 }
+__device__ __forceinline__ float group8_max_f(float v) {
+  v = fmaxf(v, __int_as_float(dpp_mov_i<0xb1>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_mov_i<0x4e>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_mov_i<0x141>(__float_as_int(v))));
+  return v;
+}
 // Exclusive prefix sum over the 8 lanes of a group (sub = l % 8): row_shr:o
 // brings lane l - o, which is in the same group when sub >= o.
 __device__ __forceinline__ int group8_excl_scan_i(int v, int sub) {

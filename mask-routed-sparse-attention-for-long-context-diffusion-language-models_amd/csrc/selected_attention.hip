@@ -665,13 +665,7 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float v = gg < G ? S[t][i] : neg_inf();
-            v = fmaxf(v, __shfl_xor(v, 1, 64));
-            v = fmaxf(v, __shfl_xor(v, 2, 64));
-            v = fmaxf(v, __shfl_xor(v, 4, 64));
-            S[t][i] = v;
-          }
+          for (int i = 0; i < 4; ++i) S[t][i] = group8_max_f(gg < G ? S[t][i] : neg_inf());
         if (owns && gg == 0) {
           const int64_t qi = q0 + ql;
           float* dst = a.tscores + (((b * a.Lq + qi) * a.Hkv + h) * K + slot) * 64;

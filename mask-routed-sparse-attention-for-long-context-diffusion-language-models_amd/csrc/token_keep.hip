@@ -5,10 +5,10 @@
 // kept when finite; ties at the threshold go to the lower flat index.  -inf
 // (and NaN) scores are never kept.
 //
-// One 512-thread workgroup per row; element e = tid + 512 i lives in
-// registers as an order key, and the block-wide bisection of block_select.h
-// finds the threshold.  HBM-bound: n * 4 bytes read and n bytes written per
-// row.
+// One wave per row (four rows per workgroup): element e = lane + 64 i lives
+// in registers as an order key and the wave-level bisection of
+// block_select.h finds the threshold without a barrier.  HBM-bound: n * 4
+// bytes read and n bytes written per row.
 #include "block_select.h"
 #include "mrsa_device.h"
 
@@ -16,37 +16,45 @@ using namespace mrsa;
 
 namespace {
 
-constexpr int kKeepThreads = 512;
-constexpr int kKeepPer = 8;  // n <= 4096
+constexpr int kRowsPerBlock = 4;
 
-__global__ void __launch_bounds__(kKeepThreads)
-    token_keep_kernel(const float* __restrict__ scores, int64_t n, int budget,
+template <int PER>
+__global__ void __launch_bounds__(64 * kRowsPerBlock)
+    token_keep_kernel(const float* __restrict__ scores, int64_t rows, int64_t n, int budget,
                       uint8_t* __restrict__ keep) {
-  using Select = BlockSelect<kKeepThreads, kKeepPer>;
-  __shared__ typename Select::Lds sel;
-  const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole waves only
   const float* sr = scores + row * n;
-  const int per = (int)((n + kKeepThreads - 1) / kKeepThreads);
-  uint32_t key[kKeepPer];
+  // Slot rows i < per are in use (uniform); only the last one may be partial
+  // (lanes >= last are past the row).  Loads are unconditional at clamped
+  // addresses so that none of them waits alone inside a branch.
+  const int per = (int)((n + 63) / 64);
+  const int last = (int)(n - 64 * (int64_t)(per - 1));
+  float v[PER];
 #pragma unroll
-  for (int i = 0; i < kKeepPer; ++i) {
-    key[i] = 0u;
-    const int64_t e = tid + (int64_t)kKeepThreads * i;
-    if (i < per && e < n) {
-      const float v = sr[e];
-      key[i] = float_order_key(v == v ? v : neg_inf());
-    }
+  for (int i = 0; i < PER; ++i) v[i] = sr[min(lane + 64 * (int64_t)i, n - 1)];
+  uint32_t key[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    key[i] = i < per ? float_order_key(v[i] == v[i] ? v[i] : neg_inf()) : 0u;
+    if (i == per - 1 && lane >= last) key[i] = 0u;
   }
-  bool pick[kKeepPer];
-  int slot[kKeepPer];
-  Select::run(key, per, budget, sel, pick, slot);
+  const uint64_t picks = WaveSelect<PER>::run(key, per, budget);
   uint8_t* kr = keep + row * n;
 #pragma unroll
-  for (int i = 0; i < kKeepPer; ++i) {
-    const int64_t e = tid + (int64_t)kKeepThreads * i;
-    if (i < per && e < n) kr[e] = pick[i] ? 1 : 0;
+  for (int i = 0; i < PER; ++i) {
+    if (i >= per) break;
+    if (i < per - 1 || lane < last) kr[lane + 64 * (int64_t)i] = (uint8_t)((picks >> i) & 1ull);
   }
+}
+
+template <int PER>
+void launch_keep(const float* scores, int64_t rows, int64_t n, int budget, uint8_t* keep,
+                 hipStream_t s) {
+  hipLaunchKernelGGL(token_keep_kernel<PER>,
+                     dim3((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock)),
+                     dim3(64 * kRowsPerBlock), 0, s, scores, rows, n, budget, keep);
 }
 
 }  // namespace
@@ -56,9 +64,12 @@ extern "C" int mrsa_token_keep_fwd(const float* scores, int64_t rows, int64_t n,
   if (rows < 0 || n < 0 || token_budget <= 0) return MRSA_ERR_INVALID_ARGUMENT;
   if (rows == 0 || n == 0) return MRSA_OK;
   if (!scores || !keep) return MRSA_ERR_INVALID_ARGUMENT;
-  if (n > (int64_t)kKeepThreads * kKeepPer || rows > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
+  if (n > 4096 || rows > ((int64_t)1 << 32)) return MRSA_ERR_UNSUPPORTED;
   const int budget = (int)(token_budget < n ? token_budget : n);
-  hipLaunchKernelGGL(token_keep_kernel, dim3((unsigned)rows), dim3(kKeepThreads), 0,
-                     (hipStream_t)stream, scores, n, budget, keep);
+  hipStream_t s = (hipStream_t)stream;
+  if (n <= 512) launch_keep<8>(scores, rows, n, budget, keep, s);
+  else if (n <= 1024) launch_keep<16>(scores, rows, n, budget, keep, s);
+  else if (n <= 2048) launch_keep<32>(scores, rows, n, budget, keep, s);
+  else launch_keep<64>(scores, rows, n, budget, keep, s);
   return mrsa_launch_status();
 }

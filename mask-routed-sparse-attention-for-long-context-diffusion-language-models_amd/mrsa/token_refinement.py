@@ -38,10 +38,12 @@ def select_global_token_keep(
     training: bool = True,
     use_gumbel: bool = False,
     gumbel_scale: float = 1.0,
+    _dtype: torch.dtype = torch.uint8,
 ) -> torch.Tensor:
     """uint8 keep mask [B, L, Hkv, K, S]: in each (b, l, h) row the
     min(budget, K * S) largest scores are kept when finite (ties to the lower
-    flat index)."""
+    flat index).  (``_dtype`` int8 gives the same 0/1 bytes as the routed
+    kernel's keep mask without a conversion pass.)"""
 
     if scores.ndim != 5:
         raise ValueError(f"scores must have shape [B,L,Hkv,K,S], got {tuple(scores.shape)}")
@@ -57,7 +59,7 @@ def select_global_token_keep(
     if n > _MAX_ROW:
         raise ValueError(f"K * chunk_size must be <= {_MAX_ROW}, got {n}")
     flat = ranking.to(torch.float32).contiguous()
-    keep = torch.empty(B, L, H, K, S, dtype=torch.uint8, device=scores.device)
+    keep = torch.empty(B, L, H, K, S, dtype=_dtype, device=scores.device)
     st = _lib.call("mrsa_token_keep_fwd", _lib.ptr(flat), B * L * H, n, int(token_budget),
                    _lib.ptr(keep), _lib.stream_of(flat))
     _lib.check(st, "token_keep")
@@ -91,5 +93,5 @@ def refine_remote_tokens_g7(
         )
         return select_global_token_keep(
             scores, token_budget, training=training, use_gumbel=use_gumbel,
-            gumbel_scale=gumbel_scale,
-        ).to(dtype=torch.int8)
+            gumbel_scale=gumbel_scale, _dtype=torch.int8,
+        )
