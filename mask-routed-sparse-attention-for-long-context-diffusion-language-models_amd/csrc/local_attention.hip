@@ -1,19 +1,32 @@
 // Bidirectional sliding-window GQA attention (flash-attn window semantics).
 //
-// Work split: one workgroup per (batch, KV head, block of 32 queries) with one
-// wave per query head of the group, so the K / V tiles of the KV head are
-// staged in LDS once and shared by all G query heads.  Each wave owns two
-// 16-query column tiles of its head.
+// Work split: one workgroup of 8 waves per (batch, KV head, block of QB
+// queries).  The block's query-head columns form column tiles of 16 columns;
+// a tile holds 16 / GP queries x GP head columns (GP = the group size rounded
+// up to a power of two; columns of heads >= G are padding), and each wave
+// owns kNT tiles (QB = 8 kNT (16 / GP): 16 queries for G = 7 with kNT = 1).
+// Q^T operands and O^T accumulators stay in registers.  With kNT = 1 a
+// workgroup needs 128 VGPRs per lane and ~69 KB of LDS, so two workgroups
+// share a CU and their barriers fall at different times: one's matrix
+// products run during the other's softmax.  (kNT = 2 shares each K / V
+// operand read between a wave's two tiles instead; both measure alike.)
 //
-// Matrix-core formulation (per 64-key tile):
-//   S^T[key][query] = K_tile (A: 64 x 128) . Q^T (B: 128 x 16)   -> 4 x 4 MFMAs
-//   online softmax down each column (query), in the exp2 domain
-//   O^T[d][query]  += V^T (A: 128 x 64) . P^T (B: 64 x 16)      -> 8 x 2 MFMAs
-// P^T is fed to the second product straight from the accumulator registers of
-// the first: lane l holds keys 16t + 4(l/16) + i of its query column, and the
-// reduction slots of the second product are numbered so that slot e of lane
-// group g is key 32j + 16(e/4) + 4g + e%4.  V^T is read from the tiled,
-// transposed V layout with the same numbering.
+// Key tiles of 64 arrive by global->LDS DMA in a ring of kRing XOR-swizzled
+// 32 KB slots (chunk_tile.h layout: K rows, then V^T rows from the tiled V
+// layout); every wave issues 4 of a tile's 32 1-KB DMA instructions from
+// 32-bit offsets against wave-uniform tile bases.  One barrier per key tile,
+// with no memory fence: each wave waits (vmcnt) for its own share of tile t,
+// the barrier publishes the whole tile and frees the slot of tile t - 1,
+// which then receives tile t + kRing - 1.  The valid-key words of all the
+// block's key tiles are built once, before the first DMA.
+//
+// Matrix-core formulation (per 64-key tile and column tile):
+//   S^T[key][col] = K_tile (A: 64 x 128) . Q^T (B: 128 x 16)   -> 16 MFMAs
+//   online softmax down each column, in the exp2 domain
+//   O^T[d][col]  += V^T (A: 128 x 64) . P^T (B: 64 x 16)      -> 16 MFMAs
+// P^T is fed to the second product straight from the accumulator registers
+// of the first: lane l holds keys 16t + 4(l/16) + i of its column, and the
+// tiled V layout numbers the reduction slots to match.
 //
 // Semantics (dream_dllm_hils/local_attention.py:35-107):
 //   * key j is visible to a query at position p iff |p - j| <= window;
@@ -21,16 +34,34 @@
 //     carry zero K and V: logit exactly 0, no contribution to the output;
 //   * P is rounded to bf16 before the PV product, the row sum uses fp32 P
 //     (flash-attn's convention); out = O / l in bf16; lse = ln(sum exp(s)).
+#include "chunk_tile.h"
 #include "mrsa_device.h"
 
 using namespace mrsa;
 
 namespace {
 
-constexpr int kQB = 32;        // queries per workgroup
-constexpr int kKPitch = 136;   // bf16 per staged K row   (272 B)
-constexpr int kVPitch = 72;    // bf16 per staged V^T row (144 B)
-constexpr int kStageVecs = 2048;  // 16-byte vectors per staged tile (K + V^T)
+#ifndef MRSA_LOCAL_NT
+#define MRSA_LOCAL_NT 1
+#endif
+#ifndef MRSA_LOCAL_RING
+#define MRSA_LOCAL_RING 2
+#endif
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kNT = MRSA_LOCAL_NT;      // column tiles per wave
+constexpr int kColTiles = kWaves * kNT;
+constexpr int kRing = MRSA_LOCAL_RING;  // key-tile slots
+// One column tile per wave leaves room (128 VGPRs, 2 x 69 KB LDS) for two
+// workgroups per CU, whose barriers fall at different times: one's matrix
+// products overlap the other's softmax.
+constexpr int kBlocksPerCU = kNT == 1 ? 2 : 1;
+#ifndef MRSA_LOCAL_DEPTH
+#define MRSA_LOCAL_DEPTH 8
+#endif
+constexpr int kDepth = MRSA_LOCAL_DEPTH;  // LDS operand reads in flight
+constexpr int kSlotBytes = 32768;
+constexpr int kMaskTiles = 512;        // key-valid words kept in LDS per block
 
 struct LocalArgs {
   const uint16_t* q;
@@ -39,7 +70,7 @@ struct LocalArgs {
   const uint8_t* key_valid;
   const int64_t* qpos;
   int64_t B, Lq, Lk;
-  int Hq, Hkv;
+  int Hq, Hkv, G;
   int64_t W;
   int64_t inert_chunk;
   float scale_log2;
@@ -55,31 +86,44 @@ struct LocalArgs {
   float* part_ml;
 };
 
-template <int G>
-__global__ void __launch_bounds__(64 * G) local_attn_kernel(LocalArgs a) {
-  constexpr int NTHR = 64 * G;
-  constexpr int PER = (kStageVecs + NTHR - 1) / NTHR;
-  __shared__ __align__(16) uint16_t Ks[64 * kKPitch + 128 * kVPitch];
-  uint16_t* const Vs = Ks + 64 * kKPitch;
-  __shared__ uint64_t inert_bits, range_bits;
-  __shared__ int64_t pos_lo, pos_hi;
+// Valid-key bits (bit s = key 64 kt + s passes key_valid) of one key tile,
+// 64 bytes read by the whole wave.
+__device__ __forceinline__ uint64_t tile_valid_bits(const LocalArgs& a, int64_t b, int64_t kt) {
+  const int lane = threadIdx.x & 63;
+  const int64_t j = kt * 64 + lane;
+  const bool ok = j < a.Lk && (!a.key_valid || a.key_valid[b * a.Lk + j] != 0);
+  return __builtin_amdgcn_ballot_w64(ok);
+}
+
+template <int GP>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2 * kBlocksPerCU, 2 * kBlocksPerCU)))
+local_attn_kernel(LocalArgs a) {
+  constexpr int QPT = 16 / GP;          // queries per column tile
+  constexpr int QB = kColTiles * QPT;   // queries per workgroup
+  extern __shared__ __align__(16) unsigned char smem[];
+  unsigned char* ring = smem;                                              // kRing slots
+  uint64_t* valid_tab = reinterpret_cast<uint64_t*>(smem + kRing * kSlotBytes);  // [kMaskTiles]
+  int64_t* pos_range = reinterpret_cast<int64_t*>(valid_tab + kMaskTiles);      // [2]
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, g = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
   const int64_t b = blockIdx.z % a.B;
   const int part = (int)(blockIdx.z / a.B);
   const int h = blockIdx.y;
-  const int64_t qb = (int64_t)blockIdx.x * kQB;
-  const int hq = h * G + g;
+  const int64_t qb = (int64_t)blockIdx.x * QB;
+  const int G = a.G;
+  const int gg = col % GP;
 
-  // Position range of this block's queries.
-  if (g == 0) {
+  // Position range of the block's queries.
+  if (wave == 0) {
     int64_t lo = INT64_MAX, hi = INT64_MIN;
-    if (lane < kQB && qb + lane < a.Lq) {
-      const int64_t p = a.qpos ? a.qpos[qb + lane] : qb + lane;
-      lo = p;
-      hi = p;
+    for (int i = lane; i < QB; i += 64) {
+      if (qb + i < a.Lq) {
+        const int64_t p = a.qpos ? a.qpos[qb + i] : qb + i;
+        lo = min(lo, p);
+        hi = max(hi, p);
+      }
     }
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -87,166 +131,173 @@ __global__ void __launch_bounds__(64 * G) local_attn_kernel(LocalArgs a) {
       hi = max(hi, (int64_t)__shfl_xor(hi, o, 64));
     }
     if (lane == 0) {
-      pos_lo = lo;
-      pos_hi = hi;
+      pos_range[0] = lo;
+      pos_range[1] = hi;
     }
   }
 
-  // Q^T operands and query positions for this lane's two columns.
-  u32x4_t Qb[2][4];
-  int qp[2];
-  bool qok[2];
-  int rel[2];  // (tile start) - (query position), refreshed per key tile
+  // Q^T operands and positions of this lane's two columns.
+  u32x4_t Qb[kNT][4];
+  int qp[kNT];
+  bool qok[kNT];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int64_t qi = qb + 16 * nt + col;
-    qok[nt] = qi < a.Lq;
-    qp[nt] = qok[nt] ? (int)(a.qpos ? a.qpos[qi] : qi) : 0;
+  for (int nt = 0; nt < kNT; ++nt) {
+    const int64_t qi = qb + (kNT * wave + nt) * QPT + col / GP;
+    qok[nt] = qi < a.Lq && gg < G;
+    qp[nt] = qi < a.Lq ? (int)(a.qpos ? a.qpos[qi] : qi) : 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       u32x4_t z = {0u, 0u, 0u, 0u};
       Qb[nt][j] = z;
       if (qok[nt])
         Qb[nt][j] = *reinterpret_cast<const u32x4_t*>(
-            a.q + ((b * a.Lq + qi) * a.Hq + hq) * 128 + 32 * j + 8 * grp);
+            a.q + ((b * a.Lq + qi) * a.Hq + h * G + gg) * 128 + 32 * j + 8 * grp);
     }
   }
   __syncthreads();
-  const int64_t plo = pos_lo, phi = pos_hi;
-  const int64_t klo = max(plo - a.W, (int64_t)0);
-  const int64_t khi = min(phi + a.W, a.Lk - 1);
-  int64_t kt0 = klo / 64, kt1 = khi / 64;
+  const int64_t plo = pos_range[0], phi = pos_range[1];
+  int64_t kt0 = max(plo - a.W, (int64_t)0) / 64;
+  int64_t kt1 = min(phi + a.W, a.Lk - 1) / 64;
   if (a.parts > 1) {
     const int64_t n = kt1 - kt0 + 1;
     const int64_t s0 = kt0 + n * part / a.parts;
     kt1 = kt0 + n * (part + 1) / a.parts - 1;
     kt0 = s0;
   }
+  const int ntiles = (int)max(kt1 - kt0 + 1, (int64_t)0);
+  const bool tab = ntiles <= kMaskTiles;
 
-  f32x4_t acc[2][8];
-  float m_run[2], l_run[2];
+  // DMA of key tile kt into ring slot `slot`: this wave's K instructions
+  // j = 2w, 2w + 1 (LDS units 64j + lane: row 4j + lane / 16, position
+  // lane % 16, holding part position ^ (row & 15)) and V^T instructions
+  // j = 2w, 2w + 1 (units 1024 + 64j + lane: row 8j + lane / 8, position
+  // lane % 8, holding part position ^ (row & 7)).  Rows past kv_len read the
+  // last row (their keys are masked; the tiled V is zero there).
+  const uint16_t* kbase = a.k + (b * a.Lk * a.Hkv + h) * (int64_t)128;
+  const int64_t kstride = (int64_t)a.Hkv * 128;
+  const uint16_t* vbase = a.vt + ((b * a.Hkv + h) * a.NTk) * (int64_t)(128 * 64);
+  // Per-lane parts of the DMA sources, tile-relative and 32-bit, against
+  // wave-uniform tile bases.
+  const int kr0 = 8 * wave + grp;  // K row of u = 0; u = 1 adds 4
+  const uint32_t kpart0 = (uint32_t)((col ^ (kr0 & 15)) * 8);
+  const uint32_t kpart1 = (uint32_t)((col ^ ((kr0 + 4) & 15)) * 8);
+  const int vr0 = 16 * wave + (lane >> 3);  // V^T row of u = 0; u = 1 adds 8
+  const uint32_t voff0 = (uint32_t)(vr0 * 64 + (((lane & 7) ^ (vr0 & 7)) * 8));
+  auto issue_tile = [&](int64_t kt, int slot) {
+    unsigned char* dst = ring + slot * kSlotBytes;
+    const uint16_t* kt_base = kbase + kt * 64 * kstride;  // uniform
+    const int last = (int)min((int64_t)63, a.Lk - 1 - kt * 64);
+    const uint32_t ks = (uint32_t)kstride;
+    __builtin_amdgcn_global_load_lds(kt_base + (uint32_t)min(kr0, last) * ks + kpart0,
+                                     (lds_void_t*)(dst + (2 * wave) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(kt_base + (uint32_t)min(kr0 + 4, last) * ks + kpart1,
+                                     (lds_void_t*)(dst + (2 * wave + 1) * 1024), 16, 0, 0);
+    const uint16_t* vt_base = vbase + kt * (128 * 64);      // uniform
+    __builtin_amdgcn_global_load_lds(vt_base + voff0, (lds_void_t*)(dst + 16384 + (2 * wave) * 1024),
+                                     16, 0, 0);
+    __builtin_amdgcn_global_load_lds(vt_base + voff0 + 8 * 64,
+                                     (lds_void_t*)(dst + 16384 + (2 * wave + 1) * 1024), 16, 0, 0);
+  };
+  // Valid-key words of the block's key tiles (when they fit the table),
+  // before the first DMA: waiting for these loads must not wait for it.
+  if (tab)
+    for (int t = wave; t < ntiles; t += kWaves) {
+      const uint64_t bits = tile_valid_bits(a, b, kt0 + t);
+      if (lane == 0) lds_write_u64(lds_addr(&valid_tab[t]), bits);
+    }
+  // Q^T operands and positions complete here, before any DMA is in flight:
+  // otherwise the compiler, tracking their loads into the loop, waits for
+  // every outstanding load (the DMA prefetch included) at each first use.
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < kNT; ++nt) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(Qb[nt][j]));
+    asm volatile("" : "+v"(qp[nt]));
+  }
+  for (int t = 0; t < kRing - 1 && t < ntiles; ++t) issue_tile(kt0 + t, t);
+
+  f32x4_t acc[kNT][8];
+  float m_run[kNT], l_run[kNT];
+#pragma unroll
+  for (int nt = 0; nt < kNT; ++nt) {
     m_run[nt] = neg_inf();
     l_run[nt] = 0.f;
 #pragma unroll
     for (int td = 0; td < 8; ++td) acc[nt][td] = zero4();
   }
 
-  // Uniform (scalar) tile bases plus 32-bit per-lane offsets keep the
-  // staging addresses out of the vector registers.
-  const uint16_t* kbase = a.k + (b * a.Lk) * (int64_t)a.Hkv * 128 + (int64_t)h * 128;
-  const uint16_t* vbase = a.vt + ((b * a.Hkv + h) * a.NTk) * (int64_t)(128 * 64);
-  const int kstride = a.Hkv * 128;
-  uint32_t goff[PER], loff[PER];
-  int krow[PER];
-#pragma unroll
-  for (int p = 0; p < PER; ++p) {
-    const int v = tid + p * NTHR;
-    if (v < 1024) {
-      const int s = v >> 4, part = v & 15;
-      goff[p] = (uint32_t)(s * kstride + part * 8);
-      loff[p] = (uint32_t)(s * kKPitch + part * 8);
-      krow[p] = s;
-    } else {
-      const int d = (v - 1024) >> 3, part = (v - 1024) & 7;
-      goff[p] = (uint32_t)((v - 1024) * 8);
-      loff[p] = (uint32_t)(64 * kKPitch + d * kVPitch + part * 8);
-      krow[p] = -1;
-    }
-  }
+  const uint32_t kofs0 = (uint32_t)(col * 128 + ((grp ^ col) * 8));
+  const uint32_t vofs0 = (uint32_t)(8192 + col * 64 + ((grp ^ (col & 7)) * 8));
+  const float c = a.scale_log2;
+  const int W32 = (int)a.W;
+  const uint64_t kLast = 1ull << 63;
 
-  u32x4_t pre[PER];
-  auto prefetch = [&](int64_t kt) {
-    const uint16_t* kt_base = kbase + kt * 64 * (int64_t)kstride;
-    const uint16_t* vt_base = vbase + kt * (128 * 64);
-    const int rows_left = (int)min((int64_t)64, a.Lk - kt * 64);
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-      const int v = tid + p * NTHR;
-      u32x4_t val = {0u, 0u, 0u, 0u};
-      if (v < 1024) {
-        if (krow[p] < rows_left) val = *reinterpret_cast<const u32x4_t*>(kt_base + goff[p]);
-      } else if (v < kStageVecs) {
-        val = *reinterpret_cast<const u32x4_t*>(vt_base + goff[p]);
-      }
-      pre[p] = val;
-    }
-  };
-  auto commit = [&]() {
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-      const int v = tid + p * NTHR;
-      if (v < kStageVecs) *reinterpret_cast<u32x4_t*>(Ks + loff[p]) = pre[p];
-    }
-  };
+  for (int t = 0; t < ntiles; ++t) {
+    // This wave's DMA of tile t has landed once at most the tiles issued
+    // after it (up to kRing - 2 of them, 4 instructions each) are pending.
+    const int later = max(0, min(kRing - 2, ntiles - 1 - t));
+    if (later >= 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if (later == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // (first pass: the valid table)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (t + kRing - 1 < ntiles) issue_tile(kt0 + t + kRing - 1, (t + kRing - 1) % kRing);
 
-  if (kt0 <= kt1) prefetch(kt0);
-  for (int64_t kt = kt0; kt <= kt1; ++kt) {
-    __syncthreads();
-    commit();
-    if (g == 0) {
-      const int64_t j = kt * 64 + lane;
-      bool inert = false;
-      if (j < a.Lk) {
-        if (a.key_valid && a.key_valid[b * a.Lk + j] == 0) inert = true;
-        if (a.inert_chunk > 0 && (j + 1) % a.inert_chunk == 0) inert = true;
-      }
-      const uint64_t ib = __ballot(inert);
-      const uint64_t rb = __ballot(j < a.Lk);
-      if (lane == 0) {
-        inert_bits = ib;
-        range_bits = rb;
-      }
-    }
-    __syncthreads();
-    if (kt < kt1) prefetch(kt + 1);
-
-    const uint64_t ibits = inert_bits, rbits = range_bits;
+    const int64_t kt = kt0 + t;
     const int64_t j0 = kt * 64;
-    rel[0] = (int)j0 - qp[0];
-    rel[1] = (int)j0 - qp[1];
-    const int W32 = (int)a.W;
+    const uint32_t sbase = lds_addr(ring + (t % kRing) * kSlotBytes);
+    // Keys of the tile: in range (rbits) and inert (ibits: failed key_valid
+    // or a landmark slot).
+    const int64_t left = a.Lk - j0;
+    const uint64_t rbits = left >= 64 ? ~0ull : ((1ull << left) - 1ull);
+    uint64_t vbits;
+    if (tab) {
+      vbits = uniform_u64(lds_read_u64(lds_addr(&valid_tab[t])));
+    } else {
+      vbits = tile_valid_bits(a, b, kt);
+    }
+    uint64_t ibits = ~vbits & rbits;
+    if (a.inert_chunk > 0) {
+      const int64_t jj = j0 + lane;
+      ibits |= __builtin_amdgcn_ballot_w64(jj < a.Lk && (jj + 1) % a.inert_chunk == 0);
+    }
+    ibits = uniform_u64(ibits);
     // Tiles entirely inside every query's window need no position mask.
     const bool full = (rbits == ~0ull) && (j0 >= phi - a.W) && (j0 + 63 <= plo + a.W);
+    // This lane's keys are 16 tt + 4 grp + i: bit 16 tt + i of the shifted
+    // words (immediate bit tests, nothing per element kept across tiles).
+    const uint64_t rsh = rbits >> (4 * grp), ish = ibits >> (4 * grp);
 
-    f32x4_t S[2][4];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) S[nt][t] = zero4();
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      u32x4_t Ka[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        Ka[t] = *reinterpret_cast<const u32x4_t*>(Ks + (16 * t + col) * kKPitch + 32 * j + 8 * grp);
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) S[nt][t] = mfma_bf16_16x16x32(Ka[t], Qb[nt][j], S[nt][t]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    // S^T of both column tiles, sharing each K operand read.
+    const uint32_t kaddr[4] = {sbase + 2 * (kofs0 ^ 0u), sbase + 2 * (kofs0 ^ 32u),
+                               sbase + 2 * (kofs0 ^ 64u), sbase + 2 * (kofs0 ^ 96u)};
+    f32x4_t S[kNT][4];
+    if constexpr (kNT == 2) qk_tile2<kDepth>(kaddr, Qb[0], Qb[kNT - 1], S[0], S[kNT - 1]);
+    else qk_tile<kDepth>(kaddr, Qb[0], S[0]);
+    const uint32_t vaddr[2] = {sbase + 2 * vofs0, sbase + 2 * (vofs0 ^ 32u)};
+    // The first V^T operands do not depend on P: read them now.
+    u32x4_t vb[16];
+    static_for<4>([&](auto oc) {
+      constexpr int o = decltype(oc)::value;
+      vb[o] = lds_read_b128<(o & 7) * 2048>(vaddr[o >> 3]);
+    });
 
-    // Logits in units of log2: s * scale_log2.  Keys outside the window (or
-    // past kv_len, or of an absent query) are -inf; inert keys inside it are
-    // exactly 0.  The scale is folded into one FMA before the exponential
-    // (scale_log2 > 0, so the maximum of the raw products is the maximum of
-    // the logits).
-    const float c = a.scale_log2;
-    const uint64_t kLast = 1ull << 63;
-    u32x4_t Pb[2][2];
+    u32x4_t Pb[kNT][2];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < kNT; ++nt) {
+      // Logits in units of log2: s * scale_log2.  Keys outside the window
+      // (or past kv_len, or of an absent column) are -inf; inert keys inside
+      // it are exactly 0.
       if (!full) {
+        const int rel = (int)j0 + 4 * grp - qp[nt];
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int s = 16 * t + 4 * grp + i;
-            const int dd = rel[nt] + s;
-            if (!((rbits >> s) & 1ull) || dd > W32 || dd < -W32 || !qok[nt])
-              S[nt][t][i] = neg_inf();
+            const int dd = rel + 16 * tt + i;
+            if (!((rsh >> (16 * tt + i)) & 1ull) || dd > W32 || dd < -W32 || !qok[nt])
+              S[nt][tt][i] = neg_inf();
           }
       }
       if (ibits == kLast) {
@@ -254,37 +305,35 @@ __global__ void __launch_bounds__(64 * G) local_attn_kernel(LocalArgs a) {
         if (grp == 3 && S[nt][3][3] != neg_inf()) S[nt][3][3] = 0.f;
       } else if (ibits != 0ull) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int s = 16 * t + 4 * grp + i;
-            if (((ibits >> s) & 1ull) && S[nt][t][i] != neg_inf()) S[nt][t][i] = 0.f;
-          }
+          for (int i = 0; i < 4; ++i)
+            if (((ish >> (16 * tt + i)) & 1ull) && S[nt][tt][i] != neg_inf()) S[nt][tt][i] = 0.f;
       }
       const float mx = across4_max(max16_raw(S[nt]));
       const float m_new = fmaxf(m_run[nt], mx * c);
-      // A column with no visible key yet keeps m = -inf; exponentiate against 0
-      // there so that every term (and alpha) is exp2(-inf) = 0.
+      // A column with no visible key yet keeps m = -inf; exponentiate against
+      // 0 there so that every term (and alpha) is exp2(-inf) = 0.
       const float m_use = m_new == neg_inf() ? 0.f : m_new;
       const float alpha = exp2_hw(m_run[nt] - m_use);
-      float pv[4][4];
-      float part[4];
+      float part4[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+      for (int tt = 0; tt < 4; ++tt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pv[t][i] = exp2_hw(__builtin_fmaf(S[nt][t][i], c, -m_use));
-        part[t] = (pv[t][0] + pv[t][1]) + (pv[t][2] + pv[t][3]);
+        for (int i = 0; i < 4; ++i)
+          S[nt][tt][i] = exp2_hw(__builtin_fmaf(S[nt][tt][i], c, -m_use));
+        part4[tt] = (S[nt][tt][0] + S[nt][tt][1]) + (S[nt][tt][2] + S[nt][tt][3]);
       }
-      const float rsum = across4_sum((part[0] + part[1]) + (part[2] + part[3]));
+      const float rsum = across4_sum((part4[0] + part4[1]) + (part4[2] + part4[3]));
       // Inert keys count in the denominator but carry zero V.
       if (ibits == kLast) {
-        if (grp == 3) pv[3][3] = 0.f;
+        if (grp == 3) S[nt][3][3] = 0.f;
       } else if (ibits != 0ull) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if ((ibits >> (16 * t + 4 * grp + i)) & 1ull) pv[t][i] = 0.f;
+            if ((ish >> (16 * tt + i)) & 1ull) S[nt][tt][i] = 0.f;
       }
       l_run[nt] = l_run[nt] * alpha + rsum;
       m_run[nt] = m_new;
@@ -294,35 +343,36 @@ __global__ void __launch_bounds__(64 * G) local_attn_kernel(LocalArgs a) {
       }
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        u32x4_t pb;
-        pb[0] = pack_bf16x2(pv[2 * jj][0], pv[2 * jj][1]);
-        pb[1] = pack_bf16x2(pv[2 * jj][2], pv[2 * jj][3]);
-        pb[2] = pack_bf16x2(pv[2 * jj + 1][0], pv[2 * jj + 1][1]);
-        pb[3] = pack_bf16x2(pv[2 * jj + 1][2], pv[2 * jj + 1][3]);
-        Pb[nt][jj] = pb;
+        Pb[nt][jj][0] = pack_bf16x2(S[nt][2 * jj][0], S[nt][2 * jj][1]);
+        Pb[nt][jj][1] = pack_bf16x2(S[nt][2 * jj][2], S[nt][2 * jj][3]);
+        Pb[nt][jj][2] = pack_bf16x2(S[nt][2 * jj + 1][0], S[nt][2 * jj + 1][1]);
+        Pb[nt][jj][3] = pack_bf16x2(S[nt][2 * jj + 1][2], S[nt][2 * jj + 1][3]);
       }
     }
-
-    // V^T rows hold each lane's eight reduction keys contiguously (tiled V
-    // layout), so one 16-byte read per operand.
-#pragma unroll
-    for (int td = 0; td < 8; ++td) {
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const u32x4_t Va =
-            *reinterpret_cast<const u32x4_t*>(Vs + (16 * td + col) * kVPitch + 32 * jj + 8 * grp);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) acc[nt][td] = mfma_bf16_16x16x32(Va, Pb[nt][jj], acc[nt][td]);
-      }
+    // O^T += V^T . P^T for both column tiles, sharing each V^T operand read,
+    // kDepth reads in flight.
+    static_for<kDepth - 4>([&](auto oc) {
+      constexpr int o = decltype(oc)::value + 4;
+      vb[o] = lds_read_b128<(o & 7) * 2048>(vaddr[o >> 3]);
+    });
+    static_for<16>([&](auto oc) {
+      constexpr int o = decltype(oc)::value;
+      lds_wait<(15 - o < kDepth - 1 ? 15 - o : kDepth - 1)>(vb[o]);
+      acc[0][o & 7] = mfma_bf16_16x16x32(vb[o], Pb[0][o >> 3], acc[0][o & 7]);
+      if constexpr (kNT == 2)
+        acc[kNT - 1][o & 7] = mfma_bf16_16x16x32(vb[o], Pb[kNT - 1][o >> 3], acc[kNT - 1][o & 7]);
+      if constexpr (o + kDepth < 16)
+        vb[o + kDepth] = lds_read_b128<((o + kDepth) & 7) * 2048>(vaddr[(o + kDepth) >> 3]);
       __builtin_amdgcn_sched_barrier(0);
-    }
+    });
   }
 
   if (a.parts > 1) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      if (!qok[nt]) continue;
-      const int64_t row = ((int64_t)part * a.B * a.Lq + b * a.Lq + qb + 16 * nt + col) * a.Hq + hq;
+    for (int nt = 0; nt < kNT; ++nt) {
+      const int64_t qi = qb + (kNT * wave + nt) * QPT + col / GP;
+      if (qi >= a.Lq || gg >= G) continue;
+      const int64_t row = ((int64_t)part * a.B * a.Lq + b * a.Lq + qi) * a.Hq + h * G + gg;
       float* prow = a.part_o + row * 128;
 #pragma unroll
       for (int td = 0; td < 8; ++td)
@@ -335,11 +385,11 @@ __global__ void __launch_bounds__(64 * G) local_attn_kernel(LocalArgs a) {
     return;
   }
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    if (!qok[nt]) continue;
-    const int64_t qi = qb + 16 * nt + col;
+  for (int nt = 0; nt < kNT; ++nt) {
+    const int64_t qi = qb + (kNT * wave + nt) * QPT + col / GP;
+    if (qi >= a.Lq || gg >= G) continue;
     const float inv = l_run[nt] > 0.f ? 1.f / l_run[nt] : 0.f;
-    uint16_t* orow = a.out + ((b * a.Lq + qi) * a.Hq + hq) * 128;
+    uint16_t* orow = a.out + ((b * a.Lq + qi) * a.Hq + h * G + gg) * 128;
 #pragma unroll
     for (int td = 0; td < 8; ++td) {
       u32x2_t o;
@@ -348,7 +398,7 @@ __global__ void __launch_bounds__(64 * G) local_attn_kernel(LocalArgs a) {
       *reinterpret_cast<u32x2_t*>(orow + 16 * td + 4 * grp) = o;
     }
     if (grp == 0)
-      a.lse[(b * a.Lq + qi) * a.Hq + hq] =
+      a.lse[(b * a.Lq + qi) * a.Hq + h * G + gg] =
           l_run[nt] > 0.f ? (m_run[nt] + log2f(l_run[nt])) * kLn2 : neg_inf();
   }
 }
@@ -382,10 +432,16 @@ __global__ void __launch_bounds__(256) local_merge_kernel(LocalArgs a, int64_t r
   if (d4 == 0) a.lse[row] = l > 0.f ? (M + log2f(l)) * kLn2 : neg_inf();
 }
 
-template <int G>
+template <int GP>
 int launch_local(const LocalArgs& a, hipStream_t s) {
-  dim3 grid((unsigned)((a.Lq + kQB - 1) / kQB), (unsigned)a.Hkv, (unsigned)(a.B * a.parts));
-  hipLaunchKernelGGL(local_attn_kernel<G>, grid, dim3(64 * G), 0, s, a);
+  constexpr int QB = kColTiles * (16 / GP);
+  const size_t smem = (size_t)kRing * kSlotBytes + kMaskTiles * 8 + 16;
+  auto kern = local_attn_kernel<GP>;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+    return MRSA_ERR_LAUNCH;
+  dim3 grid((unsigned)((a.Lq + QB - 1) / QB), (unsigned)a.Hkv, (unsigned)(a.B * a.parts));
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), smem, s, a);
   int st = mrsa_launch_status();
   if (st != MRSA_OK || a.parts == 1) return st;
   const int64_t rows = a.B * a.Lq * a.Hq;
@@ -425,6 +481,7 @@ int local_attention(const void* q, const void* k, const void* v_tiles, const uin
   a.Lk = kv_len;
   a.Hq = (int)q_heads;
   a.Hkv = (int)kv_heads;
+  a.G = (int)G;
   a.W = window;
   a.inert_chunk = inert_chunk;
   a.scale_log2 = sm_scale * kLog2e;
@@ -438,8 +495,11 @@ int local_attention(const void* q, const void* k, const void* v_tiles, const uin
   switch (G) {
     case 1: return launch_local<1>(a, s);
     case 2: return launch_local<2>(a, s);
+    case 3:
     case 4: return launch_local<4>(a, s);
-    case 7: return launch_local<7>(a, s);
+    case 5:
+    case 6:
+    case 7:
     case 8: return launch_local<8>(a, s);
     default: return MRSA_ERR_UNSUPPORTED;
   }

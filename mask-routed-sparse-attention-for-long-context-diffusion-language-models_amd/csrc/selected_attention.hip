@@ -35,6 +35,7 @@
 // ops/hils_token_score_gqa_tilelang.py:17-114) reuses the walk and the S^T
 // product and writes, per routed (query, slot), max over the group of q.k
 // times sm_scale for every key, -inf at the last slot and invalid keys.
+#include "chunk_tile.h"
 #include "mrsa_device.h"
 
 #include <type_traits>
@@ -77,7 +78,6 @@ using Split8 = Split<8, 3>;
 using Split8x2 = Split<8, 2>;
 using Split12 = Split<12, 2>;
 
-typedef __attribute__((address_space(3))) void lds_void_t;
 
 struct SelArgs {
   const uint16_t* q;
@@ -147,26 +147,6 @@ __host__ __device__ inline bool sel_layout_fits(const SelLayout& l, int R) {
   return l.total <= kMaxLds && l.p_end <= l.ring + (size_t)R * kSlotBytes;
 }
 
-// Matrix-operand reads from LDS with explicit waits.  With global->LDS DMA in
-// the same loop the compiler waits for every outstanding LDS read before each
-// use (lgkmcnt(0)); issuing the reads as asm and waiting with lgkmcnt(n) on
-// the value itself keeps eight reads in flight.  LDS reads complete in issue
-// order, so lgkmcnt(n) after a read followed by >= n later LDS reads
-// guarantees that read has landed (other LDS accesses only add to the count).
-template <int OFF>
-__device__ __forceinline__ u32x4_t lds_read_b128(uint32_t addr) {
-  u32x4_t r;
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
-  return r;
-}
-template <int N>
-__device__ __forceinline__ void lds_wait(u32x4_t& v) {
-  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "i"(N));
-}
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
 // Walk counters in LDS, accessed with asm so the compiler does not order
 // them behind the in-flight global->LDS DMA (it waits for vmcnt(0) before
 // any LDS atomic that may alias a DMA destination).
@@ -222,44 +202,6 @@ __device__ __forceinline__ void step_read(uint32_t own_addr, uint32_t mask_addr,
       : "memory");
 }
 
-__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return ((uint64_t)hi << 32) | lo;
-}
-
-template <int N, class F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
-}
-
-// S^T = K . Q^T for one column tile: 16 K operand reads from an LDS chunk slot
-// (swizzled rows, kaddr[j] = lane address of reduction step j) and 16
-// products, read o + 8 issued after product o so eight reads stay in flight.
-// DEPTH reads stay in flight (8 when registers allow, 4 for the 12-wave split).
-template <int DEPTH = 8>
-__device__ __forceinline__ void qk_tile(const uint32_t (&kaddr)[4], const u32x4_t (&Q)[4],
-                                        f32x4_t (&S)[4]) {
-#pragma unroll
-  for (int t = 0; t < 4; ++t) S[t] = zero4();
-  u32x4_t kb[16];
-  static_for<16>([&](auto oc) {
-    constexpr int o = decltype(oc)::value;
-    if constexpr (o < DEPTH) kb[o] = lds_read_b128<(o & 3) * 4096>(kaddr[o >> 2]);
-  });
-  static_for<16>([&](auto oc) {
-    constexpr int o = decltype(oc)::value;
-    lds_wait<(15 - o < DEPTH - 1 ? 15 - o : DEPTH - 1)>(kb[o]);
-    S[o & 3] = mfma_bf16_16x16x32(kb[o], Q[o >> 2], S[o & 3]);
-    if constexpr (o + DEPTH < 16)
-      kb[o + DEPTH] = lds_read_b128<((o + DEPTH) & 3) * 4096>(kaddr[(o + DEPTH) >> 2]);
-    __builtin_amdgcn_sched_barrier(0);
-  });
-}
 
 // LDS arrays the prologue fills (s_*, wr, comp_slot, misc) or uses as
 // scratch (p_*).

@@ -44,12 +44,12 @@ def _flash_window(window: int, skip_inert_slots: bool, chunk_size: int) -> int:
 
 
 def key_parts(batch: int, q_len: int, kv_heads: int, kv_len: int, flash_window: int) -> int:
-    """Workgroups per 32-query block of the window attention.  Long
+    """Workgroups per query block of the window attention.  Long
     sequences: one.  A short block (the cached block step: 32 queries, 4 KV
-    heads -> 4 workgroups over ~11 key tiles) splits its key tiles so that
+    heads -> 8 workgroups over ~11 key tiles) splits its key tiles so that
     about 64 workgroups run, at least one tile each."""
 
-    blocks = -(-q_len // 32) * kv_heads * batch
+    blocks = -(-q_len // 16) * kv_heads * batch  # 16 queries per workgroup (G = 7)
     if blocks >= 128 or blocks == 0:
         return 1
     tiles = (min(q_len, kv_len) + 2 * flash_window) // 64 + 2

@@ -88,8 +88,8 @@ def test_key_parts_heuristic():
     from mrsa.local_attention import key_parts
 
     assert key_parts(1, 16384, 4, 16384, 319) == 1
-    # Cached block step: 32 queries, window 319 -> 12 key tiles, 12 parts.
-    assert key_parts(1, 32, 4, 131072, 319) == 12
+    # Cached block step: 32 queries (8 workgroups), window 319 -> 8 parts.
+    assert key_parts(1, 32, 4, 131072, 319) == 8
     assert key_parts(1, 32, 4, 131072, 0) == 2
     assert key_parts(0, 32, 4, 4096, 319) == 1
 
