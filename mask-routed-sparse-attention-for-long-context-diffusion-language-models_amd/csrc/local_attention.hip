@@ -108,10 +108,19 @@ local_attn_kernel(LocalArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
-  const int64_t b = blockIdx.z % a.B;
-  const int part = (int)(blockIdx.z / a.B);
-  const int h = blockIdx.y;
-  const int64_t qb = (int64_t)blockIdx.x * QB;
+  // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin by
+  // linear id; renumber so that each XCD runs a contiguous range of query
+  // blocks of one head, whose key windows overlap in that XCD's L2.
+  const int64_t nx = gridDim.x, nyz = (int64_t)gridDim.y * gridDim.z;
+  const int64_t total = nx * nyz;
+  int64_t lin = blockIdx.x + nx * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
+  if (total % 8 == 0) lin = (lin % 8) * (total / 8) + lin / 8;
+  const int64_t qblock = lin % nx;
+  const int h = (int)((lin / nx) % gridDim.y);
+  const int64_t z = lin / (nx * gridDim.y);
+  const int64_t b = z % a.B;
+  const int part = (int)(z / a.B);
+  const int64_t qb = qblock * QB;
   const int G = a.G;
   const int gg = col % GP;
 
