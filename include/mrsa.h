@@ -49,6 +49,18 @@ int mrsa_fuse_hils_outputs_fwd(const void* remote_output, const void* local_outp
                                int64_t head_dim, void* stream);
 
 /*
+ * Backward of the output fusion.  Replaces _FuseHiLSOutputs.backward
+ * (ops/hils_bidir_output_fusion_tilelang.py:90-99, kernel _fusion_bwd :40-77).
+ *   local_output, grad_output:  bf16 [rows, head_dim]
+ *   local_weight:               bf16 [rows]
+ *   d_remote (out) = grad_output; d_local (out) = bf16(local_weight * grad);
+ *   d_weight (out): bf16 [rows] = bf16(sum_d grad * local) (fp32 sum)
+ */
+int mrsa_fuse_hils_outputs_bwd(const void* local_output, const void* local_weight,
+                               const void* grad_output, void* d_remote, void* d_local,
+                               void* d_weight, int64_t rows, int64_t head_dim, void* stream);
+
+/*
  * Landmark (mask-token) chunk-summary attention pool.
  * Replaces chunk_attn_pool_gqa (ops/chunk_attn_pool_gqa_tilelang.py:425-448):
  * the fused kernel _pool_gqa_fwd (:47-180) when groups > 1, and the compiled
@@ -171,6 +183,33 @@ int mrsa_route_weights_fwd(const void* scores, const int32_t* indices, const flo
                            float temperature, int has_gate_offset, float gate_offset,
                            int has_gate_scale, float gate_scale, void* remote_weights,
                            void* local_weight, void* stream);
+
+/*
+ * Backward of the route weights; the row logits are recomputed from the
+ * forward inputs.  Replaces _RouteWeights.backward
+ * (ops/hils_bidir_route_weights_tilelang.py:185-242, kernel _route_weights_bwd
+ * :97-166; plain form, there at temperature 1) and the autograd of
+ * _route_weights_torch (dream_dllm_hils/attention.py:126-235) in both forms.
+ *   forward inputs and options: as mrsa_route_weights_fwd
+ *   grad_remote: bf16 [batch, seq_len, kv_heads * groups, topk]
+ *   grad_local:  bf16 [batch, seq_len, kv_heads * groups], or NULL for zeros
+ *   d_scores (out):    fp32 [batch, seq_len, kv_heads * groups, topk]
+ *                      (0 at invalid chunk indices)
+ *   d_bias (in/out):   fp32 [batch, chunks, kv_heads, groups], caller-zeroed;
+ *                      each valid selected entry's gradient is added atomically
+ *   d_local_lse (out): fp32 [batch, seq_len, kv_heads * groups]
+ *   d_gate (in/out):   fp32 [2] = {d gate_scale, d gate_offset}, caller-zeroed;
+ *                      may be NULL when neither gate option is set
+ * Rows whose outputs are constant (every logit masked; the affine form with
+ * no valid chunk) get zero gradients.
+ */
+int mrsa_route_weights_bwd(const void* scores, const int32_t* indices, const float* prior_bias,
+                           const float* local_lse, const void* grad_remote,
+                           const void* grad_local, int64_t batch, int64_t seq_len,
+                           int64_t chunks, int64_t kv_heads, int64_t groups, int64_t topk,
+                           float temperature, int has_gate_offset, float gate_offset,
+                           int has_gate_scale, float gate_scale, float* d_scores,
+                           float* d_bias, float* d_local_lse, float* d_gate, void* stream);
 
 /*
  * Re-lays V out as 64-key tiles, each stored transposed (head_dim rows of 64

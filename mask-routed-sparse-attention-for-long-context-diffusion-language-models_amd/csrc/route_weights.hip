@@ -188,3 +188,185 @@ extern "C" int mrsa_route_weights_fwd(const void* scores, const int32_t* indices
   if (lanes <= 4) return go(std::integral_constant<int, 4>{});
   return go(std::integral_constant<int, 8>{});
 }
+
+namespace {
+
+// Backward of the route weights with the forward's work split (LPR lanes per
+// (token, query head) row, 8 slots per lane); the row's logits and
+// probabilities are recomputed rather than saved.
+//   plain form (the TileLang backward, ops/hils_bidir_route_weights_tilelang.py:97-166,
+//   generalised to temperature T):  dz = p (g - sum p g),  d logit = dz / T,
+//     d local_lse = dz_local / T, d gate_offset = -d local_lse
+//   affine form (autograd of _route_weights_torch, attention.py:180-214):
+//     q = softmax(remote / T), mass = sigmoid(s (lse(remote / T) - local / T) + o)
+//     dm = sum g_j q_j - g_local,  dgate = dm mass (1 - mass)
+//     dz_j = q_j (g_j mass - sum_k q_k g_k mass) + dgate s q_j,  d remote_j = dz_j / T
+//     d local_lse = -dgate s / T,  d s = sum dgate (lse - local / T),  d o = sum dgate
+// Rows whose outputs are constant (every logit masked; affine form with no
+// routed chunk) get zero gradients.  Gradients of the selected bias entries
+// are added atomically into d_bias, and the gate gradients into d_gate[0..1]
+// once per wave; both are zeroed by the caller.
+template <int LPR>
+__global__ void __launch_bounds__(256)
+    route_weights_bwd_kernel(const uint16_t* __restrict__ scores,
+                             const int32_t* __restrict__ indices, const float* __restrict__ bias,
+                             const float* __restrict__ lse, const uint16_t* __restrict__ g_rw,
+                             const uint16_t* __restrict__ g_lw, int64_t rows, int64_t L, int64_t C,
+                             int Hkv, int G, int K, float inv_t, int has_off, float off,
+                             int affine, float gscale, float* __restrict__ d_scores,
+                             float* __restrict__ d_bias, float* __restrict__ d_lse,
+                             float* __restrict__ d_gate) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int part = (int)(t % LPR);
+  const int64_t r0 = t / LPR;
+  const bool live = r0 < rows;
+  const int64_t r = live ? r0 : rows - 1;  // lanes past the end join the reductions
+  const int Hq = Hkv * G;
+  const int hq = (int)(r % Hq);
+  const int64_t bl = r / Hq;
+  const int64_t b = bl / L;
+  const int hk = hq / G, g = hq - hk * G;
+  const int k0 = part * 8;
+  const int32_t* ix = indices + (bl * Hkv + hk) * K + k0;
+
+  int32_t iv[8];
+  float x[8], gr[8];
+  float rmax = neg_inf();
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const bool in = k0 + j < K;
+    iv[j] = in ? ix[j] : -1;
+    gr[j] = in ? bf16_to_f32(g_rw[r * K + k0 + j]) : 0.f;
+    float v = neg_inf();
+    if (in && iv[j] >= 0 && iv[j] < C)
+      v = (bf16_to_f32(scores[r * K + k0 + j]) + bias[((b * C + iv[j]) * Hkv + hk) * G + g]) *
+          inv_t;
+    x[j] = v;
+    rmax = fmaxf(rmax, v);
+  }
+#pragma unroll
+  for (int o = 1; o < LPR; o <<= 1) rmax = fmaxf(rmax, __shfl_xor(rmax, o, 64));
+  float local = lse[r];
+  if (has_off && !affine) local -= off;
+  local *= inv_t;
+  const float gl = g_lw ? bf16_to_f32(g_lw[r]) : 0.f;
+
+  // Branches are row-uniform, so the lane reductions inside stay within
+  // active lanes.
+  float dloc = 0.f, dscale = 0.f, doff = 0.f;
+  const float m = fmaxf(rmax, local);
+  if (m == neg_inf() || (affine && rmax == neg_inf())) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = 0.f;
+  } else if (!affine) {
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      x[j] = x[j] == neg_inf() ? 0.f : expf(x[j] - m);
+      sum += x[j];
+    }
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    const float el = local == neg_inf() ? 0.f : expf(local - m);
+    sum += el;
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      x[j] /= sum;
+      dot += x[j] * gr[j];
+    }
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) dot += __shfl_xor(dot, o, 64);
+    const float pl = el / sum;
+    dot += pl * gl;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = x[j] * (gr[j] - dot) * inv_t;
+    dloc = pl * (gl - dot) * inv_t;
+    doff = has_off ? -dloc : 0.f;
+  } else {
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      x[j] = x[j] == neg_inf() ? 0.f : expf(x[j] - rmax);
+      sum += x[j];
+    }
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    const float rl = rmax + logf(sum);
+    const float gate = gscale * (rl - local) + (has_off ? off : 0.f);
+    const float mass = 1.f / (1.f + expf(-gate));
+    float qg = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      x[j] /= sum;
+      qg += x[j] * gr[j];
+    }
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) qg += __shfl_xor(qg, o, 64);
+    const float dgate = (qg - gl) * mass * (1.f - mass);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = x[j] * ((gr[j] - qg) * mass + dgate * gscale) * inv_t;
+    dloc = -dgate * gscale * inv_t;
+    dscale = dgate * (rl - local);
+    doff = has_off ? dgate : 0.f;
+  }
+  if (live) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (k0 + j >= K) continue;
+      const bool valid = iv[j] >= 0 && iv[j] < C;
+      d_scores[r * K + k0 + j] = valid ? x[j] : 0.f;
+      if (valid && x[j] != 0.f) atomicAdd(&d_bias[((b * C + iv[j]) * Hkv + hk) * G + g], x[j]);
+    }
+    if (part == 0) d_lse[r] = dloc;
+  }
+  if (d_gate) {
+    const bool mine = live && part == 0;
+    dscale = wave_sum(mine ? dscale : 0.f);
+    doff = wave_sum(mine ? doff : 0.f);
+    if ((threadIdx.x & 63) == 0) {
+      if (affine) atomicAdd(&d_gate[0], dscale);
+      if (has_off) atomicAdd(&d_gate[1], doff);
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int mrsa_route_weights_bwd(const void* scores, const int32_t* indices,
+                                      const float* prior_bias, const float* local_lse,
+                                      const void* grad_remote, const void* grad_local,
+                                      int64_t batch, int64_t seq_len, int64_t chunks,
+                                      int64_t kv_heads, int64_t groups, int64_t topk,
+                                      float temperature, int has_gate_offset, float gate_offset,
+                                      int has_gate_scale, float gate_scale, float* d_scores,
+                                      float* d_bias, float* d_local_lse, float* d_gate,
+                                      void* stream) {
+  if (batch < 0 || seq_len < 0 || chunks <= 0 || kv_heads <= 0 || groups <= 0 || topk <= 0 ||
+      !(temperature > 0.f))
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (topk > kMaxTopk) return MRSA_ERR_UNSUPPORTED;
+  const int64_t rows = batch * seq_len * kv_heads * groups;
+  if (rows == 0) return MRSA_OK;
+  if (!scores || !indices || !prior_bias || !local_lse || !grad_remote || !d_scores || !d_bias ||
+      !d_local_lse || ((has_gate_scale || has_gate_offset) && !d_gate))
+    return MRSA_ERR_INVALID_ARGUMENT;
+  hipStream_t s = (hipStream_t)stream;
+  const int lanes = (int)((topk + 7) / 8);
+  auto go = [&](auto lpr) {
+    constexpr int LPR = decltype(lpr)::value;
+    const int64_t blocks = (rows * LPR + 255) / 256;
+    if (blocks > 0x7fffffff) return (int)MRSA_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(route_weights_bwd_kernel<LPR>, dim3((unsigned)blocks), dim3(256), 0, s,
+                       (const uint16_t*)scores, indices, prior_bias, local_lse,
+                       (const uint16_t*)grad_remote, (const uint16_t*)grad_local, rows, seq_len,
+                       chunks, (int)kv_heads, (int)groups, (int)topk, 1.f / temperature,
+                       has_gate_offset, gate_offset, has_gate_scale, gate_scale, d_scores, d_bias,
+                       d_local_lse, (has_gate_scale || has_gate_offset) ? d_gate : nullptr);
+    return mrsa_launch_status();
+  };
+  if (lanes <= 1) return go(std::integral_constant<int, 1>{});
+  if (lanes <= 2) return go(std::integral_constant<int, 2>{});
+  if (lanes <= 4) return go(std::integral_constant<int, 4>{});
+  return go(std::integral_constant<int, 8>{});
+}

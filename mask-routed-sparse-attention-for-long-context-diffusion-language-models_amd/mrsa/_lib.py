@@ -31,6 +31,7 @@ SIGNATURES = {
     "mrsa_status_string": (ctypes.c_char_p, [_I]),
     "mrsa_abi_version": (_I, []),
     "mrsa_fuse_hils_outputs_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _P]),
+    "mrsa_fuse_hils_outputs_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P]),
     "mrsa_chunk_attn_pool_gqa_fwd": (
         _I,
         [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _P, _P, _P, _P, _P],
@@ -52,6 +53,11 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _F, _I, _F,
          _P, _P, _P],
+    ),
+    "mrsa_route_weights_bwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _F, _I, _F,
+         _P, _P, _P, _P, _P],
     ),
     "mrsa_value_tiles_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "mrsa_value_tiles": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P]),

@@ -205,8 +205,13 @@ def route_weights(scores, indices, prior_bias, local_lse, *, temperature=1.0,
 
     scores [B, L, Hq, K] (bf16 values), indices [B, L, Hkv, K], prior_bias
     [B, C, Hkv, G], local_lse [B, L, Hq].  Returns (remote [B, L, Hq, K],
-    local [B, L, Hq]) before the bf16 rounding.
+    local [B, L, Hq]) before the bf16 rounding.  Differentiable: gate_offset
+    and gate_scale may be 0-d tensors, whose gradients autograd then forms
+    (the reference's own backward for this function is its autograd).
     """
+
+    def gate_value(x):
+        return x.float().reshape(()) if isinstance(x, torch.Tensor) else float(x)
 
     B, L, Hq, K = scores.shape
     _, C, Hkv, G = prior_bias.shape
@@ -219,14 +224,14 @@ def route_weights(scores, indices, prior_bias, local_lse, *, temperature=1.0,
     local_logits = local_lse.float()[..., None]
     affine = gate_scale is not None
     if gate_offset is not None and not affine:
-        local_logits = local_logits - float(gate_offset)
+        local_logits = local_logits - gate_value(gate_offset)
     logits = torch.cat((remote_logits, local_logits), dim=-1) / float(temperature)
     all_masked = torch.isneginf(logits).all(dim=-1, keepdim=True)
     logits = torch.where(all_masked, torch.zeros_like(logits), logits)
     if affine:
         remote_lse = torch.logsumexp(logits[..., :K], dim=-1)
-        gate = float(gate_scale) * (remote_lse - logits[..., K]) + (
-            float(gate_offset) if gate_offset is not None else 0.0)
+        gate = gate_value(gate_scale) * (remote_lse - logits[..., K]) + (
+            gate_value(gate_offset) if gate_offset is not None else 0.0)
         mass = torch.sigmoid(gate)
         internal = torch.softmax(remote_logits / float(temperature), dim=-1)
         internal = torch.where((~valid).all(dim=-1, keepdim=True), torch.zeros_like(internal), internal)

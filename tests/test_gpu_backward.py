@@ -1,0 +1,143 @@
+"""GPU parity of the backward kernels against the oracle's autograd.
+
+Route weights: the kernel recomputes the row probabilities in fp32, as the
+oracle's forward does, so gradients agree to fp32 rounding (plus the order of
+the atomic bias sums); d_scores is returned in bf16 like the reference's
+``d_scores.to(score_dtype)``.  Fusion: d_remote and d_local bit-exact, d_weight
+within one bf16 rounding of the fp32 sum.
+"""
+
+import pytest
+import torch
+
+import mrsa
+from mrsa.fusion import fuse_hils_outputs_backward
+from mrsa.route_weights import route_weights_backward
+from oracle import mrsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def _case(seed, B, L, Hkv, G, K, C):
+    g = torch.Generator().manual_seed(seed)
+    scores = (torch.randn(B, L, Hkv * G, K, generator=g) * 2).bfloat16()
+    idx = torch.randint(0, C, (B, L, Hkv, K), generator=g).int()
+    idx[0, 3, 1 % Hkv, K // 2:] = -1
+    idx[0, 4, 0, 0] = C + 5
+    bias = torch.rand(B, C, Hkv, G, generator=g) + 1.0
+    lse = torch.randn(B, L, Hkv * G, generator=g) + 2.0
+    g_rw = torch.randn(B, L, Hkv * G, K, generator=g).bfloat16()
+    g_lw = torch.randn(B, L, Hkv * G, generator=g).bfloat16()
+    return scores, idx, bias, lse, g_rw, g_lw
+
+
+def _oracle_grads(scores, idx, bias, lse, g_rw, g_lw, gate_offset=None, gate_scale=None, T=1.0):
+    s = scores.float().requires_grad_(True)
+    b = bias.clone().requires_grad_(True)
+    l = lse.clone().requires_grad_(True)
+    go = None if gate_offset is None else torch.tensor(gate_offset, requires_grad=True)
+    gs = None if gate_scale is None else torch.tensor(gate_scale, requires_grad=True)
+    rw, lw = O.route_weights(s, idx, b, l, temperature=T, gate_offset=go, gate_scale=gs)
+    (rw * g_rw.float()).sum().add_((lw * g_lw.float()).sum()).backward()
+    return (s.grad, b.grad, l.grad, None if gs is None else gs.grad,
+            None if go is None else go.grad)
+
+
+def _close(got, exp, what, atol=1e-5, rtol=1e-4):
+    torch.testing.assert_close(got.cpu().float(), exp.float(), atol=atol, rtol=rtol, msg=what)
+
+
+@pytest.mark.parametrize("form,K,T", [("plain", 31, 1.0), ("plain", 32, 0.7), ("offset", 32, 1.0),
+                                      ("affine", 32, 1.0), ("affine", 20, 1.4), ("affine", 64, 0.8)])
+def test_route_weights_backward_vs_oracle(form, K, T):
+    _note(f"route weights bwd form={form} K={K} T={T}")
+    B, L, Hkv, G, C = 1, 300, 4, 7, 96
+    scores, idx, bias, lse, g_rw, g_lw = _case(40 + K, B, L, Hkv, G, K, C)
+    off = {"plain": None, "offset": 0.35, "affine": -0.25}[form]
+    scale = 0.9 if form == "affine" else None
+    d_s, d_b, d_l, d_g = route_weights_backward(
+        scores.to(DEV), idx.to(DEV), bias.to(DEV), lse.to(DEV), g_rw.to(DEV), g_lw.to(DEV),
+        temperature=T, gate_offset=off, gate_scale=scale)
+    e_s, e_b, e_l, e_gs, e_go = _oracle_grads(scores, idx, bias, lse, g_rw, g_lw, off, scale, T)
+    _close(d_s, e_s, "d_scores")
+    _close(d_b, e_b, "d_bias", atol=5e-5, rtol=2e-4)
+    _close(d_l, e_l, "d_local_lse")
+    if scale is not None:
+        assert abs(float(d_g[0]) - float(e_gs)) <= 1e-3 * max(1.0, abs(float(e_gs)))
+    if off is not None:
+        assert abs(float(d_g[1]) - float(e_go)) <= 1e-3 * max(1.0, abs(float(e_go)))
+
+
+def test_route_weights_backward_masked_rows_are_zero():
+    _note("route weights bwd masked rows")
+    B, L, Hkv, G, K, C = 1, 8, 2, 7, 8, 16
+    scores, idx, bias, lse, g_rw, g_lw = _case(77, B, L, Hkv, G, K, C)
+    idx[0, 2, 0, :] = -1                       # no valid chunk: affine rows constant
+    lse[0, 2, :G] = float("-inf")              # and the plain rows fully masked
+    idx[0, 5, 1, :] = -1                       # no valid chunk, finite local
+    for kw in (dict(), dict(gate_offset=0.1, gate_scale=1.1)):
+        d_s, d_b, d_l, _ = route_weights_backward(
+            scores.to(DEV), idx.to(DEV), bias.to(DEV), lse.to(DEV), g_rw.to(DEV), g_lw.to(DEV),
+            **kw)
+        assert torch.isfinite(d_s).all() and torch.isfinite(d_l).all()
+        assert float(d_s[0, 2, :G].abs().sum()) == 0.0 and float(d_l[0, 2, :G].abs().sum()) == 0.0
+        assert float(d_s[0, 5, G:].abs().sum()) == 0.0
+        e_s, e_b, e_l, _, _ = _oracle_grads(scores, idx, bias, lse, g_rw, g_lw,
+                                            kw.get("gate_offset"), kw.get("gate_scale"))
+        _close(d_s, torch.nan_to_num(e_s), "d_scores")
+        _close(d_l, torch.nan_to_num(e_l), "d_local_lse")
+        _close(d_b, e_b, "d_bias", atol=5e-5, rtol=2e-4)
+
+
+@pytest.mark.parametrize("affine", [False, True])
+def test_route_weights_autograd_api(affine):
+    _note(f"route weights autograd affine={affine}")
+    B, L, Hkv, G, K, C = 1, 64, 2, 7, 31 if not affine else 32, 40
+    scores, idx, bias, lse, g_rw, g_lw = _case(90, B, L, Hkv, G, K, C)
+    s = scores.to(DEV).requires_grad_(True)
+    b = bias.to(DEV).requires_grad_(True)
+    l = lse.to(DEV).requires_grad_(True)
+    if affine:
+        gs = torch.tensor(0.8, device=DEV, requires_grad=True)
+        go = torch.tensor(0.2, device=DEV, requires_grad=True)
+        rw, lw = mrsa.route_weights_torch(s, idx.to(DEV), b, l, temperature=1.0,
+                                          gate_offset=go, gate_scale=gs)
+    else:
+        rw, lw = mrsa.route_weights(s, idx.to(DEV), b, l)
+    (rw.float() * g_rw.to(DEV).float()).sum().add_((lw.float() * g_lw.to(DEV).float()).sum()).backward()
+    e_s, e_b, e_l, e_gs, e_go = _oracle_grads(scores, idx, bias, lse, g_rw, g_lw,
+                                              0.2 if affine else None, 0.8 if affine else None)
+    assert s.grad.dtype == torch.bfloat16 and b.grad.dtype == torch.float32
+    _close(s.grad, e_s.bfloat16(), "scores.grad", atol=1e-5, rtol=8e-3)
+    _close(b.grad, e_b, "prior_bias.grad", atol=5e-5, rtol=2e-4)
+    _close(l.grad, e_l, "local_lse.grad")
+    if affine:
+        assert abs(float(gs.grad) - float(e_gs)) <= 1e-3 * max(1.0, abs(float(e_gs)))
+        assert abs(float(go.grad) - float(e_go)) <= 1e-3 * max(1.0, abs(float(e_go)))
+
+
+@pytest.mark.parametrize("D", [128, 64, 256, 40])
+def test_fusion_backward_vs_oracle(D):
+    _note(f"fusion bwd D={D}")
+    g = torch.Generator().manual_seed(D)
+    shape = (2, 97, 5, D)
+    r = torch.randn(*shape, generator=g).bfloat16()
+    lo = torch.randn(*shape, generator=g).bfloat16()
+    w = torch.rand(*shape[:-1], generator=g).bfloat16()
+    go = torch.randn(*shape, generator=g).bfloat16()
+    rr, ll, ww = (x.clone().requires_grad_(True) for x in (r, lo, w))
+    O.fuse_outputs(rr, ll, ww).backward(go)
+    d_r, d_l, d_w = fuse_hils_outputs_backward(lo.to(DEV), w.to(DEV), go.to(DEV))
+    assert torch.equal(d_r.cpu(), rr.grad)
+    assert torch.equal(d_l.cpu(), ll.grad)
+    torch.testing.assert_close(d_w.cpu().float(), ww.grad.float(), atol=1e-6, rtol=8e-3)
+    # Through the autograd API.
+    a, b_, c = (x.to(DEV).requires_grad_(True) for x in (r, lo, w))
+    mrsa.fuse_hils_outputs(a, b_, c).backward(go.to(DEV))
+    assert torch.equal(a.grad.cpu(), rr.grad) and torch.equal(b_.grad.cpu(), ll.grad)
+    torch.testing.assert_close(c.grad.cpu().float(), ww.grad.float(), atol=1e-6, rtol=8e-3)

@@ -1,0 +1,168 @@
+"""Pins of the oracle's backward (its torch autograd) against closed forms.
+
+The reference's route-weights backward kernel
+(ops/hils_bidir_route_weights_tilelang.py:131-160) states the plain-form
+gradient as d_logit = p * (g - sum_j p_j g_j), scattered into the bias by
+chunk index; the fusion backward (ops/hils_bidir_output_fusion_tilelang.py:55-71)
+as d_local = w g, d_weight = sum_d g l.  The affine form has no kernel in
+the reference (its backward is autograd); it is pinned here by a
+hand-derived chain rule and by central differences.
+"""
+
+import math
+
+import torch
+
+from oracle import mrsa_oracle as O
+
+
+def _inputs(seed, B=1, L=4, H=2, G=3, K=5, C=9):
+    g = torch.Generator().manual_seed(seed)
+    scores = torch.randn(B, L, H * G, K, generator=g).bfloat16()
+    idx = torch.randint(0, C, (B, L, H, K), generator=g)
+    idx[0, 1, 0, 3:] = -1
+    idx[0, L - 1, H - 1, 0] = C + 2  # out of range: masked like -1
+    bias = torch.rand(B, C, H, G, generator=g)
+    lse = torch.randn(B, L, H * G, generator=g)
+    g_rw = torch.randn(B, L, H * G, K, generator=g)
+    g_lw = torch.randn(B, L, H * G, generator=g)
+    return scores, idx, bias, lse, g_rw, g_lw
+
+
+def _autograd(scores, idx, bias, lse, g_rw, g_lw, **kw):
+    s = scores.float().requires_grad_(True)
+    b = bias.clone().requires_grad_(True)
+    l = lse.clone().requires_grad_(True)
+    rw, lw = O.route_weights(s, idx, b, l, **kw)
+    (rw * g_rw).sum().add_((lw * g_lw).sum()).backward()
+    return s.grad, b.grad, l.grad
+
+
+def test_plain_backward_matches_reference_kernel_formula():
+    T, off = 0.7, 0.3
+    scores, idx, bias, lse, g_rw, g_lw = _inputs(3)
+    ds, db, dl = _autograd(scores, idx, bias, lse, g_rw, g_lw, temperature=T, gate_offset=off)
+    B, L, Hq, K = scores.shape
+    _, C, H, G = bias.shape
+    eds = torch.zeros(B, L, Hq, K, dtype=torch.float64)
+    edb = torch.zeros(B, C, H, G, dtype=torch.float64)
+    edl = torch.zeros(B, L, Hq, dtype=torch.float64)
+    for b in range(B):
+        for t in range(L):
+            for hq in range(Hq):
+                h, gg = divmod(hq, G)
+                logit = []
+                for j in range(K):
+                    c = int(idx[b, t, h, j])
+                    ok = 0 <= c < C
+                    logit.append((float(scores[b, t, hq, j]) + float(bias[b, c, h, gg])) / T
+                                 if ok else -math.inf)
+                logit.append((float(lse[b, t, hq]) - off) / T)
+                m = max(logit)
+                e = [math.exp(x - m) if x > -math.inf else 0.0 for x in logit]
+                p = [x / sum(e) for x in e]
+                gr = [float(g_rw[b, t, hq, j]) for j in range(K)] + [float(g_lw[b, t, hq])]
+                delta = sum(pi * gi for pi, gi in zip(p, gr))
+                dlogit = [pi * (gi - delta) / T for pi, gi in zip(p, gr)]
+                for j in range(K):
+                    c = int(idx[b, t, h, j])
+                    if 0 <= c < C:
+                        eds[b, t, hq, j] = dlogit[j]
+                        edb[b, c, h, gg] += dlogit[j]
+                edl[b, t, hq] = dlogit[K]
+    torch.testing.assert_close(ds.double(), eds, atol=2e-6, rtol=1e-5)
+    torch.testing.assert_close(db.double(), edb, atol=2e-6, rtol=1e-5)
+    torch.testing.assert_close(dl.double(), edl, atol=2e-6, rtol=1e-5)
+
+
+def test_affine_backward_matches_chain_rule():
+    T, sc, off = 1.3, 0.8, -0.2
+    scores, idx, bias, lse, g_rw, g_lw = _inputs(5)
+    gs = torch.tensor(sc, requires_grad=True)
+    go = torch.tensor(off, requires_grad=True)
+    s = scores.float().requires_grad_(True)
+    b = bias.clone().requires_grad_(True)
+    l = lse.clone().requires_grad_(True)
+    rw, lw = O.route_weights(s, idx, b, l, temperature=T, gate_offset=go, gate_scale=gs)
+    (rw * g_rw).sum().add_((lw * g_lw).sum()).backward()
+    B, L, Hq, K = scores.shape
+    _, C, H, G = bias.shape
+    eds = torch.zeros(B, L, Hq, K, dtype=torch.float64)
+    edl = torch.zeros(B, L, Hq, dtype=torch.float64)
+    dscale = doff = 0.0
+    for t in range(L):
+        for hq in range(Hq):
+            h, gg = divmod(hq, G)
+            x = []
+            for j in range(K):
+                c = int(idx[0, t, h, j])
+                x.append((float(scores[0, t, hq, j]) + float(bias[0, c, h, gg])) / T
+                         if 0 <= c < C else -math.inf)
+            loc = float(lse[0, t, hq]) / T
+            m = max(x)
+            e = [math.exp(v - m) if v > -math.inf else 0.0 for v in x]
+            q = [v / sum(e) for v in e]
+            rl = m + math.log(sum(e))
+            mass = 1.0 / (1.0 + math.exp(-(sc * (rl - loc) + off)))
+            gr = [float(g_rw[0, t, hq, j]) for j in range(K)]
+            dm = sum(qi * gi for qi, gi in zip(q, gr)) - float(g_lw[0, t, hq])
+            dgate = dm * mass * (1 - mass)
+            dq = [gi * mass for gi in gr]
+            qdq = sum(qi * di for qi, di in zip(q, dq))
+            for j in range(K):
+                eds[0, t, hq, j] = (q[j] * (dq[j] - qdq) + dgate * sc * q[j]) / T
+            edl[0, t, hq] = -dgate * sc / T
+            dscale += dgate * (rl - loc)
+            doff += dgate
+    torch.testing.assert_close(s.grad.double(), eds, atol=2e-6, rtol=1e-5)
+    torch.testing.assert_close(l.grad.double(), edl, atol=2e-6, rtol=1e-5)
+    assert abs(float(gs.grad) - dscale) < 1e-4 * max(1.0, abs(dscale))
+    assert abs(float(go.grad) - doff) < 1e-4 * max(1.0, abs(doff))
+
+
+def test_affine_backward_central_differences():
+    scores, idx, bias, lse, g_rw, g_lw = _inputs(8, L=2, H=1, G=2, K=4, C=6)
+
+    def loss(bias_, lse_, gs_, go_):
+        rw, lw = O.route_weights(scores, idx, bias_, lse_, temperature=0.9,
+                                 gate_offset=go_, gate_scale=gs_)
+        return float((rw.double() * g_rw).sum() + (lw.double() * g_lw).sum())
+
+    b = bias.clone().requires_grad_(True)
+    l = lse.clone().requires_grad_(True)
+    gs = torch.tensor(1.2, requires_grad=True)
+    go = torch.tensor(0.4, requires_grad=True)
+    rw, lw = O.route_weights(scores, idx, b, l, temperature=0.9, gate_offset=go, gate_scale=gs)
+    (rw * g_rw).sum().add_((lw * g_lw).sum()).backward()
+    eps = 1e-2
+    for flat in range(bias.numel()):
+        bp, bm = bias.clone(), bias.clone()
+        bp.view(-1)[flat] += eps
+        bm.view(-1)[flat] -= eps
+        fd = (loss(bp, lse, 1.2, 0.4) - loss(bm, lse, 1.2, 0.4)) / (2 * eps)
+        assert abs(fd - float(b.grad.view(-1)[flat])) < 2e-3, flat
+    for flat in range(lse.numel()):
+        lp, lm = lse.clone(), lse.clone()
+        lp.view(-1)[flat] += eps
+        lm.view(-1)[flat] -= eps
+        fd = (loss(bias, lp, 1.2, 0.4) - loss(bias, lm, 1.2, 0.4)) / (2 * eps)
+        assert abs(fd - float(l.grad.view(-1)[flat])) < 2e-3, flat
+    fd = (loss(bias, lse, 1.2 + eps, 0.4) - loss(bias, lse, 1.2 - eps, 0.4)) / (2 * eps)
+    assert abs(fd - float(gs.grad)) < 2e-3
+    fd = (loss(bias, lse, 1.2, 0.4 + eps) - loss(bias, lse, 1.2, 0.4 - eps)) / (2 * eps)
+    assert abs(fd - float(go.grad)) < 2e-3
+
+
+def test_fusion_backward_matches_reference_kernel_formula():
+    g = torch.Generator().manual_seed(2)
+    r = torch.randn(2, 3, 4, 16, generator=g).bfloat16()
+    lo = torch.randn(2, 3, 4, 16, generator=g).bfloat16()
+    w = torch.rand(2, 3, 4, generator=g).bfloat16()
+    go = torch.randn(2, 3, 4, 16, generator=g).bfloat16()
+    rr, ll, ww = (x.clone().requires_grad_(True) for x in (r, lo, w))
+    O.fuse_outputs(rr, ll, ww).backward(go)
+    assert torch.equal(rr.grad, go)
+    assert torch.equal(ll.grad, (go.float() * w.float()[..., None]).bfloat16())
+    torch.testing.assert_close(ww.grad.float(),
+                               (go.float() * lo.float()).sum(-1).bfloat16().float(),
+                               atol=0, rtol=8e-3)
