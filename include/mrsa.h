@@ -84,6 +84,26 @@ int mrsa_chunk_attn_pool_gqa_fwd(const void* mu_q, const void* k_chunked,
                                  float* prior_bias, void* stream);
 
 /*
+ * Backward of the landmark pool; the probabilities are recomputed from mu_q
+ * and K.  Replaces _ChunkAttnPoolGQA.backward
+ * (ops/chunk_attn_pool_gqa_tilelang.py:355-394, kernel _pool_gqa_bwd :183-325)
+ * and, with dense_torch_semantics != 0, the autograd of _compact_pool_torch
+ * (:17-37) that the reference runs for groups == 1.
+ *   mu_q, k_chunked, key_valid: as mrsa_chunk_attn_pool_gqa_fwd
+ *   grad_landmark: bf16 [batch_chunks, kv_heads, groups, head_dim] or NULL (zeros)
+ *   grad_entropy:  fp32 [batch_chunks, kv_heads, groups] or NULL (zeros)
+ *   d_mu_q (out):      bf16 [batch_chunks, kv_heads, groups, head_dim]
+ *   d_k_chunked (out): bf16 [batch_chunks, chunk_size, kv_heads, head_dim]
+ * Limits: as the forward.
+ */
+int mrsa_chunk_attn_pool_gqa_bwd(const void* mu_q, const void* k_chunked,
+                                 const uint8_t* key_valid, const void* grad_landmark,
+                                 const float* grad_entropy, int64_t batch_chunks,
+                                 int64_t chunk_size, int64_t kv_heads, int64_t groups,
+                                 int64_t head_dim, float sm_scale, int dense_torch_semantics,
+                                 void* d_mu_q, void* d_k_chunked, void* stream);
+
+/*
  * Remote-route drop mask (1 = the chunk may not be routed to).
  * Replaces remote_drop_mask (dream_dllm_hils/kernel_utils.py:102-161) with the
  * chunk-aligned local bounds of chunk_aligned_local_bounds (:75-99).

@@ -152,3 +152,179 @@ extern "C" int mrsa_chunk_attn_pool_gqa_fwd(const void* mu_q, const void* k_chun
                      (uint16_t*)landmark_keys, entropy, prior_bias);
   return mrsa_launch_status();
 }
+
+namespace {
+
+// Backward of the pool, one workgroup per (chunk, KV head) like the forward;
+// the probabilities are recomputed from mu_q and K rather than saved.
+// Fused-kernel semantics (_pool_gqa_bwd, ops/chunk_attn_pool_gqa_tilelang.py:183-325):
+//   pb = bf16(p) for a valid chunk, else 0;  dP = gK . k;  delta = sum_s pb dP
+//   dlogit = pb ((dP - delta) - gH (ln pb + H))  (0 where pb = 0), rounded to
+//   bf16 after the sm_scale factor;  d_mu = dlogit . K;  d_k = dlogit^T q + pb^T gK
+//   (a masked slot 0, whose logit is the constant 0, still gets its term, as
+//   in the reference kernel).
+// Dense semantics (autograd of _compact_pool_torch, :17-37): fp32 p,
+//   dp = dP - gH (ln p + 1) for p > 0, dz = p (dp - sum p dp), dlogit = dz sm_scale.
+__global__ void __launch_bounds__(kThreads)
+    pool_bwd_kernel(const uint16_t* __restrict__ mu_q, const uint16_t* __restrict__ kc,
+                    const uint8_t* __restrict__ key_valid, const uint16_t* __restrict__ g_lmk,
+                    const float* __restrict__ g_ent, int S, int H, int G, int D, float sm_scale,
+                    int dense, uint16_t* __restrict__ d_mu, uint16_t* __restrict__ d_k) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int64_t bc = blockIdx.x;
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+
+  uint16_t* ks = reinterpret_cast<uint16_t*>(smem);  // [S][D] bf16
+  float* qs = reinterpret_cast<float*>(ks + S * D);   // [G][D]
+  float* gs = qs + G * D;                             // [G][D] grad of the pooled key
+  float* ps = gs + G * D;                             // [G][S] logits -> pb
+  float* dq = ps + G * S;                             // [G][S] dP -> dlogit
+  int* flag = reinterpret_cast<int*>(dq + G * S);
+  unsigned char* vs = reinterpret_cast<unsigned char*>(flag + 1);  // [S]
+
+  const int vec_per_row = D / 8;
+  for (int v = tid; v < S * vec_per_row; v += kThreads) {
+    const int s = v / vec_per_row, c = v - s * vec_per_row;
+    reinterpret_cast<u32x4_t*>(ks + s * D)[c] =
+        reinterpret_cast<const u32x4_t*>(kc + ((bc * S + s) * H + h) * (int64_t)D)[c];
+  }
+  const int64_t qbase = ((bc * H + h) * G) * (int64_t)D;
+  for (int e = tid; e < G * D; e += kThreads) {
+    qs[e] = bf16_to_f32(mu_q[qbase + e]);
+    gs[e] = g_lmk ? bf16_to_f32(g_lmk[qbase + e]) : 0.f;
+  }
+  if (tid == 0) flag[0] = 0;
+  for (int s = tid; s < S; s += kThreads) vs[s] = key_valid[bc * S + s] != 0;
+  __syncthreads();
+  if (tid < S - 1 && vs[tid]) flag[0] = 1;
+  __syncthreads();
+  const bool chunk_valid = flag[0] != 0;
+
+  for (int p = tid; p < G * S; p += kThreads) {
+    const int g = p / S, s = p - g * S;
+    const float* qr = qs + g * D;
+    const float* gr = gs + g * D;
+    const uint16_t* kr = ks + s * D;
+    int d = (s * 8) % D;
+    float acc = 0.f, dacc = 0.f;
+    for (int i = 0; i < D; i += 2) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(kr + d);
+      acc = fmaf(qr[d], bf16_lo(w), acc);
+      acc = fmaf(qr[d + 1], bf16_hi(w), acc);
+      dacc = fmaf(gr[d], bf16_lo(w), dacc);
+      dacc = fmaf(gr[d + 1], bf16_hi(w), dacc);
+      d += 2;
+      if (d >= D) d -= D;
+    }
+    const bool real = (s < S - 1) && vs[s];
+    float logit;
+    if (dense) {
+      logit = real ? acc * sm_scale : neg_inf();
+    } else {
+      logit = (real && chunk_valid) ? acc * sm_scale : (s == 0 ? 0.f : neg_inf());
+    }
+    ps[p] = logit;
+    dq[p] = dacc;
+  }
+  __syncthreads();
+
+  for (int g = wave; g < G; g += kThreads / 64) {
+    const bool in0 = lane < S, in1 = lane + 64 < S;
+    const float v0 = in0 ? ps[g * S + lane] : neg_inf();
+    const float v1 = in1 ? ps[g * S + lane + 64] : neg_inf();
+    const float dp0 = in0 ? dq[g * S + lane] : 0.f;
+    const float dp1 = in1 ? dq[g * S + lane + 64] : 0.f;
+    const float m = wave_max(fmaxf(v0, v1));
+    float e0 = 0.f, e1 = 0.f;
+    if (m != neg_inf()) {
+      e0 = (in0 && v0 != neg_inf()) ? exp2f((v0 - m) * kLog2e) : 0.f;
+      e1 = (in1 && v1 != neg_inf()) ? exp2f((v1 - m) * kLog2e) : 0.f;
+    }
+    const float sum = wave_sum(e0 + e1);
+    const float p0 = sum > 0.f ? e0 / sum : 0.f;
+    const float p1 = sum > 0.f ? e1 / sum : 0.f;
+    const float gh = g_ent ? g_ent[(bc * H + h) * G + g] : 0.f;
+    float b0, b1, l0, l1;
+    if (!dense) {
+      const float ent =
+          -wave_sum((p0 > 0.f ? p0 * logf(p0) : 0.f) + (p1 > 0.f ? p1 * logf(p1) : 0.f));
+      b0 = chunk_valid ? bf16_to_f32(f32_to_bf16(p0)) : 0.f;
+      b1 = chunk_valid ? bf16_to_f32(f32_to_bf16(p1)) : 0.f;
+      const float delta = wave_sum(b0 * dp0 + b1 * dp1);
+      l0 = b0 > 0.f ? b0 * ((dp0 - delta) - gh * (logf(b0) + ent)) : 0.f;
+      l1 = b1 > 0.f ? b1 * ((dp1 - delta) - gh * (logf(b1) + ent)) : 0.f;
+      l0 = bf16_to_f32(f32_to_bf16(l0 * sm_scale));
+      l1 = bf16_to_f32(f32_to_bf16(l1 * sm_scale));
+    } else {
+      b0 = p0;
+      b1 = p1;
+      const float q0 = p0 > 0.f ? dp0 - gh * (logf(fmaxf(p0, 1e-30f)) + (p0 >= 1e-30f ? 1.f : 0.f))
+                                : dp0;
+      const float q1 = p1 > 0.f ? dp1 - gh * (logf(fmaxf(p1, 1e-30f)) + (p1 >= 1e-30f ? 1.f : 0.f))
+                                : dp1;
+      const float delta = wave_sum(p0 * q0 + p1 * q1);
+      l0 = p0 * (q0 - delta) * sm_scale;
+      l1 = p1 * (q1 - delta) * sm_scale;
+    }
+    if (in0) {
+      ps[g * S + lane] = b0;
+      dq[g * S + lane] = l0;
+    }
+    if (in1) {
+      ps[g * S + lane + 64] = b1;
+      dq[g * S + lane + 64] = l1;
+    }
+  }
+  __syncthreads();
+
+  for (int p = tid; p < G * D; p += kThreads) {
+    const int g = p / D, d = p - g * D;
+    const float* lr = dq + g * S;
+    float acc = 0.f;
+    for (int s = 0; s < S; ++s) acc = fmaf(lr[s], bf16_to_f32(ks[s * D + d]), acc);
+    d_mu[qbase + p] = (uint16_t)f32_to_bf16(acc);
+  }
+  for (int p = tid; p < S * D; p += kThreads) {
+    const int s = p / D, d = p - s * D;
+    float acc = 0.f;
+    for (int g = 0; g < G; ++g) {
+      acc = fmaf(dq[g * S + s], qs[g * D + d], acc);
+      acc = fmaf(ps[g * S + s], gs[g * D + d], acc);
+    }
+    d_k[((bc * S + s) * H + h) * (int64_t)D + d] = (uint16_t)f32_to_bf16(acc);
+  }
+}
+
+}  // namespace
+
+extern "C" int mrsa_chunk_attn_pool_gqa_bwd(const void* mu_q, const void* k_chunked,
+                                            const uint8_t* key_valid, const void* grad_landmark,
+                                            const float* grad_entropy, int64_t batch_chunks,
+                                            int64_t chunk_size, int64_t kv_heads, int64_t groups,
+                                            int64_t head_dim, float sm_scale,
+                                            int dense_torch_semantics, void* d_mu_q,
+                                            void* d_k_chunked, void* stream) {
+  if (batch_chunks < 0 || chunk_size < 2 || chunk_size > 128 || kv_heads <= 0 || groups <= 0 ||
+      groups > 16 || head_dim <= 0 || head_dim > 256 || head_dim % 8 != 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (batch_chunks == 0) return MRSA_OK;
+  if (!mu_q || !k_chunked || !key_valid || !d_mu_q || !d_k_chunked)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if ((uintptr_t)k_chunked % 16 != 0) return MRSA_ERR_INVALID_ARGUMENT;
+  if (batch_chunks > 0x7fffffff || kv_heads > 65535) return MRSA_ERR_UNSUPPORTED;
+  const int S = (int)chunk_size, G = (int)groups, D = (int)head_dim;
+  const size_t smem = (size_t)S * D * 2 + 2 * (size_t)G * D * 4 + 2 * (size_t)G * S * 4 + 4 + S;
+  if (smem > 64 * 1024) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&pool_bwd_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+      return MRSA_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL(pool_bwd_kernel, dim3((unsigned)batch_chunks, (unsigned)kv_heads),
+                     dim3(kThreads), smem, (hipStream_t)stream, (const uint16_t*)mu_q,
+                     (const uint16_t*)k_chunked, key_valid, (const uint16_t*)grad_landmark,
+                     grad_entropy, S, (int)kv_heads, G, D, sm_scale, dense_torch_semantics,
+                     (uint16_t*)d_mu_q, (uint16_t*)d_k_chunked);
+  return mrsa_launch_status();
+}

@@ -29,7 +29,7 @@ from .kernel_utils import (
     remote_drop_mask_rows,
 )
 from .local_attention import bidir_local_attention, cached_local_attention
-from .pool import chunk_attn_pool_gqa, chunk_attn_pool_gqa_prior
+from .pool import chunk_attn_pool_gqa, chunk_attn_pool_gqa_backward, chunk_attn_pool_gqa_prior
 from .route_layer import (
     CachedBlockStep,
     LayerKVCache,
@@ -61,6 +61,7 @@ __all__ = [
     "select_global_token_keep",
     "chunk_aligned_local_bounds",
     "chunk_attn_pool_gqa",
+    "chunk_attn_pool_gqa_backward",
     "chunk_attn_pool_gqa_prior",
     "fuse_hils_outputs",
     "group_pad_to",

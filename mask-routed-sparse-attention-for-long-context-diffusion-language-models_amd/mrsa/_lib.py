@@ -36,6 +36,10 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _P, _P, _P, _P, _P],
     ),
+    "mrsa_chunk_attn_pool_gqa_bwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _P, _P, _P],
+    ),
     "mrsa_remote_drop_mask": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P, _P]),
     "mrsa_remote_drop_mask_rows": (_I, [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]),
     "mrsa_route_topk_fwd": (

@@ -2,7 +2,10 @@
 
 Drop-in for ``ops.chunk_attn_pool_gqa_tilelang.chunk_attn_pool_gqa``
 (ops/chunk_attn_pool_gqa_tilelang.py:425-448).  Same arguments, validation
-messages and outputs; forward only.
+messages and outputs.  Under autograd the backward runs the gfx950 pool
+backward kernel (mrsa_chunk_attn_pool_gqa_bwd): the fused kernel's gradient
+(:183-325) for groups > 1, the autograd of the torch twin (:17-37) for
+groups == 1, as the reference dispatches.
 """
 
 from __future__ import annotations
@@ -65,6 +68,76 @@ def _launch(mu_q, k_chunked, key_valid, sm_scale, bias_scale=None):
     return lmk, entropy, prior
 
 
+def chunk_attn_pool_gqa_backward(mu_q, k_chunked, key_valid, grad_landmark, grad_entropy,
+                                 sm_scale):
+    """(d_mu_q, d_k_chunked) in bf16 for the pool's upstream gradients
+    (either may be None)."""
+
+    batch, chunks, kv_heads, groups, head_dim = mu_q.shape
+    chunk_size = k_chunked.shape[2]
+    mu = mu_q.contiguous()
+    kc = k_chunked.contiguous()
+    kv = key_valid.to(device=mu.device, dtype=torch.bool).contiguous()
+    g_lmk = None if grad_landmark is None else grad_landmark.to(torch.bfloat16).contiguous()
+    g_ent = None if grad_entropy is None else grad_entropy.to(torch.float32).contiguous()
+    d_mu = torch.empty_like(mu)
+    d_k = torch.empty_like(kc)
+    st = _lib.call(
+        "mrsa_chunk_attn_pool_gqa_bwd",
+        _lib.ptr(mu), _lib.ptr(kc), _lib.ptr(kv), _lib.ptr(g_lmk), _lib.ptr(g_ent),
+        batch * chunks, chunk_size, kv_heads, groups, head_dim, float(sm_scale),
+        1 if groups == 1 else 0, _lib.ptr(d_mu), _lib.ptr(d_k), _lib.stream_of(mu),
+    )
+    _lib.check(st, "chunk_attn_pool_gqa backward")
+    return d_mu, d_k
+
+
+class _ChunkAttnPoolGQA(torch.autograd.Function):
+    # ops/chunk_attn_pool_gqa_tilelang.py:328-394
+    @staticmethod
+    def forward(ctx, mu_q, k_chunked, key_valid, sm_scale):
+        lmk, entropy, _ = _launch(mu_q, k_chunked, key_valid, sm_scale)
+        ctx.save_for_backward(mu_q, k_chunked, key_valid)
+        ctx.sm_scale = sm_scale
+        return lmk, entropy
+
+    @staticmethod
+    def backward(ctx, grad_lmk, grad_entropy):
+        mu, kc, kv = ctx.saved_tensors
+        d_mu, d_k = chunk_attn_pool_gqa_backward(mu, kc, kv, grad_lmk, grad_entropy, ctx.sm_scale)
+        return d_mu, d_k, None, None
+
+
+class _ChunkAttnPoolPrior(torch.autograd.Function):
+    # the pool plus prior_bias = entropy * entropy_bias_scale (attention.py:1425-1430)
+    @staticmethod
+    def forward(ctx, mu_q, k_chunked, key_valid, bias_scale, sm_scale):
+        lmk, entropy, prior = _launch(mu_q, k_chunked, key_valid, sm_scale, bias_scale)
+        ctx.save_for_backward(mu_q, k_chunked, key_valid, bias_scale, entropy)
+        ctx.sm_scale = sm_scale
+        return lmk, entropy, prior
+
+    @staticmethod
+    def backward(ctx, grad_lmk, grad_entropy, grad_prior):
+        mu, kc, kv, scale, entropy = ctx.saved_tensors
+        d_scale = None
+        if grad_prior is not None:
+            s = scale.to(torch.float32).reshape(entropy.shape[2:])
+            extra = grad_prior.float() * s
+            grad_entropy = extra if grad_entropy is None else grad_entropy.float() + extra
+            if ctx.needs_input_grad[3]:
+                d_scale = (grad_prior.float() * entropy).sum(dim=(0, 1)).reshape(scale.shape)
+                d_scale = d_scale.to(scale.dtype)
+        d_mu, d_k = chunk_attn_pool_gqa_backward(mu, kc, kv, grad_lmk, grad_entropy, ctx.sm_scale)
+        return d_mu, d_k, None, d_scale, None
+
+
+def _needs_grad(*xs):
+    return torch.is_grad_enabled() and any(
+        isinstance(x, torch.Tensor) and x.requires_grad for x in xs
+    )
+
+
 def chunk_attn_pool_gqa(
     mu_q: torch.Tensor,
     k_chunked: torch.Tensor,
@@ -81,6 +154,8 @@ def chunk_attn_pool_gqa(
     _validate(mu_q, k_chunked, key_valid)
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(mu_q.shape[-1])
+    if _needs_grad(mu_q, k_chunked):
+        return _ChunkAttnPoolGQA.apply(mu_q, k_chunked, key_valid, float(sm_scale))
     lmk, entropy, _ = _launch(mu_q, k_chunked, key_valid, sm_scale)
     return lmk, entropy
 
@@ -101,4 +176,8 @@ def chunk_attn_pool_gqa_prior(
     _validate(mu_q, k_chunked, key_valid)
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(mu_q.shape[-1])
+    if _needs_grad(mu_q, k_chunked, entropy_bias_scale):
+        return _ChunkAttnPoolPrior.apply(
+            mu_q, k_chunked, key_valid, entropy_bias_scale, float(sm_scale)
+        )
     return _launch(mu_q, k_chunked, key_valid, sm_scale, entropy_bias_scale)

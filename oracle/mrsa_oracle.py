@@ -82,6 +82,52 @@ def chunk_attn_pool(mu_q, k_chunked, key_valid, sm_scale=None, *, dense=None):
     return lmk, entropy
 
 
+def chunk_attn_pool_bwd(mu_q, k_chunked, key_valid, grad_lmk, grad_entropy, sm_scale=None):
+    """Backward of the fused pool kernel, _pool_gqa_bwd
+    (ops/chunk_attn_pool_gqa_tilelang.py:183-325), as _ChunkAttnPoolGQA.backward
+    (:355-394) runs it for groups > 1.  Returns (d_mu_q, d_k_chunked) in bf16.
+
+    The kernel's rounding points are kept: the saved probabilities are zero
+    for an invalid chunk (:164-169) and enter as bf16 (:241-246); the logit
+    gradient p * ((dP - sum p dP) - g_H * (ln p + H)) (:264-283) is rounded to
+    bf16 after the sm_scale factor; d_mu and d_k are bf16 roundings of fp32
+    sums (:286-312).  Like the kernel, a masked slot 0 (whose logit is the
+    constant 0) still receives the logit gradient.  For groups == 1 the
+    reference differentiates _compact_pool_torch instead: autograd of
+    chunk_attn_pool(..., dense=True) is that backward.
+    """
+
+    B, C, H, G, D = mu_q.shape
+    S = k_chunked.shape[2]
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    q = mu_q.float()
+    k = k_chunked.float()
+    real = key_valid.bool().clone()
+    real[..., -1] = False
+    chunk_ok = real.any(dim=-1)
+    ok = real & chunk_ok[..., None]
+    fill = torch.full((S,), NEG_INF)
+    fill[0] = 0.0
+    logits = torch.einsum("bchgd,bcshd->bchgs", q, k) * sm_scale
+    probs = torch.softmax(torch.where(ok[:, :, None, None, :], logits, fill), dim=-1)
+    logp = torch.where(probs > 0, probs.clamp_min(1e-30).log(), torch.zeros_like(probs))
+    entropy = (-(probs * logp).sum(dim=-1)).masked_fill(~chunk_ok[:, :, None, None], 0.0)
+    pb = bf16_round(probs.masked_fill(~chunk_ok[:, :, None, None, None], 0.0))
+    gk = (torch.zeros_like(q) if grad_lmk is None else grad_lmk).bfloat16().float()
+    gb = torch.zeros(B, C, H, G) if grad_entropy is None else grad_entropy.float()
+    dP = torch.einsum("bchgd,bcshd->bchgs", gk, k)
+    delta = (pb * dP).sum(dim=-1, keepdim=True)
+    lpb = torch.where(pb > 0, pb.clamp_min(1e-30).log(), torch.zeros_like(pb))
+    dlogit = torch.where(
+        pb > 0, pb * ((dP - delta) - gb[..., None] * (lpb + entropy[..., None])),
+        torch.zeros_like(pb))
+    dl = bf16_round(dlogit * sm_scale)
+    d_mu = torch.einsum("bchgs,bcshd->bchgd", dl, k)
+    d_k = torch.einsum("bchgs,bchgd->bcshd", dl, q) + torch.einsum("bchgs,bchgd->bcshd", pb, gk)
+    return d_mu.bfloat16(), d_k.bfloat16()
+
+
 # ---------------------------------------------------------------------------
 # a1: drop mask
 # ---------------------------------------------------------------------------

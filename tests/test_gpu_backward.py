@@ -141,3 +141,77 @@ def test_fusion_backward_vs_oracle(D):
     mrsa.fuse_hils_outputs(a, b_, c).backward(go.to(DEV))
     assert torch.equal(a.grad.cpu(), rr.grad) and torch.equal(b_.grad.cpu(), ll.grad)
     torch.testing.assert_close(c.grad.cpu().float(), ww.grad.float(), atol=1e-6, rtol=8e-3)
+
+
+def _pool_inputs(seed, C, S, H, G, D):
+    g = torch.Generator().manual_seed(seed)
+    mu = torch.randn(1, C, H, G, D, generator=g).bfloat16()
+    k = torch.randn(1, C, S, H, D, generator=g).bfloat16()
+    valid = torch.rand(1, C, S, generator=g) > 0.1
+    valid[0, 1, 0] = False            # masked slot 0
+    valid[0, 2, :-1] = False          # invalid chunk
+    g_lmk = torch.randn(1, C, H, G, D, generator=g).bfloat16()
+    g_ent = torch.randn(1, C, H, G, generator=g)
+    return mu, k, valid, g_lmk, g_ent
+
+
+def _rel(a, b):
+    return float((a.float() - b.float()).norm() / b.float().norm().clamp_min(1e-12))
+
+
+@pytest.mark.parametrize("C,S,H,G,D", [(37, 64, 4, 7, 128), (9, 128, 2, 16, 256), (11, 32, 3, 5, 64)])
+def test_pool_backward_vs_oracle(C, S, H, G, D):
+    _note(f"pool bwd C={C} S={S} H={H} G={G} D={D}")
+    mu, k, valid, g_lmk, g_ent = _pool_inputs(C + S, C, S, H, G, D)
+    scale = D ** -0.5
+    d_mu, d_k = mrsa.chunk_attn_pool_gqa_backward(mu.to(DEV), k.to(DEV), valid.to(DEV),
+                                                  g_lmk.to(DEV), g_ent.to(DEV), scale)
+    e_mu, e_k = O.chunk_attn_pool_bwd(mu, k, valid, g_lmk, g_ent, scale)
+    assert _rel(d_mu.cpu(), e_mu) < 5e-3 and _rel(d_k.cpu(), e_k) < 5e-3
+    torch.testing.assert_close(d_mu.cpu().float(), e_mu.float(), atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(d_k.cpu().float(), e_k.float(), atol=2e-2, rtol=2e-2)
+    assert float(d_mu[0, 2].abs().sum()) == 0 and float(d_k[0, 2].abs().sum()) == 0
+    # autograd API, with and without the entropy gradient
+    m = mu.to(DEV).requires_grad_(True)
+    kk = k.to(DEV).requires_grad_(True)
+    lmk, ent = mrsa.chunk_attn_pool_gqa(m, kk, valid.to(DEV), scale)
+    torch.autograd.backward([lmk, ent], [g_lmk.to(DEV), g_ent.to(DEV)])
+    assert torch.equal(m.grad, d_mu) and torch.equal(kk.grad, d_k)
+    m.grad = None
+    lmk, _ = mrsa.chunk_attn_pool_gqa(m, k.to(DEV), valid.to(DEV), scale)
+    lmk.backward(g_lmk.to(DEV))
+    e_mu0, _ = O.chunk_attn_pool_bwd(mu, k, valid, g_lmk, None, scale)
+    assert _rel(m.grad.cpu(), e_mu0) < 5e-3
+
+
+def test_pool_backward_dense_groups1_vs_autograd():
+    _note("pool bwd dense G=1")
+    C, S, H, G, D = 13, 64, 4, 1, 128
+    mu, k, valid, g_lmk, g_ent = _pool_inputs(5, C, S, H, G, D)
+    valid[0, 3, :] = False            # fully masked chunk
+    scale = D ** -0.5
+    d_mu, d_k = mrsa.chunk_attn_pool_gqa_backward(mu.to(DEV), k.to(DEV), valid.to(DEV),
+                                                  g_lmk.to(DEV), g_ent.to(DEV), scale)
+    m = mu.float().requires_grad_(True)
+    kk = k.float().requires_grad_(True)
+    lmk, ent = O.chunk_attn_pool(m, kk, valid, scale, dense=True)
+    (lmk * g_lmk.float()).sum().add_((ent * g_ent).sum()).backward()
+    assert _rel(d_mu.cpu(), m.grad) < 5e-3 and _rel(d_k.cpu(), kk.grad) < 5e-3
+    torch.testing.assert_close(d_k.cpu().float(), kk.grad, atol=2e-2, rtol=2e-2)
+
+
+def test_pool_prior_backward():
+    _note("pool prior bwd")
+    C, S, H, G, D = 21, 64, 4, 7, 128
+    mu, k, valid, g_lmk, g_ent = _pool_inputs(6, C, S, H, G, D)
+    scale_t = torch.rand(H * G) + 0.5
+    g_prior = torch.randn(1, C, H, G)
+    m = mu.to(DEV).requires_grad_(True)
+    bs = scale_t.to(DEV).requires_grad_(True)
+    lmk, ent, prior = mrsa.chunk_attn_pool_gqa_prior(m, k.to(DEV), valid.to(DEV), bs)
+    torch.autograd.backward([lmk, prior], [g_lmk.to(DEV), g_prior.to(DEV)])
+    _, e_ent = O.chunk_attn_pool(mu, k, valid)
+    e_scale = (g_prior * e_ent).sum(dim=(0, 1)).reshape(-1)
+    torch.testing.assert_close(bs.grad.cpu(), e_scale, atol=1e-3, rtol=1e-3)
+    e_mu, _ = O.chunk_attn_pool_bwd(mu, k, valid, g_lmk, g_prior * scale_t.reshape(H, G), D ** -0.5)
+    assert _rel(m.grad.cpu(), e_mu) < 5e-3

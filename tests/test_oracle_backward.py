@@ -166,3 +166,72 @@ def test_fusion_backward_matches_reference_kernel_formula():
     torch.testing.assert_close(ww.grad.float(),
                                (go.float() * lo.float()).sum(-1).bfloat16().float(),
                                atol=0, rtol=8e-3)
+
+
+def _pool_case(seed, B=1, C=3, S=16, H=2, G=3, D=8):
+    g = torch.Generator().manual_seed(seed)
+    mu = torch.randn(B, C, H, G, D, generator=g).bfloat16()
+    k = torch.randn(B, C, S, H, D, generator=g).bfloat16()
+    valid = torch.rand(B, C, S, generator=g) > 0.2
+    valid[..., 0] = True
+    g_lmk = torch.randn(B, C, H, G, D, generator=g).bfloat16()
+    g_ent = torch.randn(B, C, H, G, generator=g)
+    return mu, k, valid, g_lmk, g_ent
+
+
+def _pool_autograd(mu, k, valid, g_lmk, g_ent, dense):
+    m = mu.float().requires_grad_(True)
+    kk = k.float().requires_grad_(True)
+    lmk, ent = O.chunk_attn_pool(m, kk, valid, 0.4, dense=dense)
+    (lmk * g_lmk.float()).sum().add_((ent * g_ent).sum()).backward()
+    return m.grad, kk.grad
+
+
+def _rel(a, b):
+    return float((a.float() - b.float()).norm() / b.float().norm().clamp_min(1e-12))
+
+
+def test_pool_backward_formula_matches_autograd():
+    # _pool_gqa_bwd's logit gradient p((dP - sum p dP) - g_H (ln p + H)) is the
+    # softmax/entropy chain rule; with slot 0 valid in every chunk the oracle's
+    # kernel restatement equals autograd of the fused forward up to bf16 rounding.
+    mu, k, valid, g_lmk, g_ent = _pool_case(11)
+    d_mu, d_k = O.chunk_attn_pool_bwd(mu, k, valid, g_lmk, g_ent, 0.4)
+    a_mu, a_k = _pool_autograd(mu, k, valid, g_lmk, g_ent, dense=False)
+    assert _rel(d_mu, a_mu) < 1.5e-2 and _rel(d_k, a_k) < 1.5e-2
+
+
+def test_pool_backward_masked_slot0_and_invalid_chunk():
+    mu, k, valid, g_lmk, g_ent = _pool_case(12)
+    valid[0, 1, 0] = False                 # masked slot 0: constant logit 0
+    valid[0, 2, :-1] = False               # invalid chunk: zero gradients
+    d_mu, d_k = O.chunk_attn_pool_bwd(mu, k, valid, g_lmk, g_ent, 0.4)
+    a_mu, a_k = _pool_autograd(mu, k, valid, g_lmk, g_ent, dense=False)
+    assert float(d_mu[0, 2].abs().sum()) == 0 and float(d_k[0, 2].abs().sum()) == 0
+    assert _rel(d_k[0, 1, 1:], a_k[0, 1, 1:]) < 1.5e-2
+    # the kernel's extra term: d_k[slot 0] picks up dlogit[:, 0] * mu, d_mu picks up
+    # dlogit[:, 0] * k[0]; autograd has neither (the logit there is a constant)
+    extra_k = (d_k[0, 1, 0].float() - a_k[0, 1, 0]).abs().sum()
+    assert float(extra_k) > 1e-3
+    assert _rel(d_mu[0, 0], a_mu[0, 0]) < 1.5e-2
+
+
+def test_pool_dense_backward_is_torch_twin_autograd():
+    # groups == 1: the reference differentiates _compact_pool_torch; central
+    # differences pin the oracle's dense forward gradient.
+    mu, k, valid, g_lmk, g_ent = _pool_case(13, G=1, S=8, D=4, C=2, H=1)
+    valid[0, 1, :] = False                 # fully masked chunk: zero
+    a_mu, a_k = _pool_autograd(mu, k, valid, g_lmk, g_ent, dense=True)
+    assert float(a_mu[0, 1].abs().sum()) == 0
+
+    def loss(m):
+        lmk, ent = O.chunk_attn_pool(m, k.float(), valid, 0.4, dense=True)
+        return float((lmk.double() * g_lmk.double()).sum() + (ent.double() * g_ent).sum())
+
+    eps = 1e-2
+    for flat in range(mu.numel()):
+        mp, mm = mu.float().clone(), mu.float().clone()
+        mp.view(-1)[flat] += eps
+        mm.view(-1)[flat] -= eps
+        fd = (loss(mp) - loss(mm)) / (2 * eps)
+        assert abs(fd - float(a_mu.view(-1)[flat])) < 3e-3, flat
