@@ -114,7 +114,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("route", "decode", "swa"), default="route")
+    ap.add_argument("--workload", choices=("route", "decode", "swa", "model"), default="route")
     ap.add_argument("--token-budget", type=int, default=0,
                     help="route workload with the remote-token refinement (global_qk) at "
                          "this budget (0: off, the configuration-2 default)")
@@ -137,6 +137,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.workload == "decode":
         return decode_main(args, torch, mrsa, dev)
+    if args.workload == "model":
+        return model_main(args, torch, mrsa, dev)
     if args.workload == "swa":
         return swa_main(args, torch, mrsa, dev)
     if args.copy_calibration:
@@ -304,6 +306,80 @@ def swa_main(args, torch, mrsa, dev) -> int:
                      "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
                      "flops_per_launch": flops, "avg_launch_us": kern_us},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+MODEL_L = 65536
+
+
+def model_main(args, torch, mrsa, dev) -> int:
+    """Full Dream-7B-shaped denoising forward (configuration 4): 28 layers
+    (route layers 3, 7, ..., 27 with Q-Cal; SWA-1280 elsewhere), hidden 3584,
+    MLP 18944, vocab 152064, L = 65536, random-init bf16 weights, uniform
+    random token ids with 25% set to the mask token.  One step = embeddings to
+    logits for every position."""
+
+    from mrsa.dream import DreamShape, DreamWeights, dream_flops, dream_forward, yarn_tables
+
+    shape = DreamShape()
+    L = MODEL_L
+    w = DreamWeights.random(shape, dev, seed=7)
+    g = torch.Generator().manual_seed(8)
+    ids = torch.randint(0, shape.vocab, (1, L), generator=g)
+    ids[torch.rand(1, L, generator=g) < 0.25] = shape.mask_token_id
+    ids = ids.to(dev)
+    tables = yarn_tables(L, shape, dev)
+    stream = torch.cuda.current_stream(dev)
+    times = []
+
+    def run(record):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        out = dream_forward(w, ids, tables=tables)
+        e1.record(stream)
+        if record:
+            times.append((e0, e1))
+        return out
+
+    for _ in range(args.warmup):
+        run(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        logits = run(True)
+    torch.cuda.synchronize()
+    ms_per_step = 1000.0 * (time.perf_counter() - t0) / args.steps
+    fwd_ms = sum(a.elapsed_time(b) for a, b in times) / len(times)
+    assert bool(torch.isfinite(logits[:: 997].float()).all())
+    flops = dream_flops(shape, L)
+    achieved = flops / (fwd_ms * 1e-3) / 1e12
+    line = {
+        "metric": "Dream-7B-shaped denoising forward tokens/s @64k (config 4)",
+        "value": L / (ms_per_step / 1000.0),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, random token ids, 25% mask tokens)",
+        "config": {"workload": "Dream-7B-shaped denoising forward (config 4)",
+                   "seq_len": L, "layers": shape.layers, "route_layers": shape.route_layers(),
+                   "hidden": shape.hidden, "intermediate": shape.intermediate,
+                   "vocab": shape.vocab, "q_heads": shape.q_heads,
+                   "kv_heads": shape.kv_heads, "swa_window": shape.swa_window,
+                   "qcal_rank": shape.qcal_rank, "parallelism": "single-gpu"},
+        "roofline": {"bound": "mfma", "kernel": "whole forward (GEMMs + attention)",
+                     "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                     "flops_per_step": flops, "forward_ms": fwd_ms},
+        "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -397,6 +397,43 @@ int mrsa_candidate_token_scores_fwd(const void* q, const void* k, const int32_t*
  */
 int mrsa_selftest_mfma_layout(const void* a, const void* b, float* c, void* stream);
 
+/*
+ * Decoder-layer glue of the Dream-7B-shaped forward (the layers around the
+ * attention path: dream_dllm_hils/fastdllm_v1.py:375-403).
+ *
+ * Residual add + RMSNorm (Qwen2RMSNorm as the decoder layer applies it):
+ *   sum = bf16(x + residual) (when residual != NULL; written to sum_out when given)
+ *   out = bf16(weight * bf16(sum * rsqrt(mean(sum^2) + eps)))
+ *   x, residual, sum_out, out: bf16 [rows, hidden]; weight: bf16 [hidden]
+ * Limits: hidden % 8 == 0, hidden <= 8192, 16-byte aligned rows.
+ */
+int mrsa_add_rms_norm_fwd(const void* x, const void* residual, const void* weight, int64_t rows,
+                          int64_t hidden, float eps, void* sum_out, void* out, void* stream);
+
+/*
+ * Rotary embedding of the fused QKV projection, plus the Q-Cal routing query.
+ * Replaces apply_rotary_pos_emb (dream_dllm_hils/attention.py:41-52) in the
+ * fp32 form of ops/rope_tilelang_fp32.py:19-94, and _finish_calibrated_query
+ * (attention.py:477-502; qcal.py:22-26) when qcal_delta != NULL.
+ *   qkv: bf16 [tokens, (q_heads + 2 kv_heads) * 128] (q heads, k heads, v heads)
+ *   cos_table, sin_table: fp32 [tokens, 64] (attention factor folded in)
+ *   qcal_delta: bf16 [tokens, q_heads, 128] or NULL; qcal_norm_weight: fp32 [128]
+ *   q (out): bf16 [tokens, q_heads, 128]; k, v (out): bf16 [tokens, kv_heads, 128]
+ *   route_q (out, with qcal_delta): rope(rms_norm(q_unrotated + delta) * weight)
+ */
+int mrsa_rope_qkv_fwd(const void* qkv, const float* cos_table, const float* sin_table,
+                      const void* qcal_delta, const float* qcal_norm_weight, float qcal_eps,
+                      int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                      void* q, void* k, void* v, void* route_q, void* stream);
+
+/*
+ * SwiGLU of the fused gate/up projection (Qwen2 MLP act_fn(gate) * up):
+ *   gate_up: bf16 [rows, 2 * intermediate] (gate columns first)
+ *   out:     bf16 [rows, intermediate] = bf16(bf16(silu(gate)) * up)
+ */
+int mrsa_swiglu_fwd(const void* gate_up, int64_t rows, int64_t intermediate, void* out,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -974,6 +974,151 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
   }
 }
 
+// Selection with one wave per (row, KV head, batch) and no barrier, for long
+// sequences (many rows): chunk c = lane + 64 i, so the wave selection's order
+// index is the chunk index and ties still go to the lower chunk.  The head
+// LSEs come from one pass with a per-lane online max / sum; the keys are
+// formed from the logits held in registers when PER * G <= 128 (C <= 1024 at
+// G = 8) and from a second read of the row otherwise.  Same score, LSE, drop
+// and tie rules as route_select_kernel.
+template <int G, int PER>
+__global__ void __launch_bounds__(256) route_select_wave_kernel(RouteArgs a,
+                                                                const float* __restrict__ raw) {
+  constexpr bool kHold = PER * G <= 128;
+  const int64_t C = a.C, L = a.L;
+  const int K = a.K;
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= L) return;  // wave-uniform
+  const int h = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int n = (int)((C + 63) / 64);  // <= PER
+  const int64_t row = (b * L + r) * a.Hkv + h;
+  const float* xr = raw + row * (int64_t)G * C;
+  const int64_t climit = a.is_causal ? causal_limit(a, r) : C;
+  const float* bias = a.bias ? a.bias + (b * C * a.Hkv + h) * G : nullptr;  // + c * Hkv * G + g
+
+  auto logit = [&](int g, int64_t c) -> float {
+    if (c >= climit) return neg_inf();
+    float v = xr[(int64_t)g * C + c];
+    if (bias) v += bias[c * a.Hkv * G + g];
+    return v;
+  };
+
+  float hold[kHold ? PER : 1][G];
+  float m[G], sum[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = neg_inf();
+    sum[g] = 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t c = lane + 64 * (int64_t)i;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float v = (i < n && c < C) ? logit(g, c) : neg_inf();
+      if (kHold) hold[i][g] = v;
+      if (v > m[g]) {
+        sum[g] = (m[g] == neg_inf() ? 0.f : sum[g] * expf(m[g] - v)) + 1.f;
+        m[g] = v;
+      } else if (v != neg_inf()) {
+        sum[g] += expf(v - m[g]);
+      }
+    }
+  }
+  float tot[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float mm = wave_max(m[g]);
+    const float ss = wave_sum(m[g] == neg_inf() ? 0.f : sum[g] * expf(m[g] - mm));
+    const float lse_h = mm == neg_inf() ? mm : mm + logf(ss);
+    tot[g] = a.pre_softmax ? 0.f : logaddexp_f(a.lse[row * G + g], lse_h);
+  }
+
+  int64_t lc = 0, rc = -1;
+  if (a.derive_window >= 0) {
+    lc = max(r - a.derive_window, (int64_t)0) / a.block_size;
+    rc = min(r + a.derive_window, L - 1) / a.block_size;
+  }
+  uint32_t key[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    key[i] = 0u;  // below every real key: never picked
+    const int64_t c = lane + 64 * (int64_t)i;
+    if (i >= n || c >= C) continue;
+    float best = neg_inf();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float x = kHold ? hold[i][g] : logit(g, c);
+      best = fmaxf(best, x == neg_inf() ? x : x - tot[g]);
+    }
+    bool dropped = false;
+    if (a.derive_window >= 0) {
+      bool any = false;
+      if (a.key_valid) {
+        const uint8_t* kv = a.key_valid + b * L + c * a.block_size;
+        for (int64_t t = 0; t < a.block_size - 1; ++t) any |= kv[t] != 0;
+      } else {
+        any = a.block_size > 1;
+      }
+      dropped = (c >= lc && c <= rc) || !any;
+    } else if (a.drop) {
+      dropped = a.drop[(b * L + r) * C + c] != 0;
+    }
+    key[i] = float_order_key(dropped ? neg_inf() : best);
+  }
+
+  const uint64_t picks = WaveSelect<PER>::run(key, n, K);
+  const uint64_t below = (1ull << lane) - 1ull;
+  int base = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    if (i >= n) continue;  // uniform
+    const bool p = (picks >> i) & 1ull;
+    const uint64_t pb = __builtin_amdgcn_ballot_w64(p);
+    if (p) {
+      const int slot = base + __builtin_popcountll(pb & below);
+      const int64_t c = lane + 64 * (int64_t)i;
+      a.indices[row * K + slot] = (int32_t)c;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float v = xr[(int64_t)g * C + c];
+        if (a.scores_fp32)
+          reinterpret_cast<float*>(a.scores)[(row * G + g) * K + slot] = v;
+        else
+          reinterpret_cast<uint16_t*>(a.scores)[(row * G + g) * K + slot] =
+              (uint16_t)f32_to_bf16(v);
+      }
+    }
+    base += __builtin_popcountll(pb);
+  }
+  for (int t = base + lane; t < K; t += 64) {
+    a.indices[row * K + t] = -1;
+    for (int g = 0; g < G; ++g) {
+      if (a.scores_fp32)
+        reinterpret_cast<float*>(a.scores)[(row * G + g) * K + t] = neg_inf();
+      else
+        reinterpret_cast<uint16_t*>(a.scores)[(row * G + g) * K + t] = 0xff80u;
+    }
+  }
+}
+
+// Rows (token, KV head, batch) above which the wave selection replaces the
+// workgroup selection: below it a workgroup per row spreads a short block's
+// few rows over more of the chip.
+constexpr int64_t kWaveSelectRows = 4096;
+
+template <int G>
+int launch_select_wave(const RouteArgs& a, const float* raw, hipStream_t s) {
+  dim3 grid((unsigned)((a.L + 3) / 4), (unsigned)a.Hkv, (unsigned)a.B);
+  if (a.C <= 1024)
+    hipLaunchKernelGGL((route_select_wave_kernel<G, 16>), grid, dim3(256), 0, s, a, raw);
+  else
+    hipLaunchKernelGGL((route_select_wave_kernel<G, 64>), grid, dim3(256), 0, s, a, raw);
+  return mrsa_launch_status();
+}
+
 template <int G>
 int launch_select(const RouteArgs& a, const float* raw, hipStream_t s) {
   dim3 g2((unsigned)a.L, (unsigned)a.Hkv, (unsigned)a.B);
@@ -987,6 +1132,10 @@ int launch_block(const RouteArgs& a, float* raw, hipStream_t s) {
   hipLaunchKernelGGL(route_logits_kernel, g1, dim3(64 * a.G), 0, s, a, raw);
   int st = mrsa_launch_status();
   if (st != MRSA_OK) return st;
+  if (a.B * a.L * a.Hkv >= kWaveSelectRows && a.C <= 4096 && a.L <= 0x7ffffffc) {
+    if (a.G == 7) return launch_select_wave<7>(a, raw, s);
+    if (a.G == 8) return launch_select_wave<8>(a, raw, s);
+  }
   switch (a.G) {
     case 1: return launch_select<1>(a, raw, s);
     case 2: return launch_select<2>(a, raw, s);

@@ -31,6 +31,11 @@ SIGNATURES = {
     "mrsa_status_string": (ctypes.c_char_p, [_I]),
     "mrsa_abi_version": (_I, []),
     "mrsa_fuse_hils_outputs_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _P]),
+    "mrsa_add_rms_norm_fwd": (_I, [_P, _P, _P, _I64, _I64, _F, _P, _P, _P]),
+    "mrsa_rope_qkv_fwd": (
+        _I, [_P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P],
+    ),
+    "mrsa_swiglu_fwd": (_I, [_P, _I64, _I64, _P, _P]),
     "mrsa_fuse_hils_outputs_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P]),
     "mrsa_chunk_attn_pool_gqa_fwd": (
         _I,

@@ -1,0 +1,177 @@
+"""GPU parity of the Dream-7B-shaped forward: the glue kernels against the
+oracle's glue ops, and a 4-layer model (one route layer, three SWA layers) at
+L = 4096 against the CPU composition: stage by stage with the oracle's hidden
+state fed to each layer, and end to end.
+
+Tolerances: glue outputs within one bf16 ulp per rounding (two for RMSNorm
+and the routing query, which round twice) (hardware rsqrt /
+exp and fused multiply-adds against torch's); per layer, GEMM outputs within
+1e-3 and attention within 5e-3 relative norm (bf16 output against the fp32
+oracle), route indices equal on more than 99.9% of the slots (near-ties);
+end to end, logits within 5e-2 relative norm and the arg-max token equal on
+90% of the positions (rounding flips compound through the layers).
+"""
+
+import pytest
+import torch
+
+from mrsa.dream import (DreamShape, DreamWeights, add_rms_norm, dream_forward, embed_tokens,
+                        rope_qkv, swiglu, yarn_tables)
+from mrsa.route_layer import RouteLayerConfig, route_attention, swa_attention
+from oracle import dream_oracle as DO
+from oracle import mrsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def _ulp_close(got, exp, ulps=1):
+    # relative: one bf16 ulp per rounding; absolute: one ulp of an O(1)
+    # operand, for results that cancel (x0 c - x1 s of the rotation)
+    torch.testing.assert_close(got.cpu().float(), exp.float(), atol=4e-3 * ulps,
+                               rtol=8e-3 * ulps)
+
+
+def test_add_rms_norm_vs_oracle():
+    _note("add_rms_norm")
+    g = torch.Generator().manual_seed(1)
+    for H in (3584, 896, 8192):
+        x = torch.randn(300, H, generator=g).bfloat16()
+        r = torch.randn(300, H, generator=g).bfloat16()
+        w = (1 + 0.1 * torch.randn(H, generator=g)).bfloat16()
+        tot, out = add_rms_norm(x.to(DEV), r.to(DEV), w.to(DEV), 1e-6)
+        s = (x.float() + r.float()).bfloat16()
+        assert torch.equal(tot.cpu(), s)
+        _ulp_close(out, DO.rms_norm(s, w, 1e-6), ulps=2)
+        none, out2 = add_rms_norm(x.to(DEV), None, w.to(DEV), 1e-6)
+        assert none is None
+        _ulp_close(out2, DO.rms_norm(x, w, 1e-6), ulps=2)
+
+
+def test_rope_qkv_with_qcal_vs_oracle():
+    _note("rope_qkv")
+    s = DreamShape()
+    L, Hq, Hkv, D = 200, 28, 4, 128
+    g = torch.Generator().manual_seed(2)
+    qkv = torch.randn(L, (Hq + 2 * Hkv) * D, generator=g).bfloat16()
+    delta = (0.3 * torch.randn(L, Hq, D, generator=g)).bfloat16()
+    nw = 1 + 0.1 * torch.randn(D, generator=g)
+    cos, sin = yarn_tables(L + 5000, s, "cpu")
+    cos, sin = cos[5000:].contiguous(), sin[5000:].contiguous()
+    q, k, v, rq = rope_qkv(qkv.to(DEV), cos.to(DEV), sin.to(DEV), s, delta.to(DEV), nw.to(DEV))
+    qp = qkv[:, : Hq * D].reshape(L, Hq, D)
+    kp = qkv[:, Hq * D : (Hq + Hkv) * D].reshape(L, Hkv, D)
+    _ulp_close(q[0], DO.rope(qp, cos, sin))
+    _ulp_close(k[0], DO.rope(kp, cos, sin))
+    assert torch.equal(v[0].cpu(), qkv[:, (Hq + Hkv) * D :].reshape(L, Hkv, D))
+    # two bf16 roundings in a row (norm, then rotation): within two ulps
+    _ulp_close(rq[0], DO.qcal_route_q(qp, delta, nw, cos, sin, 1e-6), ulps=2)
+    _, _, _, none = rope_qkv(qkv.to(DEV), cos.to(DEV), sin.to(DEV), s)
+    assert none is None
+
+
+def test_swiglu_vs_oracle():
+    _note("swiglu")
+    g = torch.Generator().manual_seed(3)
+    gu = (3 * torch.randn(129, 2 * 18944, generator=g)).bfloat16()
+    _ulp_close(swiglu(gu.to(DEV)), DO.swiglu(gu))
+
+
+def _cpu_weights(w):
+    return DreamWeights(shape=w.shape, embed=w.embed.cpu(), lmk_type=w.lmk_type.cpu(),
+                        final_norm=w.final_norm.cpu(), lm_head=w.lm_head.cpu(),
+                        layers=[type(lw)(**{f: (None if t is None else t.cpu())
+                                            for f, t in vars(lw).items()}) for lw in w.layers])
+
+
+SMALL = DreamShape(layers=4, hidden=896, intermediate=1536, q_heads=7, kv_heads=1, vocab=1024,
+                   route=RouteLayerConfig())
+
+
+def _rel(a, b):
+    return float((a.float().cpu() - b.float()).norm() / b.float().norm())
+
+
+def test_dream_layers_teacher_forced_vs_oracle():
+    """Each layer on the GPU path, fed the oracle's hidden state, against the
+    oracle's layer: the parity bar for the decoder (stage by stage)."""
+
+    shape, L, Hq, Hkv, D = SMALL, 4096, 7, 1, 128
+    _note(f"dream layers teacher-forced L={L}")
+    w = DreamWeights.random(shape, DEV, seed=5, std=0.05)
+    wc = _cpu_weights(w)
+    ids = torch.randint(0, shape.vocab, (1, L), generator=torch.Generator().manual_seed(6))
+    cos, sin = yarn_tables(L, shape, DEV)
+    ccos, csin = cos.cpu(), sin.cpu()
+    h = embed_tokens(w, ids.to(DEV)).cpu()
+    e = wc.embed[ids.reshape(-1)].float()
+    e[63::64] += wc.lmk_type.float()
+    assert torch.equal(h, e.to(torch.bfloat16))
+    for i, (lw, lc) in enumerate(zip(w.layers, wc.layers)):
+        _, x = add_rms_norm(h.to(DEV), None, lw.input_norm, shape.rms_eps)
+        xr = DO.rms_norm(h, lc.input_norm, shape.rms_eps)
+        _ulp_close(x, xr, ulps=2)
+        qkv = torch.nn.functional.linear(xr.to(DEV), lw.qkv_weight, lw.qkv_bias)
+        qkvr = DO.linear(xr, lc.qkv_weight, lc.qkv_bias)
+        assert _rel(qkv, qkvr) < 1e-3, (i, "qkv")
+        qp = qkvr[:, : Hq * D].reshape(L, Hq, D)
+        kp = qkvr[:, Hq * D : (Hq + Hkv) * D].reshape(L, Hkv, D)
+        v = qkvr[:, (Hq + Hkv) * D :].reshape(1, L, Hkv, D)
+        q, k = DO.rope(qp, ccos, csin)[None], DO.rope(kp, ccos, csin)[None]
+        if i in shape.route_layers():
+            delta = DO.linear(DO.linear(xr, lc.qcal_down), lc.qcal_up).reshape(L, Hq, D)
+            gq, gk, gv, grq = rope_qkv(qkvr.to(DEV), cos, sin, shape, delta.to(DEV), lw.qcal_norm)
+            rq = DO.qcal_route_q(qp, delta, lc.qcal_norm, ccos, csin, shape.qcal_eps)[None]
+            _ulp_close(grq, rq, ulps=2)
+            a, inter = route_attention(q.to(DEV), k.to(DEV), v.to(DEV), rq.to(DEV),
+                                       lw.entropy_bias_scale, None, shape.route,
+                                       return_intermediates=True)
+            ar, ir = O.route_layer(q, k, v, rq, lc.entropy_bias_scale, None)
+            same = float((inter["indices"].cpu() == ir["indices"]).float().mean())
+            print(f"[gpu-case] layer {i} route attn rel={_rel(a, ar):.2e} idx={same:.5f}", flush=True)
+            assert same > 0.999 and _rel(a, ar) < 5e-3
+        else:
+            gq, gk, gv, _ = rope_qkv(qkvr.to(DEV), cos, sin, shape)
+            a = swa_attention(q.to(DEV), k.to(DEV), v.to(DEV), None, shape.swa_window, 64)
+            ar, _ = O.local_attention(q, k, v, None, shape.swa_window, 0)
+            print(f"[gpu-case] layer {i} swa attn rel={_rel(a, ar):.2e}", flush=True)
+            assert _rel(a, ar) < 5e-3
+            ar = ar.to(torch.bfloat16)
+        _ulp_close(gq, q)
+        _ulp_close(gk, k)
+        assert torch.equal(gv.cpu(), v)
+        o = DO.linear(ar.reshape(L, Hq * D), lc.o_weight)
+        tot, x2 = add_rms_norm(o.to(DEV), h.to(DEV), lw.post_norm, shape.rms_eps)
+        h = (h.float() + o.float()).to(torch.bfloat16)
+        assert torch.equal(tot.cpu(), h)
+        xr = DO.rms_norm(h, lc.post_norm, shape.rms_eps)
+        _ulp_close(x2, xr, ulps=2)
+        gur = DO.linear(xr, lc.gate_up_weight)
+        gu = torch.nn.functional.linear(xr.to(DEV), lw.gate_up_weight)
+        assert _rel(gu, gur) < 1e-3, (i, "gate_up")
+        _ulp_close(swiglu(gur.to(DEV)), DO.swiglu(gur))
+        m = DO.linear(DO.swiglu(gur), lc.down_weight)
+        h = (h.float() + m.float()).to(torch.bfloat16)
+
+
+def test_small_dream_forward_end_to_end():
+    """The whole forward at the initializer_range of the config.  Per-element
+    rounding flips compound through the residual stream of a random network,
+    so this bounds the drift; the per-stage parity bar is the teacher-forced
+    test above."""
+
+    shape, L = SMALL, 4096
+    _note(f"dream forward layers={shape.layers} L={L}")
+    w = DreamWeights.random(shape, DEV, seed=5)
+    ids = torch.randint(0, shape.vocab, (1, L), generator=torch.Generator().manual_seed(6))
+    ids[torch.rand(1, L, generator=torch.Generator().manual_seed(7)) < 0.25] = shape.vocab - 1
+    logits = dream_forward(w, ids.to(DEV)).cpu().float()
+    ref = DO.dream_forward(_cpu_weights(w), ids).float()
+    rel = float((logits - ref).norm() / ref.norm())
+    agree = float((logits.argmax(-1) == ref.argmax(-1)).float().mean())
+    print(f"[gpu-case] dream logits rel={rel:.3e} argmax agree={agree:.4f}", flush=True)
+    assert rel < 5e-2 and agree > 0.9

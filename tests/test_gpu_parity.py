@@ -166,11 +166,17 @@ def test_route_topk_vs_oracle(L, C, G, topk):
     (40, 1000, 8, 20, "pre_softmax", False, True, False),
     (33, 700, 4, 64, "post_softmax", True, True, True),
     (5, 4096, 7, 32, "post_softmax", False, False, False),
+    # >= 4096 (token, KV head) rows: one selection wave per row
+    (1024, 1024, 7, 32, "post_softmax", False, False, False),
+    (1100, 512, 8, 32, "pre_softmax", True, True, False),
+    (1024, 2048, 7, 32, "post_softmax", False, False, True),
+    (1030, 1000, 7, 64, "post_softmax", False, True, False),
 ])
 def test_route_topk_short_block_vs_oracle(L, C, G, topk, mode, causal, fp32, shared):
-    # The logits-workspace path (matrix-core logits, one selection workgroup
-    # per row): selection modes, the causal chunk mask with a query offset,
-    # shared landmarks, fp32 scores, and up to 4096 chunks.
+    # The logits-workspace path (matrix-core logits, then one selection
+    # workgroup per row for short blocks or one selection wave per row for
+    # long sequences): selection modes, the causal chunk mask with a query
+    # offset, shared landmarks, fp32 scores, and up to 4096 chunks.
     _note(f"route short block L={L} C={C} G={G} K={topk} {mode} causal={causal}")
     Hkv = 4
     q5, lmk, lse4, bias4, drop, _ = _route_case(L, C, G, Hkv, 300 + L, drop_frac=0.1)
