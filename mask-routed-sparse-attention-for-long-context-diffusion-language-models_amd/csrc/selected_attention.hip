@@ -104,6 +104,9 @@ struct SelArgs {
   // Optional token keep mask int8 [B, Lq, Hkv, K, 64] (nonzero = key kept)
   // of the remote-token refinement; read only by the KEEP instantiation.
   const int8_t* keep;
+  // Queries per tile actually used (<= the split's capacity): tile x covers
+  // queries [x * tq, x * tq + tq).
+  int tq;
 };
 
 // LDS carve-up (byte offsets, 16-aligned).  The p_* arrays are only used by
@@ -494,9 +497,9 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   const int64_t b = blockIdx.z % a.B;
   const int part = (int)(blockIdx.z / a.B);
   const int h = blockIdx.y;
-  const int64_t q0 = (int64_t)blockIdx.x * kTQ;
+  const int64_t q0 = (int64_t)blockIdx.x * a.tq;
   const int G = a.G;
-  const int64_t nq = min((int64_t)kTQ, a.Lq - q0);  // queries of this tile that exist
+  const int64_t nq = min((int64_t)a.tq, a.Lq - q0);  // queries of this tile that exist
 
   // Zeroed counters, published by the prologue's barriers.
   if (tid == 0) *cursor = 0;
@@ -849,10 +852,37 @@ int launch_variant(SelArgs& a, const SelLayout& lay, hipStream_t s) {
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lay.total) != hipSuccess)
     return MRSA_ERR_LAUNCH;
-  dim3 grid((unsigned)((a.Lq + SP::kTQ - 1) / SP::kTQ), (unsigned)a.Hkv,
-            (unsigned)(a.B * a.parts));
+  dim3 grid((unsigned)((a.Lq + a.tq - 1) / a.tq), (unsigned)a.Hkv, (unsigned)(a.B * a.parts));
   hipLaunchKernelGGL(kern, grid, dim3(SP::kThreads), lay.total, s, a);
   return mrsa_launch_status();
+}
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Queries per tile.  One workgroup fills a CU (its LDS ring), so workgroups
+// run in rounds of `cus`.  Tiles of `cap` queries would leave the last round
+// partly empty (configuration 2: 1368 workgroups = 5.3 rounds of 256); the
+// smallest tile that needs no more rounds spreads the same work evenly over
+// them, which shortens every workgroup instead.
+int64_t tile_queries(int64_t Lq, int64_t groups, int cap, int cus) {
+  if (cus <= 0 || Lq <= cap || groups <= 0) return cap;
+  const int64_t tiles = (Lq + cap - 1) / cap;
+  const int64_t rounds = (tiles * groups + cus - 1) / cus;
+  const int64_t tiles_max = rounds * cus / groups;
+  if (tiles_max <= tiles) return cap;
+  const int64_t tq = (Lq + tiles_max - 1) / tiles_max;
+  return tq < 1 ? 1 : (tq > cap ? cap : tq);
 }
 
 // Deepest ring that fits in LDS: 4 slots, else 3.
@@ -862,6 +892,7 @@ int launch_selected(SelArgs& a, hipStream_t s) {
       MRSA_SEL_WAVES == 16, Split<16, 1>,
       std::conditional_t<MRSA_SEL_WAVES == 12, Split12,
                          std::conditional_t<MRSA_SEL_WAVES == 82, Split8x2, Split8>>>;
+  a.tq = (int)tile_queries(a.Lq, a.B * a.Hkv * a.parts, SP::kTQ, device_cus());
   const SelLayout l4 = sel_layout(SP::kTQ, SP::kWaves, a.K, a.Ck, 4, TOKEN, a.Lq, KEEP);
   if (sel_layout_fits(l4, 4)) return launch_variant<TOKEN, 4, SP, KEEP>(a, l4, s);
   const SelLayout l3 = sel_layout(SP::kTQ, SP::kWaves, a.K, a.Ck, 3, TOKEN, a.Lq, KEEP);
