@@ -161,15 +161,21 @@ int mrsa_route_topk_fwd(const void* q, const void* lmk, const float* lse_local,
                         void* scores, int scores_fp32, void* stream);
 
 /*
- * mrsa_route_topk_fwd with a caller-provided fp32 workspace.  The same
- * reference call sites; the decode caller is route_topk_g7 at
+ * mrsa_route_topk_fwd with a caller-provided workspace (16-byte aligned).
+ * The same reference call sites; the decode caller is route_topk_g7 at
  * dream_dllm_hils/fastdllm_attention.py:299-314 (32 query rows against the
- * whole cache).  When the workspace holds mrsa_route_topk_workspace_bytes()
- * bytes (16-byte aligned) and head_dim == 128, groups <= 8, chunks <= 4096,
- * the logits of all rows are computed on the matrix cores into the workspace
- * and selected by a second kernel, one workgroup per (row, KV head); other
- * shapes (and a smaller workspace) take mrsa_route_topk_fwd's paths.  Same
- * results either way.
+ * whole cache).
+ *   - Shapes of the matrix-core kernel (head_dim 128, groups 7 or 8,
+ *     chunks <= 256, topk <= 64, bf16 scores, not causal): a workspace of
+ *     at least batch * seq_len * kv_heads * groups * chunks * 2 bytes holds
+ *     the bf16 raw scores of every chunk, so the kernel runs one pass and
+ *     gathers the picks' scores from it instead of recomputing them.
+ *   - Otherwise, with mrsa_route_topk_workspace_bytes() bytes and
+ *     head_dim == 128, groups <= 8, chunks <= 4096, the logits of all rows are
+ *     computed on the matrix cores into the fp32 workspace and selected by a
+ *     second kernel, one workgroup per (row, KV head).
+ * Other shapes (and a smaller workspace) take mrsa_route_topk_fwd's paths.
+ * Same results either way.
  */
 int64_t mrsa_route_topk_workspace_bytes(int64_t batch, int64_t seq_len, int64_t chunks,
                                         int64_t kv_heads, int64_t groups);

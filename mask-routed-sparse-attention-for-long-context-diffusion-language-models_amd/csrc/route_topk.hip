@@ -17,10 +17,12 @@
 // each query head g the landmark keys of that head are staged in LDS and the
 // 16x256 logit tile of every wave is computed on the matrix cores, reduced to
 // the head's LSE and folded into the running max over heads.  The logits of
-// every head stay in registers as bf16 so the selection can emit them without
-// recomputation.  The 32nd-largest score of each row is found by bisection on
+// The 32nd-largest score of each row is found by bisection on
 // order-preserving integer keys; exact ties at the threshold are broken by
-// chunk index.
+// chunk index.  The returned raw scores of the picks come either from a
+// second pass that recomputes every head's logits, or (with a caller
+// workspace) from the bf16 raw scores pass 1 writes to HBM, gathered back at
+// the picks after the selection.
 //
 // Short-block path (route_logits_kernel + route_select_kernel, with a caller
 // workspace): logits of few query rows against up to 4096 chunks on the
@@ -114,12 +116,14 @@ struct FastLayout {
 // consecutive chunks 32*sub .. 32*sub+31: bisection on order-preserving keys
 // for the K-th largest score, exact ties at the threshold broken toward the
 // lower chunk index.  Writes the slot table (chunk -> list position or -1)
-// the indices and the per-row pick counts; slots past the picks get index -1
-// (their scores are written as -inf by the second pass).
+// the indices, the picks' chunks in list order (pick_s [64][K], when not
+// null) and the per-row pick counts; slots past the picks get index -1
+// (their scores are written as -inf by the emission of the scores).
 template <int G>
 __device__ __forceinline__ void select_step(const RouteArgs& a, const float (&M)[kNT][4],
                                             uint16_t* ms_buf, const unsigned char* cbad,
-                                            int8_t* slot_s, int* ntot_s, int64_t q0, int64_t qbase, int64_t L,
+                                            int8_t* slot_s, int* ntot_s, int16_t* pick_s,
+                                            int64_t q0, int64_t qbase, int64_t L,
                                             int64_t C, int h, int64_t b, int lane, int wave,
                                             int col, int grp, int qg, int cbase) {
   const int K = a.K;
@@ -237,6 +241,7 @@ __device__ __forceinline__ void select_step(const RouteArgs& a, const float (&M)
     const bool pick = (pickbits >> e) & 1u;
     slot_s[row * 256 + 32 * sub + e] = pick ? (int8_t)slot : (int8_t)-1;
     if (pick && r < L) a.indices[orow * K + slot] = 32 * sub + e;
+    if (pick_s && pick) pick_s[row * K + slot] = (int16_t)(32 * sub + e);
     slot += pick ? 1 : 0;
   }
   if (r < L)
@@ -244,8 +249,9 @@ __device__ __forceinline__ void select_step(const RouteArgs& a, const float (&M)
   if (sub == 0) ntot_s[row] = total;
 }
 
-template <int G>
-__global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteArgs a) {
+template <int G, bool WS>
+__global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteArgs a,
+                                                                         uint16_t* __restrict__ raw_ws) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int K = a.K;
   float* bias_s = reinterpret_cast<float*>(smem + FastLayout::bias);
@@ -378,8 +384,9 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
     if (s + 1 < 2 * G && load_next_q) load_q(head_of(s + 1), Anext);
   };
   // Logits of step s, staging step s + 1's head meanwhile.
+  constexpr int kSteps = WS ? G : 2 * G;
   auto step_logits = [&](auto transposed, int s, f32x4_t (&S)[kNT]) {
-    const bool more = s + 1 < 2 * G;
+    const bool more = s + 1 < kSteps;
     logits(transposed, lmk_buf(s & 1), Acur, S, more ? head_of(s + 1) : -1, (s + 1) & 1,
            s + 1 < G);
   };
@@ -401,10 +408,37 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
   stage_q(0);
   stage(0, 0, true);
 
+  // Raw scores bf16(s * sm_scale) of the previous head (WS), two rows per
+  // register: Rp[t][p] holds rows 4grp + 2p, 4grp + 2p + 1 of chunk
+  // cbase + 16t + col.  They are stored one step late, after the step's
+  // vmcnt wait, so that the next wait (which covers stores too) finds them
+  // long completed instead of stalling on their write latency.
+  uint32_t Rp[kNT][2];
+  // raw_ws [B][L][Hkv][G][C]: 16 lanes of a row cover 16 consecutive chunks
+  // (2-byte stores; a quad transpose to 8-byte row stores measured slower).
+  auto store_raw = [&](int gprev) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t r = qbase + 4 * grp + i;
+      if (r < L) {
+        uint16_t* wrow = raw_ws + (((b * L + r) * a.Hkv + h) * G + gprev) * C;
+#pragma unroll
+        for (int t = 0; t < kNT; ++t) {
+          const int c = cbase + 16 * t + col;
+          const uint32_t w = Rp[t][i >> 1];
+          if (c < C) wrow[c] = (uint16_t)((i & 1) ? (w >> 16) : (w & 0xffffu));
+        }
+      }
+    }
+  };
+
   // Pass 1: biased logits, LSE over all chunks, running max over heads.
   for (int s = 0; s < G; ++s) {
     const int g = s;
     begin_step(s, false);
+    if constexpr (WS) {
+      if (s > 0) store_raw(s - 1);
+    }
     // This lane's A operand rows: query 16qg + col (row & 15 == col).
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -412,6 +446,13 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
           qstage + ((16 * qg + col) * 16 + ((4 * j + grp) ^ col)) * 8);
     f32x4_t S[kNT];
     step_logits(std::false_type{}, s, S);
+    if constexpr (WS) {
+#pragma unroll
+      for (int t = 0; t < kNT; ++t) {
+        Rp[t][0] = pack_bf16x2(S[t][0] * a.sm_scale, S[t][1] * a.sm_scale);
+        Rp[t][1] = pack_bf16x2(S[t][2] * a.sm_scale, S[t][3] * a.sm_scale);
+      }
+    }
     const float* bias_g = bias_s + 256 * (s & 1);
     // x = s * scale + bias, -inf past C.
 #pragma unroll
@@ -472,8 +513,61 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
     }
   }
 
-  select_step<G>(a, M, lmk_buf((G - 1) & 1), cbad, slot_s, ntot_s, q0, qbase, L, C, h, b, lane, wave,
-                 col, grp, qg, cbase);
+  if constexpr (WS) store_raw(G - 1);
+  int16_t* pick_s = WS ? reinterpret_cast<int16_t*>(lmk_buf(G & 1)) : nullptr;  // [64][K]
+  select_step<G>(a, M, lmk_buf((G - 1) & 1), cbad, slot_s, ntot_s, pick_s, q0, qbase, L, C, h, b,
+                 lane, wave, col, grp, qg, cbase);
+  if constexpr (WS) {
+    // Picks of every head from the workspace, gathered straight into the
+    // [G][K] score rows: wave w emits rows 8w..8w+7, lane l value
+    // e = 64 it + l (head e / K, slot e % K) of each row, with the reads of
+    // all eight rows in flight before any is used.  All waves of the
+    // workgroup share one CU (one L1): the barrier's workgroup-scope fence
+    // (vmcnt(0) on the stores) makes every wave's raw scores visible to the
+    // others.
+    __syncthreads();  // pick lists and counts of every row, raw scores stored
+    constexpr int kIt = (8 * kFastMaxTopk + 63) / 64;  // G * K <= 8 * 64 values per row
+    const int gk = G * K;
+    const int nit = (gk + 63) / 64;
+    // Head and slot of value e of a row; es = K (never < a pick count) marks
+    // e >= G * K, so the last partial iteration reads nothing past the row.
+    int eg[kIt], es[kIt];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int e = 64 * it + lane;
+      eg[it] = e < gk ? e / K : 0;
+      es[it] = e < gk ? e - eg[it] * K : K;
+    }
+    const int64_t rstride = (int64_t)a.Hkv * G * C, ostride = (int64_t)a.Hkv * gk;
+    const uint16_t* rbase = raw_ws + ((b * L + q0) * a.Hkv + h) * (int64_t)G * C;
+    uint16_t* obase = sc16 + ((b * L + q0) * a.Hkv + h) * (int64_t)gk;
+    for (int it0 = 0; it0 < nit; it0 += 2) {
+      uint16_t v[8][2];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int row = 8 * wave + j;
+        const int nt = row < 64 && q0 + row < L ? ntot_s[row] : 0;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int it = it0 + u;
+          v[j][u] = 0xff80u;  // -inf past the picks
+          if (it < nit && es[it] < nt)  // es < nt <= K implies e < G * K
+            v[j][u] = rbase[row * rstride + eg[it] * C + pick_s[row * K + es[it]]];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int row = 8 * wave + j;
+        if (q0 + row >= L) continue;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int e = 64 * (it0 + u) + lane;
+          if (it0 + u < nit && e < gk) obase[row * ostride + e] = v[j][u];
+        }
+      }
+    }
+    return;
+  }
   load_q(head_of(G), Acur);
 
   // Pass 2: raw logit bf16(q.lmk * scale) of every picked chunk, heads G-1..0.
@@ -1148,15 +1242,17 @@ int launch_block(const RouteArgs& a, float* raw, hipStream_t s) {
   }
 }
 
+// raw_ws: bf16 [B][L][Hkv][G][C] raw-score workspace (one pass), or null
+// (a second pass recomputes the picks' raw scores).
 template <int G>
-int launch_fast(const RouteArgs& a, hipStream_t s) {
+int launch_fast(const RouteArgs& a, uint16_t* raw_ws, hipStream_t s) {
   const size_t smem = FastLayout::total(a.K);
-  auto kern = route_topk_mfma_kernel<G>;
+  auto kern = raw_ws ? route_topk_mfma_kernel<G, true> : route_topk_mfma_kernel<G, false>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
     return MRSA_ERR_LAUNCH;
   dim3 grid((unsigned)((a.L + kFastQ - 1) / kFastQ), (unsigned)a.Hkv, (unsigned)a.B);
-  hipLaunchKernelGGL(kern, grid, dim3(kFastThreads), smem, s, a);
+  hipLaunchKernelGGL(kern, grid, dim3(kFastThreads), smem, s, a, raw_ws);
   return mrsa_launch_status();
 }
 
@@ -1212,7 +1308,13 @@ int route_topk_dispatch(const void* q, const void* lmk, const float* lse_local, 
   const bool fast = !scores_fp32 && !is_causal && head_dim == 128 &&
                     seq_len * kv_heads * groups * head_dim < ((int64_t)1 << 31) && chunks <= 256 && topk <= kFastMaxTopk && aligned &&
                     (groups == 7 || groups == 8);
-  if (fast) return groups == 7 ? launch_fast<7>(a, s) : launch_fast<8>(a, s);
+  if (fast) {
+    uint16_t* raw_ws = nullptr;
+    if (workspace && (uintptr_t)workspace % 16 == 0 &&
+        workspace_bytes >= batch * seq_len * kv_heads * groups * chunks * 2)
+      raw_ws = (uint16_t*)workspace;
+    return groups == 7 ? launch_fast<7>(a, raw_ws, s) : launch_fast<8>(a, raw_ws, s);
+  }
   const bool block = workspace && head_dim == 128 && groups <= 8 && aligned &&
                      chunks <= (int64_t)kSelThreads * kSelMaxPer && seq_len <= 0x7fffffff &&
                      (uintptr_t)workspace % 16 == 0 &&

@@ -21,15 +21,26 @@ from .kernel_utils import group_pad_to
 _WORKSPACE_LIMIT = 16 << 30
 
 
-def _use_block_path(B, L, C, Hkv, G, D, topk, scores_fp32, is_causal):
-    """Whether the logits-workspace path runs: the matrix-core route kernel
-    covers up to 256 chunks; beyond that, with head_dim 128, groups <= 8 and
-    chunks <= 4096, the two-kernel path over an fp32 logits workspace."""
-    fast = (not scores_fp32 and not is_causal and D == 128 and C <= 256 and topk <= 64
+def _fast_shape(C, G, D, topk, scores_fp32, is_causal):
+    """Shapes of the matrix-core route kernel (up to 256 chunks, bf16 scores)."""
+    return (not scores_fp32 and not is_causal and D == 128 and C <= 256 and topk <= 64
             and G in (7, 8))
-    if fast or D != 128 or G > 8 or C > 4096:
-        return False
-    return B * L * Hkv * G * C * 4 <= _WORKSPACE_LIMIT
+
+
+def _workspace_bytes(B, L, C, Hkv, G, D, topk, scores_fp32, is_causal):
+    """Bytes of the workspace the route kernels take, 0 for none.  The
+    matrix-core kernel (up to 256 chunks) takes a bf16 raw-score workspace
+    [B, L, Hkv, G, C] and then skips the second pass that recomputes the
+    picks' raw scores; beyond 256 chunks, with head_dim 128, groups <= 8 and
+    chunks <= 4096, the two-kernel path runs over an fp32 logits workspace of
+    the same shape."""
+    if _fast_shape(C, G, D, topk, scores_fp32, is_causal):
+        n = B * L * Hkv * G * C * 2
+    elif D != 128 or G > 8 or C > 4096:
+        return 0
+    else:
+        n = B * L * Hkv * G * C * 4
+    return n if n <= _WORKSPACE_LIMIT else 0
 
 
 def route_topk_launch(
@@ -59,8 +70,9 @@ def route_topk_launch(
     drop mask of remote_drop_mask(key_valid, derive_window, block_size) is
     computed inside the kernel instead.
     Returns indices [B, L, Hkv, topk] int32 and scores [B, L, Hkv, G, topk].
-    ``use_workspace`` (None: by shape) runs the short-block path over an fp32
-    logits workspace [B, L, Hkv, G, C] where the kernel supports it.
+    ``use_workspace`` (None: by shape) passes the kernels a workspace: an fp32
+    logits workspace [B, L, Hkv, G, C] for the short-block path, a bf16
+    raw-score workspace of that shape for the one-pass matrix-core kernel.
     """
 
     if selection_mode not in {"post_softmax", "pre_softmax"}:
@@ -109,10 +121,12 @@ def route_topk_launch(
         0 if selection_mode == "post_softmax" else 1, float(sm_scale),
         _lib.ptr(indices), _lib.ptr(scores), 1 if scores_fp32 else 0,
     )
+    nbytes = _workspace_bytes(B, L, C, Hkv, G, D, topk, scores_fp32, is_causal)
     if use_workspace is None:
-        use_workspace = _use_block_path(B, L, C, Hkv, G, D, topk, scores_fp32, is_causal)
+        use_workspace = nbytes > 0
     if use_workspace:
-        nbytes = _lib.call("mrsa_route_topk_workspace_bytes", B, L, C, Hkv, G)
+        if not _fast_shape(C, G, D, topk, scores_fp32, is_causal):
+            nbytes = _lib.call("mrsa_route_topk_workspace_bytes", B, L, C, Hkv, G)
         ws = torch.empty(max(nbytes, 0) // 4, dtype=torch.float32, device=q5.device)
         st = _lib.call("mrsa_route_topk_ws_fwd", *args, _lib.ptr(ws), int(nbytes),
                        _lib.stream_of(qc))

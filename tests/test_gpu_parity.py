@@ -161,6 +161,23 @@ def test_route_topk_vs_oracle(L, C, G, topk):
     _check_route(idx, sc, q5, lmk, lse4, bias4, drop, topk, f"route L={L} C={C} G={G}")
 
 
+@pytest.mark.parametrize("L,C,G,topk", [(1000, 256, 7, 32), (300, 130, 8, 20)])
+def test_route_topk_one_pass_equals_two_pass(L, C, G, topk):
+    # The matrix-core kernel with a raw-score workspace (one pass, picks read
+    # back from the workspace) against the same kernel recomputing the picks'
+    # raw scores in a second pass: same indices, same bf16 scores.
+    _note(f"route one pass vs two pass L={L} C={C} G={G} K={topk}")
+    q5, lmk, lse4, bias4, drop, _ = _route_case(L, C, G, 4, 40 + L)
+    args = (q5.to(DEV), lmk.to(DEV), lse4.to(DEV), topk, 64)
+    kw = dict(bias4=bias4.to(DEV), drop_mask=drop.to(DEV))
+    i1, s1 = route_topk_launch(*args, use_workspace=True, **kw)
+    i2, s2 = route_topk_launch(*args, use_workspace=False, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(i1, i2)
+    assert torch.equal(s1.view(torch.int16), s2.view(torch.int16))
+    _check_route(i1, s1, q5, lmk, lse4, bias4, drop, topk, f"route one pass L={L} C={C}")
+
+
 @pytest.mark.parametrize("L,C,G,topk,mode,causal,fp32,shared", [
     (32, 2048, 7, 32, "post_softmax", False, False, False),   # the cached block step
     (40, 1000, 8, 20, "pre_softmax", False, True, False),
