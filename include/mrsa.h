@@ -371,6 +371,29 @@ int mrsa_selected_attention_keep_fwd(const void* q, const void* k, const void* v
                                      void* stream);
 
 /*
+ * Routed chunk attention with the output fusion folded in: the result is
+ * fuse_hils_outputs(remote, local_output, local_weight)
+ * (ops/hils_bidir_output_fusion_tilelang.py:138-148) of the routed output
+ * `remote` that mrsa_selected_attention_keep_fwd would write, bit for bit,
+ * without writing or re-reading `remote`.  It has no counterpart in the
+ * reference, which runs the two ops in sequence (dream_dllm_hils/
+ * attention.py:1770-1774); it serves the route-layer composition.
+ * Arguments as mrsa_selected_attention_keep_fwd (token_keep may be null),
+ * plus
+ *   local_output: bf16 [batch, q_len, q_heads, head_dim], 8-byte aligned
+ *   local_weight: bf16 [batch, q_len, q_heads]
+ */
+int mrsa_selected_attention_fused_fwd(const void* q, const void* k, const void* v_tiles,
+                                      const void* weights, const int32_t* indices,
+                                      const uint8_t* key_valid, const int8_t* token_keep,
+                                      const void* local_output, const void* local_weight,
+                                      int64_t batch, int64_t q_len, int64_t kv_len,
+                                      int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                      int64_t topk, int64_t chunk_size, int mask_last_token,
+                                      float sm_scale, int64_t parts, float* partial, void* out,
+                                      void* stream);
+
+/*
  * Global token keep: select_global_token_keep
  * (dream_dllm_hils/token_refinement.py:112-148) without training noise.  In
  * each of `rows` rows of n fp32 scores the min(token_budget, n) largest are

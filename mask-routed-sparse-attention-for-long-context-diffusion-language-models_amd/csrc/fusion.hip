@@ -10,9 +10,7 @@ using namespace mrsa;
 namespace {
 
 __device__ __forceinline__ uint32_t fuse_pair(uint32_t r, uint32_t l, float w) {
-  const float lo = __fadd_rn(bf16_lo(r), __fmul_rn(w, bf16_lo(l)));
-  const float hi = __fadd_rn(bf16_hi(r), __fmul_rn(w, bf16_hi(l)));
-  return pack_bf16x2(lo, hi);
+  return fuse_bf16x2(r, l, w);
 }
 
 // Vector path: 8 bf16 (16 bytes) per lane-iteration; head_dim % 8 == 0.

@@ -47,6 +47,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) { return pack_bf16x2(f, 0.f) & 0xffffu; }
+// Output fusion of two packed bf16 pairs: bf16(r + w * l) per element, the
+// multiply and the add rounded separately (no FMA contraction), as
+// ops/hils_bidir_output_fusion_tilelang.py:28-35 evaluates it in fp32.
+__device__ __forceinline__ uint32_t fuse_bf16x2(uint32_t r, uint32_t l, float w) {
+  const float lo = __fadd_rn(bf16_lo(r), __fmul_rn(w, bf16_lo(l)));
+  const float hi = __fadd_rn(bf16_hi(r), __fmul_rn(w, bf16_hi(l)));
+  return pack_bf16x2(lo, hi);
+}
 
 __device__ __forceinline__ f32x4_t mfma_bf16_16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),

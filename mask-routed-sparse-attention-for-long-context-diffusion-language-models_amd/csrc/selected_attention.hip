@@ -107,6 +107,12 @@ struct SelArgs {
   // Queries per tile actually used (<= the split's capacity): tile x covers
   // queries [x * tq, x * tq + tq).
   int tq;
+  // Optional output fusion (both null or both set): out = bf16(bf16(routed)
+  // + fuse_w[row] * fuse_local[row]) with local output bf16 [B, Lq, Hq, 128]
+  // and local weight bf16 [B, Lq, Hq] -- fuse_hils_outputs folded into the
+  // epilogue (or into the part sum).
+  const uint16_t* fuse_local;
+  const uint16_t* fuse_w;
 };
 
 // LDS carve-up (byte offsets, 16-aligned).  The p_* arrays are only used by
@@ -808,6 +814,21 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
         continue;
       }
       uint16_t* orow = a.out + row * 128;
+      if (a.fuse_local) {
+        const float wl = bf16_to_f32(a.fuse_w[row]);
+        const uint16_t* lrow = a.fuse_local + row * 128;
+        u32x2_t l[8];
+#pragma unroll
+        for (int td = 0; td < 8; ++td) l[td] = *reinterpret_cast<const u32x2_t*>(lrow + 16 * td + 4 * grp);
+#pragma unroll
+        for (int td = 0; td < 8; ++td) {
+          u32x2_t o;
+          o[0] = fuse_bf16x2(pack_bf16x2(acc[nt][td][0], acc[nt][td][1]), l[td][0], wl);
+          o[1] = fuse_bf16x2(pack_bf16x2(acc[nt][td][2], acc[nt][td][3]), l[td][1], wl);
+          *reinterpret_cast<u32x2_t*>(orow + 16 * td + 4 * grp) = o;
+        }
+        continue;
+      }
 #pragma unroll
       for (int td = 0; td < 8; ++td) {
         u32x2_t o;
@@ -819,10 +840,14 @@ __global__ void __launch_bounds__(SP::kThreads) selected_attn_kernel(SelArgs a) 
   }
 }
 
-// Sum of the walk parts' fp32 partial outputs, rounded to bf16 once.
+// Sum of the walk parts' fp32 partial outputs, rounded to bf16 once (and
+// fused with the local branch when fuse_local is set: 32 groups of 4 per
+// 128-wide row).
 __global__ void __launch_bounds__(256) sum_parts_kernel(const float* __restrict__ partial,
                                                         int parts, int64_t n4,
-                                                        uint16_t* __restrict__ out) {
+                                                        uint16_t* __restrict__ out,
+                                                        const uint16_t* __restrict__ fuse_local,
+                                                        const uint16_t* __restrict__ fuse_w) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n4; e += stride) {
     f32x4_t s = reinterpret_cast<const f32x4_t*>(partial)[e];
@@ -834,6 +859,12 @@ __global__ void __launch_bounds__(256) sum_parts_kernel(const float* __restrict_
     u32x2_t o;
     o[0] = pack_bf16x2(s[0], s[1]);
     o[1] = pack_bf16x2(s[2], s[3]);
+    if (fuse_local) {
+      const float wl = bf16_to_f32(fuse_w[e >> 5]);
+      const u32x2_t l = reinterpret_cast<const u32x2_t*>(fuse_local)[e];
+      o[0] = fuse_bf16x2(o[0], l[0], wl);
+      o[1] = fuse_bf16x2(o[1], l[1], wl);
+    }
     reinterpret_cast<u32x2_t*>(out)[e] = o;
   }
 }
@@ -956,6 +987,8 @@ extern "C" int mrsa_selected_attention_fwd(const void* q, const void* k, const v
   a.parts = 1;
   a.partial = nullptr;
   a.keep = nullptr;
+  a.fuse_local = nullptr;
+  a.fuse_w = nullptr;
   return launch_selected<false>(a, (hipStream_t)stream);
 }
 
@@ -1002,6 +1035,8 @@ extern "C" int mrsa_candidate_token_scores_fwd(const void* q, const void* k,
   a.parts = 1;
   a.partial = nullptr;
   a.keep = nullptr;
+  a.fuse_local = nullptr;
+  a.fuse_w = nullptr;
   return launch_selected<true>(a, s);
 }
 
@@ -1014,7 +1049,7 @@ int selected_forward(const void* q, const void* k, const void* v_tiles, const vo
                      int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
                      int64_t kv_heads, int64_t head_dim, int64_t topk, int64_t chunk_size,
                      int mask_last_token, float sm_scale, int64_t parts, float* partial,
-                     void* out, void* stream) {
+                     const void* fuse_local, const void* fuse_w, void* out, void* stream) {
   int st = check_common(q, k, indices, batch, q_len, kv_len, q_heads, kv_heads, head_dim, topk,
                         chunk_size, sm_scale);
   if (st != MRSA_OK) return st;
@@ -1049,13 +1084,18 @@ int selected_forward(const void* q, const void* k, const void* v_tiles, const vo
   a.parts = (int)parts;
   a.partial = parts > 1 ? partial : nullptr;
   a.keep = keep;
+  if ((fuse_local == nullptr) != (fuse_w == nullptr)) return MRSA_ERR_INVALID_ARGUMENT;
+  if (fuse_local && (uintptr_t)fuse_local % 8 != 0) return MRSA_ERR_INVALID_ARGUMENT;
+  a.fuse_local = (const uint16_t*)fuse_local;
+  a.fuse_w = (const uint16_t*)fuse_w;
   hipStream_t s = (hipStream_t)stream;
   st = keep ? launch_selected<false, true>(a, s) : launch_selected<false>(a, s);
   if (st != MRSA_OK || parts == 1) return st;
   const int64_t n4 = batch * q_len * q_heads * 128 / 4;
   const int64_t blocks = std::min<int64_t>((n4 + 255) / 256, 4096);
   hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)blocks), dim3(256), 0, s, partial,
-                     (int)parts, n4, (uint16_t*)out);
+                     (int)parts, n4, (uint16_t*)out, (const uint16_t*)fuse_local,
+                     (const uint16_t*)fuse_w);
   return mrsa_launch_status();
 }
 
@@ -1069,7 +1109,7 @@ extern "C" int mrsa_selected_attention_split_fwd(
     void* out, void* stream) {
   return selected_forward(q, k, v_tiles, weights, indices, key_valid, nullptr, batch, q_len,
                           kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
-                          sm_scale, parts, partial, out, stream);
+                          sm_scale, parts, partial, nullptr, nullptr, out, stream);
 }
 
 extern "C" int mrsa_selected_attention_keep_fwd(
@@ -1081,5 +1121,19 @@ extern "C" int mrsa_selected_attention_keep_fwd(
   if (batch > 0 && q_len > 0 && !token_keep) return MRSA_ERR_INVALID_ARGUMENT;
   return selected_forward(q, k, v_tiles, weights, indices, key_valid, token_keep, batch, q_len,
                           kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
-                          sm_scale, parts, partial, out, stream);
+                          sm_scale, parts, partial, nullptr, nullptr, out, stream);
+}
+
+extern "C" int mrsa_selected_attention_fused_fwd(
+    const void* q, const void* k, const void* v_tiles, const void* weights,
+    const int32_t* indices, const uint8_t* key_valid, const int8_t* token_keep,
+    const void* local_output, const void* local_weight, int64_t batch, int64_t q_len,
+    int64_t kv_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t topk,
+    int64_t chunk_size, int mask_last_token, float sm_scale, int64_t parts, float* partial,
+    void* out, void* stream) {
+  if (batch > 0 && q_len > 0 && (!local_output || !local_weight))
+    return MRSA_ERR_INVALID_ARGUMENT;
+  return selected_forward(q, k, v_tiles, weights, indices, key_valid, token_keep, batch, q_len,
+                          kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
+                          sm_scale, parts, partial, local_output, local_weight, out, stream);
 }

@@ -11,7 +11,8 @@ token budget, fusion weights from the affine gate at topk >= 32):
     routing        route_topk_g7 with remote_drop_mask(key_valid, W, S)
     weights        _route_weights_torch (affine gate)
     remote branch  selected_attention_g7
-    output         fuse_hils_outputs(remote, local, local_weight)
+    output         fuse_hils_outputs(remote, local, local_weight), folded into
+                   the routed-attention epilogue (same bits)
 
 ``swa_attention`` is ``KernelDreamSlidingWindowAttention.forward``
 (attention.py:1168-1220) between projections and o_proj.
@@ -33,7 +34,6 @@ from dataclasses import dataclass, field
 
 import torch
 
-from .fusion import fuse_hils_outputs
 from .kernel_utils import drop_mask_rows_launch
 from .local_attention import local_attention_launch
 from .pool import chunk_attn_pool_gqa_prior
@@ -151,13 +151,16 @@ def route_attention(
         token_keep = refine_remote_tokens_g7(q, k, indices, kv_bool, S, cfg.token_budget,
                                              training=False)
         _mark("token_refinement")
-    remote_out = selected_attention_launch(q, k, vt, remote_w, indices, kv_bool, S,
-                                           token_keep=token_keep)
+    # Routed attention with the output fusion in its epilogue:
+    # fuse_hils_outputs(remote, local_out, local_w) without materialising remote.
+    out = selected_attention_launch(q, k, vt, remote_w, indices, kv_bool, S,
+                                    token_keep=token_keep, fuse_local=local_out,
+                                    fuse_weight=local_w)
     _mark("selected_attention")
-    out = fuse_hils_outputs(remote_out, local_out, local_w)
-    _mark("fusion")
     if not return_intermediates:
         return out
+    remote_out = selected_attention_launch(q, k, vt, remote_w, indices, kv_bool, S,
+                                           token_keep=token_keep)
     return out, {
         "local_output": local_out, "local_lse": local_lse, "landmark_keys": lmk,
         "entropy": entropy, "prior_bias": prior, "indices": indices, "scores": scores,
@@ -413,10 +416,11 @@ def _cached_route_body(q, route_q, cache, query_positions, affected_chunks, entr
     remote_w, local_w = route_weights_launch(
         scores, indices, cache.prior_bias, local_lse, temperature=1.0
     )
-    remote_out = selected_attention_launch(q, cache.key, vt, remote_w, indices, cache.key_valid, S)
-    out = fuse_hils_outputs(remote_out, local_out, local_w)
+    out = selected_attention_launch(q, cache.key, vt, remote_w, indices, cache.key_valid, S,
+                                    fuse_local=local_out, fuse_weight=local_w)
     if not return_intermediates:
         return out
+    remote_out = selected_attention_launch(q, cache.key, vt, remote_w, indices, cache.key_valid, S)
     return out, {
         "local_output": local_out, "local_lse": local_lse, "indices": indices,
         "scores": scores, "remote_weights": remote_w, "local_weight": local_w,

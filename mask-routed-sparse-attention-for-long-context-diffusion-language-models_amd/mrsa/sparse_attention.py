@@ -83,13 +83,18 @@ def selected_attention_launch(
     sm_scale: float | None = None,
     parts: int | None = None,
     token_keep: torch.Tensor | None = None,
+    fuse_local: torch.Tensor | None = None,
+    fuse_weight: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """q [B, Lq, Hq, D], k [B, Lk, Hkv, D], weights [B, Lq, Hq, K] -> [B, Lq, Hq, D] bf16.
 
     ``parts`` splits each walk over that many workgroups (fp32 partial
     outputs summed by a second kernel); None picks it with ``walk_parts``.
     ``token_keep`` [B, Lq, Hkv, K, chunk_size] (nonzero = kept) additionally
-    masks the keys of each query's slot k.
+    masks the keys of each query's slot k.  ``fuse_local`` [B, Lq, Hq, D] and
+    ``fuse_weight`` [B, Lq, Hq] (bf16, both or neither) fold the output
+    fusion in: the result is fuse_hils_outputs(routed, fuse_local,
+    fuse_weight), bit for bit, without materialising the routed output.
     """
 
     B, Lq, Hq, D = q.shape
@@ -108,7 +113,29 @@ def selected_attention_launch(
     idx = indices.to(torch.int32).contiguous()
     kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
     out = torch.empty(B, Lq, Hq, D, dtype=torch.bfloat16, device=q.device)
-    if token_keep is not None:
+    if (fuse_local is None) != (fuse_weight is None):
+        raise ValueError("fuse_local and fuse_weight go together")
+    if fuse_local is not None:
+        if fuse_local.shape != (B, Lq, Hq, D) or fuse_weight.shape != (B, Lq, Hq):
+            raise ValueError(
+                f"fusion shapes {tuple(fuse_local.shape)} / {tuple(fuse_weight.shape)} do not "
+                f"match the output [{B}, {Lq}, {Hq}, {D}]")
+        lo = fuse_local.to(torch.bfloat16).contiguous()
+        lw = fuse_weight.to(torch.bfloat16).contiguous()
+        keep = None
+        if token_keep is not None:
+            keep = token_keep.to(device=q.device, dtype=torch.int8).contiguous()
+        partial = None
+        if parts > 1:
+            partial = torch.empty(parts, B, Lq, Hq, D, dtype=torch.float32, device=q.device)
+        st = _lib.call(
+            "mrsa_selected_attention_fused_fwd",
+            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(w), _lib.ptr(idx),
+            _lib.ptr(kv), _lib.ptr(keep), _lib.ptr(lo), _lib.ptr(lw), B, Lq, Lk, Hq, Hkv, D, K,
+            int(chunk_size), 1 if mask_last_token else 0, float(sm_scale), parts,
+            _lib.ptr(partial), _lib.ptr(out), _lib.stream_of(qc),
+        )
+    elif token_keep is not None:
         keep = token_keep.to(device=q.device, dtype=torch.int8).contiguous()
         partial = None
         if parts > 1:

@@ -378,6 +378,35 @@ def test_selected_attention_walk_split(Lq, Lk, K, parts):
     torch.testing.assert_close(out.float(), whole.float(), atol=8e-3, rtol=8e-3)
 
 
+@pytest.mark.parametrize("Lq,Lk,K,parts,keep", [(700, 2048, 32, 1, False), (32, 8192, 32, 9, False),
+                                                  (200, 2048, 16, 1, True), (40, 4096, 8, 3, True)])
+def test_selected_attention_fused_output_equals_fusion(Lq, Lk, K, parts, keep):
+    # The output fusion folded into the routed-attention epilogue (parts == 1)
+    # or into the part sum (parts > 1) gives exactly the bits of the routed
+    # output followed by fuse_hils_outputs.
+    _note(f"selected fused Lq={Lq} Lk={Lk} K={K} parts={parts} keep={keep}")
+    Hkv, G, D, C = 4, 7, 128, Lk // 64
+    q = _rand((1, Lq, Hkv * G, D), 80).bfloat16()
+    k, v = _planted_kv(Lk, Hkv, D, 81)
+    idx = _sorted_routes(Lq, Hkv, K, C, 82, neg_rows=(0,))
+    w = torch.softmax(_rand((1, Lq, Hkv * G, K), 83), -1).bfloat16()
+    valid = torch.rand(1, Lk, generator=torch.Generator().manual_seed(84)) > 0.03
+    local = _rand((1, Lq, Hkv * G, D), 85).bfloat16().to(DEV)
+    lw = torch.rand(1, Lq, Hkv * G, generator=torch.Generator().manual_seed(86)).bfloat16().to(DEV)
+    tk = None
+    if keep:
+        tk = (torch.rand(1, Lq, Hkv, K, 64, generator=torch.Generator().manual_seed(87)) > 0.5)
+        tk = tk.to(torch.int8).to(DEV)
+    args = (q.to(DEV), k.to(DEV), mrsa.value_tiles(v.to(DEV)), w.to(DEV), idx.to(DEV),
+            valid.to(DEV), 64)
+    remote = selected_attention_launch(*args, parts=parts, token_keep=tk)
+    fused = selected_attention_launch(*args, parts=parts, token_keep=tk, fuse_local=local,
+                                      fuse_weight=lw)
+    expect = mrsa.fuse_hils_outputs(remote, local, lw)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int16), expect.view(torch.int16))
+
+
 def test_selected_attention_reference_kat():
     # test_hils_non_power_two_topk.py:95-142 (cached and uncached shapes).
     for query_len in (35, 2048):
