@@ -111,8 +111,11 @@ def cpu_baseline(budget_s: float = 20.0):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # None: per workload.  The route and SWA steps take ~1-3 ms; their kernels
+    # reach steady clocks only after a few dozen launches, so the default
+    # warmup is long enough for the timed steps to see that state.
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("route", "decode", "swa", "model"), default="route")
     ap.add_argument("--token-budget", type=int, default=0,
@@ -124,6 +127,11 @@ def main() -> int:
                     help="first run a plain 1 GiB device copy three times (reference "
                          "dispatch for scaling FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
+    short = args.workload in ("route", "swa")
+    if args.steps is None:
+        args.steps = 50 if short else 20
+    if args.warmup is None:
+        args.warmup = 30 if short else 5
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
               "the route layer shards by KV head / sequence as described in DESIGN.md",
