@@ -450,6 +450,70 @@ def test_candidate_token_scores_vs_oracle():
     torch.testing.assert_close(got[fin], ref[fin], atol=1e-3, rtol=1e-3)
 
 
+def test_route_layer_config2_full_size_sampled_rows():
+    # BASELINE configuration 2 at its full size (L=16384, 28/4 heads, 256
+    # chunks, planted per-chunk key shift): the GPU route layer against the
+    # oracle stage by stage on 64 sampled query rows (sequence ends, chunk
+    # boundaries, random rows).  Each oracle stage takes that stage's GPU
+    # inputs; its rows do not depend on the other rows, so the full-size
+    # layer is checked without running the oracle over all 16384 rows.
+    _note("route layer config 2, full size, sampled rows")
+    L, Hq, Hkv, D, S, G, K = 16384, 28, 4, 128, 64, 7, 32
+    C = L // S
+    cfg = mrsa.RouteLayerConfig()
+    q = _rand((1, L, Hq, D), 90).bfloat16()
+    k, v = _planted_kv(L, Hkv, D, 91)
+    scale = torch.ones(Hq)
+    valid = torch.ones(1, L, dtype=torch.bool)
+    out, mid = mrsa.route_attention(q.to(DEV), k.to(DEV), v.to(DEV), q.to(DEV), scale.to(DEV),
+                                    valid.to(DEV), cfg, return_intermediates=True)
+    torch.cuda.synchronize()
+    mid = {n: (t.cpu() if torch.is_tensor(t) else t) for n, t in mid.items()}
+    out = out.cpu()
+    rnd = torch.randint(0, L, (56,), generator=torch.Generator().manual_seed(92)).tolist()
+    rows = torch.tensor(sorted(set([0, 1, 62, 63, 64, 8191, 16382, 16383] + rnd)))
+    n = rows.numel()
+    # Local branch (window W + S - 1 with inert landmark slots).
+    lo, ll = O.local_attention(q[:, rows], k, v, valid, cfg.local_window + S - 1, S,
+                               query_positions=rows, query_block=1)
+    _assert_close_attn(mid["local_output"][:, rows], lo, "cfg2 local rows")
+    torch.testing.assert_close(mid["local_lse"][:, rows], ll, atol=2e-3, rtol=1e-4)
+    # Landmark pool and prior over all 256 chunks.
+    lmk, ent = O.chunk_attn_pool(q[:, S - 1 :: S].reshape(1, C, Hkv, G, D),
+                                 k.reshape(1, C, S, Hkv, D), valid.reshape(1, C, S))
+    torch.testing.assert_close(mid["landmark_keys"].float().reshape(lmk.shape), lmk,
+                               atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(mid["prior_bias"].float().reshape(ent.shape), ent, atol=1e-3,
+                               rtol=1e-3)
+    # Routing of the sampled rows: indices bit-exact away from near ties.
+    drop = O.remote_drop_mask(valid, cfg.local_window, S)[:, rows]
+    ridx, rsc, sel = O.route_topk(
+        q[:, rows].reshape(1, n, Hkv, G, D), mid["landmark_keys"].reshape(1, C, Hq, D),
+        mid["local_lse"][:, rows].reshape(1, n, Hkv, G), K, S, drop_mask=drop,
+        bias4=mid["prior_bias"].reshape(1, C, Hkv, G))
+    near = O.boundary_gap(sel, K) < NEAR_TIE
+    gidx = mid["indices"][:, rows].long()
+    rows_bad = (gidx != ridx).any(-1)
+    print(f"cfg2 routing rows: {n * Hkv} near_ties={int(near.sum())} "
+          f"mismatched={int(rows_bad.sum())}", flush=True)
+    assert int((rows_bad & ~near).sum()) == 0
+    ok = (~rows_bad)[..., None, None].expand(1, n, Hkv, G, K)
+    gsc = mid["scores"][:, rows].float().reshape(1, n, Hkv, G, K)
+    torch.testing.assert_close(gsc[ok], rsc.bfloat16().float()[ok], atol=0.02, rtol=0.01)
+    # Route weights, routed attention and the fused output of the sampled rows.
+    rw, lw = O.route_weights(mid["scores"][:, rows], mid["indices"][:, rows].long(), mid["prior_bias"],
+                             mid["local_lse"][:, rows], temperature=cfg.temperature,
+                             gate_offset=cfg.gate_offset, gate_scale=cfg.gate_scale)
+    torch.testing.assert_close(mid["remote_weights"][:, rows].float(), rw, atol=1e-2, rtol=1e-2)
+    torch.testing.assert_close(mid["local_weight"][:, rows].float(), lw, atol=1e-2, rtol=1e-2)
+    remote = O.selected_attention(q[:, rows], k, v, mid["remote_weights"][:, rows],
+                                  mid["indices"][:, rows], valid, S)
+    _assert_close_attn(mid["remote_output"][:, rows], remote, "cfg2 routed rows")
+    fused = O.fuse_outputs(mid["remote_output"][:, rows], mid["local_output"][:, rows],
+                           mid["local_weight"][:, rows])
+    assert torch.equal(out[:, rows].view(torch.int16), fused.view(torch.int16))
+
+
 def test_route_layer_vs_oracle():
     _note("route layer L=2048")
     L, Hq, Hkv, D = 2048, 28, 4, 128
