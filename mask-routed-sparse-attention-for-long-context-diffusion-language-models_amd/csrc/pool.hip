@@ -59,18 +59,28 @@ __global__ void __launch_bounds__(kThreads)
   const bool chunk_valid = flag[0] != 0;
 
   // Logits: each thread owns (g, s) pairs; the start of the reduction over d
-  // is staggered by s so neighbouring threads hit different LDS banks.
+  // is staggered by s (in units of 8) so neighbouring threads hit different
+  // LDS banks.  K and q move as 16-byte LDS reads, 8 elements at a time,
+  // accumulated one by one in d order (D % 8 == 0).
   for (int p = tid; p < G * S; p += kThreads) {
     const int g = p / S, s = p - g * S;
     const float* qr = qs + g * D;
     const uint16_t* kr = ks + s * D;
     int d = (s * 8) % D;
     float acc = 0.f;
-    for (int i = 0; i < D; i += 2) {
-      const uint32_t w = *reinterpret_cast<const uint32_t*>(kr + d);
-      acc = fmaf(qr[d], bf16_lo(w), acc);
-      acc = fmaf(qr[d + 1], bf16_hi(w), acc);
-      d += 2;
+    for (int i = 0; i < D; i += 8) {
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(kr + d);
+      const f32x4_t qa = *reinterpret_cast<const f32x4_t*>(qr + d);
+      const f32x4_t qb = *reinterpret_cast<const f32x4_t*>(qr + d + 4);
+      acc = fmaf(qa[0], bf16_lo(w[0]), acc);
+      acc = fmaf(qa[1], bf16_hi(w[0]), acc);
+      acc = fmaf(qa[2], bf16_lo(w[1]), acc);
+      acc = fmaf(qa[3], bf16_hi(w[1]), acc);
+      acc = fmaf(qb[0], bf16_lo(w[2]), acc);
+      acc = fmaf(qb[1], bf16_hi(w[2]), acc);
+      acc = fmaf(qb[2], bf16_lo(w[3]), acc);
+      acc = fmaf(qb[3], bf16_hi(w[3]), acc);
+      d += 8;
       if (d >= D) d -= D;
     }
     const bool real = (s < S - 1) && vs[s];
@@ -110,14 +120,37 @@ __global__ void __launch_bounds__(kThreads)
   }
   __syncthreads();
 
-  // Pooled key: lmk[g][d] = sum_s w[g][s] * k[s][d], fp32 accumulation.
-  for (int p = tid; p < G * D; p += kThreads) {
-    const int g = p / D, d = p - g * D;
+  // Pooled key: lmk[g][d] = sum_s w[g][s] * k[s][d], fp32 accumulation in s
+  // order; each thread owns 8 consecutive d of one head (16-byte K reads).
+  const int dv = D / 8;
+  uint16_t* lbase = lmk + ((bc * H + h) * G) * (int64_t)D;
+  const bool lvec = ((uintptr_t)lmk & 15) == 0;
+  for (int p = tid; p < G * dv; p += kThreads) {
+    const int g = p / dv, c = p - g * dv;
     const float* wr = pw + g * S;
-    float acc = 0.f;
-    for (int s = 0; s < S; ++s) acc = fmaf(wr[s], bf16_to_f32(ks[s * D + d]), acc);
-    if (!dense && !chunk_valid) acc = 0.f;
-    lmk[((bc * H + h) * G) * (int64_t)D + p] = (uint16_t)f32_to_bf16(acc);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < S; ++s) {
+      const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(ks + s * D + 8 * c);
+      const float w = wr[s];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] = fmaf(w, bf16_lo(kv[j]), acc[2 * j]);
+        acc[2 * j + 1] = fmaf(w, bf16_hi(kv[j]), acc[2 * j + 1]);
+      }
+    }
+    if (!dense && !chunk_valid)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    uint16_t* dst = lbase + g * D + 8 * c;
+    if (lvec) {
+      u32x4_t o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = pack_bf16x2(acc[2 * j], acc[2 * j + 1]);
+      *reinterpret_cast<u32x4_t*>(dst) = o;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dst[j] = (uint16_t)f32_to_bf16(acc[j]);
+    }
   }
 }
 
