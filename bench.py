@@ -263,11 +263,18 @@ def swa_flops(L: int, W: int) -> float:
 def swa_main(args, torch, mrsa, dev) -> int:
     """SWA-1280 layer attention (configuration 3): tokens/s of
     swa_attention (V re-layout + window kernel) at L=16384, 28/4 heads, d=128.
-    Seeded N(0,1) q/k/v; the configuration's YaRN RoPE only changes input
-    values, not the work, and is not applied."""
+    Seeded N(0,1) q/k/v with YaRN factor-8 RoPE applied to q and k in fp32
+    over positions 0..L-1 before the bf16 cast."""
+
+    from mrsa.dream import DreamShape, yarn_rotate_fp32
 
     L, W = SWA_L, SWA_WINDOW
-    q, k, v = make_inputs(L, 2468, dev, torch.bfloat16)
+    g = torch.Generator().manual_seed(2468)
+    shape = DreamShape()
+    q = yarn_rotate_fp32(torch.randn(1, L, HQ, D, generator=g).to(dev), shape)
+    k = yarn_rotate_fp32(torch.randn(1, L, HKV, D, generator=g).to(dev), shape)
+    v = torch.randn(1, L, HKV, D, generator=g).to(dev)
+    q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
     valid = torch.ones(1, L, dtype=torch.bool, device=dev)
     stream = torch.cuda.current_stream(dev)
     times = []
@@ -329,16 +336,21 @@ def model_main(args, torch, mrsa, dev) -> int:
     random token ids with 25% set to the mask token.  One step = embeddings to
     logits for every position."""
 
-    from mrsa.dream import DreamShape, DreamWeights, dream_flops, dream_forward, yarn_tables
+    from mrsa.dream import (DreamShape, DreamWeights, dream_flops, dream_forward,
+                            landmark_layout, rope_tables)
 
     shape = DreamShape()
     L = MODEL_L
     w = DreamWeights.random(shape, dev, seed=7)
     g = torch.Generator().manual_seed(8)
-    ids = torch.randint(0, shape.vocab, (1, L), generator=g)
-    ids[torch.rand(1, L, generator=g) < 0.25] = shape.mask_token_id
+    # uniform random text tokens, 25% replaced by the mask token, in the
+    # landmark layout (mask-token landmark slot per chunk, text positions)
+    S = shape.route.chunk_size
+    text = torch.randint(0, shape.vocab, (1, L // S * (S - 1)), generator=g)
+    text[torch.rand(text.shape, generator=g) < 0.25] = shape.mask_token_id
+    ids, pos = landmark_layout(text, shape)
     ids = ids.to(dev)
-    tables = yarn_tables(L, shape, dev)
+    tables = rope_tables(pos.to(dev), shape)
     stream = torch.cuda.current_stream(dev)
     times = []
 

@@ -197,18 +197,24 @@ int mrsa_route_topk_ws_fwd(const void* q, const void* lmk, const float* lse_loca
  *   indices: int32 [batch, seq_len, kv_heads, topk]
  *   prior_bias: fp32 [batch, chunks, kv_heads, groups]
  *   local_lse: fp32 [batch, seq_len, kv_heads * groups]
- *   has_gate_scale != 0 selects the affine-sigmoid gate form
+ *   gate_offset, gate_scale: fp32 device scalars (the layer's
+ *   fusion_gate_offset / fusion_gate_scale parameters, read in place), or
+ *   NULL when not given.  A gate_scale selects the affine-sigmoid form
  *   (sigmoid(gate_scale * (remote_lse - local) + gate_offset)); otherwise the
- *   plain softmax with local_lse - gate_offset when has_gate_offset.
+ *   plain softmax with local_lse - gate_offset when gate_offset is given.
  *   remote_weights (out): bf16 [batch, seq_len, kv_heads * groups, topk]
  *   local_weight (out):   bf16 [batch, seq_len, kv_heads * groups]
+ *   gate_logit (out, or NULL): fp32 [batch, seq_len, kv_heads * groups], the
+ *   return_gate_logit=True output (attention.py:196-235): remote_lse - local
+ *   logit, affine-transformed in the affine form, 0 where every logit is
+ *   masked.
  */
 int mrsa_route_weights_fwd(const void* scores, const int32_t* indices, const float* prior_bias,
                            const float* local_lse, int64_t batch, int64_t seq_len,
                            int64_t chunks, int64_t kv_heads, int64_t groups, int64_t topk,
-                           float temperature, int has_gate_offset, float gate_offset,
-                           int has_gate_scale, float gate_scale, void* remote_weights,
-                           void* local_weight, void* stream);
+                           float temperature, const float* gate_offset, const float* gate_scale,
+                           void* remote_weights, void* local_weight, float* gate_logit,
+                           void* stream);
 
 /*
  * Backward of the route weights; the row logits are recomputed from the
@@ -219,6 +225,8 @@ int mrsa_route_weights_fwd(const void* scores, const int32_t* indices, const flo
  *   forward inputs and options: as mrsa_route_weights_fwd
  *   grad_remote: bf16 [batch, seq_len, kv_heads * groups, topk]
  *   grad_local:  bf16 [batch, seq_len, kv_heads * groups], or NULL for zeros
+ *   grad_gate_logit: fp32 [batch, seq_len, kv_heads * groups], or NULL for
+ *                zeros (upstream gradient of the gate_logit output)
  *   d_scores (out):    fp32 [batch, seq_len, kv_heads * groups, topk]
  *                      (0 at invalid chunk indices)
  *   d_bias (in/out):   fp32 [batch, chunks, kv_heads, groups], caller-zeroed;
@@ -231,11 +239,11 @@ int mrsa_route_weights_fwd(const void* scores, const int32_t* indices, const flo
  */
 int mrsa_route_weights_bwd(const void* scores, const int32_t* indices, const float* prior_bias,
                            const float* local_lse, const void* grad_remote,
-                           const void* grad_local, int64_t batch, int64_t seq_len,
-                           int64_t chunks, int64_t kv_heads, int64_t groups, int64_t topk,
-                           float temperature, int has_gate_offset, float gate_offset,
-                           int has_gate_scale, float gate_scale, float* d_scores,
-                           float* d_bias, float* d_local_lse, float* d_gate, void* stream);
+                           const void* grad_local, const float* grad_gate_logit, int64_t batch,
+                           int64_t seq_len, int64_t chunks, int64_t kv_heads, int64_t groups,
+                           int64_t topk, float temperature, const float* gate_offset,
+                           const float* gate_scale, float* d_scores, float* d_bias,
+                           float* d_local_lse, float* d_gate, void* stream);
 
 /*
  * Re-lays V out as 64-key tiles, each stored transposed (head_dim rows of 64

@@ -30,8 +30,14 @@ __global__ void __launch_bounds__(256)
     route_weights_kernel(const uint16_t* __restrict__ scores, const int32_t* __restrict__ indices,
                          const float* __restrict__ bias, const float* __restrict__ lse,
                          int64_t rows, int64_t L, int64_t C, int Hkv, int G, int K, float inv_t,
-                         int has_off, float off, int affine, float gscale,
-                         uint16_t* __restrict__ rw, uint16_t* __restrict__ lw) {
+                         const float* __restrict__ goff, const float* __restrict__ gsc,
+                         uint16_t* __restrict__ rw, uint16_t* __restrict__ lw,
+                         float* __restrict__ gate_logit) {
+  // Gate parameters are device scalars (the layer's parameters, read in
+  // place: no host round trip); a null pointer means "not given".
+  const int has_off = goff != nullptr, affine = gsc != nullptr;
+  const float off = has_off ? *goff : 0.f;
+  const float gscale = affine ? *gsc : 1.f;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int part = (int)(t % LPR);
   const int64_t r0 = t / LPR;
@@ -89,11 +95,25 @@ __global__ void __launch_bounds__(256)
   // Every lane of a row takes the same branch (m and rmax are row-uniform),
   // so the reductions inside the branches stay within active lanes.
   float lw_val = 0.f;
+  // gate_logit (attention.py:196-235): lse(remote logits) - local logit, then
+  // gate_scale * (.) + gate_offset in the affine form; 0 when every logit is
+  // masked.  -inf (or its affine image) when only the remote ones are.
+  float gl_val = 0.f;
   const float m = fmaxf(rmax, local);
   if (m == neg_inf()) {  // every logit masked: both outputs zero
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = 0.f;
   } else if (!affine) {
+    if (gate_logit) {
+      // Remote LSE against its own max (torch.logsumexp's form), so a local
+      // logit far above the remote ones cannot underflow it.
+      float rs = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) rs += x[j] == neg_inf() ? 0.f : expf(x[j] - rmax);
+#pragma unroll
+      for (int o = 1; o < LPR; o <<= 1) rs += __shfl_xor(rs, o, 64);
+      gl_val = (rmax == neg_inf() ? neg_inf() : rmax + logf(rs)) - local;
+    }
     float sum = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -112,6 +132,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = 0.f;
     lw_val = 1.f;
+    gl_val = gscale * (neg_inf() - local) + off;
   } else {
     float sum = 0.f;
 #pragma unroll
@@ -122,13 +143,15 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int o = 1; o < LPR; o <<= 1) sum += __shfl_xor(sum, o, 64);
     const float remote_lse = rmax + logf(sum);
-    const float gate = gscale * (remote_lse - local) + (has_off ? off : 0.f);
+    const float gate = gscale * (remote_lse - local) + off;
     const float mass = 1.f / (1.f + expf(-gate));
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = (x[j] / sum) * mass;
     lw_val = 1.f - mass;
+    gl_val = gate;
   }
   if (!live) return;
+  if (gate_logit && part == 0) gate_logit[r] = gl_val;
   uint16_t* out = rw + r * K + k0;
   if (VEC && k0 < K) {
     u32x4_t o4;
@@ -146,13 +169,13 @@ __global__ void __launch_bounds__(256)
 template <int LPR>
 int launch_rw(bool vec, hipStream_t s, const uint16_t* scores, const int32_t* indices,
               const float* bias, const float* lse, int64_t rows, int64_t L, int64_t C, int Hkv,
-              int G, int K, float inv_t, int has_off, float off, int affine, float gscale,
-              uint16_t* rw, uint16_t* lw) {
+              int G, int K, float inv_t, const float* goff, const float* gsc, uint16_t* rw,
+              uint16_t* lw, float* gate_logit) {
   const int64_t blocks = (rows * LPR + 255) / 256;
   if (blocks > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
   auto kern = vec ? route_weights_kernel<LPR, true> : route_weights_kernel<LPR, false>;
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, s, scores, indices, bias, lse,
-                     rows, L, C, Hkv, G, K, inv_t, has_off, off, affine, gscale, rw, lw);
+                     rows, L, C, Hkv, G, K, inv_t, goff, gsc, rw, lw, gate_logit);
   return mrsa_launch_status();
 }
 
@@ -162,9 +185,9 @@ extern "C" int mrsa_route_weights_fwd(const void* scores, const int32_t* indices
                                       const float* prior_bias, const float* local_lse,
                                       int64_t batch, int64_t seq_len, int64_t chunks,
                                       int64_t kv_heads, int64_t groups, int64_t topk,
-                                      float temperature, int has_gate_offset, float gate_offset,
-                                      int has_gate_scale, float gate_scale, void* remote_weights,
-                                      void* local_weight, void* stream) {
+                                      float temperature, const float* gate_offset,
+                                      const float* gate_scale, void* remote_weights,
+                                      void* local_weight, float* gate_logit, void* stream) {
   if (batch < 0 || seq_len < 0 || chunks <= 0 || kv_heads <= 0 || groups <= 0 || topk <= 0 ||
       !(temperature > 0.f))
     return MRSA_ERR_INVALID_ARGUMENT;
@@ -180,8 +203,8 @@ extern "C" int mrsa_route_weights_fwd(const void* scores, const int32_t* indices
   auto go = [&](auto lpr) {
     return launch_rw<decltype(lpr)::value>(
         vec, s, (const uint16_t*)scores, indices, prior_bias, local_lse, rows, seq_len, chunks,
-        (int)kv_heads, (int)groups, (int)topk, 1.f / temperature, has_gate_offset, gate_offset,
-        has_gate_scale, gate_scale, (uint16_t*)remote_weights, (uint16_t*)local_weight);
+        (int)kv_heads, (int)groups, (int)topk, 1.f / temperature, gate_offset, gate_scale,
+        (uint16_t*)remote_weights, (uint16_t*)local_weight, gate_logit);
   };
   if (lanes <= 1) return go(std::integral_constant<int, 1>{});
   if (lanes <= 2) return go(std::integral_constant<int, 2>{});
@@ -202,6 +225,9 @@ namespace {
 //     dm = sum g_j q_j - g_local,  dgate = dm mass (1 - mass)
 //     dz_j = q_j (g_j mass - sum_k q_k g_k mass) + dgate s q_j,  d remote_j = dz_j / T
 //     d local_lse = -dgate s / T,  d s = sum dgate (lse - local / T),  d o = sum dgate
+// With an upstream gradient gG of the gate logit (attention.py:196-235) the
+// plain form adds gG q_j / T to d remote_j (q = softmax of the remote logits)
+// and -gG / T to d local_lse; the affine form adds gG to dgate.
 // Rows whose outputs are constant (every logit masked; affine form with no
 // routed chunk) get zero gradients.  Gradients of the selected bias entries
 // are added atomically into d_bias, and the gate gradients into d_gate[0..1]
@@ -211,11 +237,15 @@ __global__ void __launch_bounds__(256)
     route_weights_bwd_kernel(const uint16_t* __restrict__ scores,
                              const int32_t* __restrict__ indices, const float* __restrict__ bias,
                              const float* __restrict__ lse, const uint16_t* __restrict__ g_rw,
-                             const uint16_t* __restrict__ g_lw, int64_t rows, int64_t L, int64_t C,
-                             int Hkv, int G, int K, float inv_t, int has_off, float off,
-                             int affine, float gscale, float* __restrict__ d_scores,
+                             const uint16_t* __restrict__ g_lw, const float* __restrict__ g_gl,
+                             int64_t rows, int64_t L, int64_t C, int Hkv, int G, int K,
+                             float inv_t, const float* __restrict__ goff,
+                             const float* __restrict__ gsc, float* __restrict__ d_scores,
                              float* __restrict__ d_bias, float* __restrict__ d_lse,
                              float* __restrict__ d_gate) {
+  const int has_off = goff != nullptr, affine = gsc != nullptr;
+  const float off = has_off ? *goff : 0.f;
+  const float gscale = affine ? *gsc : 1.f;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int part = (int)(t % LPR);
   const int64_t r0 = t / LPR;
@@ -250,6 +280,7 @@ __global__ void __launch_bounds__(256)
   if (has_off && !affine) local -= off;
   local *= inv_t;
   const float gl = g_lw ? bf16_to_f32(g_lw[r]) : 0.f;
+  const float gG = g_gl ? g_gl[r] : 0.f;
 
   // Branches are row-uniform, so the lane reductions inside stay within
   // active lanes.
@@ -279,9 +310,12 @@ __global__ void __launch_bounds__(256)
     for (int o = 1; o < LPR; o <<= 1) dot += __shfl_xor(dot, o, 64);
     const float pl = el / sum;
     dot += pl * gl;
+    // q_j = e_j / sum_remote e = x_j * sum / (sum - el); no remote chunk: 0.
+    const float rs = sum - el;
+    const float qf = rs > 0.f ? sum / rs : 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = x[j] * (gr[j] - dot) * inv_t;
-    dloc = pl * (gl - dot) * inv_t;
+    for (int j = 0; j < 8; ++j) x[j] = (x[j] * (gr[j] - dot) + gG * x[j] * qf) * inv_t;
+    dloc = (pl * (gl - dot) - gG) * inv_t;
     doff = has_off ? -dloc : 0.f;
   } else {
     float sum = 0.f;
@@ -303,7 +337,7 @@ __global__ void __launch_bounds__(256)
     }
 #pragma unroll
     for (int o = 1; o < LPR; o <<= 1) qg += __shfl_xor(qg, o, 64);
-    const float dgate = (qg - gl) * mass * (1.f - mass);
+    const float dgate = (qg - gl) * mass * (1.f - mass) + gG;
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = x[j] * ((gr[j] - qg) * mass + dgate * gscale) * inv_t;
     dloc = -dgate * gscale * inv_t;
@@ -336,12 +370,12 @@ __global__ void __launch_bounds__(256)
 extern "C" int mrsa_route_weights_bwd(const void* scores, const int32_t* indices,
                                       const float* prior_bias, const float* local_lse,
                                       const void* grad_remote, const void* grad_local,
-                                      int64_t batch, int64_t seq_len, int64_t chunks,
-                                      int64_t kv_heads, int64_t groups, int64_t topk,
-                                      float temperature, int has_gate_offset, float gate_offset,
-                                      int has_gate_scale, float gate_scale, float* d_scores,
-                                      float* d_bias, float* d_local_lse, float* d_gate,
-                                      void* stream) {
+                                      const float* grad_gate_logit, int64_t batch,
+                                      int64_t seq_len, int64_t chunks, int64_t kv_heads,
+                                      int64_t groups, int64_t topk, float temperature,
+                                      const float* gate_offset, const float* gate_scale,
+                                      float* d_scores, float* d_bias, float* d_local_lse,
+                                      float* d_gate, void* stream) {
   if (batch < 0 || seq_len < 0 || chunks <= 0 || kv_heads <= 0 || groups <= 0 || topk <= 0 ||
       !(temperature > 0.f))
     return MRSA_ERR_INVALID_ARGUMENT;
@@ -349,7 +383,7 @@ extern "C" int mrsa_route_weights_bwd(const void* scores, const int32_t* indices
   const int64_t rows = batch * seq_len * kv_heads * groups;
   if (rows == 0) return MRSA_OK;
   if (!scores || !indices || !prior_bias || !local_lse || !grad_remote || !d_scores || !d_bias ||
-      !d_local_lse || ((has_gate_scale || has_gate_offset) && !d_gate))
+      !d_local_lse || ((gate_scale || gate_offset) && !d_gate))
     return MRSA_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   const int lanes = (int)((topk + 7) / 8);
@@ -359,10 +393,10 @@ extern "C" int mrsa_route_weights_bwd(const void* scores, const int32_t* indices
     if (blocks > 0x7fffffff) return (int)MRSA_ERR_UNSUPPORTED;
     hipLaunchKernelGGL(route_weights_bwd_kernel<LPR>, dim3((unsigned)blocks), dim3(256), 0, s,
                        (const uint16_t*)scores, indices, prior_bias, local_lse,
-                       (const uint16_t*)grad_remote, (const uint16_t*)grad_local, rows, seq_len,
-                       chunks, (int)kv_heads, (int)groups, (int)topk, 1.f / temperature,
-                       has_gate_offset, gate_offset, has_gate_scale, gate_scale, d_scores, d_bias,
-                       d_local_lse, (has_gate_scale || has_gate_offset) ? d_gate : nullptr);
+                       (const uint16_t*)grad_remote, (const uint16_t*)grad_local,
+                       grad_gate_logit, rows, seq_len, chunks, (int)kv_heads, (int)groups,
+                       (int)topk, 1.f / temperature, gate_offset, gate_scale, d_scores, d_bias,
+                       d_local_lse, (gate_scale || gate_offset) ? d_gate : nullptr);
     return mrsa_launch_status();
   };
   if (lanes <= 1) return go(std::integral_constant<int, 1>{});

@@ -18,6 +18,7 @@ hand-written HIP kernels in ../csrc (C ABI: include/mrsa.h).  Module map:
     kernel_utils.py     remote_drop_mask(_rows), chunk_aligned_local_bounds, group_pad_to/unpad
     route_layer.py      route_attention, swa_attention  (attention.py route / SWA layers),
                         cached_route_attention + LayerKVCache (fastdllm_attention.py cached step)
+    ops.py              torch.ops.mrsa.* custom operators (schemas, CUDA and fake kernels)
 """
 
 from .fusion import fuse_hils_outputs
@@ -45,6 +46,7 @@ from .token_score import candidate_token_scores_gqa
 from .token_refinement import refine_remote_tokens_g7, select_global_token_keep
 from .topk import online_softmax_topk_head, ref_softmax_topk_max_pooling
 from ._lib import LIB_PATH, MrsaLibraryError, load as load_library
+from . import ops  # registers torch.ops.mrsa.* (after every module it wraps)
 
 __all__ = [
     "HiLS_block_M_head",

@@ -60,12 +60,12 @@ SIGNATURES = {
     ),
     "mrsa_route_weights_fwd": (
         _I,
-        [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _F, _I, _F,
-         _P, _P, _P],
+        [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P,
+         _P, _P, _P, _P],
     ),
     "mrsa_route_weights_bwd": (
         _I,
-        [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _F, _I, _F,
+        [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P,
          _P, _P, _P, _P, _P],
     ),
     "mrsa_value_tiles_bytes": (_I64, [_I64, _I64, _I64, _I64]),

@@ -69,6 +69,17 @@ def yarn_tables(seq_len: int, shape: DreamShape, device) -> tuple[torch.Tensor, 
     Returns fp32 [seq_len, head_dim / 2] tables holding bf16 values (the model
     hands cos/sin to the rotary op in bf16)."""
 
+    inv_freq, attn_factor = yarn_inv_freq(shape)
+    t = torch.arange(seq_len, dtype=torch.float32)
+    freqs = torch.outer(t, inv_freq)
+    cos = (freqs.cos() * attn_factor).to(torch.bfloat16).to(torch.float32)
+    sin = (freqs.sin() * attn_factor).to(torch.bfloat16).to(torch.float32)
+    return cos.to(device).contiguous(), sin.to(device).contiguous()
+
+
+def yarn_inv_freq(shape: DreamShape) -> tuple[torch.Tensor, float]:
+    """fp32 YaRN frequencies [head_dim / 2] and the attention factor."""
+
     dim = shape.head_dim
     base = shape.rope_theta
     factor = shape.yarn_factor
@@ -93,12 +104,21 @@ def yarn_tables(seq_len: int, shape: DreamShape, device) -> tuple[torch.Tensor, 
         extra_weight = 1.0 - ramp
         inv_freq = inv_inter * (1 - extra_weight) + inv_extra * extra_weight
         attn_factor = 0.1 * math.log(factor) + 1.0
-    inv_freq = inv_freq.to(torch.float32)
-    t = torch.arange(seq_len, dtype=torch.float32)
-    freqs = torch.outer(t, inv_freq)
-    cos = (freqs.cos() * attn_factor).to(torch.bfloat16).to(torch.float32)
-    sin = (freqs.sin() * attn_factor).to(torch.bfloat16).to(torch.float32)
-    return cos.to(device).contiguous(), sin.to(device).contiguous()
+    return inv_freq.to(torch.float32), attn_factor
+
+
+def yarn_rotate_fp32(x: torch.Tensor, shape: DreamShape) -> torch.Tensor:
+    """x [B, L, heads, D] rotated in fp32 at positions 0..L-1 with fp32 YaRN
+    cos/sin (BASELINE configuration 3's input preparation); fp32 result."""
+
+    inv_freq, attn_factor = yarn_inv_freq(shape)
+    L, half = x.shape[1], x.shape[-1] // 2
+    ang = torch.outer(torch.arange(L, dtype=torch.float32), inv_freq).to(x.device)
+    c = (ang.cos() * attn_factor)[None, :, None, :]
+    s = (ang.sin() * attn_factor)[None, :, None, :]
+    xf = x.float()
+    x1, x2 = xf[..., :half], xf[..., half:]
+    return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1)
 
 
 @dataclass
@@ -199,21 +219,65 @@ def swiglu(gate_up):
     return out
 
 
+def landmark_layout(text_ids: torch.Tensor, shape: DreamShape):
+    """The physical sequence of the "mask_type" landmark mode for one
+    all-valid document (dream_dllm_hils/data.py:970-1010): every chunk is
+    chunk_size - 1 text tokens followed by a landmark slot holding the mask
+    token; text tokens are numbered 0, 1, ... in order (landmarks skipped)
+    and each landmark takes the position after its chunk's last text token.
+
+    text_ids int64 [1, C * (chunk_size - 1)] -> (input_ids [1, C * chunk_size],
+    position_ids int64 [C * chunk_size]) on text_ids' device."""
+
+    S = shape.route.chunk_size
+    if text_ids.ndim != 2 or text_ids.shape[0] != 1 or text_ids.shape[1] % (S - 1):
+        raise ValueError(f"text_ids must be [1, C * {S - 1}], got {tuple(text_ids.shape)}")
+    C = text_ids.shape[1] // (S - 1)
+    dev = text_ids.device
+    ids = torch.cat([text_ids.reshape(C, S - 1),
+                     torch.full((C, 1), shape.mask_token_id, dtype=text_ids.dtype, device=dev)],
+                    dim=1).reshape(1, C * S)
+    return ids, landmark_positions(C * S, shape, dev)
+
+
+def landmark_positions(seq_len: int, shape: DreamShape, device) -> torch.Tensor:
+    """position_ids of landmark_layout for seq_len physical slots: slot j of
+    chunk c holds text position c (S - 1) + j, the landmark (j = S - 1) the
+    position after its chunk's last text token (data.py:999-1010)."""
+
+    S = shape.route.chunk_size
+    slot = torch.arange(seq_len, device=device)
+    return (slot // S) * (S - 1) + slot % S
+
+
+def rope_tables(position_ids: torch.Tensor, shape: DreamShape):
+    """The YaRN tables of yarn_tables, one row per position id."""
+
+    cos, sin = yarn_tables(int(position_ids.max()) + 1, shape, position_ids.device)
+    return cos[position_ids].contiguous(), sin[position_ids].contiguous()
+
+
 def embed_tokens(w: DreamWeights, input_ids: torch.Tensor) -> torch.Tensor:
     """Token embeddings plus the landmark type offset on every chunk's last
-    slot (the "mask_type" landmark mode, train_fulltext.py:2336-2350)."""
+    slot, which holds the mask token (the "mask_type" landmark mode,
+    train_fulltext.py:2305-2350; ValueError as there when a landmark slot
+    holds another token)."""
 
     S = w.shape.route.chunk_size
+    if bool((input_ids.reshape(-1)[S - 1 :: S] != w.shape.mask_token_id).any()):
+        raise ValueError("landmark_mask marks positions that are not LMK tokens")
     h = F.embedding(input_ids.reshape(-1), w.embed)
     h[S - 1 :: S] = h[S - 1 :: S] + w.lmk_type
     return h
 
 
 @torch.no_grad()
-def dream_forward(w: DreamWeights, input_ids: torch.Tensor, *, tables=None,
+def dream_forward(w: DreamWeights, input_ids: torch.Tensor, *, position_ids=None, tables=None,
                   return_hidden: bool = False) -> torch.Tensor:
-    """Denoising forward of one sequence: input_ids int64 [1, L] ->
-    logits bf16 [L, vocab] (or the final normed hidden [L, hidden])."""
+    """Denoising forward of one sequence: input_ids int64 [1, L] in the
+    landmark layout (landmark_layout) -> logits bf16 [L, vocab] (or the final
+    normed hidden [L, hidden]).  position_ids default to the layout's
+    (landmark_positions); tables = (cos, sin) rows per slot, if precomputed."""
 
     shape = w.shape
     if input_ids.ndim != 2 or input_ids.shape[0] != 1:
@@ -223,7 +287,11 @@ def dream_forward(w: DreamWeights, input_ids: torch.Tensor, *, tables=None,
         raise ValueError(f"sequence length {L} must be a multiple of {shape.route.chunk_size}")
     if input_ids.device.type != "cuda":
         raise ValueError("dream_forward requires CUDA tensors")
-    cos, sin = tables if tables is not None else yarn_tables(L, shape, input_ids.device)
+    if tables is None:
+        if position_ids is None:
+            position_ids = landmark_positions(L, shape, input_ids.device)
+        tables = rope_tables(position_ids, shape)
+    cos, sin = tables
     route = set(shape.route_layers())
     Hq, D = shape.q_heads, shape.head_dim
     h = embed_tokens(w, input_ids)

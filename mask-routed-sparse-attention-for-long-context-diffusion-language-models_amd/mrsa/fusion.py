@@ -42,6 +42,10 @@ def _validate(remote_output, local_output, local_weight):
 
 
 def _fuse_launch(remote_output, local_output, local_weight):
+    return torch.ops.mrsa.fuse_hils_outputs(remote_output, local_output, local_weight)
+
+
+def _fuse_impl(remote_output, local_output, local_weight):
     out = torch.empty_like(remote_output)
     head_dim = remote_output.shape[-1]
     rows = remote_output.numel() // max(head_dim, 1)
@@ -57,6 +61,10 @@ def _fuse_launch(remote_output, local_output, local_weight):
 def fuse_hils_outputs_backward(local_output, local_weight, grad_output):
     """(d_remote, d_local, d_weight), all bf16, for a bf16 upstream gradient."""
 
+    return torch.ops.mrsa.fuse_hils_outputs_bwd(local_output, local_weight, grad_output)
+
+
+def _fuse_bwd_impl(local_output, local_weight, grad_output):
     grad = grad_output.to(torch.bfloat16).contiguous()
     head_dim = local_output.shape[-1]
     rows = local_output.numel() // max(head_dim, 1)

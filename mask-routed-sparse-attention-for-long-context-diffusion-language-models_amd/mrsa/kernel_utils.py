@@ -110,6 +110,11 @@ def remote_drop_mask(
         raise ValueError("remote_drop_mask requires CUDA tensors")
     if window < 0:
         raise ValueError(f"window must be non-negative, got {window}")
+    return torch.ops.mrsa.remote_drop_mask(valid_mask, allowed_mask, int(window), int(chunk_size))
+
+
+def _drop_mask_impl(valid_mask, allowed_mask, window, chunk_size):
+    batch, seq_len = valid_mask.shape
     valid = valid_mask.to(torch.bool).contiguous()
     allowed = None if allowed_mask is None else allowed_mask.to(
         device=valid.device, dtype=torch.bool
@@ -162,6 +167,11 @@ def drop_mask_rows_launch(valid_mask, window, chunk_size, query_positions):
     """remote_drop_mask_rows without the argument checks (positions already
     validated by the caller; the kernel ignores none of them)."""
 
+    return torch.ops.mrsa.remote_drop_mask_rows(valid_mask, query_positions, int(window),
+                                                int(chunk_size))
+
+
+def _drop_mask_rows_impl(valid_mask, query_positions, window, chunk_size):
     batch, seq_len = valid_mask.shape
     rows = query_positions.numel()
     valid = valid_mask.to(torch.bool).contiguous()

@@ -77,7 +77,15 @@ def local_attention_launch(
         sm_scale = D ** -0.5
     if parts is None:
         parts = key_parts(B, Lq, Hkv, Lk, flash_window)
-    parts = int(parts)
+    return torch.ops.mrsa.local_attention(q, k, v_tiles, key_valid, int(flash_window),
+                                          int(inert_chunk), query_positions, float(sm_scale),
+                                          int(parts))
+
+
+def _local_attention_impl(q, k, v_tiles, key_valid, flash_window, inert_chunk, query_positions,
+                          sm_scale, parts):
+    B, Lq, Hq, D = q.shape
+    Lk, Hkv = k.shape[1], k.shape[2]
     qc = q.contiguous()
     kc = k.contiguous()
     kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()

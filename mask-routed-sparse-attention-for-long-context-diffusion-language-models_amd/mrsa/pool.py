@@ -38,6 +38,17 @@ def _validate(mu_q, k_chunked, key_valid):
 
 
 def _launch(mu_q, k_chunked, key_valid, sm_scale, bias_scale=None):
+    if bias_scale is not None and bias_scale.numel() != mu_q.shape[2] * mu_q.shape[3]:
+        raise ValueError(
+            f"bias_scale must have {mu_q.shape[2] * mu_q.shape[3]} elements, "
+            f"got {bias_scale.numel()}")
+    lmk, entropy, prior = torch.ops.mrsa.chunk_attn_pool(mu_q, k_chunked, key_valid,
+                                                         float(sm_scale), bias_scale)
+    return lmk, entropy, (prior if bias_scale is not None else None)
+
+
+def _pool_impl(mu_q, k_chunked, key_valid, sm_scale, bias_scale):
+    """Kernel call; the prior output is empty without a bias scale."""
     batch, chunks, kv_heads, groups, head_dim = mu_q.shape
     chunk_size = k_chunked.shape[2]
     mu = mu_q.contiguous()
@@ -47,22 +58,18 @@ def _launch(mu_q, k_chunked, key_valid, sm_scale, bias_scale=None):
     entropy = torch.empty(
         batch, chunks, kv_heads, groups, device=mu.device, dtype=torch.float32
     )
-    prior = None
+    prior = entropy.new_empty(0)
     scale = None
     if bias_scale is not None:
         scale = bias_scale.to(device=mu.device, dtype=torch.float32).contiguous()
-        if scale.numel() != kv_heads * groups:
-            raise ValueError(
-                f"bias_scale must have {kv_heads * groups} elements, got {scale.numel()}"
-            )
         prior = torch.empty_like(entropy)
     st = _lib.call(
         "mrsa_chunk_attn_pool_gqa_fwd",
         _lib.ptr(mu), _lib.ptr(kc), _lib.ptr(kv),
         batch * chunks, chunk_size, kv_heads, groups, head_dim,
         float(sm_scale), 1 if groups == 1 else 0,
-        _lib.ptr(scale), _lib.ptr(lmk), _lib.ptr(entropy), _lib.ptr(prior),
-        _lib.stream_of(mu),
+        _lib.ptr(scale), _lib.ptr(lmk), _lib.ptr(entropy),
+        _lib.ptr(prior) if scale is not None else None, _lib.stream_of(mu),
     )
     _lib.check(st, "chunk_attn_pool_gqa")
     return lmk, entropy, prior
@@ -73,6 +80,11 @@ def chunk_attn_pool_gqa_backward(mu_q, k_chunked, key_valid, grad_landmark, grad
     """(d_mu_q, d_k_chunked) in bf16 for the pool's upstream gradients
     (either may be None)."""
 
+    return torch.ops.mrsa.chunk_attn_pool_bwd(mu_q, k_chunked, key_valid, grad_landmark,
+                                              grad_entropy, float(sm_scale))
+
+
+def _pool_bwd_impl(mu_q, k_chunked, key_valid, grad_landmark, grad_entropy, sm_scale):
     batch, chunks, kv_heads, groups, head_dim = mu_q.shape
     chunk_size = k_chunked.shape[2]
     mu = mu_q.contiguous()

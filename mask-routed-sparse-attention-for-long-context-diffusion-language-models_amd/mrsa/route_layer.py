@@ -9,7 +9,9 @@ token budget, fusion weights from the affine gate at topk >= 32):
     landmarks      chunk_attn_pool_gqa on the routing query at each landmark slot
     prior          entropy * entropy_bias_scale
     routing        route_topk_g7 with remote_drop_mask(key_valid, W, S)
-    weights        _route_weights_torch (affine gate)
+    weights        _route_weights_torch (layer temperature, affine fusion gate) at
+                   topk >= 32; the plain route_weights (temperature 1, no
+                   gate) below that (attention.py:1571-1578, :1643-1648)
     remote branch  selected_attention_g7
     output         fuse_hils_outputs(remote, local, local_weight), folded into
                    the routed-attention epilogue (same bits)
@@ -52,8 +54,10 @@ class RouteLayerConfig:
     chunk_size: int = 64
     topk: int = 32
     temperature: float = 1.0
-    gate_offset: float | None = 0.0   # fusion_gate_offset at init (attention.py:913)
-    gate_scale: float | None = 1.0    # fusion_gate_scale at init (attention.py:914)
+    # fusion_gate_offset / fusion_gate_scale (attention.py:913-914): numbers,
+    # or the layer's one-element parameter tensors (read on the device)
+    gate_offset: float | torch.Tensor | None = 0.0
+    gate_scale: float | torch.Tensor | None = 1.0
     skip_inert_slots: bool = True     # attention.py:902
     # Remote-token refinement (attention.py:1729-1759, "global_qk" policy):
     # with token_budget > 0 each (query, KV head) keeps only its budget of
@@ -141,10 +145,16 @@ def route_attention(
     )
     scores = scores.reshape(B, L, Hq, cfg.topk)
     _mark("route_topk")
-    remote_w, local_w = route_weights_launch(
-        scores, indices, prior, local_lse, temperature=cfg.temperature,
-        gate_offset=cfg.gate_offset, gate_scale=cfg.gate_scale,
-    )
+    if cfg.topk >= 32:
+        # attention.py:1571-1621: _route_weights_torch with the route
+        # temperature and the fusion gate parameters
+        remote_w, local_w = route_weights_launch(
+            scores, indices, prior, local_lse, temperature=cfg.temperature,
+            gate_offset=cfg.gate_offset, gate_scale=cfg.gate_scale,
+        )
+    else:
+        # attention.py:1643-1648: route_weights, the plain 33-way softmax
+        remote_w, local_w = route_weights_launch(scores, indices, prior, local_lse)
     _mark("route_weights")
     token_keep = None
     if cfg.token_budget > 0:

@@ -14,6 +14,36 @@ import torch
 from . import _lib
 
 
+def _gate_tensor(x, device):
+    """A gate parameter as an fp32 device scalar the kernel reads in place.
+
+    Tensors (the layer's nn.Parameters) are used where they live, without a
+    host round trip; Python numbers become a device scalar through a fill
+    kernel (no copy from host memory).  None stays None ("not given").
+    """
+
+    if x is None:
+        return None
+    if isinstance(x, torch.Tensor):
+        if x.numel() != 1:
+            raise ValueError(f"gate parameters must hold one value, got shape {tuple(x.shape)}")
+        return x.detach().to(device=device, dtype=torch.float32).reshape(()).contiguous()
+    if torch.compiler.is_compiling() or torch._guards.detect_fake_mode() is not None:
+        # traced: a fill op in the graph (a cached tensor would be a fake one)
+        return torch.full((), float(x), dtype=torch.float32, device=device)
+    key = (float(x), device)
+    t = _GATE_CONSTANTS.get(key)
+    if t is None:
+        if len(_GATE_CONSTANTS) > 64:
+            _GATE_CONSTANTS.clear()
+        t = _GATE_CONSTANTS[key] = torch.full((), float(x), dtype=torch.float32, device=device)
+    return t
+
+
+# Device scalars made for numeric gate values, reused across calls.
+_GATE_CONSTANTS: dict = {}
+
+
 def route_weights_launch(
     scores: torch.Tensor,
     indices: torch.Tensor,
@@ -21,27 +51,44 @@ def route_weights_launch(
     local_lse: torch.Tensor,
     *,
     temperature: float = 1.0,
-    gate_offset: float | None = None,
-    gate_scale: float | None = None,
+    gate_offset=None,
+    gate_scale=None,
+    return_gate_logit: bool = False,
 ):
+    """Forward kernel call.  gate_offset / gate_scale: None, a number or a
+    one-element tensor.  Returns (remote bf16, local bf16[, gate_logit fp32])."""
+
+    dev = scores.device
+    remote, local, gl = torch.ops.mrsa.route_weights(
+        scores, indices, prior_bias, local_lse, float(temperature),
+        _gate_tensor(gate_offset, dev), _gate_tensor(gate_scale, dev), bool(return_gate_logit))
+    if return_gate_logit:
+        return remote, local, gl
+    return remote, local
+
+
+def _route_weights_impl(scores, indices, prior_bias, local_lse, temperature, off, scl,
+                        return_gate_logit):
+    """Kernel call; the gate-logit output is empty unless requested."""
     B, L, Hq, K = scores.shape
     _, C, Hkv, G = prior_bias.shape
+    dev = scores.device
     sc = scores.to(torch.bfloat16).contiguous()
     idx = indices.to(torch.int32).contiguous()
     bias = prior_bias.to(torch.float32).contiguous()
     lse = local_lse.to(torch.float32).reshape(B, L, Hq).contiguous()
-    remote = torch.empty(B, L, Hq, K, dtype=torch.bfloat16, device=scores.device)
-    local = torch.empty(B, L, Hq, dtype=torch.bfloat16, device=scores.device)
+    remote = torch.empty(B, L, Hq, K, dtype=torch.bfloat16, device=dev)
+    local = torch.empty(B, L, Hq, dtype=torch.bfloat16, device=dev)
+    gl = torch.empty(B, L, Hq if return_gate_logit else 0, dtype=torch.float32, device=dev)
     st = _lib.call(
         "mrsa_route_weights_fwd",
         _lib.ptr(sc), _lib.ptr(idx), _lib.ptr(bias), _lib.ptr(lse),
-        B, L, C, Hkv, G, K, float(temperature),
-        0 if gate_offset is None else 1, 0.0 if gate_offset is None else float(gate_offset),
-        0 if gate_scale is None else 1, 1.0 if gate_scale is None else float(gate_scale),
-        _lib.ptr(remote), _lib.ptr(local), _lib.stream_of(sc),
+        B, L, C, Hkv, G, K, float(temperature), _lib.ptr(off), _lib.ptr(scl),
+        _lib.ptr(remote), _lib.ptr(local), _lib.ptr(gl) if return_gate_logit else None,
+        _lib.stream_of(sc),
     )
     _lib.check(st, "route_weights")
-    return remote, local
+    return remote, local, gl
 
 
 def _prepared(scores, indices, prior_bias, local_lse):
@@ -56,11 +103,20 @@ def _prepared(scores, indices, prior_bias, local_lse):
 
 def route_weights_backward(
     scores, indices, prior_bias, local_lse, grad_remote, grad_local, *,
-    temperature: float = 1.0, gate_offset: float | None = None, gate_scale: float | None = None,
+    temperature: float = 1.0, gate_offset=None, gate_scale=None, grad_gate_logit=None,
 ):
     """(d_scores fp32, d_bias fp32, d_local_lse fp32, d_gate fp32[2]) for the
-    forward inputs and bf16 upstream gradients (grad_local may be None)."""
+    forward inputs and bf16 upstream gradients (grad_local and
+    grad_gate_logit may be None).  d_gate = (d gate_scale, d gate_offset)."""
 
+    dev = scores.device
+    return torch.ops.mrsa.route_weights_bwd(
+        scores, indices, prior_bias, local_lse, grad_remote, grad_local, grad_gate_logit,
+        float(temperature), _gate_tensor(gate_offset, dev), _gate_tensor(gate_scale, dev))
+
+
+def _route_weights_bwd_impl(scores, indices, prior_bias, local_lse, grad_remote, grad_local,
+                            grad_gate_logit, temperature, off, scl):
     sc, idx, bias, lse = _prepared(scores, indices, prior_bias, local_lse)
     B, L, Hq, K = sc.shape
     _, C, Hkv, G = bias.shape
@@ -70,6 +126,8 @@ def route_weights_backward(
         if grad_remote is None else grad_remote.to(torch.bfloat16).contiguous()
     )
     g_lw = None if grad_local is None else grad_local.to(torch.bfloat16).reshape(B, L, Hq).contiguous()
+    g_gl = (None if grad_gate_logit is None
+            else grad_gate_logit.to(torch.float32).reshape(B, L, Hq).contiguous())
     d_scores = torch.empty(B, L, Hq, K, dtype=torch.float32, device=dev)
     d_bias = torch.zeros(B, C, Hkv, G, dtype=torch.float32, device=dev)
     d_lse = torch.empty(B, L, Hq, dtype=torch.float32, device=dev)
@@ -77,10 +135,8 @@ def route_weights_backward(
     st = _lib.call(
         "mrsa_route_weights_bwd",
         _lib.ptr(sc), _lib.ptr(idx), _lib.ptr(bias), _lib.ptr(lse), _lib.ptr(g_rw),
-        None if g_lw is None else _lib.ptr(g_lw),
-        B, L, C, Hkv, G, K, float(temperature),
-        0 if gate_offset is None else 1, 0.0 if gate_offset is None else float(gate_offset),
-        0 if gate_scale is None else 1, 1.0 if gate_scale is None else float(gate_scale),
+        _lib.ptr(g_lw), _lib.ptr(g_gl),
+        B, L, C, Hkv, G, K, float(temperature), _lib.ptr(off), _lib.ptr(scl),
         _lib.ptr(d_scores), _lib.ptr(d_bias), _lib.ptr(d_lse), _lib.ptr(d_gate),
         _lib.stream_of(sc),
     )
@@ -96,33 +152,44 @@ def _gate_grad(param, value):
 
 class _RouteWeights(torch.autograd.Function):
     # ops/hils_bidir_route_weights_tilelang.py:169-242 (plain form) and the
-    # autograd of attention.py:126-235 (both forms)
+    # autograd of attention.py:126-235 (both forms, gate logit included)
     @staticmethod
-    def forward(ctx, scores, indices, prior_bias, local_lse, gate_offset, gate_scale, temperature):
-        off, scale = _scalar(gate_offset), _scalar(gate_scale)
+    def forward(ctx, scores, indices, prior_bias, local_lse, gate_offset, gate_scale,
+                temperature, want_gate_logit):
         prepared = _prepared(scores, indices, prior_bias, local_lse)
-        remote, local = route_weights_launch(
-            *prepared, temperature=temperature, gate_offset=off, gate_scale=scale
+        dev = scores.device
+        off = _gate_tensor(gate_offset, dev)
+        scl = _gate_tensor(gate_scale, dev)
+        outs = route_weights_launch(
+            *prepared, temperature=temperature, gate_offset=off, gate_scale=scl,
+            return_gate_logit=want_gate_logit,
         )
         ctx.save_for_backward(*prepared)
-        ctx.opts = (temperature, off, scale)
+        ctx.temperature = temperature
+        ctx.gates = (off, scl)
         ctx.params = (gate_offset, gate_scale)
         ctx.dtypes = (scores.dtype, prior_bias.dtype, local_lse.dtype)
-        return remote, local
+        if want_gate_logit:
+            return outs
+        gl = torch.zeros(0, dtype=torch.float32, device=dev)
+        ctx.mark_non_differentiable(gl)
+        return outs[0], outs[1], gl
 
     @staticmethod
-    def backward(ctx, grad_remote, grad_local):
+    def backward(ctx, grad_remote, grad_local, grad_gate_logit):
         sc, idx, bias, lse = ctx.saved_tensors
-        temperature, off, scale = ctx.opts
+        off, scl = ctx.gates
+        if grad_gate_logit is not None and grad_gate_logit.numel() == 0:
+            grad_gate_logit = None
         d_scores, d_bias, d_lse, d_gate = route_weights_backward(
-            sc, idx, bias, lse, grad_remote, grad_local,
-            temperature=temperature, gate_offset=off, gate_scale=scale,
+            sc, idx, bias, lse, grad_remote, grad_local, temperature=ctx.temperature,
+            gate_offset=off, gate_scale=scl, grad_gate_logit=grad_gate_logit,
         )
         s_dt, b_dt, l_dt = ctx.dtypes
         p_off, p_scale = ctx.params
         return (
             d_scores.to(s_dt), None, d_bias.to(b_dt), d_lse.to(l_dt),
-            _gate_grad(p_off, d_gate[1]), _gate_grad(p_scale, d_gate[0]), None,
+            _gate_grad(p_off, d_gate[1]), _gate_grad(p_scale, d_gate[0]), None, None,
         )
 
 
@@ -167,27 +234,23 @@ def route_weights(scores, indices, prior_bias, local_lse):
 
     _validate(scores, indices, prior_bias, local_lse)
     if _needs_grad(scores, prior_bias, local_lse):
-        return _RouteWeights.apply(scores, indices, prior_bias, local_lse, None, None, 1.0)
+        remote, local, _ = _RouteWeights.apply(scores, indices, prior_bias, local_lse, None, None,
+                                               1.0, False)
+        return remote, local
     return route_weights_launch(scores, indices, prior_bias, local_lse)
-
-
-def _scalar(x):
-    if x is None:
-        return None
-    if isinstance(x, torch.Tensor):
-        return float(x.detach().float().reshape(()).item())
-    return float(x)
 
 
 def route_weights_torch(
     scores, indices, prior_bias, local_lse, *, temperature, selected_gumbel=None,
     value_bonus=None, return_gate_logit=False, gate_offset=None, gate_scale=None,
 ):
-    """Same contract as attention.py:126-235 for the forward outputs.
+    """Same contract as attention.py:126-235.
 
-    gate_scale selects the affine-sigmoid form.  The training-only inputs
-    (selected_gumbel, value_bonus) and the gate-logit diagnostic are not
-    produced by the forward kernel.
+    gate_scale selects the affine-sigmoid form; gate_offset / gate_scale are
+    read on the device (the layer's parameters, no host round trip).  With
+    return_gate_logit the third output is the fp32 gate logit.  The
+    training-only additive inputs (selected_gumbel, value_bonus,
+    attention.py:172-181) are rejected with ValueError.
     """
 
     if temperature <= 0:
@@ -208,17 +271,23 @@ def route_weights_torch(
         raise ValueError(f"invalid indices shape {tuple(indices.shape)}")
     if local_lse.shape != (batch, seq_len, h_q):
         raise ValueError(f"invalid local_lse shape {tuple(local_lse.shape)}")
+    if selected_gumbel is not None and selected_gumbel.shape != scores.shape:
+        raise ValueError(f"invalid selected_gumbel shape {tuple(selected_gumbel.shape)}")
+    if value_bonus is not None and value_bonus.shape != scores.shape:
+        raise ValueError(f"invalid value_bonus shape {tuple(value_bonus.shape)}")
     if selected_gumbel is not None or value_bonus is not None:
-        raise ValueError("selected_gumbel / value_bonus are training-only inputs; not supported")
-    if return_gate_logit:
-        raise ValueError("return_gate_logit is a training diagnostic; not produced by the kernel")
+        raise ValueError(
+            "selected_gumbel / value_bonus (training-time Gumbel routing and value-aware "
+            "fusion) are not supported by the gfx950 route-weights kernel")
     if scores.device.type != "cuda":
         raise ValueError("route_weights requires CUDA tensors")
     if _needs_grad(scores, prior_bias, local_lse, gate_offset, gate_scale):
-        return _RouteWeights.apply(
-            scores, indices, prior_bias, local_lse, gate_offset, gate_scale, float(temperature)
+        remote, local, gl = _RouteWeights.apply(
+            scores, indices, prior_bias, local_lse, gate_offset, gate_scale, float(temperature),
+            bool(return_gate_logit),
         )
+        return (remote, local, gl) if return_gate_logit else (remote, local)
     return route_weights_launch(
         scores, indices, prior_bias, local_lse, temperature=temperature,
-        gate_offset=_scalar(gate_offset), gate_scale=_scalar(gate_scale),
+        gate_offset=gate_offset, gate_scale=gate_scale, return_gate_logit=return_gate_logit,
     )

@@ -23,6 +23,10 @@ def value_tiles(v: torch.Tensor) -> torch.Tensor:
 
     if v.device.type != "cuda" or v.dtype != torch.bfloat16 or v.ndim != 4:
         raise ValueError("value_tiles requires a CUDA BF16 [B, L, Hkv, D] tensor")
+    return torch.ops.mrsa.value_tiles(v)
+
+
+def _value_tiles_impl(v: torch.Tensor) -> torch.Tensor:
     B, L, H, D = v.shape
     vc = v.contiguous()
     out = torch.empty(B, H, (L + 63) // 64, D, 64, dtype=torch.bfloat16, device=v.device)
@@ -63,6 +67,11 @@ def value_tiles_rows(v: torch.Tensor, v_tiles: torch.Tensor, positions: torch.Te
     B, L, H, D = v.shape
     if v_tiles.shape != (B, H, (L + 63) // 64, D, 64) or not v_tiles.is_contiguous():
         raise ValueError("v_tiles must be the contiguous value_tiles(v) layout")
+    torch.ops.mrsa.value_tiles_rows_(v, v_tiles, positions)
+
+
+def _value_tiles_rows_impl(v: torch.Tensor, v_tiles: torch.Tensor, positions: torch.Tensor) -> None:
+    B, L, H, D = v.shape
     vc = v.contiguous()
     pos = positions.to(device=v.device, dtype=torch.long).contiguous()
     st = _lib.call("mrsa_value_tiles_rows", _lib.ptr(vc), B, L, H, D, _lib.ptr(pos),
@@ -107,19 +116,31 @@ def selected_attention_launch(
     parts = int(parts)
     if not 1 <= parts <= _SEL_MAX_PARTS:
         raise ValueError(f"parts must be in [1, {_SEL_MAX_PARTS}], got {parts}")
+    if (fuse_local is None) != (fuse_weight is None):
+        raise ValueError("fuse_local and fuse_weight go together")
+    if fuse_local is not None and (fuse_local.shape != (B, Lq, Hq, D)
+                                   or fuse_weight.shape != (B, Lq, Hq)):
+        raise ValueError(
+            f"fusion shapes {tuple(fuse_local.shape)} / {tuple(fuse_weight.shape)} do not "
+            f"match the output [{B}, {Lq}, {Hq}, {D}]")
+    return torch.ops.mrsa.selected_attention(
+        q, k, v_tiles, weights, indices, key_valid, int(chunk_size), bool(mask_last_token),
+        float(sm_scale), parts, token_keep, fuse_local, fuse_weight)
+
+
+def _selected_attention_impl(q, k, v_tiles, weights, indices, key_valid, chunk_size,
+                             mask_last_token, sm_scale, parts, token_keep, fuse_local,
+                             fuse_weight):
+    B, Lq, Hq, D = q.shape
+    Lk, Hkv = k.shape[1], k.shape[2]
+    K = indices.shape[-1]
     qc = q.contiguous()
     kc = k.contiguous()
     w = weights.to(torch.bfloat16).contiguous()
     idx = indices.to(torch.int32).contiguous()
     kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
     out = torch.empty(B, Lq, Hq, D, dtype=torch.bfloat16, device=q.device)
-    if (fuse_local is None) != (fuse_weight is None):
-        raise ValueError("fuse_local and fuse_weight go together")
     if fuse_local is not None:
-        if fuse_local.shape != (B, Lq, Hq, D) or fuse_weight.shape != (B, Lq, Hq):
-            raise ValueError(
-                f"fusion shapes {tuple(fuse_local.shape)} / {tuple(fuse_weight.shape)} do not "
-                f"match the output [{B}, {Lq}, {Hq}, {D}]")
         lo = fuse_local.to(torch.bfloat16).contiguous()
         lw = fuse_weight.to(torch.bfloat16).contiguous()
         keep = None

@@ -58,9 +58,15 @@ def select_global_token_keep(
     n = K * S
     if n > _MAX_ROW:
         raise ValueError(f"K * chunk_size must be <= {_MAX_ROW}, got {n}")
+    return torch.ops.mrsa.token_keep(ranking, int(token_budget), _dtype == torch.int8)
+
+
+def _token_keep_impl(ranking, token_budget, as_int8):
+    B, L, H, K, S = ranking.shape
     flat = ranking.to(torch.float32).contiguous()
-    keep = torch.empty(B, L, H, K, S, dtype=_dtype, device=scores.device)
-    st = _lib.call("mrsa_token_keep_fwd", _lib.ptr(flat), B * L * H, n, int(token_budget),
+    keep = torch.empty(B, L, H, K, S, dtype=torch.int8 if as_int8 else torch.uint8,
+                       device=ranking.device)
+    st = _lib.call("mrsa_token_keep_fwd", _lib.ptr(flat), B * L * H, K * S, int(token_budget),
                    _lib.ptr(keep), _lib.stream_of(flat))
     _lib.check(st, "token_keep")
     return keep

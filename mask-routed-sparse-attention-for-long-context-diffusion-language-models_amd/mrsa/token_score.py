@@ -49,6 +49,10 @@ def candidate_token_scores_gqa(q, k, indices, key_valid, chunk_size):
     """FP32 [B, Lq, Hkv, K, chunk_size] max-over-group scores of routed tokens."""
 
     _validate(q, k, indices, key_valid, chunk_size)
+    return torch.ops.mrsa.candidate_token_scores(q, k, indices, key_valid, int(chunk_size))
+
+
+def _token_scores_impl(q, k, indices, key_valid, chunk_size):
     B, Lq, Hq, D = q.shape
     Lk, Hkv = k.shape[1:3]
     K = indices.shape[-1]

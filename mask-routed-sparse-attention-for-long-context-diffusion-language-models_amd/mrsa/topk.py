@@ -91,23 +91,44 @@ def route_topk_launch(
         )
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
+    if selection_mode == "post_softmax" and lse4 is None:
+        raise ValueError("post_softmax selection needs the local LSE")
+    if drop_mask is not None and derive_window < 0 and drop_mask.shape != (B, L, C):
+        raise ValueError(f"invalid drop_mask shape {tuple(drop_mask.shape)}")
+    if selection_mode != "post_softmax":
+        lse4 = None
+    if derive_window >= 0:
+        drop_mask = None
+    else:
+        key_valid = None
+    return torch.ops.mrsa.route_topk(
+        q5, lmks, lse4, bias4, drop_mask, key_valid, int(topk), int(block_size),
+        int(derive_window), bool(is_causal), int(window_size), int(q_offset),
+        selection_mode != "post_softmax", float(sm_scale), bool(scores_fp32),
+        -1 if use_workspace is None else int(bool(use_workspace)))
+
+
+def _route_topk_impl(q5, lmks, lse4, bias4, drop_mask, key_valid, topk, block_size,
+                     derive_window, is_causal, window_size, q_offset, pre_softmax, sm_scale,
+                     scores_fp32, use_workspace):
+    B, L, Hkv, G, D = q5.shape
+    C = lmks.shape[1]
+    per_head = 1 if lmks.shape[2] == Hkv * G else 0
+    selection_mode = "pre_softmax" if pre_softmax else "post_softmax"
+    use_workspace = None if use_workspace < 0 else bool(use_workspace)
     qc = q5.to(torch.bfloat16).contiguous()
     lc = lmks.to(torch.bfloat16).contiguous()
     lse = None
-    if selection_mode == "post_softmax":
-        if lse4 is None:
-            raise ValueError("post_softmax selection needs the local LSE")
+    if lse4 is not None:
         lse = lse4.to(device=q5.device, dtype=torch.float32).reshape(B, L, Hkv, G).contiguous()
     bias = None
     if bias4 is not None:
         bias = bias4.to(device=q5.device, dtype=torch.float32).reshape(B, C, Hkv, G).contiguous()
     drop = None
-    if drop_mask is not None and derive_window < 0:
-        if drop_mask.shape != (B, L, C):
-            raise ValueError(f"invalid drop_mask shape {tuple(drop_mask.shape)}")
+    if drop_mask is not None:
         drop = drop_mask.to(device=q5.device, dtype=torch.int32).contiguous()
     kv = None
-    if derive_window >= 0 and key_valid is not None:
+    if key_valid is not None:
         kv = key_valid.to(device=q5.device, dtype=torch.bool).contiguous()
     indices = torch.empty(B, L, Hkv, topk, dtype=torch.int32, device=q5.device)
     scores = torch.empty(
@@ -127,8 +148,9 @@ def route_topk_launch(
     if use_workspace:
         if not _fast_shape(C, G, D, topk, scores_fp32, is_causal):
             nbytes = _lib.call("mrsa_route_topk_workspace_bytes", B, L, C, Hkv, G)
-        ws = torch.empty(max(nbytes, 0) // 4, dtype=torch.float32, device=q5.device)
-        st = _lib.call("mrsa_route_topk_ws_fwd", *args, _lib.ptr(ws), int(nbytes),
+        nbytes = max(int(nbytes), 0)
+        ws = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=q5.device)
+        st = _lib.call("mrsa_route_topk_ws_fwd", *args, _lib.ptr(ws), nbytes,
                        _lib.stream_of(qc))
     else:
         st = _lib.call("mrsa_route_topk_fwd", *args, _lib.stream_of(qc))

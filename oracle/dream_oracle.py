@@ -87,14 +87,36 @@ def linear(x, w, b=None):
     return y.to(torch.bfloat16)
 
 
-def dream_forward(w, input_ids, return_hidden=False):
-    """w: mrsa.dream.DreamWeights with every tensor on the CPU."""
+def landmark_positions(seq_len, chunk_size):
+    """position_ids of the "mask_type" landmark layout of one all-valid
+    document (dream_dllm_hils/data.py:999-1010): text slots numbered in
+    order with landmarks skipped; a landmark takes the position after its
+    chunk's last text token."""
+
+    pos = torch.zeros(seq_len, dtype=torch.long)
+    nxt = 0
+    for j in range(seq_len):
+        if (j + 1) % chunk_size:
+            pos[j] = nxt
+            nxt += 1
+        else:
+            pos[j] = pos[j - 1] + 1
+    return pos
+
+
+def dream_forward(w, input_ids, return_hidden=False, position_ids=None):
+    """w: mrsa.dream.DreamWeights with every tensor on the CPU; input_ids in
+    the landmark layout (every chunk's last slot holds the mask token)."""
 
     s = w.shape
     L = input_ids.shape[1]
     S = s.route.chunk_size
     D, Hq, Hkv = s.head_dim, s.q_heads, s.kv_heads
-    cos, sin = yarn_tables(L, D, s.rope_theta, s.yarn_factor, s.yarn_original_max)
+    pos = landmark_positions(L, S) if position_ids is None else position_ids.long().cpu()
+    cos, sin = yarn_tables(int(pos.max()) + 1, D, s.rope_theta, s.yarn_factor,
+                           s.yarn_original_max)
+    cos, sin = cos[pos], sin[pos]
+    assert bool((input_ids.reshape(-1)[S - 1 :: S] == s.mask_token_id).all())
     h = w.embed[input_ids.reshape(-1)].clone()
     h[S - 1 :: S] = (h[S - 1 :: S].float() + w.lmk_type.float()).to(torch.bfloat16)
     route = set(s.route_layers())

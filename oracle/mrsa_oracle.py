@@ -160,6 +160,24 @@ def remote_drop_mask(valid_mask, window, chunk_size, allowed_mask=None):
     return drop.to(torch.int32)
 
 
+def remote_drop_mask_rows(valid_mask, window, chunk_size, positions):
+    """Rows ``positions`` of remote_drop_mask (kernel_utils.py:102-161, no
+    allowed mask), built without the full [B, L, L/S] mask: the cached block
+    step reads only its query rows (fastdllm_attention.py:295-299).
+    int32 [B, len(positions), L/S]."""
+
+    B, L = valid_mask.shape
+    C = L // chunk_size
+    pos = torch.as_tensor(positions).long()
+    real = (torch.arange(L) + 1).remainder(chunk_size) != 0
+    chunk_valid = (valid_mask.bool() & real[None]).reshape(B, C, chunk_size).any(-1)
+    left = (pos - window).clamp_min(0).div(chunk_size, rounding_mode="floor")
+    right = (pos + window).clamp_max(L - 1).div(chunk_size, rounding_mode="floor")
+    ids = torch.arange(C)
+    local = (ids[None, :] >= left[:, None]) & (ids[None, :] <= right[:, None])
+    return (local[None] | ~chunk_valid[:, None, :]).to(torch.int32)
+
+
 # ---------------------------------------------------------------------------
 # a5: route scoring + top-k
 # ---------------------------------------------------------------------------
@@ -246,14 +264,17 @@ def boundary_gap(sel, topk):
 # a7: route weights
 # ---------------------------------------------------------------------------
 def route_weights(scores, indices, prior_bias, local_lse, *, temperature=1.0,
-                  gate_offset=None, gate_scale=None):
+                  gate_offset=None, gate_scale=None, return_gate_logit=False):
     """_route_weights_torch (dream_dllm_hils/attention.py:126-235), fp32 outputs.
 
     scores [B, L, Hq, K] (bf16 values), indices [B, L, Hkv, K], prior_bias
     [B, C, Hkv, G], local_lse [B, L, Hq].  Returns (remote [B, L, Hq, K],
-    local [B, L, Hq]) before the bf16 rounding.  Differentiable: gate_offset
-    and gate_scale may be 0-d tensors, whose gradients autograd then forms
-    (the reference's own backward for this function is its autograd).
+    local [B, L, Hq]) before the bf16 rounding, plus the fp32 gate logit
+    [B, L, Hq] with return_gate_logit (:196-235: lse of the remote logits
+    minus the local logit, affine-transformed in the gate form, 0 where every
+    logit is masked).  Differentiable: gate_offset and gate_scale may be 0-d
+    tensors, whose gradients autograd then forms (the reference's own
+    backward for this function is its autograd).
     """
 
     def gate_value(x):
@@ -274,10 +295,13 @@ def route_weights(scores, indices, prior_bias, local_lse, *, temperature=1.0,
     logits = torch.cat((remote_logits, local_logits), dim=-1) / float(temperature)
     all_masked = torch.isneginf(logits).all(dim=-1, keepdim=True)
     logits = torch.where(all_masked, torch.zeros_like(logits), logits)
+    remote_lse = torch.logsumexp(logits[..., :K], dim=-1)
+    gate = remote_lse - logits[..., K]
     if affine:
-        remote_lse = torch.logsumexp(logits[..., :K], dim=-1)
-        gate = gate_value(gate_scale) * (remote_lse - logits[..., K]) + (
+        gate = gate_value(gate_scale) * gate + (
             gate_value(gate_offset) if gate_offset is not None else 0.0)
+    gate_logit = torch.where(all_masked[..., 0], torch.zeros_like(gate), gate)
+    if affine:
         mass = torch.sigmoid(gate)
         internal = torch.softmax(remote_logits / float(temperature), dim=-1)
         internal = torch.where((~valid).all(dim=-1, keepdim=True), torch.zeros_like(internal), internal)
@@ -285,9 +309,11 @@ def route_weights(scores, indices, prior_bias, local_lse, *, temperature=1.0,
         local = 1.0 - mass
         remote = torch.where(all_masked, torch.zeros_like(remote), remote)
         local = torch.where(all_masked[..., 0], torch.zeros_like(local), local)
-        return remote, local
+        return (remote, local, gate_logit) if return_gate_logit else (remote, local)
     probs = torch.softmax(logits, dim=-1)
     probs = torch.where(all_masked, torch.zeros_like(probs), probs)
+    if return_gate_logit:
+        return probs[..., :K], probs[..., K], gate_logit
     return probs[..., :K], probs[..., K]
 
 
@@ -485,8 +511,15 @@ def route_layer(q, k, v, route_q, entropy_bias_scale, key_valid=None, *, local_w
         local_lse.reshape(B, L, Hkv, G), topk, S, drop_mask=drop, bias4=prior,
     )
     scores_bf = scores.reshape(B, L, Hq, topk).to(torch.bfloat16)
-    rw, lw = route_weights(scores_bf, idx, prior, local_lse, temperature=temperature,
-                           gate_offset=gate_offset, gate_scale=gate_scale)
+    if topk >= 32:
+        # attention.py:1571-1621: _route_weights_torch with the layer's
+        # temperature and fusion gate parameters
+        rw, lw = route_weights(scores_bf, idx, prior, local_lse, temperature=temperature,
+                               gate_offset=gate_offset, gate_scale=gate_scale)
+    else:
+        # attention.py:1643-1648: the TileLang route_weights, plain 33-way
+        # softmax at temperature 1 with no gate
+        rw, lw = route_weights(scores_bf, idx, prior, local_lse)
     rw = rw.to(torch.bfloat16)
     lw = lw.to(torch.bfloat16)
     keep = None
@@ -537,7 +570,7 @@ def cached_route_layer(q, route_q, cache_key, cache_value, cache_valid, landmark
         lmk, entropy = chunk_attn_pool(q_lmk, chunk_keys, chunk_valid)
         lmk_all[:, aff] = lmk.to(torch.bfloat16)
         prior_all[:, aff] = entropy * entropy_bias_scale.float().view(1, 1, Hkv, G)
-    drop = remote_drop_mask(kv, local_window, S)[:, pos]
+    drop = remote_drop_mask_rows(kv, local_window, S, pos)
     idx, scores, sel = route_topk(
         route_q.reshape(B, Lq, Hkv, G, D), lmk_all.reshape(B, C, Hq, D),
         local_lse.reshape(B, Lq, Hkv, G), topk, S, drop_mask=drop, bias4=prior_all,

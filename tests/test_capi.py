@@ -51,7 +51,7 @@ def test_status_strings_and_version(lib):
     lib.mrsa_status_string.restype = ctypes.c_char_p
     assert lib.mrsa_status_string(0) == b"ok"
     assert b"invalid" in lib.mrsa_status_string(1)
-    assert lib.mrsa_abi_version() >= 1
+    assert lib.mrsa_abi_version() >= 2
 
 
 def test_host_side_argument_errors(lib):
@@ -68,8 +68,12 @@ def test_host_side_argument_errors(lib):
                   256, 0, 1.0, 16, 16, None) == 2          # head_dim 96 unsupported
     assert L.call("mrsa_selected_attention_fwd", 16, 16, 16, 16, 16, None, 1, 64, 128, 28, 4,
                   128, 32, 32, 1, 1.0, 16, None) == 2      # chunk_size 32 unsupported
-    assert L.call("mrsa_route_weights_fwd", 16, 16, 16, 16, 1, 4, 4, 4, 7, 65, 1.0, 0, 0.0,
-                  0, 1.0, 16, 16, None) == 2               # topk > 64
+    assert L.call("mrsa_route_weights_fwd", 16, 16, 16, 16, 1, 4, 4, 4, 7, 65, 1.0, None,
+                  None, 16, 16, None, None) == 2           # topk > 64
+    assert L.call("mrsa_route_weights_fwd", 16, 16, 16, 16, 1, 4, 4, 4, 7, 32, 0.0, None,
+                  None, 16, 16, None, None) == 1           # temperature <= 0
+    assert L.call("mrsa_route_weights_bwd", 16, 16, 16, 16, 16, None, None, 1, 4, 4, 4, 7, 32,
+                  1.0, 16, None, 16, 16, 16, None, None) == 1  # gate given, no d_gate
     # Walk split: parts outside 1..64, or a missing workspace, are rejected.
     assert L.call("mrsa_selected_attention_split_fwd", 16, 16, 16, 16, 16, None, 1, 64, 128,
                   28, 4, 128, 32, 64, 1, 1.0, 0, 16, 16, None) == 1

@@ -10,6 +10,7 @@ import torch
 
 import mrsa
 from oracle import mrsa_oracle as O
+from routing_check import classify_routing
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -86,9 +87,10 @@ def test_cached_route_attention_vs_oracle():
     others = torch.arange(C) != chunk
     assert torch.equal(cache.landmark_keys.cpu()[:, others], lmk0[:, others])
     assert torch.equal(mid["drop_mask"].cpu(), rmid["drop_mask"])
-    agree = (mid["indices"].cpu().long() == rmid["indices"]).all(-1).float().mean()
-    print(f"cached route layer: index rows identical to oracle: {float(agree):.4f}", flush=True)
-    assert float(agree) > 0.98
+    classify_routing(mid["indices"], rmid["indices"], rq[:, rows], cache.landmark_keys,
+                     mid["local_lse"], cache.prior_bias,
+                     lambda r: O.remote_drop_mask_rows(valid, 256, S, rows[r]), 32, S,
+                     "cached route layer L=4096")
     _close(mid["local_output"], rmid["local_output"], "cached local branch")
     _close(out, ref, "cached route layer")
 

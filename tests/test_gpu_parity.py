@@ -17,6 +17,7 @@ from mrsa.route_weights import route_weights_launch
 from mrsa.sparse_attention import selected_attention_launch
 from mrsa.topk import route_topk_launch
 from oracle import mrsa_oracle as O
+from routing_check import classify_routing
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -46,6 +47,22 @@ def _assert_close_attn(actual, expected, what):
     print(f"{what}: max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
     assert float(err.max()) <= 2e-2, what
     assert float(err.mean()) <= 2e-3, what
+
+
+def _assert_lmk_close(actual, expected, what):
+    # Landmark keys are bf16 outputs of an fp32 pool: within one bf16 step of
+    # the oracle's value, and almost all identical after its bf16 rounding.
+    a = actual.float().cpu()
+    e = expected.float()
+    er = e.bfloat16().float()
+    step = er.abs() * 2.0 ** -7 + 1e-6      # one bf16 step at the rounded value
+    err = (a - er).abs()
+    frac_same = float((err == 0).float().mean())
+    print(f"{what}: max_abs={err.max():.3e} mean_abs={err.mean():.3e} "
+          f"same_after_rounding={frac_same:.4f}", flush=True)
+    assert bool((err <= step).all()), what
+    assert float(err.mean()) <= 1e-4, what
+    assert frac_same > 0.99, what
 
 
 def test_mfma_lane_layout():
@@ -481,8 +498,7 @@ def test_route_layer_config2_full_size_sampled_rows():
     # Landmark pool and prior over all 256 chunks.
     lmk, ent = O.chunk_attn_pool(q[:, S - 1 :: S].reshape(1, C, Hkv, G, D),
                                  k.reshape(1, C, S, Hkv, D), valid.reshape(1, C, S))
-    torch.testing.assert_close(mid["landmark_keys"].float().reshape(lmk.shape), lmk,
-                               atol=2e-2, rtol=2e-2)
+    _assert_lmk_close(mid["landmark_keys"].reshape(lmk.shape), lmk, "cfg2 landmarks")
     torch.testing.assert_close(mid["prior_bias"].float().reshape(ent.shape), ent, atol=1e-3,
                                rtol=1e-3)
     # Routing of the sampled rows: indices bit-exact away from near ties.
@@ -527,6 +543,6 @@ def test_route_layer_vs_oracle():
                                     valid.to(DEV), return_intermediates=True)
     ref, rmid = O.route_layer(q, k, v, rq, scale, valid)
     _assert_close_attn(out, ref, "route layer")
-    agree = (mid["indices"].cpu().long() == rmid["indices"]).all(-1).float().mean()
-    print(f"route layer: index rows identical to oracle: {float(agree):.4f}", flush=True)
-    assert float(agree) > 0.98
+    classify_routing(mid["indices"], rmid["indices"], rq, mid["landmark_keys"], mid["local_lse"],
+                     mid["prior_bias"], lambda r: O.remote_drop_mask(valid, 256, 64)[:, r],
+                     32, 64, "route layer L=2048")

@@ -54,3 +54,20 @@ def test_rms_norm_rope_swiglu_pins():
     gu = torch.randn(9, 64, generator=g).bfloat16()
     ref = (F.silu(gu[:, :32].float()).bfloat16().float() * gu[:, 32:].float()).bfloat16()
     assert torch.equal(DO.swiglu(gu), ref)
+
+
+def test_landmark_layout_positions():
+    # data.py:999-1010 by hand for chunk_size 4: text slots 0, 1, 2 | 3, 4, 5 | ...,
+    # each landmark one past its chunk's last text position.
+    assert DO.landmark_positions(12, 4).tolist() == [0, 1, 2, 3, 3, 4, 5, 6, 6, 7, 8, 9]
+    from mrsa.dream import landmark_layout, landmark_positions
+    from mrsa.route_layer import RouteLayerConfig
+
+    s = DreamShape(route=RouteLayerConfig(chunk_size=4))
+    text = torch.arange(100, 109)[None]
+    ids, pos = landmark_layout(text, s)
+    assert ids.tolist() == [[100, 101, 102, s.mask_token_id, 103, 104, 105, s.mask_token_id,
+                             106, 107, 108, s.mask_token_id]]
+    assert pos.tolist() == DO.landmark_positions(12, 4).tolist()
+    s64 = DreamShape()
+    assert torch.equal(landmark_positions(4096, s64, "cpu"), DO.landmark_positions(4096, 64))

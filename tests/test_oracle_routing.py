@@ -137,3 +137,51 @@ def test_route_weights_closed_form_and_all_masked():
     rw0, lw0 = O.route_weights(scores, torch.full_like(idx, -1), bias,
                                torch.full((1, 1, 1), float("-inf")))
     assert float(rw0.abs().sum()) == 0.0 and float(lw0) == 0.0
+
+
+def test_route_weights_gate_logit_closed_forms():
+    # attention.py:196-235: the gate logit is the log-odds of the remote mass.
+    g = torch.Generator().manual_seed(21)
+    B, L, H, G, K, C = 1, 6, 2, 7, 8, 20
+    scores = torch.randn(B, L, H * G, K, generator=g).bfloat16()
+    idx = torch.randint(0, C, (B, L, H, K), generator=g)
+    idx[0, 2, 1, 3:] = -1
+    bias = torch.rand(B, C, H, G, generator=g)
+    lse = torch.randn(B, L, H * G, generator=g)
+    # plain form with an offset and a temperature: log(sum remote) - log(local)
+    rw, lw, gl = O.route_weights(scores, idx, bias, lse, temperature=0.7, gate_offset=0.3,
+                                 return_gate_logit=True)
+    torch.testing.assert_close(gl, rw.sum(-1).log() - lw.log(), atol=1e-5, rtol=1e-5)
+    # affine form: sigmoid(gate logit) is the remote mass, scale and offset included
+    rw, lw, gl = O.route_weights(scores, idx, bias, lse, temperature=1.3, gate_offset=-0.4,
+                                 gate_scale=1.7, return_gate_logit=True)
+    torch.testing.assert_close(torch.sigmoid(gl), rw.sum(-1), atol=1e-6, rtol=1e-5)
+    torch.testing.assert_close(torch.sigmoid(-gl), lw, atol=1e-6, rtol=1e-5)
+    # one row by hand: a single remote chunk c=3 (score 0.5, bias 0.25), local 1.0
+    s1 = torch.tensor([[[[0.5, 0.0]]]]).bfloat16()
+    i1 = torch.tensor([[[[3, -1]]]])
+    b1 = torch.zeros(1, 5, 1, 1)
+    b1[0, 3] = 0.25
+    l1 = torch.tensor([[[1.0]]])
+    _, _, g_plain = O.route_weights(s1, i1, b1, l1, gate_offset=0.5, return_gate_logit=True)
+    assert abs(float(g_plain) - (0.75 - (1.0 - 0.5))) < 1e-6
+    _, _, g_aff = O.route_weights(s1, i1, b1, l1, gate_offset=0.5, gate_scale=2.0,
+                                  return_gate_logit=True)
+    assert abs(float(g_aff) - (2.0 * (0.75 - 1.0) + 0.5)) < 1e-6
+    # every logit masked -> 0; only the remote ones masked -> -inf
+    _, _, g0 = O.route_weights(s1, torch.full_like(i1, -1), b1,
+                               torch.full((1, 1, 1), float("-inf")), return_gate_logit=True)
+    assert float(g0) == 0.0
+    _, _, g1 = O.route_weights(s1, torch.full_like(i1, -1), b1, l1, gate_scale=1.5,
+                               return_gate_logit=True)
+    assert float(g1) == float("-inf")
+
+
+def test_remote_drop_mask_rows_equal_full_mask_rows():
+    g = torch.Generator().manual_seed(5)
+    L, S, W = 1024, 64, 256
+    valid = torch.rand(2, L, generator=g) > 0.2
+    valid[1, 128:192] = False
+    pos = torch.tensor([0, 1, 63, 64, 300, 511, 512, 700, 1000, 1023])
+    torch.testing.assert_close(O.remote_drop_mask_rows(valid, W, S, pos),
+                               O.remote_drop_mask(valid, W, S)[:, pos], rtol=0, atol=0)
