@@ -29,6 +29,7 @@ extern "C" {
 #define MRSA_ERR_INVALID_ARGUMENT 1 /* bad shape, size or pointer */
 #define MRSA_ERR_UNSUPPORTED 2      /* valid call outside what the kernels implement */
 #define MRSA_ERR_LAUNCH 3           /* the HIP runtime rejected a launch */
+#define MRSA_ERR_SCRATCH 4          /* exceeds a no-allocation entry point's static buffer */
 
 /* Human-readable text for a status code (static storage). */
 const char* mrsa_status_string(int status);
@@ -187,6 +188,32 @@ int mrsa_route_topk_ws_fwd(const void* q, const void* lmk, const float* lse_loca
                            int64_t window_size, int64_t q_offset, int selection_mode,
                            float sm_scale, int32_t* indices, void* scores, int scores_fp32,
                            void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * mrsa_route_topk_ws_fwd without a caller workspace and without allocating:
+ * the workspace is a static device buffer of MRSA_ROUTE_TOPK_SCRATCH_BYTES
+ * per GPU inside the library.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc), e.g. the cached
+ * block step's routing over up to 4096 landmarks.
+ *   Arguments as mrsa_route_topk_ws_fwd minus the workspace; same results.
+ *   Returns MRSA_ERR_SCRATCH when the short-block path (more than 256
+ *   chunks) needs more than MRSA_ROUTE_TOPK_SCRATCH_BYTES of fp32 logits
+ *   (batch * seq_len * kv_heads * groups * chunks * 4 bytes); shapes of the
+ *   matrix-core path (up to 256 chunks) need none.
+ *   Every call on a GPU shares that GPU's buffer: calls that overlap on one
+ *   GPU (other streams, other threads) race.
+ */
+#define MRSA_ROUTE_TOPK_SCRATCH_BYTES (16u << 20)
+int mrsa_route_topk_noalloc_fwd(const void* q, const void* lmk, const float* lse_local,
+                                const float* bias, const int32_t* drop_mask,
+                                const uint8_t* key_valid, int64_t derive_window, int64_t batch,
+                                int64_t seq_len, int64_t chunks, int64_t kv_heads,
+                                int64_t groups, int64_t head_dim, int64_t topk,
+                                int64_t block_size, int per_head_lmk, int is_causal,
+                                int64_t window_size, int64_t q_offset, int selection_mode,
+                                float sm_scale, int32_t* indices, void* scores, int scores_fp32,
+                                void* stream);
 
 /*
  * Route weights: softmax over [score_k + bias[idx_k] (k < topk), local_lse].

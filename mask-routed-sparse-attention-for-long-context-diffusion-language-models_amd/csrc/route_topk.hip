@@ -31,6 +31,7 @@
 //
 // General path (route_topk_generic_kernel): one workgroup per (token, KV head)
 // with scalar dot products; any head_dim / chunk count that fits LDS.
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -1353,6 +1354,69 @@ extern "C" int64_t mrsa_route_topk_workspace_bytes(int64_t batch, int64_t seq_le
                                                    int64_t kv_heads, int64_t groups) {
   if (batch < 0 || seq_len < 0 || chunks < 0 || kv_heads < 0 || groups < 0) return -1;
   return batch * seq_len * kv_heads * groups * chunks * 4;
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation variant: the workspace is a file-scope device array.
+//
+// `scratch` is one fixed buffer per GPU (each device holds its own copy for
+// the life of the process).  Host code never passes the array's name to a
+// kernel: its device address is looked up once per device with
+// hipGetSymbolAddress (with that device current) and kept in scratch_ptr.
+// Every call on one GPU shares the buffer, so calls that overlap on one GPU
+// (two streams, two threads) race; the kernels write every byte they later
+// read, so nothing needs clearing between calls.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[MRSA_ROUTE_TOPK_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The current device's address of `scratch` (looked up on first use).
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return MRSA_ERR_LAUNCH;
+  if (dev < 0 || dev >= kMaxScratchDevices) return MRSA_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr)
+      return MRSA_ERR_LAUNCH;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MRSA_OK;
+}
+}  // namespace
+
+extern "C" int mrsa_route_topk_noalloc_fwd(
+    const void* q, const void* lmk, const float* lse_local, const float* bias,
+    const int32_t* drop_mask, const uint8_t* key_valid, int64_t derive_window, int64_t batch,
+    int64_t seq_len, int64_t chunks, int64_t kv_heads, int64_t groups, int64_t head_dim,
+    int64_t topk, int64_t block_size, int per_head_lmk, int is_causal, int64_t window_size,
+    int64_t q_offset, int selection_mode, float sm_scale, int32_t* indices, void* scores,
+    int scores_fp32, void* stream) {
+  if (batch < 0 || seq_len < 0 || chunks <= 0 || kv_heads <= 0 || groups <= 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  // Workspace the workspace entry point takes for this problem: the fp32
+  // logits [batch, seq_len, kv_heads, groups, chunks] of the short-block path
+  // (beyond 256 chunks).  The matrix-core path (<= 256 chunks) runs without
+  // one.  A problem that needs more than the static buffer is rejected.
+  const bool fast_shape = chunks <= 256 && head_dim == 128 && !scores_fp32 && !is_causal &&
+                          (groups == 7 || groups == 8);
+  const int64_t need = fast_shape ? 0 : batch * seq_len * kv_heads * groups * chunks * 4;
+  if (need > (int64_t)MRSA_ROUTE_TOPK_SCRATCH_BYTES) return MRSA_ERR_SCRATCH;
+  void* ws = nullptr;
+  if (need > 0) {
+    const int st = scratch_address(&ws);
+    if (st != MRSA_OK) return st;
+  }
+  return route_topk_dispatch(q, lmk, lse_local, bias, drop_mask, key_valid, derive_window, batch,
+                             seq_len, chunks, kv_heads, groups, head_dim, topk, block_size,
+                             per_head_lmk, is_causal, window_size, q_offset, selection_mode,
+                             sm_scale, indices, scores, scores_fp32, ws, need, stream);
 }
 
 extern "C" int mrsa_route_topk_ws_fwd(const void* q, const void* lmk, const float* lse_local,

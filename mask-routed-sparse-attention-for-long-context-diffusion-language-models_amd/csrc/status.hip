@@ -9,6 +9,9 @@ extern "C" const char* mrsa_status_string(int status) {
     case MRSA_ERR_INVALID_ARGUMENT: return "invalid argument (shape, size or pointer)";
     case MRSA_ERR_UNSUPPORTED: return "unsupported configuration for the gfx950 kernels";
     case MRSA_ERR_LAUNCH: return "HIP kernel launch failed";
+    case MRSA_ERR_SCRATCH:
+      return "problem needs more workspace than the static scratch buffer of the "
+             "no-allocation entry point";
     default: return "unknown status";
   }
 }

@@ -20,6 +20,7 @@ MRSA_OK = 0
 MRSA_ERR_INVALID_ARGUMENT = 1
 MRSA_ERR_UNSUPPORTED = 2
 MRSA_ERR_LAUNCH = 3
+MRSA_ERR_SCRATCH = 4
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -57,6 +58,11 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
          _I64, _I, _I, _I64, _I64, _I, _F, _P, _P, _I, _P, _I64, _P],
+    ),
+    "mrsa_route_topk_noalloc_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+         _I64, _I, _I, _I64, _I64, _I, _F, _P, _P, _I, _P],
     ),
     "mrsa_route_weights_fwd": (
         _I,
@@ -154,7 +160,7 @@ def check(status: int, op: str) -> None:
     if status == MRSA_OK:
         return
     msg = f"{op}: {status_string(status)} (status {status})"
-    if status in (MRSA_ERR_INVALID_ARGUMENT, MRSA_ERR_UNSUPPORTED):
+    if status in (MRSA_ERR_INVALID_ARGUMENT, MRSA_ERR_UNSUPPORTED, MRSA_ERR_SCRATCH):
         raise ValueError(msg)
     raise RuntimeError(msg)
 

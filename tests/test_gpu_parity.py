@@ -50,17 +50,19 @@ def _assert_close_attn(actual, expected, what):
 
 
 def _assert_lmk_close(actual, expected, what):
-    # Landmark keys are bf16 outputs of an fp32 pool: within one bf16 step of
-    # the oracle's value, and almost all identical after its bf16 rounding.
+    # Landmark keys are bf16 outputs of a pool that weights the keys with
+    # bf16-rounded probabilities (ops/chunk_attn_pool_gqa_tilelang.py:151-158):
+    # a probability at a rounding midpoint can round the other way, so a rare
+    # element moves by more than one output step.  Bound as test_pool_vs_oracle
+    # does (1e-2 abs / rel, mean below 1e-4) and require 99% of the elements
+    # to equal the oracle's value after its bf16 rounding.
     a = actual.float().cpu()
-    e = expected.float()
-    er = e.bfloat16().float()
-    step = er.abs() * 2.0 ** -7 + 1e-6      # one bf16 step at the rounded value
+    er = expected.float().bfloat16().float()
     err = (a - er).abs()
     frac_same = float((err == 0).float().mean())
     print(f"{what}: max_abs={err.max():.3e} mean_abs={err.mean():.3e} "
           f"same_after_rounding={frac_same:.4f}", flush=True)
-    assert bool((err <= step).all()), what
+    torch.testing.assert_close(a, er, atol=1e-2, rtol=1e-2, msg=what)
     assert float(err.mean()) <= 1e-4, what
     assert frac_same > 0.99, what
 
