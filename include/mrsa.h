@@ -299,6 +299,34 @@ int mrsa_value_tiles_rows(const void* v, int64_t batch, int64_t seq_len, int64_t
                           void* v_tiles, void* stream);
 
 /*
+ * Re-lays K and V out as per-chunk fragments: for each 64-key chunk, the
+ * register images of the 32 matrix-core operand loads of the routed
+ * attention (16x16x32 bf16 products; lane l = 16 grp + j, elements e = 0..7):
+ *   f[512 i + 8 l + e]        = K[key 16 mt + j][dim 32 ks + 8 grp + e],  i = 4 mt + ks
+ *   f[8192 + 512 i + 8 l + e] = V[key 32 ks + 16 (e >> 2) + 4 grp + (e & 3)][dim 16 nt + j],
+ *                               i = 2 nt + ks
+ * so every operand load is one contiguous 1 KB read.  Keys past seq_len are zero.
+ *   k, v: bf16 [batch, seq_len, kv_heads, head_dim], 16-byte aligned; v may be
+ *         NULL (the V part is then zero: enough for the candidate token scores)
+ *   kv_frags (out): bf16 [batch, kv_heads, ceil(seq_len / 64), 16384], 16-byte aligned
+ * Limits: head_dim == 128.
+ * No reference counterpart: internal layout step of the routed attention.
+ */
+int64_t mrsa_kv_fragments_bytes(int64_t batch, int64_t seq_len, int64_t kv_heads,
+                                int64_t head_dim);
+int mrsa_kv_fragments(const void* k, const void* v, int64_t batch, int64_t seq_len,
+                      int64_t kv_heads, int64_t head_dim, void* kv_frags, void* stream);
+
+/*
+ * Rewrites the fragments of the given rows of k and v after the rows were
+ * replaced (LayerKVCache.replace, dream_dllm_hils/fastdllm_cache.py:94-125).
+ * positions: int64 [count]; entries outside [0, seq_len) are ignored.
+ */
+int mrsa_kv_fragments_rows(const void* k, const void* v, int64_t batch, int64_t seq_len,
+                           int64_t kv_heads, int64_t head_dim, const int64_t* positions,
+                           int64_t count, void* kv_frags, void* stream);
+
+/*
  * Bidirectional sliding-window GQA attention with natural-log LSE.
  * Replaces the flash-attn window call behind bidir_local_attention and
  * cached_local_attention (dream_dllm_hils/local_attention.py:67-200):
@@ -349,17 +377,18 @@ int mrsa_local_attention_split_fwd(const void* q, const void* k, const void* v_t
  * selected_attention_g7 / selected_attention_g7_cached
  * (dream_dllm_hils/routing.py:305-472); the formula is the reference's
  * test_hils_non_power_two_topk.py:122-138.
- *   q: bf16 [batch, q_len, q_heads, head_dim]; k: bf16 [batch, kv_len, kv_heads, head_dim]
- *   v_tiles: output of mrsa_value_tiles for v
+ *   q: bf16 [batch, q_len, q_heads, head_dim]
+ *   kv_frags: output of mrsa_kv_fragments for the cache's k and v (kv_len rows)
  *   weights: bf16 [batch, q_len, q_heads, topk]
  *   indices: int32 [batch, q_len, kv_heads, topk] (chunk ids; entries < 0 or
  *            >= kv_len / chunk_size are skipped)
  *   key_valid: optional bool [batch, kv_len]
  *   out: bf16 [batch, q_len, q_heads, head_dim]
  *   sm_scale: finite and > 0 (MRSA_ERR_INVALID_ARGUMENT otherwise)
- * Limits: chunk_size == 64, head_dim == 128, q_heads / kv_heads <= 8, topk <= 64.
+ * Limits: chunk_size == 64, head_dim == 128, q_heads / kv_heads <= 8, topk <= 64,
+ * kv_len < 8388608.
  */
-int mrsa_selected_attention_fwd(const void* q, const void* k, const void* v_tiles,
+int mrsa_selected_attention_fwd(const void* q, const void* kv_frags,
                                 const void* weights, const int32_t* indices,
                                 const uint8_t* key_valid, int64_t batch, int64_t q_len,
                                 int64_t kv_len, int64_t q_heads, int64_t kv_heads,
@@ -378,7 +407,7 @@ int mrsa_selected_attention_fwd(const void* q, const void* k, const void* v_tile
  *            16-byte aligned, provided by the caller (no allocation here)
  * batch * parts must not exceed 65535.
  */
-int mrsa_selected_attention_split_fwd(const void* q, const void* k, const void* v_tiles,
+int mrsa_selected_attention_split_fwd(const void* q, const void* kv_frags,
                                       const void* weights, const int32_t* indices,
                                       const uint8_t* key_valid, int64_t batch, int64_t q_len,
                                       int64_t kv_len, int64_t q_heads, int64_t kv_heads,
@@ -396,7 +425,7 @@ int mrsa_selected_attention_split_fwd(const void* q, const void* k, const void* 
  * A chunk listed twice for one query counts once with the summed weights and
  * the keep row of its first slot.
  */
-int mrsa_selected_attention_keep_fwd(const void* q, const void* k, const void* v_tiles,
+int mrsa_selected_attention_keep_fwd(const void* q, const void* kv_frags,
                                      const void* weights, const int32_t* indices,
                                      const uint8_t* key_valid, const int8_t* token_keep,
                                      int64_t batch, int64_t q_len, int64_t kv_len,
@@ -418,7 +447,7 @@ int mrsa_selected_attention_keep_fwd(const void* q, const void* k, const void* v
  *   local_output: bf16 [batch, q_len, q_heads, head_dim], 8-byte aligned
  *   local_weight: bf16 [batch, q_len, q_heads]
  */
-int mrsa_selected_attention_fused_fwd(const void* q, const void* k, const void* v_tiles,
+int mrsa_selected_attention_fused_fwd(const void* q, const void* kv_frags,
                                       const void* weights, const int32_t* indices,
                                       const uint8_t* key_valid, const int8_t* token_keep,
                                       const void* local_output, const void* local_weight,
@@ -445,10 +474,11 @@ int mrsa_token_keep_fwd(const float* scores, int64_t rows, int64_t n, int64_t to
  * Per-token candidate scores inside routed chunks: max over the query group of
  * q.k * sm_scale; -inf for the landmark slot, invalid keys and -1 chunks.
  * Replaces candidate_token_scores_gqa (ops/hils_token_score_gqa_tilelang.py:174-208).
+ *   kv_frags: output of mrsa_kv_fragments (the V part is not read)
  *   scores (out): fp32 [batch, q_len, kv_heads, topk, chunk_size]
  * Limits: as mrsa_selected_attention_fwd.
  */
-int mrsa_candidate_token_scores_fwd(const void* q, const void* k, const int32_t* indices,
+int mrsa_candidate_token_scores_fwd(const void* q, const void* kv_frags, const int32_t* indices,
                                     const uint8_t* key_valid, int64_t batch, int64_t q_len,
                                     int64_t kv_len, int64_t q_heads, int64_t kv_heads,
                                     int64_t head_dim, int64_t topk, int64_t chunk_size,

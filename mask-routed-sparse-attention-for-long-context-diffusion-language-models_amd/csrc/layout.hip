@@ -1,4 +1,5 @@
-// Layout helpers: the remote-route drop mask and the tiled, transposed V.
+// Layout helpers: the remote-route drop mask, the tiled, transposed V the
+// local attention reads and the K / V fragments the routed attention reads.
 #include "mrsa_device.h"
 
 using namespace mrsa;
@@ -98,6 +99,85 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// K and V fragments of one 64-key chunk: the register images of the matrix
+// operands the routed attention feeds to 16x16x32 bf16 matrix products
+// (lane l = 16 grp + j holds 8 consecutive elements e of one instruction):
+//   K part (operand of S^T = K . Q^T), instruction i = 4 mt + ks:
+//     f[512 i + 8 l + e]        = K[key 16 mt + j][dim 32 ks + 8 grp + e]
+//   V part (operand of O = P . V), instruction i = 2 nt + ks:
+//     f[8192 + 512 i + 8 l + e] = V[key 32 ks + 16 (e >> 2) + 4 grp + (e & 3)][dim 16 nt + j]
+// (the V key order is the tiled order above).  Every operand load of a chunk
+// is one contiguous 1 KB read.  Keys past the sequence end are zero, and the
+// whole V part without a V input (the token scores read only K).
+constexpr int kFragElems = 16384;  // bf16 per (batch, KV head, chunk)
+constexpr int kFragPitch = 136;    // LDS row pitch (elements): 16-byte aligned rows
+
+__device__ __forceinline__ int frag_k_index(int r, int d) {
+  return 512 * (4 * (r >> 4) + (d >> 5)) + 8 * (16 * ((d >> 3) & 3) + (r & 15)) + (d & 7);
+}
+__device__ __forceinline__ int frag_v_index(int r, int d) {
+  const int e = 4 * ((r >> 4) & 1) + (r & 3);
+  return 8192 + 512 * (2 * (d >> 4) + (r >> 5)) + 8 * (16 * ((r >> 2) & 3) + (d & 15)) + e;
+}
+
+__global__ void __launch_bounds__(256)
+    kv_fragments_kernel(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                        int64_t L, int64_t H, int64_t NT, uint16_t* __restrict__ frags) {
+  __shared__ __align__(16) uint16_t ks_[64 * kFragPitch];
+  __shared__ __align__(16) uint16_t vs_[64 * kFragPitch];
+  const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  // 64 rows x 16 pieces of 16 bytes for each of K and V
+  for (int p = tid; p < 1024; p += 256) {
+    const int r = p >> 4, u = p & 15;
+    const int64_t s = c * 64 + r;
+    u32x4_t xk = {0u, 0u, 0u, 0u}, xv = {0u, 0u, 0u, 0u};
+    if (s < L) {
+      const int64_t off = ((b * L + s) * H + h) * 128 + 8 * u;
+      xk = *reinterpret_cast<const u32x4_t*>(k + off);
+      if (v) xv = *reinterpret_cast<const u32x4_t*>(v + off);
+    }
+    *reinterpret_cast<u32x4_t*>(ks_ + r * kFragPitch + 8 * u) = xk;
+    *reinterpret_cast<u32x4_t*>(vs_ + r * kFragPitch + 8 * u) = xv;
+  }
+  __syncthreads();
+  uint16_t* dst = frags + ((b * H + h) * NT + c) * (int64_t)kFragElems;
+  for (int p = tid; p < 1024; p += 256) {
+    const int i = p >> 6, l = p & 63, j = l & 15, grp = l >> 4;
+    // K: 8 consecutive dims of one key row
+    const int mt = i >> 2, kq = i & 3;
+    const u32x4_t xk =
+        *reinterpret_cast<const u32x4_t*>(ks_ + (16 * mt + j) * kFragPitch + 32 * kq + 8 * grp);
+    *reinterpret_cast<u32x4_t*>(dst + 8 * p) = xk;
+    // V: one dim of 8 keys in the tiled order
+    const int nt = i >> 1, kv = i & 1, d = 16 * nt + j;
+    u32x4_t xv;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int r0 = 32 * kv + 16 * (w >> 1) + 4 * grp + 2 * (w & 1);
+      xv[w] = (uint32_t)vs_[r0 * kFragPitch + d] | ((uint32_t)vs_[(r0 + 1) * kFragPitch + d] << 16);
+    }
+    *reinterpret_cast<u32x4_t*>(dst + 8192 + 8 * p) = xv;
+  }
+}
+
+// Rewrites the fragment entries of the listed rows only; positions outside
+// [0, L) are ignored.  One thread per dim: its K and V elements.
+__global__ void __launch_bounds__(128)
+    kv_fragments_rows_kernel(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                             int64_t L, int64_t H, int64_t NT,
+                             const int64_t* __restrict__ positions,
+                             uint16_t* __restrict__ frags) {
+  const int64_t p = positions[blockIdx.x];
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  if (p < 0 || p >= L) return;
+  const int r = (int)(p & 63), d = threadIdx.x;
+  uint16_t* dst = frags + ((b * H + h) * NT + p / 64) * (int64_t)kFragElems;
+  const int64_t src = ((b * L + p) * H + h) * 128 + d;
+  dst[frag_k_index(r, d)] = k[src];
+  dst[frag_v_index(r, d)] = v[src];
+}
+
 }  // namespace
 
 extern "C" int mrsa_remote_drop_mask(const uint8_t* valid_mask, const uint8_t* allowed_mask,
@@ -173,5 +253,46 @@ extern "C" int mrsa_value_tiles_rows(const void* v, int64_t batch, int64_t seq_l
                      dim3((unsigned)count, (unsigned)kv_heads, (unsigned)batch),
                      dim3((unsigned)head_dim), 0, (hipStream_t)stream, (const uint16_t*)v,
                      seq_len, kv_heads, (int)head_dim, NT, positions, (uint16_t*)v_tiles);
+  return mrsa_launch_status();
+}
+
+extern "C" int64_t mrsa_kv_fragments_bytes(int64_t batch, int64_t seq_len, int64_t kv_heads,
+                                           int64_t head_dim) {
+  if (batch < 0 || seq_len < 0 || kv_heads < 0 || head_dim != 128) return -1;
+  return batch * kv_heads * ((seq_len + 63) / 64) * (int64_t)kFragElems * 2;
+}
+
+extern "C" int mrsa_kv_fragments(const void* k, const void* v, int64_t batch, int64_t seq_len,
+                                 int64_t kv_heads, int64_t head_dim, void* kv_frags,
+                                 void* stream) {
+  if (batch < 0 || seq_len < 0 || kv_heads <= 0 || head_dim <= 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (head_dim != 128) return MRSA_ERR_UNSUPPORTED;
+  if (batch == 0 || seq_len == 0) return MRSA_OK;
+  if (!k || !kv_frags || ((uintptr_t)k | (uintptr_t)v | (uintptr_t)kv_frags) % 16 != 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  const int64_t NT = (seq_len + 63) / 64;
+  if (kv_heads > 65535 || batch > 65535 || NT > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(kv_fragments_kernel, dim3((unsigned)NT, (unsigned)kv_heads, (unsigned)batch),
+                     dim3(256), 0, (hipStream_t)stream, (const uint16_t*)k, (const uint16_t*)v,
+                     seq_len, kv_heads, NT, (uint16_t*)kv_frags);
+  return mrsa_launch_status();
+}
+
+extern "C" int mrsa_kv_fragments_rows(const void* k, const void* v, int64_t batch,
+                                      int64_t seq_len, int64_t kv_heads, int64_t head_dim,
+                                      const int64_t* positions, int64_t count, void* kv_frags,
+                                      void* stream) {
+  if (batch < 0 || seq_len < 0 || kv_heads <= 0 || head_dim <= 0 || count < 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (head_dim != 128) return MRSA_ERR_UNSUPPORTED;
+  if (batch == 0 || seq_len == 0 || count == 0) return MRSA_OK;
+  if (!k || !v || !kv_frags || !positions) return MRSA_ERR_INVALID_ARGUMENT;
+  if (kv_heads > 65535 || batch > 65535 || count > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
+  const int64_t NT = (seq_len + 63) / 64;
+  hipLaunchKernelGGL(kv_fragments_rows_kernel,
+                     dim3((unsigned)count, (unsigned)kv_heads, (unsigned)batch), dim3(128), 0,
+                     (hipStream_t)stream, (const uint16_t*)k, (const uint16_t*)v, seq_len,
+                     kv_heads, NT, positions, (uint16_t*)kv_frags);
   return mrsa_launch_status();
 }

@@ -1,0 +1,923 @@
+// Routed (selected-chunk) attention and candidate token scores: the gather walk.
+//
+// out[q, g] = sum_k w[q, g, k] * softmax_{s in chunk idx[q, k], s valid}(q_g . k_s * scale) . V
+// Each routed chunk is normalised on its own (ops/hils_fwd_bwd_head.py:453-559;
+// formula restated in the reference test test_hils_non_power_two_topk.py:122-138):
+// the landmark slot (last key of the chunk, when mask_last_token) and invalid
+// keys are excluded, P = bf16(p * w / sum p) feeds the PV product with fp32
+// accumulation, and a chunk whose keys are all masked contributes nothing.
+// Index lists are read like the reference kernel: a query's list ends at its
+// first negative entry; entries >= kv_len / 64 are skipped.  A chunk listed
+// twice contributes once with the two weights summed (rounded to bf16).
+//
+// Work split.  A workgroup owns a tile of TQ (<= 32) queries of one KV head
+// and keeps their fp32 outputs [TQ][G][128] in LDS.  Its prologue turns the
+// tile's index lists into a walk: the ascending list of the chunks any of its
+// queries routes to, and for each such chunk (a step) the items (query,
+// weights) that own it.  Steps are dealt round-robin to the 8 waves.  A wave
+// processes a step on its own:
+//   K and V of the chunk straight into registers from the chunk's
+//   fragments (mrsa_kv_fragments: the operands' register images, so each of
+//   the 32 load instructions reads 1 KB contiguous); the step's owners are packed two per 16-column tile (column
+//   j: owner j & 1, head j >> 1), so a tile's columns are almost all useful;
+//   per tile
+//     S^T = K . Q^T                 16 MFMAs (16x16x32 bf16)
+//     per-column softmax over the 64 keys, P = bf16(p w / sum p)
+//     O_tile = P . V                16 MFMAs
+//     O_tile added into the two owners' LDS rows
+// The next tile's Q and the next step's K / V are loaded into the same
+// registers as soon as the current ones are consumed.  The epilogue barrier
+// turns the LDS outputs into bf16 rows (fused with the local branch when
+// asked) or fp32 partial sums of a walk split.
+//
+// Adding a tile.  Two waves may hold tiles of the same query at once.  LDS
+// float atomics (ds_add_f32) run at about two cycles per lane, so instead a
+// wave takes both owners' bits of a per-workgroup lock word (all or nothing:
+// ds_or_rtn, undo on conflict, so no wave ever waits while holding a bit),
+// adds with plain 16-byte reads and writes, and clears the bits.  LDS
+// operations of one wave complete in issue order, so its writes land before
+// its release and after another wave's acquire.  The wait is bounded: past
+// `spin_limit` tries the wave adds that tile with ds_add_f32 instead, which
+// is always correct.  The order of the fp32 additions into a row therefore
+// depends on timing, so the last bit of an output can differ between runs.
+//
+// LDS output rows: row (q, g) at q * G + g, 128 floats; element d = 16 nt + j
+// at 64 (nt >> 2) + 4 j + (nt & 3), so the values a lane holds for one row
+// (nt = 0..7 at its j) are two 16-byte vectors and the 16 lanes of a row
+// read 256 contiguous bytes.
+//
+// Token-score mode (candidate_token_scores_gqa,
+// ops/hils_token_score_gqa_tilelang.py:17-114) runs the same walk and writes,
+// per routed (query, slot), the max over the group of q.k times sm_scale for
+// every key, -inf at the last slot and invalid keys.
+#include "mrsa_device.h"
+
+#include <algorithm>
+#include <cstdlib>
+#include <type_traits>
+
+using namespace mrsa;
+
+namespace {
+
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kMaxTopk = 64;
+constexpr int kMaxTQ = 32;                 // owner sets and the lock are 32-bit masks
+constexpr int kMaxItems = 1024;            // TQ * K per workgroup
+constexpr int64_t kMaxParts = 64;          // walk split limit
+constexpr size_t kLdsBytes = 160 * 1024;
+constexpr int kDefaultSpinLimit = 4096;    // lock tries before the atomic path
+
+struct RaArgs {
+  const uint16_t* q;
+  const uint16_t* kvf;       // [B, Hkv, Ck, 16384] K / V fragments
+  const uint16_t* w;
+  const int32_t* idx;
+  const uint8_t* key_valid;
+  const int8_t* keep;        // [B, Lq, Hkv, K, 64] nonzero = key kept (KEEP only)
+  int64_t B, Lq, Lk;
+  int Hq, Hkv, G, K;
+  int64_t Ck;                // chunks in the cache
+  int mask_last;
+  float scale_log2;
+  float sm_scale;
+  uint16_t* out;
+  float* tscores;
+  int parts;
+  float* partial;            // [parts][B][Lq][Hq][128] fp32 when parts > 1
+  const uint16_t* fuse_local;
+  const uint16_t* fuse_w;
+  int tq;                    // queries per tile
+  int64_t ntiles;            // ceil(Lq / tq)
+  int64_t units;             // B * Hkv * parts * ntiles workgroups of work
+  int spin_limit;            // lock tries before a tile takes the atomic path
+};
+
+__host__ __device__ inline size_t al16(size_t x) { return (x + 15) & ~(size_t)15; }
+
+// LDS carve-up (byte offsets).  The output region (tq * G rows plus one sink
+// row that takes the adds of padding columns) doubles as the prologue's
+// scratch (raw index rows, list flags, staged weights, per-chunk owner bits
+// and step numbers), which is dead once the items are built.
+struct RaLayout {
+  size_t o, o_bytes;
+  size_t raw, qlen, qflag, wst, omask, step_of, scratch_end;
+  size_t chunk, off, excl, iq, islot, iw, ikeep, misc, total;
+  int items, cap;
+};
+
+__host__ __device__ inline RaLayout ra_layout(int tq, int G, int K, int64_t Ck, bool token,
+                                              bool keep) {
+  RaLayout l;
+  l.items = tq * K;
+  l.cap = (int)(Ck < l.items ? Ck : l.items);
+  l.o_bytes = token ? 0 : ((size_t)tq * G + 1) * 128 * 4;
+  size_t s = 0;
+  l.raw = s;     s = al16(s + (size_t)l.items * 4);
+  l.qlen = s;    s = al16(s + (size_t)tq * 4);
+  l.qflag = s;   s = al16(s + (size_t)tq * 4);
+  l.wst = s;     s = al16(s + (token ? 0 : (size_t)tq * 8 * K * 2));
+  l.omask = s;   s = al16(s + (size_t)Ck * 4);
+  l.step_of = s; s = al16(s + (size_t)Ck * 2);
+  l.scratch_end = s;
+  l.o = 0;
+  size_t o = al16(l.o_bytes > s ? l.o_bytes : s);
+  l.chunk = o;   o = al16(o + (size_t)l.cap * 4);
+  l.off = o;     o = al16(o + (size_t)(l.cap + 1) * 4);
+  l.excl = o;    o = al16(o + (size_t)l.cap * 8);
+  l.iq = o;      o = al16(o + (size_t)l.items);
+  l.islot = o;   o = al16(o + (size_t)l.items);
+  l.iw = o;      o = al16(o + (token ? 0 : (size_t)l.items * 8 * 2));
+  l.ikeep = o;   o = al16(o + (keep ? (size_t)l.items * 8 : 0));
+  l.misc = o;    o = al16(o + (size_t)(2 * kWaves + 8) * 4);
+  l.total = o;
+  return l;
+}
+
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Kept-key bits (bit j = key j kept) of one 64-byte token-keep row.
+__device__ __forceinline__ uint64_t kept_bits(const int8_t* kr) {
+  uint64_t bits = 0ull;
+  if (((uintptr_t)kr & 15) == 0) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const u32x4_t x = *reinterpret_cast<const u32x4_t*>(kr + 16 * v);
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          bits |= ((x[w] >> (8 * j)) & 0xffu) ? 1ull << (16 * v + 4 * w + j) : 0ull;
+    }
+  } else {
+    for (int j = 0; j < 64; ++j) bits |= kr[j] ? 1ull << j : 0ull;
+  }
+  return bits;
+}
+
+// Lock word accesses (lane 0 issues; results made wave-uniform).
+__device__ __forceinline__ uint32_t lds_or_rtn(uint32_t addr, uint32_t v) {
+  uint32_t old;
+  asm volatile("ds_or_rtn_b32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
+               : "=v"(old)
+               : "v"(addr), "v"(v)
+               : "memory");
+  return old;
+}
+__device__ __forceinline__ void lds_and(uint32_t addr, uint32_t v) {
+  asm volatile("ds_and_b32 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Operand loads are buffer loads: one buffer resource per tensor (SGPRs),
+// one per-lane byte offset (VGPR) and wave-uniform chunk offsets (SGPRs), so
+// the 32 loads of a chunk need no 64-bit address registers.  Offsets past the
+// resource's range read zero.
+constexpr int64_t kFragElems = 16384;
+constexpr uint32_t kFragBytes = 32768;
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw 32-bit dwords, no swizzle
+constexpr uint32_t kZeroOffset = 0x7ffffff0u;  // past every range: reads zero
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           (int)kRsrcWord3);
+}
+__device__ __forceinline__ u32x4_t bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+}
+
+// K operands (keys 16 mt + j, dims 32 ks + 8 grp..) and V operands (dims
+// 16 nt + j, keys 32 ks + 8 grp.. in the tiled order) of the chunk whose
+// fragments start at byte `cb`; `lo` = 16 * lane.  Instruction i of the
+// chunk's 32 reads bytes 1024 i + lo: the part below 4 KB goes into the
+// load's immediate offset, the rest into the SGPR offset.
+__device__ __forceinline__ void load_k(u32x4_t (&kb)[4][4], __amdgpu_buffer_rsrc_t r,
+                                       uint32_t lo, uint32_t cb) {
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) kb[mt][ks] = bload(r, lo + 1024u * ks, cb + 4096u * mt);
+}
+__device__ __forceinline__ void load_v(u32x4_t (&vb)[8][2], __amdgpu_buffer_rsrc_t r,
+                                       uint32_t lo, uint32_t cb) {
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int i = 2 * nt + ks;
+      vb[nt][ks] = bload(r, lo + 1024u * (i & 3), cb + 16384u + 4096u * (i >> 2));
+    }
+}
+// Q^T operand of one tile column: head row bytes 64 ks + 16 grp from `off`
+// (kZeroOffset for padding columns).
+__device__ __forceinline__ void load_q(u32x4_t (&Qb)[4], __amdgpu_buffer_rsrc_t r, uint32_t off) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) Qb[ks] = bload(r, off + 64u * ks, 0u);
+}
+
+template <bool TOKEN, bool KEEP>
+__global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  // Workgroup -> work unit, XCD-aware: workgroups are dealt to the 8 XCDs
+  // round-robin by linear id, so XCD x takes the contiguous unit range
+  // [x * per, (x + 1) * per): one KV head's consecutive query tiles, whose
+  // walks read the same chunks from that XCD's L2 at about the same time.
+  const int64_t per = (int64_t)(gridDim.x >> 3);
+  const int64_t unit = (int64_t)(blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (unit >= a.units) return;
+  const int64_t tile = unit % a.ntiles;
+  int64_t rest = unit / a.ntiles;
+  const int part = (int)(rest % a.parts);
+  rest /= a.parts;
+  const int h = (int)(rest % a.Hkv);
+  const int64_t b = rest / a.Hkv;
+
+  const int K = a.K, G = a.G, tq = a.tq;
+  const int64_t Ck = a.Ck;
+  const RaLayout L = ra_layout(tq, G, K, Ck, TOKEN, KEEP);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t q0 = tile * tq;
+  const int nq = (int)min((int64_t)tq, a.Lq - q0);
+  const int items = L.items;
+
+  int32_t* raw = reinterpret_cast<int32_t*>(smem + L.raw);         // [tq][K]
+  int32_t* qlen = reinterpret_cast<int32_t*>(smem + L.qlen);       // [tq]
+  uint32_t* qflag = reinterpret_cast<uint32_t*>(smem + L.qflag);   // [tq] list not strictly ascending
+  uint16_t* wst = reinterpret_cast<uint16_t*>(smem + L.wst);       // [tq][8][K]
+  uint32_t* omask = reinterpret_cast<uint32_t*>(smem + L.omask);   // [Ck]
+  uint16_t* step_of = reinterpret_cast<uint16_t*>(smem + L.step_of);  // [Ck]
+  float* O = reinterpret_cast<float*>(smem + L.o);                 // [tq * G][128]
+  int32_t* s_chunk = reinterpret_cast<int32_t*>(smem + L.chunk);   // [cap]
+  int32_t* s_off = reinterpret_cast<int32_t*>(smem + L.off);       // [cap + 1]
+  uint64_t* s_excl = reinterpret_cast<uint64_t*>(smem + L.excl);   // [cap] excluded keys
+  uint8_t* it_q = smem + L.iq;                                     // [items]
+  uint8_t* it_slot = smem + L.islot;                               // [items]
+  uint16_t* it_w = reinterpret_cast<uint16_t*>(smem + L.iw);       // [items][8]
+  uint64_t* it_keep = reinterpret_cast<uint64_t*>(smem + L.ikeep); // [items]
+  int32_t* misc = reinterpret_cast<int32_t*>(smem + L.misc);
+  uint32_t* lock = reinterpret_cast<uint32_t*>(misc + 2 * kWaves + 1);
+
+  // ---- prologue: the walk of this tile ----------------------------------
+  // 1. Index rows (-1 past the sequence end), list lengths and flags, owner
+  //    bits cleared, routing weights staged as [q][g][k] (heads >= G zero).
+  for (int e = tid; e < items; e += kThreads) {
+    const int qq = e / K, kk = e - qq * K;
+    raw[e] = qq < nq ? a.idx[((b * a.Lq + q0 + qq) * a.Hkv + h) * K + kk] : -1;
+  }
+  for (int i = tid; i < tq; i += kThreads) {
+    qlen[i] = K;
+    qflag[i] = 0u;
+  }
+  if (tid == 0) *lock = 0u;
+  for (int64_t c = tid; c < Ck; c += kThreads) omask[c] = 0u;
+  if constexpr (!TOKEN) {
+    const uint16_t* wrow0 = a.w + ((b * a.Lq + q0) * a.Hq + (int64_t)h * G) * K;
+    const int64_t qstride = (int64_t)a.Hq * K;
+    if ((K & 7) == 0 && ((uintptr_t)a.w & 15) == 0) {
+      const int vpr = K >> 3;
+      for (int e = tid; e < tq * 8 * vpr; e += kThreads) {
+        const int row = e / vpr, v = e - row * vpr;
+        const int qq = row >> 3, gg = row & 7;
+        u32x4_t x = {0u, 0u, 0u, 0u};
+        if (qq < nq && gg < G)
+          x = *reinterpret_cast<const u32x4_t*>(wrow0 + qq * qstride + gg * K + 8 * v);
+        *reinterpret_cast<u32x4_t*>(wst + row * K + 8 * v) = x;
+      }
+    } else {
+      for (int e = tid; e < tq * 8 * K; e += kThreads) {
+        const int row = e / K, kk = e - row * K;
+        const int qq = row >> 3, gg = row & 7;
+        wst[e] = (qq < nq && gg < G) ? wrow0[qq * qstride + gg * K + kk] : (uint16_t)0;
+      }
+    }
+  }
+  __syncthreads();
+  // 2. A list ends at its first negative entry; a list that is not strictly
+  //    ascending (up to its end) may hold duplicates.
+  for (int e = tid; e < items; e += kThreads) {
+    const int kk = e % K;
+    const int32_t c = raw[e];
+    if (c < 0) atomicMin(&qlen[e / K], kk);
+    if (kk > 0 && c >= 0 && raw[e - 1] >= 0 && c <= raw[e - 1]) atomicOr(&qflag[e / K], 1u);
+  }
+  __syncthreads();
+  // 3. Owner bits of every listed chunk.
+  for (int e = tid; e < items; e += kThreads) {
+    const int qq = e / K, kk = e - qq * K;
+    const int32_t c = raw[e];
+    if (kk < qlen[qq] && c < Ck) atomicOr(&omask[c], 1u << qq);
+  }
+  __syncthreads();
+  // 4. Steps: owned chunks in ascending order, with the offset of their
+  //    first item (items of a step are its owners in query order).
+  {
+    const int64_t cper = (Ck + kThreads - 1) / kThreads;
+    const int64_t c0 = min(Ck, (int64_t)tid * cper), c1 = min(Ck, c0 + cper);
+    int cnt = 0, pc = 0;
+    for (int64_t c = c0; c < c1; ++c) {
+      const uint32_t m = omask[c];
+      cnt += m != 0u;
+      pc += __popc(m);
+    }
+    int icnt = cnt, ipc = pc;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u1 = __shfl_up(icnt, o, 64), u2 = __shfl_up(ipc, o, 64);
+      if (lane >= o) {
+        icnt += u1;
+        ipc += u2;
+      }
+    }
+    if (lane == 63) {
+      misc[wave] = icnt;
+      misc[kWaves + wave] = ipc;
+    }
+    __syncthreads();
+    int pos = icnt - cnt, item = ipc - pc, tsteps = 0, titems = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const int x = misc[w], y = misc[kWaves + w];
+      pos += w < wave ? x : 0;
+      item += w < wave ? y : 0;
+      tsteps += x;
+      titems += y;
+    }
+    for (int64_t c = c0; c < c1; ++c) {
+      const uint32_t m = omask[c];
+      if (m) {
+        s_chunk[pos] = (int32_t)c;
+        s_off[pos] = item;
+        step_of[c] = (uint16_t)pos;
+        ++pos;
+        item += __popc(m);
+      }
+    }
+    if (tid == 0) {
+      s_off[tsteps] = titems;
+      misc[2 * kWaves] = tsteps;
+    }
+  }
+  __syncthreads();
+  // 5. Items: the first occurrence of each chunk in a query's list (a later
+  //    duplicate adds its weights to it).  Strictly ascending lists (what
+  //    route scoring emits) have no duplicates and skip the scans.
+  for (int e = tid; e < items; e += kThreads) {
+    const int qq = e / K, kk = e - qq * K;
+    const int32_t c = raw[e];
+    const int n = qlen[qq];
+    if (!(kk < n && c < Ck)) continue;
+    const bool plain = qflag[qq] == 0u;
+    if (!plain) {
+      bool first = true;
+      for (int k2 = 0; k2 < kk; ++k2) first &= raw[qq * K + k2] != c;
+      if (!first) continue;
+    }
+    const uint32_t m = omask[c];
+    const int pos = s_off[step_of[c]] + __popc(m & ((1u << qq) - 1u));
+    it_q[pos] = (uint8_t)qq;
+    it_slot[pos] = (uint8_t)kk;
+    if constexpr (!TOKEN) {
+      uint16_t wv[8];
+#pragma unroll
+      for (int gg = 0; gg < 8; ++gg) wv[gg] = wst[(qq * 8 + gg) * K + kk];
+      if (!plain) {
+        for (int k2 = kk + 1; k2 < n; ++k2) {
+          if (raw[qq * K + k2] != c) continue;
+#pragma unroll
+          for (int gg = 0; gg < 8; ++gg)
+            wv[gg] = (uint16_t)f32_to_bf16(bf16_to_f32(wv[gg]) +
+                                           bf16_to_f32(wst[(qq * 8 + gg) * K + k2]));
+        }
+      }
+      u32x4_t pk;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pk[i] = (uint32_t)wv[2 * i] | ((uint32_t)wv[2 * i + 1] << 16);
+      *reinterpret_cast<u32x4_t*>(it_w + pos * 8) = pk;
+    }
+    if constexpr (KEEP)
+      it_keep[pos] = kept_bits(a.keep + (((b * a.Lq + q0 + qq) * a.Hkv + h) * K + kk) * 64);
+  }
+  // Excluded keys of every step (bit k = key k of its chunk): the landmark
+  // slot and invalid keys.  One step per thread, its 64 valid bytes loaded
+  // at once.
+  const int nsteps = misc[2 * kWaves];
+  const uint8_t* kvrow = a.key_valid ? a.key_valid + b * a.Lk : nullptr;
+  for (int e = tid; e < nsteps; e += kThreads) {
+    uint64_t m = a.mask_last ? (1ull << 63) : 0ull;
+    if (kvrow) m |= ~kept_bits(reinterpret_cast<const int8_t*>(kvrow) + (int64_t)s_chunk[e] * 64);
+    s_excl[e] = m;
+  }
+  __syncthreads();
+  const int st_lo = (int)((int64_t)part * nsteps / a.parts);
+  const int st_hi = (int)((int64_t)(part + 1) * nsteps / a.parts);
+  // 6. Outputs start at zero (the scratch above is dead now).
+  if constexpr (!TOKEN) {
+    const int n4 = tq * G * 128 / 4;
+    for (int i = tid; i < n4; i += kThreads) reinterpret_cast<f32x4_t*>(O)[i] = zero4();
+    __syncthreads();
+  }
+
+  // ---- the walk ------------------------------------------------------------
+  const int j = lane & 15, grp = lane >> 4;
+  const int own = j & 1, gcol = j >> 1;  // this lane's tile column: owner, head
+  const float c2 = a.scale_log2;
+  const __amdgpu_buffer_rsrc_t frs =
+      make_rsrc(a.kvf + (b * a.Hkv + h) * Ck * kFragElems, (uint32_t)Ck * kFragBytes);
+  const uint32_t flo = 16u * lane;
+  // Q rows of this tile: query qi's head gcol at byte qi * qrow + 256 gcol.
+  const uint32_t qrow = (uint32_t)a.Hq * 256u;
+  const __amdgpu_buffer_rsrc_t qrs =
+      make_rsrc(a.q + ((b * a.Lq + q0) * a.Hq + (int64_t)h * G) * 128, (uint32_t)nq * qrow);
+  const uint32_t qcol = 256u * gcol + 16u * grp;
+  auto qoff = [&](int item, bool valid) {
+    return valid ? (uint32_t)it_q[max(item, 0)] * qrow + qcol : kZeroOffset;
+  };
+  const uint32_t lock_addr = lds_address(lock);
+  const int sink = tq * G;  // output row that takes the padding columns' adds
+  float ninf_v = neg_inf();
+  asm volatile("" : "+v"(ninf_v));  // kept in a register for set_where
+
+  int st = st_lo + wave;
+  int64_t c = 0, cn = 0;
+  int i0 = 0, n = 0, i0n = 0, nn = 0;
+  bool more = false;
+  uint64_t msk = 0;
+  u32x4_t kb[4][4], vb[8][2], Qb[4];
+
+  // One tile: columns 2 t + own of the step's owners.  The last tile of a
+  // step (LAST) prefetches the next step's first Q and its K (after the QK
+  // product) and V (after the PV product); other tiles prefetch the next
+  // tile's Q.  Every path issues the same loads into the same registers (a
+  // missing next step reloads the current chunk and reads Q as zeros), so
+  // the waits before each product cover only what it consumes.
+  auto do_tile = [&](int t, auto last_tag) {
+    constexpr bool LAST = decltype(last_tag)::value;
+    const int o = 2 * t + own;
+    const bool cvalid = o < n && gcol < G;
+    const int ii = i0 + (o < n ? o : n - 1);
+    // S^T = K . Q^T: lane (grp, j) gets keys 16 mt + 4 grp + r of column j.
+    f32x4_t S[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      S[mt] = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) S[mt] = mfma_bf16_16x16x32(kb[mt][ks], Qb[ks], S[mt]);
+    }
+    if constexpr (!LAST) {
+      const int o2 = o + 2;
+      load_q(Qb, qrs, qoff(i0 + min(o2, n - 1), o2 < n && gcol < G));
+    } else {
+      load_q(Qb, qrs, qoff(i0n + min(own, nn - 1), more && own < nn && gcol < G));
+      load_k(kb, frs, flo, (uint32_t)cn * kFragBytes);
+    }
+    const uint64_t msh = msk >> (4 * grp);  // bit 16 mt + r: key 16 mt + 4 grp + r
+
+    if constexpr (TOKEN) {
+      // max over the owner's head columns (lanes j, j ^ 2, j ^ 4, j ^ 8
+      // share the owner), excluded keys -inf, times sm_scale.
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = gcol < G ? S[mt][r] : neg_inf();
+          v = fmaxf(v, __shfl_xor(v, 2, 64));
+          v = fmaxf(v, __shfl_xor(v, 4, 64));
+          v = fmaxf(v, __shfl_xor(v, 8, 64));
+          S[mt][r] = v;
+        }
+      if (gcol == 0 && o < n) {
+        const int qi = it_q[ii];
+        const int slot = it_slot[ii];
+        float* dst = a.tscores + (((b * a.Lq + q0 + qi) * a.Hkv + h) * K + slot) * 64 + 4 * grp;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          f32x4_t v;
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            v[r] = ((msh >> (16 * mt + r)) & 1ull) ? neg_inf() : S[mt][r] * a.sm_scale;
+          *reinterpret_cast<f32x4_t*>(dst + 16 * mt) = v;
+        }
+      }
+    } else {
+      const float wv = cvalid ? bf16_to_f32(it_w[ii * 8 + gcol]) : 0.f;
+      // Excluded keys -> -inf in place.  Key 63 (the landmark slot, the
+      // usual only exclusion) is S[3][3] of lane group 3; other excluded
+      // keys take the per-bit path.
+      S[3][3] = set_where(S[3][3], (msk >> 63) ? 0xFFFF000000000000ull : 0ull, ninf_v);
+      if (msk & ~(1ull << 63)) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            S[mt][r] = set_where(
+                S[mt][r], __builtin_amdgcn_ballot_w64((msh >> (16 * mt + r)) & 1ull), ninf_v);
+      }
+      if constexpr (KEEP) {
+        // keys the column's keep row drops -> -inf
+        const uint64_t kbits = (o < n ? it_keep[ii] : ~0ull) >> (4 * grp);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            S[mt][r] = set_where(
+                S[mt][r], __builtin_amdgcn_ballot_w64(!((kbits >> (16 * mt + r)) & 1ull)),
+                ninf_v);
+      }
+      const float mx = across4_max(max16_raw(S));
+      const float mb = mx == neg_inf() ? 0.f : mx * c2;
+      float ps[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[mt][r] = exp2_hw(__builtin_fmaf(S[mt][r], c2, -mb));
+        ps[mt] = (S[mt][0] + S[mt][1]) + (S[mt][2] + S[mt][3]);
+      }
+      const float sum = across4_sum((ps[0] + ps[1]) + (ps[2] + ps[3]));
+      const float f = sum > 0.f ? wv * rcp_hw(sum) : 0.f;
+      // P (row j = this lane's column): reduction index 8 grp + e of k-step
+      // ks is key 32 ks + 16 (e >> 2) + 4 grp + (e & 3), the tiled-V order.
+      u32x4_t Pb[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        Pb[ks][0] = pack_bf16x2(S[2 * ks][0] * f, S[2 * ks][1] * f);
+        Pb[ks][1] = pack_bf16x2(S[2 * ks][2] * f, S[2 * ks][3] * f);
+        Pb[ks][2] = pack_bf16x2(S[2 * ks + 1][0] * f, S[2 * ks + 1][1] * f);
+        Pb[ks][3] = pack_bf16x2(S[2 * ks + 1][2] * f, S[2 * ks + 1][3] * f);
+      }
+      // O_tile = P . V: lane (grp, j) gets rows (columns) 4 grp + r, d = 16 nt + j.
+      f32x4_t acc[8];
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) {
+        acc[nt] = mfma_bf16_16x16x32(Pb[0], vb[nt][0], zero4());
+        acc[nt] = mfma_bf16_16x16x32(Pb[1], vb[nt][1], acc[nt]);
+      }
+      if constexpr (LAST) load_v(vb, frs, flo, (uint32_t)cn * kFragBytes);
+      // Add into the owners' rows: column 4 grp + r is owner r & 1, head
+      // 2 grp + (r >> 1); padding columns add into the sink row.
+      const int qa = __builtin_amdgcn_readfirstlane(it_q[i0 + 2 * t]);
+      const bool hb = 2 * t + 1 < n;
+      const int qb = hb ? __builtin_amdgcn_readfirstlane(it_q[i0 + 2 * t + 1]) : qa;
+      const uint32_t want = (1u << qa) | (hb ? 1u << qb : 0u);
+      float* row[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int g = 2 * grp + (r >> 1);
+        const bool ok = 2 * t + (r & 1) < n && g < G;
+        row[r] = O + (ok ? ((r & 1) ? qb : qa) * G + g : sink) * 128 + 4 * j;
+      }
+      bool locked = false;
+      for (int spin = 0; spin < a.spin_limit; ++spin) {
+        uint32_t old = 0u;
+        if (lane == 0) old = lds_or_rtn(lock_addr, want);
+        old = __builtin_amdgcn_readfirstlane(old);
+        if ((old & want) == 0u) {
+          locked = true;
+          break;
+        }
+        if (lane == 0) lds_and(lock_addr, ~(want & ~old));  // undo the bits set now
+        __builtin_amdgcn_s_sleep(1);
+      }
+      // The lock word is read back above with lgkmcnt(0): the row reads
+      // below are issued after it.
+      if (locked) {
+        f32x4_t x[4][2];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          x[r][0] = *reinterpret_cast<const f32x4_t*>(row[r]);
+          x[r][1] = *reinterpret_cast<const f32x4_t*>(row[r] + 64);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            x[r][0][i] += acc[i][r];
+            x[r][1][i] += acc[4 + i][r];
+          }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          *reinterpret_cast<f32x4_t*>(row[r]) = x[r][0];
+          *reinterpret_cast<f32x4_t*>(row[r] + 64) = x[r][1];
+        }
+        // The row writes are issued before the release and the LDS
+        // completes one wave's operations in order.
+        asm volatile("" ::: "memory");
+        if (lane == 0) lds_and(lock_addr, ~want);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int nt = 0; nt < 8; ++nt)
+            __hip_atomic_fetch_add(row[r] + 64 * (nt >> 2) + (nt & 3), acc[nt][r],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+  };
+
+  if (st < st_hi) {
+    c = __builtin_amdgcn_readfirstlane(s_chunk[st]);
+    i0 = __builtin_amdgcn_readfirstlane(s_off[st]);
+    n = __builtin_amdgcn_readfirstlane(s_off[st + 1]) - i0;
+    msk = uniform64(s_excl[st]);
+    load_k(kb, frs, flo, (uint32_t)c * kFragBytes);
+    if constexpr (!TOKEN) load_v(vb, frs, flo, (uint32_t)c * kFragBytes);
+    load_q(Qb, qrs, qoff(i0 + min(own, n - 1), own < n && gcol < G));
+    while (true) {
+      const int nst = st + kWaves;
+      more = nst < st_hi;
+      cn = c;
+      i0n = 0;
+      nn = 0;
+      if (more) {
+        cn = __builtin_amdgcn_readfirstlane(s_chunk[nst]);
+        i0n = __builtin_amdgcn_readfirstlane(s_off[nst]);
+        nn = __builtin_amdgcn_readfirstlane(s_off[nst + 1]) - i0n;
+      }
+      const int T = (n + 1) >> 1;
+      for (int t = 0; t + 1 < T; ++t) do_tile(t, std::false_type{});
+      do_tile(T - 1, std::true_type{});
+      if (!more) break;
+      st = nst;
+      c = cn;
+      i0 = i0n;
+      n = nn;
+      msk = uniform64(s_excl[st]);
+    }
+  }
+
+  // ---- epilogue -----------------------------------------------------------
+  if constexpr (!TOKEN) {
+    __syncthreads();
+    const int rows = nq * G;
+    for (int e = tid; e < rows * 16; e += kThreads) {
+      const int rho = e >> 4, u = e & 15;
+      const int qq = rho / G, g = rho - qq * G;
+      // d = 8 u + i = 16 nt + j: nt = u >> 1, j = 8 (u & 1) + i
+      const int nt = u >> 1, j0 = 8 * (u & 1);
+      const float* src = O + rho * 128 + 64 * (nt >> 2) + 4 * j0 + (nt & 3);
+      float x[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = src[4 * i];
+      const int64_t row = (b * a.Lq + q0 + qq) * a.Hq + h * G + g;
+      if (a.parts > 1) {
+        float* prow = a.partial + ((int64_t)part * a.B * a.Lq * a.Hq + row) * 128 + 8 * u;
+        f32x4_t x0 = {x[0], x[1], x[2], x[3]}, x1 = {x[4], x[5], x[6], x[7]};
+        reinterpret_cast<f32x4_t*>(prow)[0] = x0;
+        reinterpret_cast<f32x4_t*>(prow)[1] = x1;
+        continue;
+      }
+      u32x4_t o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+      if (a.fuse_local) {
+        const float wl = bf16_to_f32(a.fuse_w[row]);
+        const u32x4_t l = *reinterpret_cast<const u32x4_t*>(a.fuse_local + row * 128 + 8 * u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = fuse_bf16x2(o[i], l[i], wl);
+      }
+      *reinterpret_cast<u32x4_t*>(a.out + row * 128 + 8 * u) = o;
+    }
+  }
+}
+
+// Sum of the walk parts' fp32 partial outputs, rounded to bf16 once (and
+// fused with the local branch when fuse_local is set: 32 groups of 4 per
+// 128-wide row).
+__global__ void __launch_bounds__(256) sum_parts_kernel(const float* __restrict__ partial,
+                                                        int parts, int64_t n4,
+                                                        uint16_t* __restrict__ out,
+                                                        const uint16_t* __restrict__ fuse_local,
+                                                        const uint16_t* __restrict__ fuse_w) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n4; e += stride) {
+    f32x4_t s = reinterpret_cast<const f32x4_t*>(partial)[e];
+    for (int p = 1; p < parts; ++p) {
+      const f32x4_t x = reinterpret_cast<const f32x4_t*>(partial)[(int64_t)p * n4 + e];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[i] += x[i];
+    }
+    u32x2_t o;
+    o[0] = pack_bf16x2(s[0], s[1]);
+    o[1] = pack_bf16x2(s[2], s[3]);
+    if (fuse_local) {
+      const float wl = bf16_to_f32(fuse_w[e >> 5]);
+      const u32x2_t l = reinterpret_cast<const u32x2_t*>(fuse_local)[e];
+      o[0] = fuse_bf16x2(o[0], l[0], wl);
+      o[1] = fuse_bf16x2(o[1], l[1], wl);
+    }
+    reinterpret_cast<u32x2_t*>(out)[e] = o;
+  }
+}
+
+// Token-score mode fills every (query, slot) row first with -inf so that
+// slots without a routed chunk read as fully masked.
+__global__ void __launch_bounds__(256) fill_neg_inf(float* p, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += stride)
+    p[e] = neg_inf();
+}
+
+// Largest tile (<= 32 queries, <= 1024 items) whose LDS layout fits, 0 if none.
+int pick_tile(int G, int K, int64_t Ck, bool token, bool keep) {
+  for (int tq = std::min(kMaxTQ, kMaxItems / K); tq >= 4; tq -= 4) {
+    const RaLayout l = ra_layout(tq, G, K, Ck, token, keep);
+    if (l.total <= kLdsBytes && l.cap <= 65535) return tq;
+  }
+  return 0;
+}
+
+template <bool TOKEN, bool KEEP>
+int launch_routed(RaArgs& a, hipStream_t s) {
+  const int tq = pick_tile(a.G, a.K, a.Ck, TOKEN, KEEP);
+  if (tq == 0) return MRSA_ERR_UNSUPPORTED;
+  a.tq = tq;
+  a.ntiles = (a.Lq + tq - 1) / tq;
+  a.units = a.B * a.Hkv * a.parts * a.ntiles;
+  const int64_t grid = (a.units + 7) / 8 * 8;
+  if (grid > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
+  const RaLayout l = ra_layout(tq, a.G, a.K, a.Ck, TOKEN, KEEP);
+  // MRSA_LOCK_SPIN_LIMIT (tests): lock tries before a tile takes the atomic
+  // path; 0 sends every tile there.
+  const char* env = std::getenv("MRSA_LOCK_SPIN_LIMIT");
+  a.spin_limit = env ? std::max(0, std::atoi(env)) : kDefaultSpinLimit;
+  auto kern = routed_attn_kernel<TOKEN, KEEP>;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)l.total) != hipSuccess)
+    return MRSA_ERR_LAUNCH;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), l.total, s, a);
+  return mrsa_launch_status();
+}
+
+int check_common(const void* q, const void* kv_frags, const int32_t* indices, int64_t batch,
+                 int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads,
+                 int64_t head_dim, int64_t topk, int64_t chunk_size, float sm_scale) {
+  if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 ||
+      q_heads % kv_heads != 0 || head_dim <= 0 || topk <= 0 || chunk_size <= 0 ||
+      !(sm_scale > 0.f) || sm_scale == __builtin_inff())
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (kv_len % chunk_size != 0) return MRSA_ERR_INVALID_ARGUMENT;
+  if (chunk_size != 64 || head_dim != 128 || q_heads / kv_heads > 8 || topk > kMaxTopk)
+    return MRSA_ERR_UNSUPPORTED;
+  if (kv_heads > 65535 || batch > 65535) return MRSA_ERR_UNSUPPORTED;
+  // a KV head's fragments are addressed with 32-bit byte offsets
+  if (kv_len / 64 >= 131072 || q_heads > 65535) return MRSA_ERR_UNSUPPORTED;
+  if (batch > 0 && q_len > 0 && (!q || !kv_frags || !indices)) return MRSA_ERR_INVALID_ARGUMENT;
+  if (((uintptr_t)q | (uintptr_t)kv_frags) % 16 != 0) return MRSA_ERR_INVALID_ARGUMENT;
+  return MRSA_OK;
+}
+
+RaArgs base_args(const void* q, const void* kv_frags, const void* weights,
+                 const int32_t* indices, const uint8_t* key_valid, int64_t batch, int64_t q_len,
+                 int64_t kv_len, int64_t q_heads, int64_t kv_heads, int64_t topk,
+                 int mask_last_token, float sm_scale) {
+  RaArgs a;
+  a.q = (const uint16_t*)q;
+  a.kvf = (const uint16_t*)kv_frags;
+  a.w = (const uint16_t*)weights;
+  a.idx = indices;
+  a.key_valid = key_valid;
+  a.keep = nullptr;
+  a.B = batch;
+  a.Lq = q_len;
+  a.Lk = kv_len;
+  a.Hq = (int)q_heads;
+  a.Hkv = (int)kv_heads;
+  a.G = (int)(q_heads / kv_heads);
+  a.K = (int)topk;
+  a.Ck = kv_len / 64;
+  a.mask_last = mask_last_token;
+  a.scale_log2 = sm_scale * kLog2e;
+  a.sm_scale = sm_scale;
+  a.out = nullptr;
+  a.tscores = nullptr;
+  a.parts = 1;
+  a.partial = nullptr;
+  a.fuse_local = nullptr;
+  a.fuse_w = nullptr;
+  a.tq = 0;
+  a.ntiles = 0;
+  a.units = 0;
+  a.spin_limit = kDefaultSpinLimit;
+  return a;
+}
+
+// Routed attention with an optional walk split (parts > 1: fp32 partials in
+// `partial`, summed into `out`), an optional token keep mask and an optional
+// output fusion.
+int selected_forward(const void* q, const void* kv_frags, const void* weights,
+                     const int32_t* indices, const uint8_t* key_valid, const int8_t* keep,
+                     int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
+                     int64_t kv_heads, int64_t head_dim, int64_t topk, int64_t chunk_size,
+                     int mask_last_token, float sm_scale, int64_t parts, float* partial,
+                     const void* fuse_local, const void* fuse_w, void* out, void* stream) {
+  int st = check_common(q, kv_frags, indices, batch, q_len, kv_len, q_heads, kv_heads, head_dim,
+                        topk, chunk_size, sm_scale);
+  if (st != MRSA_OK) return st;
+  if (parts < 1 || parts > kMaxParts) return MRSA_ERR_INVALID_ARGUMENT;
+  if (batch * parts > 65535) return MRSA_ERR_UNSUPPORTED;
+  if (batch == 0 || q_len == 0) return MRSA_OK;
+  if (!weights || !out || (uintptr_t)out % 16 != 0) return MRSA_ERR_INVALID_ARGUMENT;
+  if (parts > 1 && (!partial || (uintptr_t)partial % 16 != 0)) return MRSA_ERR_INVALID_ARGUMENT;
+  if ((fuse_local == nullptr) != (fuse_w == nullptr)) return MRSA_ERR_INVALID_ARGUMENT;
+  if (fuse_local && (uintptr_t)fuse_local % 16 != 0) return MRSA_ERR_INVALID_ARGUMENT;
+  RaArgs a = base_args(q, kv_frags, weights, indices, key_valid, batch, q_len, kv_len, q_heads,
+                       kv_heads, topk, mask_last_token, sm_scale);
+  a.out = parts > 1 ? nullptr : (uint16_t*)out;
+  a.parts = (int)parts;
+  a.partial = parts > 1 ? partial : nullptr;
+  a.keep = keep;
+  a.fuse_local = parts > 1 ? nullptr : (const uint16_t*)fuse_local;
+  a.fuse_w = parts > 1 ? nullptr : (const uint16_t*)fuse_w;
+  hipStream_t s = (hipStream_t)stream;
+  st = keep ? launch_routed<false, true>(a, s) : launch_routed<false, false>(a, s);
+  if (st != MRSA_OK || parts == 1) return st;
+  const int64_t n4 = batch * q_len * q_heads * 128 / 4;
+  const int64_t blocks = std::min<int64_t>((n4 + 255) / 256, 4096);
+  hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)blocks), dim3(256), 0, s, partial,
+                     (int)parts, n4, (uint16_t*)out, (const uint16_t*)fuse_local,
+                     (const uint16_t*)fuse_w);
+  return mrsa_launch_status();
+}
+
+}  // namespace
+
+extern "C" int mrsa_selected_attention_fwd(const void* q, const void* kv_frags,
+                                           const void* weights, const int32_t* indices,
+                                           const uint8_t* key_valid, int64_t batch,
+                                           int64_t q_len, int64_t kv_len, int64_t q_heads,
+                                           int64_t kv_heads, int64_t head_dim, int64_t topk,
+                                           int64_t chunk_size, int mask_last_token,
+                                           float sm_scale, void* out, void* stream) {
+  return selected_forward(q, kv_frags, weights, indices, key_valid, nullptr, batch, q_len,
+                          kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
+                          sm_scale, 1, nullptr, nullptr, nullptr, out, stream);
+}
+
+extern "C" int mrsa_candidate_token_scores_fwd(const void* q, const void* kv_frags,
+                                               const int32_t* indices, const uint8_t* key_valid,
+                                               int64_t batch, int64_t q_len, int64_t kv_len,
+                                               int64_t q_heads, int64_t kv_heads,
+                                               int64_t head_dim, int64_t topk,
+                                               int64_t chunk_size, float sm_scale,
+                                               float* scores, void* stream) {
+  int st = check_common(q, kv_frags, indices, batch, q_len, kv_len, q_heads, kv_heads, head_dim,
+                        topk, chunk_size, sm_scale);
+  if (st != MRSA_OK) return st;
+  if (batch == 0 || q_len == 0) return MRSA_OK;
+  if (!scores || (uintptr_t)scores % 16 != 0) return MRSA_ERR_INVALID_ARGUMENT;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t n = batch * q_len * kv_heads * topk * chunk_size;
+  const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
+  hipLaunchKernelGGL(fill_neg_inf, dim3((unsigned)blocks), dim3(256), 0, s, scores, n);
+  st = mrsa_launch_status();
+  if (st != MRSA_OK) return st;
+  RaArgs a = base_args(q, kv_frags, nullptr, indices, key_valid, batch, q_len, kv_len, q_heads,
+                       kv_heads, topk, 1, sm_scale);
+  a.tscores = scores;
+  return launch_routed<true, false>(a, s);
+}
+
+extern "C" int mrsa_selected_attention_split_fwd(
+    const void* q, const void* kv_frags, const void* weights,
+    const int32_t* indices, const uint8_t* key_valid, int64_t batch, int64_t q_len,
+    int64_t kv_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t topk,
+    int64_t chunk_size, int mask_last_token, float sm_scale, int64_t parts, float* partial,
+    void* out, void* stream) {
+  return selected_forward(q, kv_frags, weights, indices, key_valid, nullptr, batch, q_len,
+                          kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
+                          sm_scale, parts, partial, nullptr, nullptr, out, stream);
+}
+
+extern "C" int mrsa_selected_attention_keep_fwd(
+    const void* q, const void* kv_frags, const void* weights,
+    const int32_t* indices, const uint8_t* key_valid, const int8_t* token_keep, int64_t batch,
+    int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+    int64_t topk, int64_t chunk_size, int mask_last_token, float sm_scale, int64_t parts,
+    float* partial, void* out, void* stream) {
+  if (batch > 0 && q_len > 0 && !token_keep) return MRSA_ERR_INVALID_ARGUMENT;
+  return selected_forward(q, kv_frags, weights, indices, key_valid, token_keep, batch, q_len,
+                          kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
+                          sm_scale, parts, partial, nullptr, nullptr, out, stream);
+}
+
+extern "C" int mrsa_selected_attention_fused_fwd(
+    const void* q, const void* kv_frags, const void* weights,
+    const int32_t* indices, const uint8_t* key_valid, const int8_t* token_keep,
+    const void* local_output, const void* local_weight, int64_t batch, int64_t q_len,
+    int64_t kv_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t topk,
+    int64_t chunk_size, int mask_last_token, float sm_scale, int64_t parts, float* partial,
+    void* out, void* stream) {
+  if (batch > 0 && q_len > 0 && (!local_output || !local_weight))
+    return MRSA_ERR_INVALID_ARGUMENT;
+  return selected_forward(q, kv_frags, weights, indices, key_valid, token_keep, batch, q_len,
+                          kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
+                          sm_scale, parts, partial, local_output, local_weight, out, stream);
+}

@@ -25,7 +25,9 @@ from .kernel_utils import _drop_mask_impl, _drop_mask_rows_impl
 from .local_attention import _local_attention_impl
 from .pool import _pool_bwd_impl, _pool_impl
 from .route_weights import _route_weights_bwd_impl, _route_weights_impl
-from .sparse_attention import _selected_attention_impl, _value_tiles_impl, _value_tiles_rows_impl
+from .sparse_attention import (FRAG_ELEMS, _kv_fragments_impl, _kv_fragments_rows_impl,
+                               _selected_attention_impl, _value_tiles_impl,
+                               _value_tiles_rows_impl)
 from .token_refinement import _token_keep_impl
 from .token_score import _token_scores_impl
 from .topk import _route_topk_impl
@@ -57,6 +59,28 @@ def value_tiles_rows_(v: Tensor, v_tiles: Tensor, positions: Tensor) -> None:
 
 @value_tiles_rows_.register_fake
 def _(v, v_tiles, positions):
+    return None
+
+
+# -- K / V fragments --------------------------------------------------------
+@_op("kv_fragments")
+def kv_fragments(k: Tensor, v: Optional[Tensor]) -> Tensor:
+    return _kv_fragments_impl(k, v)
+
+
+@kv_fragments.register_fake
+def _(k, v):
+    B, L, H, _ = k.shape
+    return k.new_empty(B, H, (L + 63) // 64, FRAG_ELEMS, dtype=torch.bfloat16)
+
+
+@_op("kv_fragments_rows_", mutates_args=("kv_frags",))
+def kv_fragments_rows_(k: Tensor, v: Tensor, kv_frags: Tensor, positions: Tensor) -> None:
+    _kv_fragments_rows_impl(k, v, kv_frags, positions)
+
+
+@kv_fragments_rows_.register_fake
+def _(k, v, kv_frags, positions):
     return None
 
 
@@ -168,17 +192,17 @@ def _(scores, indices, prior_bias, local_lse, grad_remote, grad_local, grad_gate
 
 # -- routed chunk attention -----------------------------------------------
 @_op("selected_attention")
-def selected_attention(q: Tensor, k: Tensor, v_tiles: Tensor, weights: Tensor, indices: Tensor,
+def selected_attention(q: Tensor, kv_frags: Tensor, weights: Tensor, indices: Tensor,
                        key_valid: Optional[Tensor], chunk_size: int, mask_last_token: bool,
                        sm_scale: float, parts: int, token_keep: Optional[Tensor],
                        fuse_local: Optional[Tensor], fuse_weight: Optional[Tensor]) -> Tensor:
-    return _selected_attention_impl(q, k, v_tiles, weights, indices, key_valid, chunk_size,
+    return _selected_attention_impl(q, kv_frags, weights, indices, key_valid, chunk_size,
                                     mask_last_token, sm_scale, parts, token_keep, fuse_local,
                                     fuse_weight)
 
 
 @selected_attention.register_fake
-def _(q, k, v_tiles, weights, indices, key_valid, chunk_size, mask_last_token, sm_scale, parts,
+def _(q, kv_frags, weights, indices, key_valid, chunk_size, mask_last_token, sm_scale, parts,
       token_keep, fuse_local, fuse_weight):
     return q.new_empty(q.shape, dtype=torch.bfloat16)
 
@@ -234,13 +258,13 @@ def _(valid_mask, query_positions, window, chunk_size):
 
 # -- remote-token refinement ----------------------------------------------
 @_op("candidate_token_scores")
-def candidate_token_scores(q: Tensor, k: Tensor, indices: Tensor, key_valid: Tensor,
+def candidate_token_scores(q: Tensor, kv_frags: Tensor, indices: Tensor, key_valid: Tensor,
                            chunk_size: int) -> Tensor:
-    return _token_scores_impl(q, k, indices, key_valid, chunk_size)
+    return _token_scores_impl(q, kv_frags, indices, key_valid, chunk_size)
 
 
 @candidate_token_scores.register_fake
-def _(q, k, indices, key_valid, chunk_size):
+def _(q, kv_frags, indices, key_valid, chunk_size):
     B, Lq, Hkv, K = indices.shape
     return q.new_empty(B, Lq, Hkv, K, chunk_size, dtype=torch.float32)
 
@@ -256,7 +280,7 @@ def _(ranking, token_budget, as_int8):
 
 
 OPERATORS = (
-    "value_tiles", "value_tiles_rows_", "local_attention", "chunk_attn_pool",
+    "value_tiles", "value_tiles_rows_", "kv_fragments", "kv_fragments_rows_", "local_attention", "chunk_attn_pool",
     "chunk_attn_pool_bwd", "route_topk", "route_weights", "route_weights_bwd",
     "selected_attention", "fuse_hils_outputs", "fuse_hils_outputs_bwd", "remote_drop_mask",
     "remote_drop_mask_rows", "candidate_token_scores", "token_keep",

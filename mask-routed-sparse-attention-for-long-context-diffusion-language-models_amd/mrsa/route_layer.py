@@ -40,7 +40,8 @@ from .kernel_utils import drop_mask_rows_launch
 from .local_attention import local_attention_launch
 from .pool import chunk_attn_pool_gqa_prior
 from .route_weights import route_weights_launch
-from .sparse_attention import selected_attention_launch, value_tiles, value_tiles_rows
+from .sparse_attention import (FRAG_ELEMS, kv_fragments, kv_fragments_rows,
+                               selected_attention_launch, value_tiles, value_tiles_rows)
 from .token_refinement import refine_remote_tokens_g7
 from .topk import route_topk_launch
 
@@ -121,6 +122,7 @@ def route_attention(
 
     _mark("start")
     vt = value_tiles(v)
+    frags = kv_fragments(k, v)
     _mark("value_tiles")
     flash_window = cfg.local_window + S - 1 if cfg.skip_inert_slots else cfg.local_window
     local_out, local_lse = local_attention_launch(
@@ -159,17 +161,17 @@ def route_attention(
     token_keep = None
     if cfg.token_budget > 0:
         token_keep = refine_remote_tokens_g7(q, k, indices, kv_bool, S, cfg.token_budget,
-                                             training=False)
+                                             training=False, kv_frags=frags)
         _mark("token_refinement")
     # Routed attention with the output fusion in its epilogue:
     # fuse_hils_outputs(remote, local_out, local_w) without materialising remote.
-    out = selected_attention_launch(q, k, vt, remote_w, indices, kv_bool, S,
+    out = selected_attention_launch(q, frags, remote_w, indices, kv_bool, S,
                                     token_keep=token_keep, fuse_local=local_out,
                                     fuse_weight=local_w)
     _mark("selected_attention")
     if not return_intermediates:
         return out
-    remote_out = selected_attention_launch(q, k, vt, remote_w, indices, kv_bool, S,
+    remote_out = selected_attention_launch(q, frags, remote_w, indices, kv_bool, S,
                                            token_keep=token_keep)
     return out, {
         "local_output": local_out, "local_lse": local_lse, "landmark_keys": lmk,
@@ -221,9 +223,11 @@ class LayerKVCache:
     key_valid bool [1, L], landmark_keys bf16 [1, C, Hkv, G, D] and prior_bias
     fp32 [1, C, Hkv, G] (the last two refreshed in place).
 
-    ``value_tiles`` is the tiled copy of ``value`` the attention kernels read
-    (built on first use).  ``replace`` keeps it in step with the rows it
-    writes; after writing ``value`` any other way, set it to None.
+    ``value_tiles`` (the tiled copy of ``value`` the window attention reads)
+    and ``kv_frags`` (the ``kv_fragments`` layout of key and value the routed
+    attention reads) are built on first use.  ``replace`` keeps them in step
+    with the rows it writes; after writing ``key`` or ``value`` any other
+    way, set both to None.
     """
 
     key: torch.Tensor
@@ -232,6 +236,7 @@ class LayerKVCache:
     landmark_keys: torch.Tensor
     prior_bias: torch.Tensor
     value_tiles: torch.Tensor | None = field(default=None, repr=False)
+    kv_frags: torch.Tensor | None = field(default=None, repr=False)
 
     @property
     def physical_length(self) -> int:
@@ -268,6 +273,8 @@ class LayerKVCache:
         self.value.index_copy_(1, positions, value)
         if self.value_tiles is not None:
             value_tiles_rows(self.value, self.value_tiles, positions)
+        if self.kv_frags is not None:
+            kv_fragments_rows(self.key, self.value, self.kv_frags, positions)
 
     def __post_init__(self) -> None:
         # fastdllm_cache.py:20-80 (the checks this path depends on)
@@ -288,6 +295,9 @@ class LayerKVCache:
         if self.value_tiles is not None and self.value_tiles.shape != (
                 batch, hkv, (self.key.shape[1] + 63) // 64, dim, 64):
             raise ValueError("value_tiles must be value_tiles(value)")
+        if self.kv_frags is not None and self.kv_frags.shape != (
+                batch, hkv, (self.key.shape[1] + 63) // 64, FRAG_ELEMS):
+            raise ValueError("kv_frags must be kv_fragments(key, value)")
 
 
 def cached_route_attention(
@@ -392,6 +402,8 @@ def _cached_route_body(q, route_q, cache, query_positions, affected_chunks, entr
     n = affected_chunks.numel()
     if cache.value_tiles is None:
         cache.value_tiles = value_tiles(cache.value)
+    if cache.kv_frags is None:
+        cache.kv_frags = kv_fragments(cache.key, cache.value)
     vt = cache.value_tiles
     flash_window = cfg.local_window + S - 1 if cfg.skip_inert_slots else cfg.local_window
     local_out, local_lse = local_attention_launch(
@@ -426,11 +438,12 @@ def _cached_route_body(q, route_q, cache, query_positions, affected_chunks, entr
     remote_w, local_w = route_weights_launch(
         scores, indices, cache.prior_bias, local_lse, temperature=1.0
     )
-    out = selected_attention_launch(q, cache.key, vt, remote_w, indices, cache.key_valid, S,
+    out = selected_attention_launch(q, cache.kv_frags, remote_w, indices, cache.key_valid, S,
                                     fuse_local=local_out, fuse_weight=local_w)
     if not return_intermediates:
         return out
-    remote_out = selected_attention_launch(q, cache.key, vt, remote_w, indices, cache.key_valid, S)
+    remote_out = selected_attention_launch(q, cache.kv_frags, remote_w, indices,
+                                           cache.key_valid, S)
     return out, {
         "local_output": local_out, "local_lse": local_lse, "indices": indices,
         "scores": scores, "remote_weights": remote_w, "local_weight": local_w,
@@ -469,12 +482,15 @@ class CachedBlockStep:
         self._graphs = {}  # affected count -> (graph, affected buffer, output)
         if cache.value_tiles is None:
             cache.value_tiles = value_tiles(cache.value)
+        if cache.kv_frags is None:
+            cache.kv_frags = kv_fragments(cache.key, cache.value)
 
     def _body(self, affected):
         c = self.cache
         c.key.index_copy_(1, self.positions, self.k_rows)
         c.value.index_copy_(1, self.positions, self.v_rows)
         value_tiles_rows(c.value, c.value_tiles, self.positions)
+        kv_fragments_rows(c.key, c.value, c.kv_frags, self.positions)
         return _cached_route_body(self.q, self.route_q, c, self.positions, affected, self.scale,
                                   self.cfg)
 

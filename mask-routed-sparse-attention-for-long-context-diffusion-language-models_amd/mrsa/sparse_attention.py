@@ -1,8 +1,9 @@
-"""Routed chunk attention (and the tiled V layout it reads).
+"""Routed chunk attention and the K / V layouts the attention kernels read.
 
 Drop-in for ``ops.hils_fwd_bwd_head.HiLS_block_M_head``
 (ops/hils_fwd_bwd_head.py:1113-1150) in its forward role, plus
-``value_tiles``, the V re-layout both attention kernels consume.
+``value_tiles`` (the tiled V the window attention reads) and
+``kv_fragments`` (the per-chunk operand images the routed attention reads).
 """
 
 from __future__ import annotations
@@ -35,8 +36,65 @@ def _value_tiles_impl(v: torch.Tensor) -> torch.Tensor:
     return out
 
 
-# Queries per routed-attention workgroup (12 waves x 2 column tiles x 2).
-_SEL_TILE_QUERIES = 48
+FRAG_ELEMS = 16384  # bf16 per (batch, KV head, 64-key chunk)
+
+
+def kv_fragments(k: torch.Tensor, v: torch.Tensor | None = None) -> torch.Tensor:
+    """K, V [B, L, Hkv, 128] bf16 -> per-chunk fragments [B, Hkv, ceil(L/64), 16384] bf16.
+
+    For each 64-key chunk, the register images of the routed attention's 32
+    matrix-core operand loads (lane l = 16 grp + j, elements e = 0..7):
+    f[512 i + 8 l + e] = K[16 mt + j][32 ks + 8 grp + e] for i = 4 mt + ks, and
+    f[8192 + 512 i + 8 l + e] = V[32 ks + 16 (e >> 2) + 4 grp + (e & 3)][16 nt + j]
+    for i = 2 nt + ks.  Keys past L are zero; without ``v`` the V half is zero
+    (candidate token scores read only K).
+    """
+
+    if k.device.type != "cuda" or k.dtype != torch.bfloat16 or k.ndim != 4 or k.shape[3] != 128:
+        raise ValueError("kv_fragments requires a CUDA BF16 [B, L, Hkv, 128] key tensor")
+    if v is not None and (v.shape != k.shape or v.dtype != k.dtype or v.device != k.device):
+        raise ValueError("kv_fragments requires v shaped, typed and placed like k")
+    return torch.ops.mrsa.kv_fragments(k, v)
+
+
+def _kv_fragments_impl(k: torch.Tensor, v: torch.Tensor | None) -> torch.Tensor:
+    B, L, H, D = k.shape
+    kc = k.contiguous()
+    vc = None if v is None else v.contiguous()
+    out = torch.empty(B, H, (L + 63) // 64, FRAG_ELEMS, dtype=torch.bfloat16, device=k.device)
+    st = _lib.call("mrsa_kv_fragments", _lib.ptr(kc), _lib.ptr(vc), B, L, H, D, _lib.ptr(out),
+                   _lib.stream_of(kc))
+    _lib.check(st, "kv_fragments")
+    return out
+
+
+def kv_fragments_rows(k: torch.Tensor, v: torch.Tensor, kv_frags: torch.Tensor,
+                      positions: torch.Tensor) -> None:
+    """Rewrite the fragments of rows ``positions`` of k and v in ``kv_frags``
+    (in place), after those rows were replaced.  Positions outside [0, L)
+    are ignored."""
+
+    if k.device.type != "cuda" or k.dtype != torch.bfloat16 or k.ndim != 4 or k.shape[3] != 128:
+        raise ValueError("kv_fragments_rows requires a CUDA BF16 [B, L, Hkv, 128] key tensor")
+    if v.shape != k.shape or v.dtype != k.dtype:
+        raise ValueError("kv_fragments_rows requires v shaped and typed like k")
+    B, L, H, _ = k.shape
+    if kv_frags.shape != (B, H, (L + 63) // 64, FRAG_ELEMS) or not kv_frags.is_contiguous():
+        raise ValueError("kv_frags must be the contiguous kv_fragments(k, v) layout")
+    torch.ops.mrsa.kv_fragments_rows_(k, v, kv_frags, positions)
+
+
+def _kv_fragments_rows_impl(k, v, kv_frags, positions) -> None:
+    B, L, H, D = k.shape
+    kc, vc = k.contiguous(), v.contiguous()
+    pos = positions.to(device=k.device, dtype=torch.long).contiguous()
+    st = _lib.call("mrsa_kv_fragments_rows", _lib.ptr(kc), _lib.ptr(vc), B, L, H, D,
+                   _lib.ptr(pos), pos.numel(), _lib.ptr(kv_frags), _lib.stream_of(kc))
+    _lib.check(st, "kv_fragments_rows")
+
+
+# Queries per routed-attention workgroup (the kernel picks up to 32).
+_SEL_TILE_QUERIES = 32
 _SEL_MAX_PARTS = 64
 
 
@@ -81,8 +139,7 @@ def _value_tiles_rows_impl(v: torch.Tensor, v_tiles: torch.Tensor, positions: to
 
 def selected_attention_launch(
     q: torch.Tensor,
-    k: torch.Tensor,
-    v_tiles: torch.Tensor,
+    kv_frags: torch.Tensor,
     weights: torch.Tensor,
     indices: torch.Tensor,
     key_valid: torch.Tensor | None,
@@ -95,7 +152,8 @@ def selected_attention_launch(
     fuse_local: torch.Tensor | None = None,
     fuse_weight: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """q [B, Lq, Hq, D], k [B, Lk, Hkv, D], weights [B, Lq, Hq, K] -> [B, Lq, Hq, D] bf16.
+    """q [B, Lq, Hq, D], kv_frags = kv_fragments(k, v) of the Lk-row cache,
+    weights [B, Lq, Hq, K] -> [B, Lq, Hq, D] bf16.
 
     ``parts`` splits each walk over that many workgroups (fp32 partial
     outputs summed by a second kernel); None picks it with ``walk_parts``.
@@ -107,7 +165,9 @@ def selected_attention_launch(
     """
 
     B, Lq, Hq, D = q.shape
-    Lk, Hkv = k.shape[1], k.shape[2]
+    if kv_frags.ndim != 4 or kv_frags.shape[0] != B or kv_frags.shape[3] != FRAG_ELEMS:
+        raise ValueError(f"kv_frags {tuple(kv_frags.shape)} is not a kv_fragments layout")
+    Hkv, Lk = kv_frags.shape[1], kv_frags.shape[2] * 64
     K = indices.shape[-1]
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
@@ -124,18 +184,18 @@ def selected_attention_launch(
             f"fusion shapes {tuple(fuse_local.shape)} / {tuple(fuse_weight.shape)} do not "
             f"match the output [{B}, {Lq}, {Hq}, {D}]")
     return torch.ops.mrsa.selected_attention(
-        q, k, v_tiles, weights, indices, key_valid, int(chunk_size), bool(mask_last_token),
+        q, kv_frags, weights, indices, key_valid, int(chunk_size), bool(mask_last_token),
         float(sm_scale), parts, token_keep, fuse_local, fuse_weight)
 
 
-def _selected_attention_impl(q, k, v_tiles, weights, indices, key_valid, chunk_size,
+def _selected_attention_impl(q, kv_frags, weights, indices, key_valid, chunk_size,
                              mask_last_token, sm_scale, parts, token_keep, fuse_local,
                              fuse_weight):
     B, Lq, Hq, D = q.shape
-    Lk, Hkv = k.shape[1], k.shape[2]
+    Hkv, Lk = kv_frags.shape[1], kv_frags.shape[2] * 64
     K = indices.shape[-1]
     qc = q.contiguous()
-    kc = k.contiguous()
+    kf = kv_frags.contiguous()
     w = weights.to(torch.bfloat16).contiguous()
     idx = indices.to(torch.int32).contiguous()
     kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
@@ -151,7 +211,7 @@ def _selected_attention_impl(q, k, v_tiles, weights, indices, key_valid, chunk_s
             partial = torch.empty(parts, B, Lq, Hq, D, dtype=torch.float32, device=q.device)
         st = _lib.call(
             "mrsa_selected_attention_fused_fwd",
-            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(w), _lib.ptr(idx),
+            _lib.ptr(qc), _lib.ptr(kf), _lib.ptr(w), _lib.ptr(idx),
             _lib.ptr(kv), _lib.ptr(keep), _lib.ptr(lo), _lib.ptr(lw), B, Lq, Lk, Hq, Hkv, D, K,
             int(chunk_size), 1 if mask_last_token else 0, float(sm_scale), parts,
             _lib.ptr(partial), _lib.ptr(out), _lib.stream_of(qc),
@@ -163,7 +223,7 @@ def _selected_attention_impl(q, k, v_tiles, weights, indices, key_valid, chunk_s
             partial = torch.empty(parts, B, Lq, Hq, D, dtype=torch.float32, device=q.device)
         st = _lib.call(
             "mrsa_selected_attention_keep_fwd",
-            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(w), _lib.ptr(idx),
+            _lib.ptr(qc), _lib.ptr(kf), _lib.ptr(w), _lib.ptr(idx),
             _lib.ptr(kv), _lib.ptr(keep), B, Lq, Lk, Hq, Hkv, D, K, int(chunk_size),
             1 if mask_last_token else 0, float(sm_scale), parts, _lib.ptr(partial),
             _lib.ptr(out), _lib.stream_of(qc),
@@ -171,7 +231,7 @@ def _selected_attention_impl(q, k, v_tiles, weights, indices, key_valid, chunk_s
     elif parts == 1:
         st = _lib.call(
             "mrsa_selected_attention_fwd",
-            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(w), _lib.ptr(idx),
+            _lib.ptr(qc), _lib.ptr(kf), _lib.ptr(w), _lib.ptr(idx),
             _lib.ptr(kv), B, Lq, Lk, Hq, Hkv, D, K, int(chunk_size),
             1 if mask_last_token else 0, float(sm_scale), _lib.ptr(out), _lib.stream_of(qc),
         )
@@ -179,7 +239,7 @@ def _selected_attention_impl(q, k, v_tiles, weights, indices, key_valid, chunk_s
         partial = torch.empty(parts, B, Lq, Hq, D, dtype=torch.float32, device=q.device)
         st = _lib.call(
             "mrsa_selected_attention_split_fwd",
-            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(w), _lib.ptr(idx),
+            _lib.ptr(qc), _lib.ptr(kf), _lib.ptr(w), _lib.ptr(idx),
             _lib.ptr(kv), B, Lq, Lk, Hq, Hkv, D, K, int(chunk_size),
             1 if mask_last_token else 0, float(sm_scale), parts, _lib.ptr(partial),
             _lib.ptr(out), _lib.stream_of(qc),
@@ -221,6 +281,6 @@ def HiLS_block_M_head(
     if any(t.requires_grad for t in (q, k, v, weights)) and torch.is_grad_enabled():
         raise ValueError("HiLS_block_M_head on gfx950 is forward-only (no autograd)")
     return selected_attention_launch(
-        q, k, value_tiles(v), weights, indices, key_valid, block_size,
+        q, kv_fragments(k, v), weights, indices, key_valid, block_size,
         mask_last_token=mask_last_token, sm_scale=sm_scale, token_keep=token_keep,
     )

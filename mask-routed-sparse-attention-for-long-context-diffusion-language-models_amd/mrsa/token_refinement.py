@@ -83,9 +83,11 @@ def refine_remote_tokens_g7(
     training: bool = True,
     use_gumbel: bool = False,
     gumbel_scale: float = 1.0,
+    kv_frags: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """int8 keep mask [B, Lq, Hkv, K, chunk_size] of the routed tokens
-    (token_refinement.py:359-392)."""
+    (token_refinement.py:359-392).  ``kv_frags``: the ``kv_fragments``
+    layout of k when the caller holds it."""
 
     if q.shape[2] != k.shape[2] * 7:
         raise ValueError("Dream token refinement requires seven query heads per KV head")
@@ -96,6 +98,7 @@ def refine_remote_tokens_g7(
             indices.to(torch.int32).contiguous(),
             key_valid.contiguous(),
             chunk_size,
+            kv_frags=kv_frags,
         )
         return select_global_token_keep(
             scores, token_budget, training=training, use_gumbel=use_gumbel,

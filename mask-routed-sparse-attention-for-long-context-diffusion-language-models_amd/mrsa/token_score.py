@@ -11,6 +11,7 @@ import math
 import torch
 
 from . import _lib
+from .sparse_attention import FRAG_ELEMS, kv_fragments
 
 
 def _validate(q, k, indices, key_valid, chunk_size):
@@ -45,22 +46,31 @@ def _validate(q, k, indices, key_valid, chunk_size):
         raise ValueError("candidate_token_scores_gqa requires contiguous tensors")
 
 
-def candidate_token_scores_gqa(q, k, indices, key_valid, chunk_size):
-    """FP32 [B, Lq, Hkv, K, chunk_size] max-over-group scores of routed tokens."""
+def candidate_token_scores_gqa(q, k, indices, key_valid, chunk_size, *, kv_frags=None):
+    """FP32 [B, Lq, Hkv, K, chunk_size] max-over-group scores of routed tokens.
+
+    ``kv_frags`` (keyword, not in the reference signature): the
+    ``kv_fragments`` layout of k when the caller already holds it; built
+    from k otherwise."""
 
     _validate(q, k, indices, key_valid, chunk_size)
-    return torch.ops.mrsa.candidate_token_scores(q, k, indices, key_valid, int(chunk_size))
+    if kv_frags is None:
+        kv_frags = kv_fragments(k)
+    elif kv_frags.shape != (k.shape[0], k.shape[2], (k.shape[1] + 63) // 64, FRAG_ELEMS):
+        raise ValueError("kv_frags must be the kv_fragments layout of k")
+    return torch.ops.mrsa.candidate_token_scores(q, kv_frags, indices, key_valid,
+                                                 int(chunk_size))
 
 
-def _token_scores_impl(q, k, indices, key_valid, chunk_size):
+def _token_scores_impl(q, kv_frags, indices, key_valid, chunk_size):
     B, Lq, Hq, D = q.shape
-    Lk, Hkv = k.shape[1:3]
+    Hkv, Lk = kv_frags.shape[1], kv_frags.shape[2] * 64
     K = indices.shape[-1]
     kv = key_valid.to(torch.bool).contiguous()
     out = torch.empty(B, Lq, Hkv, K, chunk_size, dtype=torch.float32, device=q.device)
     st = _lib.call(
         "mrsa_candidate_token_scores_fwd",
-        _lib.ptr(q), _lib.ptr(k), _lib.ptr(indices), _lib.ptr(kv),
+        _lib.ptr(q), _lib.ptr(kv_frags), _lib.ptr(indices), _lib.ptr(kv),
         B, Lq, Lk, Hq, Hkv, D, K, int(chunk_size), 1.0 / math.sqrt(D),
         _lib.ptr(out), _lib.stream_of(q),
     )

@@ -57,3 +57,22 @@ def classify_routing(gpu_idx, ref_idx, route_q, lmk, lse, prior, drop_rows, topk
     print(f"{what}: routing {counts}", flush=True)
     assert counts["unexplained"] == 0, (what, counts)
     return counts
+
+
+def assert_nearly_identical(a, b, what, frac=1e-3, atol=0.0):
+    """Two launches of a kernel whose fp32 accumulation order varies between
+    runs (the routed attention adds its chunk terms into shared fp32 rows
+    with LDS atomics): bf16 results may differ only where the fp32 sum sat at
+    a rounding boundary -- by one bf16 step (plus `atol`, for outputs fused
+    after that rounding, where one step of the unfused value can exceed a
+    step of the result), in at most `frac` of the elements."""
+
+    a = a.float().cpu()
+    b = b.float().cpu()
+    diff = (a - b).abs()
+    step = torch.maximum(a.abs(), b.abs()) * 2.0 ** -7 + atol + 1e-30
+    n = int((diff > 0).sum())
+    print(f"{what}: {n} of {a.numel()} elements differ (max {float(diff.max()):.3e})",
+          flush=True)
+    assert bool((diff <= step).all()), what
+    assert n <= frac * a.numel(), what

@@ -17,7 +17,7 @@ from mrsa.route_weights import route_weights_launch
 from mrsa.sparse_attention import selected_attention_launch
 from mrsa.topk import route_topk_launch
 from oracle import mrsa_oracle as O
-from routing_check import classify_routing
+from routing_check import assert_nearly_identical, classify_routing
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -114,6 +114,36 @@ def test_value_tiles_layout():
                   for p in range(64)]
     assert sorted(key_of_pos) == list(range(64))
     assert torch.equal(t, expect[..., key_of_pos])
+
+
+def _fragments_expected(k, v):
+    # The operand images written out from their definition: K part
+    # f[4 mt + ks][16 grp + j][e] = K[16 mt + j][32 ks + 8 grp + e]; V part
+    # f[2 nt + ks][16 grp + j][4 b + e'] = V[32 ks + 16 b + 4 grp + e'][16 nt + j].
+    B, L, H, D = k.shape
+    C = (L + 63) // 64
+    kp = torch.zeros(B, C * 64, H, D, dtype=k.dtype)
+    vp = torch.zeros(B, C * 64, H, D, dtype=k.dtype)
+    kp[:, :L] = k
+    if v is not None:
+        vp[:, :L] = v
+    kc = kp.reshape(B, C, 64, H, D).permute(0, 3, 1, 2, 4)       # [B, H, C, key, dim]
+    vc = vp.reshape(B, C, 64, H, D).permute(0, 3, 1, 2, 4)
+    kf = kc.reshape(B, H, C, 4, 16, 4, 4, 8).permute(0, 1, 2, 3, 5, 6, 4, 7)
+    vf = vc.reshape(B, H, C, 2, 2, 4, 4, 8, 16).permute(0, 1, 2, 7, 3, 5, 8, 4, 6)
+    return torch.cat([kf.reshape(B, H, C, 8192), vf.reshape(B, H, C, 8192)], dim=-1)
+
+
+def test_kv_fragments_layout():
+    # Keys past the end (L = 200: the last chunk has 8 real keys) are zero,
+    # and without v the V half is zero.
+    _note("kv fragments")
+    k = _rand((2, 200, 3, 128), 8).bfloat16()
+    v = _rand((2, 200, 3, 128), 9).bfloat16()
+    got = mrsa.kv_fragments(k.to(DEV), v.to(DEV)).cpu()
+    assert torch.equal(got.view(torch.int16), _fragments_expected(k, v).view(torch.int16))
+    got = mrsa.kv_fragments(k.to(DEV)).cpu()
+    assert torch.equal(got.view(torch.int16), _fragments_expected(k, None).view(torch.int16))
 
 
 @pytest.mark.parametrize("G,dense", [(7, False), (1, True), (3, False)])
@@ -364,7 +394,7 @@ def test_selected_attention_vs_oracle(Lq, Lk, K, unsorted):
     w = torch.softmax(_rand((1, Lq, Hkv * G, K), 44), -1).bfloat16()
     valid = torch.rand(1, Lk) > 0.03
     out = selected_attention_launch(
-        q.to(DEV), k.to(DEV), mrsa.value_tiles(v.to(DEV)), w.to(DEV), idx.to(DEV), valid.to(DEV), 64)
+        q.to(DEV), mrsa.kv_fragments(k.to(DEV), v.to(DEV)), w.to(DEV), idx.to(DEV), valid.to(DEV), 64)
     ref = O.selected_attention(q, k, v, w, idx, valid, 64)
     _assert_close_attn(out, ref, f"selected Lq={Lq}")
 
@@ -387,7 +417,7 @@ def test_selected_attention_walk_split(Lq, Lk, K, parts):
     idx[0, Lq // 2, 0, 0] = C + 3                  # out of range -> skipped
     w = torch.softmax(_rand((1, Lq, Hkv * G, K), 49), -1).bfloat16()
     valid = torch.rand(1, Lk, generator=torch.Generator().manual_seed(50)) > 0.03
-    args = (q.to(DEV), k.to(DEV), mrsa.value_tiles(v.to(DEV)), w.to(DEV), idx.to(DEV),
+    args = (q.to(DEV), mrsa.kv_fragments(k.to(DEV), v.to(DEV)), w.to(DEV), idx.to(DEV),
             valid.to(DEV), 64)
     out = selected_attention_launch(*args, parts=parts)
     whole = selected_attention_launch(*args, parts=1)
@@ -398,11 +428,16 @@ def test_selected_attention_walk_split(Lq, Lk, K, parts):
 
 
 @pytest.mark.parametrize("Lq,Lk,K,parts,keep", [(700, 2048, 32, 1, False), (32, 8192, 32, 9, False),
-                                                  (200, 2048, 16, 1, True), (40, 4096, 8, 3, True)])
+                                                  (200, 2048, 16, 1, True), (40, 4096, 8, 3, True),
+                                                  (700, 2048, 1, 1, False), (32, 8192, 1, 9, False),
+                                                  (200, 2048, 1, 1, True)])
 def test_selected_attention_fused_output_equals_fusion(Lq, Lk, K, parts, keep):
     # The output fusion folded into the routed-attention epilogue (parts == 1)
-    # or into the part sum (parts > 1) gives exactly the bits of the routed
-    # output followed by fuse_hils_outputs.
+    # or into the part sum (parts > 1) gives the bits of the routed output
+    # followed by fuse_hils_outputs.  With one routed chunk per query every
+    # output row is a single term, so two launches agree bit for bit; with
+    # more, the fp32 sum's order varies between launches (rare one-step
+    # flips).
     _note(f"selected fused Lq={Lq} Lk={Lk} K={K} parts={parts} keep={keep}")
     Hkv, G, D, C = 4, 7, 128, Lk // 64
     q = _rand((1, Lq, Hkv * G, D), 80).bfloat16()
@@ -416,14 +451,17 @@ def test_selected_attention_fused_output_equals_fusion(Lq, Lk, K, parts, keep):
     if keep:
         tk = (torch.rand(1, Lq, Hkv, K, 64, generator=torch.Generator().manual_seed(87)) > 0.5)
         tk = tk.to(torch.int8).to(DEV)
-    args = (q.to(DEV), k.to(DEV), mrsa.value_tiles(v.to(DEV)), w.to(DEV), idx.to(DEV),
+    args = (q.to(DEV), mrsa.kv_fragments(k.to(DEV), v.to(DEV)), w.to(DEV), idx.to(DEV),
             valid.to(DEV), 64)
     remote = selected_attention_launch(*args, parts=parts, token_keep=tk)
     fused = selected_attention_launch(*args, parts=parts, token_keep=tk, fuse_local=local,
                                       fuse_weight=lw)
     expect = mrsa.fuse_hils_outputs(remote, local, lw)
     torch.cuda.synchronize()
-    assert torch.equal(fused.view(torch.int16), expect.view(torch.int16))
+    if K == 1:
+        assert torch.equal(fused.view(torch.int16), expect.view(torch.int16))
+    else:
+        assert_nearly_identical(fused, expect, f"fused vs fusion K={K}", atol=0.03)
 
 
 def test_selected_attention_reference_kat():
@@ -529,7 +567,7 @@ def test_route_layer_config2_full_size_sampled_rows():
     _assert_close_attn(mid["remote_output"][:, rows], remote, "cfg2 routed rows")
     fused = O.fuse_outputs(mid["remote_output"][:, rows], mid["local_output"][:, rows],
                            mid["local_weight"][:, rows])
-    assert torch.equal(out[:, rows].view(torch.int16), fused.view(torch.int16))
+    assert_nearly_identical(out[:, rows], fused, "cfg2 fused output rows", atol=0.03)
 
 
 def test_route_layer_vs_oracle():

@@ -80,8 +80,8 @@ def test_selected_attention_token_keep_vs_oracle(Lq, Lk, parts):
     g = torch.Generator().manual_seed(130)
     keep = (torch.rand(1, Lq, 4, 32, 64, generator=g) > 0.4).to(torch.int8)
     keep[0, 1, 2, 5] = 0                                  # a slot with nothing kept
-    out = selected_attention_launch(q.to(DEV), k.to(DEV), mrsa.value_tiles(v.to(DEV)), w.to(DEV),
-                                    idx.to(DEV), valid.to(DEV), 64, parts=parts,
+    out = selected_attention_launch(q.to(DEV), mrsa.kv_fragments(k.to(DEV), v.to(DEV)),
+                                    w.to(DEV), idx.to(DEV), valid.to(DEV), 64, parts=parts,
                                     token_keep=keep.to(DEV))
     ref = O.selected_attention(q, k, v, w, idx, valid, 64, token_keep=keep)
     _close(out, ref, f"selected keep Lq={Lq}")
