@@ -158,11 +158,22 @@ __device__ __forceinline__ void pair16(float v, float& a, float& b) {
   a = __uint_as_float(r[0]);
   b = __uint_as_float(r[1]);
 }
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float d;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+__device__ __forceinline__ float max_raw(float a, float b) {
+  float d;
+  asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+// Max of the 16 accumulator values a lane holds for one 64-row tile.
 __device__ __forceinline__ float across4_max(float v) {
   float a, b;
   pair32(v, a, b);
-  pair16(fmaxf(a, b), a, b);
-  return fmaxf(a, b);
+  pair16(max_raw(a, b), a, b);
+  return max_raw(a, b);
 }
 __device__ __forceinline__ float across4_sum(float v) {
   float a, b;
@@ -204,17 +215,6 @@ __device__ __forceinline__ int wave_min_i(int v) {
 
 // v_max3 / v_max without the input canonicalisation fmaxf implies; for
 // inputs that are never NaN (matrix-core products, -inf masks).
-__device__ __forceinline__ float max3_raw(float a, float b, float c) {
-  float d;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-  return d;
-}
-__device__ __forceinline__ float max_raw(float a, float b) {
-  float d;
-  asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
-  return d;
-}
-// Max of the 16 accumulator values a lane holds for one 64-row tile.
 __device__ __forceinline__ float max16_raw(const f32x4_t (&S)[4]) {
   float m = max3_raw(max3_raw(S[0][0], S[0][1], S[0][2]), max3_raw(S[0][3], S[1][0], S[1][1]),
                      S[3][3]);

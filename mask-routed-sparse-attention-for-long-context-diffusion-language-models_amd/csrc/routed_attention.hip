@@ -96,10 +96,11 @@ struct RaArgs {
 
 __host__ __device__ inline size_t al16(size_t x) { return (x + 15) & ~(size_t)15; }
 
-// LDS carve-up (byte offsets).  The output region (tq * G rows plus one sink
-// row that takes the adds of padding columns) doubles as the prologue's
-// scratch (raw index rows, list flags, staged weights, per-chunk owner bits
-// and step numbers), which is dead once the items are built.
+// LDS carve-up (byte offsets).  The output region -- query slots of 8 head
+// rows of 128 floats (heads >= G padding), one more slot taking the adds of
+// a tile's missing second owner -- doubles as the prologue's scratch (raw
+// index rows, list flags, staged weights, per-chunk owner bits and step
+// numbers), which is dead once the items are built.
 struct RaLayout {
   size_t o, o_bytes;
   size_t raw, qlen, qflag, wst, omask, step_of, scratch_end;
@@ -112,7 +113,7 @@ __host__ __device__ inline RaLayout ra_layout(int tq, int G, int K, int64_t Ck, 
   RaLayout l;
   l.items = tq * K;
   l.cap = (int)(Ck < l.items ? Ck : l.items);
-  l.o_bytes = token ? 0 : ((size_t)tq * G + 1) * 128 * 4;
+  l.o_bytes = token ? 0 : ((size_t)tq + 1) * 8 * 128 * 4;
   size_t s = 0;
   l.raw = s;     s = al16(s + (size_t)l.items * 4);
   l.qlen = s;    s = al16(s + (size_t)tq * 4);
@@ -255,7 +256,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   uint16_t* wst = reinterpret_cast<uint16_t*>(smem + L.wst);       // [tq][8][K]
   uint32_t* omask = reinterpret_cast<uint32_t*>(smem + L.omask);   // [Ck]
   uint16_t* step_of = reinterpret_cast<uint16_t*>(smem + L.step_of);  // [Ck]
-  float* O = reinterpret_cast<float*>(smem + L.o);                 // [tq * G][128]
+  float* O = reinterpret_cast<float*>(smem + L.o);                 // [tq + 1][8][128]
   int32_t* s_chunk = reinterpret_cast<int32_t*>(smem + L.chunk);   // [cap]
   int32_t* s_off = reinterpret_cast<int32_t*>(smem + L.off);       // [cap + 1]
   uint64_t* s_excl = reinterpret_cast<uint64_t*>(smem + L.excl);   // [cap] excluded keys
@@ -421,7 +422,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   const int st_hi = (int)((int64_t)(part + 1) * nsteps / a.parts);
   // 6. Outputs start at zero (the scratch above is dead now).
   if constexpr (!TOKEN) {
-    const int n4 = tq * G * 128 / 4;
+    const int n4 = tq * 8 * 128 / 4;
     for (int i = tid; i < n4; i += kThreads) reinterpret_cast<f32x4_t*>(O)[i] = zero4();
     __syncthreads();
   }
@@ -442,7 +443,9 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     return valid ? (uint32_t)it_q[max(item, 0)] * qrow + qcol : kZeroOffset;
   };
   const uint32_t lock_addr = lds_address(lock);
-  const int sink = tq * G;  // output row that takes the padding columns' adds
+  const int sinkq = tq;  // query slot taking the adds of a missing second owner
+  // this lane's place in a query slot: head 2 grp (+1), dims 4 j (+64)
+  float* const orow = O + (2 * grp) * 128 + 4 * j;
   float ninf_v = neg_inf();
   asm volatile("" : "+v"(ninf_v));  // kept in a register for set_where
 
@@ -464,6 +467,11 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     const int o = 2 * t + own;
     const bool cvalid = o < n && gcol < G;
     const int ii = i0 + (o < n ? o : n - 1);
+    // The tile's two owners (wave-uniform), read before the products.
+    const bool hb = 2 * t + 1 < n;
+    const int qa = __builtin_amdgcn_readfirstlane(it_q[i0 + 2 * t]);
+    const int qb1 = __builtin_amdgcn_readfirstlane(it_q[i0 + 2 * t + (hb ? 1 : 0)]);
+    const float wv = TOKEN ? 0.f : (cvalid ? bf16_to_f32(it_w[ii * 8 + gcol]) : 0.f);
     // S^T = K . Q^T: lane (grp, j) gets keys 16 mt + 4 grp + r of column j.
     f32x4_t S[4];
 #pragma unroll
@@ -508,7 +516,6 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
         }
       }
     } else {
-      const float wv = cvalid ? bf16_to_f32(it_w[ii * 8 + gcol]) : 0.f;
       // Excluded keys -> -inf in place.  Key 63 (the landmark slot, the
       // usual only exclusion) is S[3][3] of lane group 3; other excluded
       // keys take the per-bit path.
@@ -562,18 +569,13 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       }
       if constexpr (LAST) load_v(vb, frs, flo, (uint32_t)cn * kFragBytes);
       // Add into the owners' rows: column 4 grp + r is owner r & 1, head
-      // 2 grp + (r >> 1); padding columns add into the sink row.
-      const int qa = __builtin_amdgcn_readfirstlane(it_q[i0 + 2 * t]);
-      const bool hb = 2 * t + 1 < n;
-      const int qb = hb ? __builtin_amdgcn_readfirstlane(it_q[i0 + 2 * t + 1]) : qa;
-      const uint32_t want = (1u << qa) | (hb ? 1u << qb : 0u);
+      // 2 grp + (r >> 1) (padding heads add zeros into padding rows); a
+      // missing second owner adds into the spare slot.
+      const int qb = hb ? qb1 : sinkq;
+      const uint32_t want = (1u << qa) | (hb ? 1u << qb1 : 0u);
       float* row[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int g = 2 * grp + (r >> 1);
-        const bool ok = 2 * t + (r & 1) < n && g < G;
-        row[r] = O + (ok ? ((r & 1) ? qb : qa) * G + g : sink) * 128 + 4 * j;
-      }
+      for (int r = 0; r < 4; ++r) row[r] = orow + ((r & 1) ? qb : qa) * 1024 + (r >> 1) * 128;
       bool locked = false;
       for (int spin = 0; spin < a.spin_limit; ++spin) {
         uint32_t old = 0u;
@@ -627,9 +629,10 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     i0 = __builtin_amdgcn_readfirstlane(s_off[st]);
     n = __builtin_amdgcn_readfirstlane(s_off[st + 1]) - i0;
     msk = uniform64(s_excl[st]);
+    // the order of the prefetches at a step's end: Q, K, then V
+    load_q(Qb, qrs, qoff(i0 + min(own, n - 1), own < n && gcol < G));
     load_k(kb, frs, flo, (uint32_t)c * kFragBytes);
     if constexpr (!TOKEN) load_v(vb, frs, flo, (uint32_t)c * kFragBytes);
-    load_q(Qb, qrs, qoff(i0 + min(own, n - 1), own < n && gcol < G));
     while (true) {
       const int nst = st + kWaves;
       more = nst < st_hi;
@@ -662,7 +665,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       const int qq = rho / G, g = rho - qq * G;
       // d = 8 u + i = 16 nt + j: nt = u >> 1, j = 8 (u & 1) + i
       const int nt = u >> 1, j0 = 8 * (u & 1);
-      const float* src = O + rho * 128 + 64 * (nt >> 2) + 4 * j0 + (nt & 3);
+      const float* src = O + (qq * 8 + g) * 128 + 64 * (nt >> 2) + 4 * j0 + (nt & 3);
       float x[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) x[i] = src[4 * i];
