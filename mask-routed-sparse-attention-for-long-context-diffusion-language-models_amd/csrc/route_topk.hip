@@ -12,17 +12,13 @@
 // selection score go to the lower chunk index (the rule of the reference's
 // fused selection kernel, topk_head_softmax.py:614-626).
 //
-// Fast path (route_topk_mfma_kernel): head_dim 128, chunks <= 256, bf16
-// scores.  A workgroup holds 64 queries of one KV head (16 per wave).  For
-// each query head g the landmark keys of that head are staged in LDS and the
-// 16x256 logit tile of every wave is computed on the matrix cores, reduced to
-// the head's LSE and folded into the running max over heads.  The logits of
-// The 32nd-largest score of each row is found by bisection on
-// order-preserving integer keys; exact ties at the threshold are broken by
-// chunk index.  The returned raw scores of the picks come either from a
-// second pass that recomputes every head's logits, or (with a caller
-// workspace) from the bf16 raw scores pass 1 writes to HBM, gathered back at
-// the picks after the selection.
+// Fast path (route_topk_fast_kernel): head_dim 128, chunks <= 256, bf16
+// scores, 7 or 8 heads per KV group, no workspace.  A workgroup holds 128
+// queries of one KV head (16 per wave); pass 1 computes every head's logits
+// on the matrix cores and folds them into the running max over heads, the
+// K-th largest score of each query is found by bisection on order-preserving
+// integer keys (exact ties at the threshold broken by chunk index), and
+// pass 2 recomputes the logits for the picks' raw scores.
 //
 // Short-block path (route_logits_kernel + route_select_kernel, with a caller
 // workspace): logits of few query rows against up to 4096 chunks on the
@@ -85,208 +81,119 @@ __device__ __forceinline__ const uint16_t* lmk_row(const RouteArgs& a, int64_t b
 
 // ---------------------------------------------------------------------------
 // Fast path.
+//
+// A workgroup takes 128 queries of one KV head, 16 per wave; a wave keeps
+// its queries' running max over heads M for all 256 chunks in registers.
+// Logits are computed transposed, S^T = lmk . q^T (16 chunks x 16 queries
+// per matrix product): lane (j, grp) holds query j's chunks 16 t + 4 grp + i
+// (t = 0..15, i = 0..3), so every per-query reduction runs over the four
+// lanes sharing j.
+//   pass 1, heads 0..G-1: x = s * scale + bias, the head's LSE over all
+//           chunks, M = max(M, x - logaddexp(local LSE, LSE));
+//   selection: the K-th largest M per query by bisection on order keys
+//           (ties at the threshold to the lower chunk), the ascending pick
+//           list of each query in LDS;
+//   pass 2, heads G-1..0: the raw logits again, rounded to bf16 into the
+//           wave's [16][256] LDS tile, gathered at the picks.
+// One head's landmark keys sit in LDS while the next head's stream in.
 // ---------------------------------------------------------------------------
-constexpr int kFastThreads = 512;  // 8 waves: 4 query groups x 2 chunk halves
-constexpr int kFastQ = 64;         // queries per workgroup
-constexpr int kNT = 8;             // chunk tiles of 16 per wave (128 chunks)
+constexpr int kFastThreads = 512;  // 8 waves x 16 queries
+constexpr int kFastQ = 128;        // queries per workgroup
 constexpr int kFastMaxTopk = 64;
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// LDS carve-up.  Two buffers of one head's landmark keys ([256][128] bf16,
-// 16-byte parts XOR-swizzled: part p of row c at unit c*16 + (p ^ (c & 15)))
-// and two of its bias row alternate, so the next head streams in while the
-// current one is computed.  The selection scores ([64][256] f32) reuse the
-// buffer of the last first-pass head.
+// LDS carve-up.  Two landmark buffers ([256][128] bf16, 16-byte parts
+// XOR-swizzled: part p of row c at unit 16 c + (p ^ (c & 15))); in pass 2
+// the one pass 1 ends off holds the waves' raw-logit tiles.  Two bias rows
+// (-inf past C), the chunk flags and the pick lists [128][K] int16.
 struct FastLayout {
-  static constexpr size_t lmk = 0;                      // [2][256][128] bf16
-  static constexpr size_t bias = 2 * 256 * 128 * 2;     // [2][256] f32
-  static constexpr size_t cbad = bias + 2 * 256 * 4;    // [256] u8
-  static constexpr size_t red_max = cbad + 256;         // [2][64] f32
-  static constexpr size_t red_sum = red_max + 2 * 64 * 4;
-  static constexpr size_t lse = red_sum + 2 * 64 * 4;  // [2][64] f32 local LSE rows
-  static constexpr size_t slot = lse + 2 * 64 * 4;      // [64][256] i8
-  static constexpr size_t ntot = slot + 64 * 256;        // [64] i32 picks per row
-  static constexpr size_t sc = ntot + 64 * 4;            // [64][K] bf16, one head's picks
-  static size_t total(int K) { return sc + (size_t)64 * K * 2; }
+  static constexpr size_t lmk = 0;                    // [2][256][128] bf16
+  static constexpr size_t bias = 2 * 256 * 128 * 2;   // [2][256] f32
+  static constexpr size_t cbad = bias + 2 * 256 * 4;  // [256] u8
+  static constexpr size_t picks = cbad + 256;         // [128][K] i16
+  static size_t total(int K) { return picks + (size_t)kFastQ * K * 2; }
 };
 
-// Selection of the fast path.  The max-over-heads scores M go to LDS
-// (row-major [64][256] f32, in the landmark buffer `ms_buf`), then wave w
-// selects rows 8w..8w+7 with eight lanes per row, each lane owning the 32
-// consecutive chunks 32*sub .. 32*sub+31: bisection on order-preserving keys
-// for the K-th largest score, exact ties at the threshold broken toward the
-// lower chunk index.  Writes the slot table (chunk -> list position or -1)
-// the indices, the picks' chunks in list order (pick_s [64][K], when not
-// null) and the per-row pick counts; slots past the picks get index -1
-// (their scores are written as -inf by the emission of the scores).
-template <int G>
-__device__ __forceinline__ void select_step(const RouteArgs& a, const float (&M)[kNT][4],
-                                            uint16_t* ms_buf, const unsigned char* cbad,
-                                            int8_t* slot_s, int* ntot_s, int16_t* pick_s,
-                                            int64_t q0, int64_t qbase, int64_t L,
-                                            int64_t C, int h, int64_t b, int lane, int wave,
-                                            int col, int grp, int qg, int cbase) {
-  const int K = a.K;
-  float* Ms = reinterpret_cast<float*>(ms_buf);
-  __syncthreads();  // every wave is done with the landmark keys in ms_buf
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t r = qbase + 4 * grp + i;
-    int64_t lc = 0, rc = -1;
-    if (a.derive_window >= 0 && r < L) {
-      lc = max(r - a.derive_window, (int64_t)0) / a.block_size;
-      rc = min(r + a.derive_window, L - 1) / a.block_size;
-    }
-#pragma unroll
-    for (int t = 0; t < kNT; ++t) {
-      const int c = cbase + 16 * t + col;
-      bool dropped = (c >= C) || (r >= L);
-      if (!dropped) {
-        if (a.derive_window >= 0)
-          dropped = (c >= lc && c <= rc) || cbad[c];
-        else if (a.drop)
-          dropped = a.drop[(b * L + r) * C + c] != 0;
-      }
-      Ms[(16 * qg + 4 * grp + i) * 256 + c] = dropped ? neg_inf() : M[t][i];
-    }
-  }
-  __syncthreads();
-
-  const int row = 8 * wave + (lane >> 3);
-  const int sub = lane & 7;
-  const int64_t r = q0 + row;
-  uint32_t key[32];
-#pragma unroll
-  for (int e = 0; e < 32; e += 4) {
-    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(Ms + row * 256 + 32 * sub + e);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) key[e + u] = float_order_key(v[u]);
-  }
-  const uint32_t kNeg = float_order_key(neg_inf());
-  int nfin = 0;
-  uint32_t kmin = 0xffffffffu, kmax = 0u;
-#pragma unroll
-  for (int e = 0; e < 32; ++e)
-    if (key[e] > kNeg) {
-      ++nfin;
-      kmin = min(kmin, key[e]);
-      kmax = max(kmax, key[e]);
-    }
-  nfin = group8_sum_i(nfin);
-  kmin = group8_min_u(kmin);
-  kmax = group8_max_u(kmax);
-  uint32_t thr_hi, thr_tie = 0u, lo = kmin, hi = kmax + 1u;
-  int need = 0;
-  bool done;
-  if (nfin <= K) {
-    thr_hi = kNeg + 1u;
-    done = true;
-  } else {
-    thr_hi = 0u;
-    done = false;
-  }
-  for (int it = 0; it < 40; ++it) {
-    if (!__any(!done)) break;
-    const uint32_t mid = lo + ((hi - lo) >> 1);
-    int cnt = 0;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) cnt += key[e] >= mid ? 1 : 0;
-    cnt = group8_sum_i(cnt);
-    if (!done) {
-      if (hi - lo <= 1u) {
-        done = true;
-      } else if (cnt == K) {
-        thr_hi = mid;
-        done = true;
-      } else if (cnt > K) {
-        lo = mid;
-      } else {
-        hi = mid;
-      }
-    }
-  }
-  if (thr_hi == 0u) {
-    int cnt_hi = 0;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) cnt_hi += key[e] >= hi ? 1 : 0;
-    cnt_hi = group8_sum_i(cnt_hi);
-    thr_hi = hi;
-    thr_tie = lo;
-    need = K - cnt_hi;
-  }
-  // Exclusive prefix over the 8 lanes of the row (chunk order == lane order).
-  auto excl8 = [&](int v) { return group8_excl_scan_i(v, sub); };
-  int my_ties = 0;
-#pragma unroll
-  for (int e = 0; e < 32; ++e) my_ties += (need > 0 && key[e] == thr_tie) ? 1 : 0;
-  int tie_rank = excl8(my_ties);
-  int my_picks = 0;
-  uint32_t pickbits = 0u;
-#pragma unroll
-  for (int e = 0; e < 32; ++e) {
-    const bool tie = need > 0 && key[e] == thr_tie;
-    const bool pick = key[e] >= thr_hi || (tie && tie_rank < need);
-    if (tie) ++tie_rank;
-    if (pick) {
-      pickbits |= 1u << e;
-      ++my_picks;
-    }
-  }
-  int slot = excl8(my_picks);
-  int total = my_picks;
-  total = group8_sum_i(total);
-  const int64_t orow = (b * L + r) * a.Hkv + h;
-#pragma unroll
-  for (int e = 0; e < 32; ++e) {
-    const bool pick = (pickbits >> e) & 1u;
-    slot_s[row * 256 + 32 * sub + e] = pick ? (int8_t)slot : (int8_t)-1;
-    if (pick && r < L) a.indices[orow * K + slot] = 32 * sub + e;
-    if (pick_s && pick) pick_s[row * K + slot] = (int16_t)(32 * sub + e);
-    slot += pick ? 1 : 0;
-  }
-  if (r < L)
-    for (int s = total + sub; s < K; s += 8) a.indices[orow * K + s] = -1;
-  if (sub == 0) ntot_s[row] = total;
+__device__ __forceinline__ int across4_sum_i(int v) {
+  const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+  const int s = (int)r[0] + (int)r[1];
+  const auto q = __builtin_amdgcn_permlane16_swap((uint32_t)s, (uint32_t)s, false, false);
+  return (int)q[0] + (int)q[1];
+}
+__device__ __forceinline__ uint32_t across4_min_u(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  const uint32_t s = min((uint32_t)r[0], (uint32_t)r[1]);
+  const auto q = __builtin_amdgcn_permlane16_swap(s, s, false, false);
+  return min((uint32_t)q[0], (uint32_t)q[1]);
+}
+__device__ __forceinline__ uint32_t across4_max_u(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  const uint32_t s = max((uint32_t)r[0], (uint32_t)r[1]);
+  const auto q = __builtin_amdgcn_permlane16_swap(s, s, false, false);
+  return max((uint32_t)q[0], (uint32_t)q[1]);
 }
 
-template <int G, bool WS>
-__global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteArgs a,
-                                                                         uint16_t* __restrict__ raw_ws) {
+// Position of chunk 16 t + 4 grp + i among the set bits of a query's four
+// per-lane masks (bit 4 t + i of lane group grp'): the bits of all groups in
+// tiles before t, of lower groups in tile t, and of lower i in this group.
+__device__ __forceinline__ int chunk_rank(const uint64_t (&m)[4], int grp, int t, int i) {
+  const uint64_t below = (1ull << (4 * t)) - 1ull;
+  int r = 0;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    r += __popcll(m[g] & below);
+    const int nib = (int)((m[g] >> (4 * t)) & 15u);
+    r += g < grp ? __popc(nib) : (g == grp ? __popc(nib & ((1 << i) - 1)) : 0);
+  }
+  return r;
+}
+
+template <int G>
+__global__ void __launch_bounds__(kFastThreads, 1) route_topk_fast_kernel(RouteArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int K = a.K;
   float* bias_s = reinterpret_cast<float*>(smem + FastLayout::bias);
   unsigned char* cbad = smem + FastLayout::cbad;
-  float* red_max = reinterpret_cast<float*>(smem + FastLayout::red_max);
-  float* red_sum = reinterpret_cast<float*>(smem + FastLayout::red_sum);
-  float* lse_s = reinterpret_cast<float*>(smem + FastLayout::lse);
-  int8_t* slot_s = reinterpret_cast<int8_t*>(smem + FastLayout::slot);
-  int* ntot_s = reinterpret_cast<int*>(smem + FastLayout::ntot);
-  uint16_t* sc_s = reinterpret_cast<uint16_t*>(smem + FastLayout::sc);
-  auto lmk_buf = [&](int i) { return reinterpret_cast<uint16_t*>(smem + FastLayout::lmk) + i * 256 * 128; };
+  int16_t* picks = reinterpret_cast<int16_t*>(smem + FastLayout::picks);
+  auto lmk_buf = [&](int i) {
+    return reinterpret_cast<uint16_t*>(smem + FastLayout::lmk) + i * 256 * 128;
+  };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int col = lane & 15, grp = lane >> 4;
-  const int qg = wave & 3, half = wave >> 2;
+  const int j = lane & 15, grp = lane >> 4;
   const int64_t b = blockIdx.z;
   const int h = blockIdx.y;
-  const int64_t q0 = (int64_t)blockIdx.x * kFastQ;
-  const int64_t qbase = q0 + 16 * qg;
-  const int64_t qa = qbase + col;  // the A-operand row this lane supplies
   const int64_t L = a.L, C = a.C;
-  const int cbase = 128 * half;
-  const uint16_t* qb_base = a.q + b * L * (int64_t)(a.Hkv * G * 128);
-  const float* lse_base = a.pre_softmax ? nullptr : a.lse + b * L * (int64_t)(a.Hkv * G);
-  uint16_t* sc16 = reinterpret_cast<uint16_t*>(a.scores);
+  const int64_t q0 = (int64_t)blockIdx.x * kFastQ;
+  const int ql = 16 * wave + j;            // this lane's query within the workgroup
+  const int64_t r = q0 + ql;
+  const bool rvalid = r < L;
+  const int64_t rr = rvalid ? r : L - 1;   // rows past L re-read row L - 1
+  const int64_t qrow = ((b * L + rr) * a.Hkv + h) * G;  // (row, head 0) of q, lse
 
+  // Chunks with no valid real key (the last slot of a chunk is its landmark).
   if (a.derive_window >= 0) {
     for (int c = tid; c < 256; c += kFastThreads) {
       bool any = false;
       if (c < C) {
         if (a.key_valid) {
           const uint8_t* kv = a.key_valid + b * L + (int64_t)c * a.block_size;
-          for (int64_t s = 0; s < a.block_size - 1; ++s) any |= kv[s] != 0;
+          if (a.block_size == 64 && ((uintptr_t)kv & 15) == 0) {
+            u32x4_t acc = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const u32x4_t x = *reinterpret_cast<const u32x4_t*>(kv + 16 * v);
+              acc[0] |= x[0];
+              acc[1] |= x[1];
+              acc[2] |= x[2];
+              acc[3] |= v == 3 ? (x[3] & 0x00ffffffu) : x[3];
+            }
+            any = (acc[0] | acc[1] | acc[2] | acc[3]) != 0u;
+          } else {
+            for (int64_t s = 0; s < a.block_size - 1; ++s) any |= kv[s] != 0;
+          }
         } else {
           any = a.block_size > 1;
         }
@@ -294,315 +201,324 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_mfma_kernel(RouteA
       cbad[c] = !any;
     }
   }
-  if (!a.bias)
-    for (int e = tid; e < 512; e += kFastThreads) bias_s[e] = 0.f;
 
-  // The walk is 2G steps: pass 1 over heads 0..G-1 (biased logits, LSE,
-  // running max), then the selection, then pass 2 over heads G-1..0 (raw
-  // logits of the picks).  Step s computes from buffer s & 1.
-  auto head_of = [&](int s) { return s < G ? s : 2 * G - 1 - s; };
-  // Global->LDS DMA of head g's landmark keys into buffer i: wave w,
-  // instruction j moves units (8w + j) * 64 + lane = row 4(8w + j) + lane / 16,
+  // Head g's landmark keys into buffer i, instruction k (0..7) of this wave:
+  // LDS units (8 wave + k) * 64 + lane = row 4 (8 wave + k) + lane / 16,
   // stored part lane & 15 (global part (lane & 15) ^ (row & 15)).  Rows >= C
-  // re-read row C - 1; their logits are masked to -inf.  Wave 0 also moves
-  // the bias row (4-byte units, rows >= C re-read row C - 1 and are unused).
-  // Instruction j (0..7) of the staging of head g into buffer i; j = 0
-  // also moves the local LSE rows (wave 1) and the bias row (wave 0).
-  auto stage_part = [&](int g, int i, int j, bool with_lse) {
-    uint16_t* dst = lmk_buf(i);
-    if (j == 0 && with_lse && lse_base && wave == 1) {
-      // Local LSE of the tile's 64 rows for head g (rows >= L re-read L - 1).
-      const int64_t r = min(q0 + lane, L - 1);
-      __builtin_amdgcn_global_load_lds(lse_base + (r * a.Hkv + h) * G + g,
-                                       (lds_void_t*)(lse_s + 64 * i), 4, 0, 0);
-    }
-    const int row = 4 * (8 * wave + j) + (lane >> 4);
+  // re-read row C - 1; their logits are masked by the bias row.
+  auto stage_part = [&](int g, int i, int k) {
+    const int row = 4 * (8 * wave + k) + (lane >> 4);
     const int part = (lane & 15) ^ (row & 15);
     const int64_t c = min((int64_t)row, C - 1);
     __builtin_amdgcn_global_load_lds(lmk_row(a, b, c, h, g) + part * 8,
-                                     (lds_void_t*)(dst + (8 * wave + j) * 512), 16, 0, 0);
-    if (j == 0 && a.bias && wave == 0) {
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb) {
-        const int64_t cb = min((int64_t)(64 * jb + lane), C - 1);
-        __builtin_amdgcn_global_load_lds(a.bias + ((b * C + cb) * a.Hkv + h) * G + g,
-                                         (lds_void_t*)(bias_s + 256 * i + 64 * jb), 4, 0, 0);
-      }
-    }
+                                     (lds_void_t*)(lmk_buf(i) + (8 * wave + k) * 512), 16, 0, 0);
   };
-  auto stage = [&](int g, int i, bool with_lse) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) stage_part(g, i, j, with_lse);
+  // Bias of chunk tid for head g (-inf past C), loaded ahead of its LDS write.
+  auto bias_of = [&](int g) {
+    float v = neg_inf();
+    if (tid < C) v = a.bias ? a.bias[((b * C + tid) * a.Hkv + h) * G + g] : 0.f;
+    return v;
   };
-  auto load_q = [&](int g, u32x4_t (&A)[4]) {
-    const uint16_t* qrow = qb_base + (uint32_t)((((int)qa * a.Hkv + h) * G + g) * 128 + 8 * grp);
+  // This lane's Q^T operand (query j, dims 32 ks + 8 grp ..) of head g.
+  auto load_q = [&](int g, u32x4_t (&Q)[4]) {
+    const uint16_t* src = a.q + (qrow + g) * 128 + 8 * grp;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      u32x4_t z = {0u, 0u, 0u, 0u};
-      A[j] = z;
-      if (qa < L) A[j] = *reinterpret_cast<const u32x4_t*>(qrow + 32 * j);
-    }
-  };
-  // S[t] = q_g (16 queries of this wave) . lmk (16 chunks of tile t).
-  // The next head's staging is issued one instruction per tile, between the
-  // products, so no wave stalls on a burst of DMA issue.
-  // S[t] = q (16 rows) . lmk (16 chunks of tile t); with TRANSPOSED the same
-  // operands give S^T: lane l holds query l % 16, chunks 16t + 4(l / 16) + i.
-  auto logits = [&](auto transposed, const uint16_t* lmk_s, const u32x4_t (&A)[4],
-                    f32x4_t (&S)[kNT], int next_g, int next_buf, bool with_lse) {
-#pragma unroll
-    for (int t = 0; t < kNT; ++t) {
-      f32x4_t acc = zero4();
-      const uint16_t* brow = lmk_s + (cbase + 16 * t + col) * 128;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const u32x4_t B = *reinterpret_cast<const u32x4_t*>(brow + (((4 * j + grp) ^ col) * 8));
-        if constexpr (decltype(transposed)::value)
-          acc = mfma_bf16_16x16x32(B, A[j], acc);
-        else
-          acc = mfma_bf16_16x16x32(A[j], B, acc);
-      }
-      S[t] = acc;
-      if (next_g >= 0) stage_part(next_g, next_buf, t, with_lse);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    for (int ks = 0; ks < 4; ++ks) Q[ks] = *reinterpret_cast<const u32x4_t*>(src + 32 * ks);
   };
 
-  float M[kNT][4];
+  // ---- pass 1 -------------------------------------------------------------
+  float M[16][4];
 #pragma unroll
-  for (int t = 0; t < kNT; ++t)
+  for (int t = 0; t < 16; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) M[t][i] = neg_inf();
-
-  u32x4_t Acur[4], Anext[4];
-  // Step prologue: head s landed (this wave's DMA and loads) and every wave
-  // is done with the other buffer; then queue step s + 1's q operands.  Its
-  // DMA follows inside the step's logits; nothing inside the step waits on
-  // vector memory, so the prefetch is never drained early.
-  auto begin_step = [&](int s, bool load_next_q) {
+    for (int e = 0; e < 4; ++e) M[t][e] = neg_inf();
+  u32x4_t Qc[4], Qn[4];
+  float lse_c = 0.f, lse_n = 0.f;
+  load_q(0, Qc);
+  if (!a.pre_softmax) lse_c = a.lse[qrow];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) stage_part(0, 0, k);
+  if (tid < 256) bias_s[tid] = bias_of(0);
+  for (int g = 0; g < G; ++g) {
+    // Head g landed (this wave's DMA; the barrier covers the others') and
+    // every wave is done with the other buffer.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (s + 1 < 2 * G && load_next_q) load_q(head_of(s + 1), Anext);
-  };
-  // Logits of step s, staging step s + 1's head meanwhile.
-  constexpr int kSteps = WS ? G : 2 * G;
-  auto step_logits = [&](auto transposed, int s, f32x4_t (&S)[kNT]) {
-    const bool more = s + 1 < kSteps;
-    logits(transposed, lmk_buf(s & 1), Acur, S, more ? head_of(s + 1) : -1, (s + 1) & 1,
-           s + 1 < G);
-  };
-  // Pass-1 q tiles travel by DMA through the slot table's space (unused
-  // until the selection): [64 rows][16 parts] of 16 bytes, part p of row r at
-  // unit r * 16 + (p ^ (r & 15)); rows >= L re-read row L - 1 (their rows are
-  // dropped).  Wave w moves units (2w + k) * 64 + lane, k = 0, 1.
-  uint16_t* qstage = reinterpret_cast<uint16_t*>(slot_s);
-  auto stage_q = [&](int g) {
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int row = 4 * (2 * wave + k) + (lane >> 4);
-      const int part = (lane & 15) ^ (row & 15);
-      const int64_t r = min(q0 + row, L - 1);
-      __builtin_amdgcn_global_load_lds(qb_base + ((r * a.Hkv + h) * G + g) * 128 + part * 8,
-                                       (lds_void_t*)(qstage + (2 * wave + k) * 512), 16, 0, 0);
+    const bool more = g + 1 < G;
+    float bnext = 0.f;
+    if (more) {
+      load_q(g + 1, Qn);
+      if (!a.pre_softmax) lse_n = a.lse[qrow + g + 1];
+      if (tid < 256) bnext = bias_of(g + 1);
     }
-  };
-  stage_q(0);
-  stage(0, 0, true);
-
-  // Raw scores bf16(s * sm_scale) of the previous head (WS), two rows per
-  // register: Rp[t][p] holds rows 4grp + 2p, 4grp + 2p + 1 of chunk
-  // cbase + 16t + col.  They are stored one step late, after the step's
-  // vmcnt wait, so that the next wait (which covers stores too) finds them
-  // long completed instead of stalling on their write latency.
-  uint32_t Rp[kNT][2];
-  // raw_ws [B][L][Hkv][G][C]: 16 lanes of a row cover 16 consecutive chunks
-  // (2-byte stores; a quad transpose to 8-byte row stores measured slower).
-  auto store_raw = [&](int gprev) {
+    // x = s * scale + bias (bias -inf past C), tile by tile after its
+    // products, with the running max for the LSE.
+    f32x4_t S[16];
+    float mx = neg_inf();
+    {
+      const uint16_t* lmk_s = lmk_buf(g & 1);
+      const float* brow = bias_s + 256 * (g & 1) + 4 * grp;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t r = qbase + 4 * grp + i;
-      if (r < L) {
-        uint16_t* wrow = raw_ws + (((b * L + r) * a.Hkv + h) * G + gprev) * C;
+      for (int t = 0; t < 16; ++t) {
+        f32x4_t acc = zero4();
+        const uint16_t* arow = lmk_s + (16 * t + j) * 128;
 #pragma unroll
-        for (int t = 0; t < kNT; ++t) {
-          const int c = cbase + 16 * t + col;
-          const uint32_t w = Rp[t][i >> 1];
-          if (c < C) wrow[c] = (uint16_t)((i & 1) ? (w >> 16) : (w & 0xffffu));
+        for (int ks = 0; ks < 4; ++ks) {
+          const u32x4_t A =
+              *reinterpret_cast<const u32x4_t*>(arow + (((4 * ks + grp) ^ j) * 8));
+          acc = mfma_bf16_16x16x32(A, Qc[ks], acc);
         }
+        if (more && (t & 1)) stage_part(g + 1, (g + 1) & 1, t >> 1);
+        const f32x4_t bv = *reinterpret_cast<const f32x4_t*>(brow + 16 * t);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S[t][e] = __builtin_fmaf(acc[e], a.sm_scale, bv[e]);
+        mx = max3_raw(mx, max_raw(S[t][0], S[t][1]), max_raw(S[t][2], S[t][3]));
       }
     }
-  };
-
-  // Pass 1: biased logits, LSE over all chunks, running max over heads.
-  for (int s = 0; s < G; ++s) {
-    const int g = s;
-    begin_step(s, false);
-    if constexpr (WS) {
-      if (s > 0) store_raw(s - 1);
+    // LSE over all chunks in base 2 with the hardware exp2 / log2.
+    const float m2 = across4_max(mx) * kLog2e;
+    float sm = 0.f;
+    if (m2 != neg_inf()) {
+      float p[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 16; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p[e] += exp2_hw(__builtin_fmaf(S[t][e], kLog2e, -m2));
+      sm = (p[0] + p[1]) + (p[2] + p[3]);
     }
-    // This lane's A operand rows: query 16qg + col (row & 15 == col).
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      Acur[j] = *reinterpret_cast<const u32x4_t*>(
-          qstage + ((16 * qg + col) * 16 + ((4 * j + grp) ^ col)) * 8);
-    f32x4_t S[kNT];
-    step_logits(std::false_type{}, s, S);
-    if constexpr (WS) {
-#pragma unroll
-      for (int t = 0; t < kNT; ++t) {
-        Rp[t][0] = pack_bf16x2(S[t][0] * a.sm_scale, S[t][1] * a.sm_scale);
-        Rp[t][1] = pack_bf16x2(S[t][2] * a.sm_scale, S[t][3] * a.sm_scale);
-      }
+    const float s2 = across4_sum(sm);
+    const float lse2 = m2 == neg_inf() ? neg_inf() : m2 + log2_hw(s2);
+    float tot = 0.f;
+    if (!a.pre_softmax) {
+      // logaddexp(local LSE, LSE) in base 2, back to natural units.  A -inf
+      // total (no visible logit at all) is clamped to -FLT_MAX: finite x - tot
+      // then ties at the top like x - (-inf) = +inf would, and -inf stays.
+      const float lv2 = lse_c * kLog2e;
+      const float hi = fmaxf(lv2, lse2), lo = fminf(lv2, lse2);
+      tot = hi == neg_inf() ? -__FLT_MAX__ : (hi + log2_hw(1.f + exp2_hw(lo - hi))) * kLn2;
     }
-    const float* bias_g = bias_s + 256 * (s & 1);
-    // x = s * scale + bias, -inf past C.
 #pragma unroll
-    for (int t = 0; t < kNT; ++t) {
-      const int c = cbase + 16 * t + col;
-      const float bv = c < C ? bias_g[c] : neg_inf();
+    for (int t = 0; t < 16; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) S[t][i] = __builtin_fmaf(S[t][i], a.sm_scale, bv);
-    }
-    float rmax[4];
+      for (int e = 0; e < 4; ++e) M[t][e] = max_raw(M[t][e], S[t][e] - tot);
+    if (more) {
+      if (tid < 256) bias_s[256 * ((g + 1) & 1) + tid] = bnext;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      rmax[i] = max_raw(max3_raw(max3_raw(S[0][i], S[1][i], S[2][i]), S[3][i], S[4][i]),
-                        max3_raw(S[5][i], S[6][i], S[7][i]));
-    // Row LSE over both chunk halves, in base 2 with the hardware exp2/log2:
-    // each half reduces (max, sum of exp2) over its 128 chunks; one LDS
-    // exchange combines them with a rescale.
-    float m2[4], s2[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      m2[i] = group16_max(rmax[i]) * kLog2e;
-      float sm = 0.f;
-      if (m2[i] != neg_inf()) {
-#pragma unroll
-        for (int t = 0; t < kNT; ++t) sm += exp2_hw(__builtin_fmaf(S[t][i], kLog2e, -m2[i]));
-      }
-      s2[i] = group16_sum(sm);
-      if (col == 0) {
-        const int row = 16 * qg + 4 * grp + i;
-        red_max[half * 64 + row] = m2[i];
-        red_sum[half * 64 + row] = s2[i];
-      }
-    }
-    __syncthreads();
-    // Every wave has read this head's q tile: stage the next one.
-    if (s + 1 < G) stage_q(s + 1);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t r = qbase + 4 * grp + i;
-      const int row = 16 * qg + 4 * grp + i;
-      const float ma = red_max[row], mb = red_max[64 + row];
-      const float mm = fmaxf(ma, mb);
-      float lse2 = neg_inf();  // log2 sum_c 2^(x_c log2 e)
-      if (mm != neg_inf())
-        lse2 = mm + log2_hw((ma == neg_inf() ? 0.f : red_sum[row] * exp2_hw(ma - mm)) +
-                            (mb == neg_inf() ? 0.f : red_sum[64 + row] * exp2_hw(mb - mm)));
-      float tot = 0.f;
-      if (!a.pre_softmax) {
-        // logaddexp(local_lse, lse) in base 2, back to natural units.  A -inf
-        // total (no visible logit at all) is clamped to -FLT_MAX: finite x - tot
-        // then ties at the top like x - (-inf) = +inf would, and -inf stays.
-        const float lv2 = r < L ? lse_s[64 * (s & 1) + row] * kLog2e : 0.f;
-        const float hi = fmaxf(lv2, lse2), lo = fminf(lv2, lse2);
-        tot = hi == neg_inf() ? -__FLT_MAX__ : (hi + log2_hw(1.f + exp2_hw(lo - hi))) * kLn2;
-      }
-#pragma unroll
-      for (int t = 0; t < kNT; ++t) M[t][i] = max_raw(M[t][i], S[t][i] - tot);
+      for (int ks = 0; ks < 4; ++ks) Qc[ks] = Qn[ks];
+      lse_c = lse_n;
     }
   }
 
-  if constexpr (WS) store_raw(G - 1);
-  int16_t* pick_s = WS ? reinterpret_cast<int16_t*>(lmk_buf(G & 1)) : nullptr;  // [64][K]
-  select_step<G>(a, M, lmk_buf((G - 1) & 1), cbad, slot_s, ntot_s, pick_s, q0, qbase, L, C, h, b,
-                 lane, wave, col, grp, qg, cbase);
-  if constexpr (WS) {
-    // Picks of every head from the workspace, gathered straight into the
-    // [G][K] score rows: wave w emits rows 8w..8w+7, lane l value
-    // e = 64 it + l (head e / K, slot e % K) of each row, with the reads of
-    // all eight rows in flight before any is used.  All waves of the
-    // workgroup share one CU (one L1): the barrier's workgroup-scope fence
-    // (vmcnt(0) on the stores) makes every wave's raw scores visible to the
-    // others.
-    __syncthreads();  // pick lists and counts of every row, raw scores stored
-    constexpr int kIt = (8 * kFastMaxTopk + 63) / 64;  // G * K <= 8 * 64 values per row
-    const int gk = G * K;
-    const int nit = (gk + 63) / 64;
-    // Head and slot of value e of a row; es = K (never < a pick count) marks
-    // e >= G * K, so the last partial iteration reads nothing past the row.
-    int eg[kIt], es[kIt];
+  // ---- selection ----------------------------------------------------------
+  // Order keys of M (dropped chunks and chunks >= C: -inf).
+  const uint32_t kNeg = float_order_key(neg_inf());
+  // One uniform branch per drop source; straight-line code per element.
+  uint32_t key[16][4];
+  if (a.derive_window >= 0) {
+    const int lc = (int)(max(rr - a.derive_window, (int64_t)0) / a.block_size);
+    const int rc = (int)(min(rr + a.derive_window, L - 1) / a.block_size);
 #pragma unroll
-    for (int it = 0; it < kIt; ++it) {
-      const int e = 64 * it + lane;
-      eg[it] = e < gk ? e / K : 0;
-      es[it] = e < gk ? e - eg[it] * K : K;
-    }
-    const int64_t rstride = (int64_t)a.Hkv * G * C, ostride = (int64_t)a.Hkv * gk;
-    const uint16_t* rbase = raw_ws + ((b * L + q0) * a.Hkv + h) * (int64_t)G * C;
-    uint16_t* obase = sc16 + ((b * L + q0) * a.Hkv + h) * (int64_t)gk;
-    for (int it0 = 0; it0 < nit; it0 += 2) {
-      uint16_t v[8][2];
+    for (int t = 0; t < 16; ++t) {
+      const int c0 = 16 * t + 4 * grp;
+      const uint32_t bad4 = *reinterpret_cast<const uint32_t*>(cbad + c0);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int row = 8 * wave + j;
-        const int nt = row < 64 && q0 + row < L ? ntot_s[row] : 0;
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int it = it0 + u;
-          v[j][u] = 0xff80u;  // -inf past the picks
-          if (it < nit && es[it] < nt)  // es < nt <= K implies e < G * K
-            v[j][u] = rbase[row * rstride + eg[it] * C + pick_s[row * K + es[it]]];
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int row = 8 * wave + j;
-        if (q0 + row >= L) continue;
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int e = 64 * (it0 + u) + lane;
-          if (it0 + u < nit && e < gk) obase[row * ostride + e] = v[j][u];
-        }
+      for (int e = 0; e < 4; ++e) {
+        const int c = c0 + e;
+        const bool dropped =
+            (c >= C) | ((c >= lc) & (c <= rc)) | (((bad4 >> (8 * e)) & 0xffu) != 0u);
+        key[t][e] = dropped ? kNeg : float_order_key(M[t][e]);
       }
     }
-    return;
+  } else if (a.drop) {
+    const int32_t* drow = a.drop + (b * L + rr) * C;
+    if (C == 256 && ((uintptr_t)a.drop & 15) == 0) {
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const u32x4_t d = *reinterpret_cast<const u32x4_t*>(drow + 16 * t + 4 * grp);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) key[t][e] = d[e] != 0u ? kNeg : float_order_key(M[t][e]);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 16; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c = 16 * t + 4 * grp + e;
+          const bool dropped = (c >= C) | (drow[min(c, (int)C - 1)] != 0);
+          key[t][e] = dropped ? kNeg : float_order_key(M[t][e]);
+        }
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 16; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        key[t][e] = 16 * t + 4 * grp + e >= C ? kNeg : float_order_key(M[t][e]);
   }
-  load_q(head_of(G), Acur);
+  int nfin = 0;
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+  for (int t = 0; t < 16; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool fin = key[t][e] > kNeg;
+      nfin += fin ? 1 : 0;
+      kmin = min(kmin, fin ? key[t][e] : 0xffffffffu);
+      kmax = max(kmax, key[t][e]);  // -inf keys are below every finite key
+    }
+  nfin = across4_sum_i(nfin);
+  kmin = across4_min_u(kmin);
+  kmax = across4_max_u(kmax);
+  // Threshold: keys >= thr_hi are picked, plus the first `need` keys equal
+  // to thr_tie in chunk order.  The search keeps count(key >= lo) = clo > K
+  // and count(key >= hi) = chi < K and stops when a probe counts exactly K
+  // (or hi = lo + 1: ties at lo).  Probes interpolate the count linearly in
+  // key space; a probe that leaves more than half the interval is followed
+  // by a bisection step, so the search never takes more than twice the
+  // steps of plain bisection.
+  uint32_t thr_hi, thr_tie = 0u, lo = kmin, hi = kmax + 1u;
+  int clo = nfin, chi = 0;
+  int need = 0;
+  bool done = nfin <= K;
+  thr_hi = done ? kNeg + 1u : 0u;
+  bool bisect = false;
+  for (int it = 0; it < 80; ++it) {
+    if (!done && hi - lo <= 1u) done = true;
+    if (!__any(!done)) break;
+    uint32_t mid = lo + ((hi - lo) >> 1);
+    if (!done && !bisect) {
+      const float f = (float)(clo - K) / (float)(clo - chi);
+      const uint32_t step = (uint32_t)((float)(hi - lo) * f);
+      mid = min(max(lo + step, lo + 1u), hi - 1u);
+    }
+    int cnt = 0;
+#pragma unroll
+    for (int t = 0; t < 16; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cnt += key[t][e] >= mid ? 1 : 0;
+    cnt = across4_sum_i(cnt);
+    if (!done) {
+      const uint32_t width = hi - lo;
+      if (cnt == K) {
+        thr_hi = mid;
+        done = true;
+      } else if (cnt > K) {
+        lo = mid;
+        clo = cnt;
+      } else {
+        hi = mid;
+        chi = cnt;
+      }
+      bisect = !bisect && (hi - lo) > (width >> 1);
+    }
+  }
+  if (thr_hi == 0u) {  // hi = lo + 1: keys >= hi, then ties at lo
+    thr_hi = hi;
+    thr_tie = lo;
+    need = K - chi;
+  }
+  // This lane's picks / ties as bit masks (bit 4 t + e), built per 32-bit half.
+  uint32_t ph[2] = {0u, 0u}, th[2] = {0u, 0u};
+  const uint32_t tie_key = need > 0 ? thr_tie : 0u;  // key 0 is never finite
+#pragma unroll
+  for (int t = 0; t < 16; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int bit = (4 * t + e) & 31;
+      ph[t >> 3] |= (uint32_t)(key[t][e] >= thr_hi) << bit;
+      th[t >> 3] |= (uint32_t)(key[t][e] == tie_key) << bit;
+    }
+  uint64_t pm = ((uint64_t)ph[1] << 32) | ph[0];
+  const uint64_t tm = ((uint64_t)th[1] << 32) | th[0];
+  // The four lanes' masks of this query, in lane-group order.
+  auto gather4 = [&](uint64_t v, uint64_t (&m)[4]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int src = j + 16 * g;
+      const uint32_t lo32 = (uint32_t)__shfl((int)(uint32_t)v, src, 64);
+      const uint32_t hi32 = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src, 64);
+      m[g] = ((uint64_t)hi32 << 32) | lo32;
+    }
+  };
+  if (__any(need > 0)) {
+    // Ties at the threshold: the first `need` in chunk order.
+    uint64_t tall[4];
+    gather4(tm, tall);
+    uint64_t x = tm;
+    while (x) {
+      const int p = __builtin_ctzll(x);
+      x &= x - 1ull;
+      if (chunk_rank(tall, grp, p >> 2, p & 3) < need) pm |= 1ull << p;
+    }
+  }
+  uint64_t pall[4];
+  gather4(pm, pall);
+  const int total = __popcll(pall[0]) + __popcll(pall[1]) + __popcll(pall[2]) + __popcll(pall[3]);
+  int16_t* plist = picks + ql * K;  // this query's ascending pick list
+  {
+    uint64_t x = pm;
+    while (x) {
+      const int p = __builtin_ctzll(x);
+      x &= x - 1ull;
+      plist[chunk_rank(pall, grp, p >> 2, p & 3)] = (int16_t)(16 * (p >> 2) + 4 * grp + (p & 3));
+    }
+  }
+  // The wave's own pick lists are read back below (LDS keeps one wave's
+  // operations in order).
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  int32_t* irow = a.indices + ((b * L + r) * a.Hkv + h) * K;
+  if (rvalid)
+    for (int s = grp; s < K; s += 4) irow[s] = s < total ? (int32_t)plist[s] : -1;
 
-  // Pass 2: raw logit bf16(q.lmk * scale) of every picked chunk, heads G-1..0.
-  // The picks of a head are gathered in list order in an LDS row buffer and
-  // written out as contiguous K-slot row segments.
-  const int nrows = (int)min((int64_t)kFastQ, L - q0);
-  for (int s = G; s < 2 * G; ++s) {
-    const int g = head_of(s);
-    begin_step(s, true);
-    f32x4_t S[kNT];
-    step_logits(std::true_type{}, s, S);
-    // S^T: this lane's row and 4 consecutive chunks per tile; one 4-byte read
-    // of the slot table per tile, most of which hold no pick.
-    const int row = 16 * qg + col;
+  // ---- pass 2 -------------------------------------------------------------
+  // Raw logits bf16(s * scale) of the picks, heads G-1..0.  Pass 1 left head
+  // G-1 in buffer pb; the other buffer holds the waves' tiles: query j's
+  // chunk c at j * 256 + 4 ((c >> 2) ^ j) + (c & 3) (8-byte units swizzled
+  // by query so a tile write touches distinct banks).
+  const int pb = (G - 1) & 1;
+  uint16_t* tile = lmk_buf(1 - pb) + wave * 16 * 256;
+  uint16_t* sc16 = reinterpret_cast<uint16_t*>(a.scores);
+  load_q(G - 1, Qc);
+  for (int g = G - 1; g >= 0; --g) {
+    if (g < G - 1) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();  // head g landed in buffer pb
+    }
+    if (g > 0) load_q(g - 1, Qn);
+    // S^T tile by tile (S[e] = q_j . lmk[16 t + 4 grp + e]) into the LDS tile.
 #pragma unroll
-    for (int t = 0; t < kNT; ++t) {
-      const uint32_t sw =
-          *reinterpret_cast<const uint32_t*>(slot_s + row * 256 + cbase + 16 * t + 4 * grp);
-      if (sw != 0xffffffffu) {
+    for (int t = 0; t < 16; ++t) {
+      f32x4_t acc = zero4();
+      const uint16_t* arow = lmk_buf(pb) + (16 * t + j) * 128;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int slot = (int)(int8_t)(sw >> (8 * i));
-          if (slot >= 0) sc_s[row * K + slot] = (uint16_t)f32_to_bf16(S[t][i] * a.sm_scale);
+      for (int ks = 0; ks < 4; ++ks) {
+        const u32x4_t A = *reinterpret_cast<const u32x4_t*>(arow + (((4 * ks + grp) ^ j) * 8));
+        acc = mfma_bf16_16x16x32(A, Qc[ks], acc);
+      }
+      u32x2_t w;
+      w[0] = pack_bf16x2(acc[0] * a.sm_scale, acc[1] * a.sm_scale);
+      w[1] = pack_bf16x2(acc[2] * a.sm_scale, acc[3] * a.sm_scale);
+      *reinterpret_cast<u32x2_t*>(tile + j * 256 + 4 * ((4 * t + grp) ^ j)) = w;
+    }
+    if (g > 0) {
+      __syncthreads();  // every wave is done with head g's keys
+#pragma unroll
+      for (int k = 0; k < 8; ++k) stage_part(g - 1, pb, k);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (rvalid) {
+      uint16_t* orow = sc16 + (((b * L + r) * a.Hkv + h) * G + g) * K;
+      for (int s = grp; s < K; s += 4) {
+        uint16_t v = 0xff80u;  // -inf past the picks
+        if (s < total) {
+          const int c = plist[s];
+          v = tile[j * 256 + 4 * ((c >> 2) ^ j) + (c & 3)];
         }
+        orow[s] = v;
       }
     }
-    __syncthreads();
-    for (int e = tid; e < nrows * K; e += kFastThreads) {
-      const int row = e / K, slot = e - row * K;
-      sc16[(((b * L + q0 + row) * a.Hkv + h) * G + g) * K + slot] =
-          slot < ntot_s[row] ? sc_s[e] : (uint16_t)0xff80u;  // -inf past the picks
-    }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) Acur[j] = Anext[j];
+    for (int ks = 0; ks < 4; ++ks) Qc[ks] = Qn[ks];
   }
 }
 
@@ -1246,14 +1162,14 @@ int launch_block(const RouteArgs& a, float* raw, hipStream_t s) {
 // raw_ws: bf16 [B][L][Hkv][G][C] raw-score workspace (one pass), or null
 // (a second pass recomputes the picks' raw scores).
 template <int G>
-int launch_fast(const RouteArgs& a, uint16_t* raw_ws, hipStream_t s) {
+int launch_fast(const RouteArgs& a, hipStream_t s) {
   const size_t smem = FastLayout::total(a.K);
-  auto kern = raw_ws ? route_topk_mfma_kernel<G, true> : route_topk_mfma_kernel<G, false>;
+  auto kern = route_topk_fast_kernel<G>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
     return MRSA_ERR_LAUNCH;
   dim3 grid((unsigned)((a.L + kFastQ - 1) / kFastQ), (unsigned)a.Hkv, (unsigned)a.B);
-  hipLaunchKernelGGL(kern, grid, dim3(kFastThreads), smem, s, a, raw_ws);
+  hipLaunchKernelGGL(kern, grid, dim3(kFastThreads), smem, s, a);
   return mrsa_launch_status();
 }
 
@@ -1307,15 +1223,9 @@ int route_topk_dispatch(const void* q, const void* lmk, const float* lse_local, 
 
   const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)lmk % 16 == 0);
   const bool fast = !scores_fp32 && !is_causal && head_dim == 128 &&
-                    seq_len * kv_heads * groups * head_dim < ((int64_t)1 << 31) && chunks <= 256 && topk <= kFastMaxTopk && aligned &&
+                    chunks <= 256 && topk <= kFastMaxTopk && aligned &&
                     (groups == 7 || groups == 8);
-  if (fast) {
-    uint16_t* raw_ws = nullptr;
-    if (workspace && (uintptr_t)workspace % 16 == 0 &&
-        workspace_bytes >= batch * seq_len * kv_heads * groups * chunks * 2)
-      raw_ws = (uint16_t*)workspace;
-    return groups == 7 ? launch_fast<7>(a, raw_ws, s) : launch_fast<8>(a, raw_ws, s);
-  }
+  if (fast) return groups == 7 ? launch_fast<7>(a, s) : launch_fast<8>(a, s);
   const bool block = workspace && head_dim == 128 && groups <= 8 && aligned &&
                      chunks <= (int64_t)kSelThreads * kSelMaxPer && seq_len <= 0x7fffffff &&
                      (uintptr_t)workspace % 16 == 0 &&

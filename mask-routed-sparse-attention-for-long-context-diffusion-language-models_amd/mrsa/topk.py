@@ -29,17 +29,14 @@ def _fast_shape(C, G, D, topk, scores_fp32, is_causal):
 
 def _workspace_bytes(B, L, C, Hkv, G, D, topk, scores_fp32, is_causal):
     """Bytes of the workspace the route kernels take, 0 for none.  The
-    matrix-core kernel (up to 256 chunks) takes a bf16 raw-score workspace
-    [B, L, Hkv, G, C] and then skips the second pass that recomputes the
-    picks' raw scores; beyond 256 chunks, with head_dim 128, groups <= 8 and
-    chunks <= 4096, the two-kernel path runs over an fp32 logits workspace of
-    the same shape."""
+    matrix-core kernel (up to 256 chunks) runs without one; beyond 256
+    chunks, with head_dim 128, groups <= 8 and chunks <= 4096, the two-kernel
+    path runs over an fp32 logits workspace [B, L, Hkv, G, C]."""
     if _fast_shape(C, G, D, topk, scores_fp32, is_causal):
-        n = B * L * Hkv * G * C * 2
-    elif D != 128 or G > 8 or C > 4096:
         return 0
-    else:
-        n = B * L * Hkv * G * C * 4
+    if D != 128 or G > 8 or C > 4096:
+        return 0
+    n = B * L * Hkv * G * C * 4
     return n if n <= _WORKSPACE_LIMIT else 0
 
 
@@ -70,9 +67,9 @@ def route_topk_launch(
     drop mask of remote_drop_mask(key_valid, derive_window, block_size) is
     computed inside the kernel instead.
     Returns indices [B, L, Hkv, topk] int32 and scores [B, L, Hkv, G, topk].
-    ``use_workspace`` (None: by shape) passes the kernels a workspace: an fp32
-    logits workspace [B, L, Hkv, G, C] for the short-block path, a bf16
-    raw-score workspace of that shape for the one-pass matrix-core kernel.
+    ``use_workspace`` (None: by shape) passes the kernels an fp32 logits
+    workspace [B, L, Hkv, G, C] for the short-block path; the matrix-core
+    kernel (up to 256 chunks) takes none.
     """
 
     if selection_mode not in {"post_softmax", "pre_softmax"}:

@@ -210,21 +210,34 @@ def test_route_topk_vs_oracle(L, C, G, topk):
     _check_route(idx, sc, q5, lmk, lse4, bias4, drop, topk, f"route L={L} C={C} G={G}")
 
 
-@pytest.mark.parametrize("L,C,G,topk", [(1000, 256, 7, 32), (300, 130, 8, 20)])
-def test_route_topk_one_pass_equals_two_pass(L, C, G, topk):
-    # The matrix-core kernel with a raw-score workspace (one pass, picks read
-    # back from the workspace) against the same kernel recomputing the picks'
-    # raw scores in a second pass: same indices, same bf16 scores.
-    _note(f"route one pass vs two pass L={L} C={C} G={G} K={topk}")
-    q5, lmk, lse4, bias4, drop, _ = _route_case(L, C, G, 4, 40 + L)
+@pytest.mark.parametrize("L,C,G,topk", [(300, 256, 7, 32), (1000, 130, 8, 20)])
+def test_route_topk_exact_ties_go_to_the_lower_chunk(L, C, G, topk):
+    # 64 chunks with identical landmarks and bias score exactly alike for
+    # every query: with 10 distinct chunks above them, the picks are those 10
+    # plus the lowest topk - 10 of the tied group (the stable order of the
+    # reference's selection).  Partial last workgroup (L % 128 != 0); two
+    # launches are identical.
+    _note(f"route ties L={L} C={C} G={G} K={topk}")
+    Hkv, D = 4, 128
+    q5, lmk, lse4, bias4, _, _ = _route_case(L, C, G, Hkv, 60 + L)
+    lmk5 = lmk.reshape(1, C, Hkv, G, D)
+    lo, hi = 40, 104
+    lmk5[:, lo:hi] = lmk5[:, 7:8]
+    bias4[:, lo:hi] = 9.0
+    bias4[:, C - 12:C - 2] = 20.0 + torch.arange(10.0).view(1, 10, 1, 1)
+    lmk = lmk5.reshape(1, C, Hkv * G, D).contiguous()
+    drop = torch.zeros(1, L, C, dtype=torch.int32)
     args = (q5.to(DEV), lmk.to(DEV), lse4.to(DEV), topk, 64)
     kw = dict(bias4=bias4.to(DEV), drop_mask=drop.to(DEV))
-    i1, s1 = route_topk_launch(*args, use_workspace=True, **kw)
-    i2, s2 = route_topk_launch(*args, use_workspace=False, **kw)
+    i1, s1 = route_topk_launch(*args, **kw)
+    i2, s2 = route_topk_launch(*args, **kw)
     torch.cuda.synchronize()
-    assert torch.equal(i1, i2)
-    assert torch.equal(s1.view(torch.int16), s2.view(torch.int16))
-    _check_route(i1, s1, q5, lmk, lse4, bias4, drop, topk, f"route one pass L={L} C={C}")
+    assert torch.equal(i1, i2) and torch.equal(s1.view(torch.int16), s2.view(torch.int16))
+    expect = torch.cat([torch.arange(lo, lo + topk - 10), torch.arange(C - 12, C - 2)])
+    assert torch.equal(i1.cpu().long(), expect.expand(1, L, Hkv, topk))
+    ridx, rsc, _ = O.route_topk(q5, lmk, lse4, topk, 64, drop_mask=drop, bias4=bias4)
+    assert torch.equal(i1.cpu().long(), ridx)
+    torch.testing.assert_close(s1.cpu().float(), rsc.bfloat16().float(), atol=0.02, rtol=0.01)
 
 
 @pytest.mark.parametrize("L,C,G,topk,mode,causal,fp32,shared", [
