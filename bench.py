@@ -280,11 +280,11 @@ def swa_main(args, torch, mrsa, dev) -> int:
     times = []
 
     def run(record):
-        vt = mrsa.value_tiles(v)
+        frags = mrsa.kv_fragments(k, v)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        out, _ = mrsa.local_attention.local_attention_launch(q, k, vt, valid, W, 0)
+        out, _ = mrsa.local_attention.local_attention_launch(q, frags, valid, W, 0)
         e1.record(stream)
         if record:
             times.append((e0, e1))

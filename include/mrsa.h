@@ -273,32 +273,6 @@ int mrsa_route_weights_bwd(const void* scores, const int32_t* indices, const flo
                            float* d_local_lse, float* d_gate, void* stream);
 
 /*
- * Re-lays V out as 64-key tiles, each stored transposed (head_dim rows of 64
- * keys), so both attention kernels can feed V to the matrix cores with
- * contiguous 16-byte loads.  Keys past seq_len inside the last tile are zero.
- * Inside a tile row, key 32a + 16b + 4c + e (a, b in {0,1}; c, e in 0..3)
- * sits at position 32a + 8c + 4b + e (matrix-core operand order).
- *   v: bf16 [batch, seq_len, kv_heads, head_dim]
- *   v_tiles (out): bf16 [batch, kv_heads, ceil(seq_len / 64), head_dim, 64]
- * No reference counterpart: internal layout step of the two attention ops.
- */
-int64_t mrsa_value_tiles_bytes(int64_t batch, int64_t seq_len, int64_t kv_heads,
-                               int64_t head_dim);
-int mrsa_value_tiles(const void* v, int64_t batch, int64_t seq_len, int64_t kv_heads,
-                     int64_t head_dim, void* v_tiles, void* stream);
-
-/*
- * Rewrites the tiles of the given rows of v after the rows were replaced
- * (the K/V write of a cached block step, LayerKVCache.replace at
- * dream_dllm_hils/fastdllm_cache.py:94-125), instead of re-tiling the whole
- * cache.  positions: int64 [count]; entries outside [0, seq_len) are ignored.
- * v_tiles as mrsa_value_tiles.
- */
-int mrsa_value_tiles_rows(const void* v, int64_t batch, int64_t seq_len, int64_t kv_heads,
-                          int64_t head_dim, const int64_t* positions, int64_t count,
-                          void* v_tiles, void* stream);
-
-/*
  * Re-lays K and V out as per-chunk fragments: for each 64-key chunk, the
  * register images of the 32 matrix-core operand loads of the routed
  * attention (16x16x32 bf16 products; lane l = 16 grp + j, elements e = 0..7):
@@ -310,7 +284,7 @@ int mrsa_value_tiles_rows(const void* v, int64_t batch, int64_t seq_len, int64_t
  *         NULL (the V part is then zero: enough for the candidate token scores)
  *   kv_frags (out): bf16 [batch, kv_heads, ceil(seq_len / 64), 16384], 16-byte aligned
  * Limits: head_dim == 128.
- * No reference counterpart: internal layout step of the routed attention.
+ * No reference counterpart: internal layout step of the two attention ops.
  */
 int64_t mrsa_kv_fragments_bytes(int64_t batch, int64_t seq_len, int64_t kv_heads,
                                 int64_t head_dim);
@@ -335,15 +309,15 @@ int mrsa_kv_fragments_rows(const void* k, const void* v, int64_t batch, int64_t 
  * (j + 1) % inert_chunk == 0, take zero K and zero V (local_attention.py:35-54):
  * they stay in the softmax denominator with logit 0 and add nothing to the
  * output.
- *   q: bf16 [batch, q_len, q_heads, head_dim];  k: bf16 [batch, kv_len, kv_heads, head_dim]
- *   v_tiles: output of mrsa_value_tiles for v
+ *   q: bf16 [batch, q_len, q_heads, head_dim]
+ *   kv_frags: output of mrsa_kv_fragments for the keys and values (kv_len rows)
  *   key_valid: optional bool [batch, kv_len];  query_positions: optional int64 [q_len]
  *   (NULL = query row i sits at position i)
  *   out: bf16 [batch, q_len, q_heads, head_dim];  lse: fp32 [batch, q_len, q_heads]
  *   sm_scale: finite and > 0 (MRSA_ERR_INVALID_ARGUMENT otherwise)
- * Limits: head_dim == 128, q_heads / kv_heads <= 8.
+ * Limits: head_dim == 128, q_heads / kv_heads <= 8, kv_len < 8388608.
  */
-int mrsa_local_attention_fwd(const void* q, const void* k, const void* v_tiles,
+int mrsa_local_attention_fwd(const void* q, const void* kv_frags,
                              const uint8_t* key_valid, const int64_t* query_positions,
                              int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
                              int64_t kv_heads, int64_t head_dim, int64_t window,
@@ -361,7 +335,7 @@ int mrsa_local_attention_fwd(const void* q, const void* k, const void* v_tiles,
  */
 int64_t mrsa_local_attention_workspace_bytes(int64_t batch, int64_t q_len, int64_t q_heads,
                                              int64_t parts);
-int mrsa_local_attention_split_fwd(const void* q, const void* k, const void* v_tiles,
+int mrsa_local_attention_split_fwd(const void* q, const void* kv_frags,
                                    const uint8_t* key_valid, const int64_t* query_positions,
                                    int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
                                    int64_t kv_heads, int64_t head_dim, int64_t window,

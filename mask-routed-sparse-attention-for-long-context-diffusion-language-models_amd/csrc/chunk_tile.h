@@ -1,11 +1,11 @@
-// Shared pieces of the chunk-tile attention kernels (routed chunks and
-// window tiles): asm LDS operand reads with explicit waits, and the S^T = K.Q^T
-// product of one 16-column tile over a 64-key tile held in an XOR-swizzled
-// LDS slot.
+// Shared pieces of the window-attention kernel: asm LDS operand reads with
+// explicit waits, and the S^T = K.Q^T product of one 16-column tile over a
+// 64-key tile held in an LDS slot.
 //
-// Slot layout (32 KB): K, 64 rows of 128 bf16 (256 B), 16-byte part P of row r
-// at position P ^ (r & 15); then V^T, 128 rows of 64 keys (128 B), part P of
-// row r at position P ^ (r & 7), keys in the tiled-V order.
+// Slot layout (32 KB): the tile's K / V fragments (mrsa_kv_fragments): 32
+// operand images of 1 KB, lane l's 16 bytes at 16 l; K image 4 mt + ks holds
+// keys 16 mt.. x dims 32 ks.., V image 2 nt + ks holds dims 16 nt.. x keys
+// 32 ks.. (tiled order).
 #pragma once
 
 #include <utility>
@@ -45,34 +45,35 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
 }
 
-// S^T = K . Q^T for one column tile: 16 K operand reads from an LDS chunk slot
-// (swizzled rows, kaddr[j] = lane address of reduction step j) and 16
-// products, read o + 8 issued after product o so eight reads stay in flight.
-// DEPTH reads stay in flight (8 when registers allow, 4 for the 12-wave split).
+// S^T = K . Q^T for one column tile: 16 K operand reads from a fragment slot
+// (laddr = slot + 16 lane; product o = rows 16 (o & 3).., reduction step
+// o >> 2 reads image 4 (o & 3) + (o >> 2)) and 16 products, read o + DEPTH
+// issued after product o so DEPTH reads stay in flight.
+template <int O>
+constexpr int kimg_off() { return (4 * (O & 3) + (O >> 2)) * 1024; }
+
 template <int DEPTH = 8>
-__device__ __forceinline__ void qk_tile(const uint32_t (&kaddr)[4], const u32x4_t (&Q)[4],
-                                        f32x4_t (&S)[4]) {
+__device__ __forceinline__ void qk_frag(uint32_t laddr, const u32x4_t (&Q)[4], f32x4_t (&S)[4]) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) S[t] = zero4();
   u32x4_t kb[16];
   static_for<16>([&](auto oc) {
     constexpr int o = decltype(oc)::value;
-    if constexpr (o < DEPTH) kb[o] = lds_read_b128<(o & 3) * 4096>(kaddr[o >> 2]);
+    if constexpr (o < DEPTH) kb[o] = lds_read_b128<kimg_off<o>()>(laddr);
   });
   static_for<16>([&](auto oc) {
     constexpr int o = decltype(oc)::value;
     lds_wait<(15 - o < DEPTH - 1 ? 15 - o : DEPTH - 1)>(kb[o]);
     S[o & 3] = mfma_bf16_16x16x32(kb[o], Q[o >> 2], S[o & 3]);
-    if constexpr (o + DEPTH < 16)
-      kb[o + DEPTH] = lds_read_b128<((o + DEPTH) & 3) * 4096>(kaddr[(o + DEPTH) >> 2]);
+    if constexpr (o + DEPTH < 16) kb[o + DEPTH] = lds_read_b128<kimg_off<o + DEPTH>()>(laddr);
     __builtin_amdgcn_sched_barrier(0);
   });
 }
 
-// qk_tile for two column tiles at once: each K operand read feeds both
+// qk_frag for two column tiles at once: each K operand read feeds both
 // products (half the LDS traffic per product).
 template <int DEPTH = 8>
-__device__ __forceinline__ void qk_tile2(const uint32_t (&kaddr)[4], const u32x4_t (&Q0)[4],
+__device__ __forceinline__ void qk_frag2(uint32_t laddr, const u32x4_t (&Q0)[4],
                                          const u32x4_t (&Q1)[4], f32x4_t (&S0)[4],
                                          f32x4_t (&S1)[4]) {
 #pragma unroll
@@ -83,15 +84,14 @@ __device__ __forceinline__ void qk_tile2(const uint32_t (&kaddr)[4], const u32x4
   u32x4_t kb[16];
   static_for<16>([&](auto oc) {
     constexpr int o = decltype(oc)::value;
-    if constexpr (o < DEPTH) kb[o] = lds_read_b128<(o & 3) * 4096>(kaddr[o >> 2]);
+    if constexpr (o < DEPTH) kb[o] = lds_read_b128<kimg_off<o>()>(laddr);
   });
   static_for<16>([&](auto oc) {
     constexpr int o = decltype(oc)::value;
     lds_wait<(15 - o < DEPTH - 1 ? 15 - o : DEPTH - 1)>(kb[o]);
     S0[o & 3] = mfma_bf16_16x16x32(kb[o], Q0[o >> 2], S0[o & 3]);
     S1[o & 3] = mfma_bf16_16x16x32(kb[o], Q1[o >> 2], S1[o & 3]);
-    if constexpr (o + DEPTH < 16)
-      kb[o + DEPTH] = lds_read_b128<((o + DEPTH) & 3) * 4096>(kaddr[(o + DEPTH) >> 2]);
+    if constexpr (o + DEPTH < 16) kb[o + DEPTH] = lds_read_b128<kimg_off<o + DEPTH>()>(laddr);
     __builtin_amdgcn_sched_barrier(0);
   });
 }

@@ -1,5 +1,5 @@
-// Layout helpers: the remote-route drop mask, the tiled, transposed V the
-// local attention reads and the K / V fragments the routed attention reads.
+// Layout helpers: the remote-route drop mask and the K / V fragments both
+// attention kernels read.
 #include "mrsa_device.h"
 
 using namespace mrsa;
@@ -45,68 +45,17 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// v[b, j, h, :] -> v_tiles[b, h, j / 64, :, tile_pos(j % 64)].
-// Within a 64-key tile, key 32a + 16b + 4c + e (a, b in {0,1}; c, e in 0..3)
-// is stored at position 32a + 8c + 4b + e: the eight keys one lane feeds to
-// a 32-deep matrix-core reduction (keys 4c..4c+3 and 16+4c..16+4c+3 of a
-// 32-key half, the order in which the S^T accumulator hands them out) are
-// then 16 contiguous bytes.
-__device__ __forceinline__ int tile_key_of_pos(int p) {
-  return (p & 32) | (((p >> 2) & 1) << 4) | (((p >> 3) & 3) << 2) | (p & 3);
-}
-
-__device__ __forceinline__ int tile_pos_of_key(int k) {
-  return (k & 32) | (((k >> 2) & 3) << 3) | (((k >> 4) & 1) << 2) | (k & 3);
-}
-
-// Rewrites the tiled copy of the listed rows only (rows of a cache that
-// were replaced); positions outside [0, L) are ignored.
-__global__ void __launch_bounds__(256)
-    value_tiles_rows_kernel(const uint16_t* __restrict__ v, int64_t L, int64_t H, int D,
-                            int64_t NT, const int64_t* __restrict__ positions,
-                            uint16_t* __restrict__ vt) {
-  const int64_t p = positions[blockIdx.x];
-  const int64_t h = blockIdx.y, b = blockIdx.z;
-  if (p < 0 || p >= L) return;
-  const int pos = tile_pos_of_key((int)(p & 63));
-  uint16_t* dst = vt + ((b * H + h) * NT + p / 64) * (int64_t)D * 64 + pos;
-  const uint16_t* src = v + ((b * L + p) * H + h) * D;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) dst[(int64_t)d * 64] = src[d];
-}
-
-__global__ void __launch_bounds__(256)
-    value_tiles_kernel(const uint16_t* __restrict__ v, int64_t L, int64_t H, int D, int64_t NT,
-                       uint16_t* __restrict__ vt) {
-  extern __shared__ uint16_t tile[];  // [64][D + 2]
-  const int64_t t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int pitch = D + 2;
-  const int half = D / 2;
-  for (int e = threadIdx.x; e < 64 * half; e += blockDim.x) {
-    const int s = e / half, d2 = e - s * half;
-    const int64_t j = t * 64 + s;
-    uint32_t w = 0;
-    if (j < L) w = *reinterpret_cast<const uint32_t*>(v + ((b * L + j) * H + h) * D + 2 * d2);
-    tile[s * pitch + 2 * d2] = (uint16_t)(w & 0xffffu);
-    tile[s * pitch + 2 * d2 + 1] = (uint16_t)(w >> 16);
-  }
-  __syncthreads();
-  uint16_t* dst = vt + ((b * H + h) * NT + t) * (int64_t)D * 64;
-  for (int e = threadIdx.x; e < D * 32; e += blockDim.x) {
-    const int d = e >> 5, p2 = e & 31;
-    const int key = tile_key_of_pos(2 * p2);  // key + 1 sits at position 2 * p2 + 1
-    const uint32_t w = (uint32_t)tile[key * pitch + d] | ((uint32_t)tile[(key + 1) * pitch + d] << 16);
-    *reinterpret_cast<uint32_t*>(dst + d * 64 + 2 * p2) = w;
-  }
-}
-
 // K and V fragments of one 64-key chunk: the register images of the matrix
-// operands the routed attention feeds to 16x16x32 bf16 matrix products
-// (lane l = 16 grp + j holds 8 consecutive elements e of one instruction):
+// operands the routed and window attention feed to 16x16x32 bf16 matrix
+// products (lane l = 16 grp + j holds 8 consecutive elements e of one
+// instruction):
 //   K part (operand of S^T = K . Q^T), instruction i = 4 mt + ks:
 //     f[512 i + 8 l + e]        = K[key 16 mt + j][dim 32 ks + 8 grp + e]
-//   V part (operand of O = P . V), instruction i = 2 nt + ks:
+//   V part (operand of O = P . V, or of O^T = V^T . P^T), instruction i = 2 nt + ks:
 //     f[8192 + 512 i + 8 l + e] = V[key 32 ks + 16 (e >> 2) + 4 grp + (e & 3)][dim 16 nt + j]
-// (the V key order is the tiled order above).  Every operand load of a chunk
+// (key 32a + 16b + 4c + e sits at reduction slot 32a + 8c + 4b + e: the eight
+// keys a lane feeds to one 32-deep reduction are the ones the S^T
+// accumulator of the first product hands it).  Every operand load of a chunk
 // is one contiguous 1 KB read.  Keys past the sequence end are zero, and the
 // whole V part without a V input (the token scores read only K).
 constexpr int kFragElems = 16384;  // bf16 per (batch, KV head, chunk)
@@ -213,46 +162,6 @@ extern "C" int mrsa_remote_drop_mask_rows(const uint8_t* valid_mask,
             (unsigned)batch);
   hipLaunchKernelGGL(drop_mask_kernel, grid, dim3(256), 0, (hipStream_t)stream, valid_mask,
                      nullptr, query_positions, rows, seq_len, window, chunk_size, drop_mask);
-  return mrsa_launch_status();
-}
-
-extern "C" int64_t mrsa_value_tiles_bytes(int64_t batch, int64_t seq_len, int64_t kv_heads,
-                                          int64_t head_dim) {
-  if (batch < 0 || seq_len < 0 || kv_heads < 0 || head_dim < 0) return -1;
-  return batch * kv_heads * ((seq_len + 63) / 64) * head_dim * 64 * 2;
-}
-
-extern "C" int mrsa_value_tiles(const void* v, int64_t batch, int64_t seq_len, int64_t kv_heads,
-                                int64_t head_dim, void* v_tiles, void* stream) {
-  if (batch < 0 || seq_len < 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 ||
-      head_dim > 256)
-    return MRSA_ERR_INVALID_ARGUMENT;
-  if (batch == 0 || seq_len == 0) return MRSA_OK;
-  if (!v || !v_tiles || (uintptr_t)v % 4 != 0 || (uintptr_t)v_tiles % 4 != 0)
-    return MRSA_ERR_INVALID_ARGUMENT;
-  if (kv_heads > 65535 || batch > 65535) return MRSA_ERR_UNSUPPORTED;
-  const int64_t NT = (seq_len + 63) / 64;
-  const size_t smem = (size_t)64 * (head_dim + 2) * 2;
-  hipLaunchKernelGGL(value_tiles_kernel, dim3((unsigned)NT, (unsigned)kv_heads, (unsigned)batch),
-                     dim3(256), smem, (hipStream_t)stream, (const uint16_t*)v, seq_len, kv_heads,
-                     (int)head_dim, NT, (uint16_t*)v_tiles);
-  return mrsa_launch_status();
-}
-
-extern "C" int mrsa_value_tiles_rows(const void* v, int64_t batch, int64_t seq_len,
-                                     int64_t kv_heads, int64_t head_dim, const int64_t* positions,
-                                     int64_t count, void* v_tiles, void* stream) {
-  if (batch < 0 || seq_len < 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 ||
-      head_dim > 256 || count < 0)
-    return MRSA_ERR_INVALID_ARGUMENT;
-  if (batch == 0 || seq_len == 0 || count == 0) return MRSA_OK;
-  if (!v || !v_tiles || !positions) return MRSA_ERR_INVALID_ARGUMENT;
-  if (kv_heads > 65535 || batch > 65535 || count > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
-  const int64_t NT = (seq_len + 63) / 64;
-  hipLaunchKernelGGL(value_tiles_rows_kernel,
-                     dim3((unsigned)count, (unsigned)kv_heads, (unsigned)batch),
-                     dim3((unsigned)head_dim), 0, (hipStream_t)stream, (const uint16_t*)v,
-                     seq_len, kv_heads, (int)head_dim, NT, positions, (uint16_t*)v_tiles);
   return mrsa_launch_status();
 }
 

@@ -11,10 +11,12 @@
 // products run during the other's softmax.  (kNT = 2 shares each K / V
 // operand read between a wave's two tiles instead; both measure alike.)
 //
-// Key tiles of 64 arrive by global->LDS DMA in a ring of kRing XOR-swizzled
-// 32 KB slots (chunk_tile.h layout: K rows, then V^T rows from the tiled V
-// layout); every wave issues 4 of a tile's 32 1-KB DMA instructions from
-// 32-bit offsets against wave-uniform tile bases.  One barrier per key tile,
+// Key tiles of 64 arrive by buffer->LDS DMA in a ring of kRing 32 KB slots
+// holding the tile's K / V fragments (mrsa_kv_fragments: the 32 matrix-core
+// operand images of 1 KB, lane l's 16 bytes at 16 l), so every operand read
+// is one 16-byte LDS read at the lane's slot address plus an immediate
+// offset, free of bank conflicts; every wave issues 4 of a tile's 32 DMA
+// instructions, with wave-uniform offsets.  One barrier per key tile,
 // with no memory fence: each wave waits (vmcnt) for its own share of tile t,
 // the barrier publishes the whole tile and frees the slot of tile t - 1,
 // which then receives tile t + kRing - 1.  The valid-key words of all the
@@ -26,7 +28,7 @@
 //   O^T[d][col]  += V^T (A: 128 x 64) . P^T (B: 64 x 16)      -> 16 MFMAs
 // P^T is fed to the second product straight from the accumulator registers
 // of the first: lane l holds keys 16t + 4(l/16) + i of its column, and the
-// tiled V layout numbers the reduction slots to match.
+// fragments' V images number the reduction slots to match (the tiled order).
 //
 // Semantics (dream_dllm_hils/local_attention.py:35-107):
 //   * key j is visible to a query at position p iff |p - j| <= window;
@@ -65,8 +67,7 @@ constexpr int kMaskTiles = 512;        // key-valid words kept in LDS per block
 
 struct LocalArgs {
   const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* vt;
+  const uint16_t* kvf;        // [B, Hkv, NTk, 16384] K / V fragments
   const uint8_t* key_valid;
   const int64_t* qpos;
   int64_t B, Lq, Lk;
@@ -176,36 +177,22 @@ local_attn_kernel(LocalArgs a) {
   const int ntiles = (int)max(kt1 - kt0 + 1, (int64_t)0);
   const bool tab = ntiles <= kMaskTiles;
 
-  // DMA of key tile kt into ring slot `slot`: this wave's K instructions
-  // j = 2w, 2w + 1 (LDS units 64j + lane: row 4j + lane / 16, position
-  // lane % 16, holding part position ^ (row & 15)) and V^T instructions
-  // j = 2w, 2w + 1 (units 1024 + 64j + lane: row 8j + lane / 8, position
-  // lane % 8, holding part position ^ (row & 7)).  Rows past kv_len read the
-  // last row (their keys are masked; the tiled V is zero there).
-  const uint16_t* kbase = a.k + (b * a.Lk * a.Hkv + h) * (int64_t)128;
-  const int64_t kstride = (int64_t)a.Hkv * 128;
-  const uint16_t* vbase = a.vt + ((b * a.Hkv + h) * a.NTk) * (int64_t)(128 * 64);
-  // Per-lane parts of the DMA sources, tile-relative and 32-bit, against
-  // wave-uniform tile bases.
-  const int kr0 = 8 * wave + grp;  // K row of u = 0; u = 1 adds 4
-  const uint32_t kpart0 = (uint32_t)((col ^ (kr0 & 15)) * 8);
-  const uint32_t kpart1 = (uint32_t)((col ^ ((kr0 + 4) & 15)) * 8);
-  const int vr0 = 16 * wave + (lane >> 3);  // V^T row of u = 0; u = 1 adds 8
-  const uint32_t voff0 = (uint32_t)(vr0 * 64 + (((lane & 7) ^ (vr0 & 7)) * 8));
+  // DMA of key tile kt into ring slot `slot`: this wave's 4 of the tile's
+  // 32 operand images (image i at slot + 1024 i; lane l's 16 bytes at 16 l).
+  // Tiles past kv_len hold zeros.
+  const __amdgpu_buffer_rsrc_t frs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.kvf + (b * a.Hkv + h) * a.NTk * (int64_t)16384), (short)0,
+      (int)(uint32_t)(a.NTk * 32768), 0x00020000);
+  const uint32_t dma_lane = 16u * lane;
   auto issue_tile = [&](int64_t kt, int slot) {
-    unsigned char* dst = ring + slot * kSlotBytes;
-    const uint16_t* kt_base = kbase + kt * 64 * kstride;  // uniform
-    const int last = (int)min((int64_t)63, a.Lk - 1 - kt * 64);
-    const uint32_t ks = (uint32_t)kstride;
-    __builtin_amdgcn_global_load_lds(kt_base + (uint32_t)min(kr0, last) * ks + kpart0,
-                                     (lds_void_t*)(dst + (2 * wave) * 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(kt_base + (uint32_t)min(kr0 + 4, last) * ks + kpart1,
-                                     (lds_void_t*)(dst + (2 * wave + 1) * 1024), 16, 0, 0);
-    const uint16_t* vt_base = vbase + kt * (128 * 64);      // uniform
-    __builtin_amdgcn_global_load_lds(vt_base + voff0, (lds_void_t*)(dst + 16384 + (2 * wave) * 1024),
-                                     16, 0, 0);
-    __builtin_amdgcn_global_load_lds(vt_base + voff0 + 8 * 64,
-                                     (lds_void_t*)(dst + 16384 + (2 * wave + 1) * 1024), 16, 0, 0);
+    unsigned char* dst = ring + slot * kSlotBytes + (4 * wave) * 1024;
+    const uint32_t src = (uint32_t)kt * 32768u + (uint32_t)(4 * wave) * 1024u;
+    // (the immediate offset of a buffer->LDS load moves the LDS address too,
+    // so the image offset goes into the scalar offset)
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(frs, (lds_void_t*)(dst + u * 1024), 16, dma_lane,
+                                               src + 1024u * u, 0, 0);
   };
   // Valid-key words of the block's key tiles (when they fit the table),
   // before the first DMA: waiting for these loads must not wait for it.
@@ -235,8 +222,6 @@ local_attn_kernel(LocalArgs a) {
     for (int td = 0; td < 8; ++td) acc[nt][td] = zero4();
   }
 
-  const uint32_t kofs0 = (uint32_t)(col * 128 + ((grp ^ col) * 8));
-  const uint32_t vofs0 = (uint32_t)(8192 + col * 64 + ((grp ^ (col & 7)) * 8));
   const float c = a.scale_log2;
   const int W32 = (int)a.W;
   const uint64_t kLast = 1ull << 63;
@@ -276,28 +261,49 @@ local_attn_kernel(LocalArgs a) {
     const bool full = (rbits == ~0ull) && (j0 >= phi - a.W) && (j0 + 63 <= plo + a.W);
     // This lane's keys are 16 tt + 4 grp + i: bit 16 tt + i of the shifted
     // words (immediate bit tests, nothing per element kept across tiles).
-    const uint64_t rsh = rbits >> (4 * grp), ish = ibits >> (4 * grp);
+    const uint64_t rsh = rbits >> (4 * grp);
 
     // S^T of both column tiles, sharing each K operand read.
-    const uint32_t kaddr[4] = {sbase + 2 * (kofs0 ^ 0u), sbase + 2 * (kofs0 ^ 32u),
-                               sbase + 2 * (kofs0 ^ 64u), sbase + 2 * (kofs0 ^ 96u)};
+    const uint32_t laddr = sbase + 16u * lane;  // this lane's 16 bytes of every image
     f32x4_t S[kNT][4];
-    if constexpr (kNT == 2) qk_tile2<kDepth>(kaddr, Qb[0], Qb[kNT - 1], S[0], S[kNT - 1]);
-    else qk_tile<kDepth>(kaddr, Qb[0], S[0]);
-    const uint32_t vaddr[2] = {sbase + 2 * vofs0, sbase + 2 * (vofs0 ^ 32u)};
-    // The first V^T operands do not depend on P: read them now.
+    if constexpr (kNT == 2) qk_frag2<kDepth>(laddr, Qb[0], Qb[kNT - 1], S[0], S[kNT - 1]);
+    else qk_frag<kDepth>(laddr, Qb[0], S[0]);
+    // The first V^T operands do not depend on P: read them now.  Product o
+    // (d rows 16 (o & 7).., keys 32 (o >> 3)..) reads V image 2 (o & 7) + (o >> 3).
     u32x4_t vb[16];
     static_for<4>([&](auto oc) {
       constexpr int o = decltype(oc)::value;
-      vb[o] = lds_read_b128<(o & 7) * 2048>(vaddr[o >> 3]);
+      vb[o] = lds_read_b128<16384 + (2 * (o & 7) + (o >> 3)) * 1024>(laddr);
     });
+
+    // Inert keys: lanes of group g hold keys 16 tt + 4 g + i.  The landmark
+    // slot (key 63, lanes 48..63) is the usual only one; other inert keys
+    // (failed key_valid) take the per-element path.  Values are patched in
+    // place (no register copies at the joins).
+    const uint64_t last_lanes = (ibits >> 63) ? 0xFFFF000000000000ull : 0ull;
+    const bool other_inert = (ibits & ~kLast) != 0ull;
+    auto inert_lanes = [&](int tt, int i) {
+      uint64_t m = 0ull;
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        m |= ((ibits >> (16 * tt + 4 * g + i)) & 1ull) ? (0xFFFFull << (16 * g)) : 0ull;
+      return m;
+    };
+    const float zero_v = 0.f;
 
     u32x4_t Pb[kNT][2];
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) {
-      // Logits in units of log2: s * scale_log2.  Keys outside the window
-      // (or past kv_len, or of an absent column) are -inf; inert keys inside
-      // it are exactly 0.
+      // Logits in units of log2: s * scale_log2.  Inert keys are exactly 0;
+      // keys outside the window (or past kv_len, or of an absent column) are
+      // -inf, which the window mask below sets after the inert zeros.
+      S[nt][3][3] = set_where(S[nt][3][3], last_lanes, zero_v);
+      if (other_inert) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) S[nt][tt][i] = set_where(S[nt][tt][i], inert_lanes(tt, i), zero_v);
+      }
       if (!full) {
         const int rel = (int)j0 + 4 * grp - qp[nt];
 #pragma unroll
@@ -308,16 +314,6 @@ local_attn_kernel(LocalArgs a) {
             if (!((rsh >> (16 * tt + i)) & 1ull) || dd > W32 || dd < -W32 || !qok[nt])
               S[nt][tt][i] = neg_inf();
           }
-      }
-      if (ibits == kLast) {
-        // Only the tile's last slot is inert (the landmark of a 64-key chunk).
-        if (grp == 3 && S[nt][3][3] != neg_inf()) S[nt][3][3] = 0.f;
-      } else if (ibits != 0ull) {
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (((ish >> (16 * tt + i)) & 1ull) && S[nt][tt][i] != neg_inf()) S[nt][tt][i] = 0.f;
       }
       const float mx = across4_max(max16_raw(S[nt]));
       const float m_new = fmaxf(m_run[nt], mx * c);
@@ -335,14 +331,12 @@ local_attn_kernel(LocalArgs a) {
       }
       const float rsum = across4_sum((part4[0] + part4[1]) + (part4[2] + part4[3]));
       // Inert keys count in the denominator but carry zero V.
-      if (ibits == kLast) {
-        if (grp == 3) S[nt][3][3] = 0.f;
-      } else if (ibits != 0ull) {
+      S[nt][3][3] = set_where(S[nt][3][3], last_lanes, zero_v);
+      if (other_inert) {
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if ((ish >> (16 * tt + i)) & 1ull) S[nt][tt][i] = 0.f;
+          for (int i = 0; i < 4; ++i) S[nt][tt][i] = set_where(S[nt][tt][i], inert_lanes(tt, i), zero_v);
       }
       l_run[nt] = l_run[nt] * alpha + rsum;
       m_run[nt] = m_new;
@@ -362,7 +356,7 @@ local_attn_kernel(LocalArgs a) {
     // kDepth reads in flight.
     static_for<kDepth - 4>([&](auto oc) {
       constexpr int o = decltype(oc)::value + 4;
-      vb[o] = lds_read_b128<(o & 7) * 2048>(vaddr[o >> 3]);
+      vb[o] = lds_read_b128<16384 + (2 * (o & 7) + (o >> 3)) * 1024>(laddr);
     });
     static_for<16>([&](auto oc) {
       constexpr int o = decltype(oc)::value;
@@ -371,7 +365,8 @@ local_attn_kernel(LocalArgs a) {
       if constexpr (kNT == 2)
         acc[kNT - 1][o & 7] = mfma_bf16_16x16x32(vb[o], Pb[kNT - 1][o >> 3], acc[kNT - 1][o & 7]);
       if constexpr (o + kDepth < 16)
-        vb[o + kDepth] = lds_read_b128<((o + kDepth) & 7) * 2048>(vaddr[(o + kDepth) >> 3]);
+        vb[o + kDepth] =
+            lds_read_b128<16384 + (2 * ((o + kDepth) & 7) + ((o + kDepth) >> 3)) * 1024>(laddr);
       __builtin_amdgcn_sched_barrier(0);
     });
   }
@@ -463,7 +458,7 @@ int launch_local(const LocalArgs& a, hipStream_t s) {
 
 namespace {
 
-int local_attention(const void* q, const void* k, const void* v_tiles, const uint8_t* key_valid,
+int local_attention(const void* q, const void* kv_frags, const uint8_t* key_valid,
                     const int64_t* query_positions, int64_t batch, int64_t q_len, int64_t kv_len,
                     int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t window,
                     int64_t inert_chunk, float sm_scale, int64_t parts, void* workspace,
@@ -473,16 +468,17 @@ int local_attention(const void* q, const void* k, const void* v_tiles, const uin
       !(sm_scale > 0.f) || sm_scale == __builtin_inff())
     return MRSA_ERR_INVALID_ARGUMENT;
   if (batch == 0 || q_len == 0) return MRSA_OK;
-  if (kv_len == 0 || !q || !k || !v_tiles || !out || !lse) return MRSA_ERR_INVALID_ARGUMENT;
+  if (kv_len == 0 || !q || !kv_frags || !out || !lse) return MRSA_ERR_INVALID_ARGUMENT;
   if (head_dim != 128) return MRSA_ERR_UNSUPPORTED;
-  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v_tiles) % 16 != 0 || (uintptr_t)out % 8 != 0)
+  if (((uintptr_t)q | (uintptr_t)kv_frags) % 16 != 0 || (uintptr_t)out % 8 != 0)
     return MRSA_ERR_INVALID_ARGUMENT;
+  // a KV head's fragments are addressed with 32-bit byte offsets
+  if ((kv_len + 63) / 64 >= 131072) return MRSA_ERR_UNSUPPORTED;
   const int64_t G = q_heads / kv_heads;
   if (kv_heads > 65535 || batch > 65535) return MRSA_ERR_UNSUPPORTED;
   LocalArgs a;
   a.q = (const uint16_t*)q;
-  a.k = (const uint16_t*)k;
-  a.vt = (const uint16_t*)v_tiles;
+  a.kvf = (const uint16_t*)kv_frags;
   a.key_valid = key_valid;
   a.qpos = query_positions;
   a.B = batch;
@@ -516,13 +512,13 @@ int local_attention(const void* q, const void* k, const void* v_tiles, const uin
 
 }  // namespace
 
-extern "C" int mrsa_local_attention_fwd(const void* q, const void* k, const void* v_tiles,
+extern "C" int mrsa_local_attention_fwd(const void* q, const void* kv_frags,
                                         const uint8_t* key_valid, const int64_t* query_positions,
                                         int64_t batch, int64_t q_len, int64_t kv_len,
                                         int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                                         int64_t window, int64_t inert_chunk, float sm_scale,
                                         void* out, float* lse, void* stream) {
-  return local_attention(q, k, v_tiles, key_valid, query_positions, batch, q_len, kv_len,
+  return local_attention(q, kv_frags, key_valid, query_positions, batch, q_len, kv_len,
                          q_heads, kv_heads, head_dim, window, inert_chunk, sm_scale, 1, nullptr,
                          out, lse, stream);
 }
@@ -533,7 +529,7 @@ extern "C" int64_t mrsa_local_attention_workspace_bytes(int64_t batch, int64_t q
   return parts > 1 ? parts * batch * q_len * q_heads * 130 * 4 : 0;
 }
 
-extern "C" int mrsa_local_attention_split_fwd(const void* q, const void* k, const void* v_tiles,
+extern "C" int mrsa_local_attention_split_fwd(const void* q, const void* kv_frags,
                                               const uint8_t* key_valid,
                                               const int64_t* query_positions, int64_t batch,
                                               int64_t q_len, int64_t kv_len, int64_t q_heads,
@@ -548,7 +544,7 @@ extern "C" int mrsa_local_attention_split_fwd(const void* q, const void* k, cons
       return MRSA_ERR_INVALID_ARGUMENT;
     if (batch * parts > 65535) return MRSA_ERR_UNSUPPORTED;
   }
-  return local_attention(q, k, v_tiles, key_valid, query_positions, batch, q_len, kv_len,
+  return local_attention(q, kv_frags, key_valid, query_positions, batch, q_len, kv_len,
                          q_heads, kv_heads, head_dim, window, inert_chunk, sm_scale, parts,
                          parts > 1 ? workspace : nullptr, out, lse, stream);
 }

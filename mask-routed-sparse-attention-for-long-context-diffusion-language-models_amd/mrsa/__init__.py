@@ -8,7 +8,7 @@ hand-written HIP kernels in ../csrc (C ABI: include/mrsa.h).  Module map:
                         online_softmax_topk_head        (ops/topk_head_softmax.py)
     routing.py          route_topk_g7, selected_attention_g7[_cached]
                                                         (dream_dllm_hils/routing.py)
-    sparse_attention.py HiLS_block_M_head, value_tiles, kv_fragments   (ops/hils_fwd_bwd_head.py)
+    sparse_attention.py HiLS_block_M_head, kv_fragments   (ops/hils_fwd_bwd_head.py)
     local_attention.py  bidir_local_attention, cached_local_attention
                                                         (dream_dllm_hils/local_attention.py)
     route_weights.py    route_weights, route_weights_torch
@@ -41,7 +41,7 @@ from .route_layer import (
 )
 from .route_weights import route_weights, route_weights_torch
 from .routing import route_topk_g7, selected_attention_g7, selected_attention_g7_cached
-from .sparse_attention import HiLS_block_M_head, kv_fragments, value_tiles
+from .sparse_attention import HiLS_block_M_head, kv_fragments
 from .token_score import candidate_token_scores_gqa
 from .token_refinement import refine_remote_tokens_g7, select_global_token_keep
 from .topk import online_softmax_topk_head, ref_softmax_topk_max_pooling
@@ -80,6 +80,5 @@ __all__ = [
     "selected_attention_g7",
     "selected_attention_g7_cached",
     "swa_attention",
-    "value_tiles",
     "kv_fragments",
 ]

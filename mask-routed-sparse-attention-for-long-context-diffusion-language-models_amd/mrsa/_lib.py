@@ -74,21 +74,18 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P,
          _P, _P, _P, _P, _P],
     ),
-    "mrsa_value_tiles_bytes": (_I64, [_I64, _I64, _I64, _I64]),
-    "mrsa_value_tiles": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P]),
-    "mrsa_value_tiles_rows": (_I, [_P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "mrsa_kv_fragments_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "mrsa_kv_fragments": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P, _P]),
     "mrsa_kv_fragments_rows": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "mrsa_local_attention_fwd": (
         _I,
-        [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F,
+        [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F,
          _P, _P, _P],
     ),
     "mrsa_local_attention_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "mrsa_local_attention_split_fwd": (
         _I,
-        [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F,
+        [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F,
          _I64, _P, _I64, _P, _P, _P],
     ),
     "mrsa_selected_attention_fwd": (

@@ -14,7 +14,7 @@ from typing import Tuple
 import torch
 
 from . import _lib
-from .sparse_attention import value_tiles
+from .sparse_attention import FRAG_ELEMS, kv_fragments
 
 
 def _validate_layout(q, k, v, key_valid) -> None:
@@ -58,43 +58,52 @@ def key_parts(batch: int, q_len: int, kv_heads: int, kv_len: int, flash_window: 
 
 def local_attention_launch(
     q: torch.Tensor,
-    k: torch.Tensor,
-    v_tiles: torch.Tensor,
+    kv_frags: torch.Tensor,
     key_valid: torch.Tensor | None,
     flash_window: int,
     inert_chunk: int,
     *,
+    kv_len: int | None = None,
     query_positions: torch.Tensor | None = None,
     sm_scale: float | None = None,
     parts: int | None = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """``parts`` splits each query block's key tiles over that many
-    workgroups (merged by a second kernel); None picks it with key_parts."""
+    """q [B, Lq, Hq, D]; kv_frags = kv_fragments(k, v) of the kv_len-row keys
+    (default: key_valid's length, else every row of the fragments).
+    ``parts`` splits each query block's key tiles over that many workgroups
+    (merged by a second kernel); None picks it with key_parts."""
 
     B, Lq, Hq, D = q.shape
-    Lk, Hkv = k.shape[1], k.shape[2]
+    if kv_frags.ndim != 4 or kv_frags.shape[0] != B or kv_frags.shape[3] != FRAG_ELEMS:
+        raise ValueError(f"kv_frags {tuple(kv_frags.shape)} is not a kv_fragments layout")
+    Hkv = kv_frags.shape[1]
+    if kv_len is None:
+        kv_len = key_valid.shape[-1] if key_valid is not None else kv_frags.shape[2] * 64
+    Lk = int(kv_len)
+    if not 0 < Lk <= kv_frags.shape[2] * 64 or (Lk + 63) // 64 != kv_frags.shape[2]:
+        raise ValueError(f"kv_len {Lk} does not match kv_frags {tuple(kv_frags.shape)}")
     if sm_scale is None:
         sm_scale = D ** -0.5
     if parts is None:
         parts = key_parts(B, Lq, Hkv, Lk, flash_window)
-    return torch.ops.mrsa.local_attention(q, k, v_tiles, key_valid, int(flash_window),
+    return torch.ops.mrsa.local_attention(q, kv_frags, key_valid, Lk, int(flash_window),
                                           int(inert_chunk), query_positions, float(sm_scale),
                                           int(parts))
 
 
-def _local_attention_impl(q, k, v_tiles, key_valid, flash_window, inert_chunk, query_positions,
-                          sm_scale, parts):
+def _local_attention_impl(q, kv_frags, key_valid, kv_len, flash_window, inert_chunk,
+                          query_positions, sm_scale, parts):
     B, Lq, Hq, D = q.shape
-    Lk, Hkv = k.shape[1], k.shape[2]
+    Hkv, Lk = kv_frags.shape[1], kv_len
     qc = q.contiguous()
-    kc = k.contiguous()
+    kf = kv_frags.contiguous()
     kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
     pos = None
     if query_positions is not None:
         pos = query_positions.to(device=q.device, dtype=torch.int64).contiguous()
     out = torch.empty(B, Lq, Hq, D, dtype=torch.bfloat16, device=q.device)
     lse = torch.empty(B, Lq, Hq, dtype=torch.float32, device=q.device)
-    args = (_lib.ptr(qc), _lib.ptr(kc), _lib.ptr(v_tiles), _lib.ptr(kv), _lib.ptr(pos),
+    args = (_lib.ptr(qc), _lib.ptr(kf), _lib.ptr(kv), _lib.ptr(pos),
             B, Lq, Lk, Hq, Hkv, D, int(flash_window), int(inert_chunk), float(sm_scale))
     if parts == 1:
         st = _lib.call("mrsa_local_attention_fwd", *args, _lib.ptr(out), _lib.ptr(lse),
@@ -134,9 +143,9 @@ def bidir_local_attention(
             "do not pass a dense L×L allowed_mask"
         )
     return local_attention_launch(
-        q, k, value_tiles(v), key_valid,
+        q, kv_fragments(k, v), key_valid,
         _flash_window(window, skip_inert_slots, chunk_size),
-        chunk_size if skip_inert_slots else 0,
+        chunk_size if skip_inert_slots else 0, kv_len=k.shape[1],
     )
 
 
@@ -174,8 +183,8 @@ def cached_local_attention(
             f"invalid window/chunk layout: L={seq_len}, W={window}, S={chunk_size}"
         )
     return local_attention_launch(
-        q, k, value_tiles(v), key_valid,
+        q, kv_fragments(k, v), key_valid,
         _flash_window(window, skip_inert_slots, chunk_size),
-        chunk_size if skip_inert_slots else 0,
+        chunk_size if skip_inert_slots else 0, kv_len=seq_len,
         query_positions=query_positions,
     )

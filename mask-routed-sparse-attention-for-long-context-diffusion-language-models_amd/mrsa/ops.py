@@ -26,8 +26,7 @@ from .local_attention import _local_attention_impl
 from .pool import _pool_bwd_impl, _pool_impl
 from .route_weights import _route_weights_bwd_impl, _route_weights_impl
 from .sparse_attention import (FRAG_ELEMS, _kv_fragments_impl, _kv_fragments_rows_impl,
-                               _selected_attention_impl, _value_tiles_impl,
-                               _value_tiles_rows_impl)
+                               _selected_attention_impl)
 from .token_refinement import _token_keep_impl
 from .token_score import _token_scores_impl
 from .topk import _route_topk_impl
@@ -38,28 +37,6 @@ _CUDA = "cuda"
 def _op(name, mutates_args=()):
     return torch.library.custom_op(f"mrsa::{name}", mutates_args=mutates_args,
                                    device_types=_CUDA)
-
-
-# -- V layout -------------------------------------------------------------
-@_op("value_tiles")
-def value_tiles(v: Tensor) -> Tensor:
-    return _value_tiles_impl(v)
-
-
-@value_tiles.register_fake
-def _(v):
-    B, L, H, D = v.shape
-    return v.new_empty(B, H, (L + 63) // 64, D, 64, dtype=torch.bfloat16)
-
-
-@_op("value_tiles_rows_", mutates_args=("v_tiles",))
-def value_tiles_rows_(v: Tensor, v_tiles: Tensor, positions: Tensor) -> None:
-    _value_tiles_rows_impl(v, v_tiles, positions)
-
-
-@value_tiles_rows_.register_fake
-def _(v, v_tiles, positions):
-    return None
 
 
 # -- K / V fragments --------------------------------------------------------
@@ -86,15 +63,16 @@ def _(k, v, kv_frags, positions):
 
 # -- window attention -----------------------------------------------------
 @_op("local_attention")
-def local_attention(q: Tensor, k: Tensor, v_tiles: Tensor, key_valid: Optional[Tensor],
+def local_attention(q: Tensor, kv_frags: Tensor, key_valid: Optional[Tensor], kv_len: int,
                     flash_window: int, inert_chunk: int, query_positions: Optional[Tensor],
                     sm_scale: float, parts: int) -> tuple[Tensor, Tensor]:
-    return _local_attention_impl(q, k, v_tiles, key_valid, flash_window, inert_chunk,
+    return _local_attention_impl(q, kv_frags, key_valid, kv_len, flash_window, inert_chunk,
                                  query_positions, sm_scale, parts)
 
 
 @local_attention.register_fake
-def _(q, k, v_tiles, key_valid, flash_window, inert_chunk, query_positions, sm_scale, parts):
+def _(q, kv_frags, key_valid, kv_len, flash_window, inert_chunk, query_positions, sm_scale,
+      parts):
     B, Lq, Hq, D = q.shape
     return (q.new_empty(B, Lq, Hq, D, dtype=torch.bfloat16),
             q.new_empty(B, Lq, Hq, dtype=torch.float32))
@@ -280,7 +258,7 @@ def _(ranking, token_budget, as_int8):
 
 
 OPERATORS = (
-    "value_tiles", "value_tiles_rows_", "kv_fragments", "kv_fragments_rows_", "local_attention", "chunk_attn_pool",
+    "kv_fragments", "kv_fragments_rows_", "local_attention", "chunk_attn_pool",
     "chunk_attn_pool_bwd", "route_topk", "route_weights", "route_weights_bwd",
     "selected_attention", "fuse_hils_outputs", "fuse_hils_outputs_bwd", "remote_drop_mask",
     "remote_drop_mask_rows", "candidate_token_scores", "token_keep",

@@ -41,7 +41,7 @@ from .local_attention import local_attention_launch
 from .pool import chunk_attn_pool_gqa_prior
 from .route_weights import route_weights_launch
 from .sparse_attention import (FRAG_ELEMS, kv_fragments, kv_fragments_rows,
-                               selected_attention_launch, value_tiles, value_tiles_rows)
+                               selected_attention_launch)
 from .token_refinement import refine_remote_tokens_g7
 from .topk import route_topk_launch
 
@@ -121,12 +121,11 @@ def route_attention(
         kv_bool = key_valid.to(device=q.device, dtype=torch.bool).contiguous()
 
     _mark("start")
-    vt = value_tiles(v)
     frags = kv_fragments(k, v)
-    _mark("value_tiles")
+    _mark("kv_fragments")
     flash_window = cfg.local_window + S - 1 if cfg.skip_inert_slots else cfg.local_window
     local_out, local_lse = local_attention_launch(
-        q, k, vt, kv_bool, flash_window, S if cfg.skip_inert_slots else 0
+        q, frags, kv_bool, flash_window, S if cfg.skip_inert_slots else 0
     )
     _mark("local_attention")
     q_lmk = route_q[:, S - 1 :: S].reshape(B, C, Hkv, G, D)
@@ -210,8 +209,8 @@ def swa_attention(
         raise ValueError("swa_attention requires CUDA bf16 tensors")
     flash_window = window + chunk_size - 1 if skip_inert_slots else window
     out, _ = local_attention_launch(
-        q, k, value_tiles(v), key_valid, flash_window,
-        chunk_size if skip_inert_slots else 0,
+        q, kv_fragments(k, v), key_valid, flash_window,
+        chunk_size if skip_inert_slots else 0, kv_len=k.shape[1],
     )
     return out
 
@@ -223,11 +222,10 @@ class LayerKVCache:
     key_valid bool [1, L], landmark_keys bf16 [1, C, Hkv, G, D] and prior_bias
     fp32 [1, C, Hkv, G] (the last two refreshed in place).
 
-    ``value_tiles`` (the tiled copy of ``value`` the window attention reads)
-    and ``kv_frags`` (the ``kv_fragments`` layout of key and value the routed
-    attention reads) are built on first use.  ``replace`` keeps them in step
-    with the rows it writes; after writing ``key`` or ``value`` any other
-    way, set both to None.
+    ``kv_frags`` (the ``kv_fragments`` layout of key and value both attention
+    kernels read) is built on first use.  ``replace`` keeps it in step with
+    the rows it writes; after writing ``key`` or ``value`` any other way,
+    set it to None.
     """
 
     key: torch.Tensor
@@ -235,7 +233,6 @@ class LayerKVCache:
     key_valid: torch.Tensor
     landmark_keys: torch.Tensor
     prior_bias: torch.Tensor
-    value_tiles: torch.Tensor | None = field(default=None, repr=False)
     kv_frags: torch.Tensor | None = field(default=None, repr=False)
 
     @property
@@ -271,8 +268,6 @@ class LayerKVCache:
             raise ValueError("replacement K/V device must match the cache")
         self.key.index_copy_(1, positions, key)
         self.value.index_copy_(1, positions, value)
-        if self.value_tiles is not None:
-            value_tiles_rows(self.value, self.value_tiles, positions)
         if self.kv_frags is not None:
             kv_fragments_rows(self.key, self.value, self.kv_frags, positions)
 
@@ -292,9 +287,6 @@ class LayerKVCache:
             raise ValueError(f"landmark_keys must have shape [B,C,{hkv},G,D]")
         if self.prior_bias.shape != lm[:-1]:
             raise ValueError(f"prior_bias must have shape {tuple(lm[:-1])}")
-        if self.value_tiles is not None and self.value_tiles.shape != (
-                batch, hkv, (self.key.shape[1] + 63) // 64, dim, 64):
-            raise ValueError("value_tiles must be value_tiles(value)")
         if self.kv_frags is not None and self.kv_frags.shape != (
                 batch, hkv, (self.key.shape[1] + 63) // 64, FRAG_ELEMS):
             raise ValueError("kv_frags must be kv_fragments(key, value)")
@@ -400,14 +392,11 @@ def _cached_route_body(q, route_q, cache, query_positions, affected_chunks, entr
     G, S = Hq // Hkv, cfg.chunk_size
     C = L // S
     n = affected_chunks.numel()
-    if cache.value_tiles is None:
-        cache.value_tiles = value_tiles(cache.value)
     if cache.kv_frags is None:
         cache.kv_frags = kv_fragments(cache.key, cache.value)
-    vt = cache.value_tiles
     flash_window = cfg.local_window + S - 1 if cfg.skip_inert_slots else cfg.local_window
     local_out, local_lse = local_attention_launch(
-        q, cache.key, vt, cache.key_valid, flash_window, S if cfg.skip_inert_slots else 0,
+        q, cache.kv_frags, cache.key_valid, flash_window, S if cfg.skip_inert_slots else 0,
         query_positions=query_positions,
     )
     if n:
@@ -480,8 +469,6 @@ class CachedBlockStep:
         self.v_rows = torch.zeros_like(self.k_rows)
         self.positions = torch.zeros(block_len, dtype=torch.long, device=dev)
         self._graphs = {}  # affected count -> (graph, affected buffer, output)
-        if cache.value_tiles is None:
-            cache.value_tiles = value_tiles(cache.value)
         if cache.kv_frags is None:
             cache.kv_frags = kv_fragments(cache.key, cache.value)
 
@@ -489,7 +476,6 @@ class CachedBlockStep:
         c = self.cache
         c.key.index_copy_(1, self.positions, self.k_rows)
         c.value.index_copy_(1, self.positions, self.v_rows)
-        value_tiles_rows(c.value, c.value_tiles, self.positions)
         kv_fragments_rows(c.key, c.value, c.kv_frags, self.positions)
         return _cached_route_body(self.q, self.route_q, c, self.positions, affected, self.scale,
                                   self.cfg)

@@ -1,9 +1,9 @@
-"""Routed chunk attention and the K / V layouts the attention kernels read.
+"""Routed chunk attention and the K / V layout both attention kernels read.
 
 Drop-in for ``ops.hils_fwd_bwd_head.HiLS_block_M_head``
 (ops/hils_fwd_bwd_head.py:1113-1150) in its forward role, plus
-``value_tiles`` (the tiled V the window attention reads) and
-``kv_fragments`` (the per-chunk operand images the routed attention reads).
+``kv_fragments`` (the per-chunk operand images the routed and window
+attention kernels read).
 """
 
 from __future__ import annotations
@@ -13,27 +13,6 @@ import math
 import torch
 
 from . import _lib
-
-
-def value_tiles(v: torch.Tensor) -> torch.Tensor:
-    """V [B, L, Hkv, D] bf16 -> 64-key tiles stored transposed [B, Hkv, ceil(L/64), D, 64].
-
-    Inside a tile row, key 32a + 16b + 4c + e (a, b in {0,1}; c, e in 0..3) sits
-    at position 32a + 8c + 4b + e, the order the matrix-core kernels read it in.
-    """
-
-    if v.device.type != "cuda" or v.dtype != torch.bfloat16 or v.ndim != 4:
-        raise ValueError("value_tiles requires a CUDA BF16 [B, L, Hkv, D] tensor")
-    return torch.ops.mrsa.value_tiles(v)
-
-
-def _value_tiles_impl(v: torch.Tensor) -> torch.Tensor:
-    B, L, H, D = v.shape
-    vc = v.contiguous()
-    out = torch.empty(B, H, (L + 63) // 64, D, 64, dtype=torch.bfloat16, device=v.device)
-    st = _lib.call("mrsa_value_tiles", _lib.ptr(vc), B, L, H, D, _lib.ptr(out), _lib.stream_of(vc))
-    _lib.check(st, "value_tiles")
-    return out
 
 
 FRAG_ELEMS = 16384  # bf16 per (batch, KV head, 64-key chunk)
@@ -114,27 +93,6 @@ def walk_parts(batch: int, q_len: int, kv_heads: int, kv_len: int, topk: int,
     steps = min(kv_len // chunk_size, min(_SEL_TILE_QUERIES, q_len) * topk)
     parts = min(_SEL_MAX_PARTS, 512 // walks, steps // 16, 65535 // max(batch, 1))
     return max(1, parts)
-
-
-def value_tiles_rows(v: torch.Tensor, v_tiles: torch.Tensor, positions: torch.Tensor) -> None:
-    """Rewrite the tiles of rows ``positions`` of v in ``v_tiles`` (in place),
-    after those rows of v were replaced.  Positions outside [0, L) are ignored."""
-
-    if v.device.type != "cuda" or v.dtype != torch.bfloat16 or v.ndim != 4:
-        raise ValueError("value_tiles_rows requires a CUDA BF16 [B, L, Hkv, D] tensor")
-    B, L, H, D = v.shape
-    if v_tiles.shape != (B, H, (L + 63) // 64, D, 64) or not v_tiles.is_contiguous():
-        raise ValueError("v_tiles must be the contiguous value_tiles(v) layout")
-    torch.ops.mrsa.value_tiles_rows_(v, v_tiles, positions)
-
-
-def _value_tiles_rows_impl(v: torch.Tensor, v_tiles: torch.Tensor, positions: torch.Tensor) -> None:
-    B, L, H, D = v.shape
-    vc = v.contiguous()
-    pos = positions.to(device=v.device, dtype=torch.long).contiguous()
-    st = _lib.call("mrsa_value_tiles_rows", _lib.ptr(vc), B, L, H, D, _lib.ptr(pos),
-                   pos.numel(), _lib.ptr(v_tiles), _lib.stream_of(vc))
-    _lib.check(st, "value_tiles_rows")
 
 
 def selected_attention_launch(

@@ -31,7 +31,7 @@ def test_header_lists_expected_entry_points():
     for expected in (
         "mrsa_chunk_attn_pool_gqa_fwd", "mrsa_remote_drop_mask", "mrsa_route_topk_fwd",
         "mrsa_route_weights_fwd", "mrsa_local_attention_fwd", "mrsa_selected_attention_fwd",
-        "mrsa_fuse_hils_outputs_fwd", "mrsa_candidate_token_scores_fwd", "mrsa_value_tiles",
+        "mrsa_fuse_hils_outputs_fwd", "mrsa_candidate_token_scores_fwd",
         "mrsa_kv_fragments", "mrsa_kv_fragments_rows",
     ):
         assert expected in names
@@ -65,7 +65,7 @@ def test_host_side_argument_errors(lib):
     assert L.call("mrsa_remote_drop_mask", None, None, 1, 100, 256, 64, None, None) == 1
     assert L.call("mrsa_chunk_attn_pool_gqa_fwd", None, None, None, 4, 64, 4, 17, 128,
                   1.0, 0, None, None, None, None, None) == 1
-    assert L.call("mrsa_local_attention_fwd", 16, 16, 16, None, None, 1, 64, 64, 28, 4, 96,
+    assert L.call("mrsa_local_attention_fwd", 16, 16, None, None, 1, 64, 64, 28, 4, 96,
                   256, 0, 1.0, 16, 16, None) == 2          # head_dim 96 unsupported
     assert L.call("mrsa_selected_attention_fwd", 16, 16, 16, 16, None, 1, 64, 128, 28, 4,
                   128, 32, 32, 1, 1.0, 16, None) == 2      # chunk_size 32 unsupported
@@ -84,7 +84,6 @@ def test_host_side_argument_errors(lib):
                   28, 4, 128, 32, 64, 1, 1.0, 4, None, 16, None) == 1
     assert L.call("mrsa_selected_attention_split_fwd", 16, 16, 16, 16, None, 2000, 64,
                   128, 28, 4, 128, 32, 64, 1, 1.0, 40, 16, 16, None) == 2  # batch * parts
-    assert L.call("mrsa_value_tiles_bytes", 1, 65, 4, 128) == 1 * 4 * 2 * 128 * 64 * 2
     assert L.call("mrsa_kv_fragments_bytes", 2, 65, 4, 128) == 2 * 4 * 2 * 16384 * 2
     assert L.call("mrsa_kv_fragments_bytes", 1, 64, 4, 96) == -1
     assert L.call("mrsa_kv_fragments", 16, None, 1, 64, 4, 96, 16, None) == 2  # head_dim 96

@@ -56,7 +56,7 @@ def test_config3_swa_full_size_sampled_rows():
     k = _yarn_rotate(torch.randn(1, L, Hkv, D, generator=g)).bfloat16()
     v = torch.randn(1, L, Hkv, D, generator=g).bfloat16()
     dq, dk, dv = q.to(DEV), k.to(DEV), v.to(DEV)
-    out, lse = local_attention_launch(dq, dk, mrsa.value_tiles(dv), None, W, 0)
+    out, lse = local_attention_launch(dq, mrsa.kv_fragments(dk, dv), None, W, 0)
     swa = mrsa.swa_attention(dq, dk, dv, None, W, 64)
     torch.cuda.synchronize()
     assert torch.equal(swa.view(torch.int16), out.view(torch.int16))

@@ -129,18 +129,6 @@ def test_cached_refresh_matches_prefill():
     assert float(error) < 0.03
 
 
-def test_value_tiles_rows_bit_exact():
-    _note("value tiles rows")
-    L, Hkv, D = 1000, 4, 128   # last tile partial
-    g = torch.Generator().manual_seed(90)
-    v = torch.randn(1, L, Hkv, D, generator=g).bfloat16().to(DEV)
-    vt = mrsa.value_tiles(v)
-    pos = torch.tensor([0, 5, 63, 64, 500, 999], device=DEV)
-    v.index_copy_(1, pos, torch.randn(1, pos.numel(), Hkv, D, generator=g).bfloat16().to(DEV))
-    mrsa.sparse_attention.value_tiles_rows(v, vt, pos)
-    assert torch.equal(vt, mrsa.value_tiles(v))
-
-
 def test_kv_fragments_rows_bit_exact():
     _note("kv fragments rows")
     L, Hkv, D = 1000, 4, 128   # last chunk partial
@@ -172,8 +160,8 @@ def test_cache_replace_keeps_tiles_and_checks_arguments():
     rows = torch.arange(L - 2 * S, L - S, device=DEV)
     empty = torch.empty(0, dtype=torch.long, device=DEV)
     qb, rqb = q[:, rows.cpu()].to(DEV), rq[:, rows.cpu()].to(DEV)
-    mrsa.cached_route_attention(qb, rqb, cache, rows, empty, scale)   # builds the tiles
-    assert cache.value_tiles is not None
+    mrsa.cached_route_attention(qb, rqb, cache, rows, empty, scale)   # builds the fragments
+    assert cache.kv_frags is not None
     kb = torch.randn(1, S, Hkv, D, generator=g).bfloat16().to(DEV)
     vb = torch.randn(1, S, Hkv, D, generator=g).bfloat16().to(DEV)
     cache.replace(rows, kb, vb)
@@ -181,7 +169,6 @@ def test_cache_replace_keeps_tiles_and_checks_arguments():
     fresh = mrsa.LayerKVCache(cache.key.clone(), cache.value.clone(), valid, lmk.clone(),
                               prior.clone())
     want = mrsa.cached_route_attention(qb, rqb, fresh, rows, empty, scale)
-    assert torch.equal(cache.value_tiles, fresh.value_tiles)
     assert torch.equal(cache.kv_frags, fresh.kv_frags)
     assert_nearly_identical(got, want, "replaced cache vs fresh cache", atol=0.03)
     with pytest.raises(ValueError, match="unique"):
@@ -247,7 +234,7 @@ def test_cached_block_step_graph_replays_match_eager():
         want = mrsa.cached_route_attention(q, rq, eager, pos, aff, scale)
         torch.cuda.synchronize()
         assert_nearly_identical(got, want, f"block {i}: graph vs eager", atol=0.03)
-    for name in ("key", "value", "value_tiles", "kv_frags", "landmark_keys", "prior_bias"):
+    for name in ("key", "value", "kv_frags", "landmark_keys", "prior_bias"):
         assert torch.equal(getattr(graphed, name), getattr(eager, name)), name
     with pytest.raises(ValueError, match="sorted"):
         step(q, rq, kb, vb, pos.flip(0), aff)

@@ -36,8 +36,8 @@ def _rand(shape, seed, scale=1.0):
 def _planted_kv(L, Hkv, D, seed, sigma=0.3):
     g = torch.Generator().manual_seed(seed)
     k = torch.randn(1, L, Hkv, D, generator=g)
-    shift = sigma * torch.randn(L // 64, Hkv, D, generator=g)
-    k = k + shift.repeat_interleave(64, dim=0)[None]
+    shift = sigma * torch.randn(-(-L // 64), Hkv, D, generator=g)
+    k = k + shift.repeat_interleave(64, dim=0)[None, :L]
     v = torch.randn(1, L, Hkv, D, generator=g)
     return k.bfloat16(), v.bfloat16()
 
@@ -100,20 +100,6 @@ def test_drop_mask_bit_exact():
     for W, al in ((256, None), (100, allowed)):
         got = mrsa.remote_drop_mask(valid.to(DEV), W, 64, None if al is None else al.to(DEV))
         assert torch.equal(got.cpu(), O.remote_drop_mask(valid, W, 64, al))
-
-
-def test_value_tiles_layout():
-    _note("value tiles")
-    v = _rand((2, 200, 3, 128), 5).bfloat16()
-    t = mrsa.value_tiles(v.to(DEV)).cpu()
-    vp = torch.zeros(2, 256, 3, 128).bfloat16()
-    vp[:, :200] = v
-    expect = vp.reshape(2, 4, 64, 3, 128).permute(0, 3, 1, 4, 2)
-    # position 32a + 8c + 4b + e holds key 32a + 16b + 4c + e
-    key_of_pos = [32 * (p // 32) + 16 * ((p // 4) % 2) + 4 * ((p // 8) % 4) + p % 4
-                  for p in range(64)]
-    assert sorted(key_of_pos) == list(range(64))
-    assert torch.equal(t, expect[..., key_of_pos])
 
 
 def _fragments_expected(k, v):
@@ -334,15 +320,17 @@ def test_route_weights_vs_oracle(affine, K):
             atol=2e-3, rtol=1e-2)
 
 
-@pytest.mark.parametrize("L,W,inert,G", [(1024, 319, 64, 7), (2048, 1280, 0, 7), (512, 100, 64, 8)])
+@pytest.mark.parametrize("L,W,inert,G", [(1024, 319, 64, 7), (2048, 1280, 0, 7), (512, 100, 64, 8),
+                                         (1000, 200, 0, 7)])
 def test_local_attention_vs_oracle(L, W, inert, G):
     _note(f"local attention L={L} W={W} inert={inert} G={G}")
     Hkv, D = 4, 128
     q = _rand((1, L, Hkv * G, D), 30).bfloat16()
     k, v = _planted_kv(L, Hkv, D, 31)
     valid = torch.rand(1, L) > 0.05
+    # L = 1000: the last fragment tile is partial (keys past L are not keys)
     out, lse = local_attention_launch(
-        q.to(DEV), k.to(DEV), mrsa.value_tiles(v.to(DEV)), valid.to(DEV), W, inert)
+        q.to(DEV), mrsa.kv_fragments(k.to(DEV), v.to(DEV)), valid.to(DEV), W, inert)
     ro, rl = O.local_attention(q, k, v, valid, W, inert)
     _assert_close_attn(out, ro, f"local L={L} W={W}")
     torch.testing.assert_close(lse.cpu(), rl, atol=2e-3, rtol=1e-4)
@@ -362,7 +350,7 @@ def test_local_attention_key_split(parts, first):
     k, v = _planted_kv(L, Hkv, D, 34)
     valid = torch.rand(1, L, generator=torch.Generator().manual_seed(35)) > 0.05
     out, lse = local_attention_launch(
-        q.to(DEV), k.to(DEV), mrsa.value_tiles(v.to(DEV)), valid.to(DEV), W, 64,
+        q.to(DEV), mrsa.kv_fragments(k.to(DEV), v.to(DEV)), valid.to(DEV), W, 64,
         query_positions=pos.to(DEV), parts=parts)
     ro, rl = O.local_attention(q, k, v, valid, W, 64, query_positions=pos)
     _assert_close_attn(out, ro, f"local split parts={parts}")

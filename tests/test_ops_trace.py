@@ -45,7 +45,7 @@ def test_route_layer_exports_as_one_graph(topk):
         ep = torch.export.export(_RouteLayer(cfg), args, strict=True)
     called = {n.target for n in ep.graph.nodes if n.op == "call_function"}
     names = {str(t) for t in called}
-    for op in ("value_tiles", "kv_fragments", "local_attention", "chunk_attn_pool", "route_topk",
+    for op in ("kv_fragments", "local_attention", "chunk_attn_pool", "route_topk",
                "route_weights", "selected_attention"):
         assert f"mrsa.{op}.default" in names, (op, sorted(names))
     out = [n for n in ep.graph.nodes if n.op == "output"][0]
