@@ -85,6 +85,23 @@ int mrsa_chunk_attn_pool_gqa_fwd(const void* mu_q, const void* k_chunked,
                                  float* prior_bias, void* stream);
 
 /*
+ * The same pool reading the landmark queries in place: query row of
+ * batch-chunk bc at mu_q + bc * mu_row_stride elements (each row holds
+ * [kv_heads][groups][head_dim] contiguous), so the mask-token rows of the
+ * route queries [B, L, Hq, D] (mu_q = route_q + (chunk_size - 1) * Hq * D,
+ * mu_row_stride = chunk_size * Hq * D) need no gather.  No reference
+ * counterpart (the reference gathers the rows with a strided slice first).
+ * mu_row_stride >= kv_heads * groups * head_dim.
+ */
+int mrsa_chunk_attn_pool_gqa_strided_fwd(const void* mu_q, int64_t mu_row_stride,
+                                         const void* k_chunked, const uint8_t* key_valid,
+                                         int64_t batch_chunks, int64_t chunk_size,
+                                         int64_t kv_heads, int64_t groups, int64_t head_dim,
+                                         float sm_scale, int dense_torch_semantics,
+                                         const float* bias_scale, void* landmark_keys,
+                                         float* entropy, float* prior_bias, void* stream);
+
+/*
  * Backward of the landmark pool; the probabilities are recomputed from mu_q
  * and K.  Replaces _ChunkAttnPoolGQA.backward
  * (ops/chunk_attn_pool_gqa_tilelang.py:355-394, kernel _pool_gqa_bwd :183-325)

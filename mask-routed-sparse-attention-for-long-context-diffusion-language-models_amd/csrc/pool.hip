@@ -24,8 +24,9 @@ namespace {
 constexpr int kThreads = 256;
 
 __global__ void __launch_bounds__(kThreads)
-    pool_kernel(const uint16_t* __restrict__ mu_q, const uint16_t* __restrict__ kc,
-                const uint8_t* __restrict__ key_valid, int S, int H, int G, int D,
+    pool_kernel(const uint16_t* __restrict__ mu_q, int64_t mu_stride,
+                const uint16_t* __restrict__ kc, const uint8_t* __restrict__ key_valid, int S,
+                int H, int G, int D,
                 float sm_scale, int dense, const float* __restrict__ bias_scale,
                 uint16_t* __restrict__ lmk, float* __restrict__ entropy,
                 float* __restrict__ prior) {
@@ -50,7 +51,7 @@ __global__ void __launch_bounds__(kThreads)
     reinterpret_cast<u32x4_t*>(ks + s * D)[c] = *src;
   }
   for (int e = tid; e < G * D; e += kThreads)
-    qs[e] = bf16_to_f32(mu_q[((bc * H + h) * G) * (int64_t)D + e]);
+    qs[e] = bf16_to_f32(mu_q[bc * mu_stride + (int64_t)(h * G) * D + e]);
   if (tid == 0) flag[0] = 0;
   for (int s = tid; s < S; s += kThreads) vs[s] = key_valid[bc * S + s] != 0;
   __syncthreads();
@@ -156,16 +157,17 @@ __global__ void __launch_bounds__(kThreads)
 
 }  // namespace
 
-extern "C" int mrsa_chunk_attn_pool_gqa_fwd(const void* mu_q, const void* k_chunked,
-                                            const uint8_t* key_valid, int64_t batch_chunks,
-                                            int64_t chunk_size, int64_t kv_heads, int64_t groups,
-                                            int64_t head_dim, float sm_scale,
-                                            int dense_torch_semantics, const float* bias_scale,
-                                            void* landmark_keys, float* entropy,
-                                            float* prior_bias, void* stream) {
+namespace {
+
+int pool_forward(const void* mu_q, int64_t mu_row_stride, const void* k_chunked,
+                 const uint8_t* key_valid, int64_t batch_chunks, int64_t chunk_size,
+                 int64_t kv_heads, int64_t groups, int64_t head_dim, float sm_scale,
+                 int dense_torch_semantics, const float* bias_scale, void* landmark_keys,
+                 float* entropy, float* prior_bias, void* stream) {
   if (batch_chunks < 0 || chunk_size < 2 || chunk_size > 128 || kv_heads <= 0 || groups <= 0 ||
       groups > 16 || head_dim <= 0 || head_dim > 256 || head_dim % 8 != 0)
     return MRSA_ERR_INVALID_ARGUMENT;
+  if (mu_row_stride < kv_heads * groups * head_dim) return MRSA_ERR_INVALID_ARGUMENT;
   if ((prior_bias != nullptr) != (bias_scale != nullptr)) return MRSA_ERR_INVALID_ARGUMENT;
   if (batch_chunks == 0) return MRSA_OK;
   if (!mu_q || !k_chunked || !key_valid || !landmark_keys || !entropy)
@@ -180,10 +182,35 @@ extern "C" int mrsa_chunk_attn_pool_gqa_fwd(const void* mu_q, const void* k_chun
       return MRSA_ERR_UNSUPPORTED;
   }
   hipLaunchKernelGGL(pool_kernel, dim3((unsigned)batch_chunks, (unsigned)kv_heads), dim3(kThreads),
-                     smem, (hipStream_t)stream, (const uint16_t*)mu_q, (const uint16_t*)k_chunked,
-                     key_valid, S, (int)kv_heads, G, D, sm_scale, dense_torch_semantics, bias_scale,
-                     (uint16_t*)landmark_keys, entropy, prior_bias);
+                     smem, (hipStream_t)stream, (const uint16_t*)mu_q, mu_row_stride,
+                     (const uint16_t*)k_chunked, key_valid, S, (int)kv_heads, G, D, sm_scale,
+                     dense_torch_semantics, bias_scale, (uint16_t*)landmark_keys, entropy,
+                     prior_bias);
   return mrsa_launch_status();
+}
+
+}  // namespace
+
+extern "C" int mrsa_chunk_attn_pool_gqa_fwd(const void* mu_q, const void* k_chunked,
+                                            const uint8_t* key_valid, int64_t batch_chunks,
+                                            int64_t chunk_size, int64_t kv_heads, int64_t groups,
+                                            int64_t head_dim, float sm_scale,
+                                            int dense_torch_semantics, const float* bias_scale,
+                                            void* landmark_keys, float* entropy,
+                                            float* prior_bias, void* stream) {
+  return pool_forward(mu_q, kv_heads * groups * head_dim, k_chunked, key_valid, batch_chunks,
+                      chunk_size, kv_heads, groups, head_dim, sm_scale, dense_torch_semantics,
+                      bias_scale, landmark_keys, entropy, prior_bias, stream);
+}
+
+extern "C" int mrsa_chunk_attn_pool_gqa_strided_fwd(
+    const void* mu_q, int64_t mu_row_stride, const void* k_chunked, const uint8_t* key_valid,
+    int64_t batch_chunks, int64_t chunk_size, int64_t kv_heads, int64_t groups, int64_t head_dim,
+    float sm_scale, int dense_torch_semantics, const float* bias_scale, void* landmark_keys,
+    float* entropy, float* prior_bias, void* stream) {
+  return pool_forward(mu_q, mu_row_stride, k_chunked, key_valid, batch_chunks, chunk_size,
+                      kv_heads, groups, head_dim, sm_scale, dense_torch_semantics, bias_scale,
+                      landmark_keys, entropy, prior_bias, stream);
 }
 
 namespace {

@@ -26,19 +26,12 @@ namespace {
 constexpr int kMaxTopk = 64;
 
 template <int LPR, bool VEC>
-__global__ void __launch_bounds__(256)
-    route_weights_kernel(const uint16_t* __restrict__ scores, const int32_t* __restrict__ indices,
-                         const float* __restrict__ bias, const float* __restrict__ lse,
-                         int64_t rows, int64_t L, int64_t C, int Hkv, int G, int K, float inv_t,
-                         const float* __restrict__ goff, const float* __restrict__ gsc,
-                         uint16_t* __restrict__ rw, uint16_t* __restrict__ lw,
-                         float* __restrict__ gate_logit) {
-  // Gate parameters are device scalars (the layer's parameters, read in
-  // place: no host round trip); a null pointer means "not given".
-  const int has_off = goff != nullptr, affine = gsc != nullptr;
-  const float off = has_off ? *goff : 0.f;
-  const float gscale = affine ? *gsc : 1.f;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void route_weights_row(
+    int64_t t, const uint16_t* __restrict__ scores,
+    const int32_t* __restrict__ indices, const float* __restrict__ bias,
+    const float* __restrict__ lse, int64_t rows, int64_t L, int64_t C, int Hkv, int G, int K,
+    float inv_t, int has_off, int affine, float off, float gscale, uint16_t* __restrict__ rw,
+    uint16_t* __restrict__ lw, float* __restrict__ gate_logit) {
   const int part = (int)(t % LPR);
   const int64_t r0 = t / LPR;
   const bool live = r0 < rows;
@@ -98,6 +91,9 @@ __global__ void __launch_bounds__(256)
   // gate_logit (attention.py:196-235): lse(remote logits) - local logit, then
   // gate_scale * (.) + gate_offset in the affine form; 0 when every logit is
   // masked.  -inf (or its affine image) when only the remote ones are.
+  // Exponentials and logarithms run in base 2 on the hardware instructions
+  // (exp(y) = 2^(y log2 e)), quotients as products with the hardware
+  // reciprocal: within a few fp32 ulps of the exact softmax.
   float gl_val = 0.f;
   const float m = fmaxf(rmax, local);
   if (m == neg_inf()) {  // every logit masked: both outputs zero
@@ -108,25 +104,29 @@ __global__ void __launch_bounds__(256)
       // Remote LSE against its own max (torch.logsumexp's form), so a local
       // logit far above the remote ones cannot underflow it.
       float rs = 0.f;
+      const float rb = rmax * kLog2e;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) rs += x[j] == neg_inf() ? 0.f : expf(x[j] - rmax);
+      for (int j = 0; j < 8; ++j)
+        rs += x[j] == neg_inf() ? 0.f : exp2_hw(__builtin_fmaf(x[j], kLog2e, -rb));
 #pragma unroll
       for (int o = 1; o < LPR; o <<= 1) rs += __shfl_xor(rs, o, 64);
-      gl_val = (rmax == neg_inf() ? neg_inf() : rmax + logf(rs)) - local;
+      gl_val = (rmax == neg_inf() ? neg_inf() : rmax + log2_hw(rs) * kLn2) - local;
     }
+    const float mb = m * kLog2e;
     float sum = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      x[j] = x[j] == neg_inf() ? 0.f : expf(x[j] - m);
+      x[j] = exp2_hw(__builtin_fmaf(x[j], kLog2e, -mb));  // -inf -> 0
       sum += x[j];
     }
 #pragma unroll
     for (int o = 1; o < LPR; o <<= 1) sum += __shfl_xor(sum, o, 64);
-    const float el = local == neg_inf() ? 0.f : expf(local - m);
+    const float el = exp2_hw(__builtin_fmaf(local, kLog2e, -mb));
     sum += el;
+    const float inv = rcp_hw(sum);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = x[j] / sum;
-    lw_val = el / sum;
+    for (int j = 0; j < 8; ++j) x[j] *= inv;
+    lw_val = el * inv;
   } else if (rmax == neg_inf()) {
     // Affine gate with no routed chunk: remote softmax zeroed, gate -> local.
 #pragma unroll
@@ -134,19 +134,21 @@ __global__ void __launch_bounds__(256)
     lw_val = 1.f;
     gl_val = gscale * (neg_inf() - local) + off;
   } else {
+    const float rb = rmax * kLog2e;
     float sum = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      x[j] = x[j] == neg_inf() ? 0.f : expf(x[j] - rmax);
+      x[j] = exp2_hw(__builtin_fmaf(x[j], kLog2e, -rb));  // -inf -> 0
       sum += x[j];
     }
 #pragma unroll
     for (int o = 1; o < LPR; o <<= 1) sum += __shfl_xor(sum, o, 64);
-    const float remote_lse = rmax + logf(sum);
+    const float remote_lse = rmax + log2_hw(sum) * kLn2;
     const float gate = gscale * (remote_lse - local) + off;
-    const float mass = 1.f / (1.f + expf(-gate));
+    const float mass = rcp_hw(1.f + exp2_hw(-gate * kLog2e));
+    const float f = rcp_hw(sum) * mass;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = (x[j] / sum) * mass;
+    for (int j = 0; j < 8; ++j) x[j] *= f;
     lw_val = 1.f - mass;
     gl_val = gate;
   }
@@ -164,6 +166,24 @@ __global__ void __launch_bounds__(256)
       if (k0 + j < K) out[j] = (uint16_t)f32_to_bf16(x[j]);
   }
   if (part == 0) lw[r] = (uint16_t)f32_to_bf16(lw_val);
+}
+
+template <int LPR, bool VEC>
+__global__ void __launch_bounds__(256)
+    route_weights_kernel(const uint16_t* __restrict__ scores, const int32_t* __restrict__ indices,
+                         const float* __restrict__ bias, const float* __restrict__ lse,
+                         int64_t rows, int64_t L, int64_t C, int Hkv, int G, int K, float inv_t,
+                         const float* __restrict__ goff, const float* __restrict__ gsc,
+                         uint16_t* __restrict__ rw, uint16_t* __restrict__ lw,
+                         float* __restrict__ gate_logit) {
+  // Gate parameters are device scalars (the layer's parameters, read in
+  // place: no host round trip); a null pointer means "not given".
+  const int has_off = goff != nullptr, affine = gsc != nullptr;
+  const float off = has_off ? *goff : 0.f;
+  const float gscale = affine ? *gsc : 1.f;
+  route_weights_row<LPR, VEC>((int64_t)blockIdx.x * blockDim.x + threadIdx.x, scores, indices,
+                              bias, lse, rows, L, C, Hkv, G, K, inv_t, has_off, affine, off,
+                              gscale, rw, lw, gate_logit);
 }
 
 template <int LPR>

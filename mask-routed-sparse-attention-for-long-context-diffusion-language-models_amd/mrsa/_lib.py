@@ -42,6 +42,10 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _P, _P, _P, _P, _P],
     ),
+    "mrsa_chunk_attn_pool_gqa_strided_fwd": (
+        _I,
+        [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _P, _P, _P, _P, _P],
+    ),
     "mrsa_chunk_attn_pool_gqa_bwd": (
         _I,
         [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _P, _P, _P],

@@ -91,7 +91,7 @@ def _(mu_q, k_chunked, key_valid, sm_scale, bias_scale):
     entropy = mu_q.new_empty(B, C, H, G, dtype=torch.float32)
     prior = (entropy.new_empty(B, C, H, G) if bias_scale is not None
              else entropy.new_empty(0))
-    return torch.empty_like(mu_q), entropy, prior
+    return mu_q.new_empty(mu_q.shape, dtype=torch.bfloat16), entropy, prior
 
 
 @_op("chunk_attn_pool_bwd")

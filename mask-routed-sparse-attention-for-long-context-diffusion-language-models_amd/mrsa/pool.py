@@ -51,10 +51,19 @@ def _pool_impl(mu_q, k_chunked, key_valid, sm_scale, bias_scale):
     """Kernel call; the prior output is empty without a bias scale."""
     batch, chunks, kv_heads, groups, head_dim = mu_q.shape
     chunk_size = k_chunked.shape[2]
-    mu = mu_q.contiguous()
+    # Query rows are read in place when each row's [Hkv, G, D] is contiguous
+    # and batch and chunk fold into one row stride (e.g. the mask-token rows
+    # route_q[:, S - 1::S] of the route queries): no gather copy.
+    st_ = mu_q.stride()
+    inner = st_[4] == 1 and st_[3] == head_dim and st_[2] == groups * head_dim
+    folds = batch == 1 or st_[0] == chunks * st_[1]
+    if inner and folds and st_[1] >= kv_heads * groups * head_dim and mu_q.dtype == torch.bfloat16:
+        mu, row_stride = mu_q, st_[1]
+    else:
+        mu, row_stride = mu_q.contiguous(), kv_heads * groups * head_dim
     kc = k_chunked.contiguous()
     kv = key_valid.to(device=mu_q.device, dtype=torch.bool).contiguous()
-    lmk = torch.empty_like(mu)
+    lmk = torch.empty(mu_q.shape, dtype=torch.bfloat16, device=mu_q.device)
     entropy = torch.empty(
         batch, chunks, kv_heads, groups, device=mu.device, dtype=torch.float32
     )
@@ -64,8 +73,8 @@ def _pool_impl(mu_q, k_chunked, key_valid, sm_scale, bias_scale):
         scale = bias_scale.to(device=mu.device, dtype=torch.float32).contiguous()
         prior = torch.empty_like(entropy)
     st = _lib.call(
-        "mrsa_chunk_attn_pool_gqa_fwd",
-        _lib.ptr(mu), _lib.ptr(kc), _lib.ptr(kv),
+        "mrsa_chunk_attn_pool_gqa_strided_fwd",
+        _lib.ptr(mu), int(row_stride), _lib.ptr(kc), _lib.ptr(kv),
         batch * chunks, chunk_size, kv_heads, groups, head_dim,
         float(sm_scale), 1 if groups == 1 else 0,
         _lib.ptr(scale), _lib.ptr(lmk), _lib.ptr(entropy),
