@@ -131,7 +131,7 @@ __host__ __device__ inline RaLayout ra_layout(int tq, int G, int K, int64_t Ck, 
   l.islot = o;   o = al16(o + (size_t)l.items);
   l.iw = o;      o = al16(o + (token ? 0 : (size_t)l.items * 8 * 2));
   l.ikeep = o;   o = al16(o + (keep ? (size_t)l.items * 8 : 0));
-  l.misc = o;    o = al16(o + (size_t)(2 * kWaves + 8) * 4);
+  l.misc = o;    o = al16(o + (size_t)(2 * kWaves + 8 + 64) * 4);
   l.total = o;
   return l;
 }
@@ -266,6 +266,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   uint64_t* it_keep = reinterpret_cast<uint64_t*>(smem + L.ikeep); // [items]
   int32_t* misc = reinterpret_cast<int32_t*>(smem + L.misc);
   uint32_t* lock = reinterpret_cast<uint32_t*>(misc + 2 * kWaves + 1);
+  uint32_t* idle_or = reinterpret_cast<uint32_t*>(misc + 2 * kWaves + 8);  // [64], never read
 
   // ---- prologue: the walk of this tile ----------------------------------
   // 1. Index rows (-1 past the sequence end), list lengths and flags, owner
@@ -429,7 +430,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
 
   // ---- the walk ------------------------------------------------------------
   const int j = lane & 15, grp = lane >> 4;
-  const int own = j & 1, gcol = j >> 1;  // this lane's tile column: owner, head
+  const int own = j >> 3, gcol = j & 7;  // this lane's tile column: owner, head
   const float c2 = a.scale_log2;
   const __amdgpu_buffer_rsrc_t frs =
       make_rsrc(a.kvf + (b * a.Hkv + h) * Ck * kFragElems, (uint32_t)Ck * kFragBytes);
@@ -444,8 +445,13 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   };
   const uint32_t lock_addr = lds_address(lock);
   const int sinkq = tq;  // query slot taking the adds of a missing second owner
-  // this lane's place in a query slot: head 2 grp (+1), dims 4 j (+64)
-  float* const orow = O + (2 * grp) * 128 + 4 * j;
+  // This lane's output row is its column's (query slot, head gcol); its
+  // accumulator nt holds dims 16 nt + 4 grp .. + 3, the 16-byte block
+  // 4 nt + grp of the row, stored at block (4 nt + grp) ^ gcol.  Even nt:
+  // lane_e + 16 nt floats into the slot, odd nt: lane_o + 16 (nt - 1).
+  const int lane_c = gcol * 128 + 4 * ((grp ^ gcol) & 3);
+  const int lane_e = lane_c + 16 * (gcol >> 2);
+  const int lane_o = lane_c + 16 - 16 * (gcol >> 2);
   float ninf_v = neg_inf();
   asm volatile("" : "+v"(ninf_v));  // kept in a register for set_where
 
@@ -488,18 +494,29 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       load_k(kb, frs, flo, (uint32_t)cn * kFragBytes);
     }
     const uint64_t msh = msk >> (4 * grp);  // bit 16 mt + r: key 16 mt + 4 grp + r
+    // First try for the owners' lock bits, issued now so that its LDS round
+    // trip overlaps the softmax (the result is read after it).
+    const uint32_t want = (1u << qa) | (hb ? 1u << qb1 : 0u);
+    // Every lane takes part (no divergent region, so the wait for the
+    // result stays where it is used): lane 0 ORs the bits into the lock word,
+    // the others OR 0 into words of their own.
+    uint32_t first_try = 0u;
+    if constexpr (!TOKEN)
+      first_try = __hip_atomic_fetch_or(lane == 0 ? lock : idle_or + lane,
+                                        lane == 0 && a.spin_limit > 0 ? want : 0u,
+                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 
     if constexpr (TOKEN) {
-      // max over the owner's head columns (lanes j, j ^ 2, j ^ 4, j ^ 8
+      // max over the owner's head columns (lanes j, j ^ 1, j ^ 2, j ^ 4
       // share the owner), excluded keys -inf, times sm_scale.
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float v = gcol < G ? S[mt][r] : neg_inf();
+          v = fmaxf(v, __shfl_xor(v, 1, 64));
           v = fmaxf(v, __shfl_xor(v, 2, 64));
           v = fmaxf(v, __shfl_xor(v, 4, 64));
-          v = fmaxf(v, __shfl_xor(v, 8, 64));
           S[mt][r] = v;
         }
       if (gcol == 0 && o < n) {
@@ -560,27 +577,24 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
         Pb[ks][2] = pack_bf16x2(S[2 * ks + 1][0] * f, S[2 * ks + 1][1] * f);
         Pb[ks][3] = pack_bf16x2(S[2 * ks + 1][2] * f, S[2 * ks + 1][3] * f);
       }
-      // O_tile = P . V: lane (grp, j) gets rows (columns) 4 grp + r, d = 16 nt + j.
-      f32x4_t acc[8];
-#pragma unroll
-      for (int nt = 0; nt < 8; ++nt) {
-        acc[nt] = mfma_bf16_16x16x32(Pb[0], vb[nt][0], zero4());
-        acc[nt] = mfma_bf16_16x16x32(Pb[1], vb[nt][1], acc[nt]);
-      }
-      if constexpr (LAST) load_v(vb, frs, flo, (uint32_t)cn * kFragBytes);
-      // Add into the owners' rows: column 4 grp + r is owner r & 1, head
-      // 2 grp + (r >> 1) (padding heads add zeros into padding rows); a
-      // missing second owner adds into the spare slot.
+      // Add the tile into its owners' rows under the lock: the rows are read
+      // into the accumulators and O^T_tile = V^T . P^T is added onto them
+      // (lane (grp, j): column j, dims 16 nt + 4 grp + r).  A missing second
+      // owner's columns go to the spare slot and padding heads to padding
+      // rows, with P = 0.
       const int qb = hb ? qb1 : sinkq;
-      const uint32_t want = (1u << qa) | (hb ? 1u << qb1 : 0u);
-      float* row[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) row[r] = orow + ((r & 1) ? qb : qa) * 1024 + (r >> 1) * 128;
+      float* const srow = O + (own ? qb : qa) * 1024;
+      float* const pe = srow + lane_e;
+      float* const po = srow + lane_o;
       bool locked = false;
+      asm volatile("" : "+v"(first_try) : "v"(Pb[1][3]));  // read after the softmax
+      uint32_t old = __builtin_amdgcn_readfirstlane(first_try);
       for (int spin = 0; spin < a.spin_limit; ++spin) {
-        uint32_t old = 0u;
-        if (lane == 0) old = lds_or_rtn(lock_addr, want);
-        old = __builtin_amdgcn_readfirstlane(old);
+        if (spin > 0) {
+          old = 0u;
+          if (lane == 0) old = lds_or_rtn(lock_addr, want);
+          old = __builtin_amdgcn_readfirstlane(old);
+        }
         if ((old & want) == 0u) {
           locked = true;
           break;
@@ -588,39 +602,39 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
         if (lane == 0) lds_and(lock_addr, ~(want & ~old));  // undo the bits set now
         __builtin_amdgcn_s_sleep(1);
       }
+      f32x4_t acc[8];
       // The lock word is read back above with lgkmcnt(0): the row reads
       // below are issued after it.
       if (locked) {
-        f32x4_t x[4][2];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          x[r][0] = *reinterpret_cast<const f32x4_t*>(row[r]);
-          x[r][1] = *reinterpret_cast<const f32x4_t*>(row[r] + 64);
+        for (int nt = 0; nt < 8; ++nt)
+          acc[nt] = *reinterpret_cast<const f32x4_t*>((nt & 1) ? po + 16 * (nt - 1) : pe + 16 * nt);
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+          acc[nt] = mfma_bf16_16x16x32(vb[nt][0], Pb[0], acc[nt]);
+          acc[nt] = mfma_bf16_16x16x32(vb[nt][1], Pb[1], acc[nt]);
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            x[r][0][i] += acc[i][r];
-            x[r][1][i] += acc[4 + i][r];
-          }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          *reinterpret_cast<f32x4_t*>(row[r]) = x[r][0];
-          *reinterpret_cast<f32x4_t*>(row[r] + 64) = x[r][1];
-        }
+        for (int nt = 0; nt < 8; ++nt)
+          *reinterpret_cast<f32x4_t*>((nt & 1) ? po + 16 * (nt - 1) : pe + 16 * nt) = acc[nt];
         // The row writes are issued before the release and the LDS
         // completes one wave's operations in order.
         asm volatile("" ::: "memory");
         if (lane == 0) lds_and(lock_addr, ~want);
       } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int nt = 0; nt < 8; ++nt) {
+          acc[nt] = mfma_bf16_16x16x32(vb[nt][0], Pb[0], zero4());
+          acc[nt] = mfma_bf16_16x16x32(vb[nt][1], Pb[1], acc[nt]);
+        }
 #pragma unroll
-          for (int nt = 0; nt < 8; ++nt)
-            __hip_atomic_fetch_add(row[r] + 64 * (nt >> 2) + (nt & 3), acc[nt][r],
+        for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            __hip_atomic_fetch_add(((nt & 1) ? po + 16 * (nt - 1) : pe + 16 * nt) + r, acc[nt][r],
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
+      if constexpr (LAST) load_v(vb, frs, flo, (uint32_t)cn * kFragBytes);
     }
   };
 
@@ -663,16 +677,14 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     for (int e = tid; e < rows * 16; e += kThreads) {
       const int rho = e >> 4, u = e & 15;
       const int qq = rho / G, g = rho - qq * G;
-      // d = 8 u + i = 16 nt + j: nt = u >> 1, j = 8 (u & 1) + i
-      const int nt = u >> 1, j0 = 8 * (u & 1);
-      const float* src = O + (qq * 8 + g) * 128 + 64 * (nt >> 2) + 4 * j0 + (nt & 3);
-      float x[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = src[4 * i];
+      // dims 8 u .. 8 u + 7: blocks 2 u and 2 u + 1, stored at block ^ g
+      const float* src = O + (qq * 8 + g) * 128;
+      const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(src + 4 * ((2 * u) ^ g));
+      const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(src + 4 * ((2 * u + 1) ^ g));
+      const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
       const int64_t row = (b * a.Lq + q0 + qq) * a.Hq + h * G + g;
       if (a.parts > 1) {
         float* prow = a.partial + ((int64_t)part * a.B * a.Lq * a.Hq + row) * 128 + 8 * u;
-        f32x4_t x0 = {x[0], x[1], x[2], x[3]}, x1 = {x[4], x[5], x[6], x[7]};
         reinterpret_cast<f32x4_t*>(prow)[0] = x0;
         reinterpret_cast<f32x4_t*>(prow)[1] = x1;
         continue;
