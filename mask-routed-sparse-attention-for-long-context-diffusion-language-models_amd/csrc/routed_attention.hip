@@ -11,20 +11,22 @@
 // twice contributes once with the two weights summed (rounded to bf16).
 //
 // Work split.  A workgroup owns a tile of TQ (<= 32) queries of one KV head
-// and keeps their fp32 outputs [TQ][G][128] in LDS.  Its prologue turns the
-// tile's index lists into a walk: the ascending list of the chunks any of its
-// queries routes to, and for each such chunk (a step) the items (query,
-// weights) that own it.  Steps are dealt round-robin to the 8 waves.  A wave
-// processes a step on its own:
+// and keeps their fp32 outputs in LDS (a slot of 8 head rows of 128 floats
+// per query, heads >= G padding).  Its prologue turns the tile's index lists
+// into a walk: the ascending list of the chunks any of its queries routes
+// to, and for each such chunk (a step) the items (query, weights) that own
+// it.  Steps are dealt round-robin to the 8 waves.  A wave processes a step
+// on its own:
 //   K and V of the chunk straight into registers from the chunk's
 //   fragments (mrsa_kv_fragments: the operands' register images, so each of
-//   the 32 load instructions reads 1 KB contiguous); the step's owners are packed two per 16-column tile (column
-//   j: owner j & 1, head j >> 1), so a tile's columns are almost all useful;
+//   the 32 load instructions reads 1 KB contiguous); the step's owners are
+//   packed two per 16-column tile (column j: owner j >> 3, head j & 7);
 //   per tile
 //     S^T = K . Q^T                 16 MFMAs (16x16x32 bf16)
 //     per-column softmax over the 64 keys, P = bf16(p w / sum p)
-//     O_tile = P . V                16 MFMAs
-//     O_tile added into the two owners' LDS rows
+//     the owners' LDS rows read into the accumulators (lane (grp, j):
+//     column j, dims 16 nt + 4 grp .. + 3), O^T += V^T . P^T (16 MFMAs)
+//     and the rows written back
 // The next tile's Q and the next step's K / V are loaded into the same
 // registers as soon as the current ones are consumed.  The epilogue barrier
 // turns the LDS outputs into bf16 rows (fused with the local branch when
@@ -34,17 +36,19 @@
 // float atomics (ds_add_f32) run at about two cycles per lane, so instead a
 // wave takes both owners' bits of a per-workgroup lock word (all or nothing:
 // ds_or_rtn, undo on conflict, so no wave ever waits while holding a bit),
-// adds with plain 16-byte reads and writes, and clears the bits.  LDS
-// operations of one wave complete in issue order, so its writes land before
-// its release and after another wave's acquire.  The wait is bounded: past
-// `spin_limit` tries the wave adds that tile with ds_add_f32 instead, which
-// is always correct.  The order of the fp32 additions into a row therefore
-// depends on timing, so the last bit of an output can differ between runs.
+// reads the rows, accumulates onto them and writes them back with 16-byte
+// accesses, and clears the bits.  The first try is issued right after the
+// QK product and its result read after the softmax.  LDS operations of one
+// wave complete in issue order, so its writes land before its release and
+// after another wave's acquire.  The wait is bounded: past `spin_limit`
+// tries the wave adds that tile with ds_add_f32 instead, which is always
+// correct.  The order of the fp32 additions into a row therefore depends on
+// timing, so the last bit of an output can differ between runs.
 //
-// LDS output rows: row (q, g) at q * G + g, 128 floats; element d = 16 nt + j
-// at 64 (nt >> 2) + 4 j + (nt & 3), so the values a lane holds for one row
-// (nt = 0..7 at its j) are two 16-byte vectors and the 16 lanes of a row
-// read 256 contiguous bytes.
+// LDS output rows: row (q, g) of slot q at (8 q + g) * 128 floats; the
+// 16-byte block b of dims 4 b .. 4 b + 3 sits at block b ^ g, so the eight
+// lanes of one 16-byte access per row group (heads 0..7 of one owner) hit
+// eight different bank groups.
 //
 // Token-score mode (candidate_token_scores_gqa,
 // ops/hils_token_score_gqa_tilelang.py:17-114) runs the same walk and writes,
