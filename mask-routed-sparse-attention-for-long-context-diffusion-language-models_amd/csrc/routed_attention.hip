@@ -15,8 +15,8 @@
 // per query, heads >= G padding).  Its prologue turns the tile's index lists
 // into a walk: the ascending list of the chunks any of its queries routes
 // to, and for each such chunk (a step) the items (query, weights) that own
-// it.  Steps are dealt round-robin to the 8 waves.  A wave processes a step
-// on its own:
+// it.  The first 8 steps go to the 8 waves, each later one to the wave that
+// claims it first (an LDS counter), and a wave processes a step on its own:
 //   K and V of the chunk straight into registers from the chunk's
 //   fragments (mrsa_kv_fragments: the operands' register images, so each of
 //   the 32 load instructions reads 1 KB contiguous); the step's owners are
@@ -270,6 +270,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   uint64_t* it_keep = reinterpret_cast<uint64_t*>(smem + L.ikeep); // [items]
   int32_t* misc = reinterpret_cast<int32_t*>(smem + L.misc);
   uint32_t* lock = reinterpret_cast<uint32_t*>(misc + 2 * kWaves + 1);
+  uint32_t* claim = reinterpret_cast<uint32_t*>(misc + 2 * kWaves + 2);  // steps claimed
   uint32_t* idle_or = reinterpret_cast<uint32_t*>(misc + 2 * kWaves + 8);  // [64], never read
 
   // ---- prologue: the walk of this tile ----------------------------------
@@ -283,7 +284,10 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     qlen[i] = K;
     qflag[i] = 0u;
   }
-  if (tid == 0) *lock = 0u;
+  if (tid == 0) {
+    *lock = 0u;
+    *claim = 0u;
+  }
   for (int64_t c = tid; c < Ck; c += kThreads) omask[c] = 0u;
   if constexpr (!TOKEN) {
     const uint16_t* wrow0 = a.w + ((b * a.Lq + q0) * a.Hq + (int64_t)h * G) * K;
@@ -652,7 +656,16 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     load_k(kb, frs, flo, (uint32_t)c * kFragBytes);
     if constexpr (!TOKEN) load_v(vb, frs, flo, (uint32_t)c * kFragBytes);
     while (true) {
-      const int nst = st + kWaves;
+      // Claim the wave's next step (steps after the first kWaves go to
+      // whichever wave asks first); the claim's round trip overlaps the
+      // step's other tiles.  Lane 0 adds 1 to the counter, the other lanes
+      // add 0 to words of their own (no divergent region).
+      const uint32_t tk = __hip_atomic_fetch_add(lane == 0 ? claim : idle_or + lane,
+                                                 lane == 0 ? 1u : 0u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+      const int T = (n + 1) >> 1;
+      for (int t = 0; t + 1 < T; ++t) do_tile(t, std::false_type{});
+      const int nst = st_lo + kWaves + (int)__builtin_amdgcn_readfirstlane(tk);
       more = nst < st_hi;
       cn = c;
       i0n = 0;
@@ -662,8 +675,6 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
         i0n = __builtin_amdgcn_readfirstlane(s_off[nst]);
         nn = __builtin_amdgcn_readfirstlane(s_off[nst + 1]) - i0n;
       }
-      const int T = (n + 1) >> 1;
-      for (int t = 0; t + 1 < T; ++t) do_tile(t, std::false_type{});
       do_tile(T - 1, std::true_type{});
       if (!more) break;
       st = nst;
