@@ -108,7 +108,7 @@ __host__ __device__ inline size_t al16(size_t x) { return (x + 15) & ~(size_t)15
 struct RaLayout {
   size_t o, o_bytes;
   size_t raw, qlen, qflag, wst, omask, step_of, scratch_end;
-  size_t chunk, off, excl, iq, islot, iw, ikeep, misc, total;
+  size_t rec, iq, islot, iw, ikeep, misc, total;
   int items, cap;
 };
 
@@ -128,9 +128,7 @@ __host__ __device__ inline RaLayout ra_layout(int tq, int G, int K, int64_t Ck, 
   l.scratch_end = s;
   l.o = 0;
   size_t o = al16(l.o_bytes > s ? l.o_bytes : s);
-  l.chunk = o;   o = al16(o + (size_t)l.cap * 4);
-  l.off = o;     o = al16(o + (size_t)(l.cap + 1) * 4);
-  l.excl = o;    o = al16(o + (size_t)l.cap * 8);
+  l.rec = o;     o = al16(o + (size_t)l.cap * 16);
   l.iq = o;      o = al16(o + (size_t)l.items);
   l.islot = o;   o = al16(o + (size_t)l.items);
   l.iw = o;      o = al16(o + (token ? 0 : (size_t)l.items * 8 * 2));
@@ -261,9 +259,9 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   uint32_t* omask = reinterpret_cast<uint32_t*>(smem + L.omask);   // [Ck]
   uint16_t* step_of = reinterpret_cast<uint16_t*>(smem + L.step_of);  // [Ck]
   float* O = reinterpret_cast<float*>(smem + L.o);                 // [tq + 1][8][128]
-  int32_t* s_chunk = reinterpret_cast<int32_t*>(smem + L.chunk);   // [cap]
-  int32_t* s_off = reinterpret_cast<int32_t*>(smem + L.off);       // [cap + 1]
-  uint64_t* s_excl = reinterpret_cast<uint64_t*>(smem + L.excl);   // [cap] excluded keys
+  // Step records [cap]: x = chunk | owners << 24, y = first item | the first
+  // tile's two owner slots << 16, (z, w) = excluded keys of the chunk.
+  u32x4_t* s_rec = reinterpret_cast<u32x4_t*>(smem + L.rec);
   uint8_t* it_q = smem + L.iq;                                     // [items]
   uint8_t* it_slot = smem + L.islot;                               // [items]
   uint16_t* it_w = reinterpret_cast<uint16_t*>(smem + L.iw);       // [items][8]
@@ -364,16 +362,16 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     for (int64_t c = c0; c < c1; ++c) {
       const uint32_t m = omask[c];
       if (m) {
-        s_chunk[pos] = (int32_t)c;
-        s_off[pos] = item;
+        s_rec[pos][0] = (uint32_t)c;
+        s_rec[pos][1] = (uint32_t)item;
         step_of[c] = (uint16_t)pos;
         ++pos;
         item += __popc(m);
       }
     }
     if (tid == 0) {
-      s_off[tsteps] = titems;
       misc[2 * kWaves] = tsteps;
+      misc[2 * kWaves + 3] = titems;
     }
   }
   __syncthreads();
@@ -392,7 +390,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       if (!first) continue;
     }
     const uint32_t m = omask[c];
-    const int pos = s_off[step_of[c]] + __popc(m & ((1u << qq) - 1u));
+    const int pos = (int)s_rec[step_of[c]][1] + __popc(m & ((1u << qq) - 1u));
     it_q[pos] = (uint8_t)qq;
     it_slot[pos] = (uint8_t)kk;
     if constexpr (!TOKEN) {
@@ -423,18 +421,31 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   const uint8_t* kvrow = a.key_valid ? a.key_valid + b * a.Lk : nullptr;
   for (int e = tid; e < nsteps; e += kThreads) {
     uint64_t m = a.mask_last ? (1ull << 63) : 0ull;
-    if (kvrow) m |= ~kept_bits(reinterpret_cast<const int8_t*>(kvrow) + (int64_t)s_chunk[e] * 64);
-    s_excl[e] = m;
+    if (kvrow) m |= ~kept_bits(reinterpret_cast<const int8_t*>(kvrow) + (int64_t)s_rec[e][0] * 64);
+    s_rec[e][2] = (uint32_t)m;
+    s_rec[e][3] = (uint32_t)(m >> 32);
   }
   __syncthreads();
+  // Owner count and the first tile's owner slots of every step (a single
+  // owner is listed twice).
+  {
+    const int titems = misc[2 * kWaves + 3];
+    for (int e = tid; e < nsteps; e += kThreads) {
+      const uint32_t i0 = s_rec[e][1];
+      const uint32_t nx = e + 1 < nsteps ? (s_rec[e + 1][1] & 0xffffu) : (uint32_t)titems;
+      const uint32_t cnt = nx - i0;
+      s_rec[e][0] |= cnt << 24;
+      s_rec[e][1] = i0 | ((uint32_t)it_q[i0] << 16) | ((uint32_t)it_q[i0 + (cnt > 1u)] << 24);
+    }
+  }
   const int st_lo = (int)((int64_t)part * nsteps / a.parts);
   const int st_hi = (int)((int64_t)(part + 1) * nsteps / a.parts);
   // 6. Outputs start at zero (the scratch above is dead now).
   if constexpr (!TOKEN) {
     const int n4 = tq * 8 * 128 / 4;
     for (int i = tid; i < n4; i += kThreads) reinterpret_cast<f32x4_t*>(O)[i] = zero4();
-    __syncthreads();
   }
+  __syncthreads();
 
   // ---- the walk ------------------------------------------------------------
   const int j = lane & 15, grp = lane >> 4;
@@ -448,8 +459,10 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   const __amdgpu_buffer_rsrc_t qrs =
       make_rsrc(a.q + ((b * a.Lq + q0) * a.Hq + (int64_t)h * G) * 128, (uint32_t)nq * qrow);
   const uint32_t qcol = 256u * gcol + 16u * grp;
-  auto qoff = [&](int item, bool valid) {
-    return valid ? (uint32_t)it_q[max(item, 0)] * qrow + qcol : kZeroOffset;
+  // Q offset of this lane's column in a tile whose owner slots are `own2`
+  // (slot of owner 0 | slot of owner 1 << 8).
+  auto qoff = [&](uint32_t own2, bool valid) {
+    return valid ? ((own2 >> (8 * own)) & 0xffu) * qrow + qcol : kZeroOffset;
   };
   const uint32_t lock_addr = lds_address(lock);
   const int sinkq = tq;  // query slot taking the adds of a missing second owner
@@ -463,12 +476,23 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   float ninf_v = neg_inf();
   asm volatile("" : "+v"(ninf_v));  // kept in a register for set_where
 
+  // The wave's first two steps are fixed; later ones are claimed one step
+  // ahead (an LDS counter), so a step's record is read a step before it runs.
   int st = st_lo + wave;
+  int nst = st + kWaves;
   int64_t c = 0, cn = 0;
   int i0 = 0, n = 0, i0n = 0, nn = 0;
+  uint32_t own2 = 0u, own2n = 0u;  // owner slots of the current / next tile
   bool more = false;
-  uint64_t msk = 0;
+  uint64_t msk = 0, mskn = 0;
   u32x4_t kb[4][4], vb[8][2], Qb[4];
+  auto decode_next = [&](const u32x4_t r) {
+    cn = (int64_t)(r[0] & 0xffffffu);
+    nn = (int)(r[0] >> 24);
+    i0n = (int)(r[1] & 0xffffu);
+    own2n = r[1] >> 16;
+    mskn = ((uint64_t)r[3] << 32) | r[2];
+  };
 
   // One tile: columns 2 t + own of the step's owners.  The last tile of a
   // step (LAST) prefetches the next step's first Q and its K (after the QK
@@ -481,10 +505,17 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     const int o = 2 * t + own;
     const bool cvalid = o < n && gcol < G;
     const int ii = i0 + (o < n ? o : n - 1);
-    // The tile's two owners (wave-uniform), read before the products.
+    // The tile's two owners (wave-uniform, read a tile ahead); the next
+    // tile's are read now and used after the QK product.
     const bool hb = 2 * t + 1 < n;
-    const int qa = __builtin_amdgcn_readfirstlane(it_q[i0 + 2 * t]);
-    const int qb1 = __builtin_amdgcn_readfirstlane(it_q[i0 + 2 * t + (hb ? 1 : 0)]);
+    const int qa = (int)(own2 & 0xffu);
+    const int qb1 = (int)(own2 >> 8);
+    uint32_t nx_a = 0u, nx_b = 0u;
+    if constexpr (!LAST) {
+      const int e2 = i0 + 2 * t + 2;
+      nx_a = it_q[e2];
+      nx_b = it_q[e2 + (2 * t + 3 < n ? 1 : 0)];
+    }
     const float wv = TOKEN ? 0.f : (cvalid ? bf16_to_f32(it_w[ii * 8 + gcol]) : 0.f);
     // S^T = K . Q^T: lane (grp, j) gets keys 16 mt + 4 grp + r of column j.
     f32x4_t S[4];
@@ -494,11 +525,14 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) S[mt] = mfma_bf16_16x16x32(kb[mt][ks], Qb[ks], S[mt]);
     }
+    uint32_t nown2;
     if constexpr (!LAST) {
-      const int o2 = o + 2;
-      load_q(Qb, qrs, qoff(i0 + min(o2, n - 1), o2 < n && gcol < G));
+      asm volatile("" : "+v"(nx_a), "+v"(nx_b) : "v"(S[3][3]));  // read after the QK issue
+      nown2 = (uint32_t)__builtin_amdgcn_readfirstlane(nx_a | (nx_b << 8));
+      load_q(Qb, qrs, qoff(nown2, o + 2 < n && gcol < G));
     } else {
-      load_q(Qb, qrs, qoff(i0n + min(own, nn - 1), more && own < nn && gcol < G));
+      nown2 = own2n;
+      load_q(Qb, qrs, qoff(nown2, more && own < nn && gcol < G));
       load_k(kb, frs, flo, (uint32_t)cn * kFragBytes);
     }
     const uint64_t msh = msk >> (4 * grp);  // bit 16 mt + r: key 16 mt + 4 grp + r
@@ -644,36 +678,44 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       }
       if constexpr (LAST) load_v(vb, frs, flo, (uint32_t)cn * kFragBytes);
     }
+    own2 = nown2;
   };
 
   if (st < st_hi) {
-    c = __builtin_amdgcn_readfirstlane(s_chunk[st]);
-    i0 = __builtin_amdgcn_readfirstlane(s_off[st]);
-    n = __builtin_amdgcn_readfirstlane(s_off[st + 1]) - i0;
-    msk = uniform64(s_excl[st]);
+    {
+      const u32x4_t r = s_rec[st];
+      c = (int64_t)__builtin_amdgcn_readfirstlane(r[0] & 0xffffffu);
+      n = __builtin_amdgcn_readfirstlane(r[0] >> 24);
+      i0 = __builtin_amdgcn_readfirstlane(r[1] & 0xffffu);
+      own2 = __builtin_amdgcn_readfirstlane(r[1] >> 16);
+      msk = uniform64(((uint64_t)r[3] << 32) | r[2]);
+    }
+    more = nst < st_hi;
+    u32x4_t rn = s_rec[more ? nst : st];
     // the order of the prefetches at a step's end: Q, K, then V
-    load_q(Qb, qrs, qoff(i0 + min(own, n - 1), own < n && gcol < G));
+    load_q(Qb, qrs, qoff(own2, own < n && gcol < G));
     load_k(kb, frs, flo, (uint32_t)c * kFragBytes);
     if constexpr (!TOKEN) load_v(vb, frs, flo, (uint32_t)c * kFragBytes);
     while (true) {
-      // Claim the wave's next step (steps after the first kWaves go to
-      // whichever wave asks first); the claim's round trip overlaps the
-      // step's other tiles.  Lane 0 adds 1 to the counter, the other lanes
-      // add 0 to words of their own (no divergent region).
+      // Claim the step after the next one (steps after the first 2 kWaves go
+      // to whichever wave asks first); the claim's round trip overlaps this
+      // step.  Lane 0 adds 1 to the counter, the other lanes add 0 to words
+      // of their own (no divergent region).
       const uint32_t tk = __hip_atomic_fetch_add(lane == 0 ? claim : idle_or + lane,
                                                  lane == 0 ? 1u : 0u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_WORKGROUP);
       const int T = (n + 1) >> 1;
       for (int t = 0; t + 1 < T; ++t) do_tile(t, std::false_type{});
-      const int nst = st_lo + kWaves + (int)__builtin_amdgcn_readfirstlane(tk);
-      more = nst < st_hi;
-      cn = c;
-      i0n = 0;
-      nn = 0;
-      if (more) {
-        cn = __builtin_amdgcn_readfirstlane(s_chunk[nst]);
-        i0n = __builtin_amdgcn_readfirstlane(s_off[nst]);
-        nn = __builtin_amdgcn_readfirstlane(s_off[nst + 1]) - i0n;
+      // the next step's record, read a step ago (the current chunk when
+      // there is none: the prefetches then reload it and read Q as zeros)
+      {
+        u32x4_t r = rn;
+        r[0] = __builtin_amdgcn_readfirstlane(r[0]);
+        r[1] = __builtin_amdgcn_readfirstlane(r[1]);
+        r[2] = __builtin_amdgcn_readfirstlane(r[2]);
+        r[3] = __builtin_amdgcn_readfirstlane(r[3]);
+        decode_next(r);
+        if (!more) cn = c;
       }
       do_tile(T - 1, std::true_type{});
       if (!more) break;
@@ -681,7 +723,10 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       c = cn;
       i0 = i0n;
       n = nn;
-      msk = uniform64(s_excl[st]);
+      msk = mskn;
+      nst = st_lo + 2 * kWaves + (int)__builtin_amdgcn_readfirstlane(tk);
+      more = nst < st_hi;
+      rn = s_rec[more ? nst : st];
     }
   }
 
