@@ -63,7 +63,8 @@ constexpr int kBlocksPerCU = kNT == 1 ? 2 : 1;
 #endif
 constexpr int kDepth = MRSA_LOCAL_DEPTH;  // LDS operand reads in flight
 constexpr int kSlotBytes = 32768;
-constexpr int kMaskTiles = 512;        // key-valid words kept in LDS per block
+constexpr float kRescaleSlack = 8.f;   // see the online softmax below
+constexpr int kMaskTiles = 512;        // inert-key words kept in LDS per block
 
 struct LocalArgs {
   const uint16_t* q;
@@ -87,13 +88,23 @@ struct LocalArgs {
   float* part_ml;
 };
 
-// Valid-key bits (bit s = key 64 kt + s passes key_valid) of one key tile,
-// 64 bytes read by the whole wave.
-__device__ __forceinline__ uint64_t tile_valid_bits(const LocalArgs& a, int64_t b, int64_t kt) {
+// Inert-key bits (bit s = key 64 kt + s carries zero K / V) of one key tile:
+// keys in range that fail key_valid, and the landmark slots (positions j with
+// (j + 1) % inert_chunk == 0) when inert_chunk > 0.  The key_valid bytes are
+// read by the whole wave; the landmark slots come from one wave-uniform
+// remainder per tile.
+__device__ __forceinline__ uint64_t tile_inert_bits(const LocalArgs& a, int64_t b, int64_t kt) {
   const int lane = threadIdx.x & 63;
-  const int64_t j = kt * 64 + lane;
-  const bool ok = j < a.Lk && (!a.key_valid || a.key_valid[b * a.Lk + j] != 0);
-  return __builtin_amdgcn_ballot_w64(ok);
+  const int64_t j0 = kt * 64;
+  const int64_t j = j0 + lane;
+  const bool bad = j < a.Lk && a.key_valid && a.key_valid[b * a.Lk + j] == 0;
+  uint64_t m = __builtin_amdgcn_ballot_w64(bad);
+  if (a.inert_chunk > 0) {
+    const int64_t r = (j0 + 1) % a.inert_chunk;
+    for (int64_t s = r == 0 ? 0 : a.inert_chunk - r; s < 64 && j0 + s < a.Lk; s += a.inert_chunk)
+      m |= 1ull << s;
+  }
+  return m;
 }
 
 template <int GP>
@@ -194,11 +205,11 @@ local_attn_kernel(LocalArgs a) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(frs, (lds_void_t*)(dst + u * 1024), 16, dma_lane,
                                                src + 1024u * u, 0, 0);
   };
-  // Valid-key words of the block's key tiles (when they fit the table),
+  // Inert-key words of the block's key tiles (when they fit the table),
   // before the first DMA: waiting for these loads must not wait for it.
   if (tab)
     for (int t = wave; t < ntiles; t += kWaves) {
-      const uint64_t bits = tile_valid_bits(a, b, kt0 + t);
+      const uint64_t bits = tile_inert_bits(a, b, kt0 + t);
       if (lane == 0) lds_write_u64(lds_addr(&valid_tab[t]), bits);
     }
   // Q^T operands and positions complete here, before any DMA is in flight:
@@ -223,7 +234,7 @@ local_attn_kernel(LocalArgs a) {
   }
 
   const float c = a.scale_log2;
-  const int W32 = (int)a.W;
+  const int W32 = (int)min(a.W, (int64_t)1 << 30);  // |positions| < 2^30 (host check)
   const uint64_t kLast = 1ull << 63;
 
   for (int t = 0; t < ntiles; ++t) {
@@ -241,27 +252,14 @@ local_attn_kernel(LocalArgs a) {
     const int64_t kt = kt0 + t;
     const int64_t j0 = kt * 64;
     const uint32_t sbase = lds_addr(ring + (t % kRing) * kSlotBytes);
-    // Keys of the tile: in range (rbits) and inert (ibits: failed key_valid
-    // or a landmark slot).
+    // Keys of the tile before kv_len (kin) and inert keys (ibits: failed
+    // key_valid or a landmark slot).
     const int64_t left = a.Lk - j0;
-    const uint64_t rbits = left >= 64 ? ~0ull : ((1ull << left) - 1ull);
-    uint64_t vbits;
-    if (tab) {
-      vbits = uniform_u64(lds_read_u64(lds_addr(&valid_tab[t])));
-    } else {
-      vbits = tile_valid_bits(a, b, kt);
-    }
-    uint64_t ibits = ~vbits & rbits;
-    if (a.inert_chunk > 0) {
-      const int64_t jj = j0 + lane;
-      ibits |= __builtin_amdgcn_ballot_w64(jj < a.Lk && (jj + 1) % a.inert_chunk == 0);
-    }
-    ibits = uniform_u64(ibits);
+    const int kin = left >= 64 ? 64 : (int)left;
+    const uint64_t ibits =
+        uniform_u64(tab ? lds_read_u64(lds_addr(&valid_tab[t])) : tile_inert_bits(a, b, kt));
     // Tiles entirely inside every query's window need no position mask.
-    const bool full = (rbits == ~0ull) && (j0 >= phi - a.W) && (j0 + 63 <= plo + a.W);
-    // This lane's keys are 16 tt + 4 grp + i: bit 16 tt + i of the shifted
-    // words (immediate bit tests, nothing per element kept across tiles).
-    const uint64_t rsh = rbits >> (4 * grp);
+    const bool full = kin == 64 && (j0 >= phi - a.W) && (j0 + 63 <= plo + a.W);
 
     // S^T of both column tiles, sharing each K operand read.
     const uint32_t laddr = sbase + 16u * lane;  // this lane's 16 bytes of every image
@@ -305,18 +303,26 @@ local_attn_kernel(LocalArgs a) {
           for (int i = 0; i < 4; ++i) S[nt][tt][i] = set_where(S[nt][tt][i], inert_lanes(tt, i), zero_v);
       }
       if (!full) {
+        // This lane's key 16 tt + i of its group (position j0 + 4 grp + 16 tt
+        // + i) is visible iff 16 tt + i lies in [klo, khi]: inside the window
+        // and before kv_len.  One unsigned compare per element: k - klo > span.
         const int rel = (int)j0 + 4 * grp - qp[nt];
+        int klo = -W32 - rel;
+        const int khi = min(W32 - rel, kin - 4 * grp - 1);
+        if (!qok[nt] || khi < klo) klo = 64;  // nothing visible
+        const uint32_t span = klo == 64 ? 0u : (uint32_t)(khi - klo);
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int dd = rel + 16 * tt + i;
-            if (!((rsh >> (16 * tt + i)) & 1ull) || dd > W32 || dd < -W32 || !qok[nt])
-              S[nt][tt][i] = neg_inf();
-          }
+          for (int i = 0; i < 4; ++i)
+            if ((uint32_t)(16 * tt + i - klo) > span) S[nt][tt][i] = neg_inf();
       }
-      const float mx = across4_max(max16_raw(S[nt]));
-      const float m_new = fmaxf(m_run[nt], mx * c);
+      // The running max moves only when a tile's max exceeds it by more
+      // than kRescaleSlack (log2 units): probabilities then stay below
+      // 2^kRescaleSlack, which fp32 sums and the relative rounding of bf16
+      // P absorb, and the accumulators are rescaled on few tiles.
+      const float mx = across4_max(max16_raw(S[nt])) * c;
+      const float m_new = mx > m_run[nt] + kRescaleSlack ? mx : m_run[nt];
       // A column with no visible key yet keeps m = -inf; exponentiate against
       // 0 there so that every term (and alpha) is exp2(-inf) = 0.
       const float m_use = m_new == neg_inf() ? 0.f : m_new;

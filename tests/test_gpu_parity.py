@@ -321,7 +321,7 @@ def test_route_weights_vs_oracle(affine, K):
 
 
 @pytest.mark.parametrize("L,W,inert,G", [(1024, 319, 64, 7), (2048, 1280, 0, 7), (512, 100, 64, 8),
-                                         (1000, 200, 0, 7)])
+                                         (1000, 200, 0, 7), (1000, 150, 48, 7)])
 def test_local_attention_vs_oracle(L, W, inert, G):
     _note(f"local attention L={L} W={W} inert={inert} G={G}")
     Hkv, D = 4, 128
