@@ -68,32 +68,7 @@ __device__ __forceinline__ void qk_frag(uint32_t laddr, const u32x4_t (&Q)[4], f
     if constexpr (o + DEPTH < 16) kb[o + DEPTH] = lds_read_b128<kimg_off<o + DEPTH>()>(laddr);
     __builtin_amdgcn_sched_barrier(0);
   });
-}
-
-// qk_frag for two column tiles at once: each K operand read feeds both
-// products (half the LDS traffic per product).
-template <int DEPTH = 8>
-__device__ __forceinline__ void qk_frag2(uint32_t laddr, const u32x4_t (&Q0)[4],
-                                         const u32x4_t (&Q1)[4], f32x4_t (&S0)[4],
-                                         f32x4_t (&S1)[4]) {
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    S0[t] = zero4();
-    S1[t] = zero4();
-  }
-  u32x4_t kb[16];
-  static_for<16>([&](auto oc) {
-    constexpr int o = decltype(oc)::value;
-    if constexpr (o < DEPTH) kb[o] = lds_read_b128<kimg_off<o>()>(laddr);
-  });
-  static_for<16>([&](auto oc) {
-    constexpr int o = decltype(oc)::value;
-    lds_wait<(15 - o < DEPTH - 1 ? 15 - o : DEPTH - 1)>(kb[o]);
-    S0[o & 3] = mfma_bf16_16x16x32(kb[o], Q0[o >> 2], S0[o & 3]);
-    S1[o & 3] = mfma_bf16_16x16x32(kb[o], Q1[o >> 2], S1[o & 3]);
-    if constexpr (o + DEPTH < 16) kb[o + DEPTH] = lds_read_b128<kimg_off<o + DEPTH>()>(laddr);
-    __builtin_amdgcn_sched_barrier(0);
-  });
+  mfma_ready(S);  // callers patch S with inline asm
 }
 
 // A wave-uniform 64-bit value in scalar registers.

@@ -1,15 +1,12 @@
 // Bidirectional sliding-window GQA attention (flash-attn window semantics).
 //
 // Work split: one workgroup of 8 waves per (batch, KV head, block of QB
-// queries).  The block's query-head columns form column tiles of 16 columns;
-// a tile holds 16 / GP queries x GP head columns (GP = the group size rounded
-// up to a power of two; columns of heads >= G are padding), and each wave
-// owns kNT tiles (QB = 8 kNT (16 / GP): 16 queries for G = 7 with kNT = 1).
-// Q^T operands and O^T accumulators stay in registers.  With kNT = 1 a
-// workgroup needs 128 VGPRs per lane and ~69 KB of LDS, so two workgroups
-// share a CU and their barriers fall at different times: one's matrix
-// products run during the other's softmax.  (kNT = 2 shares each K / V
-// operand read between a wave's two tiles instead; both measure alike.)
+// queries).  Each wave owns one column tile of 16 columns: 16 / GP queries x
+// GP head columns (GP = the group size rounded up to a power of two; columns
+// of heads >= G are padding), so QB = 8 (16 / GP): 16 queries for G = 7.
+// Q^T operands and O^T accumulators stay in registers.  A workgroup needs
+// 128 VGPRs per lane and ~69 KB of LDS, so two workgroups share a CU and
+// their barriers fall at different times.
 //
 // Key tiles of 64 arrive by buffer->LDS DMA in a ring of kRing 32 KB slots
 // holding the tile's K / V fragments (mrsa_kv_fragments: the 32 matrix-core
@@ -19,16 +16,29 @@
 // instructions, with wave-uniform offsets.  One barrier per key tile,
 // with no memory fence: each wave waits (vmcnt) for its own share of tile t,
 // the barrier publishes the whole tile and frees the slot of tile t - 1,
-// which then receives tile t + kRing - 1.  The valid-key words of all the
+// which then receives tile t + kRing - 1.  The inert-key words of all the
 // block's key tiles are built once, before the first DMA.
 //
 // Matrix-core formulation (per 64-key tile and column tile):
 //   S^T[key][col] = K_tile (A: 64 x 128) . Q^T (B: 128 x 16)   -> 16 MFMAs
-//   online softmax down each column, in the exp2 domain
+//   softmax down each column, in the exp2 domain
 //   O^T[d][col]  += V^T (A: 128 x 64) . P^T (B: 64 x 16)      -> 16 MFMAs
 // P^T is fed to the second product straight from the accumulator registers
 // of the first: lane l holds keys 16t + 4(l/16) + i of its column, and the
 // fragments' V images number the reduction slots to match (the tiled order).
+//
+// Softmax with an anchored stabiliser.  On gfx950 ordinary VALU work does not
+// overlap the matrix products of the same SIMD, so the per-tile VALU count
+// sets the speed.  A column's stabiliser m (log2 units) is the exact max of
+// its first tile with a visible key; later tiles take p = 2^(s c - m)
+// directly -- no per-tile max, no rescale -- and each lane keeps a running
+// sum of its own p (summed across the column's four lanes once, at the end).
+// p is at most 2^kSumCap: a tile whose lane sum leaves [0, 2^kSumCap] (a logit
+// far above m, or NaN) is recomputed on the exact path, which moves m to the
+// tile's max and rescales the accumulators.  The sum never underflows: the
+// anchor key itself contributes p = 1.  Mathematically this is the same
+// softmax; the fp32 values differ from a per-tile running max only in
+// rounding.
 //
 // Semantics (dream_dllm_hils/local_attention.py:35-107):
 //   * key j is visible to a query at position p iff |p - j| <= window;
@@ -43,27 +53,13 @@ using namespace mrsa;
 
 namespace {
 
-#ifndef MRSA_LOCAL_NT
-#define MRSA_LOCAL_NT 1
-#endif
-#ifndef MRSA_LOCAL_RING
-#define MRSA_LOCAL_RING 2
-#endif
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kNT = MRSA_LOCAL_NT;      // column tiles per wave
-constexpr int kColTiles = kWaves * kNT;
-constexpr int kRing = MRSA_LOCAL_RING;  // key-tile slots
-// One column tile per wave leaves room (128 VGPRs, 2 x 69 KB LDS) for two
-// workgroups per CU, whose barriers fall at different times: one's matrix
-// products overlap the other's softmax.
-constexpr int kBlocksPerCU = kNT == 1 ? 2 : 1;
-#ifndef MRSA_LOCAL_DEPTH
-#define MRSA_LOCAL_DEPTH 8
-#endif
-constexpr int kDepth = MRSA_LOCAL_DEPTH;  // LDS operand reads in flight
+constexpr int kRing = 2;               // key-tile slots
+constexpr int kBlocksPerCU = 2;        // 128 VGPRs, 2 x 69 KB LDS
+constexpr int kDepth = 8;              // LDS operand reads in flight
 constexpr int kSlotBytes = 32768;
-constexpr float kRescaleSlack = 8.f;   // see the online softmax below
+constexpr float kSumCap = 64.f;        // log2 of the largest lane sum of p on the fast path
 constexpr int kMaskTiles = 512;        // inert-key words kept in LDS per block
 
 struct LocalArgs {
@@ -111,7 +107,7 @@ template <int GP>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2 * kBlocksPerCU, 2 * kBlocksPerCU)))
 local_attn_kernel(LocalArgs a) {
   constexpr int QPT = 16 / GP;          // queries per column tile
-  constexpr int QB = kColTiles * QPT;   // queries per workgroup
+  constexpr int QB = kWaves * QPT;      // queries per workgroup
   extern __shared__ __align__(16) unsigned char smem[];
   unsigned char* ring = smem;                                              // kRing slots
   uint64_t* valid_tab = reinterpret_cast<uint64_t*>(smem + kRing * kSlotBytes);  // [kMaskTiles]
@@ -157,23 +153,18 @@ local_attn_kernel(LocalArgs a) {
     }
   }
 
-  // Q^T operands and positions of this lane's two columns.
-  u32x4_t Qb[kNT][4];
-  int qp[kNT];
-  bool qok[kNT];
+  // Q^T operands and position of this lane's column.
+  u32x4_t Qb[4];
+  const int64_t qi = qb + wave * QPT + col / GP;
+  const bool qok = qi < a.Lq && gg < G;
+  const int qp = qi < a.Lq ? (int)(a.qpos ? a.qpos[qi] : qi) : 0;
 #pragma unroll
-  for (int nt = 0; nt < kNT; ++nt) {
-    const int64_t qi = qb + (kNT * wave + nt) * QPT + col / GP;
-    qok[nt] = qi < a.Lq && gg < G;
-    qp[nt] = qi < a.Lq ? (int)(a.qpos ? a.qpos[qi] : qi) : 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      u32x4_t z = {0u, 0u, 0u, 0u};
-      Qb[nt][j] = z;
-      if (qok[nt])
-        Qb[nt][j] = *reinterpret_cast<const u32x4_t*>(
-            a.q + ((b * a.Lq + qi) * a.Hq + h * G + gg) * 128 + 32 * j + 8 * grp);
-    }
+  for (int j = 0; j < 4; ++j) {
+    u32x4_t z = {0u, 0u, 0u, 0u};
+    Qb[j] = z;
+    if (qok)
+      Qb[j] = *reinterpret_cast<const u32x4_t*>(
+          a.q + ((b * a.Lq + qi) * a.Hq + h * G + gg) * 128 + 32 * j + 8 * grp);
   }
   __syncthreads();
   const int64_t plo = pos_range[0], phi = pos_range[1];
@@ -212,28 +203,26 @@ local_attn_kernel(LocalArgs a) {
       const uint64_t bits = tile_inert_bits(a, b, kt0 + t);
       if (lane == 0) lds_write_u64(lds_addr(&valid_tab[t]), bits);
     }
-  // Q^T operands and positions complete here, before any DMA is in flight:
-  // otherwise the compiler, tracking their loads into the loop, waits for
-  // every outstanding load (the DMA prefetch included) at each first use.
+  // Q^T operands and the position complete here, before any DMA is in
+  // flight: otherwise the compiler, tracking their loads into the loop,
+  // waits for every outstanding load (the DMA prefetch included) at each
+  // first use.
 #pragma unroll
-  for (int nt = 0; nt < kNT; ++nt) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(Qb[nt][j]));
-    asm volatile("" : "+v"(qp[nt]));
-  }
+  for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(Qb[j]));
+  int qpv = qp;
+  asm volatile("" : "+v"(qpv));
   for (int t = 0; t < kRing - 1 && t < ntiles; ++t) issue_tile(kt0 + t, t);
 
-  f32x4_t acc[kNT][8];
-  float m_run[kNT], l_run[kNT];
+  f32x4_t acc[8];
 #pragma unroll
-  for (int nt = 0; nt < kNT; ++nt) {
-    m_run[nt] = neg_inf();
-    l_run[nt] = 0.f;
-#pragma unroll
-    for (int td = 0; td < 8; ++td) acc[nt][td] = zero4();
-  }
-
+  for (int td = 0; td < 8; ++td) acc[td] = zero4();
+  // Stabiliser (log2 units) and this lane's running sum of p.  Absent
+  // columns start anchored at 0: their logits are 0 or masked.
+  float m_run = qok ? neg_inf() : 0.f;
+  float l_lane = 0.f;
+  bool anchored = __all(m_run != neg_inf());
   const float c = a.scale_log2;
+  const float sum_cap = __builtin_ldexpf(1.f, (int)kSumCap);
   const int W32 = (int)min(a.W, (int64_t)1 << 30);  // |positions| < 2^30 (host check)
   const uint64_t kLast = 1ull << 63;
 
@@ -244,7 +233,7 @@ local_attn_kernel(LocalArgs a) {
     if (later >= 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
     else if (later == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // (first pass: the valid table)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // (first pass: the inert table)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (t + kRing - 1 < ntiles) issue_tile(kt0 + t + kRing - 1, (t + kRing - 1) % kRing);
@@ -260,19 +249,7 @@ local_attn_kernel(LocalArgs a) {
         uniform_u64(tab ? lds_read_u64(lds_addr(&valid_tab[t])) : tile_inert_bits(a, b, kt));
     // Tiles entirely inside every query's window need no position mask.
     const bool full = kin == 64 && (j0 >= phi - a.W) && (j0 + 63 <= plo + a.W);
-
-    // S^T of both column tiles, sharing each K operand read.
     const uint32_t laddr = sbase + 16u * lane;  // this lane's 16 bytes of every image
-    f32x4_t S[kNT][4];
-    if constexpr (kNT == 2) qk_frag2<kDepth>(laddr, Qb[0], Qb[kNT - 1], S[0], S[kNT - 1]);
-    else qk_frag<kDepth>(laddr, Qb[0], S[0]);
-    // The first V^T operands do not depend on P: read them now.  Product o
-    // (d rows 16 (o & 7).., keys 32 (o >> 3)..) reads V image 2 (o & 7) + (o >> 3).
-    u32x4_t vb[16];
-    static_for<4>([&](auto oc) {
-      constexpr int o = decltype(oc)::value;
-      vb[o] = lds_read_b128<16384 + (2 * (o & 7) + (o >> 3)) * 1024>(laddr);
-    });
 
     // Inert keys: lanes of group g hold keys 16 tt + 4 g + i.  The landmark
     // slot (key 63, lanes 48..63) is the usual only one; other inert keys
@@ -288,88 +265,100 @@ local_attn_kernel(LocalArgs a) {
       return m;
     };
     const float zero_v = 0.f;
-
-    u32x4_t Pb[kNT][2];
-#pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) {
-      // Logits in units of log2: s * scale_log2.  Inert keys are exactly 0;
-      // keys outside the window (or past kv_len, or of an absent column) are
-      // -inf, which the window mask below sets after the inert zeros.
-      S[nt][3][3] = set_where(S[nt][3][3], last_lanes, zero_v);
+    auto zero_inert = [&](f32x4_t (&X)[4]) {
+      X[3][3] = set_where(X[3][3], last_lanes, zero_v);
       if (other_inert) {
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) S[nt][tt][i] = set_where(S[nt][tt][i], inert_lanes(tt, i), zero_v);
+          for (int i = 0; i < 4; ++i) X[tt][i] = set_where(X[tt][i], inert_lanes(tt, i), zero_v);
       }
+    };
+    // S^T of the column tile from the slot, inert keys 0 and invisible keys
+    // -inf: keys outside the window, past kv_len or of an absent column.
+    auto logits = [&](f32x4_t (&X)[4]) {
+      qk_frag<kDepth>(laddr, Qb, X);
+      zero_inert(X);
       if (!full) {
         // This lane's key 16 tt + i of its group (position j0 + 4 grp + 16 tt
         // + i) is visible iff 16 tt + i lies in [klo, khi]: inside the window
         // and before kv_len.  One unsigned compare per element: k - klo > span.
-        const int rel = (int)j0 + 4 * grp - qp[nt];
+        const int rel = (int)j0 + 4 * grp - qpv;
         int klo = -W32 - rel;
         const int khi = min(W32 - rel, kin - 4 * grp - 1);
-        if (!qok[nt] || khi < klo) klo = 64;  // nothing visible
+        if (!qok || khi < klo) klo = 64;  // nothing visible
         const uint32_t span = klo == 64 ? 0u : (uint32_t)(khi - klo);
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if ((uint32_t)(16 * tt + i - klo) > span) S[nt][tt][i] = neg_inf();
+            if ((uint32_t)(16 * tt + i - klo) > span) X[tt][i] = neg_inf();
       }
-      // The running max moves only when a tile's max exceeds it by more
-      // than kRescaleSlack (log2 units): probabilities then stay below
-      // 2^kRescaleSlack, which fp32 sums and the relative rounding of bf16
-      // P absorb, and the accumulators are rescaled on few tiles.
-      const float mx = across4_max(max16_raw(S[nt])) * c;
-      const float m_new = mx > m_run[nt] + kRescaleSlack ? mx : m_run[nt];
+    };
+    auto lane_sum = [&](const f32x4_t (&X)[4]) {
+      return ((X[0][0] + X[0][1]) + (X[0][2] + X[0][3])) + ((X[1][0] + X[1][1]) + (X[1][2] + X[1][3])) +
+             (((X[2][0] + X[2][1]) + (X[2][2] + X[2][3])) + ((X[3][0] + X[3][1]) + (X[3][2] + X[3][3])));
+    };
+
+    f32x4_t S[4];
+    logits(S);
+    bool exact = !anchored;
+    if (anchored) {
+      // fast path: p = 2^(s c - m), the lane sum checked against the cap
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) S[tt][i] = exp2_hw(__builtin_fmaf(S[tt][i], c, -m_run));
+      const float ps = lane_sum(S);
+      exact = !__all(ps <= sum_cap);
+      if (!exact) l_lane += ps;
+    }
+    if (exact) {
+      // exact path: the column max as the new stabiliser, accumulators and
+      // sums rescaled (after a fast-path overflow, the tile's logits again)
+      if (anchored) logits(S);
+      const float mx = across4_max(max16_raw(S)) * c;
+      const float m_new = fmaxf(m_run, mx);
       // A column with no visible key yet keeps m = -inf; exponentiate against
       // 0 there so that every term (and alpha) is exp2(-inf) = 0.
       const float m_use = m_new == neg_inf() ? 0.f : m_new;
-      const float alpha = exp2_hw(m_run[nt] - m_use);
-      float part4[4];
+      const float alpha = exp2_hw(m_run - m_use);
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
+      for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          S[nt][tt][i] = exp2_hw(__builtin_fmaf(S[nt][tt][i], c, -m_use));
-        part4[tt] = (S[nt][tt][0] + S[nt][tt][1]) + (S[nt][tt][2] + S[nt][tt][3]);
-      }
-      const float rsum = across4_sum((part4[0] + part4[1]) + (part4[2] + part4[3]));
-      // Inert keys count in the denominator but carry zero V.
-      S[nt][3][3] = set_where(S[nt][3][3], last_lanes, zero_v);
-      if (other_inert) {
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) S[nt][tt][i] = set_where(S[nt][tt][i], inert_lanes(tt, i), zero_v);
-      }
-      l_run[nt] = l_run[nt] * alpha + rsum;
-      m_run[nt] = m_new;
+        for (int i = 0; i < 4; ++i) S[tt][i] = exp2_hw(__builtin_fmaf(S[tt][i], c, -m_use));
+      l_lane = l_lane * alpha + lane_sum(S);
+      m_run = m_new;
       if (!__all(alpha == 1.f)) {
 #pragma unroll
-        for (int td = 0; td < 8; ++td) acc[nt][td] *= alpha;
+        for (int td = 0; td < 8; ++td) acc[td] *= alpha;
       }
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        Pb[nt][jj][0] = pack_bf16x2(S[nt][2 * jj][0], S[nt][2 * jj][1]);
-        Pb[nt][jj][1] = pack_bf16x2(S[nt][2 * jj][2], S[nt][2 * jj][3]);
-        Pb[nt][jj][2] = pack_bf16x2(S[nt][2 * jj + 1][0], S[nt][2 * jj + 1][1]);
-        Pb[nt][jj][3] = pack_bf16x2(S[nt][2 * jj + 1][2], S[nt][2 * jj + 1][3]);
-      }
+      anchored = __all(m_run != neg_inf());
     }
-    // O^T += V^T . P^T for both column tiles, sharing each V^T operand read,
-    // kDepth reads in flight.
-    static_for<kDepth - 4>([&](auto oc) {
-      constexpr int o = decltype(oc)::value + 4;
+    // Inert keys count in the denominator but carry zero V.
+    zero_inert(S);
+    u32x4_t Pb[2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      Pb[jj][0] = pack_bf16x2(S[2 * jj][0], S[2 * jj][1]);
+      Pb[jj][1] = pack_bf16x2(S[2 * jj][2], S[2 * jj][3]);
+      Pb[jj][2] = pack_bf16x2(S[2 * jj + 1][0], S[2 * jj + 1][1]);
+      Pb[jj][3] = pack_bf16x2(S[2 * jj + 1][2], S[2 * jj + 1][3]);
+    }
+    // O^T += V^T . P^T, kDepth reads in flight.  Product o (d rows
+    // 16 (o & 7).., keys 32 (o >> 3)..) reads V image 2 (o & 7) + (o >> 3).
+    // (The reads are issued on one path only: a value read by asm and
+    // waited for later must not meet a second definition at a join, where
+    // the compiler may copy its register before the data has landed.)
+    u32x4_t vb[16];
+    static_for<kDepth>([&](auto oc) {
+      constexpr int o = decltype(oc)::value;
       vb[o] = lds_read_b128<16384 + (2 * (o & 7) + (o >> 3)) * 1024>(laddr);
     });
     static_for<16>([&](auto oc) {
       constexpr int o = decltype(oc)::value;
       lds_wait<(15 - o < kDepth - 1 ? 15 - o : kDepth - 1)>(vb[o]);
-      acc[0][o & 7] = mfma_bf16_16x16x32(vb[o], Pb[0][o >> 3], acc[0][o & 7]);
-      if constexpr (kNT == 2)
-        acc[kNT - 1][o & 7] = mfma_bf16_16x16x32(vb[o], Pb[kNT - 1][o >> 3], acc[kNT - 1][o & 7]);
+      acc[o & 7] = mfma_bf16_16x16x32(vb[o], Pb[o >> 3], acc[o & 7]);
       if constexpr (o + kDepth < 16)
         vb[o + kDepth] =
             lds_read_b128<16384 + (2 * ((o + kDepth) & 7) + ((o + kDepth) >> 3)) * 1024>(laddr);
@@ -377,40 +366,33 @@ local_attn_kernel(LocalArgs a) {
     });
   }
 
+  // The column's sum: its four lanes' running sums.
+  const float l_run = across4_sum(l_lane);
+  if (!qok) return;
   if (a.parts > 1) {
+    const int64_t row = ((int64_t)part * a.B * a.Lq + b * a.Lq + qi) * a.Hq + h * G + gg;
+    float* prow = a.part_o + row * 128;
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) {
-      const int64_t qi = qb + (kNT * wave + nt) * QPT + col / GP;
-      if (qi >= a.Lq || gg >= G) continue;
-      const int64_t row = ((int64_t)part * a.B * a.Lq + b * a.Lq + qi) * a.Hq + h * G + gg;
-      float* prow = a.part_o + row * 128;
-#pragma unroll
-      for (int td = 0; td < 8; ++td)
-        *reinterpret_cast<f32x4_t*>(prow + 16 * td + 4 * grp) = acc[nt][td];
-      if (grp == 0) {
-        a.part_ml[2 * row] = m_run[nt];
-        a.part_ml[2 * row + 1] = l_run[nt];
-      }
+    for (int td = 0; td < 8; ++td)
+      *reinterpret_cast<f32x4_t*>(prow + 16 * td + 4 * grp) = acc[td];
+    if (grp == 0) {
+      a.part_ml[2 * row] = m_run;
+      a.part_ml[2 * row + 1] = l_run;
     }
     return;
   }
+  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+  uint16_t* orow = a.out + ((b * a.Lq + qi) * a.Hq + h * G + gg) * 128;
 #pragma unroll
-  for (int nt = 0; nt < kNT; ++nt) {
-    const int64_t qi = qb + (kNT * wave + nt) * QPT + col / GP;
-    if (qi >= a.Lq || gg >= G) continue;
-    const float inv = l_run[nt] > 0.f ? 1.f / l_run[nt] : 0.f;
-    uint16_t* orow = a.out + ((b * a.Lq + qi) * a.Hq + h * G + gg) * 128;
-#pragma unroll
-    for (int td = 0; td < 8; ++td) {
-      u32x2_t o;
-      o[0] = pack_bf16x2(acc[nt][td][0] * inv, acc[nt][td][1] * inv);
-      o[1] = pack_bf16x2(acc[nt][td][2] * inv, acc[nt][td][3] * inv);
-      *reinterpret_cast<u32x2_t*>(orow + 16 * td + 4 * grp) = o;
-    }
-    if (grp == 0)
-      a.lse[(b * a.Lq + qi) * a.Hq + h * G + gg] =
-          l_run[nt] > 0.f ? (m_run[nt] + log2f(l_run[nt])) * kLn2 : neg_inf();
+  for (int td = 0; td < 8; ++td) {
+    u32x2_t o;
+    o[0] = pack_bf16x2(acc[td][0] * inv, acc[td][1] * inv);
+    o[1] = pack_bf16x2(acc[td][2] * inv, acc[td][3] * inv);
+    *reinterpret_cast<u32x2_t*>(orow + 16 * td + 4 * grp) = o;
   }
+  if (grp == 0)
+    a.lse[(b * a.Lq + qi) * a.Hq + h * G + gg] =
+        l_run > 0.f ? (m_run + log2f(l_run)) * kLn2 : neg_inf();
 }
 
 // Combines the key-split partials of one (query, head) row: with
@@ -444,7 +426,7 @@ __global__ void __launch_bounds__(256) local_merge_kernel(LocalArgs a, int64_t r
 
 template <int GP>
 int launch_local(const LocalArgs& a, hipStream_t s) {
-  constexpr int QB = kColTiles * (16 / GP);
+  constexpr int QB = kWaves * (16 / GP);
   const size_t smem = (size_t)kRing * kSlotBytes + kMaskTiles * 8 + 16;
   auto kern = local_attn_kernel<GP>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),

@@ -61,6 +61,17 @@ __device__ __forceinline__ f32x4_t mfma_bf16_16x16x32(u32x4_t a, u32x4_t b, f32x
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
+// Matrix-core results read by inline asm.  The compiler inserts the wait
+// states the hardware needs between an MFMA and a VALU instruction that reads
+// its result, but it cannot see into inline asm: an asm instruction (set_where,
+// max3_raw, ...) placed right after the product reads the register before the
+// MFMA has written it.  mfma_ready() ties 16 wait states (at least the 11-12
+// an 8-pass 16x16x32 product needs) to the named results; call it between the
+// last product and the first asm reader.
+__device__ __forceinline__ void mfma_ready(f32x4_t (&S)[4]) {
+  asm volatile("s_nop 7\n\ts_nop 7" : "+v"(S[0]), "+v"(S[1]), "+v"(S[2]), "+v"(S[3]));
+}
+
 __device__ __forceinline__ f32x4_t zero4() {
   f32x4_t z = {0.f, 0.f, 0.f, 0.f};
   return z;

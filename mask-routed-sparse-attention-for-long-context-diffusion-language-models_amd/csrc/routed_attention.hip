@@ -578,6 +578,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       // Excluded keys -> -inf in place.  Key 63 (the landmark slot, the
       // usual only exclusion) is S[3][3] of lane group 3; other excluded
       // keys take the per-bit path.
+      mfma_ready(S);  // the asm below reads the products
       S[3][3] = set_where(S[3][3], (msk >> 63) ? 0xFFFF000000000000ull : 0ull, ninf_v);
       if (msk & ~(1ull << 63)) {
 #pragma unroll

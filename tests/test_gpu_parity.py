@@ -336,6 +336,34 @@ def test_local_attention_vs_oracle(L, W, inert, G):
     torch.testing.assert_close(lse.cpu(), rl, atol=2e-3, rtol=1e-4)
 
 
+@pytest.mark.parametrize("W,inert", [(319, 64), (1280, 0)])
+def test_local_attention_stabiliser_recompute_and_determinism(W, inert):
+    # Queries share a direction e (q + 10 e) and the keys of two later tiles
+    # carry 80 e: their logits sit ~70 natural units above everything else
+    # (lane sums of p beyond 2^64 against each column's first-tile anchor),
+    # so those tiles take the exact recompute path, while the spread inside
+    # them stays ordinary (no single key dominates).  The kernel has no
+    # atomics: two launches must agree bit for bit.
+    _note(f"local attention stabiliser recompute W={W} inert={inert}")
+    L, Hkv, G, D = 3072, 4, 7, 128
+    e = torch.ones(D) / D ** 0.5
+    q = (_rand((1, L, Hkv * G, D), 40) + 10.0 * e).bfloat16()
+    k, v = _planted_kv(L, Hkv, D, 41)
+    k = k.float()
+    k[:, 640:704] += 80.0 * e
+    k[:, 1984:2048] += 80.0 * e
+    k = k.bfloat16()
+    valid = torch.rand(1, L, generator=torch.Generator().manual_seed(42)) > 0.02
+    frags = mrsa.kv_fragments(k.to(DEV), v.to(DEV))
+    out, lse = local_attention_launch(q.to(DEV), frags, valid.to(DEV), W, inert)
+    out2, lse2 = local_attention_launch(q.to(DEV), frags, valid.to(DEV), W, inert)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2) and torch.equal(lse, lse2), "local attention is not deterministic"
+    ro, rl = O.local_attention(q, k, v, valid, W, inert)
+    _assert_close_attn(out, ro, f"local recompute W={W}")
+    torch.testing.assert_close(lse.cpu(), rl, atol=2e-3, rtol=1e-4)
+
+
 @pytest.mark.parametrize("parts,first", [(1, 8000), (3, 8000), (12, 8160), (40, 0), (5, 100)])
 def test_local_attention_key_split(parts, first):
     # Key tiles of each 32-query block split over `parts` workgroups and
