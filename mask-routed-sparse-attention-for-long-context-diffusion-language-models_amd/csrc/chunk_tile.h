@@ -68,7 +68,6 @@ __device__ __forceinline__ void qk_frag(uint32_t laddr, const u32x4_t (&Q)[4], f
     if constexpr (o + DEPTH < 16) kb[o + DEPTH] = lds_read_b128<kimg_off<o + DEPTH>()>(laddr);
     __builtin_amdgcn_sched_barrier(0);
   });
-  mfma_ready(S);  // callers patch S with inline asm
 }
 
 // A wave-uniform 64-bit value in scalar registers.

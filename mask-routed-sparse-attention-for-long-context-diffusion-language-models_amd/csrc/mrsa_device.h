@@ -61,17 +61,6 @@ __device__ __forceinline__ f32x4_t mfma_bf16_16x16x32(u32x4_t a, u32x4_t b, f32x
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-// Matrix-core results read by inline asm.  The compiler inserts the wait
-// states the hardware needs between an MFMA and a VALU instruction that reads
-// its result, but it cannot see into inline asm: an asm instruction (set_where,
-// max3_raw, ...) placed right after the product reads the register before the
-// MFMA has written it.  mfma_ready() ties 16 wait states (at least the 11-12
-// an 8-pass 16x16x32 product needs) to the named results; call it between the
-// last product and the first asm reader.
-__device__ __forceinline__ void mfma_ready(f32x4_t (&S)[4]) {
-  asm volatile("s_nop 7\n\ts_nop 7" : "+v"(S[0]), "+v"(S[1]), "+v"(S[2]), "+v"(S[3]));
-}
-
 __device__ __forceinline__ f32x4_t zero4() {
   f32x4_t z = {0.f, 0.f, 0.f, 0.f};
   return z;
@@ -224,19 +213,20 @@ __device__ __forceinline__ int wave_min_i(int v) {
   return v;
 }
 
-// v_max3 / v_max without the input canonicalisation fmaxf implies; for
-// inputs that are never NaN (matrix-core products, -inf masks).
+// Max of the 16 accumulator values a lane holds for one 64-row tile.  Plain
+// builtins (the compiler forms v_max3 and needs no input canonicalisation
+// for matrix-core results): inline asm must not read matrix-core results,
+// since the compiler cannot insert the wait states the hardware requires
+// between an MFMA and an asm instruction that reads its result.
 __device__ __forceinline__ float max16_raw(const f32x4_t (&S)[4]) {
-  float m = max3_raw(max3_raw(S[0][0], S[0][1], S[0][2]), max3_raw(S[0][3], S[1][0], S[1][1]),
-                     S[3][3]);
-  m = max3_raw(m, max3_raw(S[1][2], S[1][3], S[2][0]), max3_raw(S[2][1], S[2][2], S[2][3]));
-  return max3_raw(m, S[3][0], max_raw(S[3][1], S[3][2]));
+  float m = __builtin_fmaxf(__builtin_fmaxf(S[0][0], S[0][1]), S[0][2]);
+#pragma unroll
+  for (int i = 3; i < 16; ++i) m = __builtin_fmaxf(m, S[i >> 2][i & 3]);
+  return m;
 }
-// x = v in the lanes set in `lanes`, in place (no register copies at the join
-// of branches that patch a few accumulator values).
+// x = v in the lanes set in `lanes` (v_cndmask with the mask as condition).
 __device__ __forceinline__ float set_where(float x, uint64_t lanes, float v) {
-  asm("v_cndmask_b32_e64 %0, %0, %1, %2" : "+v"(x) : "v"(v), "s"(lanes));
-  return x;
+  return __builtin_amdgcn_inverse_ballot_w64(lanes) ? v : x;
 }
 
 // Order-preserving map from fp32 to uint32 (larger float -> larger key).

@@ -578,7 +578,6 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       // Excluded keys -> -inf in place.  Key 63 (the landmark slot, the
       // usual only exclusion) is S[3][3] of lane group 3; other excluded
       // keys take the per-bit path.
-      mfma_ready(S);  // the asm below reads the products
       S[3][3] = set_where(S[3][3], (msk >> 63) ? 0xFFFF000000000000ull : 0ull, ninf_v);
       if (msk & ~(1ull << 63)) {
 #pragma unroll
@@ -599,26 +598,43 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
                 S[mt][r], __builtin_amdgcn_ballot_w64(!((kbits >> (16 * mt + r)) & 1ull)),
                 ninf_v);
       }
-      const float mx = across4_max(max16_raw(S));
-      const float mb = mx == neg_inf() ? 0.f : mx * c2;
-      float ps[4];
+      // The chunk's softmax P = bf16(p w / sum p) does not depend on the
+      // stabiliser of p.  Without one, p = 2^(s c) and sum p stay in fp32's
+      // range for any |s c| well below 64: the per-column max (and its
+      // cross-lane reduction) is skipped.  When some column's sum leaves
+      // [2^-64, 2^64] -- extreme logits, or no key left (sum 0) -- the wave
+      // takes the max-stabilised form, which handles both.
+      f32x4_t E[4];
+      auto exp_sum = [&](float mb) {
+        float ps[4];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) S[mt][r] = exp2_hw(__builtin_fmaf(S[mt][r], c2, -mb));
-        ps[mt] = (S[mt][0] + S[mt][1]) + (S[mt][2] + S[mt][3]);
+          for (int r = 0; r < 4; ++r) E[mt][r] = exp2_hw(__builtin_fmaf(S[mt][r], c2, -mb));
+          ps[mt] = (E[mt][0] + E[mt][1]) + (E[mt][2] + E[mt][3]);
+        }
+        return across4_sum((ps[0] + ps[1]) + (ps[2] + ps[3]));
+      };
+      float sum = 0.f;
+      bool stabilise = KEEP;  // keep rows often drop whole chunks (sum 0)
+      if constexpr (!KEEP) {
+        sum = exp_sum(0.f);
+        stabilise = !__all(sum >= 0x1p-64f && sum <= 0x1p64f);
       }
-      const float sum = across4_sum((ps[0] + ps[1]) + (ps[2] + ps[3]));
+      if (stabilise) {
+        const float mx = across4_max(max16_raw(S));
+        sum = exp_sum(mx == neg_inf() ? 0.f : mx * c2);
+      }
       const float f = sum > 0.f ? wv * rcp_hw(sum) : 0.f;
       // P (row j = this lane's column): reduction index 8 grp + e of k-step
       // ks is key 32 ks + 16 (e >> 2) + 4 grp + (e & 3), the tiled-V order.
       u32x4_t Pb[2];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        Pb[ks][0] = pack_bf16x2(S[2 * ks][0] * f, S[2 * ks][1] * f);
-        Pb[ks][1] = pack_bf16x2(S[2 * ks][2] * f, S[2 * ks][3] * f);
-        Pb[ks][2] = pack_bf16x2(S[2 * ks + 1][0] * f, S[2 * ks + 1][1] * f);
-        Pb[ks][3] = pack_bf16x2(S[2 * ks + 1][2] * f, S[2 * ks + 1][3] * f);
+        Pb[ks][0] = pack_bf16x2(E[2 * ks][0] * f, E[2 * ks][1] * f);
+        Pb[ks][1] = pack_bf16x2(E[2 * ks][2] * f, E[2 * ks][3] * f);
+        Pb[ks][2] = pack_bf16x2(E[2 * ks + 1][0] * f, E[2 * ks + 1][1] * f);
+        Pb[ks][3] = pack_bf16x2(E[2 * ks + 1][2] * f, E[2 * ks + 1][3] * f);
       }
       // Add the tile into its owners' rows under the lock: the rows are read
       // into the accumulators and O^T_tile = V^T . P^T is added onto them
@@ -734,32 +750,67 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   // ---- epilogue -----------------------------------------------------------
   if constexpr (!TOKEN) {
     __syncthreads();
+    // Work item e: output row rho = e / 16 (query rho / G, head rho % G),
+    // dims 8 u .. 8 u + 7 (u = e % 16), LDS blocks 2 u and 2 u + 1 stored at
+    // block ^ g.  A thread has at most kEpi items; with the output fusion
+    // their local-branch rows are all loaded before the first store.
+    constexpr int kEpi = kMaxTQ * 8 * 16 / kThreads;
     const int rows = nq * G;
-    for (int e = tid; e < rows * 16; e += kThreads) {
-      const int rho = e >> 4, u = e & 15;
-      const int qq = rho / G, g = rho - qq * G;
-      // dims 8 u .. 8 u + 7: blocks 2 u and 2 u + 1, stored at block ^ g
+    auto item_row = [&](int e, int& u, int& qq, int& g) {
+      const int rho = e >> 4;
+      u = e & 15;
+      qq = rho / G;
+      g = rho - qq * G;
+      return (b * a.Lq + q0 + qq) * a.Hq + h * G + g;
+    };
+    auto lds_rows = [&](int qq, int g, int u, f32x4_t& x0, f32x4_t& x1) {
       const float* src = O + (qq * 8 + g) * 128;
-      const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(src + 4 * ((2 * u) ^ g));
-      const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(src + 4 * ((2 * u + 1) ^ g));
-      const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-      const int64_t row = (b * a.Lq + q0 + qq) * a.Hq + h * G + g;
-      if (a.parts > 1) {
+      x0 = *reinterpret_cast<const f32x4_t*>(src + 4 * ((2 * u) ^ g));
+      x1 = *reinterpret_cast<const f32x4_t*>(src + 4 * ((2 * u + 1) ^ g));
+    };
+    if (a.parts > 1) {
+      for (int e = tid; e < rows * 16; e += kThreads) {
+        int u, qq, g;
+        const int64_t row = item_row(e, u, qq, g);
+        f32x4_t x0, x1;
+        lds_rows(qq, g, u, x0, x1);
         float* prow = a.partial + ((int64_t)part * a.B * a.Lq * a.Hq + row) * 128 + 8 * u;
         reinterpret_cast<f32x4_t*>(prow)[0] = x0;
         reinterpret_cast<f32x4_t*>(prow)[1] = x1;
-        continue;
       }
-      u32x4_t o;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+    } else {
+      u32x4_t lrow[kEpi];
+      float wl[kEpi];
       if (a.fuse_local) {
-        const float wl = bf16_to_f32(a.fuse_w[row]);
-        const u32x4_t l = *reinterpret_cast<const u32x4_t*>(a.fuse_local + row * 128 + 8 * u);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = fuse_bf16x2(o[i], l[i], wl);
+        for (int k = 0; k < kEpi; ++k) {
+          const int e = tid + k * kThreads;
+          if (e < rows * 16) {
+            int u, qq, g;
+            const int64_t row = item_row(e, u, qq, g);
+            wl[k] = bf16_to_f32(a.fuse_w[row]);
+            lrow[k] = *reinterpret_cast<const u32x4_t*>(a.fuse_local + row * 128 + 8 * u);
+          }
+        }
       }
-      *reinterpret_cast<u32x4_t*>(a.out + row * 128 + 8 * u) = o;
+#pragma unroll
+      for (int k = 0; k < kEpi; ++k) {
+        const int e = tid + k * kThreads;
+        if (e >= rows * 16) break;
+        int u, qq, g;
+        const int64_t row = item_row(e, u, qq, g);
+        f32x4_t x0, x1;
+        lds_rows(qq, g, u, x0, x1);
+        const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        u32x4_t o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+        if (a.fuse_local) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = fuse_bf16x2(o[i], lrow[k][i], wl[k]);
+        }
+        *reinterpret_cast<u32x4_t*>(a.out + row * 128 + 8 * u) = o;
+      }
     }
   }
 }
