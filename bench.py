@@ -48,9 +48,10 @@ L_CFG2, HQ, HKV, D, CHUNK, TOPK, WINDOW = 16384, 28, 4, 128, 64, 32, 256
 
 def selected_flops(L: int) -> float:
     """Algorithmic FLOPs of the routed chunk attention: QK^T + PV over every
-    routed (query head, chunk) pair, 64 keys per chunk (2 FLOP per MAC)."""
+    routed (query head, chunk) pair, the 63 real keys of each chunk (the
+    landmark slot is excluded), 2 FLOP per MAC."""
 
-    return 4.0 * D * HQ * L * TOPK * 64
+    return 4.0 * D * HQ * L * TOPK * 63
 
 
 def make_inputs(L: int, seed: int, device, dtype):
