@@ -426,6 +426,33 @@ int mrsa_selected_attention_keep_fwd(const void* q, const void* kv_frags,
                                      void* stream);
 
 /*
+ * Backward of the routed chunk attention: replaces the backward kernel of
+ * HiLS_block_M_head (ops/hils_fwd_bwd_head.py:573-910, called from
+ * _hils_block_M_attention_inverse.backward, :1050-1098).  Each listed
+ * (query, chunk) recomputes its chunk softmax; with the reference's rounding
+ * points P = bf16(2^(s c - lse)), di = sum P dP, dS = bf16(scale w P (dP - di)):
+ *   grad_q  = sum dS K              fp32 [batch, q_len, q_heads, head_dim] (written)
+ *   grad_k += dS^T Q, grad_v += P^T bf16(w dO)
+ *                                   fp32 [batch, kv_len, kv_heads, head_dim]
+ *                                   (accumulated with atomic adds: zero them first)
+ *   grad_weights = di               bf16 [batch, q_len, q_heads, topk] (0 for slots
+ *                                   past the list's end or out of range)
+ * Arguments as mrsa_selected_attention_keep_fwd (token_keep may be null), plus
+ *   grad_out:     bf16 [batch, q_len, q_heads, head_dim] upstream gradient
+ *   kv_frags_bwd: mrsa_kv_fragments(v, k) (the roles of k and v swapped: V as
+ *                 keys x dims, K^T as dims x keys)
+ * Requirements: head_dim 128, chunk_size 64, q_heads / kv_heads <= 16, topk <= 64.
+ */
+int mrsa_selected_attention_bwd(const void* q, const void* grad_out, const void* kv_frags,
+                                const void* kv_frags_bwd, const void* weights,
+                                const int32_t* indices, const uint8_t* key_valid,
+                                const int8_t* token_keep, int64_t batch, int64_t q_len,
+                                int64_t kv_len, int64_t q_heads, int64_t kv_heads,
+                                int64_t head_dim, int64_t topk, int64_t chunk_size,
+                                int mask_last_token, float sm_scale, float* grad_q,
+                                float* grad_k, float* grad_v, void* grad_weights, void* stream);
+
+/*
  * Routed chunk attention with the output fusion folded in: the result is
  * fuse_hils_outputs(remote, local_output, local_weight)
  * (ops/hils_bidir_output_fusion_tilelang.py:138-148) of the routed output

@@ -112,6 +112,11 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
          _I, _F, _I64, _P, _P, _P],
     ),
+    "mrsa_selected_attention_bwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+         _I, _F, _P, _P, _P, _P, _P],
+    ),
     "mrsa_token_keep_fwd": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "mrsa_candidate_token_scores_fwd": (
         _I,

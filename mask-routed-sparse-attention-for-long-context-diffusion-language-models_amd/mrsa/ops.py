@@ -26,7 +26,8 @@ from .local_attention import _local_attention_impl
 from .pool import _pool_bwd_impl, _pool_impl
 from .route_weights import _route_weights_bwd_impl, _route_weights_impl
 from .sparse_attention import (FRAG_ELEMS, _kv_fragments_impl, _kv_fragments_rows_impl,
-                               _selected_attention_impl)
+                               _selected_attention_impl,
+                               _selected_attention_bwd_impl)
 from .token_refinement import _token_keep_impl
 from .token_score import _token_scores_impl
 from .topk import _route_topk_impl
@@ -197,6 +198,28 @@ def _(remote_output, local_output, local_weight):
     return torch.empty_like(remote_output)
 
 
+@_op("selected_attention_bwd")
+def selected_attention_bwd(q: Tensor, kv_frags: Tensor, kv_frags_bwd: Tensor, weights: Tensor,
+                           indices: Tensor, key_valid: Optional[Tensor], grad_output: Tensor,
+                           chunk_size: int, mask_last_token: bool, sm_scale: float,
+                           token_keep: Optional[Tensor], kv_len: int
+                           ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    return _selected_attention_bwd_impl(q, kv_frags, kv_frags_bwd, weights, indices, key_valid,
+                                        grad_output, chunk_size, mask_last_token, sm_scale,
+                                        token_keep, kv_len)
+
+
+@selected_attention_bwd.register_fake
+def _(q, kv_frags, kv_frags_bwd, weights, indices, key_valid, grad_output, chunk_size,
+      mask_last_token, sm_scale, token_keep, kv_len):
+    B, Lq, Hq, D = q.shape
+    Hkv = kv_frags.shape[1]
+    return (q.new_empty(B, Lq, Hq, D, dtype=torch.float32),
+            q.new_empty(B, kv_len, Hkv, D, dtype=torch.float32),
+            q.new_empty(B, kv_len, Hkv, D, dtype=torch.float32),
+            q.new_empty(B, Lq, Hq, indices.shape[-1], dtype=torch.bfloat16))
+
+
 @_op("fuse_hils_outputs_bwd")
 def fuse_hils_outputs_bwd(local_output: Tensor, local_weight: Tensor,
                           grad_output: Tensor) -> tuple[Tensor, Tensor, Tensor]:
@@ -260,6 +283,7 @@ def _(ranking, token_budget, as_int8):
 OPERATORS = (
     "kv_fragments", "kv_fragments_rows_", "local_attention", "chunk_attn_pool",
     "chunk_attn_pool_bwd", "route_topk", "route_weights", "route_weights_bwd",
-    "selected_attention", "fuse_hils_outputs", "fuse_hils_outputs_bwd", "remote_drop_mask",
+    "selected_attention", "selected_attention_bwd", "fuse_hils_outputs", "fuse_hils_outputs_bwd",
+    "remote_drop_mask",
     "remote_drop_mask_rows", "candidate_token_scores", "token_keep",
 )

@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import torch
 
-from .sparse_attention import kv_fragments, selected_attention_launch
+from .sparse_attention import kv_fragments, selected_attention_autograd, selected_attention_launch
 from .topk import route_topk_launch
 
 _LOGICAL_G = 7
@@ -130,13 +130,12 @@ def _validate_selected(q, k, v, weights, indices, key_valid, chunk_size, token_k
 
 def selected_attention_g7(q, k, v, weights, indices, key_valid, chunk_size, training,
                           token_keep=None):
-    """Selected-chunk attention with compact KV (routing.py:305-328); forward only."""
+    """Selected-chunk attention with compact KV (routing.py:305-328), with
+    autograd when an input requires grad."""
 
     _validate_selected(q, k, v, weights, indices, key_valid, chunk_size, token_keep)
-    return selected_attention_launch(
-        q, kv_fragments(k, v), weights, indices, key_valid, chunk_size, mask_last_token=True,
-        token_keep=token_keep,
-    )
+    return selected_attention_autograd(q, k, v, weights, indices, key_valid, chunk_size,
+                                       mask_last_token=True, token_keep=token_keep)
 
 
 def selected_attention_g7_cached(q, k, v, weights, indices, key_valid, chunk_size,

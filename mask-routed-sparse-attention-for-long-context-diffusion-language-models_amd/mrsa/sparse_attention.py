@@ -206,6 +206,83 @@ def _selected_attention_impl(q, kv_frags, weights, indices, key_valid, chunk_siz
     return out
 
 
+def selected_attention_backward(q, k, v, weights, indices, key_valid, chunk_size, grad_output,
+                                *, mask_last_token=True, sm_scale=None, token_keep=None):
+    """Gradients (dq, dk, dv, dweights) of the routed attention, in the input
+    dtypes (ops/hils_fwd_bwd_head.py:1050-1098: fp32 accumulation, cast at
+    the end).  The fragment layouts of (k, v) and of (v, k) are built here."""
+
+    return torch.ops.mrsa.selected_attention_bwd(
+        q, kv_fragments(k, v), kv_fragments(v, k), weights, indices, key_valid,
+        grad_output, int(chunk_size), bool(mask_last_token),
+        float(sm_scale if sm_scale is not None else 1.0 / math.sqrt(q.shape[-1])), token_keep,
+        int(k.shape[1]))
+
+
+def _selected_attention_bwd_impl(q, kv_frags, kv_frags_bwd, weights, indices, key_valid,
+                                 grad_output, chunk_size, mask_last_token, sm_scale,
+                                 token_keep, kv_len):
+    B, Lq, Hq, D = q.shape
+    Hkv = kv_frags.shape[1]
+    K = indices.shape[-1]
+    qc = q.to(torch.bfloat16).contiguous()
+    go = grad_output.to(torch.bfloat16).contiguous()
+    w = weights.to(torch.bfloat16).contiguous()
+    idx = indices.to(torch.int32).contiguous()
+    kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
+    keep = None if token_keep is None else token_keep.to(device=q.device, dtype=torch.int8).contiguous()
+    dq = torch.empty(B, Lq, Hq, D, dtype=torch.float32, device=q.device)
+    dk = torch.zeros(B, kv_len, Hkv, D, dtype=torch.float32, device=q.device)
+    dv = torch.zeros(B, kv_len, Hkv, D, dtype=torch.float32, device=q.device)
+    dw = torch.empty(B, Lq, Hq, K, dtype=torch.bfloat16, device=q.device)
+    st = _lib.call(
+        "mrsa_selected_attention_bwd",
+        _lib.ptr(qc), _lib.ptr(go), _lib.ptr(kv_frags.contiguous()),
+        _lib.ptr(kv_frags_bwd.contiguous()), _lib.ptr(w), _lib.ptr(idx), _lib.ptr(kv),
+        _lib.ptr(keep), B, Lq, kv_len, Hq, Hkv, D, K, int(chunk_size),
+        1 if mask_last_token else 0, float(sm_scale), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
+        _lib.ptr(dw), _lib.stream_of(qc),
+    )
+    _lib.check(st, "selected_attention backward")
+    return dq, dk, dv, dw
+
+
+class _SelectedAttention(torch.autograd.Function):
+    # ops/hils_fwd_bwd_head.py:915-1098 (_hils_block_M_attention_inverse):
+    # the forward saves its inputs; the backward recomputes each chunk's
+    # softmax and casts the fp32 gradients to the input dtypes.
+    @staticmethod
+    def forward(ctx, q, k, v, weights, indices, key_valid, chunk_size, mask_last_token,
+                sm_scale, token_keep):
+        ctx.save_for_backward(q, k, v, weights, indices, key_valid, token_keep)
+        ctx.chunk_size, ctx.mask_last_token, ctx.sm_scale = chunk_size, mask_last_token, sm_scale
+        return selected_attention_launch(
+            q, kv_fragments(k, v), weights, indices, key_valid, chunk_size,
+            mask_last_token=mask_last_token, sm_scale=sm_scale, token_keep=token_keep)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        q, k, v, weights, indices, key_valid, token_keep = ctx.saved_tensors
+        dq, dk, dv, dw = selected_attention_backward(
+            q, k, v, weights, indices, key_valid, ctx.chunk_size, grad_output,
+            mask_last_token=ctx.mask_last_token, sm_scale=ctx.sm_scale, token_keep=token_keep)
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dw.to(weights.dtype),
+                None, None, None, None, None, None)
+
+
+def selected_attention_autograd(q, k, v, weights, indices, key_valid, chunk_size, *,
+                                mask_last_token=True, sm_scale=None, token_keep=None):
+    """Routed attention with autograd when an input requires grad (gfx950
+    forward and backward kernels), else the plain forward."""
+
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, weights)):
+        return _SelectedAttention.apply(q, k, v, weights, indices, key_valid, chunk_size,
+                                        mask_last_token, sm_scale, token_keep)
+    return selected_attention_launch(
+        q, kv_fragments(k, v), weights, indices, key_valid, chunk_size,
+        mask_last_token=mask_last_token, sm_scale=sm_scale, token_keep=token_keep)
+
+
 def HiLS_block_M_head(
     q, k, v, weights, indices,
     block_size=64, sm_scale=None, block_M=None,
@@ -213,10 +290,12 @@ def HiLS_block_M_head(
     num_threads=None, num_threads_fwd=None, num_threads_bwd=None,
     is_training=True, slope=None, key_valid=None, token_keep=None,
 ):
-    """Same arguments as ops/hils_fwd_bwd_head.py:1113-1150, forward only.
+    """Same arguments as ops/hils_fwd_bwd_head.py:1113-1150, with autograd
+    (the backward of ops/hils_fwd_bwd_head.py:573-910) when an input requires
+    grad.
 
     Tiling knobs (block_M, num_threads*) are accepted and ignored: the gfx950
-    kernel picks its own tiling.  ALiBi slopes are not supported.
+    kernels pick their own tiling.  ALiBi slopes are not supported.
     """
 
     B, L, HQ, D = q.shape
@@ -236,9 +315,7 @@ def HiLS_block_M_head(
         raise ValueError("only bf16 inputs with fp32 accumulation are supported")
     if key_valid is not None and key_valid.shape != (B, L_kv):
         raise ValueError(f"key_valid must have shape {(B, L_kv)}, got {tuple(key_valid.shape)}")
-    if any(t.requires_grad for t in (q, k, v, weights)) and torch.is_grad_enabled():
-        raise ValueError("HiLS_block_M_head on gfx950 is forward-only (no autograd)")
-    return selected_attention_launch(
-        q, kv_fragments(k, v), weights, indices, key_valid, block_size,
+    return selected_attention_autograd(
+        q, k, v, weights, indices, key_valid, block_size,
         mask_last_token=mask_last_token, sm_scale=sm_scale, token_keep=token_keep,
     )

@@ -215,3 +215,85 @@ def test_pool_prior_backward():
     torch.testing.assert_close(bs.grad.cpu(), e_scale, atol=1e-3, rtol=1e-3)
     e_mu, _ = O.chunk_attn_pool_bwd(mu, k, valid, g_lmk, g_prior * scale_t.reshape(H, G), D ** -0.5)
     assert _rel(m.grad.cpu(), e_mu) < 5e-3
+
+
+# ---------------------------------------------------------------------------
+# Routed (selected-chunk) attention backward (ops/hils_fwd_bwd_head.py:573-910)
+# against the oracle's autograd.  The kernel rounds P, bf16(w dO) and dS to
+# bf16 where the reference does and returns bf16 gradients, so each gradient
+# is compared by its relative norm error (the reference test's measure for
+# this op, test_hils_non_power_two_topk.py:139-142: rel. norm < 0.02).
+# ---------------------------------------------------------------------------
+def _rel_err(a, b):
+    a = a.float().cpu()
+    b = b.float().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-12))
+
+
+@pytest.mark.parametrize("keep", [False, True])
+def test_selected_attention_backward_vs_oracle(keep):
+    _note(f"selected attention backward keep={keep}")
+    B, Lq, Hkv, G, D, C, K = 1, 192, 4, 7, 128, 16, 8
+    Lk = C * 64
+    g = torch.Generator().manual_seed(70 + keep)
+    q = (torch.randn(B, Lq, Hkv * G, D, generator=g) * 0.5).bfloat16()
+    k = (torch.randn(B, Lk, Hkv, D, generator=g) * 0.5).bfloat16()
+    v = torch.randn(B, Lk, Hkv, D, generator=g).bfloat16()
+    w = torch.rand(B, Lq, Hkv * G, K, generator=g).bfloat16()
+    idx = torch.stack([torch.randperm(C, generator=g)[:K] for _ in range(B * Lq * Hkv)])
+    idx = idx.reshape(B, Lq, Hkv, K).int()
+    idx[0, 5, 1, 5:] = -1              # list end
+    idx[0, 6, 2, 3] = idx[0, 6, 2, 1]  # a chunk listed twice
+    idx[0, 7, 0, 2] = C + 3            # out of range: skipped
+    valid = torch.rand(B, Lk, generator=g) > 0.05
+    token_keep = None
+    if keep:
+        token_keep = (torch.rand(B, Lq, Hkv, K, 64, generator=g) > 0.3).to(torch.int8)
+    dout = torch.randn(B, Lq, Hkv * G, D, generator=g).bfloat16()
+
+    tq, tk, tv, tw = (t.to(DEV).requires_grad_(True) for t in (q, k, v, w))
+    out = mrsa.HiLS_block_M_head(tq, tk, tv, tw, idx.to(DEV), key_valid=valid.to(DEV),
+                                 token_keep=None if token_keep is None else token_keep.to(DEV))
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+
+    rq, rk, rv, rw = (t.float().requires_grad_(True) for t in (q, k, v, w))
+    ref = O.selected_attention(rq, rk, rv, rw, idx, valid, token_keep=token_keep)
+    (ref * dout.float()).sum().backward()
+    for name, got, exp in (("dq", tq.grad, rq.grad), ("dk", tk.grad, rk.grad),
+                           ("dv", tv.grad, rv.grad), ("dw", tw.grad, rw.grad)):
+        assert got.dtype == torch.bfloat16, name
+        err = _rel_err(got, exp)
+        print(f"  {name}: rel-norm error {err:.3e}", flush=True)
+        assert err < 2e-2, (name, err)
+    # slots past a list's end or out of range get zero weight gradient
+    assert float(tw.grad[0, 5, 7:14, 5:].abs().max()) == 0.0
+    assert float(tw.grad[0, 7, 0:7, 2].abs().max()) == 0.0
+
+
+def test_selected_attention_backward_split_query_block():
+    # A 32-query block against a longer cache (the cached step's shape): the
+    # forward takes the walk split, the backward is the same kernel.
+    _note("selected attention backward, 32 queries against 64 chunks")
+    B, Lq, Hkv, G, D, C, K = 1, 32, 4, 7, 128, 64, 16
+    Lk = C * 64
+    g = torch.Generator().manual_seed(80)
+    q = (torch.randn(B, Lq, Hkv * G, D, generator=g) * 0.5).bfloat16()
+    k = (torch.randn(B, Lk, Hkv, D, generator=g) * 0.5).bfloat16()
+    v = torch.randn(B, Lk, Hkv, D, generator=g).bfloat16()
+    w = torch.rand(B, Lq, Hkv * G, K, generator=g).bfloat16()
+    idx = torch.stack([torch.randperm(C, generator=g)[:K].sort().values
+                       for _ in range(B * Lq * Hkv)]).reshape(B, Lq, Hkv, K).int()
+    dout = torch.randn(B, Lq, Hkv * G, D, generator=g).bfloat16()
+    tq, tk, tv, tw = (t.to(DEV).requires_grad_(True) for t in (q, k, v, w))
+    valid = torch.ones(B, Lk, dtype=torch.bool)
+    out = mrsa.selected_attention_g7(tq, tk, tv, tw, idx.to(DEV), valid.to(DEV), 64, True)
+    out.backward(dout.to(DEV))
+    rq, rk, rv, rw = (t.float().requires_grad_(True) for t in (q, k, v, w))
+    ref = O.selected_attention(rq, rk, rv, rw, idx, valid)
+    (ref * dout.float()).sum().backward()
+    for name, got, exp in (("dq", tq.grad, rq.grad), ("dk", tk.grad, rk.grad),
+                           ("dv", tv.grad, rv.grad), ("dw", tw.grad, rw.grad)):
+        err = _rel_err(got, exp)
+        print(f"  {name}: rel-norm error {err:.3e}", flush=True)
+        assert err < 2e-2, (name, err)

@@ -235,3 +235,81 @@ def test_pool_dense_backward_is_torch_twin_autograd():
         mm.view(-1)[flat] -= eps
         fd = (loss(mp) - loss(mm)) / (2 * eps)
         assert abs(fd - float(a_mu.view(-1)[flat])) < 3e-3, flat
+
+
+# ---------------------------------------------------------------------------
+# Routed (selected-chunk) attention backward: the reference kernel
+# (ops/hils_fwd_bwd_head.py:573-910) computes the softmax-attention chain rule
+#   dV += P^T (w dO),  dW = sum_s P (dO . V_s),
+#   dS = scale w P (dO . V - dW),  dQ = dS K,  dK = dS^T Q;
+# the oracle's backward is torch autograd of its forward restatement.
+# ---------------------------------------------------------------------------
+def _sel_inputs(seed, B=1, Lq=3, Hkv=2, G=3, D=128, C=3, K=2):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Lq, Hkv * G, D, generator=g) * 0.3
+    k = torch.randn(B, C * 64, Hkv, D, generator=g) * 0.3
+    v = torch.randn(B, C * 64, Hkv, D, generator=g)
+    w = torch.rand(B, Lq, Hkv * G, K, generator=g)
+    idx = torch.randint(0, C, (B, Lq, Hkv, K), generator=g)
+    idx[0, 0, 1, 1] = -1
+    valid = torch.ones(B, C * 64, dtype=torch.bool)
+    valid[0, 5] = False
+    dout = torch.randn(B, Lq, Hkv * G, D, generator=g)
+    return q, k, v, w, idx, valid, dout
+
+
+def _sel_grads(q, k, v, w, idx, valid, dout):
+    ts = [t.clone().requires_grad_(True) for t in (q, k, v, w)]
+    out = O.selected_attention(ts[0], ts[1], ts[2], ts[3], idx, valid)
+    (out * dout).sum().backward()
+    return [t.grad for t in ts]
+
+
+def test_oracle_selected_attention_grad_closed_form_uniform_softmax():
+    # q = 0: every visible key of a chunk has p = 1 / n, so out = w mean(V)
+    # and dV_s = w dO / n, dW = dO . mean(V), dK = 0 (dS^T q = 0), and
+    # dQ = scale w / n sum_s (dO . V_s - dW) K_s.
+    B, Lq, Hkv, G, D, C = 1, 1, 1, 1, 128, 2
+    g = torch.Generator().manual_seed(3)
+    q = torch.zeros(B, Lq, Hkv * G, D)
+    k = torch.randn(B, C * 64, Hkv, D, generator=g)
+    v = torch.randn(B, C * 64, Hkv, D, generator=g)
+    w = torch.full((B, Lq, Hkv * G, 1), 0.7)
+    idx = torch.tensor([[[[1]]]])
+    valid = torch.ones(B, C * 64, dtype=torch.bool)
+    dout = torch.randn(B, Lq, Hkv * G, D, generator=g)
+    dq, dk, dv, dw = _sel_grads(q, k, v, w, idx, valid, dout)
+    keys = torch.arange(64, 127)  # chunk 1 without its landmark slot
+    vs, ks = v[0, keys, 0], k[0, keys, 0]
+    n = keys.numel()
+    do = dout[0, 0, 0]
+    torch.testing.assert_close(dv[0, keys, 0], (0.7 / n) * do.expand(n, D), atol=1e-6, rtol=1e-5)
+    assert float(dv[0, 127].abs().max()) == 0.0 and float(dv[0, :64].abs().max()) == 0.0
+    torch.testing.assert_close(dw[0, 0, 0, 0], (do * vs.mean(0)).sum(), atol=1e-5, rtol=1e-5)
+    assert float(dk.abs().max()) == 0.0
+    dp = vs @ do
+    ref_dq = (1.0 / math.sqrt(D)) * 0.7 / n * ((dp - dp.mean())[:, None] * ks).sum(0)
+    torch.testing.assert_close(dq[0, 0, 0], ref_dq, atol=1e-5, rtol=1e-4)
+
+
+def test_oracle_selected_attention_grad_central_differences():
+    q, k, v, w, idx, valid, dout = _sel_inputs(11)
+    dq, dk, dv, dw = _sel_grads(q, k, v, w, idx, valid, dout)
+
+    def f(q_, k_, v_, w_):
+        return float((O.selected_attention(q_, k_, v_, w_, idx, valid) * dout).sum())
+
+    g = torch.Generator().manual_seed(12)
+    eps = 1e-2
+    for which, grad in ((0, dq), (1, dk), (2, dv), (3, dw)):
+        base = [q, k, v, w]
+        t = base[which]
+        # a random direction through the tensor
+        d = torch.randn(t.shape, generator=g)
+        plus = [x.clone() for x in base]
+        minus = [x.clone() for x in base]
+        plus[which] = t + eps * d
+        minus[which] = t - eps * d
+        num = (f(*plus) - f(*minus)) / (2 * eps)
+        ana = float((grad * d).sum())
+        assert abs(num - ana) <= 2e-2 * max(1.0, abs(ana)), (which, num, ana)
