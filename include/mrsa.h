@@ -233,6 +233,37 @@ int mrsa_route_topk_noalloc_fwd(const void* q, const void* lmk, const float* lse
                                 void* stream);
 
 /*
+ * Backward of the route scores score[l, h, g, k] = sm_scale * q[l, h, g] .
+ * lmk[idx[l, h, k], hl] (hl = h * groups + g per-head, h shared): replaces
+ * SoftmaxTopKMaxPoolingFusedFn.backward (ops/topk_head_softmax.py:1074-1122),
+ * without its dense [batch * kv_heads * groups, seq_len, chunks] scatter
+ * buffer.  The gradient is multiplied by sm_scale and rounded to bf16 (the
+ * reference's mul_ in the gradient's bf16 dtype); slots whose index lies
+ * outside [0, chunks) contribute nothing.
+ *   q:           bf16 [batch, seq_len, kv_heads, groups, 128]
+ *   landmarks:   bf16 [batch, chunks, kv_heads * groups or kv_heads, 128]
+ *   indices:     int32 [batch, seq_len, kv_heads, topk]
+ *   grad_scores: [batch, seq_len, kv_heads, groups, topk], bf16 or fp32
+ *                (grad_scores_fp32 = 1)
+ *   grad_q (out):         bf16, the shape of q
+ *   grad_landmarks (out): bf16, the shape of landmarks (summed over the
+ *                         group for shared landmarks)
+ *   workspace: 16-byte aligned, mrsa_route_score_bwd_workspace_bytes(...)
+ *              bytes (fp32 parts of grad_landmarks; grad_q in fp32 when
+ *              chunks > 256).  The result does not depend on timing.
+ * Requirements: head_dim 128, topk <= 4096.
+ */
+int64_t mrsa_route_score_bwd_workspace_bytes(int64_t batch, int64_t seq_len, int64_t chunks,
+                                             int64_t kv_heads, int64_t groups,
+                                             int per_head_lmk);
+int mrsa_route_score_bwd(const void* q, const void* landmarks, const int32_t* indices,
+                         const void* grad_scores, int grad_scores_fp32, int64_t batch,
+                         int64_t seq_len, int64_t chunks, int64_t kv_heads, int64_t groups,
+                         int64_t head_dim, int64_t topk, int per_head_lmk, float sm_scale,
+                         void* grad_q, void* grad_landmarks, void* workspace,
+                         int64_t workspace_bytes, void* stream);
+
+/*
  * Route weights: softmax over [score_k + bias[idx_k] (k < topk), local_lse].
  * Replaces _route_weights_torch (dream_dllm_hils/attention.py:126-235; the
  * topk >= 32 path, selected at :1571-1621) and route_weights
@@ -431,18 +462,30 @@ int mrsa_selected_attention_keep_fwd(const void* q, const void* kv_frags,
  * _hils_block_M_attention_inverse.backward, :1050-1098).  Each listed
  * (query, chunk) recomputes its chunk softmax; with the reference's rounding
  * points P = bf16(2^(s c - lse)), di = sum P dP, dS = bf16(scale w P (dP - di)):
- *   grad_q  = sum dS K              fp32 [batch, q_len, q_heads, head_dim] (written)
+ *   grad_q += sum dS K              fp32 [batch, q_len, q_heads, head_dim] (added
+ *                                   with atomics: zero it first)
  *   grad_k += dS^T Q, grad_v += P^T bf16(w dO)
  *                                   fp32 [batch, kv_len, kv_heads, head_dim]
- *                                   (accumulated with atomic adds: zero them first)
- *   grad_weights = di               bf16 [batch, q_len, q_heads, topk] (0 for slots
- *                                   past the list's end or out of range)
+ *                                   (zero them first: a chunk no query routes to
+ *                                   is not written)
+ *   grad_weights = di               bf16 [batch, q_len, q_heads, topk] (slots past
+ *                                   the list's end or out of range are not
+ *                                   written: zero it first)
  * Arguments as mrsa_selected_attention_keep_fwd (token_keep may be null), plus
  *   grad_out:     bf16 [batch, q_len, q_heads, head_dim] upstream gradient
  *   kv_frags_bwd: mrsa_kv_fragments(v, k) (the roles of k and v swapped: V as
  *                 keys x dims, K^T as dims x keys)
- * Requirements: head_dim 128, chunk_size 64, q_heads / kv_heads <= 16, topk <= 64.
+ *   workspace:    256-byte aligned, mrsa_selected_attention_bwd_workspace_bytes
+ *                 bytes: the per-chunk lists of (query, slot) pairs from which
+ *                 grad_k / grad_v are computed chunk by chunk (one write per
+ *                 chunk; chunks with more than 1024 pairs add their segments'
+ *                 sums with atomics, so their last bits depend on timing).
+ * Requirements: head_dim 128, chunk_size 64, q_heads / kv_heads <= 8, topk <= 64,
+ * kv_len / 64 <= 8192, q_len < 2^24.
  */
+int64_t mrsa_selected_attention_bwd_workspace_bytes(int64_t batch, int64_t q_len,
+                                                    int64_t kv_len, int64_t kv_heads,
+                                                    int64_t topk);
 int mrsa_selected_attention_bwd(const void* q, const void* grad_out, const void* kv_frags,
                                 const void* kv_frags_bwd, const void* weights,
                                 const int32_t* indices, const uint8_t* key_valid,
@@ -450,7 +493,8 @@ int mrsa_selected_attention_bwd(const void* q, const void* grad_out, const void*
                                 int64_t kv_len, int64_t q_heads, int64_t kv_heads,
                                 int64_t head_dim, int64_t topk, int64_t chunk_size,
                                 int mask_last_token, float sm_scale, float* grad_q,
-                                float* grad_k, float* grad_v, void* grad_weights, void* stream);
+                                float* grad_k, float* grad_v, void* grad_weights,
+                                void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Routed chunk attention with the output fusion folded in: the result is

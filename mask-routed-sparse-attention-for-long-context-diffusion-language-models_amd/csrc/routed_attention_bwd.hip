@@ -10,21 +10,29 @@
 //   dP     = dO . V^T (fp32);  di = sum_s P dP  ->  dW[q, g, k] = di (bf16);
 //   dS     = bf16(scale * w * P * (dP - di));
 //   dQ    += dS . K            (fp32, summed over the query's chunks);
-//   dK    += dS^T . Q,  dV += P^T . bf16(w * dO)  (fp32 atomic adds, like the
-//            reference's atomic_add into DK / DV).
+//   dK    += dS^T . Q,  dV += P^T . bf16(w * dO)  (fp32, summed over the
+//            (query, slot) pairs that route to the chunk).
 // A chunk listed twice is processed once per slot (its gradient terms add,
 // as the weights do in the forward).
 //
-// Work split: one wave per (batch, query, KV head), four per workgroup.  The
-// wave's 16 matrix columns are the group's heads (columns >= G are zero).
+// Work split (chunk-major).  A list of the (query, slot) pairs of every
+// chunk is built first (count, scan, fill); a workgroup then owns one chunk
+// (or a segment of kSegEntries of its pairs) and recomputes each pair's
+// chunk softmax:
+//   dK / dV  stay in the workgroup's registers and are written once per
+//            chunk (added with atomics when the chunk's pairs span several
+//            segments) -- the reference instead adds each query block's
+//            dK / dV into global memory with atomics;
+//   dQ       each pair's dS . K is added into the query's fp32 dQ rows with
+//            atomics (16 lanes per 64-byte row segment);
+//   dW       written directly (one pair = one slot).
 // Operands come from two fragment layouts of the same K / V:
 //   fwd = mrsa_kv_fragments(k, v): K images (keys x dims) for S^T = K . Q^T;
 //   bwd = mrsa_kv_fragments(v, k): V images (keys x dims) for dP^T = V . dO^T
-//         and K^T images (dims x keys, tiled order) for dQ^T = K^T . dS^T.
-// dK and dV (keys x dims) run as 16x16x32 products whose reduction is the
-// 16 columns (lane groups 2 and 3 supply zeros), with dS^T / P^T and Q^T /
-// dO^T staged through per-wave LDS tiles.
+//         and K^T images (dims x keys, tiled order) for dQ = dS . K.
 #include "mrsa_device.h"
+
+#include <algorithm>
 
 using namespace mrsa;
 
@@ -52,16 +60,11 @@ struct BwdArgs {
   float* dk;                 // [B, Lk, Hkv, 128] fp32, accumulated
   float* dv;                 // [B, Lk, Hkv, 128] fp32, accumulated
   uint16_t* dw;              // [B, Lq, Hq, K] bf16
-};
-
-// Per-wave LDS tiles (bf16): Q^T and dO^T as [128 dims][16 columns], and the
-// transposes of P and dS as [64 keys][16 columns].
-struct WaveTiles {
-  uint16_t qt[128 * 16];
-  uint16_t dt[128 * 16];
-  uint16_t ps[64 * 16];
-  uint16_t ds[64 * 16];
-  float wcol[16];
+  // chunk-major pass: pair lists (entry = query | slot << 24), per chunk
+  // (b, h, c) the list start and the first work unit
+  const int32_t* list;
+  const int32_t* start;      // [B * Hkv * Ck + 1]
+  const int32_t* ustart;     // [B * Hkv * Ck + 1]
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -79,238 +82,435 @@ __device__ __forceinline__ void load_rows(u32x4_t (&x)[4][4], __amdgpu_buffer_rs
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) x[mt][ks] = bload(r, lo + 1024u * ks, cb + 4096u * mt);
 }
-// Second-half images (V^T or K^T, dims x keys): image 2 nt + ks at 16384 + 1024 (2 nt + ks).
-__device__ __forceinline__ void load_cols(u32x4_t (&x)[8][2], __amdgpu_buffer_rsrc_t r,
-                                          uint32_t lo, uint32_t cb) {
-#pragma unroll
-  for (int nt = 0; nt < 8; ++nt)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int i = 2 * nt + ks;
-      x[nt][ks] = bload(r, lo + 1024u * (i & 3), cb + 16384u + 4096u * (i >> 2));
-    }
-}
-
 // Bits of the nonzero bytes (bit j = byte j) of one 64-byte keep / key-valid
 // row: one byte per lane and a wave ballot (every lane must be active).
 __device__ __forceinline__ uint64_t nonzero_bits(const int8_t* row) {
   return __builtin_amdgcn_ballot_w64(row[threadIdx.x & 63] != 0);
 }
 
-__global__ void __launch_bounds__(kThreads) routed_attn_bwd_kernel(BwdArgs a) {
-  __shared__ WaveTiles tiles[kWaves];
-  __shared__ int32_t list_s[kWaves][kMaxTopk];
+// One column tile's chunk gradient, in place.  S^T / dP^T lane (grp, j):
+// keys 16 mt + 4 grp + r of column j; msh bit 16 mt + r set = key excluded.
+//   S  <- P  = bf16(2^(s c - lse)) over the visible keys (0 when none is)
+//   dP <- dS = bf16(sw P (dP - di)),  di = sum P dP per column (returned)
+__device__ __forceinline__ float chunk_grad(f32x4_t (&S)[4], f32x4_t (&dP)[4], uint64_t msh,
+                                            float c2, float sw) {
+  float mx = neg_inf();
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (!((msh >> (16 * mt + r)) & 1ull)) mx = fmaxf(mx, S[mt][r] * c2);
+  mx = across4_max(mx);
+  float sum = 0.f;
+  if (mx != neg_inf()) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (!((msh >> (16 * mt + r)) & 1ull)) sum += exp2_hw(S[mt][r] * c2 - mx);
+  }
+  sum = across4_sum(sum);
+  const float lse = mx == neg_inf() ? neg_inf() : mx + log2_hw(sum);
+  float di = 0.f;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool vis = !((msh >> (16 * mt + r)) & 1ull) && lse != neg_inf();
+      const float p = vis ? bf16_to_f32(f32_to_bf16(exp2_hw(S[mt][r] * c2 - lse))) : 0.f;
+      S[mt][r] = p;
+      di += p * dP[mt][r];
+    }
+  di = across4_sum(di);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      dP[mt][r] = bf16_to_f32(f32_to_bf16(sw * S[mt][r] * (dP[mt][r] - di)));
+  return di;
+}
+
+// ---- chunk-major dK / dV ---------------------------------------------------
+constexpr int kListBlock = 256;       // queries per list workgroup (one per thread)
+constexpr int kMaxListChunks = 8192;  // LDS counters of the list kernels (32 KB)
+constexpr int kSegEntries = 1024;     // (query, slot) pairs per dK / dV work unit
+
+// The valid slots of one index row: up to the first negative entry, chunks
+// below Ck.
+template <class F>
+__device__ __forceinline__ void for_each_slot(const int32_t* row, int K, int64_t Ck, F&& f) {
+  for (int k = 0; k < K; ++k) {
+    const int32_t c = row[k];
+    if (c < 0) break;
+    if (c < Ck) f(k, c);
+  }
+}
+
+// 1. Pairs per (chunk, query block) in LDS; each block's run of a chunk's
+//    list is reserved with one global add (blkbase = its offset).
+__global__ void __launch_bounds__(kListBlock) list_count_kernel(BwdArgs a, int32_t* count,
+                                                                int32_t* blkbase, int nqb) {
+  __shared__ int32_t hist[kMaxListChunks];
+  const int tid = threadIdx.x;
+  const int qb = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / a.Hkv;
+  const int h = (int)(bh % a.Hkv);
+  for (int64_t c = tid; c < a.Ck; c += kListBlock) hist[c] = 0;
+  __syncthreads();
+  const int64_t q = (int64_t)qb * kListBlock + tid;
+  if (q < a.Lq)
+    for_each_slot(a.idx + ((b * a.Lq + q) * a.Hkv + h) * a.K, a.K, a.Ck,
+                  [&](int, int32_t c) { atomicAdd(&hist[c], 1); });
+  __syncthreads();
+  for (int64_t c = tid; c < a.Ck; c += kListBlock) {
+    const int n = hist[c];
+    blkbase[(bh * nqb + qb) * a.Ck + c] = n ? atomicAdd(&count[bh * a.Ck + c], n) : 0;
+  }
+}
+
+// 2. Exclusive scans over the chunks (b, h, c): list starts and work-unit
+//    starts (ceil(count / kSegEntries) units per chunk).  One workgroup.
+__global__ void __launch_bounds__(1024) list_scan_kernel(const int32_t* count, int64_t N,
+                                                         int32_t* start, int32_t* ustart) {
+  __shared__ int32_t s1[1024], s2[1024];
+  const int tid = threadIdx.x;
+  const int64_t per = (N + 1023) / 1024;
+  const int64_t lo = min(N, tid * per), hi = min(N, lo + per);
+  int32_t t1 = 0, t2 = 0;
+  for (int64_t i = lo; i < hi; ++i) {
+    t1 += count[i];
+    t2 += (count[i] + kSegEntries - 1) / kSegEntries;
+  }
+  s1[tid] = t1;
+  s2[tid] = t2;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    const int32_t u1 = tid >= o ? s1[tid - o] : 0, u2 = tid >= o ? s2[tid - o] : 0;
+    __syncthreads();
+    s1[tid] += u1;
+    s2[tid] += u2;
+    __syncthreads();
+  }
+  int32_t r1 = s1[tid] - t1, r2 = s2[tid] - t2;
+  for (int64_t i = lo; i < hi; ++i) {
+    start[i] = r1;
+    ustart[i] = r2;
+    r1 += count[i];
+    r2 += (count[i] + kSegEntries - 1) / kSegEntries;
+  }
+  if (tid == 1023) {
+    start[N] = s1[1023];
+    ustart[N] = s2[1023];
+  }
+}
+
+// 3. Pairs written into their chunk's list: query | slot << 24.
+__global__ void __launch_bounds__(kListBlock) list_fill_kernel(BwdArgs a, const int32_t* blkbase,
+                                                               int nqb, int32_t* list) {
+  __shared__ int32_t cur[kMaxListChunks];
+  const int tid = threadIdx.x;
+  const int qb = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / a.Hkv;
+  const int h = (int)(bh % a.Hkv);
+  for (int64_t c = tid; c < a.Ck; c += kListBlock) cur[c] = 0;
+  __syncthreads();
+  const int64_t q = (int64_t)qb * kListBlock + tid;
+  if (q < a.Lq)
+    for_each_slot(a.idx + ((b * a.Lq + q) * a.Hkv + h) * a.K, a.K, a.Ck, [&](int k, int32_t c) {
+      const int p = atomicAdd(&cur[c], 1);
+      const int64_t bhc = bh * a.Ck + c;
+      list[(int64_t)a.start[bhc] + blkbase[(bh * nqb + qb) * a.Ck + c] + p] =
+          (int32_t)(q | ((int64_t)k << 24));
+    });
+}
+
+// Kept-key bits (bit j = key j kept) of one 64-byte token-keep row, per lane.
+__device__ __forceinline__ uint64_t keep_row_bits(const int8_t* kr) {
+  uint64_t bits = 0ull;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const u32x4_t x = *reinterpret_cast<const u32x4_t*>(kr + 16 * v);
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        bits |= ((x[w] >> (8 * i)) & 0xffu) ? 1ull << (16 * v + 4 * w + i) : 0ull;
+  }
+  return bits;
+}
+
+// LDS of the chunk-major kernel (bytes): the chunk's V images and K^T images
+// (16 KB each, lane l's 16 bytes of image i at 1024 i + 16 l) and one
+// round's tiles, bf16
+// [row][64 columns] with 128-byte rows whose 16-byte block b sits at
+// b ^ ((row >> 1) & 7): P^T and dS^T (64 key rows), Q^T and bf16(w dO)^T
+// (128 dim rows).
+constexpr uint32_t kKvV = 0;
+constexpr uint32_t kKvKt = 16384;
+constexpr uint32_t kKvPt = 32768;
+constexpr uint32_t kKvDs = kKvPt + 8192;
+constexpr uint32_t kKvQt = kKvDs + 8192;
+constexpr uint32_t kKvWd = kKvQt + 16384;
+constexpr uint32_t kKvBytes = kKvWd + 16384;
+
+__device__ __forceinline__ uint32_t tile_off(uint32_t base, int row, int col) {
+  return base + row * 128 + ((((col >> 3) ^ ((row >> 1) & 7))) << 4) + (col & 7) * 2;
+}
+__device__ __forceinline__ u32x4_t tile_read(const unsigned char* sm, uint32_t base, int row,
+                                             int blk) {
+  return *reinterpret_cast<const u32x4_t*>(sm + base + row * 128 +
+                                           ((blk ^ ((row >> 1) & 7)) << 4));
+}
+__device__ __forceinline__ void tile_put(unsigned char* sm, uint32_t base, int row, int col,
+                                         uint32_t v16) {
+  *reinterpret_cast<uint16_t*>(sm + tile_off(base, row, col)) = (uint16_t)v16;
+}
+
+// One workgroup per work unit: chunk (b, h, c) and a segment of its pairs.
+// A round takes 8 pairs, two per wave (16 columns: pair 8 j >> 3, head j & 7):
+//   phase 1 (per wave): S^T = K . Q^T (K images in registers), dP^T = V . dO^T
+//     (V images from LDS), the chunk gradient, and the columns of P^T, dS^T,
+//     Q^T, bf16(w dO)^T into the round's tiles;
+//   phase 2 (wave w: dims 32 w .. + 31): dK += dS^T . Q, dV += P^T . bf16(w dO)
+//     over the round's 64 columns (two k-steps).
+__global__ void __launch_bounds__(kThreads, 1) routed_attn_dkv_kernel(BwdArgs a) {
+  __shared__ __attribute__((aligned(16))) unsigned char sm[kKvBytes];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int j = lane & 15, grp = lane >> 4;
-  // (b, q, h): KV head fastest so the four waves of a workgroup share q rows.
-  const int64_t unit = (int64_t)blockIdx.x * kWaves + wave;
-  const int64_t units = a.B * a.Lq * a.Hkv;
-  if (unit >= units) return;  // wave-uniform; no workgroup barrier follows
-  const int h = (int)(unit % a.Hkv);
-  const int64_t bq = unit / a.Hkv;
-  const int64_t b = bq / a.Lq;
-  const int64_t q = bq % a.Lq;
+  const int64_t N = a.B * a.Hkv * a.Ck;
+  const int64_t u = blockIdx.x;
+  if (u >= (int64_t)a.ustart[N]) return;  // workgroup-uniform
+  // the chunk whose units hold u: ustart[lo] <= u < ustart[lo + 1]
+  int64_t lo = 0, hi = N;
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)a.ustart[mid] <= u) lo = mid;
+    else hi = mid;
+  }
+  const int64_t bhc = lo;
+  const int64_t cs = a.start[bhc], ce = a.start[bhc + 1];
+  const int64_t e0 = cs + (u - a.ustart[bhc]) * kSegEntries;
+  const int64_t e1 = min(ce, e0 + kSegEntries);
+  const bool whole = ce - cs <= kSegEntries;
+  const int64_t c = bhc % a.Ck;
+  const int64_t bh = bhc / a.Ck;
+  const int h = (int)(bh % a.Hkv);
+  const int64_t b = bh / a.Hkv;
   const int G = a.G, K = a.K;
-  const bool cvalid = j < G;
-  WaveTiles& T = tiles[wave];
 
-  // ---- this query's rows: Q^T / dO^T operands (columns j = heads) and the
-  // transposed tiles [dim][column]
-  const int64_t row0 = (b * a.Lq + q) * a.Hq + (int64_t)h * G;  // (query, head 0) row
-  u32x4_t Qb[4], Db[4];
+  uint64_t excl = a.mask_last ? (1ull << 63) : 0ull;
+  if (a.key_valid)
+    excl |= ~nonzero_bits(reinterpret_cast<const int8_t*>(a.key_valid + b * a.Lk + c * 64));
+  const uint32_t l16 = 16u * lane;
+  const uint32_t cb = (uint32_t)c * kFragBytes;
+  u32x4_t kb[4][4];
+  load_rows(kb, make_rsrc(a.fwd + (b * a.Hkv + h) * a.Ck * 16384, (uint32_t)a.Ck * kFragBytes),
+            l16, cb);
+  {
+    // V images | K^T images: the chunk's whole bwd fragment (32 KB)
+    const unsigned char* vsrc =
+        reinterpret_cast<const unsigned char*>(a.bwd + (b * a.Hkv + h) * a.Ck * 16384) + cb;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    u32x4_t z = {0u, 0u, 0u, 0u};
-    Qb[ks] = z;
-    Db[ks] = z;
-    if (cvalid) {
-      Qb[ks] = *reinterpret_cast<const u32x4_t*>(a.q + (row0 + j) * 128 + 32 * ks + 8 * grp);
-      Db[ks] = *reinterpret_cast<const u32x4_t*>(a.dout + (row0 + j) * 128 + 32 * ks + 8 * grp);
+    for (int i = 0; i < 8; ++i) {
+      const int o = 16 * (tid + kThreads * i);
+      *reinterpret_cast<u32x4_t*>(sm + kKvV + o) = *reinterpret_cast<const u32x4_t*>(vsrc + o);
     }
   }
-  for (int e = lane; e < 128 * 16; e += 64) {
-    const int d = e >> 4, col = e & 15;
-    uint16_t qv = 0, dv = 0;
-    if (col < G) {
-      qv = a.q[(row0 + col) * 128 + d];
-      dv = a.dout[(row0 + col) * 128 + d];
+  f32x4_t dk[4][2], dv[4][2];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      dk[mt][dt] = zero4();
+      dv[mt][dt] = zero4();
     }
-    T.qt[d * 16 + col] = qv;
-    T.dt[d * 16 + col] = dv;
-  }
-  // the index list (ends at the first negative entry)
-  const int32_t* irow = a.idx + ((b * a.Lq + q) * a.Hkv + h) * K;
-  if (lane < K) list_s[wave][lane] = irow[lane];
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  int n = K;
-  for (int k = 0; k < K; ++k)
-    if (list_s[wave][k] < 0) {
-      n = k;
-      break;
-    }
-
-  const uint32_t lo = 16u * lane;
-  const __amdgpu_buffer_rsrc_t frs =
-      make_rsrc(a.fwd + (b * a.Hkv + h) * a.Ck * 16384, (uint32_t)a.Ck * kFragBytes);
-  const __amdgpu_buffer_rsrc_t brs =
-      make_rsrc(a.bwd + (b * a.Hkv + h) * a.Ck * 16384, (uint32_t)a.Ck * kFragBytes);
   const float c2 = a.scale_log2;
-  f32x4_t dq[8];
-#pragma unroll
-  for (int nt = 0; nt < 8; ++nt) dq[nt] = zero4();
-  uint16_t* dwrow = a.dw + row0 * K;
+  const int g = j & 7;
+  const int col = 16 * wave + j;
+  __syncthreads();  // V images staged
 
-  for (int k = 0; k < K; ++k) {
-    const int32_t c = list_s[wave][k];
-    float di_out = 0.f;
-    const bool active = k < n && c >= 0 && c < a.Ck;
-    if (active) {
-      const float wv = cvalid ? bf16_to_f32(a.w[(row0 + j) * K + k]) : 0.f;
-      if (lane < 16) T.wcol[lane] = lane < G ? bf16_to_f32(a.w[(row0 + lane) * K + k]) : 0.f;
-      // excluded keys: landmark slot, invalid keys, dropped by the keep row
-      uint64_t excl = a.mask_last ? (1ull << 63) : 0ull;
-      if (a.key_valid)
-        excl |= ~nonzero_bits(reinterpret_cast<const int8_t*>(a.key_valid + b * a.Lk + (int64_t)c * 64));
-      if (a.keep)
-        excl |= ~nonzero_bits(a.keep + (((b * a.Lq + q) * a.Hkv + h) * K + k) * 64);
-      const uint64_t msh = excl >> (4 * grp);  // bit 16 mt + r: key 16 mt + 4 grp + r
-      const uint32_t cb = (uint32_t)c * kFragBytes;
-
-      // S^T = K . Q^T and dP^T = V . dO^T (lane (grp, j): keys 16 mt + 4 grp + r, column j)
-      f32x4_t S[4], dP[4];
-      {
-        u32x4_t kb[4][4];
-        load_rows(kb, frs, lo, cb);
+  for (int64_t r0 = e0; r0 < e1; r0 += 8) {
+    // The tile addresses derive from lane values redefined each round, so
+    // they are formed where used rather than held in registers across rounds.
+    int lj = j, lg = grp, lc = col;
+    asm volatile("" : "+v"(lj), "+v"(lg), "+v"(lc));
+    // ---- phase 1
+    const int64_t e = r0 + 2 * wave + (j >> 3);
+    const bool have = e < e1;
+    const bool cvalid = have && g < G;
+    int64_t q = 0;
+    int k = 0;
+    if (have) {
+      const int32_t v = a.list[e];
+      q = v & 0xffffff;
+      k = (v >> 24) & 63;
+    }
+    const int64_t row = (b * a.Lq + q) * a.Hq + (int64_t)h * G + g;
+    u32x4_t Qb[4], Db[4];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          S[mt] = zero4();
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) S[mt] = mfma_bf16_16x16x32(kb[mt][ks], Qb[ks], S[mt]);
-        }
-        load_rows(kb, brs, lo, cb);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          dP[mt] = zero4();
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) dP[mt] = mfma_bf16_16x16x32(kb[mt][ks], Db[ks], dP[mt]);
-        }
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x4_t z = {0u, 0u, 0u, 0u};
+      Qb[ks] = z;
+      Db[ks] = z;
+      if (cvalid) {
+        Qb[ks] = *reinterpret_cast<const u32x4_t*>(a.q + row * 128 + 32 * ks + 8 * grp);
+        Db[ks] = *reinterpret_cast<const u32x4_t*>(a.dout + row * 128 + 32 * ks + 8 * grp);
       }
-      // P = 2^(s c - lse) over the visible keys, rounded to bf16
-      float mx = neg_inf();
+    }
+    const float wv = cvalid ? bf16_to_f32(a.w[row * K + k]) : 0.f;
+    uint64_t ex = excl;
+    if (a.keep && have) ex |= ~keep_row_bits(a.keep + (((b * a.Lq + q) * a.Hkv + h) * K + k) * 64);
+    const uint64_t msh = ex >> (4 * grp);
+    f32x4_t S[4], dP[4];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < 4; ++mt) {
+      S[mt] = zero4();
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (!((msh >> (16 * mt + r)) & 1ull)) mx = fmaxf(mx, S[mt][r] * c2);
-      mx = across4_max(mx);
-      float sum = 0.f;
-      if (mx != neg_inf()) {
+      for (int ks = 0; ks < 4; ++ks) S[mt] = mfma_bf16_16x16x32(kb[mt][ks], Qb[ks], S[mt]);
+    }
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < 4; ++mt) {
+      dP[mt] = zero4();
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (!((msh >> (16 * mt + r)) & 1ull)) sum += exp2_hw(S[mt][r] * c2 - mx);
+      for (int ks = 0; ks < 4; ++ks) {
+        const u32x4_t vi =
+            *reinterpret_cast<const u32x4_t*>(sm + kKvV + 1024 * (4 * mt + ks) + l16);
+        dP[mt] = mfma_bf16_16x16x32(vi, Db[ks], dP[mt]);
       }
-      sum = across4_sum(sum);
-      const float lse = mx == neg_inf() ? neg_inf() : mx + log2_hw(sum);
-      float P[4][4];
-      float di = 0.f;
+    }
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e8 = 0; e8 < 8; ++e8) {
+        const int dim = 32 * ks + 8 * lg + e8;
+        const uint32_t qv = (Qb[ks][e8 >> 1] >> (16 * (e8 & 1))) & 0xffffu;
+        const float dov = bf16_to_f32((Db[ks][e8 >> 1] >> (16 * (e8 & 1))) & 0xffffu);
+        tile_put(sm, kKvQt, dim, lc, qv);
+        tile_put(sm, kKvWd, dim, lc, f32_to_bf16(wv * dov));
+      }
+    const float di = chunk_grad(S, dP, msh, c2, a.scale * wv);  // S <- P, dP <- dS
+    if (cvalid && grp == 0) a.dw[row * K + k] = (uint16_t)f32_to_bf16(di);
+    // dQ (columns x dims) = dS . K: A = dS packed in the tiled key order
+    // (reduction index 8 grp + e of k-step ks is key 32 ks + 16 (e >> 2) +
+    // 4 grp + (e & 3)), B = the K^T images (lane (j, grp): dim 16 nt + j, the
+    // same keys).  Lane (grp, j) of product nt: columns 4 grp + r, dim
+    // 16 nt + j, added into the column's dQ row (16 lanes = 64 contiguous
+    // bytes per row).
+    {
+      u32x4_t Sb[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        Sb[ks][0] = pack_bf16x2(dP[2 * ks][0], dP[2 * ks][1]);
+        Sb[ks][1] = pack_bf16x2(dP[2 * ks][2], dP[2 * ks][3]);
+        Sb[ks][2] = pack_bf16x2(dP[2 * ks + 1][0], dP[2 * ks + 1][1]);
+        Sb[ks][3] = pack_bf16x2(dP[2 * ks + 1][2], dP[2 * ks + 1][3]);
+      }
+      // rows of this lane's four columns 4 grp + r: pair grp >> 1, heads 4 (grp & 1) + r
+      const int64_t ep = r0 + 2 * wave + (grp >> 1);
+      int64_t qrow = -1;
+      if (ep < e1) qrow = (b * a.Lq + (a.list[ep] & 0xffffff)) * a.Hq + (int64_t)h * G;
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) {
+        f32x4_t d = mfma_bf16_16x16x32(
+            Sb[0], *reinterpret_cast<const u32x4_t*>(sm + kKvKt + 1024 * (2 * nt) + l16), zero4());
+        d = mfma_bf16_16x16x32(
+            Sb[1], *reinterpret_cast<const u32x4_t*>(sm + kKvKt + 1024 * (2 * nt + 1) + l16), d);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const bool vis = !((msh >> (16 * mt + r)) & 1ull) && lse != neg_inf();
-          const float p = vis ? bf16_to_f32(f32_to_bf16(exp2_hw(S[mt][r] * c2 - lse))) : 0.f;
-          P[mt][r] = p;
-          di += p * dP[mt][r];
-        }
-      di = across4_sum(di);
-      di_out = di;
-      // dS = bf16(scale w P (dP - di)); both transposes into the wave's tiles
-      float dS[4][4];
-      const float sw = a.scale * wv;
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          dS[mt][r] = bf16_to_f32(f32_to_bf16(sw * P[mt][r] * (dP[mt][r] - di)));
-          const int key = 16 * mt + 4 * grp + r;
-          T.ps[key * 16 + j] = (uint16_t)f32_to_bf16(P[mt][r]);
-          T.ds[key * 16 + j] = (uint16_t)f32_to_bf16(dS[mt][r]);
-        }
-      // dQ^T += K^T . dS^T (K^T images; reduction index 8 grp + e of k-step
-      // ks is key 32 ks + 16 (e >> 2) + 4 grp + (e & 3), the tiled order)
-      {
-        u32x4_t kt[8][2];
-        load_cols(kt, brs, lo, cb);
-        u32x4_t Sb[2];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          Sb[ks][0] = pack_bf16x2(dS[2 * ks][0], dS[2 * ks][1]);
-          Sb[ks][1] = pack_bf16x2(dS[2 * ks][2], dS[2 * ks][3]);
-          Sb[ks][2] = pack_bf16x2(dS[2 * ks + 1][0], dS[2 * ks + 1][1]);
-          Sb[ks][3] = pack_bf16x2(dS[2 * ks + 1][2], dS[2 * ks + 1][3]);
-        }
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) {
-          dq[nt] = mfma_bf16_16x16x32(kt[nt][0], Sb[0], dq[nt]);
-          dq[nt] = mfma_bf16_16x16x32(kt[nt][1], Sb[1], dq[nt]);
+          const int gg = 4 * (grp & 1) + r;
+          if (qrow >= 0 && gg < G) atomicAdd(a.dq + (qrow + gg) * 128 + 16 * nt + j, d[r]);
         }
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // dK (keys x dims) = dS^T . Q and dV = P^T . bf16(w dO): A = the key row
-      // of the transposed tile (columns 8 grp .. + 7; groups 2, 3 zero), B = the
-      // dim row of Q^T / dO^T.
-      const u32x4_t zero = {0u, 0u, 0u, 0u};
-      float* dkb = a.dk + ((b * a.Lk + (int64_t)c * 64) * a.Hkv + h) * 128;
-      float* dvb = a.dv + ((b * a.Lk + (int64_t)c * 64) * a.Hkv + h) * 128;
-      const int64_t krow = (int64_t)a.Hkv * 128;  // floats between keys
+    }
+    // this wave's columns of the tiles (columns without a pair or head hold
+    // zeros in dS^T and bf16(w dO)^T, so they add nothing)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = 16 * mt + 4 * lg + r;
+        tile_put(sm, kKvPt, key, lc, f32_to_bf16(S[mt][r]));
+        tile_put(sm, kKvDs, key, lc, f32_to_bf16(dP[mt][r]));
+      }
+    __syncthreads();
+    // ---- phase 2: keys x dims 32 wave .. + 31, reduction over the columns
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      u32x4_t bq[2], bw[2];
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        const int dim = 32 * wave + 16 * dt + lj;
+        bq[dt] = tile_read(sm, kKvQt, dim, 4 * ks + lg);
+        bw[dt] = tile_read(sm, kKvWd, dim, 4 * ks + lg);
+      }
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        const u32x4_t As = grp < 2 ? *reinterpret_cast<const u32x4_t*>(&T.ds[(16 * mt + j) * 16 + 8 * grp]) : zero;
-        const u32x4_t Ap = grp < 2 ? *reinterpret_cast<const u32x4_t*>(&T.ps[(16 * mt + j) * 16 + 8 * grp]) : zero;
+        const u32x4_t ad = tile_read(sm, kKvDs, 16 * mt + lj, 4 * ks + lg);
+        const u32x4_t ap = tile_read(sm, kKvPt, 16 * mt + lj, 4 * ks + lg);
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) {
-          const u32x4_t Bq = grp < 2 ? *reinterpret_cast<const u32x4_t*>(&T.qt[(16 * nt + j) * 16 + 8 * grp]) : zero;
-          u32x4_t Bd = zero;
-          if (grp < 2) {
-            const u32x4_t x = *reinterpret_cast<const u32x4_t*>(&T.dt[(16 * nt + j) * 16 + 8 * grp]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float w0 = T.wcol[8 * grp + 2 * i], w1 = T.wcol[8 * grp + 2 * i + 1];
-              Bd[i] = pack_bf16x2(w0 * bf16_lo(x[i]), w1 * bf16_hi(x[i]));
-            }
-          }
-          const f32x4_t ck = mfma_bf16_16x16x32(As, Bq, zero4());
-          const f32x4_t cv = mfma_bf16_16x16x32(Ap, Bd, zero4());
-          // lane (grp, j): keys 16 mt + 4 grp + r, dim 16 nt + j
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int64_t off = (int64_t)(16 * mt + 4 * grp + r) * krow + 16 * nt + j;
-            atomicAdd(dkb + off, ck[r]);
-            atomicAdd(dvb + off, cv[r]);
-          }
+        for (int dt = 0; dt < 2; ++dt) {
+          dk[mt][dt] = mfma_bf16_16x16x32(ad, bq[dt], dk[mt][dt]);
+          dv[mt][dt] = mfma_bf16_16x16x32(ap, bw[dt], dv[mt][dt]);
         }
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    if (cvalid && grp == 0) dwrow[(int64_t)j * K + k] = (uint16_t)f32_to_bf16(di_out);
+    __syncthreads();
   }
-  // dQ rows (lane (grp, j): column j, dims 16 nt + 4 grp + r)
-  if (cvalid) {
-    float* dqr = a.dq + (row0 + j) * 128;
+  // lane (grp, j) of tile (mt, dt): keys 16 mt + 4 grp + r, dim 32 wave + 16 dt + j
+  float* dkb = a.dk + ((b * a.Lk + c * 64) * a.Hkv + h) * 128;
+  float* dvb = a.dv + ((b * a.Lk + c * 64) * a.Hkv + h) * 128;
+  const int64_t krow = (int64_t)a.Hkv * 128;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt)
-      *reinterpret_cast<f32x4_t*>(dqr + 16 * nt + 4 * grp) = dq[nt];
-  }
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t off = (int64_t)(16 * mt + 4 * grp + r) * krow + 32 * wave + 16 * dt + j;
+        if (whole) {
+          dkb[off] = dk[mt][dt][r];
+          dvb[off] = dv[mt][dt][r];
+        } else {
+          atomicAdd(dkb + off, dk[mt][dt][r]);
+          atomicAdd(dvb + off, dv[mt][dt][r]);
+        }
+      }
+}
+
+__global__ void __launch_bounds__(256) fill_zero_i32(int32_t* p, int64_t n) {
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0;
+}
+
+struct ListPlan {
+  int nqb;
+  int64_t n;  // chunks B * Hkv * Ck
+  int64_t count, blkbase, start, ustart, list, total;  // byte offsets / size
+  int64_t max_units;
+};
+
+ListPlan list_plan(int64_t B, int64_t Lq, int64_t Hkv, int64_t K, int64_t Ck) {
+  ListPlan p;
+  p.nqb = (int)((Lq + kListBlock - 1) / kListBlock);
+  p.n = B * Hkv * Ck;
+  const int64_t pairs = B * Lq * Hkv * K;
+  int64_t o = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t at = o;
+    o += (bytes + 255) / 256 * 256;
+    return at;
+  };
+  p.count = take(p.n * 4);
+  p.blkbase = take(B * Hkv * p.nqb * Ck * 4);
+  p.start = take((p.n + 1) * 4);
+  p.ustart = take((p.n + 1) * 4);
+  p.list = take(pairs * 4);
+  p.total = o;
+  p.max_units = (pairs + kSegEntries - 1) / kSegEntries + p.n;
+  return p;
 }
 
 }  // namespace
@@ -321,18 +521,22 @@ extern "C" int mrsa_selected_attention_bwd(
     const int8_t* token_keep, int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
     int64_t kv_heads, int64_t head_dim, int64_t topk, int64_t chunk_size, int mask_last_token,
     float sm_scale, float* grad_q, float* grad_k, float* grad_v, void* grad_weights,
-    void* stream) {
+    void* workspace, int64_t workspace_bytes, void* stream) {
   if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 ||
       q_heads % kv_heads != 0 || head_dim <= 0 || topk <= 0 || chunk_size <= 0 ||
       !(sm_scale > 0.f) || sm_scale == __builtin_inff())
     return MRSA_ERR_INVALID_ARGUMENT;
   if (kv_len % chunk_size != 0) return MRSA_ERR_INVALID_ARGUMENT;
-  if (chunk_size != 64 || head_dim != 128 || q_heads / kv_heads > 16 || topk > kMaxTopk)
+  if (chunk_size != 64 || head_dim != 128 || q_heads / kv_heads > 8 || topk > kMaxTopk)
     return MRSA_ERR_UNSUPPORTED;
-  if (kv_len / 64 >= 131072) return MRSA_ERR_UNSUPPORTED;
+  if (kv_len / 64 > kMaxListChunks || q_len >= (1 << 24)) return MRSA_ERR_UNSUPPORTED;
+  if (batch * q_len * kv_heads * topk >= 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
   if (batch == 0 || q_len == 0) return MRSA_OK;
   if (!q || !grad_out || !kv_frags || !kv_frags_bwd || !weights || !indices || !grad_q ||
-      !grad_k || !grad_v || !grad_weights)
+      !grad_k || !grad_v || !grad_weights || !workspace)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  const ListPlan lp = list_plan(batch, q_len, kv_heads, topk, kv_len / 64);
+  if (workspace_bytes < lp.total || (uintptr_t)workspace % 256 != 0)
     return MRSA_ERR_INVALID_ARGUMENT;
   if (((uintptr_t)q | (uintptr_t)grad_out | (uintptr_t)kv_frags | (uintptr_t)kv_frags_bwd |
        (uintptr_t)grad_q) % 16 != 0)
@@ -361,10 +565,36 @@ extern "C" int mrsa_selected_attention_bwd(
   a.dk = grad_k;
   a.dv = grad_v;
   a.dw = (uint16_t*)grad_weights;
-  const int64_t units = batch * q_len * kv_heads;
-  const int64_t blocks = (units + kWaves - 1) / kWaves;
-  if (blocks > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(routed_attn_bwd_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
-                     (hipStream_t)stream, a);
+  if (lp.max_units > 0x7fffffff || lp.nqb > 0x7fffffff || batch * kv_heads > 65535)
+    return MRSA_ERR_UNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  // pair lists, then the chunk-major pass
+  char* ws = (char*)workspace;
+  int32_t* count = (int32_t*)(ws + lp.count);
+  int32_t* blkbase = (int32_t*)(ws + lp.blkbase);
+  int32_t* start = (int32_t*)(ws + lp.start);
+  int32_t* ustart = (int32_t*)(ws + lp.ustart);
+  int32_t* list = (int32_t*)(ws + lp.list);
+  hipLaunchKernelGGL(fill_zero_i32, dim3((unsigned)std::min<int64_t>((lp.n + 255) / 256, 4096)),
+                     dim3(256), 0, st, count, lp.n);
+  const dim3 lgrid((unsigned)lp.nqb, (unsigned)(batch * kv_heads));
+  hipLaunchKernelGGL(list_count_kernel, lgrid, dim3(kListBlock), 0, st, a, count, blkbase, lp.nqb);
+  hipLaunchKernelGGL(list_scan_kernel, dim3(1), dim3(1024), 0, st, (const int32_t*)count, lp.n,
+                     start, ustart);
+  a.start = start;
+  a.ustart = ustart;
+  hipLaunchKernelGGL(list_fill_kernel, lgrid, dim3(kListBlock), 0, st, a,
+                     (const int32_t*)blkbase, lp.nqb, list);
+  a.list = list;
+  hipLaunchKernelGGL(routed_attn_dkv_kernel, dim3((unsigned)lp.max_units), dim3(kThreads), 0, st,
+                     a);
   return mrsa_launch_status();
+}
+
+extern "C" int64_t mrsa_selected_attention_bwd_workspace_bytes(int64_t batch, int64_t q_len,
+                                                               int64_t kv_len, int64_t kv_heads,
+                                                               int64_t topk) {
+  if (batch < 0 || q_len < 0 || kv_len < 0 || kv_heads <= 0 || topk <= 0 || kv_len % 64)
+    return -1;
+  return list_plan(batch, q_len, kv_heads, topk, kv_len / 64).total;
 }

@@ -68,6 +68,12 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
          _I64, _I, _I, _I64, _I64, _I, _F, _P, _P, _I, _P],
     ),
+    "mrsa_route_score_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _I]),
+    "mrsa_route_score_bwd": (
+        _I,
+        [_P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _F, _P, _P, _P,
+         _I64, _P],
+    ),
     "mrsa_route_weights_fwd": (
         _I,
         [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P,
@@ -112,10 +118,11 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
          _I, _F, _I64, _P, _P, _P],
     ),
+    "mrsa_selected_attention_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
     "mrsa_selected_attention_bwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
-         _I, _F, _P, _P, _P, _P, _P],
+         _I, _F, _P, _P, _P, _P, _P, _I64, _P],
     ),
     "mrsa_token_keep_fwd": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "mrsa_candidate_token_scores_fwd": (

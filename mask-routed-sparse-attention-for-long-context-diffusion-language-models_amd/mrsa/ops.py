@@ -30,7 +30,7 @@ from .sparse_attention import (FRAG_ELEMS, _kv_fragments_impl, _kv_fragments_row
                                _selected_attention_bwd_impl)
 from .token_refinement import _token_keep_impl
 from .token_score import _token_scores_impl
-from .topk import _route_topk_impl
+from .topk import _route_score_bwd_impl, _route_topk_impl
 
 _CUDA = "cuda"
 
@@ -127,6 +127,18 @@ def _(q5, lmks, lse4, bias4, drop_mask, key_valid, topk, block_size, derive_wind
     return (q5.new_empty(B, L, H, topk, dtype=torch.int32),
             q5.new_empty(B, L, H, G, topk,
                          dtype=torch.float32 if scores_fp32 else torch.bfloat16))
+
+
+@_op("route_score_bwd")
+def route_score_bwd(q5: Tensor, lmks: Tensor, indices: Tensor, grad_scores: Tensor,
+                    sm_scale: float) -> tuple[Tensor, Tensor]:
+    return _route_score_bwd_impl(q5, lmks, indices, grad_scores, sm_scale)
+
+
+@route_score_bwd.register_fake
+def _(q5, lmks, indices, grad_scores, sm_scale):
+    return (q5.new_empty(q5.shape, dtype=torch.bfloat16),
+            lmks.new_empty(lmks.shape, dtype=torch.bfloat16))
 
 
 # -- route weights --------------------------------------------------------
@@ -282,7 +294,7 @@ def _(ranking, token_budget, as_int8):
 
 OPERATORS = (
     "kv_fragments", "kv_fragments_rows_", "local_attention", "chunk_attn_pool",
-    "chunk_attn_pool_bwd", "route_topk", "route_weights", "route_weights_bwd",
+    "chunk_attn_pool_bwd", "route_topk", "route_score_bwd", "route_weights", "route_weights_bwd",
     "selected_attention", "selected_attention_bwd", "fuse_hils_outputs", "fuse_hils_outputs_bwd",
     "remote_drop_mask",
     "remote_drop_mask_rows", "candidate_token_scores", "token_keep",

@@ -231,17 +231,21 @@ def _selected_attention_bwd_impl(q, kv_frags, kv_frags_bwd, weights, indices, ke
     idx = indices.to(torch.int32).contiguous()
     kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
     keep = None if token_keep is None else token_keep.to(device=q.device, dtype=torch.int8).contiguous()
-    dq = torch.empty(B, Lq, Hq, D, dtype=torch.float32, device=q.device)
+    dq = torch.zeros(B, Lq, Hq, D, dtype=torch.float32, device=q.device)
     dk = torch.zeros(B, kv_len, Hkv, D, dtype=torch.float32, device=q.device)
     dv = torch.zeros(B, kv_len, Hkv, D, dtype=torch.float32, device=q.device)
-    dw = torch.empty(B, Lq, Hq, K, dtype=torch.bfloat16, device=q.device)
+    dw = torch.zeros(B, Lq, Hq, K, dtype=torch.bfloat16, device=q.device)
+    nbytes = int(_lib.call("mrsa_selected_attention_bwd_workspace_bytes", B, Lq, kv_len, Hkv, K))
+    if nbytes < 0:
+        raise ValueError(f"invalid routed attention shapes q {tuple(q.shape)} kv_len {kv_len}")
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
     st = _lib.call(
         "mrsa_selected_attention_bwd",
         _lib.ptr(qc), _lib.ptr(go), _lib.ptr(kv_frags.contiguous()),
         _lib.ptr(kv_frags_bwd.contiguous()), _lib.ptr(w), _lib.ptr(idx), _lib.ptr(kv),
         _lib.ptr(keep), B, Lq, kv_len, Hq, Hkv, D, K, int(chunk_size),
         1 if mask_last_token else 0, float(sm_scale), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
-        _lib.ptr(dw), _lib.stream_of(qc),
+        _lib.ptr(dw), _lib.ptr(ws), nbytes, _lib.stream_of(qc),
     )
     _lib.check(st, "selected_attention backward")
     return dq, dk, dv, dw

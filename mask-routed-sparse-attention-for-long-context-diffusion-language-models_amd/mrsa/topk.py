@@ -2,8 +2,10 @@
 
 Drop-ins for ``ops.topk_head_softmax.ref_softmax_topk_max_pooling``
 (ops/topk_head_softmax.py:15-156) and ``online_softmax_topk_head``
-(:1242-1415).  Both run the gfx950 route kernel (mrsa_route_topk_fwd).
-Gumbel noise is a training-time input and is not supported here.
+(:1242-1415).  Both run the gfx950 route kernel (mrsa_route_topk_fwd); when q or the
+landmarks require grad the scores are differentiable through the route-score
+backward kernel (mrsa_route_score_bwd).  Gumbel noise is a training-time
+input and is not supported here.
 """
 
 from __future__ import annotations
@@ -98,11 +100,72 @@ def route_topk_launch(
         drop_mask = None
     else:
         key_valid = None
-    return torch.ops.mrsa.route_topk(
-        q5, lmks, lse4, bias4, drop_mask, key_valid, int(topk), int(block_size),
-        int(derive_window), bool(is_causal), int(window_size), int(q_offset),
-        selection_mode != "post_softmax", float(sm_scale), bool(scores_fp32),
-        -1 if use_workspace is None else int(bool(use_workspace)))
+    args = (q5, lmks, lse4, bias4, drop_mask, key_valid, int(topk), int(block_size),
+            int(derive_window), bool(is_causal), int(window_size), int(q_offset),
+            selection_mode != "post_softmax", float(sm_scale), bool(scores_fp32),
+            -1 if use_workspace is None else int(bool(use_workspace)))
+    if torch.is_grad_enabled() and (q5.requires_grad or lmks.requires_grad):
+        return _RouteTopK.apply(*args)
+    return torch.ops.mrsa.route_topk(*args)
+
+
+class _RouteTopK(torch.autograd.Function):
+    """Route scoring with the scores differentiable in q and the landmarks
+    (SoftmaxTopKMaxPoolingFusedFn, ops/topk_head_softmax.py:1004-1122): the
+    indices, the local LSE, the bias and the drop mask get no gradient."""
+
+    @staticmethod
+    def forward(ctx, q5, lmks, lse4, bias4, drop_mask, key_valid, topk, block_size,
+                derive_window, is_causal, window_size, q_offset, pre_softmax, sm_scale,
+                scores_fp32, use_workspace):
+        indices, scores = torch.ops.mrsa.route_topk(
+            q5, lmks, lse4, bias4, drop_mask, key_valid, topk, block_size, derive_window,
+            is_causal, window_size, q_offset, pre_softmax, sm_scale, scores_fp32,
+            use_workspace)
+        ctx.mark_non_differentiable(indices)
+        ctx.save_for_backward(q5, lmks, indices)
+        ctx.sm_scale = sm_scale
+        return indices, scores
+
+    @staticmethod
+    def backward(ctx, grad_indices, grad_scores):
+        q5, lmks, indices = ctx.saved_tensors
+        none = (None,) * 14
+        if grad_scores is None:
+            return (None, None) + none
+        grad_q, grad_lmks = torch.ops.mrsa.route_score_bwd(
+            q5, lmks, indices, grad_scores, ctx.sm_scale)
+        grad_q = grad_q.to(q5.dtype) if ctx.needs_input_grad[0] else None
+        grad_lmks = grad_lmks.to(lmks.dtype) if ctx.needs_input_grad[1] else None
+        return (grad_q, grad_lmks) + none
+
+
+def _route_score_bwd_impl(q5, lmks, indices, grad_scores, sm_scale):
+    """Gradients of the route scores in q [B, L, Hkv, G, D] and the landmarks
+    [B, C, Hkv*G or Hkv, D] (bf16, the shapes of the inputs)."""
+    B, L, Hkv, G, D = q5.shape
+    C = lmks.shape[1]
+    K = indices.shape[-1]
+    per_head = 1 if lmks.shape[2] == Hkv * G else 0
+    qc = q5.to(torch.bfloat16).contiguous()
+    lc = lmks.to(torch.bfloat16).contiguous()
+    idx = indices.to(device=q5.device, dtype=torch.int32).contiguous()
+    gs = grad_scores.reshape(B, L, Hkv, G, K)
+    if gs.dtype not in (torch.bfloat16, torch.float32):
+        gs = gs.float()
+    gs = gs.contiguous()
+    grad_q = torch.empty_like(qc)
+    grad_lmks = torch.empty_like(lc)
+    nbytes = int(_lib.call("mrsa_route_score_bwd_workspace_bytes", B, L, C, Hkv, G, per_head))
+    if nbytes < 0:
+        raise ValueError(f"invalid route score shapes q {tuple(q5.shape)} lmks {tuple(lmks.shape)}")
+    ws = torch.empty(max(nbytes, 16) // 4, dtype=torch.float32, device=q5.device)
+    st = _lib.call(
+        "mrsa_route_score_bwd", _lib.ptr(qc), _lib.ptr(lc), _lib.ptr(idx), _lib.ptr(gs),
+        1 if gs.dtype == torch.float32 else 0, B, L, C, Hkv, G, D, K, per_head, float(sm_scale),
+        _lib.ptr(grad_q), _lib.ptr(grad_lmks), _lib.ptr(ws), nbytes, _lib.stream_of(qc))
+    _lib.check(st, "route_score_bwd")
+    return grad_q, grad_lmks
 
 
 def _route_topk_impl(q5, lmks, lse4, bias4, drop_mask, key_valid, topk, block_size,

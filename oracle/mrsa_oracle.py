@@ -260,6 +260,44 @@ def boundary_gap(sel, topk):
     return torch.where(torch.isfinite(a) & torch.isfinite(b), gap, torch.full_like(gap, float("inf")))
 
 
+def route_score_bwd(q5, lmks, indices, grad_scores, sm_scale=None):
+    """SoftmaxTopKMaxPoolingFusedFn.backward (ops/topk_head_softmax.py:1074-1122).
+
+    q5 [B, L, Hkv, G, D]; lmks [B, C, Hkv*G, D] (per head) or [B, C, Hkv, D]
+    (shared); indices [B, L, Hkv, K]; grad_scores [B, L, Hkv, G, K].  The
+    gradient times sm_scale is rounded to bf16 (the reference's mul_ in the
+    bf16 gradient dtype, :1090-1091) and scattered into a dense [L, C] matrix
+    per (h, g); slots outside [0, C) are zeroed (:1084-1092).  Returns fp32
+    grad_q (bmm with the landmarks, :1107-1108) and grad_lmks (bmm with q,
+    :1110-1121; summed over g for shared landmarks).
+    """
+
+    B, L, H, G, D = q5.shape
+    C = lmks.shape[1]
+    K = indices.shape[-1]
+    per_head = lmks.shape[2] == H * G
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    idx = indices.long()[:, :, :, None, :].expand(B, L, H, G, K)
+    valid = (idx >= 0) & (idx < C)
+    val = bf16_round(grad_scores.float().reshape(B, L, H, G, K) * sm_scale)
+    val = torch.where(valid, val, torch.zeros_like(val))
+    dense = torch.zeros(B, L, H, G, C)
+    # Valid slots of one list hold distinct chunks in the reference's
+    # forward, so the scatter is a plain sum over the slots.
+    dense.scatter_add_(4, idx.clamp(0, C - 1), val)
+    q = q5.float()
+    if per_head:
+        lm = lmks.float().reshape(B, C, H, G, D)
+        grad_q = torch.einsum("blhgc,bchgd->blhgd", dense, lm)
+        grad_l = torch.einsum("blhgc,blhgd->bchgd", dense, q).reshape(B, C, H * G, D)
+    else:
+        lm = lmks.float()
+        grad_q = torch.einsum("blhgc,bchd->blhgd", dense, lm)
+        grad_l = torch.einsum("blhgc,blhgd->bchd", dense, q)
+    return grad_q, grad_l
+
+
 # ---------------------------------------------------------------------------
 # a7: route weights
 # ---------------------------------------------------------------------------

@@ -297,3 +297,102 @@ def test_selected_attention_backward_split_query_block():
         err = _rel_err(got, exp)
         print(f"  {name}: rel-norm error {err:.3e}", flush=True)
         assert err < 2e-2, (name, err)
+
+
+# -- route-score backward (ops/topk_head_softmax.py:1074-1122) ---------------
+def _score_case(seed, B, L, Hkv, G, K, C, per_head, D=128):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, L, Hkv, G, D, generator=g).bfloat16()
+    lm = torch.randn(B, C, Hkv * G if per_head else Hkv, D, generator=g).bfloat16()
+    keys = torch.rand(B * L * Hkv, C, generator=g)
+    idx = keys.topk(min(K, C), dim=-1).indices.sort(dim=-1).values.int()
+    if K > C:
+        idx = torch.cat([idx, torch.full((idx.shape[0], K - C), -1, dtype=torch.int32)], -1)
+    idx = idx.reshape(B, L, Hkv, K)
+    idx[0, min(3, L - 1), 0, K // 2:] = -1
+    idx[0, L - 1, Hkv - 1, 0] = C + 5
+    gs = torch.randn(B, L, Hkv, G, K, generator=g).bfloat16()
+    return q, lm, idx, gs
+
+
+@pytest.mark.parametrize("B,L,Hkv,G,K,C,per_head,fp32", [
+    (1, 100, 2, 7, 16, 64, True, False),
+    (2, 77, 2, 3, 8, 40, False, False),
+    (1, 70, 1, 7, 32, 300, True, False),     # two chunk blocks (fp32 grad_q path)
+    (1, 1000, 4, 7, 32, 256, True, False),   # config-2 shape, fewer rows
+    (1, 64, 2, 7, 32, 520, False, True),     # three blocks, shared, fp32 grads
+])
+def test_route_score_backward_vs_oracle(B, L, Hkv, G, K, C, per_head, fp32):
+    _note(f"route_score_bwd B={B} L={L} Hkv={Hkv} G={G} K={K} C={C} per_head={per_head}")
+    q, lm, idx, gs = _score_case(7 + C, B, L, Hkv, G, K, C, per_head)
+    if fp32:
+        gs = gs.float()
+    scale = 128 ** -0.5
+    eq, el = O.route_score_bwd(q, lm, idx, gs, scale)
+    gq, gl = torch.ops.mrsa.route_score_bwd(q.to(DEV), lm.to(DEV), idx.to(DEV), gs.to(DEV),
+                                             scale)
+    gq2, gl2 = torch.ops.mrsa.route_score_bwd(q.to(DEV), lm.to(DEV), idx.to(DEV), gs.to(DEV),
+                                               scale)
+    torch.cuda.synchronize()
+    assert gq.dtype == torch.bfloat16 and gl.dtype == torch.bfloat16
+    assert torch.equal(gq, gq2) and torch.equal(gl, gl2), "not deterministic"
+    for name, got, exp in (("grad_q", gq, eq), ("grad_lmks", gl, el)):
+        got = got.float().cpu()
+        err = _rel_err(got, exp)
+        print(f"  {name}: rel-norm error {err:.3e}")
+        assert err < 5e-3, name
+        # one bf16 rounding of the fp32 result (plus fp32 order noise)
+        assert ((got - exp).abs() <= exp.abs() * 2 ** -8 + 1e-3).all(), name
+
+
+def test_route_score_autograd_through_online_softmax_topk_head():
+    _note("route_score autograd via online_softmax_topk_head")
+    B, L, Hkv, G, D, C, K = 1, 256, 2, 7, 128, 64, 16
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(B, L, Hkv * G, D, generator=g).bfloat16().to(DEV).requires_grad_(True)
+    lm = torch.randn(B, C, Hkv * G, D, generator=g).bfloat16().to(DEV).requires_grad_(True)
+    lse = (torch.randn(B, L, Hkv * G, generator=g) + 3).to(DEV)
+    idx, sc = mrsa.online_softmax_topk_head(q, lm, lse, K, 64, 0, is_causal=False, G=G)
+    assert idx.dtype == torch.int32 and sc.shape == (B, L, Hkv * G, K)
+    assert not idx.requires_grad and sc.requires_grad
+    gout = torch.randn(B, L, Hkv * G, K, generator=g).bfloat16().to(DEV)
+    live = (idx >= 0)[:, :, :, None, :].expand(B, L, Hkv, G, K).reshape(B, L, Hkv * G, K)
+    gout = torch.where(live, gout, torch.zeros_like(gout))
+    (torch.where(live, sc.float(), torch.zeros_like(sc.float())) * gout.float()).sum().backward()
+    eq, el = O.route_score_bwd(q.detach().cpu().reshape(B, L, Hkv, G, D), lm.detach().cpu(),
+                               idx.cpu(), gout.cpu().reshape(B, L, Hkv, G, K), D ** -0.5)
+    for name, got, exp in (("q", q.grad, eq.reshape(B, L, Hkv * G, D)), ("lmks", lm.grad, el)):
+        err = _rel_err(got.float().cpu(), exp)
+        print(f"  grad {name}: rel-norm error {err:.3e}")
+        assert got.dtype == torch.bfloat16 and err < 5e-3, name
+
+
+def test_selected_attention_backward_long_chunk_lists():
+    # every query routes to chunk 3, so its pair list (1100 pairs per batch and
+    # KV head) spans two work segments whose dK / dV sums are added; batch 2.
+    _note("selected_attention_bwd long chunk lists B=2 Lq=1100")
+    B, Lq, Lk, Hkv, G, D, K = 2, 1100, 1024, 2, 7, 128, 4
+    C = Lk // 64
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(B, Lq, Hkv * G, D, generator=g).bfloat16()
+    k = torch.randn(B, Lk, Hkv, D, generator=g).bfloat16()
+    v = torch.randn(B, Lk, Hkv, D, generator=g).bfloat16()
+    w = torch.rand(B, Lq, Hkv * G, K, generator=g).bfloat16()
+    rest = torch.stack([torch.randperm(C - 1, generator=g)[:K - 1] for _ in range(B * Lq * Hkv)])
+    rest = rest + (rest >= 3).long()  # chunks other than 3
+    idx = torch.cat([torch.full((B * Lq * Hkv, 1), 3), rest], -1).sort(-1).values
+    idx = idx.reshape(B, Lq, Hkv, K).int()
+    valid = torch.rand(B, Lk, generator=g) > 0.05
+    dout = torch.randn(B, Lq, Hkv * G, D, generator=g).bfloat16()
+    tq, tk, tv, tw = (t.to(DEV).requires_grad_(True) for t in (q, k, v, w))
+    out = mrsa.HiLS_block_M_head(tq, tk, tv, tw, idx.to(DEV), key_valid=valid.to(DEV))
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    rq, rk, rv, rw = (t.float().requires_grad_(True) for t in (q, k, v, w))
+    ref = O.selected_attention(rq, rk, rv, rw, idx, valid)
+    (ref * dout.float()).sum().backward()
+    for name, got, exp in (("dq", tq.grad, rq.grad), ("dk", tk.grad, rk.grad),
+                           ("dv", tv.grad, rv.grad), ("dw", tw.grad, rw.grad)):
+        err = _rel_err(got, exp)
+        print(f"  {name}: rel-norm error {err:.3e}")
+        assert err < 2e-2, name

@@ -313,3 +313,81 @@ def test_oracle_selected_attention_grad_central_differences():
         num = (f(*plus) - f(*minus)) / (2 * eps)
         ana = float((grad * d).sum())
         assert abs(num - ana) <= 2e-2 * max(1.0, abs(ana)), (which, num, ana)
+
+
+# -- route-score backward (ops/topk_head_softmax.py:1074-1122) ---------------
+def _score_inputs(seed, B=2, L=5, H=2, G=3, K=4, C=7, D=16, per_head=True):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, L, H, G, D, generator=g).bfloat16()
+    lm = torch.randn(B, C, H * G if per_head else H, D, generator=g).bfloat16()
+    idx = torch.stack([torch.randperm(C, generator=g)[:K] for _ in range(B * L * H)])
+    idx = idx.reshape(B, L, H, K)
+    idx[0, 1, 0, 2:] = -1
+    idx[1, L - 1, H - 1, 0] = C + 3  # out of range: contributes nothing
+    gs = torch.randn(B, L, H, G, K, generator=g).bfloat16()
+    return q, lm, idx, gs
+
+
+def _score_autograd(q, lm, idx, gs, scale):
+    """Autograd of the forward score = scale * q . lmk[idx] (gathered rows)."""
+    B, L, H, G, D = q.shape
+    C = lm.shape[1]
+    qf = q.float().requires_grad_(True)
+    lf = lm.float().requires_grad_(True)
+    per_head = lm.shape[2] == H * G
+    rows = lf.reshape(B, C, H, G, D) if per_head else lf[:, :, :, None, :].expand(B, C, H, G, D)
+    ok = (idx >= 0) & (idx < C)
+    safe = idx.clamp(0, C - 1)
+    # picked[b, l, h, g, k, :] = rows[b, idx[b, l, h, k], h, g, :]
+    bi = torch.arange(B)[:, None, None, None]
+    hi = torch.arange(H)[None, None, :, None]
+    picked = rows[bi, safe, hi]  # [B, L, H, K, G, D]
+    s = scale * torch.einsum("blhgd,blhkgd->blhgk", qf, picked)
+    s = torch.where(ok[:, :, :, None, :], s, torch.zeros_like(s))
+    (s * gs.float()).sum().backward()
+    return qf.grad, lf.grad
+
+
+def test_oracle_route_score_bwd_matches_autograd_power_of_two_scale():
+    # scale 2^-3: grad * scale is exact in bf16, so the oracle must equal the
+    # autograd of the forward definition up to fp32 summation order.
+    for per_head in (True, False):
+        q, lm, idx, gs = _score_inputs(11, per_head=per_head)
+        gq, gl = O.route_score_bwd(q, lm, idx, gs, 0.125)
+        aq, al = _score_autograd(q, lm, idx, gs, 0.125)
+        torch.testing.assert_close(gq, aq, atol=1e-5, rtol=1e-5)
+        torch.testing.assert_close(gl, al, atol=1e-5, rtol=1e-5)
+
+
+def test_oracle_route_score_bwd_rounds_scaled_gradient_to_bf16():
+    # With scale 1/sqrt(D) the gradient is bf16(g * scale): equal to the
+    # scale-1 autograd fed the pre-rounded upstream gradient.
+    q, lm, idx, gs = _score_inputs(12)
+    scale = 1.0 / math.sqrt(q.shape[-1] * 1.7)
+    gq, gl = O.route_score_bwd(q, lm, idx, gs, scale)
+    pre = (gs.float() * scale).bfloat16()
+    aq, al = _score_autograd(q, lm, idx, pre, 1.0)
+    torch.testing.assert_close(gq, aq, atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(gl, al, atol=1e-5, rtol=1e-5)
+    # ... and differs from the unrounded product by more than fp32 noise
+    uq, _ = _score_autograd(q, lm, idx, gs, scale)
+    assert (gq - uq).abs().max() > 1e-4
+
+
+def test_oracle_route_score_bwd_ignores_invalid_slots_and_sums_shared_heads():
+    q, lm, idx, gs = _score_inputs(13)
+    gs2 = gs.clone()
+    bad = (idx < 0) | (idx >= lm.shape[1])
+    gs2.masked_fill_(bad[:, :, :, None, :], 7.0)
+    a = O.route_score_bwd(q, lm, idx, gs)
+    b = O.route_score_bwd(q, lm, idx, gs2)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    # shared landmarks = per-head landmarks that repeat over the group, with
+    # the per-head gradient summed over the group
+    B, L, H, G, D = q.shape
+    shared = lm.reshape(B, -1, H, G, D)[:, :, :, 0]
+    rep = shared[:, :, :, None, :].expand(B, -1, H, G, D).reshape(B, -1, H * G, D)
+    sq, sl = O.route_score_bwd(q, shared, idx, gs)
+    pq, pl = O.route_score_bwd(q, rep.contiguous(), idx, gs)
+    torch.testing.assert_close(sq, pq, atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(sl, pl.reshape(B, -1, H, G, D).sum(3), atol=1e-5, rtol=1e-5)
