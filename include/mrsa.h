@@ -533,6 +533,55 @@ int mrsa_token_keep_fwd(const float* scores, int64_t rows, int64_t n, int64_t to
                         uint8_t* keep, void* stream);
 
 /*
+ * Entropy-adaptive token keep: replaces the selection of
+ * refine_remote_tokens_entropy_g7 (dream_dllm_hils/token_refinement.py:396-438)
+ * -- gather_selected_chunk_entropy (:244-284), allocate_entropy_token_budget
+ * (:150-241) and select_entropy_adaptive_token_keep (:287-333) -- without
+ * training noise.  Per (batch, query, KV head) row of topk slots:
+ *   capacity[k]   finite scores of slot k (or given)
+ *   entropy_k     the group mean of entropy at the slot's chunk (clamped to
+ *                 [0, chunks - 1]; 0 for a negative index), or given
+ *   allocation    min(sum capacity, token_budget) slots apportioned by
+ *                 support exp(clamp(entropy, 0, ln token_budget)): baseline
+ *                 min(capacity, min_tokens_per_chunk), then topk + 1 rounds
+ *                 of capped largest remainder (ties to the lower slot)
+ *   keep          per slot, its allocation's largest finite scores (ties to
+ *                 the lower key)
+ *   scores:           fp32 [batch, seq_len, kv_heads, topk, chunk_size] or NULL
+ *   capacity:         int64 [batch, seq_len, kv_heads, topk] or NULL (count
+ *                     finite scores; one of the two must be given)
+ *   selected_entropy: fp32 [batch, seq_len, kv_heads, topk] or NULL, then
+ *   entropy:          fp32 [batch, chunks, kv_heads, groups] and
+ *   indices:          int32 [batch, seq_len, kv_heads, topk]
+ *   keep (out):       bytes [batch, seq_len, kv_heads, topk, chunk_size] 0/1,
+ *                     or NULL (allocation only)
+ *   allocation (out): int64 [batch, seq_len, kv_heads, topk]
+ * Requirements: topk <= 64, chunk_size <= 64, token_budget >= topk *
+ * min_tokens_per_chunk.  The support sum is exact before its rounding to
+ * fp32 (order-independent).
+ */
+int mrsa_token_keep_entropy_fwd(const float* scores, const int64_t* capacity,
+                                const float* selected_entropy, const float* entropy,
+                                const int32_t* indices, int64_t batch, int64_t seq_len,
+                                int64_t kv_heads, int64_t groups, int64_t chunks, int64_t topk,
+                                int64_t chunk_size, int64_t token_budget,
+                                int64_t min_tokens_per_chunk, uint8_t* keep,
+                                int64_t* allocation, void* stream);
+
+/*
+ * gather_selected_chunk_entropy (dream_dllm_hils/token_refinement.py:244-284):
+ * out[b, l, h, k] = mean over g of entropy[b, clamp(idx, 0, chunks - 1), h, g],
+ * 0 where idx < 0.
+ *   entropy: fp32 [batch, chunks, kv_heads, groups]
+ *   indices: int32 [batch, seq_len, kv_heads, topk]
+ *   out:     fp32 [batch, seq_len, kv_heads, topk]
+ */
+int mrsa_gather_selected_chunk_entropy(const float* entropy, const int32_t* indices,
+                                       int64_t batch, int64_t seq_len, int64_t chunks,
+                                       int64_t kv_heads, int64_t groups, int64_t topk, float* out,
+                                       void* stream);
+
+/*
  * Per-token candidate scores inside routed chunks: max over the query group of
  * q.k * sm_scale; -inf for the landmark slot, invalid keys and -1 chunks.
  * Replaces candidate_token_scores_gqa (ops/hils_token_score_gqa_tilelang.py:174-208).

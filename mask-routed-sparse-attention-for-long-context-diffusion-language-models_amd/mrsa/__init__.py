@@ -15,6 +15,8 @@ hand-written HIP kernels in ../csrc (C ABI: include/mrsa.h).  Module map:
                         (ops/hils_bidir_route_weights_tilelang.py, attention.py:126-235)
     fusion.py           fuse_hils_outputs               (ops/hils_bidir_output_fusion_tilelang.py)
     token_score.py      candidate_token_scores_gqa      (ops/hils_token_score_gqa_tilelang.py)
+    token_refinement.py global_qk / entropy_adaptive token keep
+                                                        (dream_dllm_hils/token_refinement.py)
     kernel_utils.py     remote_drop_mask(_rows), chunk_aligned_local_bounds, group_pad_to/unpad
     route_layer.py      route_attention, swa_attention  (attention.py route / SWA layers),
                         cached_route_attention + LayerKVCache (fastdllm_attention.py cached step)
@@ -43,7 +45,14 @@ from .route_weights import route_weights, route_weights_torch
 from .routing import route_topk_g7, selected_attention_g7, selected_attention_g7_cached
 from .sparse_attention import HiLS_block_M_head, kv_fragments
 from .token_score import candidate_token_scores_gqa
-from .token_refinement import refine_remote_tokens_g7, select_global_token_keep
+from .token_refinement import (
+    allocate_entropy_token_budget,
+    gather_selected_chunk_entropy,
+    refine_remote_tokens_entropy_g7,
+    refine_remote_tokens_g7,
+    select_entropy_adaptive_token_keep,
+    select_global_token_keep,
+)
 from .topk import online_softmax_topk_head, ref_softmax_topk_max_pooling
 from ._lib import LIB_PATH, MrsaLibraryError, load as load_library
 from . import ops  # registers torch.ops.mrsa.* (after every module it wraps)
@@ -61,6 +70,10 @@ __all__ = [
     "candidate_token_scores_gqa",
     "refine_remote_tokens_g7",
     "select_global_token_keep",
+    "allocate_entropy_token_budget",
+    "gather_selected_chunk_entropy",
+    "refine_remote_tokens_entropy_g7",
+    "select_entropy_adaptive_token_keep",
     "chunk_aligned_local_bounds",
     "chunk_attn_pool_gqa",
     "chunk_attn_pool_gqa_backward",

@@ -124,6 +124,13 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
          _I, _F, _P, _P, _P, _P, _P, _I64, _P],
     ),
+    "mrsa_token_keep_entropy_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P],
+    ),
+    "mrsa_gather_selected_chunk_entropy": (
+        _I, [_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P],
+    ),
     "mrsa_token_keep_fwd": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "mrsa_candidate_token_scores_fwd": (
         _I,

@@ -28,7 +28,7 @@ from .route_weights import _route_weights_bwd_impl, _route_weights_impl
 from .sparse_attention import (FRAG_ELEMS, _kv_fragments_impl, _kv_fragments_rows_impl,
                                _selected_attention_impl,
                                _selected_attention_bwd_impl)
-from .token_refinement import _token_keep_impl
+from .token_refinement import _gather_entropy_impl, _token_keep_entropy_impl, _token_keep_impl
 from .token_score import _token_scores_impl
 from .topk import _route_score_bwd_impl, _route_topk_impl
 
@@ -292,10 +292,37 @@ def _(ranking, token_budget, as_int8):
     return ranking.new_empty(ranking.shape, dtype=torch.int8 if as_int8 else torch.uint8)
 
 
+
+@_op("token_keep_entropy")
+def token_keep_entropy(ranking: Tensor, selected_entropy: Optional[Tensor], entropy: Optional[Tensor],
+                       indices: Optional[Tensor], token_budget: int, min_tokens_per_chunk: int,
+                       as_int8: bool) -> tuple[Tensor, Tensor]:
+    return _token_keep_entropy_impl(ranking, selected_entropy, entropy, indices, token_budget,
+                                    min_tokens_per_chunk, as_int8)
+
+
+@token_keep_entropy.register_fake
+def _(ranking, selected_entropy, entropy, indices, token_budget, min_tokens_per_chunk, as_int8):
+    B, L, H, K, S = ranking.shape
+    return (ranking.new_empty(ranking.shape, dtype=torch.int8 if as_int8 else torch.uint8),
+            ranking.new_empty(B, L, H, K, dtype=torch.int64))
+
+
+@_op("gather_selected_chunk_entropy")
+def gather_selected_chunk_entropy(entropy: Tensor, indices: Tensor) -> Tensor:
+    return _gather_entropy_impl(entropy, indices)
+
+
+@gather_selected_chunk_entropy.register_fake
+def _(entropy, indices):
+    B, L, H, K = indices.shape
+    return entropy.new_empty(B, L, H, K, dtype=torch.float32)
+
 OPERATORS = (
     "kv_fragments", "kv_fragments_rows_", "local_attention", "chunk_attn_pool",
     "chunk_attn_pool_bwd", "route_topk", "route_score_bwd", "route_weights", "route_weights_bwd",
     "selected_attention", "selected_attention_bwd", "fuse_hils_outputs", "fuse_hils_outputs_bwd",
     "remote_drop_mask",
-    "remote_drop_mask_rows", "candidate_token_scores", "token_keep",
+    "remote_drop_mask_rows", "candidate_token_scores", "token_keep", "token_keep_entropy",
+    "gather_selected_chunk_entropy",
 )

@@ -42,7 +42,7 @@ from .pool import chunk_attn_pool_gqa_prior
 from .route_weights import route_weights_launch
 from .sparse_attention import (FRAG_ELEMS, kv_fragments, kv_fragments_rows,
                                selected_attention_launch)
-from .token_refinement import refine_remote_tokens_g7
+from .token_refinement import refine_remote_tokens_entropy_g7, refine_remote_tokens_g7
 from .topk import route_topk_launch
 
 
@@ -60,11 +60,14 @@ class RouteLayerConfig:
     gate_offset: float | torch.Tensor | None = 0.0
     gate_scale: float | torch.Tensor | None = 1.0
     skip_inert_slots: bool = True     # attention.py:902
-    # Remote-token refinement (attention.py:1729-1759, "global_qk" policy):
-    # with token_budget > 0 each (query, KV head) keeps only its budget of
-    # highest-scoring routed tokens.
+    # Remote-token refinement (attention.py:1729-1759): with token_budget > 0
+    # each (query, KV head) keeps only its budget of routed tokens -- the
+    # highest-scoring ones overall ("global_qk") or per chunk under quotas
+    # from the chunks' pool entropy ("entropy_adaptive", at least
+    # min_tokens_per_chunk per non-empty chunk).
     token_budget: int = 0
     token_policy: str = "global_qk"
+    min_tokens_per_chunk: int = 1
 
 
 def _check_qkv(q, k, v, route_q):
@@ -159,8 +162,7 @@ def route_attention(
     _mark("route_weights")
     token_keep = None
     if cfg.token_budget > 0:
-        token_keep = refine_remote_tokens_g7(q, k, indices, kv_bool, S, cfg.token_budget,
-                                             training=False, kv_frags=frags)
+        token_keep = _token_keep(cfg, q, k, indices, kv_bool, entropy, frags)
         _mark("token_refinement")
     # Routed attention with the output fusion in its epilogue:
     # fuse_hils_outputs(remote, local_out, local_w) without materialising remote.
@@ -190,8 +192,22 @@ def _check_token_budget(cfg):
             f"{cfg.topk * cfg.chunk_size}")
     if cfg.token_policy not in {"global_qk", "entropy_adaptive"}:
         raise ValueError(f"unsupported token_policy={cfg.token_policy}")
-    if cfg.token_budget > 0 and cfg.token_policy != "global_qk":
-        raise ValueError("token_policy='entropy_adaptive' is not supported by the gfx950 path")
+    if cfg.min_tokens_per_chunk < 0:
+        raise ValueError("min_tokens_per_chunk must be non-negative")
+    if cfg.token_budget > 0 and cfg.token_budget < cfg.topk * cfg.min_tokens_per_chunk:
+        raise ValueError("token_budget must cover the minimum for every routed chunk")
+
+
+def _token_keep(cfg, q, k, indices, key_valid, entropy, kv_frags):
+    """The token keep mask of cfg.token_policy (attention.py:1729-1759,
+    fastdllm_attention.py:330-361), inference mode."""
+    if cfg.token_policy == "global_qk":
+        return refine_remote_tokens_g7(q, k, indices, key_valid, cfg.chunk_size,
+                                       cfg.token_budget, training=False, kv_frags=kv_frags)
+    keep, _ = refine_remote_tokens_entropy_g7(
+        q, k, indices, key_valid, entropy, cfg.chunk_size, cfg.token_budget,
+        cfg.min_tokens_per_chunk, training=False, kv_frags=kv_frags)
+    return keep
 
 
 def swa_attention(
@@ -329,6 +345,7 @@ def _check_cached_args(q, route_q, cache, query_positions, affected_chunks, cfg,
     """cached_route_attention's argument checks; the ones that read device
     values share one round trip (skipped with device_checks=False)."""
 
+    _check_token_budget(cfg)
     if q.device.type != "cuda":
         raise ValueError("cached route attention requires CUDA tensors")
     for name, t in (("q", q), ("route_q", route_q)):
@@ -427,16 +444,27 @@ def _cached_route_body(q, route_q, cache, query_positions, affected_chunks, entr
     remote_w, local_w = route_weights_launch(
         scores, indices, cache.prior_bias, local_lse, temperature=1.0
     )
+    token_keep = None
+    if cfg.token_budget > 0:
+        # fastdllm_attention.py:330-361; the entropy policy reads the entropy
+        # back from the cached prior bias (:345-350)
+        entropy = None
+        if cfg.token_policy != "global_qk":
+            entropy = cache.prior_bias / entropy_bias_scale.to(
+                device=q.device, dtype=torch.float32).view(1, 1, Hkv, G)
+        token_keep = _token_keep(cfg, q, cache.key, indices, cache.key_valid, entropy,
+                                 cache.kv_frags)
     out = selected_attention_launch(q, cache.kv_frags, remote_w, indices, cache.key_valid, S,
-                                    fuse_local=local_out, fuse_weight=local_w)
+                                    token_keep=token_keep, fuse_local=local_out,
+                                    fuse_weight=local_w)
     if not return_intermediates:
         return out
     remote_out = selected_attention_launch(q, cache.kv_frags, remote_w, indices,
-                                           cache.key_valid, S)
+                                           cache.key_valid, S, token_keep=token_keep)
     return out, {
         "local_output": local_out, "local_lse": local_lse, "indices": indices,
         "scores": scores, "remote_weights": remote_w, "local_weight": local_w,
-        "remote_output": remote_out, "drop_mask": drop,
+        "remote_output": remote_out, "drop_mask": drop, "token_keep": token_keep,
     }
 
 

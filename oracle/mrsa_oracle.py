@@ -517,18 +517,91 @@ def candidate_token_scores(q, k, indices, key_valid, chunk_size):
     return s.masked_fill(~sel_valid, NEG_INF)
 
 
+def gather_selected_chunk_entropy(entropy, indices):
+    """gather_selected_chunk_entropy (dream_dllm_hils/token_refinement.py:244-284):
+    the group mean of entropy [B, C, Hkv, G] at each routed chunk (indices
+    clamped to [0, C - 1]), 0 where the index is negative.  [B, L, Hkv, K]."""
+
+    B, C, H, G = entropy.shape
+    idx = indices.long()
+    safe = idx.clamp(0, max(C - 1, 0))
+    ent = entropy.float()
+    bi = torch.arange(B)[:, None, None, None]
+    hi = torch.arange(H)[None, None, :, None]
+    gathered = ent[bi, safe, hi].mean(dim=-1)  # [B, L, H, K]
+    return gathered.masked_fill(idx < 0, 0.0)
+
+
+def allocate_entropy_token_budget(entropy, capacity, token_budget, min_tokens_per_chunk=1):
+    """allocate_entropy_token_budget (dream_dllm_hils/token_refinement.py:150-241):
+    min(sum capacity, token_budget) token slots per row over the last
+    dimension: baseline min(capacity, min_tokens_per_chunk), then K + 1
+    rounds of capped largest-remainder apportionment by the effective
+    support exp(clamp(entropy, 0, ln budget)) (0 for empty chunks); ties in
+    the fractional parts go to the lower chunk (stable sort).  int64."""
+
+    capacity = capacity.long()
+    K = capacity.shape[-1]
+    target = capacity.sum(dim=-1).clamp_max(token_budget)
+    alloc = torch.minimum(capacity, torch.full_like(capacity, min_tokens_per_chunk))
+    remaining = target - alloc.sum(dim=-1)
+    max_entropy = math.log(max(token_budget, 1))
+    support = torch.exp(torch.nan_to_num(entropy.float(), nan=0.0, posinf=max_entropy,
+                                         neginf=0.0).clamp(min=0.0, max=max_entropy))
+    support = support.masked_fill(capacity <= 0, 0.0)
+    rank = torch.arange(K).view(*([1] * (capacity.ndim - 1)), K)
+    for _ in range(K + 1):
+        active = alloc < capacity
+        act_sup = support * active
+        den = act_sup.sum(dim=-1, keepdim=True)
+        quota = torch.where(den > 0, remaining[..., None].float() * act_sup / den.clamp_min(1e-12),
+                            torch.zeros_like(act_sup))
+        alloc = alloc + torch.minimum(torch.floor(quota).long(), capacity - alloc)
+        remaining = target - alloc.sum(dim=-1)
+        active = alloc < capacity
+        bonus_count = torch.minimum(remaining, active.sum(dim=-1))
+        frac = (quota - torch.floor(quota)).masked_fill(~active, float("-inf"))
+        order = torch.argsort(frac, dim=-1, descending=True, stable=True)
+        bonus = torch.zeros_like(alloc)
+        bonus.scatter_(-1, order, (rank < bonus_count[..., None]).long())
+        alloc = torch.minimum(alloc + bonus, capacity)
+        remaining = target - alloc.sum(dim=-1)
+    return alloc
+
+
+def select_entropy_adaptive_token_keep(scores, selected_entropy, token_budget,
+                                       min_tokens_per_chunk=1):
+    """select_entropy_adaptive_token_keep (dream_dllm_hils/token_refinement.py:
+    287-333) without training noise: per chunk, the allocation's largest
+    finite scores (stable descending order: ties to the lower key).
+    Returns (keep uint8 [B, L, H, K, S], allocation int64 [B, L, H, K])."""
+
+    sc = scores.float()
+    capacity = torch.isfinite(sc).sum(dim=-1)
+    alloc = allocate_entropy_token_budget(selected_entropy, capacity, token_budget,
+                                          min_tokens_per_chunk)
+    order = torch.argsort(sc, dim=-1, descending=True, stable=True)
+    S = sc.shape[-1]
+    rank = torch.arange(S).view(*([1] * (sc.ndim - 1)), S)
+    keep = torch.zeros_like(sc, dtype=torch.uint8)
+    keep.scatter_(-1, order, (rank < alloc[..., None]).to(torch.uint8))
+    return keep.masked_fill(~torch.isfinite(sc), 0), alloc
+
+
 # ---------------------------------------------------------------------------
 # a10: the route layer
 # ---------------------------------------------------------------------------
 def route_layer(q, k, v, route_q, entropy_bias_scale, key_valid=None, *, local_window=256,
                 chunk_size=64, topk=32, temperature=1.0, gate_offset=0.0, gate_scale=1.0,
-                skip_inert_slots=True, token_budget=0):
+                skip_inert_slots=True, token_budget=0, token_policy="global_qk",
+                min_tokens_per_chunk=1):
     """KernelDreamFullHiLSAttention.forward between projections and o_proj
     (dream_dllm_hils/attention.py:1380-1774), with the reference's bf16
-    rounding between stages.  token_budget > 0 adds the "global_qk" token
-    refinement (attention.py:1729-1769): candidate token scores of q in the
-    routed chunks, the global keep mask, and the routed attention restricted
-    to it.  Returns (out bf16, intermediates dict)."""
+    rounding between stages.  token_budget > 0 adds the token refinement
+    (attention.py:1729-1769): candidate token scores of q in the routed
+    chunks, the keep mask of the policy ("global_qk": global top budget;
+    "entropy_adaptive": per-chunk quotas from the pool entropy), and the
+    routed attention restricted to it.  Returns (out bf16, intermediates dict)."""
 
     B, L, Hq, D = q.shape
     Hkv = k.shape[2]
@@ -562,7 +635,8 @@ def route_layer(q, k, v, route_q, entropy_bias_scale, key_valid=None, *, local_w
     lw = lw.to(torch.bfloat16)
     keep = None
     if token_budget > 0:
-        keep = select_global_token_keep(candidate_token_scores(q, k, idx, kv, S), token_budget)
+        keep = _token_keep(q, k, idx, kv, S, token_budget, token_policy, entropy,
+                           min_tokens_per_chunk)
     remote = selected_attention(q, k, v, rw, idx, kv, S, token_keep=keep).to(torch.bfloat16)
     out = fuse_outputs(remote, local_out, lw)
     return out, {
@@ -573,9 +647,22 @@ def route_layer(q, k, v, route_q, entropy_bias_scale, key_valid=None, *, local_w
     }
 
 
+def _token_keep(q, k, idx, kv, S, token_budget, token_policy, entropy, min_tokens_per_chunk):
+    """The token keep mask of a policy (attention.py:1729-1759,
+    fastdllm_attention.py:330-361)."""
+
+    scores = candidate_token_scores(q, k, idx, kv, S)
+    if token_policy == "global_qk":
+        return select_global_token_keep(scores, token_budget)
+    keep, _ = select_entropy_adaptive_token_keep(
+        scores, gather_selected_chunk_entropy(entropy, idx), token_budget, min_tokens_per_chunk)
+    return keep
+
+
 def cached_route_layer(q, route_q, cache_key, cache_value, cache_valid, landmark_keys,
                        prior_bias, query_positions, affected_chunks, entropy_bias_scale, *,
-                       local_window=256, chunk_size=64, topk=32, skip_inert_slots=True):
+                       local_window=256, chunk_size=64, topk=32, skip_inert_slots=True,
+                       token_budget=0, token_policy="global_qk", min_tokens_per_chunk=1):
     """Cached block step of a route layer (dream_dllm_hils/fastdllm_attention.py:
     203-382) after the projections and the K/V update, with the reference's
     bf16 rounding between stages.  landmark_keys [1, C, Hkv, G, D] bf16 and
@@ -617,10 +704,17 @@ def cached_route_layer(q, route_q, cache_key, cache_value, cache_valid, landmark
     rw, lw = route_weights(scores_bf, idx, prior_all, local_lse, temperature=1.0)
     rw = rw.to(torch.bfloat16)
     lw = lw.to(torch.bfloat16)
-    remote = selected_attention(q, cache_key, cache_value, rw, idx, kv, S).to(torch.bfloat16)
+    keep = None
+    if token_budget > 0:
+        # fastdllm_attention.py:345-350: the entropy of the cached prior bias
+        entropy = prior_all / entropy_bias_scale.float().view(1, 1, Hkv, G)
+        keep = _token_keep(q, cache_key, idx, kv, S, token_budget, token_policy, entropy,
+                           min_tokens_per_chunk)
+    remote = selected_attention(q, cache_key, cache_value, rw, idx, kv, S,
+                                token_keep=keep).to(torch.bfloat16)
     out = fuse_outputs(remote, local_out, lw)
     return out, lmk_all, prior_all, {
         "local_output": local_out, "local_lse": local_lse, "indices": idx,
         "scores": scores_bf, "selection": sel, "remote_weights": rw, "local_weight": lw,
-        "remote_output": remote, "drop_mask": drop,
+        "remote_output": remote, "drop_mask": drop, "token_keep": keep,
     }

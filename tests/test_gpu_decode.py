@@ -201,14 +201,17 @@ def test_cached_route_attention_argument_errors():
     assert bool(torch.isfinite(out.float()).all())
 
 
-def test_cached_block_step_graph_replays_match_eager():
+@pytest.mark.parametrize("policy", [None, "entropy_adaptive"])
+def test_cached_block_step_graph_replays_match_eager(policy):
     # CachedBlockStep (HIP graph of the K/V row write + cached route layer)
     # against the eager replace + cached_route_attention on a twin cache,
     # block after block: graphs for 0 and 1 affected chunks, each replayed
     # several times with eager work and synchronisation in between; the caches
     # (keys, values, tiles, landmarks) equal, every replay's output equal up
     # to the routed attention's varying fp32 summation order.
-    _note("cached block step graph")
+    _note(f"cached block step graph token policy={policy}")
+    cfg = mrsa.RouteLayerConfig() if policy is None else mrsa.RouteLayerConfig(
+        token_budget=256, token_policy=policy)
     L, Hq, Hkv, D, S, bs = 4096, 28, 4, 128, 64, 32
     G = Hq // Hkv
     g = torch.Generator().manual_seed(95)
@@ -222,7 +225,7 @@ def test_cached_block_step_graph_replays_match_eager():
     twin = lambda: mrsa.LayerKVCache(k.clone(), v.clone(), valid.clone(), lmk.clone(),
                                      prior.clone())
     graphed, eager = twin(), twin()
-    step = mrsa.CachedBlockStep(graphed, scale, block_len=bs)
+    step = mrsa.CachedBlockStep(graphed, scale, cfg, block_len=bs)
     start = L - 8 * bs
     for i in list(range(8)) + [1, 0]:
         pos = torch.arange(start + i * bs, start + (i + 1) * bs, device=DEV)
@@ -231,7 +234,7 @@ def test_cached_block_step_graph_replays_match_eager():
         q, rq, kb, vb = rnd(1, bs, Hq, D), rnd(1, bs, Hq, D), rnd(1, bs, Hkv, D), rnd(1, bs, Hkv, D)
         got = step(q, rq, kb, vb, pos, aff).clone()
         eager.replace(pos, kb, vb)
-        want = mrsa.cached_route_attention(q, rq, eager, pos, aff, scale)
+        want = mrsa.cached_route_attention(q, rq, eager, pos, aff, scale, cfg)
         torch.cuda.synchronize()
         assert_nearly_identical(got, want, f"block {i}: graph vs eager", atol=0.03)
     for name in ("key", "value", "kv_frags", "landmark_keys", "prior_bias"):

@@ -155,3 +155,131 @@ def test_route_layer_with_token_budget_vs_oracle():
     with pytest.raises(ValueError, match="exceeds"):
         mrsa.route_attention(q.to(DEV), k.to(DEV), v.to(DEV), rq.to(DEV), scale.to(DEV),
                              valid.to(DEV), mrsa.RouteLayerConfig(token_budget=4096))
+
+
+# -- entropy_adaptive (token_refinement.py:150-438) ----------------------------
+@pytest.mark.parametrize("budget,mn,ties", [(256, 1, False), (64, 2, False), (2048, 0, False),
+                                            (100, 1, True)])
+def test_entropy_token_keep_bit_exact(budget, mn, ties):
+    _note(f"entropy token keep budget={budget} min={mn} ties={ties}")
+    g = torch.Generator().manual_seed(200 + budget)
+    B, L, H, K, S = 1, 37, 4, 32, 64
+    scores = torch.randn(B, L, H, K, S, generator=g)
+    if ties:
+        scores = scores.round(decimals=1)
+    scores[..., -1] = float("-inf")                       # landmark slots
+    scores[0, 3, :, 20:] = float("-inf")                  # -1 slots
+    scores[0, 5, 1] = float("-inf")                       # nothing routed
+    scores[0, 6, 2, :, 5:] = float("-inf")                # capacities of 5
+    ent = torch.rand(B, L, H, K, generator=g) * 4 - 0.5
+    ent[0, 7, 0, :4] = torch.tensor([float("nan"), float("inf"), float("-inf"), 9.0])
+    keep, alloc = mrsa.select_entropy_adaptive_token_keep(scores.to(DEV), ent.to(DEV), budget, mn,
+                                                          training=False)
+    rkeep, ralloc = O.select_entropy_adaptive_token_keep(scores, ent, budget, mn)
+    assert keep.dtype == torch.uint8 and alloc.dtype == torch.int64
+    assert torch.equal(alloc.cpu(), ralloc)
+    assert torch.equal(keep.cpu(), rkeep)
+    # the allocation-only entry and the gather agree with the oracle too
+    cap = torch.isfinite(scores).sum(-1)
+    a2 = mrsa.allocate_entropy_token_budget(ent.to(DEV), cap.to(DEV), budget, mn)
+    assert torch.equal(a2.cpu(), ralloc)
+
+
+def test_gather_selected_chunk_entropy_vs_oracle():
+    _note("gather selected chunk entropy")
+    g = torch.Generator().manual_seed(210)
+    ent = torch.rand(2, 40, 4, 7, generator=g) * 3
+    idx = torch.randint(-1, 43, (2, 33, 4, 32), generator=g).int()
+    got = mrsa.gather_selected_chunk_entropy(ent.to(DEV), idx.to(DEV))
+    torch.testing.assert_close(got.cpu(), O.gather_selected_chunk_entropy(ent, idx),
+                               atol=1e-6, rtol=1e-6)
+    with pytest.raises(ValueError, match="per-chunk minimum"):
+        mrsa.allocate_entropy_token_budget(ent[0, :, 0].to(DEV), torch.ones(40, 7, device=DEV),
+                                           10, 2)
+
+
+def test_refine_remote_tokens_entropy_vs_oracle():
+    _note("refine remote tokens entropy")
+    q, k, v, idx, w, valid = _route_inputs(50, 4096, 32, 220)
+    g = torch.Generator().manual_seed(221)
+    ent = torch.rand(1, 64, 4, 7, generator=g) * 3
+    keep, alloc = mrsa.refine_remote_tokens_entropy_g7(
+        q.to(DEV), k.to(DEV), idx.to(DEV), valid.to(DEV), ent.to(DEV), 64, 512, 1,
+        training=False)
+    assert keep.dtype == torch.int8 and keep.shape == (1, 50, 4, 32, 64)
+    scores = O.candidate_token_scores(q, k, idx, valid, 64)
+    rkeep, ralloc = O.select_entropy_adaptive_token_keep(
+        scores, O.gather_selected_chunk_entropy(ent, idx), 512, 1)
+    assert torch.equal(alloc.cpu(), ralloc)  # capacities are exact, so quotas match
+    differ = (keep.cpu().to(torch.uint8) != rkeep).reshape(50 * 4, -1).any(-1)
+    print(f"refine entropy: rows whose keep mask differs: {int(differ.sum())} of "
+          f"{differ.numel()}", flush=True)
+    assert int(differ.sum()) <= 2   # fp32 score differences at a chunk's quota boundary only
+
+
+def test_route_layer_entropy_policy_vs_oracle():
+    _note("route layer entropy policy budget 512")
+    L, Hq, Hkv, D = 2048, 28, 4, 128
+    g = torch.Generator().manual_seed(230)
+    q = torch.randn(1, L, Hq, D, generator=g).bfloat16()
+    rq = torch.randn(1, L, Hq, D, generator=g).bfloat16()
+    k = torch.randn(1, L, Hkv, D, generator=g)
+    k = (k + 0.3 * torch.randn(L // 64, Hkv, D, generator=g).repeat_interleave(64, 0)[None])
+    k = k.bfloat16()
+    v = torch.randn(1, L, Hkv, D, generator=g).bfloat16()
+    scale = torch.rand(Hq, generator=g) + 0.5
+    valid = torch.ones(1, L, dtype=torch.bool)
+    cfg = mrsa.RouteLayerConfig(token_budget=512, token_policy="entropy_adaptive",
+                                min_tokens_per_chunk=2)
+    out, mid = mrsa.route_attention(q.to(DEV), k.to(DEV), v.to(DEV), rq.to(DEV), scale.to(DEV),
+                                    valid.to(DEV), cfg, return_intermediates=True)
+    ref, rmid = O.route_layer(q, k, v, rq, scale, valid, token_budget=512,
+                              token_policy="entropy_adaptive", min_tokens_per_chunk=2)
+    same_routes = (mid["indices"].cpu().long() == rmid["indices"]).all(-1)
+    same_keep = (mid["token_keep"].cpu().to(torch.uint8) == rmid["token_keep"]).all(-1).all(-1)
+    rows = (same_routes & same_keep)[..., None].expand(-1, -1, -1, Hq // Hkv).reshape(1, L, Hq)
+    print(f"route layer entropy policy: rows with identical routes and keep masks: "
+          f"{float(rows.float().mean()):.4f}", flush=True)
+    assert float(rows.float().mean()) > 0.97
+    _close(out.cpu()[rows], ref[rows], "route layer with entropy token policy")
+    with pytest.raises(ValueError, match="cover the minimum"):
+        mrsa.route_attention(q.to(DEV), k.to(DEV), v.to(DEV), rq.to(DEV), scale.to(DEV),
+                             valid.to(DEV), mrsa.RouteLayerConfig(
+                                 token_budget=40, token_policy="entropy_adaptive",
+                                 min_tokens_per_chunk=2))
+
+
+@pytest.mark.parametrize("policy", ["global_qk", "entropy_adaptive"])
+def test_cached_route_attention_token_budget_vs_oracle(policy):
+    _note(f"cached route layer token budget policy={policy}")
+    L, Hq, Hkv, D, S = 4096, 28, 4, 128, 64
+    C, G = L // S, Hq // Hkv
+    g = torch.Generator().manual_seed(240)
+    q = torch.randn(1, L, Hq, D, generator=g).bfloat16()
+    rq = torch.randn(1, L, Hq, D, generator=g).bfloat16()
+    k = torch.randn(1, L, Hkv, D, generator=g)
+    k = (k + 0.3 * torch.randn(C, Hkv, D, generator=g).repeat_interleave(64, 0)[None]).bfloat16()
+    v = torch.randn(1, L, Hkv, D, generator=g).bfloat16()
+    valid = torch.ones(1, L, dtype=torch.bool)
+    scale = torch.rand(Hq, generator=g) + 0.5
+    lmk0 = torch.randn(1, C, Hkv, G, D, generator=g).bfloat16()
+    prior0 = torch.rand(1, C, Hkv, G, generator=g) * 0.5
+    chunk = 31
+    rows = torch.arange(chunk * S, (chunk + 1) * S)
+    aff = torch.tensor([chunk])
+    cache = mrsa.LayerKVCache(k.to(DEV), v.to(DEV), valid.to(DEV), lmk0.clone().to(DEV),
+                              prior0.clone().to(DEV))
+    cfg = mrsa.RouteLayerConfig(token_budget=256, token_policy=policy)
+    out, mid = mrsa.cached_route_attention(
+        q[:, rows].to(DEV), rq[:, rows].to(DEV), cache, rows.to(DEV), aff.to(DEV),
+        scale.to(DEV), cfg, return_intermediates=True)
+    ref, _, _, rmid = O.cached_route_layer(
+        q[:, rows], rq[:, rows], k, v, valid, lmk0, prior0, rows, aff, scale,
+        token_budget=256, token_policy=policy)
+    same_routes = (mid["indices"].cpu().long() == rmid["indices"]).all(-1)
+    same_keep = (mid["token_keep"].cpu().to(torch.uint8) == rmid["token_keep"]).all(-1).all(-1)
+    ok = (same_routes & same_keep)[..., None].expand(-1, -1, -1, G).reshape(1, S, Hq)
+    print(f"cached {policy}: rows with identical routes and keep masks: "
+          f"{float(ok.float().mean()):.4f}", flush=True)
+    assert float(ok.float().mean()) > 0.95
+    _close(out.cpu()[ok], ref[ok], f"cached route layer, {policy} token budget")
