@@ -34,9 +34,12 @@ def route_topk_g7(
 ):
     """Route logical G=7 query heads; same validation and outputs as the reference.
 
-    Returns (indices [B, L, Hkv, topk], scores [B, L, Hq, topk] bf16).  As in
-    the reference, inference (training=False) indices are int64 and training
-    indices int32.
+    Returns (indices [B, L, Hkv, topk], scores [B, L, Hq, topk] bf16), plus the
+    selected Gumbel noise [B, L, Hq, topk] (or None) with
+    return_selected_gumbel.  As in the reference, inference (training=False)
+    indices are int64 and training indices int32; in training with
+    use_gumbel the per-(head, chunk) noise joins the prior bias in the
+    selection and the route LSE (routing.py:96-131, :232-302).
     """
 
     if q.ndim != 4 or lmks.ndim != 5:
@@ -62,8 +65,26 @@ def route_topk_g7(
         raise ValueError(f"gumbel_scale must be non-negative, got {gumbel_scale}")
     if selection_mode not in {"post_softmax", "pre_softmax"}:
         raise ValueError(f"unsupported selection_mode={selection_mode}")
+    bias = prior_bias
+    noise = None
     if bool(use_gumbel) and bool(training) and gumbel_scale > 0:
-        raise ValueError("Gumbel route sampling is training-only; not supported by the forward kernels")
+        # routing.py:98-103 / :232-245: uniform(eps, 1 - eps) -> -log(-log(u))
+        # * gumbel_scale per (head, chunk), drawn in the reference's shapes
+        # (pre-softmax: [1, 1, h_q, C]; post-softmax: the physical G=8 heads
+        # and max(C, topk) chunks, of which the logical heads and the first C
+        # chunks are used), so the same generator state gives the same noise.
+        eps = torch.finfo(torch.float32).eps
+        if selection_mode == "pre_softmax":
+            uniform = torch.empty(1, 1, h_q, chunks, device=q.device,
+                                  dtype=torch.float32).uniform_(eps, 1.0 - eps)
+            noise = (-torch.log(-torch.log(uniform)) * float(gumbel_scale)).reshape(
+                h_kv, _LOGICAL_G, chunks)
+        else:
+            uniform = torch.empty(1, 1, h_kv * 8, max(chunks, topk), device=q.device,
+                                  dtype=torch.float32).uniform_(eps, 1.0 - eps)
+            noise = (-torch.log(-torch.log(uniform)) * float(gumbel_scale)).reshape(
+                h_kv, 8, -1)[:, :_LOGICAL_G, :chunks]
+        bias = (prior_bias.float() + noise.permute(2, 0, 1)[None]).contiguous()
 
     indices, scores = route_topk_launch(
         q.reshape(batch, seq_len, h_kv, _LOGICAL_G, dim),
@@ -71,16 +92,25 @@ def route_topk_g7(
         local_lse,
         topk,
         chunk_size,
-        bias4=prior_bias,
+        bias4=bias,
         drop_mask=drop_mask,
         selection_mode=selection_mode,
     )
     scores = scores.reshape(batch, seq_len, h_q, topk).to(q.dtype)
     if not training:
         indices = indices.to(torch.int64)
-    if return_selected_gumbel:
-        return indices, scores, None
-    return indices, scores
+    if not return_selected_gumbel:
+        return indices, scores
+    selected = None
+    if noise is not None:
+        # the noise of each head at its routed chunks, 0 at -1 slots
+        idx = indices.long()
+        safe = idx.clamp(0, chunks - 1)
+        nz = noise.reshape(1, 1, h_kv, _LOGICAL_G, chunks).expand(batch, seq_len, -1, -1, -1)
+        selected = torch.gather(nz, -1, safe[:, :, :, None, :].expand(-1, -1, -1, _LOGICAL_G, -1))
+        selected = selected.masked_fill((idx < 0)[:, :, :, None, :], 0.0)
+        selected = selected.reshape(batch, seq_len, h_q, topk)
+    return indices, scores, selected
 
 
 def _validate_selected(q, k, v, weights, indices, key_valid, chunk_size, token_keep):

@@ -4,8 +4,10 @@ Drop-ins for ``ops.topk_head_softmax.ref_softmax_topk_max_pooling``
 (ops/topk_head_softmax.py:15-156) and ``online_softmax_topk_head``
 (:1242-1415).  Both run the gfx950 route kernel (mrsa_route_topk_fwd); when q or the
 landmarks require grad the scores are differentiable through the route-score
-backward kernel (mrsa_route_score_bwd).  Gumbel noise is a training-time
-input and is not supported here.
+backward kernel (mrsa_route_score_bwd).  Gumbel noise [1, 1, h_q, S] (training
+only) is added, like the bias, to the selection logits and the route LSE and
+not to the returned scores (ops/topk_head_softmax.py:99-105, :341-353,
+:599-607): it enters the kernel folded into the per-chunk bias.
 """
 
 from __future__ import annotations
@@ -218,6 +220,21 @@ def _route_topk_impl(q5, lmks, lse4, bias4, drop_mask, key_valid, topk, block_si
     return indices, scores
 
 
+def _fold_noise(bias4, noise, B, C, Hkv, G, device):
+    """bias4 [B, C, Hkv, G] (or None) plus Gumbel noise [1, 1, Hkv * G, C]:
+    both are added to the same selection logits and route LSE terms."""
+    if noise is None:
+        return bias4
+    if tuple(noise.shape) != (1, 1, Hkv * G, C):
+        raise AssertionError(
+            f"gumbel_noise shape {tuple(noise.shape)} != ({1}, {1}, {Hkv * G}, {C})")
+    nz = noise.detach().to(device=device, dtype=torch.float32).reshape(Hkv, G, C)
+    nz = nz.permute(2, 0, 1)[None]
+    if bias4 is None:
+        return nz.expand(B, C, Hkv, G).contiguous()
+    return (bias4.to(device=device, dtype=torch.float32) + nz).contiguous()
+
+
 def _bias4(bias, B, C, Hkv, G):
     if bias is None:
         return None
@@ -243,14 +260,13 @@ def ref_softmax_topk_max_pooling(
     """Same contract as ops/topk_head_softmax.py:15-156.
 
     q [B, L, h_kv, G, D]; k_lmks [B, S, h_kv, D] or [B, S, h_kv*G, D];
-    lse_swa [B, L, h_q] or [B, L, h_kv, G]; returns indices [B, L, h_kv, topk]
-    (int64, ascending, -1 last) and fp32 raw scores [B, L, h_kv, G, topk].
+    lse_swa [B, L, h_q] or [B, L, h_kv, G]; gumbel_noise [1, 1, h_q, S] or
+    None; returns indices [B, L, h_kv, topk] (int64, ascending, -1 last) and
+    fp32 raw scores [B, L, h_kv, G, topk] (without bias or noise).
     """
 
     if selection_mode not in {"post_softmax", "pre_softmax"}:
         raise ValueError(f"unsupported selection_mode={selection_mode}")
-    if gumbel_noise is not None:
-        raise ValueError("gumbel_noise is a training-only input; the forward kernels do not take it")
     B, L, Hkv, G, D = q.shape
     C = k_lmks.shape[1]
     lse4 = None
@@ -258,7 +274,8 @@ def ref_softmax_topk_max_pooling(
         lse4 = lse_swa.reshape(B, L, Hkv, G)
     indices, scores = route_topk_launch(
         q, k_lmks, lse4, topk, block_size,
-        bias4=_bias4(bias, B, C, Hkv, G), drop_mask=drop_mask,
+        bias4=_fold_noise(_bias4(bias, B, C, Hkv, G), gumbel_noise, B, C, Hkv, G, q.device),
+        drop_mask=drop_mask,
         is_causal=is_causal, window_size=window_size, q_offset=q_offset,
         selection_mode=selection_mode, sm_scale=1.0 / math.sqrt(D), scores_fp32=True,
     )
@@ -270,7 +287,10 @@ def online_softmax_topk_head(
     is_training=True, drop_mask=None, sm_scale=None, bias=None, use_gumbel=False,
     gumbel_noise=None, G=1,
 ):
-    """Same contract as ops/topk_head_softmax.py:1242-1415 (forward only).
+    """Same contract as ops/topk_head_softmax.py:1242-1415.  The scores are
+    differentiable in q and lmks when they require grad; use_gumbel (or a
+    given gumbel_noise [1, 1, h_q, S]) adds Gumbel noise to the selection in
+    training mode.
 
     Returns (indices [B, L, h_kv, topk] int32, scores [B, L, h_q, topk] bf16);
     for is_training=False with a logical group of 7 the scores come back in
@@ -278,8 +298,9 @@ def online_softmax_topk_head(
     branch does.
     """
 
-    if use_gumbel or gumbel_noise is not None:
-        raise ValueError("Gumbel route sampling is training-only; not supported by the forward kernels")
+    use_gumbel = bool(use_gumbel) or gumbel_noise is not None
+    if use_gumbel and not is_training:
+        raise AssertionError("gumbel_noise is only supported in training mode")
     if q.dim() == 4:
         B, L, h_q, D = q.shape
         lmks_h = lmks.shape[2]
@@ -308,9 +329,17 @@ def online_softmax_topk_head(
     lse4 = lse_swa.reshape(B, L, h_kv, g_eff)
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
+    bias4 = _bias4(bias, B, C, h_kv, g_eff)
+    if use_gumbel:
+        if gumbel_noise is None:
+            # ops/topk_head_softmax.py:1177-1180
+            u = torch.rand(1, 1, h_kv * g_eff, C, device=q.device, dtype=torch.float32)
+            u.clamp_(min=1e-20, max=1 - 1e-7)
+            gumbel_noise = -torch.log(-torch.log(u))
+        bias4 = _fold_noise(bias4, gumbel_noise, B, C, h_kv, g_eff, q.device)
     indices, scores = route_topk_launch(
         q5, lmks, lse4, topk, block_size,
-        bias4=_bias4(bias, B, C, h_kv, g_eff), drop_mask=drop_mask,
+        bias4=bias4, drop_mask=drop_mask,
         is_causal=is_causal, window_size=window_size, q_offset=q_offset,
         sm_scale=sm_scale if is_training else 1.0 / math.sqrt(D),
     )

@@ -183,11 +183,13 @@ def remote_drop_mask_rows(valid_mask, window, chunk_size, positions):
 # ---------------------------------------------------------------------------
 def route_topk(q5, lmks, lse4, topk, block_size, *, drop_mask=None, bias4=None,
                selection_mode="post_softmax", is_causal=False, window_size=0, q_offset=0,
-               query_block=512):
+               query_block=512, gumbel_noise=None):
     """ref_softmax_topk_max_pooling (ops/topk_head_softmax.py:15-156).
 
     q5 [B, L, Hkv, G, D]; lmks [B, C, Hkv*G, D] or [B, C, Hkv, D];
-    lse4 [B, L, Hkv, G]; bias4 [B, C, Hkv, G]; drop_mask [B, L, C].
+    lse4 [B, L, Hkv, G]; bias4 [B, C, Hkv, G]; drop_mask [B, L, C];
+    gumbel_noise [1, 1, Hkv * G, C], added after the bias to the selection
+    logits and the route LSE (:99-105).
     Returns indices [B, L, Hkv, topk] int64 (ascending, -1 last), scores
     [B, L, Hkv, G, topk] fp32 (raw scaled q.k at the picks, -inf at -1) and
     the selection scores [B, L, Hkv, C] (max over G after the drop mask) used
@@ -221,6 +223,8 @@ def route_topk(q5, lmks, lse4, topk, block_size, *, drop_mask=None, bias4=None,
         x = logits
         if bias4 is not None:
             x = x + bias4.float().permute(0, 2, 3, 1)[:, None]
+        if gumbel_noise is not None:
+            x = x + gumbel_noise.float().reshape(1, 1, H, G, C)
         if selection_mode == "pre_softmax":
             y = x
         else:

@@ -615,3 +615,72 @@ def test_route_layer_vs_oracle():
     classify_routing(mid["indices"], rmid["indices"], rq, mid["landmark_keys"], mid["local_lse"],
                      mid["prior_bias"], lambda r: O.remote_drop_mask(valid, 256, 64)[:, r],
                      32, 64, "route layer L=2048")
+
+
+# -- Gumbel route sampling (training): ops/topk_head_softmax.py:99-105, routing.py:96-302
+def test_route_topk_gumbel_noise_vs_oracle():
+    _note("route topk with explicit gumbel noise")
+    B, L, Hkv, G, D, C, K = 1, 256, 2, 7, 128, 64, 16
+    g = torch.Generator().manual_seed(300)
+    q = torch.randn(B, L, Hkv * G, D, generator=g).bfloat16()
+    lm = torch.randn(B, C, Hkv * G, D, generator=g).bfloat16()
+    lse = torch.randn(B, L, Hkv * G, generator=g) + 3
+    bias = torch.rand(B, C, Hkv, G, generator=g)
+    noise = -torch.log(-torch.log(torch.rand(1, 1, Hkv * G, C, generator=g).clamp(1e-6, 1 - 1e-6)))
+    idx, sc = mrsa.online_softmax_topk_head(q.to(DEV), lm.to(DEV), lse.to(DEV), K, 64, 0,
+                                            is_causal=False, bias=bias.to(DEV),
+                                            gumbel_noise=noise.to(DEV), G=G)
+    ridx, rsc, sel = O.route_topk(q.reshape(B, L, Hkv, G, D), lm, lse.reshape(B, L, Hkv, G), K, 64,
+                                  bias4=bias, gumbel_noise=noise)
+    gap = O.boundary_gap(sel, K)
+    same = (idx.cpu().long() == ridx).all(-1)
+    assert bool((same | (gap < 1e-5)).all()), "index mismatch away from a near tie"
+    # scores stay raw q.k * scale (no bias, no noise)
+    ok = same[:, :, :, None].expand(-1, -1, -1, G).reshape(B, L, Hkv * G)
+    # (one bf16 ulp: the fp32 dot products are summed in different orders)
+    torch.testing.assert_close(sc.float().cpu()[ok], rsc.reshape(B, L, Hkv * G, K)[ok].bfloat16().float(),
+                               rtol=2 ** -7, atol=1e-3)
+    # the noise changes the routing
+    nidx, _ = mrsa.online_softmax_topk_head(q.to(DEV), lm.to(DEV), lse.to(DEV), K, 64, 0,
+                                            is_causal=False, bias=bias.to(DEV), G=G)
+    assert not torch.equal(nidx.cpu(), idx.cpu())
+    with pytest.raises(AssertionError, match="training"):
+        mrsa.online_softmax_topk_head(q.to(DEV), lm.to(DEV), lse.to(DEV), K, 64, 0,
+                                      is_causal=False, is_training=False,
+                                      gumbel_noise=noise.to(DEV), G=G)
+
+
+def test_route_topk_g7_gumbel_sampling_vs_oracle():
+    _note("route_topk_g7 gumbel sampling")
+    B, L, Hkv, G, D, C, K = 1, 128, 2, 7, 128, 48, 16
+    g = torch.Generator().manual_seed(310)
+    q = torch.randn(B, L, Hkv * G, D, generator=g).bfloat16().to(DEV)
+    lm = torch.randn(B, C, Hkv, G, D, generator=g).bfloat16().to(DEV)
+    lse = (torch.randn(B, L, Hkv, G, generator=g) + 3).to(DEV)
+    prior = torch.rand(B, C, Hkv, G, generator=g).to(DEV)
+    drop = torch.zeros(B, L, C, dtype=torch.int32, device=DEV)
+    drop[:, :, 5] = 1
+    torch.cuda.manual_seed(1234)
+    idx, sc, selg = mrsa.route_topk_g7(q, lm, lse, prior, drop, K, 64, 256, training=True,
+                                       use_gumbel=True, gumbel_scale=0.5,
+                                       return_selected_gumbel=True)
+    # the same draw, in the reference's physical shape
+    torch.cuda.manual_seed(1234)
+    eps = torch.finfo(torch.float32).eps
+    u = torch.empty(1, 1, Hkv * 8, max(C, K), device=DEV).uniform_(eps, 1.0 - eps)
+    noise = (-torch.log(-torch.log(u)) * 0.5).reshape(Hkv, 8, -1)[:, :7, :C].cpu()
+    ridx, _, sel = O.route_topk(q.cpu().reshape(B, L, Hkv, G, D), lm.cpu().reshape(B, C, Hkv * G, D),
+                                lse.cpu(), K, 64, drop_mask=drop.cpu(), bias4=prior.cpu(),
+                                gumbel_noise=noise.reshape(1, 1, Hkv * G, C))
+    gap = O.boundary_gap(sel, K)
+    same = (idx.cpu().long() == ridx).all(-1)
+    print(f"gumbel routing: identical lists {float(same.float().mean()):.4f}, "
+          f"near ties among the rest {int(((~same) & (gap < 1e-5)).sum())}", flush=True)
+    assert bool((same | (gap < 1e-5)).all())
+    assert idx.dtype == torch.int32
+    # selected noise: the head's noise at each routed chunk, 0 at -1 slots
+    ii = idx.cpu().long()
+    exp = torch.gather(noise[None, None].expand(B, L, Hkv, G, C), -1,
+                       ii.clamp(min=0)[:, :, :, None, :].expand(-1, -1, -1, G, -1))
+    exp = exp.masked_fill((ii < 0)[:, :, :, None, :], 0.0).reshape(B, L, Hkv * G, K)
+    assert torch.equal(selg.cpu(), exp)
