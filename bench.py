@@ -15,6 +15,10 @@ Prints ONE JSON line (rank 0).  Besides the contract fields it carries:
                 timed on this host's cores
   stages_us     average per-stage times from the same events
 
+``--workload backward`` times the backward of the routed attention and of
+the route scores at configuration 2's shapes, on the routing of the forward
+route layer (training-side: no BASELINE number exists for it).
+
 ``--workload decode`` instead times the Fast-dLLM cached block step of one
 route layer (SURVEY configuration 5): a K/V cache of L=131072 tokens (2048
 chunks), 64 successive 32-token query blocks at its tail; each step writes the
@@ -118,7 +122,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("route", "decode", "swa", "model"), default="route")
+    ap.add_argument("--workload", choices=("route", "decode", "swa", "model", "backward"),
+                    default="route")
     ap.add_argument("--token-budget", type=int, default=0,
                     help="route workload with the remote-token refinement (global_qk) at "
                          "this budget (0: off, the configuration-2 default)")
@@ -128,7 +133,7 @@ def main() -> int:
                     help="first run a plain 1 GiB device copy three times (reference "
                          "dispatch for scaling FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
-    short = args.workload in ("route", "swa")
+    short = args.workload in ("route", "swa", "backward")
     if args.steps is None:
         args.steps = 50 if short else 20
     if args.warmup is None:
@@ -150,6 +155,8 @@ def main() -> int:
         return model_main(args, torch, mrsa, dev)
     if args.workload == "swa":
         return swa_main(args, torch, mrsa, dev)
+    if args.workload == "backward":
+        return backward_main(args, torch, mrsa, dev)
     if args.copy_calibration:
         src = torch.empty(1 << 29, dtype=torch.int16, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -247,6 +254,84 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def backward_flops(L: int) -> float:
+    """Algorithmic FLOPs of the routed-attention backward: per (query head,
+    routed slot) the five 63-key x 128 products S, dP, dQ, dK, dV (2 FLOP per
+    MAC)."""
+    return 5.0 * 2.0 * 63 * D * HQ * TOPK * L
+
+
+def backward_main(args, torch, mrsa, dev) -> int:
+    """Backward of the routed chunk attention (HiLS_block_M_head's backward:
+    dQ, dK, dV, dW, K/V fragment layouts included) and of the route scores
+    (grad_q, grad_lmk) at configuration 2, with indices, weights and
+    landmarks from the forward route layer and seeded upstream gradients."""
+
+    from mrsa.sparse_attention import selected_attention_backward
+
+    L, C, G = L_CFG2, L_CFG2 // CHUNK, HQ // HKV
+    q, k, v = make_inputs(L, 1234, dev, torch.bfloat16)
+    valid = torch.ones(1, L, dtype=torch.bool, device=dev)
+    cfg = mrsa.RouteLayerConfig(local_window=WINDOW, chunk_size=CHUNK, topk=TOPK)
+    _, mid = mrsa.route_attention(q, k, v, q, torch.ones(HQ, device=dev), valid, cfg,
+                                  return_intermediates=True)
+    idx, w, lmk = mid["indices"], mid["remote_weights"], mid["landmark_keys"]
+    g = torch.Generator(device=dev).manual_seed(97)
+    dout = torch.randn(1, L, HQ, D, generator=g, device=dev).bfloat16()
+    dscore = torch.randn(1, L, HKV, G, TOPK, generator=g, device=dev).bfloat16()
+    q5 = q.reshape(1, L, HKV, G, D)
+    lmk4 = lmk.reshape(1, C, HQ, D)
+    stream = torch.cuda.current_stream(dev)
+    times = []
+
+    def run(record):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record(stream)
+        selected_attention_backward(q, k, v, w, idx, valid, CHUNK, dout)
+        e[1].record(stream)
+        torch.ops.mrsa.route_score_bwd(q5, lmk4, idx, dscore, D ** -0.5)
+        e[2].record(stream)
+        if record:
+            times.append(e)
+
+    for _ in range(args.warmup):
+        run(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run(True)
+    torch.cuda.synchronize()
+    ms_per_step = 1000.0 * (time.perf_counter() - t0) / args.steps
+    sel_us = sum(e[0].elapsed_time(e[1]) for e in times) * 1000.0 / len(times)
+    score_us = sum(e[1].elapsed_time(e[2]) for e in times) * 1000.0 / len(times)
+    flops = backward_flops(L)
+    achieved = flops / (sel_us * 1e-6) / 1e12
+    line = {
+        "metric": "MRSA routed-attention + route-score backward tokens/s @16k (config 2 shapes)",
+        "value": L / (ms_per_step / 1000.0),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "routed attention + route score backward (config 2 shapes)",
+                   "seq_len": L, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
+                   "chunk_size": CHUNK, "topk": TOPK, "parallelism": "single-gpu"},
+        "roofline": {"bound": "mfma", "kernel": "selected_attention backward (chunk-major)",
+                     "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                     "flops_per_launch": flops, "avg_launch_us": sel_us},
+        "stages_us": {"selected_attention_backward": sel_us, "route_score_backward": score_us},
+    }
     print(json.dumps(line), flush=True)
     return 0
 
