@@ -58,26 +58,24 @@ struct ScoreBwdArgs {
   float* ws;            // [parts, B, NL, C, 128] fp32 parts of grad_lmk
 };
 
-// LDS (40 KB), all bf16:
+// LDS (46 KB), all bf16:
 //   D    [32 rows][256 chunks]: row l 512 B, 16-byte block b at b ^ (l & 15)
-//   D^T  [256 chunks][32 rows]: row c 64 B, block b at b ^ ((c >> 2) & 3)
-//   Q^T  [128 dims][32 rows]:   row d 64 B, block b at b ^ ((d >> 2) & 3)
-// The swizzles put the 16 rows of one matrix-operand read in 16 different
-// 16-byte bank groups.
+//   D^T  [256 chunks][32 rows]: row c 80 B (64 used)
+//   Q^T  [128 dims][32 rows]:   row d 80 B (64 used)
+// The swizzle and the 80-byte strides put the 16 rows of one matrix-operand
+// read in 16 different 4-bank groups; Q^T is written two rows per 32-bit
+// store, also without bank conflicts.
+constexpr uint32_t kRow80 = 80;
 constexpr uint32_t kDOff = 0;
 constexpr uint32_t kDtOff = kTileQ * kBlockC * 2;
-constexpr uint32_t kQtOff = kDtOff + kBlockC * kTileQ * 2;
-constexpr uint32_t kSmemBytes = kQtOff + kDim * kTileQ * 2;
+constexpr uint32_t kQtOff = kDtOff + kBlockC * kRow80;
+constexpr uint32_t kSmemBytes = kQtOff + kDim * kRow80;
 
 __device__ __forceinline__ uint32_t d_off(int l, int c) {
   return kDOff + l * 512 + ((((c >> 3) ^ (l & 15))) << 4) + (c & 7) * 2;
 }
-__device__ __forceinline__ uint32_t t64_off(uint32_t base, int r, int l) {
-  return base + r * 64 + ((((l >> 3) ^ ((r >> 2) & 3))) << 4) + (l & 7) * 2;
-}
-
-__device__ __forceinline__ uint32_t bits16(u32x4_t v, int e) {
-  return (v[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+__device__ __forceinline__ uint32_t t80_off(uint32_t base, int r, int l) {
+  return base + r * kRow80 + l * 2;
 }
 
 __global__ __launch_bounds__(kThreads, 1) void route_score_bwd_kernel(ScoreBwdArgs a) {
@@ -145,6 +143,10 @@ __global__ __launch_bounds__(kThreads, 1) void route_score_bwd_kernel(ScoreBwdAr
         }
       }
     }
+    // The staging region becomes the D / D^T tiles: all zero to start.
+    __syncthreads();
+    for (uint32_t o = 16 * tid; o < kQtOff; o += 16 * kThreads)
+      *reinterpret_cast<u32x4_t*>(smem + o) = u32x4_t{0, 0, 0, 0};
     f32x4_t acc[2][8];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
@@ -155,17 +157,23 @@ __global__ __launch_bounds__(kThreads, 1) void route_score_bwd_kernel(ScoreBwdAr
     // list slots are loaded into registers while this item's products run.
     const int ng = g_hi - g_lo;
     const int64_t nitems = (t1 - t0) * ng;
-    u32x4_t qv = {0, 0, 0, 0};
-    int32_t pc[kPf];
+    // Q rows of a tile: thread (rows 2 p, 2 p + 1, dims 4 m .. 4 m + 3) with
+    // p = tid & 15, m = tid >> 4.
+    u32x2_t qv0 = {0u, 0u}, qv1 = {0u, 0u};
+    int32_t pc[kPf], pcp[kPf];
     float pg[kPf];
+#pragma unroll
+    for (int i = 0; i < kPf; ++i) pcp[i] = -1;
     auto fetch = [&](int64_t it) {
       const int64_t l0 = (t0 + it / ng) * kTileQ;
       const int g = g_lo + (int)(it % ng);
-      const int64_t row = l0 + (tid >> 4);
-      qv = u32x4_t{0, 0, 0, 0};
-      if (row < a.L)
-        qv = *reinterpret_cast<const u32x4_t*>(
-            a.q + (((b * a.L + row) * a.Hkv + h) * a.G + g) * kDim + (tid & 15) * 8);
+      const int64_t row = l0 + 2 * (tid & 15);
+      const int64_t qoff = (((b * a.L + row) * a.Hkv + h) * a.G + g) * kDim + 4 * (tid >> 4);
+      const int64_t qstep = (int64_t)a.Hkv * a.G * kDim;  // one row further
+      qv0 = u32x2_t{0u, 0u};
+      qv1 = u32x2_t{0u, 0u};
+      if (row < a.L) qv0 = *reinterpret_cast<const u32x2_t*>(a.q + qoff);
+      if (row + 1 < a.L) qv1 = *reinterpret_cast<const u32x2_t*>(a.q + qoff + qstep);
 #pragma unroll
       for (int i = 0; i < kPf; ++i) {
         pc[i] = -1;
@@ -185,28 +193,43 @@ __global__ __launch_bounds__(kThreads, 1) void route_score_bwd_kernel(ScoreBwdAr
       const int g = g_lo + (int)(it % ng);
       {
         __syncthreads();  // the previous products are done with the LDS tiles
+        if (K <= kPf * kThreads / kTileQ) {
+          // clear the previous item's entries (the tiles start at zero)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          *reinterpret_cast<u32x4_t*>(smem + kDOff + (tid + kThreads * i) * 16) = u32x4_t{0, 0, 0, 0};
+          for (int i = 0; i < kPf; ++i) {
+            if (pcp[i] < 0) continue;
+            *reinterpret_cast<uint16_t*>(smem + d_off(sl[i], pcp[i])) = 0;
+            *reinterpret_cast<uint16_t*>(smem + t80_off(kDtOff, pcp[i], sl[i])) = 0;
+          }
+        } else {
+          for (uint32_t o = 16 * tid; o < kQtOff; o += 16 * kThreads)
+            *reinterpret_cast<u32x4_t*>(smem + o) = u32x4_t{0, 0, 0, 0};
+        }
         {
-          // Q^T: thread (row l, dims d0..d0+7)
-          const int l = tid >> 4;
-          const int d0 = (tid & 15) * 8;
+          // Q^T: dims 4 m + e, rows 2 p and 2 p + 1 in one 32-bit store
+          const int p2 = 2 * (tid & 15);
+          const int m4 = 4 * (tid >> 4);
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            *reinterpret_cast<uint16_t*>(smem + t64_off(kQtOff, d0 + e, l)) = (uint16_t)bits16(qv, e);
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t lo = (qv0[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+            const uint32_t hi = (qv1[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+            *reinterpret_cast<uint32_t*>(smem + t80_off(kQtOff, m4 + e, p2)) = lo | (hi << 16);
+          }
         }
         __syncthreads();  // zeros written before the scatter
         auto put = [&](int l, int64_t c, float gv) {
-          if (c < c0 || c >= c0 + kBlockC || c >= a.C) return;
+          if (c < c0 || c >= c0 + kBlockC || c >= a.C) return false;
           const uint16_t val = (uint16_t)f32_to_bf16(gv * a.scale);
           const int cr = (int)(c - c0);
           *reinterpret_cast<uint16_t*>(smem + d_off(l, cr)) = val;
-          *reinterpret_cast<uint16_t*>(smem + t64_off(kDtOff, cr, l)) = val;
+          *reinterpret_cast<uint16_t*>(smem + t80_off(kDtOff, cr, l)) = val;
+          return true;
         };
 #pragma unroll
-        for (int i = 0; i < kPf; ++i)
-          if (pc[i] >= 0) put(sl[i], pc[i], pg[i]);
+        for (int i = 0; i < kPf; ++i) {
+          pcp[i] = -1;  // block-relative chunk written by this slot, for the clear
+          if (pc[i] >= 0 && put(sl[i], pc[i], pg[i])) pcp[i] = (int)(pc[i] - c0);
+        }
         // Lists longer than kPf * kThreads / kTileQ slots: the rest directly.
         for (int p = tid + kPf * kThreads; p < kTileQ * K; p += kThreads) {
           const int l = p / K;
@@ -240,14 +263,12 @@ __global__ __launch_bounds__(kThreads, 1) void route_score_bwd_kernel(ScoreBwdAr
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
           const int c = 32 * w + 16 * ct + j;
-          bo[ct] = *reinterpret_cast<const u32x4_t*>(smem + kDtOff + c * 64 +
-                                                     ((kg ^ ((c >> 2) & 3)) << 4));
+          bo[ct] = *reinterpret_cast<const u32x4_t*>(smem + kDtOff + c * kRow80 + 16 * kg);
         }
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
           const int d = 16 * dt + j;
-          const u32x4_t qa = *reinterpret_cast<const u32x4_t*>(smem + kQtOff + d * 64 +
-                                                               ((kg ^ ((d >> 2) & 3)) << 4));
+          const u32x4_t qa = *reinterpret_cast<const u32x4_t*>(smem + kQtOff + d * kRow80 + 16 * kg);
           acc[0][dt] = mfma_bf16_16x16x32(qa, bo[0], acc[0][dt]);
           acc[1][dt] = mfma_bf16_16x16x32(qa, bo[1], acc[1][dt]);
           if (dt % 4 == 3) __builtin_amdgcn_sched_barrier(0);
@@ -327,7 +348,9 @@ Plan make_plan(int64_t B, int64_t L, int64_t C, int64_t Hkv, int64_t G, int per_
   Plan p;
   const int64_t NL = per_head ? Hkv * G : Hkv;
   const int64_t ntiles = (L + kTileQ - 1) / kTileQ;
-  int64_t parts = (kTargetUnits + B * NL - 1) / (B * NL);
+  // One workgroup per CU: at most kTargetUnits so that a last, partly
+  // filled round of workgroups does not cost a whole round.
+  int64_t parts = kTargetUnits / (B * NL);
   if (parts > ntiles) parts = ntiles;
   if (parts < 1) parts = 1;
   const int64_t tpp = (ntiles + parts - 1) / parts;

@@ -25,25 +25,28 @@ namespace {
 
 constexpr int kMaxTopk = 64;
 
-template <int LPR, bool VEC>
+// I: the index type (uint32_t when every index of the call fits 32 bits,
+// which turns the row decode's divisions into 32-bit ones).
+template <int LPR, bool VEC, class I>
 __device__ __forceinline__ void route_weights_row(
-    int64_t t, const uint16_t* __restrict__ scores,
+    int64_t t64, const uint16_t* __restrict__ scores,
     const int32_t* __restrict__ indices, const float* __restrict__ bias,
-    const float* __restrict__ lse, int64_t rows, int64_t L, int64_t C, int Hkv, int G, int K,
+    const float* __restrict__ lse, int64_t rows64, int64_t L64, int64_t C64, int Hkv, int G, int K,
     float inv_t, int has_off, int affine, float off, float gscale, uint16_t* __restrict__ rw,
     uint16_t* __restrict__ lw, float* __restrict__ gate_logit) {
+  const I t = (I)t64, rows = (I)rows64, L = (I)L64, C = (I)C64;
   const int part = (int)(t % LPR);
-  const int64_t r0 = t / LPR;
+  const I r0 = t / LPR;
   const bool live = r0 < rows;
-  const int64_t r = live ? r0 : rows - 1;  // lanes past the end still join the row reductions
-  const int Hq = Hkv * G;
-  const int hq = (int)(r % Hq);
-  const int64_t bl = r / Hq;
-  const int64_t b = bl / L;
+  const I r = live ? r0 : rows - 1;  // lanes past the end still join the row reductions
+  const I Hq = (I)(Hkv * G);
+  const I bl = r / Hq;
+  const int hq = (int)(r - bl * Hq);
+  const I b = bl / L;
   const int hk = hq / G, g = hq - hk * G;
   const int k0 = part * 8;
-  const uint16_t* sc = scores + r * K + k0;
-  const int32_t* ix = indices + (bl * Hkv + hk) * K + k0;
+  const uint16_t* sc = scores + r * (I)K + k0;
+  const int32_t* ix = indices + (bl * (I)Hkv + hk) * (I)K + k0;
 
   uint32_t sv[4] = {0u, 0u, 0u, 0u};
   int32_t iv[8];
@@ -72,9 +75,9 @@ __device__ __forceinline__ void route_weights_row(
   for (int j = 0; j < 8; ++j) {
     const int32_t c = iv[j];
     float v = neg_inf();
-    if (k0 + j < K && c >= 0 && c < C) {
+    if (k0 + j < K && c >= 0 && (I)c < C) {
       const float s = (j & 1) ? bf16_hi(sv[j >> 1]) : bf16_lo(sv[j >> 1]);
-      v = (s + bias[((b * C + c) * Hkv + hk) * G + g]) * inv_t;
+      v = (s + bias[((b * C + (I)c) * (I)Hkv + hk) * (I)G + g]) * inv_t;
     }
     x[j] = v;
     rmax = fmaxf(rmax, v);
@@ -154,7 +157,7 @@ __device__ __forceinline__ void route_weights_row(
   }
   if (!live) return;
   if (gate_logit && part == 0) gate_logit[r] = gl_val;
-  uint16_t* out = rw + r * K + k0;
+  uint16_t* out = rw + r * (I)K + k0;
   if (VEC && k0 < K) {
     u32x4_t o4;
 #pragma unroll
@@ -168,7 +171,7 @@ __device__ __forceinline__ void route_weights_row(
   if (part == 0) lw[r] = (uint16_t)f32_to_bf16(lw_val);
 }
 
-template <int LPR, bool VEC>
+template <int LPR, bool VEC, class I>
 __global__ void __launch_bounds__(256)
     route_weights_kernel(const uint16_t* __restrict__ scores, const int32_t* __restrict__ indices,
                          const float* __restrict__ bias, const float* __restrict__ lse,
@@ -181,7 +184,7 @@ __global__ void __launch_bounds__(256)
   const int has_off = goff != nullptr, affine = gsc != nullptr;
   const float off = has_off ? *goff : 0.f;
   const float gscale = affine ? *gsc : 1.f;
-  route_weights_row<LPR, VEC>((int64_t)blockIdx.x * blockDim.x + threadIdx.x, scores, indices,
+  route_weights_row<LPR, VEC, I>((int64_t)blockIdx.x * blockDim.x + threadIdx.x, scores, indices,
                               bias, lse, rows, L, C, Hkv, G, K, inv_t, has_off, affine, off,
                               gscale, rw, lw, gate_logit);
 }
@@ -193,7 +196,13 @@ int launch_rw(bool vec, hipStream_t s, const uint16_t* scores, const int32_t* in
               uint16_t* lw, float* gate_logit) {
   const int64_t blocks = (rows * LPR + 255) / 256;
   if (blocks > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
-  auto kern = vec ? route_weights_kernel<LPR, true> : route_weights_kernel<LPR, false>;
+  // 32-bit indices when the largest flat index of the call fits
+  const bool small = rows * LPR < ((int64_t)1 << 31) && rows * K < ((int64_t)1 << 31) &&
+                     (rows / (Hkv * G) / L + 1) * C * Hkv * G < ((int64_t)1 << 31);
+  auto kern = small ? (vec ? route_weights_kernel<LPR, true, uint32_t>
+                           : route_weights_kernel<LPR, false, uint32_t>)
+                    : (vec ? route_weights_kernel<LPR, true, int64_t>
+                           : route_weights_kernel<LPR, false, int64_t>);
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, s, scores, indices, bias, lse,
                      rows, L, C, Hkv, G, K, inv_t, goff, gsc, rw, lw, gate_logit);
   return mrsa_launch_status();
