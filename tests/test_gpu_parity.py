@@ -493,6 +493,38 @@ def test_selected_attention_fused_output_equals_fusion(Lq, Lk, K, parts, keep):
         assert_nearly_identical(fused, expect, f"fused vs fusion K={K}", atol=0.03)
 
 
+@pytest.mark.parametrize("Lq,K,keep", [(4, 32, False), (4, 32, True), (8, 16, True)])
+def test_selected_attention_contended_lock_repeats(Lq, K, keep):
+    # Few queries that all route to the same chunks: every step of a walk
+    # has the same owners, so the eight waves of a workgroup keep asking for
+    # the same lock bits.  Waits that set momentary bits on a failed try can
+    # lock two such waves in step until one gives up and adds without the
+    # lock over another's read-modify-write (lost updates of whole rows).
+    # Every repeat must match the oracle.
+    _note(f"selected contended Lq={Lq} K={K} keep={keep}")
+    Hkv, G, D, Lk = 4, 7, 128, 2048
+    C = Lk // 64
+    q = _rand((1, Lq, Hkv * G, D), 90).bfloat16()
+    k, v = _planted_kv(Lk, Hkv, D, 91)
+    idx = _sorted_routes(Lq, Hkv, K, C, 92)
+    w = torch.softmax(_rand((1, Lq, Hkv * G, K), 93), -1).bfloat16()
+    valid = torch.rand(1, Lk, generator=torch.Generator().manual_seed(94)) > 0.03
+    tk = None
+    if keep:
+        tk = (torch.rand(1, Lq, Hkv, K, 64, generator=torch.Generator().manual_seed(95)) > 0.5)
+        tk = tk.to(torch.int8)
+    ref = O.selected_attention(q, k, v, w, idx, valid, 64, token_keep=tk)
+    args = (q.to(DEV), mrsa.kv_fragments(k.to(DEV), v.to(DEV)), w.to(DEV), idx.to(DEV),
+            valid.to(DEV), 64)
+    tkd = None if tk is None else tk.to(DEV)
+    outs = [selected_attention_launch(*args, parts=1, token_keep=tkd) for _ in range(40)]
+    torch.cuda.synchronize()
+    errs = [float((out.float().cpu() - ref.float()).abs().max()) for out in outs]
+    print(f"contended repeats: max_abs worst {max(errs):.3e} median {sorted(errs)[20]:.3e}",
+          flush=True)
+    assert max(errs) <= 2e-2, errs
+
+
 def test_selected_attention_reference_kat():
     # test_hils_non_power_two_topk.py:95-142 (cached and uncached shapes).
     for query_len in (35, 2048):
