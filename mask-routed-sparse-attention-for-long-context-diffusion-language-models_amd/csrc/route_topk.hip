@@ -58,6 +58,7 @@ struct RouteArgs {
   int32_t* indices;
   void* scores;
   int scores_fp32;
+  int vec_out;  // K % 32 == 0, indices and scores 16-byte aligned: one 16-byte store per lane
 };
 
 __device__ __forceinline__ int64_t floor_div(int64_t a, int64_t b) {
@@ -467,8 +468,42 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_fast_kernel(RouteA
   // operations in order).
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   int32_t* irow = a.indices + ((b * L + r) * a.Hkv + h) * K;
-  if (rvalid)
-    for (int s = grp; s < K; s += 4) irow[s] = s < total ? (int32_t)plist[s] : -1;
+  // Output slots: with vec_out a lane writes the K / 4 consecutive slots
+  // s0 .. s0 + K / 4 - 1 of its query (one 16-byte store per 8 scores, per
+  // 4 indices), its picks held as int16 pairs in pk; else slots grp + 4 i.
+  const bool vec = a.vec_out != 0;
+  const int per = K >> 2, nv = K >> 5, s0 = per * grp;
+  uint32_t pk[8];
+#pragma unroll
+  for (int v = 0; v < 2; ++v) {
+    u32x4_t x = {0u, 0u, 0u, 0u};
+    if (vec && v < nv) x = *reinterpret_cast<const u32x4_t*>(plist + s0 + 8 * v);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pk[4 * v + e] = x[e];
+  }
+  // chunk of this lane's slot s0 + 8 v + e (0 past the picks)
+  auto pick_at = [&](int v, int e) {
+    const int c = (int)((pk[4 * v + (e >> 1)] >> (16 * (e & 1))) & 0xffffu);
+    return s0 + 8 * v + e < total ? c : 0;
+  };
+  if (rvalid) {
+    if (vec) {
+#pragma unroll
+      for (int v = 0; v < 2; ++v) {
+        if (v >= nv) break;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          u32x4_t o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            o[e] = s0 + 8 * v + 4 * hh + e < total ? (uint32_t)pick_at(v, 4 * hh + e) : 0xffffffffu;
+          *reinterpret_cast<u32x4_t*>(irow + s0 + 8 * v + 4 * hh) = o;
+        }
+      }
+    } else {
+      for (int s = grp; s < K; s += 4) irow[s] = s < total ? (int32_t)plist[s] : -1;
+    }
+  }
 
   // ---- pass 2 -------------------------------------------------------------
   // Raw logits bf16(s * scale) of the picks, heads G-1..0.  Pass 1 left head
@@ -508,13 +543,31 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_fast_kernel(RouteA
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if (rvalid) {
       uint16_t* orow = sc16 + (((b * L + r) * a.Hkv + h) * G + g) * K;
-      for (int s = grp; s < K; s += 4) {
-        uint16_t v = 0xff80u;  // -inf past the picks
-        if (s < total) {
-          const int c = plist[s];
-          v = tile[j * 256 + 4 * ((c >> 2) ^ j) + (c & 3)];
+      if (vec) {
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+          if (v >= nv) break;
+          uint32_t w[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int c = pick_at(v, e);
+            const uint32_t x = tile[j * 256 + 4 * ((c >> 2) ^ j) + (c & 3)];
+            w[e] = s0 + 8 * v + e < total ? x : 0xff80u;  // -inf past the picks
+          }
+          u32x4_t o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = w[2 * e] | (w[2 * e + 1] << 16);
+          *reinterpret_cast<u32x4_t*>(orow + s0 + 8 * v) = o;
         }
-        orow[s] = v;
+      } else {
+        for (int s = grp; s < K; s += 4) {
+          uint16_t v = 0xff80u;  // -inf past the picks
+          if (s < total) {
+            const int c = plist[s];
+            v = tile[j * 256 + 4 * ((c >> 2) ^ j) + (c & 3)];
+          }
+          orow[s] = v;
+        }
       }
     }
 #pragma unroll
@@ -1219,6 +1272,7 @@ int route_topk_dispatch(const void* q, const void* lmk, const float* lse_local, 
   a.indices = indices;
   a.scores = scores;
   a.scores_fp32 = scores_fp32;
+  a.vec_out = topk % 32 == 0 && (uintptr_t)indices % 16 == 0 && (uintptr_t)scores % 16 == 0;
   hipStream_t s = (hipStream_t)stream;
 
   const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)lmk % 16 == 0);
