@@ -34,22 +34,24 @@
 //
 // Adding a tile.  Two waves may hold tiles of the same query at once.  LDS
 // float atomics (ds_add_f32) run at about two cycles per lane, so instead a
-// wave takes both owners' bits of a per-workgroup lock word (all or nothing,
-// so no wave ever waits while holding a bit), reads the rows, accumulates
-// onto them and writes them back with 16-byte accesses, and clears the bits.
-// The first try is a ds_or_rtn issued right after the QK product and read
-// after the softmax; on a conflict it clears the bits it set and the wave
-// waits with compare-and-swap from the word as last seen, which sets no bit
-// unless it takes both.  (Retrying with OR and undo lets two waves that want
-// the same bits block each other with their momentary bits in lockstep for
-// as long as they keep retrying.)  A wait therefore ends once the holders
-// of the bits finish their tiles.  LDS operations of one wave complete in
-// issue order, so its writes land before its release and after another
-// wave's acquire.  The order of the fp32 additions into a row depends on
-// timing, so the last bit of an output can differ between runs.  Past
-// `spin_limit` tries (about 6 ms; a guard that ends the kernel, never reached
-// while every holder finishes its tile) the wave adds the tile with
-// ds_add_f32, which is exact only when no holder is inside those rows.
+// wave takes both owners' bits of a per-workgroup lock word, reads the
+// rows, accumulates onto them and writes them back with 16-byte accesses,
+// and clears the bits.
+// The first try is a ds_or_rtn of both bits, issued right after the QK
+// product and read after the softmax.  On a conflict the wave keeps the
+// lower bit if that try took it, gives the other back and takes the missing
+// bits one at a time, lowest first, with one-bit ORs (which change nothing
+// while the bit is taken).  A wave only waits while holding bits below the
+// one it waits for, so no cycle of waits forms, and no failed try leaves a
+// bit set.  (Retrying both bits with OR and undo let two waves that want the
+// same bits block each other with their momentary bits in lockstep for as
+// long as they kept retrying.)  LDS operations of one wave complete in issue
+// order, so its writes land before its release and after another wave's
+// acquire.  The order of the fp32 additions into a row depends on timing, so
+// the last bit of an output can differ between runs.  Past `spin_limit`
+// tries (about 6 ms; a guard that ends the kernel, never reached while every
+// holder finishes its tile) the wave gives its bits back and adds the tile
+// with ds_add_f32, which is exact only when no holder is inside those rows.
 //
 // LDS output rows: row (q, g) of slot q at (8 q + g) * 128 floats; the
 // 16-byte block b of dims 4 b .. 4 b + 3 sits at block b ^ g, so the eight
@@ -169,21 +171,14 @@ __device__ __forceinline__ uint64_t kept_bits(const int8_t* kr) {
   return bits;
 }
 
-// Lock word accesses (lane 0 issues; results made wave-uniform).  The
-// compare-and-swap stores `v` where the word equals `cmp` and returns the
-// word as it was.
-__device__ __forceinline__ uint32_t lds_cas_rtn(uint32_t addr, uint32_t cmp, uint32_t v) {
+// Lock word accesses (lane 0 issues; results made wave-uniform).
+__device__ __forceinline__ uint32_t lds_or_rtn(uint32_t addr, uint32_t v) {
   uint32_t old;
-  asm volatile("ds_cmpst_rtn_b32 %0, %1, %2, %3\n\ts_waitcnt lgkmcnt(0)"
+  asm volatile("ds_or_rtn_b32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
                : "=v"(old)
-               : "v"(addr), "v"(cmp), "v"(v)
+               : "v"(addr), "v"(v)
                : "memory");
   return old;
-}
-__device__ __forceinline__ uint32_t lds_read_rtn(uint32_t addr) {
-  uint32_t x;
-  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(x) : "v"(addr) : "memory");
-  return x;
 }
 __device__ __forceinline__ void lds_and(uint32_t addr, uint32_t v) {
   asm volatile("ds_and_b32 %0, %1" ::"v"(addr), "v"(v) : "memory");
@@ -659,25 +654,27 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       float* const pe = srow + lane_e;
       float* const po = srow + lane_o;
       asm volatile("" : "+v"(first_try) : "v"(Pb[1][3]));  // read after the softmax
-      uint32_t seen = __builtin_amdgcn_readfirstlane(first_try);
+      const uint32_t seen = __builtin_amdgcn_readfirstlane(first_try);
       bool locked = a.spin_limit > 0 && (seen & want) == 0u;
       if (a.spin_limit > 0 && !locked) {
-        // Undo the bits the first try set, then wait without setting any:
-        // compare-and-swap from the word as last seen while both bits are
-        // free, a plain re-read while either is taken.
-        if (lane == 0) lds_and(lock_addr, ~(want & ~seen));
-        for (int spin = 1; spin < a.spin_limit; ++spin) {
+        // Ordered wait: keep the lower bit if the first try took it, give
+        // back the other, then take the missing bits one at a time, lowest
+        // first (a one-bit OR changes nothing when the bit is taken).
+        const uint32_t low = want & (0u - want);
+        const uint32_t keep = want & ~seen & low;
+        const uint32_t back = want & ~seen & ~keep;
+        if (lane == 0 && back) lds_and(lock_addr, ~back);
+        uint32_t need = want & ~keep;
+        for (int spin = 1; need != 0u && spin < a.spin_limit; ++spin) {
+          const uint32_t bit = need & (0u - need);
           __builtin_amdgcn_s_sleep(1);
-          const bool free_now = (seen & want) == 0u;
-          uint32_t now = 0u;
-          if (lane == 0) now = free_now ? lds_cas_rtn(lock_addr, seen, seen | want) : lds_read_rtn(lock_addr);
-          now = __builtin_amdgcn_readfirstlane(now);
-          if (free_now && now == seen) {
-            locked = true;
-            break;
-          }
-          seen = now;
+          uint32_t old = 0u;
+          if (lane == 0) old = lds_or_rtn(lock_addr, bit);
+          old = __builtin_amdgcn_readfirstlane(old);
+          if ((old & bit) == 0u) need &= ~bit;
         }
+        locked = need == 0u;
+        if (!locked && lane == 0) lds_and(lock_addr, ~(want & ~need));  // give back what was taken
       }
       f32x4_t acc[8];
       // The lock word is read back above with lgkmcnt(0): the row reads
