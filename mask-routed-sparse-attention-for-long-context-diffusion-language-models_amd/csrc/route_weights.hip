@@ -25,6 +25,25 @@ namespace {
 
 constexpr int kMaxTopk = 64;
 
+// Max / sum over the LPR lanes of a row (aligned groups of 1, 2, 4 or 8
+// lanes) with DPP lane moves: swap neighbours, swap pairs, then mirror the
+// two quads of an 8-lane half-row.  The same operand pairs as xor shuffles
+// by 1, 2, 4, so the same bits.  Every lane of the row must be active.
+template <int LPR>
+__device__ __forceinline__ float row_lanes_max(float v) {
+  if constexpr (LPR >= 2) v = fmaxf(v, dpp_mov<0xb1>(v));   // quad_perm [1,0,3,2]
+  if constexpr (LPR >= 4) v = fmaxf(v, dpp_mov<0x4e>(v));   // quad_perm [2,3,0,1]
+  if constexpr (LPR >= 8) v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
+  return v;
+}
+template <int LPR>
+__device__ __forceinline__ float row_lanes_sum(float v) {
+  if constexpr (LPR >= 2) v += dpp_mov<0xb1>(v);
+  if constexpr (LPR >= 4) v += dpp_mov<0x4e>(v);
+  if constexpr (LPR >= 8) v += dpp_mov<0x141>(v);
+  return v;
+}
+
 // I: the index type (uint32_t when every index of the call fits 32 bits,
 // which turns the row decode's divisions into 32-bit ones).
 template <int LPR, bool VEC, class I>
@@ -69,21 +88,22 @@ __device__ __forceinline__ void route_weights_row(
       iv[j] = in ? ix[j] : -1;
     }
   }
+  // The bias of every slot is loaded (chunk 0 for a masked slot), so the
+  // gathers need no divergent branches.
   float x[8];
   float rmax = neg_inf();
+  const float* brow = bias + (b * C * (I)Hkv + hk) * (I)G + g;  // chunk c at c * Hkv * G
+  const I cstride = (I)(Hkv * G);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int32_t c = iv[j];
-    float v = neg_inf();
-    if (k0 + j < K && c >= 0 && (I)c < C) {
-      const float s = (j & 1) ? bf16_hi(sv[j >> 1]) : bf16_lo(sv[j >> 1]);
-      v = (s + bias[((b * C + (I)c) * (I)Hkv + hk) * (I)G + g]) * inv_t;
-    }
-    x[j] = v;
-    rmax = fmaxf(rmax, v);
+    const bool ok = k0 + j < K && c >= 0 && (I)c < C;
+    const float bv = brow[(ok ? (I)c : (I)0) * cstride];
+    const float s = (j & 1) ? bf16_hi(sv[j >> 1]) : bf16_lo(sv[j >> 1]);
+    x[j] = ok ? (s + bv) * inv_t : neg_inf();
+    rmax = fmaxf(rmax, x[j]);
   }
-#pragma unroll
-  for (int o = 1; o < LPR; o <<= 1) rmax = fmaxf(rmax, __shfl_xor(rmax, o, 64));
+  rmax = row_lanes_max<LPR>(rmax);
   float local = lse[r];
   if (has_off && !affine) local -= off;
   local *= inv_t;
@@ -111,8 +131,7 @@ __device__ __forceinline__ void route_weights_row(
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         rs += x[j] == neg_inf() ? 0.f : exp2_hw(__builtin_fmaf(x[j], kLog2e, -rb));
-#pragma unroll
-      for (int o = 1; o < LPR; o <<= 1) rs += __shfl_xor(rs, o, 64);
+      rs = row_lanes_sum<LPR>(rs);
       gl_val = (rmax == neg_inf() ? neg_inf() : rmax + log2_hw(rs) * kLn2) - local;
     }
     const float mb = m * kLog2e;
@@ -122,8 +141,7 @@ __device__ __forceinline__ void route_weights_row(
       x[j] = exp2_hw(__builtin_fmaf(x[j], kLog2e, -mb));  // -inf -> 0
       sum += x[j];
     }
-#pragma unroll
-    for (int o = 1; o < LPR; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    sum = row_lanes_sum<LPR>(sum);
     const float el = exp2_hw(__builtin_fmaf(local, kLog2e, -mb));
     sum += el;
     const float inv = rcp_hw(sum);
@@ -144,8 +162,7 @@ __device__ __forceinline__ void route_weights_row(
       x[j] = exp2_hw(__builtin_fmaf(x[j], kLog2e, -rb));  // -inf -> 0
       sum += x[j];
     }
-#pragma unroll
-    for (int o = 1; o < LPR; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    sum = row_lanes_sum<LPR>(sum);
     const float remote_lse = rmax + log2_hw(sum) * kLn2;
     const float gate = gscale * (remote_lse - local) + off;
     const float mass = rcp_hw(1.f + exp2_hw(-gate * kLog2e));
