@@ -303,6 +303,7 @@ def test_route_weights_vs_oracle(affine, K):
     idx = torch.randint(0, C, (B, L, Hkv, K), generator=torch.Generator().manual_seed(21)).int()
     idx[0, 3, 1, K // 2:] = -1
     idx[0, 4, 2, :] = -1
+    idx[0, 6, 0, 1] = C + 7       # out of range: masked like -1
     bias = torch.rand(B, C, Hkv, G) + 3.5
     lse = _rand((B, L, Hkv * G), 22) + 5.0
     lse[0, 5, 3] = float("-inf")
