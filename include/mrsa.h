@@ -520,6 +520,18 @@ int mrsa_selected_attention_fused_fwd(const void* q, const void* kv_frags,
                                       void* stream);
 
 /*
+ * Routed-attention lock status.  It has no counterpart in the reference
+ * (whose kernels take no lock); it makes the bounded lock wait of the routed
+ * attention kernels (mrsa_selected_attention_*) observable.  A tile whose
+ * wait for its owners' rows runs out (65536 tries, or MRSA_LOCK_SPIN_LIMIT
+ * when set) adds its terms with LDS float atomics, which is exact only when
+ * no other wave is inside those rows, and counts itself here.  Waits the
+ * current device's queued work, stores the count of such tiles since the
+ * last reset in *count and clears it when `reset` is nonzero.
+ */
+int mrsa_routed_lock_giveups(uint64_t* count, int reset);
+
+/*
  * Global token keep: select_global_token_keep
  * (dream_dllm_hils/token_refinement.py:112-148) without training noise.  In
  * each of `rows` rows of n fp32 scores the min(token_budget, n) largest are

@@ -70,6 +70,12 @@
 
 using namespace mrsa;
 
+// Tiles whose bounded lock wait ran out (spin_limit > 0) since the last
+// read: each added its terms with ds_add_f32, exact only when no holder was
+// inside those rows.  One word per device, read and cleared through
+// mrsa_routed_lock_giveups.
+__device__ unsigned long long g_lock_giveups;
+
 namespace {
 
 constexpr int kWaves = 8;
@@ -696,6 +702,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
         asm volatile("" ::: "memory");
         if (lane == 0) lds_and(lock_addr, ~want);
       } else {
+        if (lane == 0 && a.spin_limit > 0) atomicAdd(&g_lock_giveups, 1ull);
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt) {
           acc[nt] = mfma_bf16_16x16x32(vb[nt][0], Pb[0], zero4());
@@ -1063,4 +1070,24 @@ extern "C" int mrsa_selected_attention_fused_fwd(
   return selected_forward(q, kv_frags, weights, indices, key_valid, token_keep, batch, q_len,
                           kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
                           sm_scale, parts, partial, local_output, local_weight, out, stream);
+}
+
+// Reads the current device's count of routed-attention tiles whose bounded
+// lock wait ran out (waits for the device's queued work first) and clears
+// it when `reset` is nonzero.
+extern "C" int mrsa_routed_lock_giveups(uint64_t* count, int reset) {
+  if (!count) return MRSA_ERR_INVALID_ARGUMENT;
+  if (hipDeviceSynchronize() != hipSuccess) return MRSA_ERR_LAUNCH;
+  unsigned long long v = 0;
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_lock_giveups), sizeof(v), 0,
+                          hipMemcpyDeviceToHost) != hipSuccess)
+    return MRSA_ERR_LAUNCH;
+  *count = (uint64_t)v;
+  if (reset) {
+    const unsigned long long z = 0;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_lock_giveups), &z, sizeof(z), 0,
+                          hipMemcpyHostToDevice) != hipSuccess)
+      return MRSA_ERR_LAUNCH;
+  }
+  return MRSA_OK;
 }

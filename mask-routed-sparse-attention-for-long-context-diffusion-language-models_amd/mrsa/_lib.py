@@ -118,6 +118,7 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
          _I, _F, _I64, _P, _P, _P],
     ),
+    "mrsa_routed_lock_giveups": (_I, [_P, _I]),
     "mrsa_selected_attention_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
     "mrsa_selected_attention_bwd": (
         _I,

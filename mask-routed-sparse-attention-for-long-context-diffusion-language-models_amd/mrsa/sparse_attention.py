@@ -95,6 +95,36 @@ def walk_parts(batch: int, q_len: int, kv_heads: int, kv_len: int, topk: int,
     return max(1, parts)
 
 
+class RoutedLockTimeout(RuntimeError):
+    """Routed-attention tiles ran out of their bounded lock wait; their
+    outputs may have lost additions."""
+
+
+def routed_lock_giveups(reset: bool = True) -> int:
+    """Number of routed-attention tiles on the current device whose bounded
+    lock wait ran out since the last reset (waits for the device's queued
+    work).  Such a tile adds its terms with LDS float atomics, which is exact
+    only when no other wave is inside the same rows."""
+
+    import ctypes
+
+    count = ctypes.c_uint64(0)
+    _lib.check(_lib.call("mrsa_routed_lock_giveups", ctypes.byref(count), 1 if reset else 0),
+               "mrsa_routed_lock_giveups")
+    return int(count.value)
+
+
+def check_routed_locks(reset: bool = True) -> None:
+    """Raise RoutedLockTimeout when any routed-attention tile gave up its lock
+    wait since the last reset."""
+
+    n = routed_lock_giveups(reset)
+    if n:
+        raise RoutedLockTimeout(
+            f"{n} routed-attention tile(s) ran out of the bounded lock wait; their rows may "
+            "have lost additions (MRSA_LOCK_SPIN_LIMIT set too low?)")
+
+
 def selected_attention_launch(
     q: torch.Tensor,
     kv_frags: torch.Tensor,

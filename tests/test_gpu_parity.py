@@ -6,6 +6,7 @@ within max-abs 2e-2 and mean-abs 2e-3 (bf16 in, fp32 accumulate).
 """
 
 import math
+import os
 
 import pytest
 import torch
@@ -717,3 +718,35 @@ def test_route_topk_g7_gumbel_sampling_vs_oracle():
                        ii.clamp(min=0)[:, :, :, None, :].expand(-1, -1, -1, G, -1))
     exp = exp.masked_fill((ii < 0)[:, :, :, None, :], 0.0).reshape(B, L, Hkv * G, K)
     assert torch.equal(selg.cpu(), exp)
+
+
+def test_routed_lock_giveups_are_reported():
+    # The bounded lock wait is forced from the host: with one try per tile,
+    # contended tiles give up and add without the lock (their sums may lose
+    # terms; no fault or hang), and the status word must say so.  With the
+    # default bound the contended shape reports none.
+    _note("routed lock give-ups reported")
+    Lq, K, Hkv, G, D, Lk = 4, 32, 4, 7, 128, 2048
+    q = _rand((1, Lq, Hkv * G, D), 96).bfloat16()
+    k, v = _planted_kv(Lk, Hkv, D, 97)
+    idx = _sorted_routes(Lq, Hkv, K, Lk // 64, 98)
+    w = torch.softmax(_rand((1, Lq, Hkv * G, K), 99), -1).bfloat16()
+    args = (q.to(DEV), mrsa.kv_fragments(k.to(DEV), v.to(DEV)), w.to(DEV), idx.to(DEV),
+            torch.ones(1, Lk, dtype=torch.bool, device=DEV), 64)
+    mrsa.routed_lock_giveups(reset=True)
+    for _ in range(10):
+        selected_attention_launch(*args, parts=1)
+    assert mrsa.routed_lock_giveups(reset=True) == 0
+    old = os.environ.get("MRSA_LOCK_SPIN_LIMIT")
+    os.environ["MRSA_LOCK_SPIN_LIMIT"] = "1"
+    try:
+        for _ in range(10):
+            selected_attention_launch(*args, parts=1)
+        with pytest.raises(mrsa.RoutedLockTimeout):
+            mrsa.check_routed_locks()
+        assert mrsa.routed_lock_giveups(reset=True) == 0  # cleared by the check
+    finally:
+        if old is None:
+            del os.environ["MRSA_LOCK_SPIN_LIMIT"]
+        else:
+            os.environ["MRSA_LOCK_SPIN_LIMIT"] = old
