@@ -71,8 +71,10 @@ def make_inputs(L: int, seed: int, device, dtype):
         v.to(device=device, dtype=dtype)
 
 
-def cpu_baseline(budget_s: float = 20.0):
-    """Oracle route layer at BASELINE configuration 1 on the host CPU."""
+def cpu_baseline(budget_s: float = 30.0):
+    """Oracle route layer at BASELINE configuration 1 on the host CPU: one
+    untimed warmup forward, then the median of 3 timed forwards (fewer only
+    when the budget runs out)."""
 
     import torch
 
@@ -88,6 +90,7 @@ def cpu_baseline(budget_s: float = 20.0):
     scale = torch.ones(HQ)
     runs = []
     t_end = time.perf_counter() + budget_s
+    O.route_layer(q.bfloat16(), k.bfloat16(), v.bfloat16(), q.bfloat16(), scale)  # warmup
     while True:
         t0 = time.perf_counter()
         O.route_layer(q.bfloat16(), k.bfloat16(), v.bfloat16(), q.bfloat16(), scale)
@@ -108,8 +111,8 @@ def cpu_baseline(budget_s: float = 20.0):
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{len(runs)} full route-layer forwards at L=4096 (config 1), fp32 CPU oracle, "
-                  f"median {best:.2f} s; cpu={cpu_model}",
+        "sample": f"1 warmup + {len(runs)} timed full route-layer forwards at L=4096 "
+                  f"(config 1), fp32 CPU oracle, median {best:.2f} s; cpu={cpu_model}",
     }
 
 
@@ -205,13 +208,20 @@ def main() -> int:
 
     sel_us = stages_us["selected_attention"]
     achieved = selected_flops(L_CFG2) / (sel_us * 1e-6) / 1e12
-    traffic = None
+    # HBM bytes per launch cannot be counted from inside the run: they come
+    # from the FETCH_SIZE / WRITE_SIZE counter passes of the committed profile
+    # (rocprofv3 --pmc over this bench), labelled with the commit they were
+    # measured at.
+    traffic, traffic_src = None, None
     tpath = os.path.join(ROOT, "profiles", "pmc_traffic.json")
     if os.path.exists(tpath):
         try:
-            traffic = json.load(open(tpath)).get("selected_attention_bytes_per_launch")
+            tj = json.load(open(tpath))
+            traffic = tj.get("selected_attention_bytes_per_launch")
+            traffic_src = f"{tj.get('source')} @ {tj.get('measured_at', '?')}"
         except (OSError, ValueError):
             traffic = None
+    giveups = mrsa.routed_lock_giveups(reset=True)
 
     line = {
         "metric": METRIC,
@@ -247,14 +257,22 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": achieved / PEAK_BF16_TFLOPS,
             "traffic": traffic,
+            "traffic_source": traffic_src,
             "flops_per_launch": selected_flops(L_CFG2),
             "avg_launch_us": sel_us,
         },
         "stages_us": stages_us,
+        "lock_giveups": giveups,
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
+    if giveups:
+        # a routed-attention tile ran out of its bounded lock wait at the
+        # default bound: replayed exactly, but a sign of a broken lock
+        print(f"bench.py: {giveups} routed-attention tiles ran out of the lock wait",
+              file=sys.stderr)
+        return 1
     return 0
 
 

@@ -349,6 +349,25 @@ int mrsa_kv_fragments_rows(const void* k, const void* v, int64_t batch, int64_t 
                            int64_t count, void* kv_frags, void* stream);
 
 /*
+ * Q fragments: per (batch, KV head, query) the 2 KB register image of the
+ * routed attention's Q^T operand for the query's q_heads / kv_heads head
+ * columns,
+ *   q_frags[((b * kv_heads + h) * seq_len + i) * 1024 + 256 ks + 64 grp + 8 g + e]
+ *     = q[b, i, h * G + g, 32 ks + 8 grp + e]   (g < G; zeros for G <= g < 8),
+ * so that the routed kernel reads the 8 head columns of a query's lane group
+ * as one 128-byte line instead of eight 64-byte pieces.
+ *   q: bf16 [batch, seq_len, q_heads, head_dim], 16-byte aligned
+ *   q_frags (out): bf16 [batch, kv_heads, seq_len, 1024], 16-byte aligned
+ * Limits: head_dim == 128, q_heads / kv_heads <= 8.
+ * No reference counterpart: internal layout step of the routed attention
+ * (mrsa_local_attention_qf_fwd writes the same images as a by-product).
+ */
+int64_t mrsa_q_fragments_bytes(int64_t batch, int64_t seq_len, int64_t kv_heads,
+                               int64_t head_dim);
+int mrsa_q_fragments(const void* q, int64_t batch, int64_t seq_len, int64_t q_heads,
+                     int64_t kv_heads, int64_t head_dim, void* q_frags, void* stream);
+
+/*
  * Bidirectional sliding-window GQA attention with natural-log LSE.
  * Replaces the flash-attn window call behind bidir_local_attention and
  * cached_local_attention (dream_dllm_hils/local_attention.py:67-200):
@@ -371,6 +390,20 @@ int mrsa_local_attention_fwd(const void* q, const void* kv_frags,
                              int64_t kv_heads, int64_t head_dim, int64_t window,
                              int64_t inert_chunk, float sm_scale, void* out, float* lse,
                              void* stream);
+
+/*
+ * mrsa_local_attention_fwd that also writes q_frags (bf16 [batch, kv_heads,
+ * q_len, 1024], 16-byte aligned), exactly what mrsa_q_fragments writes for
+ * q, from the Q operands its waves load anyway.  No reference counterpart: it
+ * serves the route-layer composition (the routed attention then reads Q as
+ * whole cache lines).  Limits as mrsa_local_attention_fwd.
+ */
+int mrsa_local_attention_qf_fwd(const void* q, const void* kv_frags,
+                                const uint8_t* key_valid, const int64_t* query_positions,
+                                int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
+                                int64_t kv_heads, int64_t head_dim, int64_t window,
+                                int64_t inert_chunk, float sm_scale, void* q_frags, void* out,
+                                float* lse, void* stream);
 
 /*
  * The same window attention for short query blocks (cached_local_attention,
@@ -520,16 +553,42 @@ int mrsa_selected_attention_fused_fwd(const void* q, const void* kv_frags,
                                       void* stream);
 
 /*
+ * mrsa_selected_attention_fused_fwd reading the queries from q_frags
+ * (mrsa_q_fragments(q) or the by-product of mrsa_local_attention_qf_fwd)
+ * instead of q: same result.  No reference counterpart; it serves the
+ * route-layer composition.  q is still passed (shape checks only).
+ */
+int mrsa_selected_attention_fused_qf_fwd(const void* q, const void* q_frags,
+                                         const void* kv_frags, const void* weights,
+                                         const int32_t* indices, const uint8_t* key_valid,
+                                         const int8_t* token_keep, const void* local_output,
+                                         const void* local_weight, int64_t batch, int64_t q_len,
+                                         int64_t kv_len, int64_t q_heads, int64_t kv_heads,
+                                         int64_t head_dim, int64_t topk, int64_t chunk_size,
+                                         int mask_last_token, float sm_scale, int64_t parts,
+                                         float* partial, void* out, void* stream);
+
+/*
  * Routed-attention lock status.  It has no counterpart in the reference
  * (whose kernels take no lock); it makes the bounded lock wait of the routed
  * attention kernels (mrsa_selected_attention_*) observable.  A tile whose
- * wait for its owners' rows runs out (65536 tries, or MRSA_LOCK_SPIN_LIMIT
- * when set) adds its terms with LDS float atomics, which is exact only when
- * no other wave is inside those rows, and counts itself here.  Waits the
- * current device's queued work, stores the count of such tiles since the
- * last reset in *count and clears it when `reset` is nonzero.
+ * wait for its owners' rows runs out (mrsa_set_routed_lock_spin_limit tries,
+ * 65536 by default) is deferred: the workgroup replays it onto the rows after
+ * its walk, when no wave holds them, so the output stays exact.  The count
+ * only reports that slow path.  It is one word per device, shared by every
+ * stream and caller: reading it waits for all of the device's queued work
+ * (hipDeviceSynchronize, so never under graph capture), stores the count
+ * since the last reset in *count and clears it when `reset` is nonzero.
  */
 int mrsa_routed_lock_giveups(uint64_t* count, int reset);
+
+/*
+ * Test hook: the lock tries of the routed-attention kernels before a tile is
+ * deferred (process-wide; read at each launch, so a captured graph keeps the
+ * value of its capture).  limit <= 0 defers every tile.  Default 65536.
+ * No reference counterpart.
+ */
+int mrsa_set_routed_lock_spin_limit(int limit);
 
 /*
  * Global token keep: select_global_token_keep

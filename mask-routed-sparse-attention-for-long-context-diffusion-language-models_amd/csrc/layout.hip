@@ -2,6 +2,8 @@
 // attention kernels read.
 #include "mrsa_device.h"
 
+#include <algorithm>
+
 using namespace mrsa;
 
 namespace {
@@ -127,6 +129,32 @@ __global__ void __launch_bounds__(128)
   dst[frag_v_index(r, d)] = v[src];
 }
 
+// Q fragments: per (batch, KV head, query) the 2 KB register image of the
+// routed attention's Q^T operand for the query's G head columns --
+//   qf[((b Hkv + h) L + i) 1024 + 256 ks + 64 grp + 8 g + e]
+//     = q[b, i, h G + g, 32 ks + 8 grp + e]   (g < G; zeros for g in [G, 8))
+// -- so the lanes of one lane group (grp) read the 8 head columns of a query
+// as one 128-byte line.  One thread per 16-byte block, stores coalesced.
+__global__ void __launch_bounds__(256)
+    q_fragments_kernel(const uint16_t* __restrict__ q, int64_t L, int Hq, int Hkv, int G,
+                       int64_t nblocks, uint16_t* __restrict__ qf) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < nblocks; e += stride) {
+    const int u = (int)(e & 127);
+    const int64_t img = e >> 7;
+    const int64_t i = img % L;
+    const int64_t bh = img / L;
+    const int h = (int)(bh % Hkv);
+    const int64_t b = bh / Hkv;
+    const int ks = u >> 5, grp = (u >> 3) & 3, g = u & 7;
+    u32x4_t x = {0u, 0u, 0u, 0u};
+    if (g < G)
+      x = *reinterpret_cast<const u32x4_t*>(q + ((b * L + i) * Hq + (int64_t)h * G + g) * 128 +
+                                            32 * ks + 8 * grp);
+    *reinterpret_cast<u32x4_t*>(qf + e * 8) = x;
+  }
+}
+
 }  // namespace
 
 extern "C" int mrsa_remote_drop_mask(const uint8_t* valid_mask, const uint8_t* allowed_mask,
@@ -203,5 +231,30 @@ extern "C" int mrsa_kv_fragments_rows(const void* k, const void* v, int64_t batc
                      dim3((unsigned)count, (unsigned)kv_heads, (unsigned)batch), dim3(128), 0,
                      (hipStream_t)stream, (const uint16_t*)k, (const uint16_t*)v, seq_len,
                      kv_heads, NT, positions, (uint16_t*)kv_frags);
+  return mrsa_launch_status();
+}
+
+extern "C" int64_t mrsa_q_fragments_bytes(int64_t batch, int64_t seq_len, int64_t kv_heads,
+                                          int64_t head_dim) {
+  if (batch < 0 || seq_len < 0 || kv_heads < 0 || head_dim != 128) return -1;
+  return batch * kv_heads * seq_len * 2048;
+}
+
+extern "C" int mrsa_q_fragments(const void* q, int64_t batch, int64_t seq_len, int64_t q_heads,
+                                int64_t kv_heads, int64_t head_dim, void* q_frags,
+                                void* stream) {
+  if (batch < 0 || seq_len < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 ||
+      q_heads % kv_heads != 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (head_dim != 128 || q_heads / kv_heads > 8) return MRSA_ERR_UNSUPPORTED;
+  if (batch == 0 || seq_len == 0) return MRSA_OK;
+  if (!q || !q_frags || ((uintptr_t)q | (uintptr_t)q_frags) % 16 != 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (q_heads > 65535) return MRSA_ERR_UNSUPPORTED;
+  const int64_t nblocks = batch * kv_heads * seq_len * 128;
+  const int64_t grid = std::min<int64_t>((nblocks + 255) / 256, 8192);
+  hipLaunchKernelGGL(q_fragments_kernel, dim3((unsigned)grid), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)q, seq_len, (int)q_heads,
+                     (int)kv_heads, (int)(q_heads / kv_heads), nblocks, (uint16_t*)q_frags);
   return mrsa_launch_status();
 }

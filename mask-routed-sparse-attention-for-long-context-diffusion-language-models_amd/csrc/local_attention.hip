@@ -82,6 +82,10 @@ struct LocalArgs {
   int parts;
   float* part_o;
   float* part_ml;
+  // Optional by-product: the Q operand images of the routed attention,
+  // [B, Hkv, Lq, 1024] bf16 (mrsa_q_fragments), written from the Q^T
+  // registers every wave loads anyway.
+  uint16_t* qf;
 };
 
 // Inert-key bits (bit s = key 64 kt + s carries zero K / V) of one key tile:
@@ -165,6 +169,14 @@ local_attn_kernel(LocalArgs a) {
     if (qok)
       Qb[j] = *reinterpret_cast<const u32x4_t*>(
           a.q + ((b * a.Lq + qi) * a.Hq + h * G + gg) * 128 + 32 * j + 8 * grp);
+  }
+  // Q fragments: lane (grp, col)'s k-step j image bytes of its column --
+  // query qi, head gg -- sit at 512 j + 128 grp + 16 gg of the query's 2 KB
+  // image (padding heads hold zeros).
+  if (a.qf && part == 0 && qi < a.Lq) {
+    uint16_t* dst = a.qf + ((b * a.Hkv + h) * a.Lq + qi) * 1024 + 64 * grp + 8 * gg;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(dst + 256 * j) = Qb[j];
   }
   __syncthreads();
   const int64_t plo = pos_range[0], phi = pos_range[1];
@@ -450,7 +462,7 @@ int local_attention(const void* q, const void* kv_frags, const uint8_t* key_vali
                     const int64_t* query_positions, int64_t batch, int64_t q_len, int64_t kv_len,
                     int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t window,
                     int64_t inert_chunk, float sm_scale, int64_t parts, void* workspace,
-                    void* out, float* lse, void* stream) {
+                    void* out, float* lse, void* stream, void* q_frags = nullptr) {
   if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 ||
       q_heads % kv_heads != 0 || head_dim <= 0 || window < 0 || inert_chunk < 0 ||
       !(sm_scale > 0.f) || sm_scale == __builtin_inff())
@@ -458,7 +470,8 @@ int local_attention(const void* q, const void* kv_frags, const uint8_t* key_vali
   if (batch == 0 || q_len == 0) return MRSA_OK;
   if (kv_len == 0 || !q || !kv_frags || !out || !lse) return MRSA_ERR_INVALID_ARGUMENT;
   if (head_dim != 128) return MRSA_ERR_UNSUPPORTED;
-  if (((uintptr_t)q | (uintptr_t)kv_frags) % 16 != 0 || (uintptr_t)out % 8 != 0)
+  if (((uintptr_t)q | (uintptr_t)kv_frags | (uintptr_t)q_frags) % 16 != 0 ||
+      (uintptr_t)out % 8 != 0)
     return MRSA_ERR_INVALID_ARGUMENT;
   // a KV head's fragments are addressed with 32-bit byte offsets
   if ((kv_len + 63) / 64 >= 131072) return MRSA_ERR_UNSUPPORTED;
@@ -484,6 +497,8 @@ int local_attention(const void* q, const void* kv_frags, const uint8_t* key_vali
   a.parts = (int)parts;
   a.part_o = (float*)workspace;
   a.part_ml = parts > 1 ? (float*)workspace + parts * batch * q_len * q_heads * 128 : nullptr;
+  a.qf = (uint16_t*)q_frags;
+  if (q_frags && G > 8) return MRSA_ERR_UNSUPPORTED;
   hipStream_t s = (hipStream_t)stream;
   switch (G) {
     case 1: return launch_local<1>(a, s);
@@ -535,4 +550,17 @@ extern "C" int mrsa_local_attention_split_fwd(const void* q, const void* kv_frag
   return local_attention(q, kv_frags, key_valid, query_positions, batch, q_len, kv_len,
                          q_heads, kv_heads, head_dim, window, inert_chunk, sm_scale, parts,
                          parts > 1 ? workspace : nullptr, out, lse, stream);
+}
+
+extern "C" int mrsa_local_attention_qf_fwd(const void* q, const void* kv_frags,
+                                           const uint8_t* key_valid,
+                                           const int64_t* query_positions, int64_t batch,
+                                           int64_t q_len, int64_t kv_len, int64_t q_heads,
+                                           int64_t kv_heads, int64_t head_dim, int64_t window,
+                                           int64_t inert_chunk, float sm_scale, void* q_frags,
+                                           void* out, float* lse, void* stream) {
+  if (batch > 0 && q_len > 0 && !q_frags) return MRSA_ERR_INVALID_ARGUMENT;
+  return local_attention(q, kv_frags, key_valid, query_positions, batch, q_len, kv_len,
+                         q_heads, kv_heads, head_dim, window, inert_chunk, sm_scale, 1, nullptr,
+                         out, lse, stream, q_frags);
 }

@@ -49,9 +49,12 @@
 // order, so its writes land before its release and after another wave's
 // acquire.  The order of the fp32 additions into a row depends on timing, so
 // the last bit of an output can differ between runs.  Past `spin_limit`
-// tries (about 6 ms; a guard that ends the kernel, never reached while every
-// holder finishes its tile) the wave gives its bits back and adds the tile
-// with ds_add_f32, which is exact only when no holder is inside those rows.
+// tries (about 6 ms; a guard that ends the wait, never reached while every
+// holder finishes its tile) the wave gives its bits back and defers the tile:
+// it appends (step, tile) to a per-workgroup queue and moves on.  After the
+// walk's barrier, when no wave holds a row, wave 0 replays the queued tiles
+// one by one (chunk, Q and softmax recomputed) onto the rows, so a deferred
+// tile costs time but never terms.
 //
 // LDS output rows: row (q, g) of slot q at (8 q + g) * 128 floats; the
 // 16-byte block b of dims 4 b .. 4 b + 3 sits at block b ^ g, so the eight
@@ -70,10 +73,10 @@
 
 using namespace mrsa;
 
-// Tiles whose bounded lock wait ran out (spin_limit > 0) since the last
-// read: each added its terms with ds_add_f32, exact only when no holder was
-// inside those rows.  One word per device, read and cleared through
-// mrsa_routed_lock_giveups.
+// Tiles whose bounded lock wait ran out since the last read (each was
+// deferred and replayed after the walk: the output stays exact; the count
+// only reports the slow path).  One word per device, shared by every stream,
+// read and cleared through mrsa_routed_lock_giveups.
 __device__ unsigned long long g_lock_giveups;
 
 namespace {
@@ -85,10 +88,11 @@ constexpr int kMaxTQ = 32;                 // owner sets and the lock are 32-bit
 constexpr int kMaxItems = 1024;            // TQ * K per workgroup
 constexpr int64_t kMaxParts = 64;          // walk split limit
 constexpr size_t kLdsBytes = 160 * 1024;
-constexpr int kDefaultSpinLimit = 65536;   // lock tries before the atomic path
+constexpr int kDefaultSpinLimit = 65536;   // lock tries before a tile is deferred
 
 struct RaArgs {
   const uint16_t* q;
+  const uint16_t* qf;        // [B, Hkv, Lq, 1024] Q operand images (mrsa_q_fragments) or null
   const uint16_t* kvf;       // [B, Hkv, Ck, 16384] K / V fragments
   const uint16_t* w;
   const int32_t* idx;
@@ -109,7 +113,7 @@ struct RaArgs {
   int tq;                    // queries per tile
   int64_t ntiles;            // ceil(Lq / tq)
   int64_t units;             // B * Hkv * parts * ntiles workgroups of work
-  int spin_limit;            // lock tries before a tile takes the atomic path
+  int spin_limit;            // lock tries before a tile is deferred (<= 0: every tile)
 };
 
 __host__ __device__ inline size_t al16(size_t x) { return (x + 15) & ~(size_t)15; }
@@ -122,7 +126,7 @@ __host__ __device__ inline size_t al16(size_t x) { return (x + 15) & ~(size_t)15
 struct RaLayout {
   size_t o, o_bytes;
   size_t raw, qlen, qflag, wst, omask, step_of, scratch_end;
-  size_t rec, iq, islot, iw, ikeep, misc, total;
+  size_t rec, iq, islot, iw, ikeep, dq, misc, total;
   int items, cap;
 };
 
@@ -147,6 +151,7 @@ __host__ __device__ inline RaLayout ra_layout(int tq, int G, int K, int64_t Ck, 
   l.islot = o;   o = al16(o + (size_t)l.items);
   l.iw = o;      o = al16(o + (token ? 0 : (size_t)l.items * 8 * 2));
   l.ikeep = o;   o = al16(o + (keep ? (size_t)l.items * 8 : 0));
+  l.dq = o;      o = al16(o + (token ? 0 : (size_t)l.items * 2));
   l.misc = o;    o = al16(o + (size_t)(2 * kWaves + 8 + 64) * 4);
   l.total = o;
   return l;
@@ -232,11 +237,15 @@ __device__ __forceinline__ void load_v(u32x4_t (&vb)[8][2], __amdgpu_buffer_rsrc
       vb[nt][ks] = bload(r, lo + 1024u * (i & 3), cb + 16384u + 4096u * (i >> 2));
     }
 }
-// Q^T operand of one tile column: head row bytes 64 ks + 16 grp from `off`
-// (kZeroOffset for padding columns).
-__device__ __forceinline__ void load_q(u32x4_t (&Qb)[4], __amdgpu_buffer_rsrc_t r, uint32_t off) {
+// Q^T operand of one tile column: k-step ks at `off` + ks * `kstep` bytes
+// (kZeroOffset for padding columns).  From q rows: off = the head row + 16
+// grp, kstep 64.  From Q fragments: off = the query's image + 128 grp + 16
+// head, kstep 512, so the 8 head columns of one lane group read one whole
+// 128-byte line.
+__device__ __forceinline__ void load_q(u32x4_t (&Qb)[4], __amdgpu_buffer_rsrc_t r, uint32_t off,
+                                       uint32_t kstep) {
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) Qb[ks] = bload(r, off + 64u * ks, 0u);
+  for (int ks = 0; ks < 4; ++ks) Qb[ks] = bload(r, off, kstep * ks);
 }
 
 template <bool TOKEN, bool KEEP>
@@ -283,6 +292,8 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   int32_t* misc = reinterpret_cast<int32_t*>(smem + L.misc);
   uint32_t* lock = reinterpret_cast<uint32_t*>(misc + 2 * kWaves + 1);
   uint32_t* claim = reinterpret_cast<uint32_t*>(misc + 2 * kWaves + 2);  // steps claimed
+  uint32_t* dcount = reinterpret_cast<uint32_t*>(misc + 2 * kWaves + 4);  // deferred tiles
+  uint16_t* dq = reinterpret_cast<uint16_t*>(smem + L.dq);         // [items] step << 4 | tile
   uint32_t* idle_or = reinterpret_cast<uint32_t*>(misc + 2 * kWaves + 8);  // [64], never read
 
   // ---- prologue: the walk of this tile ----------------------------------
@@ -299,6 +310,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   if (tid == 0) {
     *lock = 0u;
     *claim = 0u;
+    *dcount = 0u;
   }
   for (int64_t c = tid; c < Ck; c += kThreads) omask[c] = 0u;
   if constexpr (!TOKEN) {
@@ -468,11 +480,20 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   const __amdgpu_buffer_rsrc_t frs =
       make_rsrc(a.kvf + (b * a.Hkv + h) * Ck * kFragElems, (uint32_t)Ck * kFragBytes);
   const uint32_t flo = 16u * lane;
-  // Q rows of this tile: query qi's head gcol at byte qi * qrow + 256 gcol.
-  const uint32_t qrow = (uint32_t)a.Hq * 256u;
+  // Q of this tile.  From q rows: query qi's head gcol at byte qi * qrow +
+  // 256 gcol; the range ends at the tile's last real row (head G - 1 of
+  // query nq - 1): with a head offset h G the base is not row-aligned, so
+  // nq * qrow would reach past the tensor at the sequence end.  From Q
+  // fragments: query qi's 2 KB image at qi * 2048, lane bytes 128 grp + 16
+  // gcol + 512 ks.
+  const bool qfrag = a.qf != nullptr;
+  const uint32_t qrow = qfrag ? 2048u : (uint32_t)a.Hq * 256u;
+  const uint32_t qks = qfrag ? 512u : 64u;
   const __amdgpu_buffer_rsrc_t qrs =
-      make_rsrc(a.q + ((b * a.Lq + q0) * a.Hq + (int64_t)h * G) * 128, (uint32_t)nq * qrow);
-  const uint32_t qcol = 256u * gcol + 16u * grp;
+      qfrag ? make_rsrc(a.qf + ((b * a.Hkv + h) * a.Lq + q0) * 1024, (uint32_t)nq * 2048u)
+            : make_rsrc(a.q + ((b * a.Lq + q0) * a.Hq + (int64_t)h * G) * 128,
+                        (uint32_t)(nq - 1) * qrow + (uint32_t)G * 256u);
+  const uint32_t qcol = qfrag ? 128u * grp + 16u * gcol : 256u * gcol + 16u * grp;
   // Q offset of this lane's column in a tile whose owner slots are `own2`
   // (slot of owner 0 | slot of owner 1 << 8).
   auto qoff = [&](uint32_t own2, bool valid) {
@@ -500,6 +521,87 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   bool more = false;
   uint64_t msk = 0, mskn = 0;
   u32x4_t kb[4][4], vb[8][2], Qb[4];
+  // P^T operand of a tile from its S^T accumulators: excluded keys (the
+  // chunk's `mskc`, bit k = key k; keys a keep row drops) -> -inf, the
+  // chunk's softmax times the column's routing weight `wv`, rounded to bf16.
+  // Row j of P is this lane's column; reduction index 8 grp + e of k-step ks
+  // is key 32 ks + 16 (e >> 2) + 4 grp + (e & 3), the tiled-V order.
+  auto tile_P = [&](f32x4_t (&S)[4], uint64_t mskc, float wv, uint64_t kept,
+                    u32x4_t (&Pb)[2]) {
+    const uint64_t msh = mskc >> (4 * grp);  // bit 16 mt + r: key 16 mt + 4 grp + r
+    // Key 63 (the landmark slot, the usual only exclusion) is S[3][3] of
+    // lane group 3; other excluded keys take the per-bit path.
+    S[3][3] = set_where(S[3][3], (mskc >> 63) ? 0xFFFF000000000000ull : 0ull, ninf_v);
+    if (mskc & ~(1ull << 63)) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          S[mt][r] = set_where(
+              S[mt][r], __builtin_amdgcn_ballot_w64((msh >> (16 * mt + r)) & 1ull), ninf_v);
+    }
+    if constexpr (KEEP) {
+      const uint64_t kbits = kept >> (4 * grp);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          S[mt][r] = set_where(
+              S[mt][r], __builtin_amdgcn_ballot_w64(!((kbits >> (16 * mt + r)) & 1ull)), ninf_v);
+    }
+    // P = bf16(p w / sum p) does not depend on the stabiliser of p.  Without
+    // one, p = 2^(s c) and sum p stay in fp32's range for any |s c| well
+    // below 64: the per-column max (and its cross-lane reduction) is
+    // skipped.  When some column's sum leaves [2^-64, 2^64] -- extreme
+    // logits, or no key left (sum 0) -- the wave takes the max-stabilised
+    // form, which handles both.
+    f32x4_t E[4];
+    auto exp_sum = [&](float mb) {
+      float ps[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) E[mt][r] = exp2_hw(__builtin_fmaf(S[mt][r], c2, -mb));
+        ps[mt] = (E[mt][0] + E[mt][1]) + (E[mt][2] + E[mt][3]);
+      }
+      return across4_sum((ps[0] + ps[1]) + (ps[2] + ps[3]));
+    };
+    float sum = 0.f;
+    bool stabilise = KEEP;  // keep rows often drop whole chunks (sum 0)
+    if constexpr (!KEEP) {
+      sum = exp_sum(0.f);
+      stabilise = !__all(sum >= 0x1p-64f && sum <= 0x1p64f);
+    }
+    if (stabilise) {
+      const float mx = across4_max(max16_raw(S));
+      sum = exp_sum(mx == neg_inf() ? 0.f : mx * c2);
+    }
+    const float f = sum > 0.f ? wv * rcp_hw(sum) : 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      Pb[ks][0] = pack_bf16x2(E[2 * ks][0] * f, E[2 * ks][1] * f);
+      Pb[ks][1] = pack_bf16x2(E[2 * ks][2] * f, E[2 * ks][3] * f);
+      Pb[ks][2] = pack_bf16x2(E[2 * ks + 1][0] * f, E[2 * ks + 1][1] * f);
+      Pb[ks][3] = pack_bf16x2(E[2 * ks + 1][2] * f, E[2 * ks + 1][3] * f);
+    }
+  };
+  // O^T rows += V^T . P^T: this lane's row blocks (pe: even nt, po: odd nt)
+  // read into the accumulators, the 16 products, written back.
+  auto add_rows = [&](float* pe, float* po, const u32x4_t (&Pb)[2]) {
+    f32x4_t acc[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+      acc[nt] = *reinterpret_cast<const f32x4_t*>((nt & 1) ? po + 16 * (nt - 1) : pe + 16 * nt);
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      acc[nt] = mfma_bf16_16x16x32(vb[nt][0], Pb[0], acc[nt]);
+      acc[nt] = mfma_bf16_16x16x32(vb[nt][1], Pb[1], acc[nt]);
+    }
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+      *reinterpret_cast<f32x4_t*>((nt & 1) ? po + 16 * (nt - 1) : pe + 16 * nt) = acc[nt];
+  };
+
   auto decode_next = [&](const u32x4_t r) {
     cn = (int64_t)(r[0] & 0xffffffu);
     nn = (int)(r[0] >> 24);
@@ -543,10 +645,10 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     if constexpr (!LAST) {
       asm volatile("" : "+v"(nx_a), "+v"(nx_b) : "v"(S[3][3]));  // read after the QK issue
       nown2 = (uint32_t)__builtin_amdgcn_readfirstlane(nx_a | (nx_b << 8));
-      load_q(Qb, qrs, qoff(nown2, o + 2 < n && gcol < G));
+      load_q(Qb, qrs, qoff(nown2, o + 2 < n && gcol < G), qks);
     } else {
       nown2 = own2n;
-      load_q(Qb, qrs, qoff(nown2, more && own < nn && gcol < G));
+      load_q(Qb, qrs, qoff(nown2, more && own < nn && gcol < G), qks);
       load_k(kb, frs, flo, (uint32_t)cn * kFragBytes);
     }
     const uint64_t msh = msk >> (4 * grp);  // bit 16 mt + r: key 16 mt + 4 grp + r
@@ -589,67 +691,8 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
         }
       }
     } else {
-      // Excluded keys -> -inf in place.  Key 63 (the landmark slot, the
-      // usual only exclusion) is S[3][3] of lane group 3; other excluded
-      // keys take the per-bit path.
-      S[3][3] = set_where(S[3][3], (msk >> 63) ? 0xFFFF000000000000ull : 0ull, ninf_v);
-      if (msk & ~(1ull << 63)) {
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            S[mt][r] = set_where(
-                S[mt][r], __builtin_amdgcn_ballot_w64((msh >> (16 * mt + r)) & 1ull), ninf_v);
-      }
-      if constexpr (KEEP) {
-        // keys the column's keep row drops -> -inf
-        const uint64_t kbits = (o < n ? it_keep[ii] : ~0ull) >> (4 * grp);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            S[mt][r] = set_where(
-                S[mt][r], __builtin_amdgcn_ballot_w64(!((kbits >> (16 * mt + r)) & 1ull)),
-                ninf_v);
-      }
-      // The chunk's softmax P = bf16(p w / sum p) does not depend on the
-      // stabiliser of p.  Without one, p = 2^(s c) and sum p stay in fp32's
-      // range for any |s c| well below 64: the per-column max (and its
-      // cross-lane reduction) is skipped.  When some column's sum leaves
-      // [2^-64, 2^64] -- extreme logits, or no key left (sum 0) -- the wave
-      // takes the max-stabilised form, which handles both.
-      f32x4_t E[4];
-      auto exp_sum = [&](float mb) {
-        float ps[4];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) E[mt][r] = exp2_hw(__builtin_fmaf(S[mt][r], c2, -mb));
-          ps[mt] = (E[mt][0] + E[mt][1]) + (E[mt][2] + E[mt][3]);
-        }
-        return across4_sum((ps[0] + ps[1]) + (ps[2] + ps[3]));
-      };
-      float sum = 0.f;
-      bool stabilise = KEEP;  // keep rows often drop whole chunks (sum 0)
-      if constexpr (!KEEP) {
-        sum = exp_sum(0.f);
-        stabilise = !__all(sum >= 0x1p-64f && sum <= 0x1p64f);
-      }
-      if (stabilise) {
-        const float mx = across4_max(max16_raw(S));
-        sum = exp_sum(mx == neg_inf() ? 0.f : mx * c2);
-      }
-      const float f = sum > 0.f ? wv * rcp_hw(sum) : 0.f;
-      // P (row j = this lane's column): reduction index 8 grp + e of k-step
-      // ks is key 32 ks + 16 (e >> 2) + 4 grp + (e & 3), the tiled-V order.
       u32x4_t Pb[2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        Pb[ks][0] = pack_bf16x2(E[2 * ks][0] * f, E[2 * ks][1] * f);
-        Pb[ks][1] = pack_bf16x2(E[2 * ks][2] * f, E[2 * ks][3] * f);
-        Pb[ks][2] = pack_bf16x2(E[2 * ks + 1][0] * f, E[2 * ks + 1][1] * f);
-        Pb[ks][3] = pack_bf16x2(E[2 * ks + 1][2] * f, E[2 * ks + 1][3] * f);
-      }
+      tile_P(S, msk, wv, KEEP && o < n ? it_keep[ii] : ~0ull, Pb);
       // Add the tile into its owners' rows under the lock: the rows are read
       // into the accumulators and O^T_tile = V^T . P^T is added onto them
       // (lane (grp, j): column j, dims 16 nt + 4 grp + r).  A missing second
@@ -657,8 +700,6 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       // rows, with P = 0.
       const int qb = hb ? qb1 : sinkq;
       float* const srow = O + (own ? qb : qa) * 1024;
-      float* const pe = srow + lane_e;
-      float* const po = srow + lane_o;
       asm volatile("" : "+v"(first_try) : "v"(Pb[1][3]));  // read after the softmax
       const uint32_t seen = __builtin_amdgcn_readfirstlane(first_try);
       bool locked = a.spin_limit > 0 && (seen & want) == 0u;
@@ -682,42 +723,58 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
         locked = need == 0u;
         if (!locked && lane == 0) lds_and(lock_addr, ~(want & ~need));  // give back what was taken
       }
-      f32x4_t acc[8];
       // The lock word is read back above with lgkmcnt(0): the row reads
       // below are issued after it.
       if (locked) {
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt)
-          acc[nt] = *reinterpret_cast<const f32x4_t*>((nt & 1) ? po + 16 * (nt - 1) : pe + 16 * nt);
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) {
-          acc[nt] = mfma_bf16_16x16x32(vb[nt][0], Pb[0], acc[nt]);
-          acc[nt] = mfma_bf16_16x16x32(vb[nt][1], Pb[1], acc[nt]);
-        }
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt)
-          *reinterpret_cast<f32x4_t*>((nt & 1) ? po + 16 * (nt - 1) : pe + 16 * nt) = acc[nt];
+        add_rows(srow + lane_e, srow + lane_o, Pb);
         // The row writes are issued before the release and the LDS
         // completes one wave's operations in order.
         asm volatile("" ::: "memory");
         if (lane == 0) lds_and(lock_addr, ~want);
-      } else {
-        if (lane == 0 && a.spin_limit > 0) atomicAdd(&g_lock_giveups, 1ull);
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) {
-          acc[nt] = mfma_bf16_16x16x32(vb[nt][0], Pb[0], zero4());
-          acc[nt] = mfma_bf16_16x16x32(vb[nt][1], Pb[1], acc[nt]);
-        }
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            __hip_atomic_fetch_add(((nt & 1) ? po + 16 * (nt - 1) : pe + 16 * nt) + r, acc[nt][r],
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      } else if (lane == 0) {
+        // The bounded wait ran out: queue the tile for the replay after the
+        // walk (the queue holds every tile of the workgroup at most once).
+        const uint32_t slot = __hip_atomic_fetch_add(dcount, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_WORKGROUP);
+        dq[slot] = (uint16_t)(((uint32_t)st << 4) | (uint32_t)t);
+        atomicAdd(&g_lock_giveups, 1ull);
       }
       if constexpr (LAST) load_v(vb, frs, flo, (uint32_t)cn * kFragBytes);
     }
     own2 = nown2;
+  };
+
+  // A deferred tile (queue entry step << 4 | tile), recomputed from its
+  // chunk and added onto its owners' rows without the lock: it runs after
+  // the walk's barrier, on wave 0 alone.
+  auto replay_tile = [&](uint32_t entry) {
+    const u32x4_t r = s_rec[entry >> 4];
+    const int t = (int)(entry & 15u);
+    const int64_t rc = (int64_t)__builtin_amdgcn_readfirstlane(r[0] & 0xffffffu);
+    const int rn = __builtin_amdgcn_readfirstlane(r[0] >> 24);
+    const int ri0 = __builtin_amdgcn_readfirstlane(r[1] & 0xffffu);
+    const uint64_t rmsk = uniform64(((uint64_t)r[3] << 32) | r[2]);
+    const int o = 2 * t + own;
+    const bool hb = 2 * t + 1 < rn;
+    const int qa = __builtin_amdgcn_readfirstlane(it_q[ri0 + 2 * t]);
+    const int qb = hb ? __builtin_amdgcn_readfirstlane(it_q[ri0 + 2 * t + 1]) : sinkq;
+    const int ii = ri0 + (o < rn ? o : rn - 1);
+    const bool cvalid = o < rn && gcol < G;
+    const float wv = cvalid ? bf16_to_f32(it_w[ii * 8 + gcol]) : 0.f;
+    load_q(Qb, qrs, qoff((uint32_t)qa | ((uint32_t)(hb ? qb : 0) << 8), cvalid), qks);
+    load_k(kb, frs, flo, (uint32_t)rc * kFragBytes);
+    load_v(vb, frs, flo, (uint32_t)rc * kFragBytes);
+    f32x4_t S[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      S[mt] = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) S[mt] = mfma_bf16_16x16x32(kb[mt][ks], Qb[ks], S[mt]);
+    }
+    u32x4_t Pb[2];
+    tile_P(S, rmsk, wv, KEEP && o < rn ? it_keep[ii] : ~0ull, Pb);
+    float* const srow = O + (own ? qb : qa) * 1024;
+    add_rows(srow + lane_e, srow + lane_o, Pb);
   };
 
   if (st < st_hi) {
@@ -732,7 +789,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     more = nst < st_hi;
     u32x4_t rn = s_rec[more ? nst : st];
     // the order of the prefetches at a step's end: Q, K, then V
-    load_q(Qb, qrs, qoff(own2, own < n && gcol < G));
+    load_q(Qb, qrs, qoff(own2, own < n && gcol < G), qks);
     load_k(kb, frs, flo, (uint32_t)c * kFragBytes);
     if constexpr (!TOKEN) load_v(vb, frs, flo, (uint32_t)c * kFragBytes);
     while (true) {
@@ -772,6 +829,14 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   // ---- epilogue -----------------------------------------------------------
   if constexpr (!TOKEN) {
     __syncthreads();
+    // Deferred tiles, replayed while no wave is inside a row (every other
+    // wave waits at the barrier below).
+    const uint32_t nd = *dcount;
+    if (nd > 0u) {
+      if (wave == 0)
+        for (uint32_t e = 0; e < nd; ++e) replay_tile(dq[e]);
+      __syncthreads();
+    }
     // Work item e: output row rho = e / 16 (query rho / G, head rho % G),
     // dims 8 u .. 8 u + 7 (u = e % 16), LDS blocks 2 u and 2 u + 1 stored at
     // block ^ g.  A thread has at most kEpi items; with the output fusion
@@ -874,6 +939,9 @@ __global__ void __launch_bounds__(256) fill_neg_inf(float* p, int64_t n) {
     p[e] = neg_inf();
 }
 
+// Lock tries before a tile is deferred (mrsa_set_routed_lock_spin_limit).
+int g_spin_limit = kDefaultSpinLimit;
+
 // Largest tile (<= 32 queries, <= 1024 items) whose LDS layout fits, 0 if none.
 int pick_tile(int G, int K, int64_t Ck, bool token, bool keep) {
   for (int tq = std::min(kMaxTQ, kMaxItems / K); tq >= 4; tq -= 4) {
@@ -893,11 +961,7 @@ int launch_routed(RaArgs& a, hipStream_t s) {
   const int64_t grid = (a.units + 7) / 8 * 8;
   if (grid > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
   const RaLayout l = ra_layout(tq, a.G, a.K, a.Ck, TOKEN, KEEP);
-  // MRSA_LOCK_SPIN_LIMIT (tests): lock tries before a tile takes the atomic
-  // path.  0 sends every tile there (exact: no wave then takes the lock);
-  // a small positive value can mix the two paths on one row.
-  const char* env = std::getenv("MRSA_LOCK_SPIN_LIMIT");
-  a.spin_limit = env ? std::max(0, std::atoi(env)) : kDefaultSpinLimit;
+  a.spin_limit = g_spin_limit;
   auto kern = routed_attn_kernel<TOKEN, KEEP>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)l.total) != hipSuccess)
@@ -930,6 +994,7 @@ RaArgs base_args(const void* q, const void* kv_frags, const void* weights,
                  int mask_last_token, float sm_scale) {
   RaArgs a;
   a.q = (const uint16_t*)q;
+  a.qf = nullptr;
   a.kvf = (const uint16_t*)kv_frags;
   a.w = (const uint16_t*)weights;
   a.idx = indices;
@@ -967,7 +1032,8 @@ int selected_forward(const void* q, const void* kv_frags, const void* weights,
                      int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
                      int64_t kv_heads, int64_t head_dim, int64_t topk, int64_t chunk_size,
                      int mask_last_token, float sm_scale, int64_t parts, float* partial,
-                     const void* fuse_local, const void* fuse_w, void* out, void* stream) {
+                     const void* fuse_local, const void* fuse_w, void* out, void* stream,
+                     const void* q_frags = nullptr) {
   int st = check_common(q, kv_frags, indices, batch, q_len, kv_len, q_heads, kv_heads, head_dim,
                         topk, chunk_size, sm_scale);
   if (st != MRSA_OK) return st;
@@ -978,6 +1044,9 @@ int selected_forward(const void* q, const void* kv_frags, const void* weights,
   if (parts > 1 && (!partial || (uintptr_t)partial % 16 != 0)) return MRSA_ERR_INVALID_ARGUMENT;
   if ((fuse_local == nullptr) != (fuse_w == nullptr)) return MRSA_ERR_INVALID_ARGUMENT;
   if (fuse_local && (uintptr_t)fuse_local % 16 != 0) return MRSA_ERR_INVALID_ARGUMENT;
+  if (q_frags && (uintptr_t)q_frags % 16 != 0) return MRSA_ERR_INVALID_ARGUMENT;
+  // Q fragments hold 2 KB per (query, KV head): 8 head columns of 128 dims
+  if (q_frags && q_heads / kv_heads > 8) return MRSA_ERR_UNSUPPORTED;
   RaArgs a = base_args(q, kv_frags, weights, indices, key_valid, batch, q_len, kv_len, q_heads,
                        kv_heads, topk, mask_last_token, sm_scale);
   a.out = parts > 1 ? nullptr : (uint16_t*)out;
@@ -986,6 +1055,7 @@ int selected_forward(const void* q, const void* kv_frags, const void* weights,
   a.keep = keep;
   a.fuse_local = parts > 1 ? nullptr : (const uint16_t*)fuse_local;
   a.fuse_w = parts > 1 ? nullptr : (const uint16_t*)fuse_w;
+  a.qf = (const uint16_t*)q_frags;
   hipStream_t s = (hipStream_t)stream;
   st = keep ? launch_routed<false, true>(a, s) : launch_routed<false, false>(a, s);
   if (st != MRSA_OK || parts == 1) return st;
@@ -1070,6 +1140,26 @@ extern "C" int mrsa_selected_attention_fused_fwd(
   return selected_forward(q, kv_frags, weights, indices, key_valid, token_keep, batch, q_len,
                           kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
                           sm_scale, parts, partial, local_output, local_weight, out, stream);
+}
+
+extern "C" int mrsa_set_routed_lock_spin_limit(int limit) {
+  g_spin_limit = limit > 0 ? limit : 0;
+  return MRSA_OK;
+}
+
+extern "C" int mrsa_selected_attention_fused_qf_fwd(
+    const void* q, const void* q_frags, const void* kv_frags, const void* weights,
+    const int32_t* indices, const uint8_t* key_valid, const int8_t* token_keep,
+    const void* local_output, const void* local_weight, int64_t batch, int64_t q_len,
+    int64_t kv_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t topk,
+    int64_t chunk_size, int mask_last_token, float sm_scale, int64_t parts, float* partial,
+    void* out, void* stream) {
+  if (batch > 0 && q_len > 0 && (!local_output || !local_weight || !q_frags))
+    return MRSA_ERR_INVALID_ARGUMENT;
+  return selected_forward(q, kv_frags, weights, indices, key_valid, token_keep, batch, q_len,
+                          kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
+                          sm_scale, parts, partial, local_output, local_weight, out, stream,
+                          q_frags);
 }
 
 // Reads the current device's count of routed-attention tiles whose bounded

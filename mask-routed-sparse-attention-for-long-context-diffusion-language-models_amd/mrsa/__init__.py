@@ -44,7 +44,8 @@ from .route_layer import (
 from .route_weights import route_weights, route_weights_torch
 from .routing import route_topk_g7, selected_attention_g7, selected_attention_g7_cached
 from .sparse_attention import (HiLS_block_M_head, RoutedLockTimeout, check_routed_locks,
-                               kv_fragments, routed_lock_giveups)
+                               kv_fragments, q_fragments, routed_lock_giveups,
+                               set_routed_lock_spin_limit)
 from .token_score import candidate_token_scores_gqa
 from .token_refinement import (
     allocate_entropy_token_budget,
@@ -95,4 +96,9 @@ __all__ = [
     "selected_attention_g7_cached",
     "swa_attention",
     "kv_fragments",
+    "q_fragments",
+    "RoutedLockTimeout",
+    "check_routed_locks",
+    "routed_lock_giveups",
+    "set_routed_lock_spin_limit",
 ]

@@ -87,10 +87,17 @@ SIGNATURES = {
     "mrsa_kv_fragments_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "mrsa_kv_fragments": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P, _P]),
     "mrsa_kv_fragments_rows": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P]),
+    "mrsa_q_fragments_bytes": (_I64, [_I64, _I64, _I64, _I64]),
+    "mrsa_q_fragments": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P]),
     "mrsa_local_attention_fwd": (
         _I,
         [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F,
          _P, _P, _P],
+    ),
+    "mrsa_local_attention_qf_fwd": (
+        _I,
+        [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F,
+         _P, _P, _P, _P],
     ),
     "mrsa_local_attention_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "mrsa_local_attention_split_fwd": (
@@ -118,7 +125,13 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
          _I, _F, _I64, _P, _P, _P],
     ),
+    "mrsa_selected_attention_fused_qf_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+         _I, _F, _I64, _P, _P, _P],
+    ),
     "mrsa_routed_lock_giveups": (_I, [_P, _I]),
+    "mrsa_set_routed_lock_spin_limit": (_I, [_I]),
     "mrsa_selected_attention_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
     "mrsa_selected_attention_bwd": (
         _I,

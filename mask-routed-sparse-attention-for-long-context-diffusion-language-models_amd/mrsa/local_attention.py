@@ -117,6 +117,43 @@ def _local_attention_impl(q, kv_frags, key_valid, kv_len, flash_window, inert_ch
     return out, lse
 
 
+def local_attention_qf_launch(q: torch.Tensor, kv_frags: torch.Tensor,
+                              key_valid: torch.Tensor | None, flash_window: int,
+                              inert_chunk: int, *, sm_scale: float | None = None):
+    """local_attention_launch over every query row (no key split) that also
+    returns q_fragments(q, Hkv), written by the window kernel from the Q
+    operands it loads anyway: (out, lse, q_frags)."""
+
+    B, Lq, Hq, D = q.shape
+    if kv_frags.ndim != 4 or kv_frags.shape[0] != B or kv_frags.shape[3] != FRAG_ELEMS:
+        raise ValueError(f"kv_frags {tuple(kv_frags.shape)} is not a kv_fragments layout")
+    Lk = key_valid.shape[-1] if key_valid is not None else kv_frags.shape[2] * 64
+    if (Lk + 63) // 64 != kv_frags.shape[2]:
+        raise ValueError(f"kv_len {Lk} does not match kv_frags {tuple(kv_frags.shape)}")
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    return torch.ops.mrsa.local_attention_qf(q, kv_frags, key_valid, int(Lk), int(flash_window),
+                                             int(inert_chunk), float(sm_scale))
+
+
+def _local_attention_qf_impl(q, kv_frags, key_valid, kv_len, flash_window, inert_chunk,
+                             sm_scale):
+    B, Lq, Hq, D = q.shape
+    Hkv = kv_frags.shape[1]
+    qc = q.contiguous()
+    kf = kv_frags.contiguous()
+    kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
+    out = torch.empty(B, Lq, Hq, D, dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty(B, Lq, Hq, dtype=torch.float32, device=q.device)
+    qf = torch.empty(B, Hkv, Lq, 1024, dtype=torch.bfloat16, device=q.device)
+    st = _lib.call("mrsa_local_attention_qf_fwd", _lib.ptr(qc), _lib.ptr(kf), _lib.ptr(kv),
+                   None, B, Lq, kv_len, Hq, Hkv, D, int(flash_window), int(inert_chunk),
+                   float(sm_scale), _lib.ptr(qf), _lib.ptr(out), _lib.ptr(lse),
+                   _lib.stream_of(qc))
+    _lib.check(st, "local_attention_qf")
+    return out, lse, qf
+
+
 def bidir_local_attention(
     q: torch.Tensor,
     k: torch.Tensor,

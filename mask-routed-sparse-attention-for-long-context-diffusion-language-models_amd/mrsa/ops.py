@@ -25,8 +25,9 @@ from .kernel_utils import _drop_mask_impl, _drop_mask_rows_impl
 from .local_attention import _local_attention_impl
 from .pool import _pool_bwd_impl, _pool_impl
 from .route_weights import _route_weights_bwd_impl, _route_weights_impl
+from .local_attention import _local_attention_qf_impl
 from .sparse_attention import (FRAG_ELEMS, _kv_fragments_impl, _kv_fragments_rows_impl,
-                               _selected_attention_impl,
+                               _q_fragments_impl, _selected_attention_impl,
                                _selected_attention_bwd_impl)
 from .token_refinement import _gather_entropy_impl, _token_keep_entropy_impl, _token_keep_impl
 from .token_score import _token_scores_impl
@@ -62,6 +63,17 @@ def _(k, v, kv_frags, positions):
     return None
 
 
+@_op("q_fragments")
+def q_fragments(q: Tensor, kv_heads: int) -> Tensor:
+    return _q_fragments_impl(q, kv_heads)
+
+
+@q_fragments.register_fake
+def _(q, kv_heads):
+    B, L, _, _ = q.shape
+    return q.new_empty(B, kv_heads, L, 1024, dtype=torch.bfloat16)
+
+
 # -- window attention -----------------------------------------------------
 @_op("local_attention")
 def local_attention(q: Tensor, kv_frags: Tensor, key_valid: Optional[Tensor], kv_len: int,
@@ -77,6 +89,23 @@ def _(q, kv_frags, key_valid, kv_len, flash_window, inert_chunk, query_positions
     B, Lq, Hq, D = q.shape
     return (q.new_empty(B, Lq, Hq, D, dtype=torch.bfloat16),
             q.new_empty(B, Lq, Hq, dtype=torch.float32))
+
+
+@_op("local_attention_qf")
+def local_attention_qf(q: Tensor, kv_frags: Tensor, key_valid: Optional[Tensor], kv_len: int,
+                       flash_window: int, inert_chunk: int, sm_scale: float
+                       ) -> tuple[Tensor, Tensor, Tensor]:
+    return _local_attention_qf_impl(q, kv_frags, key_valid, kv_len, flash_window, inert_chunk,
+                                    sm_scale)
+
+
+@local_attention_qf.register_fake
+def _(q, kv_frags, key_valid, kv_len, flash_window, inert_chunk, sm_scale):
+    B, Lq, Hq, D = q.shape
+    Hkv = kv_frags.shape[1]
+    return (q.new_empty(B, Lq, Hq, D, dtype=torch.bfloat16),
+            q.new_empty(B, Lq, Hq, dtype=torch.float32),
+            q.new_empty(B, Hkv, Lq, 1024, dtype=torch.bfloat16))
 
 
 # -- landmark pool --------------------------------------------------------
@@ -186,15 +215,16 @@ def _(scores, indices, prior_bias, local_lse, grad_remote, grad_local, grad_gate
 def selected_attention(q: Tensor, kv_frags: Tensor, weights: Tensor, indices: Tensor,
                        key_valid: Optional[Tensor], chunk_size: int, mask_last_token: bool,
                        sm_scale: float, parts: int, token_keep: Optional[Tensor],
-                       fuse_local: Optional[Tensor], fuse_weight: Optional[Tensor]) -> Tensor:
+                       fuse_local: Optional[Tensor], fuse_weight: Optional[Tensor],
+                       q_frags: Optional[Tensor] = None) -> Tensor:
     return _selected_attention_impl(q, kv_frags, weights, indices, key_valid, chunk_size,
                                     mask_last_token, sm_scale, parts, token_keep, fuse_local,
-                                    fuse_weight)
+                                    fuse_weight, q_frags)
 
 
 @selected_attention.register_fake
 def _(q, kv_frags, weights, indices, key_valid, chunk_size, mask_last_token, sm_scale, parts,
-      token_keep, fuse_local, fuse_weight):
+      token_keep, fuse_local, fuse_weight, q_frags=None):
     return q.new_empty(q.shape, dtype=torch.bfloat16)
 
 
@@ -319,7 +349,8 @@ def _(entropy, indices):
     return entropy.new_empty(B, L, H, K, dtype=torch.float32)
 
 OPERATORS = (
-    "kv_fragments", "kv_fragments_rows_", "local_attention", "chunk_attn_pool",
+    "kv_fragments", "kv_fragments_rows_", "q_fragments", "local_attention",
+    "local_attention_qf", "chunk_attn_pool",
     "chunk_attn_pool_bwd", "route_topk", "route_score_bwd", "route_weights", "route_weights_bwd",
     "selected_attention", "selected_attention_bwd", "fuse_hils_outputs", "fuse_hils_outputs_bwd",
     "remote_drop_mask",

@@ -37,7 +37,7 @@ from dataclasses import dataclass, field
 import torch
 
 from .kernel_utils import drop_mask_rows_launch
-from .local_attention import local_attention_launch
+from .local_attention import key_parts, local_attention_launch, local_attention_qf_launch
 from .pool import chunk_attn_pool_gqa_prior
 from .route_weights import route_weights_launch
 from .sparse_attention import (FRAG_ELEMS, kv_fragments, kv_fragments_rows,
@@ -127,9 +127,16 @@ def route_attention(
     frags = kv_fragments(k, v)
     _mark("kv_fragments")
     flash_window = cfg.local_window + S - 1 if cfg.skip_inert_slots else cfg.local_window
-    local_out, local_lse = local_attention_launch(
-        q, frags, kv_bool, flash_window, S if cfg.skip_inert_slots else 0
-    )
+    q_frags = None
+    if G <= 8 and key_parts(B, L, Hkv, L, flash_window) == 1:
+        # the window kernel also writes the routed attention's Q operand
+        # images (read as whole cache lines by the routed kernel)
+        local_out, local_lse, q_frags = local_attention_qf_launch(
+            q, frags, kv_bool, flash_window, S if cfg.skip_inert_slots else 0)
+    else:
+        local_out, local_lse = local_attention_launch(
+            q, frags, kv_bool, flash_window, S if cfg.skip_inert_slots else 0
+        )
     _mark("local_attention")
     q_lmk = route_q[:, S - 1 :: S].reshape(B, C, Hkv, G, D)
     k_chunked = k.reshape(B, C, S, Hkv, D)
@@ -168,7 +175,7 @@ def route_attention(
     # fuse_hils_outputs(remote, local_out, local_w) without materialising remote.
     out = selected_attention_launch(q, frags, remote_w, indices, kv_bool, S,
                                     token_keep=token_keep, fuse_local=local_out,
-                                    fuse_weight=local_w)
+                                    fuse_weight=local_w, q_frags=q_frags)
     _mark("selected_attention")
     if not return_intermediates:
         return out

@@ -47,6 +47,34 @@ def _kv_fragments_impl(k: torch.Tensor, v: torch.Tensor | None) -> torch.Tensor:
     return out
 
 
+def q_fragments(q: torch.Tensor, kv_heads: int) -> torch.Tensor:
+    """q [B, L, Hq, 128] bf16 -> Q operand images [B, Hkv, L, 1024] bf16.
+
+    Per (batch, KV head, query) the 2 KB register image of the routed
+    attention's Q^T operand for the query's G = Hq / Hkv head columns:
+    f[256 ks + 64 grp + 8 g + e] = q[h G + g][32 ks + 8 grp + e] (zeros for
+    heads g >= G, up to 8), so the routed kernel reads each lane group's 8
+    head columns as one 128-byte line.
+    """
+
+    if q.device.type != "cuda" or q.dtype != torch.bfloat16 or q.ndim != 4 or q.shape[3] != 128:
+        raise ValueError("q_fragments requires a CUDA BF16 [B, L, Hq, 128] query tensor")
+    if kv_heads <= 0 or q.shape[2] % kv_heads or q.shape[2] // kv_heads > 8:
+        raise ValueError(f"q_fragments: {q.shape[2]} query heads over {kv_heads} KV heads "
+                         "(at most 8 per group)")
+    return torch.ops.mrsa.q_fragments(q, int(kv_heads))
+
+
+def _q_fragments_impl(q: torch.Tensor, kv_heads: int) -> torch.Tensor:
+    B, L, Hq, D = q.shape
+    qc = q.contiguous()
+    out = torch.empty(B, kv_heads, L, 1024, dtype=torch.bfloat16, device=q.device)
+    st = _lib.call("mrsa_q_fragments", _lib.ptr(qc), B, L, Hq, kv_heads, D, _lib.ptr(out),
+                   _lib.stream_of(qc))
+    _lib.check(st, "q_fragments")
+    return out
+
+
 def kv_fragments_rows(k: torch.Tensor, v: torch.Tensor, kv_frags: torch.Tensor,
                       positions: torch.Tensor) -> None:
     """Rewrite the fragments of rows ``positions`` of k and v in ``kv_frags``
@@ -96,15 +124,18 @@ def walk_parts(batch: int, q_len: int, kv_heads: int, kv_len: int, topk: int,
 
 
 class RoutedLockTimeout(RuntimeError):
-    """Routed-attention tiles ran out of their bounded lock wait; their
-    outputs may have lost additions."""
+    """Routed-attention tiles ran out of their bounded lock wait.  They were
+    deferred and replayed after their workgroup's walk (the outputs are
+    exact), but at the default bound this never happens in a healthy run."""
 
 
 def routed_lock_giveups(reset: bool = True) -> int:
     """Number of routed-attention tiles on the current device whose bounded
-    lock wait ran out since the last reset (waits for the device's queued
-    work).  Such a tile adds its terms with LDS float atomics, which is exact
-    only when no other wave is inside the same rows."""
+    lock wait ran out since the last reset.  Each such tile is deferred and
+    replayed onto its rows after the workgroup's walk, so outputs stay exact;
+    the count reports that slow path.  One counter per device, shared by all
+    streams; reading it waits for the device's queued work, so it cannot run
+    under graph capture."""
 
     import ctypes
 
@@ -121,8 +152,17 @@ def check_routed_locks(reset: bool = True) -> None:
     n = routed_lock_giveups(reset)
     if n:
         raise RoutedLockTimeout(
-            f"{n} routed-attention tile(s) ran out of the bounded lock wait; their rows may "
-            "have lost additions (MRSA_LOCK_SPIN_LIMIT set too low?)")
+            f"{n} routed-attention tile(s) ran out of the bounded lock wait and were replayed "
+            "after their walk (outputs exact; a lowered spin limit, or lock contention "
+            "that should not occur)")
+
+
+def set_routed_lock_spin_limit(limit: int = 65536) -> None:
+    """Test hook: lock tries of the routed-attention kernels before a tile is
+    deferred (process-wide, read at each launch; <= 0 defers every tile)."""
+
+    _lib.check(_lib.call("mrsa_set_routed_lock_spin_limit", int(limit)),
+               "mrsa_set_routed_lock_spin_limit")
 
 
 def selected_attention_launch(
@@ -139,6 +179,7 @@ def selected_attention_launch(
     token_keep: torch.Tensor | None = None,
     fuse_local: torch.Tensor | None = None,
     fuse_weight: torch.Tensor | None = None,
+    q_frags: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """q [B, Lq, Hq, D], kv_frags = kv_fragments(k, v) of the Lk-row cache,
     weights [B, Lq, Hq, K] -> [B, Lq, Hq, D] bf16.
@@ -150,6 +191,8 @@ def selected_attention_launch(
     ``fuse_weight`` [B, Lq, Hq] (bf16, both or neither) fold the output
     fusion in: the result is fuse_hils_outputs(routed, fuse_local,
     fuse_weight), bit for bit, without materialising the routed output.
+    ``q_frags`` = q_fragments(q, Hkv) (with the fusion only) makes the kernel
+    read the queries from their operand images: the same result.
     """
 
     B, Lq, Hq, D = q.shape
@@ -171,14 +214,19 @@ def selected_attention_launch(
         raise ValueError(
             f"fusion shapes {tuple(fuse_local.shape)} / {tuple(fuse_weight.shape)} do not "
             f"match the output [{B}, {Lq}, {Hq}, {D}]")
+    if q_frags is not None:
+        if fuse_local is None:
+            raise ValueError("q_frags is read by the fused routed attention only")
+        if q_frags.shape != (B, Hkv, Lq, 1024) or q_frags.dtype != torch.bfloat16:
+            raise ValueError(f"q_frags {tuple(q_frags.shape)} is not q_fragments(q, {Hkv})")
     return torch.ops.mrsa.selected_attention(
         q, kv_frags, weights, indices, key_valid, int(chunk_size), bool(mask_last_token),
-        float(sm_scale), parts, token_keep, fuse_local, fuse_weight)
+        float(sm_scale), parts, token_keep, fuse_local, fuse_weight, q_frags)
 
 
 def _selected_attention_impl(q, kv_frags, weights, indices, key_valid, chunk_size,
                              mask_last_token, sm_scale, parts, token_keep, fuse_local,
-                             fuse_weight):
+                             fuse_weight, q_frags=None):
     B, Lq, Hq, D = q.shape
     Hkv, Lk = kv_frags.shape[1], kv_frags.shape[2] * 64
     K = indices.shape[-1]
@@ -197,13 +245,22 @@ def _selected_attention_impl(q, kv_frags, weights, indices, key_valid, chunk_siz
         partial = None
         if parts > 1:
             partial = torch.empty(parts, B, Lq, Hq, D, dtype=torch.float32, device=q.device)
-        st = _lib.call(
-            "mrsa_selected_attention_fused_fwd",
-            _lib.ptr(qc), _lib.ptr(kf), _lib.ptr(w), _lib.ptr(idx),
-            _lib.ptr(kv), _lib.ptr(keep), _lib.ptr(lo), _lib.ptr(lw), B, Lq, Lk, Hq, Hkv, D, K,
-            int(chunk_size), 1 if mask_last_token else 0, float(sm_scale), parts,
-            _lib.ptr(partial), _lib.ptr(out), _lib.stream_of(qc),
-        )
+        if q_frags is not None:
+            st = _lib.call(
+                "mrsa_selected_attention_fused_qf_fwd",
+                _lib.ptr(qc), _lib.ptr(q_frags.contiguous()), _lib.ptr(kf), _lib.ptr(w),
+                _lib.ptr(idx), _lib.ptr(kv), _lib.ptr(keep), _lib.ptr(lo), _lib.ptr(lw),
+                B, Lq, Lk, Hq, Hkv, D, K, int(chunk_size), 1 if mask_last_token else 0,
+                float(sm_scale), parts, _lib.ptr(partial), _lib.ptr(out), _lib.stream_of(qc),
+            )
+        else:
+            st = _lib.call(
+                "mrsa_selected_attention_fused_fwd",
+                _lib.ptr(qc), _lib.ptr(kf), _lib.ptr(w), _lib.ptr(idx),
+                _lib.ptr(kv), _lib.ptr(keep), _lib.ptr(lo), _lib.ptr(lw), B, Lq, Lk, Hq, Hkv, D,
+                K, int(chunk_size), 1 if mask_last_token else 0, float(sm_scale), parts,
+                _lib.ptr(partial), _lib.ptr(out), _lib.stream_of(qc),
+            )
     elif token_keep is not None:
         keep = token_keep.to(device=q.device, dtype=torch.int8).contiguous()
         partial = None

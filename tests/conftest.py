@@ -26,3 +26,15 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture(autouse=True)
+def _routed_locks_quiet(request):
+    """After every GPU test: no routed-attention tile ran out of its bounded
+    lock wait (tests that force the bound clear the counter themselves)."""
+
+    yield
+    if "gpu" in request.keywords and torch.cuda.is_available():
+        import mrsa
+
+        mrsa.check_routed_locks()

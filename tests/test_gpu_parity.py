@@ -720,33 +720,109 @@ def test_route_topk_g7_gumbel_sampling_vs_oracle():
     assert torch.equal(selg.cpu(), exp)
 
 
-def test_routed_lock_giveups_are_reported():
+def test_routed_lock_giveups_are_reported_and_exact():
     # The bounded lock wait is forced from the host: with one try per tile,
-    # contended tiles give up and add without the lock (their sums may lose
-    # terms; no fault or hang), and the status word must say so.  With the
-    # default bound the contended shape reports none.
-    _note("routed lock give-ups reported")
+    # contended tiles give up, are deferred and replayed after the walk (no
+    # fault or hang, no lost terms), and the status word reports them.  With
+    # the default bound the contended shape reports none.  A limit of 0
+    # defers every tile.  Each output matches the oracle.
+    _note("routed lock give-ups deferred, exact and reported")
     Lq, K, Hkv, G, D, Lk = 4, 32, 4, 7, 128, 2048
     q = _rand((1, Lq, Hkv * G, D), 96).bfloat16()
     k, v = _planted_kv(Lk, Hkv, D, 97)
     idx = _sorted_routes(Lq, Hkv, K, Lk // 64, 98)
     w = torch.softmax(_rand((1, Lq, Hkv * G, K), 99), -1).bfloat16()
+    valid = torch.ones(1, Lk, dtype=torch.bool)
     args = (q.to(DEV), mrsa.kv_fragments(k.to(DEV), v.to(DEV)), w.to(DEV), idx.to(DEV),
-            torch.ones(1, Lk, dtype=torch.bool, device=DEV), 64)
+            valid.to(DEV), 64)
+    ref = O.selected_attention(q, k, v, w, idx, valid)
     mrsa.routed_lock_giveups(reset=True)
     for _ in range(10):
-        selected_attention_launch(*args, parts=1)
+        _assert_close_attn(selected_attention_launch(*args, parts=1), ref, "default bound")
     assert mrsa.routed_lock_giveups(reset=True) == 0
-    old = os.environ.get("MRSA_LOCK_SPIN_LIMIT")
-    os.environ["MRSA_LOCK_SPIN_LIMIT"] = "1"
     try:
-        for _ in range(10):
-            selected_attention_launch(*args, parts=1)
-        with pytest.raises(mrsa.RoutedLockTimeout):
-            mrsa.check_routed_locks()
-        assert mrsa.routed_lock_giveups(reset=True) == 0  # cleared by the check
+        for limit in (1, 0):
+            mrsa.set_routed_lock_spin_limit(limit)
+            for _ in range(10):
+                _assert_close_attn(selected_attention_launch(*args, parts=1), ref,
+                                   f"spin limit {limit}")
+            n = mrsa.routed_lock_giveups(reset=False)
+            print(f"spin limit {limit}: {n} deferred tiles", flush=True)
+            assert n > 0
+            with pytest.raises(mrsa.RoutedLockTimeout):
+                mrsa.check_routed_locks()
+            assert mrsa.routed_lock_giveups(reset=True) == 0  # cleared by the check
+        # every tile deferred, with token keep rows, and with the fusion
+        # reading Q fragments
+        mrsa.set_routed_lock_spin_limit(0)
+        keep = (torch.rand(1, Lq, Hkv, K, 64, generator=torch.Generator().manual_seed(95))
+                < 0.7).to(torch.int8)
+        rk = O.selected_attention(q, k, v, w, idx, valid, token_keep=keep)
+        _assert_close_attn(selected_attention_launch(*args, parts=1, token_keep=keep.to(DEV)),
+                           rk, "spin limit 0, token keep")
+        loc = _rand((1, Lq, Hkv * G, D), 94).bfloat16()
+        lw = torch.rand(1, Lq, Hkv * G).bfloat16()
+        fused = selected_attention_launch(*args, parts=1, fuse_local=loc.to(DEV),
+                                          fuse_weight=lw.to(DEV),
+                                          q_frags=mrsa.q_fragments(q.to(DEV), Hkv))
+        _assert_close_attn(fused, O.fuse_outputs(ref, loc, lw), "spin limit 0, fused, Q fragments")
+        assert mrsa.routed_lock_giveups(reset=True) > 0
     finally:
-        if old is None:
-            del os.environ["MRSA_LOCK_SPIN_LIMIT"]
-        else:
-            os.environ["MRSA_LOCK_SPIN_LIMIT"] = old
+        mrsa.set_routed_lock_spin_limit(65536)
+
+
+# -- Q fragments: the routed attention's Q^T operand images ----------------
+def test_q_fragments_layout_bit_exact():
+    _note("q fragments layout")
+    for B, L, Hkv, G in ((1, 100, 4, 7), (2, 64, 2, 8), (1, 33, 3, 4)):
+        q = _rand((B, L, Hkv * G, 128), 77).bfloat16()
+        qf = mrsa.q_fragments(q.to(DEV), Hkv).cpu().reshape(B, Hkv, L, 4, 4, 8, 8)
+        exp = torch.zeros(B, Hkv, L, 4, 4, 8, 8, dtype=torch.bfloat16)  # ks, grp, head, e
+        exp[:, :, :, :, :, :G] = q.reshape(B, L, Hkv, G, 4, 4, 8).permute(0, 2, 1, 4, 5, 3, 6)
+        assert torch.equal(qf, exp), (B, L, Hkv, G)
+
+
+@pytest.mark.parametrize("G", [7, 4])
+def test_local_attention_qf_same_outputs_and_q_fragments(G):
+    # The window kernel's Q-fragment by-product changes nothing else, and the
+    # images equal the standalone layout kernel's (for every head slot the
+    # routed kernel reads: g < G).
+    _note(f"local attention with Q fragments G={G}")
+    from mrsa.local_attention import local_attention_qf_launch
+    L, Hkv, D = 1000, 2, 128
+    q = _rand((1, L, Hkv * G, D), 81).bfloat16().to(DEV)
+    k, v = _planted_kv(1024, Hkv, D, 82)
+    valid = torch.ones(1, L, dtype=torch.bool)
+    valid[0, 300:310] = False
+    valid = valid.to(DEV)
+    frags = mrsa.kv_fragments(k[:, :L].contiguous().to(DEV), v[:, :L].contiguous().to(DEV))
+    o1, l1 = local_attention_launch(q, frags, valid, 319, 64, parts=1)
+    o2, l2, qf = local_attention_qf_launch(q, frags, valid, 319, 64)
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    ref = mrsa.q_fragments(q, Hkv).reshape(1, Hkv, L, 4, 4, 8, 8)[..., :G, :]
+    assert torch.equal(qf.reshape(1, Hkv, L, 4, 4, 8, 8)[..., :G, :], ref)
+
+
+def test_selected_attention_fused_with_q_fragments_matches():
+    _note("fused routed attention reading Q fragments")
+    Lq, Lk, Hkv, G, D, K = 300, 2048, 4, 7, 128, 32
+    q = _rand((1, Lq, Hkv * G, D), 85).bfloat16()
+    k, v = _planted_kv(Lk, Hkv, D, 86)
+    idx = _sorted_routes(Lq, Hkv, K, Lk // 64, 87)
+    w = torch.softmax(_rand((1, Lq, Hkv * G, K), 88), -1).bfloat16()
+    valid = torch.ones(1, Lk, dtype=torch.bool)
+    valid[0, 1000:1003] = False
+    loc = _rand((1, Lq, Hkv * G, D), 89).bfloat16()
+    lw = torch.rand(1, Lq, Hkv * G).bfloat16()
+    args = (q.to(DEV), mrsa.kv_fragments(k.to(DEV), v.to(DEV)), w.to(DEV), idx.to(DEV),
+            valid.to(DEV), 64)
+    kw = dict(fuse_local=loc.to(DEV), fuse_weight=lw.to(DEV))
+    qf = mrsa.q_fragments(q.to(DEV), Hkv)
+    for parts in (1, 3):
+        a = selected_attention_launch(*args, parts=parts, **kw)
+        b = selected_attention_launch(*args, parts=parts, q_frags=qf, **kw)
+        assert_nearly_identical(a, b, f"fused with Q fragments, parts={parts}", atol=0.03)
+    ref = O.fuse_outputs(O.selected_attention(q, k, v, w, idx, valid), loc, lw)
+    _assert_close_attn(b, ref, "fused with Q fragments vs oracle")
+    with pytest.raises(ValueError):
+        selected_attention_launch(*args, q_frags=qf)  # Q fragments need the fusion
