@@ -38,12 +38,15 @@
 // rows, accumulates onto them and writes them back with 16-byte accesses,
 // and clears the bits.
 // The first try is a ds_or_rtn of both bits, issued right after the QK
-// product and read after the softmax.  On a conflict the wave keeps the
-// lower bit if that try took it, gives the other back and takes the missing
-// bits one at a time, lowest first, with one-bit ORs (which change nothing
-// while the bit is taken).  A wave only waits while holding bits below the
-// one it waits for, so no cycle of waits forms, and no failed try leaves a
-// bit set.  (Retrying both bits with OR and undo let two waves that want the
+// product and read after the softmax.  On a conflict the wave gives back
+// what the try took and sets the tile aside (its P^T stays in registers, up
+// to two tiles) while it runs the step's other tiles; the step's last tile
+// then adds the set-aside ones, waiting if need be: a fresh try of both
+// bits, and on a conflict the wave keeps the lower bit if that try took it,
+// gives the other back and takes the missing bits one at a time, lowest
+// first, with one-bit ORs (which change nothing while the bit is taken).  A
+// wave only waits while holding bits below the one it waits for, so no cycle
+// of waits forms, and no failed try leaves a bit set.  (Retrying both bits with OR and undo let two waves that want the
 // same bits block each other with their momentary bits in lockstep for as
 // long as they kept retrying.)  LDS operations of one wave complete in issue
 // order, so its writes land before its release and after another wave's
@@ -610,6 +613,58 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     mskn = ((uint64_t)r[3] << 32) | r[2];
   };
 
+  // Adds a tile's P^T onto its owners' rows (srow: this lane's row slot)
+  // under the lock, waiting for it: the first try takes both bits at once;
+  // on a conflict the wave keeps the lower bit if that try took it, gives
+  // back the other and takes the missing bits one at a time, lowest first,
+  // with one-bit ORs (which change nothing while the bit is taken).  A wave
+  // only waits while holding bits below the one it waits for, so no cycle
+  // of waits forms, and no failed try leaves a bit set.  When the bounded
+  // wait runs out, the tile (step st, tile t) is queued for the replay after
+  // the walk.
+  auto add_locked = [&](float* srow, uint32_t want, int t, const u32x4_t (&Pb)[2]) {
+    bool locked = false;
+    if (a.spin_limit > 0) {
+      uint32_t seen = 0u;
+      if (lane == 0) seen = lds_or_rtn(lock_addr, want);
+      seen = __builtin_amdgcn_readfirstlane(seen);
+      const uint32_t low = want & (0u - want);
+      const uint32_t keep = want & ~seen & low;
+      const uint32_t back = want & ~seen & ~keep;
+      if ((seen & want) != 0u && lane == 0 && back) lds_and(lock_addr, ~back);
+      uint32_t need = (seen & want) == 0u ? 0u : want & ~keep;
+      for (int spin = 1; need != 0u && spin < a.spin_limit; ++spin) {
+        const uint32_t bit = need & (0u - need);
+        __builtin_amdgcn_s_sleep(1);
+        uint32_t old = 0u;
+        if (lane == 0) old = lds_or_rtn(lock_addr, bit);
+        old = __builtin_amdgcn_readfirstlane(old);
+        if ((old & bit) == 0u) need &= ~bit;
+      }
+      locked = need == 0u;
+      if (!locked && lane == 0) lds_and(lock_addr, ~(want & ~need));  // give back what was taken
+    }
+    if (locked) {
+      add_rows(srow + lane_e, srow + lane_o, Pb);
+      asm volatile("" ::: "memory");
+      if (lane == 0) lds_and(lock_addr, ~want);
+    } else if (lane == 0) {
+      // The bounded wait ran out: queue the tile for the replay after the
+      // walk (the queue holds every tile of the workgroup at most once).
+      const uint32_t slot = __hip_atomic_fetch_add(dcount, 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+      dq[slot] = (uint16_t)(((uint32_t)st << 4) | (uint32_t)t);
+      atomicAdd(&g_lock_giveups, 1ull);
+    }
+  };
+  // Up to two tiles of the current step set aside after a failed first try.
+  int nset = 0;
+  u32x4_t set0[2], set1[2];
+  float* setrow0 = O;
+  float* setrow1 = O;
+  uint32_t setwant0 = 0u, setwant1 = 0u;
+  int sett0 = 0, sett1 = 0;
+
   // One tile: columns 2 t + own of the step's owners.  The last tile of a
   // step (LAST) prefetches the next step's first Q and its K (after the QK
   // product) and V (after the PV product); other tiles prefetch the next
@@ -702,44 +757,46 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       float* const srow = O + (own ? qb : qa) * 1024;
       asm volatile("" : "+v"(first_try) : "v"(Pb[1][3]));  // read after the softmax
       const uint32_t seen = __builtin_amdgcn_readfirstlane(first_try);
-      bool locked = a.spin_limit > 0 && (seen & want) == 0u;
-      if (a.spin_limit > 0 && !locked) {
-        // Ordered wait: keep the lower bit if the first try took it, give
-        // back the other, then take the missing bits one at a time, lowest
-        // first (a one-bit OR changes nothing when the bit is taken).
-        const uint32_t low = want & (0u - want);
-        const uint32_t keep = want & ~seen & low;
-        const uint32_t back = want & ~seen & ~keep;
-        if (lane == 0 && back) lds_and(lock_addr, ~back);
-        uint32_t need = want & ~keep;
-        for (int spin = 1; need != 0u && spin < a.spin_limit; ++spin) {
-          const uint32_t bit = need & (0u - need);
-          __builtin_amdgcn_s_sleep(1);
-          uint32_t old = 0u;
-          if (lane == 0) old = lds_or_rtn(lock_addr, bit);
-          old = __builtin_amdgcn_readfirstlane(old);
-          if ((old & bit) == 0u) need &= ~bit;
-        }
-        locked = need == 0u;
-        if (!locked && lane == 0) lds_and(lock_addr, ~(want & ~need));  // give back what was taken
-      }
-      // The lock word is read back above with lgkmcnt(0): the row reads
-      // below are issued after it.
-      if (locked) {
+      // The lock word is read back with lgkmcnt(0): the row reads of
+      // add_rows are issued after it.
+      if (a.spin_limit > 0 && (seen & want) == 0u) {
         add_rows(srow + lane_e, srow + lane_o, Pb);
         // The row writes are issued before the release and the LDS
         // completes one wave's operations in order.
         asm volatile("" ::: "memory");
         if (lane == 0) lds_and(lock_addr, ~want);
-      } else if (lane == 0) {
-        // The bounded wait ran out: queue the tile for the replay after the
-        // walk (the queue holds every tile of the workgroup at most once).
-        const uint32_t slot = __hip_atomic_fetch_add(dcount, 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_WORKGROUP);
-        dq[slot] = (uint16_t)(((uint32_t)st << 4) | (uint32_t)t);
-        atomicAdd(&g_lock_giveups, 1ull);
+      } else {
+        // Some owner's rows are busy: give back the bits the try took and
+        // set the tile aside (P kept in registers) while the step's other
+        // tiles run; the last tile of the step adds it.  With both places
+        // taken, wait for the rows now.
+        const uint32_t took = want & ~seen;
+        if (lane == 0 && a.spin_limit > 0 && took) lds_and(lock_addr, ~took);
+        if (nset == 0) {
+          set0[0] = Pb[0];
+          set0[1] = Pb[1];
+          setrow0 = srow;
+          setwant0 = want;
+          sett0 = t;
+          nset = 1;
+        } else if (nset == 1) {
+          set1[0] = Pb[0];
+          set1[1] = Pb[1];
+          setrow1 = srow;
+          setwant1 = want;
+          sett1 = t;
+          nset = 2;
+        } else {
+          add_locked(srow, want, t, Pb);
+        }
       }
-      if constexpr (LAST) load_v(vb, frs, flo, (uint32_t)cn * kFragBytes);
+      if constexpr (LAST) {
+        // tiles set aside in this step (the chunk's V is still in vb)
+        if (nset > 0) add_locked(setrow0, setwant0, sett0, set0);
+        if (nset > 1) add_locked(setrow1, setwant1, sett1, set1);
+        nset = 0;
+        load_v(vb, frs, flo, (uint32_t)cn * kFragBytes);
+      }
     }
     own2 = nown2;
   };
