@@ -1230,6 +1230,16 @@ int launch_fast(const RouteArgs& a, hipStream_t s) {
 
 namespace {
 
+// The one-pass matrix-core kernel (no workspace) serves the call.  Shared by
+// the dispatcher and the no-allocation entry point, which must agree on
+// which problems need the workspace.
+bool fast_path(const void* q, const void* lmk, int64_t chunks, int64_t groups, int64_t head_dim,
+               int64_t topk, int is_causal, int scores_fp32) {
+  const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)lmk % 16 == 0);
+  return !scores_fp32 && !is_causal && head_dim == 128 && chunks <= 256 &&
+         topk <= kFastMaxTopk && aligned && (groups == 7 || groups == 8);
+}
+
 int route_topk_dispatch(const void* q, const void* lmk, const float* lse_local, const float* bias,
                         const int32_t* drop_mask, const uint8_t* key_valid,
                         int64_t derive_window, int64_t batch, int64_t seq_len, int64_t chunks,
@@ -1276,10 +1286,7 @@ int route_topk_dispatch(const void* q, const void* lmk, const float* lse_local, 
   hipStream_t s = (hipStream_t)stream;
 
   const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)lmk % 16 == 0);
-  const bool fast = !scores_fp32 && !is_causal && head_dim == 128 &&
-                    chunks <= 256 && topk <= kFastMaxTopk && aligned &&
-                    (groups == 7 || groups == 8);
-  if (fast) return groups == 7 ? launch_fast<7>(a, s) : launch_fast<8>(a, s);
+  if (fast_path(q, lmk, chunks, groups, head_dim, topk, is_causal, scores_fp32)) return groups == 7 ? launch_fast<7>(a, s) : launch_fast<8>(a, s);
   const bool block = workspace && head_dim == 128 && groups <= 8 && aligned &&
                      chunks <= (int64_t)kSelThreads * kSelMaxPer && seq_len <= 0x7fffffff &&
                      (uintptr_t)workspace % 16 == 0 &&
@@ -1365,12 +1372,13 @@ extern "C" int mrsa_route_topk_noalloc_fwd(
   if (batch < 0 || seq_len < 0 || chunks <= 0 || kv_heads <= 0 || groups <= 0)
     return MRSA_ERR_INVALID_ARGUMENT;
   // Workspace the workspace entry point takes for this problem: the fp32
-  // logits [batch, seq_len, kv_heads, groups, chunks] of the short-block path
-  // (beyond 256 chunks).  The matrix-core path (<= 256 chunks) runs without
-  // one.  A problem that needs more than the static buffer is rejected.
-  const bool fast_shape = chunks <= 256 && head_dim == 128 && !scores_fp32 && !is_causal &&
-                          (groups == 7 || groups == 8);
-  const int64_t need = fast_shape ? 0 : batch * seq_len * kv_heads * groups * chunks * 4;
+  // logits [batch, seq_len, kv_heads, groups, chunks] of the short-block path.
+  // The one-pass matrix-core path runs without one (the dispatcher's own
+  // test decides).  A problem that needs more than the static buffer is
+  // rejected.
+  const int64_t need = fast_path(q, lmk, chunks, groups, head_dim, topk, is_causal, scores_fp32)
+                           ? 0
+                           : batch * seq_len * kv_heads * groups * chunks * 4;
   if (need > (int64_t)MRSA_ROUTE_TOPK_SCRATCH_BYTES) return MRSA_ERR_SCRATCH;
   void* ws = nullptr;
   if (need > 0) {

@@ -71,3 +71,34 @@ def test_landmark_layout_positions():
     assert pos.tolist() == DO.landmark_positions(12, 4).tolist()
     s64 = DreamShape()
     assert torch.equal(landmark_positions(4096, s64, "cpu"), DO.landmark_positions(4096, 64))
+
+
+def test_yarn_factor8_matches_transformers_yarn():
+    # transformers' own YaRN initialiser (ROPE_INIT_FUNCTIONS["yarn"], the
+    # routine Dream's configuration reaches through train_fulltext.py:2820-2856)
+    # at the configuration-3/4 parameters: theta 1e6, head_dim 128, factor 8,
+    # original context 2048.  transformers computes in float32.
+    import pytest
+
+    rope_utils = pytest.importorskip("transformers.modeling_rope_utils")
+    from transformers import PretrainedConfig
+
+    def hf(factor, original):
+        cfg = PretrainedConfig()
+        cfg.hidden_size, cfg.num_attention_heads, cfg.head_dim = 3584, 28, 128
+        cfg.max_position_embeddings = 131072
+        cfg.rope_theta = 1e6
+        cfg.rope_parameters = {"rope_type": "yarn", "factor": factor, "rope_theta": 1e6,
+                               "original_max_position_embeddings": original}
+        inv, af = rope_utils.ROPE_INIT_FUNCTIONS["yarn"](cfg, "cpu")
+        return inv.double(), af
+
+    inv, af = hf(8.0, 2048)
+    inv8, af8 = DO.yarn_inv_freq(128, 1e6, 8.0, 2048)
+    assert abs(af - af8) < 1e-12
+    assert float(((inv - inv8).abs() / inv8).max()) < 1e-6
+    # the comparison is sensitive to the parameters it pins
+    inv_o, _ = hf(8.0, 4096)
+    assert float(((inv_o - inv8).abs() / inv8).max()) > 1e-2
+    inv4, af4 = hf(4.0, 2048)
+    assert float(((inv4 - inv8).abs() / inv8).max()) > 1e-2 and af4 != af8

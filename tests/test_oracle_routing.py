@@ -185,3 +185,33 @@ def test_remote_drop_mask_rows_equal_full_mask_rows():
     pos = torch.tensor([0, 1, 63, 64, 300, 511, 512, 700, 1000, 1023])
     torch.testing.assert_close(O.remote_drop_mask_rows(valid, W, S, pos),
                                O.remote_drop_mask(valid, W, S)[:, pos], rtol=0, atol=0)
+
+
+def test_route_weights_temperature_closed_form():
+    # Two remote chunks and the local branch, by hand: in both forms the two
+    # remote weights stand in the ratio exp((x1 - x2) / T) (x = score + bias);
+    # the plain form is the 3-way softmax of (x1, x2, lse) / T, the affine
+    # form gives the local branch 1 - sigmoid(scale (logsumexp(x / T) -
+    # lse / T) + offset).  A missing / T anywhere breaks one of these.
+    s = torch.tensor([[[[0.5, -0.25]]]]).bfloat16()
+    idx = torch.tensor([[[[1, 3]]]])
+    bias = torch.zeros(1, 5, 1, 1)
+    bias[0, 1] = 0.125
+    bias[0, 3] = -0.375
+    lse = torch.tensor([[[0.75]]])
+    x1, x2, l = 0.5 + 0.125, -0.25 - 0.375, 0.75
+    for T in (0.5, 1.0, 2.5):
+        rw, lw = O.route_weights(s, idx, bias, lse, temperature=T)
+        e1, e2, el = math.exp(x1 / T), math.exp(x2 / T), math.exp(l / T)
+        tot = e1 + e2 + el
+        torch.testing.assert_close(rw.flatten(), torch.tensor([e1 / tot, e2 / tot]),
+                                   atol=1e-6, rtol=1e-6)
+        assert abs(float(lw) - el / tot) < 1e-6
+        for off, sc in ((0.3, 1.7), (-0.4, 0.6)):
+            rw, lw = O.route_weights(s, idx, bias, lse, temperature=T, gate_offset=off,
+                                     gate_scale=sc)
+            assert abs(float(rw[..., 0] / rw[..., 1]) - math.exp((x1 - x2) / T)) < 1e-5
+            gate = sc * (math.log(e1 + e2) - l / T) + off
+            local = 1.0 - 1.0 / (1.0 + math.exp(-gate))
+            assert abs(float(lw) - local) < 1e-6
+            assert abs(float(rw.sum() + lw) - 1.0) < 1e-6

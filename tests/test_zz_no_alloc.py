@@ -72,3 +72,37 @@ def test_no_alloc_route_topk_rejects_oversize():
     assert "scratch" in _lib.status_string(st)
     torch.cuda.synchronize()
     assert int((idx == -7).sum()) == idx.numel()
+
+
+def _unaligned(t):
+    # the same values at a data pointer 2 bytes off 16-byte alignment
+    buf = torch.empty(t.numel() + 8, dtype=t.dtype, device=t.device)
+    v = buf[1:1 + t.numel()].view(t.shape)
+    v.copy_(t)
+    return v
+
+
+@pytest.mark.parametrize("case", ["topk80", "unaligned"])
+def test_no_alloc_route_topk_off_the_matrix_core_path(case):
+    # Shapes the one-pass kernel does not take although they have <= 256
+    # chunks: more than 64 picks, or q / landmarks not 16-byte aligned.  The
+    # no-allocation entry then hands its static buffer to the same dispatch
+    # as the workspace entry: same results, bit for bit.
+    rows, chunks, topk = (512, 200, 80) if case == "topk80" else (96, 128, 32)
+    print(f"[gpu-case] no-alloc route topk {case}: rows={rows} chunks={chunks} topk={topk}",
+          flush=True)
+    q, lmk, lse, bias, drop = _inputs(rows, chunks, 11)
+    if case == "unaligned":
+        q, lmk = _unaligned(q), _unaligned(lmk)
+    for n in range(2):
+        st, idx, sc = _call("mrsa_route_topk_noalloc_fwd", q, lmk, lse, bias, drop, topk=topk)
+        assert st == 0, _lib.status_string(st)
+        st, ridx, rsc = _call("mrsa_route_topk_ws_fwd", q, lmk, lse, bias, drop, topk=topk,
+                              ws=_workspace(rows, chunks))
+        assert st == 0, _lib.status_string(st)
+        torch.cuda.synchronize()
+        assert int((idx == -7).sum()) == 0
+        assert torch.equal(idx, ridx)
+        assert torch.equal(sc.view(torch.int16), rsc.view(torch.int16))
+        rows = rows // 2  # the second call smaller
+        q, lse, drop = q[:, :rows], lse[:, :rows].contiguous(), drop[:, :rows].contiguous()
