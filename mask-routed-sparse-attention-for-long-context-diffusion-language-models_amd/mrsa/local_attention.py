@@ -14,7 +14,7 @@ from typing import Tuple
 import torch
 
 from . import _lib
-from .sparse_attention import FRAG_ELEMS, kv_fragments
+from .sparse_attention import FRAG_ELEMS, kv_fragments, kv_fragments_cached
 
 
 def _validate_layout(q, k, v, key_valid) -> None:
@@ -180,7 +180,7 @@ def bidir_local_attention(
             "do not pass a dense L×L allowed_mask"
         )
     return local_attention_launch(
-        q, kv_fragments(k, v), key_valid,
+        q, kv_fragments_cached(k, v), key_valid,
         _flash_window(window, skip_inert_slots, chunk_size),
         chunk_size if skip_inert_slots else 0, kv_len=k.shape[1],
     )
@@ -220,7 +220,7 @@ def cached_local_attention(
             f"invalid window/chunk layout: L={seq_len}, W={window}, S={chunk_size}"
         )
     return local_attention_launch(
-        q, kv_fragments(k, v), key_valid,
+        q, kv_fragments_cached(k, v), key_valid,
         _flash_window(window, skip_inert_slots, chunk_size),
         chunk_size if skip_inert_slots else 0, kv_len=seq_len,
         query_positions=query_positions,

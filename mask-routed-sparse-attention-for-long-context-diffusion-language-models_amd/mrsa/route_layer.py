@@ -40,7 +40,7 @@ from .kernel_utils import drop_mask_rows_launch
 from .local_attention import key_parts, local_attention_launch, local_attention_qf_launch
 from .pool import chunk_attn_pool_gqa_prior
 from .route_weights import route_weights_launch
-from .sparse_attention import (FRAG_ELEMS, kv_fragments, kv_fragments_rows,
+from .sparse_attention import (FRAG_ELEMS, kv_fragments, kv_fragments_cached, kv_fragments_rows,
                                selected_attention_launch)
 from .token_refinement import refine_remote_tokens_entropy_g7, refine_remote_tokens_g7
 from .topk import route_topk_launch
@@ -232,7 +232,7 @@ def swa_attention(
         raise ValueError("swa_attention requires CUDA bf16 tensors")
     flash_window = window + chunk_size - 1 if skip_inert_slots else window
     out, _ = local_attention_launch(
-        q, kv_fragments(k, v), key_valid, flash_window,
+        q, kv_fragments_cached(k, v), key_valid, flash_window,
         chunk_size if skip_inert_slots else 0, kv_len=k.shape[1],
     )
     return out

@@ -10,7 +10,8 @@ from __future__ import annotations
 
 import torch
 
-from .sparse_attention import kv_fragments, selected_attention_autograd, selected_attention_launch
+from .sparse_attention import (kv_fragments, kv_fragments_cached, selected_attention_autograd,
+                               selected_attention_launch)
 from .topk import route_topk_launch
 
 _LOGICAL_G = 7
@@ -174,6 +175,6 @@ def selected_attention_g7_cached(q, k, v, weights, indices, key_valid, chunk_siz
 
     _validate_selected(q, k, v, weights, indices, key_valid, chunk_size, token_keep)
     return selected_attention_launch(
-        q, kv_fragments(k, v), weights, indices, key_valid, chunk_size, mask_last_token=True,
+        q, kv_fragments_cached(k, v), weights, indices, key_valid, chunk_size, mask_last_token=True,
         token_keep=token_keep,
     )

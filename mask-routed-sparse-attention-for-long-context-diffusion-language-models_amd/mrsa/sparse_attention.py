@@ -47,6 +47,54 @@ def _kv_fragments_impl(k: torch.Tensor, v: torch.Tensor | None) -> torch.Tensor:
     return out
 
 
+# Fragment layouts of recent (k, v) pairs, most recent last:
+# (key, weakref(k), weakref(v) or None, fragments).
+_FRAG_CACHE: list = []
+_FRAG_CACHE_SIZE = 4
+
+
+def _frag_key(t):
+    return (t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype, t.device, t._version)
+
+
+def kv_fragments_cached(k: torch.Tensor, v: torch.Tensor | None = None) -> torch.Tensor:
+    """kv_fragments(k, v), reusing the layout last built for the same k and v
+    tensor objects while neither has been written since (storage, shape,
+    strides and version counter unchanged: an in-place update such as
+    LayerKVCache.replace bumps the version).  The per-op drop-ins use it, so
+    a layer that calls bidir_local_attention and then selected_attention_g7
+    on the same k / v, or a decode loop that calls the cached ops against an
+    unchanged cache, lays K / V out once.  The four most recent layouts are
+    kept (each holds its source tensors only weakly); under torch.compile
+    tracing the layout is built every time."""
+
+    if torch.compiler.is_compiling() or k.device.type != "cuda":
+        return kv_fragments(k, v)
+    key = (_frag_key(k), None if v is None else _frag_key(v))
+    alive = []
+    hit = None
+    for entry in _FRAG_CACHE:
+        ek, wk, wv, frags = entry
+        tk = wk()
+        tv = None if wv is None else wv()
+        if tk is None or (wv is not None and tv is None):
+            continue  # a source tensor is gone
+        alive.append(entry)
+        if hit is None and ek == key and tk is k and tv is v:
+            hit = entry
+    _FRAG_CACHE[:] = alive
+    if hit is not None:
+        _FRAG_CACHE.remove(hit)
+        _FRAG_CACHE.append(hit)
+        return hit[3]
+    frags = kv_fragments(k, v)
+    import weakref
+
+    _FRAG_CACHE.append((key, weakref.ref(k), None if v is None else weakref.ref(v), frags))
+    del _FRAG_CACHE[:-_FRAG_CACHE_SIZE]
+    return frags
+
+
 def q_fragments(q: torch.Tensor, kv_heads: int) -> torch.Tensor:
     """q [B, L, Hq, 128] bf16 -> Q operand images [B, Hkv, L, 1024] bf16.
 
@@ -300,7 +348,7 @@ def selected_attention_backward(q, k, v, weights, indices, key_valid, chunk_size
     the end).  The fragment layouts of (k, v) and of (v, k) are built here."""
 
     return torch.ops.mrsa.selected_attention_bwd(
-        q, kv_fragments(k, v), kv_fragments(v, k), weights, indices, key_valid,
+        q, kv_fragments_cached(k, v), kv_fragments_cached(v, k), weights, indices, key_valid,
         grad_output, int(chunk_size), bool(mask_last_token),
         float(sm_scale if sm_scale is not None else 1.0 / math.sqrt(q.shape[-1])), token_keep,
         int(k.shape[1]))
@@ -348,7 +396,7 @@ class _SelectedAttention(torch.autograd.Function):
         ctx.save_for_backward(q, k, v, weights, indices, key_valid, token_keep)
         ctx.chunk_size, ctx.mask_last_token, ctx.sm_scale = chunk_size, mask_last_token, sm_scale
         return selected_attention_launch(
-            q, kv_fragments(k, v), weights, indices, key_valid, chunk_size,
+            q, kv_fragments_cached(k, v), weights, indices, key_valid, chunk_size,
             mask_last_token=mask_last_token, sm_scale=sm_scale, token_keep=token_keep)
 
     @staticmethod
@@ -370,7 +418,7 @@ def selected_attention_autograd(q, k, v, weights, indices, key_valid, chunk_size
         return _SelectedAttention.apply(q, k, v, weights, indices, key_valid, chunk_size,
                                         mask_last_token, sm_scale, token_keep)
     return selected_attention_launch(
-        q, kv_fragments(k, v), weights, indices, key_valid, chunk_size,
+        q, kv_fragments_cached(k, v), weights, indices, key_valid, chunk_size,
         mask_last_token=mask_last_token, sm_scale=sm_scale, token_keep=token_keep)
 
 

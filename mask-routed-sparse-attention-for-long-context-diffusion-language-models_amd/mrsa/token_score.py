@@ -11,7 +11,7 @@ import math
 import torch
 
 from . import _lib
-from .sparse_attention import FRAG_ELEMS, kv_fragments
+from .sparse_attention import FRAG_ELEMS, kv_fragments, kv_fragments_cached
 
 
 def _validate(q, k, indices, key_valid, chunk_size):
@@ -55,7 +55,7 @@ def candidate_token_scores_gqa(q, k, indices, key_valid, chunk_size, *, kv_frags
 
     _validate(q, k, indices, key_valid, chunk_size)
     if kv_frags is None:
-        kv_frags = kv_fragments(k)
+        kv_frags = kv_fragments_cached(k)
     elif kv_frags.shape != (k.shape[0], k.shape[2], (k.shape[1] + 63) // 64, FRAG_ELEMS):
         raise ValueError("kv_frags must be the kv_fragments layout of k")
     return torch.ops.mrsa.candidate_token_scores(q, kv_frags, indices, key_valid,

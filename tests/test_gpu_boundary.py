@@ -211,3 +211,40 @@ def test_route_layer_weight_form_by_topk(topk, temperature):
                                atol=2e-3, rtol=1e-2)
     torch.testing.assert_close(mid["local_weight"].cpu().float(), lw.bfloat16().float(),
                                atol=2e-3, rtol=1e-2)
+
+
+def test_per_op_drop_ins_reuse_the_kv_layout(monkeypatch):
+    # A layer that runs the per-op drop-ins on the same k / v (the window
+    # branch, then the routed attention; a decode loop against an unchanged
+    # cache) lays K / V out once; an in-place write to the cache (version
+    # bump) lays it out again.  Results equal the uncached path.
+    import mrsa.sparse_attention as SA
+
+    calls = []
+    real = SA.kv_fragments
+    monkeypatch.setattr(SA, "kv_fragments", lambda k, v=None: calls.append(1) or real(k, v))
+    SA._FRAG_CACHE.clear()
+    B, L, Hkv, G, D, K, S = 1, 1024, 4, 7, 128, 8, 64
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(B, 32, Hkv * G, D, generator=g).bfloat16().to(DEV)
+    k = torch.randn(B, L, Hkv, D, generator=g).bfloat16().to(DEV)
+    v = torch.randn(B, L, Hkv, D, generator=g).bfloat16().to(DEV)
+    valid = torch.ones(B, L, dtype=torch.bool, device=DEV)
+    idx = torch.stack([torch.randperm(L // S, generator=g)[:K] for _ in range(32 * Hkv)])
+    idx = idx.sort(-1).values.reshape(B, 32, Hkv, K).int().to(DEV)
+    w = torch.softmax(torch.randn(B, 32, Hkv * G, K, generator=g), -1).bfloat16().to(DEV)
+    pos = torch.arange(L - 32, L, device=DEV)
+    loc1 = mrsa.cached_local_attention(q, k, v, valid, pos, 319, S)
+    out1 = mrsa.selected_attention_g7_cached(q, k, v, w, idx, valid, S)
+    out2 = mrsa.selected_attention_g7_cached(q, k, v, w, idx, valid, S)
+    assert len(calls) == 1
+    fresh = SA.selected_attention_launch(q, real(k, v), w, idx, valid, S)
+    assert_nearly_identical(out1, fresh, "cached layout vs fresh")
+    assert_nearly_identical(out2, fresh, "cached layout, second call")
+    k[:, -1] += 1.0   # the cache is written in place: the layout is rebuilt
+    out3 = mrsa.selected_attention_g7_cached(q, k, v, w, idx, valid, S)
+    assert len(calls) == 2
+    fresh3 = SA.selected_attention_launch(q, real(k, v), w, idx, valid, S)
+    assert_nearly_identical(out3, fresh3, "layout after an in-place write")
+    del loc1
+    SA._FRAG_CACHE.clear()
