@@ -130,6 +130,9 @@ def main() -> int:
     ap.add_argument("--token-budget", type=int, default=0,
                     help="route workload with the remote-token refinement (global_qk) at "
                          "this budget (0: off, the configuration-2 default)")
+    ap.add_argument("--deterministic", action="store_true",
+                    help="routed attention in the fixed accumulation order "
+                         "(RouteLayerConfig.deterministic)")
     ap.add_argument("--decode-eager", action="store_true",
                     help="decode workload without the captured step graph")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -172,7 +175,8 @@ def main() -> int:
     scale = torch.ones(HQ, device=dev)
     key_valid = torch.ones(1, L_CFG2, dtype=torch.bool, device=dev)
     cfg = mrsa.RouteLayerConfig(local_window=WINDOW, chunk_size=CHUNK, topk=TOPK,
-                                token_budget=args.token_budget)
+                                token_budget=args.token_budget,
+                                deterministic=args.deterministic)
 
     stream = torch.cuda.current_stream(dev)
     stage_events = []
@@ -247,6 +251,7 @@ def main() -> int:
             "topk": TOPK,
             "local_window": WINDOW,
             "token_budget": args.token_budget,
+            "deterministic": args.deterministic,
             "parallelism": "single-gpu",
         },
         "roofline": {
@@ -531,7 +536,8 @@ def decode_main(args, torch, mrsa, dev) -> int:
     lmk, _, prior = mrsa.chunk_attn_pool_gqa_prior(q_lmk, k.reshape(1, C, S, HKV, D),
                                                    valid.reshape(1, C, S), scale)
     cache = mrsa.LayerKVCache(k, v, valid, lmk.contiguous(), prior.contiguous())
-    cfg = mrsa.RouteLayerConfig(local_window=WINDOW, chunk_size=S, topk=TOPK)
+    cfg = mrsa.RouteLayerConfig(local_window=WINDOW, chunk_size=S, topk=TOPK,
+                                deterministic=args.deterministic)
     start = L - nb * bs
     blocks = []
     for i in range(nb):

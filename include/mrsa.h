@@ -569,6 +569,34 @@ int mrsa_selected_attention_fused_qf_fwd(const void* q, const void* q_frags,
                                          float* partial, void* out, void* stream);
 
 /*
+ * Routed chunk attention with every option of the entry points above in one
+ * call, plus `flags`:
+ *   MRSA_ROUTED_FIXED_ORDER  each output row adds its chunk terms in
+ *                            ascending chunk order (per-query tickets instead
+ *                            of the row lock), so two launches -- and a
+ *                            captured graph and the eager call -- give the
+ *                            same bits.  The reference's forward accumulates
+ *                            each query block in a fixed order too, and it
+ *                            replaced a kernel for being nondeterministic
+ *                            (dream_dllm_hils/routing.py:133-134).
+ * q_frags may be null (q is read); with q_frags the fusion operands are
+ * required.  token_keep, local_output / local_weight and partial as in
+ * mrsa_selected_attention_fused_fwd.  Unknown flag bits:
+ * MRSA_ERR_INVALID_ARGUMENT.  No reference counterpart beyond the ones of
+ * the options it combines.
+ */
+#define MRSA_ROUTED_FIXED_ORDER 1
+int mrsa_selected_attention_ex_fwd(const void* q, const void* q_frags, const void* kv_frags,
+                                   const void* weights, const int32_t* indices,
+                                   const uint8_t* key_valid, const int8_t* token_keep,
+                                   const void* local_output, const void* local_weight,
+                                   int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
+                                   int64_t kv_heads, int64_t head_dim, int64_t topk,
+                                   int64_t chunk_size, int mask_last_token, float sm_scale,
+                                   int64_t parts, float* partial, int flags, void* out,
+                                   void* stream);
+
+/*
  * Routed-attention lock status.  It has no counterpart in the reference
  * (whose kernels take no lock); it makes the bounded lock wait of the routed
  * attention kernels (mrsa_selected_attention_*) observable.  A tile whose

@@ -117,6 +117,7 @@ struct RaArgs {
   int64_t ntiles;            // ceil(Lq / tq)
   int64_t units;             // B * Hkv * parts * ntiles workgroups of work
   int spin_limit;            // lock tries before a tile is deferred (<= 0: every tile)
+  int det;                   // fixed accumulation order (per-query tickets instead of the lock)
 };
 
 __host__ __device__ inline size_t al16(size_t x) { return (x + 15) & ~(size_t)15; }
@@ -129,12 +130,12 @@ __host__ __device__ inline size_t al16(size_t x) { return (x + 15) & ~(size_t)15
 struct RaLayout {
   size_t o, o_bytes;
   size_t raw, qlen, qflag, wst, omask, step_of, scratch_end;
-  size_t rec, iq, islot, iw, ikeep, dq, misc, total;
+  size_t rec, iq, islot, iw, ikeep, dq, irank, tick, misc, total;
   int items, cap;
 };
 
 __host__ __device__ inline RaLayout ra_layout(int tq, int G, int K, int64_t Ck, bool token,
-                                              bool keep) {
+                                              bool keep, bool det) {
   RaLayout l;
   l.items = tq * K;
   l.cap = (int)(Ck < l.items ? Ck : l.items);
@@ -155,6 +156,8 @@ __host__ __device__ inline RaLayout ra_layout(int tq, int G, int K, int64_t Ck, 
   l.iw = o;      o = al16(o + (token ? 0 : (size_t)l.items * 8 * 2));
   l.ikeep = o;   o = al16(o + (keep ? (size_t)l.items * 8 : 0));
   l.dq = o;      o = al16(o + (token ? 0 : (size_t)l.items * 2));
+  l.irank = o;   o = al16(o + (det ? (size_t)l.items : 0));
+  l.tick = o;    o = al16(o + (det ? ((size_t)tq + 1) * 4 : 0));
   l.misc = o;    o = al16(o + (size_t)(2 * kWaves + 8 + 64) * 4);
   l.total = o;
   return l;
@@ -193,6 +196,11 @@ __device__ __forceinline__ uint32_t lds_or_rtn(uint32_t addr, uint32_t v) {
                : "v"(addr), "v"(v)
                : "memory");
   return old;
+}
+__device__ __forceinline__ uint32_t lds_read_rtn(uint32_t addr) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+  return v;
 }
 __device__ __forceinline__ void lds_and(uint32_t addr, uint32_t v) {
   asm volatile("ds_and_b32 %0, %1" ::"v"(addr), "v"(v) : "memory");
@@ -270,7 +278,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
 
   const int K = a.K, G = a.G, tq = a.tq;
   const int64_t Ck = a.Ck;
-  const RaLayout L = ra_layout(tq, G, K, Ck, TOKEN, KEEP);
+  const RaLayout L = ra_layout(tq, G, K, Ck, TOKEN, KEEP, a.det != 0);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -297,6 +305,8 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   uint32_t* claim = reinterpret_cast<uint32_t*>(misc + 2 * kWaves + 2);  // steps claimed
   uint32_t* dcount = reinterpret_cast<uint32_t*>(misc + 2 * kWaves + 4);  // deferred tiles
   uint16_t* dq = reinterpret_cast<uint16_t*>(smem + L.dq);         // [items] step << 4 | tile
+  uint8_t* it_rank = smem + L.irank;                               // [items] (det)
+  uint32_t* tick = reinterpret_cast<uint32_t*>(smem + L.tick);     // [tq + 1] (det)
   uint32_t* idle_or = reinterpret_cast<uint32_t*>(misc + 2 * kWaves + 8);  // [64], never read
 
   // ---- prologue: the walk of this tile ----------------------------------
@@ -310,6 +320,8 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     qlen[i] = K;
     qflag[i] = 0u;
   }
+  if (a.det)
+    for (int i = tid; i <= tq; i += kThreads) tick[i] = 0u;
   if (tid == 0) {
     *lock = 0u;
     *claim = 0u;
@@ -404,6 +416,8 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     }
   }
   __syncthreads();
+  const int st_lo = (int)((int64_t)part * misc[2 * kWaves] / a.parts);
+  const int st_hi = (int)((int64_t)(part + 1) * misc[2 * kWaves] / a.parts);
   // 5. Items: the first occurrence of each chunk in a query's list (a later
   //    duplicate adds its weights to it).  Strictly ascending lists (what
   //    route scoring emits) have no duplicates and skip the scans.
@@ -422,6 +436,25 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     const int pos = (int)s_rec[step_of[c]][1] + __popc(m & ((1u << qq) - 1u));
     it_q[pos] = (uint8_t)qq;
     it_slot[pos] = (uint8_t)kk;
+    if (a.det) {
+      // Rank of the item in its query's walk order: the query's distinct
+      // listed chunks below c (the slot itself for a strictly ascending
+      // list, whose skipped entries >= Ck all come last).  A walk part
+      // starts its query's ticket at the items of earlier steps.
+      int rank = kk;
+      if (!plain) {
+        rank = 0;
+        for (int k2 = 0; k2 < n; ++k2) {
+          const int32_t c2 = raw[qq * K + k2];
+          if (c2 >= c || c2 >= Ck) continue;
+          bool first = true;
+          for (int k3 = 0; k3 < k2; ++k3) first &= raw[qq * K + k3] != c2;
+          rank += first ? 1 : 0;
+        }
+      }
+      it_rank[pos] = (uint8_t)rank;
+      if (step_of[c] < st_lo) atomicAdd(&tick[qq], 1u);
+    }
     if constexpr (!TOKEN) {
       uint16_t wv[8];
 #pragma unroll
@@ -467,8 +500,6 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       s_rec[e][1] = i0 | ((uint32_t)it_q[i0] << 16) | ((uint32_t)it_q[i0 + (cnt > 1u)] << 24);
     }
   }
-  const int st_lo = (int)((int64_t)part * nsteps / a.parts);
-  const int st_hi = (int)((int64_t)(part + 1) * nsteps / a.parts);
   // 6. Outputs start at zero (the scratch above is dead now).
   if constexpr (!TOKEN) {
     const int n4 = tq * 8 * 128 / 4;
@@ -622,9 +653,51 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   // of waits forms, and no failed try leaves a bit set.  When the bounded
   // wait runs out, the tile (step st, tile t) is queued for the replay after
   // the walk.
+  // Hands the owners' rows on after a tile's row writes (issued before it;
+  // the LDS completes one wave's operations in order): the lock bits back,
+  // or in the fixed-order mode each owner's ticket to its next rank.
+  auto release = [&](uint32_t want, uint32_t dwant) {
+    if (!a.det) {
+      if (lane == 0) lds_and(lock_addr, ~want);
+    } else if (lane == 0) {
+      __hip_atomic_store(tick + (dwant & 63u), ((dwant >> 12) & 63u) + 1u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_WORKGROUP);
+      if ((dwant >> 24) & 1u)
+        __hip_atomic_store(tick + ((dwant >> 6) & 63u), ((dwant >> 18) & 63u) + 1u,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  };
+  // Adds a tile's P^T onto its owners' rows (srow: this lane's row slot)
+  // under the lock, waiting for it: the first try takes both bits at once;
+  // on a conflict the wave keeps the lower bit if that try took it, gives
+  // back the other and takes the missing bits one at a time, lowest first,
+  // with one-bit ORs (which change nothing while the bit is taken).  A wave
+  // only waits while holding bits below the one it waits for, so no cycle
+  // of waits forms, and no failed try leaves a bit set.  In the fixed-order
+  // mode (`want` packed as in do_tile) the wave waits until both owners'
+  // tickets reach the tile's ranks: every earlier item of those queries
+  // belongs to an earlier step, and the earliest step in flight always has
+  // its tickets, so the waits end.  When the bounded wait runs out, the
+  // tile (step st, tile t) is queued for the replay after the walk.
   auto add_locked = [&](float* srow, uint32_t want, int t, const u32x4_t (&Pb)[2]) {
     bool locked = false;
-    if (a.spin_limit > 0) {
+    if (a.spin_limit > 0 && a.det) {
+      const uint32_t ia = want & 63u, ib = (want >> 6) & 63u;
+      const uint32_t ra = (want >> 12) & 63u, rb = (want >> 18) & 63u;
+      const bool hb2 = (want >> 24) & 1u;
+      for (int spin = 0; spin < a.spin_limit; ++spin) {
+        const uint32_t ta = __builtin_amdgcn_readfirstlane(
+            lds_read_rtn(lds_address(tick + ia)));
+        const uint32_t tb = hb2 ? __builtin_amdgcn_readfirstlane(
+                                      lds_read_rtn(lds_address(tick + ib)))
+                                : rb;
+        if (ta == ra && tb == rb) {
+          locked = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+    } else if (a.spin_limit > 0) {
       uint32_t seen = 0u;
       if (lane == 0) seen = lds_or_rtn(lock_addr, want);
       seen = __builtin_amdgcn_readfirstlane(seen);
@@ -647,7 +720,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     if (locked) {
       add_rows(srow + lane_e, srow + lane_o, Pb);
       asm volatile("" ::: "memory");
-      if (lane == 0) lds_and(lock_addr, ~want);
+      release(want, want);
     } else if (lane == 0) {
       // The bounded wait ran out: queue the tile for the replay after the
       // walk (the queue holds every tile of the workgroup at most once).
@@ -709,15 +782,23 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     const uint64_t msh = msk >> (4 * grp);  // bit 16 mt + r: key 16 mt + 4 grp + r
     // First try for the owners' lock bits, issued now so that its LDS round
     // trip overlaps the softmax (the result is read after it).
-    const uint32_t want = (1u << qa) | (hb ? 1u << qb1 : 0u);
+    uint32_t want = (1u << qa) | (hb ? 1u << qb1 : 0u);
     // Every lane takes part (no divergent region, so the wait for the
     // result stays where it is used): lane 0 ORs the bits into the lock word,
     // the others OR 0 into words of their own.
-    uint32_t first_try = 0u;
-    if constexpr (!TOKEN)
-      first_try = __hip_atomic_fetch_or(lane == 0 ? lock : idle_or + lane,
-                                        lane == 0 && a.spin_limit > 0 ? want : 0u,
-                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    uint32_t first_try = 0u, tick_b = 0u;
+    if constexpr (!TOKEN) {
+      if (a.det) {
+        // the owners' tickets (read now, compared after the softmax)
+        first_try = __hip_atomic_load(tick + qa, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        tick_b = __hip_atomic_load(tick + (hb ? qb1 : qa), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+      } else {
+        first_try = __hip_atomic_fetch_or(lane == 0 ? lock : idle_or + lane,
+                                          lane == 0 && a.spin_limit > 0 ? want : 0u,
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
 
     if constexpr (TOKEN) {
       // max over the owner's head columns (lanes j, j ^ 1, j ^ 2, j ^ 4
@@ -755,23 +836,39 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       // rows, with P = 0.
       const int qb = hb ? qb1 : sinkq;
       float* const srow = O + (own ? qb : qa) * 1024;
-      asm volatile("" : "+v"(first_try) : "v"(Pb[1][3]));  // read after the softmax
+      asm volatile("" : "+v"(first_try), "+v"(tick_b) : "v"(Pb[1][3]));  // read after the softmax
       const uint32_t seen = __builtin_amdgcn_readfirstlane(first_try);
-      // The lock word is read back with lgkmcnt(0): the row reads of
-      // add_rows are issued after it.
-      if (a.spin_limit > 0 && (seen & want) == 0u) {
+      // In the fixed-order mode `want` packs the owners and their ranks
+      // (slot a | slot b << 6 | rank a << 12 | rank b << 18 | second owner << 24)
+      // and the rows are free when both tickets equal the ranks.
+      uint32_t dwant = 0u;
+      bool free_now;
+      if (a.det) {
+        const int ra = it_rank[i0 + 2 * t];
+        const int rb = hb ? it_rank[i0 + 2 * t + 1] : 0;
+        dwant = (uint32_t)qa | ((uint32_t)qb << 6) | ((uint32_t)ra << 12) | ((uint32_t)rb << 18) |
+                ((uint32_t)hb << 24);
+        const uint32_t sb = __builtin_amdgcn_readfirstlane(tick_b);
+        free_now = seen == (uint32_t)ra && (!hb || sb == (uint32_t)rb);
+      } else {
+        free_now = (seen & want) == 0u;
+      }
+      // The lock word / tickets are read back with lgkmcnt(0): the row reads
+      // of add_rows are issued after them.
+      if (a.spin_limit > 0 && free_now) {
         add_rows(srow + lane_e, srow + lane_o, Pb);
         // The row writes are issued before the release and the LDS
         // completes one wave's operations in order.
         asm volatile("" ::: "memory");
-        if (lane == 0) lds_and(lock_addr, ~want);
+        release(want, dwant);
       } else {
         // Some owner's rows are busy: give back the bits the try took and
         // set the tile aside (P kept in registers) while the step's other
         // tiles run; the last tile of the step adds it.  With both places
         // taken, wait for the rows now.
         const uint32_t took = want & ~seen;
-        if (lane == 0 && a.spin_limit > 0 && took) lds_and(lock_addr, ~took);
+        if (!a.det && lane == 0 && a.spin_limit > 0 && took) lds_and(lock_addr, ~took);
+        if (a.det) want = dwant;
         if (nset == 0) {
           set0[0] = Pb[0];
           set0[1] = Pb[1];
@@ -890,8 +987,22 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     // wave waits at the barrier below).
     const uint32_t nd = *dcount;
     if (nd > 0u) {
-      if (wave == 0)
+      if (wave == 0) {
+        if (a.det && nd > 1u) {
+          // Fixed order: a query's deferred items are the tail of its walk
+          // order (a later item waits for the ticket of an earlier one), so
+          // replaying the queue in step order keeps each row's order.
+          if (lane == 0)
+            for (uint32_t i = 1; i < nd; ++i) {
+              const uint16_t x = dq[i];
+              uint32_t j = i;
+              for (; j > 0 && dq[j - 1] > x; --j) dq[j] = dq[j - 1];
+              dq[j] = x;
+            }
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
         for (uint32_t e = 0; e < nd; ++e) replay_tile(dq[e]);
+      }
       __syncthreads();
     }
     // Work item e: output row rho = e / 16 (query rho / G, head rho % G),
@@ -1000,9 +1111,9 @@ __global__ void __launch_bounds__(256) fill_neg_inf(float* p, int64_t n) {
 int g_spin_limit = kDefaultSpinLimit;
 
 // Largest tile (<= 32 queries, <= 1024 items) whose LDS layout fits, 0 if none.
-int pick_tile(int G, int K, int64_t Ck, bool token, bool keep) {
+int pick_tile(int G, int K, int64_t Ck, bool token, bool keep, bool det) {
   for (int tq = std::min(kMaxTQ, kMaxItems / K); tq >= 4; tq -= 4) {
-    const RaLayout l = ra_layout(tq, G, K, Ck, token, keep);
+    const RaLayout l = ra_layout(tq, G, K, Ck, token, keep, det);
     if (l.total <= kLdsBytes && l.cap <= 65535) return tq;
   }
   return 0;
@@ -1010,14 +1121,14 @@ int pick_tile(int G, int K, int64_t Ck, bool token, bool keep) {
 
 template <bool TOKEN, bool KEEP>
 int launch_routed(RaArgs& a, hipStream_t s) {
-  const int tq = pick_tile(a.G, a.K, a.Ck, TOKEN, KEEP);
+  const int tq = pick_tile(a.G, a.K, a.Ck, TOKEN, KEEP, a.det != 0);
   if (tq == 0) return MRSA_ERR_UNSUPPORTED;
   a.tq = tq;
   a.ntiles = (a.Lq + tq - 1) / tq;
   a.units = a.B * a.Hkv * a.parts * a.ntiles;
   const int64_t grid = (a.units + 7) / 8 * 8;
   if (grid > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
-  const RaLayout l = ra_layout(tq, a.G, a.K, a.Ck, TOKEN, KEEP);
+  const RaLayout l = ra_layout(tq, a.G, a.K, a.Ck, TOKEN, KEEP, a.det != 0);
   a.spin_limit = g_spin_limit;
   auto kern = routed_attn_kernel<TOKEN, KEEP>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -1078,6 +1189,7 @@ RaArgs base_args(const void* q, const void* kv_frags, const void* weights,
   a.ntiles = 0;
   a.units = 0;
   a.spin_limit = kDefaultSpinLimit;
+  a.det = 0;
   return a;
 }
 
@@ -1090,7 +1202,7 @@ int selected_forward(const void* q, const void* kv_frags, const void* weights,
                      int64_t kv_heads, int64_t head_dim, int64_t topk, int64_t chunk_size,
                      int mask_last_token, float sm_scale, int64_t parts, float* partial,
                      const void* fuse_local, const void* fuse_w, void* out, void* stream,
-                     const void* q_frags = nullptr) {
+                     const void* q_frags = nullptr, int flags = 0) {
   int st = check_common(q, kv_frags, indices, batch, q_len, kv_len, q_heads, kv_heads, head_dim,
                         topk, chunk_size, sm_scale);
   if (st != MRSA_OK) return st;
@@ -1113,6 +1225,7 @@ int selected_forward(const void* q, const void* kv_frags, const void* weights,
   a.fuse_local = parts > 1 ? nullptr : (const uint16_t*)fuse_local;
   a.fuse_w = parts > 1 ? nullptr : (const uint16_t*)fuse_w;
   a.qf = (const uint16_t*)q_frags;
+  a.det = flags & MRSA_ROUTED_FIXED_ORDER;
   hipStream_t s = (hipStream_t)stream;
   st = keep ? launch_routed<false, true>(a, s) : launch_routed<false, false>(a, s);
   if (st != MRSA_OK || parts == 1) return st;
@@ -1217,6 +1330,21 @@ extern "C" int mrsa_selected_attention_fused_qf_fwd(
                           kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
                           sm_scale, parts, partial, local_output, local_weight, out, stream,
                           q_frags);
+}
+
+extern "C" int mrsa_selected_attention_ex_fwd(
+    const void* q, const void* q_frags, const void* kv_frags, const void* weights,
+    const int32_t* indices, const uint8_t* key_valid, const int8_t* token_keep,
+    const void* local_output, const void* local_weight, int64_t batch, int64_t q_len,
+    int64_t kv_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t topk,
+    int64_t chunk_size, int mask_last_token, float sm_scale, int64_t parts, float* partial,
+    int flags, void* out, void* stream) {
+  if (flags & ~MRSA_ROUTED_FIXED_ORDER) return MRSA_ERR_INVALID_ARGUMENT;
+  if (q_frags && batch > 0 && q_len > 0 && !local_output) return MRSA_ERR_INVALID_ARGUMENT;
+  return selected_forward(q, kv_frags, weights, indices, key_valid, token_keep, batch, q_len,
+                          kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
+                          sm_scale, parts, partial, local_output, local_weight, out, stream,
+                          q_frags, flags);
 }
 
 // Reads the current device's count of routed-attention tiles whose bounded

@@ -216,15 +216,15 @@ def selected_attention(q: Tensor, kv_frags: Tensor, weights: Tensor, indices: Te
                        key_valid: Optional[Tensor], chunk_size: int, mask_last_token: bool,
                        sm_scale: float, parts: int, token_keep: Optional[Tensor],
                        fuse_local: Optional[Tensor], fuse_weight: Optional[Tensor],
-                       q_frags: Optional[Tensor] = None) -> Tensor:
+                       q_frags: Optional[Tensor] = None, deterministic: bool = False) -> Tensor:
     return _selected_attention_impl(q, kv_frags, weights, indices, key_valid, chunk_size,
                                     mask_last_token, sm_scale, parts, token_keep, fuse_local,
-                                    fuse_weight, q_frags)
+                                    fuse_weight, q_frags, deterministic)
 
 
 @selected_attention.register_fake
 def _(q, kv_frags, weights, indices, key_valid, chunk_size, mask_last_token, sm_scale, parts,
-      token_keep, fuse_local, fuse_weight, q_frags=None):
+      token_keep, fuse_local, fuse_weight, q_frags=None, deterministic=False):
     return q.new_empty(q.shape, dtype=torch.bfloat16)
 
 

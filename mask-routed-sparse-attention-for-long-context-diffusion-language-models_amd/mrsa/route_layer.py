@@ -68,6 +68,13 @@ class RouteLayerConfig:
     token_budget: int = 0
     token_policy: str = "global_qk"
     min_tokens_per_chunk: int = 1
+    # Routed attention adds each output row's chunk terms in ascending chunk
+    # order (the same bits on every launch, eager or graph-captured) instead
+    # of in the order the waves reach the row.  None: on for the cached block
+    # step (where it costs nothing measurable), off for the full-sequence
+    # layer (where the waves then wait for each other's rows: ~1.6x the
+    # routed kernel's time at configuration 2).
+    deterministic: bool | None = None
 
 
 def _check_qkv(q, k, v, route_q):
@@ -175,12 +182,14 @@ def route_attention(
     # fuse_hils_outputs(remote, local_out, local_w) without materialising remote.
     out = selected_attention_launch(q, frags, remote_w, indices, kv_bool, S,
                                     token_keep=token_keep, fuse_local=local_out,
-                                    fuse_weight=local_w, q_frags=q_frags)
+                                    fuse_weight=local_w, q_frags=q_frags,
+                                    deterministic=bool(cfg.deterministic))
     _mark("selected_attention")
     if not return_intermediates:
         return out
     remote_out = selected_attention_launch(q, frags, remote_w, indices, kv_bool, S,
-                                           token_keep=token_keep)
+                                           token_keep=token_keep,
+                                           deterministic=bool(cfg.deterministic))
     return out, {
         "local_output": local_out, "local_lse": local_lse, "landmark_keys": lmk,
         "entropy": entropy, "prior_bias": prior, "indices": indices, "scores": scores,
@@ -461,13 +470,16 @@ def _cached_route_body(q, route_q, cache, query_positions, affected_chunks, entr
                 device=q.device, dtype=torch.float32).view(1, 1, Hkv, G)
         token_keep = _token_keep(cfg, q, cache.key, indices, cache.key_valid, entropy,
                                  cache.kv_frags)
+    # the fixed accumulation order is the default of the cached step
+    det = True if cfg.deterministic is None else bool(cfg.deterministic)
     out = selected_attention_launch(q, cache.kv_frags, remote_w, indices, cache.key_valid, S,
                                     token_keep=token_keep, fuse_local=local_out,
-                                    fuse_weight=local_w)
+                                    fuse_weight=local_w, deterministic=det)
     if not return_intermediates:
         return out
     remote_out = selected_attention_launch(q, cache.kv_frags, remote_w, indices,
-                                           cache.key_valid, S, token_keep=token_keep)
+                                           cache.key_valid, S, token_keep=token_keep,
+                                           deterministic=det)
     return out, {
         "local_output": local_out, "local_lse": local_lse, "indices": indices,
         "scores": scores, "remote_weights": remote_w, "local_weight": local_w,

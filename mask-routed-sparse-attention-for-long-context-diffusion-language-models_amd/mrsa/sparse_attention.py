@@ -16,6 +16,7 @@ from . import _lib
 
 
 FRAG_ELEMS = 16384  # bf16 per (batch, KV head, 64-key chunk)
+_ROUTED_FIXED_ORDER = 1  # MRSA_ROUTED_FIXED_ORDER
 
 
 def kv_fragments(k: torch.Tensor, v: torch.Tensor | None = None) -> torch.Tensor:
@@ -228,6 +229,7 @@ def selected_attention_launch(
     fuse_local: torch.Tensor | None = None,
     fuse_weight: torch.Tensor | None = None,
     q_frags: torch.Tensor | None = None,
+    deterministic: bool = False,
 ) -> torch.Tensor:
     """q [B, Lq, Hq, D], kv_frags = kv_fragments(k, v) of the Lk-row cache,
     weights [B, Lq, Hq, K] -> [B, Lq, Hq, D] bf16.
@@ -241,6 +243,9 @@ def selected_attention_launch(
     fuse_weight), bit for bit, without materialising the routed output.
     ``q_frags`` = q_fragments(q, Hkv) (with the fusion only) makes the kernel
     read the queries from their operand images: the same result.
+    ``deterministic`` adds every output row's chunk terms in ascending chunk
+    order (per-query tickets instead of the row lock): the same bits on every
+    launch, eager or graph-captured.
     """
 
     B, Lq, Hq, D = q.shape
@@ -269,12 +274,12 @@ def selected_attention_launch(
             raise ValueError(f"q_frags {tuple(q_frags.shape)} is not q_fragments(q, {Hkv})")
     return torch.ops.mrsa.selected_attention(
         q, kv_frags, weights, indices, key_valid, int(chunk_size), bool(mask_last_token),
-        float(sm_scale), parts, token_keep, fuse_local, fuse_weight, q_frags)
+        float(sm_scale), parts, token_keep, fuse_local, fuse_weight, q_frags, bool(deterministic))
 
 
 def _selected_attention_impl(q, kv_frags, weights, indices, key_valid, chunk_size,
                              mask_last_token, sm_scale, parts, token_keep, fuse_local,
-                             fuse_weight, q_frags=None):
+                             fuse_weight, q_frags=None, deterministic=False):
     B, Lq, Hq, D = q.shape
     Hkv, Lk = kv_frags.shape[1], kv_frags.shape[2] * 64
     K = indices.shape[-1]
@@ -284,6 +289,26 @@ def _selected_attention_impl(q, kv_frags, weights, indices, key_valid, chunk_siz
     idx = indices.to(torch.int32).contiguous()
     kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
     out = torch.empty(B, Lq, Hq, D, dtype=torch.bfloat16, device=q.device)
+    if deterministic:
+        lo = lw = keep = partial = qf = None
+        if fuse_local is not None:
+            lo = fuse_local.to(torch.bfloat16).contiguous()
+            lw = fuse_weight.to(torch.bfloat16).contiguous()
+        if token_keep is not None:
+            keep = token_keep.to(device=q.device, dtype=torch.int8).contiguous()
+        if parts > 1:
+            partial = torch.empty(parts, B, Lq, Hq, D, dtype=torch.float32, device=q.device)
+        if q_frags is not None:
+            qf = q_frags.contiguous()
+        st = _lib.call(
+            "mrsa_selected_attention_ex_fwd",
+            _lib.ptr(qc), _lib.ptr(qf), _lib.ptr(kf), _lib.ptr(w), _lib.ptr(idx), _lib.ptr(kv),
+            _lib.ptr(keep), _lib.ptr(lo), _lib.ptr(lw), B, Lq, Lk, Hq, Hkv, D, K,
+            int(chunk_size), 1 if mask_last_token else 0, float(sm_scale), parts,
+            _lib.ptr(partial), _ROUTED_FIXED_ORDER, _lib.ptr(out), _lib.stream_of(qc),
+        )
+        _lib.check(st, "selected_attention")
+        return out
     if fuse_local is not None:
         lo = fuse_local.to(torch.bfloat16).contiguous()
         lw = fuse_weight.to(torch.bfloat16).contiguous()

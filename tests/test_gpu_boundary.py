@@ -238,13 +238,21 @@ def test_per_op_drop_ins_reuse_the_kv_layout(monkeypatch):
     out1 = mrsa.selected_attention_g7_cached(q, k, v, w, idx, valid, S)
     out2 = mrsa.selected_attention_g7_cached(q, k, v, w, idx, valid, S)
     assert len(calls) == 1
-    fresh = SA.selected_attention_launch(q, real(k, v), w, idx, valid, S)
-    assert_nearly_identical(out1, fresh, "cached layout vs fresh")
-    assert_nearly_identical(out2, fresh, "cached layout, second call")
+    assert torch.equal(SA.kv_fragments_cached(k, v), real(k, v))  # the layout itself
+    fresh = SA.selected_attention_launch(q, real(k, v), w, idx, valid, S, deterministic=True)
+
+    def close(a, b, what):
+        err = (a.float() - b.float()).abs()
+        print(f"{what}: max {float(err.max()):.3e} mean {float(err.mean()):.3e}", flush=True)
+        assert float(err.max()) <= 2e-3 and float(err.mean()) <= 1e-5, what
+
+    close(out1, fresh, "cached layout vs fresh")
+    close(out2, fresh, "cached layout, second call")
     k[:, -1] += 1.0   # the cache is written in place: the layout is rebuilt
     out3 = mrsa.selected_attention_g7_cached(q, k, v, w, idx, valid, S)
     assert len(calls) == 2
-    fresh3 = SA.selected_attention_launch(q, real(k, v), w, idx, valid, S)
-    assert_nearly_identical(out3, fresh3, "layout after an in-place write")
+    assert torch.equal(SA.kv_fragments_cached(k, v), real(k, v))
+    close(out3, SA.selected_attention_launch(q, real(k, v), w, idx, valid, S, deterministic=True),
+          "layout after an in-place write")
     del loc1
     SA._FRAG_CACHE.clear()

@@ -847,3 +847,108 @@ def test_selected_attention_fused_with_q_fragments_matches():
     _assert_close_attn(b, ref, "fused with Q fragments vs oracle")
     with pytest.raises(ValueError):
         selected_attention_launch(*args, q_frags=qf)  # Q fragments need the fusion
+
+
+# -- fixed-order (deterministic) routed attention -------------------------
+def test_selected_attention_fixed_order_is_deterministic():
+    # Every output row adds its chunk terms in ascending chunk order: twenty
+    # launches of the contended shape (every query routes to every chunk, so
+    # the waves always share rows) give the same bits, with walk splits,
+    # keep rows, the fusion reading Q fragments and lists that are not
+    # ascending (a duplicated chunk, an entry past the chunks, a -1 end).
+    # With the bounded wait forced to one try, the deferred tiles replay in
+    # step order: the same bits again.
+    _note("fixed-order routed attention")
+    Lq, K, Hkv, G, D, Lk = 40, 32, 4, 7, 128, 2048
+    q = _rand((1, Lq, Hkv * G, D), 196).bfloat16()
+    k, v = _planted_kv(Lk, Hkv, D, 197)
+    idx = _sorted_routes(Lq, Hkv, K, Lk // 64, 198)
+    w = torch.softmax(_rand((1, Lq, Hkv * G, K), 199), -1).bfloat16()
+    valid = torch.ones(1, Lk, dtype=torch.bool)
+    valid[0, 900:903] = False
+    kf = mrsa.kv_fragments(k.to(DEV), v.to(DEV))
+    args = (q.to(DEV), kf, w.to(DEV), idx.to(DEV), valid.to(DEV), 64)
+    ref = O.selected_attention(q, k, v, w, idx, valid)
+    keep = (torch.rand(1, Lq, Hkv, K, 64, generator=torch.Generator().manual_seed(194))
+            < 0.8).to(torch.int8)
+    loc = _rand((1, Lq, Hkv * G, D), 193).bfloat16()
+    lw = torch.rand(1, Lq, Hkv * G).bfloat16()
+    qf = mrsa.q_fragments(q.to(DEV), Hkv)
+    cases = {
+        "plain": dict(parts=1),
+        "walk split": dict(parts=3),
+        "keep": dict(parts=1, token_keep=keep.to(DEV)),
+        "fused, Q fragments": dict(parts=1, fuse_local=loc.to(DEV), fuse_weight=lw.to(DEV),
+                                   q_frags=qf),
+    }
+    firsts = {}
+    for name, kw in cases.items():
+        outs = [selected_attention_launch(*args, deterministic=True, **kw) for _ in range(20)]
+        firsts[name] = outs[0]
+        for o in outs[1:]:
+            assert torch.equal(o, outs[0]), name
+    _assert_close_attn(firsts["plain"], ref, "fixed order vs oracle")
+    _assert_close_attn(firsts["walk split"], ref, "fixed order, walk split vs oracle")
+    assert_nearly_identical(firsts["plain"], selected_attention_launch(*args, parts=1),
+                            "fixed order vs locked order")
+    # lists that are not ascending
+    idx2 = idx.clone()
+    idx2[0, :, :, 5] = idx2[0, :, :, 9]          # a duplicated chunk
+    idx2[0, 3, :, 0] = Lk // 64 + 7              # an entry past the chunks
+    idx2[0, 4, :, 20:] = -1                      # a list that ends early
+    args2 = (q.to(DEV), kf, w.to(DEV), idx2.to(DEV), valid.to(DEV), 64)
+    o2 = [selected_attention_launch(*args2, parts=1, deterministic=True) for _ in range(10)]
+    for o in o2[1:]:
+        assert torch.equal(o, o2[0])
+    _assert_close_attn(o2[0], O.selected_attention(q, k, v, w, idx2, valid), "unsorted lists")
+    # deferred tiles replay in step order: the same bits
+    try:
+        mrsa.set_routed_lock_spin_limit(1)
+        for name in ("plain", "walk split"):
+            o = selected_attention_launch(*args, deterministic=True, **cases[name])
+            assert torch.equal(o, firsts[name]), f"{name} with deferred tiles"
+        mrsa.routed_lock_giveups(reset=True)
+    finally:
+        mrsa.set_routed_lock_spin_limit(65536)
+
+
+def test_selected_attention_fixed_order_graph_replays_match_eager():
+    _note("fixed-order routed attention in a HIP graph")
+    Lq, K, Hkv, G, D, Lk = 64, 32, 4, 7, 128, 4096
+    q = _rand((1, Lq, Hkv * G, D), 296).bfloat16().to(DEV)
+    k, v = _planted_kv(Lk, Hkv, D, 297)
+    idx = _sorted_routes(Lq, Hkv, K, Lk // 64, 298).to(DEV)
+    w = torch.softmax(_rand((1, Lq, Hkv * G, K), 299), -1).bfloat16().to(DEV)
+    valid = torch.ones(1, Lk, dtype=torch.bool, device=DEV)
+    kf = mrsa.kv_fragments(k.to(DEV), v.to(DEV))
+    eager = selected_attention_launch(q, kf, w, idx, valid, 64, parts=4, deterministic=True)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        selected_attention_launch(q, kf, w, idx, valid, 64, parts=4, deterministic=True)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gout = selected_attention_launch(q, kf, w, idx, valid, 64, parts=4, deterministic=True)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, eager)
+        again = selected_attention_launch(q, kf, w, idx, valid, 64, parts=4, deterministic=True)
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager)
+
+
+def test_route_layer_config2_fixed_order_twice_same_bits():
+    _note("route layer config 2, fixed order, two runs")
+    L, Hq, Hkv, D = 16384, 28, 4, 128
+    q = _rand((1, L, Hq, D), 390).bfloat16().to(DEV)
+    k, v = _planted_kv(L, Hkv, D, 391)
+    k, v = k.to(DEV), v.to(DEV)
+    cfg = mrsa.RouteLayerConfig(deterministic=True)
+    scale = torch.ones(Hq, device=DEV)
+    a = mrsa.route_attention(q, k, v, q, scale, cfg=cfg)
+    b = mrsa.route_attention(q, k, v, q, scale, cfg=cfg)
+    assert torch.equal(a, b)
+    c = mrsa.route_attention(q, k, v, q, scale)   # the default (lock) order
+    assert_nearly_identical(a, c, "config 2: fixed order vs lock order", atol=0.03)
