@@ -259,7 +259,7 @@ __device__ __forceinline__ void load_q(u32x4_t (&Qb)[4], __amdgpu_buffer_rsrc_t 
   for (int ks = 0; ks < 4; ++ks) Qb[ks] = bload(r, off, kstep * ks);
 }
 
-template <bool TOKEN, bool KEEP>
+template <bool TOKEN, bool KEEP, bool DET>
 __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   // Workgroup -> work unit, XCD-aware: workgroups are dealt to the 8 XCDs
@@ -278,7 +278,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
 
   const int K = a.K, G = a.G, tq = a.tq;
   const int64_t Ck = a.Ck;
-  const RaLayout L = ra_layout(tq, G, K, Ck, TOKEN, KEEP, a.det != 0);
+  const RaLayout L = ra_layout(tq, G, K, Ck, TOKEN, KEEP, DET);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -320,7 +320,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     qlen[i] = K;
     qflag[i] = 0u;
   }
-  if (a.det)
+  if (DET)
     for (int i = tid; i <= tq; i += kThreads) tick[i] = 0u;
   if (tid == 0) {
     *lock = 0u;
@@ -436,7 +436,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     const int pos = (int)s_rec[step_of[c]][1] + __popc(m & ((1u << qq) - 1u));
     it_q[pos] = (uint8_t)qq;
     it_slot[pos] = (uint8_t)kk;
-    if (a.det) {
+    if (DET) {
       // Rank of the item in its query's walk order: the query's distinct
       // listed chunks below c (the slot itself for a strictly ascending
       // list, whose skipped entries >= Ck all come last).  A walk part
@@ -657,7 +657,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   // the LDS completes one wave's operations in order): the lock bits back,
   // or in the fixed-order mode each owner's ticket to its next rank.
   auto release = [&](uint32_t want, uint32_t dwant) {
-    if (!a.det) {
+    if (!DET) {
       if (lane == 0) lds_and(lock_addr, ~want);
     } else if (lane == 0) {
       __hip_atomic_store(tick + (dwant & 63u), ((dwant >> 12) & 63u) + 1u, __ATOMIC_RELAXED,
@@ -681,7 +681,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   // tile (step st, tile t) is queued for the replay after the walk.
   auto add_locked = [&](float* srow, uint32_t want, int t, const u32x4_t (&Pb)[2]) {
     bool locked = false;
-    if (a.spin_limit > 0 && a.det) {
+    if (a.spin_limit > 0 && DET) {
       const uint32_t ia = want & 63u, ib = (want >> 6) & 63u;
       const uint32_t ra = (want >> 12) & 63u, rb = (want >> 18) & 63u;
       const bool hb2 = (want >> 24) & 1u;
@@ -788,7 +788,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     // the others OR 0 into words of their own.
     uint32_t first_try = 0u, tick_b = 0u;
     if constexpr (!TOKEN) {
-      if (a.det) {
+      if (DET) {
         // the owners' tickets (read now, compared after the softmax)
         first_try = __hip_atomic_load(tick + qa, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         tick_b = __hip_atomic_load(tick + (hb ? qb1 : qa), __ATOMIC_RELAXED,
@@ -843,7 +843,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       // and the rows are free when both tickets equal the ranks.
       uint32_t dwant = 0u;
       bool free_now;
-      if (a.det) {
+      if (DET) {
         const int ra = it_rank[i0 + 2 * t];
         const int rb = hb ? it_rank[i0 + 2 * t + 1] : 0;
         dwant = (uint32_t)qa | ((uint32_t)qb << 6) | ((uint32_t)ra << 12) | ((uint32_t)rb << 18) |
@@ -867,8 +867,8 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
         // tiles run; the last tile of the step adds it.  With both places
         // taken, wait for the rows now.
         const uint32_t took = want & ~seen;
-        if (!a.det && lane == 0 && a.spin_limit > 0 && took) lds_and(lock_addr, ~took);
-        if (a.det) want = dwant;
+        if (!DET && lane == 0 && a.spin_limit > 0 && took) lds_and(lock_addr, ~took);
+        if (DET) want = dwant;
         if (nset == 0) {
           set0[0] = Pb[0];
           set0[1] = Pb[1];
@@ -988,7 +988,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     const uint32_t nd = *dcount;
     if (nd > 0u) {
       if (wave == 0) {
-        if (a.det && nd > 1u) {
+        if (DET && nd > 1u) {
           // Fixed order: a query's deferred items are the tail of its walk
           // order (a later item waits for the ticket of an earlier one), so
           // replaying the queue in step order keeps each row's order.
@@ -1121,6 +1121,7 @@ int pick_tile(int G, int K, int64_t Ck, bool token, bool keep, bool det) {
 
 template <bool TOKEN, bool KEEP>
 int launch_routed(RaArgs& a, hipStream_t s) {
+  if (TOKEN && a.det) return MRSA_ERR_UNSUPPORTED;  // token scoring has no fixed-order walk
   const int tq = pick_tile(a.G, a.K, a.Ck, TOKEN, KEEP, a.det != 0);
   if (tq == 0) return MRSA_ERR_UNSUPPORTED;
   a.tq = tq;
@@ -1130,7 +1131,8 @@ int launch_routed(RaArgs& a, hipStream_t s) {
   if (grid > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
   const RaLayout l = ra_layout(tq, a.G, a.K, a.Ck, TOKEN, KEEP, a.det != 0);
   a.spin_limit = g_spin_limit;
-  auto kern = routed_attn_kernel<TOKEN, KEEP>;
+  // the fixed-order walk is its own instance, so the lock path carries none of its branches
+  auto kern = a.det ? routed_attn_kernel<TOKEN, KEEP, !TOKEN> : routed_attn_kernel<TOKEN, KEEP, false>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)l.total) != hipSuccess)
     return MRSA_ERR_LAUNCH;
