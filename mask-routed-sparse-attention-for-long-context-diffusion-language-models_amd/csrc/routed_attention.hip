@@ -644,15 +644,6 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     mskn = ((uint64_t)r[3] << 32) | r[2];
   };
 
-  // Adds a tile's P^T onto its owners' rows (srow: this lane's row slot)
-  // under the lock, waiting for it: the first try takes both bits at once;
-  // on a conflict the wave keeps the lower bit if that try took it, gives
-  // back the other and takes the missing bits one at a time, lowest first,
-  // with one-bit ORs (which change nothing while the bit is taken).  A wave
-  // only waits while holding bits below the one it waits for, so no cycle
-  // of waits forms, and no failed try leaves a bit set.  When the bounded
-  // wait runs out, the tile (step st, tile t) is queued for the replay after
-  // the walk.
   // Hands the owners' rows on after a tile's row writes (issued before it;
   // the LDS completes one wave's operations in order): the lock bits back,
   // or in the fixed-order mode each owner's ticket to its next rank.
