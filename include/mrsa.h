@@ -368,6 +368,27 @@ int mrsa_q_fragments(const void* q, int64_t batch, int64_t seq_len, int64_t q_he
                      int64_t kv_heads, int64_t head_dim, void* q_frags, void* stream);
 
 /*
+ * mrsa_kv_fragments and mrsa_chunk_attn_pool_gqa_strided_fwd (fused
+ * semantics) in one pass over the keys: each chunk's K and V rows are read
+ * once, laid out as fragments and K pooled against the chunk's landmark
+ * query rows.  Same outputs as the two calls, bit for bit.
+ *   k, v, kv_frags as in mrsa_kv_fragments (v required)
+ *   mu_q, mu_row_stride, key_valid, sm_scale, bias_scale, landmark_keys,
+ *   entropy, prior_bias as in mrsa_chunk_attn_pool_gqa_strided_fwd with
+ *   batch_chunks = batch * seq_len / 64 and chunk_size 64
+ * Limits: head_dim == 128, 2 <= groups <= 16 (groups == 1 pools with the
+ * dense torch semantics: use the two calls), seq_len % 64 == 0.
+ * No reference counterpart beyond the two it combines (the pool replaces
+ * chunk_attn_pool_gqa, ops/chunk_attn_pool_gqa_tilelang.py:425-448).
+ */
+int mrsa_kv_fragments_pool_fwd(const void* k, const void* v, const void* mu_q,
+                               int64_t mu_row_stride, const uint8_t* key_valid, int64_t batch,
+                               int64_t seq_len, int64_t kv_heads, int64_t groups,
+                               int64_t head_dim, float sm_scale, const float* bias_scale,
+                               void* kv_frags, void* landmark_keys, float* entropy,
+                               float* prior_bias, void* stream);
+
+/*
  * Bidirectional sliding-window GQA attention with natural-log LSE.
  * Replaces the flash-attn window call behind bidir_local_attention and
  * cached_local_attention (dream_dllm_hils/local_attention.py:67-200):

@@ -1,6 +1,7 @@
 // Layout helpers: the remote-route drop mask and the K / V fragments both
 // attention kernels read.
 #include "mrsa_device.h"
+#include "pool_wave.h"
 
 #include <algorithm>
 
@@ -155,6 +156,107 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// K/V fragments and the landmark pool of the same chunks in one pass
+// (kv_fragments_kernel + the matrix-core pool): a workgroup per (chunk, KV
+// head, batch) stages the chunk's K and V rows in LDS once, writes the
+// fragments and pools K against the chunk's landmark-slot query rows.  The
+// pool is split over the four waves -- wave w takes keys 16 w .. 16 w + 15
+// and landmark dims 32 w .. 32 w + 31 -- with the column max, sum and
+// entropy partials and the P blocks exchanged through LDS (pool_wave.h
+// fixes the summation order, so the bits equal the one-wave pool's).  The
+// fragment stores are issued between the exchanges.  Needs whole chunks (L a
+// multiple of 64).
+struct PitchRows {
+  const uint16_t* ks;
+  __device__ u32x4_t row16(int key, int blk) const {
+    return *reinterpret_cast<const u32x4_t*>(ks + key * kFragPitch + 8 * blk);
+  }
+  __device__ uint32_t elem(int key, int dim) const { return ks[key * kFragPitch + dim]; }
+};
+
+__global__ void __launch_bounds__(256)
+    kv_fragments_pool_kernel(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                             int64_t L, int64_t H, int64_t NT, uint16_t* __restrict__ frags,
+                             const uint16_t* __restrict__ mu_q, int64_t mu_stride,
+                             const uint8_t* __restrict__ key_valid, int G, float sm_scale,
+                             const float* __restrict__ bias_scale, uint16_t* __restrict__ lmk,
+                             float* __restrict__ entropy, float* __restrict__ prior) {
+  __shared__ __align__(16) uint16_t ks_[64 * kFragPitch];
+  __shared__ __align__(16) uint16_t vs_[64 * kFragPitch];
+  __shared__ float red[3][4][16];       // column max, sum, sum p ln p of each key block
+  __shared__ __align__(16) u32x2_t pbl[4][64];  // bf16 P of each key block, per lane
+  const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int j = lane & 15, grp = lane >> 4;
+  const int64_t bc = b * NT + c;
+  for (int p = tid; p < 1024; p += 256) {
+    const int r = p >> 4, u = p & 15;
+    const int64_t off = ((b * L + c * 64 + r) * H + h) * 128 + 8 * u;
+    *reinterpret_cast<u32x4_t*>(ks_ + r * kFragPitch + 8 * u) =
+        *reinterpret_cast<const u32x4_t*>(k + off);
+    *reinterpret_cast<u32x4_t*>(vs_ + r * kFragPitch + 8 * u) =
+        *reinterpret_cast<const u32x4_t*>(v + off);
+  }
+  u32x4_t Qb[4];
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) {
+    Qb[q4] = u32x4_t{0u, 0u, 0u, 0u};
+    if (j < G)
+      Qb[q4] = *reinterpret_cast<const u32x4_t*>(mu_q + bc * mu_stride +
+                                                 (int64_t)(h * G + j) * 128 + 32 * q4 + 8 * grp);
+  }
+  const uint64_t real = __builtin_amdgcn_ballot_w64(key_valid[bc * 64 + lane] != 0) & ~(1ull << 63);
+  const bool chunk_valid = real != 0ull;
+  __syncthreads();
+  const PitchRows rows{ks_};
+  uint16_t* dst = frags + ((b * H + h) * NT + c) * (int64_t)kFragElems;
+  // fragment pieces p = tid + 256 i: K 16 bytes of one key row, V one dim of
+  // 8 keys in the tiled order
+  auto frag_piece = [&](int p) {
+    const int i = p >> 6, l = p & 63, jj = l & 15, gg = l >> 4;
+    const int mt = i >> 2, kq = i & 3;
+    *reinterpret_cast<u32x4_t*>(dst + 8 * p) =
+        *reinterpret_cast<const u32x4_t*>(ks_ + (16 * mt + jj) * kFragPitch + 32 * kq + 8 * gg);
+    const int nt = i >> 1, kv = i & 1, d = 16 * nt + jj;
+    u32x4_t xv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r0 = 32 * kv + 16 * (e >> 1) + 4 * gg + 2 * (e & 1);
+      xv[e] = (uint32_t)vs_[r0 * kFragPitch + d] | ((uint32_t)vs_[(r0 + 1) * kFragPitch + d] << 16);
+    }
+    *reinterpret_cast<u32x4_t*>(dst + 8192 + 8 * p) = xv;
+  };
+  f32x4_t S = pool_logits(rows, Qb, real, sm_scale, w, lane);
+  const float bmax = across4_max(pool_max4(S));
+  if (grp == 0) red[0][w][j] = bmax;
+  frag_piece(tid);
+  frag_piece(tid + 256);
+  __syncthreads();
+  const float mx = fmaxf(fmaxf(red[0][0][j], red[0][1][j]), fmaxf(red[0][2][j], red[0][3][j]));
+  const float bsum = pool_exp(S, mx);
+  if (grp == 0) red[1][w][j] = bsum;
+  frag_piece(tid + 512);
+  frag_piece(tid + 768);
+  __syncthreads();
+  const float sum = ((red[1][0][j] + red[1][1][j]) + red[1][2][j]) + red[1][3][j];
+  const float bt = pool_prob(S, sum);
+  if (grp == 0) red[2][w][j] = bt;
+  pbl[w][lane] = u32x2_t{pack_bf16x2(S[0], S[1]), pack_bf16x2(S[2], S[3])};
+  __syncthreads();
+  if (w == 0)
+    pool_stats(((red[2][0][j] + red[2][1][j]) + red[2][2][j]) + red[2][3][j], chunk_valid, G,
+               (bc * H + h) * G, bias_scale, (int)h * G, entropy, prior, lane);
+  u32x4_t Pb[2];
+#pragma unroll
+  for (int k2 = 0; k2 < 2; ++k2) {
+    const u32x2_t lo = pbl[2 * k2][lane], hi = pbl[2 * k2 + 1][lane];
+    Pb[k2] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+  }
+  uint16_t* lrow = lmk + (bc * H + h) * G * 128;
+  pool_lmk(rows, Pb, 2 * w, chunk_valid, G, lrow, lane);
+  pool_lmk(rows, Pb, 2 * w + 1, chunk_valid, G, lrow, lane);
+}
+
 }  // namespace
 
 extern "C" int mrsa_remote_drop_mask(const uint8_t* valid_mask, const uint8_t* allowed_mask,
@@ -213,6 +315,38 @@ extern "C" int mrsa_kv_fragments(const void* k, const void* v, int64_t batch, in
   hipLaunchKernelGGL(kv_fragments_kernel, dim3((unsigned)NT, (unsigned)kv_heads, (unsigned)batch),
                      dim3(256), 0, (hipStream_t)stream, (const uint16_t*)k, (const uint16_t*)v,
                      seq_len, kv_heads, NT, (uint16_t*)kv_frags);
+  return mrsa_launch_status();
+}
+
+extern "C" int mrsa_kv_fragments_pool_fwd(const void* k, const void* v, const void* mu_q,
+                                          int64_t mu_row_stride, const uint8_t* key_valid,
+                                          int64_t batch, int64_t seq_len, int64_t kv_heads,
+                                          int64_t groups, int64_t head_dim, float sm_scale,
+                                          const float* bias_scale, void* kv_frags,
+                                          void* landmark_keys, float* entropy,
+                                          float* prior_bias, void* stream) {
+  if (batch < 0 || seq_len < 0 || kv_heads <= 0 || groups <= 0 || head_dim <= 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if ((prior_bias != nullptr) != (bias_scale != nullptr)) return MRSA_ERR_INVALID_ARGUMENT;
+  if (mu_row_stride < kv_heads * groups * head_dim) return MRSA_ERR_INVALID_ARGUMENT;
+  // groups == 1 takes the reference's dense torch twin, which this kernel
+  // does not restate (mrsa_chunk_attn_pool_gqa_fwd does)
+  if (head_dim != 128 || groups < 2 || groups > 16 || seq_len % 64 != 0)
+    return MRSA_ERR_UNSUPPORTED;
+  if (batch == 0 || seq_len == 0) return MRSA_OK;
+  if (!k || !v || !mu_q || !key_valid || !kv_frags || !landmark_keys || !entropy)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)kv_frags | (uintptr_t)mu_q |
+       (uintptr_t)landmark_keys) % 16 != 0 || mu_row_stride % 8 != 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  const int64_t NT = seq_len / 64;
+  if (kv_heads > 65535 || batch > 65535 || NT > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(kv_fragments_pool_kernel,
+                     dim3((unsigned)NT, (unsigned)kv_heads, (unsigned)batch), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)k, (const uint16_t*)v, seq_len,
+                     kv_heads, NT, (uint16_t*)kv_frags, (const uint16_t*)mu_q, mu_row_stride,
+                     key_valid, (int)groups, sm_scale, bias_scale, (uint16_t*)landmark_keys,
+                     entropy, prior_bias);
   return mrsa_launch_status();
 }
 

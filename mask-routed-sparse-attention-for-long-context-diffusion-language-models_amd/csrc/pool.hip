@@ -16,6 +16,7 @@
 // chunk gives zero probabilities (nan_to_num) and the pooling uses fp32
 // probabilities.
 #include "mrsa_device.h"
+#include "pool_wave.h"
 
 using namespace mrsa;
 
@@ -158,21 +159,22 @@ __global__ void __launch_bounds__(kThreads)
 
 // Matrix-core pool for the fused semantics at chunk_size 64, head_dim 128 and
 // up to 16 query heads per KV head: one wave per (chunk, KV head), four per
-// workgroup, the same formulas as pool_kernel above.
-//   staging: the chunk's 64 key rows in the wave's LDS rows (256 bytes per
-//            key; 16-byte block b of a row stored at b ^ (key & 15));
-//   logits:  S^T = K . Q^T on the matrix cores (A: key rows from LDS, B: the
-//            query heads as 16 columns, heads >= G zero); lane (grp, j):
-//            keys 16 mt + 4 grp + r of head j;
-//   softmax and entropy per column over its lane group's 16 keys and the
-//            four lane groups;
-//   pooling: lmk^T = K^T . P^T with P rounded to bf16 and packed in the
-//            tiled key order (reduction index 8 grp + e of k-step ks is key
-//            32 ks + 16 (e >> 2) + 4 grp + (e & 3)); the K^T operand is read
-//            from the staged rows in the same order.
+// workgroup, the same formulas as pool_kernel above (pool_wave).  The
+// chunk's 64 key rows are staged in the wave's LDS rows (256 bytes per key;
+// 16-byte block b of a row stored at b ^ (key & 15)).
 constexpr int kPoolWaves = 4;
 
 __device__ __forceinline__ int pool_blk(int key, int blk) { return blk ^ (key & 15); }
+
+struct SwizzledRows {
+  const uint16_t* ks;
+  __device__ u32x4_t row16(int key, int blk) const {
+    return *reinterpret_cast<const u32x4_t*>(ks + key * 128 + 8 * pool_blk(key, blk));
+  }
+  __device__ uint32_t elem(int key, int dim) const {
+    return ks[key * 128 + 8 * pool_blk(key, dim >> 3) + (dim & 7)];
+  }
+};
 
 __global__ void __launch_bounds__(64 * kPoolWaves)
     pool_mfma_kernel(const uint16_t* __restrict__ mu_q, int64_t mu_stride,
@@ -204,97 +206,9 @@ __global__ void __launch_bounds__(64 * kPoolWaves)
                                                  32 * q4 + 8 * grp);
   }
   const uint64_t vbits = __builtin_amdgcn_ballot_w64(key_valid[bc * 64 + lane] != 0);
-  const uint64_t real = vbits & ~(1ull << 63);
-  const bool chunk_valid = real != 0ull;
   // The staged rows are read by this wave only (LDS keeps its order).
-  f32x4_t S[4];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    S[mt] = zero4();
-    const int key = 16 * mt + j;
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const u32x4_t A = *reinterpret_cast<const u32x4_t*>(ks + key * 128 + 8 * pool_blk(key, 4 * q4 + grp));
-      S[mt] = mfma_bf16_16x16x32(A, Qb[q4], S[mt]);
-    }
-  }
-  float mx = neg_inf();
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int sk = 16 * mt + 4 * grp + r;
-      const bool rl = (real >> sk) & 1ull;
-      const float lg = (rl && chunk_valid) ? S[mt][r] * sm_scale : (sk == 0 ? 0.f : neg_inf());
-      S[mt][r] = lg;
-      mx = fmaxf(mx, lg);
-    }
-  mx = across4_max(mx);
-  float sum = 0.f;
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float e = (mx != neg_inf() && S[mt][r] != neg_inf()) ? exp2f((S[mt][r] - mx) * kLog2e)
-                                                                 : 0.f;
-      S[mt][r] = e;
-      sum += e;
-    }
-  sum = across4_sum(sum);
-  float t = 0.f;
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float pr = sum > 0.f ? S[mt][r] / sum : 0.f;
-      t += pr > 0.f ? pr * logf(pr) : 0.f;
-      S[mt][r] = pr;
-    }
-  const float ent = -across4_sum(t);
-  if (grp == 0 && j < G) {
-    const float e_out = chunk_valid ? ent : 0.f;
-    const int64_t o = (bc * H + h) * G + j;
-    entropy[o] = e_out;
-    if (prior) prior[o] = e_out * bias_scale[h * G + j];
-  }
-  u32x4_t Pb[2];
-#pragma unroll
-  for (int k2 = 0; k2 < 2; ++k2) {
-    Pb[k2][0] = pack_bf16x2(S[2 * k2][0], S[2 * k2][1]);
-    Pb[k2][1] = pack_bf16x2(S[2 * k2][2], S[2 * k2][3]);
-    Pb[k2][2] = pack_bf16x2(S[2 * k2 + 1][0], S[2 * k2 + 1][1]);
-    Pb[k2][3] = pack_bf16x2(S[2 * k2 + 1][2], S[2 * k2 + 1][3]);
-  }
-  uint16_t* lrow = lmk + ((bc * H + h) * G + j) * 128;
-#pragma unroll
-  for (int nt = 0; nt < 8; ++nt) {
-    const int dim = 16 * nt + j;
-    f32x4_t acc = zero4();
-#pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      u32x4_t A;
-#pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        uint32_t pr = 0u;
-#pragma unroll
-        for (int h1 = 0; h1 < 2; ++h1) {
-          const int e = 2 * e2 + h1;
-          const int key = 32 * k2 + 16 * (e >> 2) + 4 * grp + (e & 3);
-          const uint32_t x = ks[key * 128 + 8 * pool_blk(key, dim >> 3) + (dim & 7)];
-          pr |= x << (16 * h1);
-        }
-        A[e2] = pr;
-      }
-      acc = mfma_bf16_16x16x32(A, Pb[k2], acc);
-    }
-    // lane (grp, j): dims 16 nt + 4 grp .. + 3 of head j
-    if (j < G) {
-      u32x2_t o;
-      o[0] = chunk_valid ? pack_bf16x2(acc[0], acc[1]) : 0u;
-      o[1] = chunk_valid ? pack_bf16x2(acc[2], acc[3]) : 0u;
-      *reinterpret_cast<u32x2_t*>(lrow + 16 * nt + 4 * grp) = o;
-    }
-  }
+  pool_wave(SwizzledRows{ks}, Qb, vbits & ~(1ull << 63), G, sm_scale, (bc * H + h) * G,
+            bias_scale, h * G, lmk, entropy, prior, lane);
 }
 }  // namespace
 

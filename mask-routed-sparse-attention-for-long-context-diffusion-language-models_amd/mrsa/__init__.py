@@ -32,7 +32,8 @@ from .kernel_utils import (
     remote_drop_mask_rows,
 )
 from .local_attention import bidir_local_attention, cached_local_attention
-from .pool import chunk_attn_pool_gqa, chunk_attn_pool_gqa_backward, chunk_attn_pool_gqa_prior
+from .pool import (chunk_attn_pool_gqa, chunk_attn_pool_gqa_backward, chunk_attn_pool_gqa_prior,
+                   kv_fragments_pool)
 from .route_layer import (
     CachedBlockStep,
     LayerKVCache,
@@ -97,6 +98,7 @@ __all__ = [
     "swa_attention",
     "kv_fragments",
     "q_fragments",
+    "kv_fragments_pool",
     "RoutedLockTimeout",
     "check_routed_locks",
     "routed_lock_giveups",

@@ -87,6 +87,10 @@ SIGNATURES = {
     "mrsa_kv_fragments_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "mrsa_kv_fragments": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P, _P]),
     "mrsa_kv_fragments_rows": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P]),
+    "mrsa_kv_fragments_pool_fwd": (
+        _I,
+        [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P, _P, _P],
+    ),
     "mrsa_q_fragments_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "mrsa_q_fragments": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P]),
     "mrsa_local_attention_fwd": (

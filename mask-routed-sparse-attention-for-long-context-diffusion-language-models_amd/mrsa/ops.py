@@ -23,7 +23,7 @@ from torch import Tensor
 from .fusion import _fuse_bwd_impl, _fuse_impl
 from .kernel_utils import _drop_mask_impl, _drop_mask_rows_impl
 from .local_attention import _local_attention_impl
-from .pool import _pool_bwd_impl, _pool_impl
+from .pool import _kv_fragments_pool_impl, _pool_bwd_impl, _pool_impl
 from .route_weights import _route_weights_bwd_impl, _route_weights_impl
 from .local_attention import _local_attention_qf_impl
 from .sparse_attention import (FRAG_ELEMS, _kv_fragments_impl, _kv_fragments_rows_impl,
@@ -122,6 +122,22 @@ def _(mu_q, k_chunked, key_valid, sm_scale, bias_scale):
     prior = (entropy.new_empty(B, C, H, G) if bias_scale is not None
              else entropy.new_empty(0))
     return mu_q.new_empty(mu_q.shape, dtype=torch.bfloat16), entropy, prior
+
+
+@_op("kv_fragments_pool")
+def kv_fragments_pool(k: Tensor, v: Tensor, mu_q: Tensor, key_valid: Tensor, sm_scale: float,
+                      bias_scale: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    return _kv_fragments_pool_impl(k, v, mu_q, key_valid, sm_scale, bias_scale)
+
+
+@kv_fragments_pool.register_fake
+def _(k, v, mu_q, key_valid, sm_scale, bias_scale):
+    B, L, H, _ = k.shape
+    _, C, _, G, _ = mu_q.shape
+    entropy = mu_q.new_empty(B, C, H, G, dtype=torch.float32)
+    return (k.new_empty(B, H, (L + 63) // 64, FRAG_ELEMS, dtype=torch.bfloat16),
+            mu_q.new_empty(mu_q.shape, dtype=torch.bfloat16), entropy,
+            entropy.new_empty(B, C, H, G))
 
 
 @_op("chunk_attn_pool_bwd")
@@ -350,7 +366,7 @@ def _(entropy, indices):
 
 OPERATORS = (
     "kv_fragments", "kv_fragments_rows_", "q_fragments", "local_attention",
-    "local_attention_qf", "chunk_attn_pool",
+    "local_attention_qf", "chunk_attn_pool", "kv_fragments_pool",
     "chunk_attn_pool_bwd", "route_topk", "route_score_bwd", "route_weights", "route_weights_bwd",
     "selected_attention", "selected_attention_bwd", "fuse_hils_outputs", "fuse_hils_outputs_bwd",
     "remote_drop_mask",

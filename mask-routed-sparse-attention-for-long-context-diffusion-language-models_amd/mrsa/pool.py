@@ -47,20 +47,74 @@ def _launch(mu_q, k_chunked, key_valid, sm_scale, bias_scale=None):
     return lmk, entropy, (prior if bias_scale is not None else None)
 
 
-def _pool_impl(mu_q, k_chunked, key_valid, sm_scale, bias_scale):
-    """Kernel call; the prior output is empty without a bias scale."""
+def _mu_rows(mu_q):
+    """(tensor, row stride) of the landmark query rows [B, C, Hkv, G, D].
+    They are read in place when each row's [Hkv, G, D] is contiguous and
+    batch and chunk fold into one row stride (e.g. the mask-token rows
+    route_q[:, S - 1::S] of the route queries): no gather copy."""
     batch, chunks, kv_heads, groups, head_dim = mu_q.shape
-    chunk_size = k_chunked.shape[2]
-    # Query rows are read in place when each row's [Hkv, G, D] is contiguous
-    # and batch and chunk fold into one row stride (e.g. the mask-token rows
-    # route_q[:, S - 1::S] of the route queries): no gather copy.
     st_ = mu_q.stride()
     inner = st_[4] == 1 and st_[3] == head_dim and st_[2] == groups * head_dim
     folds = batch == 1 or st_[0] == chunks * st_[1]
     if inner and folds and st_[1] >= kv_heads * groups * head_dim and mu_q.dtype == torch.bfloat16:
-        mu, row_stride = mu_q, st_[1]
-    else:
-        mu, row_stride = mu_q.contiguous(), kv_heads * groups * head_dim
+        return mu_q, st_[1]
+    return mu_q.contiguous(), kv_heads * groups * head_dim
+
+
+def _kv_fragments_pool_impl(k, v, mu_q, key_valid, sm_scale, bias_scale):
+    """K/V fragments of k, v [B, L, Hkv, 128] and the landmark pool of
+    mu_q [B, L / 64, Hkv, G, 128] over the same chunks (fused semantics),
+    in one kernel: (kv_frags, landmark_keys, entropy, prior_bias)."""
+    B, L, H, D = k.shape
+    _, C, _, G, _ = mu_q.shape
+    kc, vc = k.contiguous(), v.contiguous()
+    mu, row_stride = _mu_rows(mu_q)
+    kv = key_valid.to(device=k.device, dtype=torch.bool).contiguous()
+    frags = torch.empty(B, H, C, 16384, dtype=torch.bfloat16, device=k.device)
+    lmk = torch.empty(mu_q.shape, dtype=torch.bfloat16, device=k.device)
+    entropy = torch.empty(B, C, H, G, device=k.device, dtype=torch.float32)
+    scale = bias_scale.to(device=k.device, dtype=torch.float32).contiguous()
+    prior = torch.empty_like(entropy)
+    st = _lib.call(
+        "mrsa_kv_fragments_pool_fwd",
+        _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(mu), int(row_stride), _lib.ptr(kv),
+        B, L, H, G, D, float(sm_scale), _lib.ptr(scale), _lib.ptr(frags), _lib.ptr(lmk),
+        _lib.ptr(entropy), _lib.ptr(prior), _lib.stream_of(kc),
+    )
+    _lib.check(st, "kv_fragments_pool")
+    return frags, lmk, entropy, prior
+
+
+def kv_fragments_pool(k, v, mu_q, key_valid, entropy_bias_scale, sm_scale=None):
+    """kv_fragments(k, v) and chunk_attn_pool_gqa_prior(mu_q, k chunked,
+    key_valid chunked, entropy_bias_scale) in one pass over the keys (same
+    bits).  k, v [B, L, Hkv, 128] bf16 with L a multiple of 64; mu_q
+    [B, L / 64, Hkv, G, 128] bf16, 2 <= G <= 16; key_valid [B, L].
+    Returns (kv_frags, landmark_keys, entropy, prior_bias); no autograd."""
+
+    B, L, H, D = k.shape
+    if v is None or v.shape != k.shape or D != 128 or L % 64:
+        raise ValueError("kv_fragments_pool requires k, v [B, L, Hkv, 128] with L % 64 == 0")
+    if mu_q.ndim != 5 or tuple(mu_q.shape[:3]) != (B, L // 64, H) or mu_q.shape[4] != D:
+        raise ValueError(f"mu_q must be [B, L / 64, Hkv, G, 128], got {tuple(mu_q.shape)}")
+    G = mu_q.shape[3]
+    if not 2 <= G <= 16:
+        raise ValueError(f"kv_fragments_pool needs 2 <= groups <= 16, got {G}")
+    if tuple(key_valid.shape) != (B, L):
+        raise ValueError(f"key_valid must be [B, L] = {(B, L)}, got {tuple(key_valid.shape)}")
+    if entropy_bias_scale.numel() != H * G:
+        raise ValueError(f"bias_scale must have {H * G} elements, got {entropy_bias_scale.numel()}")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    return torch.ops.mrsa.kv_fragments_pool(k, v, mu_q, key_valid, float(sm_scale),
+                                            entropy_bias_scale)
+
+
+def _pool_impl(mu_q, k_chunked, key_valid, sm_scale, bias_scale):
+    """Kernel call; the prior output is empty without a bias scale."""
+    batch, chunks, kv_heads, groups, head_dim = mu_q.shape
+    chunk_size = k_chunked.shape[2]
+    mu, row_stride = _mu_rows(mu_q)
     kc = k_chunked.contiguous()
     kv = key_valid.to(device=mu_q.device, dtype=torch.bool).contiguous()
     lmk = torch.empty(mu_q.shape, dtype=torch.bfloat16, device=mu_q.device)

@@ -38,7 +38,7 @@ import torch
 
 from .kernel_utils import drop_mask_rows_launch
 from .local_attention import key_parts, local_attention_launch, local_attention_qf_launch
-from .pool import chunk_attn_pool_gqa_prior
+from .pool import _needs_grad, chunk_attn_pool_gqa_prior, kv_fragments_pool
 from .route_weights import route_weights_launch
 from .sparse_attention import (FRAG_ELEMS, kv_fragments, kv_fragments_cached, kv_fragments_rows,
                                selected_attention_launch)
@@ -131,7 +131,15 @@ def route_attention(
         kv_bool = key_valid.to(device=q.device, dtype=torch.bool).contiguous()
 
     _mark("start")
-    frags = kv_fragments(k, v)
+    q_lmk = route_q[:, S - 1 :: S].reshape(B, C, Hkv, G, D)
+    # K/V fragments and the landmark pool in one pass over the keys when the
+    # pool takes the fused semantics (G >= 2) and no gradient is asked for
+    fused_pool = (S == 64 and D == 128 and 2 <= G <= 16
+                  and not _needs_grad(route_q, k, entropy_bias_scale))
+    if fused_pool:
+        frags, lmk, entropy, prior = kv_fragments_pool(k, v, q_lmk, kv_bool, entropy_bias_scale)
+    else:
+        frags = kv_fragments(k, v)
     _mark("kv_fragments")
     flash_window = cfg.local_window + S - 1 if cfg.skip_inert_slots else cfg.local_window
     q_frags = None
@@ -145,11 +153,11 @@ def route_attention(
             q, frags, kv_bool, flash_window, S if cfg.skip_inert_slots else 0
         )
     _mark("local_attention")
-    q_lmk = route_q[:, S - 1 :: S].reshape(B, C, Hkv, G, D)
-    k_chunked = k.reshape(B, C, S, Hkv, D)
-    lmk, entropy, prior = chunk_attn_pool_gqa_prior(
-        q_lmk, k_chunked, kv_bool.reshape(B, C, S), entropy_bias_scale
-    )
+    if not fused_pool:
+        k_chunked = k.reshape(B, C, S, Hkv, D)
+        lmk, entropy, prior = chunk_attn_pool_gqa_prior(
+            q_lmk, k_chunked, kv_bool.reshape(B, C, S), entropy_bias_scale
+        )
     _mark("pool")
     indices, scores = route_topk_launch(
         route_q.reshape(B, L, Hkv, G, D),

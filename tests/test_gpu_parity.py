@@ -154,6 +154,34 @@ def test_pool_vs_oracle(G, dense):
     assert torch.equal(lmk2, lmk) and torch.equal(ent2, ent)
 
 
+@pytest.mark.parametrize("B,L,H,G", [(1, 2048, 4, 7), (2, 640, 3, 16), (1, 320, 2, 2),
+                                     (2, 1024, 1, 8)])
+def test_kv_fragments_pool_equals_the_two_ops(B, L, H, G):
+    # One pass over the keys: the same fragments and the same pool outputs,
+    # bit for bit, as kv_fragments + chunk_attn_pool_gqa_prior, with the
+    # landmark query rows read in place from the route queries; invalid keys,
+    # a fully invalid chunk and an invalid landmark slot included.
+    _note(f"kv fragments + pool in one pass B={B} L={L} H={H} G={G}")
+    from mrsa.pool import kv_fragments_pool
+    D, C = 128, L // 64
+    k = _rand((B, L, H, D), 11).bfloat16().to(DEV)
+    v = _rand((B, L, H, D), 12).bfloat16().to(DEV)
+    route_q = _rand((B, L, H * G, D), 13).bfloat16().to(DEV)
+    valid = torch.rand(B, L, generator=torch.Generator().manual_seed(14)) > 0.1
+    valid[0, 64:128] = False
+    valid[-1, 63] = False
+    valid = valid.to(DEV)
+    scale = (torch.rand(H * G) + 0.5).to(DEV)
+    mu = route_q[:, 63::64].reshape(B, C, H, G, D)
+    frags, lmk, ent, prior = kv_fragments_pool(k, v, mu, valid, scale)
+    lmk2, ent2, prior2 = mrsa.chunk_attn_pool_gqa_prior(mu, k.reshape(B, C, 64, H, D),
+                                                        valid.reshape(B, C, 64), scale)
+    assert torch.equal(frags.view(torch.int16), mrsa.kv_fragments(k, v).view(torch.int16))
+    assert torch.equal(lmk.view(torch.int16), lmk2.view(torch.int16))
+    assert torch.equal(ent, ent2) and torch.equal(prior, prior2)
+    assert float(lmk[0, 1].abs().max()) == 0.0 and float(ent[0, 1].abs().max()) == 0.0
+
+
 def _route_case(L, C, G, Hkv, seed, derive=False, drop_frac=0.2):
     D = 128
     q5 = _rand((1, L, Hkv, G, D), seed).bfloat16()

@@ -45,9 +45,11 @@ def test_route_layer_exports_as_one_graph(topk):
         ep = torch.export.export(_RouteLayer(cfg), args, strict=True)
     called = {n.target for n in ep.graph.nodes if n.op == "call_function"}
     names = {str(t) for t in called}
-    for op in ("kv_fragments", "chunk_attn_pool", "route_topk", "route_weights",
-               "selected_attention"):
+    for op in ("route_topk", "route_weights", "selected_attention"):
         assert f"mrsa.{op}.default" in names, (op, sorted(names))
+    # K/V fragments and the landmark pool: one pass, or the two ops
+    assert ("mrsa.kv_fragments_pool.default" in names
+            or {"mrsa.kv_fragments.default", "mrsa.chunk_attn_pool.default"} <= names), sorted(names)
     # the window attention, with its Q-fragment by-product when it runs unsplit
     assert names & {"mrsa.local_attention.default", "mrsa.local_attention_qf.default"}
     out = [n for n in ep.graph.nodes if n.op == "output"][0]
