@@ -45,8 +45,10 @@ __device__ __forceinline__ float row_lanes_sum(float v) {
 }
 
 // I: the index type (uint32_t when every index of the call fits 32 bits,
-// which turns the row decode's divisions into 32-bit ones).
-template <int LPR, bool VEC, class I>
+// which turns the row decode's divisions into 32-bit ones).  VEC: topk is a
+// multiple of 8 (every lane's 8 slots are real).  UNIT_T: temperature 1 (no
+// 1 / T products).
+template <int LPR, bool VEC, bool UNIT_T, class I>
 __device__ __forceinline__ void route_weights_row(
     int64_t t64, const uint16_t* __restrict__ scores,
     const int32_t* __restrict__ indices, const float* __restrict__ bias,
@@ -97,16 +99,16 @@ __device__ __forceinline__ void route_weights_row(
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int32_t c = iv[j];
-    const bool ok = k0 + j < K && c >= 0 && (I)c < C;
+    const bool ok = (VEC || k0 + j < K) && c >= 0 && (I)c < C;
     const float bv = brow[(ok ? (I)c : (I)0) * cstride];
     const float s = (j & 1) ? bf16_hi(sv[j >> 1]) : bf16_lo(sv[j >> 1]);
-    x[j] = ok ? (s + bv) * inv_t : neg_inf();
+    x[j] = ok ? (UNIT_T ? s + bv : (s + bv) * inv_t) : neg_inf();
     rmax = fmaxf(rmax, x[j]);
   }
   rmax = row_lanes_max<LPR>(rmax);
   float local = lse[r];
   if (has_off && !affine) local -= off;
-  local *= inv_t;
+  if (!UNIT_T) local *= inv_t;
 
   // Every lane of a row takes the same branch (m and rmax are row-uniform),
   // so the reductions inside the branches stay within active lanes.
@@ -188,7 +190,7 @@ __device__ __forceinline__ void route_weights_row(
   if (part == 0) lw[r] = (uint16_t)f32_to_bf16(lw_val);
 }
 
-template <int LPR, bool VEC, class I>
+template <int LPR, bool VEC, bool UNIT_T, class I>
 __global__ void __launch_bounds__(256)
     route_weights_kernel(const uint16_t* __restrict__ scores, const int32_t* __restrict__ indices,
                          const float* __restrict__ bias, const float* __restrict__ lse,
@@ -201,7 +203,7 @@ __global__ void __launch_bounds__(256)
   const int has_off = goff != nullptr, affine = gsc != nullptr;
   const float off = has_off ? *goff : 0.f;
   const float gscale = affine ? *gsc : 1.f;
-  route_weights_row<LPR, VEC, I>((int64_t)blockIdx.x * blockDim.x + threadIdx.x, scores, indices,
+  route_weights_row<LPR, VEC, UNIT_T, I>((int64_t)blockIdx.x * blockDim.x + threadIdx.x, scores, indices,
                               bias, lse, rows, L, C, Hkv, G, K, inv_t, has_off, affine, off,
                               gscale, rw, lw, gate_logit);
 }
@@ -216,10 +218,13 @@ int launch_rw(bool vec, hipStream_t s, const uint16_t* scores, const int32_t* in
   // 32-bit indices when the largest flat index of the call fits
   const bool small = rows * LPR < ((int64_t)1 << 31) && rows * K < ((int64_t)1 << 31) &&
                      (rows / (Hkv * G) / L + 1) * C * Hkv * G < ((int64_t)1 << 31);
-  auto kern = small ? (vec ? route_weights_kernel<LPR, true, uint32_t>
-                           : route_weights_kernel<LPR, false, uint32_t>)
-                    : (vec ? route_weights_kernel<LPR, true, int64_t>
-                           : route_weights_kernel<LPR, false, int64_t>);
+  // the common call (32-bit indices, vectors, temperature 1) has an
+  // instance of its own
+  auto kern = small ? (vec ? (inv_t == 1.f ? route_weights_kernel<LPR, true, true, uint32_t>
+                                           : route_weights_kernel<LPR, true, false, uint32_t>)
+                           : route_weights_kernel<LPR, false, false, uint32_t>)
+                    : (vec ? route_weights_kernel<LPR, true, false, int64_t>
+                           : route_weights_kernel<LPR, false, false, int64_t>);
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, s, scores, indices, bias, lse,
                      rows, L, C, Hkv, G, K, inv_t, goff, gsc, rw, lw, gate_logit);
   return mrsa_launch_status();
