@@ -531,7 +531,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   // Q offset of this lane's column in a tile whose owner slots are `own2`
   // (slot of owner 0 | slot of owner 1 << 8).
   auto qoff = [&](uint32_t own2, bool valid) {
-    return valid ? ((own2 >> (8 * own)) & 0xffu) * qrow + qcol : kZeroOffset;
+    return valid ? __umul24((own2 >> (8 * own)) & 0xffu, qrow) + qcol : kZeroOffset;
   };
   const uint32_t lock_addr = lds_address(lock);
   const int sinkq = tq;  // query slot taking the adds of a missing second owner
@@ -751,7 +751,9 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       nx_a = it_q[e2];
       nx_b = it_q[e2 + (2 * t + 3 < n ? 1 : 0)];
     }
-    const float wv = TOKEN ? 0.f : (cvalid ? bf16_to_f32(it_w[ii * 8 + gcol]) : 0.f);
+    // The column's weight, read for every lane (ii is a real item of the
+    // step) and consumed after the QK product, so that no branch waits for it.
+    uint32_t wraw = TOKEN ? 0u : it_w[ii * 8 + gcol];
     // S^T = K . Q^T: lane (grp, j) gets keys 16 mt + 4 grp + r of column j.
     f32x4_t S[4];
 #pragma unroll
@@ -762,10 +764,12 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     }
     uint32_t nown2;
     if constexpr (!LAST) {
-      asm volatile("" : "+v"(nx_a), "+v"(nx_b) : "v"(S[3][3]));  // read after the QK issue
+      // read after the QK issue
+      asm volatile("" : "+v"(nx_a), "+v"(nx_b), "+v"(wraw) : "v"(S[3][3]));
       nown2 = (uint32_t)__builtin_amdgcn_readfirstlane(nx_a | (nx_b << 8));
       load_q(Qb, qrs, qoff(nown2, o + 2 < n && gcol < G), qks);
     } else {
+      asm volatile("" : "+v"(wraw) : "v"(S[3][3]));
       nown2 = own2n;
       load_q(Qb, qrs, qoff(nown2, more && own < nn && gcol < G), qks);
       load_k(kb, frs, flo, (uint32_t)cn * kFragBytes);
@@ -819,6 +823,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       }
     } else {
       u32x4_t Pb[2];
+      const float wv = cvalid ? bf16_to_f32(wraw) : 0.f;
       tile_P(S, msk, wv, KEEP && o < n ? it_keep[ii] : ~0ull, Pb);
       // Add the tile into its owners' rows under the lock: the rows are read
       // into the accumulators and O^T_tile = V^T . P^T is added onto them
