@@ -206,13 +206,22 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_fast_kernel(RouteA
   // Head g's landmark keys into buffer i, instruction k (0..7) of this wave:
   // LDS units (8 wave + k) * 64 + lane = row 4 (8 wave + k) + lane / 16,
   // stored part lane & 15 (global part (lane & 15) ^ (row & 15)).  Rows >= C
-  // re-read row C - 1; their logits are masked by the bias row.
+  // re-read row C - 1; their logits are masked by the bias row.  The keys
+  // of batch b are one buffer (chunk c's head slot s at element c rowlen +
+  // 128 s, under 2 GB on this path): the lane's offset is a 24-bit multiply
+  // and the head slot rides in the scalar offset.
+  const uint32_t rowlen = (uint32_t)(a.per_head_lmk ? a.Hkv * G : a.Hkv) * 128u;
+  const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.lmk + b * C * (int64_t)rowlen), (short)0,
+      (int)((uint32_t)C * rowlen * 2u), 0x00020000);
   auto stage_part = [&](int g, int i, int k) {
     const int row = 4 * (8 * wave + k) + (lane >> 4);
-    const int part = (lane & 15) ^ (row & 15);
-    const int64_t c = min((int64_t)row, C - 1);
-    __builtin_amdgcn_global_load_lds(lmk_row(a, b, c, h, g) + part * 8,
-                                     (lds_void_t*)(lmk_buf(i) + (8 * wave + k) * 512), 16, 0, 0);
+    const uint32_t part = (uint32_t)((lane & 15) ^ (row & 15));
+    const uint32_t c = (uint32_t)min(row, (int)C - 1);
+    const uint32_t slot = a.per_head_lmk ? (uint32_t)(h * G + g) : (uint32_t)h;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(lrs, (lds_void_t*)(lmk_buf(i) + (8 * wave + k) * 512),
+                                             16, 2u * (__umul24(c, rowlen) + 8u * part),
+                                             256u * slot, 0, 0);
   };
   // Bias of chunk tid for head g (-inf past C), loaded ahead of its LDS write.
   auto bias_of = [&](int g) {
@@ -1233,11 +1242,13 @@ namespace {
 // The one-pass matrix-core kernel (no workspace) serves the call.  Shared by
 // the dispatcher and the no-allocation entry point, which must agree on
 // which problems need the workspace.
-bool fast_path(const void* q, const void* lmk, int64_t chunks, int64_t groups, int64_t head_dim,
-               int64_t topk, int is_causal, int scores_fp32) {
+bool fast_path(const void* q, const void* lmk, int64_t chunks, int64_t kv_heads, int64_t groups,
+               int64_t head_dim, int64_t topk, int is_causal, int scores_fp32) {
   const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)lmk % 16 == 0);
+  // (a batch's landmark keys, read through one buffer resource, stay under 2 GB)
   return !scores_fp32 && !is_causal && head_dim == 128 && chunks <= 256 &&
-         topk <= kFastMaxTopk && aligned && (groups == 7 || groups == 8);
+         topk <= kFastMaxTopk && aligned && (groups == 7 || groups == 8) &&
+         chunks * kv_heads * groups * head_dim * 2 < ((int64_t)1 << 31);
 }
 
 int route_topk_dispatch(const void* q, const void* lmk, const float* lse_local, const float* bias,
@@ -1286,7 +1297,7 @@ int route_topk_dispatch(const void* q, const void* lmk, const float* lse_local, 
   hipStream_t s = (hipStream_t)stream;
 
   const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)lmk % 16 == 0);
-  if (fast_path(q, lmk, chunks, groups, head_dim, topk, is_causal, scores_fp32)) return groups == 7 ? launch_fast<7>(a, s) : launch_fast<8>(a, s);
+  if (fast_path(q, lmk, chunks, kv_heads, groups, head_dim, topk, is_causal, scores_fp32)) return groups == 7 ? launch_fast<7>(a, s) : launch_fast<8>(a, s);
   const bool block = workspace && head_dim == 128 && groups <= 8 && aligned &&
                      chunks <= (int64_t)kSelThreads * kSelMaxPer && seq_len <= 0x7fffffff &&
                      (uintptr_t)workspace % 16 == 0 &&
@@ -1376,7 +1387,7 @@ extern "C" int mrsa_route_topk_noalloc_fwd(
   // The one-pass matrix-core path runs without one (the dispatcher's own
   // test decides).  A problem that needs more than the static buffer is
   // rejected.
-  const int64_t need = fast_path(q, lmk, chunks, groups, head_dim, topk, is_causal, scores_fp32)
+  const int64_t need = fast_path(q, lmk, chunks, kv_heads, groups, head_dim, topk, is_causal, scores_fp32)
                            ? 0
                            : batch * seq_len * kv_heads * groups * chunks * 4;
   if (need > (int64_t)MRSA_ROUTE_TOPK_SCRATCH_BYTES) return MRSA_ERR_SCRATCH;
