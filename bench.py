@@ -13,7 +13,10 @@ Prints ONE JSON line (rank 0).  Besides the contract fields it carries:
                 timed steps, HBM traffic per launch from profiles/pmc_traffic.json
   cpu_baseline  the CPU oracle's route layer at configuration 1 (L=4096, fp32)
                 timed on this host's cores
-  stages_us     average per-stage times from the same events
+  stages_us     average per-stage times from per-stage events, recorded in
+                as many extra steps after the timed region (an event between
+                dependent kernels costs a few microseconds of dispatch, so the
+                timed steps record only the two around the routed attention)
 
 ``--workload backward`` times the backward of the routed attention and of
 the route scores at configuration 2's shapes, on the routing of the forward
@@ -179,38 +182,45 @@ def main() -> int:
                                 deterministic=args.deterministic)
 
     stream = torch.cuda.current_stream(dev)
-    stage_events = []
 
-    def run(record: bool):
+    # Timed steps record two events each, around the routed attention (the
+    # dominant kernel): an event between dependent kernels costs a few
+    # microseconds of dispatch, so the per-stage events run in separate
+    # steps after the timed region.
+    def run(events):
         evs = []
-        mark = None
-        if record:
-            def mark(name):
+
+        def mark(name):
+            if events == "all" or name in ("route_weights", "token_refinement",
+                                           "selected_attention"):
                 e = torch.cuda.Event(enable_timing=True)
                 e.record(stream)
                 evs.append((name, e))
-        out = mrsa.route_attention(q, k, v, route_q, scale, key_valid, cfg, mark=mark)
-        if record:
-            stage_events.append(evs)
-        return out
+        out = mrsa.route_attention(q, k, v, route_q, scale, key_valid, cfg,
+                                   mark=mark if events else None)
+        return out, evs
 
     for _ in range(args.warmup):
-        run(False)
+        run(None)
     torch.cuda.synchronize()
+    routed_events = []
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        run(True)
+        routed_events.append(run("routed")[1])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = 1000.0 * elapsed / args.steps
+    sel = [evs[-2][1].elapsed_time(evs[-1][1]) * 1000.0 for evs in routed_events]
 
+    stage_events = [run("all")[1] for _ in range(args.steps)]
+    torch.cuda.synchronize()
     stages = {}
     for evs in stage_events:
         for (_, a), (name, b) in zip(evs[:-1], evs[1:]):
             stages.setdefault(name, []).append(a.elapsed_time(b) * 1000.0)
     stages_us = {n: sum(x) / len(x) for n, x in stages.items()}
 
-    sel_us = stages_us["selected_attention"]
+    sel_us = sum(sel) / len(sel)
     achieved = selected_flops(L_CFG2) / (sel_us * 1e-6) / 1e12
     # HBM bytes per launch cannot be counted from inside the run: they come
     # from the FETCH_SIZE / WRITE_SIZE counter passes of the committed profile
