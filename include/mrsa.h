@@ -149,6 +149,25 @@ int mrsa_remote_drop_mask_rows(const uint8_t* valid_mask, const int64_t* query_p
                                int64_t chunk_size, int32_t* drop_mask, void* stream);
 
 /*
+ * The device-side argument checks of the cached block step in one launch
+ * (one workgroup), for callers that validate before launching, as
+ * cached_route_attention's checks do (dream_dllm_hils/fastdllm_attention.py:
+ * 54-66, 84-118: positions sorted, unique and in range, affected chunks in
+ * range, each affected chunk's landmark position among the query positions).
+ *   query_positions: int64 [count]; affected_chunks: int64 [affected_count]
+ *   flags (out): int32 [4] -- [0] positions not strictly ascending, [1] a
+ *   position outside [0, cache_len), [2] an affected chunk outside
+ *   [0, cache_len / chunk_size), [3] an affected chunk whose landmark position
+ *   (c chunk_size + chunk_size - 1) is not a query position (meaningful once
+ *   [0] is clear)
+ * No reference counterpart as an entry point: the reference runs these
+ * checks as separate torch expressions with host synchronisations.
+ */
+int mrsa_cached_step_checks(const int64_t* query_positions, int64_t count,
+                            const int64_t* affected_chunks, int64_t affected_count,
+                            int64_t cache_len, int64_t chunk_size, int32_t* flags, void* stream);
+
+/*
  * Route scoring with per-KV-group top-k ("softmax then max pooling").
  * Replaces ref_softmax_topk_max_pooling (ops/topk_head_softmax.py:15-156),
  * which route_topk_g7 (dream_dllm_hils/routing.py:52-171) and

@@ -257,6 +257,45 @@ __global__ void __launch_bounds__(256)
   pool_lmk(rows, Pb, 2 * w + 1, chunk_valid, G, lrow, lane);
 }
 
+// Device-side argument checks of the cached block step in one launch (one
+// workgroup): flags[0] query positions not strictly ascending, flags[1] a
+// position outside [0, L), flags[2] an affected chunk outside [0, C),
+// flags[3] an affected chunk whose landmark position (c S + S - 1) is not a
+// query position (lower-bound search; meaningful once flags[0] is clear).
+__global__ void __launch_bounds__(256)
+    cached_step_checks_kernel(const int64_t* __restrict__ qp, int64_t lq,
+                              const int64_t* __restrict__ aff, int64_t n, int64_t L, int64_t C,
+                              int64_t S, int32_t* __restrict__ flags) {
+  __shared__ int f[4];
+  const int tid = threadIdx.x;
+  if (tid < 4) f[tid] = 0;
+  __syncthreads();
+  int a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+  for (int64_t i = tid; i < lq; i += blockDim.x) {
+    const int64_t p = qp[i];
+    if (i + 1 < lq && qp[i + 1] <= p) a0 = 1;
+    if (p < 0 || p >= L) a1 = 1;
+  }
+  for (int64_t j = tid; j < n; j += blockDim.x) {
+    const int64_t c = aff[j];
+    if (c < 0 || c >= C) a2 = 1;
+    const int64_t lp = c * S + S - 1;
+    int64_t lo = 0, hi = lq;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (qp[mid] < lp) lo = mid + 1;
+      else hi = mid;
+    }
+    if (lo >= lq || qp[lo] != lp) a3 = 1;
+  }
+  if (a0) atomicOr(&f[0], 1);
+  if (a1) atomicOr(&f[1], 1);
+  if (a2) atomicOr(&f[2], 1);
+  if (a3) atomicOr(&f[3], 1);
+  __syncthreads();
+  if (tid < 4) flags[tid] = f[tid];
+}
+
 }  // namespace
 
 extern "C" int mrsa_remote_drop_mask(const uint8_t* valid_mask, const uint8_t* allowed_mask,
@@ -347,6 +386,20 @@ extern "C" int mrsa_kv_fragments_pool_fwd(const void* k, const void* v, const vo
                      kv_heads, NT, (uint16_t*)kv_frags, (const uint16_t*)mu_q, mu_row_stride,
                      key_valid, (int)groups, sm_scale, bias_scale, (uint16_t*)landmark_keys,
                      entropy, prior_bias);
+  return mrsa_launch_status();
+}
+
+extern "C" int mrsa_cached_step_checks(const int64_t* query_positions, int64_t count,
+                                       const int64_t* affected_chunks, int64_t affected_count,
+                                       int64_t cache_len, int64_t chunk_size, int32_t* flags,
+                                       void* stream) {
+  if (count < 0 || affected_count < 0 || cache_len < 0 || chunk_size <= 0 || !flags)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if ((count > 0 && !query_positions) || (affected_count > 0 && !affected_chunks))
+    return MRSA_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(cached_step_checks_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream,
+                     query_positions, count, affected_chunks, affected_count, cache_len,
+                     cache_len / chunk_size, chunk_size, flags);
   return mrsa_launch_status();
 }
 

@@ -87,6 +87,7 @@ SIGNATURES = {
     "mrsa_kv_fragments_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "mrsa_kv_fragments": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P, _P]),
     "mrsa_kv_fragments_rows": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P]),
+    "mrsa_cached_step_checks": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P]),
     "mrsa_kv_fragments_pool_fwd": (
         _I,
         [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P, _P, _P],

@@ -36,6 +36,7 @@ from dataclasses import dataclass, field
 
 import torch
 
+from . import _lib
 from .kernel_utils import drop_mask_rows_launch
 from .local_attention import key_parts, local_attention_launch, local_attention_qf_launch
 from .pool import _needs_grad, chunk_attn_pool_gqa_prior, kv_fragments_pool
@@ -364,10 +365,26 @@ def cached_route_attention(
                               entropy_bias_scale, cfg, return_intermediates)
 
 
+def _raise_cached_flags(flags, n, C):
+    """The errors of the device-side checks (mrsa_cached_step_checks flags),
+    in the order the reference raises them."""
+    if flags[0]:
+        raise ValueError("query_positions must be sorted and unique")
+    if flags[1]:
+        raise ValueError("query_positions must be in cache range")
+    if n and flags[2]:
+        raise ValueError(f"affected_chunks must be in [0, {C})")
+    if n and flags[3]:
+        raise ValueError("all owned positions must also be query positions")
+
+
 def _check_cached_args(q, route_q, cache, query_positions, affected_chunks, cfg,
-                       device_checks=True):
+                       device_checks=True, defer=False):
     """cached_route_attention's argument checks; the ones that read device
-    values share one round trip (skipped with device_checks=False)."""
+    values run as one kernel and one round trip (skipped with
+    device_checks=False).  With defer=True the kernel is only launched and
+    (flags, n, C) is returned for _raise_cached_flags after the caller's own
+    launches (None when there is nothing to read)."""
 
     _check_token_budget(cfg)
     if q.device.type != "cuda":
@@ -396,31 +413,22 @@ def _check_cached_args(q, route_q, cache, query_positions, affected_chunks, cfg,
         raise ValueError("affected_chunks must be a 1-D torch.long tensor")
     n = affected_chunks.numel()
     if Lq and device_checks:
-        # Every argument check that needs device values, in one round trip:
-        # sorted unique positions in range, affected chunks in range, and
-        # each affected chunk's landmark row among the query positions
-        # (fastdllm_attention.py:54-66, :84-118).
-        checks = [
-            (query_positions[1:] <= query_positions[:-1]).any(),
-            ((query_positions < 0) | (query_positions >= L)).any(),
-        ]
-        if n:
-            landmark_pos = affected_chunks * S + (S - 1)
-            landmark_rows = torch.searchsorted(query_positions, landmark_pos)
-            found = query_positions[landmark_rows.clamp(max=Lq - 1)]
-            checks += [((affected_chunks < 0) | (affected_chunks >= C)).any(),
-                       ((landmark_rows >= Lq) | (found != landmark_pos)).any()]
-        flags = torch.stack(checks).tolist()
-        if flags[0]:
-            raise ValueError("query_positions must be sorted and unique")
-        if flags[1]:
-            raise ValueError("query_positions must be in cache range")
-        if n and flags[2]:
-            raise ValueError(f"affected_chunks must be in [0, {C})")
-        if n and flags[3]:
-            raise ValueError("all owned positions must also be query positions")
+        # Every argument check that needs device values, in one kernel and
+        # one round trip: sorted unique positions in range, affected chunks
+        # in range, and each affected chunk's landmark row among the query
+        # positions (fastdllm_attention.py:54-66, :84-118).
+        qp = query_positions.contiguous()
+        ac = affected_chunks.contiguous()
+        flags = torch.empty(4, dtype=torch.int32, device=q.device)
+        st = _lib.call("mrsa_cached_step_checks", _lib.ptr(qp), Lq, _lib.ptr(ac), n, L, S,
+                       _lib.ptr(flags), _lib.stream_of(qp))
+        _lib.check(st, "cached step checks")
+        if defer:
+            return flags, n, C
+        _raise_cached_flags(flags.tolist(), n, C)
     elif n:
         raise ValueError("all owned positions must also be query positions")
+    return None
 
 
 def _cached_route_body(q, route_q, cache, query_positions, affected_chunks, entropy_bias_scale,
@@ -545,13 +553,19 @@ class CachedBlockStep:
         if k_rows.dtype != self.k_rows.dtype or v_rows.dtype != self.k_rows.dtype:
             raise ValueError("replacement K/V dtype must match the cache")
         # Sorted unique in-range query positions also make the K/V rows'
-        # positions unique and in range (replace's checks).
-        _check_cached_args(q, route_q, self.cache, query_positions, affected_chunks, self.cfg)
+        # positions unique and in range (replace's checks).  The device
+        # checks run first and are read after the input copies are queued
+        # (the copies fill the graph's own buffers only).
+        pending = _check_cached_args(q, route_q, self.cache, query_positions, affected_chunks,
+                                     self.cfg, defer=True)
         self.q.copy_(q)
         self.route_q.copy_(route_q)
         self.k_rows.copy_(k_rows)
         self.v_rows.copy_(v_rows)
         self.positions.copy_(query_positions)
+        if pending is not None:
+            flags, nf, C = pending
+            _raise_cached_flags(flags.tolist(), nf, C)
         n = affected_chunks.numel()
         entry = self._graphs.get(n)
         if entry is None:

@@ -201,6 +201,35 @@ def test_cached_route_attention_argument_errors():
     assert bool(torch.isfinite(out.float()).all())
 
 
+def test_cached_block_step_argument_errors_leave_the_cache_alone():
+    # CachedBlockStep reads its device checks (one kernel) after queueing the
+    # input copies: a bad call raises the reference's errors and changes no
+    # cache row; the next good call runs normally.
+    _note("cached block step errors")
+    L, Hq, Hkv, D, S, bs = 1024, 28, 4, 128, 64, 4
+    q, rq, k, v = _cache_inputs(L, Hq, Hkv, D, 94)
+    valid = torch.ones(1, L, dtype=torch.bool, device=DEV)
+    lmk = torch.zeros(1, L // S, Hkv, Hq // Hkv, D, dtype=torch.bfloat16, device=DEV)
+    prior = torch.zeros(1, L // S, Hkv, Hq // Hkv, device=DEV)
+    cache = mrsa.LayerKVCache(k.to(DEV), v.to(DEV), valid, lmk, prior)
+    step = mrsa.CachedBlockStep(cache, torch.ones(Hq, device=DEV), block_len=bs)
+    qb, rqb = q[:, :bs].to(DEV), rq[:, :bs].to(DEV)
+    kb = (torch.randn(1, bs, Hkv, D, generator=torch.Generator().manual_seed(95))).bfloat16().to(DEV)
+    ok = torch.tensor([60, 61, 62, 63], device=DEV)
+    none = torch.empty(0, dtype=torch.long, device=DEV)
+    key0 = cache.key.clone()
+    for pos, aff, msg in ((ok.flip(0), none, "sorted"), (ok + L, none, "range"),
+                          (ok, torch.tensor([L // S], device=DEV), "affected_chunks"),
+                          (ok, torch.tensor([1], device=DEV), "owned positions")):
+        with pytest.raises(ValueError, match=msg):
+            step(qb, rqb, kb, kb, pos, aff)
+        torch.cuda.synchronize()
+        assert torch.equal(cache.key, key0), msg
+    out = step(qb, rqb, kb, kb, ok, torch.tensor([0], device=DEV))
+    assert bool(torch.isfinite(out.float()).all())
+    assert torch.equal(cache.key[:, 60:64], kb)
+
+
 @pytest.mark.parametrize("policy", [None, "entropy_adaptive"])
 def test_cached_block_step_graph_replays_match_eager(policy):
     # CachedBlockStep (HIP graph of the K/V row write + cached route layer)
