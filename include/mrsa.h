@@ -102,6 +102,34 @@ int mrsa_chunk_attn_pool_gqa_strided_fwd(const void* mu_q, int64_t mu_row_stride
                                          float* entropy, float* prior_bias, void* stream);
 
 /*
+ * Landmark refresh of the affected chunks of a K/V cache, in place: replaces
+ * the gather-pool-scatter of the cached block step
+ * (dream_dllm_hils/fastdllm_attention.py:236-292: the landmark rows of
+ * route_q located among the query positions, the chunks' key rows and valid
+ * bytes gathered from the cache, chunk_attn_pool_gqa, prior = entropy x
+ * entropy_bias_scale, index_copy_ into landmark_keys / prior_bias) with one
+ * launch that reads everything in place.  Fused pool semantics, the same
+ * bits as mrsa_chunk_attn_pool_gqa_fwd on the gathered rows.
+ *   route_q: bf16 [batch, query_len, kv_heads * groups, head_dim]
+ *   query_positions: int64 [query_len], sorted ascending
+ *   key: bf16 [batch, cache_len, kv_heads, head_dim]; key_valid: u8 [batch, cache_len]
+ *   chunks: int64 [count]; bias_scale: fp32 [kv_heads * groups]
+ *   landmark_keys (in/out): bf16 [batch, cache_len / 64, kv_heads, groups, head_dim]
+ *   prior_bias (in/out): fp32 [batch, cache_len / 64, kv_heads, groups]
+ * A chunk outside [0, cache_len / 64), or whose landmark position
+ * (64 c + 63) is not a query position, is left as it is (the argument checks
+ * of mrsa_cached_step_checks report both).
+ * Limits: chunk_size == 64, head_dim == 128, groups <= 16, cache_len % 64 == 0.
+ */
+int mrsa_pool_cached_chunks_fwd(const void* route_q, const int64_t* query_positions,
+                                int64_t query_len, const void* key, const uint8_t* key_valid,
+                                int64_t batch, int64_t cache_len, const int64_t* chunks,
+                                int64_t count, int64_t kv_heads, int64_t groups,
+                                int64_t head_dim, int64_t chunk_size, float sm_scale,
+                                const float* bias_scale, void* landmark_keys, float* prior_bias,
+                                void* stream);
+
+/*
  * Backward of the landmark pool; the probabilities are recomputed from mu_q
  * and K.  Replaces _ChunkAttnPoolGQA.backward
  * (ops/chunk_attn_pool_gqa_tilelang.py:355-394, kernel _pool_gqa_bwd :183-325)
@@ -366,6 +394,32 @@ int mrsa_kv_fragments(const void* k, const void* v, int64_t batch, int64_t seq_l
 int mrsa_kv_fragments_rows(const void* k, const void* v, int64_t batch, int64_t seq_len,
                            int64_t kv_heads, int64_t head_dim, const int64_t* positions,
                            int64_t count, void* kv_frags, void* stream);
+
+/*
+ * The row writes of LayerKVCache.replace (dream_dllm_hils/fastdllm_cache.py:
+ * 126-127, key.index_copy_(1, positions, k_rows) and the same for value) and
+ * the fragment rewrite of those rows (mrsa_kv_fragments_rows) in one launch.
+ *   k_rows, v_rows: bf16 [batch, count, kv_heads, head_dim]
+ *   positions: int64 [count]; entries outside [0, seq_len) are ignored
+ *   key, value (in/out): bf16 [batch, seq_len, kv_heads, head_dim]
+ *   kv_frags (in/out, optional): as in mrsa_kv_fragments
+ * Limits: head_dim == 128.  Positions must be unique (a duplicate leaves
+ * either row, as index_copy_ does).
+ */
+/*
+ * Up to 8 device-to-device buffer copies in one launch (src[i] -> dst[i],
+ * bytes[i] bytes; host arrays of count entries).  Every pointer and size
+ * must be a multiple of 8 bytes (MRSA_ERR_UNSUPPORTED otherwise).  For
+ * callers that refill the input buffers of a captured step (the cached block
+ * step's query, routing query, K/V rows and positions) each call.  No
+ * reference counterpart: the reference runs its cached step eagerly.
+ */
+int mrsa_copy_buffers(int32_t count, const void* const* src, void* const* dst,
+                      const int64_t* bytes, void* stream);
+
+int mrsa_kv_replace_rows(const void* k_rows, const void* v_rows, const int64_t* positions,
+                         int64_t count, int64_t batch, int64_t seq_len, int64_t kv_heads,
+                         int64_t head_dim, void* key, void* value, void* kv_frags, void* stream);
 
 /*
  * Q fragments: per (batch, KV head, query) the 2 KB register image of the

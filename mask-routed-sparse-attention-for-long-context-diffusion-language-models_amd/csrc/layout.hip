@@ -130,6 +130,33 @@ __global__ void __launch_bounds__(128)
   dst[frag_v_index(r, d)] = v[src];
 }
 
+// The K/V rows of a cache update written in one pass: row i of k_rows /
+// v_rows ([B, count, H, 128]) goes to cache position positions[i] of key /
+// value ([B, L, H, 128]) and, when frags is given, into that position's
+// fragment entries.  One thread per dim; positions outside [0, L) are
+// ignored.
+__global__ void __launch_bounds__(128)
+    kv_replace_rows_kernel(const uint16_t* __restrict__ k_rows, const uint16_t* __restrict__ v_rows,
+                           int64_t count, const int64_t* __restrict__ positions, int64_t L,
+                           int64_t H, int64_t NT, uint16_t* __restrict__ key,
+                           uint16_t* __restrict__ value, uint16_t* __restrict__ frags) {
+  const int64_t i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t p = positions[i];
+  if (p < 0 || p >= L) return;
+  const int d = threadIdx.x;
+  const uint16_t kx = k_rows[((b * count + i) * H + h) * 128 + d];
+  const uint16_t vx = v_rows[((b * count + i) * H + h) * 128 + d];
+  const int64_t dst = ((b * L + p) * H + h) * 128 + d;
+  key[dst] = kx;
+  value[dst] = vx;
+  if (frags) {
+    uint16_t* fr = frags + ((b * H + h) * NT + p / 64) * (int64_t)kFragElems;
+    const int r = (int)(p & 63);
+    fr[frag_k_index(r, d)] = kx;
+    fr[frag_v_index(r, d)] = vx;
+  }
+}
+
 // Q fragments: per (batch, KV head, query) the 2 KB register image of the
 // routed attention's Q^T operand for the query's G head columns --
 //   qf[((b Hkv + h) L + i) 1024 + 256 ks + 64 grp + 8 g + e]
@@ -296,6 +323,44 @@ __global__ void __launch_bounds__(256)
   if (tid < 4) flags[tid] = f[tid];
 }
 
+// Up to kMaxCopies buffer copies in one launch: buffer i is `units[i]` units
+// of 16 bytes (wide[i]) or 8 bytes; start[i] is the first unit of buffer i in
+// the flattened unit range [0, start[count]).
+constexpr int kMaxCopies = 8;
+struct CopyList {
+  const void* src[kMaxCopies];
+  void* dst[kMaxCopies];
+  int64_t start[kMaxCopies + 1];
+  int32_t wide[kMaxCopies];
+  int32_t count;
+};
+
+__global__ void __launch_bounds__(256) copy_list_kernel(CopyList l) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < l.start[l.count];
+       u += stride) {
+    // the buffer holding unit u (static indices only: the list stays in
+    // kernel-argument registers)
+    const void* s = l.src[0];
+    void* d = l.dst[0];
+    int64_t base = l.start[0];
+    int32_t w = l.wide[0];
+#pragma unroll
+    for (int k = 1; k < kMaxCopies; ++k)
+      if (k < l.count && u >= l.start[k]) {
+        s = l.src[k];
+        d = l.dst[k];
+        base = l.start[k];
+        w = l.wide[k];
+      }
+    const int64_t e = u - base;
+    if (w)
+      reinterpret_cast<u32x4_t*>(d)[e] = reinterpret_cast<const u32x4_t*>(s)[e];
+    else
+      reinterpret_cast<u32x2_t*>(d)[e] = reinterpret_cast<const u32x2_t*>(s)[e];
+  }
+}
+
 }  // namespace
 
 extern "C" int mrsa_remote_drop_mask(const uint8_t* valid_mask, const uint8_t* allowed_mask,
@@ -400,6 +465,52 @@ extern "C" int mrsa_cached_step_checks(const int64_t* query_positions, int64_t c
   hipLaunchKernelGGL(cached_step_checks_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream,
                      query_positions, count, affected_chunks, affected_count, cache_len,
                      cache_len / chunk_size, chunk_size, flags);
+  return mrsa_launch_status();
+}
+
+extern "C" int mrsa_copy_buffers(int32_t count, const void* const* src, void* const* dst,
+                                 const int64_t* bytes, void* stream) {
+  if (count < 0 || count > kMaxCopies) return MRSA_ERR_INVALID_ARGUMENT;
+  if (count > 0 && (!src || !dst || !bytes)) return MRSA_ERR_INVALID_ARGUMENT;
+  CopyList l{};
+  l.count = 0;
+  int64_t total = 0;
+  for (int i = 0; i < count; ++i) {
+    if (bytes[i] < 0) return MRSA_ERR_INVALID_ARGUMENT;
+    if (bytes[i] == 0) continue;
+    if (!src[i] || !dst[i]) return MRSA_ERR_INVALID_ARGUMENT;
+    const uintptr_t a = (uintptr_t)src[i] | (uintptr_t)dst[i] | (uintptr_t)bytes[i];
+    if (a % 8 != 0) return MRSA_ERR_UNSUPPORTED;
+    const int k = l.count++;
+    l.src[k] = src[i];
+    l.dst[k] = dst[i];
+    l.wide[k] = a % 16 == 0;
+    l.start[k] = total;
+    total += bytes[i] / (l.wide[k] ? 16 : 8);
+  }
+  l.start[l.count] = total;
+  if (total == 0) return MRSA_OK;
+  const int64_t grid = std::min<int64_t>((total + 255) / 256, 1024);
+  hipLaunchKernelGGL(copy_list_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+                     l);
+  return mrsa_launch_status();
+}
+
+extern "C" int mrsa_kv_replace_rows(const void* k_rows, const void* v_rows,
+                                    const int64_t* positions, int64_t count, int64_t batch,
+                                    int64_t seq_len, int64_t kv_heads, int64_t head_dim, void* key,
+                                    void* value, void* kv_frags, void* stream) {
+  if (batch < 0 || seq_len < 0 || kv_heads <= 0 || head_dim <= 0 || count < 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (head_dim != 128) return MRSA_ERR_UNSUPPORTED;
+  if (batch == 0 || seq_len == 0 || count == 0) return MRSA_OK;
+  if (!k_rows || !v_rows || !positions || !key || !value) return MRSA_ERR_INVALID_ARGUMENT;
+  if (kv_heads > 65535 || batch > 65535 || count > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(kv_replace_rows_kernel,
+                     dim3((unsigned)count, (unsigned)kv_heads, (unsigned)batch), dim3(128), 0,
+                     (hipStream_t)stream, (const uint16_t*)k_rows, (const uint16_t*)v_rows, count,
+                     positions, seq_len, kv_heads, (seq_len + 63) / 64, (uint16_t*)key,
+                     (uint16_t*)value, (uint16_t*)kv_frags);
   return mrsa_launch_status();
 }
 

@@ -210,6 +210,62 @@ __global__ void __launch_bounds__(64 * kPoolWaves)
   pool_wave(SwizzledRows{ks}, Qb, vbits & ~(1ull << 63), G, sm_scale, (bc * H + h) * G,
             bias_scale, h * G, lmk, entropy, prior, lane);
 }
+
+// Landmark refresh of listed chunks of a K/V cache in place (the cached block
+// step, fastdllm_attention.py:236-292): for listed chunk c of batch b, the
+// routing query row whose position is c * 64 + 63 (found by a binary search
+// of the sorted query positions), the chunk's 64 key rows and valid bytes
+// read straight from the cache, the pool written into the cache's landmark
+// keys and prior bias at chunk c.  One wave per (batch, listed chunk, KV
+// head), the same wave math as pool_mfma_kernel.  A listed chunk outside
+// [0, C) or whose landmark position is not a query position is skipped.
+__global__ void __launch_bounds__(64 * kPoolWaves)
+    pool_cached_kernel(const uint16_t* __restrict__ route_q, const int64_t* __restrict__ qpos,
+                       int64_t Lq, const uint16_t* __restrict__ key,
+                       const uint8_t* __restrict__ key_valid, int64_t L,
+                       const int64_t* __restrict__ chunks, int64_t n, int H, int G,
+                       int64_t units, float sm_scale, const float* __restrict__ bias_scale,
+                       uint16_t* __restrict__ lmk, float* __restrict__ prior) {
+  __shared__ __attribute__((aligned(16))) uint16_t ks_all[kPoolWaves][64 * 128];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t unit = (int64_t)blockIdx.x * kPoolWaves + wave;
+  if (unit >= units) return;  // wave-uniform; no workgroup barrier below
+  const int64_t bi = unit / H;
+  const int h = (int)(unit - bi * H);
+  const int64_t b = bi / n;
+  const int64_t c = chunks[bi - b * n];
+  const int64_t C = L / 64;
+  if (c < 0 || c >= C) return;
+  const int64_t pos = c * 64 + 63;
+  int64_t lo = 0, hi = Lq;  // first query position >= pos
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (qpos[mid] < pos)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  if (lo == Lq || qpos[lo] != pos) return;
+  const int j = lane & 15, grp = lane >> 4;
+  uint16_t* ks = ks_all[wave];
+  const int64_t bc = b * C + c;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int kk = 4 * i + grp;
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(key + ((bc * 64 + kk) * H + h) * 128 + 8 * j);
+    *reinterpret_cast<u32x4_t*>(ks + kk * 128 + 8 * pool_blk(kk, j)) = v;
+  }
+  u32x4_t Qb[4];
+  const uint16_t* qrow = route_q + ((b * Lq + lo) * H * G + (int64_t)h * G) * 128;
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) {
+    Qb[q4] = u32x4_t{0u, 0u, 0u, 0u};
+    if (j < G) Qb[q4] = *reinterpret_cast<const u32x4_t*>(qrow + j * 128 + 32 * q4 + 8 * grp);
+  }
+  const uint64_t vbits = __builtin_amdgcn_ballot_w64(key_valid[bc * 64 + lane] != 0);
+  pool_wave(SwizzledRows{ks}, Qb, vbits & ~(1ull << 63), G, sm_scale, bc * H * G + h * G,
+            bias_scale, h * G, lmk, nullptr, prior, lane);
+}
 }  // namespace
 
 namespace {
@@ -277,6 +333,36 @@ extern "C" int mrsa_chunk_attn_pool_gqa_strided_fwd(
   return pool_forward(mu_q, mu_row_stride, k_chunked, key_valid, batch_chunks, chunk_size,
                       kv_heads, groups, head_dim, sm_scale, dense_torch_semantics, bias_scale,
                       landmark_keys, entropy, prior_bias, stream);
+}
+
+extern "C" int mrsa_pool_cached_chunks_fwd(const void* route_q, const int64_t* query_positions,
+                                           int64_t query_len, const void* key,
+                                           const uint8_t* key_valid, int64_t batch,
+                                           int64_t cache_len, const int64_t* chunks,
+                                           int64_t count, int64_t kv_heads, int64_t groups,
+                                           int64_t head_dim, int64_t chunk_size, float sm_scale,
+                                           const float* bias_scale, void* landmark_keys,
+                                           float* prior_bias, void* stream) {
+  if (batch < 0 || query_len < 0 || cache_len < 0 || count < 0 || kv_heads <= 0 || groups <= 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (chunk_size != 64 || head_dim != 128 || groups > 16 || cache_len % 64 != 0)
+    return MRSA_ERR_UNSUPPORTED;
+  if (batch == 0 || count == 0 || query_len == 0 || cache_len == 0) return MRSA_OK;
+  if (!route_q || !query_positions || !key || !key_valid || !chunks || !bias_scale ||
+      !landmark_keys || !prior_bias)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (((uintptr_t)route_q | (uintptr_t)key | (uintptr_t)landmark_keys) % 16 != 0)
+    return MRSA_ERR_INVALID_ARGUMENT;
+  if (kv_heads > 65535) return MRSA_ERR_UNSUPPORTED;
+  const int64_t units = batch * count * kv_heads;
+  const int64_t blocks = (units + kPoolWaves - 1) / kPoolWaves;
+  if (blocks > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(pool_cached_kernel, dim3((unsigned)blocks), dim3(64 * kPoolWaves), 0,
+                     (hipStream_t)stream, (const uint16_t*)route_q, query_positions, query_len,
+                     (const uint16_t*)key, key_valid, cache_len, chunks, count, (int)kv_heads,
+                     (int)groups, units, sm_scale, bias_scale, (uint16_t*)landmark_keys,
+                     prior_bias);
+  return mrsa_launch_status();
 }
 
 namespace {

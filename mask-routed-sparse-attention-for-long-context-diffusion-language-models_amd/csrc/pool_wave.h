@@ -102,9 +102,9 @@ __device__ __forceinline__ void pool_lmk(const Rows& rows, const u32x4_t (&Pb)[2
   }
 }
 
-// Entropy (and prior = entropy x bias_scale when given) of the G heads from
-// the column sum t of p ln p; o = (chunk * H + h) * G, bias_scale indexed by
-// hG + head.
+// Entropy (when `entropy` is given) and prior = entropy x bias_scale (when
+// given) of the G heads from the column sum t of p ln p; o = (chunk * H + h)
+// * G, bias_scale indexed by hG + head.
 __device__ __forceinline__ void pool_stats(float t, bool chunk_valid, int G, int64_t o,
                                            const float* __restrict__ bias_scale, int hG,
                                            float* __restrict__ entropy, float* __restrict__ prior,
@@ -112,13 +112,14 @@ __device__ __forceinline__ void pool_stats(float t, bool chunk_valid, int G, int
   const int j = lane & 15, grp = lane >> 4;
   if (grp == 0 && j < G) {
     const float e_out = chunk_valid ? -t : 0.f;
-    entropy[o + j] = e_out;
+    if (entropy) entropy[o + j] = e_out;
     if (prior) prior[o + j] = e_out * bias_scale[hG + j];
   }
 }
 
 // The whole pool on one wave.  o = (chunk * H + h) * G: the first of the G
-// output rows; bias_scale / prior are optional (both or neither).
+// output rows; bias_scale / prior are optional (both or neither), and so is
+// entropy.
 template <class Rows>
 __device__ __forceinline__ void pool_wave(const Rows& rows, const u32x4_t (&Qb)[4], uint64_t real,
                                           int G, float sm_scale, int64_t o,

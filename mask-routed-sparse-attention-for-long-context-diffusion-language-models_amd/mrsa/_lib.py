@@ -88,6 +88,13 @@ SIGNATURES = {
     "mrsa_kv_fragments": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P, _P]),
     "mrsa_kv_fragments_rows": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "mrsa_cached_step_checks": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P]),
+    "mrsa_copy_buffers": (_I, [_I, _P, _P, _P, _P]),
+    "mrsa_kv_replace_rows": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P]),
+    "mrsa_pool_cached_chunks_fwd": (
+        _I,
+        [_P, _P, _I64, _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P,
+         _P],
+    ),
     "mrsa_kv_fragments_pool_fwd": (
         _I,
         [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P, _P, _P],
@@ -224,3 +231,21 @@ def stream_of(t: torch.Tensor) -> int:
 
 def call(name: str, *args) -> int:
     return getattr(load(), name)(*args)
+
+
+def copy_buffers(dst: list, src: list) -> None:
+    """dst[i].copy_(src[i]) for same-shape, same-dtype contiguous CUDA
+    tensors, in one launch (mrsa_copy_buffers; at most 8 pairs) when every
+    size and address is a multiple of 8 bytes, else one copy_ per pair."""
+
+    n = len(dst)
+    if any((t.data_ptr() | t.numel() * t.element_size()) % 8 for t in list(src) + list(dst)):
+        for d, s_ in zip(dst, src):
+            d.copy_(s_)
+        return
+    srcs = (ctypes.c_void_p * max(n, 1))(*[t.data_ptr() for t in src])
+    dsts = (ctypes.c_void_p * max(n, 1))(*[t.data_ptr() for t in dst])
+    sizes = (ctypes.c_int64 * max(n, 1))(*[t.numel() * t.element_size() for t in src])
+    st = call("mrsa_copy_buffers", n, ctypes.addressof(srcs), ctypes.addressof(dsts),
+              ctypes.addressof(sizes), stream_of(dst[0]))
+    check(st, "copy_buffers")

@@ -307,10 +307,7 @@ class LayerKVCache:
             raise ValueError("replacement K/V dtype must match the cache")
         if key.device != self.key.device or value.device != self.value.device:
             raise ValueError("replacement K/V device must match the cache")
-        self.key.index_copy_(1, positions, key)
-        self.value.index_copy_(1, positions, value)
-        if self.kv_frags is not None:
-            kv_fragments_rows(self.key, self.value, self.kv_frags, positions)
+        _write_rows(self, positions, key, value)
 
     def __post_init__(self) -> None:
         # fastdllm_cache.py:20-80 (the checks this path depends on)
@@ -331,6 +328,70 @@ class LayerKVCache:
         if self.kv_frags is not None and self.kv_frags.shape != (
                 batch, hkv, (self.key.shape[1] + 63) // 64, FRAG_ELEMS):
             raise ValueError("kv_frags must be kv_fragments(key, value)")
+
+
+def _write_rows(cache: LayerKVCache, positions: torch.Tensor, key: torch.Tensor,
+                value: torch.Tensor) -> None:
+    """The row writes of LayerKVCache.replace (fastdllm_cache.py:126-127) and
+    the fragment entries of those rows, as one launch (mrsa_kv_replace_rows)
+    for a contiguous bf16 head_dim-128 cache; otherwise index_copy_ followed
+    by kv_fragments_rows.  Arguments already checked."""
+
+    c = cache
+    if (c.key.device.type == "cuda" and c.key.dtype == torch.bfloat16 and c.key.shape[3] == 128
+            and c.key.is_contiguous() and c.value.is_contiguous()):
+        B, L, H, D = c.key.shape
+        kr, vr, pos = key.contiguous(), value.contiguous(), positions.contiguous()
+        st = _lib.call("mrsa_kv_replace_rows", _lib.ptr(kr), _lib.ptr(vr), _lib.ptr(pos),
+                       pos.numel(), B, L, H, D, _lib.ptr(c.key), _lib.ptr(c.value),
+                       _lib.ptr(c.kv_frags), _lib.stream_of(kr))
+        _lib.check(st, "kv_replace_rows")
+        return
+    c.key.index_copy_(1, positions, key)
+    c.value.index_copy_(1, positions, value)
+    if c.kv_frags is not None:
+        kv_fragments_rows(c.key, c.value, c.kv_frags, positions)
+
+
+def _refresh_landmarks(route_q, cache, query_positions, affected_chunks, entropy_bias_scale,
+                       chunk_size):
+    """Landmark keys and prior bias of the affected chunks, refreshed in place
+    (fastdllm_attention.py:236-292).  One launch (mrsa_pool_cached_chunks_fwd)
+    reads the landmark query rows, the chunks' key rows and valid bytes where
+    they lie; other shapes gather the rows and pool them with torch ops
+    around chunk_attn_pool_gqa_prior.  Arguments already checked."""
+
+    c = cache
+    B, Lq, Hq, D = route_q.shape
+    L, Hkv = c.key.shape[1], c.key.shape[2]
+    G, S, n = Hq // Hkv, chunk_size, affected_chunks.numel()
+    scale = entropy_bias_scale.to(device=route_q.device, dtype=torch.float32).contiguous()
+    fused = (S == 64 and D == 128 and G <= 16 and L % 64 == 0 and c.key.is_contiguous()
+             and c.landmark_keys.is_contiguous() and c.prior_bias.is_contiguous()
+             and c.prior_bias.dtype == torch.float32 and c.key_valid.dtype == torch.bool
+             and scale.numel() == Hq and not _needs_grad(route_q, c.key, entropy_bias_scale))
+    if fused:
+        rq, qp = route_q.contiguous(), query_positions.contiguous()
+        ac, kv = affected_chunks.contiguous(), c.key_valid.contiguous()
+        st = _lib.call("mrsa_pool_cached_chunks_fwd", _lib.ptr(rq), _lib.ptr(qp), Lq,
+                       _lib.ptr(c.key), _lib.ptr(kv), B, L, _lib.ptr(ac), n, Hkv, G, D, S,
+                       1.0 / D ** 0.5, _lib.ptr(scale), _lib.ptr(c.landmark_keys),
+                       _lib.ptr(c.prior_bias), _lib.stream_of(rq))
+        _lib.check(st, "pool_cached_chunks")
+        return
+    landmark_rows = torch.searchsorted(query_positions, affected_chunks * S + (S - 1))
+    q_lmk = route_q.index_select(1, landmark_rows).reshape(1, n, Hkv, G, D)
+    chunk_positions = (
+        affected_chunks[:, None] * S + torch.arange(S, device=route_q.device)[None, :]
+    ).reshape(-1)
+    chunk_keys = c.key.index_select(1, chunk_positions).reshape(1, n, S, Hkv, D)
+    chunk_valid = c.key_valid.index_select(1, chunk_positions).reshape(1, n, S)
+    lmk, _, prior = chunk_attn_pool_gqa_prior(
+        q_lmk.contiguous(), chunk_keys.contiguous(), chunk_valid.contiguous(),
+        entropy_bias_scale,
+    )
+    c.landmark_keys.index_copy_(1, affected_chunks, lmk.reshape(1, n, Hkv, G, D))
+    c.prior_bias.index_copy_(1, affected_chunks, prior.reshape(1, n, Hkv, G))
 
 
 def cached_route_attention(
@@ -449,19 +510,7 @@ def _cached_route_body(q, route_q, cache, query_positions, affected_chunks, entr
         query_positions=query_positions,
     )
     if n:
-        landmark_rows = torch.searchsorted(query_positions, affected_chunks * S + (S - 1))
-        q_lmk = route_q.index_select(1, landmark_rows).reshape(1, n, Hkv, G, D)
-        chunk_positions = (
-            affected_chunks[:, None] * S + torch.arange(S, device=q.device)[None, :]
-        ).reshape(-1)
-        chunk_keys = cache.key.index_select(1, chunk_positions).reshape(1, n, S, Hkv, D)
-        chunk_valid = cache.key_valid.index_select(1, chunk_positions).reshape(1, n, S)
-        lmk, _, prior = chunk_attn_pool_gqa_prior(
-            q_lmk.contiguous(), chunk_keys.contiguous(), chunk_valid.contiguous(),
-            entropy_bias_scale,
-        )
-        cache.landmark_keys.index_copy_(1, affected_chunks, lmk.reshape(1, n, Hkv, G, D))
-        cache.prior_bias.index_copy_(1, affected_chunks, prior.reshape(1, n, Hkv, G))
+        _refresh_landmarks(route_q, cache, query_positions, affected_chunks, entropy_bias_scale, S)
     drop = drop_mask_rows_launch(cache.key_valid, cfg.local_window, S, query_positions)
     indices, scores = route_topk_launch(
         route_q.reshape(1, Lq, Hkv, G, D),
@@ -537,9 +586,7 @@ class CachedBlockStep:
 
     def _body(self, affected):
         c = self.cache
-        c.key.index_copy_(1, self.positions, self.k_rows)
-        c.value.index_copy_(1, self.positions, self.v_rows)
-        kv_fragments_rows(c.key, c.value, c.kv_frags, self.positions)
+        _write_rows(c, self.positions, self.k_rows, self.v_rows)
         return _cached_route_body(self.q, self.route_q, c, self.positions, affected, self.scale,
                                   self.cfg)
 
@@ -558,16 +605,18 @@ class CachedBlockStep:
         # (the copies fill the graph's own buffers only).
         pending = _check_cached_args(q, route_q, self.cache, query_positions, affected_chunks,
                                      self.cfg, defer=True)
-        self.q.copy_(q)
-        self.route_q.copy_(route_q)
-        self.k_rows.copy_(k_rows)
-        self.v_rows.copy_(v_rows)
-        self.positions.copy_(query_positions)
+        n = affected_chunks.numel()
+        entry = self._graphs.get(n)
+        # the inputs into the graph's buffers, in one launch
+        dst = [self.q, self.route_q, self.k_rows, self.v_rows, self.positions]
+        src = [q, route_q, k_rows, v_rows, query_positions]
+        if entry is not None:
+            dst.append(entry[1])
+            src.append(affected_chunks)
+        _lib.copy_buffers(dst, [t.contiguous() for t in src])
         if pending is not None:
             flags, nf, C = pending
             _raise_cached_flags(flags.tolist(), nf, C)
-        n = affected_chunks.numel()
-        entry = self._graphs.get(n)
         if entry is None:
             affected = affected_chunks.clone()
             # One eager pass first (the step is idempotent: the same rows and
@@ -581,7 +630,6 @@ class CachedBlockStep:
             with torch.cuda.graph(graph):
                 out = self._body(affected)
             entry = self._graphs[n] = (graph, affected, out)
-        graph, affected, out = entry
-        affected.copy_(affected_chunks)
+        graph, _, out = entry
         graph.replay()
         return out

@@ -143,6 +143,103 @@ def test_kv_fragments_rows_bit_exact():
     assert torch.equal(f, mrsa.kv_fragments(k, v))
 
 
+def test_kv_replace_rows_equals_index_copy_and_fragment_rebuild():
+    # mrsa_kv_replace_rows: the rows of LayerKVCache.replace
+    # (fastdllm_cache.py:126-127) and their fragment entries in one launch.
+    _note("kv replace rows")
+    L, Hkv, D = 1000, 4, 128   # last chunk partial
+    g = torch.Generator().manual_seed(94)
+    k = torch.randn(1, L, Hkv, D, generator=g).bfloat16().to(DEV)
+    v = torch.randn(1, L, Hkv, D, generator=g).bfloat16().to(DEV)
+    valid = torch.ones(1, L, dtype=torch.bool, device=DEV)
+    cache = mrsa.LayerKVCache(k.clone(), v.clone(), valid, torch.zeros(1, 15, Hkv, 7, D,
+                              dtype=torch.bfloat16, device=DEV),
+                              torch.zeros(1, 15, Hkv, 7, device=DEV))
+    cache.kv_frags = mrsa.kv_fragments(cache.key, cache.value)
+    pos = torch.tensor([999, 0, 5, 16, 31, 32, 63, 64, 500], device=DEV)
+    kr = torch.randn(1, pos.numel(), Hkv, D, generator=g).bfloat16().to(DEV)
+    vr = torch.randn(1, pos.numel(), Hkv, D, generator=g).bfloat16().to(DEV)
+    cache.replace(pos, kr, vr)
+    k.index_copy_(1, pos, kr)
+    v.index_copy_(1, pos, vr)
+    assert torch.equal(cache.key, k) and torch.equal(cache.value, v)
+    assert torch.equal(cache.kv_frags, mrsa.kv_fragments(k, v))
+    # without fragments only the rows are written
+    bare = mrsa.LayerKVCache(cache.key.clone(), cache.value.clone(), valid,
+                             cache.landmark_keys, cache.prior_bias)
+    kr2 = torch.randn(1, 2, Hkv, D, generator=g).bfloat16().to(DEV)
+    bare.replace(torch.tensor([7, 8], device=DEV), kr2, kr2)
+    k.index_copy_(1, torch.tensor([7, 8], device=DEV), kr2)
+    assert bare.kv_frags is None and torch.equal(bare.key, k)
+
+
+def test_copy_buffers_copies_every_pair():
+    # mrsa_copy_buffers: the graph step's input copies in one launch (16-byte
+    # and 8-byte units; an unaligned pair falls back to copy_).
+    _note("copy buffers")
+    from mrsa import _lib
+    g = torch.Generator().manual_seed(97)
+    src = [torch.randn(1, 32, 28, 128, generator=g).bfloat16().to(DEV),
+           torch.randn(1, 32, 4, 128, generator=g).bfloat16().to(DEV),
+           torch.arange(32, device=DEV), torch.tensor([7], device=DEV),
+           torch.empty(0, dtype=torch.long, device=DEV),
+           torch.randn(3, 5, generator=g).to(DEV)]            # 60 bytes: unaligned size
+    dst = [torch.zeros_like(t) for t in src]
+    _lib.copy_buffers(dst[:5], src[:5])
+    for d, s in zip(dst[:5], src[:5]):
+        assert torch.equal(d, s)
+    _lib.copy_buffers(dst, src)
+    for d, s in zip(dst, src):
+        assert torch.equal(d, s)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.call("mrsa_copy_buffers", 9, None, None, None, _lib.stream_of(src[0])),
+                   "copy_buffers")
+
+
+def test_pool_cached_chunks_equals_the_gathered_pool():
+    # mrsa_pool_cached_chunks_fwd: the landmark refresh of the cached step
+    # (fastdllm_attention.py:236-292) read in place, against the gathered
+    # rows through chunk_attn_pool_gqa_prior and index_copy_ (same bits).
+    L, Hq, Hkv, D, S = 4096, 28, 4, 128, 64
+    C, G = L // S, Hq // Hkv
+    g = torch.Generator().manual_seed(95)
+    k, _ = _planted_kv(L, Hkv, D, 96)
+    k = k.to(DEV)
+    valid = torch.rand(1, L, generator=g) > 0.05
+    valid[0, 64 * 20 : 64 * 21 - 1] = False        # chunk 20: only its landmark slot valid
+    valid = valid.to(DEV)
+    scale = (torch.rand(Hq, generator=g) + 0.5).to(DEV)
+    lmk0 = torch.randn(1, C, Hkv, G, D, generator=g).bfloat16().to(DEV)
+    prior0 = torch.rand(1, C, Hkv, G, generator=g).to(DEV)
+    for rows_lo, affected in ((64 * 19 + 32, [19, 20]), (64 * 40, [40]), (0, [0])):
+        _note(f"pool cached chunks rows {rows_lo}.. affected {affected}")
+        pos = torch.arange(rows_lo, rows_lo + 96, device=DEV)
+        rq = torch.randn(1, pos.numel(), Hq, D, generator=g).bfloat16().to(DEV)
+        aff = torch.tensor(affected, device=DEV)
+        cache = mrsa.LayerKVCache(k, k, valid, lmk0.clone(), prior0.clone())
+        mrsa.route_layer._refresh_landmarks(rq, cache, pos, aff, scale, S)
+        rows = torch.searchsorted(pos, aff * S + (S - 1))
+        chunk_pos = (aff[:, None] * S + torch.arange(S, device=DEV)[None]).reshape(-1)
+        lmk, _, prior = mrsa.chunk_attn_pool_gqa_prior(
+            rq.index_select(1, rows).reshape(1, -1, Hkv, G, D).contiguous(),
+            k.index_select(1, chunk_pos).reshape(1, -1, S, Hkv, D).contiguous(),
+            valid.index_select(1, chunk_pos).reshape(1, -1, S).contiguous(), scale)
+        want_lmk, want_prior = lmk0.clone(), prior0.clone()
+        want_lmk.index_copy_(1, aff, lmk)
+        want_prior.index_copy_(1, aff, prior)
+        assert torch.equal(cache.landmark_keys, want_lmk)
+        assert torch.equal(cache.prior_bias, want_prior)
+    # a chunk out of range, or whose landmark row is not a query position,
+    # is left as it is
+    _note("pool cached chunks: skipped chunks")
+    cache = mrsa.LayerKVCache(k, k, valid, lmk0.clone(), prior0.clone())
+    pos = torch.arange(64 * 5, 64 * 5 + 32, device=DEV)
+    rq = torch.randn(1, 32, Hq, D, generator=g).bfloat16().to(DEV)
+    mrsa.route_layer._refresh_landmarks(rq, cache, pos, torch.tensor([5, C, -1], device=DEV),
+                                        scale, S)
+    assert torch.equal(cache.landmark_keys, lmk0) and torch.equal(cache.prior_bias, prior0)
+
+
 def test_cache_replace_keeps_tiles_and_checks_arguments():
     # LayerKVCache.replace (fastdllm_cache.py:94-125): rows written, the tiled
     # V copy kept in step (the next cached step equals one on a fresh cache),
