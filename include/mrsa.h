@@ -339,6 +339,22 @@ int mrsa_route_weights_fwd(const void* scores, const int32_t* indices, const flo
                            void* stream);
 
 /*
+ * mrsa_route_weights_fwd with _route_weights_torch's two additive inputs
+ * (dream_dllm_hils/attention.py:172-181): value_bonus and selected_gumbel,
+ * fp32 [batch, seq_len, kv_heads * groups, topk] (either may be null), are
+ * added to each valid slot's logit after its bias, in that order, before the
+ * temperature.
+ */
+int mrsa_route_weights_extra_fwd(const void* scores, const int32_t* indices,
+                                 const float* prior_bias, const float* local_lse, int64_t batch,
+                                 int64_t seq_len, int64_t chunks, int64_t kv_heads,
+                                 int64_t groups, int64_t topk, float temperature,
+                                 const float* gate_offset, const float* gate_scale,
+                                 const float* value_bonus, const float* selected_gumbel,
+                                 void* remote_weights, void* local_weight, float* gate_logit,
+                                 void* stream);
+
+/*
  * Backward of the route weights; the row logits are recomputed from the
  * forward inputs.  Replaces _RouteWeights.backward
  * (ops/hils_bidir_route_weights_tilelang.py:185-242, kernel _route_weights_bwd
@@ -366,6 +382,21 @@ int mrsa_route_weights_bwd(const void* scores, const int32_t* indices, const flo
                            int64_t topk, float temperature, const float* gate_offset,
                            const float* gate_scale, float* d_scores, float* d_bias,
                            float* d_local_lse, float* d_gate, void* stream);
+
+/*
+ * mrsa_route_weights_bwd for a forward with value_bonus / selected_gumbel
+ * (mrsa_route_weights_extra_fwd; the same two fp32 inputs, either null).
+ * Their gradients equal d_scores (each is added to the logit as it is).
+ */
+int mrsa_route_weights_extra_bwd(const void* scores, const int32_t* indices,
+                                 const float* prior_bias, const float* local_lse,
+                                 const void* grad_remote, const void* grad_local,
+                                 const float* grad_gate_logit, int64_t batch, int64_t seq_len,
+                                 int64_t chunks, int64_t kv_heads, int64_t groups, int64_t topk,
+                                 float temperature, const float* gate_offset,
+                                 const float* gate_scale, const float* value_bonus,
+                                 const float* selected_gumbel, float* d_scores, float* d_bias,
+                                 float* d_local_lse, float* d_gate, void* stream);
 
 /*
  * Re-lays K and V out as per-chunk fragments: for each 64-key chunk, the

@@ -2,7 +2,8 @@
 // normalised together with the local-branch LSE.
 //
 // Semantics: _route_weights_torch (dream_dllm_hils/attention.py:126-235):
-//   remote_k = valid(idx_k) ? float(score_k) + prior_bias[idx_k] : -inf
+//   remote_k = valid(idx_k) ? float(score_k) + prior_bias[idx_k]
+//              (+ value_bonus_k) (+ selected_gumbel_k) : -inf
 //   local    = local_lse (- gate_offset in the plain form when given)
 //   logits   = [remote, local] / temperature; all -inf -> both outputs 0
 //   plain form:  softmax(logits)
@@ -47,14 +48,16 @@ __device__ __forceinline__ float row_lanes_sum(float v) {
 // I: the index type (uint32_t when every index of the call fits 32 bits,
 // which turns the row decode's divisions into 32-bit ones).  VEC: topk is a
 // multiple of 8 (every lane's 8 slots are real).  UNIT_T: temperature 1 (no
-// 1 / T products).
-template <int LPR, bool VEC, bool UNIT_T, class I>
+// 1 / T products).  EX: the optional additive terms e1 (value bonus) and e2
+// (selected Gumbel noise), fp32 in the scores' layout, may be given.
+template <int LPR, bool VEC, bool UNIT_T, class I, bool EX = false>
 __device__ __forceinline__ void route_weights_row(
     int64_t t64, const uint16_t* __restrict__ scores,
     const int32_t* __restrict__ indices, const float* __restrict__ bias,
     const float* __restrict__ lse, int64_t rows64, int64_t L64, int64_t C64, int Hkv, int G, int K,
     float inv_t, int has_off, int affine, float off, float gscale, uint16_t* __restrict__ rw,
-    uint16_t* __restrict__ lw, float* __restrict__ gate_logit) {
+    uint16_t* __restrict__ lw, float* __restrict__ gate_logit, const float* __restrict__ e1,
+    const float* __restrict__ e2) {
   const I t = (I)t64, rows = (I)rows64, L = (I)L64, C = (I)C64;
   const int part = (int)(t % LPR);
   const I r0 = t / LPR;
@@ -102,7 +105,12 @@ __device__ __forceinline__ void route_weights_row(
     const bool ok = (VEC || k0 + j < K) && c >= 0 && (I)c < C;
     const float bv = brow[(ok ? (I)c : (I)0) * cstride];
     const float s = (j & 1) ? bf16_hi(sv[j >> 1]) : bf16_lo(sv[j >> 1]);
-    x[j] = ok ? (UNIT_T ? s + bv : (s + bv) * inv_t) : neg_inf();
+    float y = s + bv;
+    if constexpr (EX) {
+      if (ok && e1) y += e1[r * (I)K + k0 + j];
+      if (ok && e2) y += e2[r * (I)K + k0 + j];
+    }
+    x[j] = ok ? (UNIT_T ? y : y * inv_t) : neg_inf();
     rmax = fmaxf(rmax, x[j]);
   }
   rmax = row_lanes_max<LPR>(rmax);
@@ -190,29 +198,31 @@ __device__ __forceinline__ void route_weights_row(
   if (part == 0) lw[r] = (uint16_t)f32_to_bf16(lw_val);
 }
 
-template <int LPR, bool VEC, bool UNIT_T, class I>
+template <int LPR, bool VEC, bool UNIT_T, class I, bool EX>
 __global__ void __launch_bounds__(256)
     route_weights_kernel(const uint16_t* __restrict__ scores, const int32_t* __restrict__ indices,
                          const float* __restrict__ bias, const float* __restrict__ lse,
                          int64_t rows, int64_t L, int64_t C, int Hkv, int G, int K, float inv_t,
                          const float* __restrict__ goff, const float* __restrict__ gsc,
                          uint16_t* __restrict__ rw, uint16_t* __restrict__ lw,
-                         float* __restrict__ gate_logit) {
+                         float* __restrict__ gate_logit, const float* __restrict__ e1,
+                         const float* __restrict__ e2) {
   // Gate parameters are device scalars (the layer's parameters, read in
   // place: no host round trip); a null pointer means "not given".
   const int has_off = goff != nullptr, affine = gsc != nullptr;
   const float off = has_off ? *goff : 0.f;
   const float gscale = affine ? *gsc : 1.f;
-  route_weights_row<LPR, VEC, UNIT_T, I>((int64_t)blockIdx.x * blockDim.x + threadIdx.x, scores, indices,
-                              bias, lse, rows, L, C, Hkv, G, K, inv_t, has_off, affine, off,
-                              gscale, rw, lw, gate_logit);
+  route_weights_row<LPR, VEC, UNIT_T, I, EX>((int64_t)blockIdx.x * blockDim.x + threadIdx.x, scores,
+                                             indices, bias, lse, rows, L, C, Hkv, G, K, inv_t,
+                                             has_off, affine, off, gscale, rw, lw, gate_logit, e1,
+                                             e2);
 }
 
 template <int LPR>
 int launch_rw(bool vec, hipStream_t s, const uint16_t* scores, const int32_t* indices,
               const float* bias, const float* lse, int64_t rows, int64_t L, int64_t C, int Hkv,
               int G, int K, float inv_t, const float* goff, const float* gsc, uint16_t* rw,
-              uint16_t* lw, float* gate_logit) {
+              uint16_t* lw, float* gate_logit, const float* e1, const float* e2) {
   const int64_t blocks = (rows * LPR + 255) / 256;
   if (blocks > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
   // 32-bit indices when the largest flat index of the call fits
@@ -220,25 +230,29 @@ int launch_rw(bool vec, hipStream_t s, const uint16_t* scores, const int32_t* in
                      (rows / (Hkv * G) / L + 1) * C * Hkv * G < ((int64_t)1 << 31);
   // the common call (32-bit indices, vectors, temperature 1) has an
   // instance of its own
-  auto kern = small ? (vec ? (inv_t == 1.f ? route_weights_kernel<LPR, true, true, uint32_t>
-                                           : route_weights_kernel<LPR, true, false, uint32_t>)
-                           : route_weights_kernel<LPR, false, false, uint32_t>)
-                    : (vec ? route_weights_kernel<LPR, true, false, int64_t>
-                           : route_weights_kernel<LPR, false, false, int64_t>);
+  // instance of its own; the additive terms take the general one
+  auto kern = (e1 || e2) ? route_weights_kernel<LPR, false, false, int64_t, true>
+              : small ? (vec ? (inv_t == 1.f ? route_weights_kernel<LPR, true, true, uint32_t, false>
+                                             : route_weights_kernel<LPR, true, false, uint32_t, false>)
+                             : route_weights_kernel<LPR, false, false, uint32_t, false>)
+                      : (vec ? route_weights_kernel<LPR, true, false, int64_t, false>
+                             : route_weights_kernel<LPR, false, false, int64_t, false>);
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, s, scores, indices, bias, lse,
-                     rows, L, C, Hkv, G, K, inv_t, goff, gsc, rw, lw, gate_logit);
+                     rows, L, C, Hkv, G, K, inv_t, goff, gsc, rw, lw, gate_logit, e1, e2);
   return mrsa_launch_status();
 }
 
 }  // namespace
 
-extern "C" int mrsa_route_weights_fwd(const void* scores, const int32_t* indices,
-                                      const float* prior_bias, const float* local_lse,
-                                      int64_t batch, int64_t seq_len, int64_t chunks,
-                                      int64_t kv_heads, int64_t groups, int64_t topk,
-                                      float temperature, const float* gate_offset,
-                                      const float* gate_scale, void* remote_weights,
-                                      void* local_weight, float* gate_logit, void* stream) {
+namespace {
+
+int route_weights_fwd(const void* scores, const int32_t* indices, const float* prior_bias,
+                      const float* local_lse, int64_t batch, int64_t seq_len, int64_t chunks,
+                      int64_t kv_heads, int64_t groups, int64_t topk, float temperature,
+                      const float* gate_offset, const float* gate_scale,
+                      const float* value_bonus, const float* selected_gumbel,
+                      void* remote_weights, void* local_weight, float* gate_logit,
+                      void* stream) {
   if (batch < 0 || seq_len < 0 || chunks <= 0 || kv_heads <= 0 || groups <= 0 || topk <= 0 ||
       !(temperature > 0.f))
     return MRSA_ERR_INVALID_ARGUMENT;
@@ -255,12 +269,39 @@ extern "C" int mrsa_route_weights_fwd(const void* scores, const int32_t* indices
     return launch_rw<decltype(lpr)::value>(
         vec, s, (const uint16_t*)scores, indices, prior_bias, local_lse, rows, seq_len, chunks,
         (int)kv_heads, (int)groups, (int)topk, 1.f / temperature, gate_offset, gate_scale,
-        (uint16_t*)remote_weights, (uint16_t*)local_weight, gate_logit);
+        (uint16_t*)remote_weights, (uint16_t*)local_weight, gate_logit, value_bonus,
+        selected_gumbel);
   };
   if (lanes <= 1) return go(std::integral_constant<int, 1>{});
   if (lanes <= 2) return go(std::integral_constant<int, 2>{});
   if (lanes <= 4) return go(std::integral_constant<int, 4>{});
   return go(std::integral_constant<int, 8>{});
+}
+
+}  // namespace
+
+extern "C" int mrsa_route_weights_fwd(const void* scores, const int32_t* indices,
+                                      const float* prior_bias, const float* local_lse,
+                                      int64_t batch, int64_t seq_len, int64_t chunks,
+                                      int64_t kv_heads, int64_t groups, int64_t topk,
+                                      float temperature, const float* gate_offset,
+                                      const float* gate_scale, void* remote_weights,
+                                      void* local_weight, float* gate_logit, void* stream) {
+  return route_weights_fwd(scores, indices, prior_bias, local_lse, batch, seq_len, chunks,
+                           kv_heads, groups, topk, temperature, gate_offset, gate_scale, nullptr,
+                           nullptr, remote_weights, local_weight, gate_logit, stream);
+}
+
+extern "C" int mrsa_route_weights_extra_fwd(
+    const void* scores, const int32_t* indices, const float* prior_bias, const float* local_lse,
+    int64_t batch, int64_t seq_len, int64_t chunks, int64_t kv_heads, int64_t groups,
+    int64_t topk, float temperature, const float* gate_offset, const float* gate_scale,
+    const float* value_bonus, const float* selected_gumbel, void* remote_weights,
+    void* local_weight, float* gate_logit, void* stream) {
+  return route_weights_fwd(scores, indices, prior_bias, local_lse, batch, seq_len, chunks,
+                           kv_heads, groups, topk, temperature, gate_offset, gate_scale,
+                           value_bonus, selected_gumbel, remote_weights, local_weight, gate_logit,
+                           stream);
 }
 
 namespace {
@@ -291,7 +332,8 @@ __global__ void __launch_bounds__(256)
                              const uint16_t* __restrict__ g_lw, const float* __restrict__ g_gl,
                              int64_t rows, int64_t L, int64_t C, int Hkv, int G, int K,
                              float inv_t, const float* __restrict__ goff,
-                             const float* __restrict__ gsc, float* __restrict__ d_scores,
+                             const float* __restrict__ gsc, const float* __restrict__ e1,
+                             const float* __restrict__ e2, float* __restrict__ d_scores,
                              float* __restrict__ d_bias, float* __restrict__ d_lse,
                              float* __restrict__ d_gate) {
   const int has_off = goff != nullptr, affine = gsc != nullptr;
@@ -319,9 +361,12 @@ __global__ void __launch_bounds__(256)
     iv[j] = in ? ix[j] : -1;
     gr[j] = in ? bf16_to_f32(g_rw[r * K + k0 + j]) : 0.f;
     float v = neg_inf();
-    if (in && iv[j] >= 0 && iv[j] < C)
-      v = (bf16_to_f32(scores[r * K + k0 + j]) + bias[((b * C + iv[j]) * Hkv + hk) * G + g]) *
-          inv_t;
+    if (in && iv[j] >= 0 && iv[j] < C) {
+      float y = bf16_to_f32(scores[r * K + k0 + j]) + bias[((b * C + iv[j]) * Hkv + hk) * G + g];
+      if (e1) y += e1[r * K + k0 + j];
+      if (e2) y += e2[r * K + k0 + j];
+      v = y * inv_t;
+    }
     x[j] = v;
     rmax = fmaxf(rmax, v);
   }
@@ -418,15 +463,15 @@ __global__ void __launch_bounds__(256)
 
 }  // namespace
 
-extern "C" int mrsa_route_weights_bwd(const void* scores, const int32_t* indices,
-                                      const float* prior_bias, const float* local_lse,
-                                      const void* grad_remote, const void* grad_local,
-                                      const float* grad_gate_logit, int64_t batch,
-                                      int64_t seq_len, int64_t chunks, int64_t kv_heads,
-                                      int64_t groups, int64_t topk, float temperature,
-                                      const float* gate_offset, const float* gate_scale,
-                                      float* d_scores, float* d_bias, float* d_local_lse,
-                                      float* d_gate, void* stream) {
+namespace {
+
+int route_weights_bwd(const void* scores, const int32_t* indices, const float* prior_bias,
+                      const float* local_lse, const void* grad_remote, const void* grad_local,
+                      const float* grad_gate_logit, int64_t batch, int64_t seq_len,
+                      int64_t chunks, int64_t kv_heads, int64_t groups, int64_t topk,
+                      float temperature, const float* gate_offset, const float* gate_scale,
+                      const float* value_bonus, const float* selected_gumbel, float* d_scores,
+                      float* d_bias, float* d_local_lse, float* d_gate, void* stream) {
   if (batch < 0 || seq_len < 0 || chunks <= 0 || kv_heads <= 0 || groups <= 0 || topk <= 0 ||
       !(temperature > 0.f))
     return MRSA_ERR_INVALID_ARGUMENT;
@@ -446,12 +491,43 @@ extern "C" int mrsa_route_weights_bwd(const void* scores, const int32_t* indices
                        (const uint16_t*)scores, indices, prior_bias, local_lse,
                        (const uint16_t*)grad_remote, (const uint16_t*)grad_local,
                        grad_gate_logit, rows, seq_len, chunks, (int)kv_heads, (int)groups,
-                       (int)topk, 1.f / temperature, gate_offset, gate_scale, d_scores, d_bias,
-                       d_local_lse, (gate_scale || gate_offset) ? d_gate : nullptr);
+                       (int)topk, 1.f / temperature, gate_offset, gate_scale, value_bonus,
+                       selected_gumbel, d_scores, d_bias, d_local_lse,
+                       (gate_scale || gate_offset) ? d_gate : nullptr);
     return mrsa_launch_status();
   };
   if (lanes <= 1) return go(std::integral_constant<int, 1>{});
   if (lanes <= 2) return go(std::integral_constant<int, 2>{});
   if (lanes <= 4) return go(std::integral_constant<int, 4>{});
   return go(std::integral_constant<int, 8>{});
+}
+
+}  // namespace
+
+extern "C" int mrsa_route_weights_bwd(const void* scores, const int32_t* indices,
+                                      const float* prior_bias, const float* local_lse,
+                                      const void* grad_remote, const void* grad_local,
+                                      const float* grad_gate_logit, int64_t batch,
+                                      int64_t seq_len, int64_t chunks, int64_t kv_heads,
+                                      int64_t groups, int64_t topk, float temperature,
+                                      const float* gate_offset, const float* gate_scale,
+                                      float* d_scores, float* d_bias, float* d_local_lse,
+                                      float* d_gate, void* stream) {
+  return route_weights_bwd(scores, indices, prior_bias, local_lse, grad_remote, grad_local,
+                           grad_gate_logit, batch, seq_len, chunks, kv_heads, groups, topk,
+                           temperature, gate_offset, gate_scale, nullptr, nullptr, d_scores,
+                           d_bias, d_local_lse, d_gate, stream);
+}
+
+extern "C" int mrsa_route_weights_extra_bwd(
+    const void* scores, const int32_t* indices, const float* prior_bias, const float* local_lse,
+    const void* grad_remote, const void* grad_local, const float* grad_gate_logit,
+    int64_t batch, int64_t seq_len, int64_t chunks, int64_t kv_heads, int64_t groups,
+    int64_t topk, float temperature, const float* gate_offset, const float* gate_scale,
+    const float* value_bonus, const float* selected_gumbel, float* d_scores, float* d_bias,
+    float* d_local_lse, float* d_gate, void* stream) {
+  return route_weights_bwd(scores, indices, prior_bias, local_lse, grad_remote, grad_local,
+                           grad_gate_logit, batch, seq_len, chunks, kv_heads, groups, topk,
+                           temperature, gate_offset, gate_scale, value_bonus, selected_gumbel,
+                           d_scores, d_bias, d_local_lse, d_gate, stream);
 }

@@ -79,6 +79,16 @@ SIGNATURES = {
         [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P,
          _P, _P, _P, _P],
     ),
+    "mrsa_route_weights_extra_fwd": (
+        _I,
+        [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P,
+         _P, _P, _P, _P, _P, _P],
+    ),
+    "mrsa_route_weights_extra_bwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P,
+         _P, _P, _P, _P, _P, _P, _P],
+    ),
     "mrsa_route_weights_bwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P,

@@ -190,15 +190,16 @@ def _(q5, lmks, indices, grad_scores, sm_scale):
 @_op("route_weights")
 def route_weights(scores: Tensor, indices: Tensor, prior_bias: Tensor, local_lse: Tensor,
                   temperature: float, gate_offset: Optional[Tensor],
-                  gate_scale: Optional[Tensor],
-                  return_gate_logit: bool) -> tuple[Tensor, Tensor, Tensor]:
+                  gate_scale: Optional[Tensor], return_gate_logit: bool,
+                  value_bonus: Optional[Tensor] = None,
+                  selected_gumbel: Optional[Tensor] = None) -> tuple[Tensor, Tensor, Tensor]:
     return _route_weights_impl(scores, indices, prior_bias, local_lse, temperature, gate_offset,
-                               gate_scale, return_gate_logit)
+                               gate_scale, return_gate_logit, value_bonus, selected_gumbel)
 
 
 @route_weights.register_fake
 def _(scores, indices, prior_bias, local_lse, temperature, gate_offset, gate_scale,
-      return_gate_logit):
+      return_gate_logit, value_bonus=None, selected_gumbel=None):
     B, L, Hq, K = scores.shape
     return (scores.new_empty(B, L, Hq, K, dtype=torch.bfloat16),
             scores.new_empty(B, L, Hq, dtype=torch.bfloat16),
@@ -209,16 +210,18 @@ def _(scores, indices, prior_bias, local_lse, temperature, gate_offset, gate_sca
 def route_weights_bwd(scores: Tensor, indices: Tensor, prior_bias: Tensor, local_lse: Tensor,
                       grad_remote: Optional[Tensor], grad_local: Optional[Tensor],
                       grad_gate_logit: Optional[Tensor], temperature: float,
-                      gate_offset: Optional[Tensor],
-                      gate_scale: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+                      gate_offset: Optional[Tensor], gate_scale: Optional[Tensor],
+                      value_bonus: Optional[Tensor] = None,
+                      selected_gumbel: Optional[Tensor] = None,
+                      ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     return _route_weights_bwd_impl(scores, indices, prior_bias, local_lse, grad_remote,
                                    grad_local, grad_gate_logit, temperature, gate_offset,
-                                   gate_scale)
+                                   gate_scale, value_bonus, selected_gumbel)
 
 
 @route_weights_bwd.register_fake
 def _(scores, indices, prior_bias, local_lse, grad_remote, grad_local, grad_gate_logit,
-      temperature, gate_offset, gate_scale):
+      temperature, gate_offset, gate_scale, value_bonus=None, selected_gumbel=None):
     B, L, Hq, K = scores.shape
     return (scores.new_empty(B, L, Hq, K, dtype=torch.float32),
             prior_bias.new_empty(prior_bias.shape, dtype=torch.float32),

@@ -54,21 +54,31 @@ def route_weights_launch(
     gate_offset=None,
     gate_scale=None,
     return_gate_logit: bool = False,
+    value_bonus=None,
+    selected_gumbel=None,
 ):
     """Forward kernel call.  gate_offset / gate_scale: None, a number or a
-    one-element tensor.  Returns (remote bf16, local bf16[, gate_logit fp32])."""
+    one-element tensor; value_bonus / selected_gumbel: None or [B, L, Hq, K]
+    terms added to the remote logits.  Returns (remote bf16, local bf16[,
+    gate_logit fp32])."""
 
     dev = scores.device
     remote, local, gl = torch.ops.mrsa.route_weights(
         scores, indices, prior_bias, local_lse, float(temperature),
-        _gate_tensor(gate_offset, dev), _gate_tensor(gate_scale, dev), bool(return_gate_logit))
+        _gate_tensor(gate_offset, dev), _gate_tensor(gate_scale, dev), bool(return_gate_logit),
+        value_bonus, selected_gumbel)
     if return_gate_logit:
         return remote, local, gl
     return remote, local
 
 
+def _extra(t, like):
+    """An additive logit term as the kernels read it: fp32, contiguous."""
+    return None if t is None else t.to(device=like.device, dtype=torch.float32).contiguous()
+
+
 def _route_weights_impl(scores, indices, prior_bias, local_lse, temperature, off, scl,
-                        return_gate_logit):
+                        return_gate_logit, value_bonus=None, selected_gumbel=None):
     """Kernel call; the gate-logit output is empty unless requested."""
     B, L, Hq, K = scores.shape
     _, C, Hkv, G = prior_bias.shape
@@ -80,13 +90,24 @@ def _route_weights_impl(scores, indices, prior_bias, local_lse, temperature, off
     remote = torch.empty(B, L, Hq, K, dtype=torch.bfloat16, device=dev)
     local = torch.empty(B, L, Hq, dtype=torch.bfloat16, device=dev)
     gl = torch.empty(B, L, Hq if return_gate_logit else 0, dtype=torch.float32, device=dev)
-    st = _lib.call(
-        "mrsa_route_weights_fwd",
-        _lib.ptr(sc), _lib.ptr(idx), _lib.ptr(bias), _lib.ptr(lse),
-        B, L, C, Hkv, G, K, float(temperature), _lib.ptr(off), _lib.ptr(scl),
-        _lib.ptr(remote), _lib.ptr(local), _lib.ptr(gl) if return_gate_logit else None,
-        _lib.stream_of(sc),
-    )
+    vb, gn = _extra(value_bonus, sc), _extra(selected_gumbel, sc)
+    if vb is None and gn is None:
+        st = _lib.call(
+            "mrsa_route_weights_fwd",
+            _lib.ptr(sc), _lib.ptr(idx), _lib.ptr(bias), _lib.ptr(lse),
+            B, L, C, Hkv, G, K, float(temperature), _lib.ptr(off), _lib.ptr(scl),
+            _lib.ptr(remote), _lib.ptr(local), _lib.ptr(gl) if return_gate_logit else None,
+            _lib.stream_of(sc),
+        )
+    else:
+        st = _lib.call(
+            "mrsa_route_weights_extra_fwd",
+            _lib.ptr(sc), _lib.ptr(idx), _lib.ptr(bias), _lib.ptr(lse),
+            B, L, C, Hkv, G, K, float(temperature), _lib.ptr(off), _lib.ptr(scl),
+            _lib.ptr(vb), _lib.ptr(gn),
+            _lib.ptr(remote), _lib.ptr(local), _lib.ptr(gl) if return_gate_logit else None,
+            _lib.stream_of(sc),
+        )
     _lib.check(st, "route_weights")
     return remote, local, gl
 
@@ -104,19 +125,23 @@ def _prepared(scores, indices, prior_bias, local_lse):
 def route_weights_backward(
     scores, indices, prior_bias, local_lse, grad_remote, grad_local, *,
     temperature: float = 1.0, gate_offset=None, gate_scale=None, grad_gate_logit=None,
+    value_bonus=None, selected_gumbel=None,
 ):
     """(d_scores fp32, d_bias fp32, d_local_lse fp32, d_gate fp32[2]) for the
     forward inputs and bf16 upstream gradients (grad_local and
-    grad_gate_logit may be None).  d_gate = (d gate_scale, d gate_offset)."""
+    grad_gate_logit may be None).  d_gate = (d gate_scale, d gate_offset).
+    The gradients of value_bonus and selected_gumbel equal d_scores."""
 
     dev = scores.device
     return torch.ops.mrsa.route_weights_bwd(
         scores, indices, prior_bias, local_lse, grad_remote, grad_local, grad_gate_logit,
-        float(temperature), _gate_tensor(gate_offset, dev), _gate_tensor(gate_scale, dev))
+        float(temperature), _gate_tensor(gate_offset, dev), _gate_tensor(gate_scale, dev),
+        value_bonus, selected_gumbel)
 
 
 def _route_weights_bwd_impl(scores, indices, prior_bias, local_lse, grad_remote, grad_local,
-                            grad_gate_logit, temperature, off, scl):
+                            grad_gate_logit, temperature, off, scl, value_bonus=None,
+                            selected_gumbel=None):
     sc, idx, bias, lse = _prepared(scores, indices, prior_bias, local_lse)
     B, L, Hq, K = sc.shape
     _, C, Hkv, G = bias.shape
@@ -132,11 +157,13 @@ def _route_weights_bwd_impl(scores, indices, prior_bias, local_lse, grad_remote,
     d_bias = torch.zeros(B, C, Hkv, G, dtype=torch.float32, device=dev)
     d_lse = torch.empty(B, L, Hq, dtype=torch.float32, device=dev)
     d_gate = torch.zeros(2, dtype=torch.float32, device=dev)
+    vb, gn = _extra(value_bonus, sc), _extra(selected_gumbel, sc)
     st = _lib.call(
-        "mrsa_route_weights_bwd",
+        "mrsa_route_weights_extra_bwd",
         _lib.ptr(sc), _lib.ptr(idx), _lib.ptr(bias), _lib.ptr(lse), _lib.ptr(g_rw),
         _lib.ptr(g_lw), _lib.ptr(g_gl),
         B, L, C, Hkv, G, K, float(temperature), _lib.ptr(off), _lib.ptr(scl),
+        _lib.ptr(vb), _lib.ptr(gn),
         _lib.ptr(d_scores), _lib.ptr(d_bias), _lib.ptr(d_lse), _lib.ptr(d_gate),
         _lib.stream_of(sc),
     )
@@ -155,19 +182,23 @@ class _RouteWeights(torch.autograd.Function):
     # autograd of attention.py:126-235 (both forms, gate logit included)
     @staticmethod
     def forward(ctx, scores, indices, prior_bias, local_lse, gate_offset, gate_scale,
-                temperature, want_gate_logit):
+                temperature, want_gate_logit, value_bonus=None, selected_gumbel=None):
         prepared = _prepared(scores, indices, prior_bias, local_lse)
         dev = scores.device
         off = _gate_tensor(gate_offset, dev)
         scl = _gate_tensor(gate_scale, dev)
+        vb, gn = _extra(value_bonus, scores), _extra(selected_gumbel, scores)
         outs = route_weights_launch(
             *prepared, temperature=temperature, gate_offset=off, gate_scale=scl,
-            return_gate_logit=want_gate_logit,
+            return_gate_logit=want_gate_logit, value_bonus=vb, selected_gumbel=gn,
         )
         ctx.save_for_backward(*prepared)
         ctx.temperature = temperature
         ctx.gates = (off, scl)
         ctx.params = (gate_offset, gate_scale)
+        ctx.extras = (vb, gn)
+        ctx.extra_dtypes = tuple(None if t is None else t.dtype
+                                 for t in (value_bonus, selected_gumbel))
         ctx.dtypes = (scores.dtype, prior_bias.dtype, local_lse.dtype)
         if want_gate_logit:
             return outs
@@ -181,16 +212,22 @@ class _RouteWeights(torch.autograd.Function):
         off, scl = ctx.gates
         if grad_gate_logit is not None and grad_gate_logit.numel() == 0:
             grad_gate_logit = None
+        vb, gn = ctx.extras
         d_scores, d_bias, d_lse, d_gate = route_weights_backward(
             sc, idx, bias, lse, grad_remote, grad_local, temperature=ctx.temperature,
             gate_offset=off, gate_scale=scl, grad_gate_logit=grad_gate_logit,
+            value_bonus=vb, selected_gumbel=gn,
         )
         s_dt, b_dt, l_dt = ctx.dtypes
         p_off, p_scale = ctx.params
+        # value_bonus and selected_gumbel enter the logits as the scores do
+        n_in = len(ctx.needs_input_grad)
+        d_extra = tuple(None if dt is None or 8 + i >= n_in or not ctx.needs_input_grad[8 + i]
+                        else d_scores.to(dt) for i, dt in enumerate(ctx.extra_dtypes))
         return (
             d_scores.to(s_dt), None, d_bias.to(b_dt), d_lse.to(l_dt),
             _gate_grad(p_off, d_gate[1]), _gate_grad(p_scale, d_gate[0]), None, None,
-        )
+        ) + d_extra[:n_in - 8]
 
 
 def _needs_grad(*xs):
@@ -248,9 +285,10 @@ def route_weights_torch(
 
     gate_scale selects the affine-sigmoid form; gate_offset / gate_scale are
     read on the device (the layer's parameters, no host round trip).  With
-    return_gate_logit the third output is the fp32 gate logit.  The
-    training-only additive inputs (selected_gumbel, value_bonus,
-    attention.py:172-181) are rejected with ValueError.
+    return_gate_logit the third output is the fp32 gate logit.
+    value_bonus and selected_gumbel (attention.py:172-181: value-aware fusion
+    and top-k-restricted Gumbel noise) are added to the remote logits after
+    the bias, in that order; both are differentiable.
     """
 
     if temperature <= 0:
@@ -275,19 +313,17 @@ def route_weights_torch(
         raise ValueError(f"invalid selected_gumbel shape {tuple(selected_gumbel.shape)}")
     if value_bonus is not None and value_bonus.shape != scores.shape:
         raise ValueError(f"invalid value_bonus shape {tuple(value_bonus.shape)}")
-    if selected_gumbel is not None or value_bonus is not None:
-        raise ValueError(
-            "selected_gumbel / value_bonus (training-time Gumbel routing and value-aware "
-            "fusion) are not supported by the gfx950 route-weights kernel")
     if scores.device.type != "cuda":
         raise ValueError("route_weights requires CUDA tensors")
-    if _needs_grad(scores, prior_bias, local_lse, gate_offset, gate_scale):
+    if _needs_grad(scores, prior_bias, local_lse, gate_offset, gate_scale, value_bonus,
+                   selected_gumbel):
         remote, local, gl = _RouteWeights.apply(
             scores, indices, prior_bias, local_lse, gate_offset, gate_scale, float(temperature),
-            bool(return_gate_logit),
+            bool(return_gate_logit), value_bonus, selected_gumbel,
         )
         return (remote, local, gl) if return_gate_logit else (remote, local)
     return route_weights_launch(
         scores, indices, prior_bias, local_lse, temperature=temperature,
         gate_offset=gate_offset, gate_scale=gate_scale, return_gate_logit=return_gate_logit,
+        value_bonus=value_bonus, selected_gumbel=selected_gumbel,
     )

@@ -306,8 +306,12 @@ def route_score_bwd(q5, lmks, indices, grad_scores, sm_scale=None):
 # a7: route weights
 # ---------------------------------------------------------------------------
 def route_weights(scores, indices, prior_bias, local_lse, *, temperature=1.0,
-                  gate_offset=None, gate_scale=None, return_gate_logit=False):
+                  gate_offset=None, gate_scale=None, return_gate_logit=False,
+                  value_bonus=None, selected_gumbel=None):
     """_route_weights_torch (dream_dllm_hils/attention.py:126-235), fp32 outputs.
+
+    value_bonus and selected_gumbel ([B, L, Hq, K], optional) are added to the
+    remote logits after the bias, in that order (:172-181).
 
     scores [B, L, Hq, K] (bf16 values), indices [B, L, Hkv, K], prior_bias
     [B, C, Hkv, G], local_lse [B, L, Hq].  Returns (remote [B, L, Hq, K],
@@ -329,7 +333,12 @@ def route_weights(scores, indices, prior_bias, local_lse, *, temperature=1.0,
     safe = idx.clamp(0, C - 1)
     bias_by_head = prior_bias.float().reshape(B, C, Hq).permute(0, 2, 1)
     sel_bias = torch.gather(bias_by_head[:, None].expand(B, L, Hq, C), -1, safe)
-    remote_logits = (scores.float() + sel_bias).masked_fill(~valid, NEG_INF)
+    remote_logits = scores.float() + sel_bias
+    if value_bonus is not None:
+        remote_logits = remote_logits + value_bonus.float()
+    if selected_gumbel is not None:
+        remote_logits = remote_logits + selected_gumbel.float()
+    remote_logits = remote_logits.masked_fill(~valid, NEG_INF)
     local_logits = local_lse.float()[..., None]
     affine = gate_scale is not None
     if gate_offset is not None and not affine:

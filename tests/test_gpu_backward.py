@@ -427,3 +427,44 @@ def test_selected_attention_backward_long_chunk_lists():
         err = _rel_err(got, exp)
         print(f"  {name}: rel-norm error {err:.3e}")
         assert err < 2e-2, name
+
+
+@pytest.mark.parametrize("affine,T", [(False, 0.8), (True, 1.3)])
+def test_route_weights_value_bonus_and_gumbel_vs_oracle(affine, T):
+    # _route_weights_torch(selected_gumbel=, value_bonus=) (attention.py:172-181):
+    # forward against the oracle, and the two terms' gradients equal the
+    # scores' (fp32) -- each enters the logit as the score does.
+    _note(f"route weights extras affine={affine} T={T}")
+    B, L, Hkv, G, K, C = 1, 96, 2, 7, 32, 50
+    scores, idx, bias, lse, g_rw, g_lw = _case(123, B, L, Hkv, G, K, C)
+    g = torch.Generator().manual_seed(124)
+    vb = torch.randn(scores.shape, generator=g) * 0.5
+    gn = -torch.log(-torch.log(torch.rand(scores.shape, generator=g).clamp(1e-6, 1 - 1e-6)))
+    kw = dict(temperature=T, gate_offset=0.2 if affine else None,
+              gate_scale=0.9 if affine else None)
+    rw, lw = mrsa.route_weights_torch(scores.to(DEV), idx.to(DEV), bias.to(DEV), lse.to(DEV),
+                                      value_bonus=vb.to(DEV), selected_gumbel=gn.to(DEV), **kw)
+    erw, elw = O.route_weights(scores, idx, bias, lse, value_bonus=vb, selected_gumbel=gn, **kw)
+    _close(rw, erw.bfloat16(), "remote weights", atol=1e-3, rtol=8e-3)
+    _close(lw, elw.bfloat16(), "local weight", atol=1e-3, rtol=8e-3)
+    # without the terms the weights differ (the terms reach the kernel)
+    rw0, _ = mrsa.route_weights_torch(scores.to(DEV), idx.to(DEV), bias.to(DEV), lse.to(DEV),
+                                      **kw)
+    assert not torch.equal(rw0, rw)
+    # gradients
+    s = scores.to(DEV).float().requires_grad_(True)
+    v = vb.to(DEV).requires_grad_(True)
+    n = gn.to(DEV).requires_grad_(True)
+    rw, lw = mrsa.route_weights_torch(s, idx.to(DEV), bias.to(DEV), lse.to(DEV),
+                                      value_bonus=v, selected_gumbel=n, **kw)
+    (rw.float() * g_rw.to(DEV).float()).sum().add_((lw.float() * g_lw.to(DEV).float()).sum()).backward()
+    so = scores.float().requires_grad_(True)
+    vo = vb.clone().requires_grad_(True)
+    go = None if not affine else torch.tensor(0.2)
+    gs = None if not affine else torch.tensor(0.9)
+    erw, elw = O.route_weights(so, idx, bias, lse, temperature=T, gate_offset=go, gate_scale=gs,
+                               value_bonus=vo, selected_gumbel=gn)
+    (erw * g_rw.float()).sum().add_((elw * g_lw.float()).sum()).backward()
+    _close(v.grad, vo.grad, "value_bonus.grad")
+    _close(s.grad, so.grad, "scores.grad")
+    assert torch.equal(v.grad, n.grad) and torch.equal(v.grad, s.grad)

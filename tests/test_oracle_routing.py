@@ -215,3 +215,35 @@ def test_route_weights_temperature_closed_form():
             local = 1.0 - 1.0 / (1.0 + math.exp(-gate))
             assert abs(float(lw) - local) < 1e-6
             assert abs(float(rw.sum() + lw) - 1.0) < 1e-6
+
+
+def test_route_weights_additive_terms_enter_the_remote_logits():
+    # attention.py:172-181: value_bonus and selected_gumbel are added to the
+    # remote logits after the bias, before the temperature.  With integer
+    # values every sum is exact, so a call with the terms equals the call
+    # whose bf16 scores already hold them -- in both forms, at T != 1, with
+    # masked slots staying masked.  A term added after the temperature, to
+    # the local logit, or to a masked slot breaks the equality.
+    g = torch.Generator().manual_seed(31)
+    B, L, H, G, K, C = 1, 4, 2, 3, 8, 12
+    scores = torch.randint(-4, 5, (B, L, H * G, K), generator=g).float()
+    vb = torch.randint(-3, 4, scores.shape, generator=g).float()
+    gn = torch.randint(-2, 3, scores.shape, generator=g).float()
+    idx = torch.randint(0, C, (B, L, H, K), generator=g)
+    idx[0, 1, 0, 5:] = -1
+    idx[0, 2, 1, 0] = C + 3
+    bias = torch.randint(-2, 3, (B, C, H, G), generator=g).float()
+    lse = torch.randint(-2, 3, (B, L, H * G), generator=g).float()
+    for kw in (dict(temperature=0.5), dict(temperature=2.0, gate_offset=0.25, gate_scale=1.5),
+               dict(temperature=1.0, gate_offset=-0.5, return_gate_logit=True)):
+        got = O.route_weights(scores.bfloat16(), idx, bias, lse, value_bonus=vb,
+                              selected_gumbel=gn, **kw)
+        want = O.route_weights((scores + vb + gn).bfloat16(), idx, bias, lse, **kw)
+        for a, b in zip(got, want):
+            assert torch.equal(a, b)
+        one = O.route_weights(scores.bfloat16(), idx, bias, lse, value_bonus=vb, **kw)
+        want1 = O.route_weights((scores + vb).bfloat16(), idx, bias, lse, **kw)
+        for a, b in zip(one, want1):
+            assert torch.equal(a, b)
+    assert not torch.equal(got[0], O.route_weights(scores.bfloat16(), idx, bias, lse,
+                                                   temperature=1.0, gate_offset=-0.5)[0])
