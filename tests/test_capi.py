@@ -107,11 +107,11 @@ def test_walk_parts_heuristic():
 
     # Long sequences: one workgroup per walk.
     assert walk_parts(1, 16384, 4, 16384, 32) == 1
-    # The cached block step (32 queries, 4 KV heads, 2048 chunks): 64 parts.
-    assert walk_parts(1, 32, 4, 131072, 32) == 64
-    # Parts keep >= 16 steps each: 3 queries x 4 chunks -> 12 steps -> 1.
+    # The cached block step (32 queries, 4 KV heads, 2048 chunks): 32 parts.
+    assert walk_parts(1, 32, 4, 131072, 32) == 32
+    # Parts keep >= 32 steps each: 3 queries x 4 chunks -> 12 steps -> 1.
     assert walk_parts(1, 3, 4, 131072, 4) == 1
-    assert walk_parts(1, 32, 4, 4096, 32) == 4
+    assert walk_parts(1, 32, 4, 4096, 32) == 2
     assert walk_parts(0, 32, 4, 4096, 32) == 1
 
 
