@@ -74,6 +74,27 @@ __device__ __forceinline__ int64_t causal_limit(const RouteArgs& a, int64_t r) {
   return floor_div(tq, a.block_size);
 }
 
+// Whether a chunk has a valid real key: one of its first block_size - 1
+// valid bytes (the last slot is the landmark) is set.  Four 16-byte loads
+// for 64-key chunks at a 16-byte aligned address.
+__device__ __forceinline__ bool chunk_has_valid_key(const uint8_t* kv, int64_t block_size) {
+  if (block_size == 64 && ((uintptr_t)kv & 15) == 0) {
+    u32x4_t acc = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const u32x4_t x = *reinterpret_cast<const u32x4_t*>(kv + 16 * v);
+      acc[0] |= x[0];
+      acc[1] |= x[1];
+      acc[2] |= x[2];
+      acc[3] |= v == 3 ? (x[3] & 0x00ffffffu) : x[3];
+    }
+    return (acc[0] | acc[1] | acc[2] | acc[3]) != 0u;
+  }
+  bool any = false;
+  for (int64_t t = 0; t < block_size - 1; ++t) any |= kv[t] != 0;
+  return any;
+}
+
 __device__ __forceinline__ const uint16_t* lmk_row(const RouteArgs& a, int64_t b, int64_t c, int h,
                                                    int g) {
   if (a.per_head_lmk) return a.lmk + ((b * a.C + c) * (int64_t)(a.Hkv * a.G) + h * a.G + g) * a.D;
@@ -236,6 +257,34 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_fast_kernel(RouteA
     for (int ks = 0; ks < 4; ++ks) Q[ks] = *reinterpret_cast<const u32x4_t*>(src + 32 * ks);
   };
 
+  // An explicit drop mask, read before pass 1 while few registers are live,
+  // so that its loads are in flight together: bit 4 t + e of this lane's
+  // word is chunk 16 t + 4 grp + e (chunks >= C dropped).
+  uint64_t dropbits = 0ull;
+  if (a.derive_window < 0 && a.drop) {
+    const int32_t* drow = a.drop + (b * L + rr) * C;
+    if (C == 256 && ((uintptr_t)a.drop & 15) == 0) {
+      u32x4_t d[16];
+#pragma unroll
+      for (int t = 0; t < 16; ++t) d[t] = *reinterpret_cast<const u32x4_t*>(drow + 16 * t + 4 * grp);
+#pragma unroll
+      for (int t = 0; t < 16; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dropbits |= (uint64_t)(d[t][e] != 0u) << (4 * t + e);
+    } else {
+      int32_t d[16][4];
+#pragma unroll
+      for (int t = 0; t < 16; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) d[t][e] = drow[min(16 * t + 4 * grp + e, (int)C - 1)];
+#pragma unroll
+      for (int t = 0; t < 16; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          dropbits |= (uint64_t)((16 * t + 4 * grp + e >= C) | (d[t][e] != 0)) << (4 * t + e);
+    }
+  }
+
   // ---- pass 1 -------------------------------------------------------------
   float M[16][4];
 #pragma unroll
@@ -340,24 +389,11 @@ __global__ void __launch_bounds__(kFastThreads, 1) route_topk_fast_kernel(RouteA
       }
     }
   } else if (a.drop) {
-    const int32_t* drow = a.drop + (b * L + rr) * C;
-    if (C == 256 && ((uintptr_t)a.drop & 15) == 0) {
 #pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        const u32x4_t d = *reinterpret_cast<const u32x4_t*>(drow + 16 * t + 4 * grp);
+    for (int t = 0; t < 16; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) key[t][e] = d[e] != 0u ? kNeg : float_order_key(M[t][e]);
-      }
-    } else {
-#pragma unroll
-      for (int t = 0; t < 16; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int c = 16 * t + 4 * grp + e;
-          const bool dropped = (c >= C) | (drow[min(c, (int)C - 1)] != 0);
-          key[t][e] = dropped ? kNeg : float_order_key(M[t][e]);
-        }
-    }
+      for (int e = 0; e < 4; ++e)
+        key[t][e] = ((dropbits >> (4 * t + e)) & 1ull) ? kNeg : float_order_key(M[t][e]);
   } else {
 #pragma unroll
     for (int t = 0; t < 16; ++t)
@@ -936,29 +972,35 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
   const float* xr = raw + row * (int64_t)G * C;
   const int64_t climit = a.is_causal ? causal_limit(a, r) : C;
 
-  // 1. x = s + bias (-inf past the causal limit or the last chunk).
+  // 1. x = s + bias (-inf past the causal limit or the last chunk).  The
+  //    loads are unconditional (slots past the row read chunk 0), with no
+  //    branch between them, so that they are all in flight at once: loads
+  //    inside per-element branches were each waited for at the branch's end.
   float x[kSelMaxPer][G];
 #pragma unroll
   for (int i = 0; i < kSelMaxPer; ++i) {
     const int64_t c = tid + (int64_t)kSelThreads * i;
-    const bool ok = i < n && c < C;
-    const int64_t cc = ok ? c : 0;
+    const int64_t cc = i < n && c < C ? c : 0;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float v = neg_inf();
-      if (ok) {
-        v = xr[(int64_t)g * C + cc];
-        if (a.bias) v += a.bias[((b * C + cc) * a.Hkv + h) * G + g];
-      }
-      x[i][g] = v;
+    for (int g = 0; g < G; ++g) x[i][g] = xr[(int64_t)g * C + cc];
+  }
+  if (a.bias) {
+    const float* brow = a.bias + (b * C * a.Hkv + h) * G;  // chunk c at c Hkv G
+    const int64_t bstride = (int64_t)a.Hkv * G;
+#pragma unroll
+    for (int i = 0; i < kSelMaxPer; ++i) {
+      const int64_t c = tid + (int64_t)kSelThreads * i;
+      const int64_t cc = i < n && c < C ? c : 0;
+#pragma unroll
+      for (int g = 0; g < G; ++g) x[i][g] += brow[cc * bstride + g];
     }
   }
 #pragma unroll
   for (int i = 0; i < kSelMaxPer; ++i) {
     const int64_t c = tid + (int64_t)kSelThreads * i;
-    if (c >= climit)
+    const bool ok = i < n && c < C && c < climit;
 #pragma unroll
-      for (int g = 0; g < G; ++g) x[i][g] = neg_inf();
+    for (int g = 0; g < G; ++g) x[i][g] = ok ? x[i][g] : neg_inf();
   }
 
   // 2. Per-head LSE over every chunk (dropped ones included).
@@ -993,35 +1035,54 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
     lc = max(r - a.derive_window, (int64_t)0) / a.block_size;
     rc = min(r + a.derive_window, L - 1) / a.block_size;
   }
+  // Drop flags first, one uniform branch per drop source (loads batched as
+  // in step 1).
+  bool dropped[kSelMaxPer];
+  if (a.derive_window >= 0) {
+#pragma unroll
+    for (int i = 0; i < kSelMaxPer; ++i) {
+      const int64_t c = tid + (int64_t)kSelThreads * i;
+      const int64_t cc = i < n && c < C ? c : 0;
+      bool any = a.block_size > 1;
+      if (a.key_valid) any = chunk_has_valid_key(a.key_valid + b * L + cc * a.block_size,
+                                                 a.block_size);
+      dropped[i] = (c >= lc && c <= rc) || !any;
+    }
+  } else if (a.drop) {
+#pragma unroll
+    for (int i = 0; i < kSelMaxPer; ++i) {
+      const int64_t c = tid + (int64_t)kSelThreads * i;
+      const int64_t cc = i < n && c < C ? c : 0;
+      dropped[i] = a.drop[(b * L + r) * C + cc] != 0;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kSelMaxPer; ++i) dropped[i] = false;
+  }
   uint32_t key[kSelMaxPer];
 #pragma unroll
   for (int i = 0; i < kSelMaxPer; ++i) {
-    key[i] = 0u;  // below every real key: never picked
     const int64_t c = tid + (int64_t)kSelThreads * i;
-    if (i >= n || c >= C) continue;
     float best = neg_inf();
 #pragma unroll
     for (int g = 0; g < G; ++g) best = fmaxf(best, x[i][g] == neg_inf() ? x[i][g] : x[i][g] - tot[g]);
-    bool dropped = false;
-    if (a.derive_window >= 0) {
-      bool any = false;
-      if (a.key_valid) {
-        const uint8_t* kv = a.key_valid + b * L + c * a.block_size;
-        for (int64_t t = 0; t < a.block_size - 1; ++t) any |= kv[t] != 0;
-      } else {
-        any = a.block_size > 1;
-      }
-      dropped = (c >= lc && c <= rc) || !any;
-    } else if (a.drop) {
-      dropped = a.drop[(b * L + r) * C + c] != 0;
-    }
-    key[i] = float_order_key(dropped ? neg_inf() : best);
+    // 0 is below every real key: never picked
+    key[i] = i < n && c < C ? float_order_key(dropped[i] ? neg_inf() : best) : 0u;
   }
 
   // 4. The K largest (ties to the lower chunk), in ascending chunk order.
   bool pick[kSelMaxPer];
   int slot[kSelMaxPer];
   const int slot_base = Select::run(key, n, K, sel, pick, slot);
+  // The picks' raw scores, all loaded before any store.
+  float sv[kSelMaxPer][G];
+#pragma unroll
+  for (int i = 0; i < kSelMaxPer; ++i) {
+    const int64_t c = tid + (int64_t)kSelThreads * i;
+    const int64_t cc = i < n && c < C ? c : 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) sv[i][g] = xr[(int64_t)g * C + cc];
+  }
 #pragma unroll
   for (int i = 0; i < kSelMaxPer; ++i) {
     if (i >= n || !pick[i]) continue;
@@ -1029,7 +1090,7 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
     a.indices[row * K + slot[i]] = (int32_t)c;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float v = xr[(int64_t)g * C + c];
+      const float v = sv[i][g];
       if (a.scores_fp32)
         reinterpret_cast<float*>(a.scores)[(row * G + g) * K + slot[i]] = v;
       else
@@ -1053,15 +1114,21 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
 // LSEs come from one pass with a per-lane online max / sum; the keys are
 // formed from the logits held in registers when PER * G <= 128 (C <= 1024 at
 // G = 8) and from a second read of the row otherwise.  Same score, LSE, drop
-// and tie rules as route_select_kernel.
+// and tie rules as route_select_kernel.  Global loads are unconditional
+// (slots past the row read chunk 0) and issued kB slots at a time with no
+// branch between them: loads inside per-slot branches were each waited for
+// at the branch's end.  topk <= 64: the picks' chunks pass through the
+// wave's LDS row so that lane t writes output slot t.
 template <int G, int PER>
 __global__ void __launch_bounds__(256) route_select_wave_kernel(RouteArgs a,
                                                                 const float* __restrict__ raw) {
   constexpr bool kHold = PER * G <= 128;
+  constexpr int kB = kHold ? PER : 8;  // slots per batch of loads
+  __shared__ int32_t pick_c[4][64];
   const int64_t C = a.C, L = a.L;
   const int K = a.K;
-  const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t r = (int64_t)blockIdx.x * 4 + wv;
   if (r >= L) return;  // wave-uniform
   const int h = blockIdx.y;
   const int64_t b = blockIdx.z;
@@ -1070,15 +1137,37 @@ __global__ void __launch_bounds__(256) route_select_wave_kernel(RouteArgs a,
   const float* xr = raw + row * (int64_t)G * C;
   const int64_t climit = a.is_causal ? causal_limit(a, r) : C;
   const float* bias = a.bias ? a.bias + (b * C * a.Hkv + h) * G : nullptr;  // + c * Hkv * G + g
+  const int64_t bstride = (int64_t)a.Hkv * G;
 
-  auto logit = [&](int g, int64_t c) -> float {
-    if (c >= climit) return neg_inf();
-    float v = xr[(int64_t)g * C + c];
-    if (bias) v += bias[c * a.Hkv * G + g];
-    return v;
+  // x of slots i0 .. i0 + kB - 1: raw + bias, -inf past the row or the
+  // causal limit.
+  auto load_batch = [&](int i0, float (&v)[kB][G]) {
+#pragma unroll
+    for (int ii = 0; ii < kB; ++ii) {
+      const int64_t c = lane + 64 * (int64_t)(i0 + ii);
+      const int64_t cc = i0 + ii < n && c < C ? c : 0;
+#pragma unroll
+      for (int g = 0; g < G; ++g) v[ii][g] = xr[(int64_t)g * C + cc];
+    }
+    if (bias) {
+#pragma unroll
+      for (int ii = 0; ii < kB; ++ii) {
+        const int64_t c = lane + 64 * (int64_t)(i0 + ii);
+        const int64_t cc = i0 + ii < n && c < C ? c : 0;
+#pragma unroll
+        for (int g = 0; g < G; ++g) v[ii][g] += bias[cc * bstride + g];
+      }
+    }
+#pragma unroll
+    for (int ii = 0; ii < kB; ++ii) {
+      const int64_t c = lane + 64 * (int64_t)(i0 + ii);
+      const bool ok = i0 + ii < n && c < C && c < climit;
+#pragma unroll
+      for (int g = 0; g < G; ++g) v[ii][g] = ok ? v[ii][g] : neg_inf();
+    }
   };
 
-  float hold[kHold ? PER : 1][G];
+  float hold[kB][G];
   float m[G], sum[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -1086,19 +1175,21 @@ __global__ void __launch_bounds__(256) route_select_wave_kernel(RouteArgs a,
     sum[g] = 0.f;
   }
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int64_t c = lane + 64 * (int64_t)i;
+  for (int i0 = 0; i0 < PER; i0 += kB) {
+    if (i0 >= n) break;  // uniform
+    load_batch(i0, hold);
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float v = (i < n && c < C) ? logit(g, c) : neg_inf();
-      if (kHold) hold[i][g] = v;
-      if (v > m[g]) {
-        sum[g] = (m[g] == neg_inf() ? 0.f : sum[g] * expf(m[g] - v)) + 1.f;
-        m[g] = v;
-      } else if (v != neg_inf()) {
-        sum[g] += expf(v - m[g]);
+    for (int ii = 0; ii < kB; ++ii)
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float v = hold[ii][g];
+        if (v > m[g]) {
+          sum[g] = (m[g] == neg_inf() ? 0.f : sum[g] * expf(m[g] - v)) + 1.f;
+          m[g] = v;
+        } else if (v != neg_inf()) {
+          sum[g] += expf(v - m[g]);
+        }
       }
-    }
   }
   float tot[G];
 #pragma unroll
@@ -1109,37 +1200,45 @@ __global__ void __launch_bounds__(256) route_select_wave_kernel(RouteArgs a,
     tot[g] = a.pre_softmax ? 0.f : logaddexp_f(a.lse[row * G + g], lse_h);
   }
 
-  int64_t lc = 0, rc = -1;
+  // Drop flags (bit i: slot i), one uniform branch per drop source.
+  uint64_t dropbits = 0ull;
   if (a.derive_window >= 0) {
-    lc = max(r - a.derive_window, (int64_t)0) / a.block_size;
-    rc = min(r + a.derive_window, L - 1) / a.block_size;
+    const int64_t lc = max(r - a.derive_window, (int64_t)0) / a.block_size;
+    const int64_t rc = min(r + a.derive_window, L - 1) / a.block_size;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int64_t c = lane + 64 * (int64_t)i;
+      const int64_t cc = i < n && c < C ? c : 0;
+      bool any = a.block_size > 1;
+      if (a.key_valid) any = chunk_has_valid_key(a.key_valid + b * L + cc * a.block_size,
+                                                 a.block_size);
+      dropbits |= (uint64_t)((c >= lc && c <= rc) || !any) << i;
+    }
+  } else if (a.drop) {
+    const int32_t* drow = a.drop + (b * L + r) * C;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int64_t c = lane + 64 * (int64_t)i;
+      dropbits |= (uint64_t)(drow[i < n && c < C ? c : 0] != 0) << i;
+    }
   }
   uint32_t key[PER];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    key[i] = 0u;  // below every real key: never picked
-    const int64_t c = lane + 64 * (int64_t)i;
-    if (i >= n || c >= C) continue;
-    float best = neg_inf();
+  for (int i0 = 0; i0 < PER; i0 += kB) {
+    if (!kHold && i0 < n) load_batch(i0, hold);  // uniform
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float x = kHold ? hold[i][g] : logit(g, c);
-      best = fmaxf(best, x == neg_inf() ? x : x - tot[g]);
-    }
-    bool dropped = false;
-    if (a.derive_window >= 0) {
-      bool any = false;
-      if (a.key_valid) {
-        const uint8_t* kv = a.key_valid + b * L + c * a.block_size;
-        for (int64_t t = 0; t < a.block_size - 1; ++t) any |= kv[t] != 0;
-      } else {
-        any = a.block_size > 1;
+    for (int ii = 0; ii < kB; ++ii) {
+      const int i = i0 + ii;
+      const int64_t c = lane + 64 * (int64_t)i;
+      float best = neg_inf();
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float x = hold[ii][g];
+        best = fmaxf(best, x == neg_inf() ? x : x - tot[g]);
       }
-      dropped = (c >= lc && c <= rc) || !any;
-    } else if (a.drop) {
-      dropped = a.drop[(b * L + r) * C + c] != 0;
+      // 0 is below every real key: never picked
+      key[i] = i < n && c < C ? float_order_key(((dropbits >> i) & 1ull) ? neg_inf() : best) : 0u;
     }
-    key[i] = float_order_key(dropped ? neg_inf() : best);
   }
 
   const uint64_t picks = WaveSelect<PER>::run(key, n, K);
@@ -1150,29 +1249,26 @@ __global__ void __launch_bounds__(256) route_select_wave_kernel(RouteArgs a,
     if (i >= n) continue;  // uniform
     const bool p = (picks >> i) & 1ull;
     const uint64_t pb = __builtin_amdgcn_ballot_w64(p);
-    if (p) {
-      const int slot = base + __builtin_popcountll(pb & below);
-      const int64_t c = lane + 64 * (int64_t)i;
-      a.indices[row * K + slot] = (int32_t)c;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float v = xr[(int64_t)g * C + c];
-        if (a.scores_fp32)
-          reinterpret_cast<float*>(a.scores)[(row * G + g) * K + slot] = v;
-        else
-          reinterpret_cast<uint16_t*>(a.scores)[(row * G + g) * K + slot] =
-              (uint16_t)f32_to_bf16(v);
-      }
-    }
+    if (p) pick_c[wv][base + __builtin_popcountll(pb & below)] = (int32_t)(lane + 64 * i);
     base += __builtin_popcountll(pb);
   }
-  for (int t = base + lane; t < K; t += 64) {
-    a.indices[row * K + t] = -1;
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS row only
+  // lane t writes output slot t (K <= 64)
+  if (lane < K) {
+    const int t = lane;
+    const bool live = t < base;
+    const int32_t c = live ? pick_c[wv][t] : 0;
+    float v[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) v[g] = xr[(int64_t)g * C + c];
+    a.indices[row * K + t] = live ? c : -1;
+#pragma unroll
     for (int g = 0; g < G; ++g) {
       if (a.scores_fp32)
-        reinterpret_cast<float*>(a.scores)[(row * G + g) * K + t] = neg_inf();
+        reinterpret_cast<float*>(a.scores)[(row * G + g) * K + t] = live ? v[g] : neg_inf();
       else
-        reinterpret_cast<uint16_t*>(a.scores)[(row * G + g) * K + t] = 0xff80u;
+        reinterpret_cast<uint16_t*>(a.scores)[(row * G + g) * K + t] =
+            live ? (uint16_t)f32_to_bf16(v[g]) : (uint16_t)0xff80u;
     }
   }
 }
@@ -1205,7 +1301,8 @@ int launch_block(const RouteArgs& a, float* raw, hipStream_t s) {
   hipLaunchKernelGGL(route_logits_kernel, g1, dim3(64 * a.G), 0, s, a, raw);
   int st = mrsa_launch_status();
   if (st != MRSA_OK) return st;
-  if (a.B * a.L * a.Hkv >= kWaveSelectRows && a.C <= 4096 && a.L <= 0x7ffffffc) {
+  if (a.B * a.L * a.Hkv >= kWaveSelectRows && a.C <= 4096 && a.K <= 64 &&
+      a.L <= 0x7ffffffc) {
     if (a.G == 7) return launch_select_wave<7>(a, raw, s);
     if (a.G == 8) return launch_select_wave<8>(a, raw, s);
   }
