@@ -107,8 +107,12 @@ __device__ __forceinline__ void route_weights_row(
     const float s = (j & 1) ? bf16_hi(sv[j >> 1]) : bf16_lo(sv[j >> 1]);
     float y = s + bv;
     if constexpr (EX) {
-      if (ok && e1) y += e1[r * (I)K + k0 + j];
-      if (ok && e2) y += e2[r * (I)K + k0 + j];
+      // clamped slots: every load unconditional (see the backward kernel)
+      const I kk = r * (I)K + (I)min(k0 + j, K - 1);
+      const float t1 = e1 ? e1[kk] : 0.f;
+      const float t2 = e2 ? e2[kk] : 0.f;
+      if (e1) y += t1;
+      if (e2) y += t2;
     }
     x[j] = ok ? (UNIT_T ? y : y * inv_t) : neg_inf();
     rmax = fmaxf(rmax, x[j]);
@@ -352,21 +356,34 @@ __global__ void __launch_bounds__(256)
   const int k0 = part * 8;
   const int32_t* ix = indices + (bl * Hkv + hk) * K + k0;
 
+  // Loads are unconditional (clamped slots and chunks) and issued together:
+  // loads inside per-slot branches were each waited for at the branch end.
   int32_t iv[8];
   float x[8], gr[8];
   float rmax = neg_inf();
+  const int64_t kl = K - 1;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) iv[j] = ix[min((int64_t)j, kl - k0)];
+  float sc[8], bv[8], ex1[8], ex2[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int64_t kk = r * K + min((int64_t)(k0 + j), kl);
+    const bool ok = iv[j] >= 0 && iv[j] < C;
+    gr[j] = bf16_to_f32(g_rw[kk]);
+    sc[j] = bf16_to_f32(scores[kk]);
+    bv[j] = bias[((b * C + (ok ? iv[j] : 0)) * Hkv + hk) * G + g];
+    ex1[j] = e1 ? e1[kk] : 0.f;
+    ex2[j] = e2 ? e2[kk] : 0.f;
+  }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const bool in = k0 + j < K;
-    iv[j] = in ? ix[j] : -1;
-    gr[j] = in ? bf16_to_f32(g_rw[r * K + k0 + j]) : 0.f;
-    float v = neg_inf();
-    if (in && iv[j] >= 0 && iv[j] < C) {
-      float y = bf16_to_f32(scores[r * K + k0 + j]) + bias[((b * C + iv[j]) * Hkv + hk) * G + g];
-      if (e1) y += e1[r * K + k0 + j];
-      if (e2) y += e2[r * K + k0 + j];
-      v = y * inv_t;
-    }
+    if (!in) iv[j] = -1;
+    if (!in) gr[j] = 0.f;
+    float y = sc[j] + bv[j];
+    if (e1) y += ex1[j];
+    if (e2) y += ex2[j];
+    const float v = in && iv[j] >= 0 && iv[j] < C ? y * inv_t : neg_inf();
     x[j] = v;
     rmax = fmaxf(rmax, v);
   }
