@@ -185,13 +185,11 @@ struct WaveSelect {
     return c;
   }
 
-  // n: key slots in use per lane (<= PER <= 64, uniform).  Returns this
-  // lane's picks as bits (bit i: element (i, lane)); per-lane bits keep the
-  // picks in vector registers (an array of bools would take a scalar mask
-  // pair per element).
-  __device__ static uint64_t run(const uint32_t (&key)[PER], int n, int K) {
-    static_assert(PER <= 64, "one pick bit per key slot");
-    const int lane = threadIdx.x & 63;
+  // The threshold of the K largest candidates: keys >= thr_hi are picked,
+  // plus `need` of the keys equal to thr_tie (need = 0: no tie to break).
+  // n: key slots in use per lane (<= PER, uniform).
+  __device__ static void threshold(const uint32_t (&key)[PER], int n, int K, uint32_t& thr_hi,
+                                   uint32_t& thr_tie, int& need) {
     const uint32_t kFloor = float_order_key(neg_inf());
     int nfin = 0;
     uint32_t kmin = 0xffffffffu, kmax = 0u;
@@ -208,8 +206,8 @@ struct WaveSelect {
     for (int o = 1; o < 64; o <<= 1) nfin += __shfl_xor(nfin, o, 64);
     kmin = wave_min_u(kmin);
     kmax = wave_max_u(kmax);
-    uint32_t thr_hi, thr_tie = 0u;
-    int need = 0;
+    thr_tie = 0u;
+    need = 0;
     if (nfin <= K) {
       thr_hi = kFloor + 1u;
     } else {
@@ -232,6 +230,18 @@ struct WaveSelect {
         need = K - count_ge(key, n, hi);
       }
     }
+  }
+
+  // n: key slots in use per lane (<= PER <= 64, uniform).  Returns this
+  // lane's picks as bits (bit i: element (i, lane)); per-lane bits keep the
+  // picks in vector registers (an array of bools would take a scalar mask
+  // pair per element).
+  __device__ static uint64_t run(const uint32_t (&key)[PER], int n, int K) {
+    static_assert(PER <= 64, "one pick bit per key slot");
+    const int lane = threadIdx.x & 63;
+    uint32_t thr_hi, thr_tie;
+    int need;
+    threshold(key, n, K, thr_hi, thr_tie, need);
     const uint64_t below = (1ull << lane) - 1ull;
     int base = 0;
     uint64_t picks = 0ull;

@@ -952,6 +952,139 @@ __device__ __forceinline__ void block_reduce8(float (&v)[8], int G, float* red) 
   }
 }
 
+// The K largest keys of a selection workgroup's row (K <= kTwoLevelMaxK,
+// C <= 4096; key[i] of thread tid is chunk tid + 512 i) in two levels with
+// one barrier.  Each wave first picks the K largest of its own chunks
+// (chunks 512 i + 64 wave + lane: the wave order index 64 i + lane follows
+// the chunk order, so its ties go to the lower chunk) and lists them in LDS;
+// wave 0 then selects the K largest of the <= 8 K candidates, the ties at
+// the threshold going to the lowest chunks, and writes the picks in
+// ascending chunk order.  Each chunk of the row's K largest is among its
+// wave's K largest, so the result is the one-level selection's.
+constexpr int kTwoLevelMaxK = 64;
+
+template <int G>
+__device__ void select_two_level(const RouteArgs& a, const uint32_t (&key)[kSelMaxPer], int n,
+                                 int64_t row, const float* xr) {
+  constexpr int kCand = kSelWaves * kTwoLevelMaxK / 64;  // candidate slots per lane
+  __shared__ uint32_t ck_s[kSelWaves * kTwoLevelMaxK];
+  __shared__ uint16_t cc_s[kSelWaves * kTwoLevelMaxK];
+  __shared__ int cn_s[kSelWaves];
+  __shared__ uint32_t cmask[128];  // chunk bit sets (C <= 4096)
+  __shared__ uint32_t cpre[128];   // set bits below each word
+  const int K = a.K;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint64_t below = (1ull << lane) - 1ull;
+  {
+    const uint64_t wp = WaveSelect<kSelMaxPer>::run(key, n, K);
+    int base = 0;
+#pragma unroll
+    for (int i = 0; i < kSelMaxPer; ++i) {
+      if (i >= n) continue;
+      const bool p = (wp >> i) & 1ull;
+      const uint64_t bl = __builtin_amdgcn_ballot_w64(p);
+      if (p) {
+        const int pos = wave * K + base + __builtin_popcountll(bl & below);
+        ck_s[pos] = key[i];
+        cc_s[pos] = (uint16_t)(tid + kSelThreads * i);
+      }
+      base += __builtin_popcountll(bl);
+    }
+    if (lane == 0) cn_s[wave] = base;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // candidate e = 64 j + lane: entry e - w K of wave w = e / K
+  const int n2 = (kSelWaves * K + 63) / 64;
+  uint32_t ckey[kCand];
+  int cch[kCand];
+#pragma unroll
+  for (int j = 0; j < kCand; ++j) {
+    const int e = 64 * j + lane;
+    const int w = e / K;
+    const bool ok = j < n2 && w < kSelWaves && e - w * K < cn_s[w < kSelWaves ? w : 0];
+    ckey[j] = ok ? ck_s[e] : 0u;
+    cch[j] = ok ? (int)cc_s[e] : 0;
+  }
+  uint32_t thr_hi, thr_tie;
+  int need;
+  WaveSelect<kCand>::threshold(ckey, n2, K, thr_hi, thr_tie, need);
+  // rank[j] = the members of the set below chunk cch[j] (for members), from
+  // a chunk bit set in LDS and its per-word prefix counts (this wave only:
+  // the LDS runs one wave's operations in order).
+  auto ranks = [&](const bool (&in)[kCand], int (&rank)[kCand]) {
+    asm volatile("" ::: "memory");
+    cmask[lane] = 0u;
+    cmask[lane + 64] = 0u;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < kCand; ++j)
+      if (in[j]) atomicOr(&cmask[cch[j] >> 5], 1u << (cch[j] & 31));
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const uint32_t w0 = cmask[2 * lane], w1 = cmask[2 * lane + 1];
+    const int cnt = __popc(w0) + __popc(w1);
+    int incl = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += t;
+    }
+    cpre[2 * lane] = (uint32_t)(incl - cnt);
+    cpre[2 * lane + 1] = (uint32_t)(incl - cnt + __popc(w0));
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < kCand; ++j) {
+      rank[j] = 0;
+      if (in[j]) {
+        const int c = cch[j];
+        rank[j] = (int)cpre[c >> 5] + __popc(cmask[c >> 5] & ((1u << (c & 31)) - 1u));
+      }
+    }
+  };
+  bool pick[kCand];
+#pragma unroll
+  for (int j = 0; j < kCand; ++j) pick[j] = j < n2 && ckey[j] >= thr_hi;
+  if (need > 0) {  // wave-uniform: ties at the threshold to the lowest chunks
+    bool tie[kCand];
+    int tr[kCand];
+#pragma unroll
+    for (int j = 0; j < kCand; ++j) tie[j] = j < n2 && ckey[j] == thr_tie;
+    ranks(tie, tr);
+#pragma unroll
+    for (int j = 0; j < kCand; ++j)
+      if (tie[j] && tr[j] < need) pick[j] = true;
+  }
+  int slot[kCand];
+  ranks(pick, slot);
+  // The picks' chunks to lane slot order through the candidate area (free
+  // now), then lane t writes output slot t with all its loads in flight.
+  int total = 0;
+#pragma unroll
+  for (int j = 0; j < kCand; ++j) total += __builtin_popcountll(__builtin_amdgcn_ballot_w64(pick[j]));
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < kCand; ++j)
+    if (pick[j]) cc_s[slot[j]] = (uint16_t)cch[j];
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  if (lane < K) {
+    const int t = lane;
+    const bool live = t < total;
+    const int64_t c = live ? (int64_t)cc_s[t] : 0;
+    float v[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) v[g] = xr[(int64_t)g * a.C + c];
+    a.indices[row * K + t] = live ? (int32_t)c : -1;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (a.scores_fp32)
+        reinterpret_cast<float*>(a.scores)[(row * G + g) * K + t] = live ? v[g] : neg_inf();
+      else
+        reinterpret_cast<uint16_t*>(a.scores)[(row * G + g) * K + t] =
+            live ? (uint16_t)f32_to_bf16(v[g]) : (uint16_t)0xff80u;
+    }
+  }
+}
+
 // Selection: one workgroup per (row, KV head, batch); chunk c = tid + 512 i.
 // The row's logits and bias are read once into registers.  Same score, LSE,
 // drop and tie rules as the general kernel.
@@ -1071,6 +1204,10 @@ __global__ void __launch_bounds__(kSelThreads) route_select_kernel(RouteArgs a,
   }
 
   // 4. The K largest (ties to the lower chunk), in ascending chunk order.
+  if (K <= kTwoLevelMaxK) {
+    select_two_level<G>(a, key, n, row, xr);
+    return;
+  }
   bool pick[kSelMaxPer];
   int slot[kSelMaxPer];
   const int slot_base = Select::run(key, n, K, sel, pick, slot);

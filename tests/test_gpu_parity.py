@@ -290,6 +290,44 @@ def test_route_topk_short_block_vs_oracle(L, C, G, topk, mode, causal, fp32, sha
         assert int((differ & ~near).sum()) == 0
 
 
+@pytest.mark.parametrize("C,topk", [(2048, 32), (4096, 64), (700, 20)])
+def test_route_topk_short_block_exact_ties_to_the_lower_chunk(C, topk):
+    # The short-block selection (one workgroup per row: each wave's own K
+    # largest, then one wave over the candidates) breaks exact ties at the
+    # threshold by chunk index, like the reference's fused kernel
+    # (topk_head_softmax.py:614-626).  20 chunks score highest; 40 chunks
+    # spread over every wave's range tie below them; the rest score lowest:
+    # the picks are the 20 and the lowest-indexed of the 40.
+    _note(f"route short block exact ties C={C} K={topk}")
+    L, Hkv, G, D = 4, 4, 7, 128
+    g = torch.Generator().manual_seed(401)
+    q5 = torch.randn(1, L, Hkv, G, D, generator=g).bfloat16()
+    hi = torch.randn(Hkv * G, D, generator=g).bfloat16()
+    tie = torch.randn(Hkv * G, D, generator=g).bfloat16()
+    low = torch.randn(Hkv * G, D, generator=g).bfloat16()
+    perm = torch.randperm(C, generator=g)
+    top_set, tie_set = perm[:20], perm[20:60]
+    lmk = low.expand(1, C, Hkv * G, D).clone()
+    lmk[0, top_set] = hi
+    lmk[0, tie_set] = tie
+    # make the three groups' scores ordered hi > tie > low for every row
+    q5 = (q5.float() * 0 + (hi.float() - low.float()).reshape(Hkv, G, D) * 0.05
+          + (tie.float() - low.float()).reshape(Hkv, G, D) * 0.05).bfloat16().expand(1, L, Hkv, G, D).contiguous()
+    lse4 = torch.zeros(1, L, Hkv, G)
+    bias4 = torch.zeros(1, C, Hkv, G)
+    drop = torch.zeros(1, L, C, dtype=torch.int32)
+    idx, sc = route_topk_launch(q5.to(DEV), lmk.to(DEV), lse4.to(DEV), topk, 64,
+                                bias4=bias4.to(DEV), drop_mask=drop.to(DEV), use_workspace=True)
+    ridx, rsc, sel = O.route_topk(q5, lmk, lse4, topk, 64, drop_mask=drop, bias4=bias4)
+    # the groups are ordered and the tie group really ties
+    s0 = sel[0, 0, 0]
+    assert float(s0[top_set].min()) > float(s0[tie_set].max())
+    assert float(s0[tie_set].max()) == float(s0[tie_set].min())
+    assert float(s0[tie_set].max()) > float(s0[perm[60:]].max())
+    assert torch.equal(idx.cpu().long(), ridx)
+    torch.testing.assert_close(sc.cpu().float(), rsc.bfloat16().float(), atol=0.02, rtol=0.01)
+
+
 def test_route_topk_derived_drop_equals_explicit():
     _note("route derived drop")
     L = 16384 // 8
