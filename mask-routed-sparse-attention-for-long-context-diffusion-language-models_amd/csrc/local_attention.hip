@@ -1,9 +1,11 @@
 // Bidirectional sliding-window GQA attention (flash-attn window semantics).
 //
 // Work split: one workgroup of 8 waves per (batch, KV head, block of QB
-// queries).  Each wave owns one column tile of 16 columns: 16 / GP queries x
-// GP head columns (GP = the group size rounded up to a power of two; columns
-// of heads >= G are padding), so QB = 8 (16 / GP): 16 queries for G = 7.
+// queries).  Each wave owns one column tile of 16 (query, head) columns: for
+// G = 1, 2, 4, 8 that is 16 / G queries x G heads (QB = 8 (16 / G)); other
+// group sizes pack the workgroup's 128 columns as (query c / G, head c % G),
+// QB = floor(128 / G): 18 queries for G = 7, 2 padding columns instead of
+// the 16 a power-of-two head count would leave.
 // Q^T operands and O^T accumulators stay in registers.  A workgroup needs
 // 128 VGPRs per lane and ~69 KB of LDS, so two workgroups share a CU and
 // their barriers fall at different times.
@@ -107,11 +109,21 @@ __device__ __forceinline__ uint64_t tile_inert_bits(const LocalArgs& a, int64_t 
   return m;
 }
 
+// Column layout.  GP = G = 1, 2, 4 or 8: each wave's 16 columns are 16 / G
+// queries x G heads.  GP == 0 (packed, G = 3, 5, 6 or 7): the workgroup's
+// 16 kWaves columns are numbered c = 16 wave + col and hold (query c / G,
+// head c % G) of floor(16 kWaves / G) queries, so at most 16 kWaves mod G
+// columns are padding (2 of 128 for G = 7, where 8 head columns per query
+// would pad 16).
+__host__ __device__ constexpr int queries_per_block(int GP, int G) {
+  return GP > 0 ? kWaves * (16 / GP) : (16 * kWaves) / G;
+}
+
 template <int GP>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2 * kBlocksPerCU, 2 * kBlocksPerCU)))
 local_attn_kernel(LocalArgs a) {
-  constexpr int QPT = 16 / GP;          // queries per column tile
-  constexpr int QB = kWaves * QPT;      // queries per workgroup
+  constexpr bool kPacked = GP == 0;
+  const int QB = queries_per_block(GP, a.G);  // queries per workgroup
   extern __shared__ __align__(16) unsigned char smem[];
   unsigned char* ring = smem;                                              // kRing slots
   uint64_t* valid_tab = reinterpret_cast<uint64_t*>(smem + kRing * kSlotBytes);  // [kMaskTiles]
@@ -122,11 +134,16 @@ local_attn_kernel(LocalArgs a) {
   const int col = lane & 15, grp = lane >> 4;
   // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin by
   // linear id; renumber so that each XCD runs a contiguous range of query
-  // blocks of one head, whose key windows overlap in that XCD's L2.
+  // blocks of one head, whose key windows overlap in that XCD's L2.  With
+  // total = 8 q + r workgroups, XCD x holds q + (x < r) of them and takes
+  // the range starting at x q + min(x, r).
   const int64_t nx = gridDim.x, nyz = (int64_t)gridDim.y * gridDim.z;
   const int64_t total = nx * nyz;
   int64_t lin = blockIdx.x + nx * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
-  if (total % 8 == 0) lin = (lin % 8) * (total / 8) + lin / 8;
+  {
+    const int64_t x = lin % 8, q8 = total / 8, r8 = total % 8;
+    lin = x * q8 + min(x, r8) + lin / 8;
+  }
   const int64_t qblock = lin % nx;
   const int h = (int)((lin / nx) % gridDim.y);
   const int64_t z = lin / (nx * gridDim.y);
@@ -134,7 +151,9 @@ local_attn_kernel(LocalArgs a) {
   const int part = (int)(z / a.B);
   const int64_t qb = qblock * QB;
   const int G = a.G;
-  const int gg = col % GP;
+  const int cw = 16 * wave + col;  // the column's number in the workgroup (packed layout)
+  constexpr int GPd = kPacked ? 1 : GP;
+  const int gg = kPacked ? cw % G : col % GPd;
 
   // Position range of the block's queries.
   if (wave == 0) {
@@ -159,8 +178,9 @@ local_attn_kernel(LocalArgs a) {
 
   // Q^T operands and position of this lane's column.
   u32x4_t Qb[4];
-  const int64_t qi = qb + wave * QPT + col / GP;
-  const bool qok = qi < a.Lq && gg < G;
+  const int64_t qi = kPacked ? qb + cw / G : qb + wave * (16 / GPd) + col / GPd;
+  const bool colok = kPacked ? cw < QB * G : gg < G;  // not a padding column
+  const bool qok = qi < a.Lq && colok;
   const int qp = qi < a.Lq ? (int)(a.qpos ? a.qpos[qi] : qi) : 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -172,11 +192,15 @@ local_attn_kernel(LocalArgs a) {
   }
   // Q fragments: lane (grp, col)'s k-step j image bytes of its column --
   // query qi, head gg -- sit at 512 j + 128 grp + 16 gg of the query's 2 KB
-  // image (padding heads hold zeros).
-  if (a.qf && part == 0 && qi < a.Lq) {
-    uint16_t* dst = a.qf + ((b * a.Hkv + h) * a.Lq + qi) * 1024 + 64 * grp + 8 * gg;
+  // image; the query's columns also write zeros into head slots G..7.
+  if (a.qf && part == 0 && qok) {
+    uint16_t* dst = a.qf + ((b * a.Hkv + h) * a.Lq + qi) * 1024 + 64 * grp;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(dst + 256 * j) = Qb[j];
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(dst + 8 * gg + 256 * j) = Qb[j];
+    const u32x4_t zq = {0u, 0u, 0u, 0u};
+    for (int zs = G + gg; zs < 8; zs += G)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(dst + 8 * zs + 256 * j) = zq;
   }
   __syncthreads();
   const int64_t plo = pos_range[0], phi = pos_range[1];
@@ -438,7 +462,7 @@ __global__ void __launch_bounds__(256) local_merge_kernel(LocalArgs a, int64_t r
 
 template <int GP>
 int launch_local(const LocalArgs& a, hipStream_t s) {
-  constexpr int QB = kWaves * (16 / GP);
+  const int QB = queries_per_block(GP, a.G);
   const size_t smem = (size_t)kRing * kSlotBytes + kMaskTiles * 8 + 16;
   auto kern = local_attn_kernel<GP>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -503,12 +527,12 @@ int local_attention(const void* q, const void* kv_frags, const uint8_t* key_vali
   switch (G) {
     case 1: return launch_local<1>(a, s);
     case 2: return launch_local<2>(a, s);
-    case 3:
     case 4: return launch_local<4>(a, s);
+    case 8: return launch_local<8>(a, s);
+    case 3:
     case 5:
     case 6:
-    case 7:
-    case 8: return launch_local<8>(a, s);
+    case 7: return launch_local<0>(a, s);
     default: return MRSA_ERR_UNSUPPORTED;
   }
 }
