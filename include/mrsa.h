@@ -655,6 +655,24 @@ int mrsa_selected_attention_bwd(const void* q, const void* grad_out, const void*
                                 void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * mrsa_selected_attention_bwd with ALiBi slopes: the backward of
+ * mrsa_selected_attention_alibi_fwd (ops/hils_fwd_bwd_head.py:755-760, the
+ * bias term of the reference's backward kernel).  slope: fp32 [q_heads],
+ * required.  No gradient flows to the slopes (the reference's backward
+ * returns none for them).
+ */
+int mrsa_selected_attention_alibi_bwd(const void* q, const void* grad_out, const void* kv_frags,
+                                      const void* kv_frags_bwd, const void* weights,
+                                      const int32_t* indices, const uint8_t* key_valid,
+                                      const int8_t* token_keep, const float* slope,
+                                      int64_t batch, int64_t q_len, int64_t kv_len,
+                                      int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                      int64_t topk, int64_t chunk_size, int mask_last_token,
+                                      float sm_scale, float* grad_q, float* grad_k,
+                                      float* grad_v, void* grad_weights, void* workspace,
+                                      int64_t workspace_bytes, void* stream);
+
+/*
  * Routed chunk attention with the output fusion folded in: the result is
  * fuse_hils_outputs(remote, local_output, local_weight)
  * (ops/hils_bidir_output_fusion_tilelang.py:138-148) of the routed output
@@ -720,6 +738,25 @@ int mrsa_selected_attention_ex_fwd(const void* q, const void* q_frags, const voi
                                    int64_t chunk_size, int mask_last_token, float sm_scale,
                                    int64_t parts, float* partial, int flags, void* out,
                                    void* stream);
+
+/*
+ * mrsa_selected_attention_ex_fwd with ALiBi slopes: HiLS_block_M_head's
+ * `slope` argument (ops/hils_fwd_bwd_head.py:1113-1150; hils_torch_ref
+ * :68-76 and the forward kernel :445-451).  Before the scale, the raw logit
+ * of key s of a chunk (s = 0..63) gets -slope[head] * max(0, 62 - s):
+ *   softmax_s((q . k_s - slope[head] max(0, 62 - s)) * sm_scale)
+ * slope: fp32 [q_heads] on the device, required; every other argument as in
+ * mrsa_selected_attention_ex_fwd.
+ */
+int mrsa_selected_attention_alibi_fwd(const void* q, const void* q_frags, const void* kv_frags,
+                                      const void* weights, const int32_t* indices,
+                                      const uint8_t* key_valid, const int8_t* token_keep,
+                                      const void* local_output, const void* local_weight,
+                                      const float* slope, int64_t batch, int64_t q_len,
+                                      int64_t kv_len, int64_t q_heads, int64_t kv_heads,
+                                      int64_t head_dim, int64_t topk, int64_t chunk_size,
+                                      int mask_last_token, float sm_scale, int64_t parts,
+                                      float* partial, int flags, void* out, void* stream);
 
 /*
  * Routed-attention lock status.  It has no counterpart in the reference

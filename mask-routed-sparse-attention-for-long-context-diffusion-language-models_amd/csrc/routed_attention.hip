@@ -118,6 +118,7 @@ struct RaArgs {
   int64_t units;             // B * Hkv * parts * ntiles workgroups of work
   int spin_limit;            // lock tries before a tile is deferred (<= 0: every tile)
   int det;                   // fixed accumulation order (per-query tickets instead of the lock)
+  const float* slope;        // [Hq] ALiBi slopes (ALIBI instances only)
 };
 
 __host__ __device__ inline size_t al16(size_t x) { return (x + 15) & ~(size_t)15; }
@@ -259,7 +260,7 @@ __device__ __forceinline__ void load_q(u32x4_t (&Qb)[4], __amdgpu_buffer_rsrc_t 
   for (int ks = 0; ks < 4; ++ks) Qb[ks] = bload(r, off, kstep * ks);
 }
 
-template <bool TOKEN, bool KEEP, bool DET>
+template <bool TOKEN, bool KEEP, bool DET, bool ALIBI>
 __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   // Workgroup -> work unit, XCD-aware: workgroups are dealt to the 8 XCDs
@@ -511,6 +512,20 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   const int j = lane & 15, grp = lane >> 4;
   const int own = j >> 3, gcol = j & 7;  // this lane's tile column: owner, head
   const float c2 = a.scale_log2;
+  // ALiBi (ops/hils_fwd_bwd_head.py:445-451, hils_torch_ref :68-76): the raw
+  // logit of chunk key s gets -slope[head] * max(0, 62 - s) before the
+  // scale, i.e. ab = -slope c2 max(0, 62 - s) in the exp2 domain; this
+  // lane's keys are 16 mt + 4 grp + r of its column's head, fixed for the
+  // whole walk.
+  float ab[4][4];
+  if constexpr (ALIBI) {
+    const float sl = gcol < G ? -a.slope[h * G + gcol] * c2 : 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        ab[mt][r] = sl * fmaxf(0.f, (float)(62 - 16 * mt - r) - 4.f * (float)grp);
+  }
   const __amdgpu_buffer_rsrc_t frs =
       make_rsrc(a.kvf + (b * a.Hkv + h) * Ck * kFragElems, (uint32_t)Ck * kFragBytes);
   const uint32_t flo = 16u * lane;
@@ -595,7 +610,8 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) E[mt][r] = exp2_hw(__builtin_fmaf(S[mt][r], c2, -mb));
+        for (int r = 0; r < 4; ++r)
+          E[mt][r] = exp2_hw(__builtin_fmaf(S[mt][r], c2, ALIBI ? ab[mt][r] - mb : -mb));
         ps[mt] = (E[mt][0] + E[mt][1]) + (E[mt][2] + E[mt][3]);
       }
       return across4_sum((ps[0] + ps[1]) + (ps[2] + ps[3]));
@@ -607,8 +623,18 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       stabilise = !__all(sum >= 0x1p-64f && sum <= 0x1p64f);
     }
     if (stabilise) {
-      const float mx = across4_max(max16_raw(S));
-      sum = exp_sum(mx == neg_inf() ? 0.f : mx * c2);
+      if constexpr (ALIBI) {
+        float mx = neg_inf();
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, __builtin_fmaf(S[mt][r], c2, ab[mt][r]));
+        mx = across4_max(mx);
+        sum = exp_sum(mx == neg_inf() ? 0.f : mx);
+      } else {
+        const float mx = across4_max(max16_raw(S));
+        sum = exp_sum(mx == neg_inf() ? 0.f : mx * c2);
+      }
     }
     const float f = sum > 0.f ? wv * rcp_hw(sum) : 0.f;
 #pragma unroll
@@ -1115,7 +1141,7 @@ int pick_tile(int G, int K, int64_t Ck, bool token, bool keep, bool det) {
   return 0;
 }
 
-template <bool TOKEN, bool KEEP>
+template <bool TOKEN, bool KEEP, bool ALIBI = false>
 int launch_routed(RaArgs& a, hipStream_t s) {
   if (TOKEN && a.det) return MRSA_ERR_UNSUPPORTED;  // token scoring has no fixed-order walk
   const int tq = pick_tile(a.G, a.K, a.Ck, TOKEN, KEEP, a.det != 0);
@@ -1128,7 +1154,8 @@ int launch_routed(RaArgs& a, hipStream_t s) {
   const RaLayout l = ra_layout(tq, a.G, a.K, a.Ck, TOKEN, KEEP, a.det != 0);
   a.spin_limit = g_spin_limit;
   // the fixed-order walk is its own instance, so the lock path carries none of its branches
-  auto kern = a.det ? routed_attn_kernel<TOKEN, KEEP, !TOKEN> : routed_attn_kernel<TOKEN, KEEP, false>;
+  auto kern = a.det ? routed_attn_kernel<TOKEN, KEEP, !TOKEN, ALIBI>
+                     : routed_attn_kernel<TOKEN, KEEP, false, ALIBI>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)l.total) != hipSuccess)
     return MRSA_ERR_LAUNCH;
@@ -1188,6 +1215,7 @@ RaArgs base_args(const void* q, const void* kv_frags, const void* weights,
   a.units = 0;
   a.spin_limit = kDefaultSpinLimit;
   a.det = 0;
+  a.slope = nullptr;
   return a;
 }
 
@@ -1200,7 +1228,7 @@ int selected_forward(const void* q, const void* kv_frags, const void* weights,
                      int64_t kv_heads, int64_t head_dim, int64_t topk, int64_t chunk_size,
                      int mask_last_token, float sm_scale, int64_t parts, float* partial,
                      const void* fuse_local, const void* fuse_w, void* out, void* stream,
-                     const void* q_frags = nullptr, int flags = 0) {
+                     const void* q_frags = nullptr, int flags = 0, const float* slope = nullptr) {
   int st = check_common(q, kv_frags, indices, batch, q_len, kv_len, q_heads, kv_heads, head_dim,
                         topk, chunk_size, sm_scale);
   if (st != MRSA_OK) return st;
@@ -1224,8 +1252,12 @@ int selected_forward(const void* q, const void* kv_frags, const void* weights,
   a.fuse_w = parts > 1 ? nullptr : (const uint16_t*)fuse_w;
   a.qf = (const uint16_t*)q_frags;
   a.det = flags & MRSA_ROUTED_FIXED_ORDER;
+  a.slope = slope;
   hipStream_t s = (hipStream_t)stream;
-  st = keep ? launch_routed<false, true>(a, s) : launch_routed<false, false>(a, s);
+  if (slope)
+    st = keep ? launch_routed<false, true, true>(a, s) : launch_routed<false, false, true>(a, s);
+  else
+    st = keep ? launch_routed<false, true>(a, s) : launch_routed<false, false>(a, s);
   if (st != MRSA_OK || parts == 1) return st;
   const int64_t n4 = batch * q_len * q_heads * 128 / 4;
   const int64_t blocks = std::min<int64_t>((n4 + 255) / 256, 4096);
@@ -1343,6 +1375,22 @@ extern "C" int mrsa_selected_attention_ex_fwd(
                           kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
                           sm_scale, parts, partial, local_output, local_weight, out, stream,
                           q_frags, flags);
+}
+
+extern "C" int mrsa_selected_attention_alibi_fwd(
+    const void* q, const void* q_frags, const void* kv_frags, const void* weights,
+    const int32_t* indices, const uint8_t* key_valid, const int8_t* token_keep,
+    const void* local_output, const void* local_weight, const float* slope, int64_t batch,
+    int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+    int64_t topk, int64_t chunk_size, int mask_last_token, float sm_scale, int64_t parts,
+    float* partial, int flags, void* out, void* stream) {
+  if (flags & ~MRSA_ROUTED_FIXED_ORDER) return MRSA_ERR_INVALID_ARGUMENT;
+  if (batch > 0 && q_len > 0 && !slope) return MRSA_ERR_INVALID_ARGUMENT;
+  if (q_frags && batch > 0 && q_len > 0 && !local_output) return MRSA_ERR_INVALID_ARGUMENT;
+  return selected_forward(q, kv_frags, weights, indices, key_valid, token_keep, batch, q_len,
+                          kv_len, q_heads, kv_heads, head_dim, topk, chunk_size, mask_last_token,
+                          sm_scale, parts, partial, local_output, local_weight, out, stream,
+                          q_frags, flags, slope);
 }
 
 // Reads the current device's count of routed-attention tiles whose bounded

@@ -65,6 +65,7 @@ struct BwdArgs {
   const int32_t* list;
   const int32_t* start;      // [B * Hkv * Ck + 1]
   const int32_t* ustart;     // [B * Hkv * Ck + 1]
+  const float* slope;        // [Hq] ALiBi slopes or null
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -92,8 +93,21 @@ __device__ __forceinline__ uint64_t nonzero_bits(const int8_t* row) {
 // keys 16 mt + 4 grp + r of column j; msh bit 16 mt + r set = key excluded.
 //   S  <- P  = bf16(2^(s c - lse)) over the visible keys (0 when none is)
 //   dP <- dS = bf16(sw P (dP - di)),  di = sum P dP per column (returned)
+// With ALiBi (alibi, wave-uniform) the exp2-domain logit is s c + sl
+// max(0, 62 - key), sl = -slope[head] c for this lane's column
+// (ops/hils_fwd_bwd_head.py:755-760, the backward's bias term).
 __device__ __forceinline__ float chunk_grad(f32x4_t (&S)[4], f32x4_t (&dP)[4], uint64_t msh,
-                                            float c2, float sw) {
+                                            float c2, float sw, bool alibi = false,
+                                            float sl = 0.f, int grp = 0) {
+  if (alibi) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        S[mt][r] = __builtin_fmaf(
+            S[mt][r], c2, sl * fmaxf(0.f, (float)(62 - 16 * mt - r) - 4.f * (float)grp));
+    c2 = 1.f;
+  }
   float mx = neg_inf();
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
@@ -275,6 +289,7 @@ __device__ __forceinline__ void tile_put(unsigned char* sm, uint32_t base, int r
 //     Q^T, bf16(w dO)^T into the round's tiles;
 //   phase 2 (wave w: dims 32 w .. + 31): dK += dS^T . Q, dV += P^T . bf16(w dO)
 //     over the round's 64 columns (two k-steps).
+template <bool ALIBI>
 __global__ void __launch_bounds__(kThreads, 1) routed_attn_dkv_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char sm[kKvBytes];
   const int tid = threadIdx.x;
@@ -392,7 +407,8 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_dkv_kernel(BwdArgs a)
         tile_put(sm, kKvQt, dim, lc, qv);
         tile_put(sm, kKvWd, dim, lc, f32_to_bf16(wv * dov));
       }
-    const float di = chunk_grad(S, dP, msh, c2, a.scale * wv);  // S <- P, dP <- dS
+    const float sl = ALIBI && cvalid ? -a.slope[(int64_t)h * G + g] * c2 : 0.f;
+    const float di = chunk_grad(S, dP, msh, c2, a.scale * wv, ALIBI, sl, lg);  // S <- P, dP <- dS
     if (cvalid && grp == 0) a.dw[row * K + k] = (uint16_t)f32_to_bf16(di);
     // dQ (columns x dims) = dS . K: A = dS packed in the tiled key order
     // (reduction index 8 grp + e of k-step ks is key 32 ks + 16 (e >> 2) +
@@ -515,13 +531,15 @@ ListPlan list_plan(int64_t B, int64_t Lq, int64_t Hkv, int64_t K, int64_t Ck) {
 
 }  // namespace
 
-extern "C" int mrsa_selected_attention_bwd(
+namespace {
+
+int selected_backward(
     const void* q, const void* grad_out, const void* kv_frags, const void* kv_frags_bwd,
     const void* weights, const int32_t* indices, const uint8_t* key_valid,
     const int8_t* token_keep, int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
     int64_t kv_heads, int64_t head_dim, int64_t topk, int64_t chunk_size, int mask_last_token,
     float sm_scale, float* grad_q, float* grad_k, float* grad_v, void* grad_weights,
-    void* workspace, int64_t workspace_bytes, void* stream) {
+    void* workspace, int64_t workspace_bytes, void* stream, const float* slope) {
   if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 ||
       q_heads % kv_heads != 0 || head_dim <= 0 || topk <= 0 || chunk_size <= 0 ||
       !(sm_scale > 0.f) || sm_scale == __builtin_inff())
@@ -565,6 +583,7 @@ extern "C" int mrsa_selected_attention_bwd(
   a.dk = grad_k;
   a.dv = grad_v;
   a.dw = (uint16_t*)grad_weights;
+  a.slope = slope;
   if (lp.max_units > 0x7fffffff || lp.nqb > 0x7fffffff || batch * kv_heads > 65535)
     return MRSA_ERR_UNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
@@ -586,9 +605,42 @@ extern "C" int mrsa_selected_attention_bwd(
   hipLaunchKernelGGL(list_fill_kernel, lgrid, dim3(kListBlock), 0, st, a,
                      (const int32_t*)blkbase, lp.nqb, list);
   a.list = list;
-  hipLaunchKernelGGL(routed_attn_dkv_kernel, dim3((unsigned)lp.max_units), dim3(kThreads), 0, st,
-                     a);
+  if (slope)
+    hipLaunchKernelGGL(routed_attn_dkv_kernel<true>, dim3((unsigned)lp.max_units), dim3(kThreads),
+                       0, st, a);
+  else
+    hipLaunchKernelGGL(routed_attn_dkv_kernel<false>, dim3((unsigned)lp.max_units), dim3(kThreads),
+                       0, st, a);
   return mrsa_launch_status();
+}
+
+}  // namespace
+
+extern "C" int mrsa_selected_attention_bwd(
+    const void* q, const void* grad_out, const void* kv_frags, const void* kv_frags_bwd,
+    const void* weights, const int32_t* indices, const uint8_t* key_valid,
+    const int8_t* token_keep, int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
+    int64_t kv_heads, int64_t head_dim, int64_t topk, int64_t chunk_size, int mask_last_token,
+    float sm_scale, float* grad_q, float* grad_k, float* grad_v, void* grad_weights,
+    void* workspace, int64_t workspace_bytes, void* stream) {
+  return selected_backward(q, grad_out, kv_frags, kv_frags_bwd, weights, indices, key_valid,
+                           token_keep, batch, q_len, kv_len, q_heads, kv_heads, head_dim, topk,
+                           chunk_size, mask_last_token, sm_scale, grad_q, grad_k, grad_v,
+                           grad_weights, workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" int mrsa_selected_attention_alibi_bwd(
+    const void* q, const void* grad_out, const void* kv_frags, const void* kv_frags_bwd,
+    const void* weights, const int32_t* indices, const uint8_t* key_valid,
+    const int8_t* token_keep, const float* slope, int64_t batch, int64_t q_len, int64_t kv_len,
+    int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t topk, int64_t chunk_size,
+    int mask_last_token, float sm_scale, float* grad_q, float* grad_k, float* grad_v,
+    void* grad_weights, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (batch > 0 && q_len > 0 && !slope) return MRSA_ERR_INVALID_ARGUMENT;
+  return selected_backward(q, grad_out, kv_frags, kv_frags_bwd, weights, indices, key_valid,
+                           token_keep, batch, q_len, kv_len, q_heads, kv_heads, head_dim, topk,
+                           chunk_size, mask_last_token, sm_scale, grad_q, grad_k, grad_v,
+                           grad_weights, workspace, workspace_bytes, stream, slope);
 }
 
 extern "C" int64_t mrsa_selected_attention_bwd_workspace_bytes(int64_t batch, int64_t q_len,

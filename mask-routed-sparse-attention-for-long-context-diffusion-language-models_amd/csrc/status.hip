@@ -16,7 +16,7 @@ extern "C" const char* mrsa_status_string(int status) {
   }
 }
 
-extern "C" int mrsa_abi_version(void) { return 7; }
+extern "C" int mrsa_abi_version(void) { return 8; }
 
 // One wave: lane l loads row (l % 16) of A and column (l % 16) of B, eight
 // consecutive reduction elements starting at 8 * (l / 16), and stores the

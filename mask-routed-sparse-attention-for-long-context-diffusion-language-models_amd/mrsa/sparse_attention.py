@@ -414,40 +414,141 @@ def _selected_attention_bwd_impl(q, kv_frags, kv_frags_bwd, weights, indices, ke
     return dq, dk, dv, dw
 
 
-class _SelectedAttention(torch.autograd.Function):
-    # ops/hils_fwd_bwd_head.py:915-1098 (_hils_block_M_attention_inverse):
-    # the forward saves its inputs; the backward recomputes each chunk's
-    # softmax and casts the fp32 gradients to the input dtypes.
-    @staticmethod
-    def forward(ctx, q, k, v, weights, indices, key_valid, chunk_size, mask_last_token,
-                sm_scale, token_keep):
-        ctx.save_for_backward(q, k, v, weights, indices, key_valid, token_keep)
-        ctx.chunk_size, ctx.mask_last_token, ctx.sm_scale = chunk_size, mask_last_token, sm_scale
-        return selected_attention_launch(
-            q, kv_fragments_cached(k, v), weights, indices, key_valid, chunk_size,
+def selected_attention_alibi_launch(q, kv_frags, weights, indices, key_valid, chunk_size, slope,
+                                   *, mask_last_token=True, sm_scale=None, parts=None,
+                                   token_keep=None, deterministic=False):
+    """selected_attention_launch with ALiBi slopes (fp32 [Hq]): before the
+    scale, key s of a chunk gets -slope[head] * max(0, 62 - s) on its raw
+    logit (ops/hils_fwd_bwd_head.py:445-451, hils_torch_ref :68-76)."""
+
+    B, Lq, Hq, D = q.shape
+    if kv_frags.ndim != 4 or kv_frags.shape[0] != B or kv_frags.shape[3] != FRAG_ELEMS:
+        raise ValueError(f"kv_frags {tuple(kv_frags.shape)} is not a kv_fragments layout")
+    if slope.shape != (Hq,):
+        raise ValueError(f"slope must be 1-D with shape ({Hq},), got {tuple(slope.shape)}")
+    Hkv, Lk = kv_frags.shape[1], kv_frags.shape[2] * 64
+    K = indices.shape[-1]
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    if parts is None:
+        parts = walk_parts(B, Lq, Hkv, Lk, K, chunk_size)
+    parts = int(parts)
+    if not 1 <= parts <= _SEL_MAX_PARTS:
+        raise ValueError(f"parts must be in [1, {_SEL_MAX_PARTS}], got {parts}")
+    qc = q.contiguous()
+    w = weights.to(torch.bfloat16).contiguous()
+    idx = indices.to(torch.int32).contiguous()
+    kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
+    keep = None if token_keep is None else token_keep.to(device=q.device, dtype=torch.int8).contiguous()
+    sl = slope.to(device=q.device, dtype=torch.float32).contiguous()
+    out = torch.empty(B, Lq, Hq, D, dtype=torch.bfloat16, device=q.device)
+    partial = None
+    if parts > 1:
+        partial = torch.empty(parts, B, Lq, Hq, D, dtype=torch.float32, device=q.device)
+    st = _lib.call(
+        "mrsa_selected_attention_alibi_fwd",
+        _lib.ptr(qc), None, _lib.ptr(kv_frags.contiguous()), _lib.ptr(w), _lib.ptr(idx),
+        _lib.ptr(kv), _lib.ptr(keep), None, None, _lib.ptr(sl), B, Lq, Lk, Hq, Hkv, D, K,
+        int(chunk_size), 1 if mask_last_token else 0, float(sm_scale), parts, _lib.ptr(partial),
+        _ROUTED_FIXED_ORDER if deterministic else 0, _lib.ptr(out), _lib.stream_of(qc),
+    )
+    _lib.check(st, "selected_attention (ALiBi)")
+    return out
+
+
+def selected_attention_alibi_backward(q, k, v, weights, indices, key_valid, chunk_size,
+                                      grad_output, slope, *, mask_last_token=True,
+                                      sm_scale=None, token_keep=None):
+    """Gradients (dq, dk, dv, dweights) of selected_attention_alibi_launch, fp32
+    (ops/hils_fwd_bwd_head.py:755-760: the backward's bias term).  No
+    gradient flows to the slopes."""
+
+    B, Lq, Hq, D = q.shape
+    Lk, Hkv = k.shape[1], k.shape[2]
+    K = indices.shape[-1]
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    qc = q.to(torch.bfloat16).contiguous()
+    go = grad_output.to(torch.bfloat16).contiguous()
+    w = weights.to(torch.bfloat16).contiguous()
+    idx = indices.to(torch.int32).contiguous()
+    kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
+    keep = None if token_keep is None else token_keep.to(device=q.device, dtype=torch.int8).contiguous()
+    sl = slope.to(device=q.device, dtype=torch.float32).contiguous()
+    dq = torch.zeros(B, Lq, Hq, D, dtype=torch.float32, device=q.device)
+    dk = torch.zeros(B, Lk, Hkv, D, dtype=torch.float32, device=q.device)
+    dv = torch.zeros(B, Lk, Hkv, D, dtype=torch.float32, device=q.device)
+    dw = torch.zeros(B, Lq, Hq, K, dtype=torch.bfloat16, device=q.device)
+    nbytes = int(_lib.call("mrsa_selected_attention_bwd_workspace_bytes", B, Lq, Lk, Hkv, K))
+    if nbytes < 0:
+        raise ValueError(f"invalid routed attention shapes q {tuple(q.shape)} kv_len {Lk}")
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    st = _lib.call(
+        "mrsa_selected_attention_alibi_bwd",
+        _lib.ptr(qc), _lib.ptr(go), _lib.ptr(kv_fragments_cached(k, v)),
+        _lib.ptr(kv_fragments_cached(v, k)), _lib.ptr(w), _lib.ptr(idx), _lib.ptr(kv),
+        _lib.ptr(keep), _lib.ptr(sl), B, Lq, Lk, Hq, Hkv, D, K, int(chunk_size),
+        1 if mask_last_token else 0, float(sm_scale), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
+        _lib.ptr(dw), _lib.ptr(ws), nbytes, _lib.stream_of(qc),
+    )
+    _lib.check(st, "selected_attention backward (ALiBi)")
+    return dq, dk, dv, dw
+
+
+def _routed_forward(q, k, v, weights, indices, key_valid, chunk_size, mask_last_token,
+                    sm_scale, token_keep, slope):
+    if slope is not None:
+        return selected_attention_alibi_launch(
+            q, kv_fragments_cached(k, v), weights, indices, key_valid, chunk_size, slope,
             mask_last_token=mask_last_token, sm_scale=sm_scale, token_keep=token_keep)
-
-    @staticmethod
-    def backward(ctx, grad_output):
-        q, k, v, weights, indices, key_valid, token_keep = ctx.saved_tensors
-        dq, dk, dv, dw = selected_attention_backward(
-            q, k, v, weights, indices, key_valid, ctx.chunk_size, grad_output,
-            mask_last_token=ctx.mask_last_token, sm_scale=ctx.sm_scale, token_keep=token_keep)
-        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dw.to(weights.dtype),
-                None, None, None, None, None, None)
-
-
-def selected_attention_autograd(q, k, v, weights, indices, key_valid, chunk_size, *,
-                                mask_last_token=True, sm_scale=None, token_keep=None):
-    """Routed attention with autograd when an input requires grad (gfx950
-    forward and backward kernels), else the plain forward."""
-
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, weights)):
-        return _SelectedAttention.apply(q, k, v, weights, indices, key_valid, chunk_size,
-                                        mask_last_token, sm_scale, token_keep)
     return selected_attention_launch(
         q, kv_fragments_cached(k, v), weights, indices, key_valid, chunk_size,
         mask_last_token=mask_last_token, sm_scale=sm_scale, token_keep=token_keep)
+
+
+class _SelectedAttention(torch.autograd.Function):
+    # ops/hils_fwd_bwd_head.py:915-1098 (_hils_block_M_attention_inverse):
+    # the forward saves its inputs; the backward recomputes each chunk's
+    # softmax and casts the fp32 gradients to the input dtypes.  The ALiBi
+    # slopes get no gradient (the reference returns none for them).
+    @staticmethod
+    def forward(ctx, q, k, v, weights, indices, key_valid, chunk_size, mask_last_token,
+                sm_scale, token_keep, slope=None):
+        ctx.save_for_backward(q, k, v, weights, indices, key_valid, token_keep, slope)
+        ctx.chunk_size, ctx.mask_last_token, ctx.sm_scale = chunk_size, mask_last_token, sm_scale
+        return _routed_forward(q, k, v, weights, indices, key_valid, chunk_size, mask_last_token,
+                               sm_scale, token_keep, slope)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        q, k, v, weights, indices, key_valid, token_keep, slope = ctx.saved_tensors
+        if slope is not None:
+            dq, dk, dv, dw = selected_attention_alibi_backward(
+                q, k, v, weights, indices, key_valid, ctx.chunk_size, grad_output, slope,
+                mask_last_token=ctx.mask_last_token, sm_scale=ctx.sm_scale,
+                token_keep=token_keep)
+        else:
+            dq, dk, dv, dw = selected_attention_backward(
+                q, k, v, weights, indices, key_valid, ctx.chunk_size, grad_output,
+                mask_last_token=ctx.mask_last_token, sm_scale=ctx.sm_scale,
+                token_keep=token_keep)
+        grads = (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dw.to(weights.dtype),
+                 None, None, None, None, None, None, None)
+        return grads[:len(ctx.needs_input_grad)]
+
+
+def selected_attention_autograd(q, k, v, weights, indices, key_valid, chunk_size, *,
+                                mask_last_token=True, sm_scale=None, token_keep=None,
+                                slope=None):
+    """Routed attention with autograd when an input requires grad (gfx950
+    forward and backward kernels), else the plain forward.  ``slope`` (fp32
+    [Hq]) adds the reference's ALiBi bias."""
+
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, weights)):
+        return _SelectedAttention.apply(q, k, v, weights, indices, key_valid, chunk_size,
+                                        mask_last_token, sm_scale, token_keep, slope)
+    return _routed_forward(q, k, v, weights, indices, key_valid, chunk_size, mask_last_token,
+                           sm_scale, token_keep, slope)
 
 
 def HiLS_block_M_head(
@@ -462,7 +563,9 @@ def HiLS_block_M_head(
     grad.
 
     Tiling knobs (block_M, num_threads*) are accepted and ignored: the gfx950
-    kernels pick their own tiling.  ALiBi slopes are not supported.
+    kernels pick their own tiling.  ``slope`` (shape (HQ,)) adds the ALiBi
+    bias -slope[head] * max(0, block_size - 2 - s) to the raw logit of chunk
+    key s (ops/hils_fwd_bwd_head.py:971-978, :445-451).
     """
 
     B, L, HQ, D = q.shape
@@ -470,7 +573,10 @@ def HiLS_block_M_head(
     assert D == Dk, f"Q head_dim ({D}) must equal K head_dim ({Dk})"
     assert HQ % H == 0, f"HQ={HQ} must be divisible by H={H}"
     if slope is not None:
-        raise ValueError("ALiBi slopes are not supported by the gfx950 routed-attention kernel")
+        assert tuple(slope.shape) == (HQ,), (
+            f"slope must be 1-D with shape ({HQ},), got {tuple(slope.shape)}"
+        )
+        slope = slope.to(dtype=torch.float32, device=q.device).contiguous()
     if token_keep is not None:
         expected_keep_shape = (B, L, H, indices.shape[-1], block_size)
         if token_keep.shape != expected_keep_shape:
@@ -484,5 +590,5 @@ def HiLS_block_M_head(
         raise ValueError(f"key_valid must have shape {(B, L_kv)}, got {tuple(key_valid.shape)}")
     return selected_attention_autograd(
         q, k, v, weights, indices, key_valid, block_size,
-        mask_last_token=mask_last_token, sm_scale=sm_scale, token_keep=token_keep,
+        mask_last_token=mask_last_token, sm_scale=sm_scale, token_keep=token_keep, slope=slope,
     )

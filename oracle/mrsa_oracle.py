@@ -417,7 +417,7 @@ def local_attention(q, k, v, key_valid, window, inert_chunk=0, query_positions=N
 # a8: routed chunk attention
 # ---------------------------------------------------------------------------
 def selected_attention(q, k, v, weights, indices, key_valid, chunk_size=64,
-                       mask_last_token=True, query_block=256, token_keep=None):
+                       mask_last_token=True, query_block=256, token_keep=None, slope=None):
     """Weighted sum of per-chunk softmax attentions.
 
     Formula of the reference test test_hils_non_power_two_topk.py:122-138 and
@@ -427,7 +427,9 @@ def selected_attention(q, k, v, weights, indices, key_valid, chunk_size=64,
     q [B, Lq, Hq, D], k/v [B, Lk, Hkv, D], weights [B, Lq, Hq, K],
     indices [B, Lq, Hkv, K].  token_keep [B, Lq, Hkv, K, S] (nonzero = keep)
     additionally masks the keys of slot k of each query (:457-486, the
-    TokenKeep[b, q, h, slot, key] term).  Returns fp32 [B, Lq, Hq, D].
+    TokenKeep[b, q, h, slot, key] term).  slope [Hq] adds the ALiBi bias
+    -slope[head] * max(0, (S - 2) - s) to the raw logit of chunk key s before
+    the scale (hils_torch_ref :68-76).  Returns fp32 [B, Lq, Hq, D].
     """
 
     B, Lq, Hq, D = q.shape
@@ -448,6 +450,10 @@ def selected_attention(q, k, v, weights, indices, key_valid, chunk_size=64,
     before_neg = torch.cumsum(neg.int(), dim=-1) == 0
     ok = before_neg & (idx >= 0) & (idx < C)
     safe = idx.clamp(0, C - 1)
+    alibi = None
+    if slope is not None:
+        dist = ((S - 2) - torch.arange(S, dtype=torch.float32)).clamp(min=0)
+        alibi = -slope.float().reshape(Hkv, G)[:, :, None] * dist        # [Hkv, G, S]
     out = torch.zeros(B, Lq, Hq, D)
     bidx = torch.arange(B)[:, None, None]
     hidx = torch.arange(Hkv)[None, None, :]
@@ -463,7 +469,10 @@ def selected_attention(q, k, v, weights, indices, key_valid, chunk_size=64,
             al = allowed[bidx, c]                           # [B, l, Hkv, S]
             if token_keep is not None:
                 al = al & (token_keep[:, i0:i1, :, kk] != 0)
-            s = torch.einsum("blhgd,blhsd->blhgs", qb, kg) * scale
+            s = torch.einsum("blhgd,blhsd->blhgs", qb, kg)
+            if alibi is not None:
+                s = s + alibi
+            s = s * scale
             s = s.masked_fill(~al[:, :, :, None, :], NEG_INF)
             p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
             o = torch.einsum("blhgs,blhsd->blhgd", p, vg)

@@ -271,6 +271,86 @@ def test_selected_attention_backward_vs_oracle(keep):
     assert float(tw.grad[0, 7, 0:7, 2].abs().max()) == 0.0
 
 
+@pytest.mark.parametrize("keep", [False, True])
+def test_selected_attention_alibi_forward_backward_vs_oracle(keep):
+    # HiLS_block_M_head(slope=...): the ALiBi bias -slope[head] max(0, 62 - s)
+    # on the raw logits (ops/hils_fwd_bwd_head.py:445-451, :755-760), forward
+    # and backward against the oracle's autograd.  Slopes of the usual ALiBi
+    # scale (2^-k) and one large one, so the bias moves the softmax.
+    _note(f"selected attention with ALiBi slopes keep={keep}")
+    B, Lq, Hkv, G, D, C, K = 1, 160, 4, 7, 128, 16, 8
+    Lk = C * 64
+    g = torch.Generator().manual_seed(170 + keep)
+    q = (torch.randn(B, Lq, Hkv * G, D, generator=g) * 0.5).bfloat16()
+    k = (torch.randn(B, Lk, Hkv, D, generator=g) * 0.5).bfloat16()
+    v = torch.randn(B, Lk, Hkv, D, generator=g).bfloat16()
+    w = torch.rand(B, Lq, Hkv * G, K, generator=g).bfloat16()
+    idx = torch.stack([torch.randperm(C, generator=g)[:K] for _ in range(B * Lq * Hkv)])
+    idx = idx.reshape(B, Lq, Hkv, K).int()
+    idx[0, 5, 1, 5:] = -1
+    valid = torch.rand(B, Lk, generator=g) > 0.05
+    slope = torch.tensor([2.0 ** -(1 + h % 8) for h in range(Hkv * G)])
+    slope[3] = 1.5
+    token_keep = None
+    if keep:
+        token_keep = (torch.rand(B, Lq, Hkv, K, 64, generator=g) > 0.3).to(torch.int8)
+    dout = torch.randn(B, Lq, Hkv * G, D, generator=g).bfloat16()
+
+    tq, tk, tv, tw = (t.to(DEV).requires_grad_(True) for t in (q, k, v, w))
+    out = mrsa.HiLS_block_M_head(tq, tk, tv, tw, idx.to(DEV), key_valid=valid.to(DEV),
+                                 slope=slope.to(DEV),
+                                 token_keep=None if token_keep is None else token_keep.to(DEV))
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+
+    rq, rk, rv, rw = (t.float().requires_grad_(True) for t in (q, k, v, w))
+    ref = O.selected_attention(rq, rk, rv, rw, idx, valid, token_keep=token_keep, slope=slope)
+    (ref * dout.float()).sum().backward()
+    plain = O.selected_attention(q, k, v, w, idx, valid, token_keep=token_keep)
+    assert _rel_err(plain, ref.detach()) > 0.05  # the slopes matter at this size
+    err = _rel_err(out.detach(), ref.detach())
+    print(f"  out: rel-norm error {err:.3e}", flush=True)
+    assert err < 1e-2, err
+    for name, got, exp in (("dq", tq.grad, rq.grad), ("dk", tk.grad, rk.grad),
+                           ("dv", tv.grad, rv.grad), ("dw", tw.grad, rw.grad)):
+        err = _rel_err(got, exp)
+        print(f"  {name}: rel-norm error {err:.3e}", flush=True)
+        assert err < 2e-2, (name, err)
+
+
+def test_selected_attention_alibi_walk_split_and_fixed_order():
+    # The ALiBi instances of the walk split (partials summed by the second
+    # kernel) and of the fixed accumulation order give the one-launch result;
+    # the fixed order twice gives the same bits.
+    _note("selected attention with ALiBi: walk split and fixed order")
+    from mrsa.sparse_attention import kv_fragments, selected_attention_alibi_launch
+    B, Lq, Hkv, G, D, C, K = 1, 64, 4, 7, 128, 32, 16
+    Lk = C * 64
+    g = torch.Generator().manual_seed(181)
+    q = (torch.randn(B, Lq, Hkv * G, D, generator=g) * 0.5).bfloat16().to(DEV)
+    k = (torch.randn(B, Lk, Hkv, D, generator=g) * 0.5).bfloat16().to(DEV)
+    v = torch.randn(B, Lk, Hkv, D, generator=g).bfloat16().to(DEV)
+    w = torch.rand(B, Lq, Hkv * G, K, generator=g).bfloat16().to(DEV)
+    idx = torch.stack([torch.randperm(C, generator=g)[:K].sort().values
+                       for _ in range(B * Lq * Hkv)]).reshape(B, Lq, Hkv, K).int().to(DEV)
+    slope = torch.tensor([0.25 * (1 + h % 3) for h in range(Hkv * G)], device=DEV)
+    frags = kv_fragments(k, v)
+    one = selected_attention_alibi_launch(q, frags, w, idx, None, 64, slope, parts=1)
+    split = selected_attention_alibi_launch(q, frags, w, idx, None, 64, slope, parts=8)
+    det1 = selected_attention_alibi_launch(q, frags, w, idx, None, 64, slope, parts=1,
+                                           deterministic=True)
+    det2 = selected_attention_alibi_launch(q, frags, w, idx, None, 64, slope, parts=1,
+                                           deterministic=True)
+    torch.cuda.synchronize()
+    assert torch.equal(det1, det2)
+    ref = O.selected_attention(q.cpu(), k.cpu(), v.cpu(), w.cpu(), idx.cpu(), None,
+                               slope=slope.cpu())
+    for name, got in (("one", one), ("split", split), ("det", det1)):
+        err = _rel_err(got, ref)
+        print(f"  {name}: rel-norm error {err:.3e}", flush=True)
+        assert err < 1e-2, (name, err)
+
+
 def test_selected_attention_backward_two_runs_agree_within_rounding():
     # The routed backward is not bit-reproducible: each chunk's (query, slot)
     # pair list is filled in LDS-atomic order, dK/dV of multi-segment chunks

@@ -143,3 +143,38 @@ def test_candidate_token_scores_closed_form():
     qq = q[0, 1].float().reshape(2, 3, 16)
     kk = k[0, 3 * 64 + 7, 1].float()
     assert abs(float(s[0, 1, 1, 0, 7]) - float((qq[1] @ kk).max() / 4.0)) < 1e-5
+
+
+def test_selected_attention_alibi_closed_form():
+    # q = 0 leaves only the ALiBi term: chunk key s has logit
+    # -slope[head] * max(0, 62 - s) * scale (hils_torch_ref :68-78: bias
+    # before the scale, the last key masked), and one-hot values e_s make the
+    # output the softmax itself.  Distinct slopes per head pin the head order;
+    # scale = 1/8 (D = 64) separates "bias then scale" from "scale then bias".
+    D, S, Hkv, G = 64, 64, 2, 2
+    slope = torch.tensor([0.5, 0.125, 1.0, 0.03125])
+    q = torch.zeros(1, 1, Hkv * G, D).bfloat16()
+    k = torch.randn(1, S, Hkv, D, generator=torch.Generator().manual_seed(21)).bfloat16()
+    v = torch.eye(S, D)[None, :, None, :].repeat(1, 1, Hkv, 1).bfloat16()
+    idx = torch.zeros(1, 1, Hkv, 1, dtype=torch.int32)
+    w = torch.ones(1, 1, Hkv * G, 1).bfloat16()
+    out = O.selected_attention(q, k, v, w, idx, None, S, slope=slope)
+    s = torch.arange(S, dtype=torch.float64)
+    for h in range(Hkv * G):
+        logit = -slope[h].double() * (62 - s).clamp(min=0) / math.sqrt(D)
+        logit[-1] = float("-inf")
+        expect = torch.softmax(logit, dim=0)
+        torch.testing.assert_close(out[0, 0, h].double(), expect, atol=1e-6, rtol=1e-5)
+    # with the last key visible, keys 62 and 63 both sit at distance 0 (a
+    # shifted distance would only move the visible logits together above)
+    out = O.selected_attention(q, k, v, w, idx, None, S, mask_last_token=False, slope=slope)
+    for h in range(Hkv * G):
+        logit = -slope[h].double() * (62 - s).clamp(min=0) / math.sqrt(D)
+        torch.testing.assert_close(out[0, 0, h].double(), torch.softmax(logit, dim=0),
+                                   atol=1e-6, rtol=1e-5)
+    # slope 0 is the plain attention, bit for bit
+    q2 = torch.randn(1, 3, Hkv * G, D, generator=torch.Generator().manual_seed(22)).bfloat16()
+    plain = O.selected_attention(q2, k, v, w.repeat(1, 3, 1, 1), idx.repeat(1, 3, 1, 1), None, S)
+    zero = O.selected_attention(q2, k, v, w.repeat(1, 3, 1, 1), idx.repeat(1, 3, 1, 1), None, S,
+                                slope=torch.zeros(Hkv * G))
+    assert torch.equal(plain, zero)
