@@ -531,6 +531,35 @@ int mrsa_local_attention_qf_fwd(const void* q, const void* kv_frags,
                                 float* lse, void* stream);
 
 /*
+ * Backward of mrsa_local_attention_fwd for full sequences (q_len == kv_len,
+ * no query positions): the gradient flash-attn's flash_attn_func gives
+ * bidir_local_attention (dream_dllm_hils/local_attention.py:67-107), with
+ * _apply_key_valid's masking (:50-54): keys that fail key_valid and, when
+ * inert_chunk > 0, the landmark slots carry k' = v' = 0 (in the softmax with
+ * logit 0), so their grad_k / grad_v are 0.
+ *   q, grad_out, out: bf16 [batch, seq_len, q_heads, 128] (out and lse as the
+ *                     forward returned them); k, v: bf16 [batch, seq_len,
+ *                     kv_heads, 128]; lse: fp32 [batch, seq_len, q_heads]
+ *   window, inert_chunk, sm_scale, key_valid: as the forward's
+ *   grad_q: fp32 [batch, seq_len, q_heads, 128]; grad_k, grad_v: fp32
+ *           [batch, seq_len, kv_heads, 128] (every element written)
+ *   workspace: 256-byte aligned, mrsa_local_attention_bwd_workspace_bytes
+ *           bytes (the operand images of K, V, Q and dO, and per-row lse / D)
+ * The LSE output carries no gradient (flash-attn's autograd drops it).
+ * Rounding points as flash-attn's: P and dS are bf16 matrix operands, every
+ * sum is fp32.  Requirements: head_dim 128, 16-byte aligned tensors.
+ */
+int64_t mrsa_local_attention_bwd_workspace_bytes(int64_t batch, int64_t seq_len,
+                                                 int64_t q_heads, int64_t kv_heads);
+int mrsa_local_attention_bwd(const void* q, const void* k, const void* v,
+                             const uint8_t* key_valid, const void* out, const float* lse,
+                             const void* grad_out, int64_t batch, int64_t seq_len,
+                             int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t window,
+                             int64_t inert_chunk, float sm_scale, float* grad_q, float* grad_k,
+                             float* grad_v, void* workspace, int64_t workspace_bytes,
+                             void* stream);
+
+/*
  * The same window attention for short query blocks (cached_local_attention,
  * dream_dllm_hils/local_attention.py:147-200, at the cached block step):
  * each 32-query block's key tiles are split over `parts` workgroups (1..64)

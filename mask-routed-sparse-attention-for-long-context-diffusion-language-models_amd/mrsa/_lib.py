@@ -162,6 +162,12 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
          _I64, _I, _F, _I64, _P, _I, _P, _P],
     ),
+    "mrsa_local_attention_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
+    "mrsa_local_attention_bwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P,
+         _P, _I64, _P],
+    ),
     "mrsa_routed_lock_giveups": (_I, [_P, _I]),
     "mrsa_set_routed_lock_spin_limit": (_I, [_I]),
     "mrsa_selected_attention_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),

@@ -49,7 +49,7 @@ def key_parts(batch: int, q_len: int, kv_heads: int, kv_len: int, flash_window: 
     heads -> 8 workgroups over ~11 key tiles) splits its key tiles so that
     about 64 workgroups run, at least one tile each."""
 
-    blocks = -(-q_len // 16) * kv_heads * batch  # 16 queries per workgroup (G = 7)
+    blocks = -(-q_len // 16) * kv_heads * batch  # ~16 queries per workgroup (18 for G = 7)
     if blocks >= 128 or blocks == 0:
         return 1
     tiles = (min(q_len, kv_len) + 2 * flash_window) // 64 + 2
@@ -154,6 +154,74 @@ def _local_attention_qf_impl(q, kv_frags, key_valid, kv_len, flash_window, inert
     return out, lse, qf
 
 
+def local_attention_backward(q, k, v, key_valid, out, lse, grad_out, flash_window, inert_chunk,
+                             *, sm_scale=None):
+    """Gradients (dq, dk, dv; fp32) of the window attention of full sequences
+    (local_attention_launch with kv_len = q_len and no query positions): the
+    gradient flash-attn's flash_attn_func gives (local_attention.py:67-107),
+    with zero dk / dv for inert keys (:50-54).  out and lse are the forward's
+    outputs; the LSE carries no gradient."""
+
+    B, L, Hq, D = q.shape
+    Hkv = k.shape[2]
+    if k.shape[1] != L or v.shape != k.shape or out.shape != q.shape or grad_out.shape != q.shape:
+        raise ValueError("local attention backward requires equal Q/K lengths and matching shapes")
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    qc = q.to(torch.bfloat16).contiguous()
+    kc = k.to(torch.bfloat16).contiguous()
+    vc = v.to(torch.bfloat16).contiguous()
+    oc = out.to(torch.bfloat16).contiguous()
+    go = grad_out.to(torch.bfloat16).contiguous()
+    lc = lse.to(torch.float32).contiguous()
+    kv = None if key_valid is None else key_valid.to(device=q.device, dtype=torch.bool).contiguous()
+    dq = torch.empty(B, L, Hq, D, dtype=torch.float32, device=q.device)
+    dk = torch.empty(B, L, Hkv, D, dtype=torch.float32, device=q.device)
+    dv = torch.empty(B, L, Hkv, D, dtype=torch.float32, device=q.device)
+    nbytes = int(_lib.call("mrsa_local_attention_bwd_workspace_bytes", B, L, Hq, Hkv))
+    if nbytes < 0:
+        raise ValueError(f"invalid local attention shapes q {tuple(q.shape)} k {tuple(k.shape)}")
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    st = _lib.call(
+        "mrsa_local_attention_bwd",
+        _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(kv), _lib.ptr(oc), _lib.ptr(lc),
+        _lib.ptr(go), B, L, Hq, Hkv, D, int(flash_window), int(inert_chunk), float(sm_scale),
+        _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(ws), nbytes, _lib.stream_of(qc),
+    )
+    _lib.check(st, "local_attention backward")
+    return dq, dk, dv
+
+
+class _LocalAttention(torch.autograd.Function):
+    # flash_attn_func's autograd as bidir_local_attention uses it: gradients
+    # for q, k, v; the LSE output is not differentiable.
+    @staticmethod
+    def forward(ctx, q, k, v, key_valid, flash_window, inert_chunk):
+        out, lse = local_attention_launch(q, kv_fragments_cached(k, v), key_valid, flash_window,
+                                          inert_chunk, kv_len=k.shape[1])
+        ctx.mark_non_differentiable(lse)
+        ctx.save_for_backward(q, k, v, key_valid, out, lse)
+        ctx.flash_window, ctx.inert_chunk = flash_window, inert_chunk
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_lse):
+        q, k, v, key_valid, out, lse = ctx.saved_tensors
+        dq, dk, dv = local_attention_backward(q, k, v, key_valid, out, lse, grad_out,
+                                              ctx.flash_window, ctx.inert_chunk)
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None
+
+
+def local_attention_autograd(q, k, v, key_valid, flash_window, inert_chunk):
+    """(out, lse) of the full-sequence window attention, differentiable in q,
+    k and v when one of them requires grad."""
+
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        return _LocalAttention.apply(q, k, v, key_valid, int(flash_window), int(inert_chunk))
+    return local_attention_launch(q, kv_fragments_cached(k, v), key_valid, flash_window,
+                                  inert_chunk, kv_len=k.shape[1])
+
+
 def bidir_local_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -164,7 +232,8 @@ def bidir_local_attention(
     allowed_mask: torch.Tensor | None = None,
     skip_inert_slots: bool = False,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Bidirectional local GQA attention and natural-log LSE [B, L, Hq]."""
+    """Bidirectional local GQA attention and natural-log LSE [B, L, Hq];
+    differentiable in q, k and v (the LSE is not), as flash_attn_func is."""
 
     _validate_layout(q, k, v, key_valid)
     seq_len = q.shape[1]
@@ -179,10 +248,9 @@ def bidir_local_attention(
             "bidir_local_attention only accepts 2D key_valid; "
             "do not pass a dense L×L allowed_mask"
         )
-    return local_attention_launch(
-        q, kv_fragments_cached(k, v), key_valid,
-        _flash_window(window, skip_inert_slots, chunk_size),
-        chunk_size if skip_inert_slots else 0, kv_len=k.shape[1],
+    return local_attention_autograd(
+        q, k, v, key_valid, _flash_window(window, skip_inert_slots, chunk_size),
+        chunk_size if skip_inert_slots else 0,
     )
 
 

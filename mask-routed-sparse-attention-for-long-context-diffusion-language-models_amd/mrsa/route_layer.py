@@ -38,7 +38,8 @@ import torch
 
 from . import _lib
 from .kernel_utils import drop_mask_rows_launch
-from .local_attention import key_parts, local_attention_launch, local_attention_qf_launch
+from .local_attention import (key_parts, local_attention_autograd, local_attention_launch,
+                              local_attention_qf_launch)
 from .pool import _needs_grad, chunk_attn_pool_gqa_prior, kv_fragments_pool
 from .route_weights import route_weights_launch
 from .sparse_attention import (FRAG_ELEMS, kv_fragments, kv_fragments_cached, kv_fragments_rows,
@@ -249,10 +250,8 @@ def swa_attention(
     if q.device.type != "cuda" or q.dtype != torch.bfloat16:
         raise ValueError("swa_attention requires CUDA bf16 tensors")
     flash_window = window + chunk_size - 1 if skip_inert_slots else window
-    out, _ = local_attention_launch(
-        q, kv_fragments_cached(k, v), key_valid, flash_window,
-        chunk_size if skip_inert_slots else 0, kv_len=k.shape[1],
-    )
+    out, _ = local_attention_autograd(q, k, v, key_valid, flash_window,
+                                      chunk_size if skip_inert_slots else 0)
     return out
 
 

@@ -351,6 +351,73 @@ def test_selected_attention_alibi_walk_split_and_fixed_order():
         assert err < 1e-2, (name, err)
 
 
+@pytest.mark.parametrize("L,W,inert,G,Hkv", [(1024, 319, 64, 7, 4), (1024, 1280, 0, 7, 2),
+                                              (512, 100, 64, 4, 2), (640, 200, 0, 8, 2),
+                                              (448, 150, 64, 3, 3), (256, 40, 0, 1, 2)])
+def test_local_attention_backward_vs_oracle(L, W, inert, G, Hkv):
+    # The window attention's gradient (flash_attn_func's, as
+    # bidir_local_attention uses it) against autograd of the oracle: dq, dk,
+    # dv; inert keys (failed key_valid, landmark slots) get exactly zero dk / dv.
+    _note(f"local attention backward L={L} W={W} inert={inert} G={G} Hkv={Hkv}")
+    from mrsa.local_attention import local_attention_autograd
+    D = 128
+    g = torch.Generator().manual_seed(300 + L + W + G)
+    q = (torch.randn(1, L, Hkv * G, D, generator=g) * 0.5).bfloat16()
+    k = (torch.randn(1, L, Hkv, D, generator=g) * 0.5).bfloat16()
+    v = torch.randn(1, L, Hkv, D, generator=g).bfloat16()
+    valid = torch.rand(1, L, generator=g) > 0.05
+    dout = torch.randn(1, L, Hkv * G, D, generator=g).bfloat16()
+
+    tq, tk, tv = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    out, lse = local_attention_autograd(tq, tk, tv, valid.to(DEV), W, inert)
+    assert not lse.requires_grad
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+
+    rq, rk, rv = (t.float().requires_grad_(True) for t in (q, k, v))
+    ref, _ = O.local_attention(rq, rk, rv, valid, W, inert)
+    (ref * dout.float()).sum().backward()
+    for name, got, exp in (("dq", tq.grad, rq.grad), ("dk", tk.grad, rk.grad),
+                           ("dv", tv.grad, rv.grad)):
+        assert got.dtype == torch.bfloat16, name
+        err = _rel_err(got, exp)
+        print(f"  {name}: rel-norm error {err:.3e}", flush=True)
+        assert err < 2e-2, (name, err)
+    dead = ~valid[0]
+    if inert:
+        dead |= (torch.arange(L) + 1) % inert == 0
+    assert float(tk.grad[0, dead.to(DEV)].abs().max()) == 0.0
+    assert float(tv.grad[0, dead.to(DEV)].abs().max()) == 0.0
+
+
+def test_bidir_local_attention_and_swa_are_differentiable():
+    # The drop-ins carry the gradient through the public API: the route
+    # layer's window (skip_inert_slots: radius 256 + 63, landmark slots inert)
+    # and the SWA layer's.
+    _note("bidir_local_attention / swa_attention backward")
+    from mrsa.route_layer import swa_attention
+    L, Hkv, G, D = 512, 2, 7, 128
+    g = torch.Generator().manual_seed(321)
+    q = (torch.randn(1, L, Hkv * G, D, generator=g) * 0.5).bfloat16()
+    k = (torch.randn(1, L, Hkv, D, generator=g) * 0.5).bfloat16()
+    v = torch.randn(1, L, Hkv, D, generator=g).bfloat16()
+    valid = torch.ones(1, L, dtype=torch.bool)
+    dout = torch.randn(1, L, Hkv * G, D, generator=g).bfloat16()
+    for name, fn, W, inert in (
+            ("bidir", lambda a, b, c: mrsa.bidir_local_attention(
+                a, b, c, valid.to(DEV), 256, 64, skip_inert_slots=True)[0], 319, 64),
+            ("swa", lambda a, b, c: swa_attention(a, b, c, valid.to(DEV), window=200), 200, 0)):
+        tq, tk, tv = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+        fn(tq, tk, tv).backward(dout.to(DEV))
+        rq, rk, rv = (t.float().requires_grad_(True) for t in (q, k, v))
+        (O.local_attention(rq, rk, rv, valid, W, inert)[0] * dout.float()).sum().backward()
+        for gname, got, exp in (("dq", tq.grad, rq.grad), ("dk", tk.grad, rk.grad),
+                                ("dv", tv.grad, rv.grad)):
+            err = _rel_err(got, exp)
+            print(f"  {name} {gname}: rel-norm error {err:.3e}", flush=True)
+            assert err < 2e-2, (name, gname, err)
+
+
 def test_selected_attention_backward_two_runs_agree_within_rounding():
     # The routed backward is not bit-reproducible: each chunk's (query, slot)
     # pair list is filled in LDS-atomic order, dK/dV of multi-segment chunks

@@ -391,3 +391,42 @@ def test_oracle_route_score_bwd_ignores_invalid_slots_and_sums_shared_heads():
     pq, pl = O.route_score_bwd(q, rep.contiguous(), idx, gs)
     torch.testing.assert_close(sq, pq, atol=1e-5, rtol=1e-5)
     torch.testing.assert_close(sl, pl.reshape(B, -1, H, G, D).sum(3), atol=1e-5, rtol=1e-5)
+
+
+# -- window attention backward (flash_attn_func's gradient) -----------------
+def test_oracle_local_attention_grad_central_differences_and_inert_keys():
+    # The window-attention gradient checked by the GPU kernels is autograd of
+    # the oracle's forward (itself pinned against a dense formulation).  Pin
+    # that gradient numerically along random directions, and check the
+    # masking rule: inert keys (failed key_valid, landmark slots) get zero
+    # dk / dv because the forward uses k * m, v * m (local_attention.py:50-54).
+    g = torch.Generator().manual_seed(31)
+    B, L, Hkv, G, D, W, inert = 1, 24, 2, 3, 16, 5, 8
+    q = torch.randn(B, L, Hkv * G, D, generator=g)
+    k = torch.randn(B, L, Hkv, D, generator=g)
+    v = torch.randn(B, L, Hkv, D, generator=g)
+    valid = torch.rand(B, L, generator=g) > 0.2
+    dout = torch.randn(B, L, Hkv * G, D, generator=g)
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out, _ = O.local_attention(qr, kr, vr, valid, W, inert)
+    (out * dout).sum().backward()
+    dead = ~valid[0] | ((torch.arange(L) + 1) % inert == 0)
+    assert bool(dead.any()) and bool((~dead).any())
+    assert float(kr.grad[0, dead].abs().max()) == 0.0
+    assert float(vr.grad[0, dead].abs().max()) == 0.0
+    assert float(kr.grad[0, ~dead].abs().max()) > 0.0
+
+    def f(q_, k_, v_):
+        return float((O.local_attention(q_, k_, v_, valid, W, inert)[0].double() * dout).sum())
+
+    eps = 1e-2
+    for which, grad in ((0, qr.grad), (1, kr.grad), (2, vr.grad)):
+        base = [q, k, v]
+        d = torch.randn(base[which].shape, generator=g)
+        plus = [x.clone() for x in base]
+        minus = [x.clone() for x in base]
+        plus[which] = base[which] + eps * d
+        minus[which] = base[which] - eps * d
+        num = (f(*plus) - f(*minus)) / (2 * eps)
+        ana = float((grad * d).sum())
+        assert abs(num - ana) <= 2e-2 * max(1.0, abs(ana)), (which, num, ana)
