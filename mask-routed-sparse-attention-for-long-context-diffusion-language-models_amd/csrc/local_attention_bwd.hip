@@ -277,15 +277,18 @@ __global__ void __launch_bounds__(kThreads, 1) local_bwd_kernel(BwdArgs a) {
       const_cast<uint16_t*>(a.fb + (b * a.Hkv + h) * NT * (int64_t)kFragElems), (short)0,
       (int)(uint32_t)(NT * kTileBytes), 0x00020000);
   const uint32_t dma_lane = 16u * lane;
-  // Tile t into slot s: each wave 4 images of A|A' and 4 of B|B'.
+  // Tile t into slot s: each wave 4 images of A|A' and 4 of B|B' (the dQ
+  // pass reads no A', the images of waves 4..7).
   auto issue_tile = [&](int64_t t, int s) {
     unsigned char* da = ring + s * kSlotBytes + (4 * wave) * 1024;
     unsigned char* db = da + kTileBytes;
     const uint32_t src = (uint32_t)t * (uint32_t)kTileBytes + (uint32_t)(4 * wave) * 1024u;
+    if (DKV || wave < 4) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ras, (lds_void_t*)(da + u * 1024), 16, dma_lane,
-                                               src + 1024u * u, 0, 0);
+      for (int u = 0; u < 4; ++u)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ras, (lds_void_t*)(da + u * 1024), 16, dma_lane,
+                                                 src + 1024u * u, 0, 0);
+    }
 #pragma unroll
     for (int u = 0; u < 4; ++u)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rbs, (lds_void_t*)(db + u * 1024), 16, dma_lane,
