@@ -18,9 +18,10 @@ Prints ONE JSON line (rank 0).  Besides the contract fields it carries:
                 dependent kernels costs a few microseconds of dispatch, so the
                 timed steps record only the two around the routed attention)
 
-``--workload backward`` times the backward of the routed attention and of
-the route scores at configuration 2's shapes, on the routing of the forward
-route layer (training-side: no BASELINE number exists for it).
+``--workload backward`` times the backward of the routed attention, of the
+route scores and of the window attention (radius 319, landmark slots inert)
+at configuration 2's shapes, on the routing of the forward route layer
+(training-side: no BASELINE number exists for it).
 
 ``--workload decode`` instead times the Fast-dLLM cached block step of one
 route layer (SURVEY configuration 5): a K/V cache of L=131072 tokens (2048
@@ -304,7 +305,8 @@ def backward_main(args, torch, mrsa, dev) -> int:
     (grad_q, grad_lmk) at configuration 2, with indices, weights and
     landmarks from the forward route layer and seeded upstream gradients."""
 
-    from mrsa.sparse_attention import selected_attention_backward
+    from mrsa.local_attention import local_attention_backward, local_attention_launch
+    from mrsa.sparse_attention import kv_fragments, selected_attention_backward
 
     L, C, G = L_CFG2, L_CFG2 // CHUNK, HQ // HKV
     q, k, v = make_inputs(L, 1234, dev, torch.bfloat16)
@@ -318,16 +320,20 @@ def backward_main(args, torch, mrsa, dev) -> int:
     dscore = torch.randn(1, L, HKV, G, TOPK, generator=g, device=dev).bfloat16()
     q5 = q.reshape(1, L, HKV, G, D)
     lmk4 = lmk.reshape(1, C, HQ, D)
+    flash_window = WINDOW + CHUNK - 1
+    local_out, local_lse = local_attention_launch(q, kv_fragments(k, v), valid, flash_window, CHUNK)
     stream = torch.cuda.current_stream(dev)
     times = []
 
     def run(record):
-        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
         e[0].record(stream)
         selected_attention_backward(q, k, v, w, idx, valid, CHUNK, dout)
         e[1].record(stream)
         torch.ops.mrsa.route_score_bwd(q5, lmk4, idx, dscore, D ** -0.5)
         e[2].record(stream)
+        local_attention_backward(q, k, v, valid, local_out, local_lse, dout, flash_window, CHUNK)
+        e[3].record(stream)
         if record:
             times.append(e)
 
@@ -341,10 +347,11 @@ def backward_main(args, torch, mrsa, dev) -> int:
     ms_per_step = 1000.0 * (time.perf_counter() - t0) / args.steps
     sel_us = sum(e[0].elapsed_time(e[1]) for e in times) * 1000.0 / len(times)
     score_us = sum(e[1].elapsed_time(e[2]) for e in times) * 1000.0 / len(times)
+    window_us = sum(e[2].elapsed_time(e[3]) for e in times) * 1000.0 / len(times)
     flops = backward_flops(L)
     achieved = flops / (sel_us * 1e-6) / 1e12
     line = {
-        "metric": "MRSA routed-attention + route-score backward tokens/s @16k (config 2 shapes)",
+        "metric": "MRSA route-layer backward (routed attention + route scores + window) tokens/s @16k (config 2 shapes)",
         "value": L / (ms_per_step / 1000.0),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -356,14 +363,15 @@ def backward_main(args, torch, mrsa, dev) -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "routed attention + route score backward (config 2 shapes)",
+        "config": {"workload": "routed attention + route score + window attention backward (config 2 shapes)",
                    "seq_len": L, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
                    "chunk_size": CHUNK, "topk": TOPK, "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "kernel": "selected_attention backward (chunk-major)",
                      "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
                      "flops_per_launch": flops, "avg_launch_us": sel_us},
-        "stages_us": {"selected_attention_backward": sel_us, "route_score_backward": score_us},
+        "stages_us": {"selected_attention_backward": sel_us, "route_score_backward": score_us,
+                      "local_attention_backward": window_us},
     }
     print(json.dumps(line), flush=True)
     return 0
