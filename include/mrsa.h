@@ -649,8 +649,12 @@ int mrsa_selected_attention_keep_fwd(const void* q, const void* kv_frags,
  * _hils_block_M_attention_inverse.backward, :1050-1098).  Each listed
  * (query, chunk) recomputes its chunk softmax; with the reference's rounding
  * points P = bf16(2^(s c - lse)), di = sum P dP, dS = bf16(scale w P (dP - di)):
- *   grad_q += sum dS K              fp32 [batch, q_len, q_heads, head_dim] (added
- *                                   with atomics: zero it first)
+ *   grad_q += sum dS K              fp32 [batch, q_len, q_heads, head_dim] (added:
+ *                                   zero it first); the chunk-major pass stores
+ *                                   each (query, head, slot)'s bf16 dS and the
+ *                                   forward kernel's walk adds dS K into the rows
+ *                                   of the queries it owns (a slot that repeats
+ *                                   an earlier chunk of its list adds with atomics)
  *   grad_k += dS^T Q, grad_v += P^T bf16(w dO)
  *                                   fp32 [batch, kv_len, kv_heads, head_dim]
  *                                   (zero them first: a chunk no query routes to
@@ -666,13 +670,14 @@ int mrsa_selected_attention_keep_fwd(const void* q, const void* kv_frags,
  *                 bytes: the per-chunk lists of (query, slot) pairs from which
  *                 grad_k / grad_v are computed chunk by chunk (one write per
  *                 chunk; chunks with more than 1024 pairs add their segments'
- *                 sums with atomics, so their last bits depend on timing).
+ *                 sums with atomics, so their last bits depend on timing), and
+ *                 the dS records (128 bytes per (query, head, slot)).
  * Requirements: head_dim 128, chunk_size 64, q_heads / kv_heads <= 8, topk <= 64,
  * kv_len / 64 <= 8192, q_len < 2^24.
  */
 int64_t mrsa_selected_attention_bwd_workspace_bytes(int64_t batch, int64_t q_len,
-                                                    int64_t kv_len, int64_t kv_heads,
-                                                    int64_t topk);
+                                                    int64_t kv_len, int64_t q_heads,
+                                                    int64_t kv_heads, int64_t topk);
 int mrsa_selected_attention_bwd(const void* q, const void* grad_out, const void* kv_frags,
                                 const void* kv_frags_bwd, const void* weights,
                                 const int32_t* indices, const uint8_t* key_valid,

@@ -242,6 +242,14 @@ __device__ __forceinline__ float logaddexp_f(float a, float b) {
   return m + log1pf(expf(-fabsf(a - b)));
 }
 
+// The routed backward's dQ walk (routed_attention.hip): grad_q += the dS . K
+// terms of each query's listed chunks (first occurrences), from the dS
+// records the chunk-major backward kernel wrote ([B, Lq, Hq, K] x 64 bf16).
+int routed_dq_walk(const void* kv_frags_bwd, const void* ds_records, const int32_t* indices,
+                   const uint8_t* key_valid, int64_t batch, int64_t q_len, int64_t kv_len,
+                   int64_t q_heads, int64_t kv_heads, int64_t topk, float* grad_q,
+                   void* stream);
+
 }  // namespace mrsa
 
 // Host helpers for launch-status mapping.

@@ -119,6 +119,12 @@ struct RaArgs {
   int spin_limit;            // lock tries before a tile is deferred (<= 0: every tile)
   int det;                   // fixed accumulation order (per-query tickets instead of the lock)
   const float* slope;        // [Hq] ALiBi slopes (ALIBI instances only)
+  // EXT instances (the routed backward's dQ walk): P^T tiles read from
+  // ext_p [B, Lq, Hq, K] records of 64 bf16 (lane group g's 16 keys at 16 g,
+  // in the order tile_P packs them), the fragments' V half being K^T, and
+  // the fp32 rows added into ext_out [B, Lq, Hq, 128].
+  const uint16_t* ext_p;
+  float* ext_out;
 };
 
 __host__ __device__ inline size_t al16(size_t x) { return (x + 15) & ~(size_t)15; }
@@ -260,7 +266,7 @@ __device__ __forceinline__ void load_q(u32x4_t (&Qb)[4], __amdgpu_buffer_rsrc_t 
   for (int ks = 0; ks < 4; ++ks) Qb[ks] = bload(r, off, kstep * ks);
 }
 
-template <bool TOKEN, bool KEEP, bool DET, bool ALIBI>
+template <bool TOKEN, bool KEEP, bool DET, bool ALIBI, bool EXT = false>
 __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   // Workgroup -> work unit, XCD-aware: workgroups are dealt to the 8 XCDs
@@ -279,7 +285,8 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
 
   const int K = a.K, G = a.G, tq = a.tq;
   const int64_t Ck = a.Ck;
-  const RaLayout L = ra_layout(tq, G, K, Ck, TOKEN, KEEP, DET);
+  // (EXT items keep their duplicate slots' mask where KEEP keeps a keep row)
+  const RaLayout L = ra_layout(tq, G, K, Ck, TOKEN, KEEP || EXT, DET);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -329,7 +336,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     *dcount = 0u;
   }
   for (int64_t c = tid; c < Ck; c += kThreads) omask[c] = 0u;
-  if constexpr (!TOKEN) {
+  if constexpr (!TOKEN && !EXT) {
     const uint16_t* wrow0 = a.w + ((b * a.Lq + q0) * a.Hq + (int64_t)h * G) * K;
     const int64_t qstride = (int64_t)a.Hq * K;
     if ((K & 7) == 0 && ((uintptr_t)a.w & 15) == 0) {
@@ -476,6 +483,14 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     }
     if constexpr (KEEP)
       it_keep[pos] = kept_bits(a.keep + (((b * a.Lq + q0 + qq) * a.Hkv + h) * K + kk) * 64);
+    if constexpr (EXT) {
+      // the later slots of the list holding the same chunk: their dS records
+      // add to the item's
+      uint64_t dm = 0ull;
+      if (!plain)
+        for (int k2 = kk + 1; k2 < n; ++k2) dm |= (uint64_t)(raw[qq * K + k2] == c) << k2;
+      it_keep[pos] = dm;
+    }
   }
   // Excluded keys of every step (bit k = key k of its chunk): the landmark
   // slot and invalid keys.  One step per thread, its 64 valid bytes loaded
@@ -570,6 +585,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   bool more = false;
   uint64_t msk = 0, mskn = 0;
   u32x4_t kb[4][4], vb[8][2], Qb[4];
+  u32x4_t Pn[2];  // EXT: the next tile's records
   // P^T operand of a tile from its S^T accumulators: excluded keys (the
   // chunk's `mskc`, bit k = key k; keys a keep row drops) -> -inf, the
   // chunk's softmax times the column's routing weight `wv`, rounded to bf16.
@@ -755,6 +771,59 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
   uint32_t setwant0 = 0u, setwant1 = 0u;
   int sett0 = 0, sett1 = 0;
 
+  // EXT: the P^T operand of item ii's column -- the record of (query, head
+  // gcol, list slot) -- read for every lane from a real record (padding
+  // heads read head 0's) and zeroed after, so that no branch waits for it.
+  // A chunk listed again later in the list (it_keep[ii]: the later slots)
+  // adds those slots' records, summed in fp32 and rounded once.
+  auto ext_rec = [&](int ii) {
+    const int qq = it_q[ii];
+    return a.ext_p +
+           ((b * a.Lq + q0 + qq) * a.Hq + (int64_t)h * G + (gcol < G ? gcol : 0)) * K * 64 +
+           16 * grp;
+  };
+  // the record of item ii's column (issued a tile ahead of its use)
+  auto ext_load = [&](int ii, u32x4_t (&Pb)[2]) {
+    const uint16_t* rec = ext_rec(ii) + it_slot[ii] * 64;
+    Pb[0] = *reinterpret_cast<const u32x4_t*>(rec);
+    Pb[1] = *reinterpret_cast<const u32x4_t*>(rec + 8);
+  };
+  // padding columns zeroed; the later duplicate slots' records added
+  auto ext_finish = [&](int ii, bool cvalid, u32x4_t (&Pb)[2]) {
+    const u32x4_t z = {0u, 0u, 0u, 0u};
+    Pb[0] = cvalid ? Pb[0] : z;
+    Pb[1] = cvalid ? Pb[1] : z;
+    uint64_t dm = cvalid ? it_keep[ii] : 0ull;
+    const uint16_t* rec0 = ext_rec(ii);
+    if (dm) {
+      float f[2][8];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f[h2][2 * i] = bf16_lo(Pb[h2][i]);
+          f[h2][2 * i + 1] = bf16_hi(Pb[h2][i]);
+        }
+      while (dm) {
+        const int s2 = __builtin_ctzll(dm);
+        dm &= dm - 1ull;
+        const u32x4_t y0 = *reinterpret_cast<const u32x4_t*>(rec0 + s2 * 64);
+        const u32x4_t y1 = *reinterpret_cast<const u32x4_t*>(rec0 + s2 * 64 + 8);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f[0][2 * i] += bf16_lo(y0[i]);
+          f[0][2 * i + 1] += bf16_hi(y0[i]);
+          f[1][2 * i] += bf16_lo(y1[i]);
+          f[1][2 * i + 1] += bf16_hi(y1[i]);
+        }
+      }
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Pb[h2][i] = pack_bf16x2(f[h2][2 * i], f[h2][2 * i + 1]);
+    }
+  };
+
   // One tile: columns 2 t + own of the step's owners.  The last tile of a
   // step (LAST) prefetches the next step's first Q and its K (after the QK
   // product) and V (after the PV product); other tiles prefetch the next
@@ -779,17 +848,33 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     }
     // The column's weight, read for every lane (ii is a real item of the
     // step) and consumed after the QK product, so that no branch waits for it.
-    uint32_t wraw = TOKEN ? 0u : it_w[ii * 8 + gcol];
+    uint32_t wraw = TOKEN || EXT ? 0u : it_w[ii * 8 + gcol];
     // S^T = K . Q^T: lane (grp, j) gets keys 16 mt + 4 grp + r of column j.
     f32x4_t S[4];
+    u32x4_t Pe[2];
+    if constexpr (EXT) {
+      Pe[0] = Pn[0];
+      Pe[1] = Pn[1];
+      ext_finish(ii, cvalid, Pe);
+      // the next tile's records: the next tile of this step, or the first
+      // tile of the next step (this one again when there is none)
+      int in = ii;
+      if constexpr (!LAST) in = i0 + min(2 * t + 2 + own, n - 1);
+      else if (more) in = i0n + min(own, nn - 1);
+      ext_load(in, Pn);
+    } else {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      S[mt] = zero4();
+      for (int mt = 0; mt < 4; ++mt) {
+        S[mt] = zero4();
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) S[mt] = mfma_bf16_16x16x32(kb[mt][ks], Qb[ks], S[mt]);
+        for (int ks = 0; ks < 4; ++ks) S[mt] = mfma_bf16_16x16x32(kb[mt][ks], Qb[ks], S[mt]);
+      }
     }
     uint32_t nown2;
-    if constexpr (!LAST) {
+    if constexpr (EXT) {
+      if constexpr (!LAST) nown2 = (uint32_t)__builtin_amdgcn_readfirstlane(nx_a | (nx_b << 8));
+      else nown2 = own2n;
+    } else if constexpr (!LAST) {
       // read after the QK issue
       asm volatile("" : "+v"(nx_a), "+v"(nx_b), "+v"(wraw) : "v"(S[3][3]));
       nown2 = (uint32_t)__builtin_amdgcn_readfirstlane(nx_a | (nx_b << 8));
@@ -849,8 +934,13 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       }
     } else {
       u32x4_t Pb[2];
-      const float wv = cvalid ? bf16_to_f32(wraw) : 0.f;
-      tile_P(S, msk, wv, KEEP && o < n ? it_keep[ii] : ~0ull, Pb);
+      if constexpr (EXT) {
+        Pb[0] = Pe[0];
+        Pb[1] = Pe[1];
+      } else {
+        const float wv = cvalid ? bf16_to_f32(wraw) : 0.f;
+        tile_P(S, msk, wv, KEEP && o < n ? it_keep[ii] : ~0ull, Pb);
+      }
       // Add the tile into its owners' rows under the lock: the rows are read
       // into the accumulators and O^T_tile = V^T . P^T is added onto them
       // (lane (grp, j): column j, dims 16 nt + 4 grp + r).  A missing second
@@ -858,7 +948,8 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       // rows, with P = 0.
       const int qb = hb ? qb1 : sinkq;
       float* const srow = O + (own ? qb : qa) * 1024;
-      asm volatile("" : "+v"(first_try), "+v"(tick_b) : "v"(Pb[1][3]));  // read after the softmax
+      if constexpr (!EXT)
+        asm volatile("" : "+v"(first_try), "+v"(tick_b) : "v"(Pb[1][3]));  // read after the softmax
       const uint32_t seen = __builtin_amdgcn_readfirstlane(first_try);
       // In the fixed-order mode `want` packs the owners and their ranks
       // (slot a | slot b << 6 | rank a << 12 | rank b << 18 | second owner << 24)
@@ -936,19 +1027,25 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     const int qb = hb ? __builtin_amdgcn_readfirstlane(it_q[ri0 + 2 * t + 1]) : sinkq;
     const int ii = ri0 + (o < rn ? o : rn - 1);
     const bool cvalid = o < rn && gcol < G;
-    const float wv = cvalid ? bf16_to_f32(it_w[ii * 8 + gcol]) : 0.f;
-    load_q(Qb, qrs, qoff((uint32_t)qa | ((uint32_t)(hb ? qb : 0) << 8), cvalid), qks);
-    load_k(kb, frs, flo, (uint32_t)rc * kFragBytes);
-    load_v(vb, frs, flo, (uint32_t)rc * kFragBytes);
-    f32x4_t S[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      S[mt] = zero4();
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) S[mt] = mfma_bf16_16x16x32(kb[mt][ks], Qb[ks], S[mt]);
-    }
     u32x4_t Pb[2];
-    tile_P(S, rmsk, wv, KEEP && o < rn ? it_keep[ii] : ~0ull, Pb);
+    if constexpr (EXT) {
+      load_v(vb, frs, flo, (uint32_t)rc * kFragBytes);
+      ext_load(ii, Pb);
+      ext_finish(ii, cvalid, Pb);
+    } else {
+      const float wv = cvalid ? bf16_to_f32(it_w[ii * 8 + gcol]) : 0.f;
+      load_q(Qb, qrs, qoff((uint32_t)qa | ((uint32_t)(hb ? qb : 0) << 8), cvalid), qks);
+      load_k(kb, frs, flo, (uint32_t)rc * kFragBytes);
+      load_v(vb, frs, flo, (uint32_t)rc * kFragBytes);
+      f32x4_t S[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        S[mt] = zero4();
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) S[mt] = mfma_bf16_16x16x32(kb[mt][ks], Qb[ks], S[mt]);
+      }
+      tile_P(S, rmsk, wv, KEEP && o < rn ? it_keep[ii] : ~0ull, Pb);
+    }
     float* const srow = O + (own ? qb : qa) * 1024;
     add_rows(srow + lane_e, srow + lane_o, Pb);
   };
@@ -965,8 +1062,12 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
     more = nst < st_hi;
     u32x4_t rn = s_rec[more ? nst : st];
     // the order of the prefetches at a step's end: Q, K, then V
-    load_q(Qb, qrs, qoff(own2, own < n && gcol < G), qks);
-    load_k(kb, frs, flo, (uint32_t)c * kFragBytes);
+    if constexpr (!EXT) {
+      load_q(Qb, qrs, qoff(own2, own < n && gcol < G), qks);
+      load_k(kb, frs, flo, (uint32_t)c * kFragBytes);
+    } else {
+      ext_load(i0 + min(own, n - 1), Pn);
+    }
     if constexpr (!TOKEN) load_v(vb, frs, flo, (uint32_t)c * kFragBytes);
     while (true) {
       // Claim the step after the next one (steps after the first 2 kWaves go
@@ -1045,7 +1146,24 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_kernel(RaArgs a) {
       x0 = *reinterpret_cast<const f32x4_t*>(src + 4 * ((2 * u) ^ g));
       x1 = *reinterpret_cast<const f32x4_t*>(src + 4 * ((2 * u + 1) ^ g));
     };
-    if (a.parts > 1) {
+    if constexpr (EXT) {
+      // the rows added into ext_out (each row belongs to this workgroup alone)
+      for (int e = tid; e < rows * 16; e += kThreads) {
+        int u, qq, g;
+        const int64_t row = item_row(e, u, qq, g);
+        f32x4_t x0, x1;
+        lds_rows(qq, g, u, x0, x1);
+        f32x4_t* dst = reinterpret_cast<f32x4_t*>(a.ext_out + row * 128 + 8 * u);
+        f32x4_t y0 = dst[0], y1 = dst[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          y0[i] += x0[i];
+          y1[i] += x1[i];
+        }
+        dst[0] = y0;
+        dst[1] = y1;
+      }
+    } else if (a.parts > 1) {
       for (int e = tid; e < rows * 16; e += kThreads) {
         int u, qq, g;
         const int64_t row = item_row(e, u, qq, g);
@@ -1141,21 +1259,21 @@ int pick_tile(int G, int K, int64_t Ck, bool token, bool keep, bool det) {
   return 0;
 }
 
-template <bool TOKEN, bool KEEP, bool ALIBI = false>
+template <bool TOKEN, bool KEEP, bool ALIBI = false, bool EXT = false>
 int launch_routed(RaArgs& a, hipStream_t s) {
   if (TOKEN && a.det) return MRSA_ERR_UNSUPPORTED;  // token scoring has no fixed-order walk
-  const int tq = pick_tile(a.G, a.K, a.Ck, TOKEN, KEEP, a.det != 0);
+  const int tq = pick_tile(a.G, a.K, a.Ck, TOKEN, KEEP || EXT, a.det != 0);
   if (tq == 0) return MRSA_ERR_UNSUPPORTED;
   a.tq = tq;
   a.ntiles = (a.Lq + tq - 1) / tq;
   a.units = a.B * a.Hkv * a.parts * a.ntiles;
   const int64_t grid = (a.units + 7) / 8 * 8;
   if (grid > 0x7fffffff) return MRSA_ERR_UNSUPPORTED;
-  const RaLayout l = ra_layout(tq, a.G, a.K, a.Ck, TOKEN, KEEP, a.det != 0);
+  const RaLayout l = ra_layout(tq, a.G, a.K, a.Ck, TOKEN, KEEP || EXT, a.det != 0);
   a.spin_limit = g_spin_limit;
   // the fixed-order walk is its own instance, so the lock path carries none of its branches
-  auto kern = a.det ? routed_attn_kernel<TOKEN, KEEP, !TOKEN, ALIBI>
-                     : routed_attn_kernel<TOKEN, KEEP, false, ALIBI>;
+  auto kern = a.det ? routed_attn_kernel<TOKEN, KEEP, !TOKEN && !EXT, ALIBI, EXT>
+                     : routed_attn_kernel<TOKEN, KEEP, false, ALIBI, EXT>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)l.total) != hipSuccess)
     return MRSA_ERR_LAUNCH;
@@ -1216,6 +1334,8 @@ RaArgs base_args(const void* q, const void* kv_frags, const void* weights,
   a.spin_limit = kDefaultSpinLimit;
   a.det = 0;
   a.slope = nullptr;
+  a.ext_p = nullptr;
+  a.ext_out = nullptr;
   return a;
 }
 
@@ -1268,6 +1388,21 @@ int selected_forward(const void* q, const void* kv_frags, const void* weights,
 }
 
 }  // namespace
+
+// The routed backward's dQ walk (EXT instance): dq += sum over each query's
+// listed chunks (first occurrences) of dS . K, with the dS tiles read from
+// the records the chunk-major backward kernel wrote; kv_frags_bwd =
+// mrsa_kv_fragments(v, k), whose second half holds K^T.
+int mrsa::routed_dq_walk(const void* kv_frags_bwd, const void* ds_records,
+                         const int32_t* indices, const uint8_t* key_valid, int64_t batch,
+                         int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads,
+                         int64_t topk, float* grad_q, void* stream) {
+  RaArgs a = base_args(ds_records, kv_frags_bwd, ds_records, indices, key_valid, batch, q_len,
+                       kv_len, q_heads, kv_heads, topk, 1, 1.f);
+  a.ext_p = (const uint16_t*)ds_records;
+  a.ext_out = grad_q;
+  return launch_routed<false, false, false, true>(a, (hipStream_t)stream);
+}
 
 extern "C" int mrsa_selected_attention_fwd(const void* q, const void* kv_frags,
                                            const void* weights, const int32_t* indices,

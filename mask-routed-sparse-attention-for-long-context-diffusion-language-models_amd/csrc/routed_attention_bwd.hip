@@ -66,7 +66,12 @@ struct BwdArgs {
   const int32_t* start;      // [B * Hkv * Ck + 1]
   const int32_t* ustart;     // [B * Hkv * Ck + 1]
   const float* slope;        // [Hq] ALiBi slopes or null
+  // dS records [B, Lq, Hq, K] x 64 bf16 (lane group g's 16 keys at 16 g, in
+  // the packed P^T order of the forward's tiles), one per listed slot, for
+  // the dQ walk (null: dQ added here with atomics).
+  uint16_t* ds_rec;
 };
+
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
@@ -425,6 +430,16 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_dkv_kernel(BwdArgs a)
         Sb[ks][2] = pack_bf16x2(dP[2 * ks + 1][0], dP[2 * ks + 1][1]);
         Sb[ks][3] = pack_bf16x2(dP[2 * ks + 1][2], dP[2 * ks + 1][3]);
       }
+      if (a.ds_rec) {
+        // The dS record of this lane's column (pair e, head g): its 16 keys
+        // (the dQ walk adds dS . K afterwards).
+        if (cvalid) {
+          uint16_t* rec = a.ds_rec +
+                          ((((b * a.Lq + q) * a.Hq + (int64_t)h * G + g) * K + k) * 64 + 16 * lg);
+          *reinterpret_cast<u32x4_t*>(rec) = Sb[0];
+          *reinterpret_cast<u32x4_t*>(rec + 8) = Sb[1];
+        }
+      } else {
       // rows of this lane's four columns 4 grp + r: pair grp >> 1, heads 4 (grp & 1) + r
       const int64_t ep = r0 + 2 * wave + (grp >> 1);
       int64_t qrow = -1;
@@ -440,6 +455,7 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_dkv_kernel(BwdArgs a)
           const int gg = 4 * (grp & 1) + r;
           if (qrow >= 0 && gg < G) atomicAdd(a.dq + (qrow + gg) * 128 + 16 * nt + j, d[r]);
         }
+      }
       }
     }
     // this wave's columns of the tiles (columns without a pair or head hold
@@ -504,11 +520,11 @@ __global__ void __launch_bounds__(256) fill_zero_i32(int32_t* p, int64_t n) {
 struct ListPlan {
   int nqb;
   int64_t n;  // chunks B * Hkv * Ck
-  int64_t count, blkbase, start, ustart, list, total;  // byte offsets / size
+  int64_t count, blkbase, start, ustart, list, records, total;  // byte offsets / size
   int64_t max_units;
 };
 
-ListPlan list_plan(int64_t B, int64_t Lq, int64_t Hkv, int64_t K, int64_t Ck) {
+ListPlan list_plan(int64_t B, int64_t Lq, int64_t Hkv, int64_t K, int64_t Ck, int64_t Hq) {
   ListPlan p;
   p.nqb = (int)((Lq + kListBlock - 1) / kListBlock);
   p.n = B * Hkv * Ck;
@@ -524,6 +540,7 @@ ListPlan list_plan(int64_t B, int64_t Lq, int64_t Hkv, int64_t K, int64_t Ck) {
   p.start = take((p.n + 1) * 4);
   p.ustart = take((p.n + 1) * 4);
   p.list = take(pairs * 4);
+  p.records = take(B * Lq * Hq * K * 64 * 2);  // dS records of the dQ walk
   p.total = o;
   p.max_units = (pairs + kSegEntries - 1) / kSegEntries + p.n;
   return p;
@@ -553,7 +570,7 @@ int selected_backward(
   if (!q || !grad_out || !kv_frags || !kv_frags_bwd || !weights || !indices || !grad_q ||
       !grad_k || !grad_v || !grad_weights || !workspace)
     return MRSA_ERR_INVALID_ARGUMENT;
-  const ListPlan lp = list_plan(batch, q_len, kv_heads, topk, kv_len / 64);
+  const ListPlan lp = list_plan(batch, q_len, kv_heads, topk, kv_len / 64, q_heads);
   if (workspace_bytes < lp.total || (uintptr_t)workspace % 256 != 0)
     return MRSA_ERR_INVALID_ARGUMENT;
   if (((uintptr_t)q | (uintptr_t)grad_out | (uintptr_t)kv_frags | (uintptr_t)kv_frags_bwd |
@@ -605,13 +622,19 @@ int selected_backward(
   hipLaunchKernelGGL(list_fill_kernel, lgrid, dim3(kListBlock), 0, st, a,
                      (const int32_t*)blkbase, lp.nqb, list);
   a.list = list;
+  a.ds_rec = (uint16_t*)(ws + lp.records);
   if (slope)
     hipLaunchKernelGGL(routed_attn_dkv_kernel<true>, dim3((unsigned)lp.max_units), dim3(kThreads),
                        0, st, a);
   else
     hipLaunchKernelGGL(routed_attn_dkv_kernel<false>, dim3((unsigned)lp.max_units), dim3(kThreads),
                        0, st, a);
-  return mrsa_launch_status();
+  const int s2 = mrsa_launch_status();
+  if (s2 != MRSA_OK) return s2;
+  // dQ: the forward's walk over each query tile's chunks, adding dS . K
+  // into rows it owns (no atomics) from the records just written
+  return mrsa::routed_dq_walk(kv_frags_bwd, a.ds_rec, indices, key_valid, batch, q_len, kv_len,
+                              q_heads, kv_heads, topk, grad_q, stream);
 }
 
 }  // namespace
@@ -644,9 +667,10 @@ extern "C" int mrsa_selected_attention_alibi_bwd(
 }
 
 extern "C" int64_t mrsa_selected_attention_bwd_workspace_bytes(int64_t batch, int64_t q_len,
-                                                               int64_t kv_len, int64_t kv_heads,
-                                                               int64_t topk) {
-  if (batch < 0 || q_len < 0 || kv_len < 0 || kv_heads <= 0 || topk <= 0 || kv_len % 64)
+                                                               int64_t kv_len, int64_t q_heads,
+                                                               int64_t kv_heads, int64_t topk) {
+  if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 || topk <= 0 ||
+      kv_len % 64 || q_heads % kv_heads)
     return -1;
-  return list_plan(batch, q_len, kv_heads, topk, kv_len / 64).total;
+  return list_plan(batch, q_len, kv_heads, topk, kv_len / 64, q_heads).total;
 }

@@ -170,7 +170,7 @@ SIGNATURES = {
     ),
     "mrsa_routed_lock_giveups": (_I, [_P, _I]),
     "mrsa_set_routed_lock_spin_limit": (_I, [_I]),
-    "mrsa_selected_attention_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
+    "mrsa_selected_attention_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "mrsa_selected_attention_bwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,

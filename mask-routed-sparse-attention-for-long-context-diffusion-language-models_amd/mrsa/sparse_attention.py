@@ -398,7 +398,7 @@ def _selected_attention_bwd_impl(q, kv_frags, kv_frags_bwd, weights, indices, ke
     dk = torch.zeros(B, kv_len, Hkv, D, dtype=torch.float32, device=q.device)
     dv = torch.zeros(B, kv_len, Hkv, D, dtype=torch.float32, device=q.device)
     dw = torch.zeros(B, Lq, Hq, K, dtype=torch.bfloat16, device=q.device)
-    nbytes = int(_lib.call("mrsa_selected_attention_bwd_workspace_bytes", B, Lq, kv_len, Hkv, K))
+    nbytes = int(_lib.call("mrsa_selected_attention_bwd_workspace_bytes", B, Lq, kv_len, Hq, Hkv, K))
     if nbytes < 0:
         raise ValueError(f"invalid routed attention shapes q {tuple(q.shape)} kv_len {kv_len}")
     ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
@@ -479,7 +479,7 @@ def selected_attention_alibi_backward(q, k, v, weights, indices, key_valid, chun
     dk = torch.zeros(B, Lk, Hkv, D, dtype=torch.float32, device=q.device)
     dv = torch.zeros(B, Lk, Hkv, D, dtype=torch.float32, device=q.device)
     dw = torch.zeros(B, Lq, Hq, K, dtype=torch.bfloat16, device=q.device)
-    nbytes = int(_lib.call("mrsa_selected_attention_bwd_workspace_bytes", B, Lq, Lk, Hkv, K))
+    nbytes = int(_lib.call("mrsa_selected_attention_bwd_workspace_bytes", B, Lq, Lk, Hq, Hkv, K))
     if nbytes < 0:
         raise ValueError(f"invalid routed attention shapes q {tuple(q.shape)} kv_len {Lk}")
     ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
