@@ -23,13 +23,17 @@
 //            chunk (added with atomics when the chunk's pairs span several
 //            segments) -- the reference instead adds each query block's
 //            dK / dV into global memory with atomics;
-//   dQ       each pair's dS . K is added into the query's fp32 dQ rows with
-//            atomics (16 lanes per 64-byte row segment);
+//   dS       each pair's bf16 dS tile is stored as a record (128 bytes per
+//            (query, head, slot));
 //   dW       written directly (one pair = one slot).
+// dQ is then the forward kernel's walk over each query tile's chunks
+// (routed_attention.hip, mrsa::routed_dq_walk): the tiles take the records
+// as their P^T operand and K^T where the forward reads V, and the rows are
+// summed in LDS and added into dQ once -- no atomics.
 // Operands come from two fragment layouts of the same K / V:
 //   fwd = mrsa_kv_fragments(k, v): K images (keys x dims) for S^T = K . Q^T;
 //   bwd = mrsa_kv_fragments(v, k): V images (keys x dims) for dP^T = V . dO^T
-//         and K^T images (dims x keys, tiled order) for dQ = dS . K.
+//         and K^T images (dims x keys, tiled order) for the walk's dS . K.
 #include "mrsa_device.h"
 
 #include <algorithm>
@@ -68,7 +72,7 @@ struct BwdArgs {
   const float* slope;        // [Hq] ALiBi slopes or null
   // dS records [B, Lq, Hq, K] x 64 bf16 (lane group g's 16 keys at 16 g, in
   // the packed P^T order of the forward's tiles), one per listed slot, for
-  // the dQ walk (null: dQ added here with atomics).
+  // the dQ walk.
   uint16_t* ds_rec;
 };
 
@@ -260,15 +264,13 @@ __device__ __forceinline__ uint64_t keep_row_bits(const int8_t* kr) {
   return bits;
 }
 
-// LDS of the chunk-major kernel (bytes): the chunk's V images and K^T images
-// (16 KB each, lane l's 16 bytes of image i at 1024 i + 16 l) and one
-// round's tiles, bf16
+// LDS of the chunk-major kernel (bytes): the chunk's V images (16 KB, lane
+// l's 16 bytes of image i at 1024 i + 16 l) and one round's tiles, bf16
 // [row][64 columns] with 128-byte rows whose 16-byte block b sits at
 // b ^ ((row >> 1) & 7): P^T and dS^T (64 key rows), Q^T and bf16(w dO)^T
 // (128 dim rows).
 constexpr uint32_t kKvV = 0;
-constexpr uint32_t kKvKt = 16384;
-constexpr uint32_t kKvPt = 32768;
+constexpr uint32_t kKvPt = 16384;
 constexpr uint32_t kKvDs = kKvPt + 8192;
 constexpr uint32_t kKvQt = kKvDs + 8192;
 constexpr uint32_t kKvWd = kKvQt + 16384;
@@ -295,7 +297,7 @@ __device__ __forceinline__ void tile_put(unsigned char* sm, uint32_t base, int r
 //   phase 2 (wave w: dims 32 w .. + 31): dK += dS^T . Q, dV += P^T . bf16(w dO)
 //     over the round's 64 columns (two k-steps).
 template <bool ALIBI>
-__global__ void __launch_bounds__(kThreads, 1) routed_attn_dkv_kernel(BwdArgs a) {
+__global__ void __launch_bounds__(kThreads, 2) routed_attn_dkv_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char sm[kKvBytes];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -331,11 +333,11 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_dkv_kernel(BwdArgs a)
   load_rows(kb, make_rsrc(a.fwd + (b * a.Hkv + h) * a.Ck * 16384, (uint32_t)a.Ck * kFragBytes),
             l16, cb);
   {
-    // V images | K^T images: the chunk's whole bwd fragment (32 KB)
+    // the V images: the first half of the chunk's bwd fragment (16 KB)
     const unsigned char* vsrc =
         reinterpret_cast<const unsigned char*>(a.bwd + (b * a.Hkv + h) * a.Ck * 16384) + cb;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
       const int o = 16 * (tid + kThreads * i);
       *reinterpret_cast<u32x4_t*>(sm + kKvV + o) = *reinterpret_cast<const u32x4_t*>(vsrc + o);
     }
@@ -415,12 +417,10 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_dkv_kernel(BwdArgs a)
     const float sl = ALIBI && cvalid ? -a.slope[(int64_t)h * G + g] * c2 : 0.f;
     const float di = chunk_grad(S, dP, msh, c2, a.scale * wv, ALIBI, sl, lg);  // S <- P, dP <- dS
     if (cvalid && grp == 0) a.dw[row * K + k] = (uint16_t)f32_to_bf16(di);
-    // dQ (columns x dims) = dS . K: A = dS packed in the tiled key order
-    // (reduction index 8 grp + e of k-step ks is key 32 ks + 16 (e >> 2) +
-    // 4 grp + (e & 3)), B = the K^T images (lane (j, grp): dim 16 nt + j, the
-    // same keys).  Lane (grp, j) of product nt: columns 4 grp + r, dim
-    // 16 nt + j, added into the column's dQ row (16 lanes = 64 contiguous
-    // bytes per row).
+    // dS of this lane's column packed in the tiled key order (reduction
+    // index 8 grp + e of k-step ks is key 32 ks + 16 (e >> 2) + 4 grp +
+    // (e & 3)), the P^T operand order of the forward's tiles: stored as the
+    // column's record for the dQ walk.
     {
       u32x4_t Sb[2];
 #pragma unroll
@@ -430,32 +430,13 @@ __global__ void __launch_bounds__(kThreads, 1) routed_attn_dkv_kernel(BwdArgs a)
         Sb[ks][2] = pack_bf16x2(dP[2 * ks + 1][0], dP[2 * ks + 1][1]);
         Sb[ks][3] = pack_bf16x2(dP[2 * ks + 1][2], dP[2 * ks + 1][3]);
       }
-      if (a.ds_rec) {
-        // The dS record of this lane's column (pair e, head g): its 16 keys
-        // (the dQ walk adds dS . K afterwards).
-        if (cvalid) {
-          uint16_t* rec = a.ds_rec +
-                          ((((b * a.Lq + q) * a.Hq + (int64_t)h * G + g) * K + k) * 64 + 16 * lg);
-          *reinterpret_cast<u32x4_t*>(rec) = Sb[0];
-          *reinterpret_cast<u32x4_t*>(rec + 8) = Sb[1];
-        }
-      } else {
-      // rows of this lane's four columns 4 grp + r: pair grp >> 1, heads 4 (grp & 1) + r
-      const int64_t ep = r0 + 2 * wave + (grp >> 1);
-      int64_t qrow = -1;
-      if (ep < e1) qrow = (b * a.Lq + (a.list[ep] & 0xffffff)) * a.Hq + (int64_t)h * G;
-#pragma unroll
-      for (int nt = 0; nt < 8; ++nt) {
-        f32x4_t d = mfma_bf16_16x16x32(
-            Sb[0], *reinterpret_cast<const u32x4_t*>(sm + kKvKt + 1024 * (2 * nt) + l16), zero4());
-        d = mfma_bf16_16x16x32(
-            Sb[1], *reinterpret_cast<const u32x4_t*>(sm + kKvKt + 1024 * (2 * nt + 1) + l16), d);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int gg = 4 * (grp & 1) + r;
-          if (qrow >= 0 && gg < G) atomicAdd(a.dq + (qrow + gg) * 128 + 16 * nt + j, d[r]);
-        }
-      }
+      // The dS record of this lane's column (pair e, head g): its 16 keys
+      // (the dQ walk adds dS . K afterwards).
+      if (cvalid) {
+        uint16_t* rec =
+            a.ds_rec + ((((b * a.Lq + q) * a.Hq + (int64_t)h * G + g) * K + k) * 64 + 16 * lg);
+        *reinterpret_cast<u32x4_t*>(rec) = Sb[0];
+        *reinterpret_cast<u32x4_t*>(rec + 8) = Sb[1];
       }
     }
     // this wave's columns of the tiles (columns without a pair or head hold
