@@ -72,8 +72,10 @@ __device__ __forceinline__ void route_weights_row(
   const uint16_t* sc = scores + r * (I)K + k0;
   const int32_t* ix = indices + (bl * (I)Hkv + hk) * (I)K + k0;
 
+  // lanes past the last slot (8 LPR > K, e.g. K = 24 or 40) keep chunk -1:
+  // masked slots
   uint32_t sv[4] = {0u, 0u, 0u, 0u};
-  int32_t iv[8];
+  int32_t iv[8] = {-1, -1, -1, -1, -1, -1, -1, -1};
   if (VEC && k0 < K) {
     const u32x4_t s4 = *reinterpret_cast<const u32x4_t*>(sc);
     const u32x4_t i0 = *reinterpret_cast<const u32x4_t*>(ix);

@@ -362,7 +362,8 @@ def test_route_topk_g7_api_and_determinism():
                  lm.cpu().reshape(1, C, 28, 128), lse.cpu(), bias.cpu(), dropped.cpu(), 32, "g7 api")
 
 
-@pytest.mark.parametrize("affine,K", [(True, 32), (False, 32), (False, 64), (True, 8), (True, 20)])
+@pytest.mark.parametrize("affine,K", [(True, 32), (False, 32), (False, 64), (True, 8), (True, 20),
+                                      (False, 24), (True, 40)])
 def test_route_weights_vs_oracle(affine, K):
     _note(f"route weights affine={affine} K={K}")
     B, L, Hkv, G, C = 1, 700, 4, 7, 256
